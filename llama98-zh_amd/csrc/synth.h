@@ -1,0 +1,56 @@
+/* Seeded random-init KunMoe checkpoints in the reference's model.bin format.
+ *
+ * The writer follows the reference loader: header words in the order
+ * lz_open_bin reads them (reference src/model.c:3993-4200, version 5), then
+ * tensors in model_walk order (src/model.c:2240-2625, LAYER_SPECS
+ * src/model.c:1496-1665).  Every matrix is LZ_FMT_Q8_0 with one fp32 scale
+ * per output row (gs = in_dim); norms, A_log, dt_bias, the depthwise conv
+ * filters and the router bias are LZ_FMT_F32.
+ *
+ * Randomness is splitmix64 per (tensor, row) stream with a Box-Muller normal
+ * built from basic IEEE double operations only (no libm), so the same seed
+ * gives the same bytes on every x86-64 host and thread count.
+ */
+#ifndef L98_SYNTH_H
+#define L98_SYNTH_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct {
+    int vocab, hidden, n_layers, seq_len;
+    int attn_period;            /* layer i is full attention iff i % period == period-1 */
+    int n_heads, n_kv_heads, head_dim;
+    int kda_heads, kd, vd;      /* lin_n_k_heads == lin_n_v_heads == kda_heads */
+    int conv_kernel, gate_rank;
+    int n_experts, topk, latent, moe_inter, shared_w;
+    int mtp_inter;
+    float w_std;                /* N(0, w_std) for every matrix except the router */
+    float router_std;           /* router weight std (0: use w_std) */
+    float bias_std;             /* router selection bias std */
+} L98SynthConfig;
+
+/* Named configurations:
+ *   0  tiny    d=256, 4 layers (3 KDA + 1 attn), E=16 top-2, V=8192
+ *   1  base    d=1024, 24 layers (3:1), 16 KDA heads x64, E=64 top-6, V=65536
+ *   2  tiny    same shapes as 0 (k-sweep config uses config 0's model)
+ *   3  large   d=2048, 32 layers (3:1), 16 KDA heads x128, E=128 top-8, V=131072
+ *   4  server  config 0's shapes, router N(0,1/d), bias N(0,0.5)
+ *  10  micro   d=64 toy for fast unit tests
+ * Returns 0 on success, 1 for an unknown id. */
+int l98_synth_config(int id, L98SynthConfig *out);
+
+/* Writes <dir>/model.bin.  seq_len in cfg is what the state allocator sizes
+ * for.  Returns 0 on success, nonzero with a message in err otherwise. */
+int l98_synth_write(const char *dir, const L98SynthConfig *cfg, uint64_t seed,
+                    int n_threads, char *err, int errlen);
+
+/* Deterministic N(0,1) stream used by the writer, exposed for tests. */
+double l98_synth_normal(uint64_t *state);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
