@@ -64,3 +64,22 @@ $(OUT)/libl98ref.so: $(ORA_OBJS)
 	$(CC) -shared -o $@ $(ORA_OBJS) -lm
 
 .PHONY: all
+
+# Tap build: the reference's own LZ_TAP hook (src/forward.h:27-36) routed to
+# a recorder in the harness, to localise a divergence layer by layer.
+TAP_DEFS := -DLZ_GDN_STATE_F32=1 '-DLZ_TAP(tag,li,ptr,n)=l98_tap(tag,li,(const float*)(ptr),n)' \
+            '-Dl98_tap_decl=1' -include oracle/tap.h
+TAP_OBJS := $(addprefix $(OUT)/tap/,$(addsuffix .o,$(ENG) $(MMX) $(AVX2)))
+$(OUT)/tap/%.o: $(REF)/src/%.c oracle/tap.h
+	@mkdir -p $(OUT)/tap
+	$(CC) $(BASEFL) $(TAP_DEFS) -c -o $@ $<
+$(addprefix $(OUT)/tap/,$(addsuffix .o,$(MMX))): $(OUT)/tap/%.o: $(REF)/src/%.c
+	@mkdir -p $(OUT)/tap
+	$(CC) $(BASEFL) $(TAP_DEFS) -mmmx -msse -msse2 -c -o $@ $<
+$(OUT)/tap/$(AVX2).o: $(REF)/src/$(AVX2).c
+	@mkdir -p $(OUT)/tap
+	$(CC) $(BASEFL) $(TAP_DEFS) -mavx2 -c -o $@ $<
+$(OUT)/l98ref_tap: oracle/ref_harness.c $(TAP_OBJS)
+	$(CC) $(BASEFL) $(TAP_DEFS) -DHARNESS_ORACLE=1 -DHARNESS_TAP=1 -o $@ oracle/ref_harness.c $(TAP_OBJS) -lm
+tap: $(OUT)/l98ref_tap
+.PHONY: tap

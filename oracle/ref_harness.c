@@ -32,6 +32,27 @@
 #include "ops.h"
 #include "sampler.h"
 
+#if HARNESS_TAP
+/* Appends (tag[8], layer, n, n floats) records to $L98_TAP_FILE. */
+void l98_tap(const char *tag, int layer, const float *p, int n) {
+    static FILE *f;
+    char t[8];
+    if (!f) {
+        const char *path = getenv("L98_TAP_FILE");
+        if (!path) return;
+        f = fopen(path, "wb");
+        if (!f) return;
+    }
+    memset(t, 0, sizeof t);
+    strncpy(t, tag, sizeof t);
+    fwrite(t, 1, 8, f);
+    fwrite(&layer, 4, 1, f);
+    fwrite(&n, 4, 1, f);
+    fwrite(p, 4, (size_t)n, f);
+    fflush(f);
+}
+#endif
+
 static double now_us(void) {
     struct timespec ts;
     clock_gettime(CLOCK_MONOTONIC, &ts);
@@ -128,6 +149,7 @@ static void dump_state(const char *prefix, const LZModel *m, const LZRunState *s
         }
     }
     dump(prefix, "mtp_chain", s->mtp_chain, sizeof(float) * (size_t)c->hidden_size);
+    dump(prefix, "rope_cs", s->rope_cs, sizeof(float) * (size_t)s->seq_len * c->rotary_dim);
 }
 
 static int cmd_gen(int argc, char **argv) {
