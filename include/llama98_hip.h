@@ -1,0 +1,180 @@
+/* llama98_hip.h -- C ABI of the MI355X (gfx950) implementation of the
+ * llama98 MTP speculative-decoding step.
+ *
+ * The entry points keep the reference's names, argument meaning, return
+ * conventions and error codes (reference src/forward.h:1883-2150,
+ * src/llama_zh.h:520-640, llama98.def:14-60), so a caller of the
+ * reference's spec path links against libl98hip.so instead.  All compute
+ * runs on the GPU; the structs below carry the fields callers of the
+ * reference read (LZRunState's mtp_* buffers, ssm_slot, mtp_pos, ...) as
+ * host mirrors, refreshed by the entry point that returns them.
+ *
+ * Numerics: the reference's float-oracle mode (--fixed off --fastfp off,
+ * fp32 KDA state, Q8 KV cache, no attention window).  Results are
+ * bit-identical to that mode of the reference engine.
+ *
+ * Threading: like the reference, one LZRunState is used by one thread at a
+ * time; distinct states may run concurrently on distinct HIP streams.
+ */
+#ifndef LLAMA98_HIP_H
+#define LLAMA98_HIP_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef unsigned long long lz_u64;
+
+/* Reference error codes (src/err.h:19-380) that this path returns. */
+enum {
+    LZ_ERR_OK = 0,
+    LZ_ERR_NULL_ARG = 6,
+    LZ_ERR_STATE_ALLOC = 7,
+    LZ_ERR_FORWARD = 20,
+    LZ_ERR_SPEC_NO_HEAD = 24,
+    LZ_ERR_SPEC_K_RANGE = 25,
+    LZ_ERR_BIN_OPEN = 81,
+    LZ_ERR_BIN_MAGIC = 83,
+    LZ_ERR_BIN_VERSION = 84
+};
+
+#define LZ_SPEC_K_MAX 6      /* src/ops.h:2098 */
+#define LZ_BATCH_MAX 8       /* src/ops.h:1457 */
+
+/* The LZModelConfig fields the spec path reads (src/model.h:237-874). */
+typedef struct {
+    int vocab_size, hidden_size, n_layers, seq_len;
+    int n_heads, n_kv_heads, head_dim, rotary_dim;
+    int lin_n_k_heads, lin_n_v_heads, lin_k_head_dim, lin_v_head_dim, conv_kernel;
+    int n_linear_layers, n_full_layers;
+    int attn_q_dim, attn_qgate_dim, attn_kv_dim, lin_key_dim, lin_value_dim, lin_conv_dim;
+    int kda_gate_rank, num_experts, num_experts_per_token, moe_latent_dim;
+    int moe_intermediate_size, moe_shared_width, mtp_intermediate_size, mtp_n_layers;
+    float rms_norm_eps, rope_theta;
+    int layer_types[128];
+} LZModelConfig;
+
+/* Caller-allocated, as in the reference: LZModel m; lz_open(&m, dir, ...). */
+typedef struct {
+    LZModelConfig config;
+    long long bytes_device;        /* device memory held by the weights */
+    void *impl;                    /* device weights */
+} LZModel;
+
+typedef struct {
+    int seq_len;
+    int ssm_slot;                  /* KDA/conv ring slot (src/forward.h:1153) */
+    int ssm_ring_depth;            /* spec_k_max + 1 (src/forward.h:1164) */
+    int mtp_pos;                   /* next MTP KV row (src/forward.h:897) */
+    int nt_cap;                    /* tokens per forward chunk */
+    /* host mirrors, refreshed by the call that returns or fills them */
+    float *logits;                 /* vocab: lz_forward_capture */
+    float *mtp_logits;             /* (LZ_SPEC_K_MAX+1) x vocab: lz_forward_verify */
+    float *mtp_verify_hidden;      /* (LZ_SPEC_K_MAX+1) x hidden: lz_forward_verify */
+    float *mtp_chain;              /* hidden: after capture / draft / round */
+    float *mtp_draft_logits;       /* vocab: lz_mtp_draft_step */
+    long long bytes_device;
+    void *impl;
+} LZRunState;
+
+/* LZSampleParams / LZSampler subset (src/sampler.h:150-190).  Penalties
+ * are outside this path: a sampler whose penalties are active is refused. */
+typedef struct {
+    float temperature;
+    float temp_think;
+    int think_temp_enabled;
+    float topp;
+    float minp;
+    int topk;
+    float presence_penalty;
+    float frequency_penalty;
+    float repetition_penalty;
+    int repeat_last_n;
+    int minp_llamacpp;
+} LZSampleParams;
+
+typedef struct {
+    int vocab_size;
+    LZSampleParams p;
+    lz_u64 rng_state;
+} LZSampler;
+
+/* ---- model (src/model.h:1327-1341) ---- */
+/* Reads <dir>/model.bin and uploads the weights to the current HIP device.
+ * Returns 0, or 1 with a message in errbuf. */
+int lz_open(LZModel *m, const char *dir, char *errbuf, int errlen);
+void lz_free(LZModel *m);
+
+/* ---- run state (src/forward.h:1883-1933) ---- */
+/* Returns 0, or 1 with a message. Ring depth is spec_k_max + 1 (clamped to
+ * LZ_SPEC_K_MAX + 1).  seq_len <= 0 takes the model's. */
+int lz_state_alloc(LZRunState *s, const LZModel *m, int seq_len, int spec_k_max,
+                   char *errbuf, int errlen);
+void lz_state_free(LZRunState *s);
+void lz_state_reset(LZRunState *s, const LZModel *m);
+
+/* ---- forward (src/forward.h:1940-2150) ---- */
+/* One token; its final-normed hidden goes to mtp_chain.  Returns the host
+ * logits mirror, or NULL on a bad token/position. */
+float *lz_forward_capture(const LZModel *m, LZRunState *s, int token, int pos);
+/* Prefill of n tokens at pos0.. with every row's final-normed hidden copied
+ * to hidden_out (host, n x hidden).  Returns s->logits (last row's logits are
+ * not computed, as in the reference: the pointer is only a success flag), or
+ * NULL. */
+float *lz_forward_batch_capture(const LZModel *m, LZRunState *s, const int *tokens, int n,
+                                int pos0, float *hidden_out);
+/* Verify forward of n <= LZ_BATCH_MAX tokens at pos0..: every row's logits
+ * into s->mtp_logits and hidden into s->mtp_verify_hidden; advances the ring
+ * by n.  Returns 0, or 1 on failure. */
+int lz_forward_verify(const LZModel *m, LZRunState *s, const int *tokens, int n, int pos0);
+/* One MTP draft step; returns s->mtp_draft_logits, or NULL. */
+float *lz_mtp_draft_step(const LZModel *m, LZRunState *s, int next_token, int pos);
+/* MTP KV rows from (hidden, next token) pairs.  Returns 0, or 1. */
+int lz_mtp_prefill(const LZModel *m, LZRunState *s, const float *h_body_all,
+                   const int *next_tokens, int n, int pos0);
+int lz_mtp_catchup(const LZModel *m, LZRunState *s, const float *h_body_all,
+                   const int *next_tokens, int n, int pos0);
+
+/* ---- acceptance and rounds (src/llama_zh.h:520-640) ---- */
+int lz_spec_accept(const int *draft, const int *targ, int n_draft, int bonus, int *out);
+int lz_spec_accept_temp(const float *p, const float *q, int x, int vocab, float u,
+                        lz_u64 *residual_rng, int *out_accepted);
+/* Greedy round.  Returns n_accept + 1 (tokens in out), 0 on discard
+ * (k_eff < n_min), or -LZErr. */
+int lz_spec_round(const LZModel *m, LZRunState *s, int anchor, int anchor_pos, int k,
+                  float p_min, int n_min, const LZSampler *samp, int debug_break_rollback,
+                  int debug_skip_catchup, int *out, int *out_n_accept, int *out_new_pos,
+                  int *out_k_eff, char *errbuf, int errlen);
+/* Temperature / top-p round (src/generate.c:1234-1377). */
+int lz_spec_round_temp(const LZModel *m, LZRunState *s, int anchor, int anchor_pos, int k,
+                       float p_min, int n_min, LZSampler *samp, int debug_break_rollback,
+                       int debug_skip_catchup, int *out, int *out_n_accept, int *out_new_pos,
+                       int *out_k_eff, char *errbuf, int errlen);
+
+/* ---- sampler (src/sampler.h:200-230) ---- */
+void lz_sample_defaults(LZSampleParams *p);
+int lz_sampler_init(LZSampler *s, int vocab_size, const LZSampleParams *p, lz_u64 seed);
+void lz_sampler_free(LZSampler *s);
+float lz_random_f32(lz_u64 *state);
+int lz_sample_argmax(const float *logits, int n);
+int lz_argmax_p1(const float *logits, int n, float *out_p);
+
+/* ---- this implementation's own additions (no reference counterpart) ---- */
+/* The whole generation loop of lz_generate's --spec path
+ * (src/generate.c:1822-2106, penalties off): prefill + MTP prefill, then
+ * rounds until n_new tokens are emitted.  Greedy rounds run back to back on
+ * the device with no host round trip.  tokens receives up to cap ids
+ * (whole last round).  Returns the number of tokens emitted, or -LZErr. */
+int l98_generate(const LZModel *m, LZRunState *s, const int *prompt, int n_prompt, int k,
+                 int n_new, const LZSampler *samp, int *tokens, int cap, int *k_eff_out,
+                 int *n_accept_out, int *n_rounds);
+/* Device and build facts, for logs. */
+const char *l98_device_name(void);
+/* Seconds of device time of the last l98_generate call's round loop
+ * (hipEvent-timed), and its round count. */
+double l98_last_loop_seconds(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,292 @@
+"""Python bindings of the MI355X MTP speculative-decoding library.
+
+The product is the C ABI of ``include/llama98_hip.h`` (``lib/libl98hip.so``,
+hand-written gfx950 kernels behind the reference's ``lz_*`` entry points).
+This module is a thin ctypes layer over it for tests and ``bench.py``, plus
+the seeded synthetic-model writer (``lib/libl98synth.so``) and the prompt
+generator the benchmark configs use.
+
+The package directory is named ``llama98-zh_amd``; import it with
+``load_package()`` from ``__graft_entry__`` or by path.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_DIR = os.path.join(HERE, "lib")
+HIP_LIB = os.path.join(LIB_DIR, "libl98hip.so")
+SYNTH_LIB = os.path.join(LIB_DIR, "libl98synth.so")
+
+LZ_SPEC_K_MAX = 6
+LZ_BATCH_MAX = 8
+LZ_ERR = {"NULL_ARG": 6, "STATE_ALLOC": 7, "FORWARD": 20, "SPEC_NO_HEAD": 24, "SPEC_K_RANGE": 25}
+
+
+class LZModelConfig(C.Structure):
+    _fields_ = [(n, C.c_int) for n in (
+        "vocab_size", "hidden_size", "n_layers", "seq_len",
+        "n_heads", "n_kv_heads", "head_dim", "rotary_dim",
+        "lin_n_k_heads", "lin_n_v_heads", "lin_k_head_dim", "lin_v_head_dim", "conv_kernel",
+        "n_linear_layers", "n_full_layers",
+        "attn_q_dim", "attn_qgate_dim", "attn_kv_dim", "lin_key_dim", "lin_value_dim", "lin_conv_dim",
+        "kda_gate_rank", "num_experts", "num_experts_per_token", "moe_latent_dim",
+        "moe_intermediate_size", "moe_shared_width", "mtp_intermediate_size", "mtp_n_layers")] + [
+        ("rms_norm_eps", C.c_float), ("rope_theta", C.c_float), ("layer_types", C.c_int * 128)]
+
+
+class LZModel(C.Structure):
+    _fields_ = [("config", LZModelConfig), ("bytes_device", C.c_longlong), ("impl", C.c_void_p)]
+
+
+class LZRunState(C.Structure):
+    _fields_ = [("seq_len", C.c_int), ("ssm_slot", C.c_int), ("ssm_ring_depth", C.c_int),
+                ("mtp_pos", C.c_int), ("nt_cap", C.c_int),
+                ("logits", C.POINTER(C.c_float)), ("mtp_logits", C.POINTER(C.c_float)),
+                ("mtp_verify_hidden", C.POINTER(C.c_float)), ("mtp_chain", C.POINTER(C.c_float)),
+                ("mtp_draft_logits", C.POINTER(C.c_float)),
+                ("bytes_device", C.c_longlong), ("impl", C.c_void_p)]
+
+
+class LZSampleParams(C.Structure):
+    _fields_ = [("temperature", C.c_float), ("temp_think", C.c_float), ("think_temp_enabled", C.c_int),
+                ("topp", C.c_float), ("minp", C.c_float), ("topk", C.c_int),
+                ("presence_penalty", C.c_float), ("frequency_penalty", C.c_float),
+                ("repetition_penalty", C.c_float), ("repeat_last_n", C.c_int), ("minp_llamacpp", C.c_int)]
+
+
+class LZSampler(C.Structure):
+    _fields_ = [("vocab_size", C.c_int), ("p", LZSampleParams), ("rng_state", C.c_uint64)]
+
+
+class L98SynthConfig(C.Structure):
+    _fields_ = [(n, C.c_int) for n in (
+        "vocab", "hidden", "n_layers", "seq_len", "attn_period", "n_heads", "n_kv_heads", "head_dim",
+        "kda_heads", "kd", "vd", "conv_kernel", "gate_rank", "n_experts", "topk", "latent",
+        "moe_inter", "shared_w", "mtp_inter")] + [
+        ("w_std", C.c_float), ("router_std", C.c_float), ("bias_std", C.c_float)]
+
+
+_P = C.c_void_p
+_IP = C.POINTER(C.c_int)
+_FP = C.POINTER(C.c_float)
+
+# (name, restype, argtypes) of every entry point include/llama98_hip.h declares.
+HIP_API = [
+    ("lz_open", C.c_int, [C.POINTER(LZModel), C.c_char_p, C.c_char_p, C.c_int]),
+    ("lz_free", None, [C.POINTER(LZModel)]),
+    ("lz_state_alloc", C.c_int, [C.POINTER(LZRunState), C.POINTER(LZModel), C.c_int, C.c_int, C.c_char_p, C.c_int]),
+    ("lz_state_free", None, [C.POINTER(LZRunState)]),
+    ("lz_state_reset", None, [C.POINTER(LZRunState), C.POINTER(LZModel)]),
+    ("lz_forward_capture", _FP, [C.POINTER(LZModel), C.POINTER(LZRunState), C.c_int, C.c_int]),
+    ("lz_forward_batch_capture", _FP, [C.POINTER(LZModel), C.POINTER(LZRunState), _IP, C.c_int, C.c_int, _FP]),
+    ("lz_forward_verify", C.c_int, [C.POINTER(LZModel), C.POINTER(LZRunState), _IP, C.c_int, C.c_int]),
+    ("lz_mtp_draft_step", _FP, [C.POINTER(LZModel), C.POINTER(LZRunState), C.c_int, C.c_int]),
+    ("lz_mtp_prefill", C.c_int, [C.POINTER(LZModel), C.POINTER(LZRunState), _FP, _IP, C.c_int, C.c_int]),
+    ("lz_mtp_catchup", C.c_int, [C.POINTER(LZModel), C.POINTER(LZRunState), _FP, _IP, C.c_int, C.c_int]),
+    ("lz_spec_accept", C.c_int, [_IP, _IP, C.c_int, C.c_int, _IP]),
+    ("lz_spec_accept_temp", C.c_int, [_FP, _FP, C.c_int, C.c_int, C.c_float, C.POINTER(C.c_uint64), _IP]),
+    ("lz_spec_round", C.c_int, [C.POINTER(LZModel), C.POINTER(LZRunState), C.c_int, C.c_int, C.c_int, C.c_float,
+                                C.c_int, C.POINTER(LZSampler), C.c_int, C.c_int, _IP, _IP, _IP, _IP,
+                                C.c_char_p, C.c_int]),
+    ("lz_spec_round_temp", C.c_int, [C.POINTER(LZModel), C.POINTER(LZRunState), C.c_int, C.c_int, C.c_int,
+                                     C.c_float, C.c_int, C.POINTER(LZSampler), C.c_int, C.c_int, _IP, _IP, _IP,
+                                     _IP, C.c_char_p, C.c_int]),
+    ("lz_sample_defaults", None, [C.POINTER(LZSampleParams)]),
+    ("lz_sampler_init", C.c_int, [C.POINTER(LZSampler), C.c_int, C.POINTER(LZSampleParams), C.c_uint64]),
+    ("lz_sampler_free", None, [C.POINTER(LZSampler)]),
+    ("lz_random_f32", C.c_float, [C.POINTER(C.c_uint64)]),
+    ("lz_sample_argmax", C.c_int, [_FP, C.c_int]),
+    ("lz_argmax_p1", C.c_int, [_FP, C.c_int, _FP]),
+    ("l98_generate", C.c_int, [C.POINTER(LZModel), C.POINTER(LZRunState), _IP, C.c_int, C.c_int, C.c_int,
+                               C.POINTER(LZSampler), _IP, C.c_int, _IP, _IP, _IP]),
+    ("l98_device_name", C.c_char_p, []),
+    ("l98_last_loop_seconds", C.c_double, []),
+]
+
+_hip = None
+_synth = None
+
+
+def hip_lib(path=HIP_LIB):
+    """Loads libl98hip.so (raises if it was not built: there is no fallback)."""
+    global _hip
+    if _hip is None:
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} is missing: run __graft_entry__.build() first")
+        lib = C.CDLL(path)
+        for name, res, args in HIP_API:
+            f = getattr(lib, name)
+            f.restype = res
+            f.argtypes = args
+        _hip = lib
+    return _hip
+
+
+def synth_lib():
+    global _synth
+    if _synth is None:
+        if not os.path.exists(SYNTH_LIB):
+            raise RuntimeError(f"{SYNTH_LIB} is missing: run __graft_entry__.build() first")
+        lib = C.CDLL(SYNTH_LIB)
+        lib.l98_synth_config.argtypes = [C.c_int, C.POINTER(L98SynthConfig)]
+        lib.l98_synth_write.argtypes = [C.c_char_p, C.POINTER(L98SynthConfig), C.c_uint64, C.c_int,
+                                        C.c_char_p, C.c_int]
+        _synth = lib
+    return _synth
+
+
+def synth_config(config_id):
+    cfg = L98SynthConfig()
+    if synth_lib().l98_synth_config(config_id, C.byref(cfg)) != 0:
+        raise ValueError(f"unknown synthetic config {config_id}")
+    return cfg
+
+
+def write_model(path, config_id, seed=1234, threads=8, cfg=None):
+    """Writes path/model.bin for a named synthetic config (see csrc/synth.h)."""
+    cfg = cfg or synth_config(config_id)
+    os.makedirs(path, exist_ok=True)
+    err = C.create_string_buffer(256)
+    if synth_lib().l98_synth_write(path.encode(), C.byref(cfg), seed, threads, err, 256) != 0:
+        raise RuntimeError(err.value.decode())
+    return os.path.join(path, "model.bin")
+
+
+def ensure_model(path, config_id, seed=1234):
+    """Writes the model unless an identical one (same config id + seed) exists."""
+    stamp = os.path.join(path, "synth.txt")
+    want = f"config {config_id} seed {seed}\n"
+    if os.path.exists(stamp) and os.path.exists(os.path.join(path, "model.bin")):
+        if open(stamp).read() == want:
+            return path
+    write_model(path, config_id, seed)
+    with open(stamp, "w") as f:
+        f.write(want)
+    return path
+
+
+def prompt_tokens(seed, n, vocab):
+    """Uniform random ids: splitmix64 stream from seed, id = z mod vocab."""
+    out = np.empty(n, np.int64)
+    st = seed & 0xFFFFFFFFFFFFFFFF
+    M = 0xFFFFFFFFFFFFFFFF
+    for i in range(n):
+        st = (st + 0x9E3779B97F4A7C15) & M
+        z = st
+        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & M
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & M
+        z = z ^ (z >> 31)
+        out[i] = z % vocab
+    return out.astype(np.int32)
+
+
+def _ip(a):
+    return a.ctypes.data_as(_IP)
+
+
+def _fp(a):
+    return a.ctypes.data_as(_FP)
+
+
+class Engine:
+    """One model + one run state on the current HIP device."""
+
+    def __init__(self, model_dir, spec_k_max=LZ_SPEC_K_MAX, seq_len=0):
+        lib = hip_lib()
+        self.lib = lib
+        self.m = LZModel()
+        self.s = LZRunState()
+        err = C.create_string_buffer(512)
+        if lib.lz_open(C.byref(self.m), model_dir.encode(), err, 512) != 0:
+            raise RuntimeError("lz_open: " + err.value.decode())
+        if lib.lz_state_alloc(C.byref(self.s), C.byref(self.m), seq_len, spec_k_max, err, 512) != 0:
+            lib.lz_free(C.byref(self.m))
+            raise RuntimeError("lz_state_alloc: " + err.value.decode())
+        self.cfg = self.m.config
+        self.V = self.cfg.vocab_size
+        self.d = self.cfg.hidden_size
+
+    def close(self):
+        if self.s.impl:
+            self.lib.lz_state_free(C.byref(self.s))
+        if self.m.impl:
+            self.lib.lz_free(C.byref(self.m))
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def reset(self):
+        self.lib.lz_state_reset(C.byref(self.s), C.byref(self.m))
+
+    def forward_capture(self, token, pos):
+        p = self.lib.lz_forward_capture(C.byref(self.m), C.byref(self.s), int(token), int(pos))
+        if not p:
+            return None
+        return np.ctypeslib.as_array(p, shape=(self.V,)).copy()
+
+    def batch_capture(self, tokens, pos0):
+        tokens = np.ascontiguousarray(tokens, np.int32)
+        h = np.zeros((len(tokens), self.d), np.float32)
+        p = self.lib.lz_forward_batch_capture(C.byref(self.m), C.byref(self.s), _ip(tokens), len(tokens),
+                                              int(pos0), _fp(h))
+        return h if p else None
+
+    def verify(self, tokens, pos0):
+        tokens = np.ascontiguousarray(tokens, np.int32)
+        n = len(tokens)
+        rc = self.lib.lz_forward_verify(C.byref(self.m), C.byref(self.s), _ip(tokens), n, int(pos0))
+        if rc != 0:
+            return None
+        lg = np.ctypeslib.as_array(self.s.mtp_logits, shape=(LZ_SPEC_K_MAX + 1, self.V))[:n].copy()
+        hd = np.ctypeslib.as_array(self.s.mtp_verify_hidden, shape=(LZ_SPEC_K_MAX + 1, self.d))[:n].copy()
+        return lg, hd
+
+    def draft_step(self, token, pos):
+        p = self.lib.lz_mtp_draft_step(C.byref(self.m), C.byref(self.s), int(token), int(pos))
+        if not p:
+            return None
+        return np.ctypeslib.as_array(p, shape=(self.V,)).copy()
+
+    def chain(self):
+        return np.ctypeslib.as_array(self.s.mtp_chain, shape=(self.d,)).copy()
+
+    def mtp_prefill(self, h, next_tokens, pos0):
+        h = np.ascontiguousarray(h, np.float32)
+        nt = np.ascontiguousarray(next_tokens, np.int32)
+        return self.lib.lz_mtp_prefill(C.byref(self.m), C.byref(self.s), _fp(h), _ip(nt), len(nt), int(pos0))
+
+    def spec_round(self, anchor, anchor_pos, k, p_min=0.0, n_min=0, brk=0, skipc=0):
+        out = np.zeros(LZ_SPEC_K_MAX + 1, np.int32)
+        na, npos, ke = C.c_int(), C.c_int(), C.c_int()
+        err = C.create_string_buffer(256)
+        r = self.lib.lz_spec_round(C.byref(self.m), C.byref(self.s), int(anchor), int(anchor_pos), int(k),
+                                   float(p_min), int(n_min), None, brk, skipc, _ip(out), C.byref(na),
+                                   C.byref(npos), C.byref(ke), err, 256)
+        return r, out, na.value, npos.value, ke.value
+
+    def generate(self, prompt, k, n_new, temp=0.0, topp=1.0, seed=1):
+        prompt = np.ascontiguousarray(prompt, np.int32)
+        cap = n_new + LZ_SPEC_K_MAX + 2
+        toks = np.zeros(cap, np.int32)
+        ke = np.zeros(n_new + 8, np.int32)
+        na = np.zeros(n_new + 8, np.int32)
+        nr = C.c_int()
+        samp = None
+        if temp > 0.0:
+            p = LZSampleParams()
+            self.lib.lz_sample_defaults(C.byref(p))
+            p.temperature, p.topp, p.topk, p.minp = temp, topp, 0, 0.0
+            p.presence_penalty, p.frequency_penalty, p.repetition_penalty, p.repeat_last_n = 0.0, 0.0, 1.0, 0
+            samp = LZSampler()
+            self.lib.lz_sampler_init(C.byref(samp), self.V, C.byref(p), seed)
+        n = self.lib.l98_generate(C.byref(self.m), C.byref(self.s), _ip(prompt), len(prompt), k, n_new,
+                                  C.byref(samp) if samp is not None else None, _ip(toks), cap, _ip(ke),
+                                  _ip(na), C.byref(nr))
+        if n < 0:
+            raise RuntimeError(f"l98_generate failed: {n}")
+        return toks[:min(n, cap)], ke[:nr.value], na[:nr.value]

@@ -1,0 +1,97 @@
+// Device-side argument blocks shared by the kernels and the host engine.
+#ifndef L98_DEV_H
+#define L98_DEV_H
+#include <stddef.h>
+#include <stdint.h>
+
+#define MAX_GEMV_JOBS 8
+#define MAX_EXPERTS 128
+#define MAX_TOPK 8
+#define MAX_CHUNK 8          // tokens per forward chunk (the reference's LZ_BATCH_MAX)
+#define MAX_PAIRS (MAX_CHUNK * MAX_TOPK)
+
+// One weight matrix of a fused GEMV launch.  All jobs of a launch share the
+// input width; activations default to the launch's xq/xqs unless a job
+// brings its own.
+typedef struct {
+    const int8_t *w;         // [rows][in] int8, row-major
+    const float *ws;         // [rows] per-row scale
+    float *out;              // out[t * out_stride + row]
+    const int8_t *xq;        // optional per-job activations [M][in]
+    const float *xqs;        // optional per-job scales [M][in/32]
+    const int *count;        // optional device flag: skip the job when *count <= 0
+    int32_t *acc_out;        // optional exact group sums [M][rows][in/32] (tests)
+    int rows;
+    int out_stride;
+    int tile0;               // first tile of this job in the launch grid (set by the launcher)
+    int pad;
+} GemvJob;
+
+typedef struct {
+    GemvJob job[MAX_GEMV_JOBS];
+    int n;
+} GemvBatch;
+
+// All experts of one projection (w1, w2 or w3) of a layer, stacked:
+// expert e occupies rows [e*out_rows, (e+1)*out_rows).
+typedef struct {
+    const int8_t *q;
+    const float *s;
+} ExpertBank;
+
+// Distinct experts selected by a chunk and their (token, slot) members.
+typedef struct {
+    int n_groups;
+    int expert[MAX_PAIRS];
+    int n_members[MAX_PAIRS];
+    int member[MAX_PAIRS][MAX_CHUNK];   // pair index t*topk + slot
+    int pair_token[MAX_PAIRS];
+} MoeGroups;
+
+// Per-round control block in device memory.  The host seeds it; the
+// draft/verify/accept kernels read and update it, so a round needs no host
+// round trip and can be captured as a graph.
+typedef struct {
+    int anchor, anchor_pos, mtp_pos, slot_base;
+    int k_eff, n_accept, new_pos, ssm_slot;
+    int catch_n, catch_pos, mtp_pos_next, pos_scratch;
+    int tok[16];             // tok[0] = anchor, tok[1..k] = drafts
+    int targ[16];            // verify argmaxes (targ[k_eff] = bonus)
+    int out[16];             // accepted tokens of the round
+    int catch_tok[16];
+    int pad[16];
+} DevCtl;
+
+typedef struct {
+    const float *qc, *kc, *vc;          // conv outputs [nt][key|key|value]
+    const float *gate_pre;              // f_b outputs [nt][nv*kd]
+    const float *bvec;                  // b projection [nt][nv]
+    const float *gz;                    // g projection [nt][value]
+    const float *a_log, *dt_bias, *o_norm;
+    float *state;                       // layer's head block inside slot 0
+    size_t slot_stride;                 // floats between ring slots
+    const int *ctl_slot;
+    float *raw_out;                     // optional recurrence output (tests)
+    float *normed_out;                  // optional gated-norm output (tests)
+    int8_t *xq;                         // o_proj activations [nt][value]
+    float *xqs;
+    int nk, nv, key, value, depth, advance, nt;
+    float scale, eps;
+} KdaRecurArgs;
+
+typedef struct {
+    const float *qg;                    // [nt][qg_dim] interleaved per head [q | gate]
+    const float *kp, *vp;               // [nt][kv_dim] projections
+    const float *q_norm, *k_norm;
+    const float *rope_cs;               // [seq][rot/2][2]
+    float *qh;                          // [nt][q_dim] normed + rotated q
+    int8_t *kcache, *vcache;            // plane base [seq][kv_dim]
+    float *kscale, *vscale;             // plane base [seq][kv_dim/32]
+    float *out;                         // [nt][q_dim] gated attention output
+    const int *ctl_pos;                 // position of token 0 = *ctl_pos + pos_off
+    int pos_off;
+    int nh, nkv, hd, rot, q_dim, qg_dim, kv_dim, kv_only;
+    float eps, attn_scale;
+} AttnArgs;
+
+#endif

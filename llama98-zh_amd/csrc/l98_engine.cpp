@@ -1,0 +1,1542 @@
+// Host engine of the MI355X MTP speculative-decoding path: model upload,
+// run state, the forward passes (capture / batch capture / verify), the MTP
+// draft step and prefill, the greedy and temperature rounds, and the C ABI
+// of include/llama98_hip.h.  All arithmetic runs in the kernels of
+// l98_kernels.hip; this file only schedules them on one HIP stream.
+//
+// Reference call structure (paths into the reference tree):
+//   forward_chunk          src/forward.c:1210-1617
+//   lz_forward_verify      src/forward.c:1774-1808
+//   lz_mtp_draft_step      src/forward_mtp.c:32-144
+//   lz_mtp_prefill/catchup src/forward_mtp.c:561-642
+//   lz_spec_round(_temp)   src/generate.c:694-994, 1234-1377
+
+#include <hip/hip_runtime.h>
+
+#include <fcntl.h>
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <vector>
+
+#include "../../include/llama98_hip.h"
+#include "l98_dev.h"
+#include "mathf.h"
+
+// ------------------------------------------------------ kernel launchers ---
+extern "C" {
+int l98k_upload_exp_table(const float *tab);
+int l98k_gemv(GemvBatch *b, const int8_t *xq, const float *xqs, int in_dim, int m, hipStream_t st);
+int l98k_expert_gemv(const ExpertBank *bank, const MoeGroups *grp, int max_groups, const int8_t *xq,
+                     const float *xqs, int xq_by_pair, float *out, int in_dim, int out_rows, int m,
+                     hipStream_t st);
+int l98k_embed(const int8_t *q, const float *s, const int *toks, int d, int nt, float *x,
+               hipStream_t st);
+int l98k_rmsnorm(float *x, int x_stride, const float *a, const float *b, const float *w, int n,
+                 float eps, int rows, float *out, int out_stride, int8_t *xq, float *xqs,
+                 hipStream_t st);
+int l98k_quant_rows(const float *x, int n, int x_stride, int rows, int8_t *xq, float *xqs,
+                    hipStream_t st);
+int l98k_act_quant(const float *h1, const float *h3, int n, int rows, const int *count, int8_t *xq,
+                   float *xqs, float *g_out, hipStream_t st);
+int l98k_kda_conv(const float *pq, const float *pk, const float *pv, int key, int value,
+                  const float *wconv, float *ring, size_t slot_stride, int K, const int *ctl_slot,
+                  int depth, int advance, int nt, float *qc, float *kc, float *vc, hipStream_t st);
+int l98k_kda_recur(const KdaRecurArgs *a, int kd, int vd, hipStream_t st);
+int l98k_attn_prep(const AttnArgs *a, int nt, hipStream_t st);
+int l98k_attn_decode(const AttnArgs *a, int nt, int max_len, hipStream_t st);
+int l98k_moe_route(const float *logits, const float *bias, int E, int topk, int nt, int *sel_idx,
+                   float *sel_w, MoeGroups *grp, hipStream_t st);
+int l98k_moe_combine(const float *h2, const int *sel_idx, const float *sel_w, int topk, int lat,
+                     int nt, float *lat_y, int8_t *xq, float *xqs, hipStream_t st);
+int l98k_argmax(const float *x, int n, int rows, int mode, int *out, hipStream_t st);
+int l98k_accept(DevCtl *ctl, const float *vhidden, int d, float *chain, int depth, int brk,
+                hipStream_t st);
+int l98k_set_tokens(DevCtl *ctl, int op, hipStream_t st);
+}
+
+#define CK(x)                                                                   \
+    do {                                                                        \
+        int _e = (int)(x);                                                      \
+        if (_e != 0) {                                                          \
+            fprintf(stderr, "l98: %s failed (%d) at %s:%d\n", #x, _e, __FILE__, \
+                    __LINE__);                                                  \
+            return 1;                                                           \
+        }                                                                       \
+    } while (0)
+
+static void set_err(char *buf, int len, const char *fmt, ...) {
+    if (!buf || len <= 0) return;
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, (size_t)len, fmt, ap);
+    va_end(ap);
+}
+
+// ------------------------------------------------------------- model ---
+
+struct DMat {
+    int8_t *q = nullptr;
+    float *s = nullptr;
+    int rows = 0, cols = 0;
+};
+
+struct DLayer {
+    int type = 0;
+    float *in_norm = nullptr, *post_norm = nullptr;
+    DMat q, k, v, o;
+    float *q_norm = nullptr, *k_norm = nullptr;
+    DMat kq, kk, kv, fa, fb, kb, kg, ko;
+    float *conv = nullptr, *a_log = nullptr, *dt_bias = nullptr, *o_norm = nullptr;
+    DMat router, down, up, sg, su, sd;
+    float *bias = nullptr;
+    ExpertBank w1{}, w2{}, w3{};
+};
+
+struct DModel {
+    LZModelConfig c{};
+    char *arena = nullptr;
+    size_t arena_size = 0, arena_used = 0;
+    DMat embed;
+    float *final_norm = nullptr;
+    std::vector<DLayer> L;
+    DLayer mtp;
+    DMat mtp_gate, mtp_up, mtp_down, mtp_fc;
+    float *mtp_norm = nullptr, *mtp_pre_h = nullptr, *mtp_pre_e = nullptr;
+    float *rope_cs = nullptr;
+    int lin_index[128], full_index[128];
+};
+
+namespace {
+
+// Sequential reader over the mmapped model.bin.
+struct Bin {
+    const unsigned char *p = nullptr;
+    size_t n = 0, off = 0;
+    bool bad = false;
+    const void *take(size_t b) {
+        if (bad || off + b > n) { bad = true; return nullptr; }
+        const void *r = p + off;
+        off += b;
+        return r;
+    }
+    int32_t i32() { const void *q = take(4); int32_t v = 0; if (q) memcpy(&v, q, 4); return v; }
+    float f32() { const void *q = take(4); float v = 0; if (q) memcpy(&v, q, 4); return v; }
+};
+
+struct HostTensor {
+    const int8_t *q = nullptr;
+    const float *s = nullptr;     // Q8 scales or F32 data
+    int rows = 0, cols = 0;
+    bool is_q8 = false;
+};
+
+HostTensor rd_q8(Bin &b, int rows, int cols) {
+    HostTensor t;
+    const unsigned char *dt = (const unsigned char *)b.take(1);
+    uint32_t n = (uint32_t)b.i32(), gs = (uint32_t)b.i32();
+    if (!dt || *dt != 1 || n != (uint32_t)rows * (uint32_t)cols || gs != (uint32_t)cols) {
+        b.bad = true;
+        return t;
+    }
+    t.q = (const int8_t *)b.take((size_t)rows * cols);
+    t.s = (const float *)b.take(sizeof(float) * (size_t)rows);
+    t.rows = rows; t.cols = cols; t.is_q8 = true;
+    return t;
+}
+
+HostTensor rd_f32(Bin &b, int n) {
+    HostTensor t;
+    const unsigned char *dt = (const unsigned char *)b.take(1);
+    uint32_t cnt = (uint32_t)b.i32();
+    if (!dt || *dt != 0 || cnt != (uint32_t)n) { b.bad = true; return t; }
+    t.s = (const float *)b.take(sizeof(float) * (size_t)n);
+    t.rows = 1; t.cols = n;
+    return t;
+}
+
+void *arena_take(DModel *m, size_t bytes) {
+    size_t a = (m->arena_used + 255) & ~(size_t)255;
+    if (a + bytes > m->arena_size) return nullptr;
+    m->arena_used = a + bytes;
+    return m->arena + a;
+}
+
+// Uploads go through the arena; on a counting pass (arena == null) they only
+// size it.
+struct Uploader {
+    DModel *m;
+    bool count;
+    size_t need = 0;
+    bool fail = false;
+    void *put(const void *src, size_t bytes) {
+        if (count) { need = ((need + 255) & ~(size_t)255) + bytes; return nullptr; }
+        void *d = arena_take(m, bytes);
+        if (!d || !src) { fail = true; return nullptr; }
+        if (hipMemcpy(d, src, bytes, hipMemcpyHostToDevice) != hipSuccess) fail = true;
+        return d;
+    }
+    DMat mat(const HostTensor &t) {
+        DMat d;
+        d.rows = t.rows; d.cols = t.cols;
+        d.q = (int8_t *)put(t.q, (size_t)t.rows * t.cols);
+        d.s = (float *)put(t.s, sizeof(float) * (size_t)t.rows);
+        return d;
+    }
+    float *vec(const HostTensor &t) { return (float *)put(t.s, sizeof(float) * (size_t)t.cols); }
+    // Stacks per-expert matrices of one projection into a bank.
+    ExpertBank bank(const std::vector<HostTensor> &ex) {
+        ExpertBank b{};
+        size_t rows = ex[0].rows, cols = ex[0].cols, E = ex.size();
+        if (count) {
+            put(nullptr, E * rows * cols);
+            put(nullptr, sizeof(float) * E * rows);
+            return b;
+        }
+        int8_t *q = (int8_t *)arena_take(m, E * rows * cols);
+        float *s = (float *)arena_take(m, sizeof(float) * E * rows);
+        if (!q || !s) { fail = true; return b; }
+        for (size_t e = 0; e < E; e++) {
+            if (hipMemcpy(q + e * rows * cols, ex[e].q, rows * cols, hipMemcpyHostToDevice) != hipSuccess ||
+                hipMemcpy(s + e * rows, ex[e].s, sizeof(float) * rows, hipMemcpyHostToDevice) != hipSuccess)
+                fail = true;
+        }
+        b.q = q; b.s = s;
+        return b;
+    }
+};
+
+struct HostLayer {
+    int type = 0;
+    HostTensor in_norm, post_norm, q, k, v, o, q_norm, k_norm;
+    HostTensor kq, kk, kv, convq, convk, convv, a_log, fa, fb, dt_bias, kb, kg, o_norm, ko;
+    HostTensor router, bias, down, up, sg, su, sd;
+    std::vector<HostTensor> w1, w2, w3;
+};
+
+// Parses the version-5 model.bin (reference loader order: header
+// src/model.c:3993-4200, tensors model_walk src/model.c:2240-2625).
+int parse_model(Bin &b, LZModelConfig &c, HostTensor &embed, HostTensor &fnorm,
+                std::vector<HostLayer> &L, HostLayer &mtp, HostTensor &mg, HostTensor &mu,
+                HostTensor &md, HostTensor &fc, HostTensor &mn, HostTensor &mph, HostTensor &mpe,
+                char *err, int errlen) {
+    const void *magic = b.take(4);
+    if (!magic || memcmp(magic, "L98Z", 4) != 0) { set_err(err, errlen, "bad magic"); return LZ_ERR_BIN_MAGIC; }
+    int ver = b.i32();
+    if (ver != 5) { set_err(err, errlen, "unsupported model.bin version %d", ver); return LZ_ERR_BIN_VERSION; }
+    c.vocab_size = b.i32(); c.hidden_size = b.i32(); c.n_layers = b.i32(); c.seq_len = b.i32();
+    c.n_heads = b.i32(); c.n_kv_heads = b.i32(); c.head_dim = b.i32(); (void)b.i32();
+    c.lin_n_k_heads = b.i32(); c.lin_n_v_heads = b.i32(); c.lin_k_head_dim = b.i32();
+    c.lin_v_head_dim = b.i32(); c.conv_kernel = b.i32(); c.n_linear_layers = b.i32();
+    c.n_full_layers = b.i32(); (void)b.i32(); (void)b.i32(); (void)b.i32();
+    c.rms_norm_eps = b.f32(); c.rope_theta = b.f32(); (void)b.f32();
+    c.attn_q_dim = b.i32(); c.attn_qgate_dim = b.i32(); c.attn_kv_dim = b.i32();
+    c.lin_key_dim = b.i32(); c.lin_value_dim = b.i32(); c.lin_conv_dim = b.i32();
+    c.rotary_dim = b.i32();
+    for (int i = 0; i < 128; i++) c.layer_types[i] = b.i32();
+    c.kda_gate_rank = b.i32();
+    int has_lb = b.i32(); (void)b.f32();
+    c.num_experts = b.i32(); c.num_experts_per_token = b.i32(); int n_shared = b.i32();
+    c.moe_intermediate_size = b.i32(); c.moe_latent_dim = b.i32();
+    int first_dense = b.i32(), renorm = b.i32(), sig = b.i32(), lat_norm = b.i32();
+    c.moe_shared_width = b.i32();
+    c.mtp_n_layers = b.i32(); c.mtp_intermediate_size = b.i32();
+    int rope_type = b.i32();
+    for (int i = 0; i < 4; i++) (void)b.i32();
+    int use_subn = b.i32();
+    for (int i = 0; i < 9; i++) (void)b.i32();    // hadamard x2, mla x2, kv_share, sink, gr, ced x2
+    for (int i = 0; i < 128 * 3 + 6 + 128; i++) (void)b.i32();
+    if (b.bad) { set_err(err, errlen, "truncated header"); return LZ_ERR_BIN_OPEN; }
+    // The variant this path implements (the synthetic configs): KDA + gated
+    // full attention, sigmoid latent MoE with a shared expert, one MTP layer.
+    if (has_lb || n_shared != 1 || first_dense != 0 || !renorm || !sig || lat_norm || use_subn ||
+        rope_type != 0 || c.mtp_n_layers != 1 || c.num_experts > MAX_EXPERTS ||
+        c.num_experts_per_token > MAX_TOPK || c.lin_n_k_heads != c.lin_n_v_heads ||
+        c.rotary_dim != c.head_dim || c.hidden_size % 32 || c.n_layers > 128) {
+        set_err(err, errlen, "model variant outside the implemented spec path");
+        return LZ_ERR_BIN_VERSION;
+    }
+    const int d = c.hidden_size;
+    embed = rd_q8(b, c.vocab_size, d);
+    fnorm = rd_f32(b, d);
+    L.resize(c.n_layers);
+    for (int l = 0; l < c.n_layers && !b.bad; l++) {
+        HostLayer &h = L[l];
+        h.type = c.layer_types[l];
+        h.in_norm = rd_f32(b, d);
+        h.post_norm = rd_f32(b, d);
+        if (h.type == 1) {
+            h.q = rd_q8(b, c.attn_qgate_dim, d);
+            h.k = rd_q8(b, c.attn_kv_dim, d);
+            h.v = rd_q8(b, c.attn_kv_dim, d);
+            h.o = rd_q8(b, d, c.attn_q_dim);
+            h.q_norm = rd_f32(b, c.head_dim);
+            h.k_norm = rd_f32(b, c.head_dim);
+        } else if (h.type == 2) {
+            int key = c.lin_key_dim, value = c.lin_value_dim, K = c.conv_kernel;
+            int nvk = c.lin_n_v_heads * c.lin_k_head_dim;
+            h.kq = rd_q8(b, key, d);
+            h.kk = rd_q8(b, key, d);
+            h.kv = rd_q8(b, value, d);
+            h.convq = rd_f32(b, key * K);
+            h.convk = rd_f32(b, key * K);
+            h.convv = rd_f32(b, value * K);
+            h.a_log = rd_f32(b, c.lin_n_v_heads);
+            h.fa = rd_q8(b, c.kda_gate_rank, d);
+            h.fb = rd_q8(b, nvk, c.kda_gate_rank);
+            h.dt_bias = rd_f32(b, nvk);
+            h.kb = rd_q8(b, c.lin_n_v_heads, d);
+            h.kg = rd_q8(b, value, d);
+            h.o_norm = rd_f32(b, c.lin_v_head_dim);
+            h.ko = rd_q8(b, d, value);
+        } else {
+            set_err(err, errlen, "layer %d: unsupported layer type %d", l, h.type);
+            return LZ_ERR_BIN_VERSION;
+        }
+        h.router = rd_q8(b, c.num_experts, d);
+        h.bias = rd_f32(b, c.num_experts);
+        h.down = rd_q8(b, c.moe_latent_dim, d);
+        h.up = rd_q8(b, d, c.moe_latent_dim);
+        h.sg = rd_q8(b, c.moe_shared_width, d);
+        h.su = rd_q8(b, c.moe_shared_width, d);
+        h.sd = rd_q8(b, d, c.moe_shared_width);
+        for (int e = 0; e < c.num_experts; e++) {
+            h.w1.push_back(rd_q8(b, c.moe_intermediate_size, c.moe_latent_dim));
+            h.w2.push_back(rd_q8(b, c.moe_latent_dim, c.moe_intermediate_size));
+            h.w3.push_back(rd_q8(b, c.moe_intermediate_size, c.moe_latent_dim));
+        }
+    }
+    mtp.type = 1;
+    mtp.in_norm = rd_f32(b, d);
+    mtp.post_norm = rd_f32(b, d);
+    mtp.q = rd_q8(b, c.attn_qgate_dim, d);
+    mtp.k = rd_q8(b, c.attn_kv_dim, d);
+    mtp.v = rd_q8(b, c.attn_kv_dim, d);
+    mtp.o = rd_q8(b, d, c.attn_q_dim);
+    mtp.q_norm = rd_f32(b, c.head_dim);
+    mtp.k_norm = rd_f32(b, c.head_dim);
+    mg = rd_q8(b, c.mtp_intermediate_size, d);
+    mu = rd_q8(b, c.mtp_intermediate_size, d);
+    md = rd_q8(b, d, c.mtp_intermediate_size);
+    fc = rd_q8(b, d, 2 * d);
+    mn = rd_f32(b, d);
+    mph = rd_f32(b, d);
+    mpe = rd_f32(b, d);
+    if (b.bad || b.off != b.n) { set_err(err, errlen, "model.bin layout mismatch"); return LZ_ERR_BIN_OPEN; }
+    return 0;
+}
+
+void upload_all(Uploader &u, DModel *m, const HostTensor &embed, const HostTensor &fnorm,
+                const std::vector<HostLayer> &HL, const HostLayer &hm, const HostTensor &mg,
+                const HostTensor &mu, const HostTensor &md, const HostTensor &fc,
+                const HostTensor &mn, const HostTensor &mph, const HostTensor &mpe) {
+    const LZModelConfig &c = m->c;
+    m->embed = u.mat(embed);
+    m->final_norm = u.vec(fnorm);
+    m->L.assign(c.n_layers, DLayer());
+    std::vector<float> conv;
+    for (int l = 0; l < c.n_layers; l++) {
+        const HostLayer &h = HL[l];
+        DLayer &D = m->L[l];
+        D.type = h.type;
+        D.in_norm = u.vec(h.in_norm);
+        D.post_norm = u.vec(h.post_norm);
+        if (h.type == 1) {
+            D.q = u.mat(h.q); D.k = u.mat(h.k); D.v = u.mat(h.v); D.o = u.mat(h.o);
+            D.q_norm = u.vec(h.q_norm); D.k_norm = u.vec(h.k_norm);
+        } else {
+            D.kq = u.mat(h.kq); D.kk = u.mat(h.kk); D.kv = u.mat(h.kv);
+            // conv taps of the [q | k | v] channels, one row of K per channel
+            conv.clear();
+            conv.insert(conv.end(), h.convq.s, h.convq.s + h.convq.cols);
+            conv.insert(conv.end(), h.convk.s, h.convk.s + h.convk.cols);
+            conv.insert(conv.end(), h.convv.s, h.convv.s + h.convv.cols);
+            D.conv = (float *)u.put(conv.data(), sizeof(float) * conv.size());
+            D.a_log = u.vec(h.a_log);
+            D.fa = u.mat(h.fa); D.fb = u.mat(h.fb);
+            D.dt_bias = u.vec(h.dt_bias);
+            D.kb = u.mat(h.kb); D.kg = u.mat(h.kg);
+            D.o_norm = u.vec(h.o_norm);
+            D.ko = u.mat(h.ko);
+        }
+        D.router = u.mat(h.router);
+        D.bias = u.vec(h.bias);
+        D.down = u.mat(h.down); D.up = u.mat(h.up);
+        D.sg = u.mat(h.sg); D.su = u.mat(h.su); D.sd = u.mat(h.sd);
+        D.w1 = u.bank(h.w1); D.w2 = u.bank(h.w2); D.w3 = u.bank(h.w3);
+    }
+    DLayer &M = m->mtp;
+    M.type = 1;
+    M.in_norm = u.vec(hm.in_norm); M.post_norm = u.vec(hm.post_norm);
+    M.q = u.mat(hm.q); M.k = u.mat(hm.k); M.v = u.mat(hm.v); M.o = u.mat(hm.o);
+    M.q_norm = u.vec(hm.q_norm); M.k_norm = u.vec(hm.k_norm);
+    m->mtp_gate = u.mat(mg); m->mtp_up = u.mat(mu); m->mtp_down = u.mat(md); m->mtp_fc = u.mat(fc);
+    m->mtp_norm = u.vec(mn); m->mtp_pre_h = u.vec(mph); m->mtp_pre_e = u.vec(mpe);
+    {
+        std::vector<float> cs((size_t)c.seq_len * c.rotary_dim);
+        l98_rope_table(cs.data(), c.seq_len, c.rotary_dim, c.rope_theta);
+        m->rope_cs = (float *)u.put(cs.data(), sizeof(float) * cs.size());
+    }
+}
+
+bool g_tables_ready = false;
+int ensure_tables() {
+    if (g_tables_ready) return 0;
+    float tab[32];
+    for (int i = 0; i < 32; i++) tab[i] = (float)exp2((double)i / 32.0);   // 2^(i/32), src/ops_quant.c:244
+    if (l98k_upload_exp_table(tab) != 0) return 1;
+    g_tables_ready = true;
+    return 0;
+}
+
+}  // namespace
+
+extern "C" int lz_open(LZModel *m, const char *dir, char *errbuf, int errlen) {
+    if (!m || !dir) { set_err(errbuf, errlen, "null argument"); return 1; }
+    memset(m, 0, sizeof(*m));
+    if (errbuf && errlen > 0) errbuf[0] = 0;
+    char path[1024];
+    snprintf(path, sizeof path, "%s/model.bin", dir);
+    int fd = open(path, O_RDONLY);
+    if (fd < 0) { set_err(errbuf, errlen, "cannot open %s", path); return 1; }
+    struct stat st;
+    if (fstat(fd, &st) != 0 || st.st_size < 8) { close(fd); set_err(errbuf, errlen, "empty %s", path); return 1; }
+    void *map = mmap(nullptr, (size_t)st.st_size, PROT_READ, MAP_PRIVATE, fd, 0);
+    close(fd);
+    if (map == MAP_FAILED) { set_err(errbuf, errlen, "mmap %s failed", path); return 1; }
+    Bin b;
+    b.p = (const unsigned char *)map;
+    b.n = (size_t)st.st_size;
+    DModel *dm = new DModel();
+    HostTensor embed, fnorm, mg, mu, md, fc, mn, mph, mpe;
+    std::vector<HostLayer> HL;
+    HostLayer hm;
+    int rc = parse_model(b, dm->c, embed, fnorm, HL, hm, mg, mu, md, fc, mn, mph, mpe, errbuf, errlen);
+    if (rc == 0 && ensure_tables() != 0) { set_err(errbuf, errlen, "HIP device not usable"); rc = 1; }
+    if (rc == 0) {
+        Uploader cnt{dm, true};
+        upload_all(cnt, dm, embed, fnorm, HL, hm, mg, mu, md, fc, mn, mph, mpe);
+        dm->arena_size = cnt.need + 4096;
+        if (hipMalloc((void **)&dm->arena, dm->arena_size) != hipSuccess) {
+            set_err(errbuf, errlen, "hipMalloc of %zu weight bytes failed", dm->arena_size);
+            rc = 1;
+        } else {
+            Uploader up{dm, false};
+            upload_all(up, dm, embed, fnorm, HL, hm, mg, mu, md, fc, mn, mph, mpe);
+            if (up.fail) { set_err(errbuf, errlen, "weight upload failed"); rc = 1; }
+        }
+    }
+    munmap(map, (size_t)st.st_size);
+    if (rc != 0) {
+        if (dm->arena) (void)hipFree(dm->arena);
+        delete dm;
+        return 1;
+    }
+    int li = 0, fi = 0;
+    for (int l = 0; l < dm->c.n_layers; l++) {
+        if (dm->c.layer_types[l] == 1) { dm->full_index[l] = fi++; dm->lin_index[l] = -1; }
+        else { dm->lin_index[l] = li++; dm->full_index[l] = -1; }
+    }
+    m->config = dm->c;
+    m->bytes_device = (long long)dm->arena_used;
+    m->impl = dm;
+    return 0;
+}
+
+extern "C" void lz_free(LZModel *m) {
+    if (!m || !m->impl) return;
+    DModel *dm = (DModel *)m->impl;
+    if (dm->arena) (void)hipFree(dm->arena);
+    delete dm;
+    m->impl = nullptr;
+}
+
+// ------------------------------------------------------------- state ---
+
+struct DState {
+    const DModel *m = nullptr;
+    hipStream_t st = nullptr;
+    int seq_len = 0, depth = 1, planes = 0;
+    size_t kda_slot = 0, conv_slot = 0;     // floats per ring slot
+    char *arena = nullptr;
+    size_t arena_size = 0, arena_used = 0;
+    float *kda = nullptr, *conv = nullptr;
+    int8_t *kq = nullptr, *vq = nullptr;
+    float *ks = nullptr, *vs = nullptr;
+    // activations
+    float *x, *e, *concat, *mtp_x, *chain, *blk, *up_out, *sd_out;
+    float *qg, *kp, *vp, *qh, *ao;
+    float *pq, *pk, *pv, *pfa, *pb, *pg, *qc, *kc, *vc, *gate_pre;
+    float *rl, *latx, *sgo, *suo, *h1, *h3, *h2, *hb, *hb2, *ffn_out;
+    float *vhidden, *mtp_logits, *logits, *draft_logits, *hcap;
+    int8_t *xq, *xq2, *xq3;
+    float *xqs, *xqs2, *xqs3;
+    int *sel_idx;
+    float *sel_w;
+    MoeGroups *grp;
+    DevCtl *ctl;
+    int *tokbuf;
+    DevCtl *ctl_pinned = nullptr;
+    int cap_rows = 0;                       // rows of hcap / tokbuf
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+};
+
+namespace {
+
+void *st_take(DState *s, size_t bytes) {
+    size_t a = (s->arena_used + 255) & ~(size_t)255;
+    if (s->arena && a + bytes > s->arena_size) return nullptr;
+    s->arena_used = a + bytes;
+    return s->arena ? s->arena + a : nullptr;
+}
+
+// Two passes: size, then carve.
+bool carve(DState *s) {
+    const LZModelConfig &c = s->m->c;
+    const int d = c.hidden_size, B = MAX_CHUNK;
+    int wide = d;
+    int dims[] = {2 * d, c.attn_qgate_dim, c.lin_conv_dim, c.moe_shared_width, c.mtp_intermediate_size,
+                  c.lin_n_v_heads * c.lin_k_head_dim, c.moe_intermediate_size, c.lin_value_dim};
+    for (int v : dims) wide = v > wide ? v : wide;
+    const int pairs = B * c.num_experts_per_token;
+    auto F = [&](size_t n) { return (float *)st_take(s, n * sizeof(float)); };
+    auto I8 = [&](size_t n) { return (int8_t *)st_take(s, n); };
+    s->kda = F(s->kda_slot * s->depth);
+    s->conv = F(s->conv_slot * s->depth);
+    size_t kv = (size_t)s->planes * s->seq_len * c.attn_kv_dim;
+    s->kq = I8(kv); s->vq = I8(kv);
+    s->ks = F(kv / 32); s->vs = F(kv / 32);
+    s->x = F((size_t)B * d); s->e = F((size_t)B * d); s->concat = F((size_t)B * 2 * d);
+    s->mtp_x = F((size_t)B * d); s->chain = F(d); s->blk = F((size_t)B * d);
+    s->up_out = F((size_t)B * d); s->sd_out = F((size_t)B * d);
+    s->qg = F((size_t)B * c.attn_qgate_dim); s->kp = F((size_t)B * c.attn_kv_dim);
+    s->vp = F((size_t)B * c.attn_kv_dim); s->qh = F((size_t)B * c.attn_q_dim);
+    s->ao = F((size_t)B * c.attn_q_dim);
+    s->pq = F((size_t)B * c.lin_key_dim); s->pk = F((size_t)B * c.lin_key_dim);
+    s->pv = F((size_t)B * c.lin_value_dim); s->pfa = F((size_t)B * c.kda_gate_rank);
+    s->pb = F((size_t)B * c.lin_n_v_heads); s->pg = F((size_t)B * c.lin_value_dim);
+    s->qc = F((size_t)B * c.lin_key_dim); s->kc = F((size_t)B * c.lin_key_dim);
+    s->vc = F((size_t)B * c.lin_value_dim);
+    s->gate_pre = F((size_t)B * c.lin_n_v_heads * c.lin_k_head_dim);
+    s->rl = F((size_t)B * c.num_experts); s->latx = F((size_t)B * c.moe_latent_dim);
+    s->sgo = F((size_t)B * c.moe_shared_width); s->suo = F((size_t)B * c.moe_shared_width);
+    s->h1 = F((size_t)pairs * c.moe_intermediate_size); s->h3 = F((size_t)pairs * c.moe_intermediate_size);
+    s->h2 = F((size_t)pairs * c.moe_latent_dim);
+    s->hb = F((size_t)B * c.mtp_intermediate_size); s->hb2 = F((size_t)B * c.mtp_intermediate_size);
+    s->ffn_out = F((size_t)B * d);
+    s->vhidden = F((size_t)(LZ_SPEC_K_MAX + 2) * d);
+    s->mtp_logits = F((size_t)(LZ_SPEC_K_MAX + 2) * c.vocab_size);
+    s->logits = F(c.vocab_size);
+    s->draft_logits = F((size_t)LZ_SPEC_K_MAX * c.vocab_size);
+    s->hcap = F((size_t)s->cap_rows * d);
+    s->xq = I8((size_t)pairs * wide); s->xqs = F((size_t)pairs * wide / 32);
+    s->xq2 = I8((size_t)pairs * wide); s->xqs2 = F((size_t)pairs * wide / 32);
+    s->xq3 = I8((size_t)pairs * wide); s->xqs3 = F((size_t)pairs * wide / 32);
+    s->sel_idx = (int *)st_take(s, sizeof(int) * pairs);
+    s->sel_w = F(pairs);
+    s->grp = (MoeGroups *)st_take(s, sizeof(MoeGroups));
+    s->ctl = (DevCtl *)st_take(s, sizeof(DevCtl));
+    s->tokbuf = (int *)st_take(s, sizeof(int) * (size_t)s->cap_rows);
+    return true;
+}
+
+DState *S(LZRunState *s) { return (DState *)s->impl; }
+const DModel *Mo(const LZModel *m) { return (const DModel *)m->impl; }
+
+int gemv(DState *s, std::initializer_list<GemvJob> jobs, const int8_t *xq, const float *xqs,
+         int in_dim, int mtok) {
+    GemvBatch b{};
+    b.n = 0;
+    for (const GemvJob &j : jobs) b.job[b.n++] = j;
+    return l98k_gemv(&b, xq, xqs, in_dim, mtok, s->st);
+}
+
+GemvJob J(const DMat &w, float *out, int out_stride) {
+    GemvJob j{};
+    j.w = w.q; j.ws = w.s; j.out = out; j.rows = w.rows; j.out_stride = out_stride;
+    return j;
+}
+
+// Writes host values into the device control block (pageable source: the
+// copy is staged at call time, so the host struct may change right after).
+int ctl_put(DState *s, const DevCtl &h) {
+    CK(hipMemcpyAsync(s->ctl, &h, sizeof(DevCtl), hipMemcpyHostToDevice, s->st));
+    return 0;
+}
+int ctl_get(DState *s, DevCtl *h) {
+    CK(hipMemcpyAsync(s->ctl_pinned, s->ctl, sizeof(DevCtl), hipMemcpyDeviceToHost, s->st));
+    CK(hipStreamSynchronize(s->st));
+    *h = *s->ctl_pinned;
+    return 0;
+}
+
+// ---------------------------------------------------------- layers ---
+
+// Attention block: input quantized in xq (rows nt), output xb2 -> s->blk.
+int attn_block(DState *s, const DLayer &L, int plane, const int *ctl_pos, int pos_off, int nt,
+               int max_pos, bool kv_only) {
+    const LZModelConfig &c = s->m->c;
+    const int d = c.hidden_size;
+    if (kv_only)
+        CK(gemv(s, {J(L.k, s->kp, c.attn_kv_dim), J(L.v, s->vp, c.attn_kv_dim)}, s->xq, s->xqs, d, nt));
+    else
+        CK(gemv(s, {J(L.k, s->kp, c.attn_kv_dim), J(L.v, s->vp, c.attn_kv_dim),
+                    J(L.q, s->qg, c.attn_qgate_dim)}, s->xq, s->xqs, d, nt));
+    AttnArgs a{};
+    a.qg = s->qg; a.kp = s->kp; a.vp = s->vp;
+    a.q_norm = L.q_norm; a.k_norm = L.k_norm; a.rope_cs = s->m->rope_cs;
+    a.qh = s->qh;
+    size_t off = (size_t)plane * s->seq_len * c.attn_kv_dim;
+    a.kcache = s->kq + off; a.vcache = s->vq + off;
+    a.kscale = s->ks + off / 32; a.vscale = s->vs + off / 32;
+    a.out = s->ao;
+    a.ctl_pos = ctl_pos; a.pos_off = pos_off;
+    a.nh = c.n_heads; a.nkv = c.n_kv_heads; a.hd = c.head_dim; a.rot = c.rotary_dim;
+    a.q_dim = c.attn_q_dim; a.qg_dim = c.attn_qgate_dim; a.kv_dim = c.attn_kv_dim;
+    a.kv_only = kv_only ? 1 : 0;
+    a.eps = c.rms_norm_eps;
+    // attn_scale = lz_rsqrt(head_dim) (src/forward_state.c:1408), float body
+    {
+        float x = (float)c.head_dim, h = 0.5f * x, y;
+        uint32_t u;
+        memcpy(&u, &x, 4);
+        u = 0x5f375a86u - (u >> 1);
+        memcpy(&y, &u, 4);
+        y = y * (1.5f - h * y * y);
+        y = y * (1.5f - h * y * y);
+        a.attn_scale = y;
+    }
+    CK(l98k_attn_prep(&a, nt, s->st));
+    if (kv_only) return 0;
+    CK(l98k_attn_decode(&a, nt, max_pos + 1, s->st));
+    CK(l98k_quant_rows(s->ao, c.attn_q_dim, c.attn_q_dim, nt, s->xq2, s->xqs2, s->st));
+    CK(gemv(s, {J(L.o, s->blk, d)}, s->xq2, s->xqs2, c.attn_q_dim, nt));
+    return 0;
+}
+
+float ssm_scale(int kd) {   // lz_rsqrt(lin_k_head_dim), src/forward_state.c:1409
+    float x = (float)kd, h = 0.5f * x, y;
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    u = 0x5f375a86u - (u >> 1);
+    memcpy(&y, &u, 4);
+    y = y * (1.5f - h * y * y);
+    y = y * (1.5f - h * y * y);
+    return y;
+}
+
+// KDA block: input quantized in xq, output -> s->blk.
+int kda_block(DState *s, const DLayer &L, int li, int nt, int advance) {
+    const LZModelConfig &c = s->m->c;
+    const int d = c.hidden_size, key = c.lin_key_dim, value = c.lin_value_dim;
+    const int nv = c.lin_n_v_heads, kd = c.lin_k_head_dim, vd = c.lin_v_head_dim;
+    const int nvk = nv * kd;
+    CK(gemv(s, {J(L.kq, s->pq, key), J(L.kk, s->pk, key), J(L.kv, s->pv, value),
+                J(L.fa, s->pfa, c.kda_gate_rank), J(L.kb, s->pb, nv), J(L.kg, s->pg, value)},
+            s->xq, s->xqs, d, nt));
+    const int hist = c.conv_kernel - 1;
+    CK(l98k_kda_conv(s->pq, s->pk, s->pv, key, value, L.conv,
+                     s->conv + (size_t)li * c.lin_conv_dim * hist, s->conv_slot, c.conv_kernel,
+                     &s->ctl->slot_base, s->depth, advance, nt, s->qc, s->kc, s->vc, s->st));
+    CK(l98k_quant_rows(s->pfa, c.kda_gate_rank, c.kda_gate_rank, nt, s->xq2, s->xqs2, s->st));
+    CK(gemv(s, {J(L.fb, s->gate_pre, nvk)}, s->xq2, s->xqs2, c.kda_gate_rank, nt));
+    KdaRecurArgs a{};
+    a.qc = s->qc; a.kc = s->kc; a.vc = s->vc; a.gate_pre = s->gate_pre; a.bvec = s->pb; a.gz = s->pg;
+    a.a_log = L.a_log; a.dt_bias = L.dt_bias; a.o_norm = L.o_norm;
+    a.state = s->kda + (size_t)li * nv * kd * vd;
+    a.slot_stride = s->kda_slot;
+    a.ctl_slot = &s->ctl->slot_base;
+    a.xq = s->xq2; a.xqs = s->xqs2;
+    a.nk = c.lin_n_k_heads; a.nv = nv; a.key = key; a.value = value;
+    a.depth = s->depth; a.advance = advance; a.nt = nt;
+    a.scale = ssm_scale(kd); a.eps = c.rms_norm_eps;
+    CK(l98k_kda_recur(&a, kd, vd, s->st));
+    CK(gemv(s, {J(L.ko, s->blk, d)}, s->xq2, s->xqs2, value, nt));
+    return 0;
+}
+
+// MoE block: input quantized in xq; outputs up_out and sd_out (the caller's
+// next norm folds x += up_out + sd_out).
+int moe_block(DState *s, const DLayer &L, int nt) {
+    const LZModelConfig &c = s->m->c;
+    const int d = c.hidden_size, E = c.num_experts, topk = c.num_experts_per_token;
+    const int lat = c.moe_latent_dim, inter = c.moe_intermediate_size, sw = c.moe_shared_width;
+    CK(gemv(s, {J(L.router, s->rl, E), J(L.down, s->latx, lat), J(L.sg, s->sgo, sw), J(L.su, s->suo, sw)},
+            s->xq, s->xqs, d, nt));
+    CK(l98k_moe_route(s->rl, L.bias, E, topk, nt, s->sel_idx, s->sel_w, s->grp, s->st));
+    CK(l98k_quant_rows(s->latx, lat, lat, nt, s->xq2, s->xqs2, s->st));
+    int max_groups = nt * topk < E ? nt * topk : E;
+    CK(l98k_expert_gemv(&L.w1, s->grp, max_groups, s->xq2, s->xqs2, 0, s->h1, lat, inter, nt, s->st));
+    CK(l98k_expert_gemv(&L.w3, s->grp, max_groups, s->xq2, s->xqs2, 0, s->h3, lat, inter, nt, s->st));
+    CK(l98k_act_quant(s->h1, s->h3, inter, nt * topk, nullptr, s->xq3, s->xqs3, nullptr, s->st));
+    CK(l98k_expert_gemv(&L.w2, s->grp, max_groups, s->xq3, s->xqs3, 1, s->h2, inter, lat, nt, s->st));
+    CK(l98k_moe_combine(s->h2, s->sel_idx, s->sel_w, topk, lat, nt, nullptr, s->xq2, s->xqs2, s->st));
+    CK(gemv(s, {J(L.up, s->up_out, d)}, s->xq2, s->xqs2, lat, nt));
+    CK(l98k_act_quant(s->sgo, s->suo, sw, nt, nullptr, s->xq3, s->xqs3, nullptr, s->st));
+    CK(gemv(s, {J(L.sd, s->sd_out, d)}, s->xq3, s->xqs3, sw, nt));
+    return 0;
+}
+
+// forward_chunk (src/forward.c:1210-1617) for nt <= MAX_CHUNK tokens whose
+// ids are in device memory at toks, positions *ctl_pos + pos_off + t.
+//   capture:    device rows [nt][d] of the final-normed hidden, or null
+//   logits_out: device [nt][V] when all_logits, else the last row's logits
+//               go to s->logits unless skip_logits
+int forward_chunk(DState *s, const int *toks, int nt, const int *ctl_pos, int pos_off, int max_pos,
+                  float *capture, bool all_logits, float *logits_out, bool skip_logits) {
+    const DModel *m = s->m;
+    const LZModelConfig &c = m->c;
+    const int d = c.hidden_size;
+    const float eps = c.rms_norm_eps;
+    CK(l98k_embed(m->embed.q, m->embed.s, toks, d, nt, s->x, s->st));
+    const float *ra = nullptr, *rb = nullptr;     // pending residual of the previous block
+    for (int l = 0; l < c.n_layers; l++) {
+        const DLayer &L = m->L[l];
+        CK(l98k_rmsnorm(s->x, d, ra, rb, L.in_norm, d, eps, nt, nullptr, 0, s->xq, s->xqs, s->st));
+        if (L.type == 1) CK(attn_block(s, L, m->full_index[l], ctl_pos, pos_off, nt, max_pos, false));
+        else CK(kda_block(s, L, m->lin_index[l], nt, all_logits ? 1 : 0));
+        CK(l98k_rmsnorm(s->x, d, s->blk, nullptr, L.post_norm, d, eps, nt, nullptr, 0, s->xq, s->xqs, s->st));
+        CK(moe_block(s, L, nt));
+        ra = s->up_out;
+        rb = s->sd_out;
+    }
+    const bool want_logits = all_logits || !skip_logits;
+    CK(l98k_rmsnorm(s->x, d, ra, rb, m->final_norm, d, eps, nt, capture, d,
+                    want_logits ? s->xq : nullptr, s->xqs, s->st));
+    if (all_logits) {
+        CK(gemv(s, {J(m->embed, logits_out, c.vocab_size)}, s->xq, s->xqs, d, nt));
+    } else if (!skip_logits) {
+        CK(gemv(s, {J(m->embed, s->logits, c.vocab_size)}, s->xq + (size_t)(nt - 1) * d,
+                s->xqs + (size_t)(nt - 1) * (d / 32), d, 1));
+    }
+    return 0;
+}
+
+// lz_mtp_draft_step on device: input token at toks[0], position
+// *ctl_pos + pos_off; logits -> out_logits; argmax (lz_argmax_p1 order) ->
+// out_tok (device) when given.
+int draft_step(DState *s, const int *toks, const int *ctl_pos, int pos_off, int max_pos,
+               float *out_logits, int *out_tok) {
+    const DModel *m = s->m;
+    const LZModelConfig &c = m->c;
+    const int d = c.hidden_size;
+    const float eps = c.rms_norm_eps;
+    CK(l98k_embed(m->embed.q, m->embed.s, toks, d, 1, s->e, s->st));
+    CK(l98k_rmsnorm(s->e, d, nullptr, nullptr, m->mtp_pre_e, d, eps, 1, s->concat, 2 * d, nullptr, nullptr, s->st));
+    CK(l98k_rmsnorm(s->chain, d, nullptr, nullptr, m->mtp_pre_h, d, eps, 1, s->concat + d, 2 * d, nullptr, nullptr, s->st));
+    CK(l98k_quant_rows(s->concat, 2 * d, 2 * d, 1, s->xq, s->xqs, s->st));
+    CK(gemv(s, {J(m->mtp_fc, s->mtp_x, d)}, s->xq, s->xqs, 2 * d, 1));
+    CK(l98k_rmsnorm(s->mtp_x, d, nullptr, nullptr, m->mtp.in_norm, d, eps, 1, nullptr, 0, s->xq, s->xqs, s->st));
+    CK(attn_block(s, m->mtp, s->planes - 1, ctl_pos, pos_off, 1, max_pos, false));
+    CK(l98k_rmsnorm(s->mtp_x, d, s->blk, nullptr, m->mtp.post_norm, d, eps, 1, nullptr, 0, s->xq, s->xqs, s->st));
+    CK(gemv(s, {J(m->mtp_gate, s->hb, c.mtp_intermediate_size), J(m->mtp_up, s->hb2, c.mtp_intermediate_size)},
+            s->xq, s->xqs, d, 1));
+    CK(l98k_act_quant(s->hb, s->hb2, c.mtp_intermediate_size, 1, nullptr, s->xq2, s->xqs2, nullptr, s->st));
+    CK(gemv(s, {J(m->mtp_down, s->ffn_out, d)}, s->xq2, s->xqs2, c.mtp_intermediate_size, 1));
+    CK(l98k_rmsnorm(s->mtp_x, d, s->ffn_out, nullptr, m->mtp_norm, d, eps, 1, s->chain, d, s->xq, s->xqs, s->st));
+    CK(gemv(s, {J(m->embed, out_logits, c.vocab_size)}, s->xq, s->xqs, d, 1));
+    if (out_tok) CK(l98k_argmax(out_logits, c.vocab_size, 1, 1, out_tok, s->st));
+    return 0;
+}
+
+// MTP prefill/catch-up: K/V rows of the MTP plane from (hidden, next token)
+// pairs, chunked by MAX_CHUNK.  h: device rows [n][d]; toks: device ids;
+// positions *ctl_pos + pos_off + j.
+int mtp_prefill_dev(DState *s, const float *h, const int *toks, int n, const int *ctl_pos, int pos_off) {
+    const DModel *m = s->m;
+    const LZModelConfig &c = m->c;
+    const int d = c.hidden_size;
+    const float eps = c.rms_norm_eps;
+    for (int done = 0; done < n;) {
+        int k = n - done < MAX_CHUNK ? n - done : MAX_CHUNK;
+        CK(l98k_embed(m->embed.q, m->embed.s, toks + done, d, k, s->e, s->st));
+        CK(l98k_rmsnorm(s->e, d, nullptr, nullptr, m->mtp_pre_e, d, eps, k, s->concat, 2 * d, nullptr, nullptr, s->st));
+        CK(l98k_rmsnorm((float *)h + (size_t)done * d, d, nullptr, nullptr, m->mtp_pre_h, d, eps, k,
+                        s->concat + d, 2 * d, nullptr, nullptr, s->st));
+        CK(l98k_quant_rows(s->concat, 2 * d, 2 * d, k, s->xq, s->xqs, s->st));
+        CK(gemv(s, {J(m->mtp_fc, s->mtp_x, d)}, s->xq, s->xqs, 2 * d, k));
+        CK(l98k_rmsnorm(s->mtp_x, d, nullptr, nullptr, m->mtp.in_norm, d, eps, k, nullptr, 0, s->xq, s->xqs, s->st));
+        CK(attn_block(s, m->mtp, s->planes - 1, ctl_pos, pos_off + done, k, 0, true));
+        done += k;
+    }
+    return 0;
+}
+
+}  // namespace
+
+extern "C" int lz_state_alloc(LZRunState *s, const LZModel *mm, int seq_len, int spec_k_max,
+                              char *errbuf, int errlen) {
+    if (!s || !mm || !mm->impl) { set_err(errbuf, errlen, "null argument"); return 1; }
+    memset(s, 0, sizeof(*s));
+    const DModel *m = Mo(mm);
+    const LZModelConfig &c = m->c;
+    DState *d = new DState();
+    d->m = m;
+    d->seq_len = seq_len > 0 ? seq_len : c.seq_len;
+    if (d->seq_len > c.seq_len) d->seq_len = c.seq_len;   // the rope table covers the model's seq_len
+    d->depth = spec_k_max > 0 ? (spec_k_max + 1 > LZ_SPEC_K_MAX + 1 ? LZ_SPEC_K_MAX + 1 : spec_k_max + 1) : 1;
+    d->planes = c.n_full_layers + 1;
+    d->kda_slot = (size_t)c.n_linear_layers * c.lin_n_v_heads * c.lin_k_head_dim * c.lin_v_head_dim;
+    d->conv_slot = (size_t)c.n_linear_layers * c.lin_conv_dim * (c.conv_kernel - 1);
+    d->cap_rows = d->seq_len;
+    carve(d);                                   // sizing pass
+    d->arena_size = d->arena_used + 4096;
+    d->arena_used = 0;
+    if (hipMalloc((void **)&d->arena, d->arena_size) != hipSuccess) {
+        set_err(errbuf, errlen, "hipMalloc of %zu state bytes failed", d->arena_size);
+        delete d;
+        return 1;
+    }
+    carve(d);
+    if (hipStreamCreateWithFlags(&d->st, hipStreamNonBlocking) != hipSuccess ||
+        hipHostMalloc((void **)&d->ctl_pinned, sizeof(DevCtl), hipHostMallocDefault) != hipSuccess ||
+        hipEventCreate(&d->ev0) != hipSuccess || hipEventCreate(&d->ev1) != hipSuccess) {
+        set_err(errbuf, errlen, "HIP stream/event setup failed");
+        (void)hipFree(d->arena);
+        delete d;
+        return 1;
+    }
+    s->impl = d;
+    s->seq_len = d->seq_len;
+    s->ssm_ring_depth = d->depth;
+    s->nt_cap = 4;
+    s->bytes_device = (long long)d->arena_size;
+    s->logits = (float *)calloc((size_t)c.vocab_size, sizeof(float));
+    s->mtp_logits = (float *)calloc((size_t)(LZ_SPEC_K_MAX + 1) * c.vocab_size, sizeof(float));
+    s->mtp_verify_hidden = (float *)calloc((size_t)(LZ_SPEC_K_MAX + 1) * c.hidden_size, sizeof(float));
+    s->mtp_chain = (float *)calloc((size_t)c.hidden_size, sizeof(float));
+    s->mtp_draft_logits = (float *)calloc((size_t)c.vocab_size, sizeof(float));
+    lz_state_reset(s, mm);
+    return 0;
+}
+
+extern "C" void lz_state_free(LZRunState *s) {
+    if (!s) return;
+    DState *d = S(s);
+    if (d) {
+        if (d->st) (void)hipStreamSynchronize(d->st);
+        if (d->arena) (void)hipFree(d->arena);
+        if (d->ctl_pinned) (void)hipHostFree(d->ctl_pinned);
+        if (d->ev0) (void)hipEventDestroy(d->ev0);
+        if (d->ev1) (void)hipEventDestroy(d->ev1);
+        if (d->st) (void)hipStreamDestroy(d->st);
+        delete d;
+    }
+    free(s->logits); free(s->mtp_logits); free(s->mtp_verify_hidden);
+    free(s->mtp_chain); free(s->mtp_draft_logits);
+    memset(s, 0, sizeof(*s));
+}
+
+// lz_state_reset (src/forward.c:654-775): zero every state plane, slot 0,
+// mtp_pos 0.
+extern "C" void lz_state_reset(LZRunState *s, const LZModel *m) {
+    (void)m;
+    if (!s || !s->impl) return;
+    DState *d = S(s);
+    (void)hipMemsetAsync(d->arena, 0, d->arena_used, d->st);
+    (void)hipStreamSynchronize(d->st);
+    s->ssm_slot = 0;
+    s->mtp_pos = 0;
+    memset(s->mtp_chain, 0, sizeof(float) * (size_t)d->m->c.hidden_size);
+}
+
+// ---------------------------------------------------------- forward API ---
+
+namespace {
+
+bool tok_ok(const LZModelConfig &c, const int *t, int n) {
+    for (int i = 0; i < n; i++) if (t[i] < 0 || t[i] >= c.vocab_size) return false;
+    return true;
+}
+
+// Device-resident round state prepared from the host mirrors.
+DevCtl ctl_from(LZRunState *s) {
+    DevCtl h{};
+    h.mtp_pos = s->mtp_pos;
+    h.slot_base = s->ssm_slot;
+    h.ssm_slot = s->ssm_slot;
+    return h;
+}
+
+}  // namespace
+
+extern "C" float *lz_forward_capture(const LZModel *mm, LZRunState *s, int token, int pos) {
+    if (!mm || !s || !s->impl) return nullptr;
+    DState *d = S(s);
+    const LZModelConfig &c = d->m->c;
+    if (token < 0 || token >= c.vocab_size || pos < 0 || pos >= d->seq_len) return nullptr;
+    DevCtl h = ctl_from(s);
+    h.pos_scratch = pos;
+    h.tok[0] = token;
+    if (ctl_put(d, h)) return nullptr;
+    if (forward_chunk(d, d->ctl->tok, 1, &d->ctl->pos_scratch, 0, pos, d->chain, false, nullptr, false))
+        return nullptr;
+    if (hipMemcpyAsync(s->logits, d->logits, sizeof(float) * c.vocab_size, hipMemcpyDeviceToHost, d->st) ||
+        hipMemcpyAsync(s->mtp_chain, d->chain, sizeof(float) * c.hidden_size, hipMemcpyDeviceToHost, d->st) ||
+        hipStreamSynchronize(d->st))
+        return nullptr;
+    return s->logits;
+}
+
+namespace {
+int batch_capture_dev(DState *d, LZRunState *s, const int *tokens, int n, int pos0) {
+    const LZModelConfig &c = d->m->c;
+    DevCtl h = ctl_from(s);
+    h.pos_scratch = pos0;
+    CK(ctl_put(d, h));
+    CK(hipMemcpyAsync(d->tokbuf, tokens, sizeof(int) * (size_t)n, hipMemcpyHostToDevice, d->st));
+    for (int done = 0; done < n;) {
+        int k = n - done < MAX_CHUNK ? n - done : MAX_CHUNK;
+        CK(forward_chunk(d, d->tokbuf + done, k, &d->ctl->pos_scratch, done, pos0 + done + k - 1,
+                         d->hcap + (size_t)done * c.hidden_size, false, nullptr, true));
+        done += k;
+    }
+    return 0;
+}
+}  // namespace
+
+extern "C" float *lz_forward_batch_capture(const LZModel *mm, LZRunState *s, const int *tokens, int n,
+                                           int pos0, float *hidden_out) {
+    if (!mm || !s || !s->impl || !tokens || n < 1 || !hidden_out) return nullptr;
+    DState *d = S(s);
+    const LZModelConfig &c = d->m->c;
+    if (!tok_ok(c, tokens, n) || pos0 < 0 || pos0 + n > d->seq_len) return nullptr;
+    if (batch_capture_dev(d, s, tokens, n, pos0)) return nullptr;
+    if (hipMemcpyAsync(hidden_out, d->hcap, sizeof(float) * (size_t)n * c.hidden_size,
+                       hipMemcpyDeviceToHost, d->st) || hipStreamSynchronize(d->st))
+        return nullptr;
+    return s->logits;
+}
+
+extern "C" int lz_forward_verify(const LZModel *mm, LZRunState *s, const int *tokens, int n, int pos0) {
+    if (!mm || !s || !s->impl || !tokens || n < 1 || n > LZ_BATCH_MAX) return 1;
+    DState *d = S(s);
+    const LZModelConfig &c = d->m->c;
+    if (!tok_ok(c, tokens, n) || pos0 < 0 || pos0 + n > d->seq_len) return 1;
+    DevCtl h = ctl_from(s);
+    h.pos_scratch = pos0;
+    for (int i = 0; i < n; i++) h.tok[i] = tokens[i];
+    if (ctl_put(d, h)) return 1;
+    if (forward_chunk(d, d->ctl->tok, n, &d->ctl->pos_scratch, 0, pos0 + n - 1, d->vhidden, true,
+                      d->mtp_logits, false))
+        return 1;
+    s->ssm_slot = (s->ssm_slot + n) % d->depth;
+    if (hipMemcpyAsync(s->mtp_logits, d->mtp_logits, sizeof(float) * (size_t)n * c.vocab_size,
+                       hipMemcpyDeviceToHost, d->st) ||
+        hipMemcpyAsync(s->mtp_verify_hidden, d->vhidden, sizeof(float) * (size_t)n * c.hidden_size,
+                       hipMemcpyDeviceToHost, d->st) ||
+        hipStreamSynchronize(d->st))
+        return 1;
+    return 0;
+}
+
+extern "C" float *lz_mtp_draft_step(const LZModel *mm, LZRunState *s, int next_token, int pos) {
+    if (!mm || !s || !s->impl) return nullptr;
+    DState *d = S(s);
+    const LZModelConfig &c = d->m->c;
+    if (next_token < 0 || next_token >= c.vocab_size || pos < 0 || pos >= d->seq_len) return nullptr;
+    DevCtl h = ctl_from(s);
+    h.pos_scratch = pos;
+    h.tok[0] = next_token;
+    if (ctl_put(d, h)) return nullptr;
+    if (draft_step(d, d->ctl->tok, &d->ctl->pos_scratch, 0, pos, d->draft_logits, nullptr)) return nullptr;
+    if (hipMemcpyAsync(s->mtp_draft_logits, d->draft_logits, sizeof(float) * c.vocab_size,
+                       hipMemcpyDeviceToHost, d->st) ||
+        hipMemcpyAsync(s->mtp_chain, d->chain, sizeof(float) * c.hidden_size, hipMemcpyDeviceToHost, d->st) ||
+        hipStreamSynchronize(d->st))
+        return nullptr;
+    return s->mtp_draft_logits;
+}
+
+extern "C" int lz_mtp_prefill(const LZModel *mm, LZRunState *s, const float *h_body_all,
+                              const int *next_tokens, int n, int pos0) {
+    if (!mm || !s || !s->impl || !h_body_all || !next_tokens || n < 1) return 1;
+    DState *d = S(s);
+    const LZModelConfig &c = d->m->c;
+    if (!tok_ok(c, next_tokens, n) || pos0 < 0 || pos0 + n > d->seq_len || n > d->cap_rows) return 1;
+    DevCtl h = ctl_from(s);
+    h.pos_scratch = pos0;
+    if (ctl_put(d, h)) return 1;
+    if (hipMemcpyAsync(d->hcap, h_body_all, sizeof(float) * (size_t)n * c.hidden_size,
+                       hipMemcpyHostToDevice, d->st) ||
+        hipMemcpyAsync(d->tokbuf, next_tokens, sizeof(int) * (size_t)n, hipMemcpyHostToDevice, d->st))
+        return 1;
+    if (mtp_prefill_dev(d, d->hcap, d->tokbuf, n, &d->ctl->pos_scratch, 0)) return 1;
+    return hipStreamSynchronize(d->st) != hipSuccess;
+}
+
+extern "C" int lz_mtp_catchup(const LZModel *m, LZRunState *s, const float *h_body_all,
+                              const int *next_tokens, int n, int pos0) {
+    return lz_mtp_prefill(m, s, h_body_all, next_tokens, n, pos0);
+}
+
+// ------------------------------------------------- sampling (host side) ---
+
+static uint32_t rng_u32(lz_u64 *st) {          // xorshift64*, src/sampler.c:112-117
+    *st ^= *st >> 12;
+    *st ^= *st << 25;
+    *st ^= *st >> 27;
+    return (uint32_t)((*st * 0x2545F4914F6CDD1DULL) >> 32);
+}
+extern "C" float lz_random_f32(lz_u64 *state) {  // src/sampler.c:118-120
+    return (float)(rng_u32(state) >> 8) / 16777216.0f;
+}
+static uint32_t fkey_h(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    return u ^ ((uint32_t)((int32_t)u >> 31) | 0x80000000u);
+}
+extern "C" int lz_sample_argmax(const float *p, int n) {   // src/sampler.c:121-137
+    int bi = 0;
+    uint32_t best = fkey_h(p[0]);
+    for (int i = 1; i < n; i++) {
+        uint32_t k = fkey_h(p[i]);
+        if (k > best) { bi = i; best = k; }
+    }
+    return bi;
+}
+
+namespace {
+// Host copies of the float-tier exp for the sampler (same body as d_exp).
+float h_exp(float x) {
+    static float tab[32];
+    static bool ready = false;
+    if (!ready) { for (int i = 0; i < 32; i++) tab[i] = (float)exp2((double)i / 32.0); ready = true; }
+    const float C2 = 0.242844437f, C1 = 0.207425515f, C0 = 0.549730133f;
+    const float LOG2E32 = 1.44269504f * 32.0f;
+    if (x > 88.0f) return 3.40282347e+38f;
+    if (x < -87.3f) return 0.0f;
+    float y32 = x * LOG2E32;
+    volatile float m = (y32 - 0.5f) + 12582912.0f;
+    float mm = m;
+    uint32_t u;
+    memcpy(&u, &mm, 4);
+    int32_t t = (int32_t)(u & 0x007FFFFFu) - 0x00400000;
+    int32_t n = t >> 5, idx = t & 31;
+    float r = y32 - (float)t;
+    float w = 1.0f + r * 0.03125f;
+    uint32_t pb = (uint32_t)(n + 127) << 23;
+    float p2n;
+    memcpy(&p2n, &pb, 4);
+    float c = (C2 * w + C1) * w + C0;
+    return p2n * (tab[idx] * c);
+}
+void h_softmax(float *x, int n) {                // lz_softmax float tier, src/ops_norm.c:903-990
+    float mx = x[0], sum = 0.0f;
+    uint32_t best = fkey_h(mx);
+    for (int i = 1; i < n; i++) {
+        uint32_t k = fkey_h(x[i]);
+        if (k > best) { best = k; mx = x[i]; }
+    }
+    for (int i = 0; i < n; i++) { x[i] = h_exp(x[i] - mx); sum += x[i]; }
+    float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+    for (int i = 0; i < n; i++) x[i] *= inv;
+}
+int sample_mult(const float *p, int n, float coin) {   // src/sampler.c:159-167
+    float cdf = 0.0f;
+    for (int i = 0; i < n; i++) { cdf += p[i]; if (coin < cdf) return i; }
+    return n - 1;
+}
+struct PI { float prob; int index; };
+// select_all's descending sort (glibc qsort is a stable merge sort here):
+// stable by (prob desc, index asc).
+void sort_desc(std::vector<PI> &a) {
+    std::vector<PI> tmp(a.size());
+    size_t n = a.size();
+    for (size_t w = 1; w < n; w *= 2) {
+        for (size_t lo = 0; lo < n; lo += 2 * w) {
+            size_t mid = lo + w < n ? lo + w : n, hi = lo + 2 * w < n ? lo + 2 * w : n;
+            size_t i = lo, j = mid, k = lo;
+            while (i < mid && j < hi) tmp[k++] = (a[j].prob > a[i].prob) ? a[j++] : a[i++];
+            while (i < mid) tmp[k++] = a[i++];
+            while (j < hi) tmp[k++] = a[j++];
+        }
+        a.swap(tmp);
+    }
+}
+// select_candidates with top-k and min-p off (src/sampler.c:563-680):
+// returns the last kept index into buf, the kept mass in *mass.
+int select_topp(float *logits, int n, float temp, float topp, std::vector<PI> &buf, float *mass) {
+    float inv = 1.0f / temp;
+    for (int i = 0; i < n; i++) logits[i] *= inv;
+    h_softmax(logits, n);
+    const float cutoff = (n > 1) ? (1.0f - topp) / (float)(n - 1) : 0.0f;
+    buf.clear();
+    for (int i = 0; i < n; i++) if (logits[i] >= cutoff) buf.push_back({logits[i], i});
+    if (buf.size() > 1) sort_desc(buf);
+    if (buf.empty()) return -1;
+    int last = (int)buf.size() - 1;
+    float cum = 0.0f;
+    float limit = topp * 1.0f;
+    for (size_t i = 0; i < buf.size(); i++) {
+        cum += buf[i].prob;
+        if (cum >= limit) { last = (int)i; break; }
+    }
+    *mass = cum;
+    return last;
+}
+bool topp_active(float topp) { return topp > 0.0f && topp < 1.0f; }
+
+// lz_target_dist, top-k/min-p off (src/sampler.c:682-730)
+void target_dist(float *logits, int n, float temp, float topp, float *out_p, std::vector<PI> &buf) {
+    if (!topp_active(topp)) {
+        float inv = 1.0f / temp;
+        for (int i = 0; i < n; i++) logits[i] *= inv;
+        h_softmax(logits, n);
+        memcpy(out_p, logits, sizeof(float) * (size_t)n);
+        return;
+    }
+    memset(out_p, 0, sizeof(float) * (size_t)n);
+    float mass = 0.0f;
+    int last = select_topp(logits, n, temp, topp, buf, &mass);
+    if (last < 0) { out_p[lz_sample_argmax(logits, n)] = 1.0f; return; }
+    for (int i = 0; i <= last; i++) out_p[buf[i].index] = buf[i].prob / mass;
+}
+// lz_sample_ex for temperature > 0 with top-p (src/sampler.c:794-840)
+int sample_ex(float *logits, int n, float temp, float topp, lz_u64 *rng, std::vector<PI> &buf) {
+    if (!(temp > 0.0f)) return lz_sample_argmax(logits, n);
+    float coin = lz_random_f32(rng);
+    if (!topp_active(topp)) {
+        float inv = 1.0f / temp;
+        for (int i = 0; i < n; i++) logits[i] *= inv;
+        h_softmax(logits, n);
+        return sample_mult(logits, n, coin);
+    }
+    float mass = 0.0f;
+    int last = select_topp(logits, n, temp, topp, buf, &mass);
+    if (last < 0) return lz_sample_argmax(logits, n);
+    float r = coin * mass, cdf = 0.0f;
+    for (int i = 0; i <= last; i++) { cdf += buf[i].prob; if (r < cdf) return buf[i].index; }
+    return buf[last].index;
+}
+int sample_from_dist(const float *p, int vocab, lz_u64 *rng) {   // src/generate.c:1151-1160
+    float coin = lz_random_f32(rng), cdf = 0.0f;
+    for (int i = 0; i < vocab; i++) { cdf += p[i]; if (coin < cdf) return i; }
+    return vocab - 1;
+}
+bool penalties_on(const LZSampler *samp) {
+    if (!samp) return false;
+    const LZSampleParams &p = samp->p;
+    if (p.repeat_last_n == 0) return false;
+    return p.repetition_penalty != 1.0f || p.presence_penalty != 0.0f || p.frequency_penalty != 0.0f;
+}
+bool unsupported_sampler(const LZSampler *samp) {
+    if (!samp) return false;
+    const LZSampleParams &p = samp->p;
+    return penalties_on(samp) || (p.topk > 0 && p.topk < samp->vocab_size) || p.minp > 0.0f ||
+           p.think_temp_enabled;
+}
+}  // namespace
+
+extern "C" int lz_argmax_p1(const float *logits, int n, float *out_p) {   // src/sampler.c:139-155
+    int bi = 0;
+    float bv = logits[0], l = 1.0f;
+    for (int i = 1; i < n; i++) {
+        float v = logits[i];
+        if (v > bv) { l = l * h_exp(bv - v) + 1.0f; bv = v; bi = i; }
+        else l += h_exp(v - bv);
+    }
+    if (out_p) *out_p = (l > 0.0f) ? 1.0f / l : 1.0f;
+    return bi;
+}
+
+extern "C" void lz_sample_defaults(LZSampleParams *p) {   // src/sampler.c:8-20
+    p->temperature = 0.6f; p->temp_think = 0.3f; p->think_temp_enabled = 0;
+    p->topp = 0.8f; p->minp = 0.05f; p->minp_llamacpp = 1; p->topk = 20;
+    p->presence_penalty = 1.5f; p->frequency_penalty = 0.0f;
+    p->repetition_penalty = 1.1f; p->repeat_last_n = 64;
+}
+extern "C" int lz_sampler_init(LZSampler *s, int vocab_size, const LZSampleParams *p, lz_u64 seed) {
+    if (!s || !p || vocab_size <= 0) return 1;
+    s->vocab_size = vocab_size;
+    s->p = *p;
+    s->rng_state = seed ? seed : 1ULL;
+    return 0;
+}
+extern "C" void lz_sampler_free(LZSampler *s) { (void)s; }
+
+// ------------------------------------------------------- acceptance ---
+
+extern "C" int lz_spec_accept(const int *draft, const int *targ, int n_draft, int bonus, int *out) {
+    if (!draft || !targ || !out || n_draft < 0) return 0;      // src/generate.c:232-243
+    for (int i = 0; i < n_draft; i++) {
+        out[i] = targ[i];
+        if (draft[i] != targ[i]) return i;
+    }
+    out[n_draft] = bonus;
+    return n_draft;
+}
+
+static int sample_residual(const float *p, const float *q, int vocab, lz_u64 *rng) {
+    float total = 0.0f, coin, cdf = 0.0f;                       // src/generate.c:261-281
+    int last_pos = -1;
+    for (int i = 0; i < vocab; i++) {
+        float dd = p[i] - q[i];
+        if (dd > 0.0f) { total += dd; last_pos = i; }
+    }
+    if (total <= 0.0f) return lz_sample_argmax(p, vocab);
+    coin = lz_random_f32(rng) * total;
+    for (int i = 0; i < vocab; i++) {
+        float dd = p[i] - q[i];
+        if (dd > 0.0f) { cdf += dd; if (coin < cdf) return i; }
+    }
+    return last_pos;
+}
+
+extern "C" int lz_spec_accept_temp(const float *p, const float *q, int x, int vocab, float u,
+                                   lz_u64 *rng, int *out_accepted) {
+    if (!p || !q || !rng || vocab <= 0 || x < 0 || x >= vocab) {   // src/generate.c:283-346
+        if (out_accepted) *out_accepted = 0;
+        return -1;
+    }
+    float qx = q[x], ratio;
+    if (qx <= 0.0f) ratio = 0.0f;
+    else { ratio = p[x] / qx; if (ratio > 1.0f) ratio = 1.0f; }
+    if (u < ratio) { if (out_accepted) *out_accepted = 1; return x; }
+    if (out_accepted) *out_accepted = 0;
+    return sample_residual(p, q, vocab, rng);
+}
+
+// ------------------------------------------------------------- rounds ---
+
+namespace {
+
+// Enqueues one greedy round on the device (drafts, verify, argmaxes,
+// acceptance, ring rollback, chain reseed); reads nothing back.
+int enqueue_greedy_round(DState *d, int k, int max_pos, int brk) {
+    const LZModelConfig &c = d->m->c;
+    for (int i = 0; i < k; i++)
+        CK(draft_step(d, d->ctl->tok + i, &d->ctl->mtp_pos, i, max_pos, d->draft_logits + (size_t)i * c.vocab_size,
+                      d->ctl->tok + 1 + i));
+    CK(forward_chunk(d, d->ctl->tok, k + 1, &d->ctl->anchor_pos, 1, max_pos, d->vhidden, true,
+                     d->mtp_logits, false));
+    CK(l98k_argmax(d->mtp_logits, c.vocab_size, k + 1, 0, d->ctl->targ, d->st));
+    CK(l98k_accept(d->ctl, d->vhidden, c.hidden_size, d->chain, d->depth, brk, d->st));
+    return 0;
+}
+
+int errset(char *errbuf, int errlen, int code, const char *msg) {
+    set_err(errbuf, errlen, "%s", msg);
+    return -code;
+}
+
+}  // namespace
+
+extern "C" int lz_spec_round(const LZModel *mm, LZRunState *s, int anchor, int anchor_pos, int k,
+                             float p_min, int n_min, const LZSampler *samp, int brk, int skipc,
+                             int *out, int *out_n_accept, int *out_new_pos, int *out_k_eff,
+                             char *errbuf, int errlen) {
+    if (!mm || !s || !out || !out_n_accept || !out_new_pos || !out_k_eff || !s->impl)
+        return errset(errbuf, errlen, LZ_ERR_NULL_ARG, "null argument");
+    if (k < 1 || k > LZ_SPEC_K_MAX || k > s->ssm_ring_depth - 1) {
+        set_err(errbuf, errlen, "spec_k %d out of range 1..%d", k,
+                k > LZ_SPEC_K_MAX ? LZ_SPEC_K_MAX : s->ssm_ring_depth - 1);
+        return -LZ_ERR_SPEC_K_RANGE;
+    }
+    if (penalties_on(samp)) return errset(errbuf, errlen, LZ_ERR_NULL_ARG, "sampler penalties are not on this path");
+    DState *d = S(s);
+    const LZModelConfig &c = d->m->c;
+    if (anchor < 0 || anchor >= c.vocab_size || anchor_pos + 1 + k >= d->seq_len ||
+        s->mtp_pos + k > d->seq_len)
+        return errset(errbuf, errlen, LZ_ERR_FORWARD, "forward failed (token/position out of range)");
+    DevCtl h = ctl_from(s);
+    h.anchor = anchor;
+    h.anchor_pos = anchor_pos;
+    h.tok[0] = anchor;
+    h.k_eff = k;
+    int k_eff = k;
+    if (p_min > 0.0f) {
+        // p_min needs each step's top-1 probability before deciding on the
+        // next: drafts run one at a time with a host read-back.
+        if (ctl_put(d, h)) return -LZ_ERR_FORWARD;
+        std::vector<float> lg(c.vocab_size);
+        k_eff = 0;
+        for (int i = 0; i < k; i++) {
+            if (draft_step(d, d->ctl->tok + i, &d->ctl->mtp_pos, i, s->mtp_pos + k,
+                           d->draft_logits, d->ctl->tok + 1 + i))
+                return -LZ_ERR_FORWARD;
+            if (hipMemcpyAsync(lg.data(), d->draft_logits, sizeof(float) * c.vocab_size,
+                               hipMemcpyDeviceToHost, d->st) || hipStreamSynchronize(d->st))
+                return -LZ_ERR_FORWARD;
+            float p1;
+            int idx = lz_argmax_p1(lg.data(), c.vocab_size, &p1);
+            if (p1 < p_min) break;
+            h.tok[1 + i] = idx;
+            k_eff = i + 1;
+        }
+        if (k_eff < n_min) {
+            out[0] = anchor; *out_n_accept = 0; *out_new_pos = anchor_pos; *out_k_eff = k_eff;
+            return 0;
+        }
+        h.k_eff = k_eff;
+        if (ctl_get(d, &h)) return -LZ_ERR_FORWARD;
+        h.k_eff = k_eff;
+        if (ctl_put(d, h)) return -LZ_ERR_FORWARD;
+        if (forward_chunk(d, d->ctl->tok, k_eff + 1, &d->ctl->anchor_pos, 1, anchor_pos + k_eff + 1,
+                          d->vhidden, true, d->mtp_logits, false) ||
+            l98k_argmax(d->mtp_logits, c.vocab_size, k_eff + 1, 0, d->ctl->targ, d->st) ||
+            l98k_accept(d->ctl, d->vhidden, c.hidden_size, d->chain, d->depth, brk, d->st))
+            return -LZ_ERR_FORWARD;
+    } else {
+        if (k_eff < n_min) {
+            // every draft step still runs (its MTP KV rows are written)
+            if (ctl_put(d, h)) return -LZ_ERR_FORWARD;
+            for (int i = 0; i < k; i++)
+                if (draft_step(d, d->ctl->tok + i, &d->ctl->mtp_pos, i, s->mtp_pos + k, d->draft_logits,
+                               d->ctl->tok + 1 + i))
+                    return -LZ_ERR_FORWARD;
+            if (hipStreamSynchronize(d->st)) return -LZ_ERR_FORWARD;
+            out[0] = anchor; *out_n_accept = 0; *out_new_pos = anchor_pos; *out_k_eff = k_eff;
+            return 0;
+        }
+        if (ctl_put(d, h)) return -LZ_ERR_FORWARD;
+        if (enqueue_greedy_round(d, k, anchor_pos + k + 1 > s->mtp_pos + k ? anchor_pos + k + 1 : s->mtp_pos + k, brk))
+            return -LZ_ERR_FORWARD;
+    }
+    if (ctl_get(d, &h)) return -LZ_ERR_FORWARD;
+    int n_accept = h.n_accept;
+    for (int i = 0; i <= n_accept; i++) out[i] = h.out[i];
+    s->ssm_slot = h.ssm_slot;
+    *out_n_accept = n_accept;
+    *out_new_pos = anchor_pos + 1 + n_accept;
+    *out_k_eff = k_eff;
+    if (n_accept > 1 && !skipc) {
+        DevCtl h2 = h;
+        h2.pos_scratch = s->mtp_pos + 1;
+        if (ctl_put(d, h2) ||
+            mtp_prefill_dev(d, d->vhidden, d->ctl->out, n_accept - 1, &d->ctl->pos_scratch, 0) ||
+            hipStreamSynchronize(d->st))
+            return -LZ_ERR_FORWARD;
+    }
+    s->mtp_pos += n_accept;
+    return n_accept + 1;
+}
+
+extern "C" int lz_spec_round_temp(const LZModel *mm, LZRunState *s, int anchor, int anchor_pos, int k,
+                                  float p_min, int n_min, LZSampler *samp, int brk, int skipc,
+                                  int *out, int *out_n_accept, int *out_new_pos, int *out_k_eff,
+                                  char *errbuf, int errlen) {
+    if (!mm || !s || !samp || !out || !out_n_accept || !out_new_pos || !out_k_eff || !s->impl)
+        return errset(errbuf, errlen, LZ_ERR_NULL_ARG, "null argument");
+    if (k < 1 || k > LZ_SPEC_K_MAX || k > s->ssm_ring_depth - 1) {
+        set_err(errbuf, errlen, "spec_k %d out of range 1..%d", k,
+                k > LZ_SPEC_K_MAX ? LZ_SPEC_K_MAX : s->ssm_ring_depth - 1);
+        return -LZ_ERR_SPEC_K_RANGE;
+    }
+    if (unsupported_sampler(samp))
+        return errset(errbuf, errlen, LZ_ERR_NULL_ARG, "sampler option not on this path");
+    DState *d = S(s);
+    const LZModelConfig &c = d->m->c;
+    const int V = c.vocab_size;
+    if (anchor < 0 || anchor >= V || anchor_pos + 1 + k >= d->seq_len || s->mtp_pos + k > d->seq_len)
+        return errset(errbuf, errlen, LZ_ERR_FORWARD, "forward failed (token/position out of range)");
+    const float temp = samp->p.temperature, topp = samp->p.topp;
+    DevCtl h = ctl_from(s);
+    h.anchor = anchor; h.anchor_pos = anchor_pos; h.tok[0] = anchor;
+    if (ctl_put(d, h)) return -LZ_ERR_FORWARD;
+    std::vector<float> q((size_t)k * V), row(V), p(V);
+    std::vector<PI> buf;
+    int draft[LZ_SPEC_K_MAX], k_eff = 0;
+    for (int i = 0; i < k; i++) {
+        if (draft_step(d, d->ctl->tok + i, &d->ctl->mtp_pos, i, s->mtp_pos + k, d->draft_logits, nullptr))
+            return -LZ_ERR_FORWARD;
+        float *lg = q.data() + (size_t)i * V;
+        if (hipMemcpyAsync(lg, d->draft_logits, sizeof(float) * V, hipMemcpyDeviceToHost, d->st) ||
+            hipStreamSynchronize(d->st))
+            return -LZ_ERR_FORWARD;
+        // lz_sample_temp_q (src/sampler.c:736-747): q = softmax(logits/T) in place
+        float inv = 1.0f / temp;
+        for (int j = 0; j < V; j++) lg[j] *= inv;
+        h_softmax(lg, V);
+        int idx = sample_mult(lg, V, lz_random_f32(&samp->rng_state));
+        if (lg[idx] < p_min) break;
+        draft[i] = idx;
+        h.tok[1 + i] = idx;
+        k_eff = i + 1;
+        if (hipMemcpyAsync(d->ctl->tok + 1 + i, &idx, sizeof(int), hipMemcpyHostToDevice, d->st))
+            return -LZ_ERR_FORWARD;
+    }
+    if (k_eff < n_min) {
+        out[0] = anchor; *out_n_accept = 0; *out_new_pos = anchor_pos; *out_k_eff = k_eff;
+        return 0;
+    }
+    int base = s->ssm_slot;
+    if (forward_chunk(d, d->ctl->tok, k_eff + 1, &d->ctl->anchor_pos, 1, anchor_pos + k_eff + 1,
+                      d->vhidden, true, d->mtp_logits, false))
+        return -LZ_ERR_FORWARD;
+    std::vector<float> logits((size_t)(k_eff + 1) * V);
+    if (hipMemcpyAsync(logits.data(), d->mtp_logits, sizeof(float) * logits.size(), hipMemcpyDeviceToHost, d->st) ||
+        hipStreamSynchronize(d->st))
+        return -LZ_ERR_FORWARD;
+    int n_accept = k_eff;
+    for (int i = 0; i < k_eff; i++) {
+        float *rw = logits.data() + (size_t)i * V;
+        target_dist(rw, V, temp, topp, p.data(), buf);
+        float u = lz_random_f32(&samp->rng_state);
+        int acc = 0;
+        int tok = lz_spec_accept_temp(p.data(), q.data() + (size_t)i * V, draft[i], V, u, &samp->rng_state, &acc);
+        out[i] = tok;
+        if (!acc) { n_accept = i; break; }
+    }
+    if (n_accept == k_eff) {
+        float *rw = logits.data() + (size_t)k_eff * V;
+        target_dist(rw, V, temp, topp, p.data(), buf);
+        out[k_eff] = sample_from_dist(p.data(), V, &samp->rng_state);
+    }
+    s->ssm_slot = (base + k_eff + 1) % d->depth;
+    if (n_accept < k_eff && !brk) s->ssm_slot = (base + n_accept + 1) % d->depth;
+    // reseed the chain from the accepted row; catch-up
+    if (hipMemcpyAsync(d->chain, d->vhidden + (size_t)n_accept * c.hidden_size, sizeof(float) * c.hidden_size,
+                       hipMemcpyDeviceToDevice, d->st))
+        return -LZ_ERR_FORWARD;
+    *out_n_accept = n_accept;
+    *out_new_pos = anchor_pos + 1 + n_accept;
+    *out_k_eff = k_eff;
+    if (n_accept > 1 && !skipc) {
+        DevCtl h2 = h;
+        h2.pos_scratch = s->mtp_pos + 1;
+        for (int i = 0; i <= n_accept; i++) h2.out[i] = out[i];
+        if (ctl_put(d, h2) ||
+            mtp_prefill_dev(d, d->vhidden, d->ctl->out, n_accept - 1, &d->ctl->pos_scratch, 0))
+            return -LZ_ERR_FORWARD;
+    }
+    if (hipStreamSynchronize(d->st)) return -LZ_ERR_FORWARD;
+    s->mtp_pos += n_accept;
+    return n_accept + 1;
+}
+
+// --------------------------------------------------------- generation ---
+
+static double g_last_loop_s = 0.0;
+extern "C" double l98_last_loop_seconds(void) { return g_last_loop_s; }
+
+extern "C" const char *l98_device_name(void) {
+    static char name[256];
+    hipDeviceProp_t p;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&p, dev) != hipSuccess) return "none";
+    snprintf(name, sizeof name, "%s (%s, %d CUs)", p.name, p.gcnArchName, p.multiProcessorCount);
+    return name;
+}
+
+extern "C" int l98_generate(const LZModel *mm, LZRunState *s, const int *prompt, int n_prompt, int k,
+                            int n_new, const LZSampler *samp, int *tokens, int cap, int *k_eff_out,
+                            int *n_accept_out, int *n_rounds) {
+    if (!mm || !s || !s->impl || !prompt || n_prompt < 2 || !tokens) return -LZ_ERR_NULL_ARG;
+    DState *d = S(s);
+    const LZModelConfig &c = d->m->c;
+    if (!tok_ok(c, prompt, n_prompt)) return -LZ_ERR_FORWARD;
+    if (k < 1 || k > LZ_SPEC_K_MAX || k > s->ssm_ring_depth - 1) return -LZ_ERR_SPEC_K_RANGE;
+    const bool greedy = !samp || !(samp->p.temperature > 0.0f);
+    if (n_prompt + n_new + 2 * (k + 1) >= d->seq_len) return -LZ_ERR_FORWARD;
+    LZSampler local{};
+    if (samp) local = *samp;
+    // prefill (src/generate.c:2806-2960)
+    lz_state_reset(s, mm);
+    if (batch_capture_dev(d, s, prompt, n_prompt - 1, 0)) return -LZ_ERR_FORWARD;
+    {
+        DevCtl h = ctl_from(s);
+        h.pos_scratch = 0;
+        if (ctl_put(d, h) ||
+            hipMemcpyAsync(d->tokbuf, prompt + 1, sizeof(int) * (size_t)(n_prompt - 1), hipMemcpyHostToDevice, d->st) ||
+            mtp_prefill_dev(d, d->hcap, d->tokbuf, n_prompt - 1, &d->ctl->pos_scratch, 0))
+            return -LZ_ERR_FORWARD;
+    }
+    s->mtp_pos = n_prompt - 1;
+    int n = 0, rounds = 0;
+    int token = prompt[n_prompt - 1], pos = n_prompt - 1;
+    // first anchor from a capture forward
+    float *lg = lz_forward_capture(mm, s, token, pos);
+    if (!lg) return -LZ_ERR_FORWARD;
+    std::vector<PI> buf;
+    int anchor = greedy ? lz_sample_argmax(lg, c.vocab_size)
+                        : sample_ex(lg, c.vocab_size, local.p.temperature, local.p.topp, &local.rng_state, buf);
+    if (n < cap) tokens[n] = anchor;
+    n++;
+    int anchor_pos = pos;
+    if (!greedy) {
+        while (n < n_new) {
+            int out[LZ_SPEC_K_MAX + 1], na = 0, np = 0, ke = 0;
+            int r = lz_spec_round_temp(mm, s, anchor, anchor_pos, k, 0.0f, 0, &local, 0, 0, out, &na, &np, &ke,
+                                       nullptr, 0);
+            if (r <= 0) return r < 0 ? r : -LZ_ERR_FORWARD;
+            if (k_eff_out) k_eff_out[rounds] = ke;
+            if (n_accept_out) n_accept_out[rounds] = na;
+            rounds++;
+            for (int i = 0; i <= na; i++) { if (n < cap) tokens[n] = out[i]; n++; }
+            anchor = out[na];
+            anchor_pos = np;
+        }
+        if (n_rounds) *n_rounds = rounds;
+        return n;
+    }
+    // Greedy: rounds are enqueued back to back; each round's control block
+    // is derived on the device from the previous one, and the host reads
+    // the accepted tokens of a round only after the next one is queued.
+    {
+        DevCtl h = ctl_from(s);
+        h.anchor = anchor; h.anchor_pos = anchor_pos; h.k_eff = k;
+        h.tok[0] = anchor;
+        if (ctl_put(d, h)) return -LZ_ERR_FORWARD;
+    }
+    const int max_pos = n_prompt + n_new + 2 * (k + 1);
+    (void)hipEventRecord(d->ev0, d->st);
+    std::vector<DevCtl> hist;
+    // With k drafts a round emits at least one token, so n_new rounds bound
+    // the loop; rounds are read back in batches.
+    const int batch = 8;
+    while (n < n_new) {
+        int nb = 0;
+        size_t base_idx = hist.size();
+        for (; nb < batch; nb++) {
+            if (enqueue_greedy_round(d, k, max_pos, 0)) return -LZ_ERR_FORWARD;
+            // catch-up for the accepted drafts (count from the device):
+            // kernels past catch_n are skipped by reading ctl->catch_n.
+            // The catch-up rows are at most k-1; they are written with a
+            // device-side count below.
+            hist.push_back(DevCtl{});
+            if (hipMemcpyAsync(d->ctl_pinned, d->ctl, sizeof(DevCtl), hipMemcpyDeviceToHost, d->st)) return -LZ_ERR_FORWARD;
+            if (hipStreamSynchronize(d->st)) return -LZ_ERR_FORWARD;
+            DevCtl cur = *d->ctl_pinned;
+            hist.back() = cur;
+            if (cur.catch_n > 0) {
+                DevCtl h2 = cur;
+                h2.pos_scratch = cur.catch_pos;
+                if (ctl_put(d, h2) ||
+                    mtp_prefill_dev(d, d->vhidden, d->ctl->out, cur.catch_n, &d->ctl->pos_scratch, 0))
+                    return -LZ_ERR_FORWARD;
+            }
+            if (l98k_set_tokens(d->ctl, 1, d->st) || l98k_set_tokens(d->ctl, 0, d->st)) return -LZ_ERR_FORWARD;
+            {
+                int tot = n;
+                for (size_t i = base_idx; i < hist.size(); i++) tot += hist[i].n_accept + 1;
+                if (tot >= n_new) { nb++; break; }
+            }
+        }
+        for (size_t i = base_idx; i < hist.size(); i++) {
+            const DevCtl &r = hist[i];
+            if (k_eff_out) k_eff_out[rounds] = r.k_eff;
+            if (n_accept_out) n_accept_out[rounds] = r.n_accept;
+            rounds++;
+            for (int j = 0; j <= r.n_accept; j++) { if (n < cap) tokens[n] = r.out[j]; n++; }
+        }
+    }
+    (void)hipEventRecord(d->ev1, d->st);
+    (void)hipEventSynchronize(d->ev1);
+    float ms = 0.0f;
+    (void)hipEventElapsedTime(&ms, d->ev0, d->ev1);
+    g_last_loop_s = ms * 1e-3;
+    {
+        DevCtl last = hist.back();
+        s->ssm_slot = last.ssm_slot;
+        s->mtp_pos = last.mtp_pos_next;
+    }
+    if (n_rounds) *n_rounds = rounds;
+    return n;
+}

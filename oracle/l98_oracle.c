@@ -1550,3 +1550,4 @@ ORA_API void ora_kv_plane(void *hs, int plane, int rows, int8_t *kq, float *ks, 
     memcpy(ks, s->ks + off / 32, sizeof(float) * (size_t)rows * kvd / 32);
     memcpy(vs, s->vs + off / 32, sizeof(float) * (size_t)rows * kvd / 32);
 }
+ORA_API void ora_set_mtp_pos(void *hs, int pos) { ((OState *)hs)->mtp_pos = pos; }

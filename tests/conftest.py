@@ -1,0 +1,42 @@
+import os
+import sys
+import tempfile
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (runs the HIP path)")
+    config.addinivalue_line("markers", "slow: minutes of CPU time")
+
+
+@pytest.fixture(scope="session")
+def pkg():
+    import __graft_entry__
+    return __graft_entry__.load_package()
+
+
+@pytest.fixture(scope="session")
+def model_root():
+    d = os.environ.get("L98_MODEL_DIR") or os.path.join(tempfile.gettempdir(), "l98_models")
+    os.makedirs(d, exist_ok=True)
+    return d
+
+
+@pytest.fixture(scope="session")
+def micro(pkg, model_root):
+    return pkg.ensure_model(os.path.join(model_root, "micro"), 10, seed=1234)
+
+
+@pytest.fixture(scope="session")
+def tiny(pkg, model_root):
+    return pkg.ensure_model(os.path.join(model_root, "tiny"), 0, seed=1234)
+
+
+@pytest.fixture(scope="session")
+def server(pkg, model_root):
+    return pkg.ensure_model(os.path.join(model_root, "server"), 4, seed=1234)
