@@ -1299,6 +1299,9 @@ extern "C" int lz_spec_round(const LZModel *mm, LZRunState *s, int anchor, int a
         if (enqueue_greedy_round(d, k, anchor_pos + k + 1 > s->mtp_pos + k ? anchor_pos + k + 1 : s->mtp_pos + k, brk))
             return -LZ_ERR_FORWARD;
     }
+    // chain mirror (the reseeded mtp_chain) rides on the same sync as ctl
+    if (hipMemcpyAsync(s->mtp_chain, d->chain, sizeof(float) * c.hidden_size, hipMemcpyDeviceToHost, d->st))
+        return -LZ_ERR_FORWARD;
     if (ctl_get(d, &h)) return -LZ_ERR_FORWARD;
     int n_accept = h.n_accept;
     for (int i = 0; i <= n_accept; i++) out[i] = h.out[i];
@@ -1406,7 +1409,9 @@ extern "C" int lz_spec_round_temp(const LZModel *mm, LZRunState *s, int anchor, 
             mtp_prefill_dev(d, d->vhidden, d->ctl->out, n_accept - 1, &d->ctl->pos_scratch, 0))
             return -LZ_ERR_FORWARD;
     }
-    if (hipStreamSynchronize(d->st)) return -LZ_ERR_FORWARD;
+    if (hipMemcpyAsync(s->mtp_chain, d->chain, sizeof(float) * c.hidden_size, hipMemcpyDeviceToHost, d->st) ||
+        hipStreamSynchronize(d->st))
+        return -LZ_ERR_FORWARD;
     s->mtp_pos += n_accept;
     return n_accept + 1;
 }

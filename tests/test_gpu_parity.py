@@ -67,7 +67,7 @@ def test_verify_and_draft_bit_exact(pkg, tiny):
     dl = eng.draft_step(anchor, n - 1)
     do = ora.draft_step(anchor, n - 1)
     assert same_bits(dl, do), "draft logits: " + diff_report(dl, do)
-    assert same_bits(eng.chain(), ora.chain())
+    assert same_bits(eng.chain(), ora.chain()), "chain: " + diff_report(eng.chain(), ora.chain())
     toks = np.array([anchor, 5, 17, 4000], np.int32)
     v = eng.verify(toks, n)
     vo = ora.verify(toks, n)
@@ -93,7 +93,7 @@ def test_spec_rounds_match(pkg, tiny, k):
         assert list(g[1][:g[0]]) == list(o[1][:o[0]]), (r, g, o)
         assert eng.s.ssm_slot == ora.info()["ssm_slot"] and eng.s.mtp_pos == ora.info()["mtp_pos"]
         anchor, apos = int(g[1][g[2]]), g[3]
-    assert same_bits(eng.chain(), ora.chain())
+    assert same_bits(eng.chain(), ora.chain()), "chain: " + diff_report(eng.chain(), ora.chain())
     eng.close()
 
 
