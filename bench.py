@@ -1,0 +1,221 @@
+#!/usr/bin/env python3
+"""Benchmark of the MTP speculative-decoding step on one MI355X.
+
+Metric: accepted tokens/s at batch 1 with k = 3 drafts, and
+the verify step's HBM bandwidth as a fraction of the MI355X peak.
+
+Workload: the ~0.5B random-init KunMoe (d=1024, 24 layers in a
+3:1 KDA:attention pattern, 16 heads x 64, 64 experts top-6, latent 256,
+expert FFN 512, vocab 65536, int8 per-row weights), greedy, batch 1, a
+512-token uniform-random prompt (seed 0), MTP drafting k = 3.
+
+A step is one speculative round: k draft steps, the (k+1)-token verify
+forward, acceptance, ring rollback and MTP catch-up, all on the device (one
+HIP graph launch per round).  W warmup rounds, then K timed rounds between
+device synchronizations; value = tokens emitted in the K rounds / wall time.
+
+The JSON line also carries:
+  roofline      the dominant kernel (the tied lm_head GEMV at M = k+1 rows)
+                timed with HIP events on its own stream, algorithmic bytes /
+                mean launch time against 8 TB/s;
+  verify        the verify forward alone (M = k+1), algorithmic bytes / time;
+  round         accepted tok/s against the round's HBM roofline
+                E[n_accept+1] * 8e12 / bytes_per_round (bytes counted from
+                the distinct experts and context each round actually used);
+  cpu_baseline  the reference engine's own shipping build (AVX2 tier,
+                oracle/_ref/l98ref_ship) on one host core, same model.
+"""
+import argparse
+import json
+import os
+import subprocess
+import sys
+import tempfile
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK = 8.0e12
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def model_bytes(cfg):
+    """Per-component algorithmic bytes of the model (int8 weight + 4 B/row)."""
+    d, V = cfg.hidden_size, cfg.vocab_size
+    def mat(r, c):
+        return r * c + 4 * r
+    key, value = cfg.lin_key_dim, cfg.lin_value_dim
+    nv, kd, vd = cfg.lin_n_v_heads, cfg.lin_k_head_dim, cfg.lin_v_head_dim
+    kda = (2 * mat(key, d) + mat(value, d) + mat(cfg.kda_gate_rank, d) + mat(nv * kd, cfg.kda_gate_rank)
+           + mat(nv, d) + mat(value, d) + mat(d, value) + 4 * cfg.lin_conv_dim * cfg.conv_kernel
+           + 4 * (2 * nv * kd + vd) + 2 * 4 * nv * kd * vd            # params + fp32 state in and out
+           + 2 * 4 * cfg.lin_conv_dim * (cfg.conv_kernel - 1))
+    attn = (mat(cfg.attn_qgate_dim, d) + 2 * mat(cfg.attn_kv_dim, d) + mat(d, cfg.attn_q_dim)
+            + 8 * cfg.head_dim)
+    kv_row = 2 * cfg.attn_kv_dim + 2 * 4 * cfg.attn_kv_dim // 32       # Q8 K and V + scales, per position
+    moe_fixed = (mat(cfg.num_experts, d) + 4 * cfg.num_experts + mat(cfg.moe_latent_dim, d)
+                 + mat(d, cfg.moe_latent_dim) + 2 * mat(cfg.moe_shared_width, d) + mat(d, cfg.moe_shared_width))
+    expert = 2 * mat(cfg.moe_intermediate_size, cfg.moe_latent_dim) + mat(cfg.moe_latent_dim,
+                                                                            cfg.moe_intermediate_size)
+    norms = 2 * 4 * d
+    lm_head = mat(V, d)
+    mtp = (mat(d, 2 * d) + attn + 2 * mat(cfg.mtp_intermediate_size, d) + mat(d, cfg.mtp_intermediate_size)
+           + 5 * 4 * d)
+    return dict(kda=kda, attn=attn, kv_row=kv_row, moe_fixed=moe_fixed, expert=expert, norms=norms,
+                lm_head=lm_head, mtp=mtp)
+
+
+def round_bytes(cfg, k, ctx_verify, experts):
+    """Algorithmic HBM bytes of one round: k draft steps + an M = k+1 verify."""
+    b = model_bytes(cfg)
+    n_lin, n_full = cfg.n_linear_layers, cfg.n_full_layers
+    M = k + 1
+    draft = k * (b["mtp"] + b["lm_head"]) + b["kv_row"] * sum(ctx_verify + i for i in range(k))
+    verify = (n_lin * b["kda"] + n_full * b["attn"] + (n_lin + n_full) * (b["moe_fixed"] + b["norms"])
+              + experts * b["expert"] + b["lm_head"] + n_full * b["kv_row"] * (ctx_verify + M)
+              + 4 * M * (cfg.vocab_size + cfg.hidden_size))
+    return draft, verify
+
+
+def cpu_baseline(model_dir, vocab, k):
+    """The reference engine's shipping build on one host core, bounded sample."""
+    import __graft_entry__
+    pkg = __graft_entry__.load_package()
+    binary = os.path.join(ROOT, "oracle", "_ref", "l98ref_ship")
+    if not os.path.exists(binary):
+        return None
+    tmp = tempfile.mkdtemp(prefix="l98cpu_")
+    pf = os.path.join(tmp, "prompt.bin")
+    n_prompt, n_new = 64, 48
+    pkg.prompt_tokens(0, n_prompt, vocab).tofile(pf)
+    core = sorted(os.sched_getaffinity(0))[-1]
+    cmd = ["taskset", "-c", str(core), binary, "gen", model_dir, pf, str(k), str(n_new), "0", "1", "1",
+           os.path.join(tmp, "run"), "--timing"]
+    log("cpu baseline:", " ".join(cmd))
+    subprocess.run(cmd, check=True, timeout=300)
+    d = {}
+    for line in open(os.path.join(tmp, "run.txt")):
+        f = line.split()
+        d[f[0]] = f[1:]
+    n_tok = int(d["n_tokens"][0])
+    loop_s = float(d["loop_us"][0]) * 1e-6
+    cpu = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(n_tok / loop_s, 3), "unit": "tok/s", "cores": 1, "kind": "reference",
+            "sample": f"reference shipping build (lz_spec_round, tier {d['kernel'][0]}, gcc -O2 AVX2), "
+                      f"{n_prompt}-token prompt, {n_tok} tokens emitted in {len(d['k_eff'])} rounds, "
+                      f"k={k}, same model, 1 core of {os.cpu_count()} ({cpu})",
+            "round_ms": round(loop_s * 1e3 / max(1, len(d['k_eff'])), 3)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--k", type=int, default=3)
+    ap.add_argument("--config", type=int, default=1)
+    ap.add_argument("--prompt", type=int, default=512)
+    ap.add_argument("--model-dir", default=os.path.join(tempfile.gettempdir(), "l98_models"))
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs the single-sequence path on one GPU; --gpus {args.gpus} "
+              f"is not supported (see DESIGN.md for how the path would shard)", file=sys.stderr)
+        sys.exit(2)
+
+    import __graft_entry__
+    pkg = __graft_entry__.load_package()
+    name = {0: "tiny", 1: "base", 3: "large"}.get(args.config, f"c{args.config}")
+    mdir = os.path.join(args.model_dir, name)
+    t0 = time.time()
+    pkg.ensure_model(mdir, args.config, seed=1234)
+    log(f"model {mdir} ready in {time.time() - t0:.1f}s")
+    eng = pkg.Engine(mdir)
+    cfg = eng.cfg
+    log(f"device {pkg.hip_lib().l98_device_name().decode()}; weights {eng.m.bytes_device / 1e9:.3f} GB")
+    k = args.k
+    prompt = pkg.prompt_tokens(0, args.prompt, cfg.vocab_size)
+    t0 = time.time()
+    eng.session_start(prompt)
+    log(f"prefill of {len(prompt)} tokens: {time.time() - t0:.2f}s")
+    use_graph = not args.no_graph
+    eng.greedy_rounds(k, args.warmup, use_graph)
+    t0 = time.perf_counter()
+    toks, na, dev_ms, experts, new_pos = eng.greedy_rounds(k, args.steps, use_graph, detail=True)
+    t1 = time.perf_counter()
+    wall = t1 - t0
+    n_tok = len(toks)
+    value = n_tok / wall
+    log(f"{args.steps} rounds: {n_tok} tokens in {wall * 1e3:.1f} ms (device {dev_ms:.1f} ms), "
+        f"alpha = {na.sum() / (k * args.steps):.4f}")
+
+    # round roofline from the bytes the rounds actually moved
+    rb_d = rb_v = 0.0
+    for r in range(args.steps):
+        ctx = int(new_pos[r]) - 1 - int(na[r])      # anchor position of the round
+        dr, vr = round_bytes(cfg, k, ctx, int(experts[r]))
+        rb_d += dr
+        rb_v += vr
+    mean_round = (rb_d + rb_v) / args.steps
+    roof_toks = (n_tok / args.steps) * HBM_PEAK / mean_round
+    # dominant kernel: the tied lm_head GEMV at M = k+1 rows
+    M = k + 1
+    lm_ms = eng.time_kernel(0, M, 50)
+    V, d = cfg.vocab_size, cfg.hidden_size
+    lm_bytes = V * d + 4 * V + M * d + 4 * M * d // 32 + 4 * M * V
+    lm_bw = lm_bytes / (lm_ms * 1e-3)
+    # verify forward alone
+    ver_ms = eng.time_kernel(1, M, 20)
+    ctx_now = int(new_pos[-1])
+    ver_bytes = round_bytes(cfg, k, ctx_now, int(experts.mean()))[1]
+    ver_bw = ver_bytes / (ver_ms * 1e-3)
+    cpu = None if args.no_cpu else cpu_baseline(mdir, cfg.vocab_size, k)
+    out = {
+        "metric": "accepted tok/s @bs1 k=3; verify-step HBM GB/s as % of MI355X peak",
+        "value": round(value, 3),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8xint8->int32, fp32 epilogue/state",
+        "data": "synthetic (seeded random-init weights N(0,0.02), uniform random prompt)",
+        "config": {"workload": f"configs[{args.config}] KunMoe d={d} L={cfg.n_layers} V={V} "
+                               f"E={cfg.num_experts} top{cfg.num_experts_per_token}; k={k} greedy bs1, "
+                               f"{len(prompt)}-token prompt", "k": k, "batch": 1,
+                   "graph": use_graph},
+        "roofline": {"bound": "hbm", "kernel": f"k_gemv_q8<{M}> (tied lm_head, {V}x{d} int8)",
+                     "achieved": round(lm_bw / 1e9, 1), "peak": 8000.0, "unit": "GB/s",
+                     "frac": round(lm_bw / HBM_PEAK, 4), "traffic": None,
+                     "bytes_per_launch": lm_bytes, "launch_ms": round(lm_ms, 5)},
+        "verify": {"M": M, "ms": round(ver_ms, 4), "bytes": int(ver_bytes),
+                   "GB/s": round(ver_bw / 1e9, 1), "frac_of_peak": round(ver_bw / HBM_PEAK, 4)},
+        "round": {"alpha": round(float(na.sum()) / (k * args.steps), 4),
+                  "tokens_per_round": round(n_tok / args.steps, 4),
+                  "bytes_per_round": int(mean_round),
+                  "roofline_tok_s": round(roof_toks, 1),
+                  "frac_of_roofline": round(value / roof_toks, 4),
+                  "mean_distinct_experts": round(float(experts.mean()), 2)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out))
+    eng.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -168,6 +168,26 @@ int lz_argmax_p1(const float *logits, int n, float *out_p);
 int l98_generate(const LZModel *m, LZRunState *s, const int *prompt, int n_prompt, int k,
                  int n_new, const LZSampler *samp, int *tokens, int cap, int *k_eff_out,
                  int *n_accept_out, int *n_rounds);
+/* Prefill + MTP prefill + first capture forward of a prompt, seeding the
+ * device round state.  Returns the first emitted token, or -LZErr. */
+int l98_session_start(const LZModel *m, LZRunState *s, const int *prompt, int n_prompt,
+                      const LZSampler *samp);
+/* n greedy rounds after l98_session_start (or a previous call), back to back
+ * on the device: every scalar of a round (positions, ring slot, drafts,
+ * acceptance) stays in device memory, and with use_graph each round is one
+ * HIP graph launch.  tokens receives the emitted ids, n_accept_out each
+ * round's acceptance, device_ms the hipEvent time of the n rounds.  Returns
+ * the number of tokens emitted, or -LZErr. */
+int l98_greedy_rounds(const LZModel *m, LZRunState *s, int k, int n_rounds, int use_graph, int *tokens,
+                      int cap, int *n_accept_out, float *device_ms);
+/* l98_greedy_rounds plus, per round, the distinct (layer, expert) weight
+ * sets its verify streamed and its new_pos (for byte accounting). */
+int l98_greedy_rounds_ex(const LZModel *m, LZRunState *s, int k, int n_rounds, int use_graph, int *tokens,
+                         int cap, int *n_accept_out, int *experts_out, int *new_pos_out, float *device_ms);
+/* Mean duration of `iters` back-to-back launches of one kernel of the round
+ * (which = 0: the tied lm_head GEMV with mrows token rows), hipEvent-timed on
+ * the state's stream.  Returns 0. */
+int l98_time_kernel(const LZModel *m, LZRunState *s, int which, int mrows, int iters, float *avg_ms);
 /* Device and build facts, for logs. */
 const char *l98_device_name(void);
 /* Seconds of device time of the last l98_generate call's round loop

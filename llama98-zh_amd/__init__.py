@@ -101,6 +101,13 @@ HIP_API = [
     ("lz_argmax_p1", C.c_int, [_FP, C.c_int, _FP]),
     ("l98_generate", C.c_int, [C.POINTER(LZModel), C.POINTER(LZRunState), _IP, C.c_int, C.c_int, C.c_int,
                                C.POINTER(LZSampler), _IP, C.c_int, _IP, _IP, _IP]),
+    ("l98_session_start", C.c_int, [C.POINTER(LZModel), C.POINTER(LZRunState), _IP, C.c_int,
+                                    C.POINTER(LZSampler)]),
+    ("l98_greedy_rounds", C.c_int, [C.POINTER(LZModel), C.POINTER(LZRunState), C.c_int, C.c_int, C.c_int, _IP,
+                                    C.c_int, _IP, _FP]),
+    ("l98_greedy_rounds_ex", C.c_int, [C.POINTER(LZModel), C.POINTER(LZRunState), C.c_int, C.c_int, C.c_int,
+                                       _IP, C.c_int, _IP, _IP, _IP, _FP]),
+    ("l98_time_kernel", C.c_int, [C.POINTER(LZModel), C.POINTER(LZRunState), C.c_int, C.c_int, C.c_int, _FP]),
     ("l98_device_name", C.c_char_p, []),
     ("l98_last_loop_seconds", C.c_double, []),
 ]
@@ -268,6 +275,36 @@ class Engine:
                                    float(p_min), int(n_min), None, brk, skipc, _ip(out), C.byref(na),
                                    C.byref(npos), C.byref(ke), err, 256)
         return r, out, na.value, npos.value, ke.value
+
+    def session_start(self, prompt):
+        prompt = np.ascontiguousarray(prompt, np.int32)
+        r = self.lib.l98_session_start(C.byref(self.m), C.byref(self.s), _ip(prompt), len(prompt), None)
+        if r < 0:
+            raise RuntimeError(f"l98_session_start failed: {r}")
+        return r
+
+    def greedy_rounds(self, k, n_rounds, use_graph=True, detail=False):
+        """Runs n greedy rounds on the device; returns (tokens, n_accept, device_ms)
+        (plus per-round distinct experts and new_pos with detail=True)."""
+        cap = n_rounds * (k + 1)
+        toks = np.zeros(cap, np.int32)
+        na = np.zeros(n_rounds, np.int32)
+        ex = np.zeros(n_rounds, np.int32)
+        npos = np.zeros(n_rounds, np.int32)
+        ms = C.c_float()
+        n = self.lib.l98_greedy_rounds_ex(C.byref(self.m), C.byref(self.s), k, n_rounds, 1 if use_graph else 0,
+                                          _ip(toks), cap, _ip(na), _ip(ex), _ip(npos), C.byref(ms))
+        if n < 0:
+            raise RuntimeError(f"l98_greedy_rounds failed: {n}")
+        if detail:
+            return toks[:n], na, ms.value, ex, npos
+        return toks[:n], na, ms.value
+
+    def time_kernel(self, which, mrows, iters):
+        ms = C.c_float()
+        if self.lib.l98_time_kernel(C.byref(self.m), C.byref(self.s), which, mrows, iters, C.byref(ms)) != 0:
+            raise RuntimeError("l98_time_kernel failed")
+        return ms.value
 
     def generate(self, prompt, k, n_new, temp=0.0, topp=1.0, seed=1):
         prompt = np.ascontiguousarray(prompt, np.int32)

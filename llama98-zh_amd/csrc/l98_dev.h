@@ -58,9 +58,18 @@ typedef struct {
     int tok[16];             // tok[0] = anchor, tok[1..k] = drafts
     int targ[16];            // verify argmaxes (targ[k_eff] = bonus)
     int out[16];             // accepted tokens of the round
-    int catch_tok[16];
-    int pad[16];
+    int catch_tok[16];       // catch-up tokens; rows past catch_n carry a valid stand-in id
+    int round;               // rounds completed since the history was cleared
+    int expert_tally;        // distinct experts streamed by the MoE layers since the last round record
+    int pad[14];
 } DevCtl;
+
+// One finished round as the host reads it back.
+typedef struct {
+    int n_accept, k_eff, new_pos, ssm_slot;
+    int experts;             // distinct (layer, expert) weight sets the round's verify streamed
+    int out[8];
+} RoundRec;
 
 typedef struct {
     const float *qc, *kc, *vc;          // conv outputs [nt][key|key|value]

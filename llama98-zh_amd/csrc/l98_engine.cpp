@@ -52,13 +52,13 @@ int l98k_kda_recur(const KdaRecurArgs *a, int kd, int vd, hipStream_t st);
 int l98k_attn_prep(const AttnArgs *a, int nt, hipStream_t st);
 int l98k_attn_decode(const AttnArgs *a, int nt, int max_len, hipStream_t st);
 int l98k_moe_route(const float *logits, const float *bias, int E, int topk, int nt, int *sel_idx,
-                   float *sel_w, MoeGroups *grp, hipStream_t st);
+                   float *sel_w, MoeGroups *grp, int *tally, hipStream_t st);
 int l98k_moe_combine(const float *h2, const int *sel_idx, const float *sel_w, int topk, int lat,
                      int nt, float *lat_y, int8_t *xq, float *xqs, hipStream_t st);
 int l98k_argmax(const float *x, int n, int rows, int mode, int *out, hipStream_t st);
 int l98k_accept(DevCtl *ctl, const float *vhidden, int d, float *chain, int depth, int brk,
                 hipStream_t st);
-int l98k_set_tokens(DevCtl *ctl, int op, hipStream_t st);
+int l98k_set_tokens(DevCtl *ctl, int op, RoundRec *hist, int hist_cap, hipStream_t st);
 }
 
 #define CK(x)                                                                   \
@@ -484,7 +484,10 @@ struct DState {
     int *tokbuf;
     DevCtl *ctl_pinned = nullptr;
     int cap_rows = 0;                       // rows of hcap / tokbuf
+    RoundRec *hist = nullptr;               // device round records
+    int hist_cap = 0;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    hipGraphExec_t round_graph[LZ_SPEC_K_MAX + 1] = {};
 };
 
 namespace {
@@ -543,6 +546,8 @@ bool carve(DState *s) {
     s->grp = (MoeGroups *)st_take(s, sizeof(MoeGroups));
     s->ctl = (DevCtl *)st_take(s, sizeof(DevCtl));
     s->tokbuf = (int *)st_take(s, sizeof(int) * (size_t)s->cap_rows);
+    s->hist_cap = s->seq_len;
+    s->hist = (RoundRec *)st_take(s, sizeof(RoundRec) * (size_t)s->hist_cap);
     return true;
 }
 
@@ -669,7 +674,7 @@ int moe_block(DState *s, const DLayer &L, int nt) {
     const int lat = c.moe_latent_dim, inter = c.moe_intermediate_size, sw = c.moe_shared_width;
     CK(gemv(s, {J(L.router, s->rl, E), J(L.down, s->latx, lat), J(L.sg, s->sgo, sw), J(L.su, s->suo, sw)},
             s->xq, s->xqs, d, nt));
-    CK(l98k_moe_route(s->rl, L.bias, E, topk, nt, s->sel_idx, s->sel_w, s->grp, s->st));
+    CK(l98k_moe_route(s->rl, L.bias, E, topk, nt, s->sel_idx, s->sel_w, s->grp, &s->ctl->expert_tally, s->st));
     CK(l98k_quant_rows(s->latx, lat, lat, nt, s->xq2, s->xqs2, s->st));
     int max_groups = nt * topk < E ? nt * topk : E;
     CK(l98k_expert_gemv(&L.w1, s->grp, max_groups, s->xq2, s->xqs2, 0, s->h1, lat, inter, nt, s->st));
@@ -825,6 +830,8 @@ extern "C" void lz_state_free(LZRunState *s) {
         if (d->ctl_pinned) (void)hipHostFree(d->ctl_pinned);
         if (d->ev0) (void)hipEventDestroy(d->ev0);
         if (d->ev1) (void)hipEventDestroy(d->ev1);
+        for (auto &g : d->round_graph)
+            if (g) (void)hipGraphExecDestroy(g);
         if (d->st) (void)hipStreamDestroy(d->st);
         delete d;
     }
@@ -1207,18 +1214,30 @@ extern "C" int lz_spec_accept_temp(const float *p, const float *q, int x, int vo
 
 namespace {
 
-// Enqueues one greedy round on the device (drafts, verify, argmaxes,
-// acceptance, ring rollback, chain reseed); reads nothing back.
-int enqueue_greedy_round(DState *d, int k, int max_pos, int brk) {
+// Enqueues one greedy round on the device: k draft steps (argmax into
+// ctl->tok), the (k+1)-token verify, the per-row argmaxes, acceptance with
+// ring rollback and chain reseed, the MTP catch-up of the accepted drafts
+// (always k-1 rows, see k_accept), then the round record and the advance to
+// the next round.  Reads nothing back; every scalar lives in ctl, so the
+// sequence is graph-capturable.
+int enqueue_verify_accept(DState *d, int k_eff, int max_pos, int brk, bool catchup) {
+    const LZModelConfig &c = d->m->c;
+    CK(forward_chunk(d, d->ctl->tok, k_eff + 1, &d->ctl->anchor_pos, 1, max_pos, d->vhidden, true,
+                     d->mtp_logits, false));
+    CK(l98k_argmax(d->mtp_logits, c.vocab_size, k_eff + 1, 0, d->ctl->targ, d->st));
+    CK(l98k_accept(d->ctl, d->vhidden, c.hidden_size, d->chain, d->depth, brk, d->st));
+    if (catchup && k_eff > 1)
+        CK(mtp_prefill_dev(d, d->vhidden, d->ctl->catch_tok, k_eff - 1, &d->ctl->catch_pos, 0));
+    CK(l98k_set_tokens(d->ctl, 1, d->hist, d->hist_cap, d->st));
+    return 0;
+}
+
+int enqueue_greedy_round(DState *d, int k, int max_pos, int brk, bool catchup) {
     const LZModelConfig &c = d->m->c;
     for (int i = 0; i < k; i++)
         CK(draft_step(d, d->ctl->tok + i, &d->ctl->mtp_pos, i, max_pos, d->draft_logits + (size_t)i * c.vocab_size,
                       d->ctl->tok + 1 + i));
-    CK(forward_chunk(d, d->ctl->tok, k + 1, &d->ctl->anchor_pos, 1, max_pos, d->vhidden, true,
-                     d->mtp_logits, false));
-    CK(l98k_argmax(d->mtp_logits, c.vocab_size, k + 1, 0, d->ctl->targ, d->st));
-    CK(l98k_accept(d->ctl, d->vhidden, c.hidden_size, d->chain, d->depth, brk, d->st));
-    return 0;
+    return enqueue_verify_accept(d, k, max_pos, brk, catchup);
 }
 
 int errset(char *errbuf, int errlen, int code, const char *msg) {
@@ -1245,59 +1264,45 @@ extern "C" int lz_spec_round(const LZModel *mm, LZRunState *s, int anchor, int a
     if (anchor < 0 || anchor >= c.vocab_size || anchor_pos + 1 + k >= d->seq_len ||
         s->mtp_pos + k > d->seq_len)
         return errset(errbuf, errlen, LZ_ERR_FORWARD, "forward failed (token/position out of range)");
+    const int max_pos = d->seq_len - 1;
     DevCtl h = ctl_from(s);
     h.anchor = anchor;
     h.anchor_pos = anchor_pos;
     h.tok[0] = anchor;
     h.k_eff = k;
+    if (ctl_put(d, h)) return -LZ_ERR_FORWARD;
     int k_eff = k;
-    if (p_min > 0.0f) {
-        // p_min needs each step's top-1 probability before deciding on the
-        // next: drafts run one at a time with a host read-back.
-        if (ctl_put(d, h)) return -LZ_ERR_FORWARD;
+    if (p_min > 0.0f || k_eff < n_min) {
+        // The draft loop decides k_eff on the host: p_min needs each step's
+        // top-1 probability before the next step (lz_argmax_p1's online
+        // softmax, run on the host copy of the logits).
         std::vector<float> lg(c.vocab_size);
         k_eff = 0;
         for (int i = 0; i < k; i++) {
-            if (draft_step(d, d->ctl->tok + i, &d->ctl->mtp_pos, i, s->mtp_pos + k,
-                           d->draft_logits, d->ctl->tok + 1 + i))
+            if (draft_step(d, d->ctl->tok + i, &d->ctl->mtp_pos, i, max_pos, d->draft_logits,
+                           d->ctl->tok + 1 + i))
                 return -LZ_ERR_FORWARD;
-            if (hipMemcpyAsync(lg.data(), d->draft_logits, sizeof(float) * c.vocab_size,
-                               hipMemcpyDeviceToHost, d->st) || hipStreamSynchronize(d->st))
-                return -LZ_ERR_FORWARD;
-            float p1;
-            int idx = lz_argmax_p1(lg.data(), c.vocab_size, &p1);
-            if (p1 < p_min) break;
-            h.tok[1 + i] = idx;
+            if (p_min > 0.0f) {
+                if (hipMemcpyAsync(lg.data(), d->draft_logits, sizeof(float) * c.vocab_size,
+                                   hipMemcpyDeviceToHost, d->st) || hipStreamSynchronize(d->st))
+                    return -LZ_ERR_FORWARD;
+                float p1;
+                (void)lz_argmax_p1(lg.data(), c.vocab_size, &p1);
+                if (p1 < p_min) break;
+            }
             k_eff = i + 1;
         }
         if (k_eff < n_min) {
-            out[0] = anchor; *out_n_accept = 0; *out_new_pos = anchor_pos; *out_k_eff = k_eff;
-            return 0;
-        }
-        h.k_eff = k_eff;
-        if (ctl_get(d, &h)) return -LZ_ERR_FORWARD;
-        h.k_eff = k_eff;
-        if (ctl_put(d, h)) return -LZ_ERR_FORWARD;
-        if (forward_chunk(d, d->ctl->tok, k_eff + 1, &d->ctl->anchor_pos, 1, anchor_pos + k_eff + 1,
-                          d->vhidden, true, d->mtp_logits, false) ||
-            l98k_argmax(d->mtp_logits, c.vocab_size, k_eff + 1, 0, d->ctl->targ, d->st) ||
-            l98k_accept(d->ctl, d->vhidden, c.hidden_size, d->chain, d->depth, brk, d->st))
-            return -LZ_ERR_FORWARD;
-    } else {
-        if (k_eff < n_min) {
-            // every draft step still runs (its MTP KV rows are written)
-            if (ctl_put(d, h)) return -LZ_ERR_FORWARD;
-            for (int i = 0; i < k; i++)
-                if (draft_step(d, d->ctl->tok + i, &d->ctl->mtp_pos, i, s->mtp_pos + k, d->draft_logits,
-                               d->ctl->tok + 1 + i))
-                    return -LZ_ERR_FORWARD;
             if (hipStreamSynchronize(d->st)) return -LZ_ERR_FORWARD;
             out[0] = anchor; *out_n_accept = 0; *out_new_pos = anchor_pos; *out_k_eff = k_eff;
             return 0;
         }
-        if (ctl_put(d, h)) return -LZ_ERR_FORWARD;
-        if (enqueue_greedy_round(d, k, anchor_pos + k + 1 > s->mtp_pos + k ? anchor_pos + k + 1 : s->mtp_pos + k, brk))
+        int ke = k_eff;
+        if (hipMemcpyAsync(&d->ctl->k_eff, &ke, sizeof(int), hipMemcpyHostToDevice, d->st) ||
+            enqueue_verify_accept(d, k_eff, max_pos, brk, !skipc))
             return -LZ_ERR_FORWARD;
+    } else {
+        if (enqueue_greedy_round(d, k, max_pos, brk, !skipc)) return -LZ_ERR_FORWARD;
     }
     // chain mirror (the reseeded mtp_chain) rides on the same sync as ctl
     if (hipMemcpyAsync(s->mtp_chain, d->chain, sizeof(float) * c.hidden_size, hipMemcpyDeviceToHost, d->st))
@@ -1309,14 +1314,6 @@ extern "C" int lz_spec_round(const LZModel *mm, LZRunState *s, int anchor, int a
     *out_n_accept = n_accept;
     *out_new_pos = anchor_pos + 1 + n_accept;
     *out_k_eff = k_eff;
-    if (n_accept > 1 && !skipc) {
-        DevCtl h2 = h;
-        h2.pos_scratch = s->mtp_pos + 1;
-        if (ctl_put(d, h2) ||
-            mtp_prefill_dev(d, d->vhidden, d->ctl->out, n_accept - 1, &d->ctl->pos_scratch, 0) ||
-            hipStreamSynchronize(d->st))
-            return -LZ_ERR_FORWARD;
-    }
     s->mtp_pos += n_accept;
     return n_accept + 1;
 }
@@ -1430,19 +1427,20 @@ extern "C" const char *l98_device_name(void) {
     return name;
 }
 
-extern "C" int l98_generate(const LZModel *mm, LZRunState *s, const int *prompt, int n_prompt, int k,
-                            int n_new, const LZSampler *samp, int *tokens, int cap, int *k_eff_out,
-                            int *n_accept_out, int *n_rounds) {
-    if (!mm || !s || !s->impl || !prompt || n_prompt < 2 || !tokens) return -LZ_ERR_NULL_ARG;
+namespace {
+LZSampler g_session_samp;
+bool g_session_greedy = true;
+}
+
+extern "C" int l98_session_start(const LZModel *mm, LZRunState *s, const int *prompt, int n_prompt,
+                                 const LZSampler *samp) {
+    if (!mm || !s || !s->impl || !prompt || n_prompt < 2) return -LZ_ERR_NULL_ARG;
     DState *d = S(s);
     const LZModelConfig &c = d->m->c;
-    if (!tok_ok(c, prompt, n_prompt)) return -LZ_ERR_FORWARD;
-    if (k < 1 || k > LZ_SPEC_K_MAX || k > s->ssm_ring_depth - 1) return -LZ_ERR_SPEC_K_RANGE;
-    const bool greedy = !samp || !(samp->p.temperature > 0.0f);
-    if (n_prompt + n_new + 2 * (k + 1) >= d->seq_len) return -LZ_ERR_FORWARD;
-    LZSampler local{};
-    if (samp) local = *samp;
-    // prefill (src/generate.c:2806-2960)
+    if (!tok_ok(c, prompt, n_prompt) || n_prompt >= d->seq_len) return -LZ_ERR_FORWARD;
+    g_session_greedy = !samp || !(samp->p.temperature > 0.0f);
+    if (samp) g_session_samp = *samp;
+    // prefill + MTP prefill (src/generate.c:2806-2960)
     lz_state_reset(s, mm);
     if (batch_capture_dev(d, s, prompt, n_prompt - 1, 0)) return -LZ_ERR_FORWARD;
     {
@@ -1454,18 +1452,110 @@ extern "C" int l98_generate(const LZModel *mm, LZRunState *s, const int *prompt,
             return -LZ_ERR_FORWARD;
     }
     s->mtp_pos = n_prompt - 1;
-    int n = 0, rounds = 0;
-    int token = prompt[n_prompt - 1], pos = n_prompt - 1;
     // first anchor from a capture forward
-    float *lg = lz_forward_capture(mm, s, token, pos);
+    float *lg = lz_forward_capture(mm, s, prompt[n_prompt - 1], n_prompt - 1);
     if (!lg) return -LZ_ERR_FORWARD;
     std::vector<PI> buf;
-    int anchor = greedy ? lz_sample_argmax(lg, c.vocab_size)
-                        : sample_ex(lg, c.vocab_size, local.p.temperature, local.p.topp, &local.rng_state, buf);
+    int anchor = g_session_greedy
+        ? lz_sample_argmax(lg, c.vocab_size)
+        : sample_ex(lg, c.vocab_size, g_session_samp.p.temperature, g_session_samp.p.topp,
+                    &g_session_samp.rng_state, buf);
+    DevCtl h = ctl_from(s);
+    h.anchor = anchor;
+    h.anchor_pos = n_prompt - 1;
+    h.tok[0] = anchor;
+    if (ctl_put(d, h) || hipStreamSynchronize(d->st)) return -LZ_ERR_FORWARD;
+    return anchor;
+}
+
+extern "C" int l98_greedy_rounds(const LZModel *mm, LZRunState *s, int k, int n_rounds, int use_graph,
+                                 int *tokens, int cap, int *n_accept_out, float *device_ms) {
+    return l98_greedy_rounds_ex(mm, s, k, n_rounds, use_graph, tokens, cap, n_accept_out, nullptr, nullptr,
+                                device_ms);
+}
+
+extern "C" int l98_greedy_rounds_ex(const LZModel *mm, LZRunState *s, int k, int n_rounds, int use_graph,
+                                    int *tokens, int cap, int *n_accept_out, int *experts_out,
+                                    int *new_pos_out, float *device_ms) {
+    if (!mm || !s || !s->impl || n_rounds < 1) return -LZ_ERR_NULL_ARG;
+    if (k < 1 || k > LZ_SPEC_K_MAX || k > s->ssm_ring_depth - 1) return -LZ_ERR_SPEC_K_RANGE;
+    DState *d = S(s);
+    if (n_rounds > d->hist_cap) return -LZ_ERR_NULL_ARG;
+    const int max_pos = d->seq_len - 1;
+    // ctl.round = 0 (records restart at hist[0]); k_eff = k
+    {
+        DevCtl h;
+        if (ctl_get(d, &h)) return -LZ_ERR_FORWARD;
+        if (h.anchor_pos + 1 + (size_t)n_rounds * (k + 1) >= (size_t)d->seq_len ||
+            h.mtp_pos + (size_t)n_rounds * k + k > (size_t)d->seq_len)
+            return -LZ_ERR_FORWARD;
+        h.round = 0;
+        h.expert_tally = 0;
+        h.k_eff = k;
+        if (ctl_put(d, h)) return -LZ_ERR_FORWARD;
+    }
+    if (use_graph && !d->round_graph[k]) {
+        hipGraph_t g = nullptr;
+        if (hipStreamBeginCapture(d->st, hipStreamCaptureModeThreadLocal) != hipSuccess) return -LZ_ERR_FORWARD;
+        int rc = enqueue_greedy_round(d, k, max_pos, 0, true);
+        if (hipStreamEndCapture(d->st, &g) != hipSuccess || rc) return -LZ_ERR_FORWARD;
+        if (hipGraphInstantiate(&d->round_graph[k], g, nullptr, nullptr, 0) != hipSuccess) {
+            (void)hipGraphDestroy(g);
+            return -LZ_ERR_FORWARD;
+        }
+        (void)hipGraphDestroy(g);
+    }
+    (void)hipEventRecord(d->ev0, d->st);
+    for (int r = 0; r < n_rounds; r++) {
+        if (use_graph) {
+            if (hipGraphLaunch(d->round_graph[k], d->st) != hipSuccess) return -LZ_ERR_FORWARD;
+        } else if (enqueue_greedy_round(d, k, max_pos, 0, true)) {
+            return -LZ_ERR_FORWARD;
+        }
+    }
+    (void)hipEventRecord(d->ev1, d->st);
+    if (hipEventSynchronize(d->ev1) != hipSuccess) return -LZ_ERR_FORWARD;
+    float ms = 0.0f;
+    (void)hipEventElapsedTime(&ms, d->ev0, d->ev1);
+    if (device_ms) *device_ms = ms;
+    g_last_loop_s = ms * 1e-3;
+    std::vector<RoundRec> rec((size_t)n_rounds);
+    if (hipMemcpy(rec.data(), d->hist, sizeof(RoundRec) * rec.size(), hipMemcpyDeviceToHost) != hipSuccess)
+        return -LZ_ERR_FORWARD;
+    int n = 0;
+    for (int r = 0; r < n_rounds; r++) {
+        if (n_accept_out) n_accept_out[r] = rec[r].n_accept;
+        if (experts_out) experts_out[r] = rec[r].experts;
+        if (new_pos_out) new_pos_out[r] = rec[r].new_pos;
+        for (int j = 0; j <= rec[r].n_accept; j++) {
+            if (tokens && n < cap) tokens[n] = rec[r].out[j];
+            n++;
+        }
+    }
+    DevCtl h;
+    if (ctl_get(d, &h)) return -LZ_ERR_FORWARD;
+    s->ssm_slot = h.slot_base;
+    s->mtp_pos = h.mtp_pos;
+    if (hipMemcpy(s->mtp_chain, d->chain, sizeof(float) * d->m->c.hidden_size, hipMemcpyDeviceToHost) != hipSuccess)
+        return -LZ_ERR_FORWARD;
+    return n;
+}
+
+extern "C" int l98_generate(const LZModel *mm, LZRunState *s, const int *prompt, int n_prompt, int k,
+                            int n_new, const LZSampler *samp, int *tokens, int cap, int *k_eff_out,
+                            int *n_accept_out, int *n_rounds) {
+    if (!mm || !s || !s->impl || !prompt || n_prompt < 2 || !tokens) return -LZ_ERR_NULL_ARG;
+    if (k < 1 || k > LZ_SPEC_K_MAX || k > s->ssm_ring_depth - 1) return -LZ_ERR_SPEC_K_RANGE;
+    DState *d = S(s);
+    if (n_prompt + n_new + 2 * (k + 1) >= d->seq_len) return -LZ_ERR_FORWARD;
+    int anchor = l98_session_start(mm, s, prompt, n_prompt, samp);
+    if (anchor < 0) return anchor;
+    int n = 0, rounds = 0;
     if (n < cap) tokens[n] = anchor;
     n++;
-    int anchor_pos = pos;
-    if (!greedy) {
+    if (!g_session_greedy) {
+        LZSampler local = g_session_samp;
+        int anchor_pos = n_prompt - 1;
         while (n < n_new) {
             int out[LZ_SPEC_K_MAX + 1], na = 0, np = 0, ke = 0;
             int r = lz_spec_round_temp(mm, s, anchor, anchor_pos, k, 0.0f, 0, &local, 0, 0, out, &na, &np, &ke,
@@ -1481,67 +1571,55 @@ extern "C" int l98_generate(const LZModel *mm, LZRunState *s, const int *prompt,
         if (n_rounds) *n_rounds = rounds;
         return n;
     }
-    // Greedy: rounds are enqueued back to back; each round's control block
-    // is derived on the device from the previous one, and the host reads
-    // the accepted tokens of a round only after the next one is queued.
-    {
-        DevCtl h = ctl_from(s);
-        h.anchor = anchor; h.anchor_pos = anchor_pos; h.k_eff = k;
-        h.tok[0] = anchor;
-        if (ctl_put(d, h)) return -LZ_ERR_FORWARD;
-    }
-    const int max_pos = n_prompt + n_new + 2 * (k + 1);
-    (void)hipEventRecord(d->ev0, d->st);
-    std::vector<DevCtl> hist;
-    // With k drafts a round emits at least one token, so n_new rounds bound
-    // the loop; rounds are read back in batches.
-    const int batch = 8;
+    // Greedy: every round emits at least one token, so at most n_new - 1
+    // more rounds; run them in device batches and stop at n_new.
+    std::vector<int> na(n_new + 8);
     while (n < n_new) {
-        int nb = 0;
-        size_t base_idx = hist.size();
-        for (; nb < batch; nb++) {
-            if (enqueue_greedy_round(d, k, max_pos, 0)) return -LZ_ERR_FORWARD;
-            // catch-up for the accepted drafts (count from the device):
-            // kernels past catch_n are skipped by reading ctl->catch_n.
-            // The catch-up rows are at most k-1; they are written with a
-            // device-side count below.
-            hist.push_back(DevCtl{});
-            if (hipMemcpyAsync(d->ctl_pinned, d->ctl, sizeof(DevCtl), hipMemcpyDeviceToHost, d->st)) return -LZ_ERR_FORWARD;
-            if (hipStreamSynchronize(d->st)) return -LZ_ERR_FORWARD;
-            DevCtl cur = *d->ctl_pinned;
-            hist.back() = cur;
-            if (cur.catch_n > 0) {
-                DevCtl h2 = cur;
-                h2.pos_scratch = cur.catch_pos;
-                if (ctl_put(d, h2) ||
-                    mtp_prefill_dev(d, d->vhidden, d->ctl->out, cur.catch_n, &d->ctl->pos_scratch, 0))
-                    return -LZ_ERR_FORWARD;
-            }
-            if (l98k_set_tokens(d->ctl, 1, d->st) || l98k_set_tokens(d->ctl, 0, d->st)) return -LZ_ERR_FORWARD;
-            {
-                int tot = n;
-                for (size_t i = base_idx; i < hist.size(); i++) tot += hist[i].n_accept + 1;
-                if (tot >= n_new) { nb++; break; }
-            }
-        }
-        for (size_t i = base_idx; i < hist.size(); i++) {
-            const DevCtl &r = hist[i];
-            if (k_eff_out) k_eff_out[rounds] = r.k_eff;
-            if (n_accept_out) n_accept_out[rounds] = r.n_accept;
+        int want = n_new - n;
+        int batch = want < 64 ? want : 64;
+        std::vector<int> tk((size_t)batch * (k + 1));
+        int got = l98_greedy_rounds(mm, s, k, batch, 1, tk.data(), (int)tk.size(), na.data(), nullptr);
+        if (got < 0) return got;
+        int pos = 0;
+        for (int r = 0; r < batch && n < n_new; r++) {
+            if (k_eff_out) k_eff_out[rounds] = k;
+            if (n_accept_out) n_accept_out[rounds] = na[r];
             rounds++;
-            for (int j = 0; j <= r.n_accept; j++) { if (n < cap) tokens[n] = r.out[j]; n++; }
+            for (int j = 0; j <= na[r]; j++) { if (n < cap) tokens[n] = tk[pos + j]; n++; }
+            pos += na[r] + 1;
         }
-    }
-    (void)hipEventRecord(d->ev1, d->st);
-    (void)hipEventSynchronize(d->ev1);
-    float ms = 0.0f;
-    (void)hipEventElapsedTime(&ms, d->ev0, d->ev1);
-    g_last_loop_s = ms * 1e-3;
-    {
-        DevCtl last = hist.back();
-        s->ssm_slot = last.ssm_slot;
-        s->mtp_pos = last.mtp_pos_next;
     }
     if (n_rounds) *n_rounds = rounds;
     return n;
+}
+
+// Times `iters` back-to-back launches of one kernel of the round with HIP
+// events on the state's stream.  which: 0 = tied lm_head GEMV (vocab rows,
+// hidden input) with mrows token rows.  Returns 0 and the mean per launch.
+extern "C" int l98_time_kernel(const LZModel *mm, LZRunState *s, int which, int mrows, int iters,
+                               float *avg_ms) {
+    if (!mm || !s || !s->impl || iters < 1 || mrows < 1 || mrows > MAX_CHUNK || !avg_ms) return 1;
+    DState *d = S(s);
+    const DModel *m = d->m;
+    const LZModelConfig &c = m->c;
+    if (which != 0 && which != 1) return 1;
+    // which 1: the verify forward of mrows tokens (ctl->tok at ctl->anchor_pos
+    // + 1..).  It reads the ring state at ctl->slot_base and writes the slots
+    // after it and KV rows the next verify rewrites, so repeated launches read
+    // identical inputs and leave the session's state usable.
+    auto once = [&]() -> int {
+        if (which == 0) return gemv(d, {J(m->embed, d->mtp_logits, c.vocab_size)}, d->xq, d->xqs, c.hidden_size, mrows);
+        return forward_chunk(d, d->ctl->tok, mrows, &d->ctl->anchor_pos, 1, d->seq_len - 1, d->vhidden, true,
+                             d->mtp_logits, false);
+    };
+    if (once()) return 1;
+    (void)hipEventRecord(d->ev0, d->st);
+    for (int i = 0; i < iters; i++)
+        if (once()) return 1;
+    (void)hipEventRecord(d->ev1, d->st);
+    if (hipEventSynchronize(d->ev1) != hipSuccess) return 1;
+    float ms = 0.0f;
+    (void)hipEventElapsedTime(&ms, d->ev0, d->ev1);
+    *avg_ms = ms / (float)iters;
+    return 0;
 }

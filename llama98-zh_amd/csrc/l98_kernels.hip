@@ -662,7 +662,8 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs a) {
 // One block of 64 lanes; lanes parallel over experts.
 __global__ void k_moe_route(const float *__restrict__ logits, const float *__restrict__ bias,
                             int E, int topk, int nt, int *__restrict__ sel_idx,
-                            float *__restrict__ sel_w, MoeGroups *__restrict__ grp) {
+                            float *__restrict__ sel_w, MoeGroups *__restrict__ grp,
+                            int *__restrict__ tally) {
     __shared__ float key[MAX_EXPERTS], score[MAX_EXPERTS];
     __shared__ int s_idx[MAX_TOPK];
     const int lane = threadIdx.x;
@@ -722,6 +723,7 @@ __global__ void k_moe_route(const float *__restrict__ logits, const float *__res
                 grp->member[g][grp->n_members[g]++] = pair;
             }
         grp->n_groups = ng;
+        if (tally) *tally += ng;
     }
 }
 
@@ -802,7 +804,10 @@ __global__ void k_accept(DevCtl *ctl, const float *__restrict__ vhidden, int d,
         // catch-up pairs (verify_hidden[j], out[j]) j < n-1 at mtp_pos+1+j
         ctl->catch_n = n > 1 ? n - 1 : 0;
         ctl->catch_pos = ctl->mtp_pos + 1;
-        for (int j = 0; j < 8; j++) ctl->catch_tok[j] = ctl->out[j];
+        // Catch-up always runs k-1 rows so a round has a fixed shape; rows
+        // j >= catch_n land at MTP positions >= the next round's mtp_pos,
+        // which that round's draft steps overwrite before any read.
+        for (int j = 0; j < 8; j++) ctl->catch_tok[j] = j < ctl->catch_n ? ctl->out[j] : ctl->out[0];
         ctl->mtp_pos_next = ctl->mtp_pos + n;
         s_n = n;
     }
@@ -811,16 +816,32 @@ __global__ void k_accept(DevCtl *ctl, const float *__restrict__ vhidden, int d,
     for (int i = threadIdx.x; i < d; i += blockDim.x) chain[i] = vhidden[(size_t)n * d + i];
 }
 
-// Copies a device int (e.g. next anchor) into the token array.
-__global__ void k_set_tokens(DevCtl *ctl, int op) {
+// Round bookkeeping on the device.  op 0: draft input 0 = anchor.  op 1:
+// record the finished round in hist and advance to the next one as the
+// generation driver does with have_seed (src/generate.c:1850-1866,
+// 2096-2104): anchor = out[n_accept] at position new_pos, mtp_pos and the
+// ring slot carried over.
+__global__ void k_set_tokens(DevCtl *ctl, int op, RoundRec *hist, int hist_cap) {
     if (threadIdx.x != 0) return;
-    if (op == 0) {                 // start of a round: draft input 0 = anchor
+    if (op == 0) {
         ctl->tok[0] = ctl->anchor;
-    } else if (op == 1) {          // advance to the next round (have_seed)
+    } else if (op == 1) {
+        if (hist && ctl->round < hist_cap) {
+            RoundRec *r = hist + ctl->round;
+            r->n_accept = ctl->n_accept;
+            r->k_eff = ctl->k_eff;
+            r->new_pos = ctl->new_pos;
+            r->ssm_slot = ctl->ssm_slot;
+            r->experts = ctl->expert_tally;
+            for (int j = 0; j < 8; j++) r->out[j] = ctl->out[j];
+        }
+        ctl->expert_tally = 0;
+        ctl->round++;
         ctl->anchor = ctl->out[ctl->n_accept];
-        ctl->anchor_pos = ctl->new_pos;                  // new anchor sits at new_pos + 1 - 1
+        ctl->anchor_pos = ctl->new_pos;
         ctl->mtp_pos = ctl->mtp_pos_next;
         ctl->slot_base = ctl->ssm_slot;
+        ctl->tok[0] = ctl->anchor;
     }
 }
 
@@ -938,10 +959,10 @@ extern "C" int l98k_attn_decode(const AttnArgs *a, int nt, int max_len, hipStrea
 }
 
 extern "C" int l98k_moe_route(const float *logits, const float *bias, int E, int topk, int nt,
-                              int *sel_idx, float *sel_w, MoeGroups *grp, hipStream_t st) {
+                              int *sel_idx, float *sel_w, MoeGroups *grp, int *tally, hipStream_t st) {
     if (E > MAX_EXPERTS || topk > MAX_TOPK) return -1;
     hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(64), 0, st, logits, bias, E, topk, nt, sel_idx,
-                       sel_w, grp);
+                       sel_w, grp, tally);
     return (int)hipGetLastError();
 }
 
@@ -964,7 +985,7 @@ extern "C" int l98k_accept(DevCtl *ctl, const float *vhidden, int d, float *chai
     return (int)hipGetLastError();
 }
 
-extern "C" int l98k_set_tokens(DevCtl *ctl, int op, hipStream_t st) {
-    hipLaunchKernelGGL(k_set_tokens, dim3(1), dim3(64), 0, st, ctl, op);
+extern "C" int l98k_set_tokens(DevCtl *ctl, int op, RoundRec *hist, int hist_cap, hipStream_t st) {
+    hipLaunchKernelGGL(k_set_tokens, dim3(1), dim3(64), 0, st, ctl, op, hist, hist_cap);
     return (int)hipGetLastError();
 }
