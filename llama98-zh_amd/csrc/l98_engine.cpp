@@ -1468,6 +1468,17 @@ extern "C" int l98_session_start(const LZModel *mm, LZRunState *s, const int *pr
     return anchor;
 }
 
+// Rounds that stay inside the state whatever they accept: a round's verify
+// writes positions up to anchor_pos + k + 1 and advances the anchor by at
+// most k + 1; its drafts and catch-up write MTP rows up to mtp_pos + k - 1
+// and advance mtp_pos by at most k.
+static int rounds_that_fit(const DState *d, const DevCtl &h, int k) {
+    long a = ((long)d->seq_len - 2 - h.anchor_pos - k) / (k + 1) + 1;
+    long b = ((long)d->seq_len - h.mtp_pos - k) / k + 1;
+    long r = a < b ? a : b;
+    return r < 0 ? 0 : (int)r;
+}
+
 extern "C" int l98_greedy_rounds(const LZModel *mm, LZRunState *s, int k, int n_rounds, int use_graph,
                                  int *tokens, int cap, int *n_accept_out, float *device_ms) {
     return l98_greedy_rounds_ex(mm, s, k, n_rounds, use_graph, tokens, cap, n_accept_out, nullptr, nullptr,
@@ -1486,9 +1497,7 @@ extern "C" int l98_greedy_rounds_ex(const LZModel *mm, LZRunState *s, int k, int
     {
         DevCtl h;
         if (ctl_get(d, &h)) return -LZ_ERR_FORWARD;
-        if (h.anchor_pos + 1 + (size_t)n_rounds * (k + 1) >= (size_t)d->seq_len ||
-            h.mtp_pos + (size_t)n_rounds * k + k > (size_t)d->seq_len)
-            return -LZ_ERR_FORWARD;
+        if (n_rounds > rounds_that_fit(d, h, k)) return -LZ_ERR_FORWARD;
         h.round = 0;
         h.expert_tally = 0;
         h.k_eff = k;
@@ -1577,6 +1586,13 @@ extern "C" int l98_generate(const LZModel *mm, LZRunState *s, const int *prompt,
     while (n < n_new) {
         int want = n_new - n;
         int batch = want < 64 ? want : 64;
+        {
+            DevCtl h;
+            if (ctl_get(d, &h)) return -LZ_ERR_FORWARD;
+            int fit = rounds_that_fit(d, h, k);
+            if (fit < 1) return -LZ_ERR_FORWARD;
+            if (batch > fit) batch = fit;
+        }
         std::vector<int> tk((size_t)batch * (k + 1));
         int got = l98_greedy_rounds(mm, s, k, batch, 1, tk.data(), (int)tk.size(), na.data(), nullptr);
         if (got < 0) return got;
