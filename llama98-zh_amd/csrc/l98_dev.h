@@ -10,20 +10,20 @@
 #define MAX_CHUNK 8          // tokens per forward chunk (the reference's LZ_BATCH_MAX)
 #define MAX_PAIRS (MAX_CHUNK * MAX_TOPK)
 
-// One weight matrix of a fused GEMV launch.  All jobs of a launch share the
-// input width; activations default to the launch's xq/xqs unless a job
-// brings its own.
+// One weight matrix of a fused GEMV launch.  Jobs of one launch may differ
+// in input width; each brings its own int8 activations.
 typedef struct {
-    const int8_t *w;         // [rows][in] int8, row-major
+    const int8_t *w;         // [rows][in_dim] int8, row-major
     const float *ws;         // [rows] per-row scale
     float *out;              // out[t * out_stride + row]
-    const int8_t *xq;        // optional per-job activations [M][in]
-    const float *xqs;        // optional per-job scales [M][in/32]
-    const int *count;        // optional device flag: skip the job when *count <= 0
-    int32_t *acc_out;        // optional exact group sums [M][rows][in/32] (tests)
+    const int8_t *xq;        // activations [M][in_dim]
+    const float *xqs;        // activation scales [M][in_dim/32]
+    int32_t *acc_out;        // optional exact group sums [M][rows][in_dim/32] (tests)
     int rows;
+    int in_dim;
     int out_stride;
     int tile0;               // first tile of this job in the launch grid (set by the launcher)
+    int R;                   // rows per tile (set by the launcher)
     int pad;
 } GemvJob;
 
@@ -38,6 +38,18 @@ typedef struct {
     const int8_t *q;
     const float *s;
 } ExpertBank;
+
+// One projection of a grouped expert GEMV launch (up to two per launch,
+// e.g. w1 and w3 over the same activations).
+typedef struct {
+    const int8_t *q;         // bank: expert e rows [e*out_rows, (e+1)*out_rows)
+    const float *s;
+    float *out;              // out[pair * out_rows + row]
+    const int8_t *xq;        // activation rows (by token or by pair)
+    const float *xqs;
+    int xq_by_pair;          // 1: activation row = pair index, 0: = the pair's token
+    int pad;
+} ExpertJob;
 
 // Distinct experts selected by a chunk and their (token, slot) members.
 typedef struct {
@@ -96,7 +108,9 @@ typedef struct {
     float *qh;                          // [nt][q_dim] normed + rotated q
     int8_t *kcache, *vcache;            // plane base [seq][kv_dim]
     float *kscale, *vscale;             // plane base [seq][kv_dim/32]
-    float *out;                         // [nt][q_dim] gated attention output
+    float *out;                         // optional [nt][q_dim] gated attention output (tests)
+    int8_t *oq;                         // [nt][q_dim] its per-32 quantization (o_proj input)
+    float *oqs;                         // [nt][q_dim/32]
     const int *ctl_pos;                 // position of token 0 = *ctl_pos + pos_off
     int pos_off;
     int nh, nkv, hd, rot, q_dim, qg_dim, kv_dim, kv_only;

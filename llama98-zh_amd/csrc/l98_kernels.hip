@@ -19,16 +19,24 @@
 #include <stdint.h>
 
 #include "l98_dev.h"
+#include "l98_launch.h"
 
 // ---------------------------------------------------------------- math ---
 
 __constant__ float c_exp_tab[32];
 
+// The 2^(i/32) table of d_exp is indexed by a per-lane value, so it is read
+// from LDS (one ds_read) rather than constant memory (a vector memory load).
+#define DECLARE_EXP_TAB(tab)                                      \
+    __shared__ float tab[32];                                      \
+    if (threadIdx.x < 32) tab[threadIdx.x] = c_exp_tab[threadIdx.x]; \
+    __syncthreads()
+
 __device__ __forceinline__ float f_from_u(uint32_t u) { return __uint_as_float(u); }
 __device__ __forceinline__ uint32_t u_from_f(float f) { return __float_as_uint(f); }
 
 // lz_exp_float_body, src/ops_quant.c:300-349
-__device__ __forceinline__ float d_exp(float x) {
+__device__ __forceinline__ float d_exp(float x, const float *tab) {
     const float C2 = 0.242844437f, C1 = 0.207425515f, C0 = 0.549730133f;
     const float LOG2E32 = 1.44269504f * 32.0f;
     if (x > 88.0f) return 3.40282347e+38f;
@@ -42,7 +50,7 @@ __device__ __forceinline__ float d_exp(float x) {
     float w = 1.0f + r * 0.03125f;
     float p2n = f_from_u((uint32_t)(n + 127) << 23);
     float c = (C2 * w + C1) * w + C0;
-    return p2n * (c_exp_tab[idx] * c);
+    return p2n * (tab[idx] * c);
 }
 
 // lz_rsqrt_float_body, src/ops_quant.c:126-135
@@ -55,24 +63,24 @@ __device__ __forceinline__ float d_rsqrt(float x) {
 }
 
 // lz_sigmoid float branch, src/ops_quant.c:1816-1853
-__device__ __forceinline__ float d_sigmoid(float x) {
+__device__ __forceinline__ float d_sigmoid(float x, const float *tab) {
     if (x >= 0.0f) {
-        float z = d_exp(-x);
+        float z = d_exp(-x, tab);
         return 1.0f / (1.0f + z);
     }
-    float z = d_exp(x);
+    float z = d_exp(x, tab);
     return z / (1.0f + z);
 }
-__device__ __forceinline__ float d_silu(float x) { return x * d_sigmoid(x); }
+__device__ __forceinline__ float d_silu(float x, const float *tab) { return x * d_sigmoid(x, tab); }
 
 // lz_softplus_poly, src/ops_quant.c:1040-1060
-__device__ __forceinline__ float d_softplus(float x) {
+__device__ __forceinline__ float d_softplus(float x, const float *tab) {
     const float L[9] = {1.000000000f, -0.499995530f, 0.333203435f, -0.248529464f,
                         0.191451162f, -0.137466222f, 0.079210736f, -0.030110965f,
                         0.005384062f};
     if (x > 16.0f) return x;
     float nx = (x < 0.0f) ? x : -x;
-    float u = d_exp(nx);
+    float u = d_exp(nx, tab);
     float p = L[8];
 #pragma unroll
     for (int i = 7; i >= 0; i--) p = p * u + L[i];
@@ -101,6 +109,9 @@ __device__ __forceinline__ uint32_t d_fkey(float f) {
     uint32_t u = u_from_f(f);
     return u ^ ((uint32_t)((int32_t)u >> 31) | 0x80000000u);
 }
+__device__ __forceinline__ float d_unkey(uint32_t k) {
+    return f_from_u((k & 0x80000000u) ? (k ^ 0x80000000u) : ~k);
+}
 
 __device__ __forceinline__ float wave_max_u(uint32_t v, int width) {
     for (int o = width >> 1; o > 0; o >>= 1) {
@@ -108,6 +119,14 @@ __device__ __forceinline__ float wave_max_u(uint32_t v, int width) {
         v = w > v ? w : v;
     }
     return f_from_u(v);
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+    for (int o = 32; o > 0; o >>= 1) {
+        uint64_t w = __shfl_xor(v, o);
+        v = w > v ? w : v;
+    }
+    return v;
 }
 
 // Quantize one 32-element group held one element per lane across a
@@ -134,16 +153,54 @@ __device__ __forceinline__ void d_quant_group32(float x, int8_t *q, float *s) {
     if ((threadIdx.x & 31) == 0) *s = sg;
 }
 
-// Serial left-to-right float sum of n values in LDS (one lane).
+// Serial left-to-right float sum of n values in LDS by one lane.  The adds
+// stay in index order; the LDS reads run a chunk ahead of them (32 values
+// per chunk, double buffered) so the chain is bound by add latency, not by
+// LDS latency.  v must be 16-byte aligned.
 __device__ __forceinline__ float serial_sum(const float *v, int n) {
     float ss = 0.0f;
-    int i = 0;
-    for (; i + 4 <= n; i += 4) {
-        float4 q = *reinterpret_cast<const float4 *>(v + i);
-        ss += q.x; ss += q.y; ss += q.z; ss += q.w;
+    const float4 *v4 = reinterpret_cast<const float4 *>(v);
+    const int nc = n >> 5;                       // full chunks of 32
+    float4 a[8], b[8];
+    if (nc > 0) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) a[j] = v4[j];
     }
-    for (; i < n; i++) ss += v[i];
+    for (int c = 0; c < nc; c++) {
+        if (c + 1 < nc) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) b[j] = v4[(c + 1) * 8 + j];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) { ss += a[j].x; ss += a[j].y; ss += a[j].z; ss += a[j].w; }
+#pragma unroll
+        for (int j = 0; j < 8; j++) a[j] = b[j];
+    }
+    for (int i = nc << 5; i < n; i++) ss += v[i];
     return ss;
+}
+
+// -------------------------------------------------------------- helpers ---
+
+__device__ __forceinline__ int imin(int a, int b) { return a < b ? a : b; }
+
+// Per-32 quantization of `total` contiguous floats (a whole number of groups)
+// by the threads of a block whose size is a multiple of 32.  Element e goes
+// to xq[e], group e/32's scale to xqs[e/32].  Four loads per thread are in
+// flight before the first shuffle.
+__device__ __forceinline__ void quant_span(const float *__restrict__ x, int total, int8_t *__restrict__ xq,
+                                           float *__restrict__ xqs) {
+    const int tid = threadIdx.x, nthr = blockDim.x;
+    for (int base = 0; base < total; base += nthr * 4) {
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) v[u] = x[imin(base + u * nthr + tid, total - 1)];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int e = base + u * nthr + tid;
+            if (base + u * nthr + (tid & ~31) < total) d_quant_group32(v[u], xq + e, xqs + (e >> 5));
+        }
+    }
 }
 
 // -------------------------------------------------------------- embed ---
@@ -161,76 +218,152 @@ __global__ void k_embed(const int8_t *__restrict__ q, const float *__restrict__ 
 
 // ------------------------------------------------------- rmsnorm (+q8) ---
 
-// One 64-lane block per row.  Optionally first folds the residual:
-//   x_row = x_row + (a_row [+ b_row])      (the reference's x += xb2 with
-//   xb2 = up + shared already summed, src/forward.c:1449-1557,
-//   src/forward_moe.c:552)
-// then o = (x*inv)*(1+w) (lz_rmsnorm, src/ops_norm.c:690-747) and, when xq
-// is given, the per-32 int8 quantization of o.
-// LDS: n floats of squares.
-__global__ void k_rmsnorm(float *__restrict__ x, int x_stride, const float *__restrict__ a,
-                          const float *__restrict__ b, const float *__restrict__ w, int n,
-                          float eps, float *__restrict__ out, int out_stride,
-                          int8_t *__restrict__ xq, float *__restrict__ xqs) {
-    extern __shared__ float sh[];
-    int row = blockIdx.x;
-    float *xr = x + (size_t)row * x_stride;
+// RMSNorm(1+w) of one row held by a 64-lane block as v[j] = element
+// j*64 + lane (lz_rmsnorm, src/ops_norm.c:690-747: sum of squares serial in
+// index order, inv = rsqrt(ss/n + eps), o = (x*inv)*(1+w)), then the
+// optional store of o and its per-32 quantization.
+template <int NC>
+__device__ __forceinline__ void norm_row(const float (&v)[NC], const float (&wv)[NC], int n, float eps,
+                                         float *sh, float *s_inv, float *__restrict__ out,
+                                         int8_t *__restrict__ xq, float *__restrict__ xqs) {
     const int lane = threadIdx.x;
-    for (int i = lane; i < n; i += 64) {
-        float v = xr[i];
-        if (a) {
-            float add = a[(size_t)row * n + i];
-            if (b) add = add + b[(size_t)row * n + i];
-            v = v + add;
-            xr[i] = v;
-        }
-        sh[i] = v * v;
+#pragma unroll
+    for (int j = 0; j < NC; j++) {
+        const int i = j * 64 + lane;
+        if (i < n) sh[i] = v[j] * v[j];
     }
     __syncthreads();
-    __shared__ float s_inv;
-    if (lane == 0) s_inv = d_rsqrt(d_ss_over_n(serial_sum(sh, n), n) + eps);
+    if (lane == 0) *s_inv = d_rsqrt(d_ss_over_n(serial_sum(sh, n), n) + eps);
     __syncthreads();
-    float inv = s_inv;
-    for (int base = 0; base < n; base += 64) {
-        int i = base + lane;
-        float o = 0.0f;
-        if (i < n) {
-            o = xr[i] * inv * (1.0f + w[i]);
-            if (out) out[(size_t)row * out_stride + i] = o;
+    const float inv = *s_inv;
+#pragma unroll
+    for (int j = 0; j < NC; j++) {
+        const int i = j * 64 + lane;
+        if (j * 64 < n) {
+            float o = 0.0f;
+            if (i < n) {
+                o = v[j] * inv * (1.0f + wv[j]);
+                if (out) out[i] = o;
+            }
+            if (xq && j * 64 + (lane & ~31) < n) d_quant_group32(o, xq + i, xqs + (i >> 5));
         }
-        if (xq && base + (lane & ~31) < n)
-            d_quant_group32(o, xq + (size_t)row * n + i, xqs + (size_t)row * (n >> 5) + (i >> 5));
     }
 }
 
-// Per-32 quantization of rows (lz_quantize_q8).  block = 64 lanes, one row.
-__global__ void k_quant_rows(const float *__restrict__ x, int n, int x_stride,
-                             int8_t *__restrict__ xq, float *__restrict__ xqs) {
-    int row = blockIdx.x;
-    for (int base = 0; base < n; base += 64) {
-        int i = base + threadIdx.x;
-        if (base + (int)(threadIdx.x & ~31) >= n) break;
-        float v = x[(size_t)row * x_stride + i];
-        d_quant_group32(v, xq + (size_t)row * n + i, xqs + (size_t)row * (n >> 5) + (i >> 5));
+// One 64-lane block per row, n <= 64*NC.  Optionally first folds the
+// residual: x_row = x_row + (a_row [+ b_row]) (the reference's x += xb2 with
+// xb2 = up + shared already summed, src/forward.c:1449-1557,
+// src/forward_moe.c:552), then norm_row.  Every load of the row is issued
+// before the first use.
+template <int NC>
+__global__ __launch_bounds__(64) void k_rmsnorm(float *__restrict__ x, int x_stride,
+                                                const float *__restrict__ a, const float *__restrict__ b,
+                                                const float *__restrict__ w, int n, float eps,
+                                                float *__restrict__ out, int out_stride,
+                                                int8_t *__restrict__ xq, float *__restrict__ xqs) {
+    __shared__ __align__(16) float sh[64 * NC];
+    __shared__ float s_inv;
+    const int row = blockIdx.x, lane = threadIdx.x;
+    float *xr = x + (size_t)row * x_stride;
+    float v[NC], wv[NC];
+#pragma unroll
+    for (int j = 0; j < NC; j++) {
+        const int ic = imin(j * 64 + lane, n - 1);
+        v[j] = xr[ic];
+        wv[j] = w[ic];
     }
+    if (a) {
+        float av[NC];
+#pragma unroll
+        for (int j = 0; j < NC; j++) av[j] = a[(size_t)row * n + imin(j * 64 + lane, n - 1)];
+        if (b) {
+            float bv[NC];
+#pragma unroll
+            for (int j = 0; j < NC; j++) bv[j] = b[(size_t)row * n + imin(j * 64 + lane, n - 1)];
+#pragma unroll
+            for (int j = 0; j < NC; j++) av[j] = av[j] + bv[j];
+        }
+#pragma unroll
+        for (int j = 0; j < NC; j++) {
+            v[j] = v[j] + av[j];
+            const int i = j * 64 + lane;
+            if (i < n) xr[i] = v[j];
+        }
+    }
+    norm_row<NC>(v, wv, n, eps, sh, &s_inv, out ? out + (size_t)row * out_stride : nullptr,
+                 xq ? xq + (size_t)row * n : nullptr, xqs ? xqs + (size_t)row * (n >> 5) : nullptr);
+}
+
+// MTP input rows (lz_mtp_draft_step / lz_mtp_prefill, src/forward_mtp.c:
+// e = embed(tok); concat = [rmsnorm(e, pre_e) | rmsnorm(h, pre_h)], then the
+// per-32 quantization of concat for the fc projection).  blockIdx.y = 0: the
+// embedding half, 1: the hidden half.  d % 32 == 0, so the halves quantize
+// independently.
+template <int NC>
+__global__ __launch_bounds__(64) void k_mtp_pre(const int8_t *__restrict__ emb_q, const float *__restrict__ emb_s,
+                                                const int *__restrict__ toks, const float *__restrict__ h,
+                                                int d, const float *__restrict__ w_e,
+                                                const float *__restrict__ w_h, float eps,
+                                                int8_t *__restrict__ xq, float *__restrict__ xqs) {
+    __shared__ __align__(16) float sh[64 * NC];
+    __shared__ float s_inv;
+    const int r = blockIdx.x, half = blockIdx.y, lane = threadIdx.x;
+    const float *wn = half == 0 ? w_e : w_h;
+    float v[NC], wv[NC];
+    if (half == 0) {
+        const int tok = toks[r];
+        const int8_t *er = emb_q + (size_t)tok * d;
+        const float sc = emb_s[tok];
+#pragma unroll
+        for (int j = 0; j < NC; j++) v[j] = (float)er[imin(j * 64 + lane, d - 1)] * sc;
+    } else {
+#pragma unroll
+        for (int j = 0; j < NC; j++) v[j] = h[(size_t)r * d + imin(j * 64 + lane, d - 1)];
+    }
+#pragma unroll
+    for (int j = 0; j < NC; j++) wv[j] = wn[imin(j * 64 + lane, d - 1)];
+    norm_row<NC>(v, wv, d, eps, sh, &s_inv, nullptr, xq + (size_t)r * 2 * d + (size_t)half * d,
+                 xqs + (size_t)r * (2 * d >> 5) + (size_t)half * (d >> 5));
 }
 
 // g = silu(h1)*h3 then per-32 quantization (lz_ffn_gate_up default branch,
-// src/forward_kda.c:1067-1088, followed by lz_quantize_q8).  Row r reads
-// h1/h3 at r*stride; count may come from device memory (rows beyond it
-// exit).
-__global__ void k_act_quant(const float *__restrict__ h1, const float *__restrict__ h3,
-                            int n, const int *__restrict__ count,
-                            int8_t *__restrict__ xq, float *__restrict__ xqs,
-                            float *__restrict__ g_out) {
-    int row = blockIdx.x;
-    if (count && row >= *count) return;
-    for (int base = 0; base < n; base += 64) {
-        int i = base + threadIdx.x;
-        if (base + (int)(threadIdx.x & ~31) >= n) break;
-        float g = d_silu(h1[(size_t)row * n + i]) * h3[(size_t)row * n + i];
-        if (g_out) g_out[(size_t)row * n + i] = g;
-        d_quant_group32(g, xq + (size_t)row * n + i, xqs + (size_t)row * (n >> 5) + (i >> 5));
+// src/forward_kda.c:1067-1088, followed by lz_quantize_q8), one 64-lane
+// block per row.  Rows [0, rows) come from (h1, h3) of width n, the rest
+// from the second segment (g1, g3) of width n2, so the routed experts' and
+// the shared expert's activations quantize in one launch.
+__global__ __launch_bounds__(64) void k_act_quant(const float *__restrict__ h1, const float *__restrict__ h3,
+                                                  int n, int rows, int8_t *__restrict__ xq,
+                                                  float *__restrict__ xqs, const float *__restrict__ g1,
+                                                  const float *__restrict__ g3, int n2,
+                                                  int8_t *__restrict__ xq2, float *__restrict__ xqs2) {
+    DECLARE_EXP_TAB(tab);
+    const int lane = threadIdx.x;
+    const float *p, *q;
+    int8_t *oq;
+    float *os;
+    int w;
+    if ((int)blockIdx.x < rows) {
+        const int r = blockIdx.x;
+        w = n; p = h1 + (size_t)r * n; q = h3 + (size_t)r * n;
+        oq = xq + (size_t)r * n; os = xqs + (size_t)r * (n >> 5);
+    } else {
+        const int r = blockIdx.x - rows;
+        w = n2; p = g1 + (size_t)r * n2; q = g3 + (size_t)r * n2;
+        oq = xq2 + (size_t)r * n2; os = xqs2 + (size_t)r * (n2 >> 5);
+    }
+    for (int base = 0; base < w; base += 64 * 8) {
+        float pv[8], qv[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int ic = imin(base + j * 64 + lane, w - 1);
+            pv[j] = p[ic];
+            qv[j] = q[ic];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int i = base + j * 64 + lane;
+            if (base + j * 64 + (lane & ~31) < w) d_quant_group32(d_silu(pv[j], tab) * qv[j], oq + i, os + (i >> 5));
+        }
     }
 }
 
@@ -241,169 +374,186 @@ __global__ void k_act_quant(const float *__restrict__ h1, const float *__restric
 // (lz_matmul_xq_nt -> matmul_q8_impl + epi_q8, src/ops_matmul.c:336-466,
 // src/ops_epi.c:983-1017).
 //
-// One 64-lane block streams a tile of R consecutive rows (R*in <= 8 KiB):
-// lane l reads 16-byte chunks l, l+64, ... of the tile, so every 1 KiB of a
-// row is one coalesced wave load.  Each chunk's 16-element partial dot
-// products for all M tokens go to LDS; then R*M lanes each run one
-// (row, token) epilogue, serially over the groups, in the reference order.
-// Weights stream from HBM once per launch regardless of M (M <= 8).
+// A 256-lane block streams one tile of R rows (R*in_dim <= 32 KiB): each
+// wave issues all of its 16-byte weight loads of its 8 KiB quarter (chunks
+// lane, lane+64, ...) and the block stages the M activation rows into LDS
+// before any of them is consumed, so a tile costs one memory latency.  The
+// 16-element partial dot products (v_dot4_i32_i8) of neighbouring lanes add
+// up to the exact 32-element group sums (an integer add, order-free), which
+// go to LDS; then one lane per (row, token) runs the epilogue serially over
+// the groups, in the reference order.  Weights stream once per launch for
+// any M <= 8.
 
+#define GEMV_THREADS 256
+#define GEMV_WAVE_BYTES 8192
+#define GEMV_TILE_BYTES (GEMV_WAVE_BYTES * (GEMV_THREADS / 64))
+#define GEMV_MAXJ (GEMV_WAVE_BYTES / 16 / 64)
+#define GEMV_MAX_IN 4096
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// LDS bytes of one tile: staged activations, their scales, group sums.
+__host__ __device__ inline size_t gemv_lds_bytes(int m, int in_dim, int R) {
+    return (size_t)m * in_dim + (size_t)m * (in_dim >> 5) * 4 + (size_t)R * m * ((in_dim >> 5) + 1) * 4;
+}
+
+// s_xrow[t]: activation row of token slot t (rows of xq / xqs);
+// s_orow[t]: output row of token slot t; nm: live token slots.  The caller
+// fills both tables (first M entries) before the call; they are read after
+// the first barrier.
 template <int M>
-__global__ __launch_bounds__(64) void k_gemv_q8(GemvBatch batch, const int8_t *__restrict__ xq_base,
-                                                 const float *__restrict__ xqs_base, int in_dim,
-                                                 int R) {
-    extern __shared__ int part[];               // [R][M][cpr]
-    int blk = blockIdx.x, j = 0;
-    while (j + 1 < batch.n && blk >= batch.job[j + 1].tile0) j++;
-    const GemvJob &job = batch.job[j];
-    if (job.count && *job.count <= 0) return;
-    const int tile = blk - job.tile0;
-    const int row0 = tile * R;
-    const int rows = job.rows;
-    const int cpr = in_dim >> 4;                // 16-byte chunks per row
-    const int nb = in_dim >> 5;
-    const int8_t *xq = job.xq ? job.xq : xq_base;
-    const float *xqs = job.xqs ? job.xqs : xqs_base;
-    const int8_t *w = job.w + (size_t)row0 * in_dim;
-    const int nchunk = R * cpr;
-    const int lane = threadIdx.x;
-    for (int c = lane; c < nchunk; c += 64) {
-        int r = c / cpr;
-        int p = c - r * cpr;
-        int acc[M];
-        if (row0 + r < rows) {
-            int4 wv = *reinterpret_cast<const int4 *>(w + (size_t)c * 16);
+__device__ __forceinline__ void gemv_tile(const int8_t *__restrict__ wt, const float *__restrict__ ws, int rows_here,
+                                          int in_dim, const int8_t *__restrict__ xq,
+                                          const float *__restrict__ xqs, const int *s_xrow, const int *s_orow,
+                                          int nm, float *__restrict__ out, size_t out_stride, int row0,
+                                          int32_t *__restrict__ acc_out, int acc_rows, char *smem) {
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int cpr = in_dim >> 4, nb = in_dim >> 5;
+    const int nchunk = rows_here * cpr;
+    // weights: one 8 KiB quarter of the tile per wave, all loads in flight
+    int4 wv[GEMV_MAXJ];
+    {
+        const v4i *w4 = reinterpret_cast<const v4i *>(wt);
 #pragma unroll
-            for (int t = 0; t < M; t++) {
-                int4 xv = *reinterpret_cast<const int4 *>(xq + (size_t)t * in_dim + p * 16);
-                int s0 = __builtin_amdgcn_sdot4(wv.x, xv.x, 0, false);
-                s0 = __builtin_amdgcn_sdot4(wv.y, xv.y, s0, false);
-                s0 = __builtin_amdgcn_sdot4(wv.z, xv.z, s0, false);
-                s0 = __builtin_amdgcn_sdot4(wv.w, xv.w, s0, false);
-                acc[t] = s0;
-            }
-        } else {
-#pragma unroll
-            for (int t = 0; t < M; t++) acc[t] = 0;
+        for (int j = 0; j < GEMV_MAXJ; j++) {
+            const int c = imin(wave * (GEMV_WAVE_BYTES / 16) + lane + 64 * j, nchunk - 1);
+            const v4i q = __builtin_nontemporal_load(w4 + c);
+            wv[j] = make_int4(q.x, q.y, q.z, q.w);
         }
+    }
+    // epilogue lane's row scale, also early
+    const int er = tid / M, et = tid - er * M;
+    const float wsv = ws[row0 + imin(er, rows_here - 1)];
+    __syncthreads();                                   // s_xrow / s_orow visible
+    int4 *sx = reinterpret_cast<int4 *>(smem);                            // [M][cpr]
+    float *sxs = reinterpret_cast<float *>(smem + (size_t)M * in_dim);    // [M][nb]
+    int *part = reinterpret_cast<int *>(sxs + M * nb);                    // [R][M][nb+1]
+    {
+        const int total = M * cpr;
+        for (int base = 0; base < total; base += GEMV_THREADS * 4) {
+            int4 r[4];
 #pragma unroll
-        for (int t = 0; t < M; t++) part[(r * M + t) * cpr + p] = acc[t];
+            for (int u = 0; u < 4; u++) {
+                const int idx = imin(base + u * GEMV_THREADS + tid, total - 1);
+                const int t = idx / cpr, p = idx - t * cpr;
+                const int xr = s_xrow[t < nm ? t : 0];
+                r[u] = *reinterpret_cast<const int4 *>(xq + (size_t)xr * in_dim + p * 16);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int idx = base + u * GEMV_THREADS + tid;
+                if (idx < total) sx[idx] = r[u];
+            }
+        }
+        for (int i = tid; i < M * nb; i += GEMV_THREADS) {
+            const int t = i / nb;
+            const int xr = s_xrow[t < nm ? t : 0];
+            sxs[i] = xqs[(size_t)xr * nb + (i - t * nb)];
+        }
     }
     __syncthreads();
-    if (lane < R * M) {
-        int r = lane / M, t = lane - r * M;
-        int row = row0 + r;
-        if (row < rows) {
-            const int *pp = part + (r * M + t) * cpr;
-            const float *xs = xqs + (size_t)t * nb;
-            float dot = 0.0f;
-            for (int g = 0; g < nb; g++) {
-                int a = pp[2 * g] + pp[2 * g + 1];
-                dot += (float)a * xs[g];
+#pragma unroll
+    for (int j = 0; j < GEMV_MAXJ; j++) {
+        const int c = wave * (GEMV_WAVE_BYTES / 16) + lane + 64 * j;
+        const int r = c / cpr, p = c - r * cpr;
+#pragma unroll
+        for (int t = 0; t < M; t++) {
+            int acc = 0;
+            if (t < nm) {
+                const int4 xv = sx[t * cpr + (p < cpr ? p : 0)];
+                acc = __builtin_amdgcn_sdot4(wv[j].x, xv.x, 0, false);
+                acc = __builtin_amdgcn_sdot4(wv[j].y, xv.y, acc, false);
+                acc = __builtin_amdgcn_sdot4(wv[j].z, xv.z, acc, false);
+                acc = __builtin_amdgcn_sdot4(wv[j].w, xv.w, acc, false);
             }
-            float sum = 0.0f;
-            sum += dot * job.ws[row];
-            job.out[(size_t)t * job.out_stride + row] = sum;
-            if (job.acc_out) {
-                for (int g = 0; g < nb; g++)
-                    job.acc_out[((size_t)t * rows + row) * nb + g] = pp[2 * g] + pp[2 * g + 1];
-            }
+            acc += __shfl_xor(acc, 1);                 // chunks 2g and 2g+1 of one row
+            if (c < nchunk && !(lane & 1)) part[(r * M + t) * (nb + 1) + (p >> 1)] = acc;
         }
+    }
+    __syncthreads();
+    if (er < rows_here && et < nm) {
+        const int *pp = part + (er * M + et) * (nb + 1);
+        const float *xs = sxs + et * nb;
+        float dot = 0.0f;
+#pragma unroll 8
+        for (int g = 0; g < nb; g++) dot += (float)pp[g] * xs[g];
+        float sum = 0.0f;
+        sum += dot * wsv;
+        out[(size_t)s_orow[et] * out_stride + row0 + er] = sum;
+        if (acc_out)
+            for (int g = 0; g < nb; g++) acc_out[((size_t)et * acc_rows + row0 + er) * nb + g] = pp[g];
     }
 }
 
-// Grouped expert GEMV: job e = one distinct expert of the chunk with its
-// member (token, slot) pairs; activations are the members' own quantized
-// rows.  Weight rows stream once per distinct expert.
-//   xq rows:   xq_base + member_row * in_dim  (member_row from the group table)
-//   output:    out + member_pair * out_rows + row
 template <int M>
-__global__ __launch_bounds__(64) void k_expert_gemv(const ExpertBank bank, const MoeGroups *__restrict__ grp,
-                                                    const int8_t *__restrict__ xq_base,
-                                                    const float *__restrict__ xqs_base,
-                                                    int xq_by_pair, float *__restrict__ out,
-                                                    int in_dim, int out_rows, int R, int tiles) {
-    extern __shared__ int part[];
-    const int gi = blockIdx.x / tiles;
-    const int tile = blockIdx.x - gi * tiles;
-    if (gi >= grp->n_groups) return;
+__global__ __launch_bounds__(GEMV_THREADS) void k_gemv_q8(GemvBatch batch) {
+    extern __shared__ __align__(16) char smem[];
+    __shared__ int s_row[M];
+    int blk = blockIdx.x, j = 0;
+    while (j + 1 < batch.n && blk >= batch.job[j + 1].tile0) j++;
+    const GemvJob &job = batch.job[j];
+    const int row0 = (blk - job.tile0) * job.R;
+    const int rows_here = imin(job.R, job.rows - row0);
+    if (threadIdx.x < M) s_row[threadIdx.x] = threadIdx.x;
+    gemv_tile<M>(job.w + (size_t)row0 * job.in_dim, job.ws, rows_here, job.in_dim, job.xq, job.xqs, s_row, s_row,
+                 M, job.out, job.out_stride, row0, job.acc_out, job.rows, smem);
+}
+
+// Grouped expert GEMV: block -> (projection jb, group gi, tile).  Group gi
+// is one distinct expert of the chunk with its member (token, slot) pairs;
+// its weight rows stream once for all members.  Output row = pair.
+__global__ __launch_bounds__(GEMV_THREADS) void k_expert_gemv(ExpertJob j0, ExpertJob j1,
+                                                              const MoeGroups *__restrict__ grp,
+                                                              int max_groups, int in_dim, int out_rows, int R,
+                                                              int tiles) {
+    extern __shared__ __align__(16) char smem[];
+    __shared__ int s_xrow[MAX_CHUNK], s_orow[MAX_CHUNK];
+    const int per_job = max_groups * tiles;
+    const int jb = blockIdx.x / per_job;
+    const int rem = blockIdx.x - jb * per_job;
+    const int gi = rem / tiles;
+    const int tile = rem - gi * tiles;
+    const ExpertJob &J = jb == 0 ? j0 : j1;
+    const int ng = grp->n_groups;
+    if (gi >= ng) return;
     const int e = grp->expert[gi];
     const int nm = grp->n_members[gi];
+    if (threadIdx.x < MAX_CHUNK) {
+        const int t = threadIdx.x;
+        const int mem = grp->member[gi][t < nm ? t : 0];
+        s_orow[t] = mem;
+        s_xrow[t] = J.xq_by_pair ? mem : grp->pair_token[mem];
+    }
     const int row0 = tile * R;
-    const int cpr = in_dim >> 4;
-    const int nb = in_dim >> 5;
-    const int8_t *w = bank.q + ((size_t)e * out_rows + row0) * in_dim;
-    const float *ws = bank.s + (size_t)e * out_rows;
-    const int lane = threadIdx.x;
-    const int nchunk = R * cpr;
-    int xrow[M];
-#pragma unroll
-    for (int t = 0; t < M; t++) {
-        int mem = t < nm ? grp->member[gi][t] : grp->member[gi][0];
-        xrow[t] = xq_by_pair ? mem : grp->pair_token[mem];
-    }
-    for (int c = lane; c < nchunk; c += 64) {
-        int r = c / cpr;
-        int p = c - r * cpr;
-        int acc[M];
-        if (row0 + r < out_rows) {
-            int4 wv = *reinterpret_cast<const int4 *>(w + (size_t)c * 16);
-#pragma unroll
-            for (int t = 0; t < M; t++) {
-                acc[t] = 0;
-                if (t < nm) {
-                    int4 xv = *reinterpret_cast<const int4 *>(xq_base + (size_t)xrow[t] * in_dim + p * 16);
-                    int s0 = __builtin_amdgcn_sdot4(wv.x, xv.x, 0, false);
-                    s0 = __builtin_amdgcn_sdot4(wv.y, xv.y, s0, false);
-                    s0 = __builtin_amdgcn_sdot4(wv.z, xv.z, s0, false);
-                    s0 = __builtin_amdgcn_sdot4(wv.w, xv.w, s0, false);
-                    acc[t] = s0;
-                }
-            }
-        } else {
-#pragma unroll
-            for (int t = 0; t < M; t++) acc[t] = 0;
-        }
-#pragma unroll
-        for (int t = 0; t < M; t++) part[(r * M + t) * cpr + p] = acc[t];
-    }
-    __syncthreads();
-    if (lane < R * M) {
-        int r = lane / M, t = lane - r * M;
-        int row = row0 + r;
-        if (row < out_rows && t < nm) {
-            const int *pp = part + (r * M + t) * cpr;
-            const float *xs = xqs_base + (size_t)xrow[t] * nb;
-            float dot = 0.0f;
-            for (int g = 0; g < nb; g++) {
-                int a = pp[2 * g] + pp[2 * g + 1];
-                dot += (float)a * xs[g];
-            }
-            float sum = 0.0f;
-            sum += dot * ws[row];
-            int pair = grp->member[gi][t];
-            out[(size_t)pair * out_rows + row] = sum;
-        }
-    }
+    gemv_tile<MAX_CHUNK>(J.q + ((size_t)e * out_rows + row0) * in_dim, J.s + (size_t)e * out_rows,
+                         imin(R, out_rows - row0), in_dim, J.xq, J.xqs, s_xrow, s_orow, nm, J.out, out_rows,
+                         row0, nullptr, 0, smem);
 }
 
 // ------------------------------------------------------------ KDA conv ---
 
-// Depthwise causal conv (k taps) + SiLU over the [q | k | v] channels, one
+// Depthwise causal conv (K taps) + SiLU over the [q | k | v] channels, one
 // thread per channel, token-serial along the state ring
 // (lz_causal_conv1d_step, src/ops_conv1d.c:26-87; ring slots
-// src/forward_kda.c:680-755).  proj rows: q at qkv[t], k, v at separate
-// strides.
-__global__ void k_kda_conv(const float *__restrict__ pq, const float *__restrict__ pk,
-                           const float *__restrict__ pv, int key, int value,
-                           const float *__restrict__ wconv,      // [conv_dim][K]
-                           float *__restrict__ conv_ring, size_t slot_stride, int K,
-                           const int *__restrict__ ctl_slot, int depth, int advance, int nt,
-                           float *__restrict__ qc, float *__restrict__ kc, float *__restrict__ vc) {
-    int c = blockIdx.x * blockDim.x + threadIdx.x;
-    int conv_dim = 2 * key + value;
+// src/forward_kda.c:680-755).  The last block instead quantizes the gate's
+// low-rank rows pfa [nt][rank] per 32 (input of the f_b projection).
+template <int K>
+__global__ __launch_bounds__(256) void k_kda_conv(const float *__restrict__ pq, const float *__restrict__ pk,
+                                                  const float *__restrict__ pv, int key, int value,
+                                                  const float *__restrict__ wconv,
+                                                  float *__restrict__ conv_ring, size_t slot_stride,
+                                                  const int *__restrict__ ctl_slot, int depth, int advance,
+                                                  int nt, float *__restrict__ qc, float *__restrict__ kc,
+                                                  float *__restrict__ vc, const float *__restrict__ pfa, int rank,
+                                                  int8_t *__restrict__ fq, float *__restrict__ fqs) {
+    DECLARE_EXP_TAB(tab);
+    if (blockIdx.x == gridDim.x - 1) {
+        quant_span(pfa, nt * rank, fq, fqs);
+        return;
+    }
+    constexpr int hist = K - 1;
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    const int conv_dim = 2 * key + value;
     if (c >= conv_dim) return;
-    const int hist = K - 1;
     const float *in;
     float *out;
     int ch, width;
@@ -411,42 +561,65 @@ __global__ void k_kda_conv(const float *__restrict__ pq, const float *__restrict
     else if (c < 2 * key) { in = pk; out = kc; ch = c - key; width = key; }
     else { in = pv; out = vc; ch = c - 2 * key; width = value; }
     const int base = *ctl_slot;
-    float h[8];
+    float h[hist > 0 ? hist : 1], wr[K], xs[MAX_CHUNK];
     const float *st0 = conv_ring + (size_t)base * slot_stride + (size_t)c * hist;
+#pragma unroll
     for (int j = 0; j < hist; j++) h[j] = st0[j];
-    const float *wr = wconv + (size_t)c * K;
-    for (int t = 0; t < nt; t++) {
-        float xv = in[(size_t)t * width + ch];
-        float sum = 0.0f;
-        for (int j = 0; j < hist; j++) sum += wr[j] * h[j];
-        sum += wr[hist] * xv;
-        out[(size_t)t * width + ch] = d_silu(sum);
-        for (int j = 0; j + 1 < hist; j++) h[j] = h[j + 1];
-        if (hist > 0) h[hist - 1] = xv;
-        int so;
-        if (advance) { int si = (base + t) % depth; so = si + 1 == depth ? 0 : si + 1; }
-        else so = base;
-        float *st = conv_ring + (size_t)so * slot_stride + (size_t)c * hist;
-        for (int j = 0; j < hist; j++) st[j] = h[j];
+#pragma unroll
+    for (int j = 0; j < K; j++) wr[j] = wconv[(size_t)c * K + j];
+#pragma unroll
+    for (int t = 0; t < MAX_CHUNK; t++) xs[t] = in[(size_t)imin(t, nt - 1) * width + ch];
+#pragma unroll
+    for (int t = 0; t < MAX_CHUNK; t++) {
+        if (t < nt) {
+            const float xv = xs[t];
+            float sum = 0.0f;
+#pragma unroll
+            for (int j = 0; j < hist; j++) sum += wr[j] * h[j];
+            sum += wr[hist] * xv;
+            out[(size_t)t * width + ch] = d_silu(sum, tab);
+#pragma unroll
+            for (int j = 0; j + 1 < hist; j++) h[j] = h[j + 1];
+            if (hist > 0) h[hist - 1] = xv;
+            int so;
+            if (advance) { int si = (base + t) % depth; so = si + 1 == depth ? 0 : si + 1; }
+            else so = base;
+            if (advance || t == nt - 1) {
+                float *st = conv_ring + (size_t)so * slot_stride + (size_t)c * hist;
+#pragma unroll
+                for (int j = 0; j < hist; j++) st[j] = h[j];
+            }
+        }
     }
 }
 
 // ------------------------------------------------------ KDA recurrence ---
 //
 // One block per value head; lane j owns column j of the fp32 state S[kd][vd]
-// (registers).  Per token, serially: l2norm(q)*scale, l2norm(k), beta,
-// the per-channel decay gate, u = S^T(g.k), w = S^T(g.q), kq = k.q,
+// (registers).  Per token: l2norm(q)*scale, l2norm(k), beta, the
+// per-channel decay gate, u = S^T(g.k), w = S^T(g.q), kq = k.q,
 // delta = (v - u)*beta, out = w + delta*kq, S' = g.S + k(x)delta
 // (lz_recur_step fp32 arm, src/ops_gdn.c:2516-2560; gate build
-// src/forward_kda.c:277-300, 840-850; call site :856-940), with every
-// state written to its ring slot as the reference does.  Then the per-head
-// gated RMSNorm and the per-32 quantization for o_proj
-// (src/forward_kda.c:1000-1043).
+// src/forward_kda.c:277-300, 840-850; call site :856-940), every state
+// written to its ring slot as the reference does; then the per-head gated
+// RMSNorm and the per-32 quantization for o_proj (src/forward_kda.c:
+// 1000-1043).  Everything that does not depend on the state (inputs, gates,
+// the three serial norms' sums, k.q) is computed for all tokens at once,
+// token-parallel; only u, w and the state update run token-serially.
 template <int KD, int VD>
 __global__ __launch_bounds__(VD) void k_kda_recur(KdaRecurArgs a) {
-    __shared__ float s_q[KD], s_k[KD], s_g[KD], s_o[VD];
+    static_assert(KD == VD, "one lane per state column and per key channel");
+    DECLARE_EXP_TAB(tab);
+    __shared__ __align__(16) float s_a[MAX_CHUNK][KD];   // q, then q.g*invq*scale (qcw)
+    __shared__ __align__(16) float s_b[MAX_CHUNK][KD];   // k, then k*invk (kn)
+    __shared__ __align__(16) float s_g[MAX_CHUNK][KD];   // decay gate
+    __shared__ __align__(16) float s_c[MAX_CHUNK][KD];   // q^2, then kn*g (kcw), then o^2
+    __shared__ __align__(16) float s_d[MAX_CHUNK][KD];   // k^2
+    __shared__ float s_invq[MAX_CHUNK], s_invk[MAX_CHUNK], s_beta[MAX_CHUNK], s_kq[MAX_CHUNK],
+        s_oinv[MAX_CHUNK];
     const int h = blockIdx.x;
     const int j = threadIdx.x;
+    const int nt = a.nt;
     const int kh = (a.nk == a.nv) ? h : (h * a.nk / a.nv);
     const int base = *a.ctl_slot;
     const size_t head_off = (size_t)h * KD * VD;
@@ -456,199 +629,330 @@ __global__ __launch_bounds__(VD) void k_kda_recur(KdaRecurArgs a) {
 #pragma unroll
         for (int i = 0; i < KD; i++) S[i] = src[(size_t)i * VD + j];
     }
-    const float decay = d_exp(a.a_log[h]);
-    for (int t = 0; t < a.nt; t++) {
-        // stage q, k, gate for this head/token
-        for (int i = j; i < KD; i += VD) {
-            s_q[i] = a.qc[(size_t)t * a.key + (size_t)kh * KD + i];
-            s_k[i] = a.kc[(size_t)t * a.key + (size_t)kh * KD + i];
-            float pre = a.gate_pre[(size_t)t * a.nv * KD + (size_t)h * KD + i] + a.dt_bias[h * KD + i];
-            float gg = -decay * d_softplus(pre);
-            s_g[i] = d_exp(gg);
-        }
-        __syncthreads();
-        // l2 norms (every lane walks the same serial sums)
-        float ssq = 0.0f, ssk = 0.0f;
-        for (int i = 0; i < KD; i++) ssq += s_q[i] * s_q[i];
-        for (int i = 0; i < KD; i++) ssk += s_k[i] * s_k[i];
-        const float invq = d_rsqrt(ssq + 1e-6f), invk = d_rsqrt(ssk + 1e-6f);
-        const float beta = d_sigmoid(a.bvec[(size_t)t * a.nv + h]);
-        float u = 0.0f, w = 0.0f, kq = 0.0f;
-#pragma unroll 8
-        for (int i = 0; i < KD; i++) {
-            float qn = s_q[i] * invq * a.scale;
-            float kn = s_k[i] * invk;
-            float kcw = kn * s_g[i], qcw = qn * s_g[i];
-            kq += kn * qn;
-            u += S[i] * kcw;
-            w += S[i] * qcw;
-        }
-        const float vcv = a.vc[(size_t)t * a.value + (size_t)h * VD + j];
-        u = (vcv - 1.0f * u) * beta;
-        float o = 1.0f * w + u * kq;
-#pragma unroll 8
-        for (int i = 0; i < KD; i++) {
-            float kn = s_k[i] * invk;
-            S[i] = S[i] * s_g[i] + kn * u;
-        }
-        // write this token's state to its ring slot
-        int so;
-        if (a.advance) { int si = (base + t) % a.depth; so = si + 1 == a.depth ? 0 : si + 1; }
-        else so = base;
-        {
-            float *dst = a.state + (size_t)so * a.slot_stride + head_off;
+    float vcv[MAX_CHUNK], gzv[MAX_CHUNK], qv[MAX_CHUNK], kv[MAX_CHUNK], pre[MAX_CHUNK];
+    const float dtb = a.dt_bias[h * KD + j];
 #pragma unroll
-            for (int i = 0; i < KD; i++) dst[(size_t)i * VD + j] = S[i];
+    for (int t = 0; t < MAX_CHUNK; t++) {
+        const int tc = imin(t, nt - 1);
+        qv[t] = a.qc[(size_t)tc * a.key + (size_t)kh * KD + j];
+        kv[t] = a.kc[(size_t)tc * a.key + (size_t)kh * KD + j];
+        pre[t] = a.gate_pre[(size_t)tc * a.nv * KD + (size_t)h * KD + j];
+        vcv[t] = a.vc[(size_t)tc * a.value + (size_t)h * VD + j];
+        gzv[t] = a.gz[(size_t)tc * a.value + (size_t)h * VD + j];
+    }
+    const float bv = a.bvec[(size_t)imin(j, nt - 1) * a.nv + h];
+    const float onw = a.o_norm[j];
+    const float decay = d_exp(a.a_log[h], tab);
+#pragma unroll
+    for (int t = 0; t < MAX_CHUNK; t++) {
+        if (t < nt) {
+            s_a[t][j] = qv[t];
+            s_b[t][j] = kv[t];
+            s_c[t][j] = qv[t] * qv[t];
+            s_d[t][j] = kv[t] * kv[t];
+            const float p = pre[t] + dtb;
+            const float gg = -decay * d_softplus(p, tab);
+            s_g[t][j] = d_exp(gg, tab);
         }
-        if (a.raw_out) a.raw_out[(size_t)t * a.value + (size_t)h * VD + j] = o;
-        // gated RMSNorm over the head: ((o*inv)*w)*silu(g)  (src/ops_norm.c:749-793)
-        s_o[j] = o * o;
-        __syncthreads();
-        float ss = 0.0f;
-        for (int i = 0; i < VD; i++) ss += s_o[i];
-        float inv = d_rsqrt(d_ss_over_n(ss, VD) + a.eps);
-        float gz = a.gz[(size_t)t * a.value + (size_t)h * VD + j];
-        float y = o * inv * a.o_norm[j] * d_silu(gz);
-        if (a.normed_out) a.normed_out[(size_t)t * a.value + (size_t)h * VD + j] = y;
-        const int col = h * VD + j;
-        d_quant_group32(y, a.xq + (size_t)t * a.value + col,
-                        a.xqs + (size_t)t * (a.value >> 5) + (col >> 5));
-        __syncthreads();
+    }
+    __syncthreads();
+    if (j < nt) {                        // lane t: the token's serial norms and k.q
+        const int t = j;
+        const float invq = d_rsqrt(serial_sum(s_c[t], KD) + 1e-6f);
+        const float invk = d_rsqrt(serial_sum(s_d[t], KD) + 1e-6f);
+        float kq = 0.0f;
+        for (int i = 0; i < KD; i++) {
+            const float qn = s_a[t][i] * invq * a.scale;
+            const float kn = s_b[t][i] * invk;
+            kq += kn * qn;
+        }
+        s_invq[t] = invq;
+        s_invk[t] = invk;
+        s_kq[t] = kq;
+        s_beta[t] = d_sigmoid(bv, tab);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < MAX_CHUNK; t++) {
+        if (t < nt) {
+            const float g = s_g[t][j];
+            const float qn = s_a[t][j] * s_invq[t] * a.scale;
+            const float kn = s_b[t][j] * s_invk[t];
+            s_a[t][j] = qn * g;
+            s_b[t][j] = kn;
+            s_c[t][j] = kn * g;
+        }
+    }
+    __syncthreads();
+    float ov[MAX_CHUNK];
+#pragma unroll
+    for (int t = 0; t < MAX_CHUNK; t++) {
+        ov[t] = 0.0f;
+        if (t < nt) {
+            float u = 0.0f, w = 0.0f;
+#pragma unroll
+            for (int i = 0; i < KD; i++) {
+                u += S[i] * s_c[t][i];
+                w += S[i] * s_a[t][i];
+            }
+            u = (vcv[t] - 1.0f * u) * s_beta[t];
+            const float o = 1.0f * w + u * s_kq[t];
+#pragma unroll
+            for (int i = 0; i < KD; i++) S[i] = S[i] * s_g[t][i] + s_b[t][i] * u;
+            if (a.advance || t == nt - 1) {
+                int so;
+                if (a.advance) { int si = (base + t) % a.depth; so = si + 1 == a.depth ? 0 : si + 1; }
+                else so = base;
+                float *dst = a.state + (size_t)so * a.slot_stride + head_off;
+#pragma unroll
+                for (int i = 0; i < KD; i++) dst[(size_t)i * VD + j] = S[i];
+            }
+            if (a.raw_out) a.raw_out[(size_t)t * a.value + (size_t)h * VD + j] = o;
+            ov[t] = o;
+        }
+    }
+    __syncthreads();                     // every lane is done reading s_c
+#pragma unroll
+    for (int t = 0; t < MAX_CHUNK; t++)
+        if (t < nt) s_c[t][j] = ov[t] * ov[t];
+    __syncthreads();
+    if (j < nt) s_oinv[j] = d_rsqrt(d_ss_over_n(serial_sum(s_c[j], VD), VD) + a.eps);
+    __syncthreads();
+    // gated RMSNorm over the head: ((o*inv)*w)*silu(g)  (src/ops_norm.c:749-793)
+    const int col = h * VD + j;
+#pragma unroll
+    for (int t = 0; t < MAX_CHUNK; t++) {
+        if (t < nt) {
+            const float y = ov[t] * s_oinv[t] * onw * d_silu(gzv[t], tab);
+            if (a.normed_out) a.normed_out[(size_t)t * a.value + col] = y;
+            d_quant_group32(y, a.xq + (size_t)t * a.value + col, a.xqs + (size_t)t * (a.value >> 5) + (col >> 5));
+        }
     }
 }
 
 // ------------------------------------------------------------ attention ---
 
-// Per token: RMSNorm(1+w) of every q head (read from the interleaved
-// [q | gate] projection) and k head, NeoX rotary on the first rot dims, then
-// per-32 int8 quantization of k and v into the KV plane at slot pos
-// (attn_impl, src/forward_attn.c:878-960; lz_rope, src/ops_rope.c:21-67).
-// One block of 64 lanes per token; heads walked in turn.
-__global__ void k_attn_prep(AttnArgs a) {
-    extern __shared__ float sh[];               // hd floats
-    const int t = blockIdx.x;
+// One 64-lane block per (token, head): RMSNorm(1+w) of a q head (read from
+// the interleaved [q | gate] projection) or a k head, NeoX rotary on the
+// first rot dims, then q to qh or k quantized per 32 into the KV plane at
+// slot pos; the last nkv blocks of a token quantize v heads.
+// (attn_impl src/forward_attn.c:878-960; lz_rope src/ops_rope.c:21-67.)
+__global__ __launch_bounds__(64) void k_attn_prep(AttnArgs a) {
+    __shared__ __align__(16) float sh[256], sq[256];
+    __shared__ float s_inv;
+    const int nq = a.kv_only ? 0 : a.nh;
+    const int per_tok = nq + 2 * a.nkv;
+    const int t = blockIdx.x / per_tok;
+    const int hh = blockIdx.x - t * per_tok;
     const int lane = threadIdx.x;
     const int hd = a.hd, half = a.rot >> 1;
     const int pos = *a.ctl_pos + a.pos_off + t;
-    const float *cs = a.rope_cs + (size_t)pos * half * 2;
-    const int n_heads_total = (a.kv_only ? 0 : a.nh) + a.nkv;
-    for (int hh = 0; hh < n_heads_total; hh++) {
-        const bool isq = hh < (a.kv_only ? 0 : a.nh);
-        const int h = isq ? hh : hh - (a.kv_only ? 0 : a.nh);
-        const float *src = isq ? a.qg + (size_t)t * a.qg_dim + (size_t)h * 2 * hd
-                               : a.kp + (size_t)t * a.kv_dim + (size_t)h * hd;
-        const float *nw = isq ? a.q_norm : a.k_norm;
-        float v0 = 0.0f;
-        for (int i = lane; i < hd; i += 64) { v0 = src[i]; sh[i] = v0 * v0; }
-        __syncthreads();
-        float ss = 0.0f;
-        for (int i = 0; i < hd; i++) ss += sh[i];
-        float inv = d_rsqrt(d_ss_over_n(ss, hd) + a.eps);
-        __syncthreads();
-        for (int i = lane; i < hd; i += 64) sh[i] = src[i] * inv * (1.0f + nw[i]);
-        __syncthreads();
-        // rotary (in LDS), each lane one pair
-        for (int i = lane; i < half; i += 64) {
-            float c = cs[i * 2], s = cs[i * 2 + 1];
-            float x0 = sh[i], x1 = sh[i + half];
-            sh[i] = x0 * c - x1 * s;
-            sh[i + half] = x1 * c + x0 * s;
+    if (hh >= nq + a.nkv) {                       // v head: quantize the projection
+        const int h = hh - nq - a.nkv;
+        for (int base = 0; base < hd; base += 64) {
+            int i = base + lane;
+            if (base + (lane & ~31) < hd) {
+                int col = h * hd + i;
+                float v = a.vp[(size_t)t * a.kv_dim + col];
+                d_quant_group32(v, a.vcache + (size_t)pos * a.kv_dim + col,
+                                a.vscale + (size_t)pos * (a.kv_dim >> 5) + (col >> 5));
+            }
         }
-        __syncthreads();
-        if (isq) {
-            for (int i = lane; i < hd; i += 64) a.qh[(size_t)t * a.q_dim + (size_t)h * hd + i] = sh[i];
-        } else {
-            for (int base = 0; base < hd; base += 64) {
-                int i = base + lane;
-                if (base + (lane & ~31) >= hd) break;
+        return;
+    }
+    const bool isq = hh < nq;
+    const int h = isq ? hh : hh - nq;
+    const float *src = isq ? a.qg + (size_t)t * a.qg_dim + (size_t)h * 2 * hd
+                           : a.kp + (size_t)t * a.kv_dim + (size_t)h * hd;
+    const float *nw = isq ? a.q_norm : a.k_norm;
+    const float *cs = a.rope_cs + (size_t)pos * half * 2;
+    float v[4], w[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int ic = imin(lane + 64 * u, hd - 1);
+        v[u] = src[ic];
+        w[u] = nw[ic];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int i = lane + 64 * u;
+        if (i < hd) { sh[i] = v[u]; sq[i] = v[u] * v[u]; }
+    }
+    __syncthreads();
+    if (lane == 0) s_inv = d_rsqrt(d_ss_over_n(serial_sum(sq, hd), hd) + a.eps);
+    __syncthreads();
+    const float inv = s_inv;
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int i = lane + 64 * u;
+        if (i < hd) sh[i] = v[u] * inv * (1.0f + w[u]);
+    }
+    __syncthreads();
+    for (int i = lane; i < half; i += 64) {
+        float c = cs[i * 2], s = cs[i * 2 + 1];
+        float x0 = sh[i], x1 = sh[i + half];
+        sh[i] = x0 * c - x1 * s;
+        sh[i + half] = x1 * c + x0 * s;
+    }
+    __syncthreads();
+    if (isq) {
+        for (int i = lane; i < hd; i += 64) a.qh[(size_t)t * a.q_dim + (size_t)h * hd + i] = sh[i];
+    } else {
+        for (int base = 0; base < hd; base += 64) {
+            int i = base + lane;
+            if (base + (lane & ~31) < hd) {
                 int col = h * hd + i;
                 d_quant_group32(sh[i], a.kcache + (size_t)pos * a.kv_dim + col,
                                 a.kscale + (size_t)pos * (a.kv_dim >> 5) + (col >> 5));
             }
         }
-        __syncthreads();
-    }
-    // v: quantize the raw projection
-    for (int base = 0; base < a.kv_dim; base += 64) {
-        int i = base + lane;
-        if (base + (lane & ~31) >= a.kv_dim) break;
-        float v = a.vp[(size_t)t * a.kv_dim + i];
-        d_quant_group32(v, a.vcache + (size_t)pos * a.kv_dim + i,
-                        a.vscale + (size_t)pos * (a.kv_dim >> 5) + (i >> 5));
     }
 }
 
-// Scores, softmax and weighted sum for one (token, head) per block
+// Copies rows [r0, r0+cn) of one head's Q8 K or V (hd bytes at row stride
+// kv_dim, plus hd/32 scales at stride kv_dim/32) into LDS, every load of a
+// thread in flight before its first store.
+__device__ __forceinline__ void stage_kv(const int8_t *__restrict__ q, const float *__restrict__ sc, int kv_dim,
+                                         int hd, int r0, int cn, int8_t *dq, float *ds) {
+    const int tid = threadIdx.x, nthr = blockDim.x;
+    const int cpr = hd >> 4, spr = hd >> 5;
+    const int total = cn * cpr, stotal = cn * spr;
+    for (int base = 0; base < total; base += nthr * 4) {
+        int4 r[4];
+        float s[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int idx = imin(base + u * nthr + tid, total - 1);
+            const int row = idx / cpr, cc = idx - row * cpr;
+            r[u] = *reinterpret_cast<const int4 *>(q + (size_t)(r0 + row) * kv_dim + cc * 16);
+            const int sidx = imin(base + u * nthr + tid, stotal - 1);
+            const int srow = sidx / spr, scc = sidx - srow * spr;
+            s[u] = sc[(size_t)(r0 + srow) * (kv_dim >> 5) + scc];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int idx = base + u * nthr + tid;
+            if (idx < total) *reinterpret_cast<int4 *>(dq + (size_t)idx * 16) = r[u];
+            if (idx < stotal) ds[idx] = s[u];
+        }
+    }
+}
+
+// One block per (token, kv head) holding the kv_mul q heads that share it
 // (attn_score_loop Q8 branch, src/forward_attn.c:206-660: score_q8_row
 // :30-41, lz_softmax src/ops_norm.c:903-990, wsum_q8_row :17-21), then the
-// sigmoid output gate.  Position-parallel scores; the softmax sum and the
-// weighted sums over positions are serial, as in the reference.
-__global__ __launch_bounds__(256) void k_attn_decode(AttnArgs a) {
-    extern __shared__ float att[];              // pos+1 floats (+ q head)
-    const int t = blockIdx.x / a.nh;
-    const int h = blockIdx.x - t * a.nh;
+// sigmoid output gate and the per-32 quantization of the output row (the
+// o_proj input).  K and V rows are staged through LDS `chunk` positions at a
+// time with all loads in flight; scores are position-parallel, each head's
+// softmax sum is serial (one lane), and each output element walks the
+// positions in order.
+__global__ __launch_bounds__(512) void k_attn_decode(AttnArgs a, int max_len, int chunk) {
+    DECLARE_EXP_TAB(tab);
+    extern __shared__ __align__(16) char smem[];
+    __shared__ float s_inv[16];
+    const int kv_mul = a.nh / a.nkv;
+    const int t = blockIdx.x / a.nkv;
+    const int kvh = blockIdx.x - t * a.nkv;
     const int hd = a.hd;
-    const int kvh = h / (a.nh / a.nkv);
     const int pos = *a.ctl_pos + a.pos_off + t;
     const int L = pos + 1;
-    float *qsh = att + ((L + 3) & ~3);
-    const int tid = threadIdx.x;
-    for (int i = tid; i < hd; i += blockDim.x) qsh[i] = a.qh[(size_t)t * a.q_dim + (size_t)h * hd + i];
-    __syncthreads();
+    const int Lp = (max_len + 3) & ~3;
+    float *qsh = reinterpret_cast<float *>(smem);                 // [kv_mul][hd]
+    float *att = qsh + kv_mul * hd;                                // [kv_mul][Lp]
+    float *csc = att + (size_t)kv_mul * Lp;                        // [chunk][hd/32]
+    int8_t *cst = reinterpret_cast<int8_t *>(csc + (size_t)chunk * (hd >> 5));   // [chunk][hd]
+    const int tid = threadIdx.x, nthr = blockDim.x;
+    const int h0 = kvh * kv_mul;
+    const int8_t *kplane = a.kcache + (size_t)kvh * hd;
+    const float *ksplane = a.kscale + (size_t)kvh * (hd >> 5);
+    const int8_t *vplane = a.vcache + (size_t)kvh * hd;
+    const float *vsplane = a.vscale + (size_t)kvh * (hd >> 5);
+    for (int i = tid; i < kv_mul * hd; i += nthr)
+        qsh[i] = a.qh[(size_t)t * a.q_dim + (size_t)h0 * hd + i];
     const float scale = a.attn_scale;
-    for (int tt = tid; tt < L; tt += blockDim.x) {
-        const int8_t *kr = a.kcache + (size_t)tt * a.kv_dim + (size_t)kvh * hd;
-        const float *ks = a.kscale + (size_t)tt * (a.kv_dim >> 5) + (size_t)kvh * (hd >> 5);
-        float sum = 0.0f;
-        for (int dd = 0; dd < hd; dd += 32) {
-            float acc = 0.0f;
-            for (int e = 0; e < 32; e++) acc += qsh[dd + e] * (float)kr[dd + e];
-            sum += acc * ks[dd >> 5];
+    for (int c0 = 0; c0 < L; c0 += chunk) {
+        const int cn = imin(chunk, L - c0);
+        __syncthreads();
+        stage_kv(kplane, ksplane, a.kv_dim, hd, c0, cn, cst, csc);
+        __syncthreads();
+        for (int idx = tid; idx < kv_mul * cn; idx += nthr) {
+            const int g = idx / cn, tt = idx - g * cn;
+            const int8_t *kr = cst + (size_t)tt * hd;
+            const float *ks = csc + (size_t)tt * (hd >> 5);
+            const float *qq = qsh + g * hd;
+            float sum = 0.0f;
+            for (int dd = 0; dd < hd; dd += 32) {
+                const int4 k0 = *reinterpret_cast<const int4 *>(kr + dd);
+                const int4 k1 = *reinterpret_cast<const int4 *>(kr + dd + 16);
+                const int8_t *kb0 = reinterpret_cast<const int8_t *>(&k0);
+                const int8_t *kb1 = reinterpret_cast<const int8_t *>(&k1);
+                float acc = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 16; e++) acc += qq[dd + e] * (float)kb0[e];
+#pragma unroll
+                for (int e = 0; e < 16; e++) acc += qq[dd + 16 + e] * (float)kb1[e];
+                sum += acc * ks[dd >> 5];
+            }
+            att[g * Lp + c0 + tt] = sum * scale;
         }
-        att[tt] = sum * scale;
     }
     __syncthreads();
-    // softmax: exact max (any order), exp, serial sum, scale
-    __shared__ uint32_t s_best;
-    __shared__ float s_inv;
-    if (tid == 0) s_best = 0;
-    __syncthreads();
-    {
-        uint32_t best = 0;
-        for (int tt = tid; tt < L; tt += blockDim.x) {
-            uint32_t k = d_fkey(att[tt]);
-            best = k > best ? k : best;
+    // softmax per head: wave w handles heads w, w + nwaves, ...  (the loop
+    // count is uniform over the block so the barriers are reached by all)
+    const int wv = tid >> 6, lane = tid & 63, nw = nthr >> 6;
+    for (int g0 = 0; g0 < kv_mul; g0 += nw) {
+        const int g = g0 + wv;
+        const bool act = g < kv_mul;
+        float *ag = att + (act ? g : 0) * Lp;
+        if (act) {
+            uint32_t best = 0;
+            for (int tt = lane; tt < L; tt += 64) {
+                uint32_t k = d_fkey(ag[tt]);
+                best = k > best ? k : best;
+            }
+            for (int o = 32; o > 0; o >>= 1) {
+                uint32_t w2 = __shfl_xor(best, o);
+                best = w2 > best ? w2 : best;
+            }
+            const float mx = d_unkey(best);
+            for (int tt = lane; tt < L; tt += 64) ag[tt] = d_exp(ag[tt] - mx, tab);
         }
-        atomicMax(&s_best, best);
+        __syncthreads();
+        if (act && lane == 0) {
+            float sum = serial_sum(ag, L);
+            s_inv[g] = (sum > 0.0f) ? 1.0f / sum : 0.0f;
+        }
+        __syncthreads();
+        if (act) {
+            const float inv = s_inv[g];
+            for (int tt = lane; tt < L; tt += 64) ag[tt] *= inv;
+        }
     }
-    __syncthreads();
-    {
-        uint32_t kb = s_best;
-        uint32_t u = (kb & 0x80000000u) ? (kb ^ 0x80000000u) : ~kb;
-        float mx = f_from_u(u);
-        for (int tt = tid; tt < L; tt += blockDim.x) att[tt] = d_exp(att[tt] - mx);
+    // weighted sum: thread (g, dd) walks positions in order
+    const int nout = kv_mul * hd;
+    const int my = tid < nout ? tid : 0;
+    const int g = my / hd, dd = my - g * hd;
+    const float *ag = att + g * Lp;
+    float o = 0.0f;
+    for (int c0 = 0; c0 < L; c0 += chunk) {
+        const int cn = imin(chunk, L - c0);
+        __syncthreads();
+        stage_kv(vplane, vsplane, a.kv_dim, hd, c0, cn, cst, csc);
+        __syncthreads();
+        if (tid < nout) {
+            const int8_t *vc = cst + dd;
+            const float *vs = csc + (dd >> 5);
+            for (int r = 0; r < cn; r++)
+                o += ag[c0 + r] * (float)vc[(size_t)r * hd] * vs[(size_t)r * (hd >> 5)];
+        }
     }
-    __syncthreads();
-    if (tid == 0) {
-        float sum = serial_sum(att, L);
-        s_inv = (sum > 0.0f) ? 1.0f / sum : 0.0f;
-    }
-    __syncthreads();
-    {
-        float inv = s_inv;
-        for (int tt = tid; tt < L; tt += blockDim.x) att[tt] *= inv;
-    }
-    __syncthreads();
-    for (int dd = tid; dd < hd; dd += blockDim.x) {
-        float o = 0.0f;
-        const int8_t *vr = a.vcache + (size_t)kvh * hd + dd;
-        const float *vs = a.vscale + (size_t)(kvh * hd + dd) / 32;
-        const size_t vstride = a.kv_dim, sstride = a.kv_dim >> 5;
-        for (int tt = 0; tt < L; tt++)
-            o += att[tt] * (float)vr[(size_t)tt * vstride] * vs[(size_t)tt * sstride];
+    if (tid < nout) {
+        const int h = h0 + g;
         const float gate = a.qg[(size_t)t * a.qg_dim + (size_t)h * 2 * hd + hd + dd];
-        o *= d_sigmoid(gate);
-        a.out[(size_t)t * a.q_dim + (size_t)h * hd + dd] = o;
+        o *= d_sigmoid(gate, tab);
+        const int col = h0 * hd + tid;
+        if (a.out) a.out[(size_t)t * a.q_dim + col] = o;
+        d_quant_group32(o, a.oq + (size_t)t * a.q_dim + col, a.oqs + (size_t)t * (a.q_dim >> 5) + (col >> 5));
     }
 }
 
@@ -657,126 +961,189 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs a) {
 // Routing for every token of the chunk (lz_moe_route, src/ops_moe.c:12-163:
 // sigmoid scores, key = score + bias for selection only, repeated
 // strict-greater argmax so the lowest index wins ties, weights renormalized
-// by their serial sum), then the chunk's distinct-expert table with each
-// expert's member (token, slot) pairs, in first-appearance order.
-// One block of 64 lanes; lanes parallel over experts.
-__global__ void k_moe_route(const float *__restrict__ logits, const float *__restrict__ bias,
-                            int E, int topk, int nt, int *__restrict__ sel_idx,
-                            float *__restrict__ sel_w, MoeGroups *__restrict__ grp,
-                            int *__restrict__ tally) {
-    __shared__ float key[MAX_EXPERTS], score[MAX_EXPERTS];
-    __shared__ int s_idx[MAX_TOPK];
-    const int lane = threadIdx.x;
-    for (int t = 0; t < nt; t++) {
-        for (int i = lane; i < E; i += 64) {
-            float sc = d_sigmoid(logits[(size_t)t * E + i]);
-            float kv = sc + bias[i];
-            score[i] = sc;
-            key[i] = kv == 0.0f ? 0.0f : kv;      // -0 and +0 compare equal in the reference
-        }
-        __syncthreads();
-        for (int k = 0; k < topk; k++) {
-            // argmax with lowest index on ties: reduce (fkey, -index)
-            uint64_t best = 0;
-            for (int i = lane; i < E; i += 64) {
-                if (key[i] <= -1e30f) continue;
-                uint64_t cand = ((uint64_t)d_fkey(key[i]) << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)i);
-                best = cand > best ? cand : best;
-            }
-            for (int o = 32; o > 0; o >>= 1) {
-                uint64_t w = __shfl_xor(best, o);
-                best = w > best ? w : best;
-            }
-            if (lane == 0) {
-                int bi = best ? (int)(0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFu)) : -1;
-                s_idx[k] = bi;
-                if (bi >= 0) key[bi] = -1e30f;
-            }
-            __syncthreads();
-        }
-        if (lane == 0) {
-            float wsum = 0.0f, w[MAX_TOPK];
-            for (int k = 0; k < topk; k++) {
-                int bi = s_idx[k];
-                w[k] = bi >= 0 ? score[bi] : 0.0f;
-                if (bi >= 0) wsum += w[k];
-            }
-            for (int k = 0; k < topk; k++) {
-                if (s_idx[k] >= 0 && wsum > 0.0f) w[k] /= wsum;
-                sel_idx[t * topk + k] = s_idx[k];
-                sel_w[t * topk + k] = w[k];
-            }
-        }
-        __syncthreads();
+// by their serial sum).  The k-th pick of that loop is the expert whose key
+// has rank k in the order (key descending, index ascending), so each
+// (token, expert) thread counts its rank against the token's keys in LDS.
+// Then the chunk's distinct-expert table (one thread per expert collects
+// its (token, slot) members) and the per-32 quantization of latx [nt][lat]
+// (input of the experts' w1/w3), whose loads are issued first.
+#define ROUTE_THREADS 512
+#define ROUTE_LAT_PER_THREAD 8
+__global__ __launch_bounds__(ROUTE_THREADS) void k_moe_route(const float *__restrict__ logits,
+                                                             const float *__restrict__ bias, int E, int topk,
+                                                             int nt, int *__restrict__ sel_idx,
+                                                             float *__restrict__ sel_w, MoeGroups *__restrict__ grp,
+                                                             int *__restrict__ tally, const float *__restrict__ latx,
+                                                             int lat, int8_t *__restrict__ lq,
+                                                             float *__restrict__ lqs) {
+    DECLARE_EXP_TAB(tab);
+    __shared__ float s_key[MAX_CHUNK][MAX_EXPERTS], s_sc[MAX_CHUNK][MAX_EXPERTS];
+    __shared__ int s_sel[MAX_PAIRS];
+    __shared__ unsigned long long s_ball[2];
+    const int tid = threadIdx.x;
+    const int ltot = nt * lat;
+    float lv[ROUTE_LAT_PER_THREAD];
+#pragma unroll
+    for (int u = 0; u < ROUTE_LAT_PER_THREAD; u++) lv[u] = latx[imin(u * ROUTE_THREADS + tid, ltot - 1)];
+    for (int idx = tid; idx < nt * E; idx += ROUTE_THREADS) {
+        const int t = idx / E, i = idx - t * E;
+        const float sc = d_sigmoid(logits[(size_t)t * E + i], tab);
+        const float kv = sc + bias[i];
+        s_sc[t][i] = sc;
+        s_key[t][i] = kv == 0.0f ? 0.0f : kv;          // -0 and +0 compare equal in the reference
     }
-    if (lane == 0) {
-        int ng = 0;
-        for (int t = 0; t < nt; t++)
-            for (int k = 0; k < topk; k++) {
-                int e = sel_idx[t * topk + k];
-                int pair = t * topk + k;
-                grp->pair_token[pair] = t;
-                if (e < 0) continue;
-                int g = 0;
-                while (g < ng && grp->expert[g] != e) g++;
-                if (g == ng) { grp->expert[ng] = e; grp->n_members[ng] = 0; ng++; }
-                grp->member[g][grp->n_members[g]++] = pair;
-            }
+    __syncthreads();
+    for (int idx = tid; idx < nt * E; idx += ROUTE_THREADS) {
+        const int t = idx / E, i = idx - t * E;
+        const float ki = s_key[t][i];
+        int rank = 0;
+        for (int jj = 0; jj < E; jj++) {
+            const float kj = s_key[t][jj];
+            rank += (kj > ki || (kj == ki && jj < i)) ? 1 : 0;
+        }
+        if (rank < topk) s_sel[t * topk + rank] = i;
+    }
+    __syncthreads();
+    if (tid < nt) {
+        const int t = tid;
+        float wsum = 0.0f;
+        for (int k = 0; k < topk; k++) wsum += s_sc[t][s_sel[t * topk + k]];
+        for (int k = 0; k < topk; k++) {
+            float w = s_sc[t][s_sel[t * topk + k]];
+            if (wsum > 0.0f) w /= wsum;
+            sel_idx[t * topk + k] = s_sel[t * topk + k];
+            sel_w[t * topk + k] = w;
+        }
+    }
+    // distinct experts: thread e collects its members in pair order
+    const int np = nt * topk;
+    const int e = tid, wvi = tid >> 6, lane = tid & 63;
+    int cnt = 0, mem[MAX_CHUNK];
+    if (e < E) {
+        for (int p = 0; p < np; p++)
+            if (s_sel[p] == e && cnt < MAX_CHUNK) mem[cnt++] = p;
+    }
+    const bool has = e < E && cnt > 0;
+    const unsigned long long bal = __ballot(has);
+    if (lane == 0 && wvi < 2) s_ball[wvi] = bal;
+    __syncthreads();
+    if (has) {
+        const int gidx = __popcll(bal & ((1ull << lane) - 1ull)) + (wvi == 1 ? __popcll(s_ball[0]) : 0);
+        grp->expert[gidx] = e;
+        grp->n_members[gidx] = cnt;
+        for (int m = 0; m < cnt; m++) grp->member[gidx][m] = mem[m];
+    }
+    if (tid < np) grp->pair_token[tid] = tid / topk;
+    if (tid == 0) {
+        const int ng = __popcll(s_ball[0]) + (E > 64 ? __popcll(s_ball[1]) : 0);
         grp->n_groups = ng;
         if (tally) *tally += ng;
+    }
+#pragma unroll
+    for (int u = 0; u < ROUTE_LAT_PER_THREAD; u++) {
+        const int el = u * ROUTE_THREADS + tid;
+        if (u * ROUTE_THREADS + (tid & ~31) < ltot) d_quant_group32(lv[u], lq + el, lqs + (el >> 5));
     }
 }
 
 // lat_y[t] = sum over slots in order of w * h2 (src/forward_moe.c:128-200),
 // then its per-32 quantization for the up projection.  One 64-lane block per
 // token.
-__global__ void k_moe_combine(const float *__restrict__ h2, const int *__restrict__ sel_idx,
-                              const float *__restrict__ sel_w, int topk, int lat,
-                              float *__restrict__ lat_y, int8_t *__restrict__ xq,
-                              float *__restrict__ xqs) {
+__global__ __launch_bounds__(64) void k_moe_combine(const float *__restrict__ h2, const int *__restrict__ sel_idx,
+                                                    const float *__restrict__ sel_w, int topk, int lat,
+                                                    float *__restrict__ lat_y, int8_t *__restrict__ xq,
+                                                    float *__restrict__ xqs) {
     const int t = blockIdx.x;
-    for (int base = 0; base < lat; base += 64) {
-        int v = base + threadIdx.x;
-        if (base + (int)(threadIdx.x & ~31) >= lat) break;
-        float y = 0.0f;
-        for (int k = 0; k < topk; k++) {
-            if (sel_idx[t * topk + k] < 0) continue;
-            y += sel_w[t * topk + k] * h2[((size_t)t * topk + k) * lat + v];
+    const int lane = threadIdx.x;
+    int sidx[MAX_TOPK];
+    float sw[MAX_TOPK];
+#pragma unroll
+    for (int k = 0; k < MAX_TOPK; k++) {
+        sidx[k] = k < topk ? sel_idx[t * topk + k] : -1;
+        sw[k] = k < topk ? sel_w[t * topk + k] : 0.0f;
+    }
+    for (int base = 0; base < lat; base += 64 * 8) {
+        float hv[8][MAX_TOPK];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int vcl = imin(base + j * 64 + lane, lat - 1);
+#pragma unroll
+            for (int k = 0; k < MAX_TOPK; k++)
+                hv[j][k] = h2[((size_t)t * topk + imin(k, topk - 1)) * lat + vcl];
         }
-        if (lat_y) lat_y[(size_t)t * lat + v] = y;
-        d_quant_group32(y, xq + (size_t)t * lat + v, xqs + (size_t)t * (lat >> 5) + (v >> 5));
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int v = base + j * 64 + lane;
+            if (base + j * 64 + (lane & ~31) < lat) {
+                float y = 0.0f;
+#pragma unroll
+                for (int k = 0; k < MAX_TOPK; k++) {
+                    if (k >= topk || sidx[k] < 0) continue;
+                    y += sw[k] * hv[j][k];
+                }
+                if (lat_y && v < lat) lat_y[(size_t)t * lat + v] = y;
+                d_quant_group32(y, xq + (size_t)t * lat + v, xqs + (size_t)t * (lat >> 5) + (v >> 5));
+            }
+        }
     }
 }
 
 // -------------------------------------------------------- argmax / ctl ---
 
-// Per row argmax.  mode 0: order-preserving key, first index wins
+#define ARGMAX_BLOCKS 64
+#define LZ_ARGMAX_ROWS 8
+
+// Per row argmax, ARGMAX_BLOCKS blocks per row; the last block to finish a
+// row reduces the partials and resets the row's counter (so the kernel can
+// be replayed from a graph).  mode 0: order-preserving key, first index wins
 // (sample_argmax, src/sampler.c:121-137).  mode 1: float '>' compare, first
 // index wins (lz_argmax_p1's scan, src/sampler.c:139-155).
-__global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ x, int n, int mode,
-                                                 int *__restrict__ out) {
-    const int row = blockIdx.x;
+__global__ __launch_bounds__(256) void k_argmax(const float *__restrict__ x, int n, int mode,
+                                                unsigned long long *__restrict__ partial,
+                                                unsigned *__restrict__ counter, int *__restrict__ out) {
+    const int row = blockIdx.y, nb = gridDim.x;
     const float *r = x + (size_t)row * n;
-    uint64_t best = 0;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    const int seg = (n + nb - 1) / nb;
+    const int lo = blockIdx.x * seg, hi = lo + seg < n ? lo + seg : n;
+    unsigned long long best = 0;
+    for (int i = lo + threadIdx.x; i < hi; i += blockDim.x) {
         float v = r[i];
         uint32_t k;
         if (mode == 0) k = d_fkey(v);
         else k = (v != v) ? 0u : d_fkey(v == 0.0f ? 0.0f : v);
-        uint64_t cand = ((uint64_t)k << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)i);
+        unsigned long long cand = ((unsigned long long)k << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)i);
         best = cand > best ? cand : best;
     }
-    for (int o = 32; o > 0; o >>= 1) {
-        uint64_t w = __shfl_xor(best, o);
-        best = w > best ? w : best;
-    }
-    __shared__ uint64_t sb[16];
+    best = wave_max_u64(best);
+    __shared__ unsigned long long sb[4];
+    __shared__ bool s_last;
     if ((threadIdx.x & 63) == 0) sb[threadIdx.x >> 6] = best;
     __syncthreads();
     if (threadIdx.x == 0) {
-        uint64_t b = 0;
+        unsigned long long b = 0;
         for (int i = 0; i < (int)(blockDim.x >> 6); i++) b = sb[i] > b ? sb[i] : b;
-        out[row] = (int)(0xFFFFFFFFu - (uint32_t)(b & 0xFFFFFFFFu));
+        partial[(size_t)row * nb + blockIdx.x] = b;
+        __threadfence();
+        unsigned prev = atomicAdd(&counter[row], 1u);
+        s_last = (prev == (unsigned)nb - 1);
+    }
+    __syncthreads();
+    if (s_last) {
+        __threadfence();
+        unsigned long long b = 0;
+        for (int i = threadIdx.x; i < nb; i += blockDim.x) {
+            unsigned long long p = __atomic_load_n(&partial[(size_t)row * nb + i], __ATOMIC_RELAXED);
+            b = p > b ? p : b;
+        }
+        b = wave_max_u64(b);
+        if ((threadIdx.x & 63) == 0) sb[threadIdx.x >> 6] = b;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            unsigned long long bb = 0;
+            for (int i = 0; i < (int)(blockDim.x >> 6); i++) bb = sb[i] > bb ? sb[i] : bb;
+            out[row] = (int)(0xFFFFFFFFu - (uint32_t)(bb & 0xFFFFFFFFu));
+            counter[row] = 0;
+        }
     }
 }
 
@@ -851,51 +1218,59 @@ extern "C" int l98k_upload_exp_table(const float *tab) {
     return (int)hipMemcpyToSymbol(HIP_SYMBOL(c_exp_tab), tab, 32 * sizeof(float));
 }
 
-template <int M>
-static hipError_t launch_gemv_m(const GemvBatch &b, const int8_t *xq, const float *xqs, int in_dim,
-                                int R, int tiles, hipStream_t st) {
-    size_t lds = (size_t)R * M * (in_dim >> 4) * sizeof(int);
-    hipLaunchKernelGGL(k_gemv_q8<M>, dim3(tiles), dim3(64), lds, st, b, xq, xqs, in_dim, R);
-    return hipGetLastError();
-}
-
-extern "C" int l98k_gemv_rows_per_tile(int in_dim, int m) {
-    int r = 8192 / in_dim;
+// Rows per GEMV tile: the tile is at most GEMV_TILE_BYTES of weights and
+// R*m (row, token) epilogue pairs fit the block.
+static int gemv_rows_per_tile(int in_dim, int m) {
+    int r = GEMV_TILE_BYTES / in_dim;
     if (r < 1) r = 1;
-    if (r > 64 / m) r = 64 / m;
+    if (r > GEMV_THREADS / m) r = GEMV_THREADS / m;
     return r;
 }
 
-extern "C" int l98k_gemv(GemvBatch *b, const int8_t *xq, const float *xqs, int in_dim, int m,
-                         hipStream_t st) {
-    if (m < 1 || m > 8 || (in_dim & 31) || b->n < 1 || b->n > MAX_GEMV_JOBS) return -1;
-    int R = l98k_gemv_rows_per_tile(in_dim, m);
+template <int M>
+static hipError_t launch_gemv_m(const GemvBatch &b, size_t lds, int tiles, hipStream_t st) {
+    hipLaunchKernelGGL(k_gemv_q8<M>, dim3(tiles), dim3(GEMV_THREADS), lds, st, b);
+    return hipGetLastError();
+}
+
+extern "C" int l98k_gemv(GemvBatch *b, int m, hipStream_t st) {
+    if (m < 1 || m > MAX_CHUNK || b->n < 1 || b->n > MAX_GEMV_JOBS) return -1;
     int tiles = 0;
+    size_t lds = 0;
     for (int j = 0; j < b->n; j++) {
-        b->job[j].tile0 = tiles;
-        tiles += (b->job[j].rows + R - 1) / R;
+        GemvJob &J = b->job[j];
+        if (J.in_dim < 32 || (J.in_dim & 31) || J.in_dim > GEMV_MAX_IN || J.rows < 1 || !J.xq || !J.xqs)
+            return -1;
+        J.R = gemv_rows_per_tile(J.in_dim, m);
+        J.tile0 = tiles;
+        tiles += (J.rows + J.R - 1) / J.R;
+        size_t l = gemv_lds_bytes(m, J.in_dim, J.R);
+        lds = l > lds ? l : lds;
     }
+    if (lds > 64 * 1024) return -1;
     switch (m) {
-    case 1: return (int)launch_gemv_m<1>(*b, xq, xqs, in_dim, R, tiles, st);
-    case 2: return (int)launch_gemv_m<2>(*b, xq, xqs, in_dim, R, tiles, st);
-    case 3: return (int)launch_gemv_m<3>(*b, xq, xqs, in_dim, R, tiles, st);
-    case 4: return (int)launch_gemv_m<4>(*b, xq, xqs, in_dim, R, tiles, st);
-    case 5: return (int)launch_gemv_m<5>(*b, xq, xqs, in_dim, R, tiles, st);
-    case 6: return (int)launch_gemv_m<6>(*b, xq, xqs, in_dim, R, tiles, st);
-    case 7: return (int)launch_gemv_m<7>(*b, xq, xqs, in_dim, R, tiles, st);
-    default: return (int)launch_gemv_m<8>(*b, xq, xqs, in_dim, R, tiles, st);
+    case 1: return (int)launch_gemv_m<1>(*b, lds, tiles, st);
+    case 2: return (int)launch_gemv_m<2>(*b, lds, tiles, st);
+    case 3: return (int)launch_gemv_m<3>(*b, lds, tiles, st);
+    case 4: return (int)launch_gemv_m<4>(*b, lds, tiles, st);
+    case 5: return (int)launch_gemv_m<5>(*b, lds, tiles, st);
+    case 6: return (int)launch_gemv_m<6>(*b, lds, tiles, st);
+    case 7: return (int)launch_gemv_m<7>(*b, lds, tiles, st);
+    default: return (int)launch_gemv_m<8>(*b, lds, tiles, st);
     }
 }
 
-extern "C" int l98k_expert_gemv(const ExpertBank *bank, const MoeGroups *grp, int max_groups,
-                                const int8_t *xq, const float *xqs, int xq_by_pair, float *out,
-                                int in_dim, int out_rows, int m, hipStream_t st) {
-    int R = l98k_gemv_rows_per_tile(in_dim, 8);
-    int tiles = (out_rows + R - 1) / R;
-    size_t lds = (size_t)R * 8 * (in_dim >> 4) * sizeof(int);
-    (void)m;
-    hipLaunchKernelGGL(k_expert_gemv<8>, dim3(max_groups * tiles), dim3(64), lds, st, *bank, grp, xq,
-                       xqs, xq_by_pair, out, in_dim, out_rows, R, tiles);
+extern "C" int l98k_expert_gemv(const ExpertJob *jobs, int n_jobs, const MoeGroups *grp, int max_groups,
+                                int in_dim, int out_rows, hipStream_t st) {
+    if (n_jobs < 1 || n_jobs > 2 || in_dim < 32 || (in_dim & 31) || in_dim > GEMV_MAX_IN || max_groups < 1 ||
+        max_groups > MAX_PAIRS)
+        return -1;
+    const int R = gemv_rows_per_tile(in_dim, MAX_CHUNK);
+    const int tiles = (out_rows + R - 1) / R;
+    const size_t lds = gemv_lds_bytes(MAX_CHUNK, in_dim, R);
+    if (lds > 64 * 1024) return -1;
+    hipLaunchKernelGGL(k_expert_gemv, dim3(n_jobs * max_groups * tiles), dim3(GEMV_THREADS), lds, st, jobs[0],
+                       n_jobs > 1 ? jobs[1] : jobs[0], grp, max_groups, in_dim, out_rows, R, tiles);
     return (int)hipGetLastError();
 }
 
@@ -905,37 +1280,71 @@ extern "C" int l98k_embed(const int8_t *q, const float *s, const int *toks, int 
     return (int)hipGetLastError();
 }
 
+#define NORM_CASES(X) X(1) X(2) X(4) X(8) X(16) X(32)
+
 extern "C" int l98k_rmsnorm(float *x, int x_stride, const float *a, const float *b, const float *w,
                             int n, float eps, int rows, float *out, int out_stride, int8_t *xq,
                             float *xqs, hipStream_t st) {
-    hipLaunchKernelGGL(k_rmsnorm, dim3(rows), dim3(64), (size_t)n * sizeof(float), st, x, x_stride,
-                       a, b, w, n, eps, out, out_stride, xq, xqs);
-    return (int)hipGetLastError();
+    if (n < 1 || n > 64 * 32 || (xq && (n & 31)) || rows < 1) return -1;
+#define NORM_LAUNCH(NC)                                                                          \
+    if (n <= 64 * NC) {                                                                          \
+        hipLaunchKernelGGL(k_rmsnorm<NC>, dim3(rows), dim3(64), 0, st, x, x_stride, a, b, w, n, \
+                           eps, out, out_stride, xq, xqs);                                       \
+        return (int)hipGetLastError();                                                           \
+    }
+    NORM_CASES(NORM_LAUNCH)
+#undef NORM_LAUNCH
+    return -1;
 }
 
-extern "C" int l98k_quant_rows(const float *x, int n, int x_stride, int rows, int8_t *xq, float *xqs,
-                               hipStream_t st) {
-    hipLaunchKernelGGL(k_quant_rows, dim3(rows), dim3(64), 0, st, x, n, x_stride, xq, xqs);
-    return (int)hipGetLastError();
+extern "C" int l98k_mtp_pre(const int8_t *emb_q, const float *emb_s, const int *toks, const float *h, int d,
+                            const float *w_e, const float *w_h, float eps, int rows, int8_t *xq, float *xqs,
+                            hipStream_t st) {
+    if (d < 32 || d > 64 * 32 || (d & 31) || rows < 1) return -1;
+#define PRE_LAUNCH(NC)                                                                                  \
+    if (d <= 64 * NC) {                                                                                 \
+        hipLaunchKernelGGL(k_mtp_pre<NC>, dim3(rows, 2), dim3(64), 0, st, emb_q, emb_s, toks, h, d, w_e, \
+                           w_h, eps, xq, xqs);                                                          \
+        return (int)hipGetLastError();                                                                  \
+    }
+    NORM_CASES(PRE_LAUNCH)
+#undef PRE_LAUNCH
+    return -1;
 }
 
-extern "C" int l98k_act_quant(const float *h1, const float *h3, int n, int rows, const int *count,
-                              int8_t *xq, float *xqs, float *g_out, hipStream_t st) {
-    hipLaunchKernelGGL(k_act_quant, dim3(rows), dim3(64), 0, st, h1, h3, n, count, xq, xqs, g_out);
+extern "C" int l98k_act_quant(const float *h1, const float *h3, int n, int rows, int8_t *xq, float *xqs,
+                              const float *g1, const float *g3, int n2, int rows2, int8_t *xq2, float *xqs2,
+                              hipStream_t st) {
+    if ((n & 31) || (rows2 > 0 && (n2 & 31)) || rows < 0 || rows2 < 0 || rows + rows2 < 1) return -1;
+    hipLaunchKernelGGL(k_act_quant, dim3(rows + rows2), dim3(64), 0, st, h1, h3, n, rows, xq, xqs, g1, g3, n2,
+                       xq2, xqs2);
     return (int)hipGetLastError();
 }
 
 extern "C" int l98k_kda_conv(const float *pq, const float *pk, const float *pv, int key, int value,
                              const float *wconv, float *ring, size_t slot_stride, int K,
                              const int *ctl_slot, int depth, int advance, int nt, float *qc,
-                             float *kc, float *vc, hipStream_t st) {
-    int n = 2 * key + value;
-    hipLaunchKernelGGL(k_kda_conv, dim3((n + 255) / 256), dim3(256), 0, st, pq, pk, pv, key, value,
-                       wconv, ring, slot_stride, K, ctl_slot, depth, advance, nt, qc, kc, vc);
+                             float *kc, float *vc, const float *pfa, int rank, int8_t *fq, float *fqs,
+                             hipStream_t st) {
+    if (nt < 1 || nt > MAX_CHUNK || !pfa || rank < 32 || (rank & 31)) return -1;
+    const int n = 2 * key + value;
+    const dim3 grid((n + 255) / 256 + 1);
+    if (K == 4)
+        hipLaunchKernelGGL(k_kda_conv<4>, grid, dim3(256), 0, st, pq, pk, pv, key, value, wconv, ring,
+                           slot_stride, ctl_slot, depth, advance, nt, qc, kc, vc, pfa, rank, fq, fqs);
+    else if (K == 3)
+        hipLaunchKernelGGL(k_kda_conv<3>, grid, dim3(256), 0, st, pq, pk, pv, key, value, wconv, ring,
+                           slot_stride, ctl_slot, depth, advance, nt, qc, kc, vc, pfa, rank, fq, fqs);
+    else if (K == 2)
+        hipLaunchKernelGGL(k_kda_conv<2>, grid, dim3(256), 0, st, pq, pk, pv, key, value, wconv, ring,
+                           slot_stride, ctl_slot, depth, advance, nt, qc, kc, vc, pfa, rank, fq, fqs);
+    else
+        return -1;
     return (int)hipGetLastError();
 }
 
 extern "C" int l98k_kda_recur(const KdaRecurArgs *a, int kd, int vd, hipStream_t st) {
+    if (a->nt < 1 || a->nt > MAX_CHUNK) return -1;
     if (kd == 64 && vd == 64)
         hipLaunchKernelGGL((k_kda_recur<64, 64>), dim3(a->nv), dim3(64), 0, st, *a);
     else if (kd == 128 && vd == 128)
@@ -948,34 +1357,58 @@ extern "C" int l98k_kda_recur(const KdaRecurArgs *a, int kd, int vd, hipStream_t
 }
 
 extern "C" int l98k_attn_prep(const AttnArgs *a, int nt, hipStream_t st) {
-    hipLaunchKernelGGL(k_attn_prep, dim3(nt), dim3(64), (size_t)a->hd * sizeof(float), st, *a);
+    if (a->hd > 256 || (a->hd & 31) || a->rot > a->hd || nt < 1) return -1;
+    const int per_tok = (a->kv_only ? 0 : a->nh) + 2 * a->nkv;
+    hipLaunchKernelGGL(k_attn_prep, dim3(nt * per_tok), dim3(64), 0, st, *a);
     return (int)hipGetLastError();
 }
 
+#define ATTN_LDS_MAX (64 * 1024)
+
 extern "C" int l98k_attn_decode(const AttnArgs *a, int nt, int max_len, hipStream_t st) {
-    size_t lds = ((size_t)((max_len + 3) & ~3) + a->hd) * sizeof(float);
-    hipLaunchKernelGGL(k_attn_decode, dim3(nt * a->nh), dim3(256), lds, st, *a);
+    if (a->nkv < 1 || a->nh % a->nkv || (a->hd & 31) || nt < 1 || max_len < 1 || !a->oq || !a->oqs) return -1;
+    const int kv_mul = a->nh / a->nkv;
+    if (kv_mul > 16 || kv_mul * a->hd > 512) return -1;
+    const size_t Lp = (size_t)((max_len + 3) & ~3);
+    const size_t fixed = ((size_t)kv_mul * a->hd + (size_t)kv_mul * Lp) * sizeof(float);
+    const size_t per_pos = (size_t)a->hd + (size_t)(a->hd >> 5) * sizeof(float);
+    if (fixed + 16 * per_pos > ATTN_LDS_MAX) return -1;
+    int chunk = (int)((ATTN_LDS_MAX - fixed) / per_pos) & ~15;
+    const int need = (max_len + 15) & ~15;
+    if (chunk > need) chunk = need;
+    const size_t lds = fixed + (size_t)chunk * per_pos;
+    int thr = kv_mul * a->hd;
+    thr = thr < 256 ? 256 : thr;
+    thr = (thr + 63) & ~63;
+    hipLaunchKernelGGL(k_attn_decode, dim3(nt * a->nkv), dim3(thr), lds, st, *a, max_len, chunk);
     return (int)hipGetLastError();
 }
 
 extern "C" int l98k_moe_route(const float *logits, const float *bias, int E, int topk, int nt,
-                              int *sel_idx, float *sel_w, MoeGroups *grp, int *tally, hipStream_t st) {
-    if (E > MAX_EXPERTS || topk > MAX_TOPK) return -1;
-    hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(64), 0, st, logits, bias, E, topk, nt, sel_idx,
-                       sel_w, grp, tally);
+                              int *sel_idx, float *sel_w, MoeGroups *grp, int *tally, const float *latx,
+                              int lat, int8_t *lq, float *lqs, hipStream_t st) {
+    if (E > MAX_EXPERTS || E < topk || topk < 1 || topk > MAX_TOPK || nt < 1 || nt > MAX_CHUNK ||
+        nt * topk > MAX_PAIRS || (lat & 31) || nt * lat > ROUTE_LAT_PER_THREAD * ROUTE_THREADS)
+        return -1;
+    hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(ROUTE_THREADS), 0, st, logits, bias, E, topk, nt, sel_idx,
+                       sel_w, grp, tally, latx, lat, lq, lqs);
     return (int)hipGetLastError();
 }
 
 extern "C" int l98k_moe_combine(const float *h2, const int *sel_idx, const float *sel_w, int topk,
                                 int lat, int nt, float *lat_y, int8_t *xq, float *xqs,
                                 hipStream_t st) {
+    if (topk < 1 || topk > MAX_TOPK || (lat & 31)) return -1;
     hipLaunchKernelGGL(k_moe_combine, dim3(nt), dim3(64), 0, st, h2, sel_idx, sel_w, topk, lat,
                        lat_y, xq, xqs);
     return (int)hipGetLastError();
 }
 
-extern "C" int l98k_argmax(const float *x, int n, int rows, int mode, int *out, hipStream_t st) {
-    hipLaunchKernelGGL(k_argmax, dim3(rows), dim3(1024), 0, st, x, n, mode, out);
+extern "C" int l98k_argmax(const float *x, int n, int rows, int mode, int *out,
+                           unsigned long long *partial, unsigned *counter, hipStream_t st) {
+    if (rows < 1 || rows > LZ_ARGMAX_ROWS || n < 1) return -1;
+    hipLaunchKernelGGL(k_argmax, dim3(ARGMAX_BLOCKS, rows), dim3(256), 0, st, x, n, mode, partial,
+                       counter, out);
     return (int)hipGetLastError();
 }
 

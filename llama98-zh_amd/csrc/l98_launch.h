@@ -1,0 +1,50 @@
+// Host-side launchers of the gfx950 kernels (l98_kernels.hip).  Each returns
+// 0, a HIP error code, or -1 when the arguments do not fit the kernel's
+// shape limits (checked on the host before any launch).
+#ifndef L98_LAUNCH_H
+#define L98_LAUNCH_H
+#include <hip/hip_runtime.h>
+
+#include "l98_dev.h"
+
+extern "C" {
+int l98k_upload_exp_table(const float *tab);
+// Fused GEMV of b->n jobs over m <= MAX_CHUNK activation rows.
+int l98k_gemv(GemvBatch *b, int m, hipStream_t st);
+// Grouped expert GEMV: n_jobs (<= 2) projections over the groups in grp.
+int l98k_expert_gemv(const ExpertJob *jobs, int n_jobs, const MoeGroups *grp, int max_groups, int in_dim,
+                     int out_rows, hipStream_t st);
+int l98k_embed(const int8_t *q, const float *s, const int *toks, int d, int nt, float *x, hipStream_t st);
+// x += a (+ b) (when a), RMSNorm(1+w) -> out (when out) and per-32 int8 (when xq).
+int l98k_rmsnorm(float *x, int x_stride, const float *a, const float *b, const float *w, int n, float eps,
+                 int rows, float *out, int out_stride, int8_t *xq, float *xqs, hipStream_t st);
+// MTP input rows: [norm_e(embed(tok)) | norm_h(h)] quantized per 32 into xq [rows][2d].
+int l98k_mtp_pre(const int8_t *emb_q, const float *emb_s, const int *toks, const float *h, int d,
+                 const float *w_e, const float *w_h, float eps, int rows, int8_t *xq, float *xqs,
+                 hipStream_t st);
+// silu(h1)*h3 quantized per 32, for rows of two independent segments.
+int l98k_act_quant(const float *h1, const float *h3, int n, int rows, int8_t *xq, float *xqs,
+                   const float *g1, const float *g3, int n2, int rows2, int8_t *xq2, float *xqs2,
+                   hipStream_t st);
+// Causal conv + SiLU over [q|k|v] with the ring state; also quantizes the
+// gate low-rank rows pfa [nt][rank] into fq/fqs.
+int l98k_kda_conv(const float *pq, const float *pk, const float *pv, int key, int value, const float *wconv,
+                  float *ring, size_t slot_stride, int K, const int *ctl_slot, int depth, int advance, int nt,
+                  float *qc, float *kc, float *vc, const float *pfa, int rank, int8_t *fq, float *fqs,
+                  hipStream_t st);
+int l98k_kda_recur(const KdaRecurArgs *a, int kd, int vd, hipStream_t st);
+int l98k_attn_prep(const AttnArgs *a, int nt, hipStream_t st);
+int l98k_attn_decode(const AttnArgs *a, int nt, int max_len, hipStream_t st);
+// Routing + distinct-expert groups; also quantizes latx [nt][lat] into lq/lqs.
+int l98k_moe_route(const float *logits, const float *bias, int E, int topk, int nt, int *sel_idx, float *sel_w,
+                   MoeGroups *grp, int *tally, const float *latx, int lat, int8_t *lq, float *lqs,
+                   hipStream_t st);
+int l98k_moe_combine(const float *h2, const int *sel_idx, const float *sel_w, int topk, int lat, int nt,
+                     float *lat_y, int8_t *xq, float *xqs, hipStream_t st);
+int l98k_argmax(const float *x, int n, int rows, int mode, int *out, unsigned long long *partial,
+                unsigned *counter, hipStream_t st);
+int l98k_accept(DevCtl *ctl, const float *vhidden, int d, float *chain, int depth, int brk, hipStream_t st);
+int l98k_set_tokens(DevCtl *ctl, int op, RoundRec *hist, int hist_cap, hipStream_t st);
+}
+
+#endif
