@@ -164,9 +164,11 @@ int lz_argmax_p1(const float *logits, int n, float *out_p);
  * (src/generate.c:1822-2106, penalties off): prefill + MTP prefill, then
  * rounds until n_new tokens are emitted.  Greedy rounds run back to back on
  * the device with no host round trip.  tokens receives up to cap ids
- * (whole last round).  Returns the number of tokens emitted, or -LZErr. */
+ * (whole last round).  With a temperature sampler, samp->rng_state is
+ * advanced as the run consumed it.  Returns the number of tokens emitted,
+ * or -LZErr. */
 int l98_generate(const LZModel *m, LZRunState *s, const int *prompt, int n_prompt, int k,
-                 int n_new, const LZSampler *samp, int *tokens, int cap, int *k_eff_out,
+                 int n_new, LZSampler *samp, int *tokens, int cap, int *k_eff_out,
                  int *n_accept_out, int *n_rounds);
 /* Prefill + MTP prefill + first capture forward of a prompt, seeding the
  * device round state.  Returns the first emitted token, or -LZErr. */

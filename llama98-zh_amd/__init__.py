@@ -326,4 +326,5 @@ class Engine:
                                   _ip(na), C.byref(nr))
         if n < 0:
             raise RuntimeError(f"l98_generate failed: {n}")
+        self.last_rng = samp.rng_state if samp is not None else None   # sampler state after the run
         return toks[:min(n, cap)], ke[:nr.value], na[:nr.value]

@@ -460,6 +460,8 @@ struct DState {
     int hist_cap = 0;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     hipGraphExec_t round_graph[LZ_SPEC_K_MAX + 1] = {};
+    LZSampler session_samp{};               // the sampler of the current session (l98_session_start)
+    bool session_greedy = true;
 };
 
 namespace {
@@ -1410,19 +1412,14 @@ extern "C" const char *l98_device_name(void) {
     return name;
 }
 
-namespace {
-LZSampler g_session_samp;
-bool g_session_greedy = true;
-}
-
 extern "C" int l98_session_start(const LZModel *mm, LZRunState *s, const int *prompt, int n_prompt,
                                  const LZSampler *samp) {
     if (!mm || !s || !s->impl || !prompt || n_prompt < 2) return -LZ_ERR_NULL_ARG;
     DState *d = S(s);
     const LZModelConfig &c = d->m->c;
     if (!tok_ok(c, prompt, n_prompt) || n_prompt >= d->seq_len) return -LZ_ERR_FORWARD;
-    g_session_greedy = !samp || !(samp->p.temperature > 0.0f);
-    if (samp) g_session_samp = *samp;
+    d->session_greedy = !samp || !(samp->p.temperature > 0.0f);
+    if (samp) d->session_samp = *samp;
     // prefill + MTP prefill (src/generate.c:2806-2960)
     lz_state_reset(s, mm);
     if (batch_capture_dev(d, s, prompt, n_prompt - 1, 0)) return -LZ_ERR_FORWARD;
@@ -1439,10 +1436,10 @@ extern "C" int l98_session_start(const LZModel *mm, LZRunState *s, const int *pr
     float *lg = lz_forward_capture(mm, s, prompt[n_prompt - 1], n_prompt - 1);
     if (!lg) return -LZ_ERR_FORWARD;
     std::vector<PI> buf;
-    int anchor = g_session_greedy
+    int anchor = d->session_greedy
         ? lz_sample_argmax(lg, c.vocab_size)
-        : sample_ex(lg, c.vocab_size, g_session_samp.p.temperature, g_session_samp.p.topp,
-                    &g_session_samp.rng_state, buf);
+        : sample_ex(lg, c.vocab_size, d->session_samp.p.temperature, d->session_samp.p.topp,
+                    &d->session_samp.rng_state, buf);
     DevCtl h = ctl_from(s);
     h.anchor = anchor;
     h.anchor_pos = n_prompt - 1;
@@ -1534,7 +1531,7 @@ extern "C" int l98_greedy_rounds_ex(const LZModel *mm, LZRunState *s, int k, int
 }
 
 extern "C" int l98_generate(const LZModel *mm, LZRunState *s, const int *prompt, int n_prompt, int k,
-                            int n_new, const LZSampler *samp, int *tokens, int cap, int *k_eff_out,
+                            int n_new, LZSampler *samp, int *tokens, int cap, int *k_eff_out,
                             int *n_accept_out, int *n_rounds) {
     if (!mm || !s || !s->impl || !prompt || n_prompt < 2 || !tokens) return -LZ_ERR_NULL_ARG;
     if (k < 1 || k > LZ_SPEC_K_MAX || k > s->ssm_ring_depth - 1) return -LZ_ERR_SPEC_K_RANGE;
@@ -1545,8 +1542,8 @@ extern "C" int l98_generate(const LZModel *mm, LZRunState *s, const int *prompt,
     int n = 0, rounds = 0;
     if (n < cap) tokens[n] = anchor;
     n++;
-    if (!g_session_greedy) {
-        LZSampler local = g_session_samp;
+    if (!d->session_greedy) {
+        LZSampler &local = d->session_samp;
         int anchor_pos = n_prompt - 1;
         while (n < n_new) {
             int out[LZ_SPEC_K_MAX + 1], na = 0, np = 0, ke = 0;
@@ -1561,6 +1558,7 @@ extern "C" int l98_generate(const LZModel *mm, LZRunState *s, const int *prompt,
             anchor_pos = np;
         }
         if (n_rounds) *n_rounds = rounds;
+        if (samp) samp->rng_state = local.rng_state;
         return n;
     }
     // Greedy: every round emits at least one token, so at most n_new - 1

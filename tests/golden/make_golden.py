@@ -1,0 +1,72 @@
+#!/usr/bin/env python3
+"""Writes the golden generation fixtures (tests/golden/gen_*.json) from the
+reference engine's own build (oracle/_ref/l98ref_oracle, compiled from the
+reference sources by oracle/ref.mk) on the seeded synthetic models.
+
+Run in a container that has the reference build:
+    make -f oracle/ref.mk all && python3 tests/golden/make_golden.py
+Each fixture holds the inputs (model generator id and seed, prompt seed and
+length, k, sampling parameters) and the reference's outputs (emitted
+tokens, per-round k_eff and n_accept, final RNG state and positions), plus
+the sha256 of the generated model.bin so a change of the generator is
+caught.
+"""
+import hashlib
+import json
+import os
+import sys
+import tempfile
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+
+import oracle_lib as OL  # noqa: E402
+
+# (fixture, model dir name, generator config id, vocab, n_prompt, k, n_new, temp, topp, sampler seed)
+CASES = [
+    ("gen_micro_k3_greedy", "micro", 10, 512, 24, 3, 40, 0.0, 1.0, 1),
+    ("gen_micro_k2_temp", "micro", 10, 512, 24, 2, 32, 0.8, 0.95, 7),
+    ("gen_tiny_k1_greedy", "tiny", 0, 8192, 64, 1, 128, 0.0, 1.0, 1),      # configs[0] as stated
+    ("gen_tiny_k3_greedy", "tiny", 0, 8192, 64, 3, 128, 0.0, 1.0, 1),
+    ("gen_tiny_k4_temp", "tiny", 0, 8192, 64, 4, 64, 0.8, 0.95, 7),
+    ("gen_base_k3_greedy", "base", 1, 65536, 64, 3, 48, 0.0, 1.0, 1),
+    ("gen_base_k2_temp", "base", 1, 65536, 64, 2, 32, 0.8, 0.95, 7),
+]
+MODEL_SEED = 1234
+PROMPT_SEED = 0
+
+
+def main():
+    import __graft_entry__
+    pkg = __graft_entry__.load_package()
+    if not OL.have_reference():
+        sys.exit("reference build absent: make -f oracle/ref.mk all")
+    root = os.environ.get("L98_MODEL_DIR") or os.path.join(tempfile.gettempdir(), "l98_models")
+    only = set(sys.argv[1:])
+    for name, mdir, cid, V, n_prompt, k, n_new, temp, topp, seed in CASES:
+        if only and name not in only:
+            continue
+        model = pkg.ensure_model(os.path.join(root, mdir), cid, seed=MODEL_SEED)
+        digest = hashlib.sha256(open(os.path.join(model, "model.bin"), "rb").read()).hexdigest()
+        prompt = pkg.prompt_tokens(PROMPT_SEED, n_prompt, V)
+        r = OL.reference_generate(model, prompt, k, n_new, temp, topp, seed=seed)
+        out = {
+            "model": mdir, "config_id": cid, "model_seed": MODEL_SEED, "model_sha256": digest, "vocab": V,
+            "prompt_seed": PROMPT_SEED, "n_prompt": n_prompt, "k": k, "n_new": n_new, "temp": temp,
+            "topp": topp, "sampler_seed": seed,
+            "tokens": [int(t) for t in r["tokens"]],
+            "k_eff": [int(t) for t in r["k_eff"]],
+            "n_accept": [int(t) for t in r["n_accept"]],
+            "rng": int(r["rng"]), "final_pos": r["final_pos"], "mtp_pos": r["mtp_pos"],
+            "ssm_slot": r["ssm_slot"],
+            "source": "oracle/_ref/l98ref_oracle gen (reference engine, float-oracle mode)",
+        }
+        with open(os.path.join(HERE, name + ".json"), "w") as f:
+            json.dump(out, f, indent=1)
+        print(name, len(out["tokens"]), "tokens", flush=True)
+
+
+if __name__ == "__main__":
+    main()
