@@ -144,7 +144,8 @@ def main():
     log(f"model {mdir} ready in {time.time() - t0:.1f}s")
     eng = pkg.Engine(mdir)
     cfg = eng.cfg
-    log(f"device {pkg.hip_lib().l98_device_name().decode()}; weights {eng.m.bytes_device / 1e9:.3f} GB")
+    log(f"device {pkg.hip_lib().l98_device_name().decode()}; weights {eng.m.bytes_device / 1e9:.3f} GB, "
+        f"state {eng.s.bytes_device / 1e6:.1f} MB")
     k = args.k
     prompt = pkg.prompt_tokens(0, args.prompt, cfg.vocab_size)
     t0 = time.time()

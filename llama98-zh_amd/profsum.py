@@ -1,0 +1,77 @@
+"""Summarizes a rocprofv3 kernel trace of the speculative-decoding path.
+
+    rocprofv3 --kernel-trace --stats --output-format csv -d OUT -o prof -- python3 bench.py --no-graph ...
+    python3 llama98-zh_amd/profsum.py OUT/prof_kernel_trace.csv [--vocab V]
+
+Prints, as markdown:
+  * every kernel of the whole run (calls, total, mean, min, max);
+  * one round of the timed loop: the dispatches after one k_accept up to and
+    including the next (the last complete round), grouped by kernel;
+  * the tied lm_head GEMV launches (k_gemv_q8 dispatches whose grid covers
+    `vocab` rows), whose mean duration is the figure bench.py's roofline
+    uses.
+"""
+import argparse
+import collections
+import csv
+
+
+def load(path):
+    rows = []
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            rows.append((r["Kernel_Name"], int(r["Start_Timestamp"]), int(r["End_Timestamp"]),
+                         int(r["Grid_Size_X"]), int(r["Workgroup_Size_X"])))
+    rows.sort(key=lambda r: r[1])
+    return rows
+
+
+def short(name):
+    return name.split("(")[0].replace("void ", "")
+
+
+def table(groups, title, total_label):
+    out = [f"### {title}", "", "| kernel | calls | total us | mean us | min us | max us | % |",
+           "|---|---:|---:|---:|---:|---:|---:|"]
+    tot = sum(sum(v) for v in groups.values())
+    for k, v in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        out.append(f"| `{k}` | {len(v)} | {sum(v) / 1e3:.1f} | {sum(v) / len(v) / 1e3:.2f} | {min(v) / 1e3:.2f} | "
+                   f"{max(v) / 1e3:.2f} | {100 * sum(v) / tot:.1f} |")
+    out.append(f"| **{total_label}** | {sum(len(v) for v in groups.values())} | {tot / 1e3:.1f} | | | | |")
+    return "\n".join(out)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("trace")
+    ap.add_argument("--vocab", type=int, default=65536)
+    ap.add_argument("--gemv-rows-per-block", type=int, default=32,
+                    help="rows per GEMV tile at the lm_head's input width")
+    a = ap.parse_args()
+    rows = load(a.trace)
+    whole = collections.defaultdict(list)
+    for n, s, e, g, w in rows:
+        whole[short(n)].append(e - s)
+    print(table(whole, "Whole run", "all dispatches"))
+    acc = [i for i, r in enumerate(rows) if short(r[0]) == "k_accept"]
+    if len(acc) >= 2:
+        seg = rows[acc[-2] + 1:acc[-1] + 1]
+        grp = collections.defaultdict(list)
+        for n, s, e, g, w in seg:
+            grp[short(n)].append(e - s)
+        span = seg[-1][2] - seg[0][1]
+        print()
+        print(table(grp, f"One round (last complete round; span {span / 1e3:.1f} us without graph replay)",
+                    "round"))
+    tiles = (a.vocab + a.gemv_rows_per_block - 1) // a.gemv_rows_per_block
+    lm = collections.defaultdict(list)
+    for n, s, e, g, w in rows:
+        if short(n).startswith("k_gemv_q8") and w > 0 and g // w == tiles:
+            lm[short(n)].append(e - s)
+    if lm:
+        print()
+        print(table(lm, f"Tied lm_head GEMV ({a.vocab} rows, {tiles} tiles)", "lm_head"))
+
+
+if __name__ == "__main__":
+    main()
