@@ -10,14 +10,42 @@
 #define MAX_CHUNK 8          // tokens per forward chunk (the reference's LZ_BATCH_MAX)
 #define MAX_PAIRS (MAX_CHUNK * MAX_TOPK)
 
+// How a GEMV tile builds its int8 activation rows (in LDS, per block).
+enum {
+    PRO_XQ = 0,        // rows already quantized: xq / xqs
+    PRO_QUANT = 1,     // quantize float rows src
+    PRO_NORM = 2,      // x = src (+ a (+ b)); RMSNorm(1+w); quantize
+    PRO_SILU = 3,      // silu(src) * src2; quantize
+    PRO_COMBINE = 4    // sum over slots of sel_w * src[pair]; quantize
+};
+
+// Prologue of one GEMV job.  Rows are addressed by the tile's activation
+// row index xr (the token, or for grouped experts the token or the pair).
+typedef struct {
+    int mode;
+    int src_stride;          // floats between rows of src / src2 / x_out
+    const float *src;        // QUANT, NORM, SILU: rows; COMBINE: per-pair rows [pairs][in_dim]
+    const float *src2;       // SILU: second operand
+    const float *a, *b;      // NORM: optional residual addends [rows][in_dim]
+    const float *w;          // NORM: weight [in_dim]
+    float eps;
+    int topk;                // COMBINE
+    const int *sel_idx;      // COMBINE: [rows][topk]
+    const float *sel_w;      // COMBINE: [rows][topk]
+    float *x_out;            // NORM: the updated residual rows (written by one block)
+    float *o_out;            // NORM: the normed rows (written by one block)
+    int o_stride;
+    int pad;
+} Prologue;
+
 // One weight matrix of a fused GEMV launch.  Jobs of one launch may differ
-// in input width; each brings its own int8 activations.
+// in input width and prologue.
 typedef struct {
     const int8_t *w;         // [rows][in_dim] int8, row-major
     const float *ws;         // [rows] per-row scale
     float *out;              // out[t * out_stride + row]
-    const int8_t *xq;        // activations [M][in_dim]
-    const float *xqs;        // activation scales [M][in_dim/32]
+    const int8_t *xq;        // PRO_XQ activations [M][in_dim]
+    const float *xqs;        // PRO_XQ activation scales [M][in_dim/32]
     int32_t *acc_out;        // optional exact group sums [M][rows][in_dim/32] (tests)
     int rows;
     int in_dim;
@@ -25,6 +53,7 @@ typedef struct {
     int tile0;               // first tile of this job in the launch grid (set by the launcher)
     int R;                   // rows per tile (set by the launcher)
     int pad;
+    Prologue pro;
 } GemvJob;
 
 typedef struct {
@@ -45,10 +74,11 @@ typedef struct {
     const int8_t *q;         // bank: expert e rows [e*out_rows, (e+1)*out_rows)
     const float *s;
     float *out;              // out[pair * out_rows + row]
-    const int8_t *xq;        // activation rows (by token or by pair)
+    const int8_t *xq;        // PRO_XQ activation rows (by token or by pair)
     const float *xqs;
     int xq_by_pair;          // 1: activation row = pair index, 0: = the pair's token
     int pad;
+    Prologue pro;            // PRO_XQ, PRO_QUANT or PRO_SILU
 } ExpertJob;
 
 // Distinct experts selected by a chunk and their (token, slot) members.

@@ -440,7 +440,7 @@ struct DState {
     int8_t *kq = nullptr, *vq = nullptr;
     float *ks = nullptr, *vs = nullptr;
     // activations
-    float *x, *mtp_x, *chain, *blk, *up_out, *sd_out;
+    float *x, *x2, *mtp_x, *mtp_x2, *chain, *blk, *up_out, *sd_out;
     float *qg, *kp, *vp, *qh;
     float *pq, *pk, *pv, *pfa, *pb, *pg, *qc, *kc, *vc, *gate_pre;
     float *rl, *latx, *sgo, *suo, *h1, *h3, *h2, *hb, *hb2, *ffn_out;
@@ -489,8 +489,8 @@ bool carve(DState *s) {
     size_t kv = (size_t)s->planes * s->seq_len * c.attn_kv_dim;
     s->kq = I8(kv); s->vq = I8(kv);
     s->ks = F(kv / 32); s->vs = F(kv / 32);
-    s->x = F((size_t)B * d);
-    s->mtp_x = F((size_t)B * d); s->chain = F(d); s->blk = F((size_t)B * d);
+    s->x = F((size_t)B * d); s->x2 = F((size_t)B * d);
+    s->mtp_x = F((size_t)B * d); s->mtp_x2 = F((size_t)B * d); s->chain = F(d); s->blk = F((size_t)B * d);
     s->up_out = F((size_t)B * d); s->sd_out = F((size_t)B * d);
     s->qg = F((size_t)B * c.attn_qgate_dim); s->kp = F((size_t)B * c.attn_kv_dim);
     s->vp = F((size_t)B * c.attn_kv_dim); s->qh = F((size_t)B * c.attn_q_dim);
@@ -530,24 +530,67 @@ bool carve(DState *s) {
 DState *S(LZRunState *s) { return (DState *)s->impl; }
 const DModel *Mo(const LZModel *m) { return (const DModel *)m->impl; }
 
+// A fused GEMV launch.  Jobs with pre-quantized input and no activations
+// of their own read the state's xq / xqs.
 int gemv(DState *s, std::initializer_list<GemvJob> jobs, int mtok) {
     GemvBatch b{};
     b.n = 0;
-    for (const GemvJob &j : jobs) b.job[b.n++] = j;
+    for (const GemvJob &j : jobs) {
+        GemvJob &o = b.job[b.n++];
+        o = j;
+        if (o.pro.mode == PRO_XQ && !o.xq) { o.xq = s->xq; o.xqs = s->xqs; }
+    }
     return l98k_gemv(&b, mtok, s->st);
 }
 
-// One GEMV job: w (rows x cols) over activations xq/xqs (rows of w.cols).
-GemvJob J(const DMat &w, float *out, int out_stride, const int8_t *xq, const float *xqs) {
+// GEMV job prologues (how a tile builds its int8 activation rows).
+Prologue PX() {
+    Prologue p{};
+    p.mode = PRO_XQ;
+    return p;
+}
+Prologue PQ(const float *src, int stride) {
+    Prologue p{};
+    p.mode = PRO_QUANT; p.src = src; p.src_stride = stride;
+    return p;
+}
+Prologue PS(const float *src, const float *src2, int stride) {
+    Prologue p{};
+    p.mode = PRO_SILU; p.src = src; p.src2 = src2; p.src_stride = stride;
+    return p;
+}
+// RMSNorm(1+w) of x (+ a (+ b)); x_out receives the folded residual and
+// o_out the normed rows (both optional, written once per launch).
+Prologue PN(const float *x, int stride, const float *a, const float *b, const float *w, float eps, float *x_out,
+            float *o_out, int o_stride) {
+    Prologue p{};
+    p.mode = PRO_NORM; p.src = x; p.src_stride = stride; p.a = a; p.b = b; p.w = w; p.eps = eps;
+    p.x_out = x_out; p.o_out = o_out; p.o_stride = o_stride;
+    return p;
+}
+Prologue PC(const float *h2, const int *sel_idx, const float *sel_w, int topk) {
+    Prologue p{};
+    p.mode = PRO_COMBINE; p.src = h2; p.sel_idx = sel_idx; p.sel_w = sel_w; p.topk = topk;
+    return p;
+}
+
+// One GEMV job: w (rows x cols) whose activations the prologue builds.
+GemvJob J(const DMat &w, float *out, int out_stride, const Prologue &pro) {
     GemvJob j{};
     j.w = w.q; j.ws = w.s; j.out = out; j.rows = w.rows; j.in_dim = w.cols; j.out_stride = out_stride;
+    j.pro = pro;
+    return j;
+}
+// The same over pre-quantized activations.
+GemvJob JX(const DMat &w, float *out, int out_stride, const int8_t *xq, const float *xqs) {
+    GemvJob j = J(w, out, out_stride, PX());
     j.xq = xq; j.xqs = xqs;
     return j;
 }
 
-ExpertJob EJ(const ExpertBank &bank, float *out, const int8_t *xq, const float *xqs, int by_pair) {
+ExpertJob EJ(const ExpertBank &bank, float *out, int by_pair, const Prologue &pro) {
     ExpertJob j{};
-    j.q = bank.q; j.s = bank.s; j.out = out; j.xq = xq; j.xqs = xqs; j.xq_by_pair = by_pair;
+    j.q = bank.q; j.s = bank.s; j.out = out; j.xq_by_pair = by_pair; j.pro = pro;
     return j;
 }
 
@@ -566,18 +609,17 @@ int ctl_get(DState *s, DevCtl *h) {
 
 // ---------------------------------------------------------- layers ---
 
-// Attention block: input quantized in xq (rows nt), output xb2 -> s->blk.
-int attn_block(DState *s, const DLayer &L, int plane, const int *ctl_pos, int pos_off, int nt,
+// Attention block: the projections' input rows come from `in` (rows nt);
+// output xb2 -> s->blk.
+int attn_block(DState *s, const DLayer &L, const Prologue &in, int plane, const int *ctl_pos, int pos_off, int nt,
                int max_pos, bool kv_only) {
     const LZModelConfig &c = s->m->c;
     const int d = c.hidden_size;
-    (void)d;
     if (kv_only)
-        CK(gemv(s, {J(L.k, s->kp, c.attn_kv_dim, s->xq, s->xqs), J(L.v, s->vp, c.attn_kv_dim, s->xq, s->xqs)},
-                nt));
+        CK(gemv(s, {J(L.k, s->kp, c.attn_kv_dim, in), J(L.v, s->vp, c.attn_kv_dim, in)}, nt));
     else
-        CK(gemv(s, {J(L.k, s->kp, c.attn_kv_dim, s->xq, s->xqs), J(L.v, s->vp, c.attn_kv_dim, s->xq, s->xqs),
-                    J(L.q, s->qg, c.attn_qgate_dim, s->xq, s->xqs)}, nt));
+        CK(gemv(s, {J(L.k, s->kp, c.attn_kv_dim, in), J(L.v, s->vp, c.attn_kv_dim, in),
+                    J(L.q, s->qg, c.attn_qgate_dim, in)}, nt));
     AttnArgs a{};
     a.qg = s->qg; a.kp = s->kp; a.vp = s->vp;
     a.q_norm = L.q_norm; a.k_norm = L.k_norm; a.rope_cs = s->m->rope_cs;
@@ -606,7 +648,7 @@ int attn_block(DState *s, const DLayer &L, int plane, const int *ctl_pos, int po
     CK(l98k_attn_prep(&a, nt, s->st));
     if (kv_only) return 0;
     CK(l98k_attn_decode(&a, nt, max_pos + 1, s->st));
-    CK(gemv(s, {J(L.o, s->blk, d, s->xq2, s->xqs2)}, nt));
+    CK(gemv(s, {JX(L.o, s->blk, d, s->xq2, s->xqs2)}, nt));
     return 0;
 }
 
@@ -621,23 +663,19 @@ float ssm_scale(int kd) {   // lz_rsqrt(lin_k_head_dim), src/forward_state.c:140
     return y;
 }
 
-// KDA block: input quantized in xq, output -> s->blk.
-int kda_block(DState *s, const DLayer &L, int li, int nt, int advance) {
+// KDA block: the projections' input rows come from `in`; output -> s->blk.
+int kda_block(DState *s, const DLayer &L, const Prologue &in, int li, int nt, int advance) {
     const LZModelConfig &c = s->m->c;
     const int d = c.hidden_size, key = c.lin_key_dim, value = c.lin_value_dim;
     const int nv = c.lin_n_v_heads, kd = c.lin_k_head_dim, vd = c.lin_v_head_dim;
     const int nvk = nv * kd;
-    const int8_t *xq = s->xq;
-    const float *xqs = s->xqs;
-    CK(gemv(s, {J(L.kq, s->pq, key, xq, xqs), J(L.kk, s->pk, key, xq, xqs), J(L.kv, s->pv, value, xq, xqs),
-                J(L.fa, s->pfa, c.kda_gate_rank, xq, xqs), J(L.kb, s->pb, nv, xq, xqs),
-                J(L.kg, s->pg, value, xq, xqs)}, nt));
+    CK(gemv(s, {J(L.kq, s->pq, key, in), J(L.kk, s->pk, key, in), J(L.kv, s->pv, value, in),
+                J(L.fa, s->pfa, c.kda_gate_rank, in), J(L.kb, s->pb, nv, in), J(L.kg, s->pg, value, in)}, nt));
     const int hist = c.conv_kernel - 1;
     CK(l98k_kda_conv(s->pq, s->pk, s->pv, key, value, L.conv,
                      s->conv + (size_t)li * c.lin_conv_dim * hist, s->conv_slot, c.conv_kernel,
-                     &s->ctl->slot_base, s->depth, advance, nt, s->qc, s->kc, s->vc,
-                     s->pfa, c.kda_gate_rank, s->xq2, s->xqs2, s->st));
-    CK(gemv(s, {J(L.fb, s->gate_pre, nvk, s->xq2, s->xqs2)}, nt));
+                     &s->ctl->slot_base, s->depth, advance, nt, s->qc, s->kc, s->vc, s->st));
+    CK(gemv(s, {J(L.fb, s->gate_pre, nvk, PQ(s->pfa, c.kda_gate_rank))}, nt));
     KdaRecurArgs a{};
     a.qc = s->qc; a.kc = s->kc; a.vc = s->vc; a.gate_pre = s->gate_pre; a.bvec = s->pb; a.gz = s->pg;
     a.a_log = L.a_log; a.dt_bias = L.dt_bias; a.o_norm = L.o_norm;
@@ -649,31 +687,27 @@ int kda_block(DState *s, const DLayer &L, int li, int nt, int advance) {
     a.depth = s->depth; a.advance = advance; a.nt = nt;
     a.scale = ssm_scale(kd); a.eps = c.rms_norm_eps;
     CK(l98k_kda_recur(&a, kd, vd, s->st));
-    CK(gemv(s, {J(L.ko, s->blk, d, s->xq2, s->xqs2)}, nt));
+    CK(gemv(s, {JX(L.ko, s->blk, d, s->xq2, s->xqs2)}, nt));
     return 0;
 }
 
-// MoE block: input quantized in xq; outputs up_out and sd_out (the caller's
-// next norm folds x += up_out + sd_out).
-int moe_block(DState *s, const DLayer &L, int nt) {
+// MoE block: the router / latent-down / shared gate-up inputs come from
+// `in`; outputs up_out and sd_out (the caller's next norm folds
+// x += up_out + sd_out).
+int moe_block(DState *s, const DLayer &L, const Prologue &in, int nt) {
     const LZModelConfig &c = s->m->c;
     const int d = c.hidden_size, E = c.num_experts, topk = c.num_experts_per_token;
     const int lat = c.moe_latent_dim, inter = c.moe_intermediate_size, sw = c.moe_shared_width;
-    const int8_t *xq = s->xq;
-    const float *xqs = s->xqs;
-    CK(gemv(s, {J(L.router, s->rl, E, xq, xqs), J(L.down, s->latx, lat, xq, xqs), J(L.sg, s->sgo, sw, xq, xqs),
-                J(L.su, s->suo, sw, xq, xqs)}, nt));
-    CK(l98k_moe_route(s->rl, L.bias, E, topk, nt, s->sel_idx, s->sel_w, s->grp, &s->ctl->expert_tally,
-                      s->latx, lat, s->xq2, s->xqs2, s->st));
+    CK(gemv(s, {J(L.router, s->rl, E, in), J(L.down, s->latx, lat, in), J(L.sg, s->sgo, sw, in),
+                J(L.su, s->suo, sw, in)}, nt));
+    CK(l98k_moe_route(s->rl, L.bias, E, topk, nt, s->sel_idx, s->sel_w, s->grp, &s->ctl->expert_tally, s->st));
     const int max_groups = nt * topk < E ? nt * topk : E;
-    const ExpertJob up2[2] = {EJ(L.w1, s->h1, s->xq2, s->xqs2, 0), EJ(L.w3, s->h3, s->xq2, s->xqs2, 0)};
+    const ExpertJob up2[2] = {EJ(L.w1, s->h1, 0, PQ(s->latx, lat)), EJ(L.w3, s->h3, 0, PQ(s->latx, lat))};
     CK(l98k_expert_gemv(up2, 2, s->grp, max_groups, lat, inter, s->st));
-    CK(l98k_act_quant(s->h1, s->h3, inter, nt * topk, s->xq3, s->xqs3, s->sgo, s->suo, sw, nt, s->xq4,
-                      s->xqs4, s->st));
-    const ExpertJob down1[1] = {EJ(L.w2, s->h2, s->xq3, s->xqs3, 1)};
+    const ExpertJob down1[1] = {EJ(L.w2, s->h2, 1, PS(s->h1, s->h3, inter))};
     CK(l98k_expert_gemv(down1, 1, s->grp, max_groups, inter, lat, s->st));
-    CK(l98k_moe_combine(s->h2, s->sel_idx, s->sel_w, topk, lat, nt, nullptr, s->xq2, s->xqs2, s->st));
-    CK(gemv(s, {J(L.up, s->up_out, d, s->xq2, s->xqs2), J(L.sd, s->sd_out, d, s->xq4, s->xqs4)}, nt));
+    CK(gemv(s, {J(L.up, s->up_out, d, PC(s->h2, s->sel_idx, s->sel_w, topk)),
+                J(L.sd, s->sd_out, d, PS(s->sgo, s->suo, sw))}, nt));
     return 0;
 }
 
@@ -688,26 +722,47 @@ int forward_chunk(DState *s, const int *toks, int nt, const int *ctl_pos, int po
     const LZModelConfig &c = m->c;
     const int d = c.hidden_size;
     const float eps = c.rms_norm_eps;
-    CK(l98k_embed(m->embed.q, m->embed.s, toks, d, nt, s->x, s->st));
+    // The residual stream alternates between two buffers: a norm fused into
+    // its consumer GEMV reads one and writes the folded residual to the
+    // other, since every block of that launch reads the input.
+    float *xb[2] = {s->x, s->x2};
+    int cur = 0;
+    const bool fused = l98k_gemv_norm_fits(d, nt) != 0;
+    CK(l98k_embed(m->embed.q, m->embed.s, toks, d, nt, xb[cur], s->st));
     const float *ra = nullptr, *rb = nullptr;     // pending residual of the previous block
+    // Input rows of a block: the fused norm prologue, or a norm kernel that
+    // folds the residual in place and quantizes into xq.
+    auto norm_in = [&](const float *a, const float *b, const float *w, Prologue &P) -> int {
+        if (fused) {
+            P = PN(xb[cur], d, a, b, w, eps, a ? xb[cur ^ 1] : nullptr, nullptr, 0);
+            if (a) cur ^= 1;
+            return 0;
+        }
+        CK(l98k_rmsnorm(xb[cur], d, a, b, w, d, eps, nt, nullptr, 0, s->xq, s->xqs, s->st));
+        P = PX();
+        return 0;
+    };
     for (int l = 0; l < c.n_layers; l++) {
         const DLayer &L = m->L[l];
-        CK(l98k_rmsnorm(s->x, d, ra, rb, L.in_norm, d, eps, nt, nullptr, 0, s->xq, s->xqs, s->st));
-        if (L.type == 1) CK(attn_block(s, L, m->full_index[l], ctl_pos, pos_off, nt, max_pos, false));
-        else CK(kda_block(s, L, m->lin_index[l], nt, all_logits ? 1 : 0));
-        CK(l98k_rmsnorm(s->x, d, s->blk, nullptr, L.post_norm, d, eps, nt, nullptr, 0, s->xq, s->xqs, s->st));
-        CK(moe_block(s, L, nt));
+        Prologue P;
+        CK(norm_in(ra, rb, L.in_norm, P));
+        if (L.type == 1) CK(attn_block(s, L, P, m->full_index[l], ctl_pos, pos_off, nt, max_pos, false));
+        else CK(kda_block(s, L, P, m->lin_index[l], nt, all_logits ? 1 : 0));
+        CK(norm_in(s->blk, nullptr, L.post_norm, P));
+        CK(moe_block(s, L, P, nt));
         ra = s->up_out;
         rb = s->sd_out;
     }
+    // The lm_head's grid is far larger than the chip, so its norm runs once,
+    // in its own kernel, rather than in every tile.
     const bool want_logits = all_logits || !skip_logits;
-    CK(l98k_rmsnorm(s->x, d, ra, rb, m->final_norm, d, eps, nt, capture, d,
+    CK(l98k_rmsnorm(xb[cur], d, ra, rb, m->final_norm, d, eps, nt, capture, d,
                     want_logits ? s->xq : nullptr, s->xqs, s->st));
     if (all_logits) {
-        CK(gemv(s, {J(m->embed, logits_out, c.vocab_size, s->xq, s->xqs)}, nt));
+        CK(gemv(s, {JX(m->embed, logits_out, c.vocab_size, s->xq, s->xqs)}, nt));
     } else if (!skip_logits) {
-        CK(gemv(s, {J(m->embed, s->logits, c.vocab_size, s->xq + (size_t)(nt - 1) * d,
-                      s->xqs + (size_t)(nt - 1) * (d / 32))}, 1));
+        CK(gemv(s, {JX(m->embed, s->logits, c.vocab_size, s->xq + (size_t)(nt - 1) * d,
+                       s->xqs + (size_t)(nt - 1) * (d / 32))}, 1));
     }
     return 0;
 }
@@ -719,21 +774,18 @@ int draft_step(DState *s, const int *toks, const int *ctl_pos, int pos_off, int 
                float *out_logits, int *out_tok) {
     const DModel *m = s->m;
     const LZModelConfig &c = m->c;
-    const int d = c.hidden_size;
+    const int d = c.hidden_size, I = c.mtp_intermediate_size;
     const float eps = c.rms_norm_eps;
     CK(l98k_mtp_pre(m->embed.q, m->embed.s, toks, s->chain, d, m->mtp_pre_e, m->mtp_pre_h, eps, 1, s->xq,
                     s->xqs, s->st));
-    CK(gemv(s, {J(m->mtp_fc, s->mtp_x, d, s->xq, s->xqs)}, 1));
-    CK(l98k_rmsnorm(s->mtp_x, d, nullptr, nullptr, m->mtp.in_norm, d, eps, 1, nullptr, 0, s->xq, s->xqs, s->st));
-    CK(attn_block(s, m->mtp, s->planes - 1, ctl_pos, pos_off, 1, max_pos, false));
-    CK(l98k_rmsnorm(s->mtp_x, d, s->blk, nullptr, m->mtp.post_norm, d, eps, 1, nullptr, 0, s->xq, s->xqs, s->st));
-    CK(gemv(s, {J(m->mtp_gate, s->hb, c.mtp_intermediate_size, s->xq, s->xqs),
-                J(m->mtp_up, s->hb2, c.mtp_intermediate_size, s->xq, s->xqs)}, 1));
-    CK(l98k_act_quant(s->hb, s->hb2, c.mtp_intermediate_size, 1, s->xq2, s->xqs2, nullptr, nullptr, 0, 0,
-                      nullptr, nullptr, s->st));
-    CK(gemv(s, {J(m->mtp_down, s->ffn_out, d, s->xq2, s->xqs2)}, 1));
-    CK(l98k_rmsnorm(s->mtp_x, d, s->ffn_out, nullptr, m->mtp_norm, d, eps, 1, s->chain, d, s->xq, s->xqs, s->st));
-    CK(gemv(s, {J(m->embed, out_logits, c.vocab_size, s->xq, s->xqs)}, 1));
+    CK(gemv(s, {JX(m->mtp_fc, s->mtp_x, d, s->xq, s->xqs)}, 1));
+    CK(attn_block(s, m->mtp, PN(s->mtp_x, d, nullptr, nullptr, m->mtp.in_norm, eps, nullptr, nullptr, 0),
+                  s->planes - 1, ctl_pos, pos_off, 1, max_pos, false));
+    const Prologue post = PN(s->mtp_x, d, s->blk, nullptr, m->mtp.post_norm, eps, s->mtp_x2, nullptr, 0);
+    CK(gemv(s, {J(m->mtp_gate, s->hb, I, post), J(m->mtp_up, s->hb2, I, post)}, 1));
+    CK(gemv(s, {J(m->mtp_down, s->ffn_out, d, PS(s->hb, s->hb2, I))}, 1));
+    CK(l98k_rmsnorm(s->mtp_x2, d, s->ffn_out, nullptr, m->mtp_norm, d, eps, 1, s->chain, d, s->xq, s->xqs, s->st));
+    CK(gemv(s, {JX(m->embed, out_logits, c.vocab_size, s->xq, s->xqs)}, 1));
     if (out_tok) CK(l98k_argmax(out_logits, c.vocab_size, 1, 1, out_tok, s->amax_part, s->amax_cnt, s->st));
     return 0;
 }
@@ -750,9 +802,9 @@ int mtp_prefill_dev(DState *s, const float *h, const int *toks, int n, const int
         int k = n - done < MAX_CHUNK ? n - done : MAX_CHUNK;
         CK(l98k_mtp_pre(m->embed.q, m->embed.s, toks + done, h + (size_t)done * d, d, m->mtp_pre_e,
                         m->mtp_pre_h, eps, k, s->xq, s->xqs, s->st));
-        CK(gemv(s, {J(m->mtp_fc, s->mtp_x, d, s->xq, s->xqs)}, k));
-        CK(l98k_rmsnorm(s->mtp_x, d, nullptr, nullptr, m->mtp.in_norm, d, eps, k, nullptr, 0, s->xq, s->xqs, s->st));
-        CK(attn_block(s, m->mtp, s->planes - 1, ctl_pos, pos_off + done, k, 0, true));
+        CK(gemv(s, {JX(m->mtp_fc, s->mtp_x, d, s->xq, s->xqs)}, k));
+        CK(attn_block(s, m->mtp, PN(s->mtp_x, d, nullptr, nullptr, m->mtp.in_norm, eps, nullptr, nullptr, 0),
+                      s->planes - 1, ctl_pos, pos_off + done, k, 0, true));
         done += k;
     }
     return 0;
@@ -1605,7 +1657,7 @@ extern "C" int l98_time_kernel(const LZModel *mm, LZRunState *s, int which, int 
     // after it and KV rows the next verify rewrites, so repeated launches read
     // identical inputs and leave the session's state usable.
     auto once = [&]() -> int {
-        if (which == 0) return gemv(d, {J(m->embed, d->mtp_logits, c.vocab_size, d->xq, d->xqs)}, mrows);
+        if (which == 0) return gemv(d, {JX(m->embed, d->mtp_logits, c.vocab_size, d->xq, d->xqs)}, mrows);
         return forward_chunk(d, d->ctl->tok, mrows, &d->ctl->anchor_pos, 1, d->seq_len - 1, d->vhidden, true,
                              d->mtp_logits, false);
     };

@@ -27,10 +27,14 @@ __constant__ float c_exp_tab[32];
 
 // The 2^(i/32) table of d_exp is indexed by a per-lane value, so it is read
 // from LDS (one ds_read) rather than constant memory (a vector memory load).
-#define DECLARE_EXP_TAB(tab)                                      \
-    __shared__ float tab[32];                                      \
-    if (threadIdx.x < 32) tab[threadIdx.x] = c_exp_tab[threadIdx.x]; \
-    __syncthreads()
+// EXP_TAB_LOAD issues the load of a thread's entry early, with the kernel's
+// other loads; EXP_TAB_PUT stores it, and a barrier must follow before the
+// first d_exp.
+#define EXP_TAB_LOAD(tab)     \
+    __shared__ float tab[32]; \
+    const float tab##_v = c_exp_tab[threadIdx.x & 31]
+#define EXP_TAB_PUT(tab) \
+    if (threadIdx.x < 32) tab[threadIdx.x] = tab##_v
 
 __device__ __forceinline__ float f_from_u(uint32_t u) { return __uint_as_float(u); }
 __device__ __forceinline__ uint32_t u_from_f(float f) { return __float_as_uint(f); }
@@ -153,55 +157,37 @@ __device__ __forceinline__ void d_quant_group32(float x, int8_t *q, float *s) {
     if ((threadIdx.x & 31) == 0) *s = sg;
 }
 
-// Serial left-to-right float sum of n values in LDS by one lane.  The adds
-// stay in index order; the LDS reads run a chunk ahead of them (32 values
-// per chunk, double buffered) so the chain is bound by add latency, not by
-// LDS latency.  v must be 16-byte aligned.
-__device__ __forceinline__ float serial_sum(const float *v, int n) {
+// Serial left-to-right float sum of n values in LDS by one lane (n % 4 ==
+// 0 and v 16-byte aligned).  The adds stay in index order; the loop body
+// reads 4 values at a time and is unrolled so the LDS reads run ahead of the
+// dependent adds.  The common row width 1024 is a fully unrolled instance.
+template <int N>
+__device__ __forceinline__ float serial_sum_n(const float *v) {
     float ss = 0.0f;
-    const float4 *v4 = reinterpret_cast<const float4 *>(v);
-    const int nc = n >> 5;                       // full chunks of 32
-    float4 a[8], b[8];
-    if (nc > 0) {
 #pragma unroll
-        for (int j = 0; j < 8; j++) a[j] = v4[j];
+    for (int i = 0; i < N; i += 4) {
+        const float4 q = *reinterpret_cast<const float4 *>(v + i);
+        ss += q.x; ss += q.y; ss += q.z; ss += q.w;
     }
-    for (int c = 0; c < nc; c++) {
-        if (c + 1 < nc) {
-#pragma unroll
-            for (int j = 0; j < 8; j++) b[j] = v4[(c + 1) * 8 + j];
-        }
-#pragma unroll
-        for (int j = 0; j < 8; j++) { ss += a[j].x; ss += a[j].y; ss += a[j].z; ss += a[j].w; }
-#pragma unroll
-        for (int j = 0; j < 8; j++) a[j] = b[j];
+    return ss;
+}
+
+__device__ __forceinline__ float serial_sum(const float *v, int n) {
+    if (n == 1024) return serial_sum_n<1024>(v);
+    float ss = 0.0f;
+    int i = 0;
+#pragma unroll 8
+    for (; i + 4 <= n; i += 4) {
+        const float4 q = *reinterpret_cast<const float4 *>(v + i);
+        ss += q.x; ss += q.y; ss += q.z; ss += q.w;
     }
-    for (int i = nc << 5; i < n; i++) ss += v[i];
+    for (; i < n; i++) ss += v[i];
     return ss;
 }
 
 // -------------------------------------------------------------- helpers ---
 
 __device__ __forceinline__ int imin(int a, int b) { return a < b ? a : b; }
-
-// Per-32 quantization of `total` contiguous floats (a whole number of groups)
-// by the threads of a block whose size is a multiple of 32.  Element e goes
-// to xq[e], group e/32's scale to xqs[e/32].  Four loads per thread are in
-// flight before the first shuffle.
-__device__ __forceinline__ void quant_span(const float *__restrict__ x, int total, int8_t *__restrict__ xq,
-                                           float *__restrict__ xqs) {
-    const int tid = threadIdx.x, nthr = blockDim.x;
-    for (int base = 0; base < total; base += nthr * 4) {
-        float v[4];
-#pragma unroll
-        for (int u = 0; u < 4; u++) v[u] = x[imin(base + u * nthr + tid, total - 1)];
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int e = base + u * nthr + tid;
-            if (base + u * nthr + (tid & ~31) < total) d_quant_group32(v[u], xq + e, xqs + (e >> 5));
-        }
-    }
-}
 
 // -------------------------------------------------------------- embed ---
 
@@ -217,80 +203,135 @@ __global__ void k_embed(const int8_t *__restrict__ q, const float *__restrict__ 
 }
 
 // ------------------------------------------------------- rmsnorm (+q8) ---
+//
+// Row kernels hold a row of n floats in a 64-lane block as float4 f =
+// lane + 64*j (PJ per lane), so every 32-element quantization group is an
+// aligned lane octet (see quant_octet below).
 
-// RMSNorm(1+w) of one row held by a 64-lane block as v[j] = element
-// j*64 + lane (lz_rmsnorm, src/ops_norm.c:690-747: sum of squares serial in
-// index order, inv = rsqrt(ss/n + eps), o = (x*inv)*(1+w)), then the
-// optional store of o and its per-32 quantization.
-template <int NC>
-__device__ __forceinline__ void norm_row(const float (&v)[NC], const float (&wv)[NC], int n, float eps,
-                                         float *sh, float *s_inv, float *__restrict__ out,
-                                         int8_t *__restrict__ xq, float *__restrict__ xqs) {
-    const int lane = threadIdx.x;
+__device__ __forceinline__ uint32_t umax(uint32_t a, uint32_t b) { return a > b ? a : b; }
+
+// Max over the 8 lanes of an aligned lane octet (DPP within a row).
+__device__ __forceinline__ uint32_t octet_max(uint32_t m) {
+    m = umax(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
+    m = umax(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
+    m = umax(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x141, 0xF, 0xF, false));  // row_half_mirror
+    return m;
+}
+
+// Per-32 quantization (src/ops_quant.c:1633-1670, 2152-2286) of a group held
+// as 4 consecutive elements per lane over an aligned lane octet.  Returns the
+// four int8 packed little-endian; *sg receives the group scale.  Every lane
+// of the octet must execute it.
+__device__ __forceinline__ uint32_t quant_octet(float4 v, float *sg_out) {
+    const float INV127 = 1.0f / 127.0f;
+    uint32_t m = umax(umax(u_from_f(v.x) & 0x7FFFFFFFu, u_from_f(v.y) & 0x7FFFFFFFu),
+                      umax(u_from_f(v.z) & 0x7FFFFFFFu, u_from_f(v.w) & 0x7FFFFFFFu));
+    const float amax = f_from_u(octet_max(m));
+    float sg, inv;
+    bool fast;
+    if (amax > 0.0f) {
+        sg = amax * INV127;
+        inv = 127.0f / amax;
+        fast = (inv <= 3.40282347e+38f);
+        if (sg < 1.0e-30f) { sg = 1.0f; inv = 0.0f; fast = true; }
+    } else {
+        sg = 1.0f; inv = 0.0f; fast = true;
+    }
+    float e[4] = {v.x, v.y, v.z, v.w};
+    if (fast) {
 #pragma unroll
-    for (int j = 0; j < NC; j++) {
-        const int i = j * 64 + lane;
-        if (i < n) sh[i] = v[j] * v[j];
+        for (int i = 0; i < 4; i++) e[i] = e[i] * inv;
+    } else {                             // 127/amax overflowed: divide by the scale instead
+#pragma unroll
+        for (int i = 0; i < 4; i++) e[i] = e[i] / sg;
+    }
+    uint32_t packed = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        int qi = d_q8_round(e[i]);
+        qi = qi > 127 ? 127 : qi;
+        qi = qi < -127 ? -127 : qi;
+        packed |= ((uint32_t)qi & 0xFFu) << (8 * i);
+    }
+    *sg_out = sg;
+    return packed;
+}
+
+// RMSNorm(1+w) of the block's row v (lz_rmsnorm, src/ops_norm.c:690-747:
+// sum of squares serial in index order by lane 0, inv = rsqrt(ss/n + eps),
+// o = (x*inv)*(1+w)), then the optional store of o and its per-32
+// quantization.  n % 32 == 0.
+template <int PJ>
+__device__ __forceinline__ void norm_row(const float4 (&v)[PJ], const float4 (&wn)[PJ], int n, float eps,
+                                         float *sq, float *s_inv, float *__restrict__ out,
+                                         int8_t *__restrict__ xq, float *__restrict__ xqs) {
+    const int lane = threadIdx.x, nf = n >> 2;
+#pragma unroll
+    for (int j = 0; j < PJ; j++) {
+        const int f = lane + 64 * j;
+        if (f < nf) reinterpret_cast<float4 *>(sq)[f] =
+            make_float4(v[j].x * v[j].x, v[j].y * v[j].y, v[j].z * v[j].z, v[j].w * v[j].w);
     }
     __syncthreads();
-    if (lane == 0) *s_inv = d_rsqrt(d_ss_over_n(serial_sum(sh, n), n) + eps);
+    if (lane == 0) *s_inv = d_rsqrt(d_ss_over_n(serial_sum(sq, n), n) + eps);
     __syncthreads();
     const float inv = *s_inv;
 #pragma unroll
-    for (int j = 0; j < NC; j++) {
-        const int i = j * 64 + lane;
-        if (j * 64 < n) {
-            float o = 0.0f;
-            if (i < n) {
-                o = v[j] * inv * (1.0f + wv[j]);
-                if (out) out[i] = o;
+    for (int j = 0; j < PJ; j++) {
+        const int f = lane + 64 * j;
+        const float4 o = make_float4(v[j].x * inv * (1.0f + wn[j].x), v[j].y * inv * (1.0f + wn[j].y),
+                                     v[j].z * inv * (1.0f + wn[j].z), v[j].w * inv * (1.0f + wn[j].w));
+        if (out && f < nf) reinterpret_cast<float4 *>(out)[f] = o;
+        if (xq) {
+            float sg;
+            const uint32_t q = quant_octet(o, &sg);
+            if (f < nf) {
+                reinterpret_cast<uint32_t *>(xq)[f] = q;
+                if (!(f & 7)) xqs[f >> 3] = sg;
             }
-            if (xq && j * 64 + (lane & ~31) < n) d_quant_group32(o, xq + i, xqs + (i >> 5));
         }
     }
 }
 
-// One 64-lane block per row, n <= 64*NC.  Optionally first folds the
-// residual: x_row = x_row + (a_row [+ b_row]) (the reference's x += xb2 with
-// xb2 = up + shared already summed, src/forward.c:1449-1557,
-// src/forward_moe.c:552), then norm_row.  Every load of the row is issued
-// before the first use.
-template <int NC>
+// One 64-lane block per row, n <= 256*PJ.  Optionally first folds the
+// residual in place: x_row = x_row + (a_row [+ b_row]) (the reference's
+// x += xb2 with xb2 = up + shared already summed, src/forward.c:1449-1557,
+// src/forward_moe.c:552), then norm_row.  Every load is issued up front.
+template <int PJ>
 __global__ __launch_bounds__(64) void k_rmsnorm(float *__restrict__ x, int x_stride,
                                                 const float *__restrict__ a, const float *__restrict__ b,
                                                 const float *__restrict__ w, int n, float eps,
                                                 float *__restrict__ out, int out_stride,
                                                 int8_t *__restrict__ xq, float *__restrict__ xqs) {
-    __shared__ __align__(16) float sh[64 * NC];
+    __shared__ __align__(16) float sq[256 * PJ];
     __shared__ float s_inv;
-    const int row = blockIdx.x, lane = threadIdx.x;
-    float *xr = x + (size_t)row * x_stride;
-    float v[NC], wv[NC];
+    const int row = blockIdx.x, lane = threadIdx.x, nf = n >> 2;
+    float4 *xr = reinterpret_cast<float4 *>(x + (size_t)row * x_stride);
+    float4 v[PJ], wn[PJ];
 #pragma unroll
-    for (int j = 0; j < NC; j++) {
-        const int ic = imin(j * 64 + lane, n - 1);
-        v[j] = xr[ic];
-        wv[j] = w[ic];
+    for (int j = 0; j < PJ; j++) {
+        const int fc = imin(lane + 64 * j, nf - 1);
+        v[j] = xr[fc];
+        wn[j] = reinterpret_cast<const float4 *>(w)[fc];
     }
     if (a) {
-        float av[NC];
+        float4 av[PJ];
 #pragma unroll
-        for (int j = 0; j < NC; j++) av[j] = a[(size_t)row * n + imin(j * 64 + lane, n - 1)];
+        for (int j = 0; j < PJ; j++) av[j] = reinterpret_cast<const float4 *>(a + (size_t)row * n)[imin(lane + 64 * j, nf - 1)];
         if (b) {
-            float bv[NC];
 #pragma unroll
-            for (int j = 0; j < NC; j++) bv[j] = b[(size_t)row * n + imin(j * 64 + lane, n - 1)];
-#pragma unroll
-            for (int j = 0; j < NC; j++) av[j] = av[j] + bv[j];
+            for (int j = 0; j < PJ; j++) {
+                const float4 bv = reinterpret_cast<const float4 *>(b + (size_t)row * n)[imin(lane + 64 * j, nf - 1)];
+                av[j] = make_float4(av[j].x + bv.x, av[j].y + bv.y, av[j].z + bv.z, av[j].w + bv.w);
+            }
         }
 #pragma unroll
-        for (int j = 0; j < NC; j++) {
-            v[j] = v[j] + av[j];
-            const int i = j * 64 + lane;
-            if (i < n) xr[i] = v[j];
+        for (int j = 0; j < PJ; j++) {
+            v[j] = make_float4(v[j].x + av[j].x, v[j].y + av[j].y, v[j].z + av[j].z, v[j].w + av[j].w);
+            if (lane + 64 * j < nf) xr[lane + 64 * j] = v[j];
         }
     }
-    norm_row<NC>(v, wv, n, eps, sh, &s_inv, out ? out + (size_t)row * out_stride : nullptr,
+    norm_row<PJ>(v, wn, n, eps, sq, &s_inv, out ? out + (size_t)row * out_stride : nullptr,
                  xq ? xq + (size_t)row * n : nullptr, xqs ? xqs + (size_t)row * (n >> 5) : nullptr);
 }
 
@@ -299,72 +340,35 @@ __global__ __launch_bounds__(64) void k_rmsnorm(float *__restrict__ x, int x_str
 // per-32 quantization of concat for the fc projection).  blockIdx.y = 0: the
 // embedding half, 1: the hidden half.  d % 32 == 0, so the halves quantize
 // independently.
-template <int NC>
+template <int PJ>
 __global__ __launch_bounds__(64) void k_mtp_pre(const int8_t *__restrict__ emb_q, const float *__restrict__ emb_s,
                                                 const int *__restrict__ toks, const float *__restrict__ h,
                                                 int d, const float *__restrict__ w_e,
                                                 const float *__restrict__ w_h, float eps,
                                                 int8_t *__restrict__ xq, float *__restrict__ xqs) {
-    __shared__ __align__(16) float sh[64 * NC];
+    __shared__ __align__(16) float sq[256 * PJ];
     __shared__ float s_inv;
-    const int r = blockIdx.x, half = blockIdx.y, lane = threadIdx.x;
-    const float *wn = half == 0 ? w_e : w_h;
-    float v[NC], wv[NC];
+    const int r = blockIdx.x, half = blockIdx.y, lane = threadIdx.x, nf = d >> 2;
+    const float4 *wn4 = reinterpret_cast<const float4 *>(half == 0 ? w_e : w_h);
+    float4 v[PJ], wn[PJ];
     if (half == 0) {
         const int tok = toks[r];
-        const int8_t *er = emb_q + (size_t)tok * d;
+        const uint32_t *er = reinterpret_cast<const uint32_t *>(emb_q + (size_t)tok * d);
         const float sc = emb_s[tok];
 #pragma unroll
-        for (int j = 0; j < NC; j++) v[j] = (float)er[imin(j * 64 + lane, d - 1)] * sc;
+        for (int j = 0; j < PJ; j++) {
+            const uint32_t q = er[imin(lane + 64 * j, nf - 1)];
+            v[j] = make_float4((float)(int8_t)(q & 0xFF) * sc, (float)(int8_t)((q >> 8) & 0xFF) * sc,
+                               (float)(int8_t)((q >> 16) & 0xFF) * sc, (float)(int8_t)(q >> 24) * sc);
+        }
     } else {
 #pragma unroll
-        for (int j = 0; j < NC; j++) v[j] = h[(size_t)r * d + imin(j * 64 + lane, d - 1)];
+        for (int j = 0; j < PJ; j++) v[j] = reinterpret_cast<const float4 *>(h + (size_t)r * d)[imin(lane + 64 * j, nf - 1)];
     }
 #pragma unroll
-    for (int j = 0; j < NC; j++) wv[j] = wn[imin(j * 64 + lane, d - 1)];
-    norm_row<NC>(v, wv, d, eps, sh, &s_inv, nullptr, xq + (size_t)r * 2 * d + (size_t)half * d,
+    for (int j = 0; j < PJ; j++) wn[j] = wn4[imin(lane + 64 * j, nf - 1)];
+    norm_row<PJ>(v, wn, d, eps, sq, &s_inv, nullptr, xq + (size_t)r * 2 * d + (size_t)half * d,
                  xqs + (size_t)r * (2 * d >> 5) + (size_t)half * (d >> 5));
-}
-
-// g = silu(h1)*h3 then per-32 quantization (lz_ffn_gate_up default branch,
-// src/forward_kda.c:1067-1088, followed by lz_quantize_q8), one 64-lane
-// block per row.  Rows [0, rows) come from (h1, h3) of width n, the rest
-// from the second segment (g1, g3) of width n2, so the routed experts' and
-// the shared expert's activations quantize in one launch.
-__global__ __launch_bounds__(64) void k_act_quant(const float *__restrict__ h1, const float *__restrict__ h3,
-                                                  int n, int rows, int8_t *__restrict__ xq,
-                                                  float *__restrict__ xqs, const float *__restrict__ g1,
-                                                  const float *__restrict__ g3, int n2,
-                                                  int8_t *__restrict__ xq2, float *__restrict__ xqs2) {
-    DECLARE_EXP_TAB(tab);
-    const int lane = threadIdx.x;
-    const float *p, *q;
-    int8_t *oq;
-    float *os;
-    int w;
-    if ((int)blockIdx.x < rows) {
-        const int r = blockIdx.x;
-        w = n; p = h1 + (size_t)r * n; q = h3 + (size_t)r * n;
-        oq = xq + (size_t)r * n; os = xqs + (size_t)r * (n >> 5);
-    } else {
-        const int r = blockIdx.x - rows;
-        w = n2; p = g1 + (size_t)r * n2; q = g3 + (size_t)r * n2;
-        oq = xq2 + (size_t)r * n2; os = xqs2 + (size_t)r * (n2 >> 5);
-    }
-    for (int base = 0; base < w; base += 64 * 8) {
-        float pv[8], qv[8];
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int ic = imin(base + j * 64 + lane, w - 1);
-            pv[j] = p[ic];
-            qv[j] = q[ic];
-        }
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int i = base + j * 64 + lane;
-            if (base + j * 64 + (lane & ~31) < w) d_quant_group32(d_silu(pv[j], tab) * qv[j], oq + i, os + (i >> 5));
-        }
-    }
 }
 
 // ------------------------------------------------------------- GEMV/q8 ---
@@ -375,43 +379,295 @@ __global__ __launch_bounds__(64) void k_act_quant(const float *__restrict__ h1, 
 // src/ops_epi.c:983-1017).
 //
 // A 256-lane block streams one tile of R rows (R*in_dim <= 32 KiB): each
-// wave issues all of its 16-byte weight loads of its 8 KiB quarter (chunks
-// lane, lane+64, ...) and the block stages the M activation rows into LDS
-// before any of them is consumed, so a tile costs one memory latency.  The
-// 16-element partial dot products (v_dot4_i32_i8) of neighbouring lanes add
-// up to the exact 32-element group sums (an integer add, order-free), which
-// go to LDS; then one lane per (row, token) runs the epilogue serially over
-// the groups, in the reference order.  Weights stream once per launch for
-// any M <= 8.
+// wave issues all of its 16-byte weight loads of its 8 KiB quarter first.
+// While they are in flight the block builds the M int8 activation rows in
+// LDS (the job's prologue: copy pre-quantized rows, or quantize float rows,
+// optionally after the residual fold + RMSNorm, SiLU-mul or MoE slot
+// combine that produced them), so the producer's serial work overlaps the
+// weight latency and needs no launch of its own.  The 16-element partial
+// dot products (v_dot4_i32_i8) of neighbouring lanes add up to the exact
+// 32-element group sums (an integer add, order-free), which go to LDS; then
+// one lane per (row, token) runs the epilogue serially over the groups, in
+// the reference order.  Weights stream once per launch for any M <= 8.
 
 #define GEMV_THREADS 256
 #define GEMV_WAVE_BYTES 8192
 #define GEMV_TILE_BYTES (GEMV_WAVE_BYTES * (GEMV_THREADS / 64))
 #define GEMV_MAXJ (GEMV_WAVE_BYTES / 16 / 64)
 #define GEMV_MAX_IN 4096
+#define PRO_MAX_IN 2048                 // float prologues: <= 8 float4 per lane per row
+// Float prologues keep PJ float4 per lane per row (PJ*256 elements); the
+// kernels are instantiated for PJ = 0 (pre-quantized input only), 1, 2, 4, 8.
+static inline int pro_pj(int in_dim) {
+    const int j = (in_dim + 255) / 256;
+    return j <= 1 ? 1 : j <= 2 ? 2 : j <= 4 ? 4 : 8;
+}
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-// LDS bytes of one tile: staged activations, their scales, group sums.
-__host__ __device__ inline size_t gemv_lds_bytes(int m, int in_dim, int R) {
-    return (size_t)m * in_dim + (size_t)m * (in_dim >> 5) * 4 + (size_t)R * m * ((in_dim >> 5) + 1) * 4;
+// LDS bytes of one tile: staged activations, their scales, and the larger of
+// the group sums and the RMSNorm squares.
+__host__ __device__ inline size_t gemv_lds_bytes(int m, int in_dim, int R, int norm) {
+    const size_t part = (size_t)R * m * ((in_dim >> 5) + 1) * 4;
+    const size_t sq = norm ? (size_t)m * (in_dim + 4) * 4 : 0;
+    return (size_t)m * in_dim + (size_t)m * (in_dim >> 5) * 4 + (part > sq ? part : sq);
 }
 
-// s_xrow[t]: activation row of token slot t (rows of xq / xqs);
-// s_orow[t]: output row of token slot t; nm: live token slots.  The caller
-// fills both tables (first M entries) before the call; they are read after
-// the first barrier.
-template <int M>
+__device__ __forceinline__ float4 f4_silu_mul(float4 p, float4 q, const float *tab) {
+    return make_float4(d_silu(p.x, tab) * q.x, d_silu(p.y, tab) * q.y, d_silu(p.z, tab) * q.z,
+                       d_silu(p.w, tab) * q.w);
+}
+
+// Per-32 quantization of a tile's float rows (wave w holds rows w, w+4 as
+// float4 f = lane + 64*j) into sx / sxs.
+template <int RW, int PJN>
+__device__ __forceinline__ void quant_rows(const float4 (&v)[RW][PJN], int wave, int lane, int nm, int nf, int nb,
+                                           int in_dim, int8_t *sx, float *sxs) {
+#pragma unroll
+    for (int r = 0; r < RW; r++) {
+        const int t = wave + 4 * r;
+#pragma unroll
+        for (int j = 0; j < PJN; j++) {
+            float sg;
+            const uint32_t q = quant_octet(v[r][j], &sg);
+            const int f = lane + 64 * j;
+            if (t < nm && f < nf) {
+                reinterpret_cast<uint32_t *>(sx + (size_t)t * in_dim)[f] = q;
+                if (!(f & 7)) sxs[t * nb + (f >> 3)] = sg;
+            }
+        }
+    }
+}
+
+// Builds the tile's activation rows in LDS from the job's prologue: sx
+// [M][in_dim] int8 and sxs [M][in_dim/32].  Row t of the tile is activation
+// row xrow[t]; rows t >= nm are left unused.  The prologue's global loads are
+// issued first, then issue_w() (the tile's weight loads), then the
+// prologue's arithmetic, so the weight loads are in flight behind it and the
+// first use of a prologue value waits only for the prologue's own loads.
+// Float prologues: wave w builds rows w and w + 4 (one float4 per lane per
+// 256 elements), so the quantization groups are lane octets.  PRO_NORM
+// (lz_rmsnorm, src/ops_norm.c:690-747, after the residual fold x += a (+ b)
+// of src/forward.c:1449-1557): the squares go to LDS and lane t of wave 0
+// walks row t's sum serially, all rows at once; the block with `writer` set
+// stores the updated residual and the normed rows.  PRO_SILU:
+// lz_ffn_gate_up's silu(g)*u (src/forward_kda.c:1067-1088).  PRO_COMBINE:
+// the slot-ordered weighted sum of the experts' outputs
+// (src/forward_moe.c:128-200).  Every load is unconditional (rows past nm
+// and elements past the row end are clamped to valid addresses and their
+// values unused), and each mode is one straight-line block.  Contains block
+// barriers: call from every thread.
+#define XQ_PER_THREAD 4
+template <int M, int PJ, typename IssueW>
+__device__ __forceinline__ void build_rows(const Prologue &P, const int8_t *__restrict__ xq,
+                                           const float *__restrict__ xqs, int in_dim, const int (&xrow)[M], int nm,
+                                           bool writer, int8_t *sx, float *sxs, float *sq, float *s_inv,
+                                           float *tab, IssueW issue_w) {
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int nb = in_dim >> 5, nf = in_dim >> 2;
+    if (PJ == 0 || P.mode == PRO_XQ) {
+        // int4 chunk idx of the tile's rows: token idx / cpr, chunk idx % cpr;
+        // the stores are unconditional (clamped: past the end they rewrite
+        // the last chunk with its own value).
+        const int cpr = in_dim >> 4;
+        const int total = M * cpr, stotal = M * nb;
+        int4 r[XQ_PER_THREAD];
+        float sc[XQ_PER_THREAD];
+#pragma unroll
+        for (int u = 0; u < XQ_PER_THREAD; u++) {
+            const int idx = imin(u * GEMV_THREADS + tid, total - 1);
+            const int t = idx / cpr, p = idx - t * cpr;
+            r[u] = *reinterpret_cast<const int4 *>(xq + (size_t)xrow[t < nm ? t : 0] * in_dim + p * 16);
+            const int si = imin(u * GEMV_THREADS + tid, stotal - 1);
+            const int ts = si / nb;
+            sc[u] = xqs[(size_t)xrow[ts < nm ? ts : 0] * nb + (si - ts * nb)];
+        }
+        issue_w();
+#pragma unroll
+        for (int u = 0; u < XQ_PER_THREAD; u++) {
+            reinterpret_cast<int4 *>(sx)[imin(u * GEMV_THREADS + tid, total - 1)] = r[u];
+            sxs[imin(u * GEMV_THREADS + tid, stotal - 1)] = sc[u];
+        }
+        for (int base = XQ_PER_THREAD * GEMV_THREADS; base < total; base += GEMV_THREADS) {
+            const int idx = imin(base + tid, total - 1);
+            const int t = idx / cpr, p = idx - t * cpr;
+            reinterpret_cast<int4 *>(sx)[idx] =
+                *reinterpret_cast<const int4 *>(xq + (size_t)xrow[t < nm ? t : 0] * in_dim + p * 16);
+        }
+        for (int base = XQ_PER_THREAD * GEMV_THREADS; base < stotal; base += GEMV_THREADS) {
+            const int si = imin(base + tid, stotal - 1);
+            const int ts = si / nb;
+            sxs[si] = xqs[(size_t)xrow[ts < nm ? ts : 0] * nb + (si - ts * nb)];
+        }
+        return;
+    }
+    constexpr int RW = (M + 3) / 4;
+    constexpr int PJN = PJ > 0 ? PJ : 1;
+    int xr[RW];
+#pragma unroll
+    for (int r = 0; r < RW; r++) {
+        const int t = wave + 4 * r;
+        xr[r] = xrow[t < nm ? t : 0];
+    }
+    int fc[PJN];
+#pragma unroll
+    for (int j = 0; j < PJN; j++) fc[j] = imin(lane + 64 * j, nf - 1);
+    float4 v[RW][PJN];
+    switch (P.mode) {
+    case PRO_QUANT: {
+#pragma unroll
+        for (int r = 0; r < RW; r++)
+#pragma unroll
+            for (int j = 0; j < PJN; j++)
+                v[r][j] = reinterpret_cast<const float4 *>(P.src + (size_t)xr[r] * P.src_stride)[fc[j]];
+        issue_w();
+        quant_rows<RW, PJN>(v, wave, lane, nm, nf, nb, in_dim, sx, sxs);
+        break;
+    }
+    case PRO_SILU: {
+        const float tabv = c_exp_tab[lane & 31];
+        float4 q[RW][PJN];
+#pragma unroll
+        for (int r = 0; r < RW; r++)
+#pragma unroll
+            for (int j = 0; j < PJN; j++) {
+                v[r][j] = reinterpret_cast<const float4 *>(P.src + (size_t)xr[r] * P.src_stride)[fc[j]];
+                q[r][j] = reinterpret_cast<const float4 *>(P.src2 + (size_t)xr[r] * P.src_stride)[fc[j]];
+            }
+        issue_w();
+        if (tid < 32) tab[tid] = tabv;
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < RW; r++)
+#pragma unroll
+            for (int j = 0; j < PJN; j++) v[r][j] = f4_silu_mul(v[r][j], q[r][j], tab);
+        quant_rows<RW, PJN>(v, wave, lane, nm, nf, nb, in_dim, sx, sxs);
+        break;
+    }
+    case PRO_COMBINE: {
+        int sidx[RW][MAX_TOPK];
+        float swt[RW][MAX_TOPK];
+        float4 h[RW][MAX_TOPK][PJN];
+#pragma unroll
+        for (int r = 0; r < RW; r++)
+#pragma unroll
+            for (int k = 0; k < MAX_TOPK; k++) {
+                const int pair = xr[r] * P.topk + imin(k, P.topk - 1);
+                sidx[r][k] = P.sel_idx[pair];
+                swt[r][k] = P.sel_w[pair];
+#pragma unroll
+                for (int j = 0; j < PJN; j++)
+                    h[r][k][j] = reinterpret_cast<const float4 *>(P.src + (size_t)pair * in_dim)[fc[j]];
+            }
+        issue_w();
+#pragma unroll
+        for (int r = 0; r < RW; r++)
+#pragma unroll
+            for (int j = 0; j < PJN; j++) {
+                float4 y = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+                for (int k = 0; k < MAX_TOPK; k++) {
+                    const float wk = swt[r][k];
+                    const float4 hk = h[r][k][j];
+                    const float4 y2 = make_float4(y.x + wk * hk.x, y.y + wk * hk.y, y.z + wk * hk.z, y.w + wk * hk.w);
+                    if (k < P.topk && sidx[r][k] >= 0) y = y2;
+                }
+                v[r][j] = y;
+            }
+        quant_rows<RW, PJN>(v, wave, lane, nm, nf, nb, in_dim, sx, sxs);
+        break;
+    }
+    default: {                           // PRO_NORM
+        const bool has_a = P.a != nullptr, has_b = P.b != nullptr;
+        const float *pa = has_a ? P.a : P.src;
+        const float *pb = has_b ? P.b : pa;
+        const int sa = has_a ? in_dim : P.src_stride, sb = has_b ? in_dim : sa;
+        float4 wn[PJN], ad[RW][PJN], bd[RW][PJN];
+#pragma unroll
+        for (int j = 0; j < PJN; j++) wn[j] = reinterpret_cast<const float4 *>(P.w)[fc[j]];
+#pragma unroll
+        for (int r = 0; r < RW; r++)
+#pragma unroll
+            for (int j = 0; j < PJN; j++) {
+                v[r][j] = reinterpret_cast<const float4 *>(P.src + (size_t)xr[r] * P.src_stride)[fc[j]];
+                ad[r][j] = reinterpret_cast<const float4 *>(pa + (size_t)xr[r] * sa)[fc[j]];
+                bd[r][j] = reinterpret_cast<const float4 *>(pb + (size_t)xr[r] * sb)[fc[j]];
+            }
+        issue_w();
+        // x + (a + b), x + a, or x
+#pragma unroll
+        for (int r = 0; r < RW; r++)
+#pragma unroll
+            for (int j = 0; j < PJN; j++) {
+                float4 a2 = ad[r][j];
+                const float4 b2 = bd[r][j];
+                const float4 ab = make_float4(a2.x + b2.x, a2.y + b2.y, a2.z + b2.z, a2.w + b2.w);
+                if (has_b) a2 = ab;
+                const float4 x = v[r][j];
+                const float4 xa = make_float4(x.x + a2.x, x.y + a2.y, x.z + a2.z, x.w + a2.w);
+                if (has_a) v[r][j] = xa;
+            }
+        // rows padded by 4 floats so the summing lanes read different banks
+#pragma unroll
+        for (int r = 0; r < RW; r++) {
+            const int t = wave + 4 * r;
+#pragma unroll
+            for (int j = 0; j < PJN; j++) {
+                const int f = lane + 64 * j;
+                if (t < nm && f < nf) {
+                    const float4 x = v[r][j];
+                    reinterpret_cast<float4 *>(sq + (size_t)t * (in_dim + 4))[f] =
+                        make_float4(x.x * x.x, x.y * x.y, x.z * x.z, x.w * x.w);
+                }
+            }
+        }
+        __syncthreads();
+        if (tid < nm)
+            s_inv[tid] = d_rsqrt(d_ss_over_n(serial_sum(sq + (size_t)tid * (in_dim + 4), in_dim), in_dim) + P.eps);
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < RW; r++) {
+            const int t = wave + 4 * r;
+            const float inv = s_inv[t < nm ? t : 0];
+#pragma unroll
+            for (int j = 0; j < PJN; j++) {
+                const int f = lane + 64 * j;
+                const float4 x = v[r][j], w = wn[j];
+                const float4 o = make_float4(x.x * inv * (1.0f + w.x), x.y * inv * (1.0f + w.y),
+                                             x.z * inv * (1.0f + w.z), x.w * inv * (1.0f + w.w));
+                if (writer && t < nm && f < nf) {
+                    if (P.x_out) reinterpret_cast<float4 *>(P.x_out + (size_t)xr[r] * P.src_stride)[f] = x;
+                    if (P.o_out) reinterpret_cast<float4 *>(P.o_out + (size_t)xr[r] * P.o_stride)[f] = o;
+                }
+                v[r][j] = o;
+            }
+        }
+        quant_rows<RW, PJN>(v, wave, lane, nm, nf, nb, in_dim, sx, sxs);
+        break;
+    }
+    }
+}
+
+// One GEMV tile.  xrow[t]: activation row of token slot t (registers);
+// s_orow[t]: output row of token slot t (LDS, read after a barrier); nm:
+// live token slots.  The caller fills the LDS exp table first.
+template <int M, int PJ>
 __device__ __forceinline__ void gemv_tile(const int8_t *__restrict__ wt, const float *__restrict__ ws, int rows_here,
-                                          int in_dim, const int8_t *__restrict__ xq,
-                                          const float *__restrict__ xqs, const int *s_xrow, const int *s_orow,
-                                          int nm, float *__restrict__ out, size_t out_stride, int row0,
-                                          int32_t *__restrict__ acc_out, int acc_rows, char *smem) {
+                                          int in_dim, const Prologue &P, const int8_t *__restrict__ xq,
+                                          const float *__restrict__ xqs, const int (&xrow)[M], const int *s_orow,
+                                          int nm, bool writer, float *__restrict__ out, size_t out_stride,
+                                          int row0, int32_t *__restrict__ acc_out, int acc_rows, char *smem,
+                                          float *s_inv, float *tab) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int cpr = in_dim >> 4, nb = in_dim >> 5;
     const int nchunk = rows_here * cpr;
+    int8_t *sx = reinterpret_cast<int8_t *>(smem);                                   // [M][in_dim]
+    float *sxs = reinterpret_cast<float *>(smem + (size_t)M * in_dim);                // [M][nb]
+    int *part = reinterpret_cast<int *>(sxs + M * nb);                                // [R][M][nb+1]
     // weights: one 8 KiB quarter of the tile per wave, all loads in flight
     int4 wv[GEMV_MAXJ];
-    {
+    const int er = tid / M, et = tid - er * M;
+    float wsv = 0.0f;
+    auto issue_w = [&]() {
         const v4i *w4 = reinterpret_cast<const v4i *>(wt);
 #pragma unroll
         for (int j = 0; j < GEMV_MAXJ; j++) {
@@ -419,54 +675,52 @@ __device__ __forceinline__ void gemv_tile(const int8_t *__restrict__ wt, const f
             const v4i q = __builtin_nontemporal_load(w4 + c);
             wv[j] = make_int4(q.x, q.y, q.z, q.w);
         }
-    }
-    // epilogue lane's row scale, also early
-    const int er = tid / M, et = tid - er * M;
-    const float wsv = ws[row0 + imin(er, rows_here - 1)];
-    __syncthreads();                                   // s_xrow / s_orow visible
-    int4 *sx = reinterpret_cast<int4 *>(smem);                            // [M][cpr]
-    float *sxs = reinterpret_cast<float *>(smem + (size_t)M * in_dim);    // [M][nb]
-    int *part = reinterpret_cast<int *>(sxs + M * nb);                    // [R][M][nb+1]
-    {
-        const int total = M * cpr;
-        for (int base = 0; base < total; base += GEMV_THREADS * 4) {
-            int4 r[4];
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const int idx = imin(base + u * GEMV_THREADS + tid, total - 1);
-                const int t = idx / cpr, p = idx - t * cpr;
-                const int xr = s_xrow[t < nm ? t : 0];
-                r[u] = *reinterpret_cast<const int4 *>(xq + (size_t)xr * in_dim + p * 16);
-            }
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const int idx = base + u * GEMV_THREADS + tid;
-                if (idx < total) sx[idx] = r[u];
-            }
-        }
-        for (int i = tid; i < M * nb; i += GEMV_THREADS) {
-            const int t = i / nb;
-            const int xr = s_xrow[t < nm ? t : 0];
-            sxs[i] = xqs[(size_t)xr * nb + (i - t * nb)];
-        }
-    }
+        wsv = ws[row0 + imin(er, rows_here - 1)];     // the epilogue lane's row scale
+    };
+    build_rows<M, PJ>(P, xq, xqs, in_dim, xrow, nm, writer, sx, sxs, reinterpret_cast<float *>(part), s_inv, tab,
+                      issue_w);
     __syncthreads();
-#pragma unroll
-    for (int j = 0; j < GEMV_MAXJ; j++) {
+    // Partial dot products.  With a power-of-two chunk count per row, lane
+    // l's chunks of every row sit at the same in-row offsets (l + 64v) mod
+    // cpr for v < cpr/64, so each activation chunk is read from LDS once and
+    // reused for all of the lane's weight chunks at that offset.
+    const int4 *sx4 = reinterpret_cast<const int4 *>(sx);
+    auto dot_store = [&](int j, const int4 (&xv)[M]) {
         const int c = wave * (GEMV_WAVE_BYTES / 16) + lane + 64 * j;
         const int r = c / cpr, p = c - r * cpr;
 #pragma unroll
         for (int t = 0; t < M; t++) {
-            int acc = 0;
-            if (t < nm) {
-                const int4 xv = sx[t * cpr + (p < cpr ? p : 0)];
-                acc = __builtin_amdgcn_sdot4(wv[j].x, xv.x, 0, false);
-                acc = __builtin_amdgcn_sdot4(wv[j].y, xv.y, acc, false);
-                acc = __builtin_amdgcn_sdot4(wv[j].z, xv.z, acc, false);
-                acc = __builtin_amdgcn_sdot4(wv[j].w, xv.w, acc, false);
+            int a = __builtin_amdgcn_sdot4(wv[j].x, xv[t].x, 0, false);
+            a = __builtin_amdgcn_sdot4(wv[j].y, xv[t].y, a, false);
+            a = __builtin_amdgcn_sdot4(wv[j].z, xv[t].z, a, false);
+            a = __builtin_amdgcn_sdot4(wv[j].w, xv[t].w, a, false);
+            a += __builtin_amdgcn_update_dpp(0, a, 0xB1, 0xF, 0xF, false);     // lane ^ 1: chunks 2g, 2g+1
+            if (t < nm && c < nchunk && !(lane & 1)) part[(r * M + t) * (nb + 1) + (p >> 1)] = a;
+        }
+    };
+    if ((cpr & (cpr - 1)) == 0 && cpr <= 256) {
+        const int nv = cpr > 64 ? cpr >> 6 : 1;
+#pragma unroll
+        for (int vv = 0; vv < 4; vv++) {
+            if (vv < nv) {
+                const int p = (lane + 64 * vv) & (cpr - 1);
+                int4 xv[M];
+#pragma unroll
+                for (int t = 0; t < M; t++) xv[t] = sx4[(t < nm ? t : 0) * cpr + p];
+#pragma unroll
+                for (int j = 0; j < GEMV_MAXJ; j++)
+                    if ((j & (nv - 1)) == vv) dot_store(j, xv);
             }
-            acc += __shfl_xor(acc, 1);                 // chunks 2g and 2g+1 of one row
-            if (c < nchunk && !(lane & 1)) part[(r * M + t) * (nb + 1) + (p >> 1)] = acc;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < GEMV_MAXJ; j++) {
+            const int c = wave * (GEMV_WAVE_BYTES / 16) + lane + 64 * j;
+            const int p = c - (c / cpr) * cpr;
+            int4 xv[M];
+#pragma unroll
+            for (int t = 0; t < M; t++) xv[t] = sx4[(t < nm ? t : 0) * cpr + p];
+            dot_store(j, xv);
         }
     }
     __syncthreads();
@@ -484,29 +738,36 @@ __device__ __forceinline__ void gemv_tile(const int8_t *__restrict__ wt, const f
     }
 }
 
-template <int M>
+template <int M, int PJ>
 __global__ __launch_bounds__(GEMV_THREADS) void k_gemv_q8(GemvBatch batch) {
     extern __shared__ __align__(16) char smem[];
     __shared__ int s_row[M];
+    __shared__ float s_inv[M], tab[32];
     int blk = blockIdx.x, j = 0;
     while (j + 1 < batch.n && blk >= batch.job[j + 1].tile0) j++;
     const GemvJob &job = batch.job[j];
     const int row0 = (blk - job.tile0) * job.R;
     const int rows_here = imin(job.R, job.rows - row0);
     if (threadIdx.x < M) s_row[threadIdx.x] = threadIdx.x;
-    gemv_tile<M>(job.w + (size_t)row0 * job.in_dim, job.ws, rows_here, job.in_dim, job.xq, job.xqs, s_row, s_row,
-                 M, job.out, job.out_stride, row0, job.acc_out, job.rows, smem);
+    int xrow[M];
+#pragma unroll
+    for (int t = 0; t < M; t++) xrow[t] = t;
+    gemv_tile<M, PJ>(job.w + (size_t)row0 * job.in_dim, job.ws, rows_here, job.in_dim, job.pro, job.xq, job.xqs,
+                     xrow, s_row, M, blk == 0, job.out, job.out_stride, row0, job.acc_out, job.rows, smem, s_inv,
+                     tab);
 }
 
 // Grouped expert GEMV: block -> (projection jb, group gi, tile).  Group gi
 // is one distinct expert of the chunk with its member (token, slot) pairs;
 // its weight rows stream once for all members.  Output row = pair.
+template <int PJ>
 __global__ __launch_bounds__(GEMV_THREADS) void k_expert_gemv(ExpertJob j0, ExpertJob j1,
                                                               const MoeGroups *__restrict__ grp,
                                                               int max_groups, int in_dim, int out_rows, int R,
                                                               int tiles) {
     extern __shared__ __align__(16) char smem[];
-    __shared__ int s_xrow[MAX_CHUNK], s_orow[MAX_CHUNK];
+    __shared__ int s_orow[MAX_CHUNK];
+    __shared__ float s_inv[MAX_CHUNK], tab[32];
     const int per_job = max_groups * tiles;
     const int jb = blockIdx.x / per_job;
     const int rem = blockIdx.x - jb * per_job;
@@ -517,16 +778,17 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_expert_gemv(ExpertJob j0, Expe
     if (gi >= ng) return;
     const int e = grp->expert[gi];
     const int nm = grp->n_members[gi];
-    if (threadIdx.x < MAX_CHUNK) {
-        const int t = threadIdx.x;
+    int xrow[MAX_CHUNK];
+#pragma unroll
+    for (int t = 0; t < MAX_CHUNK; t++) {
         const int mem = grp->member[gi][t < nm ? t : 0];
-        s_orow[t] = mem;
-        s_xrow[t] = J.xq_by_pair ? mem : grp->pair_token[mem];
+        xrow[t] = J.xq_by_pair ? mem : grp->pair_token[mem];
+        if (threadIdx.x == t) s_orow[t] = mem;
     }
     const int row0 = tile * R;
-    gemv_tile<MAX_CHUNK>(J.q + ((size_t)e * out_rows + row0) * in_dim, J.s + (size_t)e * out_rows,
-                         imin(R, out_rows - row0), in_dim, J.xq, J.xqs, s_xrow, s_orow, nm, J.out, out_rows,
-                         row0, nullptr, 0, smem);
+    gemv_tile<MAX_CHUNK, PJ>(J.q + ((size_t)e * out_rows + row0) * in_dim, J.s + (size_t)e * out_rows,
+                             imin(R, out_rows - row0), in_dim, J.pro, J.xq, J.xqs, xrow, s_orow, nm, false, J.out,
+                             out_rows, row0, nullptr, 0, smem, s_inv, tab);
 }
 
 // ------------------------------------------------------------ KDA conv ---
@@ -534,8 +796,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_expert_gemv(ExpertJob j0, Expe
 // Depthwise causal conv (K taps) + SiLU over the [q | k | v] channels, one
 // thread per channel, token-serial along the state ring
 // (lz_causal_conv1d_step, src/ops_conv1d.c:26-87; ring slots
-// src/forward_kda.c:680-755).  The last block instead quantizes the gate's
-// low-rank rows pfa [nt][rank] per 32 (input of the f_b projection).
+// src/forward_kda.c:680-755).
 template <int K>
 __global__ __launch_bounds__(256) void k_kda_conv(const float *__restrict__ pq, const float *__restrict__ pk,
                                                   const float *__restrict__ pv, int key, int value,
@@ -543,32 +804,30 @@ __global__ __launch_bounds__(256) void k_kda_conv(const float *__restrict__ pq, 
                                                   float *__restrict__ conv_ring, size_t slot_stride,
                                                   const int *__restrict__ ctl_slot, int depth, int advance,
                                                   int nt, float *__restrict__ qc, float *__restrict__ kc,
-                                                  float *__restrict__ vc, const float *__restrict__ pfa, int rank,
-                                                  int8_t *__restrict__ fq, float *__restrict__ fqs) {
-    DECLARE_EXP_TAB(tab);
-    if (blockIdx.x == gridDim.x - 1) {
-        quant_span(pfa, nt * rank, fq, fqs);
-        return;
-    }
+                                                  float *__restrict__ vc) {
+    EXP_TAB_LOAD(tab);
     constexpr int hist = K - 1;
-    const int c = blockIdx.x * blockDim.x + threadIdx.x;
     const int conv_dim = 2 * key + value;
-    if (c >= conv_dim) return;
+    const int c = imin(blockIdx.x * blockDim.x + threadIdx.x, conv_dim - 1);   // extra lanes redo the last channel, store nothing
+    const bool live = blockIdx.x * blockDim.x + threadIdx.x < conv_dim;
     const float *in;
     float *out;
     int ch, width;
     if (c < key) { in = pq; out = qc; ch = c; width = key; }
     else if (c < 2 * key) { in = pk; out = kc; ch = c - key; width = key; }
     else { in = pv; out = vc; ch = c - 2 * key; width = value; }
-    const int base = *ctl_slot;
     float h[hist > 0 ? hist : 1], wr[K], xs[MAX_CHUNK];
-    const float *st0 = conv_ring + (size_t)base * slot_stride + (size_t)c * hist;
-#pragma unroll
-    for (int j = 0; j < hist; j++) h[j] = st0[j];
 #pragma unroll
     for (int j = 0; j < K; j++) wr[j] = wconv[(size_t)c * K + j];
 #pragma unroll
     for (int t = 0; t < MAX_CHUNK; t++) xs[t] = in[(size_t)imin(t, nt - 1) * width + ch];
+    const int base = *ctl_slot;
+    const float *st0 = conv_ring + (size_t)base * slot_stride + (size_t)c * hist;
+#pragma unroll
+    for (int j = 0; j < hist; j++) h[j] = st0[j];
+    EXP_TAB_PUT(tab);
+    __syncthreads();
+    if (!live) return;
 #pragma unroll
     for (int t = 0; t < MAX_CHUNK; t++) {
         if (t < nt) {
@@ -609,7 +868,7 @@ __global__ __launch_bounds__(256) void k_kda_conv(const float *__restrict__ pq, 
 template <int KD, int VD>
 __global__ __launch_bounds__(VD) void k_kda_recur(KdaRecurArgs a) {
     static_assert(KD == VD, "one lane per state column and per key channel");
-    DECLARE_EXP_TAB(tab);
+    EXP_TAB_LOAD(tab);
     __shared__ __align__(16) float s_a[MAX_CHUNK][KD];   // q, then q.g*invq*scale (qcw)
     __shared__ __align__(16) float s_b[MAX_CHUNK][KD];   // k, then k*invk (kn)
     __shared__ __align__(16) float s_g[MAX_CHUNK][KD];   // decay gate
@@ -621,14 +880,8 @@ __global__ __launch_bounds__(VD) void k_kda_recur(KdaRecurArgs a) {
     const int j = threadIdx.x;
     const int nt = a.nt;
     const int kh = (a.nk == a.nv) ? h : (h * a.nk / a.nv);
-    const int base = *a.ctl_slot;
     const size_t head_off = (size_t)h * KD * VD;
-    float S[KD];
-    {
-        const float *src = a.state + (size_t)base * a.slot_stride + head_off;
-#pragma unroll
-        for (int i = 0; i < KD; i++) S[i] = src[(size_t)i * VD + j];
-    }
+    // token inputs first (independent of the ring slot), then the state
     float vcv[MAX_CHUNK], gzv[MAX_CHUNK], qv[MAX_CHUNK], kv[MAX_CHUNK], pre[MAX_CHUNK];
     const float dtb = a.dt_bias[h * KD + j];
 #pragma unroll
@@ -642,24 +895,33 @@ __global__ __launch_bounds__(VD) void k_kda_recur(KdaRecurArgs a) {
     }
     const float bv = a.bvec[(size_t)imin(j, nt - 1) * a.nv + h];
     const float onw = a.o_norm[j];
-    const float decay = d_exp(a.a_log[h], tab);
+    const float alog = a.a_log[h];
+    const int base = *a.ctl_slot;
+    float S[KD];
+    {
+        const float *src = a.state + (size_t)base * a.slot_stride + head_off;
+#pragma unroll
+        for (int i = 0; i < KD; i++) S[i] = src[(size_t)i * VD + j];
+    }
+    EXP_TAB_PUT(tab);
+    __syncthreads();
+    const float decay = d_exp(alog, tab);
+    // rows t >= nt hold the last token's values and are never read
 #pragma unroll
     for (int t = 0; t < MAX_CHUNK; t++) {
-        if (t < nt) {
-            s_a[t][j] = qv[t];
-            s_b[t][j] = kv[t];
-            s_c[t][j] = qv[t] * qv[t];
-            s_d[t][j] = kv[t] * kv[t];
-            const float p = pre[t] + dtb;
-            const float gg = -decay * d_softplus(p, tab);
-            s_g[t][j] = d_exp(gg, tab);
-        }
+        s_a[t][j] = qv[t];
+        s_b[t][j] = kv[t];
+        s_c[t][j] = qv[t] * qv[t];
+        s_d[t][j] = kv[t] * kv[t];
+        const float p = pre[t] + dtb;
+        const float gg = -decay * d_softplus(p, tab);
+        s_g[t][j] = d_exp(gg, tab);
     }
     __syncthreads();
     if (j < nt) {                        // lane t: the token's serial norms and k.q
         const int t = j;
-        const float invq = d_rsqrt(serial_sum(s_c[t], KD) + 1e-6f);
-        const float invk = d_rsqrt(serial_sum(s_d[t], KD) + 1e-6f);
+        const float invq = d_rsqrt(serial_sum_n<KD>(s_c[t]) + 1e-6f);
+        const float invk = d_rsqrt(serial_sum_n<KD>(s_d[t]) + 1e-6f);
         float kq = 0.0f;
         for (int i = 0; i < KD; i++) {
             const float qn = s_a[t][i] * invq * a.scale;
@@ -716,7 +978,7 @@ __global__ __launch_bounds__(VD) void k_kda_recur(KdaRecurArgs a) {
     for (int t = 0; t < MAX_CHUNK; t++)
         if (t < nt) s_c[t][j] = ov[t] * ov[t];
     __syncthreads();
-    if (j < nt) s_oinv[j] = d_rsqrt(d_ss_over_n(serial_sum(s_c[j], VD), VD) + a.eps);
+    if (j < nt) s_oinv[j] = d_rsqrt(d_ss_over_n(serial_sum_n<VD>(s_c[j]), VD) + a.eps);
     __syncthreads();
     // gated RMSNorm over the head: ((o*inv)*w)*silu(g)  (src/ops_norm.c:749-793)
     const int col = h * VD + j;
@@ -829,11 +1091,13 @@ __device__ __forceinline__ void stage_kv(const int8_t *__restrict__ q, const flo
             const int srow = sidx / spr, scc = sidx - srow * spr;
             s[u] = sc[(size_t)(r0 + srow) * (kv_dim >> 5) + scc];
         }
+        // unconditional stores (clamped: past the end they rewrite the last
+        // element with its own value), so the loads stay ahead of them
 #pragma unroll
         for (int u = 0; u < 4; u++) {
             const int idx = base + u * nthr + tid;
-            if (idx < total) *reinterpret_cast<int4 *>(dq + (size_t)idx * 16) = r[u];
-            if (idx < stotal) ds[idx] = s[u];
+            *reinterpret_cast<int4 *>(dq + (size_t)imin(idx, total - 1) * 16) = r[u];
+            ds[imin(idx, stotal - 1)] = s[u];
         }
     }
 }
@@ -847,7 +1111,7 @@ __device__ __forceinline__ void stage_kv(const int8_t *__restrict__ q, const flo
 // softmax sum is serial (one lane), and each output element walks the
 // positions in order.
 __global__ __launch_bounds__(512) void k_attn_decode(AttnArgs a, int max_len, int chunk) {
-    DECLARE_EXP_TAB(tab);
+    EXP_TAB_LOAD(tab);
     extern __shared__ __align__(16) char smem[];
     __shared__ float s_inv[16];
     const int kv_mul = a.nh / a.nkv;
@@ -869,6 +1133,7 @@ __global__ __launch_bounds__(512) void k_attn_decode(AttnArgs a, int max_len, in
     const float *vsplane = a.vscale + (size_t)kvh * (hd >> 5);
     for (int i = tid; i < kv_mul * hd; i += nthr)
         qsh[i] = a.qh[(size_t)t * a.q_dim + (size_t)h0 * hd + i];
+    EXP_TAB_PUT(tab);                    // read after the first chunk's barriers
     const float scale = a.attn_scale;
     for (int c0 = 0; c0 < L; c0 += chunk) {
         const int cn = imin(chunk, L - c0);
@@ -965,32 +1230,40 @@ __global__ __launch_bounds__(512) void k_attn_decode(AttnArgs a, int max_len, in
 // has rank k in the order (key descending, index ascending), so each
 // (token, expert) thread counts its rank against the token's keys in LDS.
 // Then the chunk's distinct-expert table (one thread per expert collects
-// its (token, slot) members) and the per-32 quantization of latx [nt][lat]
-// (input of the experts' w1/w3), whose loads are issued first.
+// its (token, slot) members).
 #define ROUTE_THREADS 512
-#define ROUTE_LAT_PER_THREAD 8
 __global__ __launch_bounds__(ROUTE_THREADS) void k_moe_route(const float *__restrict__ logits,
                                                              const float *__restrict__ bias, int E, int topk,
                                                              int nt, int *__restrict__ sel_idx,
                                                              float *__restrict__ sel_w, MoeGroups *__restrict__ grp,
-                                                             int *__restrict__ tally, const float *__restrict__ latx,
-                                                             int lat, int8_t *__restrict__ lq,
-                                                             float *__restrict__ lqs) {
-    DECLARE_EXP_TAB(tab);
+                                                             int *__restrict__ tally) {
+    EXP_TAB_LOAD(tab);
     __shared__ float s_key[MAX_CHUNK][MAX_EXPERTS], s_sc[MAX_CHUNK][MAX_EXPERTS];
     __shared__ int s_sel[MAX_PAIRS];
     __shared__ unsigned long long s_ball[2];
     const int tid = threadIdx.x;
-    const int ltot = nt * lat;
-    float lv[ROUTE_LAT_PER_THREAD];
+    // nt*E <= 2 * ROUTE_THREADS: two (token, expert) items per thread, loaded up front
+    float lg[2], bs[2];
 #pragma unroll
-    for (int u = 0; u < ROUTE_LAT_PER_THREAD; u++) lv[u] = latx[imin(u * ROUTE_THREADS + tid, ltot - 1)];
-    for (int idx = tid; idx < nt * E; idx += ROUTE_THREADS) {
+    for (int u = 0; u < 2; u++) {
+        const int idx = imin(u * ROUTE_THREADS + tid, nt * E - 1);
         const int t = idx / E, i = idx - t * E;
-        const float sc = d_sigmoid(logits[(size_t)t * E + i], tab);
-        const float kv = sc + bias[i];
-        s_sc[t][i] = sc;
-        s_key[t][i] = kv == 0.0f ? 0.0f : kv;          // -0 and +0 compare equal in the reference
+        lg[u] = logits[(size_t)t * E + i];
+        bs[u] = bias[i];
+    }
+    if (tid < MAX_PAIRS) s_sel[tid] = -1;
+    EXP_TAB_PUT(tab);
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const int idx = u * ROUTE_THREADS + tid;
+        if (idx < nt * E) {
+            const int t = idx / E, i = idx - t * E;
+            const float sc = d_sigmoid(lg[u], tab);
+            const float kv = sc + bs[u];
+            s_sc[t][i] = sc;
+            s_key[t][i] = kv == 0.0f ? 0.0f : kv;      // -0 and +0 compare equal in the reference
+        }
     }
     __syncthreads();
     for (int idx = tid; idx < nt * E; idx += ROUTE_THREADS) {
@@ -1004,14 +1277,18 @@ __global__ __launch_bounds__(ROUTE_THREADS) void k_moe_route(const float *__rest
         if (rank < topk) s_sel[t * topk + rank] = i;
     }
     __syncthreads();
-    if (tid < nt) {
+    if (tid < nt) {                      // weights renormalized by their serial sum
         const int t = tid;
         float wsum = 0.0f;
-        for (int k = 0; k < topk; k++) wsum += s_sc[t][s_sel[t * topk + k]];
         for (int k = 0; k < topk; k++) {
-            float w = s_sc[t][s_sel[t * topk + k]];
-            if (wsum > 0.0f) w /= wsum;
-            sel_idx[t * topk + k] = s_sel[t * topk + k];
+            const int e = s_sel[t * topk + k];
+            if (e >= 0) wsum += s_sc[t][e];
+        }
+        for (int k = 0; k < topk; k++) {
+            const int e = s_sel[t * topk + k];
+            float w = e >= 0 ? s_sc[t][e] : 0.0f;
+            if (e >= 0 && wsum > 0.0f) w /= wsum;
+            sel_idx[t * topk + k] = e;
             sel_w[t * topk + k] = w;
         }
     }
@@ -1038,53 +1315,6 @@ __global__ __launch_bounds__(ROUTE_THREADS) void k_moe_route(const float *__rest
         const int ng = __popcll(s_ball[0]) + (E > 64 ? __popcll(s_ball[1]) : 0);
         grp->n_groups = ng;
         if (tally) *tally += ng;
-    }
-#pragma unroll
-    for (int u = 0; u < ROUTE_LAT_PER_THREAD; u++) {
-        const int el = u * ROUTE_THREADS + tid;
-        if (u * ROUTE_THREADS + (tid & ~31) < ltot) d_quant_group32(lv[u], lq + el, lqs + (el >> 5));
-    }
-}
-
-// lat_y[t] = sum over slots in order of w * h2 (src/forward_moe.c:128-200),
-// then its per-32 quantization for the up projection.  One 64-lane block per
-// token.
-__global__ __launch_bounds__(64) void k_moe_combine(const float *__restrict__ h2, const int *__restrict__ sel_idx,
-                                                    const float *__restrict__ sel_w, int topk, int lat,
-                                                    float *__restrict__ lat_y, int8_t *__restrict__ xq,
-                                                    float *__restrict__ xqs) {
-    const int t = blockIdx.x;
-    const int lane = threadIdx.x;
-    int sidx[MAX_TOPK];
-    float sw[MAX_TOPK];
-#pragma unroll
-    for (int k = 0; k < MAX_TOPK; k++) {
-        sidx[k] = k < topk ? sel_idx[t * topk + k] : -1;
-        sw[k] = k < topk ? sel_w[t * topk + k] : 0.0f;
-    }
-    for (int base = 0; base < lat; base += 64 * 8) {
-        float hv[8][MAX_TOPK];
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int vcl = imin(base + j * 64 + lane, lat - 1);
-#pragma unroll
-            for (int k = 0; k < MAX_TOPK; k++)
-                hv[j][k] = h2[((size_t)t * topk + imin(k, topk - 1)) * lat + vcl];
-        }
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int v = base + j * 64 + lane;
-            if (base + j * 64 + (lane & ~31) < lat) {
-                float y = 0.0f;
-#pragma unroll
-                for (int k = 0; k < MAX_TOPK; k++) {
-                    if (k >= topk || sidx[k] < 0) continue;
-                    y += sw[k] * hv[j][k];
-                }
-                if (lat_y && v < lat) lat_y[(size_t)t * lat + v] = y;
-                d_quant_group32(y, xq + (size_t)t * lat + v, xqs + (size_t)t * (lat >> 5) + (v >> 5));
-            }
-        }
     }
 }
 
@@ -1227,37 +1457,74 @@ static int gemv_rows_per_tile(int in_dim, int m) {
     return r;
 }
 
-template <int M>
-static hipError_t launch_gemv_m(const GemvBatch &b, size_t lds, int tiles, hipStream_t st) {
-    hipLaunchKernelGGL(k_gemv_q8<M>, dim3(tiles), dim3(GEMV_THREADS), lds, st, b);
+template <int M, int PJ>
+static hipError_t launch_gemv_mp(const GemvBatch &b, size_t lds, int tiles, hipStream_t st) {
+    hipLaunchKernelGGL((k_gemv_q8<M, PJ>), dim3(tiles), dim3(GEMV_THREADS), lds, st, b);
     return hipGetLastError();
+}
+
+template <int M>
+static hipError_t launch_gemv_m(const GemvBatch &b, size_t lds, int tiles, int pj, hipStream_t st) {
+    switch (pj) {
+    case 0: return launch_gemv_mp<M, 0>(b, lds, tiles, st);
+    case 1: return launch_gemv_mp<M, 1>(b, lds, tiles, st);
+    case 2: return launch_gemv_mp<M, 2>(b, lds, tiles, st);
+    case 4: return launch_gemv_mp<M, 4>(b, lds, tiles, st);
+    default: return launch_gemv_mp<M, 8>(b, lds, tiles, st);
+    }
+}
+
+// Checks one job's prologue against the kernel's limits.
+static bool prologue_ok(const Prologue &P, int in_dim, const int8_t *xq, const float *xqs) {
+    if (P.mode == PRO_XQ) return xq && xqs;
+    if (in_dim > PRO_MAX_IN || !P.src) return false;
+    if (P.mode == PRO_QUANT) return P.src_stride >= in_dim && !(P.src_stride & 3);
+    if (P.mode == PRO_SILU) return P.src2 && P.src_stride >= in_dim && !(P.src_stride & 3);
+    if (P.mode == PRO_NORM) return P.w && P.src_stride >= in_dim && !(P.src_stride & 3) && !(P.o_stride & 3);
+    if (P.mode == PRO_COMBINE) return P.sel_idx && P.sel_w && P.topk >= 1 && P.topk <= MAX_TOPK;
+    return false;
 }
 
 extern "C" int l98k_gemv(GemvBatch *b, int m, hipStream_t st) {
     if (m < 1 || m > MAX_CHUNK || b->n < 1 || b->n > MAX_GEMV_JOBS) return -1;
-    int tiles = 0;
+    int tiles = 0, pj = 0;
     size_t lds = 0;
     for (int j = 0; j < b->n; j++) {
         GemvJob &J = b->job[j];
-        if (J.in_dim < 32 || (J.in_dim & 31) || J.in_dim > GEMV_MAX_IN || J.rows < 1 || !J.xq || !J.xqs)
+        if (J.in_dim < 32 || (J.in_dim & 31) || J.in_dim > GEMV_MAX_IN || J.rows < 1 ||
+            !prologue_ok(J.pro, J.in_dim, J.xq, J.xqs))
             return -1;
         J.R = gemv_rows_per_tile(J.in_dim, m);
         J.tile0 = tiles;
         tiles += (J.rows + J.R - 1) / J.R;
-        size_t l = gemv_lds_bytes(m, J.in_dim, J.R);
+        size_t l = gemv_lds_bytes(m, J.in_dim, J.R, J.pro.mode == PRO_NORM);
         lds = l > lds ? l : lds;
+        if (J.pro.mode != PRO_XQ) pj = pro_pj(J.in_dim) > pj ? pro_pj(J.in_dim) : pj;
     }
     if (lds > 64 * 1024) return -1;
     switch (m) {
-    case 1: return (int)launch_gemv_m<1>(*b, lds, tiles, st);
-    case 2: return (int)launch_gemv_m<2>(*b, lds, tiles, st);
-    case 3: return (int)launch_gemv_m<3>(*b, lds, tiles, st);
-    case 4: return (int)launch_gemv_m<4>(*b, lds, tiles, st);
-    case 5: return (int)launch_gemv_m<5>(*b, lds, tiles, st);
-    case 6: return (int)launch_gemv_m<6>(*b, lds, tiles, st);
-    case 7: return (int)launch_gemv_m<7>(*b, lds, tiles, st);
-    default: return (int)launch_gemv_m<8>(*b, lds, tiles, st);
+    case 1: return (int)launch_gemv_m<1>(*b, lds, tiles, pj, st);
+    case 2: return (int)launch_gemv_m<2>(*b, lds, tiles, pj, st);
+    case 3: return (int)launch_gemv_m<3>(*b, lds, tiles, pj, st);
+    case 4: return (int)launch_gemv_m<4>(*b, lds, tiles, pj, st);
+    case 5: return (int)launch_gemv_m<5>(*b, lds, tiles, pj, st);
+    case 6: return (int)launch_gemv_m<6>(*b, lds, tiles, pj, st);
+    case 7: return (int)launch_gemv_m<7>(*b, lds, tiles, pj, st);
+    default: return (int)launch_gemv_m<8>(*b, lds, tiles, pj, st);
     }
+}
+
+// Tiles of a GEMV over `rows` rows of in_dim with m token rows.
+extern "C" int l98k_gemv_tiles(int rows, int in_dim, int m) {
+    const int R = gemv_rows_per_tile(in_dim, m);
+    return (rows + R - 1) / R;
+}
+
+// Whether a GEMV over m rows of width in_dim with a fused RMSNorm prologue
+// fits the kernel's LDS.
+extern "C" int l98k_gemv_norm_fits(int in_dim, int m) {
+    if (in_dim > PRO_MAX_IN || m < 1 || m > MAX_CHUNK) return 0;
+    return gemv_lds_bytes(m, in_dim, gemv_rows_per_tile(in_dim, m), 1) <= 64 * 1024;
 }
 
 extern "C" int l98k_expert_gemv(const ExpertJob *jobs, int n_jobs, const MoeGroups *grp, int max_groups,
@@ -1265,12 +1532,26 @@ extern "C" int l98k_expert_gemv(const ExpertJob *jobs, int n_jobs, const MoeGrou
     if (n_jobs < 1 || n_jobs > 2 || in_dim < 32 || (in_dim & 31) || in_dim > GEMV_MAX_IN || max_groups < 1 ||
         max_groups > MAX_PAIRS)
         return -1;
+    for (int j = 0; j < n_jobs; j++)
+        if (jobs[j].pro.mode == PRO_NORM || jobs[j].pro.mode == PRO_COMBINE ||
+            !prologue_ok(jobs[j].pro, in_dim, jobs[j].xq, jobs[j].xqs))
+            return -1;
     const int R = gemv_rows_per_tile(in_dim, MAX_CHUNK);
     const int tiles = (out_rows + R - 1) / R;
-    const size_t lds = gemv_lds_bytes(MAX_CHUNK, in_dim, R);
+    const size_t lds = gemv_lds_bytes(MAX_CHUNK, in_dim, R, 0);
     if (lds > 64 * 1024) return -1;
-    hipLaunchKernelGGL(k_expert_gemv, dim3(n_jobs * max_groups * tiles), dim3(GEMV_THREADS), lds, st, jobs[0],
-                       n_jobs > 1 ? jobs[1] : jobs[0], grp, max_groups, in_dim, out_rows, R, tiles);
+    int pj = 0;
+    for (int j = 0; j < n_jobs; j++)
+        if (jobs[j].pro.mode != PRO_XQ) pj = pro_pj(in_dim);
+    const dim3 grid(n_jobs * max_groups * tiles), blk(GEMV_THREADS);
+    const ExpertJob &a = jobs[0], &b2 = n_jobs > 1 ? jobs[1] : jobs[0];
+    switch (pj) {
+    case 0: hipLaunchKernelGGL(k_expert_gemv<0>, grid, blk, lds, st, a, b2, grp, max_groups, in_dim, out_rows, R, tiles); break;
+    case 1: hipLaunchKernelGGL(k_expert_gemv<1>, grid, blk, lds, st, a, b2, grp, max_groups, in_dim, out_rows, R, tiles); break;
+    case 2: hipLaunchKernelGGL(k_expert_gemv<2>, grid, blk, lds, st, a, b2, grp, max_groups, in_dim, out_rows, R, tiles); break;
+    case 4: hipLaunchKernelGGL(k_expert_gemv<4>, grid, blk, lds, st, a, b2, grp, max_groups, in_dim, out_rows, R, tiles); break;
+    default: hipLaunchKernelGGL(k_expert_gemv<8>, grid, blk, lds, st, a, b2, grp, max_groups, in_dim, out_rows, R, tiles); break;
+    }
     return (int)hipGetLastError();
 }
 
@@ -1280,15 +1561,15 @@ extern "C" int l98k_embed(const int8_t *q, const float *s, const int *toks, int 
     return (int)hipGetLastError();
 }
 
-#define NORM_CASES(X) X(1) X(2) X(4) X(8) X(16) X(32)
+#define NORM_CASES(X) X(1) X(2) X(4) X(8)
 
 extern "C" int l98k_rmsnorm(float *x, int x_stride, const float *a, const float *b, const float *w,
                             int n, float eps, int rows, float *out, int out_stride, int8_t *xq,
                             float *xqs, hipStream_t st) {
-    if (n < 1 || n > 64 * 32 || (xq && (n & 31)) || rows < 1) return -1;
-#define NORM_LAUNCH(NC)                                                                          \
-    if (n <= 64 * NC) {                                                                          \
-        hipLaunchKernelGGL(k_rmsnorm<NC>, dim3(rows), dim3(64), 0, st, x, x_stride, a, b, w, n, \
+    if (n < 32 || n > 256 * 8 || (n & 31) || (x_stride & 3) || (out && (out_stride & 3)) || rows < 1) return -1;
+#define NORM_LAUNCH(PJ)                                                                          \
+    if (n <= 256 * PJ) {                                                                         \
+        hipLaunchKernelGGL(k_rmsnorm<PJ>, dim3(rows), dim3(64), 0, st, x, x_stride, a, b, w, n, \
                            eps, out, out_stride, xq, xqs);                                       \
         return (int)hipGetLastError();                                                           \
     }
@@ -1300,10 +1581,10 @@ extern "C" int l98k_rmsnorm(float *x, int x_stride, const float *a, const float 
 extern "C" int l98k_mtp_pre(const int8_t *emb_q, const float *emb_s, const int *toks, const float *h, int d,
                             const float *w_e, const float *w_h, float eps, int rows, int8_t *xq, float *xqs,
                             hipStream_t st) {
-    if (d < 32 || d > 64 * 32 || (d & 31) || rows < 1) return -1;
-#define PRE_LAUNCH(NC)                                                                                  \
-    if (d <= 64 * NC) {                                                                                 \
-        hipLaunchKernelGGL(k_mtp_pre<NC>, dim3(rows, 2), dim3(64), 0, st, emb_q, emb_s, toks, h, d, w_e, \
+    if (d < 32 || d > 256 * 8 || (d & 31) || rows < 1) return -1;
+#define PRE_LAUNCH(PJ)                                                                                  \
+    if (d <= 256 * PJ) {                                                                                \
+        hipLaunchKernelGGL(k_mtp_pre<PJ>, dim3(rows, 2), dim3(64), 0, st, emb_q, emb_s, toks, h, d, w_e, \
                            w_h, eps, xq, xqs);                                                          \
         return (int)hipGetLastError();                                                                  \
     }
@@ -1312,32 +1593,22 @@ extern "C" int l98k_mtp_pre(const int8_t *emb_q, const float *emb_s, const int *
     return -1;
 }
 
-extern "C" int l98k_act_quant(const float *h1, const float *h3, int n, int rows, int8_t *xq, float *xqs,
-                              const float *g1, const float *g3, int n2, int rows2, int8_t *xq2, float *xqs2,
-                              hipStream_t st) {
-    if ((n & 31) || (rows2 > 0 && (n2 & 31)) || rows < 0 || rows2 < 0 || rows + rows2 < 1) return -1;
-    hipLaunchKernelGGL(k_act_quant, dim3(rows + rows2), dim3(64), 0, st, h1, h3, n, rows, xq, xqs, g1, g3, n2,
-                       xq2, xqs2);
-    return (int)hipGetLastError();
-}
-
 extern "C" int l98k_kda_conv(const float *pq, const float *pk, const float *pv, int key, int value,
                              const float *wconv, float *ring, size_t slot_stride, int K,
                              const int *ctl_slot, int depth, int advance, int nt, float *qc,
-                             float *kc, float *vc, const float *pfa, int rank, int8_t *fq, float *fqs,
-                             hipStream_t st) {
-    if (nt < 1 || nt > MAX_CHUNK || !pfa || rank < 32 || (rank & 31)) return -1;
+                             float *kc, float *vc, hipStream_t st) {
+    if (nt < 1 || nt > MAX_CHUNK) return -1;
     const int n = 2 * key + value;
-    const dim3 grid((n + 255) / 256 + 1);
+    const dim3 grid((n + 255) / 256);
     if (K == 4)
         hipLaunchKernelGGL(k_kda_conv<4>, grid, dim3(256), 0, st, pq, pk, pv, key, value, wconv, ring,
-                           slot_stride, ctl_slot, depth, advance, nt, qc, kc, vc, pfa, rank, fq, fqs);
+                           slot_stride, ctl_slot, depth, advance, nt, qc, kc, vc);
     else if (K == 3)
         hipLaunchKernelGGL(k_kda_conv<3>, grid, dim3(256), 0, st, pq, pk, pv, key, value, wconv, ring,
-                           slot_stride, ctl_slot, depth, advance, nt, qc, kc, vc, pfa, rank, fq, fqs);
+                           slot_stride, ctl_slot, depth, advance, nt, qc, kc, vc);
     else if (K == 2)
         hipLaunchKernelGGL(k_kda_conv<2>, grid, dim3(256), 0, st, pq, pk, pv, key, value, wconv, ring,
-                           slot_stride, ctl_slot, depth, advance, nt, qc, kc, vc, pfa, rank, fq, fqs);
+                           slot_stride, ctl_slot, depth, advance, nt, qc, kc, vc);
     else
         return -1;
     return (int)hipGetLastError();
@@ -1385,22 +1656,12 @@ extern "C" int l98k_attn_decode(const AttnArgs *a, int nt, int max_len, hipStrea
 }
 
 extern "C" int l98k_moe_route(const float *logits, const float *bias, int E, int topk, int nt,
-                              int *sel_idx, float *sel_w, MoeGroups *grp, int *tally, const float *latx,
-                              int lat, int8_t *lq, float *lqs, hipStream_t st) {
+                              int *sel_idx, float *sel_w, MoeGroups *grp, int *tally, hipStream_t st) {
     if (E > MAX_EXPERTS || E < topk || topk < 1 || topk > MAX_TOPK || nt < 1 || nt > MAX_CHUNK ||
-        nt * topk > MAX_PAIRS || (lat & 31) || nt * lat > ROUTE_LAT_PER_THREAD * ROUTE_THREADS)
+        nt * topk > MAX_PAIRS || nt * E > 2 * ROUTE_THREADS)
         return -1;
     hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(ROUTE_THREADS), 0, st, logits, bias, E, topk, nt, sel_idx,
-                       sel_w, grp, tally, latx, lat, lq, lqs);
-    return (int)hipGetLastError();
-}
-
-extern "C" int l98k_moe_combine(const float *h2, const int *sel_idx, const float *sel_w, int topk,
-                                int lat, int nt, float *lat_y, int8_t *xq, float *xqs,
-                                hipStream_t st) {
-    if (topk < 1 || topk > MAX_TOPK || (lat & 31)) return -1;
-    hipLaunchKernelGGL(k_moe_combine, dim3(nt), dim3(64), 0, st, h2, sel_idx, sel_w, topk, lat,
-                       lat_y, xq, xqs);
+                       sel_w, grp, tally);
     return (int)hipGetLastError();
 }
 

@@ -9,8 +9,11 @@
 
 extern "C" {
 int l98k_upload_exp_table(const float *tab);
-// Fused GEMV of b->n jobs over m <= MAX_CHUNK activation rows.
+// Fused GEMV of b->n jobs over m <= MAX_CHUNK activation rows; each job's
+// prologue builds its int8 input rows.
 int l98k_gemv(GemvBatch *b, int m, hipStream_t st);
+// 1 when a GEMV with an RMSNorm prologue over m rows of in_dim fits the kernel.
+int l98k_gemv_norm_fits(int in_dim, int m);
 // Grouped expert GEMV: n_jobs (<= 2) projections over the groups in grp.
 int l98k_expert_gemv(const ExpertJob *jobs, int n_jobs, const MoeGroups *grp, int max_groups, int in_dim,
                      int out_rows, hipStream_t st);
@@ -22,25 +25,16 @@ int l98k_rmsnorm(float *x, int x_stride, const float *a, const float *b, const f
 int l98k_mtp_pre(const int8_t *emb_q, const float *emb_s, const int *toks, const float *h, int d,
                  const float *w_e, const float *w_h, float eps, int rows, int8_t *xq, float *xqs,
                  hipStream_t st);
-// silu(h1)*h3 quantized per 32, for rows of two independent segments.
-int l98k_act_quant(const float *h1, const float *h3, int n, int rows, int8_t *xq, float *xqs,
-                   const float *g1, const float *g3, int n2, int rows2, int8_t *xq2, float *xqs2,
-                   hipStream_t st);
-// Causal conv + SiLU over [q|k|v] with the ring state; also quantizes the
-// gate low-rank rows pfa [nt][rank] into fq/fqs.
+// Causal conv + SiLU over [q|k|v] with the ring state.
 int l98k_kda_conv(const float *pq, const float *pk, const float *pv, int key, int value, const float *wconv,
                   float *ring, size_t slot_stride, int K, const int *ctl_slot, int depth, int advance, int nt,
-                  float *qc, float *kc, float *vc, const float *pfa, int rank, int8_t *fq, float *fqs,
-                  hipStream_t st);
+                  float *qc, float *kc, float *vc, hipStream_t st);
 int l98k_kda_recur(const KdaRecurArgs *a, int kd, int vd, hipStream_t st);
 int l98k_attn_prep(const AttnArgs *a, int nt, hipStream_t st);
 int l98k_attn_decode(const AttnArgs *a, int nt, int max_len, hipStream_t st);
-// Routing + distinct-expert groups; also quantizes latx [nt][lat] into lq/lqs.
+// Routing + distinct-expert groups.
 int l98k_moe_route(const float *logits, const float *bias, int E, int topk, int nt, int *sel_idx, float *sel_w,
-                   MoeGroups *grp, int *tally, const float *latx, int lat, int8_t *lq, float *lqs,
-                   hipStream_t st);
-int l98k_moe_combine(const float *h2, const int *sel_idx, const float *sel_w, int topk, int lat, int nt,
-                     float *lat_y, int8_t *xq, float *xqs, hipStream_t st);
+                   MoeGroups *grp, int *tally, hipStream_t st);
 int l98k_argmax(const float *x, int n, int rows, int mode, int *out, unsigned long long *partial,
                 unsigned *counter, hipStream_t st);
 int l98k_accept(DevCtl *ctl, const float *vhidden, int d, float *chain, int depth, int brk, hipStream_t st);
