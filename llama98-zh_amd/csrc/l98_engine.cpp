@@ -441,7 +441,7 @@ struct DState {
     float *ks = nullptr, *vs = nullptr;
     // activations
     float *x, *x2, *mtp_x, *mtp_x2, *chain, *blk, *up_out, *sd_out;
-    float *qg, *kp, *vp, *qh;
+    float *qg, *kp, *vp, *qh, *att;
     float *pq, *pk, *pv, *pfa, *pb, *pg, *qc, *kc, *vc, *gate_pre;
     float *rl, *latx, *sgo, *suo, *h1, *h3, *h2, *hb, *hb2, *ffn_out;
     float *vhidden, *mtp_logits, *logits, *draft_logits, *hcap;
@@ -494,6 +494,7 @@ bool carve(DState *s) {
     s->up_out = F((size_t)B * d); s->sd_out = F((size_t)B * d);
     s->qg = F((size_t)B * c.attn_qgate_dim); s->kp = F((size_t)B * c.attn_kv_dim);
     s->vp = F((size_t)B * c.attn_kv_dim); s->qh = F((size_t)B * c.attn_q_dim);
+    s->att = F((size_t)B * c.n_heads * (size_t)((s->seq_len + 3) & ~3));
     s->pq = F((size_t)B * c.lin_key_dim); s->pk = F((size_t)B * c.lin_key_dim);
     s->pv = F((size_t)B * c.lin_value_dim); s->pfa = F((size_t)B * c.kda_gate_rank);
     s->pb = F((size_t)B * c.lin_n_v_heads); s->pg = F((size_t)B * c.lin_value_dim);
@@ -645,9 +646,11 @@ int attn_block(DState *s, const DLayer &L, const Prologue &in, int plane, const 
         y = y * (1.5f - h * y * y);
         a.attn_scale = y;
     }
-    CK(l98k_attn_prep(&a, nt, s->st));
-    if (kv_only) return 0;
-    CK(l98k_attn_decode(&a, nt, max_pos + 1, s->st));
+    if (kv_only) {
+        CK(l98k_attn_prep(&a, nt, s->st));
+        return 0;
+    }
+    CK(l98k_attn(&a, nt, max_pos + 1, s->att, s->st));
     CK(gemv(s, {JX(L.o, s->blk, d, s->xq2, s->xqs2)}, nt));
     return 0;
 }

@@ -31,7 +31,11 @@ int l98k_kda_conv(const float *pq, const float *pk, const float *pv, int key, in
                   float *qc, float *kc, float *vc, hipStream_t st);
 int l98k_kda_recur(const KdaRecurArgs *a, int kd, int vd, hipStream_t st);
 int l98k_attn_prep(const AttnArgs *a, int nt, hipStream_t st);
-int l98k_attn_decode(const AttnArgs *a, int nt, int max_len, hipStream_t st);
+// Attention of nt tokens (positions *ctl_pos + pos_off + t) against the KV
+// plane: scores with the q/k preparation and the chunk's own K/V cache rows,
+// then softmax, value sum, output gate and quantization into oq / oqs.
+// att: scratch [MAX_CHUNK][nh][round4(max_len)] floats.
+int l98k_attn(const AttnArgs *a, int nt, int max_len, float *att, hipStream_t st);
 // Routing + distinct-expert groups.
 int l98k_moe_route(const float *logits, const float *bias, int E, int topk, int nt, int *sel_idx, float *sel_w,
                    MoeGroups *grp, int *tally, hipStream_t st);
