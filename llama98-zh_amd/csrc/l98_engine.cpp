@@ -703,12 +703,12 @@ int moe_block(DState *s, const DLayer &L, const Prologue &in, int nt) {
     const int lat = c.moe_latent_dim, inter = c.moe_intermediate_size, sw = c.moe_shared_width;
     CK(gemv(s, {J(L.router, s->rl, E, in), J(L.down, s->latx, lat, in), J(L.sg, s->sgo, sw, in),
                 J(L.su, s->suo, sw, in)}, nt));
-    CK(l98k_moe_route(s->rl, L.bias, E, topk, nt, s->sel_idx, s->sel_w, s->grp, &s->ctl->expert_tally, s->st));
     const int max_groups = nt * topk < E ? nt * topk : E;
     const ExpertJob up2[2] = {EJ(L.w1, s->h1, 0, PQ(s->latx, lat)), EJ(L.w3, s->h3, 0, PQ(s->latx, lat))};
-    CK(l98k_expert_gemv(up2, 2, s->grp, max_groups, lat, inter, s->st));
+    CK(l98k_moe_up(up2, 2, s->rl, L.bias, E, topk, nt, s->sel_idx, s->sel_w, s->grp, &s->ctl->expert_tally, lat,
+                   inter, s->st));
     const ExpertJob down1[1] = {EJ(L.w2, s->h2, 1, PS(s->h1, s->h3, inter))};
-    CK(l98k_expert_gemv(down1, 1, s->grp, max_groups, inter, lat, s->st));
+    CK(l98k_expert_gemv(down1, 1, s->grp, max_groups, inter, lat, nt, s->st));
     CK(gemv(s, {J(L.up, s->up_out, d, PC(s->h2, s->sel_idx, s->sel_w, topk)),
                 J(L.sd, s->sd_out, d, PS(s->sgo, s->suo, sw))}, nt));
     return 0;

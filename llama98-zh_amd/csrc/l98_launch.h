@@ -16,7 +16,7 @@ int l98k_gemv(GemvBatch *b, int m, hipStream_t st);
 int l98k_gemv_norm_fits(int in_dim, int m);
 // Grouped expert GEMV: n_jobs (<= 2) projections over the groups in grp.
 int l98k_expert_gemv(const ExpertJob *jobs, int n_jobs, const MoeGroups *grp, int max_groups, int in_dim,
-                     int out_rows, hipStream_t st);
+                     int out_rows, int nt, hipStream_t st);
 int l98k_embed(const int8_t *q, const float *s, const int *toks, int d, int nt, float *x, hipStream_t st);
 // x += a (+ b) (when a), RMSNorm(1+w) -> out (when out) and per-32 int8 (when xq).
 int l98k_rmsnorm(float *x, int x_stride, const float *a, const float *b, const float *w, int n, float eps,
@@ -36,9 +36,12 @@ int l98k_attn_prep(const AttnArgs *a, int nt, hipStream_t st);
 // then softmax, value sum, output gate and quantization into oq / oqs.
 // att: scratch [MAX_CHUNK][nh][round4(max_len)] floats.
 int l98k_attn(const AttnArgs *a, int nt, int max_len, float *att, hipStream_t st);
-// Routing + distinct-expert groups.
-int l98k_moe_route(const float *logits, const float *bias, int E, int topk, int nt, int *sel_idx, float *sel_w,
-                   MoeGroups *grp, int *tally, hipStream_t st);
+// Routing of nt tokens (computed in every block) and the routed experts'
+// first projections (n_jobs <= 2, e.g. w1 and w3 over the latent rows);
+// publishes sel_idx / sel_w / grp (and adds the distinct-expert count to
+// *tally) for the down projection and the combine.
+int l98k_moe_up(const ExpertJob *jobs, int n_jobs, const float *logits, const float *bias, int E, int topk, int nt,
+                int *sel_idx, float *sel_w, MoeGroups *grp, int *tally, int in_dim, int out_rows, hipStream_t st);
 int l98k_argmax(const float *x, int n, int rows, int mode, int *out, unsigned long long *partial,
                 unsigned *counter, hipStream_t st);
 int l98k_accept(DevCtl *ctl, const float *vhidden, int d, float *chain, int depth, int brk, hipStream_t st);
