@@ -9,6 +9,7 @@
 #define MAX_TOPK 8
 #define MAX_CHUNK 8          // tokens per forward chunk (the reference's LZ_BATCH_MAX)
 #define MAX_PAIRS (MAX_CHUNK * MAX_TOPK)
+#define KDA_MAX_RANK 128     // gate low-rank width handled by the KDA step kernel
 
 // How a GEMV tile builds its int8 activation rows (in LDS, per block).
 enum {
@@ -113,9 +114,16 @@ typedef struct {
     int out[8];
 } RoundRec;
 
+// One KDA layer's token step (conv, gate up-projection, recurrence, gated
+// norm) for a chunk of nt tokens; one block per head.
 typedef struct {
-    const float *qc, *kc, *vc;          // conv outputs [nt][key|key|value]
-    const float *gate_pre;              // f_b outputs [nt][nv*kd]
+    const float *pq, *pk, *pv;          // projections before the conv [nt][key | key | value]
+    const float *pfa;                   // gate low-rank projection [nt][rank]
+    const int8_t *fb_q;                 // gate up-projection [nv*kd][rank] int8
+    const float *fb_s;                  // its row scales
+    const float *conv_w;                // [conv_dim][K] taps, channels [q | k | v]
+    float *conv_ring;                   // the layer's history inside ring slot 0, [conv_dim][K-1]
+    size_t conv_slot_stride;            // floats between ring slots
     const float *bvec;                  // b projection [nt][nv]
     const float *gz;                    // g projection [nt][value]
     const float *a_log, *dt_bias, *o_norm;
@@ -126,9 +134,9 @@ typedef struct {
     float *normed_out;                  // optional gated-norm output (tests)
     int8_t *xq;                         // o_proj activations [nt][value]
     float *xqs;
-    int nk, nv, key, value, depth, advance, nt;
+    int nv, key, value, rank, depth, advance, nt;
     float scale, eps;
-} KdaRecurArgs;
+} KdaStepArgs;
 
 typedef struct {
     const float *qg;                    // [nt][qg_dim] interleaved per head [q | gate]

@@ -1,0 +1,302 @@
+// Device arithmetic shared by the gfx950 kernels of the MTP
+// speculative-decoding step.
+//
+// Every floating-point expression below is evaluated in the reference's
+// float-oracle order (reference src/ops_*.c, cited per kernel), and the file
+// is compiled with -ffp-contract=off, so results are bit-identical to the
+// reference engine, not merely close:
+//   * sums the reference accumulates serially stay serial (one lane walks
+//     them in index order); integer sums (int8 dot products) and max
+//     reductions are order-free and run as wave reductions;
+//   * exp / rsqrt / sigmoid / softplus are the reference's own float bodies
+//     (magic-number floor, 32-entry 2^(i/32) table, two Newton steps), not
+//     the device libm;
+//   * int8 rounding is the reference's 1.5*2^23 magic add (round to nearest
+//     even).
+// Per-round scalars (positions, ring slot, token ids) are read from a device
+// control block, so a whole round can be replayed as a HIP graph.
+#ifndef L98_DEVMATH_H
+#define L98_DEVMATH_H
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "l98_dev.h"
+#include "l98_launch.h"
+
+// ---------------------------------------------------------------- math ---
+
+// Each translation unit holds its own copy of the table (static), uploaded
+// by its l98k_upload_exp_table_* (all of them run from l98k_upload_exp_table).
+static __constant__ float c_exp_tab[32];
+
+// The 2^(i/32) table of d_exp is indexed by a per-lane value, so it is read
+// from LDS (one ds_read) rather than constant memory (a vector memory load).
+// EXP_TAB_LOAD issues the load of a thread's entry early, with the kernel's
+// other loads; EXP_TAB_PUT stores it, and a barrier must follow before the
+// first d_exp.
+#define EXP_TAB_LOAD(tab)     \
+    __shared__ float tab[32]; \
+    const float tab##_v = c_exp_tab[threadIdx.x & 31]
+#define EXP_TAB_PUT(tab) \
+    if (threadIdx.x < 32) tab[threadIdx.x] = tab##_v
+
+__device__ __forceinline__ float f_from_u(uint32_t u) { return __uint_as_float(u); }
+__device__ __forceinline__ uint32_t u_from_f(float f) { return __float_as_uint(f); }
+
+// lz_exp_float_body, src/ops_quant.c:300-349
+__device__ __forceinline__ float d_exp(float x, const float *tab) {
+    const float C2 = 0.242844437f, C1 = 0.207425515f, C0 = 0.549730133f;
+    const float LOG2E32 = 1.44269504f * 32.0f;
+    if (x > 88.0f) return 3.40282347e+38f;
+    if (x < -87.3f) return 0.0f;
+    float y32 = x * LOG2E32;
+    float m = (y32 - 0.5f) + 12582912.0f;
+    int32_t t = (int32_t)(u_from_f(m) & 0x007FFFFFu) - 0x00400000;
+    int32_t n = t >> 5;
+    int32_t idx = t & 31;
+    float r = y32 - (float)t;
+    float w = 1.0f + r * 0.03125f;
+    float p2n = f_from_u((uint32_t)(n + 127) << 23);
+    float c = (C2 * w + C1) * w + C0;
+    return p2n * (tab[idx] * c);
+}
+
+// lz_rsqrt_float_body, src/ops_quant.c:126-135
+__device__ __forceinline__ float d_rsqrt(float x) {
+    float h = 0.5f * x;
+    float y = f_from_u(0x5f375a86u - (u_from_f(x) >> 1));
+    y = y * (1.5f - h * y * y);
+    y = y * (1.5f - h * y * y);
+    return y;
+}
+
+// lz_sigmoid float branch, src/ops_quant.c:1816-1853
+__device__ __forceinline__ float d_sigmoid(float x, const float *tab) {
+    if (x >= 0.0f) {
+        float z = d_exp(-x, tab);
+        return 1.0f / (1.0f + z);
+    }
+    float z = d_exp(x, tab);
+    return z / (1.0f + z);
+}
+__device__ __forceinline__ float d_silu(float x, const float *tab) { return x * d_sigmoid(x, tab); }
+
+// lz_softplus_poly, src/ops_quant.c:1040-1060
+__device__ __forceinline__ float d_softplus(float x, const float *tab) {
+    const float L[9] = {1.000000000f, -0.499995530f, 0.333203435f, -0.248529464f,
+                        0.191451162f, -0.137466222f, 0.079210736f, -0.030110965f,
+                        0.005384062f};
+    if (x > 16.0f) return x;
+    float nx = (x < 0.0f) ? x : -x;
+    float u = d_exp(nx, tab);
+    float p = L[8];
+#pragma unroll
+    for (int i = 7; i >= 0; i--) p = p * u + L[i];
+    float lp = u * p;
+    if (x > 0.0f) return x + lp;
+    return lp;
+}
+
+// q8_round (--fastfp off), src/ops_quant.h:145-178
+__device__ __forceinline__ int d_q8_round(float v) {
+    float t = v + 12582912.0f;
+    return (int)(u_from_f(t) & 0x007FFFFFu) - 0x00400000;
+}
+
+// sum of squares / n for power-of-two n is a multiply (src/ops_norm.c:161-170)
+__device__ __forceinline__ float d_ss_over_n(float ss, int n) {
+    if ((n & (n - 1)) == 0) {
+        int e = 31 - __clz(n);
+        return ss * f_from_u((uint32_t)(127 - e) << 23);
+    }
+    return ss / (float)n;
+}
+
+// Order-preserving float key (src/sampler.c:121)
+__device__ __forceinline__ uint32_t d_fkey(float f) {
+    uint32_t u = u_from_f(f);
+    return u ^ ((uint32_t)((int32_t)u >> 31) | 0x80000000u);
+}
+__device__ __forceinline__ float d_unkey(uint32_t k) {
+    return f_from_u((k & 0x80000000u) ? (k ^ 0x80000000u) : ~k);
+}
+
+__device__ __forceinline__ float wave_max_u(uint32_t v, int width) {
+    for (int o = width >> 1; o > 0; o >>= 1) {
+        uint32_t w = __shfl_xor(v, o, width);
+        v = w > v ? w : v;
+    }
+    return f_from_u(v);
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+    for (int o = 32; o > 0; o >>= 1) {
+        uint64_t w = __shfl_xor(v, o);
+        v = w > v ? w : v;
+    }
+    return v;
+}
+
+// Quantize one 32-element group held one element per lane across a
+// 32-lane half wave (lane & 31 = element).  Writes q[lane] and, from lane
+// 0 of the half, the scale.  src/ops_quant.c:1633-1670, 2152-2286.
+__device__ __forceinline__ void d_quant_group32(float x, int8_t *q, float *s) {
+    const float INV127 = 1.0f / 127.0f;
+    uint32_t a = u_from_f(x) & 0x7FFFFFFFu;
+    float amax = wave_max_u(a, 32);
+    float sg, inv;
+    bool fast;
+    if (amax > 0.0f) {
+        sg = amax * INV127;
+        inv = 127.0f / amax;
+        fast = (inv <= 3.40282347e+38f);
+        if (sg < 1.0e-30f) { sg = 1.0f; inv = 0.0f; fast = true; }
+    } else {
+        sg = 1.0f; inv = 0.0f; fast = true;
+    }
+    int qi = fast ? d_q8_round(x * inv) : d_q8_round(x / sg);
+    qi = qi > 127 ? 127 : qi;
+    qi = qi < -127 ? -127 : qi;
+    *q = (int8_t)qi;
+    if ((threadIdx.x & 31) == 0) *s = sg;
+}
+
+// Serial left-to-right float sum of n values in LDS by one lane (v 16-byte
+// aligned).  The adds stay in index order.  serial_sum_n unrolls a short
+// fixed length; serial_sum walks blocks of 32 values with the next block's
+// eight 16-byte reads issued before the current block's adds, so the loop
+// body stays small and the LDS latency hides behind the dependent adds.
+template <int N>
+__device__ __forceinline__ float serial_sum_n(const float *v) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < N; i += 4) {
+        const float4 q = *reinterpret_cast<const float4 *>(v + i);
+        ss += q.x; ss += q.y; ss += q.z; ss += q.w;
+    }
+    return ss;
+}
+
+__device__ __forceinline__ float serial_sum(const float *v, int n) {
+    float ss = 0.0f;
+    const int nb = n >> 5;
+    if (nb > 0) {
+        float4 cur[8], nxt[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) cur[u] = reinterpret_cast<const float4 *>(v)[u];
+#pragma unroll 1
+        for (int b = 0; b < nb; b++) {
+            const int bn = b + 1 < nb ? b + 1 : b;          // last block re-reads itself
+#pragma unroll
+            for (int u = 0; u < 8; u++) nxt[u] = reinterpret_cast<const float4 *>(v + 32 * bn)[u];
+#pragma unroll
+            for (int u = 0; u < 8; u++) { ss += cur[u].x; ss += cur[u].y; ss += cur[u].z; ss += cur[u].w; }
+#pragma unroll
+            for (int u = 0; u < 8; u++) cur[u] = nxt[u];
+        }
+    }
+    for (int i = nb << 5; i < n; i++) ss += v[i];
+    return ss;
+}
+
+// -------------------------------------------------------------- helpers ---
+
+__device__ __forceinline__ int imin(int a, int b) { return a < b ? a : b; }
+__device__ __forceinline__ int imax(int a, int b) { return a > b ? a : b; }
+
+// ------------------------------------------------------- rmsnorm (+q8) ---
+//
+// Row kernels hold a row of n floats in a 64-lane block as float4 f =
+// lane + 64*j (PJ per lane), so every 32-element quantization group is an
+// aligned lane octet (see quant_octet below).
+
+__device__ __forceinline__ uint32_t umax(uint32_t a, uint32_t b) { return a > b ? a : b; }
+
+// Max over the 8 lanes of an aligned lane octet (DPP within a row).
+__device__ __forceinline__ uint32_t octet_max(uint32_t m) {
+    m = umax(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0xB1, 0xF, 0xF, false));   // quad_perm 1,0,3,2
+    m = umax(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x4E, 0xF, 0xF, false));   // quad_perm 2,3,0,1
+    m = umax(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x141, 0xF, 0xF, false));  // row_half_mirror
+    return m;
+}
+
+// Per-32 quantization (src/ops_quant.c:1633-1670, 2152-2286) of a group held
+// as 4 consecutive elements per lane over an aligned lane octet.  Returns the
+// four int8 packed little-endian; *sg receives the group scale.  Every lane
+// of the octet must execute it.
+__device__ __forceinline__ uint32_t quant_octet(float4 v, float *sg_out) {
+    const float INV127 = 1.0f / 127.0f;
+    uint32_t m = umax(umax(u_from_f(v.x) & 0x7FFFFFFFu, u_from_f(v.y) & 0x7FFFFFFFu),
+                      umax(u_from_f(v.z) & 0x7FFFFFFFu, u_from_f(v.w) & 0x7FFFFFFFu));
+    const float amax = f_from_u(octet_max(m));
+    float sg, inv;
+    bool fast;
+    if (amax > 0.0f) {
+        sg = amax * INV127;
+        inv = 127.0f / amax;
+        fast = (inv <= 3.40282347e+38f);
+        if (sg < 1.0e-30f) { sg = 1.0f; inv = 0.0f; fast = true; }
+    } else {
+        sg = 1.0f; inv = 0.0f; fast = true;
+    }
+    float e[4] = {v.x, v.y, v.z, v.w};
+    if (fast) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) e[i] = e[i] * inv;
+    } else {                             // 127/amax overflowed: divide by the scale instead
+#pragma unroll
+        for (int i = 0; i < 4; i++) e[i] = e[i] / sg;
+    }
+    uint32_t packed = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        int qi = d_q8_round(e[i]);
+        qi = qi > 127 ? 127 : qi;
+        qi = qi < -127 ? -127 : qi;
+        packed |= ((uint32_t)qi & 0xFFu) << (8 * i);
+    }
+    *sg_out = sg;
+    return packed;
+}
+
+// RMSNorm(1+w) of the block's row v (lz_rmsnorm, src/ops_norm.c:690-747:
+// sum of squares serial in index order by lane 0, inv = rsqrt(ss/n + eps),
+// o = (x*inv)*(1+w)), then the optional store of o and its per-32
+// quantization.  n % 32 == 0.
+template <int PJ>
+__device__ __forceinline__ void norm_row(const float4 (&v)[PJ], const float4 (&wn)[PJ], int n, float eps,
+                                         float *sq, float *s_inv, float *__restrict__ out,
+                                         int8_t *__restrict__ xq, float *__restrict__ xqs) {
+    const int lane = threadIdx.x, nf = n >> 2;
+#pragma unroll
+    for (int j = 0; j < PJ; j++) {
+        const int f = lane + 64 * j;
+        if (f < nf) reinterpret_cast<float4 *>(sq)[f] =
+            make_float4(v[j].x * v[j].x, v[j].y * v[j].y, v[j].z * v[j].z, v[j].w * v[j].w);
+    }
+    __syncthreads();
+    if (lane == 0) *s_inv = d_rsqrt(d_ss_over_n(serial_sum(sq, n), n) + eps);
+    __syncthreads();
+    const float inv = *s_inv;
+#pragma unroll
+    for (int j = 0; j < PJ; j++) {
+        const int f = lane + 64 * j;
+        const float4 o = make_float4(v[j].x * inv * (1.0f + wn[j].x), v[j].y * inv * (1.0f + wn[j].y),
+                                     v[j].z * inv * (1.0f + wn[j].z), v[j].w * inv * (1.0f + wn[j].w));
+        if (out && f < nf) reinterpret_cast<float4 *>(out)[f] = o;
+        if (xq) {
+            float sg;
+            const uint32_t q = quant_octet(o, &sg);
+            if (f < nf) {
+                reinterpret_cast<uint32_t *>(xq)[f] = q;
+                if (!(f & 7)) xqs[f >> 3] = sg;
+            }
+        }
+    }
+}
+
+// One 64-lane block per row, n <= 256*PJ.  Optionally first folds the
+// residual in place: x_row = x_row + (a_row [+ b_row]) (the reference's
+// x += xb2 with xb2 = up + shared already summed, src/forward.c:1449-1557,
+// src/forward_moe.c:552), then norm_row.  Every load is issued up front.
+#endif

@@ -442,7 +442,7 @@ struct DState {
     // activations
     float *x, *x2, *mtp_x, *mtp_x2, *chain, *blk, *up_out, *sd_out;
     float *qg, *kp, *vp, *qh, *att;
-    float *pq, *pk, *pv, *pfa, *pb, *pg, *qc, *kc, *vc, *gate_pre;
+    float *pq, *pk, *pv, *pfa, *pb, *pg;
     float *rl, *latx, *sgo, *suo, *h1, *h3, *h2, *hb, *hb2, *ffn_out;
     float *vhidden, *mtp_logits, *logits, *draft_logits, *hcap;
     int8_t *xq, *xq2, *xq3, *xq4;
@@ -498,9 +498,6 @@ bool carve(DState *s) {
     s->pq = F((size_t)B * c.lin_key_dim); s->pk = F((size_t)B * c.lin_key_dim);
     s->pv = F((size_t)B * c.lin_value_dim); s->pfa = F((size_t)B * c.kda_gate_rank);
     s->pb = F((size_t)B * c.lin_n_v_heads); s->pg = F((size_t)B * c.lin_value_dim);
-    s->qc = F((size_t)B * c.lin_key_dim); s->kc = F((size_t)B * c.lin_key_dim);
-    s->vc = F((size_t)B * c.lin_value_dim);
-    s->gate_pre = F((size_t)B * c.lin_n_v_heads * c.lin_k_head_dim);
     s->rl = F((size_t)B * c.num_experts); s->latx = F((size_t)B * c.moe_latent_dim);
     s->sgo = F((size_t)B * c.moe_shared_width); s->suo = F((size_t)B * c.moe_shared_width);
     s->h1 = F((size_t)pairs * c.moe_intermediate_size); s->h3 = F((size_t)pairs * c.moe_intermediate_size);
@@ -671,25 +668,25 @@ int kda_block(DState *s, const DLayer &L, const Prologue &in, int li, int nt, in
     const LZModelConfig &c = s->m->c;
     const int d = c.hidden_size, key = c.lin_key_dim, value = c.lin_value_dim;
     const int nv = c.lin_n_v_heads, kd = c.lin_k_head_dim, vd = c.lin_v_head_dim;
-    const int nvk = nv * kd;
     CK(gemv(s, {J(L.kq, s->pq, key, in), J(L.kk, s->pk, key, in), J(L.kv, s->pv, value, in),
                 J(L.fa, s->pfa, c.kda_gate_rank, in), J(L.kb, s->pb, nv, in), J(L.kg, s->pg, value, in)}, nt));
     const int hist = c.conv_kernel - 1;
-    CK(l98k_kda_conv(s->pq, s->pk, s->pv, key, value, L.conv,
-                     s->conv + (size_t)li * c.lin_conv_dim * hist, s->conv_slot, c.conv_kernel,
-                     &s->ctl->slot_base, s->depth, advance, nt, s->qc, s->kc, s->vc, s->st));
-    CK(gemv(s, {J(L.fb, s->gate_pre, nvk, PQ(s->pfa, c.kda_gate_rank))}, nt));
-    KdaRecurArgs a{};
-    a.qc = s->qc; a.kc = s->kc; a.vc = s->vc; a.gate_pre = s->gate_pre; a.bvec = s->pb; a.gz = s->pg;
+    KdaStepArgs a{};
+    a.pq = s->pq; a.pk = s->pk; a.pv = s->pv; a.pfa = s->pfa;
+    a.fb_q = L.fb.q; a.fb_s = L.fb.s;
+    a.conv_w = L.conv;
+    a.conv_ring = s->conv + (size_t)li * c.lin_conv_dim * hist;
+    a.conv_slot_stride = s->conv_slot;
+    a.bvec = s->pb; a.gz = s->pg;
     a.a_log = L.a_log; a.dt_bias = L.dt_bias; a.o_norm = L.o_norm;
     a.state = s->kda + (size_t)li * nv * kd * vd;
     a.slot_stride = s->kda_slot;
     a.ctl_slot = &s->ctl->slot_base;
     a.xq = s->xq2; a.xqs = s->xqs2;
-    a.nk = c.lin_n_k_heads; a.nv = nv; a.key = key; a.value = value;
+    a.nv = nv; a.key = key; a.value = value; a.rank = c.kda_gate_rank;
     a.depth = s->depth; a.advance = advance; a.nt = nt;
     a.scale = ssm_scale(kd); a.eps = c.rms_norm_eps;
-    CK(l98k_kda_recur(&a, kd, vd, s->st));
+    CK(l98k_kda_step(&a, kd, c.conv_kernel, s->st));
     CK(gemv(s, {JX(L.ko, s->blk, d, s->xq2, s->xqs2)}, nt));
     return 0;
 }

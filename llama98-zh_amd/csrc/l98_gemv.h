@@ -1,0 +1,393 @@
+// The int8 GEMV tile engine shared by the dense and the grouped-expert
+// GEMV kernels, with its host-side shape helpers.
+#ifndef L98_GEMV_H
+#define L98_GEMV_H
+#include "l98_devmath.h"
+
+// ------------------------------------------------------------- GEMV/q8 ---
+//
+// o[t][row] = 0.0f + (sum_s float(acc[t,row,s]) * xqs[t][s]) * ws[row]
+// with acc the exact int32 sum over each 32-element group
+// (lz_matmul_xq_nt -> matmul_q8_impl + epi_q8, src/ops_matmul.c:336-466,
+// src/ops_epi.c:983-1017).
+//
+// A 256-lane block streams one tile of R rows (R*in_dim <= 32 KiB): each
+// wave issues all of its 16-byte weight loads of its 8 KiB quarter first.
+// While they are in flight the block builds the M int8 activation rows in
+// LDS (the job's prologue: copy pre-quantized rows, or quantize float rows,
+// optionally after the residual fold + RMSNorm, SiLU-mul or MoE slot
+// combine that produced them), so the producer's serial work overlaps the
+// weight latency and needs no launch of its own.  The 16-element partial
+// dot products (v_dot4_i32_i8) of neighbouring lanes add up to the exact
+// 32-element group sums (an integer add, order-free), which go to LDS; then
+// one lane per (row, token) runs the epilogue serially over the groups, in
+// the reference order.  Weights stream once per launch for any M <= 8.
+
+#define GEMV_THREADS 256
+#define GEMV_WAVE_BYTES 8192
+#define GEMV_TILE_BYTES (GEMV_WAVE_BYTES * (GEMV_THREADS / 64))
+#define GEMV_MAXJ (GEMV_WAVE_BYTES / 16 / 64)
+#define GEMV_MAX_IN 4096
+#define PRO_MAX_IN 2048                 // float prologues: <= 8 float4 per lane per row
+// Float prologues keep PJ float4 per lane per row (PJ*256 elements); the
+// kernels are instantiated for PJ = 0 (pre-quantized input only), 1, 2, 4, 8.
+static inline int pro_pj(int in_dim) {
+    const int j = (in_dim + 255) / 256;
+    return j <= 1 ? 1 : j <= 2 ? 2 : j <= 4 ? 4 : 8;
+}
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// LDS bytes of one tile: staged activations, their scales, and the larger of
+// the group sums and the RMSNorm squares.
+__host__ __device__ inline size_t gemv_lds_bytes(int m, int in_dim, int R, int norm) {
+    const size_t part = (size_t)R * m * ((in_dim >> 5) + 1) * 4;
+    const size_t sq = norm ? (size_t)m * (in_dim + 4) * 4 : 0;
+    return (size_t)m * in_dim + (size_t)m * (in_dim >> 5) * 4 + (part > sq ? part : sq);
+}
+
+__device__ __forceinline__ float4 f4_silu_mul(float4 p, float4 q, const float *tab) {
+    return make_float4(d_silu(p.x, tab) * q.x, d_silu(p.y, tab) * q.y, d_silu(p.z, tab) * q.z,
+                       d_silu(p.w, tab) * q.w);
+}
+
+// Per-32 quantization of a tile's float rows (wave w holds rows w, w+4 as
+// float4 f = lane + 64*j) into sx / sxs.
+template <int RW, int PJN>
+__device__ __forceinline__ void quant_rows(const float4 (&v)[RW][PJN], int wave, int lane, int nm, int nf, int nb,
+                                           int in_dim, int8_t *sx, float *sxs) {
+#pragma unroll
+    for (int r = 0; r < RW; r++) {
+        const int t = wave + 4 * r;
+#pragma unroll
+        for (int j = 0; j < PJN; j++) {
+            float sg;
+            const uint32_t q = quant_octet(v[r][j], &sg);
+            const int f = lane + 64 * j;
+            if (t < nm && f < nf) {
+                reinterpret_cast<uint32_t *>(sx + (size_t)t * in_dim)[f] = q;
+                if (!(f & 7)) sxs[t * nb + (f >> 3)] = sg;
+            }
+        }
+    }
+}
+
+// Builds the tile's activation rows in LDS from the job's prologue: sx
+// [M][in_dim] int8 and sxs [M][in_dim/32].  Row t of the tile is activation
+// row xrow[t]; rows t >= nm are left unused.  The prologue's global loads are
+// issued first, then issue_w() (the tile's weight loads), then the
+// prologue's arithmetic, so the weight loads are in flight behind it and the
+// first use of a prologue value waits only for the prologue's own loads.
+// Float prologues: wave w builds rows w and w + 4 (one float4 per lane per
+// 256 elements), so the quantization groups are lane octets.  PRO_NORM
+// (lz_rmsnorm, src/ops_norm.c:690-747, after the residual fold x += a (+ b)
+// of src/forward.c:1449-1557): the squares go to LDS and lane t of wave 0
+// walks row t's sum serially, all rows at once; the block with `writer` set
+// stores the updated residual and the normed rows.  PRO_SILU:
+// lz_ffn_gate_up's silu(g)*u (src/forward_kda.c:1067-1088).  PRO_COMBINE:
+// the slot-ordered weighted sum of the experts' outputs
+// (src/forward_moe.c:128-200).  Every load is unconditional (rows past nm
+// and elements past the row end are clamped to valid addresses and their
+// values unused), and each mode is one straight-line block.  Contains block
+// barriers: call from every thread.
+#define XQ_PER_THREAD 4
+// Prologue-mode sets a kernel instance is compiled for (bit 1 << PRO_*);
+// every other mode's code is left out of the instance.
+#define MB(m) (1 << (m))
+#define MODES_X MB(PRO_XQ)
+#define MODES_N MB(PRO_NORM)
+#define MODES_S MB(PRO_SILU)
+#define MODES_Q MB(PRO_QUANT)
+#define MODES_CS (MB(PRO_COMBINE) | MB(PRO_SILU))
+template <int M, int PJ, int MODES, typename IssueW>
+__device__ __forceinline__ void build_rows(const Prologue &P, const int8_t *__restrict__ xq,
+                                           const float *__restrict__ xqs, int in_dim, const int (&xrow)[M], int nm,
+                                           bool writer, int8_t *sx, float *sxs, float *sq, float *s_inv,
+                                           float *tab, IssueW issue_w) {
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int nb = in_dim >> 5, nf = in_dim >> 2;
+    if (PJ == 0 || ((MODES & MB(PRO_XQ)) && P.mode == PRO_XQ)) {
+        // int4 chunk idx of the tile's rows: token idx / cpr, chunk idx % cpr;
+        // the stores are unconditional (clamped: past the end they rewrite
+        // the last chunk with its own value).
+        const int cpr = in_dim >> 4;
+        const int total = M * cpr, stotal = M * nb;
+        int4 r[XQ_PER_THREAD];
+        float sc[XQ_PER_THREAD];
+#pragma unroll
+        for (int u = 0; u < XQ_PER_THREAD; u++) {
+            const int idx = imin(u * GEMV_THREADS + tid, total - 1);
+            const int t = idx / cpr, p = idx - t * cpr;
+            r[u] = *reinterpret_cast<const int4 *>(xq + (size_t)xrow[t < nm ? t : 0] * in_dim + p * 16);
+            const int si = imin(u * GEMV_THREADS + tid, stotal - 1);
+            const int ts = si / nb;
+            sc[u] = xqs[(size_t)xrow[ts < nm ? ts : 0] * nb + (si - ts * nb)];
+        }
+        issue_w();
+#pragma unroll
+        for (int u = 0; u < XQ_PER_THREAD; u++) {
+            reinterpret_cast<int4 *>(sx)[imin(u * GEMV_THREADS + tid, total - 1)] = r[u];
+            sxs[imin(u * GEMV_THREADS + tid, stotal - 1)] = sc[u];
+        }
+        for (int base = XQ_PER_THREAD * GEMV_THREADS; base < total; base += GEMV_THREADS) {
+            const int idx = imin(base + tid, total - 1);
+            const int t = idx / cpr, p = idx - t * cpr;
+            reinterpret_cast<int4 *>(sx)[idx] =
+                *reinterpret_cast<const int4 *>(xq + (size_t)xrow[t < nm ? t : 0] * in_dim + p * 16);
+        }
+        for (int base = XQ_PER_THREAD * GEMV_THREADS; base < stotal; base += GEMV_THREADS) {
+            const int si = imin(base + tid, stotal - 1);
+            const int ts = si / nb;
+            sxs[si] = xqs[(size_t)xrow[ts < nm ? ts : 0] * nb + (si - ts * nb)];
+        }
+        return;
+    }
+    constexpr int RW = (M + 3) / 4;
+    constexpr int PJN = PJ > 0 ? PJ : 1;
+    int xr[RW];
+#pragma unroll
+    for (int r = 0; r < RW; r++) {
+        const int t = wave + 4 * r;
+        xr[r] = xrow[t < nm ? t : 0];
+    }
+    int fc[PJN];
+#pragma unroll
+    for (int j = 0; j < PJN; j++) fc[j] = imin(lane + 64 * j, nf - 1);
+    float4 v[RW][PJN];
+    if ((MODES & MB(PRO_QUANT)) && P.mode == PRO_QUANT) {
+#pragma unroll
+        for (int r = 0; r < RW; r++)
+#pragma unroll
+            for (int j = 0; j < PJN; j++)
+                v[r][j] = reinterpret_cast<const float4 *>(P.src + (size_t)xr[r] * P.src_stride)[fc[j]];
+        issue_w();
+        quant_rows<RW, PJN>(v, wave, lane, nm, nf, nb, in_dim, sx, sxs);
+    } else if ((MODES & MB(PRO_SILU)) && P.mode == PRO_SILU) {
+        const float tabv = c_exp_tab[lane & 31];
+        float4 q[RW][PJN];
+#pragma unroll
+        for (int r = 0; r < RW; r++)
+#pragma unroll
+            for (int j = 0; j < PJN; j++) {
+                v[r][j] = reinterpret_cast<const float4 *>(P.src + (size_t)xr[r] * P.src_stride)[fc[j]];
+                q[r][j] = reinterpret_cast<const float4 *>(P.src2 + (size_t)xr[r] * P.src_stride)[fc[j]];
+            }
+        issue_w();
+        if (tid < 32) tab[tid] = tabv;
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < RW; r++)
+#pragma unroll
+            for (int j = 0; j < PJN; j++) v[r][j] = f4_silu_mul(v[r][j], q[r][j], tab);
+        quant_rows<RW, PJN>(v, wave, lane, nm, nf, nb, in_dim, sx, sxs);
+    } else if ((MODES & MB(PRO_COMBINE)) && P.mode == PRO_COMBINE) {
+        int sidx[RW][MAX_TOPK];
+        float swt[RW][MAX_TOPK];
+        float4 h[RW][MAX_TOPK][PJN];
+#pragma unroll
+        for (int r = 0; r < RW; r++)
+#pragma unroll
+            for (int k = 0; k < MAX_TOPK; k++) {
+                const int pair = xr[r] * P.topk + imin(k, P.topk - 1);
+                sidx[r][k] = P.sel_idx[pair];
+                swt[r][k] = P.sel_w[pair];
+#pragma unroll
+                for (int j = 0; j < PJN; j++)
+                    h[r][k][j] = reinterpret_cast<const float4 *>(P.src + (size_t)pair * in_dim)[fc[j]];
+            }
+        issue_w();
+#pragma unroll
+        for (int r = 0; r < RW; r++)
+#pragma unroll
+            for (int j = 0; j < PJN; j++) {
+                float4 y = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+                for (int k = 0; k < MAX_TOPK; k++) {
+                    const float wk = swt[r][k];
+                    const float4 hk = h[r][k][j];
+                    const float4 y2 = make_float4(y.x + wk * hk.x, y.y + wk * hk.y, y.z + wk * hk.z, y.w + wk * hk.w);
+                    if (k < P.topk && sidx[r][k] >= 0) y = y2;
+                }
+                v[r][j] = y;
+            }
+        quant_rows<RW, PJN>(v, wave, lane, nm, nf, nb, in_dim, sx, sxs);
+    } else if (MODES & MB(PRO_NORM)) {   // PRO_NORM
+        const bool has_a = P.a != nullptr, has_b = P.b != nullptr;
+        const float *pa = has_a ? P.a : P.src;
+        const float *pb = has_b ? P.b : pa;
+        const int sa = has_a ? in_dim : P.src_stride, sb = has_b ? in_dim : sa;
+        float4 wn[PJN], ad[RW][PJN], bd[RW][PJN];
+#pragma unroll
+        for (int j = 0; j < PJN; j++) wn[j] = reinterpret_cast<const float4 *>(P.w)[fc[j]];
+#pragma unroll
+        for (int r = 0; r < RW; r++)
+#pragma unroll
+            for (int j = 0; j < PJN; j++) {
+                v[r][j] = reinterpret_cast<const float4 *>(P.src + (size_t)xr[r] * P.src_stride)[fc[j]];
+                ad[r][j] = reinterpret_cast<const float4 *>(pa + (size_t)xr[r] * sa)[fc[j]];
+                bd[r][j] = reinterpret_cast<const float4 *>(pb + (size_t)xr[r] * sb)[fc[j]];
+            }
+        issue_w();
+        // x + (a + b), x + a, or x
+#pragma unroll
+        for (int r = 0; r < RW; r++)
+#pragma unroll
+            for (int j = 0; j < PJN; j++) {
+                float4 a2 = ad[r][j];
+                const float4 b2 = bd[r][j];
+                const float4 ab = make_float4(a2.x + b2.x, a2.y + b2.y, a2.z + b2.z, a2.w + b2.w);
+                if (has_b) a2 = ab;
+                const float4 x = v[r][j];
+                const float4 xa = make_float4(x.x + a2.x, x.y + a2.y, x.z + a2.z, x.w + a2.w);
+                if (has_a) v[r][j] = xa;
+            }
+        // rows padded by 4 floats so the summing lanes read different banks
+#pragma unroll
+        for (int r = 0; r < RW; r++) {
+            const int t = wave + 4 * r;
+#pragma unroll
+            for (int j = 0; j < PJN; j++) {
+                const int f = lane + 64 * j;
+                if (t < nm && f < nf) {
+                    const float4 x = v[r][j];
+                    reinterpret_cast<float4 *>(sq + (size_t)t * (in_dim + 4))[f] =
+                        make_float4(x.x * x.x, x.y * x.y, x.z * x.z, x.w * x.w);
+                }
+            }
+        }
+        __syncthreads();
+        if (tid < nm)
+            s_inv[tid] = d_rsqrt(d_ss_over_n(serial_sum(sq + (size_t)tid * (in_dim + 4), in_dim), in_dim) + P.eps);
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < RW; r++) {
+            const int t = wave + 4 * r;
+            const float inv = s_inv[t < nm ? t : 0];
+#pragma unroll
+            for (int j = 0; j < PJN; j++) {
+                const int f = lane + 64 * j;
+                const float4 x = v[r][j], w = wn[j];
+                const float4 o = make_float4(x.x * inv * (1.0f + w.x), x.y * inv * (1.0f + w.y),
+                                             x.z * inv * (1.0f + w.z), x.w * inv * (1.0f + w.w));
+                if (writer && t < nm && f < nf) {
+                    if (P.x_out) reinterpret_cast<float4 *>(P.x_out + (size_t)xr[r] * P.src_stride)[f] = x;
+                    if (P.o_out) reinterpret_cast<float4 *>(P.o_out + (size_t)xr[r] * P.o_stride)[f] = o;
+                }
+                v[r][j] = o;
+            }
+        }
+        quant_rows<RW, PJN>(v, wave, lane, nm, nf, nb, in_dim, sx, sxs);
+    }
+}
+
+// One GEMV tile.  xrow[t]: activation row of token slot t (registers);
+// s_orow[t]: output row of token slot t (LDS, read after a barrier); nm:
+// live token slots.  The caller fills the LDS exp table first.
+template <int M, int PJ, int MODES>
+__device__ __forceinline__ void gemv_tile(const int8_t *__restrict__ wt, const float *__restrict__ ws, int rows_here,
+                                          int in_dim, const Prologue &P, const int8_t *__restrict__ xq,
+                                          const float *__restrict__ xqs, const int (&xrow)[M], const int *s_orow,
+                                          int nm, bool writer, float *__restrict__ out, size_t out_stride,
+                                          int row0, int32_t *__restrict__ acc_out, int acc_rows, char *smem,
+                                          float *s_inv, float *tab) {
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int cpr = in_dim >> 4, nb = in_dim >> 5;
+    const int nchunk = rows_here * cpr;
+    int8_t *sx = reinterpret_cast<int8_t *>(smem);                                   // [M][in_dim]
+    float *sxs = reinterpret_cast<float *>(smem + (size_t)M * in_dim);                // [M][nb]
+    int *part = reinterpret_cast<int *>(sxs + M * nb);                                // [R][M][nb+1]
+    // weights: one 8 KiB quarter of the tile per wave, all loads in flight
+    int4 wv[GEMV_MAXJ];
+    const int er = tid / M, et = tid - er * M;
+    float wsv = 0.0f;
+    auto issue_w = [&]() {
+        const v4i *w4 = reinterpret_cast<const v4i *>(wt);
+#pragma unroll
+        for (int j = 0; j < GEMV_MAXJ; j++) {
+            const int c = imin(wave * (GEMV_WAVE_BYTES / 16) + lane + 64 * j, nchunk - 1);
+            const v4i q = __builtin_nontemporal_load(w4 + c);
+            wv[j] = make_int4(q.x, q.y, q.z, q.w);
+        }
+        wsv = ws[row0 + imin(er, rows_here - 1)];     // the epilogue lane's row scale
+    };
+    build_rows<M, PJ, MODES>(P, xq, xqs, in_dim, xrow, nm, writer, sx, sxs, reinterpret_cast<float *>(part), s_inv, tab,
+                      issue_w);
+    __syncthreads();
+    // Partial dot products.  With a power-of-two chunk count per row, lane
+    // l's chunks of every row sit at the same in-row offsets (l + 64v) mod
+    // cpr for v < cpr/64, so each activation chunk is read from LDS once and
+    // reused for all of the lane's weight chunks at that offset.
+    const int4 *sx4 = reinterpret_cast<const int4 *>(sx);
+    auto dot_store = [&](int j, const int4 (&xv)[M]) {
+        const int c = wave * (GEMV_WAVE_BYTES / 16) + lane + 64 * j;
+        const int r = c / cpr, p = c - r * cpr;
+#pragma unroll
+        for (int t = 0; t < M; t++) {
+            int a = __builtin_amdgcn_sdot4(wv[j].x, xv[t].x, 0, false);
+            a = __builtin_amdgcn_sdot4(wv[j].y, xv[t].y, a, false);
+            a = __builtin_amdgcn_sdot4(wv[j].z, xv[t].z, a, false);
+            a = __builtin_amdgcn_sdot4(wv[j].w, xv[t].w, a, false);
+            a += __builtin_amdgcn_update_dpp(0, a, 0xB1, 0xF, 0xF, false);     // lane ^ 1: chunks 2g, 2g+1
+            if (t < nm && c < nchunk && !(lane & 1)) part[(r * M + t) * (nb + 1) + (p >> 1)] = a;
+        }
+    };
+    if ((cpr & (cpr - 1)) == 0 && cpr <= 256) {
+        const int nv = cpr > 64 ? cpr >> 6 : 1;
+#pragma unroll
+        for (int vv = 0; vv < 4; vv++) {
+            if (vv < nv) {
+                const int p = (lane + 64 * vv) & (cpr - 1);
+                int4 xv[M];
+#pragma unroll
+                for (int t = 0; t < M; t++) xv[t] = sx4[(t < nm ? t : 0) * cpr + p];
+#pragma unroll
+                for (int j = 0; j < GEMV_MAXJ; j++)
+                    if ((j & (nv - 1)) == vv) dot_store(j, xv);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < GEMV_MAXJ; j++) {
+            const int c = wave * (GEMV_WAVE_BYTES / 16) + lane + 64 * j;
+            const int p = c - (c / cpr) * cpr;
+            int4 xv[M];
+#pragma unroll
+            for (int t = 0; t < M; t++) xv[t] = sx4[(t < nm ? t : 0) * cpr + p];
+            dot_store(j, xv);
+        }
+    }
+    __syncthreads();
+    if (er < rows_here && et < nm) {
+        const int *pp = part + (er * M + et) * (nb + 1);
+        const float *xs = sxs + et * nb;
+        float dot = 0.0f;
+#pragma unroll 8
+        for (int g = 0; g < nb; g++) dot += (float)pp[g] * xs[g];
+        float sum = 0.0f;
+        sum += dot * wsv;
+        out[(size_t)s_orow[et] * out_stride + row0 + er] = sum;
+        if (acc_out)
+            for (int g = 0; g < nb; g++) acc_out[((size_t)et * acc_rows + row0 + er) * nb + g] = pp[g];
+    }
+}
+
+
+// Rows per GEMV tile: the tile is at most GEMV_TILE_BYTES of weights and
+// R*m (row, token) epilogue pairs fit the block.
+static int gemv_rows_per_tile(int in_dim, int m) {
+    int r = GEMV_TILE_BYTES / in_dim;
+    if (r < 1) r = 1;
+    if (r > GEMV_THREADS / m) r = GEMV_THREADS / m;
+    return r;
+}
+
+static bool prologue_ok(const Prologue &P, int in_dim, const int8_t *xq, const float *xqs) {
+    if (P.mode == PRO_XQ) return xq && xqs;
+    if (in_dim > PRO_MAX_IN || !P.src) return false;
+    if (P.mode == PRO_QUANT) return P.src_stride >= in_dim && !(P.src_stride & 3);
+    if (P.mode == PRO_SILU) return P.src2 && P.src_stride >= in_dim && !(P.src_stride & 3);
+    if (P.mode == PRO_NORM) return P.w && P.src_stride >= in_dim && !(P.src_stride & 3) && !(P.o_stride & 3);
+    if (P.mode == PRO_COMBINE) return P.sel_idx && P.sel_w && P.topk >= 1 && P.topk <= MAX_TOPK;
+    return false;
+}
+
+#endif

@@ -1,0 +1,433 @@
+// Attention kernels against the Q8 KV cache
+// (bit-exact restatement of the reference float-oracle path; see
+// l98_devmath.h for the numeric contract).
+#include "l98_devmath.h"
+
+// ------------------------------------------------------------ attention ---
+
+// One 64-lane block per (token, head): RMSNorm(1+w) of a q head (read from
+// the interleaved [q | gate] projection) or a k head, NeoX rotary on the
+// first rot dims, then q to qh or k quantized per 32 into the KV plane at
+// slot pos; the last nkv blocks of a token quantize v heads.
+// (attn_impl src/forward_attn.c:878-960; lz_rope src/ops_rope.c:21-67.)
+__global__ __launch_bounds__(64) void k_attn_prep(AttnArgs a) {
+    __shared__ __align__(16) float sh[256], sq[256];
+    __shared__ float s_inv;
+    const int nq = a.kv_only ? 0 : a.nh;
+    const int per_tok = nq + 2 * a.nkv;
+    const int t = blockIdx.x / per_tok;
+    const int hh = blockIdx.x - t * per_tok;
+    const int lane = threadIdx.x;
+    const int hd = a.hd, half = a.rot >> 1;
+    const int pos = *a.ctl_pos + a.pos_off + t;
+    if (hh >= nq + a.nkv) {                       // v head: quantize the projection
+        const int h = hh - nq - a.nkv;
+        for (int base = 0; base < hd; base += 64) {
+            int i = base + lane;
+            if (base + (lane & ~31) < hd) {
+                int col = h * hd + i;
+                float v = a.vp[(size_t)t * a.kv_dim + col];
+                d_quant_group32(v, a.vcache + (size_t)pos * a.kv_dim + col,
+                                a.vscale + (size_t)pos * (a.kv_dim >> 5) + (col >> 5));
+            }
+        }
+        return;
+    }
+    const bool isq = hh < nq;
+    const int h = isq ? hh : hh - nq;
+    const float *src = isq ? a.qg + (size_t)t * a.qg_dim + (size_t)h * 2 * hd
+                           : a.kp + (size_t)t * a.kv_dim + (size_t)h * hd;
+    const float *nw = isq ? a.q_norm : a.k_norm;
+    const float *cs = a.rope_cs + (size_t)pos * half * 2;
+    float v[4], w[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int ic = imin(lane + 64 * u, hd - 1);
+        v[u] = src[ic];
+        w[u] = nw[ic];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int i = lane + 64 * u;
+        if (i < hd) { sh[i] = v[u]; sq[i] = v[u] * v[u]; }
+    }
+    __syncthreads();
+    if (lane == 0) s_inv = d_rsqrt(d_ss_over_n(serial_sum(sq, hd), hd) + a.eps);
+    __syncthreads();
+    const float inv = s_inv;
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int i = lane + 64 * u;
+        if (i < hd) sh[i] = v[u] * inv * (1.0f + w[u]);
+    }
+    __syncthreads();
+    for (int i = lane; i < half; i += 64) {
+        float c = cs[i * 2], s = cs[i * 2 + 1];
+        float x0 = sh[i], x1 = sh[i + half];
+        sh[i] = x0 * c - x1 * s;
+        sh[i + half] = x1 * c + x0 * s;
+    }
+    __syncthreads();
+    if (isq) {
+        for (int i = lane; i < hd; i += 64) a.qh[(size_t)t * a.q_dim + (size_t)h * hd + i] = sh[i];
+    } else {
+        for (int base = 0; base < hd; base += 64) {
+            int i = base + lane;
+            if (base + (lane & ~31) < hd) {
+                int col = h * hd + i;
+                d_quant_group32(sh[i], a.kcache + (size_t)pos * a.kv_dim + col,
+                                a.kscale + (size_t)pos * (a.kv_dim >> 5) + (col >> 5));
+            }
+        }
+    }
+}
+
+// Attention of the chunk's tokens against the Q8 KV cache, in two kernels
+// (attn_score_loop Q8 branch, src/forward_attn.c:206-660; score_q8_row
+// :30-41; lz_softmax src/ops_norm.c:903-990; wsum_q8_row :17-21).
+//
+// k_attn_scores: one block per (64-position slice, kv head, token).  The
+// block prepares what it needs itself: the kv_mul q heads of the token
+// (RMSNorm(1+w), NeoX rotary: src/forward_attn.c:878-960, src/ops_rope.c:
+// 21-67) and, for positions of the chunk's own tokens, the K rows from the
+// K projection (norm, rotary, per-32 quantization); every other K row comes
+// from the cache.  The block of token t' whose slice holds t''s position
+// writes t''s K and V rows to the cache, so each new row is written once.
+// One thread per (q head, position) computes the score: each 32-group
+// product sum serial, then the groups serial (score_q8_row order), times
+// attn_scale.  Scores go to att [token][head][position].
+#define ATT_SLICE 64
+#define ATT_MAX_HD 128
+#define ATT_MAX_VEC 24                  // kv_mul q heads + up to MAX_CHUNK new K rows
+
+__global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a, float *__restrict__ att, int att_stride) {
+    __shared__ __align__(16) float s_x[ATT_MAX_VEC * ATT_MAX_HD];     // vectors being prepared
+    __shared__ __align__(16) float s_sq[ATT_MAX_VEC * (ATT_MAX_HD + 4)];
+    __shared__ float s_inv[ATT_MAX_VEC];
+    __shared__ __align__(16) int8_t s_k[ATT_SLICE * (ATT_MAX_HD + 16)];   // K rows, padded
+    __shared__ float s_ks[ATT_SLICE * (ATT_MAX_HD / 32)];
+    const int slice = blockIdx.x, kvh = blockIdx.y, t = blockIdx.z;
+    const int tid = threadIdx.x;
+    const int hd = a.hd, half = a.rot >> 1, kv_mul = a.nh / a.nkv, nb = hd >> 5;
+    const int kstride = hd + 16;
+    const int pos0 = *a.ctl_pos + a.pos_off;
+    const int pos_t = pos0 + t, L = pos_t + 1;
+    const int p_lo = slice * ATT_SLICE;
+    if (p_lo >= L) return;
+    const int n_here = imin(ATT_SLICE, L - p_lo);
+    // new rows of this slice: chunk tokens t' <= t with position in the slice
+    const int nr_lo = imin(imin(t + 1, imax(0, p_lo - pos0)), t + 1);
+    const int nr_hi = imin(t + 1, imax(0, p_lo + n_here - pos0));
+    const int n_new = nr_hi - nr_lo;
+    const int nvec = kv_mul + n_new;
+    const int h0 = kvh * kv_mul;
+    // 1. loads: cached K rows of the slice (p < pos0), the vectors to prepare
+    const int cpr = hd >> 4;
+    const int n_cached = imax(0, imin(n_here, pos0 - p_lo));
+    for (int base = 0; base < ATT_SLICE * cpr; base += 256) {
+        const int idx = base + tid;
+        const int r = idx / cpr, c = idx - r * cpr;
+        if (r < n_cached)
+            *reinterpret_cast<int4 *>(s_k + r * kstride + c * 16) =
+                *reinterpret_cast<const int4 *>(a.kcache + (size_t)(p_lo + r) * a.kv_dim + kvh * hd + c * 16);
+    }
+    for (int idx = tid; idx < n_cached * nb; idx += 256) {
+        const int r = idx / nb, g = idx - r * nb;
+        s_ks[r * nb + g] = a.kscale[(size_t)(p_lo + r) * (a.kv_dim >> 5) + kvh * nb + g];
+    }
+    for (int f = tid; f < nvec * hd; f += 256) {
+        const int v = f / hd, i = f - v * hd;
+        const float x = v < kv_mul ? a.qg[(size_t)t * a.qg_dim + (size_t)(h0 + v) * 2 * hd + i]
+                                   : a.kp[(size_t)(nr_lo + v - kv_mul) * a.kv_dim + kvh * hd + i];
+        s_x[v * hd + i] = x;
+        s_sq[v * (hd + 4) + i] = x * x;
+    }
+    __syncthreads();
+    // 2. RMSNorm sums, one lane per vector (serial, index order)
+    if (tid < nvec) s_inv[tid] = d_rsqrt(d_ss_over_n(serial_sum(s_sq + tid * (hd + 4), hd), hd) + a.eps);
+    __syncthreads();
+    for (int f = tid; f < nvec * hd; f += 256) {
+        const int v = f / hd, i = f - v * hd;
+        const float w = v < kv_mul ? a.q_norm[i] : a.k_norm[i];
+        s_x[v * hd + i] = s_x[v * hd + i] * s_inv[v] * (1.0f + w);
+    }
+    __syncthreads();
+    // 3. rotary on the first rot dims (pairs i, i + half)
+    for (int f = tid; f < nvec * half; f += 256) {
+        const int v = f / half, i = f - v * half;
+        const int pos = v < kv_mul ? pos_t : pos0 + nr_lo + v - kv_mul;
+        const float c = a.rope_cs[((size_t)pos * half + i) * 2], s = a.rope_cs[((size_t)pos * half + i) * 2 + 1];
+        const float x0 = s_x[v * hd + i], x1 = s_x[v * hd + i + half];
+        s_x[v * hd + i] = x0 * c - x1 * s;
+        s_x[v * hd + i + half] = x1 * c + x0 * s;
+    }
+    __syncthreads();
+    // 4. new K rows: per-32 quantization into the slice (and the cache, by the
+    //    token's own block); its V row goes to the cache too.  Groups are 32
+    //    consecutive lanes (hd % 32 == 0, 256 % hd == 0 or hd % 256 == 0).
+    for (int base = 0; base < ATT_MAX_VEC * ATT_MAX_HD; base += 256) {
+        const int f = base + tid;
+        const int nk = n_new * hd;
+        if (base >= nk) break;                       // uniform over the block
+        const int fc = imin(f, nk - 1);
+        const int r = fc / hd, i = fc - r * hd;
+        const int tt = nr_lo + r, p = pos0 + tt;
+        const float y = s_x[(kv_mul + r) * hd + i];
+        int8_t q;
+        float sg;
+        d_quant_group32(y, &q, &sg);
+        if (f < nk) {
+            s_k[(p - p_lo) * kstride + i] = q;
+            if ((i & 31) == 0) s_ks[(p - p_lo) * nb + (i >> 5)] = sg;
+            if (tt == t) {
+                a.kcache[(size_t)p * a.kv_dim + kvh * hd + i] = q;
+                if ((i & 31) == 0) a.kscale[(size_t)p * (a.kv_dim >> 5) + kvh * nb + (i >> 5)] = sg;
+            }
+        }
+        const float vv = a.vp[(size_t)tt * a.kv_dim + kvh * hd + i];
+        int8_t qv;
+        float sv;
+        d_quant_group32(vv, &qv, &sv);
+        if (f < nk && tt == t) {
+            a.vcache[(size_t)p * a.kv_dim + kvh * hd + i] = qv;
+            if ((i & 31) == 0) a.vscale[(size_t)p * (a.kv_dim >> 5) + kvh * nb + (i >> 5)] = sv;
+        }
+    }
+    __syncthreads();
+    // 5. scores: item = (q head g, position) ; a wave shares g
+    const float scale = a.attn_scale;
+    for (int item = tid; item < kv_mul * ATT_SLICE; item += 256) {
+        const int g = item / ATT_SLICE, pl = item - g * ATT_SLICE;
+        if (pl >= n_here) continue;
+        const int8_t *kr = s_k + pl * kstride;
+        const float *ks = s_ks + pl * nb;
+        const float *qq = s_x + g * hd;
+        float sum = 0.0f;
+        for (int dd = 0; dd < hd; dd += 32) {
+            const int4 k0 = *reinterpret_cast<const int4 *>(kr + dd);
+            const int4 k1 = *reinterpret_cast<const int4 *>(kr + dd + 16);
+            const int8_t *kb0 = reinterpret_cast<const int8_t *>(&k0);
+            const int8_t *kb1 = reinterpret_cast<const int8_t *>(&k1);
+            float acc = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc += qq[dd + e] * (float)kb0[e];
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc += qq[dd + 16 + e] * (float)kb1[e];
+            sum += acc * ks[dd >> 5];
+        }
+        att[((size_t)t * a.nh + h0 + g) * att_stride + p_lo + pl] = sum * scale;
+    }
+}
+
+// k_attn_av: one block of 8 waves per (q head, token).  Softmax over the
+// token's scores (max, exp, serial sum, scale), then the value sum
+// out[d] = sum_p a[p] * v[p][d] * vs[p][d/32] walked in position order by
+// one lane per d.  The V rows of up to `sc` positions are staged in LDS
+// with every load in flight; the products (a*v)*vs of 64 positions at a
+// time are formed by the producer waves into a double buffer [d][64] while
+// the consumer lanes (hd/64 waves) add the previous 64 in order, so the
+// consumer's loop is one LDS read per four adds.  Then the sigmoid output
+// gate and the per-32 quantization of the head's output (the o_proj input).
+#define AV_CH 64
+#define AV_PAD 68                        // floats per d row of the product buffer (bank spread)
+
+// Stages V rows [p0, p0 + n) of kv head kvh (hd int8 + hd/32 scales each)
+// into LDS with every load of the block in flight before the first store
+// (n * hd / 16 <= AV_THREADS * AV_STAGE_MAX).
+#define AV_THREADS 512
+#define AV_STAGE_MAX 16
+__device__ __forceinline__ void av_stage(const int8_t *__restrict__ vc, const float *__restrict__ vs, int kv_dim,
+                                         int kvh, int hd, int p0, int n, int8_t *s_v, float *s_vs) {
+    const int tid = threadIdx.x, cpr = hd >> 4, nb = hd >> 5;
+    const int total = n * cpr, stotal = n * nb;
+    int4 r[AV_STAGE_MAX];
+    float q[AV_STAGE_MAX / 2];
+#pragma unroll
+    for (int u = 0; u < AV_STAGE_MAX; u++) {
+        const int idx = imin(u * AV_THREADS + tid, total - 1);
+        const int row = idx / cpr, c = idx - row * cpr;
+        r[u] = *reinterpret_cast<const int4 *>(vc + (size_t)(p0 + row) * kv_dim + kvh * hd + c * 16);
+    }
+#pragma unroll
+    for (int u = 0; u < AV_STAGE_MAX / 2; u++) {
+        const int sidx = imin(u * AV_THREADS + tid, stotal - 1);
+        const int srow = sidx / nb, g = sidx - srow * nb;
+        q[u] = vs[(size_t)(p0 + srow) * (kv_dim >> 5) + kvh * nb + g];
+    }
+#pragma unroll
+    for (int u = 0; u < AV_STAGE_MAX; u++)
+        if (u * AV_THREADS < total) reinterpret_cast<int4 *>(s_v)[imin(u * AV_THREADS + tid, total - 1)] = r[u];
+#pragma unroll
+    for (int u = 0; u < AV_STAGE_MAX / 2; u++)
+        if (u * AV_THREADS < stotal) s_vs[imin(u * AV_THREADS + tid, stotal - 1)] = q[u];
+}
+
+__global__ __launch_bounds__(AV_THREADS) void k_attn_av(AttnArgs a, const float *__restrict__ att, int att_stride,
+                                                 int sc) {
+    EXP_TAB_LOAD(tab);
+    extern __shared__ __align__(16) char smem[];
+    __shared__ uint32_t s_red[AV_THREADS / 64];
+    __shared__ float s_inv;
+    const int h = blockIdx.x, t = blockIdx.y;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int hd = a.hd, nb = hd >> 5, kv_mul = a.nh / a.nkv, kvh = h / kv_mul;
+    const int pos_t = *a.ctl_pos + a.pos_off + t, L = pos_t + 1;
+    const int Lp = (att_stride + 3) & ~3;
+    float *s_a = reinterpret_cast<float *>(smem);                                   // [Lp]
+    float *prod = s_a + Lp;                                                          // [2][hd][AV_PAD]
+    int8_t *s_v = reinterpret_cast<int8_t *>(prod + 2 * hd * AV_PAD);               // [sc][hd]
+    float *s_vs = reinterpret_cast<float *>(s_v + (size_t)sc * hd);                  // [sc][nb]
+    const float *arow = att + ((size_t)t * a.nh + h) * att_stride;
+    const int cpr = hd >> 4;
+    // scores -> LDS, then the V stage (its loads wait behind the score loads)
+    for (int p = tid; p < L; p += AV_THREADS) s_a[p] = arow[p];
+    av_stage(a.vcache, a.vscale, a.kv_dim, kvh, hd, 0, imin(sc, L), s_v, s_vs);
+    EXP_TAB_PUT(tab);
+    __syncthreads();
+    // softmax: max (order-preserving key), exp, serial sum, scale
+    uint32_t best = 0;
+    for (int p = tid; p < L; p += AV_THREADS) best = umax(best, d_fkey(s_a[p]));
+    for (int o = 32; o > 0; o >>= 1) best = umax(best, (uint32_t)__shfl_xor((int)best, o));
+    if (lane == 0) s_red[wave] = best;
+    __syncthreads();
+    uint32_t bk = s_red[0];
+#pragma unroll
+    for (int w = 1; w < AV_THREADS / 64; w++) bk = umax(bk, s_red[w]);
+    const float mx = d_unkey(bk);
+    for (int p = tid; p < L; p += AV_THREADS) s_a[p] = d_exp(s_a[p] - mx, tab);
+    __syncthreads();
+    if (tid == 0) {
+        const float sum = serial_sum(s_a, L);
+        s_inv = (sum > 0.0f) ? 1.0f / sum : 0.0f;
+    }
+    __syncthreads();
+    const float inv = s_inv;
+    for (int p = tid; p < L; p += AV_THREADS) s_a[p] *= inv;
+    __syncthreads();
+    // value sum
+    const int ncons = (hd + 63) >> 6;              // consumer waves
+    const bool cons = wave < ncons;
+    const int d = wave * 64 + lane;
+    const int nprod = AV_THREADS - ncons * 64, ptid = tid - ncons * 64;
+    float o = 0.0f;
+    // products of chunk positions [q0, q0 + AV_CH) of the staged range starting at sp0
+    auto produce = [&](int q0, int sp0, int nsc, int buf) {
+        float *pb = prod + (size_t)buf * hd * AV_PAD;
+        for (int u = ptid; u < AV_CH * cpr; u += nprod) {
+            const int pl = u / cpr, seg = u - pl * cpr;
+            const int p = q0 + pl;                   // absolute position
+            const int ls = p - sp0;                  // row in the stage
+            // rows past the staged range use row 0 with a = 0: the product
+            // is +-0, and adding +-0 leaves the sum unchanged
+            const bool live = ls < nsc;
+            const int4 v4 = reinterpret_cast<const int4 *>(s_v)[(live ? ls : 0) * cpr + seg];
+            const float ap = live ? s_a[p] : 0.0f, vsc = s_vs[(live ? ls : 0) * nb + (seg >> 1)];
+            const int vw[4] = {v4.x, v4.y, v4.z, v4.w};
+            float pr[16];
+#pragma unroll
+            for (int i = 0; i < 16; i++) pr[i] = ap * (float)(int8_t)((vw[i >> 2] >> (8 * (i & 3))) & 0xFF) * vsc;
+#pragma unroll
+            for (int i = 0; i < 16; i++) pb[(seg * 16 + i) * AV_PAD + pl] = pr[i];
+        }
+    };
+    for (int sp0 = 0; sp0 < L; sp0 += sc) {
+        const int nsc = imin(sc, L - sp0);
+        if (sp0 > 0) {
+            __syncthreads();
+            av_stage(a.vcache, a.vscale, a.kv_dim, kvh, hd, sp0, nsc, s_v, s_vs);
+            __syncthreads();
+        }
+        const int nch = (nsc + AV_CH - 1) / AV_CH;
+        if (!cons) produce(sp0, sp0, nsc, 0);
+        __syncthreads();
+        for (int c = 0; c < nch; c++) {
+            if (cons) {
+                if (d < hd) {
+                    const float *pr = prod + (size_t)(c & 1) * hd * AV_PAD + (size_t)d * AV_PAD;
+#pragma unroll
+                    for (int i = 0; i < AV_CH; i += 4) {
+                        const float4 q = *reinterpret_cast<const float4 *>(pr + i);
+                        o += q.x; o += q.y; o += q.z; o += q.w;
+                    }
+                }
+            } else if (c + 1 < nch) {
+                produce(sp0 + (c + 1) * AV_CH, sp0, nsc, (c + 1) & 1);
+            }
+            __syncthreads();
+        }
+    }
+    if (cons) {
+        const int dc = d < hd ? d : hd - 1;
+        const float gate = a.qg[(size_t)t * a.qg_dim + (size_t)h * 2 * hd + hd + dc];
+        o *= d_sigmoid(gate, tab);
+        const int col = h * hd + dc;
+        if (a.out && d < hd) a.out[(size_t)t * a.q_dim + col] = o;
+        int8_t q;
+        float sg;
+        d_quant_group32(o, &q, &sg);
+        if (d < hd) {
+            a.oq[(size_t)t * a.q_dim + col] = q;
+            if ((dc & 31) == 0) a.oqs[(size_t)t * (a.q_dim >> 5) + (col >> 5)] = sg;
+        }
+    }
+}
+
+// ---------------------------------------------------------- host glue ---
+
+extern "C" int l98k_upload_exp_table_attn(const float *tab) {
+    return (int)hipMemcpyToSymbol(HIP_SYMBOL(c_exp_tab), tab, 32 * sizeof(float));
+}
+
+extern "C" int l98k_attn_prep(const AttnArgs *a, int nt, hipStream_t st) {
+    if (a->hd > 256 || (a->hd & 31) || a->rot > a->hd || nt < 1) return -1;
+    const int per_tok = (a->kv_only ? 0 : a->nh) + 2 * a->nkv;
+    hipLaunchKernelGGL(k_attn_prep, dim3(nt * per_tok), dim3(64), 0, st, *a);
+    return (int)hipGetLastError();
+}
+
+// Largest dynamic LDS a block may use on this device (queried once).
+static int lds_limit() {
+    static int lim = 0;
+    if (!lim) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0)
+            v = 64 * 1024;
+        lim = v;
+    }
+    return lim;
+}
+
+extern "C" int l98k_attn(const AttnArgs *a, int nt, int max_len, float *att, hipStream_t st) {
+    if (a->nkv < 1 || a->nh % a->nkv || (a->hd & 31) || a->hd > ATT_MAX_HD || a->rot > a->hd || (a->rot & 1) ||
+        nt < 1 || nt > MAX_CHUNK || max_len < 1 || !a->oq || !a->oqs || !att)
+        return -1;
+    const int kv_mul = a->nh / a->nkv;
+    if (kv_mul + MAX_CHUNK > ATT_MAX_VEC) return -1;
+    const int att_stride = (max_len + 3) & ~3;
+    const int slices = (max_len + ATT_SLICE - 1) / ATT_SLICE;
+    hipLaunchKernelGGL(k_attn_scores, dim3(slices, a->nkv, nt), dim3(256), 0, st, *a, att, att_stride);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+    // value-sum kernel: scores, the product double buffer, then as many
+    // staged V positions (multiple of 64) as the LDS limit leaves
+    const int hd = a->hd;
+    const size_t fixed = ((size_t)att_stride + 2 * (size_t)hd * AV_PAD) * sizeof(float);
+    const size_t per_pos = (size_t)hd + (size_t)(hd >> 5) * sizeof(float);
+    const int lim = lds_limit() - 1024;          // the kernel's static LDS (exp table, reductions) fits in the rest
+    if (fixed + AV_CH * per_pos > (size_t)lim) return -1;
+    int sc = (int)(((size_t)lim - fixed) / per_pos) & ~(AV_CH - 1);
+    const int need = (max_len + AV_CH - 1) & ~(AV_CH - 1);
+    if (sc > need) sc = need;
+    const int sc_regs = (AV_THREADS * AV_STAGE_MAX / (hd >> 4)) & ~(AV_CH - 1);   // one register-staged pass
+    if (sc > sc_regs) sc = sc_regs;
+    const size_t lds = fixed + (size_t)sc * per_pos;
+    static bool attr_set = false;
+    if (!attr_set) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k_attn_av),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, lim);
+        attr_set = true;
+    }
+    hipLaunchKernelGGL(k_attn_av, dim3(a->nh, nt), dim3(AV_THREADS), lds, st, *a, att, att_stride, sc);
+    return (int)hipGetLastError();
+}
+

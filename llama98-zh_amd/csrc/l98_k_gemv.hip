@@ -1,0 +1,94 @@
+// Dense fused int8 GEMV kernels of the MTP speculative-decoding step
+// (bit-exact restatement of the reference float-oracle path; see
+// l98_devmath.h for the numeric contract).
+#include "l98_gemv.h"
+
+// One launch over b.n jobs; m <= M live token rows (M a power of two).
+template <int M, int PJ, int MODES>
+__global__ __launch_bounds__(GEMV_THREADS) void k_gemv_q8(GemvBatch batch, int m) {
+    extern __shared__ __align__(16) char smem[];
+    __shared__ int s_row[M];
+    __shared__ float s_inv[M], tab[32];
+    int blk = blockIdx.x, j = 0;
+    while (j + 1 < batch.n && blk >= batch.job[j + 1].tile0) j++;
+    const GemvJob &job = batch.job[j];
+    const int row0 = (blk - job.tile0) * job.R;
+    const int rows_here = imin(job.R, job.rows - row0);
+    if (threadIdx.x < M) s_row[threadIdx.x] = threadIdx.x < m ? threadIdx.x : 0;
+    int xrow[M];
+#pragma unroll
+    for (int t = 0; t < M; t++) xrow[t] = t < m ? t : 0;
+    gemv_tile<M, PJ, MODES>(job.w + (size_t)row0 * job.in_dim, job.ws, rows_here, job.in_dim, job.pro, job.xq,
+                            job.xqs, xrow, s_row, m, blk == 0, job.out, job.out_stride, row0, job.acc_out, job.rows,
+                            smem, s_inv, tab);
+}
+
+// ---------------------------------------------------------- host glue ---
+
+extern "C" int l98k_upload_exp_table_gemv(const float *tab) {
+    return (int)hipMemcpyToSymbol(HIP_SYMBOL(c_exp_tab), tab, 32 * sizeof(float));
+}
+
+// Instances: token slots M in {1, 2, 4, 8}; prologue sets: pre-quantized
+// (PJ 0), RMSNorm (PJ 1..8), SiLU-mul (PJ 1..4), combine + SiLU-mul
+// (PJ 1..4).
+#define GEMV_CASE(M_, PJ_, MODES_)                                                                         \
+    case (M_) * 1000 + (PJ_) * 100 + (MODES_):                                                            \
+        hipLaunchKernelGGL((k_gemv_q8<M_, PJ_, MODES_>), dim3(tiles), dim3(GEMV_THREADS), lds, st, *b, m); \
+        break;
+#define GEMV_CASES_M(M_)                                                                   \
+    GEMV_CASE(M_, 0, MODES_X)                                                              \
+    GEMV_CASE(M_, 1, MODES_N) GEMV_CASE(M_, 2, MODES_N) GEMV_CASE(M_, 4, MODES_N) GEMV_CASE(M_, 8, MODES_N) \
+    GEMV_CASE(M_, 1, MODES_S) GEMV_CASE(M_, 2, MODES_S) GEMV_CASE(M_, 4, MODES_S)          \
+    GEMV_CASE(M_, 1, MODES_CS) GEMV_CASE(M_, 2, MODES_CS) GEMV_CASE(M_, 4, MODES_CS)
+
+// Checks every job's prologue against the kernel's limits, lays the jobs'
+// tiles out in one grid and launches the instance for the jobs' prologue
+// set (pre-quantized, RMSNorm, SiLU-mul, or combine + SiLU-mul).
+extern "C" int l98k_gemv(GemvBatch *b, int m, hipStream_t st) {
+    if (m < 1 || m > MAX_CHUNK || b->n < 1 || b->n > MAX_GEMV_JOBS) return -1;
+    const int M = m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8;
+    int tiles = 0, pj = 0, modes = 0;
+    size_t lds = 0;
+    for (int j = 0; j < b->n; j++) {
+        GemvJob &J = b->job[j];
+        if (J.in_dim < 32 || (J.in_dim & 31) || J.in_dim > GEMV_MAX_IN || J.rows < 1 ||
+            !prologue_ok(J.pro, J.in_dim, J.xq, J.xqs))
+            return -1;
+        J.R = gemv_rows_per_tile(J.in_dim, M);
+        J.tile0 = tiles;
+        tiles += (J.rows + J.R - 1) / J.R;
+        size_t l = gemv_lds_bytes(M, J.in_dim, J.R, J.pro.mode == PRO_NORM);
+        lds = l > lds ? l : lds;
+        modes |= MB(J.pro.mode);
+        if (J.pro.mode != PRO_XQ) pj = pro_pj(J.in_dim) > pj ? pro_pj(J.in_dim) : pj;
+    }
+    if (lds > 64 * 1024) return -1;
+    if (modes == MODES_X) pj = 0;
+    else if (modes == MB(PRO_COMBINE)) modes = MODES_CS;
+    else if (modes != MODES_N && modes != MODES_S && modes != MODES_CS) return -1;
+    switch (M * 1000 + pj * 100 + modes) {
+        GEMV_CASES_M(1)
+        GEMV_CASES_M(2)
+        GEMV_CASES_M(4)
+        GEMV_CASES_M(8)
+    default:
+        return -1;
+    }
+    return (int)hipGetLastError();
+}
+
+// Tiles of a GEMV over `rows` rows of in_dim with m token rows.
+extern "C" int l98k_gemv_tiles(int rows, int in_dim, int m) {
+    const int R = gemv_rows_per_tile(in_dim, m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8);
+    return (rows + R - 1) / R;
+}
+
+// Whether a GEMV over m rows of width in_dim with a fused RMSNorm prologue
+// fits the kernel's LDS.
+extern "C" int l98k_gemv_norm_fits(int in_dim, int m) {
+    if (in_dim > PRO_MAX_IN || m < 1 || m > MAX_CHUNK) return 0;
+    const int M = m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8;
+    return gemv_lds_bytes(M, in_dim, gemv_rows_per_tile(in_dim, M), 1) <= 64 * 1024;
+}
+

@@ -1,0 +1,288 @@
+// Row kernels (embedding, RMSNorm, MTP input), argmax and round control
+// (bit-exact restatement of the reference float-oracle path; see
+// l98_devmath.h for the numeric contract).
+#include "l98_devmath.h"
+
+// -------------------------------------------------------------- embed ---
+
+// lz_t_row_f32 for a Q8_0 per-row table: x = float(q) * scale[row].
+__global__ void k_embed(const int8_t *__restrict__ q, const float *__restrict__ s,
+                        const int *__restrict__ toks, int d, float *__restrict__ x) {
+    int t = blockIdx.y;
+    int tok = toks[t];
+    const int8_t *row = q + (size_t)tok * d;
+    float sc = s[tok];
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < d; i += gridDim.x * blockDim.x)
+        x[(size_t)t * d + i] = (float)row[i] * sc;
+}
+
+template <int PJ>
+__global__ __launch_bounds__(64) void k_rmsnorm(float *__restrict__ x, int x_stride,
+                                                const float *__restrict__ a, const float *__restrict__ b,
+                                                const float *__restrict__ w, int n, float eps,
+                                                float *__restrict__ out, int out_stride,
+                                                int8_t *__restrict__ xq, float *__restrict__ xqs) {
+    __shared__ __align__(16) float sq[256 * PJ];
+    __shared__ float s_inv;
+    const int row = blockIdx.x, lane = threadIdx.x, nf = n >> 2;
+    float4 *xr = reinterpret_cast<float4 *>(x + (size_t)row * x_stride);
+    float4 v[PJ], wn[PJ];
+#pragma unroll
+    for (int j = 0; j < PJ; j++) {
+        const int fc = imin(lane + 64 * j, nf - 1);
+        v[j] = xr[fc];
+        wn[j] = reinterpret_cast<const float4 *>(w)[fc];
+    }
+    if (a) {
+        float4 av[PJ];
+#pragma unroll
+        for (int j = 0; j < PJ; j++) av[j] = reinterpret_cast<const float4 *>(a + (size_t)row * n)[imin(lane + 64 * j, nf - 1)];
+        if (b) {
+#pragma unroll
+            for (int j = 0; j < PJ; j++) {
+                const float4 bv = reinterpret_cast<const float4 *>(b + (size_t)row * n)[imin(lane + 64 * j, nf - 1)];
+                av[j] = make_float4(av[j].x + bv.x, av[j].y + bv.y, av[j].z + bv.z, av[j].w + bv.w);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < PJ; j++) {
+            v[j] = make_float4(v[j].x + av[j].x, v[j].y + av[j].y, v[j].z + av[j].z, v[j].w + av[j].w);
+            if (lane + 64 * j < nf) xr[lane + 64 * j] = v[j];
+        }
+    }
+    norm_row<PJ>(v, wn, n, eps, sq, &s_inv, out ? out + (size_t)row * out_stride : nullptr,
+                 xq ? xq + (size_t)row * n : nullptr, xqs ? xqs + (size_t)row * (n >> 5) : nullptr);
+}
+
+// MTP input rows (lz_mtp_draft_step / lz_mtp_prefill, src/forward_mtp.c:
+// e = embed(tok); concat = [rmsnorm(e, pre_e) | rmsnorm(h, pre_h)], then the
+// per-32 quantization of concat for the fc projection).  blockIdx.y = 0: the
+// embedding half, 1: the hidden half.  d % 32 == 0, so the halves quantize
+// independently.
+template <int PJ>
+__global__ __launch_bounds__(64) void k_mtp_pre(const int8_t *__restrict__ emb_q, const float *__restrict__ emb_s,
+                                                const int *__restrict__ toks, const float *__restrict__ h,
+                                                int d, const float *__restrict__ w_e,
+                                                const float *__restrict__ w_h, float eps,
+                                                int8_t *__restrict__ xq, float *__restrict__ xqs) {
+    __shared__ __align__(16) float sq[256 * PJ];
+    __shared__ float s_inv;
+    const int r = blockIdx.x, half = blockIdx.y, lane = threadIdx.x, nf = d >> 2;
+    const float4 *wn4 = reinterpret_cast<const float4 *>(half == 0 ? w_e : w_h);
+    float4 v[PJ], wn[PJ];
+    if (half == 0) {
+        const int tok = toks[r];
+        const uint32_t *er = reinterpret_cast<const uint32_t *>(emb_q + (size_t)tok * d);
+        const float sc = emb_s[tok];
+#pragma unroll
+        for (int j = 0; j < PJ; j++) {
+            const uint32_t q = er[imin(lane + 64 * j, nf - 1)];
+            v[j] = make_float4((float)(int8_t)(q & 0xFF) * sc, (float)(int8_t)((q >> 8) & 0xFF) * sc,
+                               (float)(int8_t)((q >> 16) & 0xFF) * sc, (float)(int8_t)(q >> 24) * sc);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < PJ; j++) v[j] = reinterpret_cast<const float4 *>(h + (size_t)r * d)[imin(lane + 64 * j, nf - 1)];
+    }
+#pragma unroll
+    for (int j = 0; j < PJ; j++) wn[j] = wn4[imin(lane + 64 * j, nf - 1)];
+    norm_row<PJ>(v, wn, d, eps, sq, &s_inv, nullptr, xq + (size_t)r * 2 * d + (size_t)half * d,
+                 xqs + (size_t)r * (2 * d >> 5) + (size_t)half * (d >> 5));
+}
+
+// -------------------------------------------------------- argmax / ctl ---
+
+#define ARGMAX_BLOCKS 64
+#define LZ_ARGMAX_ROWS 8
+
+// Per row argmax, ARGMAX_BLOCKS blocks per row; the last block to finish a
+// row reduces the partials and resets the row's counter (so the kernel can
+// be replayed from a graph).  mode 0: order-preserving key, first index wins
+// (sample_argmax, src/sampler.c:121-137).  mode 1: float '>' compare, first
+// index wins (lz_argmax_p1's scan, src/sampler.c:139-155).
+__global__ __launch_bounds__(256) void k_argmax(const float *__restrict__ x, int n, int mode,
+                                                unsigned long long *__restrict__ partial,
+                                                unsigned *__restrict__ counter, int *__restrict__ out) {
+    const int row = blockIdx.y, nb = gridDim.x;
+    const float *r = x + (size_t)row * n;
+    const int seg = (n + nb - 1) / nb;
+    const int lo = blockIdx.x * seg, hi = lo + seg < n ? lo + seg : n;
+    unsigned long long best = 0;
+    for (int i = lo + threadIdx.x; i < hi; i += blockDim.x) {
+        float v = r[i];
+        uint32_t k;
+        if (mode == 0) k = d_fkey(v);
+        else k = (v != v) ? 0u : d_fkey(v == 0.0f ? 0.0f : v);
+        unsigned long long cand = ((unsigned long long)k << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)i);
+        best = cand > best ? cand : best;
+    }
+    best = wave_max_u64(best);
+    __shared__ unsigned long long sb[4];
+    __shared__ bool s_last;
+    if ((threadIdx.x & 63) == 0) sb[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long b = 0;
+        for (int i = 0; i < (int)(blockDim.x >> 6); i++) b = sb[i] > b ? sb[i] : b;
+        partial[(size_t)row * nb + blockIdx.x] = b;
+        __threadfence();
+        unsigned prev = atomicAdd(&counter[row], 1u);
+        s_last = (prev == (unsigned)nb - 1);
+    }
+    __syncthreads();
+    if (s_last) {
+        __threadfence();
+        unsigned long long b = 0;
+        for (int i = threadIdx.x; i < nb; i += blockDim.x) {
+            unsigned long long p = __atomic_load_n(&partial[(size_t)row * nb + i], __ATOMIC_RELAXED);
+            b = p > b ? p : b;
+        }
+        b = wave_max_u64(b);
+        if ((threadIdx.x & 63) == 0) sb[threadIdx.x >> 6] = b;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            unsigned long long bb = 0;
+            for (int i = 0; i < (int)(blockDim.x >> 6); i++) bb = sb[i] > bb ? sb[i] : bb;
+            out[row] = (int)(0xFFFFFFFFu - (uint32_t)(bb & 0xFFFFFFFFu));
+            counter[row] = 0;
+        }
+    }
+}
+
+// Acceptance of a greedy round (lz_spec_accept, src/generate.c:232-243) and
+// the device-side bookkeeping of lz_spec_round (src/generate.c:802-993):
+// ring rollback, mtp_chain reseed from the accepted row, catch-up count,
+// next anchor and positions.
+__global__ void k_accept(DevCtl *ctl, const float *__restrict__ vhidden, int d,
+                         float *__restrict__ chain, int depth, int brk) {
+    __shared__ int s_n;
+    if (threadIdx.x == 0) {
+        int k_eff = ctl->k_eff;
+        int n = k_eff;
+        for (int i = 0; i < k_eff; i++) {
+            ctl->out[i] = ctl->targ[i];
+            if (ctl->tok[1 + i] != ctl->targ[i]) { n = i; break; }
+        }
+        if (n == k_eff) ctl->out[k_eff] = ctl->targ[k_eff];
+        ctl->n_accept = n;
+        int base = ctl->slot_base;
+        int slot = (base + k_eff + 1) % depth;           // what the verify left
+        if (n < k_eff && !brk) slot = (base + n + 1) % depth;
+        ctl->ssm_slot = slot;
+        ctl->new_pos = ctl->anchor_pos + 1 + n;
+        // catch-up pairs (verify_hidden[j], out[j]) j < n-1 at mtp_pos+1+j
+        ctl->catch_n = n > 1 ? n - 1 : 0;
+        ctl->catch_pos = ctl->mtp_pos + 1;
+        // Catch-up always runs k-1 rows so a round has a fixed shape; rows
+        // j >= catch_n land at MTP positions >= the next round's mtp_pos,
+        // which that round's draft steps overwrite before any read.
+        for (int j = 0; j < 8; j++) ctl->catch_tok[j] = j < ctl->catch_n ? ctl->out[j] : ctl->out[0];
+        ctl->mtp_pos_next = ctl->mtp_pos + n;
+        s_n = n;
+    }
+    __syncthreads();
+    const int n = s_n;
+    for (int i = threadIdx.x; i < d; i += blockDim.x) chain[i] = vhidden[(size_t)n * d + i];
+}
+
+// Round bookkeeping on the device.  op 0: draft input 0 = anchor.  op 1:
+// record the finished round in hist and advance to the next one as the
+// generation driver does with have_seed (src/generate.c:1850-1866,
+// 2096-2104): anchor = out[n_accept] at position new_pos, mtp_pos and the
+// ring slot carried over.
+__global__ void k_set_tokens(DevCtl *ctl, int op, RoundRec *hist, int hist_cap) {
+    if (threadIdx.x != 0) return;
+    if (op == 0) {
+        ctl->tok[0] = ctl->anchor;
+    } else if (op == 1) {
+        if (hist && ctl->round < hist_cap) {
+            RoundRec *r = hist + ctl->round;
+            r->n_accept = ctl->n_accept;
+            r->k_eff = ctl->k_eff;
+            r->new_pos = ctl->new_pos;
+            r->ssm_slot = ctl->ssm_slot;
+            r->experts = ctl->expert_tally;
+            for (int j = 0; j < 8; j++) r->out[j] = ctl->out[j];
+        }
+        ctl->expert_tally = 0;
+        ctl->round++;
+        ctl->anchor = ctl->out[ctl->n_accept];
+        ctl->anchor_pos = ctl->new_pos;
+        ctl->mtp_pos = ctl->mtp_pos_next;
+        ctl->slot_base = ctl->ssm_slot;
+        ctl->tok[0] = ctl->anchor;
+    }
+}
+
+// ---------------------------------------------------------- host glue ---
+
+extern "C" int l98k_upload_exp_table_misc(const float *tab) {
+    return (int)hipMemcpyToSymbol(HIP_SYMBOL(c_exp_tab), tab, 32 * sizeof(float));
+}
+
+extern "C" int l98k_upload_exp_table(const float *tab) {
+    int e;
+    if ((e = l98k_upload_exp_table_misc(tab)) != 0) return e;
+    if ((e = l98k_upload_exp_table_gemv(tab)) != 0) return e;
+    if ((e = l98k_upload_exp_table_moe(tab)) != 0) return e;
+    if ((e = l98k_upload_exp_table_kda(tab)) != 0) return e;
+    return l98k_upload_exp_table_attn(tab);
+}
+
+extern "C" int l98k_embed(const int8_t *q, const float *s, const int *toks, int d, int nt,
+                          float *x, hipStream_t st) {
+    hipLaunchKernelGGL(k_embed, dim3((d + 255) / 256, nt), dim3(256), 0, st, q, s, toks, d, x);
+    return (int)hipGetLastError();
+}
+
+#define NORM_CASES(X) X(1) X(2) X(4) X(8)
+
+extern "C" int l98k_rmsnorm(float *x, int x_stride, const float *a, const float *b, const float *w,
+                            int n, float eps, int rows, float *out, int out_stride, int8_t *xq,
+                            float *xqs, hipStream_t st) {
+    if (n < 32 || n > 256 * 8 || (n & 31) || (x_stride & 3) || (out && (out_stride & 3)) || rows < 1) return -1;
+#define NORM_LAUNCH(PJ)                                                                          \
+    if (n <= 256 * PJ) {                                                                         \
+        hipLaunchKernelGGL(k_rmsnorm<PJ>, dim3(rows), dim3(64), 0, st, x, x_stride, a, b, w, n, \
+                           eps, out, out_stride, xq, xqs);                                       \
+        return (int)hipGetLastError();                                                           \
+    }
+    NORM_CASES(NORM_LAUNCH)
+#undef NORM_LAUNCH
+    return -1;
+}
+
+extern "C" int l98k_mtp_pre(const int8_t *emb_q, const float *emb_s, const int *toks, const float *h, int d,
+                            const float *w_e, const float *w_h, float eps, int rows, int8_t *xq, float *xqs,
+                            hipStream_t st) {
+    if (d < 32 || d > 256 * 8 || (d & 31) || rows < 1) return -1;
+#define PRE_LAUNCH(PJ)                                                                                  \
+    if (d <= 256 * PJ) {                                                                                \
+        hipLaunchKernelGGL(k_mtp_pre<PJ>, dim3(rows, 2), dim3(64), 0, st, emb_q, emb_s, toks, h, d, w_e, \
+                           w_h, eps, xq, xqs);                                                          \
+        return (int)hipGetLastError();                                                                  \
+    }
+    NORM_CASES(PRE_LAUNCH)
+#undef PRE_LAUNCH
+    return -1;
+}
+
+extern "C" int l98k_argmax(const float *x, int n, int rows, int mode, int *out,
+                           unsigned long long *partial, unsigned *counter, hipStream_t st) {
+    if (rows < 1 || rows > LZ_ARGMAX_ROWS || n < 1) return -1;
+    hipLaunchKernelGGL(k_argmax, dim3(ARGMAX_BLOCKS, rows), dim3(256), 0, st, x, n, mode, partial,
+                       counter, out);
+    return (int)hipGetLastError();
+}
+
+extern "C" int l98k_accept(DevCtl *ctl, const float *vhidden, int d, float *chain, int depth,
+                           int brk, hipStream_t st) {
+    hipLaunchKernelGGL(k_accept, dim3(1), dim3(256), 0, st, ctl, vhidden, d, chain, depth, brk);
+    return (int)hipGetLastError();
+}
+
+extern "C" int l98k_set_tokens(DevCtl *ctl, int op, RoundRec *hist, int hist_cap, hipStream_t st) {
+    hipLaunchKernelGGL(k_set_tokens, dim3(1), dim3(64), 0, st, ctl, op, hist, hist_cap);
+    return (int)hipGetLastError();
+}
+

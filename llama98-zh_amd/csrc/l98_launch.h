@@ -9,6 +9,12 @@
 
 extern "C" {
 int l98k_upload_exp_table(const float *tab);
+// per translation unit (l98k_upload_exp_table runs all of them)
+int l98k_upload_exp_table_misc(const float *tab);
+int l98k_upload_exp_table_gemv(const float *tab);
+int l98k_upload_exp_table_moe(const float *tab);
+int l98k_upload_exp_table_kda(const float *tab);
+int l98k_upload_exp_table_attn(const float *tab);
 // Fused GEMV of b->n jobs over m <= MAX_CHUNK activation rows; each job's
 // prologue builds its int8 input rows.
 int l98k_gemv(GemvBatch *b, int m, hipStream_t st);
@@ -25,11 +31,9 @@ int l98k_rmsnorm(float *x, int x_stride, const float *a, const float *b, const f
 int l98k_mtp_pre(const int8_t *emb_q, const float *emb_s, const int *toks, const float *h, int d,
                  const float *w_e, const float *w_h, float eps, int rows, int8_t *xq, float *xqs,
                  hipStream_t st);
-// Causal conv + SiLU over [q|k|v] with the ring state.
-int l98k_kda_conv(const float *pq, const float *pk, const float *pv, int key, int value, const float *wconv,
-                  float *ring, size_t slot_stride, int K, const int *ctl_slot, int depth, int advance, int nt,
-                  float *qc, float *kc, float *vc, hipStream_t st);
-int l98k_kda_recur(const KdaRecurArgs *a, int kd, int vd, hipStream_t st);
+// One KDA layer step for a chunk: conv, gate up-projection, recurrence,
+// gated norm and o_proj quantization (kd in {32, 64, 128}, conv taps K in 2..4).
+int l98k_kda_step(const KdaStepArgs *a, int kd, int K, hipStream_t st);
 int l98k_attn_prep(const AttnArgs *a, int nt, hipStream_t st);
 // Attention of nt tokens (positions *ctl_pos + pos_off + t) against the KV
 // plane: scores with the q/k preparation and the chunk's own K/V cache rows,
