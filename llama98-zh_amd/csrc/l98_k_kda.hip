@@ -5,13 +5,14 @@
 
 // ---------------------------------------------------------- KDA layer ---
 //
-// One block per head (nk == nv); lane j owns q/k channel j of the head, v
-// channel j, and column j of the fp32 state S[kd][vd] (registers).  For the
-// chunk's tokens, in one launch:
-//   * the depthwise causal conv + SiLU of the lane's q, k and v channels
-//     along the ring (lz_causal_conv1d_step, src/ops_conv1d.c:26-87: taps
-//     summed in order, then the current input; ring slots
-//     src/forward_kda.c:680-755);
+// One block of 4*kd threads per head (nk == nv).  Channel phases use thread
+// j < kd for q/k channel j and v channel j of the head; the recurrence uses
+// a lane quad per state column: thread 4c + r holds rows [r*kd/4, (r+1)*kd/4)
+// of column c of the fp32 state S[kd][vd] (stored column-major per head).
+// For the chunk's tokens, in one launch:
+//   * the depthwise causal conv + SiLU of the q, k and v channels along the
+//     ring (lz_causal_conv1d_step, src/ops_conv1d.c:26-87: taps summed in
+//     order, then the current input; ring slots src/forward_kda.c:680-755);
 //   * the gate up-projection row h*kd + j of f_b over the per-32 quantized
 //     low-rank input (lz_matmul_xq_nt + epi_q8, src/ops_matmul.c:468-660,
 //     src/ops_epi.c:983-1017: exact int32 group sums, groups summed in
@@ -20,43 +21,62 @@
 //     l2norm(k), beta, kq = k.q, then per token u = S^T(g.k), w = S^T(g.q),
 //     delta = (v - u)*beta, out = w + delta*kq, S' = g.S + k(x)delta
 //     (lz_recur_step fp32 arm, src/ops_gdn.c:2516-2560; call site
-//     src/forward_kda.c:856-940), every state written to its ring slot;
+//     src/forward_kda.c:856-940), every state written to its ring slot.
+//     u and w keep the reference's row order: the quad's first lane sums
+//     its rows from 0, passes the partial to the next lane (DPP), which
+//     continues with its rows, and so on; the row products and the state
+//     update are spread over the quad;
 //   * the per-head gated RMSNorm and the per-32 quantization for o_proj
 //     (src/forward_kda.c:1000-1043).
-// Everything that does not depend on the state is computed for all tokens
-// at once; only u, w and the state update run token-serially.
-template <int KD, int K>
-__global__ __launch_bounds__(KD) void k_kda_step(KdaStepArgs a) {
-    constexpr int VD = KD, HIST = K - 1;
+// Work that does not depend on the state is done for all NT token slots at
+// once (NT a power of two >= nt; slots past nt repeat the last token and
+// store nothing), as straight-line code with independent work per token.
+__device__ __forceinline__ float dpp_quad_shr1(float v) {        // lane r <- lane r-1 (lane 0 keeps its own)
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x90, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float dpp_quad_bcast3(float v) {      // every lane <- lane 3 of its quad
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xFF, 0xF, 0xF, false));
+}
+
+template <int KD, int K, int NT>
+__global__ __launch_bounds__(4 * KD) void k_kda_step(KdaStepArgs a) {
+    constexpr int VD = KD, HIST = K - 1, NTHR = 4 * KD, RPL = KD / 4;
+    constexpr int NF4 = (NT * KDA_MAX_RANK / 4 + NTHR - 1) / NTHR;      // float4 of the gate input per thread
+    constexpr int NO4 = (NT * VD / 4 + NTHR - 1) / NTHR;                // float4 of the output per thread
     EXP_TAB_LOAD(tab);
-    __shared__ __align__(16) float s_a[MAX_CHUNK][KD];   // q, then q.g*invq*scale (qcw)
+    __shared__ __align__(16) float s_a[MAX_CHUNK][KD];   // q, then q.g*invq*scale (qcw), then y
     __shared__ __align__(16) float s_b[MAX_CHUNK][KD];   // k, then k*invk (kn)
     __shared__ __align__(16) float s_g[MAX_CHUNK][KD];   // decay gate
     __shared__ __align__(16) float s_c[MAX_CHUNK][KD];   // q^2, then kn*g (kcw), then o^2
-    __shared__ __align__(16) float s_d[MAX_CHUNK][KD];   // k^2
-    __shared__ __align__(16) int8_t s_fq[MAX_CHUNK][KDA_MAX_RANK];
-    __shared__ float s_fs[MAX_CHUNK][KDA_MAX_RANK / 32];
+    __shared__ __align__(16) float s_d[MAX_CHUNK][KD];   // k^2, then o
+    __shared__ __align__(16) float s_v[MAX_CHUNK][KD];   // conv v
+    __shared__ __align__(16) int8_t s_fq[MAX_CHUNK * KDA_MAX_RANK];
+    __shared__ float s_fs[MAX_CHUNK * KDA_MAX_RANK / 32];
     __shared__ float s_invq[MAX_CHUNK], s_invk[MAX_CHUNK], s_beta[MAX_CHUNK], s_kq[MAX_CHUNK],
         s_oinv[MAX_CHUNK];
     const int h = blockIdx.x;
-    const int j = threadIdx.x;
+    const int tid = threadIdx.x;
+    const bool chan = tid < KD;
+    const int j = chan ? tid : KD - 1;     // channel of the channel phases (clamped for the others)
+    const int col = tid >> 2, quarter = tid & 3, row0 = quarter * RPL;
     const int nt = a.nt, key = a.key, value = a.value, rank = a.rank;
     const size_t head_off = (size_t)h * KD * VD;
     const int base = *a.ctl_slot;
-    // ---- loads: token inputs, conv taps and history, f_b row, state
+    // ---- loads: token inputs, gate input, conv taps and history, f_b row, state
     const int cq = h * KD + j, ck = key + h * KD + j, cv = 2 * key + h * VD + j;   // conv channels
-    float xq[MAX_CHUNK], xk[MAX_CHUNK], xv[MAX_CHUNK], gzv[MAX_CHUNK], fa[MAX_CHUNK][KDA_MAX_RANK / KD + 1];
+    float xq[NT], xk[NT], xv[NT], gzv[NT];
 #pragma unroll
-    for (int t = 0; t < MAX_CHUNK; t++) {
+    for (int t = 0; t < NT; t++) {
         const int tc = imin(t, nt - 1);
         xq[t] = a.pq[(size_t)tc * key + h * KD + j];
         xk[t] = a.pk[(size_t)tc * key + h * KD + j];
         xv[t] = a.pv[(size_t)tc * value + h * VD + j];
         gzv[t] = a.gz[(size_t)tc * value + h * VD + j];
-#pragma unroll
-        for (int r = 0; r < KDA_MAX_RANK / KD + 1; r++)
-            fa[t][r] = a.pfa[(size_t)tc * rank + imin(r * KD + j, rank - 1)];
     }
+    const int nfa4 = nt * rank / 4;
+    float4 fa4[NF4];
+#pragma unroll
+    for (int u = 0; u < NF4; u++) fa4[u] = reinterpret_cast<const float4 *>(a.pfa)[imin(u * NTHR + tid, nfa4 - 1)];
     float wq[K], wk[K], wv[K], hq[HIST > 0 ? HIST : 1], hk[HIST > 0 ? HIST : 1], hv[HIST > 0 ? HIST : 1];
 #pragma unroll
     for (int i = 0; i < K; i++) {
@@ -82,116 +102,130 @@ __global__ __launch_bounds__(KD) void k_kda_step(KdaStepArgs a) {
     const float dtb = a.dt_bias[h * KD + j];
     const float onw = a.o_norm[j];
     const float alog = a.a_log[h];
-    float S[KD];
+    float S[RPL];
     {
-        const float *src = a.state + (size_t)base * a.slot_stride + head_off;
+        const float4 *src = reinterpret_cast<const float4 *>(a.state + (size_t)base * a.slot_stride + head_off +
+                                                             (size_t)col * KD + row0);
 #pragma unroll
-        for (int i = 0; i < KD; i++) S[i] = src[(size_t)i * VD + j];
-    }
-    EXP_TAB_PUT(tab);
-    // ---- per-32 quantization of the low-rank gate input (groups are lane
-    // halves: rank % 32 == 0, chunks of KD elements)
-#pragma unroll
-    for (int t = 0; t < MAX_CHUNK; t++) {
-        if (t < nt) {
-#pragma unroll
-            for (int r = 0; r < KDA_MAX_RANK / KD + 1; r++) {
-                if (r * KD < rank) {
-                    const int ri = r * KD + j;
-                    int8_t q;
-                    float sg;
-                    d_quant_group32(fa[t][r], &q, &sg);
-                    if (ri < rank) {
-                        s_fq[t][ri] = q;
-                        if ((ri & 31) == 0) s_fs[t][ri >> 5] = sg;
-                    }
-                }
-            }
+        for (int i = 0; i < RPL / 4; i++) {
+            const float4 q = src[i];
+            S[4 * i] = q.x; S[4 * i + 1] = q.y; S[4 * i + 2] = q.z; S[4 * i + 3] = q.w;
         }
     }
-    __syncthreads();
-    const float decay = d_exp(alog, tab);
-    // ---- conv (token-serial along the history) and the gate row
-    float qv[MAX_CHUNK], kv[MAX_CHUNK], vcv[MAX_CHUNK];
-    const int ring_owner = 1;              // nk == nv: every head owns its channels
-    (void)ring_owner;
+    EXP_TAB_PUT(tab);
+    // ---- per-32 quantization of the gate input: four values per thread, a
+    // group per aligned lane octet (rank % 32 == 0)
 #pragma unroll
-    for (int t = 0; t < MAX_CHUNK; t++) {
-        qv[t] = kv[t] = vcv[t] = 0.0f;
-        if (t < nt) {
-            float sq = 0.0f, sk = 0.0f, sv = 0.0f;
+    for (int u = 0; u < NF4; u++) {
+        float sg;
+        const uint32_t q = quant_octet(fa4[u], &sg);
+        const int f = u * NTHR + tid;
+        if (f < nfa4) {
+            reinterpret_cast<uint32_t *>(s_fq)[f] = q;
+            if (!(f & 7)) s_fs[f >> 3] = sg;
+        }
+    }
+    // ---- conv, all token slots: token t reads history seq[t .. t+HIST-1]
+    // and input seq[t+HIST], seq = [ring history | the chunk's inputs]
+    float qv[NT], kv[NT], vv[NT];
 #pragma unroll
-            for (int i = 0; i < HIST; i++) {
-                sq += wq[i] * hq[i];
-                sk += wk[i] * hk[i];
-                sv += wv[i] * hv[i];
-            }
-            sq += wq[HIST] * xq[t];
-            sk += wk[HIST] * xk[t];
-            sv += wv[HIST] * xv[t];
-            qv[t] = d_silu(sq, tab);
-            kv[t] = d_silu(sk, tab);
-            vcv[t] = d_silu(sv, tab);
+    for (int t = 0; t < NT; t++) {
+        float sq = 0.0f, sk = 0.0f, sv = 0.0f;
 #pragma unroll
-            for (int i = 0; i + 1 < HIST; i++) { hq[i] = hq[i + 1]; hk[i] = hk[i + 1]; hv[i] = hv[i + 1]; }
-            if (HIST > 0) { hq[HIST - 1] = xq[t]; hk[HIST - 1] = xk[t]; hv[HIST - 1] = xv[t]; }
-            if (a.advance || t == nt - 1) {
+        for (int i = 0; i < HIST; i++) {
+            const int si = t + i;                          // position in seq
+            const float q0 = si < HIST ? hq[si < HIST ? si : 0] : xq[si >= HIST ? si - HIST : 0];
+            const float k0 = si < HIST ? hk[si < HIST ? si : 0] : xk[si >= HIST ? si - HIST : 0];
+            const float v0 = si < HIST ? hv[si < HIST ? si : 0] : xv[si >= HIST ? si - HIST : 0];
+            sq += wq[i] * q0;
+            sk += wk[i] * k0;
+            sv += wv[i] * v0;
+        }
+        sq += wq[HIST] * xq[t];
+        sk += wk[HIST] * xk[t];
+        sv += wv[HIST] * xv[t];
+        qv[t] = d_silu(sq, tab);
+        kv[t] = d_silu(sk, tab);
+        vv[t] = d_silu(sv, tab);
+    }
+    // ring: the history after token t is seq[t+1 .. t+HIST]
+    if (chan) {
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            if (t < nt && (a.advance || t == nt - 1)) {
                 int so;
                 if (a.advance) { const int si = (base + t) % a.depth; so = si + 1 == a.depth ? 0 : si + 1; }
                 else so = base;
                 float *r1 = a.conv_ring + (size_t)so * a.conv_slot_stride;
 #pragma unroll
                 for (int i = 0; i < HIST; i++) {
-                    r1[(size_t)cq * HIST + i] = hq[i];
-                    r1[(size_t)ck * HIST + i] = hk[i];
-                    r1[(size_t)cv * HIST + i] = hv[i];
+                    const int si = t + 1 + i;
+                    r1[(size_t)cq * HIST + i] = si < HIST ? hq[si < HIST ? si : 0] : xq[si >= HIST ? si - HIST : 0];
+                    r1[(size_t)ck * HIST + i] = si < HIST ? hk[si < HIST ? si : 0] : xk[si >= HIST ? si - HIST : 0];
+                    r1[(size_t)cv * HIST + i] = si < HIST ? hv[si < HIST ? si : 0] : xv[si >= HIST ? si - HIST : 0];
                 }
             }
         }
     }
-    // gate pre-activation of row h*kd + j for each token, then the decay gate
+    __syncthreads();                     // gate input quantized, exp table in place
+    const float decay = d_exp(alog, tab);
+    // ---- gate row of each token, then the decay gate
+    float gv[NT];
 #pragma unroll
-    for (int t = 0; t < MAX_CHUNK; t++) {
-        if (t < nt) {
-            float dot = 0.0f;
+    for (int t = 0; t < NT; t++) {
+        const int tc = imin(t, nt - 1);
+        float dot = 0.0f;
 #pragma unroll
-            for (int g = 0; g < KDA_MAX_RANK / 32; g++) {
-                if (g * 32 < rank) {
-                    const int4 *xr = reinterpret_cast<const int4 *>(&s_fq[t][g * 32]);
-                    const int4 x0 = xr[0], x1 = xr[1];
-                    const int4 w0 = fbw[2 * g], w1 = fbw[2 * g + 1];
-                    int acc = __builtin_amdgcn_sdot4(w0.x, x0.x, 0, false);
-                    acc = __builtin_amdgcn_sdot4(w0.y, x0.y, acc, false);
-                    acc = __builtin_amdgcn_sdot4(w0.z, x0.z, acc, false);
-                    acc = __builtin_amdgcn_sdot4(w0.w, x0.w, acc, false);
-                    acc = __builtin_amdgcn_sdot4(w1.x, x1.x, acc, false);
-                    acc = __builtin_amdgcn_sdot4(w1.y, x1.y, acc, false);
-                    acc = __builtin_amdgcn_sdot4(w1.z, x1.z, acc, false);
-                    acc = __builtin_amdgcn_sdot4(w1.w, x1.w, acc, false);
-                    dot += (float)acc * s_fs[t][g];
-                }
+        for (int g = 0; g < KDA_MAX_RANK / 32; g++) {
+            if (g * 32 < rank) {
+                const int4 *xr = reinterpret_cast<const int4 *>(s_fq + tc * rank + g * 32);
+                const int4 x0 = xr[0], x1 = xr[1];
+                const int4 w0 = fbw[2 * g], w1 = fbw[2 * g + 1];
+                int acc = __builtin_amdgcn_sdot4(w0.x, x0.x, 0, false);
+                acc = __builtin_amdgcn_sdot4(w0.y, x0.y, acc, false);
+                acc = __builtin_amdgcn_sdot4(w0.z, x0.z, acc, false);
+                acc = __builtin_amdgcn_sdot4(w0.w, x0.w, acc, false);
+                acc = __builtin_amdgcn_sdot4(w1.x, x1.x, acc, false);
+                acc = __builtin_amdgcn_sdot4(w1.y, x1.y, acc, false);
+                acc = __builtin_amdgcn_sdot4(w1.z, x1.z, acc, false);
+                acc = __builtin_amdgcn_sdot4(w1.w, x1.w, acc, false);
+                dot += (float)acc * s_fs[(tc * rank >> 5) + g];
             }
-            float pre = 0.0f;
-            pre += dot * fbs;
-            const float p = pre + dtb;
-            const float gg = -decay * d_softplus(p, tab);
-            s_g[t][j] = d_exp(gg, tab);
+        }
+        float pre = 0.0f;
+        pre += dot * fbs;
+        const float p = pre + dtb;
+        const float gg = -decay * d_softplus(p, tab);
+        gv[t] = d_exp(gg, tab);
+    }
+    if (chan) {
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            s_g[t][j] = gv[t];
             s_a[t][j] = qv[t];
             s_b[t][j] = kv[t];
             s_c[t][j] = qv[t] * qv[t];
             s_d[t][j] = kv[t] * kv[t];
+            s_v[t][j] = vv[t];
         }
     }
     __syncthreads();
-    if (j < nt) {                        // lane t: the token's serial norms and k.q
-        const int t = j;
+    if (tid < nt) {                      // thread t: the token's serial norms and k.q
+        const int t = tid;
         const float invq = d_rsqrt(serial_sum_n<KD>(s_c[t]) + 1e-6f);
         const float invk = d_rsqrt(serial_sum_n<KD>(s_d[t]) + 1e-6f);
         float kq = 0.0f;
-        for (int i = 0; i < KD; i++) {
-            const float qn = s_a[t][i] * invq * a.scale;
-            const float kn = s_b[t][i] * invk;
-            kq += kn * qn;
+#pragma unroll 4
+        for (int i = 0; i < KD; i += 4) {
+            const float4 q4 = *reinterpret_cast<const float4 *>(&s_a[t][i]);
+            const float4 k4 = *reinterpret_cast<const float4 *>(&s_b[t][i]);
+            const float qq[4] = {q4.x, q4.y, q4.z, q4.w}, kk[4] = {k4.x, k4.y, k4.z, k4.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float qn = qq[e] * invq * a.scale;
+                const float kn = kk[e] * invk;
+                kq += kn * qn;
+            }
         }
         s_invq[t] = invq;
         s_invk[t] = invk;
@@ -199,9 +233,9 @@ __global__ __launch_bounds__(KD) void k_kda_step(KdaStepArgs a) {
         s_beta[t] = d_sigmoid(bv, tab);
     }
     __syncthreads();
+    if (chan) {
 #pragma unroll
-    for (int t = 0; t < MAX_CHUNK; t++) {
-        if (t < nt) {
+        for (int t = 0; t < NT; t++) {
             const float g = s_g[t][j];
             const float qn = s_a[t][j] * s_invq[t] * a.scale;
             const float kn = s_b[t][j] * s_invk[t];
@@ -211,48 +245,89 @@ __global__ __launch_bounds__(KD) void k_kda_step(KdaStepArgs a) {
         }
     }
     __syncthreads();
-    float ov[MAX_CHUNK];
+    // ---- the token-serial recurrence on the lane quads
+#pragma unroll 1
+    for (int t = 0; t < nt; t++) {
+        float pu[RPL], pw[RPL];
 #pragma unroll
-    for (int t = 0; t < MAX_CHUNK; t++) {
-        ov[t] = 0.0f;
-        if (t < nt) {
-            float u = 0.0f, w = 0.0f;
+        for (int i = 0; i < RPL; i += 4) {
+            const float4 c4 = *reinterpret_cast<const float4 *>(&s_c[t][row0 + i]);
+            const float4 a4 = *reinterpret_cast<const float4 *>(&s_a[t][row0 + i]);
+            pu[i] = S[i] * c4.x; pu[i + 1] = S[i + 1] * c4.y; pu[i + 2] = S[i + 2] * c4.z; pu[i + 3] = S[i + 3] * c4.w;
+            pw[i] = S[i] * a4.x; pw[i + 1] = S[i + 1] * a4.y; pw[i + 2] = S[i + 2] * a4.z; pw[i + 3] = S[i + 3] * a4.w;
+        }
+        float u = 0.0f, w = 0.0f;
 #pragma unroll
-            for (int i = 0; i < KD; i++) {
-                u += S[i] * s_c[t][i];
-                w += S[i] * s_a[t][i];
-            }
-            u = (vcv[t] - 1.0f * u) * s_beta[t];
-            const float o = 1.0f * w + u * s_kq[t];
+        for (int ph = 0; ph < 4; ph++) {
+            if (ph) { u = dpp_quad_shr1(u); w = dpp_quad_shr1(w); }
 #pragma unroll
-            for (int i = 0; i < KD; i++) S[i] = S[i] * s_g[t][i] + s_b[t][i] * u;
-            if (a.advance || t == nt - 1) {
-                int so;
-                if (a.advance) { const int si = (base + t) % a.depth; so = si + 1 == a.depth ? 0 : si + 1; }
-                else so = base;
-                float *dst = a.state + (size_t)so * a.slot_stride + head_off;
+            for (int i = 0; i < RPL; i++) { u += pu[i]; w += pw[i]; }
+        }
+        u = dpp_quad_bcast3(u);
+        w = dpp_quad_bcast3(w);
+        const float ut = (s_v[t][col] - 1.0f * u) * s_beta[t];
+        const float o = 1.0f * w + ut * s_kq[t];
 #pragma unroll
-                for (int i = 0; i < KD; i++) dst[(size_t)i * VD + j] = S[i];
-            }
-            if (a.raw_out) a.raw_out[(size_t)t * value + (size_t)h * VD + j] = o;
-            ov[t] = o;
+        for (int i = 0; i < RPL; i += 4) {
+            const float4 g4 = *reinterpret_cast<const float4 *>(&s_g[t][row0 + i]);
+            const float4 b4 = *reinterpret_cast<const float4 *>(&s_b[t][row0 + i]);
+            S[i] = S[i] * g4.x + b4.x * ut;
+            S[i + 1] = S[i + 1] * g4.y + b4.y * ut;
+            S[i + 2] = S[i + 2] * g4.z + b4.z * ut;
+            S[i + 3] = S[i + 3] * g4.w + b4.w * ut;
+        }
+        if (a.advance || t == nt - 1) {
+            int so;
+            if (a.advance) { const int si = (base + t) % a.depth; so = si + 1 == a.depth ? 0 : si + 1; }
+            else so = base;
+            float4 *dst = reinterpret_cast<float4 *>(a.state + (size_t)so * a.slot_stride + head_off +
+                                                     (size_t)col * KD + row0);
+#pragma unroll
+            for (int i = 0; i < RPL / 4; i++) dst[i] = make_float4(S[4 * i], S[4 * i + 1], S[4 * i + 2], S[4 * i + 3]);
+        }
+        if (quarter == 0) {
+            if (a.raw_out) a.raw_out[(size_t)t * value + (size_t)h * VD + col] = o;
+            s_d[t][col] = o;
         }
     }
-    __syncthreads();                     // every lane is done reading s_c
-#pragma unroll
-    for (int t = 0; t < MAX_CHUNK; t++)
-        if (t < nt) s_c[t][j] = ov[t] * ov[t];
     __syncthreads();
-    if (j < nt) s_oinv[j] = d_rsqrt(d_ss_over_n(serial_sum_n<VD>(s_c[j]), VD) + a.eps);
+    if (chan) {
+#pragma unroll
+        for (int t = 0; t < NT; t++)
+            if (t < nt) s_c[t][j] = s_d[t][j] * s_d[t][j];
+    }
+    __syncthreads();
+    if (tid < nt) s_oinv[tid] = d_rsqrt(d_ss_over_n(serial_sum_n<VD>(s_c[tid]), VD) + a.eps);
     __syncthreads();
     // gated RMSNorm over the head: ((o*inv)*w)*silu(g)  (src/ops_norm.c:749-793)
-    const int col = h * VD + j;
+    float yv[NT];
 #pragma unroll
-    for (int t = 0; t < MAX_CHUNK; t++) {
-        if (t < nt) {
-            const float y = ov[t] * s_oinv[t] * onw * d_silu(gzv[t], tab);
-            if (a.normed_out) a.normed_out[(size_t)t * value + col] = y;
-            d_quant_group32(y, a.xq + (size_t)t * value + col, a.xqs + (size_t)t * (value >> 5) + (col >> 5));
+    for (int t = 0; t < NT; t++) {
+        const int tc = imin(t, nt - 1);
+        yv[t] = s_d[tc][j] * s_oinv[tc] * onw * d_silu(gzv[t], tab);
+    }
+    if (chan) {
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            if (t < nt) {
+                if (a.normed_out) a.normed_out[(size_t)t * value + h * VD + j] = yv[t];
+                s_a[t][j] = yv[t];
+            }
+        }
+    }
+    __syncthreads();
+    // per-32 quantization of the output rows, four values per thread
+    const int no4 = nt * VD / 4;
+#pragma unroll
+    for (int u = 0; u < NO4; u++) {
+        const int f = u * NTHR + tid;
+        const int fc = imin(f, no4 - 1);
+        const int t = (4 * fc) / VD, c = 4 * fc - t * VD;
+        float sg;
+        const uint32_t q = quant_octet(*reinterpret_cast<const float4 *>(&s_a[t][c]), &sg);
+        if (f < no4) {
+            reinterpret_cast<uint32_t *>(a.xq + (size_t)t * value + h * VD)[c >> 2] = q;
+            if (!(c & 31)) a.xqs[(size_t)t * (value >> 5) + ((h * VD + c) >> 5)] = sg;
         }
     }
 }
@@ -267,19 +342,30 @@ extern "C" int l98k_kda_step(const KdaStepArgs *a, int kd, int K, hipStream_t st
     if (a->nt < 1 || a->nt > MAX_CHUNK || a->rank < 32 || (a->rank & 31) || a->rank > KDA_MAX_RANK ||
         a->key != a->nv * kd || a->value != a->nv * kd || K < 2 || K > 4)
         return -1;
-#define KDA_STEP(KD_, K_) hipLaunchKernelGGL((k_kda_step<KD_, K_>), dim3(a->nv), dim3(KD_), 0, st, *a)
+    const int nt = a->nt, NT = nt <= 1 ? 1 : nt <= 2 ? 2 : nt <= 4 ? 4 : 8;
+    // conv width 4 (every synthetic config) has an instance per token bound;
+    // other widths run the 8-slot instance
+#define KDA_STEP(KD_, K_, NT_) hipLaunchKernelGGL((k_kda_step<KD_, K_, NT_>), dim3(a->nv), dim3(4 * (KD_)), 0, st, *a)
+#define KDA_K4(KD_)                                 \
+    switch (NT) {                                   \
+    case 1: KDA_STEP(KD_, 4, 1); break;             \
+    case 2: KDA_STEP(KD_, 4, 2); break;             \
+    case 4: KDA_STEP(KD_, 4, 4); break;             \
+    default: KDA_STEP(KD_, 4, 8); break;            \
+    }
     switch (kd * 8 + K) {
-    case 64 * 8 + 4: KDA_STEP(64, 4); break;
-    case 64 * 8 + 3: KDA_STEP(64, 3); break;
-    case 64 * 8 + 2: KDA_STEP(64, 2); break;
-    case 128 * 8 + 4: KDA_STEP(128, 4); break;
-    case 128 * 8 + 3: KDA_STEP(128, 3); break;
-    case 128 * 8 + 2: KDA_STEP(128, 2); break;
-    case 32 * 8 + 4: KDA_STEP(32, 4); break;
-    case 32 * 8 + 3: KDA_STEP(32, 3); break;
-    case 32 * 8 + 2: KDA_STEP(32, 2); break;
+    case 64 * 8 + 4: KDA_K4(64); break;
+    case 64 * 8 + 3: KDA_STEP(64, 3, 8); break;
+    case 64 * 8 + 2: KDA_STEP(64, 2, 8); break;
+    case 128 * 8 + 4: KDA_K4(128); break;
+    case 128 * 8 + 3: KDA_STEP(128, 3, 8); break;
+    case 128 * 8 + 2: KDA_STEP(128, 2, 8); break;
+    case 32 * 8 + 4: KDA_K4(32); break;
+    case 32 * 8 + 3: KDA_STEP(32, 3, 8); break;
+    case 32 * 8 + 2: KDA_STEP(32, 2, 8); break;
     default: return -1;
     }
+#undef KDA_K4
 #undef KDA_STEP
     return (int)hipGetLastError();
 }
