@@ -40,9 +40,9 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 // LDS bytes of one tile: staged activations, their scales, and the larger of
 // the group sums and the RMSNorm squares.
 __host__ __device__ inline size_t gemv_lds_bytes(int m, int in_dim, int R, int norm) {
-    const size_t part = (size_t)R * m * ((in_dim >> 5) + 1) * 4;
+    const size_t part = (size_t)R * m * ((in_dim >> 5) + 4) * 4;
     const size_t sq = norm ? (size_t)m * (in_dim + 4) * 4 : 0;
-    return (size_t)m * in_dim + (size_t)m * (in_dim >> 5) * 4 + (part > sq ? part : sq);
+    return (size_t)m * in_dim + (size_t)((m * (in_dim >> 5) + 3) & ~3) * 4 + (part > sq ? part : sq);
 }
 
 __device__ __forceinline__ float4 f4_silu_mul(float4 p, float4 q, const float *tab) {
@@ -279,22 +279,23 @@ __device__ __forceinline__ void build_rows(const Prologue &P, const int8_t *__re
     }
 }
 
-// One GEMV tile.  xrow[t]: activation row of token slot t (registers);
-// s_orow[t]: output row of token slot t (LDS, read after a barrier); nm:
-// live token slots.  The caller fills the LDS exp table first.
+// One GEMV tile of rows_here <= R rows.  xrow[t]: activation row of token
+// slot t (registers); s_orow[t]: output row of token slot t (LDS, read after
+// a barrier); nm: live token slots.  The caller fills the LDS exp table
+// first.
 template <int M, int PJ, int MODES>
 __device__ __forceinline__ void gemv_tile(const int8_t *__restrict__ wt, const float *__restrict__ ws, int rows_here,
-                                          int in_dim, const Prologue &P, const int8_t *__restrict__ xq,
+                                          int R, int in_dim, const Prologue &P, const int8_t *__restrict__ xq,
                                           const float *__restrict__ xqs, const int (&xrow)[M], const int *s_orow,
                                           int nm, bool writer, float *__restrict__ out, size_t out_stride,
                                           int row0, int32_t *__restrict__ acc_out, int acc_rows, char *smem,
                                           float *s_inv, float *tab) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int cpr = in_dim >> 4, nb = in_dim >> 5;
+    const int cpr = in_dim >> 4, nb = in_dim >> 5, pstride = nb + 4;
     const int nchunk = rows_here * cpr;
     int8_t *sx = reinterpret_cast<int8_t *>(smem);                                   // [M][in_dim]
     float *sxs = reinterpret_cast<float *>(smem + (size_t)M * in_dim);                // [M][nb]
-    int *part = reinterpret_cast<int *>(sxs + M * nb);                                // [R][M][nb+1]
+    int *part = reinterpret_cast<int *>(sxs + ((M * nb + 3) & ~3));                   // [R][M][nb+4]
     // weights: one 8 KiB quarter of the tile per wave, all loads in flight
     int4 wv[GEMV_MAXJ];
     const int er = tid / M, et = tid - er * M;
@@ -309,59 +310,70 @@ __device__ __forceinline__ void gemv_tile(const int8_t *__restrict__ wt, const f
         }
         wsv = ws[row0 + imin(er, rows_here - 1)];     // the epilogue lane's row scale
     };
-    build_rows<M, PJ, MODES>(P, xq, xqs, in_dim, xrow, nm, writer, sx, sxs, reinterpret_cast<float *>(part), s_inv, tab,
-                      issue_w);
+    build_rows<M, PJ, MODES>(P, xq, xqs, in_dim, xrow, nm, writer, sx, sxs, reinterpret_cast<float *>(part), s_inv,
+                             tab, issue_w);
     __syncthreads();
-    // Partial dot products.  With a power-of-two chunk count per row, lane
-    // l's chunks of every row sit at the same in-row offsets (l + 64v) mod
-    // cpr for v < cpr/64, so each activation chunk is read from LDS once and
-    // reused for all of the lane's weight chunks at that offset.
+    // Partial dot products.  Lane chunk j is c0 + 64 j; its (row, offset)
+    // advance by 64 chunks per step.  When cpr divides 64 every chunk of
+    // the lane sits at the same in-row offset and its activation chunks are
+    // read from LDS once.  Neighbouring lanes hold the two 16-byte halves of
+    // a 32-element group: after the pair sum (DPP) both store the same exact
+    // int32 group sum to the same slot.  Chunk steps past the tile's R rows
+    // are skipped (wave-uniform); chunks past the live rows repeat the last
+    // chunk's weights into rows the epilogue ignores.
     const int4 *sx4 = reinterpret_cast<const int4 *>(sx);
-    auto dot_store = [&](int j, const int4 (&xv)[M]) {
-        const int c = wave * (GEMV_WAVE_BYTES / 16) + lane + 64 * j;
-        const int r = c / cpr, p = c - r * cpr;
+    const int c0 = wave * (GEMV_WAVE_BYTES / 16) + lane;
+    const int q64 = 64 / cpr, m64 = 64 - q64 * cpr;
+    const int cmax = R * cpr;
+    const bool reuse = m64 == 0;
+    int r = c0 / cpr, p = c0 - r * cpr;
+    int4 xv[M];
+    if (reuse) {
 #pragma unroll
-        for (int t = 0; t < M; t++) {
-            int a = __builtin_amdgcn_sdot4(wv[j].x, xv[t].x, 0, false);
-            a = __builtin_amdgcn_sdot4(wv[j].y, xv[t].y, a, false);
-            a = __builtin_amdgcn_sdot4(wv[j].z, xv[t].z, a, false);
-            a = __builtin_amdgcn_sdot4(wv[j].w, xv[t].w, a, false);
-            a += __builtin_amdgcn_update_dpp(0, a, 0xB1, 0xF, 0xF, false);     // lane ^ 1: chunks 2g, 2g+1
-            if (t < nm && c < nchunk && !(lane & 1)) part[(r * M + t) * (nb + 1) + (p >> 1)] = a;
-        }
-    };
-    if ((cpr & (cpr - 1)) == 0 && cpr <= 256) {
-        const int nv = cpr > 64 ? cpr >> 6 : 1;
+        for (int t = 0; t < M; t++) xv[t] = sx4[t * cpr + p];
+    }
 #pragma unroll
-        for (int vv = 0; vv < 4; vv++) {
-            if (vv < nv) {
-                const int p = (lane + 64 * vv) & (cpr - 1);
-                int4 xv[M];
+    for (int j = 0; j < GEMV_MAXJ; j++) {
+        if (wave * (GEMV_WAVE_BYTES / 16) + 64 * j < cmax) {
+            if (!reuse) {
 #pragma unroll
-                for (int t = 0; t < M; t++) xv[t] = sx4[(t < nm ? t : 0) * cpr + p];
+                for (int t = 0; t < M; t++) xv[t] = sx4[t * cpr + p];
+            }
+            int *dst = part + r * M * pstride + (p >> 1);
 #pragma unroll
-                for (int j = 0; j < GEMV_MAXJ; j++)
-                    if ((j & (nv - 1)) == vv) dot_store(j, xv);
+            for (int t = 0; t < M; t++) {
+                int a = __builtin_amdgcn_sdot4(wv[j].x, xv[t].x, 0, false);
+                a = __builtin_amdgcn_sdot4(wv[j].y, xv[t].y, a, false);
+                a = __builtin_amdgcn_sdot4(wv[j].z, xv[t].z, a, false);
+                a = __builtin_amdgcn_sdot4(wv[j].w, xv[t].w, a, false);
+                a += __builtin_amdgcn_update_dpp(0, a, 0xB1, 0xF, 0xF, false);     // lane ^ 1
+                dst[t * pstride] = a;
             }
         }
-    } else {
-#pragma unroll
-        for (int j = 0; j < GEMV_MAXJ; j++) {
-            const int c = wave * (GEMV_WAVE_BYTES / 16) + lane + 64 * j;
-            const int p = c - (c / cpr) * cpr;
-            int4 xv[M];
-#pragma unroll
-            for (int t = 0; t < M; t++) xv[t] = sx4[(t < nm ? t : 0) * cpr + p];
-            dot_store(j, xv);
-        }
+        r += q64;
+        p += m64;
+        if (p >= cpr) { p -= cpr; r++; }
     }
     __syncthreads();
+    // Epilogue, one lane per (row, token): sum_s float(acc[s]) * xqs[s] in
+    // group order, then times the row scale (src/ops_epi.c:983-1017).
     if (er < rows_here && et < nm) {
-        const int *pp = part + (er * M + et) * (nb + 1);
+        const int *pp = part + (er * M + et) * pstride;
         const float *xs = sxs + et * nb;
         float dot = 0.0f;
-#pragma unroll 8
-        for (int g = 0; g < nb; g++) dot += (float)pp[g] * xs[g];
+        if ((nb & 3) == 0) {
+#pragma unroll 2
+            for (int g = 0; g < nb; g += 4) {
+                const int4 q = *reinterpret_cast<const int4 *>(pp + g);
+                const float4 x4 = *reinterpret_cast<const float4 *>(xs + g);
+                dot += (float)q.x * x4.x;
+                dot += (float)q.y * x4.y;
+                dot += (float)q.z * x4.z;
+                dot += (float)q.w * x4.w;
+            }
+        } else {
+            for (int g = 0; g < nb; g++) dot += (float)pp[g] * xs[g];
+        }
         float sum = 0.0f;
         sum += dot * wsv;
         out[(size_t)s_orow[et] * out_stride + row0 + er] = sum;

@@ -18,7 +18,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv_q8(GemvBatch batch, int m
     int xrow[M];
 #pragma unroll
     for (int t = 0; t < M; t++) xrow[t] = t < m ? t : 0;
-    gemv_tile<M, PJ, MODES>(job.w + (size_t)row0 * job.in_dim, job.ws, rows_here, job.in_dim, job.pro, job.xq,
+    gemv_tile<M, PJ, MODES>(job.w + (size_t)row0 * job.in_dim, job.ws, rows_here, job.R, job.in_dim, job.pro, job.xq,
                             job.xqs, xrow, s_row, m, blk == 0, job.out, job.out_stride, row0, job.acc_out, job.rows,
                             smem, s_inv, tab);
 }

@@ -33,7 +33,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_expert_gemv(ExpertJob j0, Expe
     }
     const int row0 = tile * R;
     gemv_tile<M, PJ, MODES_S>(J.q + ((size_t)e * out_rows + row0) * in_dim, J.s + (size_t)e * out_rows,
-                             imin(R, out_rows - row0), in_dim, J.pro, J.xq, J.xqs, xrow, s_orow, nm, false, J.out,
+                             imin(R, out_rows - row0), R, in_dim, J.pro, J.xq, J.xqs, xrow, s_orow, nm, false, J.out,
                              out_rows, row0, nullptr, 0, smem, s_inv, tab);
 }
 
@@ -237,7 +237,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_up(ExpertJob j0, ExpertJob
     }
     const int row0 = tile * R;
     gemv_tile<M, PJ, MODES_Q>(J.q + ((size_t)e * out_rows + row0) * in_dim, J.s + (size_t)e * out_rows,
-                             imin(R, out_rows - row0), in_dim, J.pro, J.xq, J.xqs, xrow, s_orow, nm, false, J.out,
+                             imin(R, out_rows - row0), R, in_dim, J.pro, J.xq, J.xqs, xrow, s_orow, nm, false, J.out,
                              out_rows, row0, nullptr, 0, smem, s_inv, tab);
 }
 
