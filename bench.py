@@ -17,7 +17,9 @@ device synchronizations; value = tokens emitted in the K rounds / wall time.
 The JSON line also carries:
   roofline      the dominant kernel (the tied lm_head GEMV at M = k+1 rows)
                 timed with HIP events on its own stream, algorithmic bytes /
-                mean launch time against 8 TB/s;
+                mean launch time against 8 TB/s (back to back, as the draft
+                steps of a round run it; cold_* after a cache-evicting copy);
+                traffic from the committed rocprofv3 byte-counter summary;
   verify        the verify forward alone (M = k+1), algorithmic bytes / time;
   round         accepted tok/s against the round's HBM roofline
                 E[n_accept+1] * 8e12 / bytes_per_round (bytes counted from
@@ -79,6 +81,19 @@ def round_bytes(cfg, k, ctx_verify, experts):
               + experts * b["expert"] + b["lm_head"] + n_full * b["kv_row"] * (ctx_verify + M)
               + 4 * M * (cfg.vocab_size + cfg.hidden_size))
     return draft, verify
+
+
+def measured_traffic(config, k):
+    """HBM bytes per launch of the tied lm_head GEMV from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (copy-calibrated), for the
+    configs[1], k = 3 workload it was measured on; None otherwise."""
+    path = os.path.join(ROOT, "profiles", "lm_head_gemv_m4_traffic.md")
+    if config != 1 or k != 3 or not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":")[1])
+    return None
 
 
 def cpu_baseline(model_dir, vocab, k):
@@ -174,6 +189,7 @@ def main():
     # dominant kernel: the tied lm_head GEMV at M = k+1 rows
     M = k + 1
     lm_ms = eng.time_kernel(0, M, 50)
+    lm_cold_ms = eng.time_kernel(3, M, 10)      # each launch after a cache-evicting copy
     V, d = cfg.vocab_size, cfg.hidden_size
     lm_bytes = V * d + 4 * V + M * d + 4 * M * d // 32 + 4 * M * V
     lm_bw = lm_bytes / (lm_ms * 1e-3)
@@ -202,8 +218,10 @@ def main():
                    "graph": use_graph},
         "roofline": {"bound": "hbm", "kernel": f"k_gemv_q8<{M}> (tied lm_head, {V}x{d} int8)",
                      "achieved": round(lm_bw / 1e9, 1), "peak": 8000.0, "unit": "GB/s",
-                     "frac": round(lm_bw / HBM_PEAK, 4), "traffic": None,
-                     "bytes_per_launch": lm_bytes, "launch_ms": round(lm_ms, 5)},
+                     "frac": round(lm_bw / HBM_PEAK, 4), "traffic": measured_traffic(args.config, k),
+                     "bytes_per_launch": lm_bytes, "launch_ms": round(lm_ms, 5),
+                     "cold_launch_ms": round(lm_cold_ms, 5),
+                     "cold_frac": round(lm_bytes / (lm_cold_ms * 1e-3) / HBM_PEAK, 4)},
         "verify": {"M": M, "ms": round(ver_ms, 4), "bytes": int(ver_bytes),
                    "GB/s": round(ver_bw / 1e9, 1), "frac_of_peak": round(ver_bw / HBM_PEAK, 4)},
         "round": {"alpha": round(float(na.sum()) / (k * args.steps), 4),

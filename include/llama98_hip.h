@@ -186,9 +186,12 @@ int l98_greedy_rounds(const LZModel *m, LZRunState *s, int k, int n_rounds, int 
  * sets its verify streamed and its new_pos (for byte accounting). */
 int l98_greedy_rounds_ex(const LZModel *m, LZRunState *s, int k, int n_rounds, int use_graph, int *tokens,
                          int cap, int *n_accept_out, int *experts_out, int *new_pos_out, float *device_ms);
-/* Mean duration of `iters` back-to-back launches of one kernel of the round
- * (which = 0: the tied lm_head GEMV with mrows token rows), hipEvent-timed on
- * the state's stream.  Returns 0. */
+/* Mean duration of `iters` launches, hipEvent-timed on the state's stream.
+ * which = 0: the tied lm_head GEMV with mrows token rows, back to back;
+ * 1: the verify forward of mrows tokens; 2: a device copy of the lm_head's
+ * int8 bytes (calibration for byte counters); 3: the lm_head GEMV after a
+ * cache-evicting 512 MiB copy each time (only the GEMV timed).  Returns 0
+ * (1 on a bad argument or a device error). */
 int l98_time_kernel(const LZModel *m, LZRunState *s, int which, int mrows, int iters, float *avg_ms);
 /* Device and build facts, for logs. */
 const char *l98_device_name(void);

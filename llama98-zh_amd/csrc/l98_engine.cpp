@@ -1642,33 +1642,61 @@ extern "C" int l98_generate(const LZModel *mm, LZRunState *s, const int *prompt,
     return n;
 }
 
-// Times `iters` back-to-back launches of one kernel of the round with HIP
-// events on the state's stream.  which: 0 = tied lm_head GEMV (vocab rows,
-// hidden input) with mrows token rows.  Returns 0 and the mean per launch.
+// Times `iters` launches of one kernel of the round with HIP events on the
+// state's stream; returns 0 and the mean per launch.  which:
+//   0  tied lm_head GEMV (vocab rows, hidden input) with mrows token rows,
+//      back to back;
+//   1  the verify forward of mrows tokens (ctl->tok at ctl->anchor_pos + 1..).
+//      It reads the ring state at ctl->slot_base and writes the slots after
+//      it and KV rows the next verify rewrites, so repeated launches read
+//      identical inputs and leave the session's state usable;
+//   2  a device-to-device copy of the lm_head's vocab x hidden int8 bytes
+//      (the calibration kernel for the HBM byte counters);
+//   3  the lm_head GEMV as in 0, each launch after a 512 MiB copy that
+//      evicts the device's last-level cache (only the GEMV is timed).
 extern "C" int l98_time_kernel(const LZModel *mm, LZRunState *s, int which, int mrows, int iters,
                                float *avg_ms) {
     if (!mm || !s || !s->impl || iters < 1 || mrows < 1 || mrows > MAX_CHUNK || !avg_ms) return 1;
     DState *d = S(s);
     const DModel *m = d->m;
     const LZModelConfig &c = m->c;
-    if (which != 0 && which != 1) return 1;
-    // which 1: the verify forward of mrows tokens (ctl->tok at ctl->anchor_pos
-    // + 1..).  It reads the ring state at ctl->slot_base and writes the slots
-    // after it and KV rows the next verify rewrites, so repeated launches read
-    // identical inputs and leave the session's state usable.
+    if (which < 0 || which > 3) return 1;
+    const size_t wbytes = (size_t)c.vocab_size * c.hidden_size;
+    const size_t flush_bytes = (size_t)512 << 20;
+    void *scratch = nullptr;
+    if (which >= 2 && hipMalloc(&scratch, which == 2 ? wbytes : 2 * flush_bytes) != hipSuccess) return 1;
     auto once = [&]() -> int {
-        if (which == 0) return gemv(d, {JX(m->embed, d->mtp_logits, c.vocab_size, d->xq, d->xqs)}, mrows);
+        if (which == 0 || which == 3)
+            return gemv(d, {JX(m->embed, d->mtp_logits, c.vocab_size, d->xq, d->xqs)}, mrows);
+        if (which == 2)
+            return hipMemcpyAsync(scratch, m->embed.q, wbytes, hipMemcpyDeviceToDevice, d->st) != hipSuccess;
         return forward_chunk(d, d->ctl->tok, mrows, &d->ctl->anchor_pos, 1, d->seq_len - 1, d->vhidden, true,
                              d->mtp_logits, false);
     };
-    if (once()) return 1;
-    (void)hipEventRecord(d->ev0, d->st);
-    for (int i = 0; i < iters; i++)
-        if (once()) return 1;
-    (void)hipEventRecord(d->ev1, d->st);
-    if (hipEventSynchronize(d->ev1) != hipSuccess) return 1;
+    int rc = 0;
     float ms = 0.0f;
-    (void)hipEventElapsedTime(&ms, d->ev0, d->ev1);
+    if (once()) rc = 1;
+    if (!rc && which != 3) {
+        (void)hipEventRecord(d->ev0, d->st);
+        for (int i = 0; i < iters && !rc; i++) rc = once();
+        (void)hipEventRecord(d->ev1, d->st);
+        if (!rc && hipEventSynchronize(d->ev1) != hipSuccess) rc = 1;
+        if (!rc) (void)hipEventElapsedTime(&ms, d->ev0, d->ev1);
+    } else if (!rc) {
+        char *fl = (char *)scratch;
+        for (int i = 0; i < iters && !rc; i++) {
+            if (hipMemcpyAsync(fl + flush_bytes, fl, flush_bytes, hipMemcpyDeviceToDevice, d->st) != hipSuccess) rc = 1;
+            (void)hipEventRecord(d->ev0, d->st);
+            if (!rc) rc = once();
+            (void)hipEventRecord(d->ev1, d->st);
+            float one = 0.0f;
+            if (!rc && hipEventSynchronize(d->ev1) != hipSuccess) rc = 1;
+            if (!rc) (void)hipEventElapsedTime(&one, d->ev0, d->ev1);
+            ms += one;
+        }
+    }
+    if (scratch) (void)hipFree(scratch);
+    if (rc) return 1;
     *avg_ms = ms / (float)iters;
     return 0;
 }
