@@ -383,6 +383,31 @@ __device__ __forceinline__ void gemv_tile(const int8_t *__restrict__ wt, const f
 }
 
 
+// Dynamic LDS a GEMV block may use: the device's per-block limit (160 KiB
+// on gfx950), less room for the kernels' static LDS.  Queried once.
+static inline size_t gemv_lds_limit() {
+    static size_t lim = 0;
+    if (!lim) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0)
+            v = 64 * 1024;
+        lim = (size_t)v - 12 * 1024;
+    }
+    return lim;
+}
+
+// Lets kernel `k` take dynamic LDS above the default 64 KiB (once per kernel).
+#define ALLOW_BIG_LDS(k)                                                                                  \
+    do {                                                                                                  \
+        static bool done_ = false;                                                                        \
+        if (!done_) {                                                                                     \
+            (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k), hipFuncAttributeMaxDynamicSharedMemorySize, \
+                                      (int)gemv_lds_limit());                                             \
+            done_ = true;                                                                                 \
+        }                                                                                                 \
+    } while (0)
+
 // Rows per GEMV tile: the tile is at most GEMV_TILE_BYTES of weights and
 // R*m (row, token) epilogue pairs fit the block.
 static int gemv_rows_per_tile(int in_dim, int m) {

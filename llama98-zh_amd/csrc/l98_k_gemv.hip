@@ -34,6 +34,7 @@ extern "C" int l98k_upload_exp_table_gemv(const float *tab) {
 // (PJ 1..4).
 #define GEMV_CASE(M_, PJ_, MODES_)                                                                         \
     case (M_) * 1000 + (PJ_) * 100 + (MODES_):                                                            \
+        ALLOW_BIG_LDS((k_gemv_q8<M_, PJ_, MODES_>));                                                      \
         hipLaunchKernelGGL((k_gemv_q8<M_, PJ_, MODES_>), dim3(tiles), dim3(GEMV_THREADS), lds, st, *b, m); \
         break;
 #define GEMV_CASES_M(M_)                                                                   \
@@ -63,7 +64,7 @@ extern "C" int l98k_gemv(GemvBatch *b, int m, hipStream_t st) {
         modes |= MB(J.pro.mode);
         if (J.pro.mode != PRO_XQ) pj = pro_pj(J.in_dim) > pj ? pro_pj(J.in_dim) : pj;
     }
-    if (lds > 64 * 1024) return -1;
+    if (lds > gemv_lds_limit()) return -1;
     if (modes == MODES_X) pj = 0;
     else if (modes == MB(PRO_COMBINE)) modes = MODES_CS;
     else if (modes != MODES_N && modes != MODES_S && modes != MODES_CS) return -1;
@@ -89,6 +90,6 @@ extern "C" int l98k_gemv_tiles(int rows, int in_dim, int m) {
 extern "C" int l98k_gemv_norm_fits(int in_dim, int m) {
     if (in_dim > PRO_MAX_IN || m < 1 || m > MAX_CHUNK) return 0;
     const int M = m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8;
-    return gemv_lds_bytes(M, in_dim, gemv_rows_per_tile(in_dim, M), 1) <= 64 * 1024;
+    return gemv_lds_bytes(M, in_dim, gemv_rows_per_tile(in_dim, M), 1) <= gemv_lds_limit();
 }
 

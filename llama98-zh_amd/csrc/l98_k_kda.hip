@@ -125,6 +125,7 @@ __global__ __launch_bounds__(4 * KD) void k_kda_step(KdaStepArgs a) {
             if (!(f & 7)) s_fs[f >> 3] = sg;
         }
     }
+    __syncthreads();                     // gate input quantized, exp table in place
     // ---- conv, all token slots: token t reads history seq[t .. t+HIST-1]
     // and input seq[t+HIST], seq = [ring history | the chunk's inputs]
     float qv[NT], kv[NT], vv[NT];
@@ -167,7 +168,6 @@ __global__ __launch_bounds__(4 * KD) void k_kda_step(KdaStepArgs a) {
             }
         }
     }
-    __syncthreads();                     // gate input quantized, exp table in place
     const float decay = d_exp(alog, tab);
     // ---- gate row of each token, then the decay gate
     float gv[NT];

@@ -250,21 +250,20 @@ extern "C" int l98k_upload_exp_table_moe(const float *tab) {
 // Member slots of a grouped expert launch: a power of two >= nt.
 static int expert_m(int nt) { return nt <= 1 ? 1 : nt <= 2 ? 2 : nt <= 4 ? 4 : 8; }
 
+#define EXPERT_CASE(KERNEL, M_, PJ_, ...)                                                \
+    case M_ * 16 + PJ_:                                                                  \
+        ALLOW_BIG_LDS((KERNEL<M_, PJ_>));                                                \
+        hipLaunchKernelGGL((KERNEL<M_, PJ_>), __VA_ARGS__);                              \
+        break;
 #define EXPERT_DISPATCH(KERNEL, M, PJ, ...)                                              \
     do {                                                                                 \
         switch (M * 16 + PJ) {                                                           \
-        case 1 * 16 + 1: hipLaunchKernelGGL((KERNEL<1, 1>), __VA_ARGS__); break;         \
-        case 1 * 16 + 2: hipLaunchKernelGGL((KERNEL<1, 2>), __VA_ARGS__); break;         \
-        case 1 * 16 + 4: hipLaunchKernelGGL((KERNEL<1, 4>), __VA_ARGS__); break;         \
-        case 2 * 16 + 1: hipLaunchKernelGGL((KERNEL<2, 1>), __VA_ARGS__); break;         \
-        case 2 * 16 + 2: hipLaunchKernelGGL((KERNEL<2, 2>), __VA_ARGS__); break;         \
-        case 2 * 16 + 4: hipLaunchKernelGGL((KERNEL<2, 4>), __VA_ARGS__); break;         \
-        case 4 * 16 + 1: hipLaunchKernelGGL((KERNEL<4, 1>), __VA_ARGS__); break;         \
-        case 4 * 16 + 2: hipLaunchKernelGGL((KERNEL<4, 2>), __VA_ARGS__); break;         \
-        case 4 * 16 + 4: hipLaunchKernelGGL((KERNEL<4, 4>), __VA_ARGS__); break;         \
-        case 8 * 16 + 1: hipLaunchKernelGGL((KERNEL<8, 1>), __VA_ARGS__); break;         \
-        case 8 * 16 + 2: hipLaunchKernelGGL((KERNEL<8, 2>), __VA_ARGS__); break;         \
-        case 8 * 16 + 4: hipLaunchKernelGGL((KERNEL<8, 4>), __VA_ARGS__); break;         \
+            EXPERT_CASE(KERNEL, 1, 1, __VA_ARGS__) EXPERT_CASE(KERNEL, 1, 2, __VA_ARGS__)  \
+            EXPERT_CASE(KERNEL, 1, 4, __VA_ARGS__) EXPERT_CASE(KERNEL, 2, 1, __VA_ARGS__)  \
+            EXPERT_CASE(KERNEL, 2, 2, __VA_ARGS__) EXPERT_CASE(KERNEL, 2, 4, __VA_ARGS__)  \
+            EXPERT_CASE(KERNEL, 4, 1, __VA_ARGS__) EXPERT_CASE(KERNEL, 4, 2, __VA_ARGS__)  \
+            EXPERT_CASE(KERNEL, 4, 4, __VA_ARGS__) EXPERT_CASE(KERNEL, 8, 1, __VA_ARGS__)  \
+            EXPERT_CASE(KERNEL, 8, 2, __VA_ARGS__) EXPERT_CASE(KERNEL, 8, 4, __VA_ARGS__)  \
         default: return -1;                                                              \
         }                                                                                \
     } while (0)
@@ -288,7 +287,7 @@ extern "C" int l98k_expert_gemv(const ExpertJob *jobs, int n_jobs, const MoeGrou
     const int R = gemv_rows_per_tile(in_dim, M);
     const int tiles = (out_rows + R - 1) / R;
     const size_t lds = gemv_lds_bytes(M, in_dim, R, 0);
-    if (lds > 64 * 1024) return -1;
+    if (lds > gemv_lds_limit()) return -1;
     const int pj = pro_pj(in_dim);
     const dim3 grid(n_jobs * max_groups * tiles), blk(GEMV_THREADS);
     const ExpertJob &a = jobs[0], &b2 = n_jobs > 1 ? jobs[1] : jobs[0];
@@ -307,7 +306,7 @@ extern "C" int l98k_moe_up(const ExpertJob *jobs, int n_jobs, const float *logit
     const int R = gemv_rows_per_tile(in_dim, M);
     const int tiles = (out_rows + R - 1) / R;
     const size_t lds = gemv_lds_bytes(M, in_dim, R, 0);
-    if (lds > 64 * 1024) return -1;
+    if (lds > gemv_lds_limit()) return -1;
     const int pj = pro_pj(in_dim);
     const dim3 grid(n_jobs * max_groups * tiles), blk(GEMV_THREADS);
     const ExpertJob &a = jobs[0], &b2 = n_jobs > 1 ? jobs[1] : jobs[0];

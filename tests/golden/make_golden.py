@@ -33,6 +33,8 @@ CASES = [
     ("gen_tiny_k4_temp", "tiny", 0, 8192, 64, 4, 64, 0.8, 0.95, 7),
     ("gen_base_k3_greedy", "base", 1, 65536, 64, 3, 48, 0.0, 1.0, 1),
     ("gen_base_k2_temp", "base", 1, 65536, 64, 2, 32, 0.8, 0.95, 7),
+    ("gen_large_k3_greedy", "large", 3, 131072, 40, 3, 24, 0.0, 1.0, 1),     # configs[3] shape, short run
+    ("gen_server_k3_greedy", "server", 4, 8192, 48, 3, 48, 0.0, 1.0, 1),    # configs[4] model (skewed router)
 ]
 MODEL_SEED = 1234
 PROMPT_SEED = 0
@@ -49,7 +51,11 @@ def main():
         if only and name not in only:
             continue
         model = pkg.ensure_model(os.path.join(root, mdir), cid, seed=MODEL_SEED)
-        digest = hashlib.sha256(open(os.path.join(model, "model.bin"), "rb").read()).hexdigest()
+        h = hashlib.sha256()
+        with open(os.path.join(model, "model.bin"), "rb") as f:
+            for blk in iter(lambda: f.read(1 << 24), b""):
+                h.update(blk)
+        digest = h.hexdigest()
         prompt = pkg.prompt_tokens(PROMPT_SEED, n_prompt, V)
         r = OL.reference_generate(model, prompt, k, n_new, temp, topp, seed=seed)
         out = {
