@@ -57,9 +57,13 @@ typedef struct {
     Prologue pro;
 } GemvJob;
 
+// A fused GEMV launch.  The jobs' first tiles lead the struct so a block
+// finds its job with one scalar load of tile0[].
 typedef struct {
-    GemvJob job[MAX_GEMV_JOBS];
     int n;
+    int tile0[MAX_GEMV_JOBS];    // first tile of each job (set by the launcher); unused entries past n
+    int pad[3];
+    GemvJob job[MAX_GEMV_JOBS];
 } GemvBatch;
 
 // All experts of one projection (w1, w2 or w3) of a layer, stacked:

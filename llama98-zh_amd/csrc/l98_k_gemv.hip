@@ -9,8 +9,10 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv_q8(GemvBatch batch, int m
     extern __shared__ __align__(16) char smem[];
     __shared__ int s_row[M];
     __shared__ float s_inv[M], tab[32];
-    int blk = blockIdx.x, j = 0;
-    while (j + 1 < batch.n && blk >= batch.job[j + 1].tile0) j++;
+    const int blk = blockIdx.x;
+    int j = 0;
+#pragma unroll
+    for (int i = 1; i < MAX_GEMV_JOBS; i++) j += (i < batch.n && blk >= batch.tile0[i]) ? 1 : 0;
     const GemvJob &job = batch.job[j];
     const int row0 = (blk - job.tile0) * job.R;
     const int rows_here = imin(job.R, job.rows - row0);
@@ -58,6 +60,7 @@ extern "C" int l98k_gemv(GemvBatch *b, int m, hipStream_t st) {
             return -1;
         J.R = gemv_rows_per_tile(J.in_dim, M);
         J.tile0 = tiles;
+        b->tile0[j] = tiles;
         tiles += (J.rows + J.R - 1) / J.R;
         size_t l = gemv_lds_bytes(M, J.in_dim, J.R, J.pro.mode == PRO_NORM);
         lds = l > lds ? l : lds;
