@@ -133,6 +133,53 @@ def cpu_baseline(model_dir, vocab, k):
             "round_ms": round(loop_s * 1e3 / max(1, len(d['k_eff'])), 3)}
 
 
+def bench_server(args, pkg):
+    """n_seq sessions of the server model with ragged contexts
+    (uniform in [256, 2048], seed 0), k = 3.  Times the batched verify of
+    k+1 tokens per session (all sessions in flight together, one stream
+    each) and the batched greedy rounds; prints one JSON line."""
+    import numpy as np
+    mdir = os.path.join(args.model_dir, "server")
+    pkg.ensure_model(mdir, 4, seed=1234)
+    eng = pkg.Engine(mdir)
+    k, n_seq = args.k, args.sessions
+    rng = np.random.default_rng(0)
+    ctx = rng.integers(256, 2049, size=n_seq)
+    states = []
+    t0 = time.time()
+    for i in range(n_seq):
+        st = eng.add_session()
+        eng.session_start_on(st, pkg.prompt_tokens(1000 + i, int(ctx[i]), eng.V))
+        states.append(st)
+    log(f"{n_seq} sessions prefilled ({int(ctx.sum())} prompt tokens) in {time.time() - t0:.1f}s")
+    toks = np.array([[(13 * i + 7 * j + 5) % eng.V for j in range(k + 1)] for i in range(n_seq)], np.int32)
+    pos0 = ctx.astype(np.int32)
+    for _ in range(args.warmup):
+        eng.verify_batch(states, toks, pos0, copy_out=False)
+    ms = [eng.verify_batch(states, toks, pos0, copy_out=False)[0] for _ in range(args.steps)]
+    step_ms = float(np.mean(ms))
+    value = n_seq * (k + 1) / (step_ms * 1e-3)
+    # batched greedy rounds (rounds continue from each session's prefill)
+    nr = min(args.steps, 32)
+    r_ms, outs = eng.greedy_rounds_batch(states, k, nr)
+    emitted = sum(len(o) for o in outs)
+    out = {
+        "metric": f"batched verify tok/s ({n_seq} sessions x k+1={k + 1} tokens, ragged contexts 256-2048)",
+        "value": round(value, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8xint8->int32, fp32 epilogue/state",
+        "data": "synthetic (seeded random-init weights, router N(0,1) logits + N(0,0.5) expert bias; random prompts)",
+        "config": {"workload": f"configs[4] server batch: {n_seq} sessions of the configs[0]-shape model, k={k}, "
+                               f"contexts {int(ctx.min())}-{int(ctx.max())}", "sessions": n_seq, "k": k},
+        "rounds": {"rounds": nr, "wall_ms": round(r_ms, 3), "tokens": emitted,
+                   "tok_s": round(emitted / (r_ms * 1e-3), 1)},
+    }
+    print(json.dumps(out))
+    for st in states:
+        eng.free_session(st)
+    eng.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -144,6 +191,7 @@ def main():
     ap.add_argument("--model-dir", default=os.path.join(tempfile.gettempdir(), "l98_models"))
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--sessions", type=int, default=32, help="configs[4]: concurrent sessions")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs the single-sequence path on one GPU; --gpus {args.gpus} "
@@ -152,6 +200,9 @@ def main():
 
     import __graft_entry__
     pkg = __graft_entry__.load_package()
+    if args.config == 4:
+        bench_server(args, pkg)
+        return
     name = {0: "tiny", 1: "base", 3: "large"}.get(args.config, f"c{args.config}")
     mdir = os.path.join(args.model_dir, name)
     t0 = time.time()

@@ -186,6 +186,25 @@ int l98_greedy_rounds(const LZModel *m, LZRunState *s, int k, int n_rounds, int 
  * sets its verify streamed and its new_pos (for byte accounting). */
 int l98_greedy_rounds_ex(const LZModel *m, LZRunState *s, int k, int n_rounds, int use_graph, int *tokens,
                          int cap, int *n_accept_out, int *experts_out, int *new_pos_out, float *device_ms);
+/* Session batches (configs[4]'s server-style verify).  No counterpart in the
+ * reference, which keeps one sequence per LZRunState and has no batching;
+ * the reference-equivalent result is n_seq independent calls.  Each session
+ * is enqueued on its own stream and the calls return when all are done.
+ *
+ * l98_verify_batch: lz_forward_verify (src/forward.h:2060) of n_tok
+ * tokens for each of n_seq sessions of one model; session i verifies
+ * tokens[i*n_tok ..] at positions pos0[i]...  With copy_out the logits and
+ * captured hidden rows land in each state's mtp_logits / mtp_verify_hidden
+ * as lz_forward_verify leaves them.  wall_ms: host time of the batch.
+ * Returns 0, or 1 on a bad argument or a device error. */
+int l98_verify_batch(const LZModel *m, LZRunState **states, int n_seq, const int *tokens, int n_tok,
+                     const int *pos0, int copy_out, float *wall_ms);
+/* l98_greedy_rounds for n_seq sessions started with l98_session_start:
+ * n_rounds rounds each (one HIP graph launch per round and session).
+ * tokens[i*cap ..] receives session i's emitted ids, n_out[i] their count.
+ * Returns the total tokens emitted, or -LZErr. */
+int l98_greedy_rounds_batch(const LZModel *m, LZRunState **states, int n_seq, int k, int n_rounds, int *tokens,
+                            int cap, int *n_out, float *wall_ms);
 /* Mean duration of `iters` launches, hipEvent-timed on the state's stream.
  * which = 0: the tied lm_head GEMV with mrows token rows, back to back;
  * 1: the verify forward of mrows tokens; 2: a device copy of the lm_head's

@@ -108,6 +108,10 @@ HIP_API = [
     ("l98_greedy_rounds_ex", C.c_int, [C.POINTER(LZModel), C.POINTER(LZRunState), C.c_int, C.c_int, C.c_int,
                                        _IP, C.c_int, _IP, _IP, _IP, _FP]),
     ("l98_time_kernel", C.c_int, [C.POINTER(LZModel), C.POINTER(LZRunState), C.c_int, C.c_int, C.c_int, _FP]),
+    ("l98_verify_batch", C.c_int, [C.POINTER(LZModel), C.POINTER(C.POINTER(LZRunState)), C.c_int, _IP, C.c_int,
+                                   _IP, C.c_int, _FP]),
+    ("l98_greedy_rounds_batch", C.c_int, [C.POINTER(LZModel), C.POINTER(C.POINTER(LZRunState)), C.c_int, C.c_int,
+                                          C.c_int, _IP, C.c_int, _IP, _FP]),
     ("l98_device_name", C.c_char_p, []),
     ("l98_last_loop_seconds", C.c_double, []),
 ]
@@ -305,6 +309,62 @@ class Engine:
         if self.lib.l98_time_kernel(C.byref(self.m), C.byref(self.s), which, mrows, iters, C.byref(ms)) != 0:
             raise RuntimeError("l98_time_kernel failed")
         return ms.value
+
+    def add_session(self, seq_len=0, spec_k_max=LZ_SPEC_K_MAX):
+        """Another run state on the same model (an independent session)."""
+        st = LZRunState()
+        err = C.create_string_buffer(512)
+        if self.lib.lz_state_alloc(C.byref(st), C.byref(self.m), seq_len, spec_k_max, err, 512) != 0:
+            raise RuntimeError("lz_state_alloc: " + err.value.decode())
+        return st
+
+    def free_session(self, st):
+        if st.impl:
+            self.lib.lz_state_free(C.byref(st))
+
+    def session_start_on(self, st, prompt):
+        prompt = np.ascontiguousarray(prompt, np.int32)
+        r = self.lib.l98_session_start(C.byref(self.m), C.byref(st), _ip(prompt), len(prompt), None)
+        if r < 0:
+            raise RuntimeError(f"l98_session_start failed: {r}")
+        return r
+
+    def _state_ptrs(self, states):
+        arr = (C.POINTER(LZRunState) * len(states))()
+        for i, st in enumerate(states):
+            arr[i] = C.pointer(st)
+        return arr
+
+    def verify_batch(self, states, tokens, pos0, copy_out=True):
+        """l98_verify_batch; returns (wall_ms, [(logits, hidden) per session] or None)."""
+        tokens = np.ascontiguousarray(tokens, np.int32)
+        n_seq, n_tok = tokens.shape
+        pos0 = np.ascontiguousarray(pos0, np.int32)
+        ms = C.c_float()
+        rc = self.lib.l98_verify_batch(C.byref(self.m), self._state_ptrs(states), n_seq, _ip(tokens), n_tok,
+                                       _ip(pos0), 1 if copy_out else 0, C.byref(ms))
+        if rc != 0:
+            raise RuntimeError("l98_verify_batch failed")
+        if not copy_out:
+            return ms.value, None
+        out = []
+        for st in states:
+            lg = np.ctypeslib.as_array(st.mtp_logits, shape=(LZ_SPEC_K_MAX + 1, self.V))[:n_tok].copy()
+            hd = np.ctypeslib.as_array(st.mtp_verify_hidden, shape=(LZ_SPEC_K_MAX + 1, self.d))[:n_tok].copy()
+            out.append((lg, hd))
+        return ms.value, out
+
+    def greedy_rounds_batch(self, states, k, n_rounds):
+        """l98_greedy_rounds_batch; returns (wall_ms, [tokens per session])."""
+        cap = n_rounds * (k + 1)
+        toks = np.zeros((len(states), cap), np.int32)
+        n_out = np.zeros(len(states), np.int32)
+        ms = C.c_float()
+        n = self.lib.l98_greedy_rounds_batch(C.byref(self.m), self._state_ptrs(states), len(states), k, n_rounds,
+                                             _ip(toks), cap, _ip(n_out), C.byref(ms))
+        if n < 0:
+            raise RuntimeError(f"l98_greedy_rounds_batch failed: {n}")
+        return ms.value, [toks[i, :n_out[i]].copy() for i in range(len(states))]
 
     def generate(self, prompt, k, n_new, temp=0.0, topp=1.0, seed=1):
         prompt = np.ascontiguousarray(prompt, np.int32)

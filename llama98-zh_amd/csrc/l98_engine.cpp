@@ -21,6 +21,7 @@
 #include <string.h>
 #include <sys/mman.h>
 #include <sys/stat.h>
+#include <time.h>
 #include <unistd.h>
 
 #include <vector>
@@ -1580,6 +1581,130 @@ extern "C" int l98_greedy_rounds_ex(const LZModel *mm, LZRunState *s, int k, int
     if (hipMemcpy(s->mtp_chain, d->chain, sizeof(float) * d->m->c.hidden_size, hipMemcpyDeviceToHost) != hipSuccess)
         return -LZ_ERR_FORWARD;
     return n;
+}
+
+// ------------------------------------------------------ session batches ---
+//
+// Several independent sessions (one LZRunState each, as the reference keeps
+// one sequence per state) advanced together: each session's work is
+// enqueued on its own stream, interleaved, so the device runs them
+// concurrently; the host waits once for all of them.
+
+static double now_ms() {
+    timespec t;
+    clock_gettime(CLOCK_MONOTONIC, &t);
+    return t.tv_sec * 1e3 + t.tv_nsec * 1e-6;
+}
+
+static int batch_ok(const LZModel *mm, LZRunState **states, int n_seq) {
+    if (!mm || !mm->impl || !states || n_seq < 1) return 0;
+    for (int i = 0; i < n_seq; i++)
+        if (!states[i] || !states[i]->impl || S(states[i])->m != Mo(mm)) return 0;
+    return 1;
+}
+
+extern "C" int l98_verify_batch(const LZModel *mm, LZRunState **states, int n_seq, const int *tokens, int n_tok,
+                                const int *pos0, int copy_out, float *wall_ms) {
+    if (!batch_ok(mm, states, n_seq) || !tokens || !pos0 || n_tok < 1 || n_tok > LZ_BATCH_MAX) return 1;
+    const LZModelConfig &c = Mo(mm)->c;
+    for (int i = 0; i < n_seq; i++) {
+        DState *d = S(states[i]);
+        if (!tok_ok(c, tokens + (size_t)i * n_tok, n_tok) || pos0[i] < 0 || pos0[i] + n_tok > d->seq_len) return 1;
+        if (hipStreamSynchronize(d->st) != hipSuccess) return 1;
+    }
+    const double t0 = now_ms();
+    for (int i = 0; i < n_seq; i++) {
+        LZRunState *s = states[i];
+        DState *d = S(s);
+        DevCtl h = ctl_from(s);
+        h.pos_scratch = pos0[i];
+        for (int j = 0; j < n_tok; j++) h.tok[j] = tokens[(size_t)i * n_tok + j];
+        if (ctl_put(d, h)) return 1;
+        if (forward_chunk(d, d->ctl->tok, n_tok, &d->ctl->pos_scratch, 0, pos0[i] + n_tok - 1, d->vhidden, true,
+                          d->mtp_logits, false))
+            return 1;
+        s->ssm_slot = (s->ssm_slot + n_tok) % d->depth;
+    }
+    for (int i = 0; i < n_seq; i++)
+        if (hipStreamSynchronize(S(states[i])->st) != hipSuccess) return 1;
+    if (wall_ms) *wall_ms = (float)(now_ms() - t0);
+    if (copy_out) {
+        for (int i = 0; i < n_seq; i++) {
+            LZRunState *s = states[i];
+            DState *d = S(s);
+            if (hipMemcpyAsync(s->mtp_logits, d->mtp_logits, sizeof(float) * (size_t)n_tok * c.vocab_size,
+                               hipMemcpyDeviceToHost, d->st) ||
+                hipMemcpyAsync(s->mtp_verify_hidden, d->vhidden, sizeof(float) * (size_t)n_tok * c.hidden_size,
+                               hipMemcpyDeviceToHost, d->st))
+                return 1;
+        }
+        for (int i = 0; i < n_seq; i++)
+            if (hipStreamSynchronize(S(states[i])->st) != hipSuccess) return 1;
+    }
+    return 0;
+}
+
+extern "C" int l98_greedy_rounds_batch(const LZModel *mm, LZRunState **states, int n_seq, int k, int n_rounds,
+                                       int *tokens, int cap, int *n_out, float *wall_ms) {
+    if (!batch_ok(mm, states, n_seq) || n_rounds < 1 || !n_out) return -LZ_ERR_NULL_ARG;
+    for (int i = 0; i < n_seq; i++) {
+        LZRunState *s = states[i];
+        DState *d = S(s);
+        if (k < 1 || k > LZ_SPEC_K_MAX || k > s->ssm_ring_depth - 1) return -LZ_ERR_SPEC_K_RANGE;
+        if (n_rounds > d->hist_cap) return -LZ_ERR_NULL_ARG;
+        DevCtl h;
+        if (ctl_get(d, &h)) return -LZ_ERR_FORWARD;
+        if (n_rounds > rounds_that_fit(d, h, k)) return -LZ_ERR_FORWARD;
+        h.round = 0;
+        h.expert_tally = 0;
+        h.k_eff = k;
+        if (ctl_put(d, h)) return -LZ_ERR_FORWARD;
+        if (!d->round_graph[k]) {
+            hipGraph_t g = nullptr;
+            if (hipStreamBeginCapture(d->st, hipStreamCaptureModeThreadLocal) != hipSuccess) return -LZ_ERR_FORWARD;
+            int rc = enqueue_greedy_round(d, k, d->seq_len - 1, 0, true);
+            if (hipStreamEndCapture(d->st, &g) != hipSuccess || rc) return -LZ_ERR_FORWARD;
+            if (hipGraphInstantiate(&d->round_graph[k], g, nullptr, nullptr, 0) != hipSuccess) {
+                (void)hipGraphDestroy(g);
+                return -LZ_ERR_FORWARD;
+            }
+            (void)hipGraphDestroy(g);
+        }
+        if (hipStreamSynchronize(d->st) != hipSuccess) return -LZ_ERR_FORWARD;
+    }
+    const double t0 = now_ms();
+    for (int r = 0; r < n_rounds; r++)
+        for (int i = 0; i < n_seq; i++) {
+            DState *d = S(states[i]);
+            if (hipGraphLaunch(d->round_graph[k], d->st) != hipSuccess) return -LZ_ERR_FORWARD;
+        }
+    for (int i = 0; i < n_seq; i++)
+        if (hipStreamSynchronize(S(states[i])->st) != hipSuccess) return -LZ_ERR_FORWARD;
+    if (wall_ms) *wall_ms = (float)(now_ms() - t0);
+    int total = 0;
+    std::vector<RoundRec> rec((size_t)n_rounds);
+    for (int i = 0; i < n_seq; i++) {
+        LZRunState *s = states[i];
+        DState *d = S(s);
+        if (hipMemcpy(rec.data(), d->hist, sizeof(RoundRec) * rec.size(), hipMemcpyDeviceToHost) != hipSuccess)
+            return -LZ_ERR_FORWARD;
+        int n = 0;
+        for (int r = 0; r < n_rounds; r++)
+            for (int j = 0; j <= rec[r].n_accept; j++) {
+                if (tokens && n < cap) tokens[(size_t)i * cap + n] = rec[r].out[j];
+                n++;
+            }
+        n_out[i] = n;
+        total += n;
+        DevCtl h;
+        if (ctl_get(d, &h)) return -LZ_ERR_FORWARD;
+        s->ssm_slot = h.slot_base;
+        s->mtp_pos = h.mtp_pos;
+        if (hipMemcpy(s->mtp_chain, d->chain, sizeof(float) * d->m->c.hidden_size, hipMemcpyDeviceToHost) !=
+            hipSuccess)
+            return -LZ_ERR_FORWARD;
+    }
+    return total;
 }
 
 extern "C" int l98_generate(const LZModel *mm, LZRunState *s, const int *prompt, int n_prompt, int k,

@@ -1,0 +1,66 @@
+"""Session batches on the GPU (configs[4]'s server-style verify): several
+independent sessions of one model advanced together, each on its own
+stream.  Every session's results must equal what the same session gives
+alone (the reference keeps one sequence per state, so n independent
+reference runs are the specification), bit for bit against the CPU
+restatement of the reference."""
+import numpy as np
+import pytest
+
+from oracle_lib import Oracle
+from test_gpu_parity import diff_report, same_bits
+
+pytestmark = pytest.mark.gpu
+
+
+def test_verify_batch_matches_single_sessions(pkg, server):
+    print("[case] verify batch, server model, 6 sessions", flush=True)
+    eng = pkg.Engine(server)
+    lens = [17, 33, 48, 21, 60, 40]
+    states, oras = [], []
+    try:
+        for i, n in enumerate(lens):
+            st = eng.add_session()
+            prompt = pkg.prompt_tokens(100 + i, n, 8192)
+            eng.session_start_on(st, prompt)
+            states.append(st)
+            o = Oracle(server)
+            o.session_start(prompt)             # prefill; l98_session_start also captures the last token
+            o.forward_capture(prompt[-1], n - 1)
+            oras.append(o)
+        toks = np.array([[(7 * i + 3 * j + 1) % 8192 for j in range(4)] for i in range(len(lens))], np.int32)
+        pos0 = np.array(lens, np.int32)
+        _, out = eng.verify_batch(states, toks, pos0)
+        for i, (lg, hd) in enumerate(out):
+            ref = oras[i].verify(toks[i], lens[i])
+            assert same_bits(lg, ref[0]), f"session {i} verify logits: " + diff_report(lg, ref[0])
+            assert same_bits(hd, ref[1]), f"session {i} verify hidden: " + diff_report(hd, ref[1])
+    finally:
+        for st in states:
+            eng.free_session(st)
+        eng.close()
+
+
+def test_greedy_rounds_batch_matches_single_sessions(pkg, server):
+    print("[case] greedy rounds batch, server model, 5 sessions", flush=True)
+    eng = pkg.Engine(server)
+    lens = [24, 41, 30, 52, 19]
+    k, n_rounds = 3, 12
+    states, firsts = [], []
+    try:
+        for i, n in enumerate(lens):
+            st = eng.add_session()
+            prompt = pkg.prompt_tokens(200 + i, n, 8192)
+            firsts.append(eng.session_start_on(st, prompt))
+            states.append(st)
+        _, toks = eng.greedy_rounds_batch(states, k, n_rounds)
+        for i, n in enumerate(lens):
+            prompt = pkg.prompt_tokens(200 + i, n, 8192)
+            want = Oracle(server).generate(prompt, k, len(toks[i]) + 1)[0]
+            got = np.concatenate([[firsts[i]], toks[i]])
+            m = min(len(got), len(want))
+            assert m >= n_rounds and np.array_equal(got[:m], want[:m]), (i, got[:m], want[:m])
+    finally:
+        for st in states:
+            eng.free_session(st)
+        eng.close()
