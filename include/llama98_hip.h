@@ -212,6 +212,12 @@ int l98_greedy_rounds_batch(const LZModel *m, LZRunState **states, int n_seq, in
  * cache-evicting 512 MiB copy each time (only the GEMV timed).  Returns 0
  * (1 on a bad argument or a device error). */
 int l98_time_kernel(const LZModel *m, LZRunState *s, int which, int mrows, int iters, float *avg_ms);
+/* For each of `rows` rows of n (<= 2048) non-negative floats (host
+ * arrays), the float the serial loop s = 0; s += x[i] gives, computed on the
+ * device by the parallel routine the RMSNorm kernels use for their sums of
+ * squares.  No reference counterpart: a check of that routine on arbitrary
+ * inputs.  Returns 0 (1 on a bad argument or a device error). */
+int l98_row_sums(const float *x, int rows, int n, float *out);
 /* Device and build facts, for logs. */
 const char *l98_device_name(void);
 /* Seconds of device time of the last l98_generate call's round loop

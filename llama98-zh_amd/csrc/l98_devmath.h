@@ -204,6 +204,207 @@ __device__ __forceinline__ float serial_sum(const float *v, int n) {
 __device__ __forceinline__ int imin(int a, int b) { return a < b ? a : b; }
 __device__ __forceinline__ int imax(int a, int b) { return a > b ? a : b; }
 
+// ------------------------------------------- exact sums, one wave wide ---
+//
+// wave_sum_nonneg returns, on every lane of a wave, exactly the float that
+// the serial loop  s = 0; for i < n: s += v[i]  produces, for non-negative
+// v (sums of squares, sums of exponentials), in a fraction of the serial
+// loop's 8-cycle-per-add latency.
+//
+// While the running sum s stays inside one binade [2^E, 2^(E+1)), s is a
+// multiple of that binade's ulp u, and s + p rounds to s + RN(p / u) * u:
+// the rounding no longer depends on s, except for an exact tie (where the
+// parity of s / u decides) and except for the add that leaves the binade.
+// So:
+//   1. an approximate prefix sum (a wave scan) guesses, per element, the
+//      binade of the running sum before and after it;
+//   2. every element whose guess changes binade, whose p / u is a tie, or
+//      whose p is not small against the binade is "special"; every other
+//      element contributes the integer q = RN(p / u) grid steps;
+//   3. one walk over the special elements in index order does each of them
+//      as a real float add and each run of ordinary elements between two of
+//      them as one exact add of (sum of q) * u, after checking that the
+//      real running sum is in the guessed binade at the start of the run and
+//      does not pass its top at the end (s only grows, so nothing in between
+//      can leave it).  A run that fails the check is added serially.
+// The guesses only decide how much work is serial; the value is exact for
+// any guesses.  Inputs with an infinity or NaN, or more special elements
+// than the walk's table holds, take the serial loop.
+//
+// Element i sits in lane i / C, slot i % C.  rec: LDS table of 128 entries
+// for this wave.  v (16-byte aligned) holds the row in the ps_slot layout
+// below; C % 4 == 0, n <= 64 * C.
+struct PsRec {
+    float p;
+    uint32_t info;                      // binade guess | (index + 1) << 8
+    uint32_t ps;                        // sum of q before the element
+    uint32_t pad;
+};
+
+__device__ __forceinline__ int f_binade(float x) { return (int)((u_from_f(x) >> 23) & 0xFFu); }
+__device__ __forceinline__ float f_rl(float x, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l)); }
+
+// Inclusive wave scans: row prefix sums by DPP row_shr, then the row
+// carries by row_bcast:15 and row_bcast:31.  The float scan only feeds the
+// binade guesses, so its association order is free.
+#define L98_DPP_ADD(x, ctrl, rmask) \
+    (x) = (x) + __builtin_amdgcn_update_dpp(0, (x), (ctrl), (rmask), 0xF, false)
+__device__ __forceinline__ uint32_t wave_scan_u32(uint32_t v) {
+    int x = (int)v;
+    L98_DPP_ADD(x, 0x111, 0xF);
+    L98_DPP_ADD(x, 0x112, 0xF);
+    L98_DPP_ADD(x, 0x114, 0xF);
+    L98_DPP_ADD(x, 0x118, 0xF);
+    L98_DPP_ADD(x, 0x142, 0xA);
+    L98_DPP_ADD(x, 0x143, 0xC);
+    return (uint32_t)x;
+}
+#define L98_DPP_FADD(x, ctrl, rmask) \
+    (x) = (x) + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), (ctrl), (rmask), 0xF, false))
+__device__ __forceinline__ float wave_scan_f32(float x) {
+    L98_DPP_FADD(x, 0x111, 0xF);
+    L98_DPP_FADD(x, 0x112, 0xF);
+    L98_DPP_FADD(x, 0x114, 0xF);
+    L98_DPP_FADD(x, 0x118, 0xF);
+    L98_DPP_FADD(x, 0x142, 0xA);
+    L98_DPP_FADD(x, 0x143, 0xC);
+    return x;
+}
+// lane l receives lane l-1's value, lane 0 receives 0 (DPP wave_shr:1)
+__device__ __forceinline__ float wave_shr1_f32(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x138, 0xF, 0xF, false));
+}
+
+// Row layout of wave_sum_nonneg's input: element i at ps_slot<C>(i), i.e.
+// lane chunks of C floats, each followed by 4 floats of padding, so that the
+// lanes' 16-byte reads of their chunks fall in distinct LDS banks.
+template <int C>
+__host__ __device__ constexpr int ps_slot(int i) { return (i / C) * (C + 4) + i % C; }
+template <int C>
+__host__ __device__ constexpr int ps_row_floats() { return 64 * (C + 4); }
+
+// One element of the classification: from the guesses before (E0) and
+// after (E1) it, whether it is ordinary (plain) and its grid steps q.
+__device__ __forceinline__ uint32_t ps_classify(float p, int E0, int E1, uint32_t *q) {
+    const int eb = E0 > 1 ? E0 : 1;
+    const float sc = __builtin_amdgcn_ldexpf(p, 150 - eb);
+    const uint32_t tiex = u_from_f(__builtin_amdgcn_fractf(sc)) ^ 0x3F000000u;       // 0 iff a tie
+    const uint32_t cross = (uint32_t)(E0 ^ E1);
+    const uint32_t plain = (tiex < 1u ? tiex : 1u) >> (cross < 1u ? cross : 1u);   // shifts count mod 32
+    const uint32_t qq = (uint32_t)__builtin_rintf(sc);
+    *q = (qq < 0x1000001u ? qq : 0x1000001u) * plain;
+    return plain;
+}
+
+template <int C>
+__device__ float wave_sum_nonneg(const float *v, int n, PsRec *rec) {
+    static_assert(C % 4 == 0 && C <= 32, "C: multiple of 4, at most 32");
+    const int lane = threadIdx.x & 63, i0 = lane * C;
+    const float4 *vl = reinterpret_cast<const float4 *>(v + lane * (C + 4));
+    // the row holds 64 * (C + 4) floats, so no read is out of range;
+    // elements past n read as 0
+    float p[C];
+#pragma unroll
+    for (int g = 0; g < C / 4; g++) {
+        const float4 x = vl[g];
+        p[4 * g] = i0 + 4 * g < n ? x.x : 0.0f;
+        p[4 * g + 1] = i0 + 4 * g + 1 < n ? x.y : 0.0f;
+        p[4 * g + 2] = i0 + 4 * g + 2 < n ? x.z : 0.0f;
+        p[4 * g + 3] = i0 + 4 * g + 3 < n ? x.w : 0.0f;
+    }
+    float T = 0.0f;
+#pragma unroll
+    for (int c = 0; c < C; c++) T += p[c];
+    const float incl = wave_scan_f32(T);
+    const float off = wave_shr1_f32(incl);
+    // Guessed binades before and after each element.  The guess after the
+    // lane's last element is `incl` itself, so it equals the next lane's
+    // guess before its first element bit for bit.
+    int Eb[C + 1];
+    {
+        float A = off;
+        Eb[0] = f_binade(off);
+#pragma unroll
+        for (int c = 0; c < C; c++) {
+            A = (c == C - 1) ? incl : A + p[c];
+            Eb[c + 1] = f_binade(A);
+        }
+    }
+    uint32_t plain[C], q[C], cnt = 0, qs = 0;
+#pragma unroll
+    for (int c = 0; c < C; c++) {
+        plain[c] = ps_classify(p[c], Eb[c], Eb[c + 1], &q[c]);
+        cnt += 1u - plain[c];
+        qs += q[c];
+    }
+    const uint32_t cincl = wave_scan_u32(cnt);
+    const uint32_t qincl = wave_scan_u32(qs);
+    // lane sums below 2^26 keep the 32-bit scan from wrapping (64 * 2^26)
+    const bool bad = !(T <= 3.0e38f) || f_binade(incl) >= 254 || qs >= 0x4000000u;
+    // the number of special elements, counted on the scalar unit from
+    // ballots (a readlane feeding a scalar instruction stalls far longer)
+    int Kall = 0;
+#pragma unroll
+    for (int c = 0; c < C; c++) Kall += __popcll(__ballot(plain[c] == 0u));
+    const int K = Kall < 62 ? Kall : 62;
+    // Each special element's record goes to its rank; ordinary elements
+    // write their lane's spare slot 64 + lane (distinct addresses: writes to
+    // one address from many lanes would serialize).
+    {
+        uint32_t r = cincl - cnt + 1, ps = qincl - qs;
+#pragma unroll
+        for (int c = 0; c < C; c++) {
+            PsRec rc;
+            rc.p = p[c];
+            rc.info = (uint32_t)Eb[c + 1] | ((uint32_t)(i0 + c + 1) << 8);
+            rc.ps = ps;
+            rc.pad = 0u;
+            rec[plain[c] ? 64u + lane : (r < 63u ? r : 63u)] = rc;
+            r += 1u - plain[c];
+            ps += q[c];
+        }
+    }
+    if (lane == 0) { PsRec e; e.p = 0.0f; e.info = 0u; e.ps = 0u; e.pad = 0u; rec[0] = e; }
+    if (lane == 63) { PsRec e; e.p = 0.0f; e.info = (uint32_t)(n + 1) << 8; e.ps = qincl; e.pad = 0u; rec[K + 1] = e; }
+    __builtin_amdgcn_s_waitcnt(0xC07F);               // lgkmcnt(0): the table is written
+    __builtin_amdgcn_wave_barrier();
+    // Lane j: record j and the run after it.  The run may be taken in one
+    // add iff lo <= s <= hi for the running sum s after record j: lo is the
+    // guessed binade's bottom, hi the largest s with s + Qu at most the
+    // binade's top.  Lanes past the last record walk an empty step.
+    const PsRec me = rec[imin(lane, K + 1)];
+    const PsRec nx = rec[imin(lane + 1, K + 1)];
+    const int E = (int)(me.info & 255u), ia = (int)(me.info >> 8), ib = (int)(nx.info >> 8) - 1;
+    const int eb = E > 1 ? E : 1;
+    const uint32_t Q = nx.ps - me.ps;
+    const float top = __builtin_amdgcn_ldexpf(1.0f, eb - 126);
+    const float Qu0 = (float)(Q < 16777216u ? Q : 16777216u) * __builtin_amdgcn_ldexpf(1.0f, eb - 150);
+    const bool empty = ib <= ia || lane > K;
+    const float P = lane > K ? 0.0f : me.p;
+    const float lo0 = E ? __builtin_amdgcn_ldexpf(1.0f, E - 127) : 0.0f, hi0 = top - Qu0;
+    // an infeasible run (too many steps, or an empty interval) gets lo = hi
+    // = -1, which no s >= 0 passes
+    const bool feasible = Q <= 16777216u && hi0 >= lo0;
+    const float lo = empty ? 0.0f : feasible ? lo0 : -1.0f;
+    const float hi = empty ? __builtin_inff() : feasible ? hi0 : -1.0f;
+    const float Qu = empty ? 0.0f : Qu0;
+    // Fast walk, systolic: each step hands every lane its left neighbour's
+    // running sum (DPP wave_shr:1; lane 0 gets 0) and applies the lane's
+    // record, so after step j lane j holds its final value.  Then every
+    // lane checks its run: med3(s, lo, hi) == s iff lo <= s <= hi.
+    float s1 = 0.0f, sout = 0.0f;
+    for (int j = 0; j <= K; j++) {
+        s1 = wave_shr1_f32(sout) + P;
+        sout = s1 + Qu;
+    }
+    const bool fail = bad || Kall > 62 || __builtin_amdgcn_fmed3f(s1, lo, hi) != s1;
+    if (__ballot(fail) == 0) return f_rl(sout, K);
+    // Slow path: a plain serial loop.
+    float s = 0.0f;
+    for (int i = 0; i < n; i++) s += v[ps_slot<C>(i)];
+    return s;
+}
+
 // ------------------------------------------------------- rmsnorm (+q8) ---
 //
 // Row kernels hold a row of n floats in a 64-lane block as float4 f =
@@ -260,22 +461,24 @@ __device__ __forceinline__ uint32_t quant_octet(float4 v, float *sg_out) {
 }
 
 // RMSNorm(1+w) of the block's row v (lz_rmsnorm, src/ops_norm.c:690-747:
-// sum of squares serial in index order by lane 0, inv = rsqrt(ss/n + eps),
-// o = (x*inv)*(1+w)), then the optional store of o and its per-32
-// quantization.  n % 32 == 0.
+// sum of squares in index order, inv = rsqrt(ss/n + eps), o =
+// (x*inv)*(1+w)), then the optional store of o and its per-32 quantization.
+// The sum is wave_sum_nonneg's (sq: ps_row_floats<4 * PJ>() floats, rec its
+// table).  n % 32 == 0.
 template <int PJ>
 __device__ __forceinline__ void norm_row(const float4 (&v)[PJ], const float4 (&wn)[PJ], int n, float eps,
-                                         float *sq, float *s_inv, float *__restrict__ out,
+                                         float *sq, PsRec *rec, float *s_inv, float *__restrict__ out,
                                          int8_t *__restrict__ xq, float *__restrict__ xqs) {
     const int lane = threadIdx.x, nf = n >> 2;
 #pragma unroll
     for (int j = 0; j < PJ; j++) {
         const int f = lane + 64 * j;
-        if (f < nf) reinterpret_cast<float4 *>(sq)[f] =
+        if (f < nf) *reinterpret_cast<float4 *>(sq + ps_slot<4 * PJ>(4 * f)) =
             make_float4(v[j].x * v[j].x, v[j].y * v[j].y, v[j].z * v[j].z, v[j].w * v[j].w);
     }
     __syncthreads();
-    if (lane == 0) *s_inv = d_rsqrt(d_ss_over_n(serial_sum(sq, n), n) + eps);
+    const float ss = wave_sum_nonneg<4 * PJ>(sq, n, rec);
+    if (lane == 0) *s_inv = d_rsqrt(d_ss_over_n(ss, n) + eps);
     __syncthreads();
     const float inv = *s_inv;
 #pragma unroll

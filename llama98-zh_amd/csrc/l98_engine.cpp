@@ -1456,6 +1456,21 @@ extern "C" int lz_spec_round_temp(const LZModel *mm, LZRunState *s, int anchor, 
 static double g_last_loop_s = 0.0;
 extern "C" double l98_last_loop_seconds(void) { return g_last_loop_s; }
 
+extern "C" int l98_row_sums(const float *x, int rows, int n, float *out) {
+    if (!x || !out || rows < 1 || n < 1 || n > 2048) return 1;
+    float *dx = nullptr, *dout = nullptr;
+    int rc = 0;
+    if (hipMalloc(&dx, sizeof(float) * (size_t)rows * n) != hipSuccess ||
+        hipMalloc(&dout, sizeof(float) * (size_t)rows) != hipSuccess)
+        rc = 1;
+    if (!rc && hipMemcpy(dx, x, sizeof(float) * (size_t)rows * n, hipMemcpyHostToDevice) != hipSuccess) rc = 1;
+    if (!rc && l98k_row_sums(dx, rows, n, dout, nullptr)) rc = 1;
+    if (!rc && hipMemcpy(out, dout, sizeof(float) * (size_t)rows, hipMemcpyDeviceToHost) != hipSuccess) rc = 1;
+    if (dx) (void)hipFree(dx);
+    if (dout) (void)hipFree(dout);
+    return rc;
+}
+
 extern "C" const char *l98_device_name(void) {
     static char name[256];
     hipDeviceProp_t p;

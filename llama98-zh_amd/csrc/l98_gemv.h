@@ -38,10 +38,11 @@ static inline int pro_pj(int in_dim) {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 // LDS bytes of one tile: staged activations, their scales, and the larger of
-// the group sums and the RMSNorm squares.
-__host__ __device__ inline size_t gemv_lds_bytes(int m, int in_dim, int R, int norm) {
+// the group sums and the RMSNorm squares (m rows in the exact sum's layout
+// for 4 * pj elements per lane, then the four waves' walk tables).
+__host__ __device__ inline size_t gemv_lds_bytes(int m, int in_dim, int R, int norm, int pj) {
     const size_t part = (size_t)R * m * ((in_dim >> 5) + 4) * 4;
-    const size_t sq = norm ? (size_t)m * (in_dim + 4) * 4 : 0;
+    const size_t sq = norm ? (size_t)m * 64 * (4 * pj + 4) * 4 + 4 * 128 * sizeof(PsRec) : 0;
     return (size_t)m * in_dim + (size_t)((m * (in_dim >> 5) + 3) & ~3) * 4 + (part > sq ? part : sq);
 }
 
@@ -80,8 +81,8 @@ __device__ __forceinline__ void quant_rows(const float4 (&v)[RW][PJN], int wave,
 // Float prologues: wave w builds rows w and w + 4 (one float4 per lane per
 // 256 elements), so the quantization groups are lane octets.  PRO_NORM
 // (lz_rmsnorm, src/ops_norm.c:690-747, after the residual fold x += a (+ b)
-// of src/forward.c:1449-1557): the squares go to LDS and lane t of wave 0
-// walks row t's sum serially, all rows at once; the block with `writer` set
+// of src/forward.c:1449-1557): the squares go to LDS and wave w takes the
+// index-order sum of rows w and w + 4 (wave_sum_nonneg); the block with `writer` set
 // stores the updated residual and the normed rows.  PRO_SILU:
 // lz_ffn_gate_up's silu(g)*u (src/forward_kda.c:1067-1088).  PRO_COMBINE:
 // the slot-ordered weighted sum of the experts' outputs
@@ -240,7 +241,10 @@ __device__ __forceinline__ void build_rows(const Prologue &P, const int8_t *__re
                 const float4 xa = make_float4(x.x + a2.x, x.y + a2.y, x.z + a2.z, x.w + a2.w);
                 if (has_a) v[r][j] = xa;
             }
-        // rows padded by 4 floats so the summing lanes read different banks
+        // squares in the layout of the exact wave sum (4 * PJN elements per
+        // lane); wave w sums rows w and w + 4
+        constexpr int PC = 4 * PJN;
+        constexpr int rowf = ps_row_floats<PC>();
 #pragma unroll
         for (int r = 0; r < RW; r++) {
             const int t = wave + 4 * r;
@@ -249,14 +253,17 @@ __device__ __forceinline__ void build_rows(const Prologue &P, const int8_t *__re
                 const int f = lane + 64 * j;
                 if (t < nm && f < nf) {
                     const float4 x = v[r][j];
-                    reinterpret_cast<float4 *>(sq + (size_t)t * (in_dim + 4))[f] =
+                    *reinterpret_cast<float4 *>(sq + (size_t)t * rowf + ps_slot<PC>(4 * f)) =
                         make_float4(x.x * x.x, x.y * x.y, x.z * x.z, x.w * x.w);
                 }
             }
         }
         __syncthreads();
-        if (tid < nm)
-            s_inv[tid] = d_rsqrt(d_ss_over_n(serial_sum(sq + (size_t)tid * (in_dim + 4), in_dim), in_dim) + P.eps);
+        PsRec *rec = reinterpret_cast<PsRec *>(sq + (size_t)M * rowf) + wave * 128;
+        for (int t = wave; t < nm; t += 4) {
+            const float ss = wave_sum_nonneg<PC>(sq + (size_t)t * rowf, in_dim, rec);
+            if (lane == 0) s_inv[t] = d_rsqrt(d_ss_over_n(ss, in_dim) + P.eps);
+        }
         __syncthreads();
 #pragma unroll
         for (int r = 0; r < RW; r++) {

@@ -62,10 +62,13 @@ extern "C" int l98k_gemv(GemvBatch *b, int m, hipStream_t st) {
         J.tile0 = tiles;
         b->tile0[j] = tiles;
         tiles += (J.rows + J.R - 1) / J.R;
-        size_t l = gemv_lds_bytes(M, J.in_dim, J.R, J.pro.mode == PRO_NORM);
-        lds = l > lds ? l : lds;
         modes |= MB(J.pro.mode);
         if (J.pro.mode != PRO_XQ) pj = pro_pj(J.in_dim) > pj ? pro_pj(J.in_dim) : pj;
+    }
+    for (int j = 0; j < b->n; j++) {
+        const GemvJob &J = b->job[j];
+        const size_t l = gemv_lds_bytes(M, J.in_dim, J.R, J.pro.mode == PRO_NORM, pj);
+        lds = l > lds ? l : lds;
     }
     if (lds > gemv_lds_limit()) return -1;
     if (modes == MODES_X) pj = 0;
@@ -93,6 +96,6 @@ extern "C" int l98k_gemv_tiles(int rows, int in_dim, int m) {
 extern "C" int l98k_gemv_norm_fits(int in_dim, int m) {
     if (in_dim > PRO_MAX_IN || m < 1 || m > MAX_CHUNK) return 0;
     const int M = m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8;
-    return gemv_lds_bytes(M, in_dim, gemv_rows_per_tile(in_dim, M), 1) <= gemv_lds_limit();
+    return gemv_lds_bytes(M, in_dim, gemv_rows_per_tile(in_dim, M), 1, pro_pj(in_dim)) <= gemv_lds_limit();
 }
 

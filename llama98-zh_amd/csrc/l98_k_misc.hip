@@ -22,7 +22,8 @@ __global__ __launch_bounds__(64) void k_rmsnorm(float *__restrict__ x, int x_str
                                                 const float *__restrict__ w, int n, float eps,
                                                 float *__restrict__ out, int out_stride,
                                                 int8_t *__restrict__ xq, float *__restrict__ xqs) {
-    __shared__ __align__(16) float sq[256 * PJ];
+    __shared__ __align__(16) float sq[ps_row_floats<4 * PJ>()];
+    __shared__ PsRec rec[128];
     __shared__ float s_inv;
     const int row = blockIdx.x, lane = threadIdx.x, nf = n >> 2;
     float4 *xr = reinterpret_cast<float4 *>(x + (size_t)row * x_stride);
@@ -50,7 +51,7 @@ __global__ __launch_bounds__(64) void k_rmsnorm(float *__restrict__ x, int x_str
             if (lane + 64 * j < nf) xr[lane + 64 * j] = v[j];
         }
     }
-    norm_row<PJ>(v, wn, n, eps, sq, &s_inv, out ? out + (size_t)row * out_stride : nullptr,
+    norm_row<PJ>(v, wn, n, eps, sq, rec, &s_inv, out ? out + (size_t)row * out_stride : nullptr,
                  xq ? xq + (size_t)row * n : nullptr, xqs ? xqs + (size_t)row * (n >> 5) : nullptr);
 }
 
@@ -65,7 +66,8 @@ __global__ __launch_bounds__(64) void k_mtp_pre(const int8_t *__restrict__ emb_q
                                                 int d, const float *__restrict__ w_e,
                                                 const float *__restrict__ w_h, float eps,
                                                 int8_t *__restrict__ xq, float *__restrict__ xqs) {
-    __shared__ __align__(16) float sq[256 * PJ];
+    __shared__ __align__(16) float sq[ps_row_floats<4 * PJ>()];
+    __shared__ PsRec rec[128];
     __shared__ float s_inv;
     const int r = blockIdx.x, half = blockIdx.y, lane = threadIdx.x, nf = d >> 2;
     const float4 *wn4 = reinterpret_cast<const float4 *>(half == 0 ? w_e : w_h);
@@ -86,8 +88,31 @@ __global__ __launch_bounds__(64) void k_mtp_pre(const int8_t *__restrict__ emb_q
     }
 #pragma unroll
     for (int j = 0; j < PJ; j++) wn[j] = wn4[imin(lane + 64 * j, nf - 1)];
-    norm_row<PJ>(v, wn, d, eps, sq, &s_inv, nullptr, xq + (size_t)r * 2 * d + (size_t)half * d,
+    norm_row<PJ>(v, wn, d, eps, sq, rec, &s_inv, nullptr, xq + (size_t)r * 2 * d + (size_t)half * d,
                  xqs + (size_t)r * (2 * d >> 5) + (size_t)half * (d >> 5));
+}
+
+// Index-order sums of non-negative rows (wave_sum_nonneg, the sum the
+// RMSNorm kernels use), one 64-lane block per row: the library's check of
+// that routine on arbitrary inputs.
+template <int C>
+__global__ __launch_bounds__(64) void k_row_sums(const float *__restrict__ x, int n, float *__restrict__ out) {
+    __shared__ __align__(16) float row[ps_row_floats<C>()];
+    __shared__ PsRec rec[128];
+    const float *xr = x + (size_t)blockIdx.x * n;
+    for (int i = threadIdx.x; i < n; i += 64) row[ps_slot<C>(i)] = xr[i];
+    __syncthreads();
+    const float s = wave_sum_nonneg<C>(row, n, rec);
+    if (threadIdx.x == 0) out[blockIdx.x] = s;
+}
+
+extern "C" int l98k_row_sums(const float *x, int rows, int n, float *out, hipStream_t st) {
+    if (rows < 1 || n < 1 || n > 2048) return -1;
+    if (n <= 256) hipLaunchKernelGGL(k_row_sums<4>, dim3(rows), dim3(64), 0, st, x, n, out);
+    else if (n <= 512) hipLaunchKernelGGL(k_row_sums<8>, dim3(rows), dim3(64), 0, st, x, n, out);
+    else if (n <= 1024) hipLaunchKernelGGL(k_row_sums<16>, dim3(rows), dim3(64), 0, st, x, n, out);
+    else hipLaunchKernelGGL(k_row_sums<32>, dim3(rows), dim3(64), 0, st, x, n, out);
+    return (int)hipGetLastError();
 }
 
 // -------------------------------------------------------- argmax / ctl ---

@@ -286,7 +286,7 @@ extern "C" int l98k_expert_gemv(const ExpertJob *jobs, int n_jobs, const MoeGrou
     const int M = expert_m(nt);
     const int R = gemv_rows_per_tile(in_dim, M);
     const int tiles = (out_rows + R - 1) / R;
-    const size_t lds = gemv_lds_bytes(M, in_dim, R, 0);
+    const size_t lds = gemv_lds_bytes(M, in_dim, R, 0, 0);
     if (lds > gemv_lds_limit()) return -1;
     const int pj = pro_pj(in_dim);
     const dim3 grid(n_jobs * max_groups * tiles), blk(GEMV_THREADS);
@@ -305,7 +305,7 @@ extern "C" int l98k_moe_up(const ExpertJob *jobs, int n_jobs, const float *logit
     const int M = expert_m(nt);
     const int R = gemv_rows_per_tile(in_dim, M);
     const int tiles = (out_rows + R - 1) / R;
-    const size_t lds = gemv_lds_bytes(M, in_dim, R, 0);
+    const size_t lds = gemv_lds_bytes(M, in_dim, R, 0, 0);
     if (lds > gemv_lds_limit()) return -1;
     const int pj = pro_pj(in_dim);
     const dim3 grid(n_jobs * max_groups * tiles), blk(GEMV_THREADS);

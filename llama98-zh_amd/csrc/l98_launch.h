@@ -46,6 +46,7 @@ int l98k_attn(const AttnArgs *a, int nt, int max_len, float *att, hipStream_t st
 // *tally) for the down projection and the combine.
 int l98k_moe_up(const ExpertJob *jobs, int n_jobs, const float *logits, const float *bias, int E, int topk, int nt,
                 int *sel_idx, float *sel_w, MoeGroups *grp, int *tally, int in_dim, int out_rows, hipStream_t st);
+int l98k_row_sums(const float *x, int rows, int n, float *out, hipStream_t st);
 int l98k_argmax(const float *x, int n, int rows, int mode, int *out, unsigned long long *partial,
                 unsigned *counter, hipStream_t st);
 int l98k_accept(DevCtl *ctl, const float *vhidden, int d, float *chain, int depth, int brk, hipStream_t st);

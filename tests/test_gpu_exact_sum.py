@@ -1,0 +1,93 @@
+"""The parallel index-order sum the RMSNorm kernels use for their sums of
+squares (wave_sum_nonneg) against the serial float loop it replaces, on
+inputs chosen to break it: exact ties against the running sum's grid,
+binade crossings at every scale, leading zeros, denormals, powers of two
+with few mantissa bits, huge values near the float range, single spikes,
+and infinities / NaNs (which must take its serial path).  The model-level
+parity tests only see ordinary activations; these rows cover the rest."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+
+def serial_sum(x):
+    # s = 0; for v in x: s += v, in float32 (add.accumulate is sequential)
+    return np.add.accumulate(x.astype(np.float32), dtype=np.float32)[-1] if len(x) else np.float32(0)
+
+
+def rows_of(kind, n, count, rng):
+    out = np.empty((count, n), np.float32)
+    for r in range(count):
+        if kind == "squares":
+            v = rng.standard_normal(n).astype(np.float32) ** 2
+        elif kind == "wide":
+            v = (rng.standard_normal(n) * 2.0 ** rng.integers(-20, 20, n)).astype(np.float32) ** 2
+        elif kind == "ties":
+            v = (rng.integers(0, 16, n) * 0.5).astype(np.float32)
+        elif kind == "short_mantissa":
+            v = (rng.integers(0, 1024, n) / 1024.0).astype(np.float32)
+        elif kind == "leading_zeros":
+            v = rng.standard_normal(n).astype(np.float32) ** 2
+            v[: n // 2] = 0
+        elif kind == "denormal":
+            v = np.ldexp(rng.random(n), -140).astype(np.float32)
+        elif kind == "softmax_like":
+            v = np.exp(rng.standard_normal(n) * 3).astype(np.float32)
+        elif kind == "spikes":
+            v = rng.random(n).astype(np.float32)
+            hit = rng.random(n) < 0.02
+            v[hit] = np.ldexp(1.0, rng.integers(0, 30, hit.sum())).astype(np.float32)
+        elif kind == "tiny_first":
+            v = rng.standard_normal(n).astype(np.float32) ** 2
+            v[0] = 1e-30
+        elif kind == "few_bits":
+            v = np.ldexp(1.0 + rng.integers(0, 8, n) / 8.0, rng.integers(0, 6, n)).astype(np.float32)
+        elif kind == "huge":
+            v = np.ldexp(rng.random(n), 100).astype(np.float32)
+            v[rng.random(n) < 0.15] = 0
+        elif kind == "ones":
+            v = np.ones(n, np.float32)
+        elif kind == "inf":
+            v = rng.random(n).astype(np.float32)
+            v[rng.integers(0, n)] = np.inf
+        elif kind == "nan":
+            v = rng.random(n).astype(np.float32)
+            v[rng.integers(0, n)] = np.nan
+        else:
+            raise ValueError(kind)
+        out[r] = v
+    return out
+
+
+KINDS = ["squares", "wide", "ties", "short_mantissa", "leading_zeros", "denormal", "softmax_like", "spikes",
+         "tiny_first", "few_bits", "huge", "ones", "inf", "nan"]
+
+
+def test_serial_sum_is_the_float_loop():
+    rng = np.random.default_rng(5)
+    for n in (1, 7, 300):
+        x = (rng.standard_normal(n) ** 2).astype(np.float32)
+        s = np.float32(0)
+        for v in x:
+            s = np.float32(s + v)
+        assert serial_sum(x).tobytes() == s.tobytes()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n", [1, 64, 77, 256, 512, 768, 1000, 1024, 1500, 2048])
+def test_row_sums_match_serial_loop(pkg, n):
+    lib = pkg.hip_lib()
+    rng = np.random.default_rng(1000 + n)
+    rows = np.concatenate([rows_of(k, n, 24, rng) for k in KINDS])
+    out = np.zeros(len(rows), np.float32)
+    fp = C.POINTER(C.c_float)
+    assert lib.l98_row_sums(np.ascontiguousarray(rows).ctypes.data_as(fp), len(rows), n,
+                            out.ctypes.data_as(fp)) == 0
+    want = np.array([serial_sum(r) for r in rows], np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(out), nan)
+    bad = np.nonzero(out[~nan].view(np.uint32) != want[~nan].view(np.uint32))[0]
+    kinds = np.repeat(KINDS, 24)[~nan]
+    assert len(bad) == 0, f"n={n}: {len(bad)} rows differ, e.g. kind {kinds[bad[0]]}: " \
+                          f"{out[~nan][bad[0]]!r} vs {want[~nan][bad[0]]!r}"
