@@ -286,48 +286,18 @@ __device__ __forceinline__ void build_rows(const Prologue &P, const int8_t *__re
     }
 }
 
-// One GEMV tile of rows_here <= R rows.  xrow[t]: activation row of token
-// slot t (registers); s_orow[t]: output row of token slot t (LDS, read after
-// a barrier); nm: live token slots.  The caller fills the LDS exp table
-// first.
-template <int M, int PJ, int MODES>
-__device__ __forceinline__ void gemv_tile(const int8_t *__restrict__ wt, const float *__restrict__ ws, int rows_here,
-                                          int R, int in_dim, const Prologue &P, const int8_t *__restrict__ xq,
-                                          const float *__restrict__ xqs, const int (&xrow)[M], const int *s_orow,
-                                          int nm, bool writer, float *__restrict__ out, size_t out_stride,
-                                          int row0, int32_t *__restrict__ acc_out, int acc_rows, char *smem,
-                                          float *s_inv, float *tab) {
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int cpr = in_dim >> 4, nb = in_dim >> 5, pstride = nb + 4;
-    const int nchunk = rows_here * cpr;
-    int8_t *sx = reinterpret_cast<int8_t *>(smem);                                   // [M][in_dim]
-    float *sxs = reinterpret_cast<float *>(smem + (size_t)M * in_dim);                // [M][nb]
-    int *part = reinterpret_cast<int *>(sxs + ((M * nb + 3) & ~3));                   // [R][M][nb+4]
-    // weights: one 8 KiB quarter of the tile per wave, all loads in flight
-    int4 wv[GEMV_MAXJ];
-    const int er = tid / M, et = tid - er * M;
-    float wsv = 0.0f;
-    auto issue_w = [&]() {
-        const v4i *w4 = reinterpret_cast<const v4i *>(wt);
-#pragma unroll
-        for (int j = 0; j < GEMV_MAXJ; j++) {
-            const int c = imin(wave * (GEMV_WAVE_BYTES / 16) + lane + 64 * j, nchunk - 1);
-            const v4i q = __builtin_nontemporal_load(w4 + c);
-            wv[j] = make_int4(q.x, q.y, q.z, q.w);
-        }
-        wsv = ws[row0 + imin(er, rows_here - 1)];     // the epilogue lane's row scale
-    };
-    build_rows<M, PJ, MODES>(P, xq, xqs, in_dim, xrow, nm, writer, sx, sxs, reinterpret_cast<float *>(part), s_inv,
-                             tab, issue_w);
-    __syncthreads();
-    // Partial dot products.  Lane chunk j is c0 + 64 j; its (row, offset)
-    // advance by 64 chunks per step.  When cpr divides 64 every chunk of
-    // the lane sits at the same in-row offset and its activation chunks are
-    // read from LDS once.  Neighbouring lanes hold the two 16-byte halves of
-    // a 32-element group: after the pair sum (DPP) both store the same exact
-    // int32 group sum to the same slot.  Chunk steps past the tile's R rows
-    // are skipped (wave-uniform); chunks past the live rows repeat the last
-    // chunk's weights into rows the epilogue ignores.
+// Partial dot products of one tile.  Lane chunk j is c0 + 64 j; its (row,
+// offset) advance by 64 chunks per step.  When cpr divides 64 every chunk
+// of the lane sits at the same in-row offset and its activation chunks are
+// read from LDS once.  Neighbouring lanes hold the two 16-byte halves of a
+// 32-element group: after the pair sum (DPP) both store the same exact
+// int32 group sum to the same slot.  Chunk steps past the tile's R rows are
+// skipped (wave-uniform); chunks past the live rows repeat the last chunk's
+// weights into rows the epilogue ignores.
+template <int M>
+__device__ __forceinline__ void tile_dot(const int4 (&wv)[GEMV_MAXJ], const int8_t *sx, int *part, int in_dim, int R) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int cpr = in_dim >> 4, pstride = (in_dim >> 5) + 4;
     const int4 *sx4 = reinterpret_cast<const int4 *>(sx);
     const int c0 = wave * (GEMV_WAVE_BYTES / 16) + lane;
     const int q64 = 64 / cpr, m64 = 64 - q64 * cpr;
@@ -361,34 +331,86 @@ __device__ __forceinline__ void gemv_tile(const int8_t *__restrict__ wt, const f
         p += m64;
         if (p >= cpr) { p -= cpr; r++; }
     }
+}
+
+// Epilogue of one (row er, token et) pair: sum_s float(acc[s]) * xqs[s] in
+// group order, then times the row scale (src/ops_epi.c:983-1017).
+__device__ __forceinline__ float tile_epilogue(const int *pp, const float *xs, int nb, float wsv) {
+    float dot = 0.0f;
+    if ((nb & 3) == 0) {
+        // the LDS reads run up to three groups of four ahead of the
+        // dependent adds
+        const int4 *pp4 = reinterpret_cast<const int4 *>(pp);
+        const float4 *xs4 = reinterpret_cast<const float4 *>(xs);
+        const int n4 = nb >> 2;
+        int4 q0 = pp4[0], q1 = pp4[imin(1, n4 - 1)], q2 = pp4[imin(2, n4 - 1)];
+        float4 x0 = xs4[0], x1 = xs4[imin(1, n4 - 1)], x2 = xs4[imin(2, n4 - 1)];
+        for (int g = 0; g < n4; g++) {
+            const int4 q3 = pp4[imin(g + 3, n4 - 1)];
+            const float4 x3 = xs4[imin(g + 3, n4 - 1)];
+            dot += (float)q0.x * x0.x;
+            dot += (float)q0.y * x0.y;
+            dot += (float)q0.z * x0.z;
+            dot += (float)q0.w * x0.w;
+            q0 = q1; q1 = q2; q2 = q3;
+            x0 = x1; x1 = x2; x2 = x3;
+        }
+    } else {
+        for (int g = 0; g < nb; g++) dot += (float)pp[g] * xs[g];
+    }
+    float sum = 0.0f;
+    sum += dot * wsv;
+    return sum;
+}
+
+// The tile's weights: one 8 KiB quarter per wave, all loads in flight.
+__device__ __forceinline__ void tile_load(int4 (&wv)[GEMV_MAXJ], const int8_t *__restrict__ wt, int nchunk) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const v4i *w4 = reinterpret_cast<const v4i *>(wt);
+#pragma unroll
+    for (int j = 0; j < GEMV_MAXJ; j++) {
+        const int c = imin(wave * (GEMV_WAVE_BYTES / 16) + lane + 64 * j, nchunk - 1);
+        const v4i q = __builtin_nontemporal_load(w4 + c);
+        wv[j] = make_int4(q.x, q.y, q.z, q.w);
+    }
+}
+
+// One GEMV tile of rows_here <= R rows.  xrow[t]: activation row of token
+// slot t (registers); s_orow[t]: output row of token slot t (LDS, read after
+// a barrier); nm: live token slots.  The caller fills the LDS exp table
+// first.
+template <int M, int PJ, int MODES>
+__device__ __forceinline__ void gemv_tile(const int8_t *__restrict__ wt, const float *__restrict__ ws, int rows_here,
+                                          int R, int in_dim, const Prologue &P, const int8_t *__restrict__ xq,
+                                          const float *__restrict__ xqs, const int (&xrow)[M], const int *s_orow,
+                                          int nm, bool writer, float *__restrict__ out, size_t out_stride,
+                                          int row0, int32_t *__restrict__ acc_out, int acc_rows, char *smem,
+                                          float *s_inv, float *tab) {
+    const int tid = threadIdx.x;
+    const int cpr = in_dim >> 4, nb = in_dim >> 5, pstride = nb + 4;
+    const int nchunk = rows_here * cpr;
+    int8_t *sx = reinterpret_cast<int8_t *>(smem);                                   // [M][in_dim]
+    float *sxs = reinterpret_cast<float *>(smem + (size_t)M * in_dim);                // [M][nb]
+    int *part = reinterpret_cast<int *>(sxs + ((M * nb + 3) & ~3));                   // [R][M][nb+4]
+    int4 wv[GEMV_MAXJ];
+    const int er = tid / M, et = tid - er * M;
+    float wsv = 0.0f;
+    auto issue_w = [&]() {
+        tile_load(wv, wt, nchunk);
+        wsv = ws[row0 + imin(er, rows_here - 1)];     // the epilogue lane's row scale
+    };
+    build_rows<M, PJ, MODES>(P, xq, xqs, in_dim, xrow, nm, writer, sx, sxs, reinterpret_cast<float *>(part), s_inv,
+                             tab, issue_w);
     __syncthreads();
-    // Epilogue, one lane per (row, token): sum_s float(acc[s]) * xqs[s] in
-    // group order, then times the row scale (src/ops_epi.c:983-1017).
+    tile_dot<M>(wv, sx, part, in_dim, R);
+    __syncthreads();
     if (er < rows_here && et < nm) {
         const int *pp = part + (er * M + et) * pstride;
-        const float *xs = sxs + et * nb;
-        float dot = 0.0f;
-        if ((nb & 3) == 0) {
-#pragma unroll 2
-            for (int g = 0; g < nb; g += 4) {
-                const int4 q = *reinterpret_cast<const int4 *>(pp + g);
-                const float4 x4 = *reinterpret_cast<const float4 *>(xs + g);
-                dot += (float)q.x * x4.x;
-                dot += (float)q.y * x4.y;
-                dot += (float)q.z * x4.z;
-                dot += (float)q.w * x4.w;
-            }
-        } else {
-            for (int g = 0; g < nb; g++) dot += (float)pp[g] * xs[g];
-        }
-        float sum = 0.0f;
-        sum += dot * wsv;
-        out[(size_t)s_orow[et] * out_stride + row0 + er] = sum;
+        out[(size_t)s_orow[et] * out_stride + row0 + er] = tile_epilogue(pp, sxs + et * nb, nb, wsv);
         if (acc_out)
             for (int g = 0; g < nb; g++) acc_out[((size_t)et * acc_rows + row0 + er) * nb + g] = pp[g];
     }
 }
-
 
 // Dynamic LDS a GEMV block may use: the device's per-block limit (160 KiB
 // on gfx950), less room for the kernels' static LDS.  Queried once.
