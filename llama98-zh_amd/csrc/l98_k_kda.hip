@@ -5,10 +5,13 @@
 
 // ---------------------------------------------------------- KDA layer ---
 //
-// One block of 4*kd threads per head (nk == nv).  Channel phases use thread
-// j < kd for q/k channel j and v channel j of the head; the recurrence uses
-// a lane quad per state column: thread 4c + r holds rows [r*kd/4, (r+1)*kd/4)
-// of column c of the fp32 state S[kd][vd] (stored column-major per head).
+// One block of 4*kd threads per head (nk == nv).  The conv phase gives
+// thread group g = tid / kd row type g (q, k, v, output gate input) of
+// channel tid % kd for every token, the gate rows go to the groups token by
+// token, and the later channel phases use the first group; the recurrence
+// uses a lane quad per state column: thread 4c + r holds rows
+// [r*kd/4, (r+1)*kd/4) of column c of the fp32 state S[kd][vd] (stored
+// column-major per head).
 // For the chunk's tokens, in one launch:
 //   * the depthwise causal conv + SiLU of the q, k and v channels along the
 //     ring (lz_causal_conv1d_step, src/ops_conv1d.c:26-87: taps summed in
@@ -54,44 +57,38 @@ __global__ __launch_bounds__(4 * KD) void k_kda_step(KdaStepArgs a) {
     __shared__ float s_fs[MAX_CHUNK * KDA_MAX_RANK / 32];
     __shared__ float s_invq[MAX_CHUNK], s_invk[MAX_CHUNK], s_beta[MAX_CHUNK], s_kq[MAX_CHUNK],
         s_oinv[MAX_CHUNK];
+    __shared__ __align__(16) float s_z[MAX_CHUNK][KD];   // silu of the output gate input
     const int h = blockIdx.x;
     const int tid = threadIdx.x;
     const bool chan = tid < KD;
-    const int j = chan ? tid : KD - 1;     // channel of the channel phases (clamped for the others)
+    // Channel phases: thread group grp = tid / kd takes row type grp (0: q,
+    // 1: k, 2: v, 3: the output gate input) of channel j for every token, and
+    // the gate rows of tokens grp, grp + 4, ...; the later phases use the
+    // first group (chan: tid < kd, j = tid).
+    const int grp = tid / KD, j = tid - grp * KD;
     const int col = tid >> 2, quarter = tid & 3, row0 = quarter * RPL;
     const int nt = a.nt, key = a.key, value = a.value, rank = a.rank;
     const size_t head_off = (size_t)h * KD * VD;
     const int base = *a.ctl_slot;
-    // ---- loads: token inputs, gate input, conv taps and history, f_b row, state
-    const int cq = h * KD + j, ck = key + h * KD + j, cv = 2 * key + h * VD + j;   // conv channels
-    float xq[NT], xk[NT], xv[NT], gzv[NT];
+    // ---- loads: the thread's row of every token, conv taps and history,
+    // gate input, f_b row, state
+    const int cch = grp == 0 ? h * KD + j : grp == 1 ? key + h * KD + j : 2 * key + h * VD + imin(j, VD - 1);
+    const float *xsrc = grp == 0 ? a.pq : grp == 1 ? a.pk : grp == 2 ? a.pv : a.gz;
+    const int xstride = grp < 2 ? key : value;
+    float xin[NT];
 #pragma unroll
-    for (int t = 0; t < NT; t++) {
-        const int tc = imin(t, nt - 1);
-        xq[t] = a.pq[(size_t)tc * key + h * KD + j];
-        xk[t] = a.pk[(size_t)tc * key + h * KD + j];
-        xv[t] = a.pv[(size_t)tc * value + h * VD + j];
-        gzv[t] = a.gz[(size_t)tc * value + h * VD + j];
-    }
+    for (int t = 0; t < NT; t++) xin[t] = xsrc[(size_t)imin(t, nt - 1) * xstride + h * KD + j];
     const int nfa4 = nt * rank / 4;
     float4 fa4[NF4];
 #pragma unroll
     for (int u = 0; u < NF4; u++) fa4[u] = reinterpret_cast<const float4 *>(a.pfa)[imin(u * NTHR + tid, nfa4 - 1)];
-    float wq[K], wk[K], wv[K], hq[HIST > 0 ? HIST : 1], hk[HIST > 0 ? HIST : 1], hv[HIST > 0 ? HIST : 1];
+    float wc[K], hc[HIST > 0 ? HIST : 1];
 #pragma unroll
-    for (int i = 0; i < K; i++) {
-        wq[i] = a.conv_w[(size_t)cq * K + i];
-        wk[i] = a.conv_w[(size_t)ck * K + i];
-        wv[i] = a.conv_w[(size_t)cv * K + i];
-    }
+    for (int i = 0; i < K; i++) wc[i] = a.conv_w[(size_t)cch * K + i];
     {
         const float *r0 = a.conv_ring + (size_t)base * a.conv_slot_stride;
 #pragma unroll
-        for (int i = 0; i < HIST; i++) {
-            hq[i] = r0[(size_t)cq * HIST + i];
-            hk[i] = r0[(size_t)ck * HIST + i];
-            hv[i] = r0[(size_t)cv * HIST + i];
-        }
+        for (int i = 0; i < HIST; i++) hc[i] = r0[(size_t)cch * HIST + i];
     }
     const int4 *fbrow = reinterpret_cast<const int4 *>(a.fb_q + (size_t)(h * KD + j) * rank);
     int4 fbw[KDA_MAX_RANK / 16];
@@ -126,31 +123,26 @@ __global__ __launch_bounds__(4 * KD) void k_kda_step(KdaStepArgs a) {
         }
     }
     __syncthreads();                     // gate input quantized, exp table in place
-    // ---- conv, all token slots: token t reads history seq[t .. t+HIST-1]
-    // and input seq[t+HIST], seq = [ring history | the chunk's inputs]
-    float qv[NT], kv[NT], vv[NT];
+    // ---- conv + silu of the thread's row, all token slots: token t reads
+    // history seq[t .. t+HIST-1] and input seq[t+HIST], seq = [ring history |
+    // the chunk's inputs]; the output gate input only takes the silu
 #pragma unroll
     for (int t = 0; t < NT; t++) {
-        float sq = 0.0f, sk = 0.0f, sv = 0.0f;
+        float sc = 0.0f;
 #pragma unroll
         for (int i = 0; i < HIST; i++) {
             const int si = t + i;                          // position in seq
-            const float q0 = si < HIST ? hq[si < HIST ? si : 0] : xq[si >= HIST ? si - HIST : 0];
-            const float k0 = si < HIST ? hk[si < HIST ? si : 0] : xk[si >= HIST ? si - HIST : 0];
-            const float v0 = si < HIST ? hv[si < HIST ? si : 0] : xv[si >= HIST ? si - HIST : 0];
-            sq += wq[i] * q0;
-            sk += wk[i] * k0;
-            sv += wv[i] * v0;
+            sc += wc[i] * (si < HIST ? hc[si < HIST ? si : 0] : xin[si >= HIST ? si - HIST : 0]);
         }
-        sq += wq[HIST] * xq[t];
-        sk += wk[HIST] * xk[t];
-        sv += wv[HIST] * xv[t];
-        qv[t] = d_silu(sq, tab);
-        kv[t] = d_silu(sk, tab);
-        vv[t] = d_silu(sv, tab);
+        sc += wc[HIST] * xin[t];
+        const float y = d_silu(grp == 3 ? xin[t] : sc, tab);
+        if (grp == 0) { s_a[t][j] = y; s_c[t][j] = y * y; }
+        else if (grp == 1) { s_b[t][j] = y; s_d[t][j] = y * y; }
+        else if (grp == 2) { s_v[t][j] = y; }
+        else s_z[t][j] = y;
     }
     // ring: the history after token t is seq[t+1 .. t+HIST]
-    if (chan) {
+    if (grp < 3) {
 #pragma unroll
         for (int t = 0; t < NT; t++) {
             if (t < nt && (a.advance || t == nt - 1)) {
@@ -161,52 +153,41 @@ __global__ __launch_bounds__(4 * KD) void k_kda_step(KdaStepArgs a) {
 #pragma unroll
                 for (int i = 0; i < HIST; i++) {
                     const int si = t + 1 + i;
-                    r1[(size_t)cq * HIST + i] = si < HIST ? hq[si < HIST ? si : 0] : xq[si >= HIST ? si - HIST : 0];
-                    r1[(size_t)ck * HIST + i] = si < HIST ? hk[si < HIST ? si : 0] : xk[si >= HIST ? si - HIST : 0];
-                    r1[(size_t)cv * HIST + i] = si < HIST ? hv[si < HIST ? si : 0] : xv[si >= HIST ? si - HIST : 0];
+                    r1[(size_t)cch * HIST + i] = si < HIST ? hc[si < HIST ? si : 0] : xin[si >= HIST ? si - HIST : 0];
                 }
             }
         }
     }
+    // ---- gate rows of tokens grp, grp + 4, ..., then the decay gate
     const float decay = d_exp(alog, tab);
-    // ---- gate row of each token, then the decay gate
-    float gv[NT];
 #pragma unroll
-    for (int t = 0; t < NT; t++) {
-        const int tc = imin(t, nt - 1);
-        float dot = 0.0f;
+    for (int t0 = 0; t0 < NT; t0 += 4) {
+        const int t = t0 + grp;
+        if (t < NT) {
+            const int tc = imin(t, nt - 1);
+            float dot = 0.0f;
 #pragma unroll
-        for (int g = 0; g < KDA_MAX_RANK / 32; g++) {
-            if (g * 32 < rank) {
-                const int4 *xr = reinterpret_cast<const int4 *>(s_fq + tc * rank + g * 32);
-                const int4 x0 = xr[0], x1 = xr[1];
-                const int4 w0 = fbw[2 * g], w1 = fbw[2 * g + 1];
-                int acc = __builtin_amdgcn_sdot4(w0.x, x0.x, 0, false);
-                acc = __builtin_amdgcn_sdot4(w0.y, x0.y, acc, false);
-                acc = __builtin_amdgcn_sdot4(w0.z, x0.z, acc, false);
-                acc = __builtin_amdgcn_sdot4(w0.w, x0.w, acc, false);
-                acc = __builtin_amdgcn_sdot4(w1.x, x1.x, acc, false);
-                acc = __builtin_amdgcn_sdot4(w1.y, x1.y, acc, false);
-                acc = __builtin_amdgcn_sdot4(w1.z, x1.z, acc, false);
-                acc = __builtin_amdgcn_sdot4(w1.w, x1.w, acc, false);
-                dot += (float)acc * s_fs[(tc * rank >> 5) + g];
+            for (int g = 0; g < KDA_MAX_RANK / 32; g++) {
+                if (g * 32 < rank) {
+                    const int4 *xr = reinterpret_cast<const int4 *>(s_fq + tc * rank + g * 32);
+                    const int4 x0 = xr[0], x1 = xr[1];
+                    const int4 w0 = fbw[2 * g], w1 = fbw[2 * g + 1];
+                    int acc = __builtin_amdgcn_sdot4(w0.x, x0.x, 0, false);
+                    acc = __builtin_amdgcn_sdot4(w0.y, x0.y, acc, false);
+                    acc = __builtin_amdgcn_sdot4(w0.z, x0.z, acc, false);
+                    acc = __builtin_amdgcn_sdot4(w0.w, x0.w, acc, false);
+                    acc = __builtin_amdgcn_sdot4(w1.x, x1.x, acc, false);
+                    acc = __builtin_amdgcn_sdot4(w1.y, x1.y, acc, false);
+                    acc = __builtin_amdgcn_sdot4(w1.z, x1.z, acc, false);
+                    acc = __builtin_amdgcn_sdot4(w1.w, x1.w, acc, false);
+                    dot += (float)acc * s_fs[(tc * rank >> 5) + g];
+                }
             }
-        }
-        float pre = 0.0f;
-        pre += dot * fbs;
-        const float p = pre + dtb;
-        const float gg = -decay * d_softplus(p, tab);
-        gv[t] = d_exp(gg, tab);
-    }
-    if (chan) {
-#pragma unroll
-        for (int t = 0; t < NT; t++) {
-            s_g[t][j] = gv[t];
-            s_a[t][j] = qv[t];
-            s_b[t][j] = kv[t];
-            s_c[t][j] = qv[t] * qv[t];
-            s_d[t][j] = kv[t] * kv[t];
-            s_v[t][j] = vv[t];
+            float pre = 0.0f;
+            pre += dot * fbs;
+            const float p = pre + dtb;
+            const float gg = -decay * d_softplus(p, tab);
+            s_g[t][j] = d_exp(gg, tab);
         }
     }
     __syncthreads();
@@ -304,7 +285,7 @@ __global__ __launch_bounds__(4 * KD) void k_kda_step(KdaStepArgs a) {
 #pragma unroll
     for (int t = 0; t < NT; t++) {
         const int tc = imin(t, nt - 1);
-        yv[t] = s_d[tc][j] * s_oinv[tc] * onw * d_silu(gzv[t], tab);
+        yv[t] = s_d[tc][j] * s_oinv[tc] * onw * s_z[t][j];
     }
     if (chan) {
 #pragma unroll
