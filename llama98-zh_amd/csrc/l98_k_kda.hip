@@ -191,39 +191,50 @@ __global__ __launch_bounds__(4 * KD) void k_kda_step(KdaStepArgs a) {
         }
     }
     __syncthreads();
-    if (tid < nt) {                      // thread t: the token's serial norms and k.q
-        const int t = tid;
-        const float invq = d_rsqrt(serial_sum_n<KD>(s_c[t]) + 1e-6f);
-        const float invk = d_rsqrt(serial_sum_n<KD>(s_d[t]) + 1e-6f);
-        float kq = 0.0f;
-#pragma unroll 4
-        for (int i = 0; i < KD; i += 4) {
-            const float4 q4 = *reinterpret_cast<const float4 *>(&s_a[t][i]);
-            const float4 k4 = *reinterpret_cast<const float4 *>(&s_b[t][i]);
-            const float qq[4] = {q4.x, q4.y, q4.z, q4.w}, kk[4] = {k4.x, k4.y, k4.z, k4.w};
+    // Token norms (lz_l2norm at src/forward_kda.c:889-901, src/ops_norm.c:795;
+    // k.q in lz_recur_step, src/ops_gdn.c:2516-2560): lane t of the first wave sums
+    // q_t^2 and lane t of the second wave k_t^2, each in index order from a
+    // row read whole into registers; then every thread forms its elements'
+    // normalized q and k (qn = q*invq*scale, kn = k*invk) and the stored
+    // products qn*g, kn*g, kn*qn; then lane t sums kn*qn in index order.
+    if ((tid < nt) || (tid >= 64 && tid < 64 + nt)) {
+        const int t = tid & 63;
+        const float *row = tid < 64 ? s_c[t] : s_d[t];
+        float4 r4[KD / 4];
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const float qn = qq[e] * invq * a.scale;
-                const float kn = kk[e] * invk;
-                kq += kn * qn;
-            }
-        }
-        s_invq[t] = invq;
-        s_invk[t] = invk;
-        s_kq[t] = kq;
-        s_beta[t] = d_sigmoid(bv, tab);
+        for (int i = 0; i < KD / 4; i++) r4[i] = reinterpret_cast<const float4 *>(row)[i];
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < KD / 4; i++) { ss += r4[i].x; ss += r4[i].y; ss += r4[i].z; ss += r4[i].w; }
+        const float inv = d_rsqrt(ss + 1e-6f);
+        if (tid < 64) s_invq[t] = inv;
+        else s_invk[t] = inv;
     }
+    if (tid < nt) s_beta[tid] = d_sigmoid(bv, tab);
     __syncthreads();
-    if (chan) {
 #pragma unroll
-        for (int t = 0; t < NT; t++) {
+    for (int t0 = 0; t0 < NT; t0 += 4) {
+        const int t = t0 + grp;
+        if (t < NT) {
+            const int tc = imin(t, nt - 1);
             const float g = s_g[t][j];
-            const float qn = s_a[t][j] * s_invq[t] * a.scale;
-            const float kn = s_b[t][j] * s_invk[t];
+            const float qn = s_a[t][j] * s_invq[tc] * a.scale;
+            const float kn = s_b[t][j] * s_invk[tc];
             s_a[t][j] = qn * g;
             s_b[t][j] = kn;
             s_c[t][j] = kn * g;
+            s_d[t][j] = kn * qn;
         }
+    }
+    __syncthreads();
+    if (tid < nt) {
+        float4 r4[KD / 4];
+#pragma unroll
+        for (int i = 0; i < KD / 4; i++) r4[i] = reinterpret_cast<const float4 *>(s_d[tid])[i];
+        float kq = 0.0f;
+#pragma unroll
+        for (int i = 0; i < KD / 4; i++) { kq += r4[i].x; kq += r4[i].y; kq += r4[i].z; kq += r4[i].w; }
+        s_kq[tid] = kq;
     }
     __syncthreads();
     // ---- the token-serial recurrence on the lane quads
