@@ -399,9 +399,28 @@ __device__ float wave_sum_nonneg(const float *v, int n, PsRec *rec) {
     }
     const bool fail = bad || Kall > 62 || __builtin_amdgcn_fmed3f(s1, lo, hi) != s1;
     if (__ballot(fail) == 0) return f_rl(sout, K);
-    // Slow path: a plain serial loop.
+    // Slow path: the serial loop, a lane chunk at a time with the next
+    // chunk's reads in flight (elements past n read as 0).
     float s = 0.0f;
-    for (int i = 0; i < n; i++) s += v[ps_slot<C>(i)];
+    const int nch = (n + C - 1) / C;
+    float4 cur[C / 4], nxt[C / 4];
+#pragma unroll
+    for (int m = 0; m < C / 4; m++) cur[m] = reinterpret_cast<const float4 *>(v)[m];
+    for (int l = 0; l < nch; l++) {
+        const int ln = l + 1 < nch ? l + 1 : l;
+#pragma unroll
+        for (int m = 0; m < C / 4; m++) nxt[m] = reinterpret_cast<const float4 *>(v + ln * (C + 4))[m];
+#pragma unroll
+        for (int m = 0; m < C / 4; m++) {
+            const int i = l * C + 4 * m;
+            s += i < n ? cur[m].x : 0.0f;
+            s += i + 1 < n ? cur[m].y : 0.0f;
+            s += i + 2 < n ? cur[m].z : 0.0f;
+            s += i + 3 < n ? cur[m].w : 0.0f;
+        }
+#pragma unroll
+        for (int m = 0; m < C / 4; m++) cur[m] = nxt[m];
+    }
     return s;
 }
 
