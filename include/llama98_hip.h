@@ -218,6 +218,16 @@ int l98_time_kernel(const LZModel *m, LZRunState *s, int which, int mrows, int i
  * squares.  No reference counterpart: a check of that routine on arbitrary
  * inputs.  Returns 0 (1 on a bad argument or a device error). */
 int l98_row_sums(const float *x, int rows, int n, float *out);
+/* Index-order prefix queries over `rows` rows of n non-negative floats
+ * (host arrays), answered on the device by the routine the temperature
+ * sampler uses for its softmax sums and cdf scans: mode 0 gives in outv[r]
+ * the float the serial loop s = 0; s += x[i] ends with (out[r] = -1);
+ * mode 1 the first index i whose running sum exceeds c[r], mode 2 the first
+ * whose running sum reaches c[r], in out[r] with that running sum in
+ * outv[r] (-1 and the total when there is none).  No reference
+ * counterpart: a check of that routine.  Returns 0 (1 on a bad argument or
+ * a device error). */
+int l98_prefix_query(const float *x, int rows, int n, int mode, const float *c, int *out, float *outv);
 /* Device and build facts, for logs. */
 const char *l98_device_name(void);
 /* Seconds of device time of the last l98_generate call's round loop

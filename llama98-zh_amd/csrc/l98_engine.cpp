@@ -463,6 +463,17 @@ struct DState {
     hipGraphExec_t round_graph[LZ_SPEC_K_MAX + 1] = {};
     LZSampler session_samp{};               // the sampler of the current session (l98_session_start)
     bool session_greedy = true;
+    // temperature sampling scratch (allocated on first use)
+    char *smp_arena = nullptr;
+    float *smp_q = nullptr;                 // [LZ_SPEC_K_MAX][V] draft distributions of a round
+    float *smp_p = nullptr, *smp_probs = nullptr;
+    uint32_t *smp_keys = nullptr, *smp_skeys = nullptr;
+    int *smp_vals = nullptr, *smp_svals = nullptr;
+    void *smp_tmp = nullptr;
+    size_t smp_tmp_bytes = 0;
+    unsigned long long *smp_rng = nullptr;
+    int *smp_out = nullptr;                 // [16] small results
+    float *smp_outf = nullptr;              // [16]
 };
 
 namespace {
@@ -865,6 +876,7 @@ extern "C" void lz_state_free(LZRunState *s) {
     if (d) {
         if (d->st) (void)hipStreamSynchronize(d->st);
         if (d->arena) (void)hipFree(d->arena);
+        if (d->smp_arena) (void)hipFree(d->smp_arena);
         if (d->ctl_pinned) (void)hipHostFree(d->ctl_pinned);
         if (d->ev0) (void)hipEventDestroy(d->ev0);
         if (d->ev1) (void)hipEventDestroy(d->ev1);
@@ -1072,99 +1084,7 @@ float h_exp(float x) {
     float c = (C2 * w + C1) * w + C0;
     return p2n * (tab[idx] * c);
 }
-void h_softmax(float *x, int n) {                // lz_softmax float tier, src/ops_norm.c:903-990
-    float mx = x[0], sum = 0.0f;
-    uint32_t best = fkey_h(mx);
-    for (int i = 1; i < n; i++) {
-        uint32_t k = fkey_h(x[i]);
-        if (k > best) { best = k; mx = x[i]; }
-    }
-    for (int i = 0; i < n; i++) { x[i] = h_exp(x[i] - mx); sum += x[i]; }
-    float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
-    for (int i = 0; i < n; i++) x[i] *= inv;
-}
-int sample_mult(const float *p, int n, float coin) {   // src/sampler.c:159-167
-    float cdf = 0.0f;
-    for (int i = 0; i < n; i++) { cdf += p[i]; if (coin < cdf) return i; }
-    return n - 1;
-}
-struct PI { float prob; int index; };
-// select_all's descending sort (glibc qsort is a stable merge sort here):
-// stable by (prob desc, index asc).
-void sort_desc(std::vector<PI> &a) {
-    std::vector<PI> tmp(a.size());
-    size_t n = a.size();
-    for (size_t w = 1; w < n; w *= 2) {
-        for (size_t lo = 0; lo < n; lo += 2 * w) {
-            size_t mid = lo + w < n ? lo + w : n, hi = lo + 2 * w < n ? lo + 2 * w : n;
-            size_t i = lo, j = mid, k = lo;
-            while (i < mid && j < hi) tmp[k++] = (a[j].prob > a[i].prob) ? a[j++] : a[i++];
-            while (i < mid) tmp[k++] = a[i++];
-            while (j < hi) tmp[k++] = a[j++];
-        }
-        a.swap(tmp);
-    }
-}
-// select_candidates with top-k and min-p off (src/sampler.c:563-680):
-// returns the last kept index into buf, the kept mass in *mass.
-int select_topp(float *logits, int n, float temp, float topp, std::vector<PI> &buf, float *mass) {
-    float inv = 1.0f / temp;
-    for (int i = 0; i < n; i++) logits[i] *= inv;
-    h_softmax(logits, n);
-    const float cutoff = (n > 1) ? (1.0f - topp) / (float)(n - 1) : 0.0f;
-    buf.clear();
-    for (int i = 0; i < n; i++) if (logits[i] >= cutoff) buf.push_back({logits[i], i});
-    if (buf.size() > 1) sort_desc(buf);
-    if (buf.empty()) return -1;
-    int last = (int)buf.size() - 1;
-    float cum = 0.0f;
-    float limit = topp * 1.0f;
-    for (size_t i = 0; i < buf.size(); i++) {
-        cum += buf[i].prob;
-        if (cum >= limit) { last = (int)i; break; }
-    }
-    *mass = cum;
-    return last;
-}
 bool topp_active(float topp) { return topp > 0.0f && topp < 1.0f; }
-
-// lz_target_dist, top-k/min-p off (src/sampler.c:682-730)
-void target_dist(float *logits, int n, float temp, float topp, float *out_p, std::vector<PI> &buf) {
-    if (!topp_active(topp)) {
-        float inv = 1.0f / temp;
-        for (int i = 0; i < n; i++) logits[i] *= inv;
-        h_softmax(logits, n);
-        memcpy(out_p, logits, sizeof(float) * (size_t)n);
-        return;
-    }
-    memset(out_p, 0, sizeof(float) * (size_t)n);
-    float mass = 0.0f;
-    int last = select_topp(logits, n, temp, topp, buf, &mass);
-    if (last < 0) { out_p[lz_sample_argmax(logits, n)] = 1.0f; return; }
-    for (int i = 0; i <= last; i++) out_p[buf[i].index] = buf[i].prob / mass;
-}
-// lz_sample_ex for temperature > 0 with top-p (src/sampler.c:794-840)
-int sample_ex(float *logits, int n, float temp, float topp, lz_u64 *rng, std::vector<PI> &buf) {
-    if (!(temp > 0.0f)) return lz_sample_argmax(logits, n);
-    float coin = lz_random_f32(rng);
-    if (!topp_active(topp)) {
-        float inv = 1.0f / temp;
-        for (int i = 0; i < n; i++) logits[i] *= inv;
-        h_softmax(logits, n);
-        return sample_mult(logits, n, coin);
-    }
-    float mass = 0.0f;
-    int last = select_topp(logits, n, temp, topp, buf, &mass);
-    if (last < 0) return lz_sample_argmax(logits, n);
-    float r = coin * mass, cdf = 0.0f;
-    for (int i = 0; i <= last; i++) { cdf += buf[i].prob; if (r < cdf) return buf[i].index; }
-    return buf[last].index;
-}
-int sample_from_dist(const float *p, int vocab, lz_u64 *rng) {   // src/generate.c:1151-1160
-    float coin = lz_random_f32(rng), cdf = 0.0f;
-    for (int i = 0; i < vocab; i++) { cdf += p[i]; if (coin < cdf) return i; }
-    return vocab - 1;
-}
 bool penalties_on(const LZSampler *samp) {
     if (!samp) return false;
     const LZSampleParams &p = samp->p;
@@ -1356,6 +1276,82 @@ extern "C" int lz_spec_round(const LZModel *mm, LZRunState *s, int anchor, int a
     return n_accept + 1;
 }
 
+namespace {
+
+// The temperature sampling scratch of a state, carved from one allocation
+// on first use: the round's draft distributions, a target distribution, the
+// softmax and the top-p candidate keys/indices (sorted copies too), the
+// sort's scratch, the generator state and small results.
+bool smp_ensure(DState *d) {
+    if (d->smp_arena) return true;
+    const size_t V = (size_t)d->m->c.vocab_size;
+    size_t tmp = 0;
+    if (l98k_smp_sort_desc(nullptr, nullptr, nullptr, nullptr, (int)V, nullptr, &tmp, d->st)) return false;
+    size_t off = 0;
+    auto take = [&](size_t bytes) { size_t a = off; off = (off + bytes + 255) & ~(size_t)255; return a; };
+    const size_t oq = take(sizeof(float) * V * LZ_SPEC_K_MAX), op = take(sizeof(float) * V),
+                 opr = take(sizeof(float) * V), ok = take(4 * V), osk = take(4 * V), ov = take(4 * V),
+                 osv = take(4 * V), ot = take(tmp), orng = take(8), oo = take(64), oof = take(64);
+    char *a = nullptr;
+    if (hipMalloc(&a, off) != hipSuccess) return false;
+    d->smp_arena = a;
+    d->smp_q = (float *)(a + oq);
+    d->smp_p = (float *)(a + op);
+    d->smp_probs = (float *)(a + opr);
+    d->smp_keys = (uint32_t *)(a + ok);
+    d->smp_skeys = (uint32_t *)(a + osk);
+    d->smp_vals = (int *)(a + ov);
+    d->smp_svals = (int *)(a + osv);
+    d->smp_tmp = a + ot;
+    d->smp_tmp_bytes = tmp;
+    d->smp_rng = (unsigned long long *)(a + orng);
+    d->smp_out = (int *)(a + oo);
+    d->smp_outf = (float *)(a + oof);
+    return true;
+}
+
+// lz_target_dist (top-k and min-p off, src/sampler.c:682-730) of a device
+// logits row into d->smp_p: softmax(row / T), then with top-p the
+// candidates >= (1 - top_p) / (V - 1) sorted by probability (stable), the
+// prefix up to the first cumulative mass >= top_p renormalized.
+int dev_target_dist(DState *d, const float *row, int V, float temp, float topp) {
+    const float inv = 1.0f / temp;
+    if (!topp_active(topp)) return l98k_smp_softmax(row, V, inv, d->smp_p, 0.0f, nullptr, nullptr, nullptr, d->st);
+    const float cutoff = (V > 1) ? (1.0f - topp) / (float)(V - 1) : 0.0f;
+    size_t tb = d->smp_tmp_bytes;
+    if (l98k_smp_softmax(row, V, inv, d->smp_probs, cutoff, d->smp_keys, d->smp_vals, d->smp_out + 8, d->st) ||
+        l98k_smp_sort_desc(d->smp_keys, d->smp_skeys, d->smp_vals, d->smp_svals, V, d->smp_tmp, &tb, d->st))
+        return 1;
+    return l98k_smp_topp_dist(d->smp_probs, V, d->smp_skeys, d->smp_svals, d->smp_out + 8, topp, d->smp_p, d->st);
+}
+
+// lz_sample_ex for temperature > 0 (src/sampler.c:794-840) on a device
+// logits row; the generator state round-trips through the device.
+int dev_sample_ex(DState *d, const float *row, int V, float temp, float topp, lz_u64 *rng, int *tok) {
+    if (!smp_ensure(d)) return 1;
+    const float inv = 1.0f / temp;
+    if (hipMemcpyAsync(d->smp_rng, rng, sizeof(lz_u64), hipMemcpyHostToDevice, d->st)) return 1;
+    if (!topp_active(topp)) {
+        if (l98k_smp_softmax(row, V, inv, d->smp_probs, 0.0f, nullptr, nullptr, nullptr, d->st) ||
+            l98k_smp_draw(d->smp_probs, V, d->smp_rng, d->smp_out, nullptr, nullptr, d->st))
+            return 1;
+    } else {
+        const float cutoff = (V > 1) ? (1.0f - topp) / (float)(V - 1) : 0.0f;
+        size_t tb = d->smp_tmp_bytes;
+        if (l98k_smp_softmax(row, V, inv, d->smp_probs, cutoff, d->smp_keys, d->smp_vals, d->smp_out + 8, d->st) ||
+            l98k_smp_sort_desc(d->smp_keys, d->smp_skeys, d->smp_vals, d->smp_svals, V, d->smp_tmp, &tb, d->st) ||
+            l98k_smp_sample_topp(d->smp_probs, V, d->smp_skeys, d->smp_svals, d->smp_out + 8, topp, d->smp_rng,
+                                 d->smp_out, d->st))
+            return 1;
+    }
+    if (hipMemcpyAsync(tok, d->smp_out, sizeof(int), hipMemcpyDeviceToHost, d->st) ||
+        hipMemcpyAsync(rng, d->smp_rng, sizeof(lz_u64), hipMemcpyDeviceToHost, d->st) || hipStreamSynchronize(d->st))
+        return 1;
+    return 0;
+}
+
+}  // namespace
+
 extern "C" int lz_spec_round_temp(const LZModel *mm, LZRunState *s, int anchor, int anchor_pos, int k,
                                   float p_min, int n_min, LZSampler *samp, int brk, int skipc,
                                   int *out, int *out_n_accept, int *out_new_pos, int *out_k_eff,
@@ -1378,27 +1374,30 @@ extern "C" int lz_spec_round_temp(const LZModel *mm, LZRunState *s, int anchor, 
     DevCtl h = ctl_from(s);
     h.anchor = anchor; h.anchor_pos = anchor_pos; h.tok[0] = anchor;
     if (ctl_put(d, h)) return -LZ_ERR_FORWARD;
-    std::vector<float> q((size_t)k * V), row(V), p(V);
-    std::vector<PI> buf;
+    if (!smp_ensure(d) ||
+        hipMemcpyAsync(d->smp_rng, &samp->rng_state, sizeof(lz_u64), hipMemcpyHostToDevice, d->st))
+        return -LZ_ERR_FORWARD;
     int draft[LZ_SPEC_K_MAX], k_eff = 0;
+    const float inv = 1.0f / temp;
     for (int i = 0; i < k; i++) {
         if (draft_step(d, d->ctl->tok + i, &d->ctl->mtp_pos, i, s->mtp_pos + k, d->draft_logits, nullptr))
             return -LZ_ERR_FORWARD;
-        float *lg = q.data() + (size_t)i * V;
-        if (hipMemcpyAsync(lg, d->draft_logits, sizeof(float) * V, hipMemcpyDeviceToHost, d->st) ||
+        // lz_sample_temp_q (src/sampler.c:736-747): q = softmax(logits/T),
+        // then the multinomial draw; the draw also becomes the next draft
+        // step's input token
+        float *qi = d->smp_q + (size_t)i * V;
+        int idx = 0;
+        float qidx = 0.0f;
+        if (l98k_smp_softmax(d->draft_logits, V, inv, qi, 0.0f, nullptr, nullptr, nullptr, d->st) ||
+            l98k_smp_draw(qi, V, d->smp_rng, d->smp_out, d->smp_outf, d->ctl->tok + 1 + i, d->st) ||
+            hipMemcpyAsync(&idx, d->smp_out, sizeof(int), hipMemcpyDeviceToHost, d->st) ||
+            hipMemcpyAsync(&qidx, d->smp_outf, sizeof(float), hipMemcpyDeviceToHost, d->st) ||
             hipStreamSynchronize(d->st))
             return -LZ_ERR_FORWARD;
-        // lz_sample_temp_q (src/sampler.c:736-747): q = softmax(logits/T) in place
-        float inv = 1.0f / temp;
-        for (int j = 0; j < V; j++) lg[j] *= inv;
-        h_softmax(lg, V);
-        int idx = sample_mult(lg, V, lz_random_f32(&samp->rng_state));
-        if (lg[idx] < p_min) break;
+        if (qidx < p_min) break;
         draft[i] = idx;
         h.tok[1 + i] = idx;
         k_eff = i + 1;
-        if (hipMemcpyAsync(d->ctl->tok + 1 + i, &idx, sizeof(int), hipMemcpyHostToDevice, d->st))
-            return -LZ_ERR_FORWARD;
     }
     if (k_eff < n_min) {
         out[0] = anchor; *out_n_accept = 0; *out_new_pos = anchor_pos; *out_k_eff = k_eff;
@@ -1408,25 +1407,28 @@ extern "C" int lz_spec_round_temp(const LZModel *mm, LZRunState *s, int anchor, 
     if (forward_chunk(d, d->ctl->tok, k_eff + 1, &d->ctl->anchor_pos, 1, anchor_pos + k_eff + 1,
                       d->vhidden, true, d->mtp_logits, false))
         return -LZ_ERR_FORWARD;
-    std::vector<float> logits((size_t)(k_eff + 1) * V);
-    if (hipMemcpyAsync(logits.data(), d->mtp_logits, sizeof(float) * logits.size(), hipMemcpyDeviceToHost, d->st) ||
-        hipStreamSynchronize(d->st))
-        return -LZ_ERR_FORWARD;
+    // acceptance on the device (lz_spec_accept_temp, src/generate.c:283-346):
+    // the target distribution of each verify row, then u, then the residual
+    // draw on a rejection; the bonus draw when every draft is accepted
     int n_accept = k_eff;
     for (int i = 0; i < k_eff; i++) {
-        float *rw = logits.data() + (size_t)i * V;
-        target_dist(rw, V, temp, topp, p.data(), buf);
-        float u = lz_random_f32(&samp->rng_state);
-        int acc = 0;
-        int tok = lz_spec_accept_temp(p.data(), q.data() + (size_t)i * V, draft[i], V, u, &samp->rng_state, &acc);
-        out[i] = tok;
-        if (!acc) { n_accept = i; break; }
+        int res[2] = {0, 0};
+        if (dev_target_dist(d, d->mtp_logits + (size_t)i * V, V, temp, topp) ||
+            l98k_smp_accept(d->smp_p, d->smp_q + (size_t)i * V, V, draft[i], d->smp_rng, d->smp_out, d->st) ||
+            hipMemcpyAsync(res, d->smp_out, sizeof(res), hipMemcpyDeviceToHost, d->st) || hipStreamSynchronize(d->st))
+            return -LZ_ERR_FORWARD;
+        out[i] = res[0];
+        if (!res[1]) { n_accept = i; break; }
     }
     if (n_accept == k_eff) {
-        float *rw = logits.data() + (size_t)k_eff * V;
-        target_dist(rw, V, temp, topp, p.data(), buf);
-        out[k_eff] = sample_from_dist(p.data(), V, &samp->rng_state);
+        if (dev_target_dist(d, d->mtp_logits + (size_t)k_eff * V, V, temp, topp) ||
+            l98k_smp_draw(d->smp_p, V, d->smp_rng, d->smp_out, nullptr, nullptr, d->st) ||
+            hipMemcpyAsync(out + k_eff, d->smp_out, sizeof(int), hipMemcpyDeviceToHost, d->st))
+            return -LZ_ERR_FORWARD;
     }
+    if (hipMemcpyAsync(&samp->rng_state, d->smp_rng, sizeof(lz_u64), hipMemcpyDeviceToHost, d->st) ||
+        hipStreamSynchronize(d->st))
+        return -LZ_ERR_FORWARD;
     s->ssm_slot = (base + k_eff + 1) % d->depth;
     if (n_accept < k_eff && !brk) s->ssm_slot = (base + n_accept + 1) % d->depth;
     // reseed the chain from the accepted row; catch-up
@@ -1471,6 +1473,24 @@ extern "C" int l98_row_sums(const float *x, int rows, int n, float *out) {
     return rc;
 }
 
+extern "C" int l98_prefix_query(const float *x, int rows, int n, int mode, const float *c, int *out, float *outv) {
+    if (!x || !out || !outv || rows < 1 || n < 1 || mode < 0 || mode > 2 || (mode && !c)) return 1;
+    float *dx = nullptr, *dc = nullptr, *dv = nullptr;
+    int *dout = nullptr, rc = 0;
+    if (hipMalloc(&dx, sizeof(float) * (size_t)rows * n) != hipSuccess || hipMalloc(&dc, sizeof(float) * rows) != hipSuccess ||
+        hipMalloc(&dv, sizeof(float) * rows) != hipSuccess || hipMalloc(&dout, sizeof(int) * rows) != hipSuccess)
+        rc = 1;
+    if (!rc && hipMemcpy(dx, x, sizeof(float) * (size_t)rows * n, hipMemcpyHostToDevice) != hipSuccess) rc = 1;
+    if (!rc && mode && hipMemcpy(dc, c, sizeof(float) * rows, hipMemcpyHostToDevice) != hipSuccess) rc = 1;
+    if (!rc && l98k_smp_xprefix(dx, rows, n, mode, mode ? dc : nullptr, dout, dv, nullptr)) rc = 1;
+    if (!rc && (hipMemcpy(out, dout, sizeof(int) * rows, hipMemcpyDeviceToHost) != hipSuccess ||
+                hipMemcpy(outv, dv, sizeof(float) * rows, hipMemcpyDeviceToHost) != hipSuccess))
+        rc = 1;
+    for (void *q : {(void *)dx, (void *)dc, (void *)dv, (void *)dout})
+        if (q) (void)hipFree(q);
+    return rc;
+}
+
 extern "C" const char *l98_device_name(void) {
     static char name[256];
     hipDeviceProp_t p;
@@ -1503,11 +1523,11 @@ extern "C" int l98_session_start(const LZModel *mm, LZRunState *s, const int *pr
     // first anchor from a capture forward
     float *lg = lz_forward_capture(mm, s, prompt[n_prompt - 1], n_prompt - 1);
     if (!lg) return -LZ_ERR_FORWARD;
-    std::vector<PI> buf;
-    int anchor = d->session_greedy
-        ? lz_sample_argmax(lg, c.vocab_size)
-        : sample_ex(lg, c.vocab_size, d->session_samp.p.temperature, d->session_samp.p.topp,
-                    &d->session_samp.rng_state, buf);
+    int anchor = 0;
+    if (d->session_greedy) anchor = lz_sample_argmax(lg, c.vocab_size);
+    else if (dev_sample_ex(d, d->logits, c.vocab_size, d->session_samp.p.temperature, d->session_samp.p.topp,
+                           &d->session_samp.rng_state, &anchor))
+        return -LZ_ERR_FORWARD;
     DevCtl h = ctl_from(s);
     h.anchor = anchor;
     h.anchor_pos = n_prompt - 1;

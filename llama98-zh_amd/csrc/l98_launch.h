@@ -1,4 +1,4 @@
-// Host-side launchers of the gfx950 kernels (l98_kernels.hip).  Each returns
+// Host-side launchers of the gfx950 kernels (l98_k_*.hip).  Each returns
 // 0, a HIP error code, or -1 when the arguments do not fit the kernel's
 // shape limits (checked on the host before any launch).
 #ifndef L98_LAUNCH_H
@@ -15,6 +15,30 @@ int l98k_upload_exp_table_gemv(const float *tab);
 int l98k_upload_exp_table_moe(const float *tab);
 int l98k_upload_exp_table_kda(const float *tab);
 int l98k_upload_exp_table_attn(const float *tab);
+int l98k_upload_exp_table_smp(const float *tab);
+// Temperature sampling (one block per call; l98_k_sample.hip).
+// probs = softmax(logits * inv_t); with keys: the top-p candidate keys and
+// indices for l98k_smp_sort_desc and their count.
+int l98k_smp_softmax(const float *logits, int n, float inv_t, float *probs, float cutoff, uint32_t *keys, int *vals,
+                     int *n_cand, hipStream_t st);
+// A draw from p by the cdf (rng advanced on the device); ctl_tok optional.
+int l98k_smp_draw(const float *p, int n, unsigned long long *rng, int *out_tok, float *out_p, int *ctl_tok,
+                  hipStream_t st);
+// Stable descending (key, index) sort; tmp == nullptr sizes the scratch.
+int l98k_smp_sort_desc(const uint32_t *keys, uint32_t *keys_out, const int *vals, int *vals_out, int n, void *tmp,
+                       size_t *tmp_bytes, hipStream_t st);
+// Top-p target distribution from the softmax and the sorted candidates.
+int l98k_smp_topp_dist(const float *probs, int n, const uint32_t *skeys, const int *svals, const int *n_cand,
+                       float topp, float *p_out, hipStream_t st);
+// Speculative acceptance of draft x with residual resampling: out[0] token, out[1] accepted.
+int l98k_smp_accept(const float *p, const float *q, int n, int x, unsigned long long *rng, int *out, hipStream_t st);
+// lz_sample_ex's top-p draw after the candidate sort.
+int l98k_smp_sample_topp(const float *probs, int n, const uint32_t *skeys, const int *svals, const int *n_cand,
+                         float topp, unsigned long long *rng, int *out_tok, hipStream_t st);
+// Exact index-order prefix queries over rows of n (mode 0 total, 1 first
+// prefix > c, 2 first prefix >= c): out = index (-1 none), outv = value.
+int l98k_smp_xprefix(const float *x, int rows, int n, int mode, const float *c, int *out, float *outv,
+                     hipStream_t st);
 // Fused GEMV of b->n jobs over m <= MAX_CHUNK activation rows; each job's
 // prologue builds its int8 input rows.
 int l98k_gemv(GemvBatch *b, int m, hipStream_t st);

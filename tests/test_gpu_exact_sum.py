@@ -91,3 +91,48 @@ def test_row_sums_match_serial_loop(pkg, n):
     kinds = np.repeat(KINDS, 24)[~nan]
     assert len(bad) == 0, f"n={n}: {len(bad)} rows differ, e.g. kind {kinds[bad[0]]}: " \
                           f"{out[~nan][bad[0]]!r} vs {want[~nan][bad[0]]!r}"
+
+
+def serial_prefix(x):
+    return np.add.accumulate(x.astype(np.float32), dtype=np.float32)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n", [1, 100, 1024, 5000, 32000, 65536, 131072])
+def test_prefix_queries_match_serial_loop(pkg, n):
+    """The sampler's engine (one block per row over global memory): totals,
+    first prefix above a coin, first prefix reaching a limit."""
+    lib = pkg.hip_lib()
+    rng = np.random.default_rng(77 + n)
+    kinds = [k for k in KINDS if k not in ("inf", "nan")]
+    per = 2 if n >= 32000 else 4
+    rows = np.concatenate([rows_of(k, n, per, rng) for k in kinds])
+    pre = np.stack([serial_prefix(r) for r in rows])
+    tot = pre[:, -1]
+    fp, ip = C.POINTER(C.c_float), C.POINTER(C.c_int)
+    xs = np.ascontiguousarray(rows)
+    for mode in (0, 1, 2):
+        # thresholds inside the range, at exact prefix values, and past the end
+        c = np.empty(len(rows), np.float32)
+        for r in range(len(rows)):
+            pick = rng.integers(0, 3)
+            if pick == 0:
+                c[r] = np.float32(tot[r] * rng.random())
+            elif pick == 1:
+                c[r] = pre[r, rng.integers(0, n)]
+            else:
+                c[r] = np.float32(tot[r] * 2 + 1)
+        out = np.zeros(len(rows), np.int32)
+        outv = np.zeros(len(rows), np.float32)
+        assert lib.l98_prefix_query(xs.ctypes.data_as(fp), len(rows), n, mode, c.ctypes.data_as(fp),
+                                    out.ctypes.data_as(ip), outv.ctypes.data_as(fp)) == 0
+        for r in range(len(rows)):
+            if mode == 0:
+                want_i, want_v = -1, tot[r]
+            else:
+                hit = np.nonzero(c[r] < pre[r] if mode == 1 else pre[r] >= c[r])[0]
+                want_i = int(hit[0]) if len(hit) else -1
+                want_v = pre[r, want_i] if len(hit) else tot[r]
+            assert out[r] == want_i, f"n={n} mode={mode} row {r}: index {out[r]} vs {want_i}"
+            assert outv[r].tobytes() == np.float32(want_v).tobytes(), \
+                f"n={n} mode={mode} row {r}: {outv[r]!r} vs {want_v!r}"
