@@ -1138,34 +1138,37 @@ extern "C" int lz_spec_accept(const int *draft, const int *targ, int n_draft, in
     return n_draft;
 }
 
-static int sample_residual(const float *p, const float *q, int vocab, lz_u64 *rng) {
-    float total = 0.0f, coin, cdf = 0.0f;                       // src/generate.c:261-281
-    int last_pos = -1;
-    for (int i = 0; i < vocab; i++) {
-        float dd = p[i] - q[i];
-        if (dd > 0.0f) { total += dd; last_pos = i; }
-    }
-    if (total <= 0.0f) return lz_sample_argmax(p, vocab);
-    coin = lz_random_f32(rng) * total;
-    for (int i = 0; i < vocab; i++) {
-        float dd = p[i] - q[i];
-        if (dd > 0.0f) { cdf += dd; if (coin < cdf) return i; }
-    }
-    return last_pos;
-}
-
 extern "C" int lz_spec_accept_temp(const float *p, const float *q, int x, int vocab, float u,
                                    lz_u64 *rng, int *out_accepted) {
     if (!p || !q || !rng || vocab <= 0 || x < 0 || x >= vocab) {   // src/generate.c:283-346
         if (out_accepted) *out_accepted = 0;
         return -1;
     }
-    float qx = q[x], ratio;
-    if (qx <= 0.0f) ratio = 0.0f;
-    else { ratio = p[x] / qx; if (ratio > 1.0f) ratio = 1.0f; }
-    if (u < ratio) { if (out_accepted) *out_accepted = 1; return x; }
-    if (out_accepted) *out_accepted = 0;
-    return sample_residual(p, q, vocab, rng);
+    // the host rows go to the device and through the round's acceptance
+    // kernel (with this u); the generator state comes back
+    float *dp = nullptr, *dq = nullptr;
+    unsigned long long *drng = nullptr;
+    int *dout = nullptr, res[2] = {-1, 0}, rc = 0;
+    if (hipMalloc(&dp, sizeof(float) * (size_t)vocab) != hipSuccess ||
+        hipMalloc(&dq, sizeof(float) * (size_t)vocab) != hipSuccess ||
+        hipMalloc(&drng, sizeof(*drng)) != hipSuccess || hipMalloc(&dout, sizeof(res)) != hipSuccess)
+        rc = 1;
+    if (!rc && (hipMemcpy(dp, p, sizeof(float) * (size_t)vocab, hipMemcpyHostToDevice) != hipSuccess ||
+                hipMemcpy(dq, q, sizeof(float) * (size_t)vocab, hipMemcpyHostToDevice) != hipSuccess ||
+                hipMemcpy(drng, rng, sizeof(*drng), hipMemcpyHostToDevice) != hipSuccess))
+        rc = 1;
+    if (!rc && l98k_smp_accept(dp, dq, vocab, x, &u, drng, dout, nullptr)) rc = 1;
+    if (!rc && (hipMemcpy(res, dout, sizeof(res), hipMemcpyDeviceToHost) != hipSuccess ||
+                hipMemcpy(rng, drng, sizeof(*drng), hipMemcpyDeviceToHost) != hipSuccess))
+        rc = 1;
+    for (void *m : {(void *)dp, (void *)dq, (void *)drng, (void *)dout})
+        if (m) (void)hipFree(m);
+    if (rc) {
+        if (out_accepted) *out_accepted = 0;
+        return -1;
+    }
+    if (out_accepted) *out_accepted = res[1];
+    return res[0];
 }
 
 // ------------------------------------------------------------- rounds ---
@@ -1414,7 +1417,7 @@ extern "C" int lz_spec_round_temp(const LZModel *mm, LZRunState *s, int anchor, 
     for (int i = 0; i < k_eff; i++) {
         int res[2] = {0, 0};
         if (dev_target_dist(d, d->mtp_logits + (size_t)i * V, V, temp, topp) ||
-            l98k_smp_accept(d->smp_p, d->smp_q + (size_t)i * V, V, draft[i], d->smp_rng, d->smp_out, d->st) ||
+            l98k_smp_accept(d->smp_p, d->smp_q + (size_t)i * V, V, draft[i], nullptr, d->smp_rng, d->smp_out, d->st) ||
             hipMemcpyAsync(res, d->smp_out, sizeof(res), hipMemcpyDeviceToHost, d->st) || hipStreamSynchronize(d->st))
             return -LZ_ERR_FORWARD;
         out[i] = res[0];

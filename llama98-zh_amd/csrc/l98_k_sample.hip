@@ -447,12 +447,13 @@ __global__ __launch_bounds__(SMP_THREADS) void k_smp_topp_dist(const float *__re
     for (int j = tid; j <= last; j += SMP_THREADS) p_out[svals[j]] = __uint_as_float(skeys[j]) / mass;
 }
 
-// lz_spec_accept_temp on device rows: u = rng; accept x iff u < min(1,
+// lz_spec_accept_temp on device rows: u (given, or drawn); accept x iff u < min(1,
 // p[x]/q[x]); otherwise the residual draw over max(p - q, 0) (argmax of p
 // when its mass is 0; the last positive index when no cdf passes the coin).
 // out[0] = token, out[1] = accepted.
 __global__ __launch_bounds__(SMP_THREADS) void k_smp_accept(const float *__restrict__ p, const float *__restrict__ q,
-                                                            int n, int x, unsigned long long *__restrict__ rng,
+                                                            int n, int x, float u_in, int have_u,
+                                                            unsigned long long *__restrict__ rng,
                                                             int *__restrict__ out) {
     __shared__ SmpLds L;
     const int tid = threadIdx.x;
@@ -461,7 +462,7 @@ __global__ __launch_bounds__(SMP_THREADS) void k_smp_accept(const float *__restr
         float ratio;
         if (qx <= 0.0f) ratio = 0.0f;
         else { ratio = p[x] / qx; if (ratio > 1.0f) ratio = 1.0f; }
-        const float u = d_random_f32(rng);
+        const float u = have_u ? u_in : d_random_f32(rng);
         L.iv = u < ratio ? 1 : 0;
     }
     __syncthreads();
@@ -559,10 +560,10 @@ extern "C" int l98k_smp_topp_dist(const float *probs, int n, const uint32_t *ske
     return (int)hipGetLastError();
 }
 
-extern "C" int l98k_smp_accept(const float *p, const float *q, int n, int x, unsigned long long *rng, int *out,
-                               hipStream_t st) {
+extern "C" int l98k_smp_accept(const float *p, const float *q, int n, int x, const float *u, unsigned long long *rng,
+                               int *out, hipStream_t st) {
     if (n < 1 || x < 0 || x >= n) return -1;
-    hipLaunchKernelGGL(k_smp_accept, dim3(1), dim3(SMP_THREADS), 0, st, p, q, n, x, rng, out);
+    hipLaunchKernelGGL(k_smp_accept, dim3(1), dim3(SMP_THREADS), 0, st, p, q, n, x, u ? *u : 0.0f, u ? 1 : 0, rng, out);
     return (int)hipGetLastError();
 }
 

@@ -30,8 +30,10 @@ int l98k_smp_sort_desc(const uint32_t *keys, uint32_t *keys_out, const int *vals
 // Top-p target distribution from the softmax and the sorted candidates.
 int l98k_smp_topp_dist(const float *probs, int n, const uint32_t *skeys, const int *svals, const int *n_cand,
                        float topp, float *p_out, hipStream_t st);
-// Speculative acceptance of draft x with residual resampling: out[0] token, out[1] accepted.
-int l98k_smp_accept(const float *p, const float *q, int n, int x, unsigned long long *rng, int *out, hipStream_t st);
+// Speculative acceptance of draft x with residual resampling (u given, or
+// drawn when u is null): out[0] token, out[1] accepted.
+int l98k_smp_accept(const float *p, const float *q, int n, int x, const float *u, unsigned long long *rng, int *out,
+                    hipStream_t st);
 // lz_sample_ex's top-p draw after the candidate sort.
 int l98k_smp_sample_topp(const float *probs, int n, const uint32_t *skeys, const int *svals, const int *n_cand,
                          float topp, unsigned long long *rng, int *out_tok, hipStream_t st);

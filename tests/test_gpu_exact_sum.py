@@ -136,3 +136,42 @@ def test_prefix_queries_match_serial_loop(pkg, n):
             assert out[r] == want_i, f"n={n} mode={mode} row {r}: index {out[r]} vs {want_i}"
             assert outv[r].tobytes() == np.float32(want_v).tobytes(), \
                 f"n={n} mode={mode} row {r}: {outv[r]!r} vs {want_v!r}"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("V", [16, 65536])
+def test_spec_accept_temp_on_device_matches_oracle(pkg, V):
+    """The library's lz_spec_accept_temp (host rows through the device
+    acceptance kernel) against the oracle's restatement: u just below, at and
+    above p[x]/q[x], a rejected draft's residual draw and the generator
+    state it leaves, and q[x] = 0."""
+    import oracle_lib as OL
+    O = OL.lib()
+    lib = pkg.hip_lib()
+    lib.lz_spec_accept_temp.restype = C.c_int
+    lib.lz_spec_accept_temp.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_float,
+                                        C.POINTER(C.c_uint64), C.POINTER(C.c_int)]
+    fp = C.POINTER(C.c_float)
+    rng = np.random.default_rng(V)
+    p = rng.dirichlet(np.ones(V)).astype(np.float32)
+    q = rng.dirichlet(np.ones(V)).astype(np.float32)
+    xs = range(V) if V <= 16 else rng.integers(0, V, 12)
+    for x in xs:
+        x = int(x)
+        ratio = np.float32(p[x] / q[x])
+        for u in (np.nextafter(ratio, np.float32(0)), ratio, np.nextafter(ratio, np.float32(2))):
+            u = np.float32(min(u, np.float32(0.999999)))
+            st, st2 = C.c_uint64(12345), C.c_uint64(12345)
+            acc, acc2 = C.c_int(), C.c_int()
+            tok = O.o_spec_accept_temp(p.ctypes.data_as(fp), q.ctypes.data_as(fp), x, V, float(u), C.byref(st),
+                                       C.byref(acc))
+            t2 = lib.lz_spec_accept_temp(p.ctypes.data, q.ctypes.data, x, V, C.c_float(u), C.byref(st2),
+                                         C.byref(acc2))
+            assert (t2, acc2.value, st2.value) == (tok, acc.value, st.value), (x, u)
+    q0 = q.copy()
+    q0[3] = 0.0
+    st, st2 = C.c_uint64(1), C.c_uint64(1)
+    acc, acc2 = C.c_int(), C.c_int()
+    tok = O.o_spec_accept_temp(p.ctypes.data_as(fp), q0.ctypes.data_as(fp), 3, V, 0.0, C.byref(st), C.byref(acc))
+    t2 = lib.lz_spec_accept_temp(p.ctypes.data, q0.ctypes.data, 3, V, C.c_float(0.0), C.byref(st2), C.byref(acc2))
+    assert (t2, acc2.value, st2.value) == (tok, acc.value, st.value)
