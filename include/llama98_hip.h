@@ -228,6 +228,15 @@ int l98_row_sums(const float *x, int rows, int n, float *out);
  * counterpart: a check of that routine.  Returns 0 (1 on a bad argument or
  * a device error). */
 int l98_prefix_query(const float *x, int rows, int n, int mode, const float *c, int *out, float *outv);
+/* MoE routing of nt (<= 8) tokens over E (<= 128) experts, top-k (<= 8),
+ * computed on the device by the routine the expert kernels run in each
+ * block: host logits[nt][E] and bias[E] (NULL: zeros) in, idx[nt][topk]
+ * and renormalized weights w[nt][topk] out, as lz_moe_route
+ * (src/ops_moe.c:12-163, sigmoid scores, no temperature) fills idx_out /
+ * w_out per token.  A check of that routine on arbitrary logits; the
+ * reference routes inside forward_moe (src/forward_moe.c:96-98).  Returns 0
+ * (1 on a bad argument or a device error). */
+int l98_moe_route(const float *logits, const float *bias, int nt, int E, int topk, int *idx, float *w);
 /* Device and build facts, for logs. */
 const char *l98_device_name(void);
 /* Seconds of device time of the last l98_generate call's round loop

@@ -114,6 +114,7 @@ HIP_API = [
                                           C.c_int, _IP, C.c_int, _IP, _FP]),
     ("l98_row_sums", C.c_int, [_FP, C.c_int, C.c_int, _FP]),
     ("l98_prefix_query", C.c_int, [_FP, C.c_int, C.c_int, C.c_int, _FP, _IP, _FP]),
+    ("l98_moe_route", C.c_int, [_FP, _FP, C.c_int, C.c_int, C.c_int, _IP, _FP]),
     ("l98_device_name", C.c_char_p, []),
     ("l98_last_loop_seconds", C.c_double, []),
 ]

@@ -1476,6 +1476,30 @@ extern "C" int l98_row_sums(const float *x, int rows, int n, float *out) {
     return rc;
 }
 
+extern "C" int l98_moe_route(const float *logits, const float *bias, int nt, int E, int topk, int *idx, float *w) {
+    if (!logits || !idx || !w || nt < 1 || nt > MAX_CHUNK || E < 1 || E > MAX_EXPERTS || topk < 1 || topk > MAX_TOPK)
+        return 1;
+    if (ensure_tables()) return 1;
+    float *dl = nullptr, *db = nullptr, *dw = nullptr;
+    int *di = nullptr, rc = 0;
+    if (hipMalloc(&dl, sizeof(float) * (size_t)nt * E) != hipSuccess || hipMalloc(&db, sizeof(float) * E) != hipSuccess ||
+        hipMalloc(&dw, sizeof(float) * nt * topk) != hipSuccess || hipMalloc(&di, sizeof(int) * nt * topk) != hipSuccess)
+        rc = 1;
+    if (!rc && hipMemcpy(dl, logits, sizeof(float) * (size_t)nt * E, hipMemcpyHostToDevice) != hipSuccess) rc = 1;
+    if (!rc && (bias ? hipMemcpy(db, bias, sizeof(float) * E, hipMemcpyHostToDevice)
+                     : hipMemset(db, 0, sizeof(float) * E)) != hipSuccess)
+        rc = 1;
+    if (!rc && l98k_moe_route(dl, db, E, topk, nt, di, dw, nullptr)) rc = 1;
+    if (!rc && (hipMemcpy(idx, di, sizeof(int) * nt * topk, hipMemcpyDeviceToHost) != hipSuccess ||
+                hipMemcpy(w, dw, sizeof(float) * nt * topk, hipMemcpyDeviceToHost) != hipSuccess))
+        rc = 1;
+    if (dl) (void)hipFree(dl);
+    if (db) (void)hipFree(db);
+    if (dw) (void)hipFree(dw);
+    if (di) (void)hipFree(di);
+    return rc;
+}
+
 extern "C" int l98_prefix_query(const float *x, int rows, int n, int mode, const float *c, int *out, float *outv) {
     if (!x || !out || !outv || rows < 1 || n < 1 || mode < 0 || mode > 2 || (mode && !c)) return 1;
     float *dx = nullptr, *dc = nullptr, *dv = nullptr;

@@ -40,121 +40,210 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_expert_gemv(ExpertJob j0, Expe
 // ----------------------------------------------------------------- MoE ---
 
 // Routing for every token of the chunk (lz_moe_route, src/ops_moe.c:12-163:
-// sigmoid scores, key = score + bias for selection only, repeated
-// strict-greater argmax so the lowest index wins ties, weights renormalized
-// by their serial sum).  The k-th pick of that loop is the expert whose key
-// has rank k in the order (key descending, index ascending), so each
-// (token, expert) item counts its rank against the token's keys in LDS.
-// Then the chunk's distinct experts (a bit set): group g is the g-th
-// selected expert in ascending order, its members the (token, slot) pairs
-// that picked it, in pair order (route_group).  Every block of the expert
-// launch computes the same tables from the same router logits, so the
-// experts' weights need no separate routing launch.  GEMV_THREADS threads;
-// nt * E <= 4 * GEMV_THREADS.  Contains block barriers.
+// sigmoid scores, key = score + bias for selection only, top_k rounds of a
+// strict-greater argmax over the keys not yet taken, weights renormalized
+// by their serial sum).  Wave w routes tokens w and w + 4, lane l holds
+// experts l and l + 64.  One round is the reference's scan restated for a
+// wave (src/ops_moe.c:130-142): the candidates are the keys not <= the
+// sentinel -1e30 (taken ones leave the set); when the first candidate's key
+// is NaN nothing beats it and it wins, otherwise the winner is the lowest
+// index whose key equals the largest non-NaN candidate key (ties and
+// -0 == +0 go to the earlier index).  Without NaN keys a round is one
+// integer max over order-preserving images of the keys.  Then the chunk's distinct experts (a
+// bit set): group g is the g-th selected expert in ascending order, its
+// members the (token, slot) pairs that picked it, in pair order
+// (route_group).  Every block of the expert launch computes the same tables
+// from the same router logits, so the experts' weights need no separate
+// routing launch.  GEMV_THREADS threads; E <= 128, nt <= 8.  Contains
+// block barriers.
 struct __align__(16) RouteLds {
-    float key[MAX_CHUNK][MAX_EXPERTS];
-    float sc[MAX_CHUNK][MAX_EXPERTS];
     __align__(16) int sel[MAX_PAIRS];
     float w[MAX_PAIRS];
-    unsigned long long present[2];       // selected experts, one bit each
+    unsigned long long tmask[MAX_CHUNK][2];   // token t's selected experts
+};
+struct RouteSet {
+    unsigned long long lo, hi;           // selected experts of the chunk, one bit each
     int ng;                              // distinct experts
 };
 
-__device__ __forceinline__ void route_block(const float *__restrict__ logits, const float *__restrict__ bias, int E,
-                                            int topk, int nt, RouteLds &R, float *tab) {
-    const int tid = threadIdx.x;
-    const float tabv = c_exp_tab[tid & 31];
-    float lg[4], bs[4];
+// Inclusive DPP max scan step (lanes outside the source row read -inf);
+// after the six row_shr / row_bcast steps lane 63 holds the wave's largest
+// value
+#define L98_DPP_FMAX(x, ctrl, rmask) \
+    (x) = fmaxf((x), __int_as_float(__builtin_amdgcn_update_dpp((int)0xFF800000u, __float_as_int(x), (ctrl), (rmask), 0xF, false)))
+
+// Order-preserving unsigned image of a non-NaN float (-0 taken as +0, as
+// the selection loop's comparisons see it); every image is >= 1.
+__device__ __forceinline__ uint32_t route_ord(float x) {
+    const uint32_t b = u_from_f(x == 0.0f ? 0.0f : x);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+#define L98_DPP_UMAX(x, ctrl, rmask)                                                              \
+    do {                                                                                          \
+        const uint32_t o_ = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(x), (ctrl), (rmask), 0xF, true); \
+        (x) = o_ > (x) ? o_ : (x);                                                                \
+    } while (0)
+
+// One token's top_k rounds in one wave: S key slots per lane (experts lane
+// and lane + 64).  Lanes k < topk write the token's pair k.
+template <int S>
+__device__ __forceinline__ void route_token(const float (&lg)[2], const float (&bs)[2], int E, int topk, int t,
+                                            RouteLds &R, const float *tab) {
+    const float SENT = -1e30f;
+    const int lane = threadIdx.x & 63;
+    float sc[S], key[S];
+    bool live[S];
+    unsigned long long nanm = 0ull;
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
-        const int idx = imin(u * GEMV_THREADS + tid, nt * E - 1);
-        const int t = idx / E, i = idx - t * E;
-        lg[u] = logits[(size_t)t * E + i];
-        bs[u] = bias[i];
+    for (int s = 0; s < S; s++) {
+        sc[s] = d_sigmoid(lg[s], tab);
+        key[s] = sc[s] + bs[s];
+        live[s] = lane + 64 * s < E;
+        nanm |= __ballot(live[s] && key[s] != key[s]);
     }
-    if (tid < MAX_PAIRS) R.sel[tid] = -1;
+    int ek[MAX_TOPK];
+    float wk[MAX_TOPK];
+    float wsum = 0.0f;
+    unsigned long long mlo = 0ull, mhi = 0ull;
+    const int rounds = imin(topk, E);
+    if (nanm == 0ull) {
+        // no NaN key: the winner is the lowest index holding the largest
+        // candidate key, found as the largest order image (0 = none left)
+        uint32_t u[S];
+#pragma unroll
+        for (int s = 0; s < S; s++) u[s] = (live[s] && !(key[s] <= SENT)) ? route_ord(key[s]) : 0u;
+#pragma unroll
+        for (int k = 0; k < MAX_TOPK; k++) {
+            ek[k] = -1;
+            wk[k] = 0.0f;
+            if (k >= rounds) continue;
+            uint32_t v = u[0];
+            if (S == 2) v = u[S - 1] > v ? u[S - 1] : v;
+            L98_DPP_UMAX(v, 0x111, 0xF);
+            L98_DPP_UMAX(v, 0x112, 0xF);
+            L98_DPP_UMAX(v, 0x114, 0xF);
+            L98_DPP_UMAX(v, 0x118, 0xF);
+            L98_DPP_UMAX(v, 0x142, 0xA);
+            L98_DPP_UMAX(v, 0x143, 0xC);
+            const uint32_t m = (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+            if (m == 0u) continue;
+            const unsigned long long b0 = __ballot(u[0] == m);
+            int best;
+            if (S == 1 || b0) {
+                best = __builtin_ctzll(b0);
+                mlo |= 1ull << best;
+                if (lane == best) u[0] = 0u;
+            } else {
+                best = 64 + __builtin_ctzll(__ballot(u[S - 1] == m));
+                mhi |= 1ull << (best - 64);
+                if (lane == best - 64) u[S - 1] = 0u;
+            }
+            ek[k] = best;
+            wk[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(best < 64 ? sc[0] : sc[S - 1]), best & 63));
+            wsum += wk[k];
+        }
+    } else {
+        // a NaN key: the loop's own order (the first remaining candidate
+        // wins when its key is NaN; NaN never beats a number)
+#pragma unroll
+        for (int k = 0; k < MAX_TOPK; k++) {
+            ek[k] = -1;
+            wk[k] = 0.0f;
+            if (k >= rounds) continue;
+            bool c[S];
+            unsigned long long b[2] = {0ull, 0ull};
+#pragma unroll
+            for (int s = 0; s < S; s++) {
+                c[s] = live[s] && !(key[s] <= SENT);
+                b[s] = __ballot(c[s]);
+            }
+            if ((b[0] | b[1]) == 0ull) continue;
+            const int f = b[0] ? __builtin_ctzll(b[0]) : 64 + __builtin_ctzll(b[1]);
+            const float kf =
+                __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f < 64 ? key[0] : key[S - 1]), f & 63));
+            int best = f;
+            if (kf == kf) {
+                float mx = -INFINITY;
+#pragma unroll
+                for (int s = 0; s < S; s++)
+                    if (c[s] && key[s] == key[s]) mx = fmaxf(mx, key[s]);
+                L98_DPP_FMAX(mx, 0x111, 0xF);
+                L98_DPP_FMAX(mx, 0x112, 0xF);
+                L98_DPP_FMAX(mx, 0x114, 0xF);
+                L98_DPP_FMAX(mx, 0x118, 0xF);
+                L98_DPP_FMAX(mx, 0x142, 0xA);
+                L98_DPP_FMAX(mx, 0x143, 0xC);
+                mx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 63));
+                const unsigned long long e0 = __ballot(c[0] && key[0] == mx);
+                best = (S == 1 || e0) ? __builtin_ctzll(e0) : 64 + __builtin_ctzll(__ballot(c[S - 1] && key[S - 1] == mx));
+            }
+            ek[k] = best;
+            wk[k] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(best < 64 ? sc[0] : sc[S - 1]), best & 63));
+            wsum += wk[k];
+            if (best < 64) {
+                mlo |= 1ull << best;
+                if (lane == best) key[0] = SENT;
+            } else {
+                mhi |= 1ull << (best - 64);
+                if (lane == best - 64) key[S - 1] = SENT;
+            }
+        }
+    }
+    int my_e = -1;
+    float my_w = 0.0f;
+#pragma unroll
+    for (int k = 0; k < MAX_TOPK; k++)
+        if (lane == k) { my_e = ek[k]; my_w = wk[k]; }
+    if (my_e >= 0 && wsum > 0.0f) my_w /= wsum;
+    if (lane < topk) {
+        R.sel[t * topk + lane] = my_e;
+        R.w[t * topk + lane] = my_w;
+    }
+    if (lane == 0) {
+        R.tmask[t][0] = mlo;
+        R.tmask[t][1] = mhi;
+    }
+}
+
+__device__ __forceinline__ RouteSet route_block(const float *__restrict__ logits, const float *__restrict__ bias,
+                                                int E, int topk, int nt, RouteLds &R, float *tab) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float tabv = c_exp_tab[tid & 31];
+    float lg[2][2], bs[2];
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+        const int e = imin(lane + 64 * s, E - 1);
+        bs[s] = bias[e];
+#pragma unroll
+        for (int h = 0; h < 2; h++) lg[h][s] = logits[(size_t)imin(wave + 4 * h, nt - 1) * E + e];
+    }
     if (tid < 32) tab[tid] = tabv;
     __syncthreads();
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
-        const int idx = u * GEMV_THREADS + tid;
-        if (idx < nt * E) {
-            const int t = idx / E, i = idx - t * E;
-            const float sc = d_sigmoid(lg[u], tab);
-            const float kv = sc + bs[u];
-            R.sc[t][i] = sc;
-            R.key[t][i] = kv == 0.0f ? 0.0f : kv;      // -0 and +0 compare equal in the reference
-        }
+    for (int h = 0; h < 2; h++) {
+        const int t = wave + 4 * h;
+        if (t >= nt) break;                  // wave-uniform
+        if (E <= 64)
+            route_token<1>(lg[h], bs, E, topk, t, R, tab);
+        else
+            route_token<2>(lg[h], bs, E, topk, t, R, tab);
     }
     __syncthreads();
-    // the token's keys are read 16 at a time (all reads in flight) and
-    // compared in registers
-    for (int idx = tid; idx < nt * E; idx += GEMV_THREADS) {
-        const int t = idx / E, i = idx - t * E;
-        const float ki = R.key[t][i];
-        int rank = 0;
-        for (int j0 = 0; j0 < E; j0 += 16) {
-            float4 kq[4];
-#pragma unroll
-            for (int u = 0; u < 4; u++) kq[u] = *reinterpret_cast<const float4 *>(&R.key[t][j0 + 4 * u]);
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const float kk[4] = {kq[u].x, kq[u].y, kq[u].z, kq[u].w};
-#pragma unroll
-                for (int v = 0; v < 4; v++) {
-                    const int jj = j0 + 4 * u + v;
-                    rank += (jj < E && (kk[v] > ki || (kk[v] == ki && jj < i))) ? 1 : 0;
-                }
-            }
-        }
-        if (rank < topk) R.sel[t * topk + rank] = i;
+    RouteSet rs{0ull, 0ull, 0};
+    for (int t = 0; t < nt; t++) {
+        rs.lo |= R.tmask[t][0];
+        rs.hi |= R.tmask[t][1];
     }
-    __syncthreads();
-    if (tid < nt) {                      // weights renormalized by their serial sum
-        const int t = tid;
-        int ek[MAX_TOPK];
-        float sk[MAX_TOPK];
-#pragma unroll
-        for (int k = 0; k < MAX_TOPK; k++) ek[k] = R.sel[t * topk + imin(k, topk - 1)];
-#pragma unroll
-        for (int k = 0; k < MAX_TOPK; k++) sk[k] = R.sc[t][ek[k] >= 0 ? ek[k] : 0];
-        float wsum = 0.0f;
-#pragma unroll
-        for (int k = 0; k < MAX_TOPK; k++)
-            if (k < topk && ek[k] >= 0) wsum += sk[k];
-#pragma unroll
-        for (int k = 0; k < MAX_TOPK; k++) {
-            float w = ek[k] >= 0 ? sk[k] : 0.0f;
-            if (ek[k] >= 0 && wsum > 0.0f) w /= wsum;
-            if (k < topk) R.w[t * topk + k] = w;
-        }
-    }
-    // distinct experts, ascending: wave 0 holds pair p's expert in lane p
-    // (nt * topk <= 64) and ORs the one-hot expert bits across the wave
-    if (tid < 64) {
-        const int np = nt * topk;
-        const int ep = tid < np ? R.sel[tid] : -1;
-        unsigned long long lo = (ep >= 0 && ep < 64) ? 1ull << ep : 0ull;
-        unsigned long long hi = (ep >= 64) ? 1ull << (ep - 64) : 0ull;
-        for (int o = 32; o > 0; o >>= 1) {
-            lo |= __shfl_xor(lo, o);
-            hi |= __shfl_xor(hi, o);
-        }
-        if (tid == 0) {
-            R.present[0] = lo;
-            R.present[1] = hi;
-            R.ng = __popcll(lo) + __popcll(hi);
-        }
-    }
-    __syncthreads();
+    rs.ng = __popcll(rs.lo) + __popcll(rs.hi);
+    return rs;
 }
 
 // Expert of distinct group gi (the gi-th selected expert in ascending
 // order) and its member pairs in pair order (a wave-uniform scan; call from
 // whole waves).  Returns the member count; mem[m] for m < count.
-__device__ __forceinline__ int route_group(const RouteLds &R, int nt, int topk, int gi, int *e_out,
-                                           int (&mem)[MAX_CHUNK]) {
-    unsigned long long lo = R.present[0], hi = R.present[1];
+__device__ __forceinline__ int route_group(const RouteLds &R, const RouteSet &rs, int nt, int topk, int gi,
+                                           int *e_out, int (&mem)[MAX_CHUNK]) {
+    unsigned long long lo = rs.lo, hi = rs.hi;
     const int nlo = __popcll(lo);
     int e;
     if (gi < nlo) {
@@ -198,8 +287,8 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_up(ExpertJob j0, ExpertJob
     const int rem = blockIdx.x - jb * per_job;
     const int gi = rem / tiles;
     const int tile = rem - gi * tiles;
-    route_block(logits, bias, E, topk, nt, rt, tab);
-    const int ng = rt.ng;
+    const RouteSet rs = route_block(logits, bias, E, topk, nt, rt, tab);
+    const int ng = rs.ng;
     if (blockIdx.x == 0) {                 // publish the routing
         const int tid = threadIdx.x;
         if (tid < nt * topk) {
@@ -209,9 +298,9 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_up(ExpertJob j0, ExpertJob
         }
         if (tid < E) {                     // thread e: its group slot and members, in pair order
             const int e = tid;
-            const unsigned long long word = rt.present[e >> 6], bit = 1ull << (e & 63);
+            const unsigned long long word = (e >> 6) ? rs.hi : rs.lo, bit = 1ull << (e & 63);
             if (word & bit) {
-                const int g = __popcll(word & (bit - 1ull)) + ((e >> 6) ? __popcll(rt.present[0]) : 0);
+                const int g = __popcll(word & (bit - 1ull)) + ((e >> 6) ? __popcll(rs.lo) : 0);
                 int cnt = 0;
                 for (int p = 0; p < nt * topk; p++)
                     if (rt.sel[p] == e && cnt < MAX_CHUNK) grp->member[g][cnt++] = p;
@@ -227,7 +316,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_up(ExpertJob j0, ExpertJob
     if (gi >= ng) return;
     const ExpertJob &J = jb == 0 ? j0 : j1;
     int e, gmem[MAX_CHUNK];
-    const int nm = route_group(rt, nt, topk, gi, &e, gmem);
+    const int nm = route_group(rt, rs, nt, topk, gi, &e, gmem);
     int xrow[M];
 #pragma unroll
     for (int t = 0; t < M; t++) {
@@ -299,7 +388,7 @@ extern "C" int l98k_moe_up(const ExpertJob *jobs, int n_jobs, const float *logit
                            int topk, int nt, int *sel_idx, float *sel_w, MoeGroups *grp, int *tally, int in_dim,
                            int out_rows, hipStream_t st) {
     if (E > MAX_EXPERTS || E < topk || topk < 1 || topk > MAX_TOPK || nt < 1 || nt > MAX_CHUNK ||
-        nt * topk > MAX_PAIRS || nt * E > 4 * GEMV_THREADS || !expert_jobs_ok(jobs, n_jobs, in_dim, PRO_QUANT))
+        nt * topk > MAX_PAIRS || !expert_jobs_ok(jobs, n_jobs, in_dim, PRO_QUANT))
         return -1;
     const int max_groups = nt * topk < E ? nt * topk : E;
     const int M = expert_m(nt);
@@ -312,6 +401,29 @@ extern "C" int l98k_moe_up(const ExpertJob *jobs, int n_jobs, const float *logit
     const ExpertJob &a = jobs[0], &b2 = n_jobs > 1 ? jobs[1] : jobs[0];
     EXPERT_DISPATCH(k_moe_up, M, pj, grid, blk, lds, st, a, b2, logits, bias, E, topk, nt, sel_idx, sel_w, grp, tally,
                     max_groups, in_dim, out_rows, R, tiles);
+    return (int)hipGetLastError();
+}
+
+// The routing of k_moe_up alone (one block): sel_idx / sel_w as k_moe_up
+// publishes them, nt * topk pairs in (token, slot) order.
+__global__ __launch_bounds__(GEMV_THREADS) void k_moe_route(const float *__restrict__ logits,
+                                                            const float *__restrict__ bias, int E, int topk, int nt,
+                                                            int *__restrict__ sel_idx, float *__restrict__ sel_w) {
+    __shared__ RouteLds rt;
+    __shared__ float tab[32];
+    (void)route_block(logits, bias, E, topk, nt, rt, tab);
+    const int tid = threadIdx.x;
+    if (tid < nt * topk) {
+        sel_idx[tid] = rt.sel[tid];
+        sel_w[tid] = rt.w[tid];
+    }
+}
+
+extern "C" int l98k_moe_route(const float *logits, const float *bias, int E, int topk, int nt, int *sel_idx,
+                              float *sel_w, hipStream_t st) {
+    if (E < 1 || E > MAX_EXPERTS || topk < 1 || topk > MAX_TOPK || nt < 1 || nt > MAX_CHUNK || nt * topk > MAX_PAIRS)
+        return -1;
+    hipLaunchKernelGGL(k_moe_route, dim3(1), dim3(GEMV_THREADS), 0, st, logits, bias, E, topk, nt, sel_idx, sel_w);
     return (int)hipGetLastError();
 }
 

@@ -70,6 +70,9 @@ int l98k_attn(const AttnArgs *a, int nt, int max_len, float *att, hipStream_t st
 // first projections (n_jobs <= 2, e.g. w1 and w3 over the latent rows);
 // publishes sel_idx / sel_w / grp (and adds the distinct-expert count to
 // *tally) for the down projection and the combine.
+// routing only (the tables k_moe_up computes in each block), for checks
+int l98k_moe_route(const float *logits, const float *bias, int E, int topk, int nt, int *sel_idx, float *sel_w,
+                   hipStream_t st);
 int l98k_moe_up(const ExpertJob *jobs, int n_jobs, const float *logits, const float *bias, int E, int topk, int nt,
                 int *sel_idx, float *sel_w, MoeGroups *grp, int *tally, int in_dim, int out_rows, hipStream_t st);
 int l98k_row_sums(const float *x, int rows, int n, float *out, hipStream_t st);
