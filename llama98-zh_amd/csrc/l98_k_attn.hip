@@ -220,7 +220,8 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a, float *__restri
 }
 
 // k_attn_av: one block of 8 waves per (q head, token).  Softmax over the
-// token's scores (max, exp, serial sum, scale), then the value sum
+// token's scores (max, exp, the serial loop's sum - taken by the exact wave
+// sum up to 2048 positions -, scale), then the value sum
 // out[d] = sum_p a[p] * v[p][d] * vs[p][d/32] walked in position order by
 // one lane per d.  The V rows of up to `sc` positions are staged in LDS
 // with every load in flight; the products (a*v)*vs of 64 positions at a
@@ -230,6 +231,7 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a, float *__restri
 // gate and the per-32 quantization of the head's output (the o_proj input).
 #define AV_CH 64
 #define AV_PAD 68                        // floats per d row of the product buffer (bank spread)
+#define AV_ESUM_FLOATS (64 * (32 + 4))  // padded exp row of the exact wave sum (L <= 2048)
 
 // Stages V rows [p0, p0 + n) of kv head kvh (hd int8 + hd/32 scales each)
 // into LDS with every load of the block in flight before the first store
@@ -268,6 +270,7 @@ __global__ __launch_bounds__(AV_THREADS) void k_attn_av(AttnArgs a, const float 
     extern __shared__ __align__(16) char smem[];
     __shared__ uint32_t s_red[AV_THREADS / 64];
     __shared__ float s_inv;
+    __shared__ PsRec s_rec[128];
     const int h = blockIdx.x, t = blockIdx.y;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int hd = a.hd, nb = hd >> 5, kv_mul = a.nh / a.nkv, kvh = h / kv_mul;
@@ -277,6 +280,7 @@ __global__ __launch_bounds__(AV_THREADS) void k_attn_av(AttnArgs a, const float 
     float *prod = s_a + Lp;                                                          // [2][hd][AV_PAD]
     int8_t *s_v = reinterpret_cast<int8_t *>(prod + 2 * hd * AV_PAD);               // [sc][hd]
     float *s_vs = reinterpret_cast<float *>(s_v + (size_t)sc * hd);                  // [sc][nb]
+    float *s_e = s_vs + (size_t)sc * nb;                                             // [AV_ESUM_FLOATS]
     const float *arow = att + ((size_t)t * a.nh + h) * att_stride;
     const int cpr = hd >> 4;
     // scores -> LDS, then the V stage (its loads wait behind the score loads)
@@ -294,11 +298,26 @@ __global__ __launch_bounds__(AV_THREADS) void k_attn_av(AttnArgs a, const float 
 #pragma unroll
     for (int w = 1; w < AV_THREADS / 64; w++) bk = umax(bk, s_red[w]);
     const float mx = d_unkey(bk);
-    for (int p = tid; p < L; p += AV_THREADS) s_a[p] = d_exp(s_a[p] - mx, tab);
+    // the exps also go to the padded row layout of the exact wave sum
+    // (lane chunks of 8, 16 or 32 for L up to 512, 1024, 2048)
+    const int esh = L <= 512 ? 3 : L <= 1024 ? 4 : 5, ech = 1 << esh;
+    for (int p = tid; p < L; p += AV_THREADS) {
+        const float e = d_exp(s_a[p] - mx, tab);
+        s_a[p] = e;
+        s_e[(p >> esh) * (ech + 4) + (p & (ech - 1))] = e;
+    }
     __syncthreads();
-    if (tid == 0) {
-        const float sum = serial_sum(s_a, L);
-        s_inv = (sum > 0.0f) ? 1.0f / sum : 0.0f;
+    if (wave == 0) {                     // the serial loop's sum, bit for bit
+        float sum;
+        if (L > 2048)
+            sum = serial_sum(s_a, L);
+        else if (esh == 3)
+            sum = wave_sum_nonneg<8>(s_e, L, s_rec);
+        else if (esh == 4)
+            sum = wave_sum_nonneg<16>(s_e, L, s_rec);
+        else
+            sum = wave_sum_nonneg<32>(s_e, L, s_rec);
+        if (lane == 0) s_inv = (sum > 0.0f) ? 1.0f / sum : 0.0f;
     }
     __syncthreads();
     const float inv = s_inv;
@@ -411,9 +430,9 @@ extern "C" int l98k_attn(const AttnArgs *a, int nt, int max_len, float *att, hip
     // value-sum kernel: scores, the product double buffer, then as many
     // staged V positions (multiple of 64) as the LDS limit leaves
     const int hd = a->hd;
-    const size_t fixed = ((size_t)att_stride + 2 * (size_t)hd * AV_PAD) * sizeof(float);
+    const size_t fixed = ((size_t)att_stride + 2 * (size_t)hd * AV_PAD + AV_ESUM_FLOATS) * sizeof(float);
     const size_t per_pos = (size_t)hd + (size_t)(hd >> 5) * sizeof(float);
-    const int lim = lds_limit() - 1024;          // the kernel's static LDS (exp table, reductions) fits in the rest
+    const int lim = lds_limit() - 4096;          // the kernel's static LDS (exp table, reductions, sum records) fits in the rest
     if (fixed + AV_CH * per_pos > (size_t)lim) return -1;
     int sc = (int)(((size_t)lim - fixed) / per_pos) & ~(AV_CH - 1);
     const int need = (max_len + AV_CH - 1) & ~(AV_CH - 1);

@@ -41,9 +41,13 @@ def start_both(pkg, model, prompt):
     return eng, ora
 
 
-@pytest.mark.parametrize("name,n_prompt", [("micro", 20), ("tiny", 40)])
+# server (seq_len 2304) contexts reach the softmax denominator's three
+# exact-sum widths (up to 1024 and 2048 positions) and the serial loop past
+# 2048
+@pytest.mark.parametrize("name,n_prompt", [("micro", 20), ("tiny", 40), ("server", 700), ("server", 1500),
+                                           ("server", 2200)])
 def test_capture_and_prefill_bit_exact(pkg, request, name, n_prompt):
-    print(f"[case] capture {name}", flush=True)
+    print(f"[case] capture {name} n_prompt={n_prompt}", flush=True)
     model = request.getfixturevalue(name)
     V = 512 if name == "micro" else 8192
     prompt = pkg.prompt_tokens(0, n_prompt, V)
