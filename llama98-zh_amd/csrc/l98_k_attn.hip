@@ -238,23 +238,71 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a, float *__restri
 // (n * hd / 16 <= AV_THREADS * AV_STAGE_MAX).
 #define AV_THREADS 512
 #define AV_STAGE_MAX 16
+// STEP: cpr = hd/16 and nb = hd/32 divide AV_THREADS, so item
+// u * AV_THREADS + tid is tid's (row, column) plus u * (AV_THREADS / cpr)
+// rows, with no division per round.  Every round's load is issued (rounds
+// past the end read the last item again) before the first store: the empty
+// asm takes every loaded register, so the compiler can neither sink a load
+// into its store's branch nor copy it out of one, either of which would wait
+// out the loads' latency one after another.
+// With a score row (arow, L <= AV_SCORE_MAX * AV_THREADS), its loads join
+// the same batch and it is stored to s_a.
+#define AV_SCORE_MAX 4
+template <bool STEP>
 __device__ __forceinline__ void av_stage(const int8_t *__restrict__ vc, const float *__restrict__ vs, int kv_dim,
-                                         int kvh, int hd, int p0, int n, int8_t *s_v, float *s_vs) {
+                                         int kvh, int hd, int p0, int n, int8_t *s_v, float *s_vs,
+                                         const float *__restrict__ arow, int L, float *s_a) {
     const int tid = threadIdx.x, cpr = hd >> 4, nb = hd >> 5;
     const int total = n * cpr, stotal = n * nb;
+    const int8_t *vbase = vc + (size_t)p0 * kv_dim + kvh * hd;
+    const float *sbase = vs + (size_t)p0 * (kv_dim >> 5) + kvh * nb;
+    const int rstep = AV_THREADS / cpr, sstep = AV_THREADS / nb;
+    const int r0 = tid / cpr, c0 = tid - r0 * cpr, rl = (total - 1) / cpr, cl = total - 1 - rl * cpr;
+    const int q0 = tid / nb, g0 = tid - q0 * nb, ql = (stotal - 1) / nb, gl = stotal - 1 - ql * nb;
     int4 r[AV_STAGE_MAX];
-    float q[AV_STAGE_MAX / 2];
+    float q[AV_STAGE_MAX / 2], sa[AV_SCORE_MAX];
+#pragma unroll
+    for (int k = 0; k < AV_SCORE_MAX; k++) sa[k] = arow ? arow[imin(k * AV_THREADS + tid, L - 1)] : 0.0f;
 #pragma unroll
     for (int u = 0; u < AV_STAGE_MAX; u++) {
-        const int idx = imin(u * AV_THREADS + tid, total - 1);
-        const int row = idx / cpr, c = idx - row * cpr;
-        r[u] = *reinterpret_cast<const int4 *>(vc + (size_t)(p0 + row) * kv_dim + kvh * hd + c * 16);
+        const int idx = u * AV_THREADS + tid;
+        int row, c;
+        if (STEP) {
+            const bool in = idx < total;
+            row = in ? u * rstep + r0 : rl;
+            c = in ? c0 : cl;
+        } else {
+            const int ic = imin(idx, total - 1);
+            row = ic / cpr;
+            c = ic - row * cpr;
+        }
+        r[u] = *reinterpret_cast<const int4 *>(vbase + (size_t)row * kv_dim + c * 16);
     }
 #pragma unroll
     for (int u = 0; u < AV_STAGE_MAX / 2; u++) {
-        const int sidx = imin(u * AV_THREADS + tid, stotal - 1);
-        const int srow = sidx / nb, g = sidx - srow * nb;
-        q[u] = vs[(size_t)(p0 + srow) * (kv_dim >> 5) + kvh * nb + g];
+        const int sidx = u * AV_THREADS + tid;
+        int srow, g;
+        if (STEP) {
+            const bool in = sidx < stotal;
+            srow = in ? u * sstep + q0 : ql;
+            g = in ? g0 : gl;
+        } else {
+            const int ic = imin(sidx, stotal - 1);
+            srow = ic / nb;
+            g = ic - srow * nb;
+        }
+        q[u] = sbase[(size_t)srow * (kv_dim >> 5) + g];
+    }
+#pragma unroll
+    for (int u = 0; u < AV_STAGE_MAX; u++) asm volatile("" : "+v"(r[u].x), "+v"(r[u].y), "+v"(r[u].z), "+v"(r[u].w));
+#pragma unroll
+    for (int u = 0; u < AV_STAGE_MAX / 2; u++) asm volatile("" : "+v"(q[u]));
+#pragma unroll
+    for (int k = 0; k < AV_SCORE_MAX; k++) asm volatile("" : "+v"(sa[k]));
+    if (arow) {
+#pragma unroll
+        for (int k = 0; k < AV_SCORE_MAX; k++)
+            if (k * AV_THREADS + tid < L) s_a[k * AV_THREADS + tid] = sa[k];
     }
 #pragma unroll
     for (int u = 0; u < AV_STAGE_MAX; u++)
@@ -262,6 +310,14 @@ __device__ __forceinline__ void av_stage(const int8_t *__restrict__ vc, const fl
 #pragma unroll
     for (int u = 0; u < AV_STAGE_MAX / 2; u++)
         if (u * AV_THREADS < stotal) s_vs[imin(u * AV_THREADS + tid, stotal - 1)] = q[u];
+}
+__device__ __forceinline__ void av_stage_any(const int8_t *__restrict__ vc, const float *__restrict__ vs, int kv_dim,
+                                             int kvh, int hd, int p0, int n, int8_t *s_v, float *s_vs,
+                                             const float *__restrict__ arow, int L, float *s_a) {
+    if (AV_THREADS % (hd >> 4) == 0 && AV_THREADS % (hd >> 5) == 0)
+        av_stage<true>(vc, vs, kv_dim, kvh, hd, p0, n, s_v, s_vs, arow, L, s_a);
+    else
+        av_stage<false>(vc, vs, kv_dim, kvh, hd, p0, n, s_v, s_vs, arow, L, s_a);
 }
 
 __global__ __launch_bounds__(AV_THREADS) void k_attn_av(AttnArgs a, const float *__restrict__ att, int att_stride,
@@ -283,9 +339,10 @@ __global__ __launch_bounds__(AV_THREADS) void k_attn_av(AttnArgs a, const float 
     float *s_e = s_vs + (size_t)sc * nb;                                             // [AV_ESUM_FLOATS]
     const float *arow = att + ((size_t)t * a.nh + h) * att_stride;
     const int cpr = hd >> 4;
-    // scores -> LDS, then the V stage (its loads wait behind the score loads)
-    for (int p = tid; p < L; p += AV_THREADS) s_a[p] = arow[p];
-    av_stage(a.vcache, a.vscale, a.kv_dim, kvh, hd, 0, imin(sc, L), s_v, s_vs);
+    // scores and the first V stage -> LDS, their loads in one batch (score
+    // rows past AV_SCORE_MAX * AV_THREADS positions: the rest after)
+    av_stage_any(a.vcache, a.vscale, a.kv_dim, kvh, hd, 0, imin(sc, L), s_v, s_vs, arow, L, s_a);
+    for (int p = AV_SCORE_MAX * AV_THREADS + tid; p < L; p += AV_THREADS) s_a[p] = arow[p];
     EXP_TAB_PUT(tab);
     __syncthreads();
     // softmax: max (order-preserving key), exp, serial sum, scale
@@ -353,7 +410,7 @@ __global__ __launch_bounds__(AV_THREADS) void k_attn_av(AttnArgs a, const float 
         const int nsc = imin(sc, L - sp0);
         if (sp0 > 0) {
             __syncthreads();
-            av_stage(a.vcache, a.vscale, a.kv_dim, kvh, hd, sp0, nsc, s_v, s_vs);
+            av_stage_any(a.vcache, a.vscale, a.kv_dim, kvh, hd, sp0, nsc, s_v, s_vs, nullptr, 0, nullptr);
             __syncthreads();
         }
         const int nch = (nsc + AV_CH - 1) / AV_CH;
@@ -362,12 +419,14 @@ __global__ __launch_bounds__(AV_THREADS) void k_attn_av(AttnArgs a, const float 
         for (int c = 0; c < nch; c++) {
             if (cons) {
                 if (d < hd) {
+                    // all of the chunk's reads in flight before the first add
                     const float *pr = prod + (size_t)(c & 1) * hd * AV_PAD + (size_t)d * AV_PAD;
+                    float4 q[AV_CH / 4];
 #pragma unroll
-                    for (int i = 0; i < AV_CH; i += 4) {
-                        const float4 q = *reinterpret_cast<const float4 *>(pr + i);
-                        o += q.x; o += q.y; o += q.z; o += q.w;
-                    }
+                    for (int i = 0; i < AV_CH / 4; i++) q[i] = *reinterpret_cast<const float4 *>(pr + 4 * i);
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int i = 0; i < AV_CH / 4; i++) { o += q[i].x; o += q[i].y; o += q[i].z; o += q[i].w; }
                 }
             } else if (c + 1 < nch) {
                 produce(sp0 + (c + 1) * AV_CH, sp0, nsc, (c + 1) & 1);
