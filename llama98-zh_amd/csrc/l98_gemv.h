@@ -99,6 +99,20 @@ __device__ __forceinline__ void quant_rows(const float4 (&v)[RW][PJN], int wave,
 #define MODES_S MB(PRO_SILU)
 #define MODES_Q MB(PRO_QUANT)
 #define MODES_CS (MB(PRO_COMBINE) | MB(PRO_SILU))
+// The activation loads of a prologue go out before the tile's weight loads:
+// the empty asm with a memory clobber keeps every earlier load above it
+// (no pass may sink one into a later conditional use, behind the weights,
+// where its wait would retire the weights too), and sched_barrier keeps the
+// scheduler from interleaving them.  The prologue's arithmetic (the norm's
+// exact sum) then runs while the weights are in flight.
+#define PRO_ISSUE_W()                            \
+    do {                                         \
+        asm volatile("" ::: "memory");           \
+        __builtin_amdgcn_sched_barrier(0);       \
+        issue_w();                               \
+        __builtin_amdgcn_sched_barrier(0);       \
+    } while (0)
+
 template <int M, int PJ, int MODES, typename IssueW>
 __device__ __forceinline__ void build_rows(const Prologue &P, const int8_t *__restrict__ xq,
                                            const float *__restrict__ xqs, int in_dim, const int (&xrow)[M], int nm,
@@ -123,7 +137,7 @@ __device__ __forceinline__ void build_rows(const Prologue &P, const int8_t *__re
             const int ts = si / nb;
             sc[u] = xqs[(size_t)xrow[ts < nm ? ts : 0] * nb + (si - ts * nb)];
         }
-        issue_w();
+        PRO_ISSUE_W();
 #pragma unroll
         for (int u = 0; u < XQ_PER_THREAD; u++) {
             reinterpret_cast<int4 *>(sx)[imin(u * GEMV_THREADS + tid, total - 1)] = r[u];
@@ -160,7 +174,7 @@ __device__ __forceinline__ void build_rows(const Prologue &P, const int8_t *__re
 #pragma unroll
             for (int j = 0; j < PJN; j++)
                 v[r][j] = reinterpret_cast<const float4 *>(P.src + (size_t)xr[r] * P.src_stride)[fc[j]];
-        issue_w();
+        PRO_ISSUE_W();
         quant_rows<RW, PJN>(v, wave, lane, nm, nf, nb, in_dim, sx, sxs);
     } else if ((MODES & MB(PRO_SILU)) && P.mode == PRO_SILU) {
         const float tabv = c_exp_tab[lane & 31];
@@ -172,7 +186,7 @@ __device__ __forceinline__ void build_rows(const Prologue &P, const int8_t *__re
                 v[r][j] = reinterpret_cast<const float4 *>(P.src + (size_t)xr[r] * P.src_stride)[fc[j]];
                 q[r][j] = reinterpret_cast<const float4 *>(P.src2 + (size_t)xr[r] * P.src_stride)[fc[j]];
             }
-        issue_w();
+        PRO_ISSUE_W();
         if (tid < 32) tab[tid] = tabv;
         __syncthreads();
 #pragma unroll
@@ -195,7 +209,7 @@ __device__ __forceinline__ void build_rows(const Prologue &P, const int8_t *__re
                 for (int j = 0; j < PJN; j++)
                     h[r][k][j] = reinterpret_cast<const float4 *>(P.src + (size_t)pair * in_dim)[fc[j]];
             }
-        issue_w();
+        PRO_ISSUE_W();
 #pragma unroll
         for (int r = 0; r < RW; r++)
 #pragma unroll
@@ -227,7 +241,7 @@ __device__ __forceinline__ void build_rows(const Prologue &P, const int8_t *__re
                 ad[r][j] = reinterpret_cast<const float4 *>(pa + (size_t)xr[r] * sa)[fc[j]];
                 bd[r][j] = reinterpret_cast<const float4 *>(pb + (size_t)xr[r] * sb)[fc[j]];
             }
-        issue_w();
+        PRO_ISSUE_W();
         // x + (a + b), x + a, or x
 #pragma unroll
         for (int r = 0; r < RW; r++)
