@@ -177,7 +177,14 @@ __device__ __forceinline__ void build_rows(const Prologue &P, const int8_t *__re
         PRO_ISSUE_W();
         quant_rows<RW, PJN>(v, wave, lane, nm, nf, nb, in_dim, sx, sxs);
     } else if ((MODES & MB(PRO_SILU)) && P.mode == PRO_SILU) {
-        const float tabv = c_exp_tab[lane & 31];
+        // the table entry through an opaque global pointer: a plain global
+        // load, which the barrier below keeps ahead of the weights (a
+        // constant-memory load may be moved after them, and a flat load's
+        // wait would retire them too; either way the table's store would
+        // wait the weights out)
+        const float *tabp = c_exp_tab;
+        asm volatile("" : "+s"(tabp));
+        const float tabv = ((const __attribute__((address_space(1))) float *)tabp)[lane & 31];
         float4 q[RW][PJN];
 #pragma unroll
         for (int r = 0; r < RW; r++)

@@ -20,14 +20,25 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_expert_gemv(ExpertJob j0, Expe
     const int gi = rem / tiles;
     const int tile = rem - gi * tiles;
     const ExpertJob &J = jb == 0 ? j0 : j1;
-    const int ng = grp->n_groups;
+    // the group's table entries in one batch, before the group count is
+    // known (gi < max_groups <= MAX_PAIRS keeps every read inside the table;
+    // a block past the count returns before it uses them), so the weights
+    // and activations wait on one round trip instead of three
+    int ng = grp->n_groups, e = grp->expert[gi], nm = grp->n_members[gi];
+    int memv[M];
+#pragma unroll
+    for (int t = 0; t < M; t++) memv[t] = grp->member[gi][t];
+    asm volatile("" : "+s"(ng), "+s"(e), "+s"(nm));
+#pragma unroll
+    for (int t = 0; t < M; t++) asm volatile("" : "+s"(memv[t]));
     if (gi >= ng) return;
-    const int e = grp->expert[gi];
-    const int nm = grp->n_members[gi];
     int xrow[M];
 #pragma unroll
     for (int t = 0; t < M; t++) {
-        const int mem = grp->member[gi][t < nm ? t : 0];
+        int mem = memv[0];
+#pragma unroll
+        for (int u = 1; u < M; u++)
+            if (u == t && t < nm) mem = memv[u];
         xrow[t] = J.xq_by_pair ? mem : grp->pair_token[mem];
         if (threadIdx.x == t) s_orow[t] = mem;
     }
