@@ -237,16 +237,33 @@ __global__ __launch_bounds__(4 * KD) void k_kda_step(KdaStepArgs a) {
         s_kq[tid] = kq;
     }
     __syncthreads();
-    // ---- the token-serial recurrence on the lane quads
+    // ---- the token-serial recurrence on the lane quads.  Every LDS read of
+    // a token is issued at the top of its step (one wait, not one per use);
+    // the state slot advances without a division.
+    int so_t = 0;
+    if (a.advance) {
+        const int si0 = base % a.depth;
+        so_t = si0 + 1 == a.depth ? 0 : si0 + 1;
+    }
 #pragma unroll 1
     for (int t = 0; t < nt; t++) {
+        float4 c4[RPL / 4], a4[RPL / 4], g4[RPL / 4], b4[RPL / 4];
+#pragma unroll
+        for (int i = 0; i < RPL / 4; i++) {
+            c4[i] = *reinterpret_cast<const float4 *>(&s_c[t][row0 + 4 * i]);
+            a4[i] = *reinterpret_cast<const float4 *>(&s_a[t][row0 + 4 * i]);
+            g4[i] = *reinterpret_cast<const float4 *>(&s_g[t][row0 + 4 * i]);
+            b4[i] = *reinterpret_cast<const float4 *>(&s_b[t][row0 + 4 * i]);
+        }
+        const float vt = s_v[t][col], bt = s_beta[t], kqt = s_kq[t];
+        __builtin_amdgcn_sched_barrier(0);
         float pu[RPL], pw[RPL];
 #pragma unroll
-        for (int i = 0; i < RPL; i += 4) {
-            const float4 c4 = *reinterpret_cast<const float4 *>(&s_c[t][row0 + i]);
-            const float4 a4 = *reinterpret_cast<const float4 *>(&s_a[t][row0 + i]);
-            pu[i] = S[i] * c4.x; pu[i + 1] = S[i + 1] * c4.y; pu[i + 2] = S[i + 2] * c4.z; pu[i + 3] = S[i + 3] * c4.w;
-            pw[i] = S[i] * a4.x; pw[i + 1] = S[i + 1] * a4.y; pw[i + 2] = S[i + 2] * a4.z; pw[i + 3] = S[i + 3] * a4.w;
+        for (int i = 0; i < RPL / 4; i++) {
+            pu[4 * i] = S[4 * i] * c4[i].x; pu[4 * i + 1] = S[4 * i + 1] * c4[i].y;
+            pu[4 * i + 2] = S[4 * i + 2] * c4[i].z; pu[4 * i + 3] = S[4 * i + 3] * c4[i].w;
+            pw[4 * i] = S[4 * i] * a4[i].x; pw[4 * i + 1] = S[4 * i + 1] * a4[i].y;
+            pw[4 * i + 2] = S[4 * i + 2] * a4[i].z; pw[4 * i + 3] = S[4 * i + 3] * a4[i].w;
         }
         float u = 0.0f, w = 0.0f;
 #pragma unroll
@@ -257,26 +274,24 @@ __global__ __launch_bounds__(4 * KD) void k_kda_step(KdaStepArgs a) {
         }
         u = dpp_quad_bcast3(u);
         w = dpp_quad_bcast3(w);
-        const float ut = (s_v[t][col] - 1.0f * u) * s_beta[t];
-        const float o = 1.0f * w + ut * s_kq[t];
+        const float ut = (vt - 1.0f * u) * bt;
+        const float o = 1.0f * w + ut * kqt;
 #pragma unroll
-        for (int i = 0; i < RPL; i += 4) {
-            const float4 g4 = *reinterpret_cast<const float4 *>(&s_g[t][row0 + i]);
-            const float4 b4 = *reinterpret_cast<const float4 *>(&s_b[t][row0 + i]);
-            S[i] = S[i] * g4.x + b4.x * ut;
-            S[i + 1] = S[i + 1] * g4.y + b4.y * ut;
-            S[i + 2] = S[i + 2] * g4.z + b4.z * ut;
-            S[i + 3] = S[i + 3] * g4.w + b4.w * ut;
+        for (int i = 0; i < RPL / 4; i++) {
+            S[4 * i] = S[4 * i] * g4[i].x + b4[i].x * ut;
+            S[4 * i + 1] = S[4 * i + 1] * g4[i].y + b4[i].y * ut;
+            S[4 * i + 2] = S[4 * i + 2] * g4[i].z + b4[i].z * ut;
+            S[4 * i + 3] = S[4 * i + 3] * g4[i].w + b4[i].w * ut;
         }
         if (a.advance || t == nt - 1) {
-            int so;
-            if (a.advance) { const int si = (base + t) % a.depth; so = si + 1 == a.depth ? 0 : si + 1; }
-            else so = base;
+            // slot (base + t) % depth + 1 (wrapping) when advancing, else base
+            const int so = a.advance ? so_t : base;
             float4 *dst = reinterpret_cast<float4 *>(a.state + (size_t)so * a.slot_stride + head_off +
                                                      (size_t)col * KD + row0);
 #pragma unroll
             for (int i = 0; i < RPL / 4; i++) dst[i] = make_float4(S[4 * i], S[4 * i + 1], S[4 * i + 2], S[4 * i + 3]);
         }
+        so_t = so_t + 1 == a.depth ? 0 : so_t + 1;
         if (quarter == 0) {
             if (a.raw_out) a.raw_out[(size_t)t * value + (size_t)h * VD + col] = o;
             s_d[t][col] = o;
