@@ -47,8 +47,8 @@ __device__ __forceinline__ uint32_t u_from_f(float f) { return __float_as_uint(f
 __device__ __forceinline__ float d_exp(float x, const float *tab) {
     const float C2 = 0.242844437f, C1 = 0.207425515f, C0 = 0.549730133f;
     const float LOG2E32 = 1.44269504f * 32.0f;
-    if (x > 88.0f) return 3.40282347e+38f;
-    if (x < -87.3f) return 0.0f;
+    // the body runs for every lane (idx is always in [0, 31]) and the range
+    // cases are selected after it: no divergent branch around the table read
     float y32 = x * LOG2E32;
     float m = (y32 - 0.5f) + 12582912.0f;
     int32_t t = (int32_t)(u_from_f(m) & 0x007FFFFFu) - 0x00400000;
@@ -58,7 +58,8 @@ __device__ __forceinline__ float d_exp(float x, const float *tab) {
     float w = 1.0f + r * 0.03125f;
     float p2n = f_from_u((uint32_t)(n + 127) << 23);
     float c = (C2 * w + C1) * w + C0;
-    return p2n * (tab[idx] * c);
+    const float body = p2n * (tab[idx] * c);
+    return x > 88.0f ? 3.40282347e+38f : x < -87.3f ? 0.0f : body;
 }
 
 // lz_rsqrt_float_body, src/ops_quant.c:126-135
@@ -71,13 +72,12 @@ __device__ __forceinline__ float d_rsqrt(float x) {
 }
 
 // lz_sigmoid float branch, src/ops_quant.c:1816-1853
+// (x >= 0: 1 / (1 + exp(-x)); else exp(x) / (1 + exp(x)), as one path:
+// each lane's exp argument and numerator are those of its branch)
 __device__ __forceinline__ float d_sigmoid(float x, const float *tab) {
-    if (x >= 0.0f) {
-        float z = d_exp(-x, tab);
-        return 1.0f / (1.0f + z);
-    }
-    float z = d_exp(x, tab);
-    return z / (1.0f + z);
+    const bool nonneg = x >= 0.0f;
+    const float z = d_exp(nonneg ? -x : x, tab);
+    return (nonneg ? 1.0f : z) / (1.0f + z);
 }
 __device__ __forceinline__ float d_silu(float x, const float *tab) { return x * d_sigmoid(x, tab); }
 
@@ -86,15 +86,13 @@ __device__ __forceinline__ float d_softplus(float x, const float *tab) {
     const float L[9] = {1.000000000f, -0.499995530f, 0.333203435f, -0.248529464f,
                         0.191451162f, -0.137466222f, 0.079210736f, -0.030110965f,
                         0.005384062f};
-    if (x > 16.0f) return x;
     float nx = (x < 0.0f) ? x : -x;
     float u = d_exp(nx, tab);
     float p = L[8];
 #pragma unroll
     for (int i = 7; i >= 0; i--) p = p * u + L[i];
     float lp = u * p;
-    if (x > 0.0f) return x + lp;
-    return lp;
+    return x > 16.0f ? x : x > 0.0f ? x + lp : lp;
 }
 
 // q8_round (--fastfp off), src/ops_quant.h:145-178

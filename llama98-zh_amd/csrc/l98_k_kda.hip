@@ -70,6 +70,13 @@ __global__ __launch_bounds__(4 * KD) void k_kda_step(KdaStepArgs a) {
     const int nt = a.nt, key = a.key, value = a.value, rank = a.rank;
     const size_t head_off = (size_t)h * KD * VD;
     const int base = *a.ctl_slot;
+    // ring slot written after token 0: (base % depth) + 1, wrapping, when
+    // advancing (token t: t slots further, wrapping), else base
+    int so0 = base;
+    if (a.advance) {
+        const int si0 = base % a.depth;
+        so0 = si0 + 1 == a.depth ? 0 : si0 + 1;
+    }
     // ---- loads: the thread's row of every token, conv taps and history,
     // gate input, f_b row, state
     const int cch = grp == 0 ? h * KD + j : grp == 1 ? key + h * KD + j : 2 * key + h * VD + imin(j, VD - 1);
@@ -143,12 +150,11 @@ __global__ __launch_bounds__(4 * KD) void k_kda_step(KdaStepArgs a) {
     }
     // ring: the history after token t is seq[t+1 .. t+HIST]
     if (grp < 3) {
+        int so_t = so0;
 #pragma unroll
         for (int t = 0; t < NT; t++) {
             if (t < nt && (a.advance || t == nt - 1)) {
-                int so;
-                if (a.advance) { const int si = (base + t) % a.depth; so = si + 1 == a.depth ? 0 : si + 1; }
-                else so = base;
+                const int so = a.advance ? so_t : base;
                 float *r1 = a.conv_ring + (size_t)so * a.conv_slot_stride;
 #pragma unroll
                 for (int i = 0; i < HIST; i++) {
@@ -156,6 +162,7 @@ __global__ __launch_bounds__(4 * KD) void k_kda_step(KdaStepArgs a) {
                     r1[(size_t)cch * HIST + i] = si < HIST ? hc[si < HIST ? si : 0] : xin[si >= HIST ? si - HIST : 0];
                 }
             }
+            so_t = so_t + 1 == a.depth ? 0 : so_t + 1;
         }
     }
     // ---- gate rows of tokens grp, grp + 4, ..., then the decay gate
@@ -240,11 +247,7 @@ __global__ __launch_bounds__(4 * KD) void k_kda_step(KdaStepArgs a) {
     // ---- the token-serial recurrence on the lane quads.  Every LDS read of
     // a token is issued at the top of its step (one wait, not one per use);
     // the state slot advances without a division.
-    int so_t = 0;
-    if (a.advance) {
-        const int si0 = base % a.depth;
-        so_t = si0 + 1 == a.depth ? 0 : si0 + 1;
-    }
+    int so_t = so0;
 #pragma unroll 1
     for (int t = 0; t < nt; t++) {
         float4 c4[RPL / 4], a4[RPL / 4], g4[RPL / 4], b4[RPL / 4];
