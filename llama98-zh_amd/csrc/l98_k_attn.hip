@@ -229,8 +229,9 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a, float *__restri
 // the consumer lanes (hd/64 waves) add the previous 64 in order, so the
 // consumer's loop is one LDS read per four adds.  Then the sigmoid output
 // gate and the per-32 quantization of the head's output (the o_proj input).
-#define AV_CH 64
-#define AV_PAD 68                        // floats per d row of the product buffer (bank spread)
+// CH: positions per product chunk (128 where the block's LDS holds the
+// larger double buffer, else 64); a d row of the buffer is CH + 4 floats
+// (bank spread)
 #define AV_ESUM_FLOATS (64 * (32 + 4))  // padded exp row of the exact wave sum (L <= 2048)
 
 // Stages V rows [p0, p0 + n) of kv head kvh (hd int8 + hd/32 scales each)
@@ -320,6 +321,7 @@ __device__ __forceinline__ void av_stage_any(const int8_t *__restrict__ vc, cons
         av_stage<false>(vc, vs, kv_dim, kvh, hd, p0, n, s_v, s_vs, arow, L, s_a);
 }
 
+template <int CH>
 __global__ __launch_bounds__(AV_THREADS) void k_attn_av(AttnArgs a, const float *__restrict__ att, int att_stride,
                                                  int sc) {
     EXP_TAB_LOAD(tab);
@@ -333,6 +335,7 @@ __global__ __launch_bounds__(AV_THREADS) void k_attn_av(AttnArgs a, const float 
     const int pos_t = *a.ctl_pos + a.pos_off + t, L = pos_t + 1;
     const int Lp = (att_stride + 3) & ~3;
     float *s_a = reinterpret_cast<float *>(smem);                                   // [Lp]
+    constexpr int AV_CH = CH, AV_PAD = CH + 4;
     float *prod = s_a + Lp;                                                          // [2][hd][AV_PAD]
     int8_t *s_v = reinterpret_cast<int8_t *>(prod + 2 * hd * AV_PAD);               // [sc][hd]
     float *s_vs = reinterpret_cast<float *>(s_v + (size_t)sc * hd);                  // [sc][nb]
@@ -487,25 +490,39 @@ extern "C" int l98k_attn(const AttnArgs *a, int nt, int max_len, float *att, hip
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
     // value-sum kernel: scores, the product double buffer, then as many
-    // staged V positions (multiple of 64) as the LDS limit leaves
+    // staged V positions (a multiple of the chunk) as the LDS limit leaves;
+    // 128-position chunks when a whole chunk of V still fits beside them
     const int hd = a->hd;
-    const size_t fixed = ((size_t)att_stride + 2 * (size_t)hd * AV_PAD + AV_ESUM_FLOATS) * sizeof(float);
     const size_t per_pos = (size_t)hd + (size_t)(hd >> 5) * sizeof(float);
     const int lim = lds_limit() - 4096;          // the kernel's static LDS (exp table, reductions, sum records) fits in the rest
-    if (fixed + AV_CH * per_pos > (size_t)lim) return -1;
-    int sc = (int)(((size_t)lim - fixed) / per_pos) & ~(AV_CH - 1);
-    const int need = (max_len + AV_CH - 1) & ~(AV_CH - 1);
-    if (sc > need) sc = need;
-    const int sc_regs = (AV_THREADS * AV_STAGE_MAX / (hd >> 4)) & ~(AV_CH - 1);   // one register-staged pass
-    if (sc > sc_regs) sc = sc_regs;
-    const size_t lds = fixed + (size_t)sc * per_pos;
+    auto plan = [&](int ch, int *sc_out, size_t *lds_out) {
+        const size_t fixed = ((size_t)att_stride + 2 * (size_t)hd * (ch + 4) + AV_ESUM_FLOATS) * sizeof(float);
+        if (fixed + (size_t)ch * per_pos > (size_t)lim) return false;
+        int sc = (int)(((size_t)lim - fixed) / per_pos) & ~(ch - 1);
+        const int need = (max_len + ch - 1) & ~(ch - 1);
+        if (sc > need) sc = need;
+        const int sc_regs = (AV_THREADS * AV_STAGE_MAX / (hd >> 4)) & ~(ch - 1);   // one register-staged pass
+        if (sc > sc_regs) sc = sc_regs;
+        *sc_out = sc;
+        *lds_out = fixed + (size_t)sc * per_pos;
+        return true;
+    };
     static bool attr_set = false;
     if (!attr_set) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k_attn_av),
+        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k_attn_av<128>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, lim);
+        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k_attn_av<64>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, lim);
         attr_set = true;
     }
-    hipLaunchKernelGGL(k_attn_av, dim3(a->nh, nt), dim3(AV_THREADS), lds, st, *a, att, att_stride, sc);
+    int sc = 0;
+    size_t lds = 0;
+    if (plan(128, &sc, &lds))
+        hipLaunchKernelGGL(k_attn_av<128>, dim3(a->nh, nt), dim3(AV_THREADS), lds, st, *a, att, att_stride, sc);
+    else if (plan(64, &sc, &lds))
+        hipLaunchKernelGGL(k_attn_av<64>, dim3(a->nh, nt), dim3(AV_THREADS), lds, st, *a, att, att_stride, sc);
+    else
+        return -1;
     return (int)hipGetLastError();
 }
 
