@@ -70,6 +70,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_expert_gemv(ExpertJob j0, Expe
 struct __align__(16) RouteLds {
     __align__(16) int sel[MAX_PAIRS];
     float w[MAX_PAIRS];
+    int tok[MAX_PAIRS];                       // token of pair p (p / topk)
     unsigned long long tmask[MAX_CHUNK][2];   // token t's selected experts
 };
 struct RouteSet {
@@ -209,6 +210,7 @@ __device__ __forceinline__ void route_token(const float (&lg)[2], const float (&
     if (lane < topk) {
         R.sel[t * topk + lane] = my_e;
         R.w[t * topk + lane] = my_w;
+        R.tok[t * topk + lane] = t;
     }
     if (lane == 0) {
         R.tmask[t][0] = mlo;
@@ -298,6 +300,8 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_up(ExpertJob j0, ExpertJob
     const int rem = blockIdx.x - jb * per_job;
     const int gi = rem / tiles;
     const int tile = rem - gi * tiles;
+    // the projection's arguments read now, so their loads overlap the routing
+    const ExpertJob J = jb == 0 ? j0 : j1;
     const RouteSet rs = route_block(logits, bias, E, topk, nt, rt, tab);
     const int ng = rs.ng;
     if (blockIdx.x == 0) {                 // publish the routing
@@ -325,14 +329,13 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_up(ExpertJob j0, ExpertJob
         }
     }
     if (gi >= ng) return;
-    const ExpertJob &J = jb == 0 ? j0 : j1;
     int e, gmem[MAX_CHUNK];
     const int nm = route_group(rt, rs, nt, topk, gi, &e, gmem);
     int xrow[M];
 #pragma unroll
     for (int t = 0; t < M; t++) {
         const int mem = gmem[t < nm ? t : 0];
-        xrow[t] = J.xq_by_pair ? mem : mem / topk;
+        xrow[t] = J.xq_by_pair ? mem : rt.tok[mem];
         if (threadIdx.x == t) s_orow[t] = mem;
     }
     const int row0 = tile * R;
