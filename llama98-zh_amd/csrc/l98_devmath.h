@@ -295,7 +295,7 @@ __device__ __forceinline__ uint32_t ps_classify(float p, int E0, int E1, uint32_
 }
 
 template <int C>
-__device__ float wave_sum_nonneg(const float *v, int n, PsRec *rec) {
+__device__ __forceinline__ float wave_sum_nonneg(const float *v, int n, PsRec *rec) {
     static_assert(C % 4 == 0 && C <= 32, "C: multiple of 4, at most 32");
     const int lane = threadIdx.x & 63, i0 = lane * C;
     const float4 *vl = reinterpret_cast<const float4 *>(v + lane * (C + 4));
