@@ -145,7 +145,7 @@ __device__ __forceinline__ float d_random_f32(unsigned long long *st) {
 // get(i) returns x[i], and 0 for i >= n), answered for `mode` by the whole
 // block.  Thread t owns elements [t*CH, (t+1)*CH).  Contains barriers.
 template <class G>
-__device__ void xprefix(const G &get, int n, int mode, float c, SmpLds &L) {
+__device__ __forceinline__ void xprefix(const G &get, int n, int mode, float c, SmpLds &L) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int CH = (n + SMP_THREADS - 1) / SMP_THREADS;
     const int i0 = tid * CH;
