@@ -232,7 +232,7 @@ __device__ __forceinline__ int imax(int a, int b) { return a > b ? a : b; }
 // Element i sits in lane i / C, slot i % C.  rec: LDS table of 128 entries
 // for this wave.  v (16-byte aligned) holds the row in the ps_slot layout
 // below; C % 4 == 0, n <= 64 * C.
-struct PsRec {
+struct __align__(16) PsRec {
     float p;
     uint32_t info;                      // binade guess | (index + 1) << 8
     uint32_t ps;                        // sum of q before the element

@@ -24,7 +24,7 @@
 #define SMP_WAVES (SMP_THREADS / 64)
 #define SMP_RMAX 1024                    // special elements the walk's table holds
 
-struct XRec {
+struct __align__(16) XRec {
     float p;
     uint32_t info;                       // binade guess | (index + 1) << 8
     uint32_t a, b;                       // before the sort: thread, local q prefix; after: q prefix lo, hi
