@@ -2,6 +2,7 @@
 // (bit-exact restatement of the reference float-oracle path; see
 // l98_devmath.h for the numeric contract).
 #include "l98_gemv.h"
+#include <climits>
 
 // One launch over b.n jobs; m <= M live token rows (M a power of two).
 template <int M, int PJ, int MODES>
@@ -10,10 +11,14 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv_q8(GemvBatch batch, int m
     __shared__ int s_row[M];
     __shared__ float s_inv[M], tab[32];
     const int blk = blockIdx.x;
+    // tile0[] ascends and its entries past n hold INT_MAX (the launcher), so
+    // the job is the last one whose first tile is <= blk; the whole job is
+    // then read at once (one batch of scalar loads, not one per use)
     int j = 0;
 #pragma unroll
-    for (int i = 1; i < MAX_GEMV_JOBS; i++) j += (i < batch.n && blk >= batch.tile0[i]) ? 1 : 0;
-    const GemvJob &job = batch.job[j];
+    for (int i = 1; i < MAX_GEMV_JOBS; i++) j = blk >= batch.tile0[i] ? i : j;
+    j = __builtin_amdgcn_readfirstlane(j);
+    const GemvJob job = batch.job[j];
     const int row0 = (blk - job.tile0) * job.R;
     const int rows_here = imin(job.R, job.rows - row0);
     if (threadIdx.x < M) s_row[threadIdx.x] = threadIdx.x < m ? threadIdx.x : 0;
@@ -53,6 +58,7 @@ extern "C" int l98k_gemv(GemvBatch *b, int m, hipStream_t st) {
     const int M = m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8;
     int tiles = 0, pj = 0, modes = 0;
     size_t lds = 0;
+    for (int j = b->n; j < MAX_GEMV_JOBS; j++) b->tile0[j] = INT_MAX;
     for (int j = 0; j < b->n; j++) {
         GemvJob &J = b->job[j];
         if (J.in_dim < 32 || (J.in_dim & 31) || J.in_dim > GEMV_MAX_IN || J.rows < 1 ||
