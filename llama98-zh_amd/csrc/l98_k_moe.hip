@@ -14,12 +14,10 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_expert_gemv(ExpertJob j0, Expe
     extern __shared__ __align__(16) char smem[];
     __shared__ int s_orow[M];
     __shared__ float s_inv[M], tab[32];
-    const int per_job = max_groups * tiles;
-    const int jb = blockIdx.x / per_job;
-    const int rem = blockIdx.x - jb * per_job;
-    const int gi = rem / tiles;
-    const int tile = rem - gi * tiles;
-    const ExpertJob &J = jb == 0 ? j0 : j1;
+    const int tile = blockIdx.x, gi = blockIdx.y, jb = blockIdx.z;   // grid (tiles, max_groups, jobs)
+    (void)max_groups;
+    const ExpertJob J = jb == 0 ? j0 : j1;
+    asm volatile("" ::"s"(in_dim), "s"(out_rows), "s"(R));
     // the group's table entries in one batch, before the group count is
     // known (gi < max_groups <= MAX_PAIRS keeps every read inside the table;
     // a block past the count returns before it uses them), so the weights
@@ -28,7 +26,9 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_expert_gemv(ExpertJob j0, Expe
     int memv[M];
 #pragma unroll
     for (int t = 0; t < M; t++) memv[t] = grp->member[gi][t];
-    asm volatile("" : "+s"(ng), "+s"(e), "+s"(nm));
+    // the job's fields the tile uses join the same wait
+    asm volatile("" : "+s"(ng), "+s"(e), "+s"(nm) : "s"(J.q), "s"(J.s), "s"(J.out), "s"(J.pro.src), "s"(J.pro.src2),
+                 "s"(J.pro.src_stride), "s"(J.xq_by_pair));
 #pragma unroll
     for (int t = 0; t < M; t++) asm volatile("" : "+s"(memv[t]));
     if (gi >= ng) return;
@@ -295,16 +295,14 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_up(ExpertJob j0, ExpertJob
     __shared__ RouteLds rt;
     __shared__ int s_orow[M];
     __shared__ float s_inv[M], tab[32];
-    const int per_job = max_groups * tiles;
-    const int jb = blockIdx.x / per_job;
-    const int rem = blockIdx.x - jb * per_job;
-    const int gi = rem / tiles;
-    const int tile = rem - gi * tiles;
+    const int tile = blockIdx.x, gi = blockIdx.y, jb = blockIdx.z;   // grid (tiles, max_groups, jobs)
+    (void)max_groups;
     // the projection's arguments read now, so their loads overlap the routing
     const ExpertJob J = jb == 0 ? j0 : j1;
+    asm volatile("" ::"s"(J.q), "s"(J.s), "s"(J.out), "s"(J.pro.src), "s"(J.pro.src_stride), "s"(J.xq_by_pair));
     const RouteSet rs = route_block(logits, bias, E, topk, nt, rt, tab);
     const int ng = rs.ng;
-    if (blockIdx.x == 0) {                 // publish the routing
+    if ((blockIdx.x | blockIdx.y | blockIdx.z) == 0) {   // publish the routing
         const int tid = threadIdx.x;
         if (tid < nt * topk) {
             sel_idx[tid] = rt.sel[tid];
@@ -392,7 +390,7 @@ extern "C" int l98k_expert_gemv(const ExpertJob *jobs, int n_jobs, const MoeGrou
     const size_t lds = gemv_lds_bytes(M, in_dim, R, 0, 0);
     if (lds > gemv_lds_limit()) return -1;
     const int pj = pro_pj(in_dim);
-    const dim3 grid(n_jobs * max_groups * tiles), blk(GEMV_THREADS);
+    const dim3 grid(tiles, max_groups, n_jobs), blk(GEMV_THREADS);
     const ExpertJob &a = jobs[0], &b2 = n_jobs > 1 ? jobs[1] : jobs[0];
     EXPERT_DISPATCH(k_expert_gemv, M, pj, grid, blk, lds, st, a, b2, grp, max_groups, in_dim, out_rows, R, tiles);
     return (int)hipGetLastError();
@@ -411,7 +409,7 @@ extern "C" int l98k_moe_up(const ExpertJob *jobs, int n_jobs, const float *logit
     const size_t lds = gemv_lds_bytes(M, in_dim, R, 0, 0);
     if (lds > gemv_lds_limit()) return -1;
     const int pj = pro_pj(in_dim);
-    const dim3 grid(n_jobs * max_groups * tiles), blk(GEMV_THREADS);
+    const dim3 grid(tiles, max_groups, n_jobs), blk(GEMV_THREADS);
     const ExpertJob &a = jobs[0], &b2 = n_jobs > 1 ? jobs[1] : jobs[0];
     EXPERT_DISPATCH(k_moe_up, M, pj, grid, blk, lds, st, a, b2, logits, bias, E, topk, nt, sel_idx, sel_w, grp, tally,
                     max_groups, in_dim, out_rows, R, tiles);
