@@ -479,7 +479,9 @@ static int lds_limit() {
 }
 
 extern "C" int l98k_attn(const AttnArgs *a, int nt, int max_len, float *att, hipStream_t st) {
-    if (a->nkv < 1 || a->nh % a->nkv || (a->hd & 31) || a->hd > ATT_MAX_HD || a->rot > a->hd || (a->rot & 1) ||
+    // hd divides 256: the new K rows' quantization takes 32-lane groups of
+    // a 256-thread block
+    if (a->nkv < 1 || a->nh % a->nkv || (a->hd & 31) || 256 % a->hd || a->hd > ATT_MAX_HD || a->rot > a->hd || (a->rot & 1) ||
         nt < 1 || nt > MAX_CHUNK || max_len < 1 || !a->oq || !a->oqs || !att)
         return -1;
     const int kv_mul = a->nh / a->nkv;
