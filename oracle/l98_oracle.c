@@ -22,7 +22,17 @@
  *     against libm within their documented error;
  *   - quantize / matmul / argmax / route / accept are checked against closed
  *     forms and brute force (integer sums, first-index tie breaks, injected
- *     u boundaries).
+ *     u boundaries);
+ *   - o_fwht_i32 / o_fwht_f32 are compared with the reference's exported
+ *     lz_fwht_i32 / lz_fwht and with a dense Sylvester matrix product;
+ *     o_subn_fwht_quant / o_subn_rot_f32 restate static functions of
+ *     src/forward_kda.c that no exported symbol reaches: they are checked by
+ *     closed forms (a zero row, each group's largest code being 127, the
+ *     dequantized row against H.x / sqrt(blk), the float rotation against
+ *     the dense product), built from the reference's exported pow2f,
+ *     q8_amax and lz_rsqrt_float_body; the scale's left-to-right multiply
+ *     order follows the text of src/forward_kda.c:79 and is otherwise
+ *     unpinned.
  */
 #define _POSIX_C_SOURCE 200809L
 #include <float.h>
@@ -233,6 +243,112 @@ ORA_API void o_quantize_q8(const float *x, int n, int8_t *q, float *s) {
             q[g * 32 + k] = (int8_t)((qi < -127) ? -127 : qi);
         }
     }
+}
+
+/* lz_fwht_i32's scalar body (src/fwht.c:65-196; the loop at :186-195): the
+ * Sylvester butterflies u+v, u-v at strides 1, 2, 4, ... n/2 over a copy of
+ * x, in wrapping int32 (computed in uint32 so the wrap is defined). */
+ORA_API void o_fwht_i32(int32_t *y, const int32_t *x, int n) {
+    int len, i, j;
+    for (i = 0; i < n; i++) y[i] = x[i];
+    for (len = 1; len < n; len <<= 1)
+        for (i = 0; i < n; i += len << 1)
+            for (j = 0; j < len; j++) {
+                uint32_t u = (uint32_t)y[i + j], v = (uint32_t)y[i + j + len];
+                y[i + j] = (int32_t)(u + v);
+                y[i + j + len] = (int32_t)(u - v);
+            }
+}
+
+/* lz_fwht (src/fwht.c:198-320; the loop at :310-319): the same butterflies
+ * in float, in place. */
+ORA_API void o_fwht_f32(float *v, int n) {
+    int len, i, j;
+    for (len = 1; len < n; len <<= 1)
+        for (i = 0; i < n; i += len << 1)
+            for (j = 0; j < len; j++) {
+                float a = v[i + j], b = v[i + j + len];
+                v[i + j] = a + b;
+                v[i + j + len] = a - b;
+            }
+}
+
+/* pow2f (src/ops_quant.c:77-83): 2^e from the exponent field; 0 below
+ * 2^-126, 2^127 above. */
+static float o_pow2f(int e) {
+    union { float f; uint32_t u; } b;
+    if (e < -126) return 0.0f;
+    if (e > 127) e = 127;
+    b.u = (uint32_t)(e + 127) << 23;
+    return b.f;
+}
+
+/* subn_fwht_quant (src/forward_kda.c:43-92), the SubLN o_proj / down_proj
+ * input quantization of one row of n floats:
+ *   amax by |bits|; a zero row gives q = 0, s = 1;
+ *   S = pow2f(14 - e(amax)), so the row max lands in [2^14, 2^15);
+ *   t = block-diagonal FWHT (block blk) of q8_round(x * S), exact int32;
+ *   per group of gw elements (gw = n unless gw is a multiple of 32 dividing
+ *   n): tam = max |t|, scale = (float)tam * (1/S) * rsqrt(blk) * (1/127)
+ *   left to right; tam == 0 or scale < 1e-30 gives scale 1 and q = 0;
+ *   else q = clamp(q8_round(t * (127/tam)), +-127);
+ *   s holds the group's scale in each of its n/32 slots. */
+ORA_API void o_subn_fwht_quant(const float *x, int n, int blk, int gw, int8_t *q, float *s) {
+    static const float INV127 = 1.0f / 127.0f;
+    union { float f; uint32_t u; } b;
+    uint32_t am = 0;
+    float S, inv_S, rs;
+    int i, e, base;
+    int32_t *f = (int32_t *)malloc(sizeof(int32_t) * 2 * (size_t)n);
+    for (i = 0; i < n; i++) {
+        b.f = x[i];
+        if ((b.u & 0x7FFFFFFFu) > am) am = b.u & 0x7FFFFFFFu;
+    }
+    b.u = am;
+    if (b.f <= 0.0f) {
+        for (i = 0; i < n; i++) q[i] = 0;
+        for (i = 0; i < n / 32; i++) s[i] = 1.0f;
+        free(f);
+        return;
+    }
+    e = (int)((am >> 23) & 0xFFu) - 127;
+    S = o_pow2f(14 - e);
+    inv_S = 1.0f / S;
+    for (i = 0; i < n; i++) f[i] = q8_round(x[i] * S);
+    for (base = 0; base < n; base += blk) o_fwht_i32(f + n + base, f + base, blk);
+    if (gw <= 0 || (gw & 31) != 0 || (n % gw) != 0) gw = n;
+    rs = o_rsqrt((float)blk);
+    for (base = 0; base < n; base += gw) {
+        int32_t tam = 0;
+        float scale, inv_q;
+        for (i = base; i < base + gw; i++) {
+            int32_t a = f[n + i] < 0 ? (int32_t)(0u - (uint32_t)f[n + i]) : f[n + i];
+            if (a > tam) tam = a;
+        }
+        scale = (float)tam * inv_S * rs * INV127;
+        if (tam == 0 || scale < 1.0e-30f) {
+            scale = 1.0f;
+            inv_q = 0.0f;
+        } else {
+            inv_q = 127.0f / (float)tam;
+        }
+        for (i = base; i < base + gw; i++) {
+            int qv = q8_round((float)f[n + i] * inv_q);
+            qv = qv > 127 ? 127 : qv;
+            q[i] = (int8_t)(qv < -127 ? -127 : qv);
+        }
+        for (i = base / 32; i < (base + gw) / 32; i++) s[i] = scale;
+    }
+    free(f);
+}
+
+/* subn_rot_f32 (src/forward_kda.c:130-135): the same block-diagonal
+ * Hadamard on the float row, then each element times rsqrt(blk). */
+ORA_API void o_subn_rot_f32(float *x, int n, int blk) {
+    float inv = o_rsqrt((float)blk);
+    int i;
+    for (i = 0; i < n; i += blk) o_fwht_f32(x + i, blk);
+    for (i = 0; i < n; i++) x[i] *= inv;
 }
 
 /* lz_matmul_xq_nt for a Q8_0 per-row weight (gs = in), SIMD row kernel +

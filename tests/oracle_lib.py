@@ -64,6 +64,10 @@ def lib():
             "o_l2norm": (None, [_FP, _FP, C.c_int, C.c_float]),
             "o_softmax": (None, [_FP, C.c_int]),
             "o_quantize_q8": (None, [_FP, C.c_int, _P, _FP]),
+            "o_fwht_i32": (None, [_IP, _IP, C.c_int]),
+            "o_fwht_f32": (None, [_FP, C.c_int]),
+            "o_subn_fwht_quant": (None, [_FP, C.c_int, C.c_int, C.c_int, _P, _FP]),
+            "o_subn_rot_f32": (None, [_FP, C.c_int, C.c_int]),
             "o_matmul_q8": (None, [_FP, _P, _FP, _P, _FP, C.c_int, C.c_int, C.c_int, _IP]),
             "o_recur_step": (None, [_FP, _FP, _FP, _FP, _FP, _FP, _FP, C.c_float, C.c_int, C.c_int]),
             "o_moe_route": (None, [_FP, _FP, C.c_int, C.c_int, _IP, _FP]),
