@@ -19,6 +19,8 @@
 #ifndef LLAMA98_HIP_H
 #define LLAMA98_HIP_H
 
+#include <stdint.h>
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -218,6 +220,26 @@ int l98_time_kernel(const LZModel *m, LZRunState *s, int which, int mrows, int i
  * squares.  No reference counterpart: a check of that routine on arbitrary
  * inputs.  Returns 0 (1 on a bad argument or a device error). */
 int l98_row_sums(const float *x, int rows, int n, float *out);
+
+/* Block-diagonal Walsh-Hadamard transforms of the SubLN variant
+ * (use_subn = 1, hadamard_o / hadamard_down > 0), on the device, over host
+ * arrays of `rows` rows of n <= 8192 elements; blk is a power of two
+ * dividing n.  Each returns 0 (1 on a bad argument or a device error).
+ *
+ * l98_fwht_i32 replaces lz_fwht_i32 (src/fwht.c:65, src/fwht.h), applied to
+ * each blk-block of each row: y = H x in wrapping int32. */
+int l98_fwht_i32(const int32_t *x, int32_t *y, int rows, int n, int blk);
+/* l98_fwht_f32 replaces lz_fwht (src/fwht.c:198, declared in src/ops.h) on
+ * each blk-block, in place; rot = 1 then multiplies every element by
+ * rsqrt(blk) (lz_rsqrt_float_body), which is subn_rot_f32
+ * (src/forward_kda.c:130-135). */
+int l98_fwht_f32(float *v, int rows, int n, int blk, int rot);
+/* subn_fwht_quant (src/forward_kda.c:43-92, a static function of the
+ * reference, so no FFI binds it today): each row of n (n % 32 == 0) floats
+ * to n int8 codes in q and n / 32 scales in s, one scale per gw elements
+ * (gw = n unless gw is a multiple of 32 dividing n), repeated in each of
+ * the group's 32-element slots, as lz_matmul_xq_nt reads them. */
+int l98_subn_fwht_quant(const float *x, int rows, int n, int blk, int gw, int8_t *q, float *s);
 /* Index-order prefix queries over `rows` rows of n non-negative floats
  * (host arrays), answered on the device by the routine the temperature
  * sampler uses for its softmax sums and cdf scans: mode 0 gives in outv[r]

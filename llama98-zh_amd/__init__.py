@@ -113,6 +113,9 @@ HIP_API = [
     ("l98_greedy_rounds_batch", C.c_int, [C.POINTER(LZModel), C.POINTER(C.POINTER(LZRunState)), C.c_int, C.c_int,
                                           C.c_int, _IP, C.c_int, _IP, _FP]),
     ("l98_row_sums", C.c_int, [_FP, C.c_int, C.c_int, _FP]),
+    ("l98_fwht_i32", C.c_int, [_IP, _IP, C.c_int, C.c_int, C.c_int]),
+    ("l98_fwht_f32", C.c_int, [_FP, C.c_int, C.c_int, C.c_int, C.c_int]),
+    ("l98_subn_fwht_quant", C.c_int, [_FP, C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p, _FP]),
     ("l98_prefix_query", C.c_int, [_FP, C.c_int, C.c_int, C.c_int, _FP, _IP, _FP]),
     ("l98_moe_route", C.c_int, [_FP, _FP, C.c_int, C.c_int, C.c_int, _IP, _FP]),
     ("l98_device_name", C.c_char_p, []),

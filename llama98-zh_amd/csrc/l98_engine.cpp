@@ -1476,6 +1476,50 @@ extern "C" int l98_row_sums(const float *x, int rows, int n, float *out) {
     return rc;
 }
 
+// Host arrays in, host arrays out: device copies, one launch, copies back.
+namespace {
+struct DevBuf {
+    void *p = nullptr;
+    ~DevBuf() { if (p) (void)hipFree(p); }
+    bool get(const void *src, size_t bytes) {
+        if (hipMalloc(&p, bytes) != hipSuccess) { p = nullptr; return false; }
+        return !src || hipMemcpy(p, src, bytes, hipMemcpyHostToDevice) == hipSuccess;
+    }
+    bool put(void *dst, size_t bytes) const { return hipMemcpy(dst, p, bytes, hipMemcpyDeviceToHost) == hipSuccess; }
+};
+bool fwht_args_ok(int rows, int n, int blk) {
+    return rows >= 1 && n >= 1 && n <= 8192 && blk >= 1 && blk <= n && (blk & (blk - 1)) == 0 && n % blk == 0;
+}
+}  // namespace
+
+extern "C" int l98_fwht_i32(const int32_t *x, int32_t *y, int rows, int n, int blk) {
+    if (!x || !y || !fwht_args_ok(rows, n, blk)) return 1;
+    const size_t b = sizeof(int32_t) * (size_t)rows * n;
+    DevBuf dx, dy;
+    if (!dx.get(x, b) || !dy.get(nullptr, b)) return 1;
+    if (l98k_fwht_i32((const int32_t *)dx.p, (int32_t *)dy.p, rows, n, blk, nullptr)) return 1;
+    return dy.put(y, b) ? 0 : 1;
+}
+
+extern "C" int l98_fwht_f32(float *v, int rows, int n, int blk, int rot) {
+    if (!v || !fwht_args_ok(rows, n, blk)) return 1;
+    const size_t b = sizeof(float) * (size_t)rows * n;
+    DevBuf dv;
+    if (!dv.get(v, b)) return 1;
+    if (l98k_fwht_f32((float *)dv.p, rows, n, blk, rot, nullptr)) return 1;
+    return dv.put(v, b) ? 0 : 1;
+}
+
+extern "C" int l98_subn_fwht_quant(const float *x, int rows, int n, int blk, int gw, int8_t *q, float *s) {
+    if (!x || !q || !s || !fwht_args_ok(rows, n, blk) || n % 32 != 0) return 1;
+    const size_t nx = (size_t)rows * n;
+    DevBuf dx, dq, ds;
+    if (!dx.get(x, sizeof(float) * nx) || !dq.get(nullptr, nx) || !ds.get(nullptr, sizeof(float) * (nx / 32)))
+        return 1;
+    if (l98k_subn_quant((const float *)dx.p, rows, n, blk, gw, (int8_t *)dq.p, (float *)ds.p, nullptr)) return 1;
+    return dq.put(q, nx) && ds.put(s, sizeof(float) * (nx / 32)) ? 0 : 1;
+}
+
 extern "C" int l98_moe_route(const float *logits, const float *bias, int nt, int E, int topk, int *idx, float *w) {
     if (!logits || !idx || !w || nt < 1 || nt > MAX_CHUNK || E < 1 || E > MAX_EXPERTS || topk < 1 || topk > MAX_TOPK)
         return 1;

@@ -76,6 +76,13 @@ int l98k_moe_route(const float *logits, const float *bias, int E, int topk, int 
 int l98k_moe_up(const ExpertJob *jobs, int n_jobs, const float *logits, const float *bias, int E, int topk, int nt,
                 int *sel_idx, float *sel_w, MoeGroups *grp, int *tally, int in_dim, int out_rows, hipStream_t st);
 int l98k_row_sums(const float *x, int rows, int n, float *out, hipStream_t st);
+// Block-diagonal Walsh-Hadamard transforms, one block per row of n <= 8192
+// (blk a power of two dividing n): lz_fwht_i32 / lz_fwht on each block,
+// rot = 1 adds subn_rot_f32's rsqrt(blk) factor; l98k_subn_quant is
+// subn_fwht_quant (n % 32 == 0; q: rows x n, s: rows x n / 32).
+int l98k_fwht_i32(const int32_t *x, int32_t *y, int rows, int n, int blk, hipStream_t st);
+int l98k_fwht_f32(float *v, int rows, int n, int blk, int rot, hipStream_t st);
+int l98k_subn_quant(const float *x, int rows, int n, int blk, int gw, int8_t *q, float *s, hipStream_t st);
 int l98k_argmax(const float *x, int n, int rows, int mode, int *out, unsigned long long *partial,
                 unsigned *counter, hipStream_t st);
 int l98k_accept(DevCtl *ctl, const float *vhidden, int d, float *chain, int depth, int brk, hipStream_t st);
