@@ -40,7 +40,13 @@ enum {
     LZ_ERR_BIN_VERSION = 84
 };
 
+#define LZ_KVF_Q8 0           /* src/forward.h:428 */
+#define LZ_PROF_N 7           /* src/forward.h:502 */
 #define LZ_SPEC_K_MAX 6      /* src/ops.h:2098 */
+/* This library's own draft-width cap: the l98_* generation loops run k up to
+ * 7 (a verify of M = 8 = LZ_BATCH_MAX rows).  The reference-named entry
+ * points keep the reference's LZ_SPEC_K_MAX check and error. */
+#define L98_SPEC_K_GPU 7
 #define LZ_BATCH_MAX 8       /* src/ops.h:1457 */
 
 /* The LZModelConfig fields the spec path reads (src/model.h:237-874). */
@@ -71,8 +77,8 @@ typedef struct {
     int nt_cap;                    /* tokens per forward chunk */
     /* host mirrors, refreshed by the call that returns or fills them */
     float *logits;                 /* vocab: lz_forward_capture */
-    float *mtp_logits;             /* (LZ_SPEC_K_MAX+1) x vocab: lz_forward_verify */
-    float *mtp_verify_hidden;      /* (LZ_SPEC_K_MAX+1) x hidden: lz_forward_verify */
+    float *mtp_logits;             /* (L98_SPEC_K_GPU+1) x vocab: lz_forward_verify */
+    float *mtp_verify_hidden;      /* (L98_SPEC_K_GPU+1) x hidden: lz_forward_verify */
     float *mtp_chain;              /* hidden: after capture / draft / round */
     float *mtp_draft_logits;       /* vocab: lz_mtp_draft_step */
     long long bytes_device;
@@ -102,20 +108,32 @@ typedef struct {
 } LZSampler;
 
 /* ---- model (src/model.h:1327-1341) ---- */
-/* Reads <dir>/model.bin and uploads the weights to the current HIP device.
- * Returns 0, or 1 with a message in errbuf. */
+/* lz_load_config (src/model.h:1327): the model's configuration without
+ * loading it.  This path reads model.bin only: path is a model.bin or a
+ * directory holding one (a config.json is refused).  Returns 0, or 1 with a
+ * message. */
+int lz_load_config(LZModelConfig *c, const char *path, char *errbuf, int errlen);
+/* Reads <dir>/model.bin and uploads the weights to the current HIP device
+ * (the reference also reads a model.bin whole in lz_open,
+ * src/model.c:3264-3266).  Returns 0, or 1 with a message in errbuf. */
 int lz_open(LZModel *m, const char *dir, char *errbuf, int errlen);
+/* lz_read_weights (src/model.h:1337): the weights of a model.bin are loaded
+ * by lz_open, so this returns 0 for an open model, 1 otherwise. */
+int lz_read_weights(LZModel *m, char *errbuf, int errlen);
 void lz_free(LZModel *m);
 
 /* ---- run state (src/forward.h:1883-1933) ---- */
-/* Returns 0, or 1 with a message. Ring depth is spec_k_max + 1 (clamped to
- * LZ_SPEC_K_MAX + 1).  seq_len <= 0 takes the model's. */
+/* Returns 0, or 1 with a message. Ring depth is spec_k_max + 1 (spec_k_max
+ * clamped to L98_SPEC_K_GPU).  seq_len <= 0 takes the model's. */
 int lz_state_alloc(LZRunState *s, const LZModel *m, int seq_len, int spec_k_max,
                    char *errbuf, int errlen);
 void lz_state_free(LZRunState *s);
 void lz_state_reset(LZRunState *s, const LZModel *m);
 
-/* ---- forward (src/forward.h:1940-2150) ---- */
+/* ---- forward (src/forward.h:1937-2150) ---- */
+/* lz_forward (src/forward.h:1937): one token at pos; returns the host
+ * logits mirror s->logits (do not free), or NULL.  mtp_chain is untouched. */
+float *lz_forward(const LZModel *m, LZRunState *s, int token, int pos);
 /* One token; its final-normed hidden goes to mtp_chain.  Returns the host
  * logits mirror, or NULL on a bad token/position. */
 float *lz_forward_capture(const LZModel *m, LZRunState *s, int token, int pos);
@@ -160,6 +178,33 @@ void lz_sampler_free(LZSampler *s);
 float lz_random_f32(lz_u64 *state);
 int lz_sample_argmax(const float *logits, int n);
 int lz_argmax_p1(const float *logits, int n, float *out_p);
+
+/* ---- exported data (llama98.def:117-157; src/forward.c:29-448,
+ * src/generate.c:226) ----
+ * Counters, updated as the reference's are: lz_debug_us_draft / _verify /
+ * _capture / _catchup (microseconds; device time between stream marks for
+ * the device-resident round), lz_debug_n_capture / _catchup /
+ * _ring_rollback / _chunks / _lmhead.  The device-resident loops
+ * (l98_greedy_rounds, l98_generate) add their rounds' rollback, catch-up,
+ * chunk and lm_head counts but no per-phase times.
+ * Knobs: this path implements one setting of each, which is the value they
+ * hold: Q8 K and V caches, no KV rotation, no attention sink or window
+ * (lz_attn_window 0; the reference's default -1 selects an automatic
+ * window), the model's own top-k (lz_moe_topk 0) at lz_moe_tau 1, and no
+ * MTP attention probes.  lz_state_alloc and every forward or round entry
+ * point refuse to run when a caller has set another value.  lz_prof_us
+ * stays zero: per-section times come from rocprofv3 on this path. */
+extern long long lz_debug_us_draft, lz_debug_us_verify, lz_debug_us_capture, lz_debug_us_catchup;
+extern long long lz_debug_n_capture, lz_debug_n_catchup, lz_debug_n_ring_rollback;
+extern long long lz_debug_n_chunks, lz_debug_n_lmhead, lz_debug_n_kv_rot, lz_debug_attn_skip;
+extern long long lz_debug_mtp_attn_rows;
+extern float lz_debug_mtp_attn_scale;
+extern int lz_debug_mtp_attn_window;
+extern int lz_kv_kfmt, lz_kv_vfmt, lz_kv_rot_enable, lz_attn_sink, lz_attn_window;
+extern int lz_moe_topk;
+extern float lz_moe_tau;
+extern int lz_prof_enable;
+extern float lz_prof_us[LZ_PROF_N];
 
 /* ---- this implementation's own additions (no reference counterpart) ---- */
 /* The whole generation loop of lz_generate's --spec path
@@ -259,6 +304,13 @@ int l98_prefix_query(const float *x, int rows, int n, int mode, const float *c, 
  * reference routes inside forward_moe (src/forward_moe.c:96-98).  Returns 0
  * (1 on a bad argument or a device error). */
 int l98_moe_route(const float *logits, const float *bias, int nt, int E, int topk, int *idx, float *w);
+/* The device argmax of the draft steps and verify rows, on `rows` (<= 8)
+ * host rows of n floats: mode 0 is lz_sample_argmax (src/sampler.c:226-243,
+ * order-preserving key, first index wins), mode 1 the index lz_argmax_p1
+ * returns (src/sampler.c:279-295: float '>' from element 0, so a NaN at 0
+ * stays the answer).  A check of the kernel the rounds run; the reference
+ * has no device.  Returns 0 (1 on a bad argument or a device error). */
+int l98_argmax_rows(const float *x, int rows, int n, int mode, int *out);
 /* Device and build facts, for logs. */
 const char *l98_device_name(void);
 /* Seconds of device time of the last l98_generate call's round loop

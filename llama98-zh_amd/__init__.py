@@ -20,6 +20,7 @@ HIP_LIB = os.path.join(LIB_DIR, "libl98hip.so")
 SYNTH_LIB = os.path.join(LIB_DIR, "libl98synth.so")
 
 LZ_SPEC_K_MAX = 6
+L98_SPEC_K_GPU = 7      # the library's own loops take k up to 7 (verify M = 8)
 LZ_BATCH_MAX = 8
 LZ_ERR = {"NULL_ARG": 6, "STATE_ALLOC": 7, "FORWARD": 20, "SPEC_NO_HEAD": 24, "SPEC_K_RANGE": 25}
 
@@ -65,7 +66,8 @@ class L98SynthConfig(C.Structure):
         "vocab", "hidden", "n_layers", "seq_len", "attn_period", "n_heads", "n_kv_heads", "head_dim",
         "kda_heads", "kd", "vd", "conv_kernel", "gate_rank", "n_experts", "topk", "latent",
         "moe_inter", "shared_w", "mtp_inter")] + [
-        ("w_std", C.c_float), ("router_std", C.c_float), ("bias_std", C.c_float)]
+        ("w_std", C.c_float), ("router_std", C.c_float), ("bias_std", C.c_float), ("resid_std", C.c_float),
+        ("mtp_echo", C.c_int)]
 
 
 _P = C.c_void_p
@@ -74,7 +76,10 @@ _FP = C.POINTER(C.c_float)
 
 # (name, restype, argtypes) of every entry point include/llama98_hip.h declares.
 HIP_API = [
+    ("lz_load_config", C.c_int, [C.POINTER(LZModelConfig), C.c_char_p, C.c_char_p, C.c_int]),
     ("lz_open", C.c_int, [C.POINTER(LZModel), C.c_char_p, C.c_char_p, C.c_int]),
+    ("lz_read_weights", C.c_int, [C.POINTER(LZModel), C.c_char_p, C.c_int]),
+    ("lz_forward", _FP, [C.POINTER(LZModel), C.POINTER(LZRunState), C.c_int, C.c_int]),
     ("lz_free", None, [C.POINTER(LZModel)]),
     ("lz_state_alloc", C.c_int, [C.POINTER(LZRunState), C.POINTER(LZModel), C.c_int, C.c_int, C.c_char_p, C.c_int]),
     ("lz_state_free", None, [C.POINTER(LZRunState)]),
@@ -118,9 +123,27 @@ HIP_API = [
     ("l98_subn_fwht_quant", C.c_int, [_FP, C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p, _FP]),
     ("l98_prefix_query", C.c_int, [_FP, C.c_int, C.c_int, C.c_int, _FP, _IP, _FP]),
     ("l98_moe_route", C.c_int, [_FP, _FP, C.c_int, C.c_int, C.c_int, _IP, _FP]),
+    ("l98_argmax_rows", C.c_int, [_FP, C.c_int, C.c_int, C.c_int, _IP]),
     ("l98_device_name", C.c_char_p, []),
     ("l98_last_loop_seconds", C.c_double, []),
 ]
+
+# Exported data (llama98.def:117-157): name -> ctypes type.
+HIP_DATA = {n: C.c_longlong for n in (
+    "lz_debug_us_draft", "lz_debug_us_verify", "lz_debug_us_capture", "lz_debug_us_catchup",
+    "lz_debug_n_capture", "lz_debug_n_catchup", "lz_debug_n_ring_rollback", "lz_debug_n_chunks",
+    "lz_debug_n_lmhead", "lz_debug_n_kv_rot", "lz_debug_attn_skip", "lz_debug_mtp_attn_rows")}
+HIP_DATA.update({n: C.c_int for n in (
+    "lz_debug_mtp_attn_window", "lz_kv_kfmt", "lz_kv_vfmt", "lz_kv_rot_enable", "lz_attn_sink", "lz_attn_window",
+    "lz_moe_topk", "lz_prof_enable")})
+HIP_DATA.update({"lz_debug_mtp_attn_scale": C.c_float, "lz_moe_tau": C.c_float, "lz_prof_us": C.c_float * 7})
+
+
+def hip_data(name):
+    """The library's exported variable `name` (a ctypes object: .value reads
+    and writes it)."""
+    return HIP_DATA[name].in_dll(hip_lib(), name)
+
 
 _hip = None
 _synth = None
@@ -259,8 +282,8 @@ class Engine:
         rc = self.lib.lz_forward_verify(C.byref(self.m), C.byref(self.s), _ip(tokens), n, int(pos0))
         if rc != 0:
             return None
-        lg = np.ctypeslib.as_array(self.s.mtp_logits, shape=(LZ_SPEC_K_MAX + 1, self.V))[:n].copy()
-        hd = np.ctypeslib.as_array(self.s.mtp_verify_hidden, shape=(LZ_SPEC_K_MAX + 1, self.d))[:n].copy()
+        lg = np.ctypeslib.as_array(self.s.mtp_logits, shape=(L98_SPEC_K_GPU + 1, self.V))[:n].copy()
+        hd = np.ctypeslib.as_array(self.s.mtp_verify_hidden, shape=(L98_SPEC_K_GPU + 1, self.d))[:n].copy()
         return lg, hd
 
     def draft_step(self, token, pos):
@@ -278,7 +301,7 @@ class Engine:
         return self.lib.lz_mtp_prefill(C.byref(self.m), C.byref(self.s), _fp(h), _ip(nt), len(nt), int(pos0))
 
     def spec_round(self, anchor, anchor_pos, k, p_min=0.0, n_min=0, brk=0, skipc=0):
-        out = np.zeros(LZ_SPEC_K_MAX + 1, np.int32)
+        out = np.zeros(L98_SPEC_K_GPU + 1, np.int32)
         na, npos, ke = C.c_int(), C.c_int(), C.c_int()
         err = C.create_string_buffer(256)
         r = self.lib.lz_spec_round(C.byref(self.m), C.byref(self.s), int(anchor), int(anchor_pos), int(k),
@@ -355,8 +378,8 @@ class Engine:
             return ms.value, None
         out = []
         for st in states:
-            lg = np.ctypeslib.as_array(st.mtp_logits, shape=(LZ_SPEC_K_MAX + 1, self.V))[:n_tok].copy()
-            hd = np.ctypeslib.as_array(st.mtp_verify_hidden, shape=(LZ_SPEC_K_MAX + 1, self.d))[:n_tok].copy()
+            lg = np.ctypeslib.as_array(st.mtp_logits, shape=(L98_SPEC_K_GPU + 1, self.V))[:n_tok].copy()
+            hd = np.ctypeslib.as_array(st.mtp_verify_hidden, shape=(L98_SPEC_K_GPU + 1, self.d))[:n_tok].copy()
             out.append((lg, hd))
         return ms.value, out
 
@@ -372,9 +395,48 @@ class Engine:
             raise RuntimeError(f"l98_greedy_rounds_batch failed: {n}")
         return ms.value, [toks[i, :n_out[i]].copy() for i in range(len(states))]
 
+    def generate_host(self, prompt, k, n_new, p_min=0.0, n_min=0, brk=0, skipc=0):
+        """The reference's --spec generation loop driven from the host through
+        the reference entry points (lz_forward_batch_capture, lz_mtp_prefill,
+        lz_forward_capture, lz_sample_argmax, lz_spec_round), greedy, as
+        src/generate.c:1822-2106 drives them; a discarded round records
+        n_accept -1.  Returns (tokens, k_eff per round, n_accept per round)."""
+        prompt = np.ascontiguousarray(prompt, np.int32)
+        n_prompt = len(prompt)
+        self.reset()
+        h = self.batch_capture(prompt[:-1], 0)
+        if h is None or self.mtp_prefill(h, prompt[1:], self.s.mtp_pos) != 0:
+            raise RuntimeError("prefill failed")
+        self.s.mtp_pos = n_prompt - 1
+        toks, ke, na = [], [], []
+        token, pos, have_seed = int(prompt[-1]), n_prompt - 1, False
+        while len(toks) < n_new:
+            if have_seed:
+                anchor, anchor_pos = token, pos - 1
+            else:
+                lg = self.forward_capture(token, pos)
+                if lg is None:
+                    raise RuntimeError("lz_forward_capture failed")
+                anchor_pos = pos
+                anchor = self.lib.lz_sample_argmax(_fp(lg), self.V)
+                toks.append(anchor)
+                if len(toks) >= n_new:
+                    break
+            r, out, n_acc, new_pos, k_eff = self.spec_round(anchor, anchor_pos, k, p_min, n_min, brk, skipc)
+            if r < 0:
+                raise RuntimeError(f"lz_spec_round failed: {r}")
+            ke.append(k_eff)
+            na.append(n_acc if r > 0 else -1)
+            have_seed = r > 0
+            if r > 0:
+                toks.extend(int(t) for t in out[:n_acc + 1])
+            pos = new_pos + 1
+            token = int(out[n_acc])
+        return np.array(toks, np.int32), np.array(ke, np.int32), np.array(na, np.int32)
+
     def generate(self, prompt, k, n_new, temp=0.0, topp=1.0, seed=1):
         prompt = np.ascontiguousarray(prompt, np.int32)
-        cap = n_new + LZ_SPEC_K_MAX + 2
+        cap = n_new + L98_SPEC_K_GPU + 2
         toks = np.zeros(cap, np.int32)
         ke = np.zeros(n_new + 8, np.int32)
         na = np.zeros(n_new + 8, np.int32)

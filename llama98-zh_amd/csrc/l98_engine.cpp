@@ -50,6 +50,55 @@ static void set_err(char *buf, int len, const char *fmt, ...) {
     va_end(ap);
 }
 
+// ------------------------------------------------------ data symbols ---
+// The reference's exported data (llama98.def:117-157; definitions
+// src/forward.c:29-448, src/generate.c:226).  The counters are updated by
+// the entry points below as the reference's are; the knobs hold the one
+// configuration this path implements, and an entry point refuses to run if
+// a caller has set another (knobs_ok).
+
+extern "C" {
+long long lz_debug_us_draft = 0, lz_debug_us_verify = 0, lz_debug_us_capture = 0, lz_debug_us_catchup = 0;
+long long lz_debug_n_capture = 0, lz_debug_n_catchup = 0, lz_debug_n_ring_rollback = 0;
+long long lz_debug_n_chunks = 0, lz_debug_n_lmhead = 0, lz_debug_n_kv_rot = 0, lz_debug_attn_skip = 0;
+long long lz_debug_mtp_attn_rows = 0;
+float lz_debug_mtp_attn_scale = 1.0f;
+int lz_debug_mtp_attn_window = 0;
+int lz_kv_kfmt = LZ_KVF_Q8, lz_kv_vfmt = LZ_KVF_Q8;
+int lz_kv_rot_enable = 0, lz_attn_sink = 0, lz_attn_window = 0;
+int lz_moe_topk = 0;
+float lz_moe_tau = 1.0f;
+int lz_prof_enable = 0;
+float lz_prof_us[LZ_PROF_N];
+}
+
+static long long us_since(const timespec &t0) {
+    timespec t1;
+    clock_gettime(CLOCK_MONOTONIC, &t1);
+    return (long long)(t1.tv_sec - t0.tv_sec) * 1000000LL + (t1.tv_nsec - t0.tv_nsec) / 1000;
+}
+static timespec now_ts() {
+    timespec t;
+    clock_gettime(CLOCK_MONOTONIC, &t);
+    return t;
+}
+
+// 1 when the process-global knobs select what this path computes: Q8 K and
+// V caches, no KV rotation, no attention sink or window, the model's own
+// routed top-k at temperature 1, and no MTP attention probes.
+static int knobs_ok(int model_topk, char *errbuf, int errlen) {
+    const char *bad = nullptr;
+    if (lz_kv_kfmt != LZ_KVF_Q8 || lz_kv_vfmt != LZ_KVF_Q8) bad = "lz_kv_kfmt / lz_kv_vfmt other than Q8";
+    else if (lz_kv_rot_enable) bad = "lz_kv_rot_enable";
+    else if (lz_attn_sink || lz_attn_window) bad = "an attention sink or window";
+    else if (lz_moe_topk != 0 && lz_moe_topk != model_topk) bad = "lz_moe_topk other than the model's top-k";
+    else if (lz_moe_tau != 1.0f) bad = "lz_moe_tau other than 1";
+    else if (lz_debug_mtp_attn_scale != 1.0f || lz_debug_mtp_attn_window) bad = "the MTP attention probes";
+    if (!bad) return 1;
+    if (errbuf && errlen > 0) snprintf(errbuf, (size_t)errlen, "%s: not on this path", bad);
+    return 0;
+}
+
 // ------------------------------------------------------------- model ---
 
 struct DMat {
@@ -428,6 +477,44 @@ extern "C" void lz_free(LZModel *m) {
     m->impl = nullptr;
 }
 
+// lz_read_weights (src/model.c:4887-4901): a model.bin is read whole by
+// lz_open (src/model.c:3264-3266), so this only reports whether it is open.
+extern "C" int lz_read_weights(LZModel *m, char *errbuf, int errlen) {
+    if (!m || !m->impl) { set_err(errbuf, errlen, "model not open"); return 1; }
+    return 0;
+}
+
+// lz_load_config (src/model.h:1327): the configuration of a model without
+// loading it.  This path reads model.bin only, so `path` names a model.bin
+// or a directory holding one; its header fills *c after the same checks
+// lz_open makes.
+extern "C" int lz_load_config(LZModelConfig *c, const char *path, char *errbuf, int errlen) {
+    if (!c || !path) { set_err(errbuf, errlen, "null argument"); return 1; }
+    if (errbuf && errlen > 0) errbuf[0] = 0;
+    char file[1024];
+    struct stat st;
+    if (stat(path, &st) == 0 && S_ISDIR(st.st_mode)) snprintf(file, sizeof file, "%s/model.bin", path);
+    else snprintf(file, sizeof file, "%s", path);
+    int fd = open(file, O_RDONLY);
+    if (fd < 0) { set_err(errbuf, errlen, "cannot open %s", file); return 1; }
+    if (fstat(fd, &st) != 0 || st.st_size < 8) { close(fd); set_err(errbuf, errlen, "empty %s", file); return 1; }
+    void *map = mmap(nullptr, (size_t)st.st_size, PROT_READ, MAP_PRIVATE, fd, 0);
+    close(fd);
+    if (map == MAP_FAILED) { set_err(errbuf, errlen, "mmap %s failed", file); return 1; }
+    Bin b;
+    b.p = (const unsigned char *)map;
+    b.n = (size_t)st.st_size;
+    LZModelConfig cfg{};
+    HostTensor embed, fnorm, mg, mu, md, fc, mn, mph, mpe;
+    std::vector<HostLayer> HL;
+    HostLayer hm;
+    int rc = parse_model(b, cfg, embed, fnorm, HL, hm, mg, mu, md, fc, mn, mph, mpe, errbuf, errlen);
+    munmap(map, (size_t)st.st_size);
+    if (rc != 0) return 1;
+    *c = cfg;
+    return 0;
+}
+
 // ------------------------------------------------------------- state ---
 
 struct DState {
@@ -460,12 +547,13 @@ struct DState {
     RoundRec *hist = nullptr;               // device round records
     int hist_cap = 0;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
-    hipGraphExec_t round_graph[LZ_SPEC_K_MAX + 1] = {};
+    hipEvent_t ph[4] = {};                  // phase marks of a host-driven round (draft / verify / catch-up)
+    hipGraphExec_t round_graph[L98_SPEC_K_GPU + 1] = {};
     LZSampler session_samp{};               // the sampler of the current session (l98_session_start)
     bool session_greedy = true;
     // temperature sampling scratch (allocated on first use)
     char *smp_arena = nullptr;
-    float *smp_q = nullptr;                 // [LZ_SPEC_K_MAX][V] draft distributions of a round
+    float *smp_q = nullptr;                 // [L98_SPEC_K_GPU][V] draft distributions of a round
     float *smp_p = nullptr, *smp_probs = nullptr;
     uint32_t *smp_keys = nullptr, *smp_skeys = nullptr;
     int *smp_vals = nullptr, *smp_svals = nullptr;
@@ -516,10 +604,10 @@ bool carve(DState *s) {
     s->h2 = F((size_t)pairs * c.moe_latent_dim);
     s->hb = F((size_t)B * c.mtp_intermediate_size); s->hb2 = F((size_t)B * c.mtp_intermediate_size);
     s->ffn_out = F((size_t)B * d);
-    s->vhidden = F((size_t)(LZ_SPEC_K_MAX + 2) * d);
-    s->mtp_logits = F((size_t)(LZ_SPEC_K_MAX + 2) * c.vocab_size);
+    s->vhidden = F((size_t)(L98_SPEC_K_GPU + 1) * d);
+    s->mtp_logits = F((size_t)(L98_SPEC_K_GPU + 1) * c.vocab_size);
     s->logits = F(c.vocab_size);
-    s->draft_logits = F((size_t)LZ_SPEC_K_MAX * c.vocab_size);
+    s->draft_logits = F((size_t)L98_SPEC_K_GPU * c.vocab_size);
     s->hcap = F((size_t)s->cap_rows * d);
     s->xq = I8((size_t)pairs * wide); s->xqs = F((size_t)pairs * wide / 32);
     s->xq2 = I8((size_t)pairs * wide); s->xqs2 = F((size_t)pairs * wide / 32);
@@ -530,8 +618,8 @@ bool carve(DState *s) {
     s->grp = (MoeGroups *)st_take(s, sizeof(MoeGroups));
     s->ctl = (DevCtl *)st_take(s, sizeof(DevCtl));
     s->tokbuf = (int *)st_take(s, sizeof(int) * (size_t)s->cap_rows);
-    s->amax_part = (unsigned long long *)st_take(s, sizeof(unsigned long long) * (LZ_SPEC_K_MAX + 2) * 64);
-    s->amax_cnt = (unsigned *)st_take(s, sizeof(unsigned) * (LZ_SPEC_K_MAX + 2));
+    s->amax_part = (unsigned long long *)st_take(s, sizeof(unsigned long long) * (L98_SPEC_K_GPU + 1) * 64);
+    s->amax_cnt = (unsigned *)st_take(s, sizeof(unsigned) * (L98_SPEC_K_GPU + 1));
     s->hist_cap = s->seq_len;
     s->hist = (RoundRec *)st_take(s, sizeof(RoundRec) * (size_t)s->hist_cap);
     return true;
@@ -608,6 +696,12 @@ ExpertJob EJ(const ExpertBank &bank, float *out, int by_pair, const Prologue &pr
 // copy is staged at call time, so the host struct may change right after).
 int ctl_put(DState *s, const DevCtl &h) {
     CK(hipMemcpyAsync(s->ctl, &h, sizeof(DevCtl), hipMemcpyHostToDevice, s->st));
+    return 0;
+}
+// The host-API entry points that read mtp_chain take the caller's copy:
+// as in the reference, the struct field is the state a caller may set.
+int chain_put(DState *d, const LZRunState *s) {
+    CK(hipMemcpyAsync(d->chain, s->mtp_chain, sizeof(float) * d->m->c.hidden_size, hipMemcpyHostToDevice, d->st));
     return 0;
 }
 int ctl_get(DState *s, DevCtl *h) {
@@ -830,11 +924,12 @@ extern "C" int lz_state_alloc(LZRunState *s, const LZModel *mm, int seq_len, int
     memset(s, 0, sizeof(*s));
     const DModel *m = Mo(mm);
     const LZModelConfig &c = m->c;
+    if (!knobs_ok(c.num_experts_per_token, errbuf, errlen)) return 1;
     DState *d = new DState();
     d->m = m;
     d->seq_len = seq_len > 0 ? seq_len : c.seq_len;
     if (d->seq_len > c.seq_len) d->seq_len = c.seq_len;   // the rope table covers the model's seq_len
-    d->depth = spec_k_max > 0 ? (spec_k_max + 1 > LZ_SPEC_K_MAX + 1 ? LZ_SPEC_K_MAX + 1 : spec_k_max + 1) : 1;
+    d->depth = spec_k_max > 0 ? (spec_k_max > L98_SPEC_K_GPU ? L98_SPEC_K_GPU : spec_k_max) + 1 : 1;
     d->planes = c.n_full_layers + 1;
     d->kda_slot = (size_t)c.n_linear_layers * c.lin_n_v_heads * c.lin_k_head_dim * c.lin_v_head_dim;
     d->conv_slot = (size_t)c.n_linear_layers * c.lin_conv_dim * (c.conv_kernel - 1);
@@ -850,7 +945,9 @@ extern "C" int lz_state_alloc(LZRunState *s, const LZModel *mm, int seq_len, int
     carve(d);
     if (hipStreamCreateWithFlags(&d->st, hipStreamNonBlocking) != hipSuccess ||
         hipHostMalloc((void **)&d->ctl_pinned, sizeof(DevCtl), hipHostMallocDefault) != hipSuccess ||
-        hipEventCreate(&d->ev0) != hipSuccess || hipEventCreate(&d->ev1) != hipSuccess) {
+        hipEventCreate(&d->ev0) != hipSuccess || hipEventCreate(&d->ev1) != hipSuccess ||
+        hipEventCreate(&d->ph[0]) != hipSuccess || hipEventCreate(&d->ph[1]) != hipSuccess ||
+        hipEventCreate(&d->ph[2]) != hipSuccess || hipEventCreate(&d->ph[3]) != hipSuccess) {
         set_err(errbuf, errlen, "HIP stream/event setup failed");
         (void)hipFree(d->arena);
         delete d;
@@ -862,8 +959,8 @@ extern "C" int lz_state_alloc(LZRunState *s, const LZModel *mm, int seq_len, int
     s->nt_cap = 4;
     s->bytes_device = (long long)d->arena_size;
     s->logits = (float *)calloc((size_t)c.vocab_size, sizeof(float));
-    s->mtp_logits = (float *)calloc((size_t)(LZ_SPEC_K_MAX + 1) * c.vocab_size, sizeof(float));
-    s->mtp_verify_hidden = (float *)calloc((size_t)(LZ_SPEC_K_MAX + 1) * c.hidden_size, sizeof(float));
+    s->mtp_logits = (float *)calloc((size_t)(L98_SPEC_K_GPU + 1) * c.vocab_size, sizeof(float));
+    s->mtp_verify_hidden = (float *)calloc((size_t)(L98_SPEC_K_GPU + 1) * c.hidden_size, sizeof(float));
     s->mtp_chain = (float *)calloc((size_t)c.hidden_size, sizeof(float));
     s->mtp_draft_logits = (float *)calloc((size_t)c.vocab_size, sizeof(float));
     lz_state_reset(s, mm);
@@ -880,6 +977,8 @@ extern "C" void lz_state_free(LZRunState *s) {
         if (d->ctl_pinned) (void)hipHostFree(d->ctl_pinned);
         if (d->ev0) (void)hipEventDestroy(d->ev0);
         if (d->ev1) (void)hipEventDestroy(d->ev1);
+        for (hipEvent_t e : d->ph)
+            if (e) (void)hipEventDestroy(e);
         for (auto &g : d->round_graph)
             if (g) (void)hipGraphExecDestroy(g);
         if (d->st) (void)hipStreamDestroy(d->st);
@@ -923,27 +1022,51 @@ DevCtl ctl_from(LZRunState *s) {
 
 }  // namespace
 
-extern "C" float *lz_forward_capture(const LZModel *mm, LZRunState *s, int token, int pos) {
+namespace {
+// One token forward (src/forward.c:1623-1632 with capture, forward.h:1937
+// without): logits to s->logits; with capture the final-normed hidden also
+// becomes mtp_chain.
+float *forward_one(const LZModel *mm, LZRunState *s, int token, int pos, bool capture) {
     if (!mm || !s || !s->impl) return nullptr;
     DState *d = S(s);
     const LZModelConfig &c = d->m->c;
     if (token < 0 || token >= c.vocab_size || pos < 0 || pos >= d->seq_len) return nullptr;
+    if (!knobs_ok(c.num_experts_per_token, nullptr, 0)) return nullptr;
+    const timespec t0 = now_ts();
     DevCtl h = ctl_from(s);
     h.pos_scratch = pos;
     h.tok[0] = token;
     if (ctl_put(d, h)) return nullptr;
-    if (forward_chunk(d, d->ctl->tok, 1, &d->ctl->pos_scratch, 0, pos, d->chain, false, nullptr, false))
+    if (forward_chunk(d, d->ctl->tok, 1, &d->ctl->pos_scratch, 0, pos, capture ? d->chain : nullptr, false, nullptr,
+                      false))
         return nullptr;
     if (hipMemcpyAsync(s->logits, d->logits, sizeof(float) * c.vocab_size, hipMemcpyDeviceToHost, d->st) ||
-        hipMemcpyAsync(s->mtp_chain, d->chain, sizeof(float) * c.hidden_size, hipMemcpyDeviceToHost, d->st) ||
+        (capture &&
+         hipMemcpyAsync(s->mtp_chain, d->chain, sizeof(float) * c.hidden_size, hipMemcpyDeviceToHost, d->st)) ||
         hipStreamSynchronize(d->st))
         return nullptr;
+    lz_debug_n_chunks++;
+    lz_debug_n_lmhead++;
+    if (capture) {
+        lz_debug_us_capture += us_since(t0);
+        lz_debug_n_capture++;
+    }
     return s->logits;
+}
+}  // namespace
+
+extern "C" float *lz_forward_capture(const LZModel *mm, LZRunState *s, int token, int pos) {
+    return forward_one(mm, s, token, pos, true);
+}
+
+extern "C" float *lz_forward(const LZModel *mm, LZRunState *s, int token, int pos) {
+    return forward_one(mm, s, token, pos, false);
 }
 
 namespace {
 int batch_capture_dev(DState *d, LZRunState *s, const int *tokens, int n, int pos0) {
     const LZModelConfig &c = d->m->c;
+    if (!knobs_ok(c.num_experts_per_token, nullptr, 0)) return 1;
     DevCtl h = ctl_from(s);
     h.pos_scratch = pos0;
     CK(ctl_put(d, h));
@@ -953,6 +1076,7 @@ int batch_capture_dev(DState *d, LZRunState *s, const int *tokens, int n, int po
         CK(forward_chunk(d, d->tokbuf + done, k, &d->ctl->pos_scratch, done, pos0 + done + k - 1,
                          d->hcap + (size_t)done * c.hidden_size, false, nullptr, true));
         done += k;
+        lz_debug_n_chunks++;
     }
     return 0;
 }
@@ -976,6 +1100,8 @@ extern "C" int lz_forward_verify(const LZModel *mm, LZRunState *s, const int *to
     DState *d = S(s);
     const LZModelConfig &c = d->m->c;
     if (!tok_ok(c, tokens, n) || pos0 < 0 || pos0 + n > d->seq_len) return 1;
+    if (!knobs_ok(c.num_experts_per_token, nullptr, 0)) return 1;
+    const timespec t0 = now_ts();
     DevCtl h = ctl_from(s);
     h.pos_scratch = pos0;
     for (int i = 0; i < n; i++) h.tok[i] = tokens[i];
@@ -990,6 +1116,9 @@ extern "C" int lz_forward_verify(const LZModel *mm, LZRunState *s, const int *to
                        hipMemcpyDeviceToHost, d->st) ||
         hipStreamSynchronize(d->st))
         return 1;
+    lz_debug_n_chunks++;
+    lz_debug_n_lmhead++;
+    lz_debug_us_verify += us_since(t0);
     return 0;
 }
 
@@ -998,16 +1127,19 @@ extern "C" float *lz_mtp_draft_step(const LZModel *mm, LZRunState *s, int next_t
     DState *d = S(s);
     const LZModelConfig &c = d->m->c;
     if (next_token < 0 || next_token >= c.vocab_size || pos < 0 || pos >= d->seq_len) return nullptr;
+    if (!knobs_ok(c.num_experts_per_token, nullptr, 0)) return nullptr;
+    const timespec t0 = now_ts();
     DevCtl h = ctl_from(s);
     h.pos_scratch = pos;
     h.tok[0] = next_token;
-    if (ctl_put(d, h)) return nullptr;
+    if (ctl_put(d, h) || chain_put(d, s)) return nullptr;
     if (draft_step(d, d->ctl->tok, &d->ctl->pos_scratch, 0, pos, d->draft_logits, nullptr)) return nullptr;
     if (hipMemcpyAsync(s->mtp_draft_logits, d->draft_logits, sizeof(float) * c.vocab_size,
                        hipMemcpyDeviceToHost, d->st) ||
         hipMemcpyAsync(s->mtp_chain, d->chain, sizeof(float) * c.hidden_size, hipMemcpyDeviceToHost, d->st) ||
         hipStreamSynchronize(d->st))
         return nullptr;
+    lz_debug_us_draft += us_since(t0);
     return s->mtp_draft_logits;
 }
 
@@ -1030,7 +1162,11 @@ extern "C" int lz_mtp_prefill(const LZModel *mm, LZRunState *s, const float *h_b
 
 extern "C" int lz_mtp_catchup(const LZModel *m, LZRunState *s, const float *h_body_all,
                               const int *next_tokens, int n, int pos0) {
-    return lz_mtp_prefill(m, s, h_body_all, next_tokens, n, pos0);
+    const timespec t0 = now_ts();          // src/forward_mtp.c:635-642
+    int rc = lz_mtp_prefill(m, s, h_body_all, next_tokens, n, pos0);
+    lz_debug_us_catchup += us_since(t0);
+    lz_debug_n_catchup++;
+    return rc;
 }
 
 // ------------------------------------------------- sampling (host side) ---
@@ -1181,12 +1317,13 @@ namespace {
 // (always k-1 rows, see k_accept), then the round record and the advance to
 // the next round.  Reads nothing back; every scalar lives in ctl, so the
 // sequence is graph-capturable.
-int enqueue_verify_accept(DState *d, int k_eff, int max_pos, int brk, bool catchup) {
+int enqueue_verify_accept(DState *d, int k_eff, int max_pos, int brk, bool catchup, hipEvent_t mark = nullptr) {
     const LZModelConfig &c = d->m->c;
     CK(forward_chunk(d, d->ctl->tok, k_eff + 1, &d->ctl->anchor_pos, 1, max_pos, d->vhidden, true,
                      d->mtp_logits, false));
     CK(l98k_argmax(d->mtp_logits, c.vocab_size, k_eff + 1, 0, d->ctl->targ, d->amax_part, d->amax_cnt, d->st));
     CK(l98k_accept(d->ctl, d->vhidden, c.hidden_size, d->chain, d->depth, brk, d->st));
+    if (mark) CK(hipEventRecord(mark, d->st));
     if (catchup && k_eff > 1)
         CK(mtp_prefill_dev(d, d->vhidden, d->ctl->catch_tok, k_eff - 1, &d->ctl->catch_pos, 0));
     CK(l98k_set_tokens(d->ctl, 1, d->hist, d->hist_cap, d->st));
@@ -1222,6 +1359,7 @@ extern "C" int lz_spec_round(const LZModel *mm, LZRunState *s, int anchor, int a
     if (penalties_on(samp)) return errset(errbuf, errlen, LZ_ERR_NULL_ARG, "sampler penalties are not on this path");
     DState *d = S(s);
     const LZModelConfig &c = d->m->c;
+    if (!knobs_ok(c.num_experts_per_token, errbuf, errlen)) return -LZ_ERR_FORWARD;
     if (anchor < 0 || anchor >= c.vocab_size || anchor_pos + 1 + k >= d->seq_len ||
         s->mtp_pos + k > d->seq_len)
         return errset(errbuf, errlen, LZ_ERR_FORWARD, "forward failed (token/position out of range)");
@@ -1231,7 +1369,9 @@ extern "C" int lz_spec_round(const LZModel *mm, LZRunState *s, int anchor, int a
     h.anchor_pos = anchor_pos;
     h.tok[0] = anchor;
     h.k_eff = k;
-    if (ctl_put(d, h)) return -LZ_ERR_FORWARD;
+    if (ctl_put(d, h) || chain_put(d, s)) return -LZ_ERR_FORWARD;
+    // phase marks for the reference's draft / verify / catch-up timers
+    if (hipEventRecord(d->ph[0], d->st)) return -LZ_ERR_FORWARD;
     int k_eff = k;
     if (p_min > 0.0f || k_eff < n_min) {
         // The draft loop decides k_eff on the host: p_min needs each step's
@@ -1254,17 +1394,29 @@ extern "C" int lz_spec_round(const LZModel *mm, LZRunState *s, int anchor, int a
             k_eff = i + 1;
         }
         if (k_eff < n_min) {
-            if (hipStreamSynchronize(d->st)) return -LZ_ERR_FORWARD;
+            // discard: the draft steps ran and overwrote the chain, which
+            // the reference leaves in s->mtp_chain
+            if (hipMemcpyAsync(s->mtp_chain, d->chain, sizeof(float) * c.hidden_size, hipMemcpyDeviceToHost,
+                               d->st) ||
+                hipStreamSynchronize(d->st))
+                return -LZ_ERR_FORWARD;
             out[0] = anchor; *out_n_accept = 0; *out_new_pos = anchor_pos; *out_k_eff = k_eff;
             return 0;
         }
         int ke = k_eff;
-        if (hipMemcpyAsync(&d->ctl->k_eff, &ke, sizeof(int), hipMemcpyHostToDevice, d->st) ||
-            enqueue_verify_accept(d, k_eff, max_pos, brk, !skipc))
+        if (hipEventRecord(d->ph[1], d->st) ||
+            hipMemcpyAsync(&d->ctl->k_eff, &ke, sizeof(int), hipMemcpyHostToDevice, d->st) ||
+            enqueue_verify_accept(d, k_eff, max_pos, brk, !skipc, d->ph[2]))
             return -LZ_ERR_FORWARD;
     } else {
-        if (enqueue_greedy_round(d, k, max_pos, brk, !skipc)) return -LZ_ERR_FORWARD;
+        for (int i = 0; i < k; i++)
+            if (draft_step(d, d->ctl->tok + i, &d->ctl->mtp_pos, i, max_pos, d->draft_logits + (size_t)i * c.vocab_size,
+                           d->ctl->tok + 1 + i))
+                return -LZ_ERR_FORWARD;
+        if (hipEventRecord(d->ph[1], d->st) || enqueue_verify_accept(d, k, max_pos, brk, !skipc, d->ph[2]))
+            return -LZ_ERR_FORWARD;
     }
+    if (hipEventRecord(d->ph[3], d->st)) return -LZ_ERR_FORWARD;
     // chain mirror (the reseeded mtp_chain) rides on the same sync as ctl
     if (hipMemcpyAsync(s->mtp_chain, d->chain, sizeof(float) * c.hidden_size, hipMemcpyDeviceToHost, d->st))
         return -LZ_ERR_FORWARD;
@@ -1276,6 +1428,21 @@ extern "C" int lz_spec_round(const LZModel *mm, LZRunState *s, int anchor, int a
     *out_new_pos = anchor_pos + 1 + n_accept;
     *out_k_eff = k_eff;
     s->mtp_pos += n_accept;
+    // the reference's counters (src/generate.c:826, src/forward_mtp.c:639-640,
+    // src/forward.c:86-88): device time between the phase marks
+    {
+        float ms[3] = {0, 0, 0};
+        for (int i = 0; i < 3; i++) (void)hipEventElapsedTime(&ms[i], d->ph[i], d->ph[i + 1]);
+        lz_debug_us_draft += (long long)(ms[0] * 1000.0f);
+        lz_debug_us_verify += (long long)(ms[1] * 1000.0f);
+        lz_debug_n_chunks++;
+        lz_debug_n_lmhead++;
+        if (n_accept < k_eff) lz_debug_n_ring_rollback++;
+        if (n_accept > 1 && !skipc) {
+            lz_debug_us_catchup += (long long)(ms[2] * 1000.0f);
+            lz_debug_n_catchup++;
+        }
+    }
     return n_accept + 1;
 }
 
@@ -1292,7 +1459,7 @@ bool smp_ensure(DState *d) {
     if (l98k_smp_sort_desc(nullptr, nullptr, nullptr, nullptr, (int)V, nullptr, &tmp, d->st)) return false;
     size_t off = 0;
     auto take = [&](size_t bytes) { size_t a = off; off = (off + bytes + 255) & ~(size_t)255; return a; };
-    const size_t oq = take(sizeof(float) * V * LZ_SPEC_K_MAX), op = take(sizeof(float) * V),
+    const size_t oq = take(sizeof(float) * V * L98_SPEC_K_GPU), op = take(sizeof(float) * V),
                  opr = take(sizeof(float) * V), ok = take(4 * V), osk = take(4 * V), ov = take(4 * V),
                  osv = take(4 * V), ot = take(tmp), orng = take(8), oo = take(64), oof = take(64);
     char *a = nullptr;
@@ -1355,15 +1522,17 @@ int dev_sample_ex(DState *d, const float *row, int V, float temp, float topp, lz
 
 }  // namespace
 
-extern "C" int lz_spec_round_temp(const LZModel *mm, LZRunState *s, int anchor, int anchor_pos, int k,
-                                  float p_min, int n_min, LZSampler *samp, int brk, int skipc,
-                                  int *out, int *out_n_accept, int *out_new_pos, int *out_k_eff,
-                                  char *errbuf, int errlen) {
+namespace {
+// lz_spec_round_temp with the draft width bounded by k_cap: LZ_SPEC_K_MAX
+// for the reference entry point, L98_SPEC_K_GPU for this library's own
+// generation loop.
+int spec_round_temp(const LZModel *mm, LZRunState *s, int anchor, int anchor_pos, int k, float p_min, int n_min,
+                    LZSampler *samp, int brk, int skipc, int *out, int *out_n_accept, int *out_new_pos,
+                    int *out_k_eff, char *errbuf, int errlen, int k_cap) {
     if (!mm || !s || !samp || !out || !out_n_accept || !out_new_pos || !out_k_eff || !s->impl)
         return errset(errbuf, errlen, LZ_ERR_NULL_ARG, "null argument");
-    if (k < 1 || k > LZ_SPEC_K_MAX || k > s->ssm_ring_depth - 1) {
-        set_err(errbuf, errlen, "spec_k %d out of range 1..%d", k,
-                k > LZ_SPEC_K_MAX ? LZ_SPEC_K_MAX : s->ssm_ring_depth - 1);
+    if (k < 1 || k > k_cap || k > s->ssm_ring_depth - 1) {
+        set_err(errbuf, errlen, "spec_k %d out of range 1..%d", k, k > k_cap ? k_cap : s->ssm_ring_depth - 1);
         return -LZ_ERR_SPEC_K_RANGE;
     }
     if (unsupported_sampler(samp))
@@ -1371,16 +1540,18 @@ extern "C" int lz_spec_round_temp(const LZModel *mm, LZRunState *s, int anchor, 
     DState *d = S(s);
     const LZModelConfig &c = d->m->c;
     const int V = c.vocab_size;
+    if (!knobs_ok(c.num_experts_per_token, errbuf, errlen)) return -LZ_ERR_FORWARD;
+    timespec t0 = now_ts();
     if (anchor < 0 || anchor >= V || anchor_pos + 1 + k >= d->seq_len || s->mtp_pos + k > d->seq_len)
         return errset(errbuf, errlen, LZ_ERR_FORWARD, "forward failed (token/position out of range)");
     const float temp = samp->p.temperature, topp = samp->p.topp;
     DevCtl h = ctl_from(s);
     h.anchor = anchor; h.anchor_pos = anchor_pos; h.tok[0] = anchor;
-    if (ctl_put(d, h)) return -LZ_ERR_FORWARD;
+    if (ctl_put(d, h) || chain_put(d, s)) return -LZ_ERR_FORWARD;
     if (!smp_ensure(d) ||
         hipMemcpyAsync(d->smp_rng, &samp->rng_state, sizeof(lz_u64), hipMemcpyHostToDevice, d->st))
         return -LZ_ERR_FORWARD;
-    int draft[LZ_SPEC_K_MAX], k_eff = 0;
+    int draft[L98_SPEC_K_GPU], k_eff = 0;
     const float inv = 1.0f / temp;
     for (int i = 0; i < k; i++) {
         if (draft_step(d, d->ctl->tok + i, &d->ctl->mtp_pos, i, s->mtp_pos + k, d->draft_logits, nullptr))
@@ -1403,13 +1574,20 @@ extern "C" int lz_spec_round_temp(const LZModel *mm, LZRunState *s, int anchor, 
         k_eff = i + 1;
     }
     if (k_eff < n_min) {
+        if (hipMemcpyAsync(s->mtp_chain, d->chain, sizeof(float) * c.hidden_size, hipMemcpyDeviceToHost, d->st) ||
+            hipStreamSynchronize(d->st))
+            return -LZ_ERR_FORWARD;
         out[0] = anchor; *out_n_accept = 0; *out_new_pos = anchor_pos; *out_k_eff = k_eff;
         return 0;
     }
+    lz_debug_us_draft += us_since(t0);
+    t0 = now_ts();
     int base = s->ssm_slot;
     if (forward_chunk(d, d->ctl->tok, k_eff + 1, &d->ctl->anchor_pos, 1, anchor_pos + k_eff + 1,
                       d->vhidden, true, d->mtp_logits, false))
         return -LZ_ERR_FORWARD;
+    lz_debug_n_chunks++;
+    lz_debug_n_lmhead++;
     // acceptance on the device (lz_spec_accept_temp, src/generate.c:283-346):
     // the target distribution of each verify row, then u, then the residual
     // draw on a rejection; the bonus draw when every draft is accepted
@@ -1432,7 +1610,9 @@ extern "C" int lz_spec_round_temp(const LZModel *mm, LZRunState *s, int anchor, 
     if (hipMemcpyAsync(&samp->rng_state, d->smp_rng, sizeof(lz_u64), hipMemcpyDeviceToHost, d->st) ||
         hipStreamSynchronize(d->st))
         return -LZ_ERR_FORWARD;
+    lz_debug_us_verify += us_since(t0);
     s->ssm_slot = (base + k_eff + 1) % d->depth;
+    if (n_accept < k_eff) lz_debug_n_ring_rollback++;
     if (n_accept < k_eff && !brk) s->ssm_slot = (base + n_accept + 1) % d->depth;
     // reseed the chain from the accepted row; catch-up
     if (hipMemcpyAsync(d->chain, d->vhidden + (size_t)n_accept * c.hidden_size, sizeof(float) * c.hidden_size,
@@ -1442,18 +1622,31 @@ extern "C" int lz_spec_round_temp(const LZModel *mm, LZRunState *s, int anchor, 
     *out_new_pos = anchor_pos + 1 + n_accept;
     *out_k_eff = k_eff;
     if (n_accept > 1 && !skipc) {
+        t0 = now_ts();
         DevCtl h2 = h;
         h2.pos_scratch = s->mtp_pos + 1;
         for (int i = 0; i <= n_accept; i++) h2.out[i] = out[i];
         if (ctl_put(d, h2) ||
-            mtp_prefill_dev(d, d->vhidden, d->ctl->out, n_accept - 1, &d->ctl->pos_scratch, 0))
+            mtp_prefill_dev(d, d->vhidden, d->ctl->out, n_accept - 1, &d->ctl->pos_scratch, 0) ||
+            hipStreamSynchronize(d->st))
             return -LZ_ERR_FORWARD;
+        lz_debug_us_catchup += us_since(t0);
+        lz_debug_n_catchup++;
     }
     if (hipMemcpyAsync(s->mtp_chain, d->chain, sizeof(float) * c.hidden_size, hipMemcpyDeviceToHost, d->st) ||
         hipStreamSynchronize(d->st))
         return -LZ_ERR_FORWARD;
     s->mtp_pos += n_accept;
     return n_accept + 1;
+}
+}  // namespace
+
+extern "C" int lz_spec_round_temp(const LZModel *mm, LZRunState *s, int anchor, int anchor_pos, int k,
+                                  float p_min, int n_min, LZSampler *samp, int brk, int skipc,
+                                  int *out, int *out_n_accept, int *out_new_pos, int *out_k_eff,
+                                  char *errbuf, int errlen) {
+    return spec_round_temp(mm, s, anchor, anchor_pos, k, p_min, n_min, samp, brk, skipc, out, out_n_accept,
+                           out_new_pos, out_k_eff, errbuf, errlen, LZ_SPEC_K_MAX);
 }
 
 // --------------------------------------------------------- generation ---
@@ -1544,6 +1737,19 @@ extern "C" int l98_moe_route(const float *logits, const float *bias, int nt, int
     return rc;
 }
 
+extern "C" int l98_argmax_rows(const float *x, int rows, int n, int mode, int *out) {
+    if (!x || !out || rows < 1 || rows > MAX_CHUNK || n < 1 || (mode != 0 && mode != 1)) return 1;
+    DevBuf dx, dpart, dcnt, dout;
+    if (!dx.get(x, sizeof(float) * (size_t)rows * n) || !dpart.get(nullptr, sizeof(unsigned long long) * rows * 64) ||
+        !dcnt.get(nullptr, sizeof(unsigned) * rows) || !dout.get(nullptr, sizeof(int) * rows))
+        return 1;
+    if (hipMemset(dcnt.p, 0, sizeof(unsigned) * rows) != hipSuccess) return 1;
+    if (l98k_argmax((const float *)dx.p, n, rows, mode, (int *)dout.p, (unsigned long long *)dpart.p,
+                    (unsigned *)dcnt.p, nullptr))
+        return 1;
+    return dout.put(out, sizeof(int) * rows) ? 0 : 1;
+}
+
 extern "C" int l98_prefix_query(const float *x, int rows, int n, int mode, const float *c, int *out, float *outv) {
     if (!x || !out || !outv || rows < 1 || n < 1 || mode < 0 || mode > 2 || (mode && !c)) return 1;
     float *dx = nullptr, *dc = nullptr, *dv = nullptr;
@@ -1628,7 +1834,7 @@ extern "C" int l98_greedy_rounds_ex(const LZModel *mm, LZRunState *s, int k, int
                                     int *tokens, int cap, int *n_accept_out, int *experts_out,
                                     int *new_pos_out, float *device_ms) {
     if (!mm || !s || !s->impl || n_rounds < 1) return -LZ_ERR_NULL_ARG;
-    if (k < 1 || k > LZ_SPEC_K_MAX || k > s->ssm_ring_depth - 1) return -LZ_ERR_SPEC_K_RANGE;
+    if (k < 1 || k > L98_SPEC_K_GPU || k > s->ssm_ring_depth - 1) return -LZ_ERR_SPEC_K_RANGE;
     DState *d = S(s);
     if (n_rounds > d->hist_cap) return -LZ_ERR_NULL_ARG;
     const int max_pos = d->seq_len - 1;
@@ -1672,6 +1878,10 @@ extern "C" int l98_greedy_rounds_ex(const LZModel *mm, LZRunState *s, int k, int
         return -LZ_ERR_FORWARD;
     int n = 0;
     for (int r = 0; r < n_rounds; r++) {
+        if (rec[r].n_accept < rec[r].k_eff) lz_debug_n_ring_rollback++;
+        if (rec[r].n_accept > 1) lz_debug_n_catchup++;
+        lz_debug_n_chunks++;
+        lz_debug_n_lmhead++;
         if (n_accept_out) n_accept_out[r] = rec[r].n_accept;
         if (experts_out) experts_out[r] = rec[r].experts;
         if (new_pos_out) new_pos_out[r] = rec[r].new_pos;
@@ -1756,7 +1966,7 @@ extern "C" int l98_greedy_rounds_batch(const LZModel *mm, LZRunState **states, i
     for (int i = 0; i < n_seq; i++) {
         LZRunState *s = states[i];
         DState *d = S(s);
-        if (k < 1 || k > LZ_SPEC_K_MAX || k > s->ssm_ring_depth - 1) return -LZ_ERR_SPEC_K_RANGE;
+        if (k < 1 || k > L98_SPEC_K_GPU || k > s->ssm_ring_depth - 1) return -LZ_ERR_SPEC_K_RANGE;
         if (n_rounds > d->hist_cap) return -LZ_ERR_NULL_ARG;
         DevCtl h;
         if (ctl_get(d, &h)) return -LZ_ERR_FORWARD;
@@ -1817,7 +2027,7 @@ extern "C" int l98_generate(const LZModel *mm, LZRunState *s, const int *prompt,
                             int n_new, LZSampler *samp, int *tokens, int cap, int *k_eff_out,
                             int *n_accept_out, int *n_rounds) {
     if (!mm || !s || !s->impl || !prompt || n_prompt < 2 || !tokens) return -LZ_ERR_NULL_ARG;
-    if (k < 1 || k > LZ_SPEC_K_MAX || k > s->ssm_ring_depth - 1) return -LZ_ERR_SPEC_K_RANGE;
+    if (k < 1 || k > L98_SPEC_K_GPU || k > s->ssm_ring_depth - 1) return -LZ_ERR_SPEC_K_RANGE;
     DState *d = S(s);
     if (n_prompt + n_new + 2 * (k + 1) >= d->seq_len) return -LZ_ERR_FORWARD;
     int anchor = l98_session_start(mm, s, prompt, n_prompt, samp);
@@ -1829,9 +2039,9 @@ extern "C" int l98_generate(const LZModel *mm, LZRunState *s, const int *prompt,
         LZSampler &local = d->session_samp;
         int anchor_pos = n_prompt - 1;
         while (n < n_new) {
-            int out[LZ_SPEC_K_MAX + 1], na = 0, np = 0, ke = 0;
-            int r = lz_spec_round_temp(mm, s, anchor, anchor_pos, k, 0.0f, 0, &local, 0, 0, out, &na, &np, &ke,
-                                       nullptr, 0);
+            int out[L98_SPEC_K_GPU + 1], na = 0, np = 0, ke = 0;
+            int r = spec_round_temp(mm, s, anchor, anchor_pos, k, 0.0f, 0, &local, 0, 0, out, &na, &np, &ke,
+                                    nullptr, 0, L98_SPEC_K_GPU);
             if (r <= 0) return r < 0 ? r : -LZ_ERR_FORWARD;
             if (k_eff_out) k_eff_out[rounds] = ke;
             if (n_accept_out) n_accept_out[rounds] = na;
@@ -1844,12 +2054,16 @@ extern "C" int l98_generate(const LZModel *mm, LZRunState *s, const int *prompt,
         if (samp) samp->rng_state = local.rng_state;
         return n;
     }
-    // Greedy: every round emits at least one token, so at most n_new - 1
-    // more rounds; run them in device batches and stop at n_new.
+    // Greedy: a round emits 1..k+1 tokens and the loop stops at the first
+    // round that reaches n_new, as the reference's does.  A device batch of
+    // want / (k+1) rounds cannot pass n_new, so batches never run a round
+    // the reference would not (the state after the call is the reference's).
     std::vector<int> na(n_new + 8);
     while (n < n_new) {
         int want = n_new - n;
-        int batch = want < 64 ? want : 64;
+        int batch = want / (k + 1);
+        if (batch < 1) batch = 1;
+        if (batch > 64) batch = 64;
         {
             DevCtl h;
             if (ctl_get(d, &h)) return -LZ_ERR_FORWARD;

@@ -168,7 +168,14 @@ __global__ __launch_bounds__(256) void k_argmax(const float *__restrict__ x, int
         if (threadIdx.x == 0) {
             unsigned long long bb = 0;
             for (int i = 0; i < (int)(blockDim.x >> 6); i++) bb = sb[i] > bb ? sb[i] : bb;
-            out[row] = (int)(0xFFFFFFFFu - (uint32_t)(bb & 0xFFFFFFFFu));
+            int idx = (int)(0xFFFFFFFFu - (uint32_t)(bb & 0xFFFFFFFFu));
+            // lz_argmax_p1 starts from element 0 and takes only v > best:
+            // a NaN there is never beaten, so the row's answer is 0.
+            if (mode == 1) {
+                const float r0 = r[0];
+                if (r0 != r0) idx = 0;
+            }
+            out[row] = idx;
             counter[row] = 0;
         }
     }

@@ -17,20 +17,14 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_expert_gemv(ExpertJob j0, Expe
     const int tile = blockIdx.x, gi = blockIdx.y, jb = blockIdx.z;   // grid (tiles, max_groups, jobs)
     (void)max_groups;
     const ExpertJob J = jb == 0 ? j0 : j1;
-    asm volatile("" ::"s"(in_dim), "s"(out_rows), "s"(R));
     // the group's table entries in one batch, before the group count is
     // known (gi < max_groups <= MAX_PAIRS keeps every read inside the table;
     // a block past the count returns before it uses them), so the weights
     // and activations wait on one round trip instead of three
-    int ng = grp->n_groups, e = grp->expert[gi], nm = grp->n_members[gi];
+    const int ng = grp->n_groups, e = grp->expert[gi], nm = grp->n_members[gi];
     int memv[M];
 #pragma unroll
     for (int t = 0; t < M; t++) memv[t] = grp->member[gi][t];
-    // the job's fields the tile uses join the same wait
-    asm volatile("" : "+s"(ng), "+s"(e), "+s"(nm) : "s"(J.q), "s"(J.s), "s"(J.out), "s"(J.pro.src), "s"(J.pro.src2),
-                 "s"(J.pro.src_stride), "s"(J.xq_by_pair));
-#pragma unroll
-    for (int t = 0; t < M; t++) asm volatile("" : "+s"(memv[t]));
     if (gi >= ng) return;
     int xrow[M];
 #pragma unroll
@@ -299,7 +293,6 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_up(ExpertJob j0, ExpertJob
     (void)max_groups;
     // the projection's arguments read now, so their loads overlap the routing
     const ExpertJob J = jb == 0 ? j0 : j1;
-    asm volatile("" ::"s"(J.q), "s"(J.s), "s"(J.out), "s"(J.pro.src), "s"(J.pro.src_stride), "s"(J.xq_by_pair));
     const RouteSet rs = route_block(logits, bias, E, topk, nt, rt, tab);
     const int ng = rs.ng;
     if ((blockIdx.x | blockIdx.y | blockIdx.z) == 0) {   // publish the routing

@@ -15,6 +15,9 @@
 enum { FMT_F32 = 0, FMT_Q8_0 = 1 };
 enum { LT_FULL = 1, LT_KDA = 2 };
 #define MAX_LAYERS 128
+/* The echo variant (config 11): vocabulary and residual-writer std. */
+#define ECHO_VOCAB 64
+#define ECHO_RESID_STD 0.085f
 
 /* ---------------------------------------------------------------- RNG --- */
 
@@ -126,12 +129,18 @@ int l98_synth_config(int id, L98SynthConfig *c) {
         c->n_experts = 128; c->topk = 8; c->latent = 512; c->moe_inter = 768;
         c->shared_w = 768; c->mtp_inter = 768;
         return 0;
-    case 10:
+    case 10: case 11:
         c->vocab = 512; c->hidden = 64; c->n_layers = 4; c->seq_len = 160;
         c->n_heads = 2; c->n_kv_heads = 1; c->head_dim = 32;
         c->kda_heads = 2; c->kd = 32; c->vd = 32; c->gate_rank = 32;
         c->n_experts = 8; c->topk = 2; c->latent = 32; c->moe_inter = 64;
         c->shared_w = 64; c->mtp_inter = 64;
+        if (id == 11) {
+            c->vocab = ECHO_VOCAB;
+            c->seq_len = 256;
+            c->resid_std = ECHO_RESID_STD;
+            c->mtp_echo = 1;
+        }
         return 0;
     default:
         return 1;
@@ -155,7 +164,7 @@ static void put_u32(Writer *w, uint32_t v) { put_bytes(w, &v, 4); }
 static void put_i32(Writer *w, int32_t v) { put_bytes(w, &v, 4); }
 static void put_f32(Writer *w, float v) { put_bytes(w, &v, 4); }
 
-typedef enum { INIT_NORMAL, INIT_UNIFORM, INIT_CONST, INIT_ALOG, INIT_DTBIAS } InitKind;
+typedef enum { INIT_NORMAL, INIT_UNIFORM, INIT_CONST, INIT_ALOG, INIT_DTBIAS, INIT_EYE } InitKind;
 
 typedef struct {
     uint64_t seed;
@@ -177,8 +186,11 @@ static uint64_t row_stream(uint64_t seed, uint32_t tensor_id, int row) {
     return s;
 }
 
-static float init_value(const Job *j, uint64_t *st) {
+static float init_value(const Job *j, uint64_t *st, int r, int c) {
     switch (j->kind) {
+    case INIT_EYE:              /* left square block I, right block N(0, a) */
+        if (c >= j->rows) return (float)((double)j->a * l98_synth_normal(st));
+        return r == c ? 1.0f : 0.0f;
     case INIT_NORMAL:
         return (float)((double)j->b + (double)j->a * l98_synth_normal(st));
     case INIT_UNIFORM:
@@ -201,7 +213,7 @@ static void *job_run(void *arg) {
     if (!row) return NULL;
     for (int r = j->r0; r < j->r1; r++) {
         uint64_t st = row_stream(j->seed, j->tensor_id, r);
-        for (int c = 0; c < j->cols; c++) row[c] = init_value(j, &st);
+        for (int c = 0; c < j->cols; c++) row[c] = init_value(j, &st, r, c);
         if (!j->quantize) {
             memcpy(j->f + (size_t)r * j->cols, row, sizeof(float) * (size_t)j->cols);
             continue;
@@ -279,6 +291,10 @@ static void emit_tensor(Writer *w, int rows, int cols, InitKind kind, float a,
 
 static void matrix(Writer *w, int rows, int cols, float std) {
     emit_tensor(w, rows, cols, INIT_NORMAL, std, 0.0f, 1);
+}
+/* An all-zero int8 matrix (every row scale 1, every code 0). */
+static void zero_matrix(Writer *w, int rows, int cols) {
+    emit_tensor(w, rows, cols, INIT_CONST, 0.0f, 0.0f, 1);
 }
 static void vec_norm(Writer *w, int n, float mean, float std) {
     emit_tensor(w, 1, n, INIT_NORMAL, std, mean, 0);
@@ -361,6 +377,7 @@ int l98_synth_write(const char *dir, const L98SynthConfig *c, uint64_t seed,
 
     const float ws = c->w_std;
     const float rs = c->router_std > 0.0f ? c->router_std : ws;
+    const float os = c->resid_std > 0.0f ? c->resid_std : ws;   /* residual writers */
     /* Tensors in model_walk order (src/model.c:2240-2625). */
     matrix(&w, c->vocab, d, ws);                       /* embed_tokens (tied lm_head) */
     vec_norm(&w, d, 0.0f, ws);                         /* norm */
@@ -371,7 +388,7 @@ int l98_synth_write(const char *dir, const L98SynthConfig *c, uint64_t seed,
             matrix(&w, qgate, d, ws);                  /* q_proj ([q|gate] per head) */
             matrix(&w, kv_dim, d, ws);                 /* k_proj */
             matrix(&w, kv_dim, d, ws);                 /* v_proj */
-            matrix(&w, d, q_dim, ws);                  /* o_proj */
+            matrix(&w, d, q_dim, os);                  /* o_proj */
             vec_norm(&w, hd, 0.0f, ws);                /* q_norm */
             vec_norm(&w, hd, 0.0f, ws);                /* k_norm */
         } else {
@@ -388,34 +405,42 @@ int l98_synth_write(const char *dir, const L98SynthConfig *c, uint64_t seed,
             matrix(&w, c->kda_heads, d, ws);           /* b_proj */
             matrix(&w, value, d, ws);                  /* g_proj */
             vec_norm(&w, c->vd, 1.0f, ws);             /* o_norm (gain w, not 1+w) */
-            matrix(&w, d, value, ws);                  /* o_proj */
+            matrix(&w, d, value, os);                  /* o_proj */
         }
         matrix(&w, c->n_experts, d, rs);               /* mlp.gate (router) */
         emit_tensor(&w, 1, c->n_experts, INIT_NORMAL, c->bias_std, 0.0f, 0);
         matrix(&w, c->latent, d, ws);                  /* routed_expert_down_proj */
-        matrix(&w, d, c->latent, ws);                  /* routed_expert_up_proj */
+        matrix(&w, d, c->latent, os);                  /* routed_expert_up_proj */
         matrix(&w, c->shared_w, d, ws);                /* shared gate_proj */
         matrix(&w, c->shared_w, d, ws);                /* shared up_proj */
-        matrix(&w, d, c->shared_w, ws);                /* shared down_proj */
+        matrix(&w, d, c->shared_w, os);                /* shared down_proj */
         for (int e = 0; e < c->n_experts; e++) {
             matrix(&w, c->moe_inter, c->latent, ws);   /* w1 */
             matrix(&w, c->latent, c->moe_inter, ws);   /* w2 */
             matrix(&w, c->moe_inter, c->latent, ws);   /* w3 */
         }
     }
-    /* MTP block: full-attention rows, dense FFN, then the head's own. */
+    /* MTP block: full-attention rows, dense FFN, then the head's own.  The
+     * echo head keeps the block's K/V rows (the MTP KV plane still fills)
+     * but zeroes what it adds to its residual, and its fc passes the
+     * normalized embedding half through (the hidden half adds a little
+     * noise, so the chain moves a step's top-1 probability), so its logits
+     * are about E . norm(E[tok]) and the draft is the input token. */
     vec_norm(&w, d, 0.0f, ws);
     vec_norm(&w, d, 0.0f, ws);
     matrix(&w, qgate, d, ws);
     matrix(&w, kv_dim, d, ws);
     matrix(&w, kv_dim, d, ws);
-    matrix(&w, d, q_dim, ws);
+    if (c->mtp_echo) zero_matrix(&w, d, q_dim);
+    else matrix(&w, d, q_dim, ws);
     vec_norm(&w, hd, 0.0f, ws);
     vec_norm(&w, hd, 0.0f, ws);
     matrix(&w, c->mtp_inter, d, ws);                   /* gate_proj */
     matrix(&w, c->mtp_inter, d, ws);                   /* up_proj */
-    matrix(&w, d, c->mtp_inter, ws);                   /* down_proj */
-    matrix(&w, d, 2 * d, ws);                          /* mtp.fc */
+    if (c->mtp_echo) zero_matrix(&w, d, c->mtp_inter); /* down_proj */
+    else matrix(&w, d, c->mtp_inter, ws);
+    if (c->mtp_echo) emit_tensor(&w, d, 2 * d, INIT_EYE, ws, 0.0f, 1);     /* mtp.fc = [I | N(0, ws)] */
+    else matrix(&w, d, 2 * d, ws);                     /* mtp.fc */
     vec_norm(&w, d, 0.0f, ws);                         /* mtp.norm */
     vec_norm(&w, d, 0.0f, ws);                         /* pre_fc_norm_hidden */
     vec_norm(&w, d, 0.0f, ws);                         /* pre_fc_norm_embedding */

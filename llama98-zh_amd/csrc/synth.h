@@ -30,6 +30,12 @@ typedef struct {
     float w_std;                /* N(0, w_std) for every matrix except the router */
     float router_std;           /* router weight std (0: use w_std) */
     float bias_std;             /* router selection bias std */
+    float resid_std;            /* std of the matrices that write the residual stream
+                                   (attention / KDA o_proj, routed up_proj, shared
+                                   down_proj); 0: use w_std */
+    int mtp_echo;               /* 1: MTP fc = [I | N(0, w_std)], MTP o_proj and
+                                   down_proj zero, so the head drafts its own input
+                                   token */
 } L98SynthConfig;
 
 /* Named configurations:
@@ -39,6 +45,9 @@ typedef struct {
  *   3  large   d=2048, 32 layers (3:1), 16 KDA heads x128, E=128 top-8, V=131072
  *   4  server  config 0's shapes, router N(0,1/d), bias N(0,0.5)
  *  10  micro   d=64 toy for fast unit tests
+ *  11  echo    micro's shapes with a small vocabulary, an echoing MTP head and
+ *              damped residual writers: greedy drafts are accepted at every
+ *              depth, so the accepted-draft path of a round runs
  * Returns 0 on success, 1 for an unknown id. */
 int l98_synth_config(int id, L98SynthConfig *out);
 

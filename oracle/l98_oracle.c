@@ -663,6 +663,10 @@ ORA_API const float *ora_rope_table(void *h) { return ((OModel *)h)->rope_cs; }
 
 #define MAXB 8                                   /* LZ_BATCH_MAX, src/ops.h:1457 */
 #define SPEC_K_MAX 6                             /* src/ops.h:2098 */
+/* The GPU library's own loops also run k = 7 (a verify of 8 rows), which the
+ * reference's cap refuses; the rounds below take k up to SPEC_K_EXT with the
+ * same algorithm and an 8-slot ring, so that width has a CPU checker too. */
+#define SPEC_K_EXT 7
 
 typedef struct {
     OModel *m;
@@ -725,7 +729,7 @@ ORA_API void *ora_state_new(void *hm, int seq_len, int spec_k_max) {
     if (!s) return NULL;
     s->m = m;
     s->seq_len = seq_len > 0 ? seq_len : m->seq_len;
-    s->depth = spec_k_max > 0 ? (spec_k_max + 1 > SPEC_K_MAX + 1 ? SPEC_K_MAX + 1 : spec_k_max + 1) : 1;
+    s->depth = spec_k_max > 0 ? (spec_k_max > SPEC_K_EXT ? SPEC_K_EXT : spec_k_max) + 1 : 1;
     s->nt_cap = 4;
     s->planes = m->n_full + 1;
     {
@@ -754,11 +758,11 @@ ORA_API void *ora_state_new(void *hm, int seq_len, int spec_k_max) {
     s->xq = (int8_t *)calloc((size_t)MAXB * wide, 1);
     s->xqs = (float *)calloc((size_t)MAXB * wide / 32 + 8, sizeof(float));
     s->logits = (float *)calloc((size_t)m->vocab, sizeof(float));
-    s->mtp_logits = (float *)calloc((size_t)(SPEC_K_MAX + 2) * m->vocab, sizeof(float));
-    s->mtp_hidden = (float *)calloc((size_t)(SPEC_K_MAX + 2) * m->d, sizeof(float));
+    s->mtp_logits = (float *)calloc((size_t)(SPEC_K_EXT + 1) * m->vocab, sizeof(float));
+    s->mtp_hidden = (float *)calloc((size_t)(SPEC_K_EXT + 1) * m->d, sizeof(float));
     s->mtp_chain = (float *)calloc((size_t)m->d, sizeof(float));
     s->mtp_draft = (float *)calloc((size_t)m->vocab, sizeof(float));
-    s->mtp_draft_q = (float *)calloc((size_t)SPEC_K_MAX * m->vocab, sizeof(float));
+    s->mtp_draft_q = (float *)calloc((size_t)SPEC_K_EXT * m->vocab, sizeof(float));
     s->target_p = (float *)calloc((size_t)m->vocab, sizeof(float));
     s->t0 = (float *)calloc((size_t)MAXB * wide * 4, sizeof(float));
     s->t1 = (float *)calloc((size_t)MAXB * wide * 4, sizeof(float));
@@ -1474,9 +1478,9 @@ ORA_API int ora_spec_round(void *hs, int anchor, int anchor_pos, int k, float p_
                            int *out_k_eff) {
     OState *s = (OState *)hs;
     const OModel *m = s->m;
-    int draft[SPEC_K_MAX], vt[SPEC_K_MAX + 1], targ[SPEC_K_MAX];
+    int draft[SPEC_K_EXT], vt[SPEC_K_EXT + 1], targ[SPEC_K_EXT];
     int k_eff = 0, n_accept, bonus, base;
-    if (k < 1 || k > SPEC_K_MAX || k > s->depth - 1) return -1;
+    if (k < 1 || k > SPEC_K_EXT || k > s->depth - 1) return -1;
     for (int i = 0; i < k; i++) {
         int in_tok = i == 0 ? anchor : draft[i - 1];
         float p1;
@@ -1518,9 +1522,9 @@ ORA_API int ora_spec_round_temp(void *hs, int anchor, int anchor_pos, int k, flo
     OState *s = (OState *)hs;
     const OModel *m = s->m;
     const int V = m->vocab;
-    int draft[SPEC_K_MAX], vt[SPEC_K_MAX + 1];
+    int draft[SPEC_K_EXT], vt[SPEC_K_EXT + 1];
     int k_eff = 0, n_accept, base;
-    if (k < 1 || k > SPEC_K_MAX || k > s->depth - 1) return -1;
+    if (k < 1 || k > SPEC_K_EXT || k > s->depth - 1) return -1;
     for (int i = 0; i < k; i++) {
         int in_tok = i == 0 ? anchor : draft[i - 1];
         float *lg = ora_mtp_draft_step(s, in_tok, s->mtp_pos + i);
@@ -1585,11 +1589,13 @@ ORA_API int ora_session_start(void *hs, const int *prompt, int n_prompt) {
 
 /* The generation loop of lz_generate_spec_round (src/generate.c:1822-2106)
  * with penalties off: tokens[] receives the emitted ids (the whole last
- * round, so up to n_new + k).  Returns the number written or < 0. */
-ORA_API int ora_generate(void *hs, const int *prompt, int n_prompt, int k, int n_new,
-                         float temp, float topp, uint64_t seed, int brk, int skipc,
-                         int *tokens, int cap, int *k_eff_out, int *n_acc_out, int *n_rounds,
-                         uint64_t *rng_out) {
+ * round, so up to n_new + k).  p_min / n_min go to every round as the
+ * reference harness (oracle/ref_harness.c) passes them; a discarded round
+ * records n_accept -1.  Returns the number written or < 0. */
+ORA_API int ora_generate_ex(void *hs, const int *prompt, int n_prompt, int k, int n_new,
+                            float temp, float topp, uint64_t seed, int brk, int skipc, float p_min,
+                            int n_min, int *tokens, int cap, int *k_eff_out, int *n_acc_out,
+                            int *n_rounds, uint64_t *rng_out) {
     OState *s = (OState *)hs;
     const OModel *m = s->m;
     uint64_t rng = seed ? seed : 1;
@@ -1598,7 +1604,7 @@ ORA_API int ora_generate(void *hs, const int *prompt, int n_prompt, int k, int n
     token = prompt[n_prompt - 1];
     pos = n_prompt - 1;
     while (n < n_new) {
-        int anchor, anchor_pos, out[SPEC_K_MAX + 1], n_accept = 0, new_pos = 0, k_eff = 0, ne;
+        int anchor, anchor_pos, out[SPEC_K_EXT + 1], n_accept = 0, new_pos = 0, k_eff = 0, ne;
         if (have_seed) {
             anchor = token;
             anchor_pos = pos - 1;
@@ -1613,10 +1619,10 @@ ORA_API int ora_generate(void *hs, const int *prompt, int n_prompt, int k, int n
             if (n >= n_new) break;
         }
         if (temp > 0.0f)
-            ne = ora_spec_round_temp(s, anchor, anchor_pos, k, 0.0f, 0, temp, topp, &rng, brk, skipc,
-                                     out, &n_accept, &new_pos, &k_eff);
+            ne = ora_spec_round_temp(s, anchor, anchor_pos, k, p_min, n_min, temp, topp, &rng, brk,
+                                     skipc, out, &n_accept, &new_pos, &k_eff);
         else
-            ne = ora_spec_round(s, anchor, anchor_pos, k, 0.0f, 0, brk, skipc, out, &n_accept,
+            ne = ora_spec_round(s, anchor, anchor_pos, k, p_min, n_min, brk, skipc, out, &n_accept,
                                 &new_pos, &k_eff);
         if (ne < 0) return -3;
         if (k_eff_out) k_eff_out[rounds] = k_eff;
@@ -1634,6 +1640,14 @@ ORA_API int ora_generate(void *hs, const int *prompt, int n_prompt, int k, int n
     if (n_rounds) *n_rounds = rounds;
     if (rng_out) *rng_out = rng;
     return n;
+}
+
+ORA_API int ora_generate(void *hs, const int *prompt, int n_prompt, int k, int n_new,
+                         float temp, float topp, uint64_t seed, int brk, int skipc,
+                         int *tokens, int cap, int *k_eff_out, int *n_acc_out, int *n_rounds,
+                         uint64_t *rng_out) {
+    return ora_generate_ex(hs, prompt, n_prompt, k, n_new, temp, topp, seed, brk, skipc, 0.0f, 0,
+                           tokens, cap, k_eff_out, n_acc_out, n_rounds, rng_out);
 }
 
 /* State accessors for the tests. */

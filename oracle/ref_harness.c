@@ -206,9 +206,9 @@ static int cmd_gen(int argc, char **argv) {
     token = prompt[n_prompt - 1];
     pos = n_prompt - 1;
     toks = (int *)malloc(sizeof(int) * (size_t)(n_new + 16));
-    rk = (int *)malloc(sizeof(int) * (size_t)(n_new + 16));
-    ra = (int *)malloc(sizeof(int) * (size_t)(n_new + 16));
-    rt = (double *)malloc(sizeof(double) * (size_t)(n_new + 16));
+    rk = (int *)malloc(sizeof(int) * (size_t)(2 * n_new + 16));
+    ra = (int *)malloc(sizeof(int) * (size_t)(2 * n_new + 16));
+    rt = (double *)malloc(sizeof(double) * (size_t)(2 * n_new + 16));
     t_loop0 = now_us();
     while (n_tok < n_new) {
         int anchor, anchor_pos, out_t[LZ_SPEC_K_MAX + 1];

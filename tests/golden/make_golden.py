@@ -24,7 +24,8 @@ sys.path.insert(0, os.path.join(ROOT, "tests"))
 
 import oracle_lib as OL  # noqa: E402
 
-# (fixture, model dir name, generator config id, vocab, n_prompt, k, n_new, temp, topp, sampler seed)
+# (fixture, model dir name, generator config id, vocab, n_prompt, k, n_new, temp, topp, sampler seed
+#  [, options]); options: prompt_seed, p_min, n_min, brk (debug_break_rollback), skipc (debug_skip_catchup)
 CASES = [
     ("gen_micro_k3_greedy", "micro", 10, 512, 24, 3, 40, 0.0, 1.0, 1),
     ("gen_micro_k2_temp", "micro", 10, 512, 24, 2, 32, 0.8, 0.95, 7),
@@ -35,6 +36,19 @@ CASES = [
     ("gen_base_k2_temp", "base", 1, 65536, 64, 2, 32, 0.8, 0.95, 7),
     ("gen_large_k3_greedy", "large", 3, 131072, 40, 3, 24, 0.0, 1.0, 1),     # configs[3] shape, short run
     ("gen_server_k3_greedy", "server", 4, 8192, 48, 3, 48, 0.0, 1.0, 1),    # configs[4] model (skewed router)
+    ("gen_tiny_k1_temp", "tiny", 0, 8192, 64, 1, 64, 0.8, 0.95, 7),          # configs[2] at k = 1
+    # The echo model (config 11): greedy drafts are accepted at every depth,
+    # so these runs take the accepted-draft branches of a round (bonus token,
+    # partial rollback, catch-up rows, chain reseed from row n).
+    ("gen_echo_k1_greedy", "echo", 11, 64, 24, 1, 160, 0.0, 1.0, 1, {"prompt_seed": 11}),
+    ("gen_echo_k3_greedy", "echo", 11, 64, 24, 3, 160, 0.0, 1.0, 1, {"prompt_seed": 11}),
+    ("gen_echo_k6_greedy", "echo", 11, 64, 24, 6, 200, 0.0, 1.0, 1, {"prompt_seed": 11}),
+    ("gen_echo_k3_pmin", "echo", 11, 64, 24, 3, 100, 0.0, 1.0, 1, {"prompt_seed": 2, "p_min": 0.05775}),
+    ("gen_echo_k3_pmin_nmin", "echo", 11, 64, 24, 3, 100, 0.0, 1.0, 1,
+     {"prompt_seed": 2, "p_min": 0.05775, "n_min": 2}),
+    ("gen_echo_k3_brk", "echo", 11, 64, 24, 3, 100, 0.0, 1.0, 1, {"prompt_seed": 11, "brk": 1}),
+    ("gen_echo_k3_skipc", "echo", 11, 64, 24, 3, 100, 0.0, 1.0, 1, {"prompt_seed": 11, "skipc": 1}),
+    ("gen_echo_k3_temp", "echo", 11, 64, 24, 3, 100, 0.8, 0.95, 7, {"prompt_seed": 11}),
 ]
 MODEL_SEED = 1234
 PROMPT_SEED = 0
@@ -47,21 +61,35 @@ def main():
         sys.exit("reference build absent: make -f oracle/ref.mk all")
     root = os.environ.get("L98_MODEL_DIR") or os.path.join(tempfile.gettempdir(), "l98_models")
     only = set(sys.argv[1:])
-    for name, mdir, cid, V, n_prompt, k, n_new, temp, topp, seed in CASES:
+    for case in CASES:
+        name, mdir, cid, V, n_prompt, k, n_new, temp, topp, seed = case[:10]
+        opt = case[10] if len(case) > 10 else {}
         if only and name not in only:
             continue
+        pseed = opt.get("prompt_seed", PROMPT_SEED)
+        p_min, n_min = float(opt.get("p_min", 0.0)), int(opt.get("n_min", 0))
+        brk, skipc = int(opt.get("brk", 0)), int(opt.get("skipc", 0))
+        extra = []
+        if p_min > 0:
+            extra += ["--pmin", repr(p_min)]
+        if n_min > 0:
+            extra += ["--nmin", str(n_min)]
+        if brk:
+            extra.append("--break-rollback")
+        if skipc:
+            extra.append("--skip-catchup")
         model = pkg.ensure_model(os.path.join(root, mdir), cid, seed=MODEL_SEED)
         h = hashlib.sha256()
         with open(os.path.join(model, "model.bin"), "rb") as f:
             for blk in iter(lambda: f.read(1 << 24), b""):
                 h.update(blk)
         digest = h.hexdigest()
-        prompt = pkg.prompt_tokens(PROMPT_SEED, n_prompt, V)
-        r = OL.reference_generate(model, prompt, k, n_new, temp, topp, seed=seed)
+        prompt = pkg.prompt_tokens(pseed, n_prompt, V)
+        r = OL.reference_generate(model, prompt, k, n_new, temp, topp, seed=seed, extra=extra)
         out = {
             "model": mdir, "config_id": cid, "model_seed": MODEL_SEED, "model_sha256": digest, "vocab": V,
-            "prompt_seed": PROMPT_SEED, "n_prompt": n_prompt, "k": k, "n_new": n_new, "temp": temp,
-            "topp": topp, "sampler_seed": seed,
+            "prompt_seed": pseed, "n_prompt": n_prompt, "k": k, "n_new": n_new, "temp": temp,
+            "topp": topp, "sampler_seed": seed, "p_min": p_min, "n_min": n_min, "brk": brk, "skipc": skipc,
             "tokens": [int(t) for t in r["tokens"]],
             "k_eff": [int(t) for t in r["k_eff"]],
             "n_accept": [int(t) for t in r["n_accept"]],

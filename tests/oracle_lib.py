@@ -44,6 +44,9 @@ def lib():
                                          _IP, _IP, _IP, _IP]),
             "ora_generate": (C.c_int, [_P, _IP, C.c_int, C.c_int, C.c_int, C.c_float, C.c_float, C.c_uint64,
                                        C.c_int, C.c_int, _IP, C.c_int, _IP, _IP, _IP, C.POINTER(C.c_uint64)]),
+            "ora_generate_ex": (C.c_int, [_P, _IP, C.c_int, C.c_int, C.c_int, C.c_float, C.c_float, C.c_uint64,
+                                          C.c_int, C.c_int, C.c_float, C.c_int, _IP, C.c_int, _IP, _IP, _IP,
+                                          C.POINTER(C.c_uint64)]),
             "ora_state_info": (C.c_int, [_P, _IP]),
             "ora_set_slot": (None, [_P, C.c_int]),
             "ora_set_mtp_pos": (None, [_P, C.c_int]),
@@ -181,16 +184,16 @@ class Oracle:
                                  brk, skipc, ip(out), C.byref(na), C.byref(npos), C.byref(ke))
         return r, out, na.value, npos.value, ke.value
 
-    def generate(self, prompt, k, n_new, temp=0.0, topp=1.0, seed=1, brk=0, skipc=0):
+    def generate(self, prompt, k, n_new, temp=0.0, topp=1.0, seed=1, brk=0, skipc=0, p_min=0.0, n_min=0):
         p = np.ascontiguousarray(prompt, np.int32)
         cap = n_new + 16
         toks = np.zeros(cap, np.int32)
-        ke = np.zeros(n_new + 8, np.int32)
-        na = np.zeros(n_new + 8, np.int32)
+        ke = np.zeros(2 * n_new + 8, np.int32)
+        na = np.zeros(2 * n_new + 8, np.int32)
         nr = C.c_int()
         rng = C.c_uint64()
-        n = lib().ora_generate(self.s, ip(p), len(p), k, n_new, temp, topp, seed, brk, skipc, ip(toks), cap,
-                               ip(ke), ip(na), C.byref(nr), C.byref(rng))
+        n = lib().ora_generate_ex(self.s, ip(p), len(p), k, n_new, temp, topp, seed, brk, skipc, float(p_min),
+                                  int(n_min), ip(toks), cap, ip(ke), ip(na), C.byref(nr), C.byref(rng))
         if n < 0:
             raise RuntimeError(f"ora_generate failed {n}")
         return toks[:min(n, cap)], ke[:nr.value], na[:nr.value], rng.value

@@ -453,6 +453,50 @@ def test_greedy_spec_width_invariant(pkg, tiny):
         assert np.array_equal(gen_case(tiny, prompt, k, 40)[0][:40], t1), k
 
 
+@pytest.fixture(scope="module")
+def echo(pkg, model_root):
+    return pkg.ensure_model(os.path.join(model_root, "echo"), 11, seed=1234)
+
+
+def test_echo_model_accepts_and_keeps_the_greedy_sequence(pkg, echo):
+    """On the echo model drafts are accepted at every depth, and the emitted
+    sequence is still the plain greedy one whatever the width: the accept,
+    bonus, rollback, reseed and catch-up steps change the work, not the
+    output (a wrong rollback slot or reseed row would change it)."""
+    prompt = pkg.prompt_tokens(11, 24, 64)
+    t1, _, na1, _ = gen_case(echo, prompt, 1, 120)
+    assert 1 in set(na1)
+    for k in (2, 3, 4, 5, 6):
+        tk, _, na, _ = gen_case(echo, prompt, k, 120)
+        assert np.array_equal(tk[:120], t1[:120]), k
+        assert max(na) == k, k
+    # the knob that breaks the rollback changes the output once a draft is rejected mid-way
+    broken = gen_case(echo, prompt, 3, 120, brk=1)[0]
+    assert not np.array_equal(broken[:120], t1[:120])
+
+
+def test_argmax_p1_nan_at_zero():
+    """lz_argmax_p1 starts from element 0 and moves only on v > best, so a
+    NaN at 0 is never beaten (src/sampler.c:279-295); NaN elsewhere never
+    wins, and -0 ties +0 (the first stays)."""
+    L = OL.lib()
+    x = np.array([np.nan, 1.0, 5.0, -2.0], np.float32)
+    p = C.c_float()
+    assert L.o_argmax_p1(fp(x), 4, C.byref(p)) == 0
+    x = np.array([1.0, np.nan, 5.0, np.nan], np.float32)
+    assert L.o_argmax_p1(fp(x), 4, C.byref(p)) == 2
+    x = np.array([-0.0, 0.0, -1.0], np.float32)
+    assert L.o_argmax_p1(fp(x), 3, C.byref(p)) == 0
+    if OL.have_reference():
+        R = C.CDLL(OL.REF_SO)
+        R.lz_argmax_p1.restype = C.c_int
+        R.lz_argmax_p1.argtypes = [C.POINTER(C.c_float), C.c_int, C.POINTER(C.c_float)]
+        for row in ([np.nan, 1.0, 5.0], [1.0, np.nan, 5.0], [-0.0, 0.0], [-np.inf, np.nan, 2.0]):
+            x = np.array(row, np.float32)
+            q = C.c_float()
+            assert R.lz_argmax_p1(fp(x), len(x), C.byref(q)) == L.o_argmax_p1(fp(x), len(x), C.byref(p)), row
+
+
 def test_verify_rows_equal_single_steps(pkg, tiny):
     """lz_forward_verify's rows == the same tokens forwarded one at a time."""
     prompt = pkg.prompt_tokens(1, 30, 8192)
@@ -507,7 +551,9 @@ def test_oracle_matches_golden(pkg, model_root, fname):
     digest = hashlib.sha256(open(os.path.join(model, "model.bin"), "rb").read()).hexdigest()
     assert digest == g["model_sha256"], "synthetic model generator changed"
     prompt = pkg.prompt_tokens(g["prompt_seed"], g["n_prompt"], g["vocab"])
-    toks, ke, na, rng = gen_case(model, prompt, g["k"], g["n_new"], g["temp"], g["topp"], g["sampler_seed"])
+    toks, ke, na, rng = gen_case(model, prompt, g["k"], g["n_new"], g["temp"], g["topp"], g["sampler_seed"],
+                                 brk=g.get("brk", 0), skipc=g.get("skipc", 0), p_min=g.get("p_min", 0.0),
+                                 n_min=g.get("n_min", 0))
     n = len(g["tokens"])
     assert list(toks[:n]) == g["tokens"]
     assert list(ke) == g["k_eff"] and list(na) == g["n_accept"] and rng == g["rng"]
@@ -528,3 +574,32 @@ def test_hip_library_exports_every_declared_symbol():
     lib = C.CDLL(so)
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
+    # the exported data of llama98.def:117-157 that the header declares
+    data = set()
+    for decl in re.findall(r"^extern [^;(\n]+;", hdr, flags=re.M):
+        data.update(re.findall(r"\b(lz_\w+)", decl))
+    assert {"lz_debug_n_ring_rollback", "lz_kv_kfmt", "lz_attn_window", "lz_moe_topk", "lz_prof_us"} <= data
+    missing = [n for n in sorted(data) if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_load_config_reads_the_header(pkg, model_root, micro):
+    """lz_load_config (host logic: the model.bin header, no device) gives
+    the synthetic writer's shapes, from the file or its directory, and
+    refuses a missing file and a config.json."""
+    so = os.path.join(ROOT, "llama98-zh_amd", "lib", "libl98hip.so")
+    if not os.path.exists(so):
+        pytest.skip("HIP library not built")
+    lib = pkg.hip_lib()
+    want = pkg.synth_config(10)
+    for path in (micro, os.path.join(micro, "model.bin")):
+        c = pkg.LZModelConfig()
+        err = C.create_string_buffer(256)
+        assert lib.lz_load_config(C.byref(c), path.encode(), err, 256) == 0, err.value
+        assert (c.vocab_size, c.hidden_size, c.n_layers, c.num_experts, c.num_experts_per_token) == (
+            want.vocab, want.hidden, want.n_layers, want.n_experts, want.topk)
+        assert c.layer_types[3] == 1 and c.layer_types[0] == 2
+    c = pkg.LZModelConfig()
+    err = C.create_string_buffer(256)
+    assert lib.lz_load_config(C.byref(c), os.path.join(micro, "absent.bin").encode(), err, 256) == 1
+    assert b"cannot open" in err.value
