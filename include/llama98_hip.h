@@ -311,6 +311,17 @@ int l98_moe_route(const float *logits, const float *bias, int nt, int E, int top
  * stays the answer).  A check of the kernel the rounds run; the reference
  * has no device.  Returns 0 (1 on a bad argument or a device error). */
 int l98_argmax_rows(const float *x, int rows, int n, int mode, int *out);
+/* lz_spec_accept_temp (src/generate.c:283-346) on host rows with no device
+ * allocation: no counterpart in the reference; for callers that cannot call
+ * hipMalloc (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid it).  The rows, the generator state and the result are staged
+ * in a static device array of 2 * L98_NOALLOC_MAX_VOCAB floats + 256 bytes
+ * per GPU, held until the process ends; calls that overlap on one GPU race
+ * on it.  Returns what lz_spec_accept_temp returns (the token, -1 on bad
+ * input), -2 when vocab > L98_NOALLOC_MAX_VOCAB, -3 on a device error. */
+#define L98_NOALLOC_MAX_VOCAB 262144
+int l98_spec_accept_temp_noalloc(const float *p, const float *q, int x, int vocab, float u,
+                                 lz_u64 *residual_rng, int *out_accepted);
 /* Device and build facts, for logs. */
 const char *l98_device_name(void);
 /* Seconds of device time of the last l98_generate call's round loop

@@ -20,6 +20,7 @@ HIP_LIB = os.path.join(LIB_DIR, "libl98hip.so")
 SYNTH_LIB = os.path.join(LIB_DIR, "libl98synth.so")
 
 LZ_SPEC_K_MAX = 6
+L98_NOALLOC_MAX_VOCAB = 262144   # l98_spec_accept_temp_noalloc's static staging
 L98_SPEC_K_GPU = 7      # the library's own loops take k up to 7 (verify M = 8)
 LZ_BATCH_MAX = 8
 LZ_ERR = {"NULL_ARG": 6, "STATE_ALLOC": 7, "FORWARD": 20, "SPEC_NO_HEAD": 24, "SPEC_K_RANGE": 25}
@@ -92,6 +93,8 @@ HIP_API = [
     ("lz_mtp_catchup", C.c_int, [C.POINTER(LZModel), C.POINTER(LZRunState), _FP, _IP, C.c_int, C.c_int]),
     ("lz_spec_accept", C.c_int, [_IP, _IP, C.c_int, C.c_int, _IP]),
     ("lz_spec_accept_temp", C.c_int, [_FP, _FP, C.c_int, C.c_int, C.c_float, C.POINTER(C.c_uint64), _IP]),
+    ("l98_spec_accept_temp_noalloc", C.c_int, [_FP, _FP, C.c_int, C.c_int, C.c_float, C.POINTER(C.c_uint64),
+                                               _IP]),
     ("lz_spec_round", C.c_int, [C.POINTER(LZModel), C.POINTER(LZRunState), C.c_int, C.c_int, C.c_int, C.c_float,
                                 C.c_int, C.POINTER(LZSampler), C.c_int, C.c_int, _IP, _IP, _IP, _IP,
                                 C.c_char_p, C.c_int]),

@@ -24,6 +24,7 @@
 #include <time.h>
 #include <unistd.h>
 
+#include <mutex>
 #include <vector>
 
 #include "../../include/llama98_hip.h"
@@ -1303,6 +1304,62 @@ extern "C" int lz_spec_accept_temp(const float *p, const float *q, int x, int vo
         if (out_accepted) *out_accepted = 0;
         return -1;
     }
+    if (out_accepted) *out_accepted = res[1];
+    return res[0];
+}
+
+// ------------------------------------------- no-allocation acceptance ---
+// l98_spec_accept_temp_noalloc: lz_spec_accept_temp on host rows with its
+// device staging (the two rows, the generator state and the result) in a
+// file-scope device array instead of hipMalloc'd buffers, for callers that
+// cannot allocate.  Each GPU holds its own copy of the array until the
+// process ends; its address on a device is taken once, with that device
+// current (the array's name is only a host-side stand-in).  Every call on a
+// device shares the array, so calls that overlap on one device race.
+
+#define NOALLOC_MAX_VOCAB L98_NOALLOC_MAX_VOCAB
+#define NOALLOC_MAX_DEVICES 64
+static __device__ __align__(256) unsigned char scratch[2 * sizeof(float) * NOALLOC_MAX_VOCAB + 256];
+static char *g_scratch_ptr[NOALLOC_MAX_DEVICES];
+static std::mutex g_scratch_mu;
+
+// The array's address on the current device (taken on the first call there).
+static char *scratch_on_current_device() {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= NOALLOC_MAX_DEVICES) return nullptr;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *ptr = nullptr;
+        if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
+        g_scratch_ptr[dev] = (char *)ptr;
+    }
+    return g_scratch_ptr[dev];
+}
+
+extern "C" int l98_spec_accept_temp_noalloc(const float *p, const float *q, int x, int vocab, float u, lz_u64 *rng,
+                                            int *out_accepted) {
+    if (out_accepted) *out_accepted = 0;
+    if (!p || !q || !rng || vocab <= 0 || x < 0 || x >= vocab) return -1;   // as src/generate.c:283-346
+    if (vocab > NOALLOC_MAX_VOCAB) {
+        fprintf(stderr, "l98_spec_accept_temp_noalloc: vocab %d exceeds the static staging of %d\n", vocab,
+                NOALLOC_MAX_VOCAB);
+        return -2;
+    }
+    char *base = scratch_on_current_device();
+    if (!base) return -3;
+    float *dp = (float *)base, *dq = dp + NOALLOC_MAX_VOCAB;
+    unsigned long long *drng = (unsigned long long *)(dq + NOALLOC_MAX_VOCAB);
+    int *dout = (int *)(drng + 2);
+    int res[2] = {-1, 0};
+    // the kernel reads rows [0, vocab) only and writes both result words on
+    // every path, so nothing in the array needs clearing
+    if (hipMemcpy(dp, p, sizeof(float) * (size_t)vocab, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(dq, q, sizeof(float) * (size_t)vocab, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(drng, rng, sizeof(*drng), hipMemcpyHostToDevice) != hipSuccess ||
+        l98k_smp_accept(dp, dq, vocab, x, &u, drng, dout, nullptr) != 0 ||
+        hipMemcpy(res, dout, sizeof(res), hipMemcpyDeviceToHost) != hipSuccess ||
+        hipMemcpy(rng, drng, sizeof(*drng), hipMemcpyDeviceToHost) != hipSuccess)
+        return -3;
     if (out_accepted) *out_accepted = res[1];
     return res[0];
 }
