@@ -26,13 +26,13 @@
  *   - o_fwht_i32 / o_fwht_f32 are compared with the reference's exported
  *     lz_fwht_i32 / lz_fwht and with a dense Sylvester matrix product;
  *     o_subn_fwht_quant / o_subn_rot_f32 restate static functions of
- *     src/forward_kda.c that no exported symbol reaches: they are checked by
- *     closed forms (a zero row, each group's largest code being 127, the
+ *     src/forward_kda.c: they are checked bit for bit against those very
+ *     functions, exported by a test-only translation unit that compiles
+ *     the reference's forward_kda.c in place (oracle/ref_subn.c), which
+ *     pins the scale's multiply order (tam * inv_S) * rsqrt(blk) / 127; and
+ *     by closed forms (a zero row, each group's largest code being 127, the
  *     dequantized row against H.x / sqrt(blk), the float rotation against
- *     the dense product), built from the reference's exported pow2f,
- *     q8_amax and lz_rsqrt_float_body; the scale's left-to-right multiply
- *     order follows the text of src/forward_kda.c:79 and is otherwise
- *     unpinned.
+ *     the dense product).
  */
 #define _POSIX_C_SOURCE 200809L
 #include <float.h>

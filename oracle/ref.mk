@@ -33,7 +33,7 @@ SHIP_DEFS :=
 ORA_OBJS  := $(addprefix $(OUT)/oracle/,$(addsuffix .o,$(ENG) $(MMX) $(AVX2)))
 SHIP_OBJS := $(addprefix $(OUT)/ship/,$(addsuffix .o,$(ENG) $(MMX) $(AVX2)))
 
-all: $(OUT)/l98ref_oracle $(OUT)/l98ref_ship $(OUT)/libl98ref.so
+all: $(OUT)/l98ref_oracle $(OUT)/l98ref_ship $(OUT)/libl98ref.so $(OUT)/libl98ref_subn.so
 
 $(OUT)/oracle/%.o: $(REF)/src/%.c
 	@mkdir -p $(OUT)/oracle
@@ -64,6 +64,16 @@ $(OUT)/libl98ref.so: $(ORA_OBJS)
 	$(CC) -shared -o $@ $(ORA_OBJS) -lm
 
 .PHONY: all
+
+# The reference's static subn_fwht_quant / subn_rot_f32 exported by a
+# wrapper translation unit that compiles src/forward_kda.c in place
+# (oracle/ref_subn.c), linked with every other oracle-mode object.
+SUBN_OBJS := $(filter-out $(OUT)/oracle/forward_kda.o,$(ORA_OBJS))
+$(OUT)/ref_subn.o: oracle/ref_subn.c $(REF)/src/forward_kda.c
+	@mkdir -p $(OUT)
+	$(CC) $(BASEFL) $(ORA_DEFS) -c -o $@ oracle/ref_subn.c
+$(OUT)/libl98ref_subn.so: $(OUT)/ref_subn.o $(SUBN_OBJS)
+	$(CC) -shared -o $@ $(OUT)/ref_subn.o $(SUBN_OBJS) -lm
 
 # Tap build: the reference's own LZ_TAP hook (src/forward.h:27-36) routed to
 # a recorder in the harness, to localise a divergence layer by layer.

@@ -151,3 +151,54 @@ def test_subn_rot_f32_dense_product(n, blk):
         assert r.tobytes() == want.tobytes()
     x = rng.standard_normal(n).astype(np.float32)
     assert np.allclose(o_subn_rot(x, blk), block_h(x.astype(np.float64), blk) / np.sqrt(blk), rtol=0, atol=1e-4)
+
+
+@pytest.fixture(scope="module")
+def ref_subn():
+    """The reference's own static subn_fwht_quant / subn_rot_f32, exported by
+    oracle/ref_subn.c (built by oracle/ref.mk), in the float-oracle mode."""
+    import os
+    path = os.path.join(OL.REF_DIR, "libl98ref_subn.so")
+    if not os.path.exists(path):
+        pytest.skip("reference build absent (oracle/_ref)")
+    L = C.CDLL(path)
+    L.lz_float_ref_select.restype = C.c_char_p
+    L.lz_float_ref_select.argtypes = [C.c_char_p]
+    L.lz_fastfp_select.restype = C.c_char_p
+    L.lz_fastfp_select.argtypes = [C.c_char_p]
+    L.lz_float_ref_select(b"off")
+    L.lz_fastfp_select(b"off")
+    L.l98ref_subn_fwht_quant.argtypes = [FP, C.c_int, C.c_int, C.c_int, C.c_void_p, FP]
+    L.l98ref_subn_rot_f32.argtypes = [FP, C.c_int, C.c_int]
+    return L
+
+
+SUBN_SHAPES = [(256, 64, 0), (512, 64, 32), (1024, 256, 0), (1024, 256, 128), (2048, 64, 2048), (768, 256, 96),
+               (512, 512, 64), (8192, 8192, 0), (4096, 128, 64)]
+
+
+@pytest.mark.parametrize("n,blk,gw", SUBN_SHAPES)
+def test_subn_fwht_quant_bitwise_vs_reference(ref_subn, n, blk, gw):
+    """The oracle's subn_fwht_quant against the reference's own static
+    function: codes and scales bit for bit, which pins the scale's multiply
+    order (tam * inv_S) * rsqrt(blk) * (1/127)."""
+    rng = np.random.default_rng(3 * n + blk + gw)
+    rows = subn_rows(n, rng) + [np.zeros(n, np.float32),
+                                (rng.standard_normal(n) * 2.0 ** rng.integers(-60, 60, n)).astype(np.float32)]
+    for x in rows:
+        x = np.ascontiguousarray(x, np.float32)
+        q, s = o_subn_quant(x, blk, gw)
+        qr = np.empty(n, np.int8)
+        sr = np.empty(n // 32, np.float32)
+        ref_subn.l98ref_subn_fwht_quant(x.ctypes.data_as(FP), n, blk, gw, qr.ctypes.data, sr.ctypes.data_as(FP))
+        assert np.array_equal(q, qr)
+        assert s.tobytes() == sr.tobytes()
+
+
+@pytest.mark.parametrize("n,blk", [(64, 64), (512, 64), (1024, 256), (2048, 512), (8192, 8192)])
+def test_subn_rot_f32_bitwise_vs_reference(ref_subn, n, blk):
+    rng = np.random.default_rng(n + blk)
+    for x in subn_rows(n, rng):
+        vr = np.array(x, np.float32)
+        ref_subn.l98ref_subn_rot_f32(vr.ctypes.data_as(FP), n, blk)
+        assert o_subn_rot(x, blk).tobytes() == vr.tobytes()
