@@ -322,6 +322,14 @@ int l98_argmax_rows(const float *x, int rows, int n, int mode, int *out);
 #define L98_NOALLOC_MAX_VOCAB 262144
 int l98_spec_accept_temp_noalloc(const float *p, const float *q, int x, int vocab, float u,
                                  lz_u64 *residual_rng, int *out_accepted);
+/* The wide int8 GEMM of the many-row forwards (prefill chunks, batched
+ * verify) on host arrays: out[t][n] = (sum_s float(acc[t,n,s]) * xqs[t][s])
+ * * ws[n] for M token rows of K (K % 32 == 0) int8 codes against N weight
+ * rows, acc the exact int32 group sums, as lz_matmul_xq_nt computes it
+ * (src/ops_matmul.c:336-466, src/ops_epi.c:983-1017).  A check of the
+ * matrix-core kernel; returns 0 (1 on a bad argument or a device error). */
+int l98_gemm_q8(const int8_t *w, const float *ws, int N, int K, const int8_t *xq, const float *xqs, int M,
+                float *out);
 /* Device and build facts, for logs. */
 const char *l98_device_name(void);
 /* Seconds of device time of the last l98_generate call's round loop

@@ -1794,6 +1794,19 @@ extern "C" int l98_moe_route(const float *logits, const float *bias, int nt, int
     return rc;
 }
 
+extern "C" int l98_gemm_q8(const int8_t *w, const float *ws, int N, int K, const int8_t *xq, const float *xqs, int M,
+                           float *out) {
+    if (!w || !ws || !xq || !xqs || !out || N < 1 || M < 1 || K < 32 || (K & 31)) return 1;
+    DevBuf dw, dws, dx, dxs, dout;
+    if (!dw.get(w, (size_t)N * K) || !dws.get(ws, sizeof(float) * N) || !dx.get(xq, (size_t)M * K) ||
+        !dxs.get(xqs, sizeof(float) * (size_t)M * (K / 32)) || !dout.get(nullptr, sizeof(float) * (size_t)M * N))
+        return 1;
+    if (l98k_mfma_gemm((const int8_t *)dw.p, (const float *)dws.p, N, K, (const int8_t *)dx.p, (const float *)dxs.p, M,
+                       (float *)dout.p, N, nullptr))
+        return 1;
+    return dout.put(out, sizeof(float) * (size_t)M * N) ? 0 : 1;
+}
+
 extern "C" int l98_argmax_rows(const float *x, int rows, int n, int mode, int *out) {
     if (!x || !out || rows < 1 || rows > MAX_CHUNK || n < 1 || (mode != 0 && mode != 1)) return 1;
     DevBuf dx, dpart, dcnt, dout;

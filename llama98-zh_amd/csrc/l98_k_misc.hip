@@ -259,6 +259,7 @@ extern "C" int l98k_upload_exp_table(const float *tab) {
     if ((e = l98k_upload_exp_table_moe(tab)) != 0) return e;
     if ((e = l98k_upload_exp_table_kda(tab)) != 0) return e;
     if ((e = l98k_upload_exp_table_smp(tab)) != 0) return e;
+    if ((e = l98k_upload_exp_table_mfma(tab)) != 0) return e;
     return l98k_upload_exp_table_attn(tab);
 }
 

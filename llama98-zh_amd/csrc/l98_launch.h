@@ -16,6 +16,21 @@ int l98k_upload_exp_table_moe(const float *tab);
 int l98k_upload_exp_table_kda(const float *tab);
 int l98k_upload_exp_table_attn(const float *tab);
 int l98k_upload_exp_table_smp(const float *tab);
+int l98k_upload_exp_table_mfma(const float *tab);
+// Wide int8 GEMM on the matrix cores (l98_k_mfma.hip): out[t][n] for M
+// token rows, bit-identical to the GEMV path per token.
+int l98k_mfma_gemm(const int8_t *W, const float *ws, int N, int K, const int8_t *X, const float *Xs, int M, float *out,
+                   int out_stride, hipStream_t st);
+// Grouped over experts: group g < *ng multiplies expert gexp[g]'s bank rows
+// with its columns list[goff[g] .. + gcnt[g]] (activation row xmap[col] or
+// col, output row col).
+int l98k_mfma_gemm_grouped(const int8_t *bank, const float *bank_s, int N, int K, const int8_t *X, const float *Xs,
+                           const int *ng, int max_groups, const int *gexp, const int *goff, const int *gcnt,
+                           const int *list, const int *xmap, int max_cols, float *out, int out_stride, hipStream_t st);
+// Quantized GEMM inputs of `rows` rows: mode 0 quantize, 1 silu(src)*src2,
+// 2 slot-ordered expert combine; the GEMV prologues' arithmetic.
+int l98k_wide_pro(int mode, const float *src, const float *src2, int src_stride, const int *sel_idx,
+                  const float *sel_w, int topk, int n, int rows, int8_t *xq, float *xqs, hipStream_t st);
 // Temperature sampling (one block per call; l98_k_sample.hip).
 // probs = softmax(logits * inv_t); with keys: the top-p candidate keys and
 // indices for l98k_smp_sort_desc and their count.
