@@ -132,6 +132,7 @@ struct DModel {
     float *mtp_norm = nullptr, *mtp_pre_h = nullptr, *mtp_pre_e = nullptr;
     float *rope_cs = nullptr;
     int lin_index[128], full_index[128];
+    struct DWide *wide = nullptr;       // scratch of the many-row forwards (first use)
 };
 
 namespace {
@@ -470,9 +471,15 @@ extern "C" int lz_open(LZModel *m, const char *dir, char *errbuf, int errlen) {
     return 0;
 }
 
+namespace {
+void wide_free(DModel *m);
+}
+
 extern "C" void lz_free(LZModel *m) {
     if (!m || !m->impl) return;
     DModel *dm = (DModel *)m->impl;
+    (void)hipDeviceSynchronize();
+    wide_free(dm);
     if (dm->arena) (void)hipFree(dm->arena);
     delete dm;
     m->impl = nullptr;
@@ -917,6 +924,227 @@ int mtp_prefill_dev(DState *s, const float *h, const int *toks, int n, const int
     return 0;
 }
 
+// ------------------------------------------------------- wide forward ---
+//
+// Many token rows through the trunk at once: a prefill chunk of one session
+// (consecutive positions) or the verify rows of several sessions (each its
+// own ring, KV planes and positions).  Every projection is one matrix-core
+// GEMM over all rows (l98_k_mfma.hip); the routed experts are grouped GEMMs
+// over the (token, slot) pairs that chose each expert; the KDA recurrence
+// and attention run per session in 8-row sub-chunks with the chunked
+// path's kernels.  Each row gets exactly the arithmetic of the chunked path
+// (forward_chunk above), so results are bit-identical for any grouping of
+// rows.
+
+struct WideItem {
+    DState *d;                // the session
+    int row0, n, pos0;        // its rows [row0, row0 + n) at positions pos0 ..
+};
+
+}  // namespace
+
+struct DWide {
+    int cap = 0;              // rows
+    char *arena = nullptr;
+    float *x, *blk, *up_out, *sd_out, *hcap;
+    int8_t *xq, *xq2, *latq, *hq, *cq, *shq;
+    float *xqs, *xqs2, *latqs, *hqs, *cqs, *shqs;
+    float *pq, *pk, *pv, *pfa, *pb, *pg, *qg, *kp, *vp, *qh;
+    float *rl, *latx, *sgo, *suo, *h1, *h3, *h2;
+    int *sel_idx;
+    float *sel_w;
+    int *ng, *gexp, *goff, *gcnt, *list, *pair_token;
+    int *toks;
+    float *att;
+    float *logits = nullptr;  // rows x vocab, sized on demand
+    int logits_rows = 0;
+};
+
+namespace {
+
+#define WIDE_MAX 512          // rows of one wide forward
+#define WIDE_MIN 16           // prefills shorter than this take the chunked path
+
+DWide *wide_get(const DModel *cm) {
+    DModel *m = const_cast<DModel *>(cm);
+    if (m->wide) return m->wide;
+    const LZModelConfig &c = m->c;
+    const size_t R = WIDE_MAX, d = c.hidden_size, pairs = R * c.num_experts_per_token;
+    size_t wide = d;
+    for (int v : {c.attn_qgate_dim, c.lin_value_dim, c.attn_q_dim, c.moe_shared_width, c.moe_latent_dim})
+        wide = (size_t)v > wide ? (size_t)v : wide;
+    DWide *w = new DWide();
+    size_t off = 0;
+    auto take = [&](size_t bytes) { size_t o = off; off = (off + bytes + 255) & ~(size_t)255; return o; };
+    const size_t ox = take(4 * R * d), oblk = take(4 * R * d), oup = take(4 * R * d), osd = take(4 * R * d),
+                 ohc = take(4 * R * d), oxq = take(R * d), oxqs = take(4 * R * d / 32), oxq2 = take(R * wide),
+                 oxqs2 = take(4 * R * wide / 32), olq = take(R * c.moe_latent_dim),
+                 olqs = take(4 * R * c.moe_latent_dim / 32), ohq = take(pairs * c.moe_intermediate_size),
+                 ohqs = take(4 * pairs * c.moe_intermediate_size / 32), ocq = take(R * c.moe_latent_dim),
+                 ocqs = take(4 * R * c.moe_latent_dim / 32), oshq = take(R * c.moe_shared_width),
+                 oshqs = take(4 * R * c.moe_shared_width / 32), opq = take(4 * R * c.lin_key_dim),
+                 opk = take(4 * R * c.lin_key_dim), opv = take(4 * R * c.lin_value_dim),
+                 opfa = take(4 * R * c.kda_gate_rank), opb = take(4 * R * c.lin_n_v_heads),
+                 opg = take(4 * R * c.lin_value_dim), oqg = take(4 * R * c.attn_qgate_dim),
+                 okp = take(4 * R * c.attn_kv_dim), ovp = take(4 * R * c.attn_kv_dim), oqh = take(4 * R * c.attn_q_dim),
+                 orl = take(4 * R * c.num_experts), olx = take(4 * R * c.moe_latent_dim),
+                 osg = take(4 * R * c.moe_shared_width), osu = take(4 * R * c.moe_shared_width),
+                 oh1 = take(4 * pairs * c.moe_intermediate_size), oh3 = take(4 * pairs * c.moe_intermediate_size),
+                 oh2 = take(4 * pairs * c.moe_latent_dim), osi = take(4 * pairs), osw = take(4 * pairs),
+                 ong = take(4), oge = take(4 * MAX_EXPERTS), ogo = take(4 * MAX_EXPERTS), ogc = take(4 * MAX_EXPERTS),
+                 oli = take(4 * pairs), opt = take(4 * pairs), otk = take(4 * R),
+                 oat = take(4 * (size_t)MAX_CHUNK * c.n_heads * (size_t)((c.seq_len + 3) & ~3));
+    if (hipMalloc((void **)&w->arena, off) != hipSuccess) { delete w; return nullptr; }
+    char *a = w->arena;
+    w->cap = WIDE_MAX;
+    w->x = (float *)(a + ox); w->blk = (float *)(a + oblk); w->up_out = (float *)(a + oup); w->sd_out = (float *)(a + osd);
+    w->hcap = (float *)(a + ohc);
+    w->xq = (int8_t *)(a + oxq); w->xqs = (float *)(a + oxqs); w->xq2 = (int8_t *)(a + oxq2); w->xqs2 = (float *)(a + oxqs2);
+    w->latq = (int8_t *)(a + olq); w->latqs = (float *)(a + olqs); w->hq = (int8_t *)(a + ohq); w->hqs = (float *)(a + ohqs);
+    w->cq = (int8_t *)(a + ocq); w->cqs = (float *)(a + ocqs); w->shq = (int8_t *)(a + oshq); w->shqs = (float *)(a + oshqs);
+    w->pq = (float *)(a + opq); w->pk = (float *)(a + opk); w->pv = (float *)(a + opv); w->pfa = (float *)(a + opfa);
+    w->pb = (float *)(a + opb); w->pg = (float *)(a + opg); w->qg = (float *)(a + oqg); w->kp = (float *)(a + okp);
+    w->vp = (float *)(a + ovp); w->qh = (float *)(a + oqh);
+    w->rl = (float *)(a + orl); w->latx = (float *)(a + olx); w->sgo = (float *)(a + osg); w->suo = (float *)(a + osu);
+    w->h1 = (float *)(a + oh1); w->h3 = (float *)(a + oh3); w->h2 = (float *)(a + oh2);
+    w->sel_idx = (int *)(a + osi); w->sel_w = (float *)(a + osw);
+    w->ng = (int *)(a + ong); w->gexp = (int *)(a + oge); w->goff = (int *)(a + ogo); w->gcnt = (int *)(a + ogc);
+    w->list = (int *)(a + oli); w->pair_token = (int *)(a + opt); w->toks = (int *)(a + otk);
+    w->att = (float *)(a + oat);
+    m->wide = w;
+    return w;
+}
+
+void wide_free(DModel *m) {
+    if (!m->wide) return;
+    if (m->wide->arena) (void)hipFree(m->wide->arena);
+    if (m->wide->logits) (void)hipFree(m->wide->logits);
+    delete m->wide;
+    m->wide = nullptr;
+}
+
+// Dense MFMA GEMM of a weight matrix over the rows' quantized activations.
+int mf(const DMat &W, const int8_t *xq, const float *xqs, int R, float *out, int out_stride, hipStream_t st) {
+    return l98k_mfma_gemm(W.q, W.s, W.rows, W.cols, xq, xqs, R, out, out_stride, st);
+}
+
+// The trunk over R rows of w->toks (device ids), grouped into sessions by
+// items (row order).  advance: KDA ring advance per token (verify) or not
+// (prefill).  capture: device rows [R][d] of the final-normed hidden, or
+// null; logits: device rows [R][V] of the tied lm_head, or null.  Every
+// launch goes on stream st; the sessions' control blocks must hold their
+// slot bases and positions (pos_scratch = the item's pos0) before.
+int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, int R, bool advance, float *capture,
+                 float *logits, hipStream_t st) {
+    const LZModelConfig &c = m->c;
+    const int d = c.hidden_size, E = c.num_experts, topk = c.num_experts_per_token;
+    const int lat = c.moe_latent_dim, inter = c.moe_intermediate_size, sw = c.moe_shared_width;
+    const float eps = c.rms_norm_eps;
+    if (R < 1 || R > w->cap) return 1;
+    CK(l98k_embed(m->embed.q, m->embed.s, w->toks, d, R, w->x, st));
+    const float *ra = nullptr, *rb = nullptr;
+    for (int l = 0; l < c.n_layers; l++) {
+        const DLayer &L = m->L[l];
+        CK(l98k_rmsnorm(w->x, d, ra, rb, L.in_norm, d, eps, R, nullptr, 0, w->xq, w->xqs, st));
+        if (L.type == 1) {
+            const int qgd = c.attn_qgate_dim, kvd = c.attn_kv_dim, qd = c.attn_q_dim;
+            CK(mf(L.q, w->xq, w->xqs, R, w->qg, qgd, st));
+            CK(mf(L.k, w->xq, w->xqs, R, w->kp, kvd, st));
+            CK(mf(L.v, w->xq, w->xqs, R, w->vp, kvd, st));
+            const int plane = m->full_index[l];
+            for (int it = 0; it < n_items; it++) {
+                const WideItem &I = items[it];
+                DState *s = I.d;
+                for (int c0 = 0; c0 < I.n; c0 += MAX_CHUNK) {
+                    const int k = I.n - c0 < MAX_CHUNK ? I.n - c0 : MAX_CHUNK;
+                    const int r = I.row0 + c0;
+                    AttnArgs a{};
+                    a.qg = w->qg + (size_t)r * qgd; a.kp = w->kp + (size_t)r * kvd; a.vp = w->vp + (size_t)r * kvd;
+                    a.q_norm = L.q_norm; a.k_norm = L.k_norm; a.rope_cs = m->rope_cs;
+                    a.qh = w->qh + (size_t)r * qd;
+                    const size_t off = (size_t)plane * s->seq_len * kvd;
+                    a.kcache = s->kq + off; a.vcache = s->vq + off;
+                    a.kscale = s->ks + off / 32; a.vscale = s->vs + off / 32;
+                    a.out = nullptr;
+                    a.oq = w->xq2 + (size_t)r * qd; a.oqs = w->xqs2 + (size_t)r * (qd / 32);
+                    a.ctl_pos = &s->ctl->pos_scratch; a.pos_off = c0;
+                    a.nh = c.n_heads; a.nkv = c.n_kv_heads; a.hd = c.head_dim; a.rot = c.rotary_dim;
+                    a.q_dim = qd; a.qg_dim = qgd; a.kv_dim = kvd;
+                    a.kv_only = 0;
+                    a.eps = eps;
+                    a.attn_scale = ssm_scale(c.head_dim);
+                    CK(l98k_attn(&a, k, I.pos0 + c0 + k, w->att, st));
+                }
+            }
+            CK(mf(L.o, w->xq2, w->xqs2, R, w->blk, d, st));
+        } else {
+            const int key = c.lin_key_dim, value = c.lin_value_dim, nv = c.lin_n_v_heads, kd = c.lin_k_head_dim;
+            const int rank = c.kda_gate_rank, hist = c.conv_kernel - 1;
+            CK(mf(L.kq, w->xq, w->xqs, R, w->pq, key, st));
+            CK(mf(L.kk, w->xq, w->xqs, R, w->pk, key, st));
+            CK(mf(L.kv, w->xq, w->xqs, R, w->pv, value, st));
+            CK(mf(L.fa, w->xq, w->xqs, R, w->pfa, rank, st));
+            CK(mf(L.kb, w->xq, w->xqs, R, w->pb, nv, st));
+            CK(mf(L.kg, w->xq, w->xqs, R, w->pg, value, st));
+            const int li = m->lin_index[l];
+            for (int it = 0; it < n_items; it++) {
+                const WideItem &I = items[it];
+                DState *s = I.d;
+                if (advance && I.n > MAX_CHUNK) return 1;       // one ring advance per verify chunk
+                for (int c0 = 0; c0 < I.n; c0 += MAX_CHUNK) {
+                    const int k = I.n - c0 < MAX_CHUNK ? I.n - c0 : MAX_CHUNK;
+                    const int r = I.row0 + c0;
+                    KdaStepArgs a{};
+                    a.pq = w->pq + (size_t)r * key; a.pk = w->pk + (size_t)r * key; a.pv = w->pv + (size_t)r * value;
+                    a.pfa = w->pfa + (size_t)r * rank;
+                    a.fb_q = L.fb.q; a.fb_s = L.fb.s;
+                    a.conv_w = L.conv;
+                    a.conv_ring = s->conv + (size_t)li * c.lin_conv_dim * hist;
+                    a.conv_slot_stride = s->conv_slot;
+                    a.bvec = w->pb + (size_t)r * nv; a.gz = w->pg + (size_t)r * value;
+                    a.a_log = L.a_log; a.dt_bias = L.dt_bias; a.o_norm = L.o_norm;
+                    a.state = s->kda + (size_t)li * nv * kd * c.lin_v_head_dim;
+                    a.slot_stride = s->kda_slot;
+                    a.ctl_slot = &s->ctl->slot_base;
+                    a.xq = w->xq2 + (size_t)r * value; a.xqs = w->xqs2 + (size_t)r * (value / 32);
+                    a.nv = nv; a.key = key; a.value = value; a.rank = rank;
+                    a.depth = s->depth; a.advance = advance ? 1 : 0; a.nt = k;
+                    a.scale = ssm_scale(kd); a.eps = eps;
+                    CK(l98k_kda_step(&a, kd, c.conv_kernel, st));
+                }
+            }
+            CK(mf(L.ko, w->xq2, w->xqs2, R, w->blk, d, st));
+        }
+        CK(l98k_rmsnorm(w->x, d, w->blk, nullptr, L.post_norm, d, eps, R, nullptr, 0, w->xq, w->xqs, st));
+        // latent MoE (src/forward_moe.c:220-553) with the shared expert
+        CK(mf(L.router, w->xq, w->xqs, R, w->rl, E, st));
+        CK(mf(L.down, w->xq, w->xqs, R, w->latx, lat, st));
+        CK(mf(L.sg, w->xq, w->xqs, R, w->sgo, sw, st));
+        CK(mf(L.su, w->xq, w->xqs, R, w->suo, sw, st));
+        const int pairs = R * topk;
+        CK(l98k_moe_route_wide(w->rl, L.bias, E, topk, R, w->sel_idx, w->sel_w, st));
+        CK(l98k_moe_group(w->sel_idx, pairs, topk, E, w->ng, w->gexp, w->goff, w->gcnt, w->list, w->pair_token, st));
+        CK(l98k_wide_pro(0, w->latx, nullptr, lat, nullptr, nullptr, 0, lat, R, w->latq, w->latqs, st));
+        const int maxg = pairs < E ? pairs : E;
+        CK(l98k_mfma_gemm_grouped(L.w1.q, L.w1.s, inter, lat, w->latq, w->latqs, w->ng, maxg, w->gexp, w->goff,
+                                  w->gcnt, w->list, w->pair_token, R, w->h1, inter, st));
+        CK(l98k_mfma_gemm_grouped(L.w3.q, L.w3.s, inter, lat, w->latq, w->latqs, w->ng, maxg, w->gexp, w->goff,
+                                  w->gcnt, w->list, w->pair_token, R, w->h3, inter, st));
+        CK(l98k_wide_pro(1, w->h1, w->h3, inter, nullptr, nullptr, 0, inter, pairs, w->hq, w->hqs, st));
+        CK(l98k_mfma_gemm_grouped(L.w2.q, L.w2.s, lat, inter, w->hq, w->hqs, w->ng, maxg, w->gexp, w->goff, w->gcnt,
+                                  w->list, nullptr, R, w->h2, lat, st));
+        CK(l98k_wide_pro(2, w->h2, nullptr, lat, w->sel_idx, w->sel_w, topk, lat, R, w->cq, w->cqs, st));
+        CK(mf(L.up, w->cq, w->cqs, R, w->up_out, d, st));
+        CK(l98k_wide_pro(1, w->sgo, w->suo, sw, nullptr, nullptr, 0, sw, R, w->shq, w->shqs, st));
+        CK(mf(L.sd, w->shq, w->shqs, R, w->sd_out, d, st));
+        ra = w->up_out;
+        rb = w->sd_out;
+    }
+    CK(l98k_rmsnorm(w->x, d, ra, rb, m->final_norm, d, eps, R, capture, d, logits ? w->xq : nullptr, w->xqs, st));
+    if (logits) CK(mf(m->embed, w->xq, w->xqs, R, logits, c.vocab_size, st));
+    return 0;
+}
+
 }  // namespace
 
 extern "C" int lz_state_alloc(LZRunState *s, const LZModel *mm, int seq_len, int spec_k_max,
@@ -1072,6 +1300,22 @@ int batch_capture_dev(DState *d, LZRunState *s, const int *tokens, int n, int po
     h.pos_scratch = pos0;
     CK(ctl_put(d, h));
     CK(hipMemcpyAsync(d->tokbuf, tokens, sizeof(int) * (size_t)n, hipMemcpyHostToDevice, d->st));
+    DWide *w = n >= WIDE_MIN ? wide_get(d->m) : nullptr;
+    if (w) {
+        // wide chunks of up to WIDE_MAX rows: each one's positions start at
+        // pos_scratch, which the chunk's own control write moves along
+        for (int done = 0; done < n;) {
+            const int k = n - done < w->cap ? n - done : w->cap;
+            h.pos_scratch = pos0 + done;
+            CK(ctl_put(d, h));
+            CK(hipMemcpyAsync(w->toks, d->tokbuf + done, sizeof(int) * (size_t)k, hipMemcpyDeviceToDevice, d->st));
+            const WideItem item{d, 0, k, pos0 + done};
+            CK(wide_forward(d->m, w, &item, 1, k, false, d->hcap + (size_t)done * c.hidden_size, nullptr, d->st));
+            done += k;
+            lz_debug_n_chunks++;
+        }
+        return 0;
+    }
     for (int done = 0; done < n;) {
         int k = n - done < MAX_CHUNK ? n - done : MAX_CHUNK;
         CK(forward_chunk(d, d->tokbuf + done, k, &d->ctl->pos_scratch, done, pos0 + done + k - 1,
@@ -1998,21 +2242,61 @@ extern "C" int l98_verify_batch(const LZModel *mm, LZRunState **states, int n_se
         if (!tok_ok(c, tokens + (size_t)i * n_tok, n_tok) || pos0[i] < 0 || pos0[i] + n_tok > d->seq_len) return 1;
         if (hipStreamSynchronize(d->st) != hipSuccess) return 1;
     }
-    const double t0 = now_ms();
-    for (int i = 0; i < n_seq; i++) {
-        LZRunState *s = states[i];
-        DState *d = S(s);
-        DevCtl h = ctl_from(s);
-        h.pos_scratch = pos0[i];
-        for (int j = 0; j < n_tok; j++) h.tok[j] = tokens[(size_t)i * n_tok + j];
-        if (ctl_put(d, h)) return 1;
-        if (forward_chunk(d, d->ctl->tok, n_tok, &d->ctl->pos_scratch, 0, pos0[i] + n_tok - 1, d->vhidden, true,
-                          d->mtp_logits, false))
-            return 1;
-        s->ssm_slot = (s->ssm_slot + n_tok) % d->depth;
+    const int R = n_seq * n_tok;
+    DWide *w = R <= WIDE_MAX ? wide_get(Mo(mm)) : nullptr;
+    if (w && w->logits_rows < R) {
+        if (w->logits) (void)hipFree(w->logits);
+        w->logits = nullptr;
+        w->logits_rows = 0;
+        if (hipMalloc((void **)&w->logits, sizeof(float) * (size_t)R * c.vocab_size) != hipSuccess) return 1;
+        w->logits_rows = R;
     }
-    for (int i = 0; i < n_seq; i++)
-        if (hipStreamSynchronize(S(states[i])->st) != hipSuccess) return 1;
+    if (!knobs_ok(c.num_experts_per_token, nullptr, 0)) return 1;
+    const double t0 = now_ms();
+    if (w) {
+        // every session's rows through one wide forward on the first
+        // session's stream: one launch per op over all R rows
+        hipStream_t st = S(states[0])->st;
+        std::vector<WideItem> items((size_t)n_seq);
+        std::vector<DevCtl> hs((size_t)n_seq);
+        for (int i = 0; i < n_seq; i++) {
+            DState *d = S(states[i]);
+            hs[i] = ctl_from(states[i]);
+            hs[i].pos_scratch = pos0[i];
+            if (hipMemcpyAsync(d->ctl, &hs[i], sizeof(DevCtl), hipMemcpyHostToDevice, st)) return 1;
+            items[i] = WideItem{d, i * n_tok, n_tok, pos0[i]};
+        }
+        if (hipMemcpyAsync(w->toks, tokens, sizeof(int) * (size_t)R, hipMemcpyHostToDevice, st) ||
+            wide_forward(Mo(mm), w, items.data(), n_seq, R, true, w->hcap, w->logits, st))
+            return 1;
+        for (int i = 0; i < n_seq; i++) {
+            DState *d = S(states[i]);
+            if (hipMemcpyAsync(d->mtp_logits, w->logits + (size_t)i * n_tok * c.vocab_size,
+                               sizeof(float) * (size_t)n_tok * c.vocab_size, hipMemcpyDeviceToDevice, st) ||
+                hipMemcpyAsync(d->vhidden, w->hcap + (size_t)i * n_tok * c.hidden_size,
+                               sizeof(float) * (size_t)n_tok * c.hidden_size, hipMemcpyDeviceToDevice, st))
+                return 1;
+            states[i]->ssm_slot = (states[i]->ssm_slot + n_tok) % d->depth;
+        }
+        if (hipStreamSynchronize(st) != hipSuccess) return 1;
+        lz_debug_n_chunks++;
+        lz_debug_n_lmhead++;
+    } else {
+        for (int i = 0; i < n_seq; i++) {
+            LZRunState *s = states[i];
+            DState *d = S(s);
+            DevCtl h = ctl_from(s);
+            h.pos_scratch = pos0[i];
+            for (int j = 0; j < n_tok; j++) h.tok[j] = tokens[(size_t)i * n_tok + j];
+            if (ctl_put(d, h)) return 1;
+            if (forward_chunk(d, d->ctl->tok, n_tok, &d->ctl->pos_scratch, 0, pos0[i] + n_tok - 1, d->vhidden, true,
+                              d->mtp_logits, false))
+                return 1;
+            s->ssm_slot = (s->ssm_slot + n_tok) % d->depth;
+        }
+        for (int i = 0; i < n_seq; i++)
+            if (hipStreamSynchronize(S(states[i])->st) != hipSuccess) return 1;
+    }
     if (wall_ms) *wall_ms = (float)(now_ms() - t0);
     if (copy_out) {
         for (int i = 0; i < n_seq; i++) {

@@ -432,3 +432,80 @@ extern "C" int l98k_moe_route(const float *logits, const float *bias, int E, int
     return (int)hipGetLastError();
 }
 
+
+// ------------------------------------------------------ wide routing ---
+// Routing of many token rows: block g routes rows [8 g, 8 g + 8) with the
+// in-block router above (lz_moe_route per token, src/ops_moe.c:12-163), so
+// every row's selection and weights are those of the chunked path.
+__global__ __launch_bounds__(GEMV_THREADS) void k_moe_route_wide(const float *__restrict__ logits,
+                                                                 const float *__restrict__ bias, int E, int topk,
+                                                                 int rows, int *__restrict__ sel_idx,
+                                                                 float *__restrict__ sel_w) {
+    __shared__ RouteLds rt;
+    __shared__ float tab[32];
+    const int r0 = blockIdx.x * MAX_CHUNK;
+    const int nt = imin(MAX_CHUNK, rows - r0);
+    (void)route_block(logits + (size_t)r0 * E, bias, E, topk, nt, rt, tab);
+    const int tid = threadIdx.x;
+    if (tid < nt * topk) {
+        sel_idx[(size_t)r0 * topk + tid] = rt.sel[tid];
+        sel_w[(size_t)r0 * topk + tid] = rt.w[tid];
+    }
+}
+
+// The rows' (token, slot) pairs grouped by expert, for the grouped GEMMs:
+// group g < *ng is expert gexp[g] (ascending) with gcnt[g] pairs at
+// list[goff[g] ..]; pair_token[p] = p / topk.  Pairs without an expert
+// (sel_idx < 0) join no group.  One block; the order of a group's pairs is
+// free (every pair's output is computed on its own).
+__global__ __launch_bounds__(1024) void k_moe_group(const int *__restrict__ sel_idx, int npairs, int topk, int E,
+                                                    int *__restrict__ ng, int *__restrict__ gexp,
+                                                    int *__restrict__ goff, int *__restrict__ gcnt,
+                                                    int *__restrict__ list, int *__restrict__ pair_token) {
+    __shared__ int cnt[MAX_EXPERTS], off[MAX_EXPERTS], gid[MAX_EXPERTS], cur[MAX_EXPERTS];
+    const int tid = threadIdx.x;
+    if (tid < MAX_EXPERTS) { cnt[tid] = 0; cur[tid] = 0; }
+    __syncthreads();
+    for (int p = tid; p < npairs; p += blockDim.x) {
+        pair_token[p] = p / topk;
+        const int e = sel_idx[p];
+        if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int o = 0, g = 0;
+        for (int e = 0; e < E; e++) {
+            off[e] = o;
+            gid[e] = cnt[e] ? g : -1;
+            if (cnt[e]) {
+                gexp[g] = e;
+                goff[g] = o;
+                gcnt[g] = cnt[e];
+                g++;
+            }
+            o += cnt[e];
+        }
+        *ng = g;
+    }
+    __syncthreads();
+    for (int p = tid; p < npairs; p += blockDim.x) {
+        const int e = sel_idx[p];
+        if (e >= 0 && e < E) list[off[e] + atomicAdd(&cur[e], 1)] = p;
+    }
+}
+
+extern "C" int l98k_moe_route_wide(const float *logits, const float *bias, int E, int topk, int rows, int *sel_idx,
+                                   float *sel_w, hipStream_t st) {
+    if (E < 1 || E > MAX_EXPERTS || topk < 1 || topk > MAX_TOPK || rows < 1) return -1;
+    hipLaunchKernelGGL(k_moe_route_wide, dim3((rows + MAX_CHUNK - 1) / MAX_CHUNK), dim3(GEMV_THREADS), 0, st, logits,
+                       bias, E, topk, rows, sel_idx, sel_w);
+    return (int)hipGetLastError();
+}
+
+extern "C" int l98k_moe_group(const int *sel_idx, int npairs, int topk, int E, int *ng, int *gexp, int *goff,
+                              int *gcnt, int *list, int *pair_token, hipStream_t st) {
+    if (npairs < 1 || E < 1 || E > MAX_EXPERTS || topk < 1) return -1;
+    hipLaunchKernelGGL(k_moe_group, dim3(1), dim3(1024), 0, st, sel_idx, npairs, topk, E, ng, gexp, goff, gcnt, list,
+                       pair_token);
+    return (int)hipGetLastError();
+}
