@@ -15,17 +15,24 @@ HIP graph launch per round).  W warmup rounds, then K timed rounds between
 device synchronizations; value = tokens emitted in the K rounds / wall time.
 
 The JSON line also carries:
-  roofline      the dominant kernel (the tied lm_head GEMV at M = k+1 rows)
-                timed with HIP events on its own stream, algorithmic bytes /
-                mean launch time against 8 TB/s (back to back, as the draft
-                steps of a round run it; cold_* after a cache-evicting copy);
-                traffic from the committed rocprofv3 byte-counter summary;
-  verify        the verify forward alone (M = k+1), algorithmic bytes / time;
+  roofline      the kernel with the largest share of the round's time: the
+                RMSNorm-prologue GEMV k_gemv_q8<M, PJ, norm> (the verify's
+                KDA, attention and MoE layer-input projections, one launch
+                each per layer).  Each of its three launch shapes is timed
+                with HIP events on the state's stream, every layer's launch
+                in order, back to back; achieved = algorithmic bytes /
+                duration summed over one round's launches; traffic from the
+                committed rocprofv3 byte-counter summary;
+  lm_head       the tied lm_head GEMV at M = k+1 (back to back, and cold);
+  verify        the verify forward alone (M = k+1), algorithmic bytes / time,
+                beside the reference's verify on the host;
   round         accepted tok/s against the round's HBM roofline
                 E[n_accept+1] * 8e12 / bytes_per_round (bytes counted from
                 the distinct experts and context each round actually used);
+  prefill       the prompt's prefill (512-row matrix-core chunks);
   cpu_baseline  the reference engine's own shipping build (AVX2 tier,
-                oracle/_ref/l98ref_ship) on one host core, same model.
+                oracle/_ref/l98ref_ship) on one host core, same model and
+                prompt, with its float-oracle build timed beside it.
 """
 import argparse
 import json
@@ -83,41 +90,69 @@ def round_bytes(cfg, k, ctx_verify, experts):
     return draft, verify
 
 
+def norm_gemv_shapes(cfg, M):
+    """The RMSNorm-prologue GEMV's launches in a verify of M rows: (name,
+    l98_time_kernel mode, launches per round, algorithmic bytes per launch).
+    Bytes: every weight row once (int8 + 4 B scale), the residual rows and
+    addends read once (4 B each), the folded residual written once, the
+    norm weight, and the outputs."""
+    d = cfg.hidden_size
+    def b(rows, addends):
+        return rows * (d + 4) + 4 * M * d * (1 + addends) + 4 * M * d + 4 * d + 4 * M * rows
+    kda_rows = 2 * cfg.lin_key_dim + 2 * cfg.lin_value_dim + cfg.kda_gate_rank + cfg.lin_n_v_heads
+    attn_rows = cfg.attn_qgate_dim + 2 * cfg.attn_kv_dim
+    moe_rows = cfg.num_experts + cfg.moe_latent_dim + 2 * cfg.moe_shared_width
+    return [("kda input", 4, cfg.n_linear_layers, b(kda_rows, 2)),
+            ("attention input", 5, cfg.n_full_layers, b(attn_rows, 2)),
+            ("moe input", 6, cfg.n_layers, b(moe_rows, 1))]
+
+
 def measured_traffic(config, k):
-    """HBM bytes per launch of the tied lm_head GEMV from the committed
-    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (copy-calibrated), for the
-    configs[1], k = 3 workload it was measured on; None otherwise."""
-    path = os.path.join(ROOT, "profiles", "lm_head_gemv_m4_traffic.md")
+    """HBM bytes per round of the RMSNorm-prologue GEMV launches (and per
+    lm_head launch) from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    summary (copy-calibrated), for the configs[1], k = 3 workload it was
+    measured on; None otherwise."""
+    path = os.path.join(ROOT, "profiles", "norm_gemv_and_lm_head_traffic_configs1_m4.md")
+    out = {}
     if config != 1 or k != 3 or not os.path.exists(path):
-        return None
+        return out
     for line in open(path):
-        if line.startswith("traffic_bytes_per_launch:"):
-            return int(line.split(":")[1])
-    return None
+        if ":" in line and line.split(":")[0] in ("norm_gemv_traffic_bytes_per_round", "lm_head_traffic_bytes_per_launch"):
+            out[line.split(":")[0]] = int(line.split(":")[1])
+    return out
 
 
-def cpu_baseline(model_dir, vocab, k):
-    """The reference engine's shipping build on one host core, bounded sample."""
+def cpu_baseline(model_dir, vocab, k, n_prompt):
+    """The reference engine on one host core each, on a bounded sample of
+    the benched workload (the same model and prompt; a few rounds): the
+    shipping build (the baseline) and the float-oracle build, run side by
+    side on two pinned cores.  Each times its prefill, its rounds and then
+    its verify forward of M = k+1 rows alone."""
     import __graft_entry__
     pkg = __graft_entry__.load_package()
-    binary = os.path.join(ROOT, "oracle", "_ref", "l98ref_ship")
-    if not os.path.exists(binary):
+    bins = {m: os.path.join(ROOT, "oracle", "_ref", f"l98ref_{m}") for m in ("ship", "oracle")}
+    if not all(os.path.exists(b) for b in bins.values()):
         return None
     tmp = tempfile.mkdtemp(prefix="l98cpu_")
     pf = os.path.join(tmp, "prompt.bin")
-    n_prompt, n_new = 64, 48
+    n_new = 12
     pkg.prompt_tokens(0, n_prompt, vocab).tofile(pf)
-    core = sorted(os.sched_getaffinity(0))[-1]
-    cmd = ["taskset", "-c", str(core), binary, "gen", model_dir, pf, str(k), str(n_new), "0", "1", "1",
-           os.path.join(tmp, "run"), "--timing"]
-    log("cpu baseline:", " ".join(cmd))
-    subprocess.run(cmd, check=True, timeout=300)
-    d = {}
-    for line in open(os.path.join(tmp, "run.txt")):
-        f = line.split()
-        d[f[0]] = f[1:]
-    n_tok = int(d["n_tokens"][0])
-    loop_s = float(d["loop_us"][0]) * 1e-6
+    cores = sorted(os.sched_getaffinity(0))
+    procs = {}
+    for i, (mode, binary) in enumerate(bins.items()):
+        cmd = ["taskset", "-c", str(cores[-1 - i]), binary, "gen", model_dir, pf, str(k), str(n_new), "0", "1", "1",
+               os.path.join(tmp, mode), "--timing", "--verify-iters", "3"]
+        log("cpu baseline:", " ".join(cmd))
+        procs[mode] = (subprocess.Popen(cmd), cores[-1 - i])
+    res = {}
+    for mode, (p, core) in procs.items():
+        if p.wait(timeout=600) != 0:
+            return None
+        d = {}
+        for line in open(os.path.join(tmp, mode + ".txt")):
+            f = line.split()
+            d[f[0]] = f[1:]
+        res[mode] = d
     cpu = "unknown"
     try:
         for line in open("/proc/cpuinfo"):
@@ -126,11 +161,20 @@ def cpu_baseline(model_dir, vocab, k):
                 break
     except OSError:
         pass
-    return {"value": round(n_tok / loop_s, 3), "unit": "tok/s", "cores": 1, "kind": "reference",
-            "sample": f"reference shipping build (lz_spec_round, tier {d['kernel'][0]}, gcc -O2 AVX2), "
-                      f"{n_prompt}-token prompt, {n_tok} tokens emitted in {len(d['k_eff'])} rounds, "
-                      f"k={k}, same model, 1 core of {os.cpu_count()} ({cpu})",
-            "round_ms": round(loop_s * 1e3 / max(1, len(d['k_eff'])), 3)}
+    def summary(d):
+        n_tok, loop_s = int(d["n_tokens"][0]), float(d["loop_us"][0]) * 1e-6
+        return {"tok_s": round(n_tok / loop_s, 3), "tokens": n_tok, "rounds": len(d["k_eff"]),
+                "round_ms": round(loop_s * 1e3 / max(1, len(d["k_eff"])), 3),
+                "prefill_s": round(float(d["prefill_us"][0]) * 1e-6, 2),
+                "verify_ms": round(float(d["verify_us_median"][0]) * 1e-3, 3), "tier": d["kernel"][0]}
+    ship, ora = summary(res["ship"]), summary(res["oracle"])
+    return {"value": ship["tok_s"], "unit": "tok/s", "cores": 1, "kind": "reference",
+            "sample": f"reference shipping build (lz_spec_round, tier {ship['tier']}, gcc -O2 AVX2) on 1 core of "
+                      f"{os.cpu_count()} ({cpu}): {n_prompt}-token prompt prefilled ({ship['prefill_s']} s), then "
+                      f"{ship['tokens']} tokens in {ship['rounds']} rounds at k={k} on the same model; its verify "
+                      f"forward of M={k + 1} rows alone: {ship['verify_ms']} ms",
+            "round_ms": ship["round_ms"], "verify_ms": ship["verify_ms"], "prefill_s": ship["prefill_s"],
+            "oracle_mode": ora}
 
 
 def bench_server(args, pkg):
@@ -214,9 +258,11 @@ def main():
         f"state {eng.s.bytes_device / 1e6:.1f} MB")
     k = args.k
     prompt = pkg.prompt_tokens(0, args.prompt, cfg.vocab_size)
-    t0 = time.time()
+    eng.session_start(prompt)                   # first use: the wide scratch and code load
+    t0 = time.perf_counter()
     eng.session_start(prompt)
-    log(f"prefill of {len(prompt)} tokens: {time.time() - t0:.2f}s")
+    prefill_s = time.perf_counter() - t0
+    log(f"prefill of {len(prompt)} tokens: {prefill_s:.3f}s")
     use_graph = not args.no_graph
     eng.greedy_rounds(k, args.warmup, use_graph)
     t0 = time.perf_counter()
@@ -237,8 +283,19 @@ def main():
         rb_v += vr
     mean_round = (rb_d + rb_v) / args.steps
     roof_toks = (n_tok / args.steps) * HBM_PEAK / mean_round
-    # dominant kernel: the tied lm_head GEMV at M = k+1 rows
+    # dominant kernel: the RMSNorm-prologue GEMV, its three launch shapes
     M = k + 1
+    shapes = norm_gemv_shapes(cfg, M)
+    ng_rows = []
+    for name, mode, count, nbytes in shapes:
+        t_ms = eng.time_kernel(mode, M, 10)
+        ng_rows.append({"launch": name, "per_round": count, "bytes": nbytes, "us": round(t_ms * 1e3, 3),
+                        "GB/s": round(nbytes / (t_ms * 1e-3) / 1e9, 1)})
+    ng_bytes = sum(r["bytes"] * r["per_round"] for r in ng_rows)
+    ng_s = sum(r["us"] * 1e-6 * r["per_round"] for r in ng_rows)
+    ng_bw = ng_bytes / ng_s
+    traffic = measured_traffic(args.config, k)
+    # the tied lm_head GEMV at M = k+1 rows
     lm_ms = eng.time_kernel(0, M, 50)
     lm_cold_ms = eng.time_kernel(3, M, 10)      # each launch after a cache-evicting copy
     V, d = cfg.vocab_size, cfg.hidden_size
@@ -249,7 +306,7 @@ def main():
     ctx_now = int(new_pos[-1])
     ver_bytes = round_bytes(cfg, k, ctx_now, int(experts.mean()))[1]
     ver_bw = ver_bytes / (ver_ms * 1e-3)
-    cpu = None if args.no_cpu else cpu_baseline(mdir, cfg.vocab_size, k)
+    cpu = None if args.no_cpu else cpu_baseline(mdir, cfg.vocab_size, k, len(prompt))
     out = {
         "metric": "accepted tok/s @bs1 k=3; verify-step HBM GB/s as % of MI355X peak",
         "value": round(value, 3),
@@ -267,14 +324,26 @@ def main():
                                f"E={cfg.num_experts} top{cfg.num_experts_per_token}; k={k} greedy bs1, "
                                f"{len(prompt)}-token prompt", "k": k, "batch": 1,
                    "graph": use_graph},
-        "roofline": {"bound": "hbm", "kernel": f"k_gemv_q8<{M}> (tied lm_head, {V}x{d} int8)",
-                     "achieved": round(lm_bw / 1e9, 1), "peak": 8000.0, "unit": "GB/s",
-                     "frac": round(lm_bw / HBM_PEAK, 4), "traffic": measured_traffic(args.config, k),
-                     "bytes_per_launch": lm_bytes, "launch_ms": round(lm_ms, 5),
-                     "cold_launch_ms": round(lm_cold_ms, 5),
-                     "cold_frac": round(lm_bytes / (lm_cold_ms * 1e-3) / HBM_PEAK, 4)},
+        "roofline": {"bound": "hbm",
+                     "kernel": f"k_gemv_q8<{M}, PJ, norm> (RMSNorm-prologue GEMV of the verify's layer inputs, "
+                               f"{sum(r['per_round'] for r in ng_rows)} launches per round)",
+                     "achieved": round(ng_bw / 1e9, 1), "peak": 8000.0, "unit": "GB/s",
+                     "frac": round(ng_bw / HBM_PEAK, 4),
+                     "traffic": traffic.get("norm_gemv_traffic_bytes_per_round"),
+                     "bytes_per_round": int(ng_bytes), "us_per_round": round(ng_s * 1e6, 1),
+                     "launches": ng_rows},
+        "lm_head": {"kernel": f"k_gemv_q8<{M}, 0, pre-quantized> (tied lm_head, {V}x{d} int8)",
+                    "bytes_per_launch": lm_bytes, "launch_ms": round(lm_ms, 5),
+                    "frac": round(lm_bw / HBM_PEAK, 4), "cold_launch_ms": round(lm_cold_ms, 5),
+                    "cold_frac": round(lm_bytes / (lm_cold_ms * 1e-3) / HBM_PEAK, 4),
+                    "traffic": traffic.get("lm_head_traffic_bytes_per_launch")},
         "verify": {"M": M, "ms": round(ver_ms, 4), "bytes": int(ver_bytes),
-                   "GB/s": round(ver_bw / 1e9, 1), "frac_of_peak": round(ver_bw / HBM_PEAK, 4)},
+                   "GB/s": round(ver_bw / 1e9, 1), "frac_of_peak": round(ver_bw / HBM_PEAK, 4),
+                   "cpu_reference_ms": cpu["verify_ms"] if cpu else None},
+        "prefill": {"tokens": len(prompt) - 1, "s": round(prefill_s, 4),
+                    "tok_s": round((len(prompt) - 1) / prefill_s, 1),
+                    "note": "lz_forward_batch_capture in 512-row matrix-core chunks + MTP prefill + first capture",
+                    "cpu_reference_s": cpu["prefill_s"] if cpu else None},
         "round": {"alpha": round(float(na.sum()) / (k * args.steps), 4),
                   "tokens_per_round": round(n_tok / args.steps, 4),
                   "bytes_per_round": int(mean_round),

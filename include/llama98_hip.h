@@ -256,8 +256,10 @@ int l98_greedy_rounds_batch(const LZModel *m, LZRunState **states, int n_seq, in
  * which = 0: the tied lm_head GEMV with mrows token rows, back to back;
  * 1: the verify forward of mrows tokens; 2: a device copy of the lm_head's
  * int8 bytes (calibration for byte counters); 3: the lm_head GEMV after a
- * cache-evicting 512 MiB copy each time (only the GEMV timed).  Returns 0
- * (1 on a bad argument or a device error). */
+ * cache-evicting 512 MiB copy each time (only the GEMV timed); 4, 5, 6: the
+ * RMSNorm-prologue GEMV of every KDA layer's, attention layer's and layer's
+ * MoE input projections in order, back to back (mean per launch).
+ * Returns 0 (1 on a bad argument or a device error). */
 int l98_time_kernel(const LZModel *m, LZRunState *s, int which, int mrows, int iters, float *avg_ms);
 /* For each of `rows` rows of n (<= 2048) non-negative floats (host
  * arrays), the float the serial loop s = 0; s += x[i] gives, computed on the

@@ -2452,30 +2452,66 @@ extern "C" int l98_generate(const LZModel *mm, LZRunState *s, const int *prompt,
 //   2  a device-to-device copy of the lm_head's vocab x hidden int8 bytes
 //      (the calibration kernel for the HBM byte counters);
 //   3  the lm_head GEMV as in 0, each launch after a 512 MiB copy that
-//      evicts the device's last-level cache (only the GEMV is timed).
+//      evicts the device's last-level cache (only the GEMV is timed);
+//   4  the RMSNorm-prologue GEMV of the KDA layers' inputs (q, k, v, f_a,
+//      b, g projections) over mrows rows, every KDA layer in order, back to
+//      back (the mean is per launch);
+//   5  the same for the attention layers' inputs (k, v, q);
+//   6  the same for every layer's MoE input (router, latent down, shared
+//      gate and up).  4-6 read the state's residual rows and write only
+//      scratch rows, so the session stays usable.
 extern "C" int l98_time_kernel(const LZModel *mm, LZRunState *s, int which, int mrows, int iters,
                                float *avg_ms) {
     if (!mm || !s || !s->impl || iters < 1 || mrows < 1 || mrows > MAX_CHUNK || !avg_ms) return 1;
     DState *d = S(s);
     const DModel *m = d->m;
     const LZModelConfig &c = m->c;
-    if (which < 0 || which > 3) return 1;
+    if (which < 0 || which > 6) return 1;
+    std::vector<int> layers;                    // the layers modes 4-6 run, in order
+    for (int l = 0; l < c.n_layers; l++)
+        if ((which == 4 && m->L[l].type == 2) || (which == 5 && m->L[l].type == 1) || which == 6) layers.push_back(l);
+    if (which >= 4 && layers.empty()) return 1;
+    const int per_iter = which >= 4 ? (int)layers.size() : 1;
     const size_t wbytes = (size_t)c.vocab_size * c.hidden_size;
     const size_t flush_bytes = (size_t)512 << 20;
+    const bool cold = which == 3;
     void *scratch = nullptr;
     if (which >= 2 && hipMalloc(&scratch, which == 2 ? wbytes : 2 * flush_bytes) != hipSuccess) return 1;
+    const int d_ = c.hidden_size;
+    const float eps = c.rms_norm_eps;
     auto once = [&]() -> int {
         if (which == 0 || which == 3)
             return gemv(d, {JX(m->embed, d->mtp_logits, c.vocab_size, d->xq, d->xqs)}, mrows);
         if (which == 2)
             return hipMemcpyAsync(scratch, m->embed.q, wbytes, hipMemcpyDeviceToDevice, d->st) != hipSuccess;
+        for (int l : layers) {
+            const DLayer &L = m->L[l];
+            int rc = 0;
+            if (which == 4) {
+                const Prologue P = PN(d->x, d_, d->up_out, d->sd_out, L.in_norm, eps, d->x2, nullptr, 0);
+                rc = gemv(d, {J(L.kq, d->pq, c.lin_key_dim, P), J(L.kk, d->pk, c.lin_key_dim, P),
+                              J(L.kv, d->pv, c.lin_value_dim, P), J(L.fa, d->pfa, c.kda_gate_rank, P),
+                              J(L.kb, d->pb, c.lin_n_v_heads, P), J(L.kg, d->pg, c.lin_value_dim, P)}, mrows);
+            } else if (which == 5) {
+                const Prologue P = PN(d->x, d_, d->up_out, d->sd_out, L.in_norm, eps, d->x2, nullptr, 0);
+                rc = gemv(d, {J(L.k, d->kp, c.attn_kv_dim, P), J(L.v, d->vp, c.attn_kv_dim, P),
+                              J(L.q, d->qg, c.attn_qgate_dim, P)}, mrows);
+            } else {
+                const Prologue P = PN(d->x, d_, d->blk, nullptr, L.post_norm, eps, d->x2, nullptr, 0);
+                rc = gemv(d, {J(L.router, d->rl, c.num_experts, P), J(L.down, d->latx, c.moe_latent_dim, P),
+                              J(L.sg, d->sgo, c.moe_shared_width, P), J(L.su, d->suo, c.moe_shared_width, P)},
+                          mrows);
+            }
+            if (rc) return rc;
+        }
+        if (which >= 4) return 0;
         return forward_chunk(d, d->ctl->tok, mrows, &d->ctl->anchor_pos, 1, d->seq_len - 1, d->vhidden, true,
                              d->mtp_logits, false);
     };
     int rc = 0;
     float ms = 0.0f;
     if (once()) rc = 1;
-    if (!rc && which != 3) {
+    if (!rc && !cold) {
         (void)hipEventRecord(d->ev0, d->st);
         for (int i = 0; i < iters && !rc; i++) rc = once();
         (void)hipEventRecord(d->ev1, d->st);
@@ -2496,6 +2532,6 @@ extern "C" int l98_time_kernel(const LZModel *mm, LZRunState *s, int which, int 
     }
     if (scratch) (void)hipFree(scratch);
     if (rc) return 1;
-    *avg_ms = ms / (float)iters;
+    *avg_ms = ms / (float)iters / (float)per_iter;
     return 0;
 }

@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Per-kernel mean of a rocprofv3 --pmc counter (FETCH_SIZE / WRITE_SIZE,
-KiB per dispatch), for the lm_head GEMV and the calibration copy that
-llama98-zh_amd/profile_lmhead.py dispatches.
+KiB per dispatch), per kernel name and grid, for the kernels and the
+calibration copy that llama98-zh_amd/profile_kernels.py dispatches.
 
     python3 llama98-zh_amd/pmcsum.py OUT/pmc_counter_collection.csv [--vocab 65536 --hidden 1024]
 """

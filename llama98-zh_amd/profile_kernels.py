@@ -1,0 +1,49 @@
+#!/usr/bin/env python3
+"""Dispatches for the HBM byte counters of the round's kernels.
+
+On the configs[1] model after a short prefill, runs `--iters` launches each
+of (l98_time_kernel modes):
+  0  the tied lm_head GEMV at M = k+1 = 4 token rows (back to back);
+  4  the RMSNorm-prologue GEMV of every KDA layer's input projections;
+  5  the same for the attention layers' inputs;
+  6  the same for every layer's MoE input (4-6 back to back, in layer
+     order);
+  2  a device copy of the lm_head's vocab x hidden int8 bytes, the
+     calibration kernel (its FETCH_SIZE and WRITE_SIZE per dispatch stand
+     for a known byte count).
+Meant to run under
+
+    rocprofv3 --pmc FETCH_SIZE --output-format csv -d OUT -o pmc -- python3 llama98-zh_amd/profile_kernels.py
+    rocprofv3 --pmc WRITE_SIZE --output-format csv -d OUT -o pmc -- python3 llama98-zh_amd/profile_kernels.py
+
+and summarized by llama98-zh_amd/pmcsum.py.
+"""
+import argparse
+import os
+import sys
+import tempfile
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, ROOT)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--iters", type=int, default=20)
+    ap.add_argument("--model-dir", default=os.path.join(tempfile.gettempdir(), "l98_models"))
+    args = ap.parse_args()
+    import __graft_entry__
+    pkg = __graft_entry__.load_package()
+    mdir = os.path.join(args.model_dir, "base")
+    pkg.ensure_model(mdir, 1, seed=1234)
+    eng = pkg.Engine(mdir)
+    eng.session_start(pkg.prompt_tokens(0, 32, eng.V))
+    for which, name in ((0, "lm_head"), (4, "kda input"), (5, "attention input"), (6, "moe input"), (2, "copy")):
+        ms = eng.time_kernel(which, 4, args.iters)
+        print(f"mode {which} ({name}, M=4): {ms * 1e3:.2f} us/launch", flush=True)
+    print(f"copy bytes {eng.V * eng.d}", flush=True)
+    eng.close()
+
+
+if __name__ == "__main__":
+    main()

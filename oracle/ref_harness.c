@@ -14,6 +14,9 @@
  *       opts: --dump-rounds N   write logits/hidden of the first N rounds
  *             --break-rollback  --skip-catchup  --pmin P  --nmin N
  *             --timing          per-round wall times
+ *             --verify-iters N  after the run, time N lz_forward_verify
+ *                               calls of M = K+1 tokens at the final
+ *                               position (ring slot restored between calls)
  *   l98ref_* verify MODEL_DIR PROMPT_FILE K ITERS OUT_PREFIX
  *       times lz_forward_verify of M=K+1 tokens in isolation (the ring slot
  *       is restored between calls, so every call reads the same state)
@@ -152,13 +155,19 @@ static void dump_state(const char *prefix, const LZModel *m, const LZRunState *s
     dump(prefix, "rope_cs", s->rope_cs, sizeof(float) * (size_t)s->seq_len * c->rotary_dim);
 }
 
+static int cmp_d(const void *a, const void *b) {
+    double x = *(const double *)a, y = *(const double *)b;
+    return x < y ? -1 : x > y;
+}
+
 static int cmd_gen(int argc, char **argv) {
     const char *dir = argv[2], *pf = argv[3];
     int k = atoi(argv[4]), n_new = atoi(argv[5]);
     float temp = (float)atof(argv[6]), topp = (float)atof(argv[7]);
     unsigned long long seed = strtoull(argv[8], NULL, 10);
     const char *prefix = argv[9];
-    int dump_rounds = 0, brk = 0, skipc = 0, n_min = 0, timing = 0;
+    int dump_rounds = 0, brk = 0, skipc = 0, n_min = 0, timing = 0, verify_iters = 0;
+    double verify_med = 0.0, verify_min = 0.0;
     float p_min = 0.0f;
     int i, n_prompt, rc;
     char err[512];
@@ -181,6 +190,7 @@ static int cmd_gen(int argc, char **argv) {
         else if (!strcmp(argv[i], "--pmin") && i + 1 < argc) p_min = (float)atof(argv[++i]);
         else if (!strcmp(argv[i], "--nmin") && i + 1 < argc) n_min = atoi(argv[++i]);
         else if (!strcmp(argv[i], "--timing")) timing = 1;
+        else if (!strcmp(argv[i], "--verify-iters") && i + 1 < argc) verify_iters = atoi(argv[++i]);
     }
     select_mode();
     prompt = read_prompt(pf, &n_prompt);
@@ -266,6 +276,24 @@ static int cmd_gen(int argc, char **argv) {
     }
     t_loop = now_us() - t_loop0;
     dump_state(prefix, &m, &s, pos);
+    if (verify_iters > 0 && pos + k + 1 < s.seq_len) {
+        /* the verify forward alone at the run's final position: the same
+           M = k+1 tokens each time, from the same ring slot */
+        int vt[LZ_SPEC_K_MAX + 1], base_slot = s.ssm_slot;
+        double *tv = (double *)malloc(sizeof(double) * (size_t)verify_iters);
+        for (i = 0; i <= k; i++) vt[i] = toks[(n_tok - 1 - i + n_tok) % n_tok];
+        for (i = 0; i < verify_iters; i++) {
+            double t0 = now_us();
+            s.ssm_slot = base_slot;
+            if (lz_forward_verify(&m, &s, vt, k + 1, pos) != 0) { fprintf(stderr, "verify failed\n"); return 3; }
+            tv[i] = now_us() - t0;
+        }
+        s.ssm_slot = base_slot;
+        qsort(tv, (size_t)verify_iters, sizeof(double), cmp_d);
+        verify_med = tv[verify_iters / 2];
+        verify_min = tv[0];
+        free(tv);
+    }
 
     snprintf(path, sizeof path, "%s.txt", prefix);
     out = fopen(path, "w");
@@ -276,6 +304,7 @@ static int cmd_gen(int argc, char **argv) {
     fprintf(out, "final_pos %d\nmtp_pos %d\nssm_slot %d\nrng %llu\n", pos, s.mtp_pos, s.ssm_slot,
             (unsigned long long)samp.rng_state);
     fprintf(out, "prefill_us %.1f\nloop_us %.1f\n", t_prefill, t_loop);
+    if (verify_iters > 0) fprintf(out, "verify_M %d\nverify_us_median %.1f\nverify_us_min %.1f\n", k + 1, verify_med, verify_min);
     fprintf(out, "tokens");
     for (i = 0; i < n_tok; i++) fprintf(out, " %d", toks[i]);
     fprintf(out, "\nk_eff");
@@ -295,11 +324,6 @@ static int cmd_gen(int argc, char **argv) {
     lz_free(&m);
     free(prompt); free(toks); free(rk); free(ra); free(rt);
     return rc;
-}
-
-static int cmp_d(const void *a, const void *b) {
-    double x = *(const double *)a, y = *(const double *)b;
-    return x < y ? -1 : x > y;
 }
 
 static int cmd_verify(int argc, char **argv) {
