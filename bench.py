@@ -224,6 +224,39 @@ def bench_server(args, pkg):
     eng.close()
 
 
+def bench_ksweep(args, pkg):
+    """the configs[0] model at temperature 0.8, top-p 0.95, a
+    fixed sampler seed, draft widths k in {1, 2, 4, 7} (k = 7 through the
+    library's own generation loop: the reference caps k at 6); per k the
+    generation's tok/s and acceptance, and the verify forward of M = k+1
+    rows timed alone.  Prints one JSON line."""
+    import numpy as np
+    mdir = os.path.join(args.model_dir, "tiny")
+    pkg.ensure_model(mdir, 0, seed=1234)
+    eng = pkg.Engine(mdir, spec_k_max=pkg.L98_SPEC_K_GPU)
+    prompt = pkg.prompt_tokens(0, 64, eng.V)
+    rows = []
+    for k in (1, 2, 4, 7):
+        eng.generate(prompt, k, 16, 0.8, 0.95, 7)                 # warm
+        t0 = time.perf_counter()
+        toks, ke, na = eng.generate(prompt, k, 128, 0.8, 0.95, 7)
+        wall = time.perf_counter() - t0
+        ver_ms = eng.time_kernel(1, k + 1, 20)
+        rows.append({"k": k, "M": k + 1, "tokens": int(len(toks)), "rounds": int(len(na)),
+                     "alpha": round(float(np.clip(na, 0, None).sum()) / max(1, int(np.sum(ke))), 4),
+                     "tok_s": round(len(toks) / wall, 1), "verify_ms": round(ver_ms, 4)})
+    out = {"metric": "temperature spec decode tok/s and verify ms per draft width (configs[2])",
+           "value": rows[-1]["tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": 128, "warmup": 16,
+           "ms_per_step": rows[-1]["verify_ms"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+           "dtype": "int8xint8->int32, fp32 epilogue/state",
+           "data": "synthetic (seeded random-init weights; 64-token random prompt; sampler seed 7)",
+           "config": {"workload": "configs[2]: configs[0] model, T=0.8 top-p 0.95, k in {1,2,4,7}, "
+                                  "generation of 128 tokens per k (prefill included), verify timed alone"},
+           "sweep": rows}
+    print(json.dumps(out))
+    eng.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -247,12 +280,15 @@ def main():
     if args.config == 4:
         bench_server(args, pkg)
         return
+    if args.config == 2:
+        bench_ksweep(args, pkg)
+        return
     name = {0: "tiny", 1: "base", 3: "large"}.get(args.config, f"c{args.config}")
     mdir = os.path.join(args.model_dir, name)
     t0 = time.time()
     pkg.ensure_model(mdir, args.config, seed=1234)
     log(f"model {mdir} ready in {time.time() - t0:.1f}s")
-    eng = pkg.Engine(mdir)
+    eng = pkg.Engine(mdir, spec_k_max=pkg.L98_SPEC_K_GPU)    # ring depth 8: the sweep's M = 8 verify
     cfg = eng.cfg
     log(f"device {pkg.hip_lib().l98_device_name().decode()}; weights {eng.m.bytes_device / 1e9:.3f} GB, "
         f"state {eng.s.bytes_device / 1e6:.1f} MB")
@@ -306,6 +342,12 @@ def main():
     ctx_now = int(new_pos[-1])
     ver_bytes = round_bytes(cfg, k, ctx_now, int(experts.mean()))[1]
     ver_bw = ver_bytes / (ver_ms * 1e-3)
+    # configs[2]'s verify widths on this model: M = k+1 rows timed alone
+    sweep = []
+    for ks in (1, 2, 4, 7):
+        t_ms = eng.time_kernel(1, ks + 1, 10)
+        vb = round_bytes(cfg, ks, ctx_now, int(experts.mean()))[1]
+        sweep.append({"k": ks, "M": ks + 1, "ms": round(t_ms, 4), "GB/s": round(vb / (t_ms * 1e-3) / 1e9, 1)})
     cpu = None if args.no_cpu else cpu_baseline(mdir, cfg.vocab_size, k, len(prompt))
     out = {
         "metric": "accepted tok/s @bs1 k=3; verify-step HBM GB/s as % of MI355X peak",
@@ -339,7 +381,7 @@ def main():
                     "traffic": traffic.get("lm_head_traffic_bytes_per_launch")},
         "verify": {"M": M, "ms": round(ver_ms, 4), "bytes": int(ver_bytes),
                    "GB/s": round(ver_bw / 1e9, 1), "frac_of_peak": round(ver_bw / HBM_PEAK, 4),
-                   "cpu_reference_ms": cpu["verify_ms"] if cpu else None},
+                   "cpu_reference_ms": cpu["verify_ms"] if cpu else None, "sweep": sweep},
         "prefill": {"tokens": len(prompt) - 1, "s": round(prefill_s, 4),
                     "tok_s": round((len(prompt) - 1) / prefill_s, 1),
                     "note": "lz_forward_batch_capture in 512-row matrix-core chunks + MTP prefill + first capture",

@@ -159,4 +159,21 @@ typedef struct {
     float eps, attn_scale;
 } AttnArgs;
 
+// One session's rows of a many-session attention launch (l98k_attn_items).
+typedef struct {
+    int8_t *kq, *vq;                    // the session's KV planes, plane 0 base [planes][seq][kv_dim]
+    float *ks, *vs;                     // their scales [planes][seq][kv_dim/32]
+    const int *ctl_pos;                 // position of the item's first row
+    int row0, n, seq_len, pad;
+} AttnItem;
+
+// One session's rows of a many-session KDA launch (l98k_kda_items).
+typedef struct {
+    float *state;                       // the session's KDA ring, layer 0 head block of slot 0
+    float *conv_ring;                   // its conv history ring, layer 0 of slot 0
+    const int *ctl_slot;                // ring slot base
+    size_t slot_stride, conv_slot_stride;
+    int row0, n, depth, pad;
+} KdaItem;
+
 #endif

@@ -958,6 +958,10 @@ struct DWide {
     float *att;
     float *logits = nullptr;  // rows x vocab, sized on demand
     int logits_rows = 0;
+    KdaItem *kitems;          // per-session tables of the item launches [WIDE_MAX]
+    AttnItem *aitems;
+    float *att_items = nullptr;   // attention scratch of an item launch, sized on demand
+    size_t att_items_floats = 0;
 };
 
 namespace {
@@ -993,6 +997,7 @@ DWide *wide_get(const DModel *cm) {
                  oh2 = take(4 * pairs * c.moe_latent_dim), osi = take(4 * pairs), osw = take(4 * pairs),
                  ong = take(4), oge = take(4 * MAX_EXPERTS), ogo = take(4 * MAX_EXPERTS), ogc = take(4 * MAX_EXPERTS),
                  oli = take(4 * pairs), opt = take(4 * pairs), otk = take(4 * R),
+                 oki = take(sizeof(KdaItem) * R), oai = take(sizeof(AttnItem) * R),
                  oat = take(4 * (size_t)MAX_CHUNK * c.n_heads * (size_t)((c.seq_len + 3) & ~3));
     if (hipMalloc((void **)&w->arena, off) != hipSuccess) { delete w; return nullptr; }
     char *a = w->arena;
@@ -1011,6 +1016,8 @@ DWide *wide_get(const DModel *cm) {
     w->ng = (int *)(a + ong); w->gexp = (int *)(a + oge); w->goff = (int *)(a + ogo); w->gcnt = (int *)(a + ogc);
     w->list = (int *)(a + oli); w->pair_token = (int *)(a + opt); w->toks = (int *)(a + otk);
     w->att = (float *)(a + oat);
+    w->kitems = (KdaItem *)(a + oki);
+    w->aitems = (AttnItem *)(a + oai);
     m->wide = w;
     return w;
 }
@@ -1019,6 +1026,7 @@ void wide_free(DModel *m) {
     if (!m->wide) return;
     if (m->wide->arena) (void)hipFree(m->wide->arena);
     if (m->wide->logits) (void)hipFree(m->wide->logits);
+    if (m->wide->att_items) (void)hipFree(m->wide->att_items);
     delete m->wide;
     m->wide = nullptr;
 }
@@ -1040,7 +1048,34 @@ int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, 
     const int d = c.hidden_size, E = c.num_experts, topk = c.num_experts_per_token;
     const int lat = c.moe_latent_dim, inter = c.moe_intermediate_size, sw = c.moe_shared_width;
     const float eps = c.rms_norm_eps;
-    if (R < 1 || R > w->cap) return 1;
+    if (R < 1 || R > w->cap || n_items < 1 || n_items > w->cap) return 1;
+    // the sessions' tables for the item launches
+    bool attn_items = n_items > 1;
+    int max_len = 1;
+    {
+        std::vector<KdaItem> ki((size_t)n_items);
+        std::vector<AttnItem> ai((size_t)n_items);
+        for (int i = 0; i < n_items; i++) {
+            const WideItem &I = items[i];
+            DState *s = I.d;
+            if (advance && I.n > MAX_CHUNK) return 1;       // one ring advance per verify chunk
+            attn_items = attn_items && I.n <= MAX_CHUNK;
+            max_len = I.pos0 + I.n > max_len ? I.pos0 + I.n : max_len;
+            ki[i] = KdaItem{s->kda, s->conv, &s->ctl->slot_base, s->kda_slot, s->conv_slot, I.row0, I.n, s->depth, 0};
+            ai[i] = AttnItem{s->kq, s->vq, s->ks, s->vs, &s->ctl->pos_scratch, I.row0, I.n, s->seq_len, 0};
+        }
+        CK(hipMemcpyAsync(w->kitems, ki.data(), sizeof(KdaItem) * ki.size(), hipMemcpyHostToDevice, st));
+        CK(hipMemcpyAsync(w->aitems, ai.data(), sizeof(AttnItem) * ai.size(), hipMemcpyHostToDevice, st));
+    }
+    const size_t att_item = (size_t)MAX_CHUNK * c.n_heads * (size_t)((max_len + 3) & ~3);
+    if (attn_items && w->att_items_floats < att_item * n_items) {
+        CK(hipStreamSynchronize(st));
+        if (w->att_items) (void)hipFree(w->att_items);
+        w->att_items = nullptr;
+        w->att_items_floats = 0;
+        CK(hipMalloc((void **)&w->att_items, sizeof(float) * att_item * n_items));
+        w->att_items_floats = att_item * n_items;
+    }
     CK(l98k_embed(m->embed.q, m->embed.s, w->toks, d, R, w->x, st));
     const float *ra = nullptr, *rb = nullptr;
     for (int l = 0; l < c.n_layers; l++) {
@@ -1052,7 +1087,22 @@ int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, 
             CK(mf(L.k, w->xq, w->xqs, R, w->kp, kvd, st));
             CK(mf(L.v, w->xq, w->xqs, R, w->vp, kvd, st));
             const int plane = m->full_index[l];
-            for (int it = 0; it < n_items; it++) {
+            if (attn_items) {
+                // every session's rows in one launch per kernel
+                AttnArgs a{};
+                a.qg = w->qg; a.kp = w->kp; a.vp = w->vp;
+                a.q_norm = L.q_norm; a.k_norm = L.k_norm; a.rope_cs = m->rope_cs;
+                a.qh = w->qh;
+                a.out = nullptr;
+                a.oq = w->xq2; a.oqs = w->xqs2;
+                a.nh = c.n_heads; a.nkv = c.n_kv_heads; a.hd = c.head_dim; a.rot = c.rotary_dim;
+                a.q_dim = qd; a.qg_dim = qgd; a.kv_dim = kvd;
+                a.kv_only = 0;
+                a.eps = eps;
+                a.attn_scale = ssm_scale(c.head_dim);
+                CK(l98k_attn_items(&a, w->aitems, n_items, plane, max_len, w->att_items, att_item, st));
+            }
+            for (int it = 0; it < n_items && !attn_items; it++) {
                 const WideItem &I = items[it];
                 DState *s = I.d;
                 for (int c0 = 0; c0 < I.n; c0 += MAX_CHUNK) {
@@ -1087,32 +1137,20 @@ int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, 
             CK(mf(L.kb, w->xq, w->xqs, R, w->pb, nv, st));
             CK(mf(L.kg, w->xq, w->xqs, R, w->pg, value, st));
             const int li = m->lin_index[l];
-            for (int it = 0; it < n_items; it++) {
-                const WideItem &I = items[it];
-                DState *s = I.d;
-                if (advance && I.n > MAX_CHUNK) return 1;       // one ring advance per verify chunk
-                for (int c0 = 0; c0 < I.n; c0 += MAX_CHUNK) {
-                    const int k = I.n - c0 < MAX_CHUNK ? I.n - c0 : MAX_CHUNK;
-                    const int r = I.row0 + c0;
-                    KdaStepArgs a{};
-                    a.pq = w->pq + (size_t)r * key; a.pk = w->pk + (size_t)r * key; a.pv = w->pv + (size_t)r * value;
-                    a.pfa = w->pfa + (size_t)r * rank;
-                    a.fb_q = L.fb.q; a.fb_s = L.fb.s;
-                    a.conv_w = L.conv;
-                    a.conv_ring = s->conv + (size_t)li * c.lin_conv_dim * hist;
-                    a.conv_slot_stride = s->conv_slot;
-                    a.bvec = w->pb + (size_t)r * nv; a.gz = w->pg + (size_t)r * value;
-                    a.a_log = L.a_log; a.dt_bias = L.dt_bias; a.o_norm = L.o_norm;
-                    a.state = s->kda + (size_t)li * nv * kd * c.lin_v_head_dim;
-                    a.slot_stride = s->kda_slot;
-                    a.ctl_slot = &s->ctl->slot_base;
-                    a.xq = w->xq2 + (size_t)r * value; a.xqs = w->xqs2 + (size_t)r * (value / 32);
-                    a.nv = nv; a.key = key; a.value = value; a.rank = rank;
-                    a.depth = s->depth; a.advance = advance ? 1 : 0; a.nt = k;
-                    a.scale = ssm_scale(kd); a.eps = eps;
-                    CK(l98k_kda_step(&a, kd, c.conv_kernel, st));
-                }
-            }
+            // every session's rows in one launch (a prefill's rows in
+            // sub-chunks inside its blocks)
+            KdaStepArgs a{};
+            a.pq = w->pq; a.pk = w->pk; a.pv = w->pv; a.pfa = w->pfa;
+            a.fb_q = L.fb.q; a.fb_s = L.fb.s;
+            a.conv_w = L.conv;
+            a.bvec = w->pb; a.gz = w->pg;
+            a.a_log = L.a_log; a.dt_bias = L.dt_bias; a.o_norm = L.o_norm;
+            a.xq = w->xq2; a.xqs = w->xqs2;
+            a.nv = nv; a.key = key; a.value = value; a.rank = rank;
+            a.advance = advance ? 1 : 0;
+            a.scale = ssm_scale(kd); a.eps = eps;
+            CK(l98k_kda_items(&a, w->kitems, n_items, (size_t)li * nv * kd * c.lin_v_head_dim,
+                              (size_t)li * c.lin_conv_dim * hist, kd, c.conv_kernel, st));
             CK(mf(L.ko, w->xq2, w->xqs2, R, w->blk, d, st));
         }
         CK(l98k_rmsnorm(w->x, d, w->blk, nullptr, L.post_norm, d, eps, R, nullptr, 0, w->xq, w->xqs, st));

@@ -100,13 +100,13 @@ __global__ __launch_bounds__(64) void k_attn_prep(AttnArgs a) {
 #define ATT_MAX_HD 128
 #define ATT_MAX_VEC 24                  // kv_mul q heads + up to MAX_CHUNK new K rows
 
-__global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a, float *__restrict__ att, int att_stride) {
+__device__ __forceinline__ void attn_scores_body(const AttnArgs &a, float *__restrict__ att, int att_stride, int slice,
+                                                 int kvh, int t) {
     __shared__ __align__(16) float s_x[ATT_MAX_VEC * ATT_MAX_HD];     // vectors being prepared
     __shared__ __align__(16) float s_sq[ATT_MAX_VEC * (ATT_MAX_HD + 4)];
     __shared__ float s_inv[ATT_MAX_VEC];
     __shared__ __align__(16) int8_t s_k[ATT_SLICE * (ATT_MAX_HD + 16)];   // K rows, padded
     __shared__ float s_ks[ATT_SLICE * (ATT_MAX_HD / 32)];
-    const int slice = blockIdx.x, kvh = blockIdx.y, t = blockIdx.z;
     const int tid = threadIdx.x;
     const int hd = a.hd, half = a.rot >> 1, kv_mul = a.nh / a.nkv, nb = hd >> 5;
     const int kstride = hd + 16;
@@ -219,6 +219,43 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a, float *__restri
     }
 }
 
+__global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a, float *__restrict__ att, int att_stride) {
+    attn_scores_body(a, att, att_stride, blockIdx.x, blockIdx.y, blockIdx.z);
+}
+
+// One launch over several sessions' rows (the session batch's verify):
+// item i is a session's rows [row0, row0 + n) (n <= MAX_CHUNK) against its
+// own KV plane, positions *ctl_pos + t; the launch's AttnArgs carry the
+// layer's weights and the row buffers at row 0.  Block z = (item, token).
+__device__ __forceinline__ AttnArgs attn_item_args(const AttnArgs &b, const AttnItem &it, int plane) {
+    AttnArgs a = b;
+    const size_t off = (size_t)plane * it.seq_len * b.kv_dim;
+    a.qg = b.qg + (size_t)it.row0 * b.qg_dim;
+    a.kp = b.kp + (size_t)it.row0 * b.kv_dim;
+    a.vp = b.vp + (size_t)it.row0 * b.kv_dim;
+    a.qh = b.qh + (size_t)it.row0 * b.q_dim;
+    a.kcache = it.kq + off;
+    a.vcache = it.vq + off;
+    a.kscale = it.ks + off / 32;
+    a.vscale = it.vs + off / 32;
+    a.out = b.out ? b.out + (size_t)it.row0 * b.q_dim : nullptr;
+    a.oq = b.oq + (size_t)it.row0 * b.q_dim;
+    a.oqs = b.oqs + (size_t)it.row0 * (b.q_dim >> 5);
+    a.ctl_pos = it.ctl_pos;
+    a.pos_off = 0;
+    return a;
+}
+
+__global__ __launch_bounds__(256) void k_attn_scores_items(AttnArgs b, const AttnItem *__restrict__ items, int plane,
+                                                           float *__restrict__ att, int att_stride,
+                                                           size_t att_item) {
+    const int item = blockIdx.z / MAX_CHUNK, t = blockIdx.z - item * MAX_CHUNK;
+    const AttnItem it = items[item];
+    if (t >= it.n) return;
+    const AttnArgs a = attn_item_args(b, it, plane);
+    attn_scores_body(a, att + (size_t)item * att_item, att_stride, blockIdx.x, blockIdx.y, t);
+}
+
 // k_attn_av: one block of 8 waves per (q head, token).  Softmax over the
 // token's scores (max, exp, the serial loop's sum - taken by the exact wave
 // sum up to 2048 positions -, scale), then the value sum
@@ -322,14 +359,13 @@ __device__ __forceinline__ void av_stage_any(const int8_t *__restrict__ vc, cons
 }
 
 template <int CH>
-__global__ __launch_bounds__(AV_THREADS) void k_attn_av(AttnArgs a, const float *__restrict__ att, int att_stride,
-                                                 int sc) {
+__device__ __forceinline__ void attn_av_body(const AttnArgs &a, const float *__restrict__ att, int att_stride, int sc,
+                                             int h, int t) {
     EXP_TAB_LOAD(tab);
     extern __shared__ __align__(16) char smem[];
     __shared__ uint32_t s_red[AV_THREADS / 64];
     __shared__ float s_inv;
     __shared__ PsRec s_rec[128];
-    const int h = blockIdx.x, t = blockIdx.y;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int hd = a.hd, nb = hd >> 5, kv_mul = a.nh / a.nkv, kvh = h / kv_mul;
     const int pos_t = *a.ctl_pos + a.pos_off + t, L = pos_t + 1;
@@ -453,6 +489,23 @@ __global__ __launch_bounds__(AV_THREADS) void k_attn_av(AttnArgs a, const float 
     }
 }
 
+template <int CH>
+__global__ __launch_bounds__(AV_THREADS) void k_attn_av(AttnArgs a, const float *__restrict__ att, int att_stride,
+                                                 int sc) {
+    attn_av_body<CH>(a, att, att_stride, sc, blockIdx.x, blockIdx.y);
+}
+
+template <int CH>
+__global__ __launch_bounds__(AV_THREADS) void k_attn_av_items(AttnArgs b, const AttnItem *__restrict__ items,
+                                                       int plane, const float *__restrict__ att, int att_stride,
+                                                       size_t att_item, int sc) {
+    const int item = blockIdx.y / MAX_CHUNK, t = blockIdx.y - item * MAX_CHUNK;
+    const AttnItem it = items[item];
+    if (t >= it.n) return;
+    const AttnArgs a = attn_item_args(b, it, plane);
+    attn_av_body<CH>(a, att + (size_t)item * att_item, att_stride, sc, blockIdx.x, t);
+}
+
 // ---------------------------------------------------------- host glue ---
 
 extern "C" int l98k_upload_exp_table_attn(const float *tab) {
@@ -476,6 +529,72 @@ static int lds_limit() {
         lim = v;
     }
     return lim;
+}
+
+// The value-sum launch's LDS plan for scores rows of att_stride floats:
+// the CH = 128 instance when its double buffer fits, else 64; sc staged V
+// positions.  Returns false when neither fits.
+static bool av_plan(int hd, int max_len, int att_stride, int *ch_out, int *sc_out, size_t *lds_out) {
+    const size_t per_pos = (size_t)hd + (size_t)(hd >> 5) * sizeof(float);
+    const int lim = lds_limit() - 4096;
+    for (int ch : {128, 64}) {
+        const size_t fixed = ((size_t)att_stride + 2 * (size_t)hd * (ch + 4) + AV_ESUM_FLOATS) * sizeof(float);
+        if (fixed + (size_t)ch * per_pos > (size_t)lim) continue;
+        int sc = (int)(((size_t)lim - fixed) / per_pos) & ~(ch - 1);
+        const int need = (max_len + ch - 1) & ~(ch - 1);
+        if (sc > need) sc = need;
+        const int sc_regs = (AV_THREADS * AV_STAGE_MAX / (hd >> 4)) & ~(ch - 1);
+        if (sc > sc_regs) sc = sc_regs;
+        *ch_out = ch;
+        *sc_out = sc;
+        *lds_out = fixed + (size_t)sc * per_pos;
+        return true;
+    }
+    return false;
+}
+
+static void av_allow_lds() {
+    static bool attr_set = false;
+    if (attr_set) return;
+    const int lim = lds_limit() - 4096;
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k_attn_av<128>), hipFuncAttributeMaxDynamicSharedMemorySize, lim);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k_attn_av<64>), hipFuncAttributeMaxDynamicSharedMemorySize, lim);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k_attn_av_items<128>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, lim);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k_attn_av_items<64>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, lim);
+    attr_set = true;
+}
+
+// Attention of several sessions' rows in one launch per kernel: items
+// (device) give each session's rows [row0, row0 + n) (n <= MAX_CHUNK), KV
+// plane bases and position; base carries the layer's weights and the row
+// buffers at row 0.  max_len: the longest item's last position + 1; att:
+// n_items scratch blocks of att_item floats.
+extern "C" int l98k_attn_items(const AttnArgs *a, const AttnItem *items, int n_items, int plane, int max_len,
+                               float *att, size_t att_item, hipStream_t st) {
+    if (a->nkv < 1 || a->nh % a->nkv || (a->hd & 31) || 256 % a->hd || a->hd > ATT_MAX_HD || a->rot > a->hd ||
+        (a->rot & 1) || n_items < 1 || max_len < 1 || !a->oq || !a->oqs || !att || a->kv_only)
+        return -1;
+    if (a->nh / a->nkv + MAX_CHUNK > ATT_MAX_VEC) return -1;
+    const int att_stride = (max_len + 3) & ~3;
+    if ((size_t)MAX_CHUNK * a->nh * att_stride > att_item) return -1;
+    const int slices = (max_len + ATT_SLICE - 1) / ATT_SLICE;
+    hipLaunchKernelGGL(k_attn_scores_items, dim3(slices, a->nkv, n_items * MAX_CHUNK), dim3(256), 0, st, *a, items,
+                       plane, att, att_stride, att_item);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+    av_allow_lds();
+    int ch = 0, sc = 0;
+    size_t lds = 0;
+    if (!av_plan(a->hd, max_len, att_stride, &ch, &sc, &lds)) return -1;
+    if (ch == 128)
+        hipLaunchKernelGGL(k_attn_av_items<128>, dim3(a->nh, n_items * MAX_CHUNK), dim3(AV_THREADS), lds, st, *a, items,
+                           plane, att, att_stride, att_item, sc);
+    else
+        hipLaunchKernelGGL(k_attn_av_items<64>, dim3(a->nh, n_items * MAX_CHUNK), dim3(AV_THREADS), lds, st, *a, items,
+                           plane, att, att_stride, att_item, sc);
+    return (int)hipGetLastError();
 }
 
 extern "C" int l98k_attn(const AttnArgs *a, int nt, int max_len, float *att, hipStream_t st) {

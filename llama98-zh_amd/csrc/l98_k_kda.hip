@@ -42,7 +42,7 @@ __device__ __forceinline__ float dpp_quad_bcast3(float v) {      // every lane <
 }
 
 template <int KD, int K, int NT>
-__global__ __launch_bounds__(4 * KD) void k_kda_step(KdaStepArgs a) {
+__device__ __forceinline__ void kda_step_body(const KdaStepArgs &a, int h) {
     constexpr int VD = KD, HIST = K - 1, NTHR = 4 * KD, RPL = KD / 4;
     constexpr int NF4 = (NT * KDA_MAX_RANK / 4 + NTHR - 1) / NTHR;      // float4 of the gate input per thread
     constexpr int NO4 = (NT * VD / 4 + NTHR - 1) / NTHR;                // float4 of the output per thread
@@ -58,7 +58,6 @@ __global__ __launch_bounds__(4 * KD) void k_kda_step(KdaStepArgs a) {
     __shared__ float s_invq[MAX_CHUNK], s_invk[MAX_CHUNK], s_beta[MAX_CHUNK], s_kq[MAX_CHUNK],
         s_oinv[MAX_CHUNK];
     __shared__ __align__(16) float s_z[MAX_CHUNK][KD];   // silu of the output gate input
-    const int h = blockIdx.x;
     const int tid = threadIdx.x;
     const bool chan = tid < KD;
     // Channel phases: thread group grp = tid / kd takes row type grp (0: q,
@@ -342,6 +341,46 @@ __global__ __launch_bounds__(4 * KD) void k_kda_step(KdaStepArgs a) {
     }
 }
 
+template <int KD, int K, int NT>
+__global__ __launch_bounds__(4 * KD) void k_kda_step(KdaStepArgs a) {
+    kda_step_body<KD, K, NT>(a, blockIdx.x);
+}
+
+// Several sessions' rows in one launch: block (head, item); item i is a
+// session's rows [row0, row0 + n) against its own state and conv rings
+// (layer offsets added here), in MAX_CHUNK-row sub-chunks in order (a
+// sub-chunk reads back the state and conv history the previous one wrote,
+// from the same threads).  The launch's args carry the layer's weights and
+// the row buffers at row 0.  Rows advance the ring only for n <= MAX_CHUNK.
+template <int KD, int K>
+__global__ __launch_bounds__(4 * KD) void k_kda_items(KdaStepArgs b, const KdaItem *__restrict__ items,
+                                                      size_t state_off, size_t conv_off) {
+    const KdaItem it = items[blockIdx.y];
+    KdaStepArgs a = b;
+    a.state = it.state + state_off;
+    a.conv_ring = it.conv_ring + conv_off;
+    a.ctl_slot = it.ctl_slot;
+    a.slot_stride = it.slot_stride;
+    a.conv_slot_stride = it.conv_slot_stride;
+    a.depth = it.depth;
+    for (int c0 = 0; c0 < it.n; c0 += MAX_CHUNK) {
+        const int r = it.row0 + c0;
+        a.nt = imin(MAX_CHUNK, it.n - c0);
+        a.pq = b.pq + (size_t)r * b.key;
+        a.pk = b.pk + (size_t)r * b.key;
+        a.pv = b.pv + (size_t)r * b.value;
+        a.pfa = b.pfa + (size_t)r * b.rank;
+        a.bvec = b.bvec + (size_t)r * b.nv;
+        a.gz = b.gz + (size_t)r * b.value;
+        a.xq = b.xq + (size_t)r * b.value;
+        a.xqs = b.xqs + (size_t)r * (b.value >> 5);
+        a.raw_out = b.raw_out ? b.raw_out + (size_t)r * b.value : nullptr;
+        a.normed_out = b.normed_out ? b.normed_out + (size_t)r * b.value : nullptr;
+        if (c0) __syncthreads();
+        kda_step_body<KD, K, MAX_CHUNK>(a, blockIdx.x);
+    }
+}
+
 // ---------------------------------------------------------- host glue ---
 
 extern "C" int l98k_upload_exp_table_kda(const float *tab) {
@@ -377,5 +416,28 @@ extern "C" int l98k_kda_step(const KdaStepArgs *a, int kd, int K, hipStream_t st
     }
 #undef KDA_K4
 #undef KDA_STEP
+    return (int)hipGetLastError();
+}
+
+extern "C" int l98k_kda_items(const KdaStepArgs *a, const KdaItem *items, int n_items, size_t state_off,
+                              size_t conv_off, int kd, int K, hipStream_t st) {
+    if (n_items < 1 || a->rank < 32 || (a->rank & 31) || a->rank > KDA_MAX_RANK || a->key != a->nv * kd ||
+        a->value != a->nv * kd || K < 2 || K > 4)
+        return -1;
+#define KDA_ITEMS(KD_, K_) \
+    hipLaunchKernelGGL((k_kda_items<KD_, K_>), dim3(a->nv, n_items), dim3(4 * (KD_)), 0, st, *a, items, state_off, conv_off)
+    switch (kd * 8 + K) {
+    case 64 * 8 + 4: KDA_ITEMS(64, 4); break;
+    case 64 * 8 + 3: KDA_ITEMS(64, 3); break;
+    case 64 * 8 + 2: KDA_ITEMS(64, 2); break;
+    case 128 * 8 + 4: KDA_ITEMS(128, 4); break;
+    case 128 * 8 + 3: KDA_ITEMS(128, 3); break;
+    case 128 * 8 + 2: KDA_ITEMS(128, 2); break;
+    case 32 * 8 + 4: KDA_ITEMS(32, 4); break;
+    case 32 * 8 + 3: KDA_ITEMS(32, 3); break;
+    case 32 * 8 + 2: KDA_ITEMS(32, 2); break;
+    default: return -1;
+    }
+#undef KDA_ITEMS
     return (int)hipGetLastError();
 }

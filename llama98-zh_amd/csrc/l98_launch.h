@@ -75,7 +75,15 @@ int l98k_mtp_pre(const int8_t *emb_q, const float *emb_s, const int *toks, const
 // One KDA layer step for a chunk: conv, gate up-projection, recurrence,
 // gated norm and o_proj quantization (kd in {32, 64, 128}, conv taps K in 2..4).
 int l98k_kda_step(const KdaStepArgs *a, int kd, int K, hipStream_t st);
+// The KDA step of several sessions' rows in one launch (items in device
+// memory; state_off / conv_off: the layer's offsets inside each ring slot).
+int l98k_kda_items(const KdaStepArgs *a, const KdaItem *items, int n_items, size_t state_off, size_t conv_off,
+                   int kd, int K, hipStream_t st);
 int l98k_attn_prep(const AttnArgs *a, int nt, hipStream_t st);
+// Attention of several sessions' rows in one launch per kernel (items in
+// device memory); att: n_items blocks of att_item floats.
+int l98k_attn_items(const AttnArgs *a, const AttnItem *items, int n_items, int plane, int max_len, float *att,
+                    size_t att_item, hipStream_t st);
 // Attention of nt tokens (positions *ctl_pos + pos_off + t) against the KV
 // plane: scores with the q/k preparation and the chunk's own K/V cache rows,
 // then softmax, value sum, output gate and quantization into oq / oqs.

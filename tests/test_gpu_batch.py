@@ -64,3 +64,48 @@ def test_greedy_rounds_batch_matches_single_sessions(pkg, server):
         for st in states:
             eng.free_session(st)
         eng.close()
+
+
+def test_verify_batch_32_sessions_ragged_contexts(pkg, server):
+    """configs[4]'s shape: 32 sessions with contexts uniform in [256, 2048],
+    4 verify rows each, through the batch (one launch per kernel over all
+    128 rows) against the same 32 sessions verified one by one, bit for
+    bit; three of them also against the CPU restatement."""
+    import ctypes as C
+    print("[case] verify batch, 32 sessions, contexts 256-2048", flush=True)
+    eng = pkg.Engine(server)
+    rng = np.random.default_rng(0)
+    ctx = rng.integers(256, 2049, size=32)
+    batch, single = [], []
+    try:
+        for i, n in enumerate(ctx):
+            prompt = pkg.prompt_tokens(1000 + i, int(n), 8192)
+            for group in (batch, single):
+                st = eng.add_session()
+                eng.session_start_on(st, prompt)
+                group.append(st)
+        toks = np.array([[(13 * i + 7 * j + 5) % 8192 for j in range(4)] for i in range(32)], np.int32)
+        pos0 = ctx.astype(np.int32)
+        _, out = eng.verify_batch(batch, toks, pos0)
+        V, d = eng.V, eng.d
+        for i, st in enumerate(single):
+            t = np.ascontiguousarray(toks[i])
+            assert eng.lib.lz_forward_verify(C.byref(eng.m), C.byref(st), t.ctypes.data_as(C.POINTER(C.c_int)), 4,
+                                             int(pos0[i])) == 0
+            lg = np.ctypeslib.as_array(st.mtp_logits, shape=(pkg.L98_SPEC_K_GPU + 1, V))[:4]
+            hd = np.ctypeslib.as_array(st.mtp_verify_hidden, shape=(pkg.L98_SPEC_K_GPU + 1, d))[:4]
+            assert same_bits(out[i][0], lg), f"session {i} (ctx {ctx[i]}) logits: " + diff_report(out[i][0], lg)
+            assert same_bits(out[i][1], hd), f"session {i} (ctx {ctx[i]}) hidden: " + diff_report(out[i][1], hd)
+            assert batch[i].ssm_slot == st.ssm_slot
+        for i in (0, int(np.argmax(ctx)), 17):
+            o = Oracle(server)
+            prompt = pkg.prompt_tokens(1000 + i, int(ctx[i]), 8192)
+            o.session_start(prompt)
+            o.forward_capture(prompt[-1], int(ctx[i]) - 1)
+            ref = o.verify(toks[i], int(ctx[i]))
+            assert same_bits(out[i][0], ref[0]) and same_bits(out[i][1], ref[1]), f"session {i} vs oracle"
+            o.close()
+    finally:
+        for st in batch + single:
+            eng.free_session(st)
+        eng.close()
