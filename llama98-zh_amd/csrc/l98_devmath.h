@@ -477,6 +477,19 @@ __device__ __forceinline__ uint32_t quant_octet(float4 v, float *sg_out) {
     return packed;
 }
 
+// epi_q8 of a row with one 32-element group (a per-row weight scale over
+// in_dim == 32, so r = gs / 32 == 1: src/ops_epi.c:1012-1021): four
+// accumulators, only the first of which takes a term,
+//   a0 = 0 + float(acc) * (xs * ws);  o = (a0 + 0) + (0 + 0).
+// Rows of more groups take the r > 1 form, 0 + (sum_s float(acc_s) * xs_s)
+// * ws.
+__device__ __forceinline__ float epi_one_group(int acc, float xs, float ws) {
+    float a0 = 0.0f;
+    const float a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+    a0 += (float)acc * (xs * ws);
+    return (a0 + a2) + (a1 + a3);
+}
+
 // RMSNorm(1+w) of the block's row v (lz_rmsnorm, src/ops_norm.c:690-747:
 // sum of squares in index order, inv = rsqrt(ss/n + eps), o =
 // (x*inv)*(1+w)), then the optional store of o and its per-32 quantization.

@@ -355,8 +355,10 @@ __device__ __forceinline__ void tile_dot(const int4 (&wv)[GEMV_MAXJ], const int8
 }
 
 // Epilogue of one (row er, token et) pair: sum_s float(acc[s]) * xqs[s] in
-// group order, then times the row scale (src/ops_epi.c:983-1017).
+// group order, then times the row scale (src/ops_epi.c:983-1017); a
+// one-group row takes epi_one_group.
 __device__ __forceinline__ float tile_epilogue(const int *pp, const float *xs, int nb, float wsv) {
+    if (nb == 1) return epi_one_group(pp[0], xs[0], wsv);
     float dot = 0.0f;
     if ((nb & 3) == 0) {
         // the LDS reads run up to three groups of four ahead of the

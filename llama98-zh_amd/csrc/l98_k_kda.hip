@@ -172,6 +172,7 @@ __device__ __forceinline__ void kda_step_body(const KdaStepArgs &a, int h) {
         if (t < NT) {
             const int tc = imin(t, nt - 1);
             float dot = 0.0f;
+            int acc0 = 0;
 #pragma unroll
             for (int g = 0; g < KDA_MAX_RANK / 32; g++) {
                 if (g * 32 < rank) {
@@ -187,10 +188,12 @@ __device__ __forceinline__ void kda_step_body(const KdaStepArgs &a, int h) {
                     acc = __builtin_amdgcn_sdot4(w1.z, x1.z, acc, false);
                     acc = __builtin_amdgcn_sdot4(w1.w, x1.w, acc, false);
                     dot += (float)acc * s_fs[(tc * rank >> 5) + g];
+                    if (g == 0) acc0 = acc;
                 }
             }
             float pre = 0.0f;
-            pre += dot * fbs;
+            if (rank == 32) pre = epi_one_group(acc0, s_fs[tc * rank >> 5], fbs);
+            else pre += dot * fbs;
             const float p = pre + dtb;
             const float gg = -decay * d_softplus(p, tab);
             s_g[t][j] = d_exp(gg, tab);

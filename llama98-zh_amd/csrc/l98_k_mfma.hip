@@ -9,7 +9,8 @@
 // 32-element group: started from a zero accumulator it returns the exact
 // group sums of a 16 x 16 (row, token) tile, which the lanes then fold into
 // fp32 in group order, one multiply and one add per group and output, as
-// the reference's epilogue does.  The result is bit-identical to the GEMV
+// the reference's epilogue does (a one-group row, K == 32, takes the
+// reference's r == 1 association instead: epi_one_group).  The result is bit-identical to the GEMV
 // path for every token, whatever the number of tokens.
 //
 // Operand layout of the 16x16x32 int8 MFMA (64 lanes): lane l supplies
@@ -101,17 +102,22 @@ __global__ __launch_bounds__(MF_THREADS) void k_mfma_q8(const int8_t *__restrict
             }
         }
     }
+    // one group (K == 32): f holds the exact group sum (|acc| < 2^24) for
+    // epi_one_group's association
+    const bool one = nb == 1;
+    float s0 = 0.0f;
     for (; g < nb; g++) {
         long a[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) a[i] = ld8(wp[i] + 32 * g);
         const long b = ld8(xp + 32 * g);
         const float s = xsp[g];
+        s0 = s;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const v4i_t d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[i], b, zero, 0, 0, 0);
 #pragma unroll
-            for (int v = 0; v < 4; v++) f[i][v] += (float)d[v] * s;
+            for (int v = 0; v < 4; v++) f[i][v] += one ? (float)d[v] : (float)d[v] * s;
         }
     }
     if (cl >= ncols) return;
@@ -123,7 +129,8 @@ __global__ __launch_bounds__(MF_THREADS) void k_mfma_q8(const int8_t *__restrict
             const int n = n0 + 16 * i + 4 * (lane >> 4) + v;
             if (n < N) {
                 float sum = 0.0f;
-                sum += f[i][v] * wsg[n];
+                if (one) sum = epi_one_group((int)f[i][v], s0, wsg[n]);
+                else sum += f[i][v] * wsg[n];
                 op[n] = sum;
             }
         }

@@ -103,7 +103,7 @@ int l98_synth_config(int id, L98SynthConfig *c) {
     c->w_std = 0.02f;
     c->bias_std = 0.01f;
     switch (id) {
-    case 0: case 2: case 4:
+    case 0: case 2: case 4: case 5:
         c->vocab = 8192; c->hidden = 256; c->n_layers = 4; c->seq_len = 512;
         c->n_heads = 4; c->n_kv_heads = 2; c->head_dim = 64;
         c->kda_heads = 4; c->kd = 64; c->vd = 64; c->gate_rank = 64;
@@ -113,6 +113,11 @@ int l98_synth_config(int id, L98SynthConfig *c) {
             c->seq_len = 2304;
             c->router_std = 0.0625f;      /* 1/sqrt(256): unit-variance logits */
             c->bias_std = 0.5f;
+        }
+        if (id == 5) {
+            c->use_subn = 1;
+            c->hadamard_o = 64;
+            c->hadamard_down = 256;
         }
         return 0;
     case 1:
@@ -129,7 +134,7 @@ int l98_synth_config(int id, L98SynthConfig *c) {
         c->n_experts = 128; c->topk = 8; c->latent = 512; c->moe_inter = 768;
         c->shared_w = 768; c->mtp_inter = 768;
         return 0;
-    case 10: case 11:
+    case 10: case 11: case 12:
         c->vocab = 512; c->hidden = 64; c->n_layers = 4; c->seq_len = 160;
         c->n_heads = 2; c->n_kv_heads = 1; c->head_dim = 32;
         c->kda_heads = 2; c->kd = 32; c->vd = 32; c->gate_rank = 32;
@@ -140,6 +145,11 @@ int l98_synth_config(int id, L98SynthConfig *c) {
             c->seq_len = 256;
             c->resid_std = ECHO_RESID_STD;
             c->mtp_echo = 1;
+        }
+        if (id == 12) {
+            c->use_subn = 1;
+            c->hadamard_o = 32;
+            c->hadamard_down = 64;
         }
         return 0;
     default:
@@ -364,7 +374,7 @@ int l98_synth_write(const char *dir, const L98SynthConfig *c, uint64_t seed,
     put_i32(&w, 1); put_i32(&w, c->mtp_inter);         /* mtp_n_layers, mtp_intermediate_size */
     put_i32(&w, 0); put_f32(&w, 1.0f); put_f32(&w, 4096.0f);
     put_f32(&w, 32.0f); put_f32(&w, 1.0f);             /* rope scaling: none */
-    put_i32(&w, 0); put_i32(&w, 0); put_i32(&w, 0);    /* use_subn, hadamard_o, hadamard_down */
+    put_i32(&w, c->use_subn); put_i32(&w, c->hadamard_o); put_i32(&w, c->hadamard_down);
     put_i32(&w, 0); put_i32(&w, 0); put_i32(&w, 0);    /* mla_q, mla_o, attn_kv_share */
     put_i32(&w, 0); put_i32(&w, 0); put_i32(&w, 0); put_i32(&w, 0); /* sink, gated_residual, ced_split, ced_kv */
     for (int i = 0; i < MAX_LAYERS; i++) put_i32(&w, 0);   /* csa2_on */
@@ -391,6 +401,12 @@ int l98_synth_write(const char *dir, const L98SynthConfig *c, uint64_t seed,
             matrix(&w, d, q_dim, os);                  /* o_proj */
             vec_norm(&w, hd, 0.0f, ws);                /* q_norm */
             vec_norm(&w, hd, 0.0f, ws);                /* k_norm */
+            if (c->use_subn) {                         /* q/k/v/o_proj.norm */
+                vec_norm(&w, d, 0.0f, ws);
+                vec_norm(&w, d, 0.0f, ws);
+                vec_norm(&w, d, 0.0f, ws);
+                vec_norm(&w, q_dim, 0.0f, ws);
+            }
         } else {
             matrix(&w, key, d, ws);                    /* q_proj */
             matrix(&w, key, d, ws);                    /* k_proj */
@@ -406,6 +422,13 @@ int l98_synth_write(const char *dir, const L98SynthConfig *c, uint64_t seed,
             matrix(&w, value, d, ws);                  /* g_proj */
             vec_norm(&w, c->vd, 1.0f, ws);             /* o_norm (gain w, not 1+w) */
             matrix(&w, d, value, os);                  /* o_proj */
+            if (c->use_subn) {                         /* q/k/v/g/o_proj.norm */
+                vec_norm(&w, d, 0.0f, ws);
+                vec_norm(&w, d, 0.0f, ws);
+                vec_norm(&w, d, 0.0f, ws);
+                vec_norm(&w, d, 0.0f, ws);
+                vec_norm(&w, value, 0.0f, ws);
+            }
         }
         matrix(&w, c->n_experts, d, rs);               /* mlp.gate (router) */
         emit_tensor(&w, 1, c->n_experts, INIT_NORMAL, c->bias_std, 0.0f, 0);
@@ -414,6 +437,14 @@ int l98_synth_write(const char *dir, const L98SynthConfig *c, uint64_t seed,
         matrix(&w, c->shared_w, d, ws);                /* shared gate_proj */
         matrix(&w, c->shared_w, d, ws);                /* shared up_proj */
         matrix(&w, d, c->shared_w, os);                /* shared down_proj */
+        if (c->use_subn) {          /* gate, routed down/up, shared gate/up/down .norm */
+            vec_norm(&w, d, 0.0f, ws);
+            vec_norm(&w, d, 0.0f, ws);
+            vec_norm(&w, c->latent, 0.0f, ws);
+            vec_norm(&w, d, 0.0f, ws);
+            vec_norm(&w, d, 0.0f, ws);
+            vec_norm(&w, c->shared_w, 0.0f, ws);
+        }
         for (int e = 0; e < c->n_experts; e++) {
             matrix(&w, c->moe_inter, c->latent, ws);   /* w1 */
             matrix(&w, c->latent, c->moe_inter, ws);   /* w2 */
@@ -428,6 +459,10 @@ int l98_synth_write(const char *dir, const L98SynthConfig *c, uint64_t seed,
      * are about E . norm(E[tok]) and the draft is the input token. */
     vec_norm(&w, d, 0.0f, ws);
     vec_norm(&w, d, 0.0f, ws);
+    if (c->use_subn) {                                 /* mlp.gate/up_proj.norm */
+        vec_norm(&w, d, 0.0f, ws);
+        vec_norm(&w, d, 0.0f, ws);
+    }
     matrix(&w, qgate, d, ws);
     matrix(&w, kv_dim, d, ws);
     matrix(&w, kv_dim, d, ws);
@@ -435,10 +470,17 @@ int l98_synth_write(const char *dir, const L98SynthConfig *c, uint64_t seed,
     else matrix(&w, d, q_dim, ws);
     vec_norm(&w, hd, 0.0f, ws);
     vec_norm(&w, hd, 0.0f, ws);
+    if (c->use_subn) {                                 /* self_attn.q/k/v/o_proj.norm */
+        vec_norm(&w, d, 0.0f, ws);
+        vec_norm(&w, d, 0.0f, ws);
+        vec_norm(&w, d, 0.0f, ws);
+        vec_norm(&w, q_dim, 0.0f, ws);
+    }
     matrix(&w, c->mtp_inter, d, ws);                   /* gate_proj */
     matrix(&w, c->mtp_inter, d, ws);                   /* up_proj */
     if (c->mtp_echo) zero_matrix(&w, d, c->mtp_inter); /* down_proj */
     else matrix(&w, d, c->mtp_inter, ws);
+    if (c->use_subn) vec_norm(&w, c->mtp_inter, 0.0f, ws);   /* down_proj.norm */
     if (c->mtp_echo) emit_tensor(&w, d, 2 * d, INIT_EYE, ws, 0.0f, 1);     /* mtp.fc = [I | N(0, ws)] */
     else matrix(&w, d, 2 * d, ws);                     /* mtp.fc */
     vec_norm(&w, d, 0.0f, ws);                         /* mtp.norm */

@@ -36,6 +36,11 @@ typedef struct {
     int mtp_echo;               /* 1: MTP fc = [I | N(0, w_std)], MTP o_proj and
                                    down_proj zero, so the head drafts its own input
                                    token */
+    int use_subn;               /* 1: SubLN - no pre-layer norms; every projection
+                                   normalizes its own input with its own weight */
+    int hadamard_o;             /* SubLN block Hadamard of the KDA o_proj input (0 off) */
+    int hadamard_down;          /* SubLN block Hadamard of the dense FFN down_proj
+                                   input (the MTP head's FFN; 0 off) */
 } L98SynthConfig;
 
 /* Named configurations:
@@ -48,6 +53,10 @@ typedef struct {
  *  11  echo    micro's shapes with a small vocabulary, an echoing MTP head and
  *              damped residual writers: greedy drafts are accepted at every
  *              depth, so the accepted-draft path of a round runs
+ *   5  subln   config 0's shapes with use_subn = 1, hadamard_o = 64,
+ *              hadamard_down = 256 (the survey's C1s variant)
+ *  12  micro-subln  micro's shapes with use_subn = 1, hadamard_o = 32,
+ *              hadamard_down = 64
  * Returns 0 on success, 1 for an unknown id. */
 int l98_synth_config(int id, L98SynthConfig *out);
 

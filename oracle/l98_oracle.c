@@ -207,42 +207,53 @@ static int q8_round(float v) {
     return (int)(t.u & 0x007FFFFFu) - 0x00400000;
 }
 
-/* q8_group_scale + lz_quantize_q8 for gs = 32 (src/ops_quant.c:1444-1475,
- * 1633-1670, 2152-2286): amax by |bits|, s = amax/127 (as amax*(1/127f)),
- * inv = 127/amax, q = clamp(rne(x*inv), +-127); a zero or tiny group gets
- * s = 1, q = 0; a group whose 127/amax overflows divides by s instead. */
-ORA_API void o_quantize_q8(const float *x, int n, int8_t *q, float *s) {
+/* q8_group_scale + the element loop of lz_quantize_q8 over one group of n
+ * elements (src/ops_quant.c:1444-1475, 1633-1670, 2152-2286): amax by |bits|,
+ * s = amax/127 (as amax*(1/127f)), inv = 127/amax, q = clamp(rne(x*inv),
+ * +-127); a zero or tiny group gets s = 1, q = 0; a group whose 127/amax
+ * overflows divides by s instead.  Returns the group's scale. */
+static float quant_group(const float *grp, int n, int8_t *q) {
     static const float INV127 = 1.0f / 127.0f;
-    int g, k;
-    for (g = 0; g < n / 32; g++) {
-        const float *grp = x + g * 32;
-        union { float f; uint32_t u; } b;
-        uint32_t am = 0;
-        float amax, sg, inv;
-        int fast;
-        for (k = 0; k < 32; k++) {
-            uint32_t a;
-            b.f = grp[k];
-            a = b.u & 0x7FFFFFFFu;
-            if (a > am) am = a;
-        }
-        b.u = am;
-        amax = b.f;
-        if (amax > 0.0f) {
-            sg = amax * INV127;
-            inv = 127.0f / amax;
-            fast = (inv <= FLT_MAX);
-            if (sg < 1.0e-30f) { sg = 1.0f; inv = 0.0f; fast = 1; }
-        } else {
-            sg = 1.0f; inv = 0.0f; fast = 1;
-        }
-        s[g] = sg;
-        for (k = 0; k < 32; k++) {
-            int qi = fast ? q8_round(grp[k] * inv) : q8_round(grp[k] / sg);
-            qi = (qi > 127) ? 127 : qi;
-            q[g * 32 + k] = (int8_t)((qi < -127) ? -127 : qi);
-        }
+    union { float f; uint32_t u; } b;
+    uint32_t am = 0;
+    float amax, sg, inv;
+    int fast, k;
+    for (k = 0; k < n; k++) {
+        uint32_t a;
+        b.f = grp[k];
+        a = b.u & 0x7FFFFFFFu;
+        if (a > am) am = a;
     }
+    b.u = am;
+    amax = b.f;
+    if (amax > 0.0f) {
+        sg = amax * INV127;
+        inv = 127.0f / amax;
+        fast = (inv <= FLT_MAX);
+        if (sg < 1.0e-30f) { sg = 1.0f; inv = 0.0f; fast = 1; }
+    } else {
+        sg = 1.0f; inv = 0.0f; fast = 1;
+    }
+    for (k = 0; k < n; k++) {
+        int qi = fast ? q8_round(grp[k] * inv) : q8_round(grp[k] / sg);
+        qi = (qi > 127) ? 127 : qi;
+        q[k] = (int8_t)((qi < -127) ? -127 : qi);
+    }
+    return sg;
+}
+
+/* lz_quantize_q8 for gs = 32: one quant_group per 32 elements. */
+ORA_API void o_quantize_q8(const float *x, int n, int8_t *q, float *s) {
+    for (int g = 0; g < n / 32; g++) s[g] = quant_group(x + g * 32, 32, q + g * 32);
+}
+
+/* lz_quantize_q8_tok (src/ops_quant.c:2284-2314): q8_group_scale over the
+ * whole row, the same element loop, and the one scale replicated into all
+ * n/32 slots. */
+ORA_API void o_quantize_q8_tok(const float *x, int n, int8_t *q, float *s) {
+    if (n < 32) return;
+    const float sg = quant_group(x, n, q);
+    for (int g = 0; g < n / 32; g++) s[g] = sg;
 }
 
 /* lz_fwht_i32's scalar body (src/fwht.c:65-196; the loop at :186-195): the
@@ -352,9 +363,13 @@ ORA_API void o_subn_rot_f32(float *x, int n, int blk) {
 }
 
 /* lz_matmul_xq_nt for a Q8_0 per-row weight (gs = in), SIMD row kernel +
- * epi_q8 r>1 branch (src/ops_matmul.c:336-466; src/ops_epi.c:983-1017):
+ * epi_q8 (src/ops_matmul.c:336-466; src/ops_epi.c:983-1022), r = gs/32:
  *   acc[t,i,s] = sum_{e<32} w[i,32s+e] xq[t,32s+e]       (exact int32)
- *   dot = sum_s float(acc)*xqs[t,s]  (serial from 0.0f), o = (0.0f + dot*ws[i])
+ *   r > 1 (in > 32): dot = sum_s float(acc)*xqs[t,s] (serial from 0.0f),
+ *                    o = 0.0f + dot*ws[i]
+ *   r == 1 (in == 32, one group): a0 = 0.0f + float(acc)*(xqs[t,0]*ws[i]),
+ *                    o = (a0 + 0.0f) + (0.0f + 0.0f)  (four accumulators,
+ *                    three of them untouched)
  * The SIMD kernel's x256 accumulator and 2^-8 post-scale are exact powers of
  * two and cancel.  acc_out (optional) receives acc[t][i][s]. */
 ORA_API void o_matmul_q8(float *o, const int8_t *xq, const float *xqs,
@@ -371,9 +386,15 @@ ORA_API void o_matmul_q8(float *o, const int8_t *xq, const float *xqs,
                 for (int e = 0; e < 32; e++)
                     acc += (int32_t)wr[s * 32 + e] * (int32_t)xr[s * 32 + e];
                 if (acc_out) acc_out[((size_t)t * out + i) * nb + s] = acc;
-                dot += (float)acc * xqs[(size_t)t * nb + s];
+                if (nb == 1) {
+                    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+                    a0 += (float)acc * (xqs[(size_t)t * nb] * ws[i]);
+                    sum = (a0 + a2) + (a1 + a3);
+                } else {
+                    dot += (float)acc * xqs[(size_t)t * nb + s];
+                }
             }
-            sum += dot * ws[i];
+            if (nb > 1) sum += dot * ws[i];
             o[(size_t)t * out + i] = sum;
         }
     }
@@ -433,6 +454,13 @@ typedef struct {
     QMat router, down, up, sg, su, sd;
     float *bias;
     QMat *w1, *w2, *w3;
+    /* SubLN per-projection input norms (use_subn only; src/model.c:1511-1665):
+     * attention q/k/v/o, KDA q/k/v/g/o, MoE router / routed down / routed up
+     * / shared gate / up / down, dense FFN gate / up / down (the MTP head's) */
+    float *sn_q, *sn_k, *sn_v, *sn_o;
+    float *kn_q, *kn_k, *kn_v, *kn_g, *kn_o;
+    float *mn_gate, *mn_down, *mn_up, *mn_sg, *mn_su, *mn_sd;
+    float *fn_gate, *fn_up, *fn_down;
 } OLayer;
 
 typedef struct {
@@ -443,6 +471,7 @@ typedef struct {
     int types[128];
     int gate_rank, n_experts, topk, moe_inter, latent, shared_w;
     int mtp_inter;
+    int use_subn, hadamard_o, hadamard_down;
     QMat embed;
     float *final_norm;
     OLayer *L;
@@ -518,11 +547,17 @@ ORA_API void ora_close(void *h) {
             free_q(&L->w1[e]); free_q(&L->w2[e]); free_q(&L->w3[e]);
         }
         free(L->w1); free(L->w2); free(L->w3);
+        free(L->sn_q); free(L->sn_k); free(L->sn_v); free(L->sn_o);
+        free(L->kn_q); free(L->kn_k); free(L->kn_v); free(L->kn_g); free(L->kn_o);
+        free(L->mn_gate); free(L->mn_down); free(L->mn_up);
+        free(L->mn_sg); free(L->mn_su); free(L->mn_sd);
     }
     free(m->L);
     free(m->mtp.in_norm); free(m->mtp.post_norm);
     free_q(&m->mtp.q); free_q(&m->mtp.k); free_q(&m->mtp.v); free_q(&m->mtp.o);
     free(m->mtp.q_norm); free(m->mtp.k_norm);
+    free(m->mtp.sn_q); free(m->mtp.sn_k); free(m->mtp.sn_v); free(m->mtp.sn_o);
+    free(m->mtp.fn_gate); free(m->mtp.fn_up); free(m->mtp.fn_down);
     free_q(&m->mtp_gate); free_q(&m->mtp_up); free_q(&m->mtp_down); free_q(&m->mtp_fc);
     free(m->mtp_norm); free(m->mtp_pre_h); free(m->mtp_pre_e);
     free(m->rope_cs);
@@ -563,10 +598,36 @@ ORA_API void *ora_open(const char *dir, char *err, int errlen) {
     (void)rd_i32(&r); (void)rd_i32(&r); (void)rd_i32(&r); (void)rd_i32(&r);
     m->shared_w = rd_i32(&r);
     (void)rd_i32(&r); m->mtp_inter = rd_i32(&r);
-    {   /* rest of the v5 tail: 5 rope words, 10 flags, 3x128, 6, 128 */
-        int skip = 5 + 10 + 3 * 128 + 6 + 128;
+    for (int i = 0; i < 5; i++) (void)rd_i32(&r);             /* rope scaling */
+    m->use_subn = rd_i32(&r);
+    m->hadamard_o = rd_i32(&r);
+    m->hadamard_down = rd_i32(&r);
+    {   /* rest of the v5 tail: 7 flags, 3x128, 6, 128 */
+        int skip = 7 + 3 * 128 + 6 + 128;
         for (int i = 0; i < skip; i++) (void)rd_i32(&r);
     }
+    /* resolve_hadamard (src/model.c:139-182): -1 derives (hadamard_o: the
+     * whole lin_value_dim on a dense model when it is a power of two, else
+     * 0; hadamard_down: the largest power of two <= 512 dividing
+     * intermediate_size); an explicit block must be 0 or a power of two
+     * dividing its width, and hadamard_down must divide the MTP width. */
+    if (m->hadamard_o == -1) {
+        int oblk = m->n_experts == 0 ? m->value : 0;
+        if (oblk < 2 || (oblk & (oblk - 1))) oblk = 0;
+        m->hadamard_o = oblk;
+    } else if (m->hadamard_o < 0 || (m->hadamard_o & (m->hadamard_o - 1)) ||
+               (m->hadamard_o && m->value % m->hadamard_o)) {
+        r.bad = 1;
+    }
+    if (m->hadamard_down == -1) {
+        int dblk = 512;
+        while (dblk > 1 && m->inter % dblk) dblk >>= 1;
+        m->hadamard_down = dblk == 1 ? 0 : dblk;
+    } else if (m->hadamard_down < 0 || (m->hadamard_down & (m->hadamard_down - 1)) ||
+               (m->hadamard_down && m->inter % m->hadamard_down)) {
+        r.bad = 1;
+    }
+    if (m->use_subn && m->hadamard_down > 1 && m->mtp_inter % m->hadamard_down) r.bad = 1;
     const int d = m->d;
     rd_q8(&r, &m->embed, m->vocab, d);
     m->final_norm = rd_f32v(&r, d);
@@ -583,6 +644,12 @@ ORA_API void *ora_open(const char *dir, char *err, int errlen) {
             rd_q8(&r, &L->o, d, m->q_dim);
             L->q_norm = rd_f32v(&r, m->hd);
             L->k_norm = rd_f32v(&r, m->hd);
+            if (m->use_subn) {
+                L->sn_q = rd_f32v(&r, d);
+                L->sn_k = rd_f32v(&r, d);
+                L->sn_v = rd_f32v(&r, d);
+                L->sn_o = rd_f32v(&r, m->q_dim);
+            }
         } else {
             rd_q8(&r, &L->kq, m->key, d);
             rd_q8(&r, &L->kk, m->key, d);
@@ -598,6 +665,13 @@ ORA_API void *ora_open(const char *dir, char *err, int errlen) {
             rd_q8(&r, &L->kg, m->value, d);
             L->o_norm = rd_f32v(&r, m->vd);
             rd_q8(&r, &L->ko, d, m->value);
+            if (m->use_subn) {
+                L->kn_q = rd_f32v(&r, d);
+                L->kn_k = rd_f32v(&r, d);
+                L->kn_v = rd_f32v(&r, d);
+                L->kn_g = rd_f32v(&r, d);
+                L->kn_o = rd_f32v(&r, m->value);
+            }
         }
         rd_q8(&r, &L->router, m->n_experts, d);
         L->bias = rd_f32v(&r, m->n_experts);
@@ -606,6 +680,14 @@ ORA_API void *ora_open(const char *dir, char *err, int errlen) {
         rd_q8(&r, &L->sg, m->shared_w, d);
         rd_q8(&r, &L->su, m->shared_w, d);
         rd_q8(&r, &L->sd, d, m->shared_w);
+        if (m->use_subn) {
+            L->mn_gate = rd_f32v(&r, d);
+            L->mn_down = rd_f32v(&r, d);
+            L->mn_up = rd_f32v(&r, m->latent);
+            L->mn_sg = rd_f32v(&r, d);
+            L->mn_su = rd_f32v(&r, d);
+            L->mn_sd = rd_f32v(&r, m->shared_w);
+        }
         L->w1 = (QMat *)calloc((size_t)m->n_experts, sizeof(QMat));
         L->w2 = (QMat *)calloc((size_t)m->n_experts, sizeof(QMat));
         L->w3 = (QMat *)calloc((size_t)m->n_experts, sizeof(QMat));
@@ -618,15 +700,26 @@ ORA_API void *ora_open(const char *dir, char *err, int errlen) {
     m->mtp.type = 1;
     m->mtp.in_norm = rd_f32v(&r, d);
     m->mtp.post_norm = rd_f32v(&r, d);
+    if (m->use_subn) {
+        m->mtp.fn_gate = rd_f32v(&r, d);
+        m->mtp.fn_up = rd_f32v(&r, d);
+    }
     rd_q8(&r, &m->mtp.q, m->qg_dim, d);
     rd_q8(&r, &m->mtp.k, m->kv_dim, d);
     rd_q8(&r, &m->mtp.v, m->kv_dim, d);
     rd_q8(&r, &m->mtp.o, d, m->q_dim);
     m->mtp.q_norm = rd_f32v(&r, m->hd);
     m->mtp.k_norm = rd_f32v(&r, m->hd);
+    if (m->use_subn) {
+        m->mtp.sn_q = rd_f32v(&r, d);
+        m->mtp.sn_k = rd_f32v(&r, d);
+        m->mtp.sn_v = rd_f32v(&r, d);
+        m->mtp.sn_o = rd_f32v(&r, m->q_dim);
+    }
     rd_q8(&r, &m->mtp_gate, m->mtp_inter, d);
     rd_q8(&r, &m->mtp_up, m->mtp_inter, d);
     rd_q8(&r, &m->mtp_down, d, m->mtp_inter);
+    if (m->use_subn) m->mtp.fn_down = rd_f32v(&r, m->mtp_inter);
     rd_q8(&r, &m->mtp_fc, d, 2 * d);
     m->mtp_norm = rd_f32v(&r, d);
     m->mtp_pre_h = rd_f32v(&r, d);
@@ -797,6 +890,27 @@ static void mm(OState *s, float *o, const QMat *w, int nt) {
     o_matmul_q8(o, s->xq, s->xqs, w->q, w->s, w->cols, w->rows, nt, NULL);
 }
 
+/* One SubLN projection (subn_norm_q8, src/forward_kda.c:203-236, and its
+ * twins in forward_attn / forward_moe / dense_ffn_step): RMSNorm(1+w) of
+ * each input row with the projection's own weight into tmp, its int8
+ * quantization (per 32 elements, or one scale per row when tok), then the
+ * matmul. */
+static void subn_proj(OState *s, const float *x, const float *wn, const QMat *W, float *out, int nt, int tok,
+                      float *tmp) {
+    const int n = W->cols;
+    for (int t = 0; t < nt; t++) o_rmsnorm(tmp + (size_t)t * n, x + (size_t)t * n, wn, n, s->m->eps);
+    for (int t = 0; t < nt; t++) {
+        if (tok) o_quantize_q8_tok(tmp + (size_t)t * n, n, s->xq + (size_t)t * n, s->xqs + (size_t)t * (n / 32));
+        else o_quantize_q8(tmp + (size_t)t * n, n, s->xq + (size_t)t * n, s->xqs + (size_t)t * (n / 32));
+    }
+    mm(s, out, W, nt);
+}
+
+/* subn_scale_gs + lz_subn_scale_group with the default scale choice
+ * (src/forward_kda.c:106-110, src/ops_sched.c:517-520): per-32 scales on a
+ * MoE model, one scale per row on a dense (BitLinear) one. */
+static int subn_tok(const OModel *m) { return m->n_experts == 0; }
+
 /* lz_causal_conv1d_step, src/ops_conv1d.c:26-87. */
 static void conv_step(float *o, const float *x, const float *st_in, float *st_out,
                       const float *w, int n_ch, int k) {
@@ -855,14 +969,30 @@ static void forward_kda(OState *s, const OLayer *L, int li, int nt, int advance,
     float gate[MAXB * 1024], ssm_out[MAXB * 1024], decay[64];
     float qn[512], kn[512];
     (void)d;
-    /* one quantization of xb shared by q/k/v/f_a/b/g (:615-633) */
-    quant_rows(s, s->xb, m->d, nt);
-    mm(s, q, &L->kq, nt);
-    mm(s, k, &L->kk, nt);
-    mm(s, v, &L->kv, nt);
-    mm(s, fa, &L->fa, nt);
-    mm(s, bvec, &L->kb, nt);
-    mm(s, g, &L->kg, nt);
+    if (m->use_subn) {
+        /* SubLN (:559-612): q/k/v/g each normalize the raw residual with
+         * their own weight; f_a and b share one quantization of the raw row */
+        const int tok = subn_tok(m);
+        subn_proj(s, s->xb, L->kn_q, &L->kq, q, nt, tok, s->xb2);
+        subn_proj(s, s->xb, L->kn_k, &L->kk, k, nt, tok, s->xb2);
+        subn_proj(s, s->xb, L->kn_v, &L->kv, v, nt, tok, s->xb2);
+        subn_proj(s, s->xb, L->kn_g, &L->kg, g, nt, tok, s->xb2);
+        for (int t = 0; t < nt; t++) {
+            if (tok) o_quantize_q8_tok(s->xb + (size_t)t * d, d, s->xq + (size_t)t * d, s->xqs + (size_t)t * (d / 32));
+            else o_quantize_q8(s->xb + (size_t)t * d, d, s->xq + (size_t)t * d, s->xqs + (size_t)t * (d / 32));
+        }
+        mm(s, fa, &L->fa, nt);
+        mm(s, bvec, &L->kb, nt);
+    } else {
+        /* one quantization of xb shared by q/k/v/f_a/b/g (:615-633) */
+        quant_rows(s, s->xb, m->d, nt);
+        mm(s, q, &L->kq, nt);
+        mm(s, k, &L->kk, nt);
+        mm(s, v, &L->kv, nt);
+        mm(s, fa, &L->fa, nt);
+        mm(s, bvec, &L->kb, nt);
+        mm(s, g, &L->kg, nt);
+    }
     tap("kq", layer, q, key); tap("kk", layer, k, key); tap("kv", layer, v, value);
     tap("kfa", layer, fa, m->gate_rank); tap("kb", layer, bvec, nv); tap("kg", layer, g, value);
     /* causal conv + SiLU, token-serial over the ring (:680-755) */
@@ -924,8 +1054,27 @@ static void forward_kda(OState *s, const OLayer *L, int li, int nt, int advance,
             o_rmsnorm_gated(ssm_out + (size_t)t * value + (size_t)h * vd,
                             ssm_out + (size_t)t * value + (size_t)h * vd,
                             g + (size_t)t * value + (size_t)h * vd, L->o_norm, vd, m->eps);
-    tap("sgdn", layer, ssm_out, value);
-    quant_rows(s, ssm_out, value, nt);
+    if (m->use_subn) {
+        /* o_proj's own RMSNorm over the whole value row, then the block
+         * Hadamard quantization, or the plain one when hadamard_o <= 1
+         * (:954-996) */
+        const int tok = subn_tok(m), gw = tok ? 0 : 32;
+        for (int t = 0; t < nt; t++) {
+            float *row = ssm_out + (size_t)t * value;
+            o_rmsnorm(row, row, L->kn_o, value, m->eps);
+            if (m->hadamard_o > 1)
+                o_subn_fwht_quant(row, value, m->hadamard_o, gw, s->xq + (size_t)t * value,
+                                  s->xqs + (size_t)t * (value / 32));
+            else if (tok)
+                o_quantize_q8_tok(row, value, s->xq + (size_t)t * value, s->xqs + (size_t)t * (value / 32));
+            else
+                o_quantize_q8(row, value, s->xq + (size_t)t * value, s->xqs + (size_t)t * (value / 32));
+        }
+        tap("sgdn", layer, ssm_out, value);
+    } else {
+        tap("sgdn", layer, ssm_out, value);
+        quant_rows(s, ssm_out, value, nt);
+    }
     mm(s, s->xb2, &L->ko, nt);
 }
 
@@ -941,10 +1090,18 @@ static void forward_attn(OState *s, const OLayer *L, int plane, int pos0, int nt
     float *kscale = s->ks + (size_t)plane * s->seq_len * kvd / 32;
     float *vscale = s->vs + (size_t)plane * s->seq_len * kvd / 32;
     float scale = o_rsqrt((float)hd);              /* attn_scale, src/forward_state.c:1408 */
-    quant_rows(s, s->xb, d, nt);
-    mm(s, kt, &L->k, nt);
-    mm(s, vt, &L->v, nt);
-    if (!kv_only) mm(s, qg, &L->q, nt);
+    if (m->use_subn) {
+        /* SubLN (:787-822): q/k/v each normalize the raw residual with their
+         * own weight, per-32 quantization */
+        if (!kv_only) subn_proj(s, s->xb, L->sn_q, &L->q, qg, nt, 0, s->xb2);
+        subn_proj(s, s->xb, L->sn_k, &L->k, kt, nt, 0, s->xb2);
+        subn_proj(s, s->xb, L->sn_v, &L->v, vt, nt, 0, s->xb2);
+    } else {
+        quant_rows(s, s->xb, d, nt);
+        mm(s, kt, &L->k, nt);
+        mm(s, vt, &L->v, nt);
+        if (!kv_only) mm(s, qg, &L->q, nt);
+    }
     for (int t = 0; t < nt; t++) {
         int pos = pos0 + t;
         float *qgt = qg + (size_t)t * qgd, *qht = qh + (size_t)t * qd;
@@ -996,6 +1153,8 @@ static void forward_attn(OState *s, const OLayer *L, int plane, int pos0, int nt
         }
     }
     tap("ax", layer, ao, qd);
+    if (m->use_subn)                                      /* o_proj's own norm (:1015-1024) */
+        for (int t = 0; t < nt; t++) o_rmsnorm(ao + (size_t)t * qd, ao + (size_t)t * qd, L->sn_o, qd, m->eps);
     quant_rows(s, ao, qd, nt);
     mm(s, s->xb2, &L->o, nt);
 }
@@ -1035,9 +1194,17 @@ static void forward_moe(OState *s, const OLayer *L, int nt, int layer) {
     float *rl = s->t0, *latx = s->t1, *laty = s->t2, *h1 = s->t3, *h3 = s->t4, *h2 = s->t5;
     int8_t lq[2048]; float lqs[64];
     int8_t hq[4096]; float hqs[128];
-    quant_rows(s, s->xb, d, nt);                          /* shared by router, down, shared expert */
-    mm(s, rl, &L->router, nt);
-    mm(s, latx, &L->down, nt);
+    float *nx = (float *)malloc(sizeof(float) * (size_t)nt * d);
+    if (m->use_subn) {
+        /* SubLN (:349-389): the router and the latent down-projection each
+         * normalize the raw residual with their own weight */
+        subn_proj(s, s->xb, L->mn_gate, &L->router, rl, nt, 0, nx);
+        subn_proj(s, s->xb, L->mn_down, &L->down, latx, nt, 0, nx);
+    } else {
+        quant_rows(s, s->xb, d, nt);                      /* shared by router, down, shared expert */
+        mm(s, rl, &L->router, nt);
+        mm(s, latx, &L->down, nt);
+    }
     tap("mrt", layer, rl, E); tap("mlat", layer, latx, lat);
     for (int t = 0; t < nt; t++) {
         int idx[16]; float w[16];
@@ -1056,34 +1223,71 @@ static void forward_moe(OState *s, const OLayer *L, int nt, int layer) {
             for (int v = 0; v < lat; v++) ly[v] += w[kk] * h2[v];
         }
     }
-    /* shared expert gate/up read the router's quantization of xb */
     {
         float *sgo = (float *)malloc(sizeof(float) * (size_t)nt * sw);
         float *suo = (float *)malloc(sizeof(float) * (size_t)nt * sw);
         float *sdo = (float *)malloc(sizeof(float) * (size_t)nt * d);
         tap("mrou", layer, laty, lat);
-        mm(s, sgo, &L->sg, nt);
-        mm(s, suo, &L->su, nt);
+        if (m->use_subn) {
+            /* shared gate / up with their own norms (:455-480); the routed
+             * output's own norm before up_proj (:418-430) */
+            subn_proj(s, s->xb, L->mn_sg, &L->sg, sgo, nt, 0, nx);
+            subn_proj(s, s->xb, L->mn_su, &L->su, suo, nt, 0, nx);
+            for (int t = 0; t < nt; t++)
+                o_rmsnorm(laty + (size_t)t * lat, laty + (size_t)t * lat, L->mn_up, lat, m->eps);
+        } else {
+            /* shared expert gate/up read the router's quantization of xb */
+            mm(s, sgo, &L->sg, nt);
+            mm(s, suo, &L->su, nt);
+        }
         quant_rows(s, laty, lat, nt);
         mm(s, s->xb2, &L->up, nt);
         for (int i = 0; i < nt * sw; i++) sgo[i] = o_silu(sgo[i]) * suo[i];
+        if (m->use_subn)                                  /* shared down's own norm (:515-525) */
+            for (int t = 0; t < nt; t++)
+                o_rmsnorm(sgo + (size_t)t * sw, sgo + (size_t)t * sw, L->mn_sd, sw, m->eps);
         quant_rows(s, sgo, sw, nt);
         mm(s, sdo, &L->sd, nt);
         for (int i = 0; i < nt * d; i++) s->xb2[i] += sdo[i];
         free(sgo); free(suo); free(sdo);
     }
+    free(nx);
 }
 
-/* dense_ffn_step, use_subn = 0 (src/forward_kda.c:1089-1250). */
-static void dense_ffn(OState *s, const QMat *gp, const QMat *up, const QMat *dp, int nt) {
+/* dense_ffn_step (src/forward_kda.c:1089-1250).  SubLN: gate and up each
+ * normalize the raw input with their own weight and quantize it with one
+ * scale per row (the float arm's lz_quantize_q8_tok, :1102-1160); the
+ * SwiGLU output gets down's own norm, then the block Hadamard quantization
+ * (hadamard_down > 1), else the plain one (:1195-1240). */
+static void dense_ffn(OState *s, const OLayer *F, const QMat *gp, const QMat *up, const QMat *dp, int nt) {
     const OModel *m = s->m;
     int inter = gp->rows;
     float *hb = s->t0, *hb2 = s->t1;
-    quant_rows(s, s->xb, m->d, nt);
-    mm(s, hb, gp, nt);
-    mm(s, hb2, up, nt);
+    if (m->use_subn) {
+        subn_proj(s, s->xb, F->fn_gate, gp, hb, nt, 1, s->xb2);
+        subn_proj(s, s->xb, F->fn_up, up, hb2, nt, 1, s->xb2);
+    } else {
+        quant_rows(s, s->xb, m->d, nt);
+        mm(s, hb, gp, nt);
+        mm(s, hb2, up, nt);
+    }
     for (int i = 0; i < nt * inter; i++) hb[i] = o_silu(hb[i]) * hb2[i];
-    quant_rows(s, hb, inter, nt);
+    if (m->use_subn) {
+        const int tok = subn_tok(m), gw = tok ? 0 : 32;
+        for (int t = 0; t < nt; t++) {
+            float *row = hb2 + (size_t)t * inter;
+            o_rmsnorm(row, hb + (size_t)t * inter, F->fn_down, inter, m->eps);
+            if (m->hadamard_down > 1)
+                o_subn_fwht_quant(row, inter, m->hadamard_down, gw, s->xq + (size_t)t * inter,
+                                  s->xqs + (size_t)t * (inter / 32));
+            else if (tok)
+                o_quantize_q8_tok(row, inter, s->xq + (size_t)t * inter, s->xqs + (size_t)t * (inter / 32));
+            else
+                o_quantize_q8(row, inter, s->xq + (size_t)t * inter, s->xqs + (size_t)t * (inter / 32));
+        }
+    } else {
+        quant_rows(s, hb, inter, nt);
+    }
     mm(s, s->xb2, dp, nt);
 }
 
@@ -1110,16 +1314,22 @@ static int forward_chunk(OState *s, const int *tokens, int nt, int pos0, float *
     tap("emb", -1, s->x, d);
     for (int l = 0; l < m->n_layers; l++) {
         const OLayer *L = &m->L[l];
-        for (int t = 0; t < nt; t++)
-            o_rmsnorm(s->xb + (size_t)t * d, s->x + (size_t)t * d, L->in_norm, d, m->eps);
+        if (m->use_subn)                                 /* SubLN: no pre-layer norm (:1426-1449) */
+            memcpy(s->xb, s->x, sizeof(float) * (size_t)nt * d);
+        else
+            for (int t = 0; t < nt; t++)
+                o_rmsnorm(s->xb + (size_t)t * d, s->x + (size_t)t * d, L->in_norm, d, m->eps);
         tap("an", l, s->xb, d);
         if (L->type == 1) forward_attn(s, L, s->full_index[l], pos0, nt, 0, l);
         else forward_kda(s, L, s->lin_index[l], nt, all_logits, base, l);
         tap("blk", l, s->xb2, d);
         for (int i = 0; i < nt * d; i++) s->x[i] += s->xb2[i];
         tap("res", l, s->x, d);
-        for (int t = 0; t < nt; t++)
-            o_rmsnorm(s->xb + (size_t)t * d, s->x + (size_t)t * d, L->post_norm, d, m->eps);
+        if (m->use_subn)                                 /* (:1535-1542) */
+            memcpy(s->xb, s->x, sizeof(float) * (size_t)nt * d);
+        else
+            for (int t = 0; t < nt; t++)
+                o_rmsnorm(s->xb + (size_t)t * d, s->x + (size_t)t * d, L->post_norm, d, m->eps);
         tap("pn", l, s->xb, d);
         forward_moe(s, L, nt, l);
         tap("ffn", l, s->xb2, d);
@@ -1204,11 +1414,13 @@ ORA_API float *ora_mtp_draft_step(void *hs, int tok, int pos) {
     o_rmsnorm(concat + d, s->mtp_chain, m->mtp_pre_h, d, m->eps);
     o_quantize_q8(concat, 2 * d, s->xq, s->xqs);
     o_matmul_q8(mtp_x, s->xq, s->xqs, m->mtp_fc.q, m->mtp_fc.s, 2 * d, d, 1, NULL);
-    o_rmsnorm(s->xb, mtp_x, m->mtp.in_norm, d, m->eps);
+    if (m->use_subn) memcpy(s->xb, mtp_x, sizeof(float) * (size_t)d);   /* (:82-88) */
+    else o_rmsnorm(s->xb, mtp_x, m->mtp.in_norm, d, m->eps);
     forward_attn(s, &m->mtp, m->n_full, pos, 1, 0, -1);
     for (int i = 0; i < d; i++) mtp_x[i] += s->xb2[i];
-    o_rmsnorm(s->xb, mtp_x, m->mtp.post_norm, d, m->eps);
-    dense_ffn(s, &m->mtp_gate, &m->mtp_up, &m->mtp_down, 1);
+    if (m->use_subn) memcpy(s->xb, mtp_x, sizeof(float) * (size_t)d);   /* (:99-105) */
+    else o_rmsnorm(s->xb, mtp_x, m->mtp.post_norm, d, m->eps);
+    dense_ffn(s, &m->mtp, &m->mtp_gate, &m->mtp_up, &m->mtp_down, 1);
     for (int i = 0; i < d; i++) mtp_x[i] += s->xb2[i];
     o_rmsnorm(s->mtp_chain, mtp_x, m->mtp_norm, d, m->eps);
     o_quantize_q8(s->mtp_chain, d, s->xq, s->xqs);
@@ -1239,8 +1451,11 @@ ORA_API int ora_mtp_prefill(void *hs, const float *h_all, const int *next, int n
             o_quantize_q8(concat, 2 * d, s->xq, s->xqs);
             o_matmul_q8(mx + (size_t)t * d, s->xq, s->xqs, m->mtp_fc.q, m->mtp_fc.s, 2 * d, d, 1, NULL);
         }
-        for (int t = 0; t < k; t++)
-            o_rmsnorm(s->xb + (size_t)t * d, mx + (size_t)t * d, m->mtp.in_norm, d, m->eps);
+        if (m->use_subn)                                 /* (:600-611) */
+            memcpy(s->xb, mx, sizeof(float) * (size_t)k * d);
+        else
+            for (int t = 0; t < k; t++)
+                o_rmsnorm(s->xb + (size_t)t * d, mx + (size_t)t * d, m->mtp.in_norm, d, m->eps);
         if (pos0 + done + k > s->seq_len) { free(concat); free(mx); return 1; }
         forward_attn(s, &m->mtp, m->n_full, pos0 + done, k, 1, -1);
         done += k;

@@ -40,3 +40,13 @@ def tiny(pkg, model_root):
 @pytest.fixture(scope="session")
 def server(pkg, model_root):
     return pkg.ensure_model(os.path.join(model_root, "server"), 4, seed=1234)
+
+
+@pytest.fixture(scope="session")
+def micro_subln(pkg, model_root):
+    return pkg.ensure_model(os.path.join(model_root, "micro_subln"), 12, seed=1234)
+
+
+@pytest.fixture(scope="session")
+def subln(pkg, model_root):
+    return pkg.ensure_model(os.path.join(model_root, "subln"), 5, seed=1234)

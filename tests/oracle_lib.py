@@ -54,6 +54,7 @@ def lib():
             "ora_conv_state": (_FP, [_P, C.c_int]),
             "ora_mtp_logits": (_FP, [_P]),
             "ora_mtp_hidden": (_FP, [_P]),
+            "ora_draft_logits": (_FP, [_P]),
             "ora_mtp_chain": (_FP, [_P]),
             "ora_logits": (_FP, [_P]),
             "ora_kv_plane": (None, [_P, C.c_int, C.c_int, _P, _FP, _P, _FP]),
@@ -67,6 +68,7 @@ def lib():
             "o_l2norm": (None, [_FP, _FP, C.c_int, C.c_float]),
             "o_softmax": (None, [_FP, C.c_int]),
             "o_quantize_q8": (None, [_FP, C.c_int, _P, _FP]),
+            "o_quantize_q8_tok": (None, [_FP, C.c_int, _P, _FP]),
             "o_fwht_i32": (None, [_IP, _IP, C.c_int]),
             "o_fwht_f32": (None, [_FP, C.c_int]),
             "o_subn_fwht_quant": (None, [_FP, C.c_int, C.c_int, C.c_int, _P, _FP]),

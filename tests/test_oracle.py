@@ -603,3 +603,95 @@ def test_load_config_reads_the_header(pkg, model_root, micro):
     err = C.create_string_buffer(256)
     assert lib.lz_load_config(C.byref(c), os.path.join(micro, "absent.bin").encode(), err, 256) == 1
     assert b"cannot open" in err.value
+
+
+# ------------------------------------------------------------- SubLN path ---
+
+def _greedy_rounds_oracle(model, prompt, k, n_rounds):
+    """The harness's greedy loop (oracle/ref_harness.c cmd_gen) driven round
+    by round on the oracle: the capture logits, then each round's verify
+    logits, verify hidden rows and last draft logits."""
+    o = Oracle(model)
+    out = {}
+    try:
+        n = len(prompt)
+        assert o.session_start(prompt) == 0
+        lg = o.forward_capture(prompt[-1], n - 1)
+        out["capture0"] = lg
+        anchor, anchor_pos = int(np.argmax(lg)), n - 1
+        L = OL.lib()
+        for r in range(n_rounds):
+            rc, toks, na, npos, ke = o.spec_round(anchor, anchor_pos, k)
+            assert rc > 0
+            out[f"verify{r}"] = np.ctypeslib.as_array(L.ora_mtp_logits(o.s), shape=(8, o.V))[:ke + 1].copy()
+            out[f"vhidden{r}"] = np.ctypeslib.as_array(L.ora_mtp_hidden(o.s), shape=(8, o.d))[:ke + 1].copy()
+            out[f"draft{r}"] = np.ctypeslib.as_array(L.ora_draft_logits(o.s), shape=(o.V,)).copy()
+            anchor, anchor_pos = int(toks[na]), npos
+    finally:
+        o.close()
+    return out
+
+
+@pytest.mark.parametrize("name,vocab,k", [("micro", 512, 3), ("echo", 64, 3), ("tiny", 8192, 2),
+                                          ("micro_subln", 512, 3), ("subln", 8192, 3), ("subln", 8192, 1)])
+def test_rounds_bitwise_vs_reference(pkg, request, tmp_path, name, vocab, k):
+    """The capture, every round's verify logits and hidden rows and the last
+    draft step's logits equal the reference engine's bit for bit, round
+    after round (not only the emitted tokens).  micro and echo have 32-wide
+    projections (expert w1/w3, f_b), whose single-group epilogue takes the
+    reference's r == 1 branch; echo accepts drafts, so later rounds start
+    from rolled-back and caught-up state.  subln / micro_subln have
+    use_subn = 1: per-projection input norms, no pre-layer norms, the
+    block-Hadamard quantization of the KDA o_proj and MTP down_proj inputs,
+    per-token scales on the MTP FFN gate/up inputs."""
+    if not OL.have_reference():
+        pytest.skip("reference build absent; the SubLN golden fixtures cover this")
+    model = request.getfixturevalue(name)
+    prompt = pkg.prompt_tokens(21, 40, vocab)
+    n_rounds = 4
+    r = OL.reference_generate(model, prompt, k, 12, tmpdir=str(tmp_path), extra=("--dump-rounds", str(n_rounds)))
+    mine = _greedy_rounds_oracle(model, prompt, k, n_rounds)
+    for tag, got in mine.items():
+        want = np.fromfile(f"{r['prefix']}.{tag}.bin", np.float32).reshape(got.shape)
+        assert np.array_equal(bits(got), bits(want)), tag
+
+
+def test_subln_generation_identical_to_reference_engine(pkg, micro_subln, subln, tmp_path):
+    if not OL.have_reference():
+        pytest.skip("reference build absent; the SubLN golden fixtures cover this")
+    for model, V, k, temp in ((micro_subln, 512, 2, 0.8), (subln, 8192, 3, 0.0), (subln, 8192, 2, 0.8)):
+        prompt = pkg.prompt_tokens(3, 48, V)
+        toks, ke, na, rng = gen_case(model, prompt, k, 40, temp, 0.95 if temp else 1.0, seed=9)
+        r = OL.reference_generate(model, prompt, k, 40, temp, 0.95 if temp else 1.0, seed=9, tmpdir=str(tmp_path))
+        n = min(len(toks), len(r["tokens"]))
+        assert n >= 40 and np.array_equal(toks[:n], r["tokens"][:n]), (model, k, temp)
+        assert np.array_equal(ke, r["k_eff"]) and np.array_equal(na, r["n_accept"]) and rng == r["rng"]
+
+
+def test_quantize_q8_tok_bitwise_vs_reference_and_closed_form():
+    """lz_quantize_q8_tok: one scale (the whole row's amax / 127) replicated
+    into every 32-slot, codes as the per-32 quantizer's element loop."""
+    L = OL.lib()
+    rng = np.random.default_rng(5)
+    for n in (32, 64, 256, 1024):
+        for scale in (1e-3, 1.0, 3e4):
+            x = (rng.standard_normal(n) * scale).astype(np.float32)
+            q = np.zeros(n, np.int8)
+            s = np.zeros(n // 32, np.float32)
+            L.o_quantize_q8_tok(fp(x), n, q.ctypes.data, fp(s))
+            amax = np.float32(np.max(np.abs(x)))
+            assert np.all(s == s[0]) and s[0] == np.float32(amax * np.float32(1.0 / 127.0))
+            assert np.max(np.abs(q.astype(np.int32))) == 127
+            assert np.all(np.abs(q.astype(np.float64) * s[0] - x) <= 0.5001 * s[0] + 1e-30)
+            if OL.have_reference():
+                R = ref()
+                R.lz_quantize_q8_tok.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p]
+                q2 = np.zeros(n, np.int8)
+                s2 = np.zeros(n // 32, np.float32)
+                R.lz_quantize_q8_tok(x.ctypes.data, n, q2.ctypes.data, s2.ctypes.data)
+                assert np.array_equal(q, q2) and np.array_equal(bits(s), bits(s2))
+    z = np.zeros(64, np.float32)
+    q = np.ones(64, np.int8)
+    s = np.zeros(2, np.float32)
+    L.o_quantize_q8_tok(fp(z), 64, q.ctypes.data, fp(s))
+    assert not q.any() and np.all(s == 1.0)
