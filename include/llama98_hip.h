@@ -60,6 +60,7 @@ typedef struct {
     int moe_intermediate_size, moe_shared_width, mtp_intermediate_size, mtp_n_layers;
     float rms_norm_eps, rope_theta;
     int layer_types[128];
+    int use_subn, hadamard_o, hadamard_down;   /* SubLN (src/model.h: use_subn, hadamard_o/_down) */
 } LZModelConfig;
 
 /* Caller-allocated, as in the reference: LZModel m; lz_open(&m, dir, ...). */

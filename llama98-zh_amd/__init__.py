@@ -35,7 +35,8 @@ class LZModelConfig(C.Structure):
         "attn_q_dim", "attn_qgate_dim", "attn_kv_dim", "lin_key_dim", "lin_value_dim", "lin_conv_dim",
         "kda_gate_rank", "num_experts", "num_experts_per_token", "moe_latent_dim",
         "moe_intermediate_size", "moe_shared_width", "mtp_intermediate_size", "mtp_n_layers")] + [
-        ("rms_norm_eps", C.c_float), ("rope_theta", C.c_float), ("layer_types", C.c_int * 128)]
+        ("rms_norm_eps", C.c_float), ("rope_theta", C.c_float), ("layer_types", C.c_int * 128),
+        ("use_subn", C.c_int), ("hadamard_o", C.c_int), ("hadamard_down", C.c_int)]
 
 
 class LZModel(C.Structure):
@@ -399,12 +400,17 @@ class Engine:
             raise RuntimeError(f"l98_greedy_rounds_batch failed: {n}")
         return ms.value, [toks[i, :n_out[i]].copy() for i in range(len(states))]
 
-    def generate_host(self, prompt, k, n_new, p_min=0.0, n_min=0, brk=0, skipc=0):
+    def generate_host(self, prompt, k, n_new, p_min=0.0, n_min=0, brk=0, skipc=0, on_round=None):
         """The reference's --spec generation loop driven from the host through
         the reference entry points (lz_forward_batch_capture, lz_mtp_prefill,
         lz_forward_capture, lz_sample_argmax, lz_spec_round), greedy, as
         src/generate.c:1822-2106 drives them; a discarded round records
-        n_accept -1.  Returns (tokens, k_eff per round, n_accept per round)."""
+        n_accept -1.  on_round(tag, array), when given, receives what the
+        reference harness's --dump-rounds writes: "capture<r>" logits of each
+        capture and, after each round r that emitted, "verify<r>" and
+        "vhidden<r>" (the state's mtp_logits / mtp_verify_hidden rows) and
+        "draft<r>" (mtp_draft_logits).  Returns (tokens, k_eff per round,
+        n_accept per round)."""
         prompt = np.ascontiguousarray(prompt, np.int32)
         n_prompt = len(prompt)
         self.reset()
@@ -421,6 +427,8 @@ class Engine:
                 lg = self.forward_capture(token, pos)
                 if lg is None:
                     raise RuntimeError("lz_forward_capture failed")
+                if on_round:
+                    on_round(f"capture{len(ke)}", lg)
                 anchor_pos = pos
                 anchor = self.lib.lz_sample_argmax(_fp(lg), self.V)
                 toks.append(anchor)
@@ -429,6 +437,12 @@ class Engine:
             r, out, n_acc, new_pos, k_eff = self.spec_round(anchor, anchor_pos, k, p_min, n_min, brk, skipc)
             if r < 0:
                 raise RuntimeError(f"lz_spec_round failed: {r}")
+            if on_round and r > 0:
+                rnd = len(ke)
+                on_round(f"verify{rnd}", np.ctypeslib.as_array(self.s.mtp_logits, shape=(k_eff + 1, self.V)).copy())
+                on_round(f"vhidden{rnd}",
+                         np.ctypeslib.as_array(self.s.mtp_verify_hidden, shape=(k_eff + 1, self.d)).copy())
+                on_round(f"draft{rnd}", np.ctypeslib.as_array(self.s.mtp_draft_logits, shape=(self.V,)).copy())
             ke.append(k_eff)
             na.append(n_acc if r > 0 else -1)
             have_seed = r > 0

@@ -442,11 +442,15 @@ __device__ __forceinline__ uint32_t octet_max(uint32_t m) {
 // as 4 consecutive elements per lane over an aligned lane octet.  Returns the
 // four int8 packed little-endian; *sg receives the group scale.  Every lane
 // of the octet must execute it.
-__device__ __forceinline__ uint32_t quant_octet(float4 v, float *sg_out) {
+__device__ __forceinline__ uint32_t abs_bits4(float4 v) {
+    return umax(umax(u_from_f(v.x) & 0x7FFFFFFFu, u_from_f(v.y) & 0x7FFFFFFFu),
+                umax(u_from_f(v.z) & 0x7FFFFFFFu, u_from_f(v.w) & 0x7FFFFFFFu));
+}
+
+// The element loop of the quantization for a group whose amax is given
+// (q8_group_scale's decisions, then the rounding of each element).
+__device__ __forceinline__ uint32_t quant4_amax(float4 v, float amax, float *sg_out) {
     const float INV127 = 1.0f / 127.0f;
-    uint32_t m = umax(umax(u_from_f(v.x) & 0x7FFFFFFFu, u_from_f(v.y) & 0x7FFFFFFFu),
-                      umax(u_from_f(v.z) & 0x7FFFFFFFu, u_from_f(v.w) & 0x7FFFFFFFu));
-    const float amax = f_from_u(octet_max(m));
     float sg, inv;
     bool fast;
     if (amax > 0.0f) {
@@ -477,6 +481,10 @@ __device__ __forceinline__ uint32_t quant_octet(float4 v, float *sg_out) {
     return packed;
 }
 
+__device__ __forceinline__ uint32_t quant_octet(float4 v, float *sg_out) {
+    return quant4_amax(v, f_from_u(octet_max(abs_bits4(v))), sg_out);
+}
+
 // epi_q8 of a row with one 32-element group (a per-row weight scale over
 // in_dim == 32, so r = gs / 32 == 1: src/ops_epi.c:1012-1021): four
 // accumulators, only the first of which takes a term,
@@ -495,35 +503,51 @@ __device__ __forceinline__ float epi_one_group(int acc, float xs, float ws) {
 // (x*inv)*(1+w)), then the optional store of o and its per-32 quantization.
 // The sum is wave_sum_nonneg's (sq: ps_row_floats<4 * PJ>() floats, rec its
 // table).  n % 32 == 0.
+// norm == false skips the norm (o = v: the row is only stored and/or
+// quantized); tok selects one scale for the whole row (lz_quantize_q8_tok,
+// src/ops_quant.c:2284-2314: the row's amax, the same element loop, the
+// scale in every 32-slot) instead of one per 32 elements.
 template <int PJ>
 __device__ __forceinline__ void norm_row(const float4 (&v)[PJ], const float4 (&wn)[PJ], int n, float eps,
                                          float *sq, PsRec *rec, float *s_inv, float *__restrict__ out,
-                                         int8_t *__restrict__ xq, float *__restrict__ xqs) {
+                                         int8_t *__restrict__ xq, float *__restrict__ xqs, bool norm = true,
+                                         bool tok = false) {
     const int lane = threadIdx.x, nf = n >> 2;
+    float inv = 1.0f;
+    if (norm) {
 #pragma unroll
-    for (int j = 0; j < PJ; j++) {
-        const int f = lane + 64 * j;
-        if (f < nf) *reinterpret_cast<float4 *>(sq + ps_slot<4 * PJ>(4 * f)) =
-            make_float4(v[j].x * v[j].x, v[j].y * v[j].y, v[j].z * v[j].z, v[j].w * v[j].w);
+        for (int j = 0; j < PJ; j++) {
+            const int f = lane + 64 * j;
+            if (f < nf) *reinterpret_cast<float4 *>(sq + ps_slot<4 * PJ>(4 * f)) =
+                make_float4(v[j].x * v[j].x, v[j].y * v[j].y, v[j].z * v[j].z, v[j].w * v[j].w);
+        }
+        __syncthreads();
+        const float ss = wave_sum_nonneg<4 * PJ>(sq, n, rec);
+        if (lane == 0) *s_inv = d_rsqrt(d_ss_over_n(ss, n) + eps);
+        __syncthreads();
+        inv = *s_inv;
     }
-    __syncthreads();
-    const float ss = wave_sum_nonneg<4 * PJ>(sq, n, rec);
-    if (lane == 0) *s_inv = d_rsqrt(d_ss_over_n(ss, n) + eps);
-    __syncthreads();
-    const float inv = *s_inv;
+    float4 o[PJ];
+    uint32_t am = 0;
 #pragma unroll
     for (int j = 0; j < PJ; j++) {
         const int f = lane + 64 * j;
-        const float4 o = make_float4(v[j].x * inv * (1.0f + wn[j].x), v[j].y * inv * (1.0f + wn[j].y),
-                                     v[j].z * inv * (1.0f + wn[j].z), v[j].w * inv * (1.0f + wn[j].w));
-        if (out && f < nf) reinterpret_cast<float4 *>(out)[f] = o;
-        if (xq) {
-            float sg;
-            const uint32_t q = quant_octet(o, &sg);
-            if (f < nf) {
-                reinterpret_cast<uint32_t *>(xq)[f] = q;
-                if (!(f & 7)) xqs[f >> 3] = sg;
-            }
+        o[j] = norm ? make_float4(v[j].x * inv * (1.0f + wn[j].x), v[j].y * inv * (1.0f + wn[j].y),
+                                  v[j].z * inv * (1.0f + wn[j].z), v[j].w * inv * (1.0f + wn[j].w))
+                    : v[j];
+        if (out && f < nf) reinterpret_cast<float4 *>(out)[f] = o[j];
+        if (f < nf) am = umax(am, abs_bits4(o[j]));
+    }
+    if (!xq) return;
+    const float row_amax = tok ? wave_max_u(am, 64) : 0.0f;
+#pragma unroll
+    for (int j = 0; j < PJ; j++) {
+        const int f = lane + 64 * j;
+        float sg;
+        const uint32_t q = tok ? quant4_amax(o[j], row_amax, &sg) : quant_octet(o[j], &sg);
+        if (f < nf) {
+            reinterpret_cast<uint32_t *>(xq)[f] = q;
+            if (!(f & 7)) xqs[f >> 3] = sg;
         }
     }
 }

@@ -118,6 +118,14 @@ struct DLayer {
     DMat router, down, up, sg, su, sd;
     float *bias = nullptr;
     ExpertBank w1{}, w2{}, w3{};
+    // SubLN per-projection input norms (use_subn): attention q/k/v/o, KDA
+    // q/k/v/g/o, MoE router / routed down / routed up / shared gate / up /
+    // down; the MTP block's dense FFN gate / up / down
+    float *sn_q = nullptr, *sn_k = nullptr, *sn_v = nullptr, *sn_o = nullptr;
+    float *kn_q = nullptr, *kn_k = nullptr, *kn_v = nullptr, *kn_g = nullptr, *kn_o = nullptr;
+    float *mn_gate = nullptr, *mn_down = nullptr, *mn_up = nullptr, *mn_sg = nullptr, *mn_su = nullptr,
+          *mn_sd = nullptr;
+    float *fn_gate = nullptr, *fn_up = nullptr, *fn_down = nullptr;
 };
 
 struct DModel {
@@ -240,6 +248,8 @@ struct HostLayer {
     HostTensor kq, kk, kv, convq, convk, convv, a_log, fa, fb, dt_bias, kb, kg, o_norm, ko;
     HostTensor router, bias, down, up, sg, su, sd;
     std::vector<HostTensor> w1, w2, w3;
+    HostTensor sn_q, sn_k, sn_v, sn_o, kn_q, kn_k, kn_v, kn_g, kn_o;
+    HostTensor mn_gate, mn_down, mn_up, mn_sg, mn_su, mn_sd, fn_gate, fn_up, fn_down;
 };
 
 // Parses the version-5 model.bin (reference loader order: header
@@ -253,7 +263,8 @@ int parse_model(Bin &b, LZModelConfig &c, HostTensor &embed, HostTensor &fnorm,
     int ver = b.i32();
     if (ver != 5) { set_err(err, errlen, "unsupported model.bin version %d", ver); return LZ_ERR_BIN_VERSION; }
     c.vocab_size = b.i32(); c.hidden_size = b.i32(); c.n_layers = b.i32(); c.seq_len = b.i32();
-    c.n_heads = b.i32(); c.n_kv_heads = b.i32(); c.head_dim = b.i32(); (void)b.i32();
+    c.n_heads = b.i32(); c.n_kv_heads = b.i32(); c.head_dim = b.i32();
+    const int inter_word = b.i32();                 // intermediate_size (no dense body layer here)
     c.lin_n_k_heads = b.i32(); c.lin_n_v_heads = b.i32(); c.lin_k_head_dim = b.i32();
     c.lin_v_head_dim = b.i32(); c.conv_kernel = b.i32(); c.n_linear_layers = b.i32();
     c.n_full_layers = b.i32(); (void)b.i32(); (void)b.i32(); (void)b.i32();
@@ -271,13 +282,42 @@ int parse_model(Bin &b, LZModelConfig &c, HostTensor &embed, HostTensor &fnorm,
     c.mtp_n_layers = b.i32(); c.mtp_intermediate_size = b.i32();
     int rope_type = b.i32();
     for (int i = 0; i < 4; i++) (void)b.i32();
-    int use_subn = b.i32();
-    for (int i = 0; i < 9; i++) (void)b.i32();    // hadamard x2, mla x2, kv_share, sink, gr, ced x2
+    c.use_subn = b.i32();
+    c.hadamard_o = b.i32();
+    c.hadamard_down = b.i32();
+    for (int i = 0; i < 7; i++) (void)b.i32();    // mla x2, kv_share, sink, gr, ced x2
     for (int i = 0; i < 128 * 3 + 6 + 128; i++) (void)b.i32();
     if (b.bad) { set_err(err, errlen, "truncated header"); return LZ_ERR_BIN_OPEN; }
+    // resolve_hadamard (src/model.c:139-182): -1 derives the block from the
+    // widths; an explicit block is 0 (off) or a power of two dividing its
+    // width (lin_value_dim for hadamard_o, intermediate_size and the MTP
+    // width for hadamard_down).
+    {
+        auto pow2_div = [](int blk, int dim) { return blk == 0 || (blk > 0 && !(blk & (blk - 1)) && dim > 0 && dim % blk == 0); };
+        if (c.hadamard_o == -1) {
+            int oblk = c.num_experts == 0 ? c.lin_value_dim : 0;
+            c.hadamard_o = (oblk >= 2 && !(oblk & (oblk - 1))) ? oblk : 0;
+        }
+        if (c.hadamard_down == -1) {
+            int dblk = 512;
+            while (dblk > 1 && inter_word % dblk) dblk >>= 1;
+            c.hadamard_down = dblk == 1 ? 0 : dblk;
+        }
+        if (!pow2_div(c.hadamard_o, c.lin_value_dim) || !pow2_div(c.hadamard_down, inter_word) ||
+            (c.use_subn && c.hadamard_down > 1 && c.mtp_intermediate_size % c.hadamard_down)) {
+            set_err(err, errlen, "hadamard block does not divide its width");
+            return LZ_ERR_BIN_VERSION;
+        }
+    }
     // The variant this path implements (the synthetic configs): KDA + gated
-    // full attention, sigmoid latent MoE with a shared expert, one MTP layer.
-    if (has_lb || n_shared != 1 || first_dense != 0 || !renorm || !sig || lat_norm || use_subn ||
+    // full attention, sigmoid latent MoE with a shared expert, one MTP layer;
+    // SubLN (use_subn) on that MoE variant, whose scales are per 32 elements
+    // (the default subn scale on a model with experts).
+    if (has_lb || n_shared != 1 || first_dense != 0 || !renorm || !sig || lat_norm ||
+        (c.use_subn != 0 && c.use_subn != 1) ||
+        (c.use_subn && (c.num_experts < 1 || c.hidden_size > 2048 || c.lin_value_dim > 2048 ||
+                        c.attn_q_dim > 2048 || c.mtp_intermediate_size > 2048 || c.moe_shared_width > 2048 ||
+                        c.moe_latent_dim > 2048)) ||
         rope_type != 0 || c.mtp_n_layers != 1 || c.num_experts > MAX_EXPERTS ||
         c.num_experts_per_token > MAX_TOPK || c.lin_n_k_heads != c.lin_n_v_heads ||
         c.rotary_dim != c.head_dim || c.hidden_size % 32 || c.n_layers > 128) {
@@ -300,6 +340,10 @@ int parse_model(Bin &b, LZModelConfig &c, HostTensor &embed, HostTensor &fnorm,
             h.o = rd_q8(b, d, c.attn_q_dim);
             h.q_norm = rd_f32(b, c.head_dim);
             h.k_norm = rd_f32(b, c.head_dim);
+            if (c.use_subn) {
+                h.sn_q = rd_f32(b, d); h.sn_k = rd_f32(b, d); h.sn_v = rd_f32(b, d);
+                h.sn_o = rd_f32(b, c.attn_q_dim);
+            }
         } else if (h.type == 2) {
             int key = c.lin_key_dim, value = c.lin_value_dim, K = c.conv_kernel;
             int nvk = c.lin_n_v_heads * c.lin_k_head_dim;
@@ -317,6 +361,10 @@ int parse_model(Bin &b, LZModelConfig &c, HostTensor &embed, HostTensor &fnorm,
             h.kg = rd_q8(b, value, d);
             h.o_norm = rd_f32(b, c.lin_v_head_dim);
             h.ko = rd_q8(b, d, value);
+            if (c.use_subn) {
+                h.kn_q = rd_f32(b, d); h.kn_k = rd_f32(b, d); h.kn_v = rd_f32(b, d); h.kn_g = rd_f32(b, d);
+                h.kn_o = rd_f32(b, value);
+            }
         } else {
             set_err(err, errlen, "layer %d: unsupported layer type %d", l, h.type);
             return LZ_ERR_BIN_VERSION;
@@ -328,6 +376,10 @@ int parse_model(Bin &b, LZModelConfig &c, HostTensor &embed, HostTensor &fnorm,
         h.sg = rd_q8(b, c.moe_shared_width, d);
         h.su = rd_q8(b, c.moe_shared_width, d);
         h.sd = rd_q8(b, d, c.moe_shared_width);
+        if (c.use_subn) {
+            h.mn_gate = rd_f32(b, d); h.mn_down = rd_f32(b, d); h.mn_up = rd_f32(b, c.moe_latent_dim);
+            h.mn_sg = rd_f32(b, d); h.mn_su = rd_f32(b, d); h.mn_sd = rd_f32(b, c.moe_shared_width);
+        }
         for (int e = 0; e < c.num_experts; e++) {
             h.w1.push_back(rd_q8(b, c.moe_intermediate_size, c.moe_latent_dim));
             h.w2.push_back(rd_q8(b, c.moe_latent_dim, c.moe_intermediate_size));
@@ -337,15 +389,21 @@ int parse_model(Bin &b, LZModelConfig &c, HostTensor &embed, HostTensor &fnorm,
     mtp.type = 1;
     mtp.in_norm = rd_f32(b, d);
     mtp.post_norm = rd_f32(b, d);
+    if (c.use_subn) { mtp.fn_gate = rd_f32(b, d); mtp.fn_up = rd_f32(b, d); }
     mtp.q = rd_q8(b, c.attn_qgate_dim, d);
     mtp.k = rd_q8(b, c.attn_kv_dim, d);
     mtp.v = rd_q8(b, c.attn_kv_dim, d);
     mtp.o = rd_q8(b, d, c.attn_q_dim);
     mtp.q_norm = rd_f32(b, c.head_dim);
     mtp.k_norm = rd_f32(b, c.head_dim);
+    if (c.use_subn) {
+        mtp.sn_q = rd_f32(b, d); mtp.sn_k = rd_f32(b, d); mtp.sn_v = rd_f32(b, d);
+        mtp.sn_o = rd_f32(b, c.attn_q_dim);
+    }
     mg = rd_q8(b, c.mtp_intermediate_size, d);
     mu = rd_q8(b, c.mtp_intermediate_size, d);
     md = rd_q8(b, d, c.mtp_intermediate_size);
+    if (c.use_subn) mtp.fn_down = rd_f32(b, c.mtp_intermediate_size);
     fc = rd_q8(b, d, 2 * d);
     mn = rd_f32(b, d);
     mph = rd_f32(b, d);
@@ -392,12 +450,26 @@ void upload_all(Uploader &u, DModel *m, const HostTensor &embed, const HostTenso
         D.down = u.mat(h.down); D.up = u.mat(h.up);
         D.sg = u.mat(h.sg); D.su = u.mat(h.su); D.sd = u.mat(h.sd);
         D.w1 = u.bank(h.w1); D.w2 = u.bank(h.w2); D.w3 = u.bank(h.w3);
+        if (c.use_subn) {
+            if (h.type == 1) {
+                D.sn_q = u.vec(h.sn_q); D.sn_k = u.vec(h.sn_k); D.sn_v = u.vec(h.sn_v); D.sn_o = u.vec(h.sn_o);
+            } else {
+                D.kn_q = u.vec(h.kn_q); D.kn_k = u.vec(h.kn_k); D.kn_v = u.vec(h.kn_v); D.kn_g = u.vec(h.kn_g);
+                D.kn_o = u.vec(h.kn_o);
+            }
+            D.mn_gate = u.vec(h.mn_gate); D.mn_down = u.vec(h.mn_down); D.mn_up = u.vec(h.mn_up);
+            D.mn_sg = u.vec(h.mn_sg); D.mn_su = u.vec(h.mn_su); D.mn_sd = u.vec(h.mn_sd);
+        }
     }
     DLayer &M = m->mtp;
     M.type = 1;
     M.in_norm = u.vec(hm.in_norm); M.post_norm = u.vec(hm.post_norm);
     M.q = u.mat(hm.q); M.k = u.mat(hm.k); M.v = u.mat(hm.v); M.o = u.mat(hm.o);
     M.q_norm = u.vec(hm.q_norm); M.k_norm = u.vec(hm.k_norm);
+    if (c.use_subn) {
+        M.sn_q = u.vec(hm.sn_q); M.sn_k = u.vec(hm.sn_k); M.sn_v = u.vec(hm.sn_v); M.sn_o = u.vec(hm.sn_o);
+        M.fn_gate = u.vec(hm.fn_gate); M.fn_up = u.vec(hm.fn_up); M.fn_down = u.vec(hm.fn_down);
+    }
     m->mtp_gate = u.mat(mg); m->mtp_up = u.mat(mu); m->mtp_down = u.mat(md); m->mtp_fc = u.mat(fc);
     m->mtp_norm = u.vec(mn); m->mtp_pre_h = u.vec(mph); m->mtp_pre_e = u.vec(mpe);
     {
@@ -543,6 +615,7 @@ struct DState {
     float *vhidden, *mtp_logits, *logits, *draft_logits, *hcap;
     int8_t *xq, *xq2, *xq3, *xq4;
     float *xqs, *xqs2, *xqs3, *xqs4;
+    float *sub_a = nullptr, *sub_b = nullptr;   // SubLN float rows before their norm / transform
     int *sel_idx;
     float *sel_w;
     MoeGroups *grp;
@@ -587,7 +660,8 @@ bool carve(DState *s) {
     const int d = c.hidden_size, B = MAX_CHUNK;
     int wide = d;
     int dims[] = {2 * d, c.attn_qgate_dim, c.lin_conv_dim, c.moe_shared_width, c.mtp_intermediate_size,
-                  c.lin_n_v_heads * c.lin_k_head_dim, c.moe_intermediate_size, c.lin_value_dim};
+                  c.lin_n_v_heads * c.lin_k_head_dim, c.moe_intermediate_size, c.lin_value_dim,
+                  c.attn_q_dim, c.moe_latent_dim};
     for (int v : dims) wide = v > wide ? v : wide;
     const int pairs = B * c.num_experts_per_token;
     auto F = [&](size_t n) { return (float *)st_take(s, n * sizeof(float)); };
@@ -621,6 +695,7 @@ bool carve(DState *s) {
     s->xq2 = I8((size_t)pairs * wide); s->xqs2 = F((size_t)pairs * wide / 32);
     s->xq3 = I8((size_t)pairs * wide); s->xqs3 = F((size_t)pairs * wide / 32);
     s->xq4 = I8((size_t)B * wide); s->xqs4 = F((size_t)B * wide / 32);
+    if (c.use_subn) { s->sub_a = F((size_t)B * wide); s->sub_b = F((size_t)B * wide); }
     s->sel_idx = (int *)st_take(s, sizeof(int) * pairs);
     s->sel_w = F(pairs);
     s->grp = (MoeGroups *)st_take(s, sizeof(MoeGroups));
@@ -680,6 +755,15 @@ Prologue PC(const float *h2, const int *sel_idx, const float *sel_w, int topk) {
     return p;
 }
 
+// A norm prologue with the projection's own weight: under SubLN every
+// projection normalizes the raw residual itself (w == nullptr quantizes the
+// folded rows without a norm: the KDA f_a / b inputs).
+Prologue PW(const Prologue &in, const float *w) {
+    Prologue p = in;
+    p.w = w;
+    return p;
+}
+
 // One GEMV job: w (rows x cols) whose activations the prologue builds.
 GemvJob J(const DMat &w, float *out, int out_stride, const Prologue &pro) {
     GemvJob j{};
@@ -727,11 +811,13 @@ int attn_block(DState *s, const DLayer &L, const Prologue &in, int plane, const 
                int max_pos, bool kv_only) {
     const LZModelConfig &c = s->m->c;
     const int d = c.hidden_size;
+    const bool sub = c.use_subn != 0;      // q/k/v/o own norms (src/forward_attn.c:787-822, 1015-1024)
+    const Prologue pk = sub ? PW(in, L.sn_k) : in, pv = sub ? PW(in, L.sn_v) : in, pq = sub ? PW(in, L.sn_q) : in;
     if (kv_only)
-        CK(gemv(s, {J(L.k, s->kp, c.attn_kv_dim, in), J(L.v, s->vp, c.attn_kv_dim, in)}, nt));
+        CK(gemv(s, {J(L.k, s->kp, c.attn_kv_dim, pk), J(L.v, s->vp, c.attn_kv_dim, pv)}, nt));
     else
-        CK(gemv(s, {J(L.k, s->kp, c.attn_kv_dim, in), J(L.v, s->vp, c.attn_kv_dim, in),
-                    J(L.q, s->qg, c.attn_qgate_dim, in)}, nt));
+        CK(gemv(s, {J(L.k, s->kp, c.attn_kv_dim, pk), J(L.v, s->vp, c.attn_kv_dim, pv),
+                    J(L.q, s->qg, c.attn_qgate_dim, pq)}, nt));
     AttnArgs a{};
     a.qg = s->qg; a.kp = s->kp; a.vp = s->vp;
     a.q_norm = L.q_norm; a.k_norm = L.k_norm; a.rope_cs = s->m->rope_cs;
@@ -739,7 +825,7 @@ int attn_block(DState *s, const DLayer &L, const Prologue &in, int plane, const 
     size_t off = (size_t)plane * s->seq_len * c.attn_kv_dim;
     a.kcache = s->kq + off; a.vcache = s->vq + off;
     a.kscale = s->ks + off / 32; a.vscale = s->vs + off / 32;
-    a.out = nullptr;
+    a.out = sub ? s->sub_a : nullptr;
     a.oq = s->xq2; a.oqs = s->xqs2;
     a.ctl_pos = ctl_pos; a.pos_off = pos_off;
     a.nh = c.n_heads; a.nkv = c.n_kv_heads; a.hd = c.head_dim; a.rot = c.rotary_dim;
@@ -762,6 +848,9 @@ int attn_block(DState *s, const DLayer &L, const Prologue &in, int plane, const 
         return 0;
     }
     CK(l98k_attn(&a, nt, max_pos + 1, s->att, s->st));
+    if (sub)
+        CK(l98k_rmsnorm_ex(s->sub_a, c.attn_q_dim, nullptr, nullptr, L.sn_o, c.attn_q_dim, c.rms_norm_eps, nt,
+                           nullptr, 0, s->xq2, s->xqs2, 0, s->st));
     CK(gemv(s, {JX(L.o, s->blk, d, s->xq2, s->xqs2)}, nt));
     return 0;
 }
@@ -782,8 +871,13 @@ int kda_block(DState *s, const DLayer &L, const Prologue &in, int li, int nt, in
     const LZModelConfig &c = s->m->c;
     const int d = c.hidden_size, key = c.lin_key_dim, value = c.lin_value_dim;
     const int nv = c.lin_n_v_heads, kd = c.lin_k_head_dim, vd = c.lin_v_head_dim;
-    CK(gemv(s, {J(L.kq, s->pq, key, in), J(L.kk, s->pk, key, in), J(L.kv, s->pv, value, in),
-                J(L.fa, s->pfa, c.kda_gate_rank, in), J(L.kb, s->pb, nv, in), J(L.kg, s->pg, value, in)}, nt));
+    // SubLN: q/k/v/g normalize the raw residual with their own weights, f_a
+    // and b quantize it without a norm (src/forward_kda.c:559-612)
+    const bool sub = c.use_subn != 0;
+    auto P = [&](const float *w) { return sub ? PW(in, w) : in; };
+    CK(gemv(s, {J(L.kq, s->pq, key, P(L.kn_q)), J(L.kk, s->pk, key, P(L.kn_k)), J(L.kv, s->pv, value, P(L.kn_v)),
+                J(L.fa, s->pfa, c.kda_gate_rank, P(nullptr)), J(L.kb, s->pb, nv, P(nullptr)),
+                J(L.kg, s->pg, value, P(L.kn_g))}, nt));
     const int hist = c.conv_kernel - 1;
     KdaStepArgs a{};
     a.pq = s->pq; a.pk = s->pk; a.pv = s->pv; a.pfa = s->pfa;
@@ -797,10 +891,19 @@ int kda_block(DState *s, const DLayer &L, const Prologue &in, int li, int nt, in
     a.slot_stride = s->kda_slot;
     a.ctl_slot = &s->ctl->slot_base;
     a.xq = s->xq2; a.xqs = s->xqs2;
+    a.normed_out = sub ? s->sub_a : nullptr;
     a.nv = nv; a.key = key; a.value = value; a.rank = c.kda_gate_rank;
     a.depth = s->depth; a.advance = advance; a.nt = nt;
     a.scale = ssm_scale(kd); a.eps = c.rms_norm_eps;
     CK(l98k_kda_step(&a, kd, c.conv_kernel, s->st));
+    if (sub) {
+        // o_proj's own norm over the value row, then the block-Hadamard
+        // quantization (src/forward_kda.c:954-996); per-32 scales
+        const bool had = c.hadamard_o > 1;
+        CK(l98k_rmsnorm_ex(s->sub_a, value, nullptr, nullptr, L.kn_o, value, c.rms_norm_eps, nt,
+                           had ? s->sub_b : nullptr, value, had ? nullptr : s->xq2, s->xqs2, 0, s->st));
+        if (had) CK(l98k_subn_quant(s->sub_b, nt, value, c.hadamard_o, 32, s->xq2, s->xqs2, s->st));
+    }
     CK(gemv(s, {JX(L.ko, s->blk, d, s->xq2, s->xqs2)}, nt));
     return 0;
 }
@@ -812,14 +915,29 @@ int moe_block(DState *s, const DLayer &L, const Prologue &in, int nt) {
     const LZModelConfig &c = s->m->c;
     const int d = c.hidden_size, E = c.num_experts, topk = c.num_experts_per_token;
     const int lat = c.moe_latent_dim, inter = c.moe_intermediate_size, sw = c.moe_shared_width;
-    CK(gemv(s, {J(L.router, s->rl, E, in), J(L.down, s->latx, lat, in), J(L.sg, s->sgo, sw, in),
-                J(L.su, s->suo, sw, in)}, nt));
+    const bool sub = c.use_subn != 0;      // own norms (src/forward_moe.c:349-389, 418-430, 455-525)
+    auto P = [&](const float *w) { return sub ? PW(in, w) : in; };
+    CK(gemv(s, {J(L.router, s->rl, E, P(L.mn_gate)), J(L.down, s->latx, lat, P(L.mn_down)),
+                J(L.sg, s->sgo, sw, P(L.mn_sg)), J(L.su, s->suo, sw, P(L.mn_su))}, nt));
     const int max_groups = nt * topk < E ? nt * topk : E;
     const ExpertJob up2[2] = {EJ(L.w1, s->h1, 0, PQ(s->latx, lat)), EJ(L.w3, s->h3, 0, PQ(s->latx, lat))};
     CK(l98k_moe_up(up2, 2, s->rl, L.bias, E, topk, nt, s->sel_idx, s->sel_w, s->grp, &s->ctl->expert_tally, lat,
                    inter, s->st));
     const ExpertJob down1[1] = {EJ(L.w2, s->h2, 1, PS(s->h1, s->h3, inter))};
     CK(l98k_expert_gemv(down1, 1, s->grp, max_groups, inter, lat, nt, s->st));
+    if (sub) {
+        // the routed combine and the shared SwiGLU, each normalized with its
+        // own weight before its quantization
+        const float eps = c.rms_norm_eps;
+        CK(l98k_wide_pro_f(2, s->h2, nullptr, 0, s->sel_idx, s->sel_w, topk, lat, nt, s->sub_a, s->st));
+        CK(l98k_rmsnorm_ex(s->sub_a, lat, nullptr, nullptr, L.mn_up, lat, eps, nt, nullptr, 0, s->xq3, s->xqs3, 0,
+                           s->st));
+        CK(l98k_wide_pro_f(1, s->sgo, s->suo, sw, nullptr, nullptr, 0, sw, nt, s->sub_b, s->st));
+        CK(l98k_rmsnorm_ex(s->sub_b, sw, nullptr, nullptr, L.mn_sd, sw, eps, nt, nullptr, 0, s->xq4, s->xqs4, 0,
+                           s->st));
+        CK(gemv(s, {JX(L.up, s->up_out, d, s->xq3, s->xqs3), JX(L.sd, s->sd_out, d, s->xq4, s->xqs4)}, nt));
+        return 0;
+    }
     CK(gemv(s, {J(L.up, s->up_out, d, PC(s->h2, s->sel_idx, s->sel_w, topk)),
                 J(L.sd, s->sd_out, d, PS(s->sgo, s->suo, sw))}, nt));
     return 0;
@@ -842,6 +960,7 @@ int forward_chunk(DState *s, const int *toks, int nt, const int *ctl_pos, int po
     float *xb[2] = {s->x, s->x2};
     int cur = 0;
     const bool fused = l98k_gemv_norm_fits(d, nt) != 0;
+    if (c.use_subn && !fused) return -1;      // SubLN's per-projection norms run in the GEMV prologues
     CK(l98k_embed(m->embed.q, m->embed.s, toks, d, nt, xb[cur], s->st));
     const float *ra = nullptr, *rb = nullptr;     // pending residual of the previous block
     // Input rows of a block: the fused norm prologue, or a norm kernel that
@@ -895,10 +1014,29 @@ int draft_step(DState *s, const int *toks, const int *ctl_pos, int pos_off, int 
     CK(gemv(s, {JX(m->mtp_fc, s->mtp_x, d, s->xq, s->xqs)}, 1));
     CK(attn_block(s, m->mtp, PN(s->mtp_x, d, nullptr, nullptr, m->mtp.in_norm, eps, nullptr, nullptr, 0),
                   s->planes - 1, ctl_pos, pos_off, 1, max_pos, false));
-    const Prologue post = PN(s->mtp_x, d, s->blk, nullptr, m->mtp.post_norm, eps, s->mtp_x2, nullptr, 0);
-    CK(gemv(s, {J(m->mtp_gate, s->hb, I, post), J(m->mtp_up, s->hb2, I, post)}, 1));
-    CK(gemv(s, {J(m->mtp_down, s->ffn_out, d, PS(s->hb, s->hb2, I))}, 1));
-    CK(l98k_rmsnorm(s->mtp_x2, d, s->ffn_out, nullptr, m->mtp_norm, d, eps, 1, s->chain, d, s->xq, s->xqs, s->st));
+    float *mx = s->mtp_x2;
+    if (c.use_subn) {
+        // dense FFN, SubLN (src/forward_kda.c:1102-1240): the residual folds
+        // in place; gate / up normalize it with their own weights, one scale
+        // per row; the SwiGLU output takes down's own norm, then the
+        // block-Hadamard quantization
+        const float *fnw = m->mtp.fn_down;
+        const bool had = c.hadamard_down > 1;
+        mx = s->mtp_x;
+        CK(l98k_rmsnorm_ex(mx, d, s->blk, nullptr, m->mtp.fn_gate, d, eps, 1, nullptr, 0, s->xq, s->xqs, 1, s->st));
+        CK(l98k_rmsnorm_ex(mx, d, nullptr, nullptr, m->mtp.fn_up, d, eps, 1, nullptr, 0, s->xq3, s->xqs3, 1, s->st));
+        CK(gemv(s, {JX(m->mtp_gate, s->hb, I, s->xq, s->xqs), JX(m->mtp_up, s->hb2, I, s->xq3, s->xqs3)}, 1));
+        CK(l98k_wide_pro_f(1, s->hb, s->hb2, I, nullptr, nullptr, 0, I, 1, s->sub_a, s->st));
+        CK(l98k_rmsnorm_ex(s->sub_a, I, nullptr, nullptr, fnw, I, eps, 1, had ? s->sub_b : nullptr, I,
+                           had ? nullptr : s->xq, s->xqs, 0, s->st));
+        if (had) CK(l98k_subn_quant(s->sub_b, 1, I, c.hadamard_down, 32, s->xq, s->xqs, s->st));
+        CK(gemv(s, {JX(m->mtp_down, s->ffn_out, d, s->xq, s->xqs)}, 1));
+    } else {
+        const Prologue post = PN(s->mtp_x, d, s->blk, nullptr, m->mtp.post_norm, eps, s->mtp_x2, nullptr, 0);
+        CK(gemv(s, {J(m->mtp_gate, s->hb, I, post), J(m->mtp_up, s->hb2, I, post)}, 1));
+        CK(gemv(s, {J(m->mtp_down, s->ffn_out, d, PS(s->hb, s->hb2, I))}, 1));
+    }
+    CK(l98k_rmsnorm(mx, d, s->ffn_out, nullptr, m->mtp_norm, d, eps, 1, s->chain, d, s->xq, s->xqs, s->st));
     CK(gemv(s, {JX(m->embed, out_logits, c.vocab_size, s->xq, s->xqs)}, 1));
     if (out_tok) CK(l98k_argmax(out_logits, c.vocab_size, 1, 1, out_tok, s->amax_part, s->amax_cnt, s->st));
     return 0;
@@ -969,8 +1107,11 @@ namespace {
 #define WIDE_MAX 512          // rows of one wide forward
 #define WIDE_MIN 16           // prefills shorter than this take the chunked path
 
+// nullptr (the callers take the chunked path) for a SubLN model, whose
+// per-projection norms this many-row forward does not carry.
 DWide *wide_get(const DModel *cm) {
     DModel *m = const_cast<DModel *>(cm);
+    if (m->c.use_subn) return nullptr;
     if (m->wide) return m->wide;
     const LZModelConfig &c = m->c;
     const size_t R = WIDE_MAX, d = c.hidden_size, pairs = R * c.num_experts_per_token;
@@ -1737,6 +1878,8 @@ extern "C" int lz_spec_round(const LZModel *mm, LZRunState *s, int anchor, int a
             // the reference leaves in s->mtp_chain
             if (hipMemcpyAsync(s->mtp_chain, d->chain, sizeof(float) * c.hidden_size, hipMemcpyDeviceToHost,
                                d->st) ||
+                hipMemcpyAsync(s->mtp_draft_logits, d->draft_logits, sizeof(float) * c.vocab_size,
+                               hipMemcpyDeviceToHost, d->st) ||
                 hipStreamSynchronize(d->st))
                 return -LZ_ERR_FORWARD;
             out[0] = anchor; *out_n_accept = 0; *out_new_pos = anchor_pos; *out_k_eff = k_eff;
@@ -1756,8 +1899,18 @@ extern "C" int lz_spec_round(const LZModel *mm, LZRunState *s, int anchor, int a
             return -LZ_ERR_FORWARD;
     }
     if (hipEventRecord(d->ph[3], d->st)) return -LZ_ERR_FORWARD;
-    // chain mirror (the reseeded mtp_chain) rides on the same sync as ctl
-    if (hipMemcpyAsync(s->mtp_chain, d->chain, sizeof(float) * c.hidden_size, hipMemcpyDeviceToHost, d->st))
+    // the fields the reference's round leaves for its caller (the reseeded
+    // mtp_chain, the verify logits and hidden rows, the last draft step's
+    // logits) ride on the same sync as ctl
+    const float *last_draft = (p_min > 0.0f || k < n_min) ? d->draft_logits
+                                                          : d->draft_logits + (size_t)(k - 1) * c.vocab_size;
+    if (hipMemcpyAsync(s->mtp_chain, d->chain, sizeof(float) * c.hidden_size, hipMemcpyDeviceToHost, d->st) ||
+        hipMemcpyAsync(s->mtp_logits, d->mtp_logits, sizeof(float) * (size_t)(k_eff + 1) * c.vocab_size,
+                       hipMemcpyDeviceToHost, d->st) ||
+        hipMemcpyAsync(s->mtp_verify_hidden, d->vhidden, sizeof(float) * (size_t)(k_eff + 1) * c.hidden_size,
+                       hipMemcpyDeviceToHost, d->st) ||
+        hipMemcpyAsync(s->mtp_draft_logits, last_draft, sizeof(float) * c.vocab_size, hipMemcpyDeviceToHost,
+                       d->st))
         return -LZ_ERR_FORWARD;
     if (ctl_get(d, &h)) return -LZ_ERR_FORWARD;
     int n_accept = h.n_accept;

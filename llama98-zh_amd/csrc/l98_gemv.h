@@ -233,13 +233,14 @@ __device__ __forceinline__ void build_rows(const Prologue &P, const int8_t *__re
             }
         quant_rows<RW, PJN>(v, wave, lane, nm, nf, nb, in_dim, sx, sxs);
     } else if (MODES & MB(PRO_NORM)) {   // PRO_NORM
-        const bool has_a = P.a != nullptr, has_b = P.b != nullptr;
+        // P.w == nullptr: the folded rows are quantized without a norm
+        const bool has_a = P.a != nullptr, has_b = P.b != nullptr, do_norm = P.w != nullptr;
         const float *pa = has_a ? P.a : P.src;
         const float *pb = has_b ? P.b : pa;
         const int sa = has_a ? in_dim : P.src_stride, sb = has_b ? in_dim : sa;
         float4 wn[PJN], ad[RW][PJN], bd[RW][PJN];
 #pragma unroll
-        for (int j = 0; j < PJN; j++) wn[j] = reinterpret_cast<const float4 *>(P.w)[fc[j]];
+        for (int j = 0; j < PJN; j++) wn[j] = reinterpret_cast<const float4 *>(do_norm ? P.w : P.src)[fc[j]];
 #pragma unroll
         for (int r = 0; r < RW; r++)
 #pragma unroll
@@ -266,36 +267,39 @@ __device__ __forceinline__ void build_rows(const Prologue &P, const int8_t *__re
         // lane); wave w sums rows w and w + 4
         constexpr int PC = 4 * PJN;
         constexpr int rowf = ps_row_floats<PC>();
+        if (do_norm) {
 #pragma unroll
-        for (int r = 0; r < RW; r++) {
-            const int t = wave + 4 * r;
+            for (int r = 0; r < RW; r++) {
+                const int t = wave + 4 * r;
 #pragma unroll
-            for (int j = 0; j < PJN; j++) {
-                const int f = lane + 64 * j;
-                if (t < nm && f < nf) {
-                    const float4 x = v[r][j];
-                    *reinterpret_cast<float4 *>(sq + (size_t)t * rowf + ps_slot<PC>(4 * f)) =
-                        make_float4(x.x * x.x, x.y * x.y, x.z * x.z, x.w * x.w);
+                for (int j = 0; j < PJN; j++) {
+                    const int f = lane + 64 * j;
+                    if (t < nm && f < nf) {
+                        const float4 x = v[r][j];
+                        *reinterpret_cast<float4 *>(sq + (size_t)t * rowf + ps_slot<PC>(4 * f)) =
+                            make_float4(x.x * x.x, x.y * x.y, x.z * x.z, x.w * x.w);
+                    }
                 }
             }
+            __syncthreads();
+            PsRec *rec = reinterpret_cast<PsRec *>(sq + (size_t)M * rowf) + wave * 128;
+            for (int t = wave; t < nm; t += 4) {
+                const float ss = wave_sum_nonneg<PC>(sq + (size_t)t * rowf, in_dim, rec);
+                if (lane == 0) s_inv[t] = d_rsqrt(d_ss_over_n(ss, in_dim) + P.eps);
+            }
+            __syncthreads();
         }
-        __syncthreads();
-        PsRec *rec = reinterpret_cast<PsRec *>(sq + (size_t)M * rowf) + wave * 128;
-        for (int t = wave; t < nm; t += 4) {
-            const float ss = wave_sum_nonneg<PC>(sq + (size_t)t * rowf, in_dim, rec);
-            if (lane == 0) s_inv[t] = d_rsqrt(d_ss_over_n(ss, in_dim) + P.eps);
-        }
-        __syncthreads();
 #pragma unroll
         for (int r = 0; r < RW; r++) {
             const int t = wave + 4 * r;
-            const float inv = s_inv[t < nm ? t : 0];
+            const float inv = do_norm ? s_inv[t < nm ? t : 0] : 1.0f;
 #pragma unroll
             for (int j = 0; j < PJN; j++) {
                 const int f = lane + 64 * j;
                 const float4 x = v[r][j], w = wn[j];
-                const float4 o = make_float4(x.x * inv * (1.0f + w.x), x.y * inv * (1.0f + w.y),
-                                             x.z * inv * (1.0f + w.z), x.w * inv * (1.0f + w.w));
+                const float4 o = do_norm ? make_float4(x.x * inv * (1.0f + w.x), x.y * inv * (1.0f + w.y),
+                                                       x.z * inv * (1.0f + w.z), x.w * inv * (1.0f + w.w))
+                                         : x;
                 if (writer && t < nm && f < nf) {
                     if (P.x_out) reinterpret_cast<float4 *>(P.x_out + (size_t)xr[r] * P.src_stride)[f] = x;
                     if (P.o_out) reinterpret_cast<float4 *>(P.o_out + (size_t)xr[r] * P.o_stride)[f] = o;
@@ -474,7 +478,7 @@ static bool prologue_ok(const Prologue &P, int in_dim, const int8_t *xq, const f
     if (in_dim > PRO_MAX_IN || !P.src) return false;
     if (P.mode == PRO_QUANT) return P.src_stride >= in_dim && !(P.src_stride & 3);
     if (P.mode == PRO_SILU) return P.src2 && P.src_stride >= in_dim && !(P.src_stride & 3);
-    if (P.mode == PRO_NORM) return P.w && P.src_stride >= in_dim && !(P.src_stride & 3) && !(P.o_stride & 3);
+    if (P.mode == PRO_NORM) return P.src_stride >= in_dim && !(P.src_stride & 3) && !(P.o_stride & 3);
     if (P.mode == PRO_COMBINE) return P.sel_idx && P.sel_w && P.topk >= 1 && P.topk <= MAX_TOPK;
     return false;
 }

@@ -153,7 +153,8 @@ __global__ __launch_bounds__(MF_THREADS) void k_mfma_q8(const int8_t *__restrict
 __global__ __launch_bounds__(64) void k_wide_pro(int mode, const float *__restrict__ src,
                                                  const float *__restrict__ src2, int src_stride,
                                                  const int *__restrict__ sel_idx, const float *__restrict__ sel_w,
-                                                 int topk, int n, int8_t *__restrict__ xq, float *__restrict__ xqs) {
+                                                 int topk, int n, int8_t *__restrict__ xq, float *__restrict__ xqs,
+                                                 float *__restrict__ fout) {
     EXP_TAB_LOAD(tab);
     EXP_TAB_PUT(tab);
     __syncthreads();
@@ -182,11 +183,14 @@ __global__ __launch_bounds__(64) void k_wide_pro(int mode, const float *__restri
             }
             v = y;
         }
-        float sg;
-        const uint32_t q = quant_octet(v, &sg);
-        if (f < nf) {
-            reinterpret_cast<uint32_t *>(xq + (size_t)row * n)[f] = q;
-            if (!(f & 7)) xqs[(size_t)row * nb + (f >> 3)] = sg;
+        if (fout && f < nf) reinterpret_cast<float4 *>(fout + (size_t)row * n)[f] = v;
+        if (xq) {
+            float sg;
+            const uint32_t q = quant_octet(v, &sg);
+            if (f < nf) {
+                reinterpret_cast<uint32_t *>(xq + (size_t)row * n)[f] = q;
+                if (!(f & 7)) xqs[(size_t)row * nb + (f >> 3)] = sg;
+            }
         }
     }
 }
@@ -227,7 +231,20 @@ extern "C" int l98k_wide_pro(int mode, const float *src, const float *src2, int 
     if (rows < 1 || n < 32 || (n & 31) || n > 4 * 64 * WP_MAXJ || mode < 0 || mode > 2) return -1;
     if (mode < 2 && (src_stride < n || (src_stride & 3))) return -1;
     if (mode == 2 && (topk < 1 || topk > MAX_TOPK || !sel_idx || !sel_w)) return -1;
+    if (!xq || !xqs) return -1;
     hipLaunchKernelGGL(k_wide_pro, dim3(rows), dim3(64), 0, st, mode, src, src2, src_stride, sel_idx, sel_w, topk, n,
-                       xq, xqs);
+                       xq, xqs, (float *)nullptr);
+    return (int)hipGetLastError();
+}
+
+// The same rows in float, unquantized (row stride n): the input of a norm
+// that comes before the quantization.
+extern "C" int l98k_wide_pro_f(int mode, const float *src, const float *src2, int src_stride, const int *sel_idx,
+                               const float *sel_w, int topk, int n, int rows, float *fout, hipStream_t st) {
+    if (rows < 1 || n < 32 || (n & 31) || n > 4 * 64 * WP_MAXJ || mode < 0 || mode > 2 || !fout) return -1;
+    if (mode < 2 && (src_stride < n || (src_stride & 3))) return -1;
+    if (mode == 2 && (topk < 1 || topk > MAX_TOPK || !sel_idx || !sel_w)) return -1;
+    hipLaunchKernelGGL(k_wide_pro, dim3(rows), dim3(64), 0, st, mode, src, src2, src_stride, sel_idx, sel_w, topk, n,
+                       (int8_t *)nullptr, (float *)nullptr, fout);
     return (int)hipGetLastError();
 }

@@ -21,7 +21,7 @@ __global__ __launch_bounds__(64) void k_rmsnorm(float *__restrict__ x, int x_str
                                                 const float *__restrict__ a, const float *__restrict__ b,
                                                 const float *__restrict__ w, int n, float eps,
                                                 float *__restrict__ out, int out_stride,
-                                                int8_t *__restrict__ xq, float *__restrict__ xqs) {
+                                                int8_t *__restrict__ xq, float *__restrict__ xqs, int tok) {
     __shared__ __align__(16) float sq[ps_row_floats<4 * PJ>()];
     __shared__ PsRec rec[128];
     __shared__ float s_inv;
@@ -32,7 +32,7 @@ __global__ __launch_bounds__(64) void k_rmsnorm(float *__restrict__ x, int x_str
     for (int j = 0; j < PJ; j++) {
         const int fc = imin(lane + 64 * j, nf - 1);
         v[j] = xr[fc];
-        wn[j] = reinterpret_cast<const float4 *>(w)[fc];
+        wn[j] = reinterpret_cast<const float4 *>(w ? w : x)[fc];
     }
     if (a) {
         float4 av[PJ];
@@ -52,7 +52,8 @@ __global__ __launch_bounds__(64) void k_rmsnorm(float *__restrict__ x, int x_str
         }
     }
     norm_row<PJ>(v, wn, n, eps, sq, rec, &s_inv, out ? out + (size_t)row * out_stride : nullptr,
-                 xq ? xq + (size_t)row * n : nullptr, xqs ? xqs + (size_t)row * (n >> 5) : nullptr);
+                 xq ? xq + (size_t)row * n : nullptr, xqs ? xqs + (size_t)row * (n >> 5) : nullptr, w != nullptr,
+                 tok != 0);
 }
 
 // MTP input rows (lz_mtp_draft_step / lz_mtp_prefill, src/forward_mtp.c:
@@ -271,19 +272,28 @@ extern "C" int l98k_embed(const int8_t *q, const float *s, const int *toks, int 
 
 #define NORM_CASES(X) X(1) X(2) X(4) X(8)
 
-extern "C" int l98k_rmsnorm(float *x, int x_stride, const float *a, const float *b, const float *w,
-                            int n, float eps, int rows, float *out, int out_stride, int8_t *xq,
-                            float *xqs, hipStream_t st) {
-    if (n < 32 || n > 256 * 8 || (n & 31) || (x_stride & 3) || (out && (out_stride & 3)) || rows < 1) return -1;
+extern "C" int l98k_rmsnorm_ex(float *x, int x_stride, const float *a, const float *b, const float *w,
+                               int n, float eps, int rows, float *out, int out_stride, int8_t *xq,
+                               float *xqs, int tok, hipStream_t st) {
+    if (n < 32 || n > 256 * 8 || (n & 31) || (x_stride & 3) || (out && (out_stride & 3)) || rows < 1 ||
+        (xq && !xqs))
+        return -1;
 #define NORM_LAUNCH(PJ)                                                                          \
     if (n <= 256 * PJ) {                                                                         \
         hipLaunchKernelGGL(k_rmsnorm<PJ>, dim3(rows), dim3(64), 0, st, x, x_stride, a, b, w, n, \
-                           eps, out, out_stride, xq, xqs);                                       \
+                           eps, out, out_stride, xq, xqs, tok);                                  \
         return (int)hipGetLastError();                                                           \
     }
     NORM_CASES(NORM_LAUNCH)
 #undef NORM_LAUNCH
     return -1;
+}
+
+extern "C" int l98k_rmsnorm(float *x, int x_stride, const float *a, const float *b, const float *w,
+                            int n, float eps, int rows, float *out, int out_stride, int8_t *xq,
+                            float *xqs, hipStream_t st) {
+    if (!w) return -1;
+    return l98k_rmsnorm_ex(x, x_stride, a, b, w, n, eps, rows, out, out_stride, xq, xqs, 0, st);
 }
 
 extern "C" int l98k_mtp_pre(const int8_t *emb_q, const float *emb_s, const int *toks, const float *h, int d,

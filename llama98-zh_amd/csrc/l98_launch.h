@@ -31,6 +31,10 @@ int l98k_mfma_gemm_grouped(const int8_t *bank, const float *bank_s, int N, int K
 // 2 slot-ordered expert combine; the GEMV prologues' arithmetic.
 int l98k_wide_pro(int mode, const float *src, const float *src2, int src_stride, const int *sel_idx,
                   const float *sel_w, int topk, int n, int rows, int8_t *xq, float *xqs, hipStream_t st);
+// The same rows left in float (fout, row stride n), for a norm before the
+// quantization (the SubLN routed-up and shared-down inputs).
+int l98k_wide_pro_f(int mode, const float *src, const float *src2, int src_stride, const int *sel_idx,
+                    const float *sel_w, int topk, int n, int rows, float *fout, hipStream_t st);
 // Temperature sampling (one block per call; l98_k_sample.hip).
 // probs = softmax(logits * inv_t); with keys: the top-p candidate keys and
 // indices for l98k_smp_sort_desc and their count.
@@ -68,6 +72,11 @@ int l98k_embed(const int8_t *q, const float *s, const int *toks, int d, int nt, 
 // x += a (+ b) (when a), RMSNorm(1+w) -> out (when out) and per-32 int8 (when xq).
 int l98k_rmsnorm(float *x, int x_stride, const float *a, const float *b, const float *w, int n, float eps,
                  int rows, float *out, int out_stride, int8_t *xq, float *xqs, hipStream_t st);
+// The same with w == nullptr allowed (no norm: the folded row is only stored
+// and/or quantized) and tok = 1 for one int8 scale per row
+// (lz_quantize_q8_tok) instead of one per 32 elements.
+int l98k_rmsnorm_ex(float *x, int x_stride, const float *a, const float *b, const float *w, int n, float eps,
+                    int rows, float *out, int out_stride, int8_t *xq, float *xqs, int tok, hipStream_t st);
 // MTP input rows: [norm_e(embed(tok)) | norm_h(h)] quantized per 32 into xq [rows][2d].
 int l98k_mtp_pre(const int8_t *emb_q, const float *emb_s, const int *toks, const float *h, int d,
                  const float *w_e, const float *w_h, float eps, int rows, int8_t *xq, float *xqs,

@@ -9,7 +9,11 @@ Each fixture holds the inputs (model generator id and seed, prompt seed and
 length, k, sampling parameters) and the reference's outputs (emitted
 tokens, per-round k_eff and n_accept, final RNG state and positions), plus
 the sha256 of the generated model.bin so a change of the generator is
-caught.
+caught.  Greedy cases with the "dump" option also hold, for the first
+rounds, the sha256 of the bytes of the capture logits, of each round's
+verify logits and hidden rows and of its last draft step's logits (the
+harness's --dump-rounds files), so a run can be checked bit for bit on the
+values, not only on the emitted tokens.
 """
 import hashlib
 import json
@@ -49,6 +53,16 @@ CASES = [
     ("gen_echo_k3_brk", "echo", 11, 64, 24, 3, 100, 0.0, 1.0, 1, {"prompt_seed": 11, "brk": 1}),
     ("gen_echo_k3_skipc", "echo", 11, 64, 24, 3, 100, 0.0, 1.0, 1, {"prompt_seed": 11, "skipc": 1}),
     ("gen_echo_k3_temp", "echo", 11, 64, 24, 3, 100, 0.8, 0.95, 7, {"prompt_seed": 11}),
+    # Round values (--dump-rounds) of greedy runs, 32-wide projections (micro,
+    # echo) included.
+    ("gen_micro_k3_rounds", "micro", 10, 512, 24, 3, 40, 0.0, 1.0, 1, {"dump": 6}),
+    ("gen_echo_k3_rounds", "echo", 11, 64, 24, 3, 60, 0.0, 1.0, 1, {"prompt_seed": 11, "dump": 6}),
+    ("gen_tiny_k3_rounds", "tiny", 0, 8192, 64, 3, 32, 0.0, 1.0, 1, {"dump": 4}),
+    # SubLN (use_subn = 1, the survey's C1s variant, and a micro twin).
+    ("gen_subln_k3_greedy", "subln", 5, 8192, 64, 3, 96, 0.0, 1.0, 1, {"dump": 4}),
+    ("gen_subln_k1_greedy", "subln", 5, 8192, 64, 1, 48, 0.0, 1.0, 1),
+    ("gen_subln_k2_temp", "subln", 5, 8192, 64, 2, 48, 0.8, 0.95, 7),
+    ("gen_micro_subln_k3_greedy", "micro_subln", 12, 512, 24, 3, 48, 0.0, 1.0, 1, {"dump": 6}),
 ]
 MODEL_SEED = 1234
 PROMPT_SEED = 0
@@ -78,6 +92,9 @@ def main():
             extra.append("--break-rollback")
         if skipc:
             extra.append("--skip-catchup")
+        dump = int(opt.get("dump", 0))
+        if dump:
+            extra += ["--dump-rounds", str(dump)]
         model = pkg.ensure_model(os.path.join(root, mdir), cid, seed=MODEL_SEED)
         h = hashlib.sha256()
         with open(os.path.join(model, "model.bin"), "rb") as f:
@@ -97,6 +114,14 @@ def main():
             "ssm_slot": r["ssm_slot"],
             "source": "oracle/_ref/l98ref_oracle gen (reference engine, float-oracle mode)",
         }
+        if dump:
+            sums = {}
+            for tag in ["capture%d" % i for i in range(dump)] + \
+                    ["%s%d" % (t, i) for i in range(dump) for t in ("verify", "vhidden", "draft")]:
+                path = "%s.%s.bin" % (r["prefix"], tag)
+                if os.path.exists(path):
+                    sums[tag] = hashlib.sha256(open(path, "rb").read()).hexdigest()
+            out["round_sha256"] = sums
         with open(os.path.join(HERE, name + ".json"), "w") as f:
             json.dump(out, f, indent=1)
         print(name, len(out["tokens"]), "tokens", flush=True)

@@ -123,3 +123,32 @@ def test_accept_paths_are_covered():
     assert set(g("gen_echo_k3_pmin.json")["k_eff"]) == {0, 1, 2, 3}
     assert -1 in g("gen_echo_k3_pmin_nmin.json")["n_accept"]
     assert max(g("gen_echo_k3_temp.json")["n_accept"]) == 3
+
+
+ROUND_FIXTURES = [f for f in FIXTURES if "round_sha256" in json.load(open(os.path.join(GOLDEN, f)))]
+
+
+@pytest.mark.parametrize("fname", ROUND_FIXTURES)
+def test_round_values_match_reference_fixture(pkg, model_root, fname):
+    """Bit for bit on the values, not only the tokens: the capture logits and,
+    round after round, the verify logits, verify hidden rows and last draft
+    logits that lz_spec_round leaves in the state hash to what the reference
+    engine left in its own state (its harness's --dump-rounds files)."""
+    import hashlib
+    g, model, prompt = load(pkg, model_root, fname)
+    print(f"[case] golden rounds {fname}", flush=True)
+    want = g["round_sha256"]
+    got = {}
+
+    def keep(tag, a):
+        if tag in want:
+            got[tag] = hashlib.sha256(np.ascontiguousarray(a, np.float32).tobytes()).hexdigest()
+
+    eng = pkg.Engine(model)
+    try:
+        eng.generate_host(prompt, g["k"], g["n_new"], on_round=keep)
+    finally:
+        eng.close()
+    assert set(got) == set(want), sorted(set(want) - set(got))
+    bad = [t for t in want if got[t] != want[t]]
+    assert not bad, f"values differ from the reference at {bad}"

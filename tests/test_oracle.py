@@ -557,6 +557,12 @@ def test_oracle_matches_golden(pkg, model_root, fname):
     n = len(g["tokens"])
     assert list(toks[:n]) == g["tokens"]
     assert list(ke) == g["k_eff"] and list(na) == g["n_accept"] and rng == g["rng"]
+    if "round_sha256" in g:
+        want = g["round_sha256"]
+        n_rounds = 1 + max(int(re.sub(r"^[a-z]+", "", t)) for t in want)
+        mine = _greedy_rounds_oracle(model, prompt, g["k"], n_rounds)
+        for tag, h in want.items():
+            assert hashlib.sha256(mine[tag].tobytes()).hexdigest() == h, tag
 
 
 # ---------------------------------------------------------- C-ABI export ---
