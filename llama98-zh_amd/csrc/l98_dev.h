@@ -43,7 +43,7 @@ typedef struct {
 // in input width and prologue.
 typedef struct {
     const int8_t *w;         // [rows][in_dim] int8, row-major
-    const float *ws;         // [rows] per-row scale
+    const float *ws;         // [rows][in_dim/gs] scales (one per row when gs is 0)
     float *out;              // out[t * out_stride + row]
     const int8_t *xq;        // PRO_XQ activations [M][in_dim]
     const float *xqs;        // PRO_XQ activation scales [M][in_dim/32]
@@ -53,7 +53,7 @@ typedef struct {
     int out_stride;
     int tile0;               // first tile of this job in the launch grid (set by the launcher)
     int R;                   // rows per tile (set by the launcher)
-    int pad;
+    int gs;                  // weight scale group (a multiple of 32 dividing in_dim; 0: the row)
     Prologue pro;
 } GemvJob;
 
@@ -70,7 +70,8 @@ typedef struct {
 // expert e occupies rows [e*out_rows, (e+1)*out_rows).
 typedef struct {
     const int8_t *q;
-    const float *s;
+    const float *s;          // expert e: [out_rows][in/gs] from e*out_rows*(in/gs)
+    int gs;                  // weight scale group (0: the row)
 } ExpertBank;
 
 // One projection of a grouped expert GEMV launch (up to two per launch,
@@ -82,7 +83,7 @@ typedef struct {
     const int8_t *xq;        // PRO_XQ activation rows (by token or by pair)
     const float *xqs;
     int xq_by_pair;          // 1: activation row = pair index, 0: = the pair's token
-    int pad;
+    int gs;                  // weight scale group (0: the row)
     Prologue pro;            // PRO_XQ, PRO_QUANT or PRO_SILU
 } ExpertJob;
 
@@ -124,7 +125,7 @@ typedef struct {
     const float *pq, *pk, *pv;          // projections before the conv [nt][key | key | value]
     const float *pfa;                   // gate low-rank projection [nt][rank]
     const int8_t *fb_q;                 // gate up-projection [nv*kd][rank] int8
-    const float *fb_s;                  // its row scales
+    const float *fb_s;                  // its scales [nv*kd][rank/fb_gs]
     const float *conv_w;                // [conv_dim][K] taps, channels [q | k | v]
     float *conv_ring;                   // the layer's history inside ring slot 0, [conv_dim][K-1]
     size_t conv_slot_stride;            // floats between ring slots
@@ -140,6 +141,7 @@ typedef struct {
     float *xqs;
     int nv, key, value, rank, depth, advance, nt;
     float scale, eps;
+    int fb_gs;                          // f_b scale group (0: the row)
 } KdaStepArgs;
 
 typedef struct {

@@ -24,6 +24,7 @@
 #include <time.h>
 #include <unistd.h>
 
+#include <memory>
 #include <mutex>
 #include <vector>
 
@@ -104,8 +105,9 @@ static int knobs_ok(int model_topk, char *errbuf, int errlen) {
 
 struct DMat {
     int8_t *q = nullptr;
-    float *s = nullptr;
+    float *s = nullptr;       // [rows][cols/gs] scales
     int rows = 0, cols = 0;
+    int gs = 0;               // scale group (== cols: one per row)
 };
 
 struct DLayer {
@@ -141,6 +143,9 @@ struct DModel {
     float *rope_cs = nullptr;
     int lin_index[128], full_index[128];
     struct DWide *wide = nullptr;       // scratch of the many-row forwards (first use)
+    int version = 5;                    // model.bin version word
+    bool has_mtp = true;                // a version-4 file carries no MTP head
+    bool grouped = false;               // some matrix has more than one scale per row
 };
 
 namespace {
@@ -160,33 +165,100 @@ struct Bin {
     float f32() { const void *q = take(4); float v = 0; if (q) memcpy(&v, q, 4); return v; }
 };
 
+// A tensor of the file: codes point into the mapped file; the f32 values
+// (Q8 scales, or the data of an F32 tensor) into the file when stored as
+// f32, else into `own`, widened at load.
 struct HostTensor {
     const int8_t *q = nullptr;
-    const float *s = nullptr;     // Q8 scales or F32 data
-    int rows = 0, cols = 0;
+    const float *s = nullptr;     // Q8 scales [rows][cols/gs] or F32 data
+    int rows = 0, cols = 0, gs = 0;
     bool is_q8 = false;
+    std::shared_ptr<std::vector<float>> own;
 };
 
-HostTensor rd_q8(Bin &b, int rows, int cols) {
+// lz_f16_to_f32 (src/compat.c:283-312): binary16 widened exactly.
+float f16_to_f32(unsigned h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 0x1Fu, m = h & 0x3FFu, u;
+    if (e == 0) {
+        if (m == 0) u = sign;
+        else {
+            int sh = 0;
+            while (!(m & 0x400u)) { m <<= 1; sh++; }
+            u = sign | ((uint32_t)(127 - 14 - sh) << 23) | ((m & 0x3FFu) << 13);
+        }
+    } else if (e == 0x1Fu) {
+        u = sign | 0x7F800000u | (m << 13);
+    } else {
+        u = sign | ((e + 127u - 15u) << 23) | (m << 13);
+    }
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+// lz_scale_u8_decode (src/compat.c:340-345): base * (u / 255), the quotient
+// and the product each rounded to float.
+float scale_u8_decode(float base, float u) {
+    volatile float levels = 255.0f;
+    volatile float q = u / levels;
+    volatile float p = base * q;
+    return p;
+}
+
+// A Q8_0 tensor (visit_read_bin, src/model.c:3567-3812): u32 gs (a multiple
+// of 32 dividing the row here), the codes, and the scale plane in the
+// file's layout (read_scale_plane, src/model.c:3510-3554): 0 f32 per
+// group; 1 binary16 per group; 2 a binary16 base per row, then a u8 per
+// group decoded as base * (u / 255).  The device holds f32 scales.
+HostTensor rd_q8(Bin &b, int rows, int cols, int layout) {
     HostTensor t;
     const unsigned char *dt = (const unsigned char *)b.take(1);
     uint32_t n = (uint32_t)b.i32(), gs = (uint32_t)b.i32();
-    if (!dt || *dt != 1 || n != (uint32_t)rows * (uint32_t)cols || gs != (uint32_t)cols) {
+    if (!dt || *dt != 1 || n != (uint32_t)rows * (uint32_t)cols || gs == 0 || (gs & 31) || (uint32_t)cols % gs) {
         b.bad = true;
         return t;
     }
     t.q = (const int8_t *)b.take((size_t)rows * cols);
-    t.s = (const float *)b.take(sizeof(float) * (size_t)rows);
-    t.rows = rows; t.cols = cols; t.is_q8 = true;
+    const size_t ng = (size_t)rows * (cols / gs);
+    if (layout == 0) {
+        t.s = (const float *)b.take(sizeof(float) * ng);
+    } else {
+        t.own = std::make_shared<std::vector<float>>(ng);
+        if (layout == 1) {
+            const uint16_t *h = (const uint16_t *)b.take(2 * ng);
+            if (h)
+                for (size_t i = 0; i < ng; i++) (*t.own)[i] = f16_to_f32(h[i]);
+        } else {
+            const uint16_t *base = (const uint16_t *)b.take(2 * (size_t)rows);
+            const uint8_t *u = (const uint8_t *)b.take(ng);
+            const size_t gpr = ng / (size_t)rows;
+            if (base && u)
+                for (size_t i = 0; i < ng; i++) (*t.own)[i] = scale_u8_decode(f16_to_f32(base[i / gpr]), (float)u[i]);
+        }
+        t.s = t.own->data();
+    }
+    t.rows = rows; t.cols = cols; t.gs = (int)gs; t.is_q8 = true;
     return t;
 }
 
+// An F32 tensor of n elements, stored as f32 or as BF16 (dtype 6, widened
+// by <<16 as lz_t_f32 does, src/ops_epi.c:1210-1223).
 HostTensor rd_f32(Bin &b, int n) {
     HostTensor t;
     const unsigned char *dt = (const unsigned char *)b.take(1);
     uint32_t cnt = (uint32_t)b.i32();
-    if (!dt || *dt != 0 || cnt != (uint32_t)n) { b.bad = true; return t; }
-    t.s = (const float *)b.take(sizeof(float) * (size_t)n);
+    if (!dt || (*dt != 0 && *dt != 6) || cnt != (uint32_t)n) { b.bad = true; return t; }
+    if (*dt == 0) {
+        t.s = (const float *)b.take(sizeof(float) * (size_t)n);
+    } else {
+        const uint16_t *h = (const uint16_t *)b.take(2 * (size_t)n);
+        t.own = std::make_shared<std::vector<float>>((size_t)n);
+        if (h)
+            for (int i = 0; i < n; i++) {
+                const uint32_t u = (uint32_t)h[i] << 16;
+                memcpy(&(*t.own)[i], &u, 4);
+            }
+        t.s = t.own->data();
+    }
     t.rows = 1; t.cols = n;
     return t;
 }
@@ -214,9 +286,10 @@ struct Uploader {
     }
     DMat mat(const HostTensor &t) {
         DMat d;
-        d.rows = t.rows; d.cols = t.cols;
+        d.rows = t.rows; d.cols = t.cols; d.gs = t.gs;
         d.q = (int8_t *)put(t.q, (size_t)t.rows * t.cols);
-        d.s = (float *)put(t.s, sizeof(float) * (size_t)t.rows);
+        d.s = (float *)put(t.s, sizeof(float) * (size_t)t.rows * (t.cols / t.gs));
+        if (t.gs != t.cols) m->grouped = true;
         return d;
     }
     float *vec(const HostTensor &t) { return (float *)put(t.s, sizeof(float) * (size_t)t.cols); }
@@ -224,17 +297,23 @@ struct Uploader {
     ExpertBank bank(const std::vector<HostTensor> &ex) {
         ExpertBank b{};
         size_t rows = ex[0].rows, cols = ex[0].cols, E = ex.size();
+        const int gs = ex[0].gs;
+        for (const HostTensor &t : ex)
+            if (t.gs != gs) fail = true;          // one group size per bank
+        const size_t nws = cols / (size_t)(gs > 0 ? gs : (int)cols);
+        b.gs = gs == (int)cols ? 0 : gs;
+        if (b.gs) m->grouped = true;
         if (count) {
             put(nullptr, E * rows * cols);
-            put(nullptr, sizeof(float) * E * rows);
+            put(nullptr, sizeof(float) * E * rows * nws);
             return b;
         }
         int8_t *q = (int8_t *)arena_take(m, E * rows * cols);
-        float *s = (float *)arena_take(m, sizeof(float) * E * rows);
+        float *s = (float *)arena_take(m, sizeof(float) * E * rows * nws);
         if (!q || !s) { fail = true; return b; }
         for (size_t e = 0; e < E; e++) {
             if (hipMemcpy(q + e * rows * cols, ex[e].q, rows * cols, hipMemcpyHostToDevice) != hipSuccess ||
-                hipMemcpy(s + e * rows, ex[e].s, sizeof(float) * rows, hipMemcpyHostToDevice) != hipSuccess)
+                hipMemcpy(s + e * rows * nws, ex[e].s, sizeof(float) * rows * nws, hipMemcpyHostToDevice) != hipSuccess)
                 fail = true;
         }
         b.q = q; b.s = s;
@@ -257,11 +336,12 @@ struct HostLayer {
 int parse_model(Bin &b, LZModelConfig &c, HostTensor &embed, HostTensor &fnorm,
                 std::vector<HostLayer> &L, HostLayer &mtp, HostTensor &mg, HostTensor &mu,
                 HostTensor &md, HostTensor &fc, HostTensor &mn, HostTensor &mph, HostTensor &mpe,
-                char *err, int errlen) {
+                char *err, int errlen, int &ver_out, int &layout_out) {
     const void *magic = b.take(4);
     if (!magic || memcmp(magic, "L98Z", 4) != 0) { set_err(err, errlen, "bad magic"); return LZ_ERR_BIN_MAGIC; }
-    int ver = b.i32();
-    if (ver != 5) { set_err(err, errlen, "unsupported model.bin version %d", ver); return LZ_ERR_BIN_VERSION; }
+    const int ver = b.i32();
+    ver_out = ver;
+    if (ver < 4 || ver > 9) { set_err(err, errlen, "unsupported model.bin version %d", ver); return LZ_ERR_BIN_VERSION; }
     c.vocab_size = b.i32(); c.hidden_size = b.i32(); c.n_layers = b.i32(); c.seq_len = b.i32();
     c.n_heads = b.i32(); c.n_kv_heads = b.i32(); c.head_dim = b.i32();
     const int inter_word = b.i32();                 // intermediate_size (no dense body layer here)
@@ -279,15 +359,51 @@ int parse_model(Bin &b, LZModelConfig &c, HostTensor &embed, HostTensor &fnorm,
     c.moe_intermediate_size = b.i32(); c.moe_latent_dim = b.i32();
     int first_dense = b.i32(), renorm = b.i32(), sig = b.i32(), lat_norm = b.i32();
     c.moe_shared_width = b.i32();
-    c.mtp_n_layers = b.i32(); c.mtp_intermediate_size = b.i32();
-    int rope_type = b.i32();
-    for (int i = 0; i < 4; i++) (void)b.i32();
-    c.use_subn = b.i32();
-    c.hadamard_o = b.i32();
-    c.hadamard_down = b.i32();
-    for (int i = 0; i < 7; i++) (void)b.i32();    // mla x2, kv_share, sink, gr, ced x2
-    for (int i = 0; i < 128 * 3 + 6 + 128; i++) (void)b.i32();
+    // The version ladder of lz_open_bin (src/model.c:3925-3989, 4105-4460):
+    // v4 stops after the 13-word tail (no MTP head; the fields after it keep
+    // their "off" defaults, the hadamard blocks -1 = derived); v5 carries the
+    // rest of the tail and the 522 appended words; v6 the application table,
+    // mtp_n_draft, the rotated-vocabulary words and the scale layout; v7, v8,
+    // v9 one word each.  This path takes the identity schedule, at most one
+    // draft slot, no rotated vocabulary, and none of the v7-v9 mechanisms.
+    int rope_type = 0, mla_q = 0, mla_o = 0, kv_share = 0, sink = 0, gr = 0, ced_split = 0, ced_kv = 0;
+    bool csa2 = false;
+    c.mtp_n_layers = 0;
+    c.hadamard_o = c.hadamard_down = -1;
+    if (ver >= 5) {
+        c.mtp_n_layers = b.i32(); c.mtp_intermediate_size = b.i32();
+        rope_type = b.i32();
+        for (int i = 0; i < 4; i++) (void)b.i32();
+        c.use_subn = b.i32();
+        c.hadamard_o = b.i32();
+        c.hadamard_down = b.i32();
+        mla_q = b.i32(); mla_o = b.i32(); kv_share = b.i32();
+        sink = b.i32(); gr = b.i32(); ced_split = b.i32(); ced_kv = b.i32();
+        for (int i = 0; i < 128; i++) csa2 |= b.i32() != 0;      // csa2_on
+        for (int i = 0; i < 128 * 2 + 6 + 128; i++) (void)b.i32();
+    }
+    bool schedule_ok = true, draft_ok = true, rot_ok = true, mix_ok = true;
+    layout_out = 0;
+    if (ver >= 6) {
+        schedule_ok = b.i32() == c.n_layers;                                      // exec_len
+        for (int i = 0; i < 128; i++) schedule_ok &= b.i32() == (i < c.n_layers ? i : 0);   // app_layer
+        for (int i = 0; i < 128; i++) schedule_ok &= b.i32() == 0;               // app_loop
+        draft_ok = b.i32() <= 1;                                                 // mtp_n_draft
+        rot_ok = b.i32() == 0;                                                   // embed_hadamard
+        (void)b.i32();                                                           // embed_signs_seed
+        layout_out = b.i32();                                                    // scale_layout
+        if (ver >= 7) mix_ok &= b.i32() == 0;                                    // loop_input_mix
+        if (ver >= 8) mix_ok &= b.i32() == 0;                                    // ced_local
+        if (ver >= 9) (void)b.i32();                                             // loop_input_mix_from
+    }
     if (b.bad) { set_err(err, errlen, "truncated header"); return LZ_ERR_BIN_OPEN; }
+    if (!schedule_ok || !draft_ok || !rot_ok || !mix_ok || layout_out < 0 || layout_out > 2 || mla_q || mla_o ||
+        kv_share || sink || gr || ced_split || ced_kv || csa2) {
+        set_err(err, errlen, "model.bin v%d: a mechanism outside the implemented spec path "
+                "(looped schedule, draft slots, rotated vocabulary, input mixing, MLA, KV sharing, sinks, GR, CED "
+                "or CSA2)", ver);
+        return LZ_ERR_BIN_VERSION;
+    }
     // resolve_hadamard (src/model.c:139-182): -1 derives the block from the
     // widths; an explicit block is 0 (off) or a power of two dividing its
     // width (lin_value_dim for hadamard_o, intermediate_size and the MTP
@@ -318,14 +434,14 @@ int parse_model(Bin &b, LZModelConfig &c, HostTensor &embed, HostTensor &fnorm,
         (c.use_subn && (c.num_experts < 1 || c.hidden_size > 2048 || c.lin_value_dim > 2048 ||
                         c.attn_q_dim > 2048 || c.mtp_intermediate_size > 2048 || c.moe_shared_width > 2048 ||
                         c.moe_latent_dim > 2048)) ||
-        rope_type != 0 || c.mtp_n_layers != 1 || c.num_experts > MAX_EXPERTS ||
+        rope_type != 0 || c.mtp_n_layers > 1 || c.mtp_n_layers < 0 || c.num_experts > MAX_EXPERTS ||
         c.num_experts_per_token > MAX_TOPK || c.lin_n_k_heads != c.lin_n_v_heads ||
         c.rotary_dim != c.head_dim || c.hidden_size % 32 || c.n_layers > 128) {
         set_err(err, errlen, "model variant outside the implemented spec path");
         return LZ_ERR_BIN_VERSION;
     }
     const int d = c.hidden_size;
-    embed = rd_q8(b, c.vocab_size, d);
+    embed = rd_q8(b, c.vocab_size, d, layout_out);
     fnorm = rd_f32(b, d);
     L.resize(c.n_layers);
     for (int l = 0; l < c.n_layers && !b.bad; l++) {
@@ -334,10 +450,10 @@ int parse_model(Bin &b, LZModelConfig &c, HostTensor &embed, HostTensor &fnorm,
         h.in_norm = rd_f32(b, d);
         h.post_norm = rd_f32(b, d);
         if (h.type == 1) {
-            h.q = rd_q8(b, c.attn_qgate_dim, d);
-            h.k = rd_q8(b, c.attn_kv_dim, d);
-            h.v = rd_q8(b, c.attn_kv_dim, d);
-            h.o = rd_q8(b, d, c.attn_q_dim);
+            h.q = rd_q8(b, c.attn_qgate_dim, d, layout_out);
+            h.k = rd_q8(b, c.attn_kv_dim, d, layout_out);
+            h.v = rd_q8(b, c.attn_kv_dim, d, layout_out);
+            h.o = rd_q8(b, d, c.attn_q_dim, layout_out);
             h.q_norm = rd_f32(b, c.head_dim);
             h.k_norm = rd_f32(b, c.head_dim);
             if (c.use_subn) {
@@ -347,20 +463,20 @@ int parse_model(Bin &b, LZModelConfig &c, HostTensor &embed, HostTensor &fnorm,
         } else if (h.type == 2) {
             int key = c.lin_key_dim, value = c.lin_value_dim, K = c.conv_kernel;
             int nvk = c.lin_n_v_heads * c.lin_k_head_dim;
-            h.kq = rd_q8(b, key, d);
-            h.kk = rd_q8(b, key, d);
-            h.kv = rd_q8(b, value, d);
+            h.kq = rd_q8(b, key, d, layout_out);
+            h.kk = rd_q8(b, key, d, layout_out);
+            h.kv = rd_q8(b, value, d, layout_out);
             h.convq = rd_f32(b, key * K);
             h.convk = rd_f32(b, key * K);
             h.convv = rd_f32(b, value * K);
             h.a_log = rd_f32(b, c.lin_n_v_heads);
-            h.fa = rd_q8(b, c.kda_gate_rank, d);
-            h.fb = rd_q8(b, nvk, c.kda_gate_rank);
+            h.fa = rd_q8(b, c.kda_gate_rank, d, layout_out);
+            h.fb = rd_q8(b, nvk, c.kda_gate_rank, layout_out);
             h.dt_bias = rd_f32(b, nvk);
-            h.kb = rd_q8(b, c.lin_n_v_heads, d);
-            h.kg = rd_q8(b, value, d);
+            h.kb = rd_q8(b, c.lin_n_v_heads, d, layout_out);
+            h.kg = rd_q8(b, value, d, layout_out);
             h.o_norm = rd_f32(b, c.lin_v_head_dim);
-            h.ko = rd_q8(b, d, value);
+            h.ko = rd_q8(b, d, value, layout_out);
             if (c.use_subn) {
                 h.kn_q = rd_f32(b, d); h.kn_k = rd_f32(b, d); h.kn_v = rd_f32(b, d); h.kn_g = rd_f32(b, d);
                 h.kn_o = rd_f32(b, value);
@@ -369,42 +485,46 @@ int parse_model(Bin &b, LZModelConfig &c, HostTensor &embed, HostTensor &fnorm,
             set_err(err, errlen, "layer %d: unsupported layer type %d", l, h.type);
             return LZ_ERR_BIN_VERSION;
         }
-        h.router = rd_q8(b, c.num_experts, d);
+        h.router = rd_q8(b, c.num_experts, d, layout_out);
         h.bias = rd_f32(b, c.num_experts);
-        h.down = rd_q8(b, c.moe_latent_dim, d);
-        h.up = rd_q8(b, d, c.moe_latent_dim);
-        h.sg = rd_q8(b, c.moe_shared_width, d);
-        h.su = rd_q8(b, c.moe_shared_width, d);
-        h.sd = rd_q8(b, d, c.moe_shared_width);
+        h.down = rd_q8(b, c.moe_latent_dim, d, layout_out);
+        h.up = rd_q8(b, d, c.moe_latent_dim, layout_out);
+        h.sg = rd_q8(b, c.moe_shared_width, d, layout_out);
+        h.su = rd_q8(b, c.moe_shared_width, d, layout_out);
+        h.sd = rd_q8(b, d, c.moe_shared_width, layout_out);
         if (c.use_subn) {
             h.mn_gate = rd_f32(b, d); h.mn_down = rd_f32(b, d); h.mn_up = rd_f32(b, c.moe_latent_dim);
             h.mn_sg = rd_f32(b, d); h.mn_su = rd_f32(b, d); h.mn_sd = rd_f32(b, c.moe_shared_width);
         }
         for (int e = 0; e < c.num_experts; e++) {
-            h.w1.push_back(rd_q8(b, c.moe_intermediate_size, c.moe_latent_dim));
-            h.w2.push_back(rd_q8(b, c.moe_latent_dim, c.moe_intermediate_size));
-            h.w3.push_back(rd_q8(b, c.moe_intermediate_size, c.moe_latent_dim));
+            h.w1.push_back(rd_q8(b, c.moe_intermediate_size, c.moe_latent_dim, layout_out));
+            h.w2.push_back(rd_q8(b, c.moe_latent_dim, c.moe_intermediate_size, layout_out));
+            h.w3.push_back(rd_q8(b, c.moe_intermediate_size, c.moe_latent_dim, layout_out));
         }
     }
     mtp.type = 1;
+    if (c.mtp_n_layers == 0) {      // no MTP head (a version-4 file)
+        if (b.bad || b.off != b.n) { set_err(err, errlen, "model.bin layout mismatch"); return LZ_ERR_BIN_OPEN; }
+        return 0;
+    }
     mtp.in_norm = rd_f32(b, d);
     mtp.post_norm = rd_f32(b, d);
     if (c.use_subn) { mtp.fn_gate = rd_f32(b, d); mtp.fn_up = rd_f32(b, d); }
-    mtp.q = rd_q8(b, c.attn_qgate_dim, d);
-    mtp.k = rd_q8(b, c.attn_kv_dim, d);
-    mtp.v = rd_q8(b, c.attn_kv_dim, d);
-    mtp.o = rd_q8(b, d, c.attn_q_dim);
+    mtp.q = rd_q8(b, c.attn_qgate_dim, d, layout_out);
+    mtp.k = rd_q8(b, c.attn_kv_dim, d, layout_out);
+    mtp.v = rd_q8(b, c.attn_kv_dim, d, layout_out);
+    mtp.o = rd_q8(b, d, c.attn_q_dim, layout_out);
     mtp.q_norm = rd_f32(b, c.head_dim);
     mtp.k_norm = rd_f32(b, c.head_dim);
     if (c.use_subn) {
         mtp.sn_q = rd_f32(b, d); mtp.sn_k = rd_f32(b, d); mtp.sn_v = rd_f32(b, d);
         mtp.sn_o = rd_f32(b, c.attn_q_dim);
     }
-    mg = rd_q8(b, c.mtp_intermediate_size, d);
-    mu = rd_q8(b, c.mtp_intermediate_size, d);
-    md = rd_q8(b, d, c.mtp_intermediate_size);
+    mg = rd_q8(b, c.mtp_intermediate_size, d, layout_out);
+    mu = rd_q8(b, c.mtp_intermediate_size, d, layout_out);
+    md = rd_q8(b, d, c.mtp_intermediate_size, layout_out);
     if (c.use_subn) mtp.fn_down = rd_f32(b, c.mtp_intermediate_size);
-    fc = rd_q8(b, d, 2 * d);
+    fc = rd_q8(b, d, 2 * d, layout_out);
     mn = rd_f32(b, d);
     mph = rd_f32(b, d);
     mpe = rd_f32(b, d);
@@ -463,6 +583,7 @@ void upload_all(Uploader &u, DModel *m, const HostTensor &embed, const HostTenso
     }
     DLayer &M = m->mtp;
     M.type = 1;
+    if (c.mtp_n_layers > 0) {
     M.in_norm = u.vec(hm.in_norm); M.post_norm = u.vec(hm.post_norm);
     M.q = u.mat(hm.q); M.k = u.mat(hm.k); M.v = u.mat(hm.v); M.o = u.mat(hm.o);
     M.q_norm = u.vec(hm.q_norm); M.k_norm = u.vec(hm.k_norm);
@@ -472,6 +593,7 @@ void upload_all(Uploader &u, DModel *m, const HostTensor &embed, const HostTenso
     }
     m->mtp_gate = u.mat(mg); m->mtp_up = u.mat(mu); m->mtp_down = u.mat(md); m->mtp_fc = u.mat(fc);
     m->mtp_norm = u.vec(mn); m->mtp_pre_h = u.vec(mph); m->mtp_pre_e = u.vec(mpe);
+    }
     {
         std::vector<float> cs((size_t)c.seq_len * c.rotary_dim);
         l98_rope_table(cs.data(), c.seq_len, c.rotary_dim, c.rope_theta);
@@ -511,7 +633,10 @@ extern "C" int lz_open(LZModel *m, const char *dir, char *errbuf, int errlen) {
     HostTensor embed, fnorm, mg, mu, md, fc, mn, mph, mpe;
     std::vector<HostLayer> HL;
     HostLayer hm;
-    int rc = parse_model(b, dm->c, embed, fnorm, HL, hm, mg, mu, md, fc, mn, mph, mpe, errbuf, errlen);
+    int ver = 5, layout = 0;
+    int rc = parse_model(b, dm->c, embed, fnorm, HL, hm, mg, mu, md, fc, mn, mph, mpe, errbuf, errlen, ver, layout);
+    dm->version = ver;
+    dm->has_mtp = dm->c.mtp_n_layers > 0;
     if (rc == 0 && ensure_tables() != 0) { set_err(errbuf, errlen, "HIP device not usable"); rc = 1; }
     if (rc == 0) {
         Uploader cnt{dm, true};
@@ -588,7 +713,8 @@ extern "C" int lz_load_config(LZModelConfig *c, const char *path, char *errbuf, 
     HostTensor embed, fnorm, mg, mu, md, fc, mn, mph, mpe;
     std::vector<HostLayer> HL;
     HostLayer hm;
-    int rc = parse_model(b, cfg, embed, fnorm, HL, hm, mg, mu, md, fc, mn, mph, mpe, errbuf, errlen);
+    int ver = 5, layout = 0;
+    int rc = parse_model(b, cfg, embed, fnorm, HL, hm, mg, mu, md, fc, mn, mph, mpe, errbuf, errlen, ver, layout);
     munmap(map, (size_t)st.st_size);
     if (rc != 0) return 1;
     *c = cfg;
@@ -768,6 +894,7 @@ Prologue PW(const Prologue &in, const float *w) {
 GemvJob J(const DMat &w, float *out, int out_stride, const Prologue &pro) {
     GemvJob j{};
     j.w = w.q; j.ws = w.s; j.out = out; j.rows = w.rows; j.in_dim = w.cols; j.out_stride = out_stride;
+    j.gs = w.gs == w.cols ? 0 : w.gs;
     j.pro = pro;
     return j;
 }
@@ -780,7 +907,7 @@ GemvJob JX(const DMat &w, float *out, int out_stride, const int8_t *xq, const fl
 
 ExpertJob EJ(const ExpertBank &bank, float *out, int by_pair, const Prologue &pro) {
     ExpertJob j{};
-    j.q = bank.q; j.s = bank.s; j.out = out; j.xq_by_pair = by_pair; j.pro = pro;
+    j.q = bank.q; j.s = bank.s; j.out = out; j.xq_by_pair = by_pair; j.pro = pro; j.gs = bank.gs;
     return j;
 }
 
@@ -881,7 +1008,7 @@ int kda_block(DState *s, const DLayer &L, const Prologue &in, int li, int nt, in
     const int hist = c.conv_kernel - 1;
     KdaStepArgs a{};
     a.pq = s->pq; a.pk = s->pk; a.pv = s->pv; a.pfa = s->pfa;
-    a.fb_q = L.fb.q; a.fb_s = L.fb.s;
+    a.fb_q = L.fb.q; a.fb_s = L.fb.s; a.fb_gs = L.fb.gs == L.fb.cols ? 0 : L.fb.gs;
     a.conv_w = L.conv;
     a.conv_ring = s->conv + (size_t)li * c.lin_conv_dim * hist;
     a.conv_slot_stride = s->conv_slot;
@@ -961,7 +1088,7 @@ int forward_chunk(DState *s, const int *toks, int nt, const int *ctl_pos, int po
     int cur = 0;
     const bool fused = l98k_gemv_norm_fits(d, nt) != 0;
     if (c.use_subn && !fused) return -1;      // SubLN's per-projection norms run in the GEMV prologues
-    CK(l98k_embed(m->embed.q, m->embed.s, toks, d, nt, xb[cur], s->st));
+    CK(l98k_embed(m->embed.q, m->embed.s, toks, d, m->embed.gs, nt, xb[cur], s->st));
     const float *ra = nullptr, *rb = nullptr;     // pending residual of the previous block
     // Input rows of a block: the fused norm prologue, or a norm kernel that
     // folds the residual in place and quantizes into xq.
@@ -1009,7 +1136,7 @@ int draft_step(DState *s, const int *toks, const int *ctl_pos, int pos_off, int 
     const LZModelConfig &c = m->c;
     const int d = c.hidden_size, I = c.mtp_intermediate_size;
     const float eps = c.rms_norm_eps;
-    CK(l98k_mtp_pre(m->embed.q, m->embed.s, toks, s->chain, d, m->mtp_pre_e, m->mtp_pre_h, eps, 1, s->xq,
+    CK(l98k_mtp_pre(m->embed.q, m->embed.s, m->embed.gs, toks, s->chain, d, m->mtp_pre_e, m->mtp_pre_h, eps, 1, s->xq,
                     s->xqs, s->st));
     CK(gemv(s, {JX(m->mtp_fc, s->mtp_x, d, s->xq, s->xqs)}, 1));
     CK(attn_block(s, m->mtp, PN(s->mtp_x, d, nullptr, nullptr, m->mtp.in_norm, eps, nullptr, nullptr, 0),
@@ -1052,7 +1179,7 @@ int mtp_prefill_dev(DState *s, const float *h, const int *toks, int n, const int
     const float eps = c.rms_norm_eps;
     for (int done = 0; done < n;) {
         int k = n - done < MAX_CHUNK ? n - done : MAX_CHUNK;
-        CK(l98k_mtp_pre(m->embed.q, m->embed.s, toks + done, h + (size_t)done * d, d, m->mtp_pre_e,
+        CK(l98k_mtp_pre(m->embed.q, m->embed.s, m->embed.gs, toks + done, h + (size_t)done * d, d, m->mtp_pre_e,
                         m->mtp_pre_h, eps, k, s->xq, s->xqs, s->st));
         CK(gemv(s, {JX(m->mtp_fc, s->mtp_x, d, s->xq, s->xqs)}, k));
         CK(attn_block(s, m->mtp, PN(s->mtp_x, d, nullptr, nullptr, m->mtp.in_norm, eps, nullptr, nullptr, 0),
@@ -1108,10 +1235,12 @@ namespace {
 #define WIDE_MIN 16           // prefills shorter than this take the chunked path
 
 // nullptr (the callers take the chunked path) for a SubLN model, whose
-// per-projection norms this many-row forward does not carry.
+// per-projection norms this many-row forward does not carry, and for a
+// model with grouped weight scales (its matrix-core epilogue takes one
+// scale per row).
 DWide *wide_get(const DModel *cm) {
     DModel *m = const_cast<DModel *>(cm);
-    if (m->c.use_subn) return nullptr;
+    if (m->c.use_subn || m->grouped) return nullptr;
     if (m->wide) return m->wide;
     const LZModelConfig &c = m->c;
     const size_t R = WIDE_MAX, d = c.hidden_size, pairs = R * c.num_experts_per_token;
@@ -1217,7 +1346,7 @@ int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, 
         CK(hipMalloc((void **)&w->att_items, sizeof(float) * att_item * n_items));
         w->att_items_floats = att_item * n_items;
     }
-    CK(l98k_embed(m->embed.q, m->embed.s, w->toks, d, R, w->x, st));
+    CK(l98k_embed(m->embed.q, m->embed.s, w->toks, d, m->embed.gs, R, w->x, st));
     const float *ra = nullptr, *rb = nullptr;
     for (int l = 0; l < c.n_layers; l++) {
         const DLayer &L = m->L[l];
@@ -1282,7 +1411,7 @@ int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, 
             // sub-chunks inside its blocks)
             KdaStepArgs a{};
             a.pq = w->pq; a.pk = w->pk; a.pv = w->pv; a.pfa = w->pfa;
-            a.fb_q = L.fb.q; a.fb_s = L.fb.s;
+            a.fb_q = L.fb.q; a.fb_s = L.fb.s; a.fb_gs = L.fb.gs == L.fb.cols ? 0 : L.fb.gs;
             a.conv_w = L.conv;
             a.bvec = w->pb; a.gz = w->pg;
             a.a_log = L.a_log; a.dt_bias = L.dt_bias; a.o_norm = L.o_norm;
@@ -1521,6 +1650,7 @@ extern "C" float *lz_forward_batch_capture(const LZModel *mm, LZRunState *s, con
 
 extern "C" int lz_forward_verify(const LZModel *mm, LZRunState *s, const int *tokens, int n, int pos0) {
     if (!mm || !s || !s->impl || !tokens || n < 1 || n > LZ_BATCH_MAX) return 1;
+    if (!Mo(mm)->has_mtp) return 1;               // the verify needs the MTP head (src/forward.c:1780)
     DState *d = S(s);
     const LZModelConfig &c = d->m->c;
     if (!tok_ok(c, tokens, n) || pos0 < 0 || pos0 + n > d->seq_len) return 1;
@@ -1547,7 +1677,7 @@ extern "C" int lz_forward_verify(const LZModel *mm, LZRunState *s, const int *to
 }
 
 extern "C" float *lz_mtp_draft_step(const LZModel *mm, LZRunState *s, int next_token, int pos) {
-    if (!mm || !s || !s->impl) return nullptr;
+    if (!mm || !s || !s->impl || !Mo(mm)->has_mtp) return nullptr;
     DState *d = S(s);
     const LZModelConfig &c = d->m->c;
     if (next_token < 0 || next_token >= c.vocab_size || pos < 0 || pos >= d->seq_len) return nullptr;
@@ -1569,7 +1699,7 @@ extern "C" float *lz_mtp_draft_step(const LZModel *mm, LZRunState *s, int next_t
 
 extern "C" int lz_mtp_prefill(const LZModel *mm, LZRunState *s, const float *h_body_all,
                               const int *next_tokens, int n, int pos0) {
-    if (!mm || !s || !s->impl || !h_body_all || !next_tokens || n < 1) return 1;
+    if (!mm || !s || !s->impl || !h_body_all || !next_tokens || n < 1 || !Mo(mm)->has_mtp) return 1;
     DState *d = S(s);
     const LZModelConfig &c = d->m->c;
     if (!tok_ok(c, next_tokens, n) || pos0 < 0 || pos0 + n > d->seq_len || n > d->cap_rows) return 1;
@@ -1831,6 +1961,7 @@ extern "C" int lz_spec_round(const LZModel *mm, LZRunState *s, int anchor, int a
                              char *errbuf, int errlen) {
     if (!mm || !s || !out || !out_n_accept || !out_new_pos || !out_k_eff || !s->impl)
         return errset(errbuf, errlen, LZ_ERR_NULL_ARG, "null argument");
+    if (!Mo(mm)->has_mtp) return errset(errbuf, errlen, LZ_ERR_SPEC_NO_HEAD, "model has no MTP head");
     if (k < 1 || k > LZ_SPEC_K_MAX || k > s->ssm_ring_depth - 1) {
         set_err(errbuf, errlen, "spec_k %d out of range 1..%d", k,
                 k > LZ_SPEC_K_MAX ? LZ_SPEC_K_MAX : s->ssm_ring_depth - 1);
@@ -2023,6 +2154,7 @@ int spec_round_temp(const LZModel *mm, LZRunState *s, int anchor, int anchor_pos
                     int *out_k_eff, char *errbuf, int errlen, int k_cap) {
     if (!mm || !s || !samp || !out || !out_n_accept || !out_new_pos || !out_k_eff || !s->impl)
         return errset(errbuf, errlen, LZ_ERR_NULL_ARG, "null argument");
+    if (!Mo(mm)->has_mtp) return errset(errbuf, errlen, LZ_ERR_SPEC_NO_HEAD, "model has no MTP head");
     if (k < 1 || k > k_cap || k > s->ssm_ring_depth - 1) {
         set_err(errbuf, errlen, "spec_k %d out of range 1..%d", k, k > k_cap ? k_cap : s->ssm_ring_depth - 1);
         return -LZ_ERR_SPEC_K_RANGE;
@@ -2285,6 +2417,7 @@ extern "C" const char *l98_device_name(void) {
 extern "C" int l98_session_start(const LZModel *mm, LZRunState *s, const int *prompt, int n_prompt,
                                  const LZSampler *samp) {
     if (!mm || !s || !s->impl || !prompt || n_prompt < 2) return -LZ_ERR_NULL_ARG;
+    if (!Mo(mm)->has_mtp) return -LZ_ERR_SPEC_NO_HEAD;
     DState *d = S(s);
     const LZModelConfig &c = d->m->c;
     if (!tok_ok(c, prompt, n_prompt) || n_prompt >= d->seq_len) return -LZ_ERR_FORWARD;
@@ -2339,6 +2472,7 @@ extern "C" int l98_greedy_rounds_ex(const LZModel *mm, LZRunState *s, int k, int
                                     int *tokens, int cap, int *n_accept_out, int *experts_out,
                                     int *new_pos_out, float *device_ms) {
     if (!mm || !s || !s->impl || n_rounds < 1) return -LZ_ERR_NULL_ARG;
+    if (!Mo(mm)->has_mtp) return -LZ_ERR_SPEC_NO_HEAD;
     if (k < 1 || k > L98_SPEC_K_GPU || k > s->ssm_ring_depth - 1) return -LZ_ERR_SPEC_K_RANGE;
     DState *d = S(s);
     if (n_rounds > d->hist_cap) return -LZ_ERR_NULL_ARG;
@@ -2427,6 +2561,7 @@ static int batch_ok(const LZModel *mm, LZRunState **states, int n_seq) {
 extern "C" int l98_verify_batch(const LZModel *mm, LZRunState **states, int n_seq, const int *tokens, int n_tok,
                                 const int *pos0, int copy_out, float *wall_ms) {
     if (!batch_ok(mm, states, n_seq) || !tokens || !pos0 || n_tok < 1 || n_tok > LZ_BATCH_MAX) return 1;
+    if (!Mo(mm)->has_mtp) return 1;
     const LZModelConfig &c = Mo(mm)->c;
     for (int i = 0; i < n_seq; i++) {
         DState *d = S(states[i]);
@@ -2508,6 +2643,7 @@ extern "C" int l98_verify_batch(const LZModel *mm, LZRunState **states, int n_se
 extern "C" int l98_greedy_rounds_batch(const LZModel *mm, LZRunState **states, int n_seq, int k, int n_rounds,
                                        int *tokens, int cap, int *n_out, float *wall_ms) {
     if (!batch_ok(mm, states, n_seq) || n_rounds < 1 || !n_out) return -LZ_ERR_NULL_ARG;
+    if (!Mo(mm)->has_mtp) return -LZ_ERR_SPEC_NO_HEAD;
     for (int i = 0; i < n_seq; i++) {
         LZRunState *s = states[i];
         DState *d = S(s);

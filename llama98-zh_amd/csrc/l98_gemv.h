@@ -358,6 +358,34 @@ __device__ __forceinline__ void tile_dot(const int4 (&wv)[GEMV_MAXJ], const int8
     }
 }
 
+// Epilogue of a row whose weight scales come in groups of r 32-element
+// groups (r = gs/32 < nb), epi_q8 (src/ops_epi.c:983-1022): r > 1, per run
+// of r groups dot = sum float(acc)*xqs from 0, sum += dot*ws[run] in run
+// order; r == 1, four accumulators take groups g, g+1, g+2, g+3 of each
+// whole four (the rest go to the first) as float(acc)*(xqs*ws), then
+// (a0 + a2) + (a1 + a3).  wsr: the row's scales (global memory).
+__device__ __forceinline__ float tile_epilogue_g(const int *pp, const float *xs, int nb, int r, const float *wsr) {
+    float sum = 0.0f;
+    if (r > 1) {
+        for (int run = 0; run < nb / r; run++) {
+            float dot = 0.0f;
+            for (int g = 0; g < r; g++) dot += (float)pp[run * r + g] * xs[run * r + g];
+            sum += dot * wsr[run];
+        }
+        return sum;
+    }
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+    int g = 0;
+    for (; g + 3 < nb; g += 4) {
+        a0 += (float)pp[g] * (xs[g] * wsr[g]);
+        a1 += (float)pp[g + 1] * (xs[g + 1] * wsr[g + 1]);
+        a2 += (float)pp[g + 2] * (xs[g + 2] * wsr[g + 2]);
+        a3 += (float)pp[g + 3] * (xs[g + 3] * wsr[g + 3]);
+    }
+    for (; g < nb; g++) a0 += (float)pp[g] * (xs[g] * wsr[g]);
+    return (a0 + a2) + (a1 + a3);
+}
+
 // Epilogue of one (row er, token et) pair: sum_s float(acc[s]) * xqs[s] in
 // group order, then times the row scale (src/ops_epi.c:983-1017); a
 // one-group row takes epi_one_group.
@@ -412,7 +440,9 @@ __device__ __forceinline__ void gemv_tile(const int8_t *__restrict__ wt, const f
                                           const float *__restrict__ xqs, const int (&xrow)[M], const int *s_orow,
                                           int nm, bool writer, float *__restrict__ out, size_t out_stride,
                                           int row0, int32_t *__restrict__ acc_out, int acc_rows, char *smem,
-                                          float *s_inv, float *tab) {
+                                          float *s_inv, float *tab, int gs = 0) {
+    // scales per row (ws holds [rows][nws]); one per row is the common case
+    const int nws = (gs > 0 && gs < in_dim) ? in_dim / gs : 1;
     const int tid = threadIdx.x;
     const int cpr = in_dim >> 4, nb = in_dim >> 5, pstride = nb + 4;
     const int nchunk = rows_here * cpr;
@@ -424,7 +454,7 @@ __device__ __forceinline__ void gemv_tile(const int8_t *__restrict__ wt, const f
     float wsv = 0.0f;
     auto issue_w = [&]() {
         tile_load(wv, wt, nchunk);
-        wsv = ws[row0 + imin(er, rows_here - 1)];     // the epilogue lane's row scale
+        wsv = ws[(size_t)(row0 + imin(er, rows_here - 1)) * nws];     // the epilogue lane's (first) row scale
     };
     build_rows<M, PJ, MODES>(P, xq, xqs, in_dim, xrow, nm, writer, sx, sxs, reinterpret_cast<float *>(part), s_inv,
                              tab, issue_w);
@@ -433,7 +463,9 @@ __device__ __forceinline__ void gemv_tile(const int8_t *__restrict__ wt, const f
     __syncthreads();
     if (er < rows_here && et < nm) {
         const int *pp = part + (er * M + et) * pstride;
-        out[(size_t)s_orow[et] * out_stride + row0 + er] = tile_epilogue(pp, sxs + et * nb, nb, wsv);
+        out[(size_t)s_orow[et] * out_stride + row0 + er] =
+            nws == 1 ? tile_epilogue(pp, sxs + et * nb, nb, wsv)
+                     : tile_epilogue_g(pp, sxs + et * nb, nb, gs >> 5, ws + (size_t)(row0 + er) * nws);
         if (acc_out)
             for (int g = 0; g < nb; g++) acc_out[((size_t)et * acc_rows + row0 + er) * nb + g] = pp[g];
     }

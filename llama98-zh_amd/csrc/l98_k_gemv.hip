@@ -27,7 +27,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv_q8(GemvBatch batch, int m
     for (int t = 0; t < M; t++) xrow[t] = t < m ? t : 0;
     gemv_tile<M, PJ, MODES>(job.w + (size_t)row0 * job.in_dim, job.ws, rows_here, job.R, job.in_dim, job.pro, job.xq,
                             job.xqs, xrow, s_row, m, blk == 0, job.out, job.out_stride, row0, job.acc_out, job.rows,
-                            smem, s_inv, tab);
+                            smem, s_inv, tab, job.gs);
 }
 
 // ---------------------------------------------------------- host glue ---
@@ -62,7 +62,7 @@ extern "C" int l98k_gemv(GemvBatch *b, int m, hipStream_t st) {
     for (int j = 0; j < b->n; j++) {
         GemvJob &J = b->job[j];
         if (J.in_dim < 32 || (J.in_dim & 31) || J.in_dim > GEMV_MAX_IN || J.rows < 1 ||
-            !prologue_ok(J.pro, J.in_dim, J.xq, J.xqs))
+            !prologue_ok(J.pro, J.in_dim, J.xq, J.xqs) || (J.gs && ((J.gs & 31) || J.in_dim % J.gs)))
             return -1;
         J.R = gemv_rows_per_tile(J.in_dim, M);
         J.tile0 = tiles;

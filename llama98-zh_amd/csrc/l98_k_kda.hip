@@ -100,7 +100,12 @@ __device__ __forceinline__ void kda_step_body(const KdaStepArgs &a, int h) {
     int4 fbw[KDA_MAX_RANK / 16];
 #pragma unroll
     for (int u = 0; u < KDA_MAX_RANK / 16; u++) fbw[u] = fbrow[imin(u, (rank >> 4) - 1)];
-    const float fbs = a.fb_s[h * KD + j];
+    // f_b's scales: one per row, or rank/fb_gs per row (groups of fb_gs)
+    const int fb_nws = (a.fb_gs > 0 && a.fb_gs < rank) ? rank / a.fb_gs : 1;
+    float fbsv[KDA_MAX_RANK / 32];
+#pragma unroll
+    for (int u = 0; u < KDA_MAX_RANK / 32; u++) fbsv[u] = a.fb_s[(size_t)(h * KD + j) * fb_nws + imin(u, fb_nws - 1)];
+    const float fbs = fbsv[0];
     const float bv = a.bvec[(size_t)imin(j, nt - 1) * a.nv + h];
     const float dtb = a.dt_bias[h * KD + j];
     const float onw = a.o_norm[j];
@@ -173,8 +178,10 @@ __device__ __forceinline__ void kda_step_body(const KdaStepArgs &a, int h) {
             const int tc = imin(t, nt - 1);
             float dot = 0.0f;
             int acc0 = 0;
+            int accg[KDA_MAX_RANK / 32];
 #pragma unroll
             for (int g = 0; g < KDA_MAX_RANK / 32; g++) {
+                accg[g] = 0;
                 if (g * 32 < rank) {
                     const int4 *xr = reinterpret_cast<const int4 *>(s_fq + tc * rank + g * 32);
                     const int4 x0 = xr[0], x1 = xr[1];
@@ -189,11 +196,49 @@ __device__ __forceinline__ void kda_step_body(const KdaStepArgs &a, int h) {
                     acc = __builtin_amdgcn_sdot4(w1.w, x1.w, acc, false);
                     dot += (float)acc * s_fs[(tc * rank >> 5) + g];
                     if (g == 0) acc0 = acc;
+                    accg[g] = acc;
                 }
             }
             float pre = 0.0f;
-            if (rank == 32) pre = epi_one_group(acc0, s_fs[tc * rank >> 5], fbs);
-            else pre += dot * fbs;
+            if (fb_nws > 1) {
+                // grouped scales (epi_q8 with r = fb_gs/32 < rank/32)
+                const int nb = rank >> 5, r = a.fb_gs >> 5;
+                const float *xs = s_fs + (tc * rank >> 5);
+                if (r > 1) {
+                    // runs of r groups (static register indices)
+                    int run = 0;
+                    float d2 = 0.0f;
+#pragma unroll
+                    for (int g = 0; g < KDA_MAX_RANK / 32; g++) {
+                        if (g < nb) {
+                            d2 += (float)accg[g] * xs[g];
+                            if ((g + 1) % r == 0) {
+                                const float wr = run == 0 ? fbsv[0] : run == 1 ? fbsv[1] : run == 2 ? fbsv[2] : fbsv[3];
+                                pre += d2 * wr;
+                                d2 = 0.0f;
+                                run++;
+                            }
+                        }
+                    }
+                } else {
+                    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+                    if (nb == 4) {
+                        a0 += (float)accg[0] * (xs[0] * fbsv[0]);
+                        a1 += (float)accg[1] * (xs[1] * fbsv[1]);
+                        a2 += (float)accg[2] * (xs[2] * fbsv[2]);
+                        a3 += (float)accg[3] * (xs[3] * fbsv[3]);
+                    } else {
+#pragma unroll
+                        for (int g = 0; g < KDA_MAX_RANK / 32; g++)
+                            if (g < nb) a0 += (float)accg[g] * (xs[g] * fbsv[g]);
+                    }
+                    pre = (a0 + a2) + (a1 + a3);
+                }
+            } else if (rank == 32) {
+                pre = epi_one_group(acc0, s_fs[tc * rank >> 5], fbs);
+            } else {
+                pre += dot * fbs;
+            }
             const float p = pre + dtb;
             const float gg = -decay * d_softplus(p, tab);
             s_g[t][j] = d_exp(gg, tab);

@@ -6,14 +6,16 @@
 // -------------------------------------------------------------- embed ---
 
 // lz_t_row_f32 for a Q8_0 per-row table: x = float(q) * scale[row].
+// lz_t_row_f32 of a Q8_0 row (src/ops_epi.c:1276-1280): q * its group's
+// scale, groups of gs (gs = d: one scale per row).
 __global__ void k_embed(const int8_t *__restrict__ q, const float *__restrict__ s,
-                        const int *__restrict__ toks, int d, float *__restrict__ x) {
+                        const int *__restrict__ toks, int d, int gs, float *__restrict__ x) {
     int t = blockIdx.y;
     int tok = toks[t];
     const int8_t *row = q + (size_t)tok * d;
-    float sc = s[tok];
+    const float *sr = s + (size_t)tok * (d / gs);
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < d; i += gridDim.x * blockDim.x)
-        x[(size_t)t * d + i] = (float)row[i] * sc;
+        x[(size_t)t * d + i] = (float)row[i] * sr[i / gs];
 }
 
 template <int PJ>
@@ -64,7 +66,7 @@ __global__ __launch_bounds__(64) void k_rmsnorm(float *__restrict__ x, int x_str
 template <int PJ>
 __global__ __launch_bounds__(64) void k_mtp_pre(const int8_t *__restrict__ emb_q, const float *__restrict__ emb_s,
                                                 const int *__restrict__ toks, const float *__restrict__ h,
-                                                int d, const float *__restrict__ w_e,
+                                                int d, int gs, const float *__restrict__ w_e,
                                                 const float *__restrict__ w_h, float eps,
                                                 int8_t *__restrict__ xq, float *__restrict__ xqs) {
     __shared__ __align__(16) float sq[ps_row_floats<4 * PJ>()];
@@ -76,10 +78,12 @@ __global__ __launch_bounds__(64) void k_mtp_pre(const int8_t *__restrict__ emb_q
     if (half == 0) {
         const int tok = toks[r];
         const uint32_t *er = reinterpret_cast<const uint32_t *>(emb_q + (size_t)tok * d);
-        const float sc = emb_s[tok];
+        const float *sr = emb_s + (size_t)tok * (d / gs);
 #pragma unroll
         for (int j = 0; j < PJ; j++) {
-            const uint32_t q = er[imin(lane + 64 * j, nf - 1)];
+            const int fe = imin(lane + 64 * j, nf - 1);
+            const uint32_t q = er[fe];
+            const float sc = sr[4 * fe / gs];      // the four codes share a 32-group
             v[j] = make_float4((float)(int8_t)(q & 0xFF) * sc, (float)(int8_t)((q >> 8) & 0xFF) * sc,
                                (float)(int8_t)((q >> 16) & 0xFF) * sc, (float)(int8_t)(q >> 24) * sc);
         }
@@ -264,9 +268,11 @@ extern "C" int l98k_upload_exp_table(const float *tab) {
     return l98k_upload_exp_table_attn(tab);
 }
 
-extern "C" int l98k_embed(const int8_t *q, const float *s, const int *toks, int d, int nt,
+extern "C" int l98k_embed(const int8_t *q, const float *s, const int *toks, int d, int gs, int nt,
                           float *x, hipStream_t st) {
-    hipLaunchKernelGGL(k_embed, dim3((d + 255) / 256, nt), dim3(256), 0, st, q, s, toks, d, x);
+    if (gs <= 0) gs = d;
+    if (gs & 31 || d % gs) return -1;
+    hipLaunchKernelGGL(k_embed, dim3((d + 255) / 256, nt), dim3(256), 0, st, q, s, toks, d, gs, x);
     return (int)hipGetLastError();
 }
 
@@ -296,13 +302,14 @@ extern "C" int l98k_rmsnorm(float *x, int x_stride, const float *a, const float 
     return l98k_rmsnorm_ex(x, x_stride, a, b, w, n, eps, rows, out, out_stride, xq, xqs, 0, st);
 }
 
-extern "C" int l98k_mtp_pre(const int8_t *emb_q, const float *emb_s, const int *toks, const float *h, int d,
-                            const float *w_e, const float *w_h, float eps, int rows, int8_t *xq, float *xqs,
+extern "C" int l98k_mtp_pre(const int8_t *emb_q, const float *emb_s, int gs, const int *toks, const float *h,
+                            int d, const float *w_e, const float *w_h, float eps, int rows, int8_t *xq, float *xqs,
                             hipStream_t st) {
-    if (d < 32 || d > 256 * 8 || (d & 31) || rows < 1) return -1;
+    if (gs <= 0) gs = d;
+    if (d < 32 || d > 256 * 8 || (d & 31) || rows < 1 || (gs & 31) || d % gs) return -1;
 #define PRE_LAUNCH(PJ)                                                                                  \
     if (d <= 256 * PJ) {                                                                                \
-        hipLaunchKernelGGL(k_mtp_pre<PJ>, dim3(rows, 2), dim3(64), 0, st, emb_q, emb_s, toks, h, d, w_e, \
+        hipLaunchKernelGGL(k_mtp_pre<PJ>, dim3(rows, 2), dim3(64), 0, st, emb_q, emb_s, toks, h, d, gs, w_e, \
                            w_h, eps, xq, xqs);                                                          \
         return (int)hipGetLastError();                                                                  \
     }

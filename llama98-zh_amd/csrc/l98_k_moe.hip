@@ -37,9 +37,10 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_expert_gemv(ExpertJob j0, Expe
         if (threadIdx.x == t) s_orow[t] = mem;
     }
     const int row0 = tile * R;
-    gemv_tile<M, PJ, MODES_S>(J.q + ((size_t)e * out_rows + row0) * in_dim, J.s + (size_t)e * out_rows,
+    const int nws = (J.gs > 0 && J.gs < in_dim) ? in_dim / J.gs : 1;
+    gemv_tile<M, PJ, MODES_S>(J.q + ((size_t)e * out_rows + row0) * in_dim, J.s + (size_t)e * out_rows * nws,
                              imin(R, out_rows - row0), R, in_dim, J.pro, J.xq, J.xqs, xrow, s_orow, nm, false, J.out,
-                             out_rows, row0, nullptr, 0, smem, s_inv, tab);
+                             out_rows, row0, nullptr, 0, smem, s_inv, tab, J.gs);
 }
 
 // ----------------------------------------------------------------- MoE ---
@@ -330,9 +331,10 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_up(ExpertJob j0, ExpertJob
         if (threadIdx.x == t) s_orow[t] = mem;
     }
     const int row0 = tile * R;
-    gemv_tile<M, PJ, MODES_Q>(J.q + ((size_t)e * out_rows + row0) * in_dim, J.s + (size_t)e * out_rows,
+    const int nws = (J.gs > 0 && J.gs < in_dim) ? in_dim / J.gs : 1;
+    gemv_tile<M, PJ, MODES_Q>(J.q + ((size_t)e * out_rows + row0) * in_dim, J.s + (size_t)e * out_rows * nws,
                              imin(R, out_rows - row0), R, in_dim, J.pro, J.xq, J.xqs, xrow, s_orow, nm, false, J.out,
-                             out_rows, row0, nullptr, 0, smem, s_inv, tab);
+                             out_rows, row0, nullptr, 0, smem, s_inv, tab, J.gs);
 }
 
 // ---------------------------------------------------------- host glue ---

@@ -68,7 +68,7 @@ int l98k_gemv_norm_fits(int in_dim, int m);
 // Grouped expert GEMV: n_jobs (<= 2) projections over the groups in grp.
 int l98k_expert_gemv(const ExpertJob *jobs, int n_jobs, const MoeGroups *grp, int max_groups, int in_dim,
                      int out_rows, int nt, hipStream_t st);
-int l98k_embed(const int8_t *q, const float *s, const int *toks, int d, int nt, float *x, hipStream_t st);
+int l98k_embed(const int8_t *q, const float *s, const int *toks, int d, int gs, int nt, float *x, hipStream_t st);
 // x += a (+ b) (when a), RMSNorm(1+w) -> out (when out) and per-32 int8 (when xq).
 int l98k_rmsnorm(float *x, int x_stride, const float *a, const float *b, const float *w, int n, float eps,
                  int rows, float *out, int out_stride, int8_t *xq, float *xqs, hipStream_t st);
@@ -78,7 +78,7 @@ int l98k_rmsnorm(float *x, int x_stride, const float *a, const float *b, const f
 int l98k_rmsnorm_ex(float *x, int x_stride, const float *a, const float *b, const float *w, int n, float eps,
                     int rows, float *out, int out_stride, int8_t *xq, float *xqs, int tok, hipStream_t st);
 // MTP input rows: [norm_e(embed(tok)) | norm_h(h)] quantized per 32 into xq [rows][2d].
-int l98k_mtp_pre(const int8_t *emb_q, const float *emb_s, const int *toks, const float *h, int d,
+int l98k_mtp_pre(const int8_t *emb_q, const float *emb_s, int gs, const int *toks, const float *h, int d,
                  const float *w_e, const float *w_h, float eps, int rows, int8_t *xq, float *xqs,
                  hipStream_t st);
 // One KDA layer step for a chunk: conv, gate up-projection, recurrence,

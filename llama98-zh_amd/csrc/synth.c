@@ -12,7 +12,7 @@
 
 /* Format codes of the reference (src/model.h:71-77) and layer kinds
  * (src/model.h:37-39). */
-enum { FMT_F32 = 0, FMT_Q8_0 = 1 };
+enum { FMT_F32 = 0, FMT_Q8_0 = 1, FMT_BF16 = 6 };
 enum { LT_FULL = 1, LT_KDA = 2 };
 #define MAX_LAYERS 128
 /* The echo variant (config 11): vocabulary and residual-writer std. */
@@ -134,6 +134,20 @@ int l98_synth_config(int id, L98SynthConfig *c) {
         c->n_experts = 128; c->topk = 8; c->latent = 512; c->moe_inter = 768;
         c->shared_w = 768; c->mtp_inter = 768;
         return 0;
+    case 13: case 16: case 17:
+        if (l98_synth_config(10, c)) return 1;
+        c->bin_version = id == 13 ? 9 : id == 16 ? 7 : 8;
+        c->gs = id == 16 ? 0 : 32;
+        c->scale_layout = id == 13 ? 1 : id == 17 ? 2 : 0;
+        c->bf16_small = id == 13 ? 1 : 0;
+        return 0;
+    case 14: case 15:
+        if (l98_synth_config(0, c)) return 1;
+        c->bin_version = id == 14 ? 6 : 4;
+        c->gs = id == 14 ? 128 : 64;
+        c->scale_layout = id == 14 ? 2 : 0;
+        c->bf16_small = id == 14 ? 1 : 0;
+        return 0;
     case 10: case 11: case 12:
         c->vocab = 512; c->hidden = 64; c->n_layers = 4; c->seq_len = 160;
         c->n_heads = 2; c->n_kv_heads = 1; c->head_dim = 32;
@@ -165,7 +179,58 @@ typedef struct {
     uint32_t tensor_id;         /* position in model_walk order */
     int n_threads;
     int failed;
+    int gs, scale_layout, bf16;  /* Q8_0 group size (0: per row), scale plane, BF16 small tensors */
 } Writer;
+
+/* IEEE binary16 from binary32, round to nearest even (finite, normal or
+ * subnormal results; the scales written here are far inside the range). */
+static uint16_t f32_to_f16(float f) {
+    union { float f; uint32_t u; } b;
+    b.f = f;
+    uint32_t sign = (b.u >> 16) & 0x8000u, a = b.u & 0x7FFFFFFFu;
+    if (a >= 0x477FF000u) return (uint16_t)(sign | 0x7BFFu);          /* clamp to the largest finite */
+    if (a < 0x33000001u) return (uint16_t)sign;                        /* rounds to zero */
+    int e = (int)(a >> 23) - 127;
+    uint32_t m = (a & 0x7FFFFFu) | 0x800000u;
+    int shift = e >= -14 ? 13 : 13 + (-14 - e);                        /* subnormals shift further */
+    uint32_t r = m >> shift, rem = m & ((1u << shift) - 1u), half = 1u << (shift - 1);
+    if (rem > half || (rem == half && (r & 1u))) r++;
+    uint32_t h;
+    if (e >= -14) h = ((uint32_t)(e + 15) << 10) + (r - 0x400u);       /* a carry into the exponent is fine */
+    else h = r;
+    return (uint16_t)(sign | h);
+}
+static float f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 0x1Fu, m = h & 0x3FFu, u;
+    if (e == 0) {
+        if (m == 0) u = sign;
+        else {
+            int sh = 0;
+            while (!(m & 0x400u)) { m <<= 1; sh++; }
+            u = sign | ((uint32_t)(127 - 14 - sh) << 23) | ((m & 0x3FFu) << 13);
+        }
+    } else {
+        u = sign | ((e + 127u - 15u) << 23) | (m << 13);
+    }
+    union { uint32_t u; float f; } b;
+    b.u = u;
+    return b.f;
+}
+/* bf16 of an f32, round to nearest even (finite inputs). */
+static uint16_t f32_to_bf16(float f) {
+    union { float f; uint32_t u; } b;
+    b.f = f;
+    uint32_t r = b.u + 0x7FFFu + ((b.u >> 16) & 1u);
+    return (uint16_t)(r >> 16);
+}
+/* The layout-2 decode the reader applies: base * (u / 255), each step
+ * rounded to float. */
+static float u8_decode(float base, float u) {
+    volatile float levels = 255.0f;
+    volatile float q = u / levels;
+    volatile float p = base * q;
+    return p;
+}
 
 static void put_bytes(Writer *w, const void *p, size_t n) {
     if (!w->failed && fwrite(p, 1, n, w->f) != n) w->failed = 1;
@@ -183,9 +248,12 @@ typedef struct {
     InitKind kind;
     float a, b;                 /* NORMAL: std, mean; UNIFORM: lo, hi; CONST: value */
     int quantize;
+    int gs, layout;             /* Q8: group size, scale plane layout */
     float *f;                   /* rows*cols floats (F32 tensors) */
     int8_t *q;                  /* rows*cols int8 (Q8 tensors) */
-    float *scale;               /* rows scales */
+    float *scale;               /* rows*cols/gs decoded scales */
+    uint16_t *s16;              /* layout 1: binary16 per group; layout 2: binary16 per row */
+    uint8_t *u8;                /* layout 2: u8 per group */
     int r0, r1;
 } Job;
 
@@ -228,22 +296,47 @@ static void *job_run(void *arg) {
             memcpy(j->f + (size_t)r * j->cols, row, sizeof(float) * (size_t)j->cols);
             continue;
         }
-        /* Per-output-row symmetric int8: s = amax/127, q = rne(w/s). */
-        float amax = 0.0f;
-        for (int c = 0; c < j->cols; c++) {
-            float a = row[c] < 0 ? -row[c] : row[c];
-            if (a > amax) amax = a;
+        /* Symmetric int8 per group of gs: s = amax/127 in the stored form
+         * (f32, binary16, or a row's binary16 base times u8/255), then
+         * q = rne(w / s) with the scale the reader decodes. */
+        const int ng = j->cols / j->gs;
+        float sg[4096];
+        float base = 0.0f;
+        for (int g = 0; g < ng; g++) {
+            float amax = 0.0f;
+            for (int c = g * j->gs; c < (g + 1) * j->gs; c++) {
+                float a = row[c] < 0 ? -row[c] : row[c];
+                if (a > amax) amax = a;
+            }
+            sg[g] = amax > 0.0f ? amax / 127.0f : 1.0f;
+            if (sg[g] > base) base = sg[g];
         }
-        float s = amax > 0.0f ? amax / 127.0f : 1.0f;
+        if (j->layout == 2) {
+            const uint16_t b16 = f32_to_f16(base);
+            const float bd = f16_to_f32(b16);
+            j->s16[r] = b16;
+            for (int g = 0; g < ng; g++) {
+                int u = (int)__builtin_rintf(255.0f * (sg[g] / bd));
+                u = u < 1 ? 1 : u > 255 ? 255 : u;
+                j->u8[(size_t)r * ng + g] = (uint8_t)u;
+                sg[g] = u8_decode(bd, (float)u);
+            }
+        } else if (j->layout == 1) {
+            for (int g = 0; g < ng; g++) {
+                const uint16_t h = f32_to_f16(sg[g]);
+                j->s16[(size_t)r * ng + g] = h;
+                sg[g] = f16_to_f32(h);
+            }
+        }
         int8_t *qr = j->q + (size_t)r * j->cols;
         for (int c = 0; c < j->cols; c++) {
-            float v = amax > 0.0f ? row[c] / s : 0.0f;
-            int qi = (int)__builtin_rintf(v);
+            const float s = sg[c / j->gs];
+            int qi = (int)__builtin_rintf(row[c] / s);
             if (qi > 127) qi = 127;
             if (qi < -127) qi = -127;
             qr[c] = (int8_t)qi;
         }
-        j->scale[r] = s;
+        for (int g = 0; g < ng; g++) j->scale[(size_t)r * ng + g] = sg[g];
     }
     free(row);
     return NULL;
@@ -258,15 +351,20 @@ static void emit_tensor(Writer *w, int rows, int cols, InitKind kind, float a,
     memset(&base, 0, sizeof(base));
     base.seed = w->seed; base.tensor_id = tid; base.rows = rows; base.cols = cols;
     base.kind = kind; base.a = a; base.b = b; base.quantize = quantize;
+    base.gs = (w->gs > 0 && cols % w->gs == 0 && cols / w->gs <= 4096) ? w->gs : cols;
+    base.layout = w->scale_layout;
+    const size_t ngt = n / (size_t)base.gs;
     if (quantize) {
         base.q = (int8_t *)malloc(n);
-        base.scale = (float *)malloc(sizeof(float) * (size_t)rows);
+        base.scale = (float *)malloc(sizeof(float) * ngt);
+        base.s16 = (uint16_t *)malloc(sizeof(uint16_t) * (ngt > (size_t)rows ? ngt : (size_t)rows));
+        base.u8 = (uint8_t *)malloc(ngt);
     } else {
         base.f = (float *)malloc(sizeof(float) * n);
     }
-    if ((quantize && (!base.q || !base.scale)) || (!quantize && !base.f)) {
+    if ((quantize && (!base.q || !base.scale || !base.s16 || !base.u8)) || (!quantize && !base.f)) {
         w->failed = 1;
-        free(base.q); free(base.scale); free(base.f);
+        free(base.q); free(base.scale); free(base.f); free(base.s16); free(base.u8);
         return;
     }
     int nt = w->n_threads;
@@ -284,19 +382,30 @@ static void emit_tensor(Writer *w, int rows, int cols, InitKind kind, float a,
     }
     if (nt > 1)
         for (int t = 0; t < nt; t++) pthread_join(th[t], NULL);
-    /* Record: u8 dtype, u32 n, then Q8_0: u32 gs, int8[n], f32[n/gs]
-     * (scale_layout 0); F32: f32[n]  (reference src/model.c:3567-3812). */
-    uint8_t dt = quantize ? FMT_Q8_0 : FMT_F32;
+    /* Record: u8 dtype, u32 n, then Q8_0: u32 gs, int8[n], the scale plane
+     * (layout 0: f32[n/gs]; 1: binary16[n/gs]; 2: binary16[rows] row bases,
+     * u8[n/gs]); F32: f32[n]; BF16: u16[n]  (reference src/model.c:3424-3812). */
+    uint8_t dt = quantize ? FMT_Q8_0 : (w->bf16 ? FMT_BF16 : FMT_F32);
     put_bytes(w, &dt, 1);
     put_u32(w, (uint32_t)n);
     if (quantize) {
-        put_u32(w, (uint32_t)cols);
+        put_u32(w, (uint32_t)base.gs);
         put_bytes(w, base.q, n);
-        put_bytes(w, base.scale, sizeof(float) * (size_t)rows);
+        if (base.layout == 0) put_bytes(w, base.scale, sizeof(float) * ngt);
+        else if (base.layout == 1) put_bytes(w, base.s16, sizeof(uint16_t) * ngt);
+        else {
+            put_bytes(w, base.s16, sizeof(uint16_t) * (size_t)rows);
+            put_bytes(w, base.u8, ngt);
+        }
+    } else if (w->bf16) {
+        for (size_t i = 0; i < n; i++) {
+            const uint16_t h = f32_to_bf16(base.f[i]);
+            put_bytes(w, &h, 2);
+        }
     } else {
         put_bytes(w, base.f, sizeof(float) * n);
     }
-    free(base.q); free(base.scale); free(base.f);
+    free(base.q); free(base.scale); free(base.f); free(base.s16); free(base.u8);
 }
 
 static void matrix(Writer *w, int rows, int cols, float std) {
@@ -324,10 +433,19 @@ int l98_synth_write(const char *dir, const L98SynthConfig *c, uint64_t seed,
     }
     mkdir(dir, 0755);
     snprintf(path, sizeof(path), "%s/model.bin", dir);
+    const int ver = c->bin_version ? c->bin_version : 5;
+    if (ver < 4 || ver > 9 || (c->gs && (c->gs % 32)) || c->scale_layout < 0 || c->scale_layout > 2 ||
+        (ver < 6 && c->scale_layout != 0) || (ver == 4 && c->use_subn)) {
+        if (err && errlen > 0) snprintf(err, (size_t)errlen, "bad format options");
+        return 1;
+    }
     Writer w;
     memset(&w, 0, sizeof(w));
     w.seed = seed;
     w.n_threads = n_threads;
+    w.gs = c->gs;
+    w.scale_layout = c->scale_layout;
+    w.bf16 = c->bf16_small;
     w.f = fopen(path, "wb");
     if (!w.f) {
         if (err && errlen > 0)
@@ -349,9 +467,9 @@ int l98_synth_write(const char *dir, const L98SynthConfig *c, uint64_t seed,
         if (full) n_full++; else n_lin++;
     }
 
-    /* Header, in lz_open_bin's read order (src/model.c:3993-4200). */
+    /* Header, in lz_open_bin's read order (src/model.c:3993-4460). */
     put_bytes(&w, "L98Z", 4);
-    put_u32(&w, 5);
+    put_u32(&w, (uint32_t)ver);
     put_i32(&w, c->vocab); put_i32(&w, d); put_i32(&w, c->n_layers);
     put_i32(&w, c->seq_len); put_i32(&w, nh); put_i32(&w, nkv); put_i32(&w, hd);
     put_i32(&w, c->shared_w);                          /* intermediate_size (unused: no dense body layer) */
@@ -370,6 +488,7 @@ int l98_synth_write(const char *dir, const L98SynthConfig *c, uint64_t seed,
     put_i32(&w, 0);                                    /* first_k_dense_replace */
     put_i32(&w, 1); put_i32(&w, 1); put_i32(&w, 0);    /* renormalize, sigmoid, latent_use_norm */
     put_i32(&w, c->shared_w);
+    if (ver >= 5) {
     /* version-5 tail */
     put_i32(&w, 1); put_i32(&w, c->mtp_inter);         /* mtp_n_layers, mtp_intermediate_size */
     put_i32(&w, 0); put_f32(&w, 1.0f); put_f32(&w, 4096.0f);
@@ -384,6 +503,17 @@ int l98_synth_write(const char *dir, const L98SynthConfig *c, uint64_t seed,
     put_i32(&w, 4); put_i32(&w, 64); put_i32(&w, 1);   /* csa2_compress_m, topk, indexer_heads */
     put_i32(&w, hd); put_i32(&w, 1);                   /* indexer_head_dim, indexer_q_lora_rank */
     for (int i = 0; i < MAX_LAYERS; i++) put_i32(&w, 0);   /* csa2_compress_m_layer */
+    }
+    if (ver >= 6) {                                    /* the identity application table, ... */
+        put_i32(&w, c->n_layers);
+        for (int i = 0; i < MAX_LAYERS; i++) put_i32(&w, i < c->n_layers ? i : 0);   /* app_layer */
+        for (int i = 0; i < MAX_LAYERS; i++) put_i32(&w, 0);                        /* app_loop */
+        put_i32(&w, 1); put_i32(&w, 0); put_i32(&w, 0);    /* mtp_n_draft, embed_hadamard, embed_signs_seed */
+        put_i32(&w, c->scale_layout);
+    }
+    if (ver >= 7) put_i32(&w, 0);                      /* loop_input_mix */
+    if (ver >= 8) put_i32(&w, 0);                      /* ced_local */
+    if (ver >= 9) put_i32(&w, 2);                      /* loop_input_mix_from */
 
     const float ws = c->w_std;
     const float rs = c->router_std > 0.0f ? c->router_std : ws;
@@ -451,12 +581,14 @@ int l98_synth_write(const char *dir, const L98SynthConfig *c, uint64_t seed,
             matrix(&w, c->moe_inter, c->latent, ws);   /* w3 */
         }
     }
-    /* MTP block: full-attention rows, dense FFN, then the head's own.  The
+    /* MTP block (none in a version-4 file): full-attention rows, dense FFN,
+     * then the head's own.  The
      * echo head keeps the block's K/V rows (the MTP KV plane still fills)
      * but zeroes what it adds to its residual, and its fc passes the
      * normalized embedding half through (the hidden half adds a little
      * noise, so the chain moves a step's top-1 probability), so its logits
      * are about E . norm(E[tok]) and the draft is the input token. */
+    if (ver >= 5) {
     vec_norm(&w, d, 0.0f, ws);
     vec_norm(&w, d, 0.0f, ws);
     if (c->use_subn) {                                 /* mlp.gate/up_proj.norm */
@@ -486,6 +618,7 @@ int l98_synth_write(const char *dir, const L98SynthConfig *c, uint64_t seed,
     vec_norm(&w, d, 0.0f, ws);                         /* mtp.norm */
     vec_norm(&w, d, 0.0f, ws);                         /* pre_fc_norm_hidden */
     vec_norm(&w, d, 0.0f, ws);                         /* pre_fc_norm_embedding */
+    }
 
     if (fclose(w.f) != 0) w.failed = 1;
     if (w.failed) {

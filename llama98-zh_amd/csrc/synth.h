@@ -41,6 +41,20 @@ typedef struct {
     int hadamard_o;             /* SubLN block Hadamard of the KDA o_proj input (0 off) */
     int hadamard_down;          /* SubLN block Hadamard of the dense FFN down_proj
                                    input (the MTP head's FFN; 0 off) */
+    int bin_version;            /* model.bin version word: 4..9 (0: 5).  4 is the
+                                   published shape: the 13-word tail only, so no
+                                   MTP head and none of its tensors; 6..9 append
+                                   the application table (identity), mtp_n_draft
+                                   1, no rotated vocabulary, the scale layout, and
+                                   from 7 / 8 / 9 loop_input_mix 0, ced_local 0,
+                                   loop_input_mix_from 2 */
+    int gs;                     /* Q8_0 group size (a multiple of 32 dividing the
+                                   row; 0: one group per row) */
+    int scale_layout;           /* Q8_0 scale plane (version >= 6): 0 f32 per
+                                   group, 1 binary16 per group, 2 a binary16 base
+                                   per row and a u8 per group (base * u / 255) */
+    int bf16_small;             /* 1: the F32 tensors (norms, conv taps, A_log,
+                                   dt_bias, router bias) stored as BF16 */
 } L98SynthConfig;
 
 /* Named configurations:
@@ -57,6 +71,13 @@ typedef struct {
  *              hadamard_down = 256 (the survey's C1s variant)
  *  12  micro-subln  micro's shapes with use_subn = 1, hadamard_o = 32,
  *              hadamard_down = 64
+ *  13  micro's shapes as a version-9 file: Q8_0 groups of 32, binary16
+ *              scales, BF16 small tensors
+ *  14  tiny's shapes as a version-6 file: Q8_0 groups of 128, scale layout 2
+ *              (row base + u8 codes), BF16 small tensors
+ *  15  tiny's shapes as a version-4 file (no MTP head): groups of 64
+ *  16  micro's shapes as a version-7 file, per-row groups, f32 scales
+ *  17  micro's shapes as a version-8 file, groups of 32, scale layout 2
  * Returns 0 on success, 1 for an unknown id. */
 int l98_synth_config(int id, L98SynthConfig *out);
 

@@ -362,42 +362,63 @@ ORA_API void o_subn_rot_f32(float *x, int n, int blk) {
     for (i = 0; i < n; i++) x[i] *= inv;
 }
 
-/* lz_matmul_xq_nt for a Q8_0 per-row weight (gs = in), SIMD row kernel +
- * epi_q8 (src/ops_matmul.c:336-466; src/ops_epi.c:983-1022), r = gs/32:
+/* lz_matmul_xq_nt for a Q8_0 weight with groups of gs (a multiple of 32
+ * dividing in), the SIMD row kernel + epi_q8 (src/ops_matmul.c:336-466;
+ * src/ops_epi.c:983-1022), r = gs/32, wsr the row's in/gs scales:
  *   acc[t,i,s] = sum_{e<32} w[i,32s+e] xq[t,32s+e]       (exact int32)
- *   r > 1 (in > 32): dot = sum_s float(acc)*xqs[t,s] (serial from 0.0f),
- *                    o = 0.0f + dot*ws[i]
- *   r == 1 (in == 32, one group): a0 = 0.0f + float(acc)*(xqs[t,0]*ws[i]),
- *                    o = (a0 + 0.0f) + (0.0f + 0.0f)  (four accumulators,
- *                    three of them untouched)
+ *   r > 1: per run of r groups from 0.0f, dot = sum float(acc)*xqs (in s
+ *          order); sum (from 0.0f) += dot*wsr[run], runs in order; o = sum
+ *   r == 1: four accumulators a[j] (from 0.0f), group s adds
+ *          float(acc)*(xqs[s]*wsr[s]) to a[s % 4] for the groups of whole
+ *          fours and to a[0] for the rest; o = (a0 + a2) + (a1 + a3)
  * The SIMD kernel's x256 accumulator and 2^-8 post-scale are exact powers of
  * two and cancel.  acc_out (optional) receives acc[t][i][s]. */
-ORA_API void o_matmul_q8(float *o, const int8_t *xq, const float *xqs,
-                         const int8_t *w, const float *ws, int in, int out, int nt,
-                         int32_t *acc_out) {
-    int nb = in / 32;
+ORA_API void o_matmul_q8g(float *o, const int8_t *xq, const float *xqs,
+                          const int8_t *w, const float *ws, int in, int out, int nt, int gs,
+                          int32_t *acc_out) {
+    const int nb = in / 32, r = gs / 32, nws = in / gs;
+    int32_t acc[512];
     for (int i = 0; i < out; i++) {
         const int8_t *wr = w + (size_t)i * in;
+        const float *wsr = ws + (size_t)i * nws;
         for (int t = 0; t < nt; t++) {
             const int8_t *xr = xq + (size_t)t * in;
-            float dot = 0.0f, sum = 0.0f;
-            for (int s = 0; s < nb; s++) {
-                int32_t acc = 0;
-                for (int e = 0; e < 32; e++)
-                    acc += (int32_t)wr[s * 32 + e] * (int32_t)xr[s * 32 + e];
-                if (acc_out) acc_out[((size_t)t * out + i) * nb + s] = acc;
-                if (nb == 1) {
-                    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-                    a0 += (float)acc * (xqs[(size_t)t * nb] * ws[i]);
-                    sum = (a0 + a2) + (a1 + a3);
-                } else {
-                    dot += (float)acc * xqs[(size_t)t * nb + s];
-                }
+            const float *xs = xqs + (size_t)t * nb;
+            for (int g = 0; g < nb; g++) {
+                int32_t a = 0;
+                for (int e = 0; e < 32; e++) a += (int32_t)wr[g * 32 + e] * (int32_t)xr[g * 32 + e];
+                acc[g] = a;
+                if (acc_out) acc_out[((size_t)t * out + i) * nb + g] = a;
             }
-            if (nb > 1) sum += dot * ws[i];
+            float sum = 0.0f;
+            if (r > 1) {
+                for (int run = 0; run < nb / r; run++) {
+                    float dot = 0.0f;
+                    for (int g = 0; g < r; g++) dot += (float)acc[run * r + g] * xs[run * r + g];
+                    sum += dot * wsr[run];
+                }
+            } else {
+                float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+                int g = 0;
+                for (; g + 3 < nb; g += 4) {
+                    a0 += (float)acc[g] * (xs[g] * wsr[g]);
+                    a1 += (float)acc[g + 1] * (xs[g + 1] * wsr[g + 1]);
+                    a2 += (float)acc[g + 2] * (xs[g + 2] * wsr[g + 2]);
+                    a3 += (float)acc[g + 3] * (xs[g + 3] * wsr[g + 3]);
+                }
+                for (; g < nb; g++) a0 += (float)acc[g] * (xs[g] * wsr[g]);
+                sum = (a0 + a2) + (a1 + a3);
+            }
             o[(size_t)t * out + i] = sum;
         }
     }
+}
+
+/* The per-row weight (gs = in). */
+ORA_API void o_matmul_q8(float *o, const int8_t *xq, const float *xqs,
+                         const int8_t *w, const float *ws, int in, int out, int nt,
+                         int32_t *acc_out) {
+    o_matmul_q8g(o, xq, xqs, w, ws, in, out, nt, in, acc_out);
 }
 
 /* lz_rope non-SIMD body, src/ops_rope.c:21-67 (NeoX half split). */
@@ -438,7 +459,7 @@ static void tap(const char *tag, int layer, const float *p, int n) {
 /* Model.                                                                  */
 /* ---------------------------------------------------------------------- */
 
-typedef struct { int rows, cols; int8_t *q; float *s; } QMat;
+typedef struct { int rows, cols, gs; int8_t *q; float *s; } QMat;   /* s: rows*cols/gs */
 
 typedef struct {
     int type;                                    /* 1 full, 2 KDA */
@@ -472,6 +493,7 @@ typedef struct {
     int gate_rank, n_experts, topk, moe_inter, latent, shared_w;
     int mtp_inter;
     int use_subn, hadamard_o, hadamard_down;
+    int version, scale_layout, has_mtp;
     QMat embed;
     float *final_norm;
     OLayer *L;
@@ -481,37 +503,104 @@ typedef struct {
     float *rope_cs;                              /* [seq_len][rot/2][2] */
 } OModel;
 
-typedef struct { FILE *f; int bad; } Rd;
+typedef struct { FILE *f; int bad; int layout; } Rd;
 static void rd(Rd *r, void *p, size_t n) {
     if (!r->bad && fread(p, 1, n, r->f) != n) r->bad = 1;
 }
 static int32_t rd_i32(Rd *r) { int32_t v = 0; rd(r, &v, 4); return v; }
 static float rd_f32(Rd *r) { float v = 0; rd(r, &v, 4); return v; }
 
+/* lz_f16_to_f32 (src/compat.c:283-312): binary16 widened exactly. */
+static float f16_to_f32(unsigned h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 0x1Fu, m = h & 0x3FFu, u;
+    union { uint32_t u; float f; } b;
+    if (e == 0) {
+        if (m == 0) u = sign;
+        else {
+            int sh = 0;
+            while (!(m & 0x400u)) { m <<= 1; sh++; }
+            u = sign | ((uint32_t)(127 - 14 - sh) << 23) | ((m & 0x3FFu) << 13);
+        }
+    } else if (e == 0x1Fu) {
+        u = sign | 0x7F800000u | (m << 13);
+    } else {
+        u = sign | ((e + 127u - 15u) << 23) | (m << 13);
+    }
+    b.u = u;
+    return b.f;
+}
+
+/* An F32 tensor of n elements, stored as f32 or as BF16 (dtype 6: the high
+ * half of each f32, widened by <<16 as lz_t_f32 does, src/ops_epi.c:1210). */
 static float *rd_f32v(Rd *r, int n) {
     uint8_t dt = 0xFF;
     uint32_t cnt = 0;
     float *p;
     rd(r, &dt, 1); rd(r, &cnt, 4);
-    if (dt != 0 || (int)cnt != n) { r->bad = 1; return NULL; }
+    if ((dt != 0 && dt != 6) || (int)cnt != n) { r->bad = 1; return NULL; }
     p = (float *)malloc(sizeof(float) * (size_t)n);
     if (!p) { r->bad = 1; return NULL; }
-    rd(r, p, sizeof(float) * (size_t)n);
+    if (dt == 0) {
+        rd(r, p, sizeof(float) * (size_t)n);
+    } else {
+        uint16_t *h = (uint16_t *)malloc(2 * (size_t)n);
+        if (!h) { r->bad = 1; free(p); return NULL; }
+        rd(r, h, 2 * (size_t)n);
+        for (int i = 0; i < n; i++) {
+            union { uint32_t u; float f; } b;
+            b.u = (uint32_t)h[i] << 16;
+            p[i] = b.f;
+        }
+        free(h);
+    }
     return p;
 }
+
+/* layout-2 decode (src/compat.c:340-345): base * (u / 255), each step
+ * rounded to float. */
+static float u8_decode(float base, float u) {
+    volatile float levels = 255.0f;
+    volatile float q = u / levels;
+    volatile float p = base * q;
+    return p;
+}
+
+/* A Q8_0 tensor: u32 gs (a multiple of 32 dividing the row), the codes,
+ * then the scale plane in the file's layout (read_scale_plane,
+ * src/model.c:3510-3554): 0 f32 per group; 1 binary16 per group; 2 a
+ * binary16 base per row, then a u8 per group decoded as base * (u / 255). */
 static void rd_q8(Rd *r, QMat *m, int rows, int cols) {
     uint8_t dt = 0xFF;
     uint32_t cnt = 0, gs = 0;
+    size_t ng;
     rd(r, &dt, 1); rd(r, &cnt, 4); rd(r, &gs, 4);
-    m->rows = rows; m->cols = cols;
-    if (dt != 1 || cnt != (uint32_t)rows * (uint32_t)cols || gs != (uint32_t)cols) {
-        r->bad = 1; m->q = NULL; m->s = NULL; return;
+    m->rows = rows; m->cols = cols; m->gs = (int)gs; m->q = NULL; m->s = NULL;
+    if (dt != 1 || cnt != (uint32_t)rows * (uint32_t)cols || gs == 0 || gs % 32 || (uint32_t)cols % gs) {
+        r->bad = 1; return;
     }
+    ng = (size_t)rows * (cols / gs);
     m->q = (int8_t *)malloc((size_t)rows * cols);
-    m->s = (float *)malloc(sizeof(float) * (size_t)rows);
+    m->s = (float *)malloc(sizeof(float) * ng);
     if (!m->q || !m->s) { r->bad = 1; return; }
     rd(r, m->q, (size_t)rows * cols);
-    rd(r, m->s, sizeof(float) * (size_t)rows);
+    if (r->layout == 0) {
+        rd(r, m->s, sizeof(float) * ng);
+    } else if (r->layout == 1) {
+        uint16_t *h = (uint16_t *)malloc(2 * ng);
+        if (!h) { r->bad = 1; return; }
+        rd(r, h, 2 * ng);
+        for (size_t i = 0; i < ng; i++) m->s[i] = f16_to_f32(h[i]);
+        free(h);
+    } else {
+        uint16_t *h = (uint16_t *)malloc(2 * (size_t)rows);
+        uint8_t *u = (uint8_t *)malloc(ng);
+        const size_t gpr = ng / (size_t)rows;
+        if (!h || !u) { r->bad = 1; free(h); free(u); return; }
+        rd(r, h, 2 * (size_t)rows);
+        rd(r, u, ng);
+        for (size_t i = 0; i < ng; i++) m->s[i] = u8_decode(f16_to_f32(h[i / gpr]), (float)u[i]);
+        free(h); free(u);
+    }
 }
 
 static void free_q(QMat *m) { free(m->q); free(m->s); }
@@ -575,9 +664,11 @@ ORA_API void *ora_open(const char *dir, char *err, int errlen) {
     snprintf(path, sizeof path, "%s/model.bin", dir);
     r.f = fopen(path, "rb");
     r.bad = 0;
+    r.layout = 0;
     if (!r.f) { snprintf(err, (size_t)errlen, "open %s", path); free(m); return NULL; }
     rd(&r, magic, 4);
-    if (memcmp(magic, "L98Z", 4) != 0 || rd_i32(&r) != 5) {
+    m->version = rd_i32(&r);
+    if (memcmp(magic, "L98Z", 4) != 0 || m->version < 4 || m->version > 9) {
         snprintf(err, (size_t)errlen, "bad magic/version");
         fclose(r.f); free(m); return NULL;
     }
@@ -597,15 +688,39 @@ ORA_API void *ora_open(const char *dir, char *err, int errlen) {
     m->moe_inter = rd_i32(&r); m->latent = rd_i32(&r);
     (void)rd_i32(&r); (void)rd_i32(&r); (void)rd_i32(&r); (void)rd_i32(&r);
     m->shared_w = rd_i32(&r);
-    (void)rd_i32(&r); m->mtp_inter = rd_i32(&r);
-    for (int i = 0; i < 5; i++) (void)rd_i32(&r);             /* rope scaling */
-    m->use_subn = rd_i32(&r);
-    m->hadamard_o = rd_i32(&r);
-    m->hadamard_down = rd_i32(&r);
-    {   /* rest of the v5 tail: 7 flags, 3x128, 6, 128 */
-        int skip = 7 + 3 * 128 + 6 + 128;
-        for (int i = 0; i < skip; i++) (void)rd_i32(&r);
+    /* lz_open_bin's version ladder (src/model.c:3925-3989, 4105-4460): v4
+     * stops after the 13-word tail (no MTP head, hadamard blocks derived);
+     * v5 carries the rest of the tail and the 522 appended words; v6 the
+     * application table, mtp_n_draft, the rotated-vocabulary words and
+     * the scale layout; v7 / v8 / v9 one word each.  The path restated
+     * here has the identity schedule, at most one draft slot, no rotated
+     * vocabulary and none of the v7-v9 mechanisms. */
+    m->has_mtp = 0;
+    m->hadamard_o = m->hadamard_down = -1;
+    if (m->version >= 5) {
+        m->has_mtp = rd_i32(&r); m->mtp_inter = rd_i32(&r);
+        for (int i = 0; i < 5; i++) (void)rd_i32(&r);             /* rope scaling */
+        m->use_subn = rd_i32(&r);
+        m->hadamard_o = rd_i32(&r);
+        m->hadamard_down = rd_i32(&r);
+        for (int i = 0; i < 7 + 3 * 128 + 6 + 128; i++) (void)rd_i32(&r);   /* mla .. csa2 */
     }
+    if (m->version >= 6) {
+        int exec_len = rd_i32(&r), bad = exec_len != m->n_layers;
+        for (int i = 0; i < 128; i++) bad |= rd_i32(&r) != (i < m->n_layers ? i : 0);   /* app_layer */
+        for (int i = 0; i < 128; i++) bad |= rd_i32(&r) != 0;                          /* app_loop */
+        bad |= rd_i32(&r) > 1;                                                          /* mtp_n_draft */
+        bad |= rd_i32(&r) != 0;                                                         /* embed_hadamard */
+        (void)rd_i32(&r);                                                               /* embed_signs_seed */
+        r.layout = rd_i32(&r);
+        bad |= r.layout < 0 || r.layout > 2;
+        if (m->version >= 7) bad |= rd_i32(&r) != 0;                                    /* loop_input_mix */
+        if (m->version >= 8) bad |= rd_i32(&r) != 0;                                    /* ced_local */
+        if (m->version >= 9) (void)rd_i32(&r);                                          /* loop_input_mix_from */
+        if (bad) r.bad = 1;
+    }
+    m->scale_layout = r.layout;
+    if (m->has_mtp != 0 && m->has_mtp != 1) r.bad = 1;
     /* resolve_hadamard (src/model.c:139-182): -1 derives (hadamard_o: the
      * whole lin_value_dim on a dense model when it is a power of two, else
      * 0; hadamard_down: the largest power of two <= 512 dividing
@@ -698,6 +813,7 @@ ORA_API void *ora_open(const char *dir, char *err, int errlen) {
         }
     }
     m->mtp.type = 1;
+    if (m->has_mtp) {
     m->mtp.in_norm = rd_f32v(&r, d);
     m->mtp.post_norm = rd_f32v(&r, d);
     if (m->use_subn) {
@@ -724,6 +840,7 @@ ORA_API void *ora_open(const char *dir, char *err, int errlen) {
     m->mtp_norm = rd_f32v(&r, d);
     m->mtp_pre_h = rd_f32v(&r, d);
     m->mtp_pre_e = rd_f32v(&r, d);
+    }
     {
         char extra;
         if (!r.bad && fread(&extra, 1, 1, r.f) == 1) r.bad = 1;   /* trailing bytes */
@@ -740,12 +857,13 @@ ORA_API void *ora_open(const char *dir, char *err, int errlen) {
 
 ORA_API int ora_config(void *h, int *out, int n) {
     OModel *m = (OModel *)h;
-    int v[24] = {m->vocab, m->d, m->n_layers, m->seq_len, m->nh, m->nkv, m->hd,
+    int v[29] = {m->vocab, m->d, m->n_layers, m->seq_len, m->nh, m->nkv, m->hd,
                  m->nk, m->nv, m->kd, m->vd, m->K, m->n_lin, m->n_full,
                  m->gate_rank, m->n_experts, m->topk, m->latent, m->moe_inter,
-                 m->shared_w, m->mtp_inter, m->q_dim, m->kv_dim, m->conv_dim};
-    for (int i = 0; i < n && i < 24; i++) out[i] = v[i];
-    return 24;
+                 m->shared_w, m->mtp_inter, m->q_dim, m->kv_dim, m->conv_dim,
+                 m->version, m->scale_layout, m->has_mtp, m->embed.gs, m->use_subn};
+    for (int i = 0; i < n && i < 29; i++) out[i] = v[i];
+    return 29;
 }
 
 ORA_API const float *ora_rope_table(void *h) { return ((OModel *)h)->rope_cs; }
@@ -887,7 +1005,7 @@ static void quant_rows(OState *s, const float *x, int n, int nt) {
         o_quantize_q8(x + (size_t)t * n, n, s->xq + (size_t)t * n, s->xqs + (size_t)t * (n / 32));
 }
 static void mm(OState *s, float *o, const QMat *w, int nt) {
-    o_matmul_q8(o, s->xq, s->xqs, w->q, w->s, w->cols, w->rows, nt, NULL);
+    o_matmul_q8g(o, s->xq, s->xqs, w->q, w->s, w->cols, w->rows, nt, w->gs, NULL);
 }
 
 /* One SubLN projection (subn_norm_q8, src/forward_kda.c:203-236, and its
@@ -1010,8 +1128,8 @@ static void forward_kda(OState *s, const OLayer *L, int li, int nt, int advance,
     /* f_b per token on its own quantization of the f_a row (:760-815) */
     for (int t = 0; t < nt; t++) {
         o_quantize_q8(fa + (size_t)t * m->gate_rank, m->gate_rank, s->xq, s->xqs);
-        o_matmul_q8(gate + (size_t)t * nvk, s->xq, s->xqs, L->fb.q, L->fb.s,
-                    m->gate_rank, nvk, 1, NULL);
+        o_matmul_q8g(gate + (size_t)t * nvk, s->xq, s->xqs, L->fb.q, L->fb.s,
+                     m->gate_rank, nvk, 1, L->fb.gs, NULL);
     }
     /* decay gate (:277-300, :840-850) */
     for (int h = 0; h < nv; h++) decay[h] = o_exp(L->a_log[h]);
@@ -1215,11 +1333,11 @@ static void forward_moe(OState *s, const OLayer *L, int nt, int layer) {
         for (int kk = 0; kk < m->topk; kk++) {
             int e = idx[kk];
             if (e < 0) continue;
-            o_matmul_q8(h1, lq, lqs, L->w1[e].q, L->w1[e].s, lat, inter, 1, NULL);
-            o_matmul_q8(h3, lq, lqs, L->w3[e].q, L->w3[e].s, lat, inter, 1, NULL);
+            o_matmul_q8g(h1, lq, lqs, L->w1[e].q, L->w1[e].s, lat, inter, 1, L->w1[e].gs, NULL);
+            o_matmul_q8g(h3, lq, lqs, L->w3[e].q, L->w3[e].s, lat, inter, 1, L->w3[e].gs, NULL);
             for (int i = 0; i < inter; i++) h1[i] = o_silu(h1[i]) * h3[i];
             o_quantize_q8(h1, inter, hq, hqs);
-            o_matmul_q8(h2, hq, hqs, L->w2[e].q, L->w2[e].s, inter, lat, 1, NULL);
+            o_matmul_q8g(h2, hq, hqs, L->w2[e].q, L->w2[e].s, inter, lat, 1, L->w2[e].gs, NULL);
             for (int v = 0; v < lat; v++) ly[v] += w[kk] * h2[v];
         }
     }
@@ -1291,10 +1409,11 @@ static void dense_ffn(OState *s, const OLayer *F, const QMat *gp, const QMat *up
     mm(s, s->xb2, dp, nt);
 }
 
-static void embed_row(const OModel *m, int tok, float *out) {   /* lz_t_row_f32 Q8 */
+/* lz_t_row_f32 of a Q8_0 row (src/ops_epi.c:1276-1280): q * its group's scale. */
+static void embed_row(const OModel *m, int tok, float *out) {
     const int8_t *q = m->embed.q + (size_t)tok * m->d;
-    float sc = m->embed.s[tok];
-    for (int i = 0; i < m->d; i++) out[i] = (float)q[i] * sc;
+    const float *sc = m->embed.s + (size_t)tok * (m->d / m->embed.gs);
+    for (int i = 0; i < m->d; i++) out[i] = (float)q[i] * sc[i / m->embed.gs];
 }
 
 /* forward_chunk, src/forward.c:1210-1617, for one chunk of nt <= 8 tokens.
@@ -1388,7 +1507,7 @@ ORA_API int ora_forward_verify(void *hs, const int *tokens, int n, int pos0) {
     OState *s = (OState *)hs;
     int done = 0;
     const OModel *m = s->m;
-    if (n < 1) return 1;
+    if (n < 1 || !m->has_mtp) return 1;                 /* the verify needs the MTP head (:1780) */
     while (done < n) {
         int k = n - done;
         if (k > s->nt_cap) k = s->nt_cap;
@@ -1407,13 +1526,13 @@ ORA_API float *ora_mtp_draft_step(void *hs, int tok, int pos) {
     const int d = m->d;
     float *emb = s->t5, *concat = s->x, *mx = s->xb2 + 0;
     float mtp_x[4096];
-    if (tok < 0 || tok >= m->vocab || pos < 0 || pos >= s->seq_len) return NULL;
+    if (!m->has_mtp || tok < 0 || tok >= m->vocab || pos < 0 || pos >= s->seq_len) return NULL;
     (void)mx;
     embed_row(m, tok, emb);
     o_rmsnorm(concat, emb, m->mtp_pre_e, d, m->eps);
     o_rmsnorm(concat + d, s->mtp_chain, m->mtp_pre_h, d, m->eps);
     o_quantize_q8(concat, 2 * d, s->xq, s->xqs);
-    o_matmul_q8(mtp_x, s->xq, s->xqs, m->mtp_fc.q, m->mtp_fc.s, 2 * d, d, 1, NULL);
+    o_matmul_q8g(mtp_x, s->xq, s->xqs, m->mtp_fc.q, m->mtp_fc.s, 2 * d, d, 1, m->mtp_fc.gs, NULL);
     if (m->use_subn) memcpy(s->xb, mtp_x, sizeof(float) * (size_t)d);   /* (:82-88) */
     else o_rmsnorm(s->xb, mtp_x, m->mtp.in_norm, d, m->eps);
     forward_attn(s, &m->mtp, m->n_full, pos, 1, 0, -1);
@@ -1424,7 +1543,7 @@ ORA_API float *ora_mtp_draft_step(void *hs, int tok, int pos) {
     for (int i = 0; i < d; i++) mtp_x[i] += s->xb2[i];
     o_rmsnorm(s->mtp_chain, mtp_x, m->mtp_norm, d, m->eps);
     o_quantize_q8(s->mtp_chain, d, s->xq, s->xqs);
-    o_matmul_q8(s->mtp_draft, s->xq, s->xqs, m->embed.q, m->embed.s, d, m->vocab, 1, NULL);
+    o_matmul_q8g(s->mtp_draft, s->xq, s->xqs, m->embed.q, m->embed.s, d, m->vocab, 1, m->embed.gs, NULL);
     return s->mtp_draft;
 }
 
@@ -1439,7 +1558,7 @@ ORA_API int ora_mtp_prefill(void *hs, const float *h_all, const int *next, int n
     float *concat = (float *)malloc(sizeof(float) * 2 * (size_t)d);
     float *mx = (float *)malloc(sizeof(float) * (size_t)MAXB * d);
     float emb[4096];
-    if (!h_all || !next || n < 1) { free(concat); free(mx); return 1; }
+    if (!m->has_mtp || !h_all || !next || n < 1) { free(concat); free(mx); return 1; }
     while (done < n) {
         int k = n - done;
         if (k > s->nt_cap) k = s->nt_cap;
@@ -1449,7 +1568,7 @@ ORA_API int ora_mtp_prefill(void *hs, const float *h_all, const int *next, int n
             o_rmsnorm(concat, emb, m->mtp_pre_e, d, m->eps);
             o_rmsnorm(concat + d, h_all + (size_t)(done + t) * d, m->mtp_pre_h, d, m->eps);
             o_quantize_q8(concat, 2 * d, s->xq, s->xqs);
-            o_matmul_q8(mx + (size_t)t * d, s->xq, s->xqs, m->mtp_fc.q, m->mtp_fc.s, 2 * d, d, 1, NULL);
+            o_matmul_q8g(mx + (size_t)t * d, s->xq, s->xqs, m->mtp_fc.q, m->mtp_fc.s, 2 * d, d, 1, m->mtp_fc.gs, NULL);
         }
         if (m->use_subn)                                 /* (:600-611) */
             memcpy(s->xb, mx, sizeof(float) * (size_t)k * d);
@@ -1796,7 +1915,7 @@ ORA_API int ora_session_start(void *hs, const int *prompt, int n_prompt) {
     if (n_prompt < 2) return 1;
     h = (float *)malloc(sizeof(float) * (size_t)(n_prompt - 1) * s->m->d);
     rc = ora_forward_batch_capture(s, prompt, n_prompt - 1, 0, h);
-    if (!rc) rc = ora_mtp_prefill(s, h, prompt + 1, n_prompt - 1, s->mtp_pos);
+    if (!rc && s->m->has_mtp) rc = ora_mtp_prefill(s, h, prompt + 1, n_prompt - 1, s->mtp_pos);
     s->mtp_pos = n_prompt - 1;
     free(h);
     return rc;

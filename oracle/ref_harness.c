@@ -17,6 +17,8 @@
  *             --verify-iters N  after the run, time N lz_forward_verify
  *                               calls of M = K+1 tokens at the final
  *                               position (ring slot restored between calls)
+ *   l98ref_* capture MODEL_DIR PROMPT_FILE OUT_PREFIX
+ *       a prefill and one capture, logits and hidden rows dumped
  *   l98ref_* verify MODEL_DIR PROMPT_FILE K ITERS OUT_PREFIX
  *       times lz_forward_verify of M=K+1 tokens in isolation (the ring slot
  *       is restored between calls, so every call reads the same state)
@@ -365,7 +367,48 @@ static int cmd_verify(int argc, char **argv) {
     return 0;
 }
 
+/* l98ref_* capture MODEL_DIR PROMPT_FILE OUT_PREFIX
+ *   lz_forward_batch_capture of prompt[0..n-2] at 0, then
+ *   lz_forward_capture(prompt[n-1], n-1): dumps its logits ("capture") and
+ *   the final-normed hidden rows of the prefill ("hidden") and of the last
+ *   token ("chain").  Needs no MTP head (a version-4 model has none). */
+static int cmd_capture(int argc, char **argv) {
+    const char *dir = argv[2], *pf = argv[3], *prefix = argv[4];
+    int n_prompt;
+    char err[512];
+    LZModel m;
+    LZRunState s;
+    int *prompt;
+    float *h_all, *lg;
+    (void)argc;
+    select_mode();
+    prompt = read_prompt(pf, &n_prompt);
+    if (!prompt || n_prompt < 2 || lz_open(&m, dir, err, sizeof err) != 0) {
+        fprintf(stderr, "open: %s\n", err);
+        return 2;
+    }
+    if (lz_state_alloc(&s, &m, m.config.seq_len, LZ_SPEC_K_MAX, err, sizeof err) != 0) {
+        fprintf(stderr, "lz_state_alloc: %s\n", err);
+        return 2;
+    }
+    h_all = (float *)malloc(sizeof(float) * (size_t)(n_prompt - 1) * m.config.hidden_size);
+    if (!h_all) return 2;
+    if (!lz_forward_batch_capture(&m, &s, prompt, n_prompt - 1, 0, h_all)) return 3;
+    lg = lz_forward_capture(&m, &s, prompt[n_prompt - 1], n_prompt - 1);
+    if (!lg) return 3;
+    dump(prefix, "capture", lg, sizeof(float) * (size_t)m.config.vocab_size);
+    dump(prefix, "hidden", h_all, sizeof(float) * (size_t)(n_prompt - 1) * m.config.hidden_size);
+    if (s.mtp_chain)   /* no MTP head, no chain (src/forward.c:1623-1629) */
+        dump(prefix, "chain", s.mtp_chain, sizeof(float) * (size_t)m.config.hidden_size);
+    free(h_all);
+    free(prompt);
+    lz_state_free(&s);
+    lz_free(&m);
+    return 0;
+}
+
 int main(int argc, char **argv) {
+    if (argc >= 5 && !strcmp(argv[1], "capture")) return cmd_capture(argc, argv);
     if (argc >= 10 && !strcmp(argv[1], "gen")) return cmd_gen(argc, argv);
     if (argc >= 7 && !strcmp(argv[1], "verify")) return cmd_verify(argc, argv);
     fprintf(stderr, "usage: see oracle/ref_harness.c\n");

@@ -63,6 +63,20 @@ CASES = [
     ("gen_subln_k1_greedy", "subln", 5, 8192, 64, 1, 48, 0.0, 1.0, 1),
     ("gen_subln_k2_temp", "subln", 5, 8192, 64, 2, 48, 0.8, 0.95, 7),
     ("gen_micro_subln_k3_greedy", "micro_subln", 12, 512, 24, 3, 48, 0.0, 1.0, 1, {"dump": 6}),
+    # model.bin versions 6-9 with grouped Q8_0 scales, binary16 and u8 scale
+    # planes and BF16 small tensors.
+    ("gen_fmt13_v9_k3_greedy", "fmt13", 13, 512, 24, 3, 40, 0.0, 1.0, 1, {"dump": 4}),
+    ("gen_fmt14_v6_k3_greedy", "fmt14", 14, 8192, 48, 3, 40, 0.0, 1.0, 1, {"dump": 4}),
+    ("gen_fmt14_v6_k2_temp", "fmt14", 14, 8192, 48, 2, 32, 0.8, 0.95, 7),
+    ("gen_fmt16_v7_k2_greedy", "fmt16", 16, 512, 24, 2, 40, 0.0, 1.0, 1, {"dump": 4}),
+    ("gen_fmt17_v8_k3_greedy", "fmt17", 17, 512, 24, 3, 40, 0.0, 1.0, 1, {"dump": 4}),
+]
+# Prefill + one capture (the harness's capture command; needs no MTP head):
+# (fixture, model dir name, generator config id, vocab, n_prompt)
+CAPTURES = [
+    ("cap_fmt15_v4", "fmt15", 15, 8192, 40),       # version 4: no MTP head, groups of 64
+    ("cap_fmt14_v6", "fmt14", 14, 8192, 40),
+    ("cap_fmt13_v9", "fmt13", 13, 512, 40),
 ]
 MODEL_SEED = 1234
 PROMPT_SEED = 0
@@ -127,5 +141,33 @@ def main():
         print(name, len(out["tokens"]), "tokens", flush=True)
 
 
+def main_captures():
+    import subprocess
+    import __graft_entry__
+    import numpy as np
+    pkg = __graft_entry__.load_package()
+    root = os.environ.get("L98_MODEL_DIR") or os.path.join(tempfile.gettempdir(), "l98_models")
+    only = set(sys.argv[1:])
+    for name, mdir, cid, V, n_prompt in CAPTURES:
+        if only and name not in only:
+            continue
+        model = pkg.ensure_model(os.path.join(root, mdir), cid, seed=MODEL_SEED)
+        digest = hashlib.sha256(open(os.path.join(model, "model.bin"), "rb").read()).hexdigest()
+        prompt = pkg.prompt_tokens(PROMPT_SEED, n_prompt, V)
+        tmp = tempfile.mkdtemp(prefix="l98cap_")
+        pf = os.path.join(tmp, "prompt.bin")
+        np.ascontiguousarray(prompt, np.int32).tofile(pf)
+        subprocess.run([OL.REF_ORACLE_BIN, "capture", model, pf, os.path.join(tmp, "c")], check=True)
+        sums = {t: hashlib.sha256(open(os.path.join(tmp, "c.%s.bin" % t), "rb").read()).hexdigest()
+                for t in ("capture", "hidden")}
+        out = {"model": mdir, "config_id": cid, "model_seed": MODEL_SEED, "model_sha256": digest, "vocab": V,
+               "prompt_seed": PROMPT_SEED, "n_prompt": n_prompt, "sha256": sums,
+               "source": "oracle/_ref/l98ref_oracle capture (reference engine, float-oracle mode)"}
+        with open(os.path.join(HERE, name + ".json"), "w") as f:
+            json.dump(out, f, indent=1)
+        print(name, flush=True)
+
+
 if __name__ == "__main__":
     main()
+    main_captures()

@@ -533,7 +533,8 @@ def test_rope_table_bitwise_vs_reference(pkg, tiny, tmp_path):
 # ------------------------------------------------------- golden fixtures ---
 
 def golden_files():
-    return sorted(f for f in os.listdir(GOLDEN) if f.endswith(".json")) if os.path.isdir(GOLDEN) else []
+    return sorted(f for f in os.listdir(GOLDEN) if f.startswith("gen_") and f.endswith(".json")) \
+        if os.path.isdir(GOLDEN) else []
 
 
 def test_golden_fixtures_present():
@@ -639,8 +640,9 @@ def _greedy_rounds_oracle(model, prompt, k, n_rounds):
 
 
 @pytest.mark.parametrize("name,vocab,k", [("micro", 512, 3), ("echo", 64, 3), ("tiny", 8192, 2),
-                                          ("micro_subln", 512, 3), ("subln", 8192, 3), ("subln", 8192, 1)])
-def test_rounds_bitwise_vs_reference(pkg, request, tmp_path, name, vocab, k):
+                                          ("micro_subln", 512, 3), ("subln", 8192, 3), ("subln", 8192, 1),
+                                          ("fmt13", 512, 3), ("fmt14", 8192, 2)])
+def test_rounds_bitwise_vs_reference(pkg, request, model_root, tmp_path, name, vocab, k):
     """The capture, every round's verify logits and hidden rows and the last
     draft step's logits equal the reference engine's bit for bit, round
     after round (not only the emitted tokens).  micro and echo have 32-wide
@@ -652,7 +654,10 @@ def test_rounds_bitwise_vs_reference(pkg, request, tmp_path, name, vocab, k):
     per-token scales on the MTP FFN gate/up inputs."""
     if not OL.have_reference():
         pytest.skip("reference build absent; the SubLN golden fixtures cover this")
-    model = request.getfixturevalue(name)
+    if name.startswith("fmt"):
+        model = pkg.ensure_model(os.path.join(model_root, name), int(name[3:]), seed=1234)
+    else:
+        model = request.getfixturevalue(name)
     prompt = pkg.prompt_tokens(21, 40, vocab)
     n_rounds = 4
     r = OL.reference_generate(model, prompt, k, 12, tmpdir=str(tmp_path), extra=("--dump-rounds", str(n_rounds)))
@@ -701,3 +706,53 @@ def test_quantize_q8_tok_bitwise_vs_reference_and_closed_form():
     s = np.zeros(2, np.float32)
     L.o_quantize_q8_tok(fp(z), 64, q.ctypes.data, fp(s))
     assert not q.any() and np.all(s == 1.0)
+
+
+# ------------------------------------------------- model.bin versions 4-9 ---
+
+CAPTURE_FIXTURES = sorted(f for f in os.listdir(GOLDEN) if f.startswith("cap_") and f.endswith(".json"))
+
+
+@pytest.mark.parametrize("fname", CAPTURE_FIXTURES)
+def test_oracle_capture_matches_golden(pkg, model_root, fname):
+    """Versions 4 (no MTP head), 6 and 9 of model.bin: grouped Q8_0 scales
+    (groups of 32, 64, 128), binary16 and row-base + u8 scale planes, BF16
+    small tensors.  The prefill's hidden rows and the capture logits hash to
+    the reference engine's."""
+    g = json.load(open(os.path.join(GOLDEN, fname)))
+    model = pkg.ensure_model(os.path.join(model_root, g["model"]), g["config_id"], seed=g["model_seed"])
+    assert hashlib.sha256(open(os.path.join(model, "model.bin"), "rb").read()).hexdigest() == g["model_sha256"]
+    prompt = pkg.prompt_tokens(g["prompt_seed"], g["n_prompt"], g["vocab"])
+    o = Oracle(model)
+    try:
+        h = o.batch_capture(prompt[:-1], 0)
+        lg = o.forward_capture(prompt[-1], len(prompt) - 1)
+    finally:
+        o.close()
+    assert hashlib.sha256(h.tobytes()).hexdigest() == g["sha256"]["hidden"]
+    assert hashlib.sha256(lg.tobytes()).hexdigest() == g["sha256"]["capture"]
+
+
+def test_model_bin_format_options_vs_reference(pkg, model_root, tmp_path):
+    """Every synthetic format variant loads in the reference engine and the
+    oracle and gives the same capture bits; a version-4 model has no MTP
+    head, so the verify refuses there."""
+    if not OL.have_reference():
+        pytest.skip("reference build absent; the cap_ / gen_fmt fixtures cover this")
+    import subprocess
+    for cid, V in ((13, 512), (14, 8192), (15, 8192), (16, 512), (17, 512)):
+        model = pkg.ensure_model(os.path.join(model_root, f"fmt{cid}"), cid, seed=1234)
+        prompt = pkg.prompt_tokens(9, 33, V)
+        pf = str(tmp_path / "p.bin")
+        np.ascontiguousarray(prompt, np.int32).tofile(pf)
+        subprocess.run([OL.REF_ORACLE_BIN, "capture", model, pf, str(tmp_path / f"c{cid}")], check=True)
+        want = np.fromfile(str(tmp_path / f"c{cid}.capture.bin"), np.float32)
+        o = Oracle(model)
+        try:
+            o.batch_capture(prompt[:-1], 0)
+            got = o.forward_capture(prompt[-1], len(prompt) - 1)
+            if cid == 15:
+                assert o.verify([1, 2], len(prompt)) is None
+        finally:
+            o.close()
+        assert np.array_equal(bits(got), bits(want)), cid
