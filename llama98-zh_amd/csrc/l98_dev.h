@@ -17,7 +17,8 @@ enum {
     PRO_QUANT = 1,     // quantize float rows src
     PRO_NORM = 2,      // x = src (+ a (+ b)); RMSNorm(1+w); quantize
     PRO_SILU = 3,      // silu(src) * src2; quantize
-    PRO_COMBINE = 4    // sum over slots of sel_w * src[pair]; quantize
+    PRO_COMBINE = 4,   // sum over slots of sel_w * src[pair]; quantize
+    PRO_FOLD = 5       // x = src (+ a (+ b)); quantize (PRO_NORM without the norm)
 };
 
 // Prologue of one GEMV job.  Rows are addressed by the tile's activation

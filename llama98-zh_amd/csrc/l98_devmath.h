@@ -503,18 +503,17 @@ __device__ __forceinline__ float epi_one_group(int acc, float xs, float ws) {
 // (x*inv)*(1+w)), then the optional store of o and its per-32 quantization.
 // The sum is wave_sum_nonneg's (sq: ps_row_floats<4 * PJ>() floats, rec its
 // table).  n % 32 == 0.
-// norm == false skips the norm (o = v: the row is only stored and/or
-// quantized); tok selects one scale for the whole row (lz_quantize_q8_tok,
+// NORM == false skips the norm (o = v: the row is only stored and/or
+// quantized); TOK selects one scale for the whole row (lz_quantize_q8_tok,
 // src/ops_quant.c:2284-2314: the row's amax, the same element loop, the
 // scale in every 32-slot) instead of one per 32 elements.
-template <int PJ>
+template <int PJ, bool NORM = true, bool TOK = false>
 __device__ __forceinline__ void norm_row(const float4 (&v)[PJ], const float4 (&wn)[PJ], int n, float eps,
                                          float *sq, PsRec *rec, float *s_inv, float *__restrict__ out,
-                                         int8_t *__restrict__ xq, float *__restrict__ xqs, bool norm = true,
-                                         bool tok = false) {
+                                         int8_t *__restrict__ xq, float *__restrict__ xqs) {
     const int lane = threadIdx.x, nf = n >> 2;
     float inv = 1.0f;
-    if (norm) {
+    if constexpr (NORM) {
 #pragma unroll
         for (int j = 0; j < PJ; j++) {
             const int f = lane + 64 * j;
@@ -527,27 +526,48 @@ __device__ __forceinline__ void norm_row(const float4 (&v)[PJ], const float4 (&w
         __syncthreads();
         inv = *s_inv;
     }
-    float4 o[PJ];
-    uint32_t am = 0;
+    if constexpr (!TOK) {
 #pragma unroll
-    for (int j = 0; j < PJ; j++) {
-        const int f = lane + 64 * j;
-        o[j] = norm ? make_float4(v[j].x * inv * (1.0f + wn[j].x), v[j].y * inv * (1.0f + wn[j].y),
-                                  v[j].z * inv * (1.0f + wn[j].z), v[j].w * inv * (1.0f + wn[j].w))
-                    : v[j];
-        if (out && f < nf) reinterpret_cast<float4 *>(out)[f] = o[j];
-        if (f < nf) am = umax(am, abs_bits4(o[j]));
-    }
-    if (!xq) return;
-    const float row_amax = tok ? wave_max_u(am, 64) : 0.0f;
+        for (int j = 0; j < PJ; j++) {
+            const int f = lane + 64 * j;
+            float4 o = v[j];
+            if constexpr (NORM)
+                o = make_float4(v[j].x * inv * (1.0f + wn[j].x), v[j].y * inv * (1.0f + wn[j].y),
+                                v[j].z * inv * (1.0f + wn[j].z), v[j].w * inv * (1.0f + wn[j].w));
+            if (out && f < nf) reinterpret_cast<float4 *>(out)[f] = o;
+            if (xq) {
+                float sg;
+                const uint32_t q = quant_octet(o, &sg);
+                if (f < nf) {
+                    reinterpret_cast<uint32_t *>(xq)[f] = q;
+                    if (!(f & 7)) xqs[f >> 3] = sg;
+                }
+            }
+        }
+    } else {
+        float4 o[PJ];
+        uint32_t am = 0;
 #pragma unroll
-    for (int j = 0; j < PJ; j++) {
-        const int f = lane + 64 * j;
-        float sg;
-        const uint32_t q = tok ? quant4_amax(o[j], row_amax, &sg) : quant_octet(o[j], &sg);
-        if (f < nf) {
-            reinterpret_cast<uint32_t *>(xq)[f] = q;
-            if (!(f & 7)) xqs[f >> 3] = sg;
+        for (int j = 0; j < PJ; j++) {
+            const int f = lane + 64 * j;
+            o[j] = v[j];
+            if constexpr (NORM)
+                o[j] = make_float4(v[j].x * inv * (1.0f + wn[j].x), v[j].y * inv * (1.0f + wn[j].y),
+                                   v[j].z * inv * (1.0f + wn[j].z), v[j].w * inv * (1.0f + wn[j].w));
+            if (out && f < nf) reinterpret_cast<float4 *>(out)[f] = o[j];
+            if (f < nf) am = umax(am, abs_bits4(o[j]));
+        }
+        if (!xq) return;
+        const float row_amax = wave_max_u(am, 64);
+#pragma unroll
+        for (int j = 0; j < PJ; j++) {
+            const int f = lane + 64 * j;
+            float sg;
+            const uint32_t q = quant4_amax(o[j], row_amax, &sg);
+            if (f < nf) {
+                reinterpret_cast<uint32_t *>(xq)[f] = q;
+                if (!(f & 7)) xqs[f >> 3] = sg;
+            }
         }
     }
 }

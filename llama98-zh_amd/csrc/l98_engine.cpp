@@ -887,6 +887,7 @@ Prologue PC(const float *h2, const int *sel_idx, const float *sel_w, int topk) {
 Prologue PW(const Prologue &in, const float *w) {
     Prologue p = in;
     p.w = w;
+    if (!w) p.mode = PRO_FOLD;
     return p;
 }
 

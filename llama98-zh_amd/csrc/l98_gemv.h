@@ -99,6 +99,10 @@ __device__ __forceinline__ void quant_rows(const float4 (&v)[RW][PJN], int wave,
 #define MODES_S MB(PRO_SILU)
 #define MODES_Q MB(PRO_QUANT)
 #define MODES_CS (MB(PRO_COMBINE) | MB(PRO_SILU))
+#define MODES_NF (MB(PRO_NORM) | MB(PRO_FOLD))
+// Instance flag: the jobs' weights have grouped scales (more than one per
+// row); instances without it keep one scale per row in a register.
+#define MG (1 << 7)
 // The activation loads of a prologue go out before the tile's weight loads:
 // the empty asm with a memory clobber keeps every earlier load above it
 // (no pass may sink one into a later conditional use, behind the weights,
@@ -232,9 +236,11 @@ __device__ __forceinline__ void build_rows(const Prologue &P, const int8_t *__re
                 v[r][j] = y;
             }
         quant_rows<RW, PJN>(v, wave, lane, nm, nf, nb, in_dim, sx, sxs);
-    } else if (MODES & MB(PRO_NORM)) {   // PRO_NORM
-        // P.w == nullptr: the folded rows are quantized without a norm
-        const bool has_a = P.a != nullptr, has_b = P.b != nullptr, do_norm = P.w != nullptr;
+    } else if (MODES & (MB(PRO_NORM) | MB(PRO_FOLD))) {   // PRO_NORM, PRO_FOLD
+        // PRO_FOLD: the folded rows are quantized without a norm (only in
+        // instances compiled for it; elsewhere do_norm is a constant)
+        const bool do_norm = !(MODES & MB(PRO_FOLD)) || P.mode == PRO_NORM;
+        const bool has_a = P.a != nullptr, has_b = P.b != nullptr;
         const float *pa = has_a ? P.a : P.src;
         const float *pb = has_b ? P.b : pa;
         const int sa = has_a ? in_dim : P.src_stride, sb = has_b ? in_dim : sa;
@@ -441,8 +447,10 @@ __device__ __forceinline__ void gemv_tile(const int8_t *__restrict__ wt, const f
                                           int nm, bool writer, float *__restrict__ out, size_t out_stride,
                                           int row0, int32_t *__restrict__ acc_out, int acc_rows, char *smem,
                                           float *s_inv, float *tab, int gs = 0) {
-    // scales per row (ws holds [rows][nws]); one per row is the common case
-    const int nws = (gs > 0 && gs < in_dim) ? in_dim / gs : 1;
+    // scales per row (ws holds [rows][nws]): one unless the instance is
+    // compiled for grouped scales
+    constexpr bool GROUPED = (MODES & MG) != 0;
+    const int nws = (GROUPED && gs > 0 && gs < in_dim) ? in_dim / gs : 1;
     const int tid = threadIdx.x;
     const int cpr = in_dim >> 4, nb = in_dim >> 5, pstride = nb + 4;
     const int nchunk = rows_here * cpr;
@@ -463,9 +471,10 @@ __device__ __forceinline__ void gemv_tile(const int8_t *__restrict__ wt, const f
     __syncthreads();
     if (er < rows_here && et < nm) {
         const int *pp = part + (er * M + et) * pstride;
-        out[(size_t)s_orow[et] * out_stride + row0 + er] =
-            nws == 1 ? tile_epilogue(pp, sxs + et * nb, nb, wsv)
-                     : tile_epilogue_g(pp, sxs + et * nb, nb, gs >> 5, ws + (size_t)(row0 + er) * nws);
+        float o;
+        if (GROUPED && nws > 1) o = tile_epilogue_g(pp, sxs + et * nb, nb, gs >> 5, ws + (size_t)(row0 + er) * nws);
+        else o = tile_epilogue(pp, sxs + et * nb, nb, wsv);
+        out[(size_t)s_orow[et] * out_stride + row0 + er] = o;
         if (acc_out)
             for (int g = 0; g < nb; g++) acc_out[((size_t)et * acc_rows + row0 + er) * nb + g] = pp[g];
     }
@@ -510,7 +519,8 @@ static bool prologue_ok(const Prologue &P, int in_dim, const int8_t *xq, const f
     if (in_dim > PRO_MAX_IN || !P.src) return false;
     if (P.mode == PRO_QUANT) return P.src_stride >= in_dim && !(P.src_stride & 3);
     if (P.mode == PRO_SILU) return P.src2 && P.src_stride >= in_dim && !(P.src_stride & 3);
-    if (P.mode == PRO_NORM) return P.src_stride >= in_dim && !(P.src_stride & 3) && !(P.o_stride & 3);
+    if (P.mode == PRO_NORM) return P.w && P.src_stride >= in_dim && !(P.src_stride & 3) && !(P.o_stride & 3);
+    if (P.mode == PRO_FOLD) return P.src_stride >= in_dim && !(P.src_stride & 3) && !(P.o_stride & 3);
     if (P.mode == PRO_COMBINE) return P.sel_idx && P.sel_w && P.topk >= 1 && P.topk <= MAX_TOPK;
     return false;
 }

@@ -37,18 +37,23 @@ extern "C" int l98k_upload_exp_table_gemv(const float *tab) {
 }
 
 // Instances: token slots M in {1, 2, 4, 8}; prologue sets: pre-quantized
-// (PJ 0), RMSNorm (PJ 1..8), SiLU-mul (PJ 1..4), combine + SiLU-mul
-// (PJ 1..4).
+// (PJ 0), RMSNorm (PJ 1..8), RMSNorm with fold-only jobs (PJ 1..8),
+// SiLU-mul (PJ 1..4), combine + SiLU-mul (PJ 1..4); each with one scale per
+// weight row or with grouped scales (MG).
 #define GEMV_CASE(M_, PJ_, MODES_)                                                                         \
-    case (M_) * 1000 + (PJ_) * 100 + (MODES_):                                                            \
+    case (M_) * 100000 + (PJ_) * 1000 + (MODES_):                                                            \
         ALLOW_BIG_LDS((k_gemv_q8<M_, PJ_, MODES_>));                                                      \
         hipLaunchKernelGGL((k_gemv_q8<M_, PJ_, MODES_>), dim3(tiles), dim3(GEMV_THREADS), lds, st, *b, m); \
         break;
-#define GEMV_CASES_M(M_)                                                                   \
-    GEMV_CASE(M_, 0, MODES_X)                                                              \
-    GEMV_CASE(M_, 1, MODES_N) GEMV_CASE(M_, 2, MODES_N) GEMV_CASE(M_, 4, MODES_N) GEMV_CASE(M_, 8, MODES_N) \
-    GEMV_CASE(M_, 1, MODES_S) GEMV_CASE(M_, 2, MODES_S) GEMV_CASE(M_, 4, MODES_S)          \
-    GEMV_CASE(M_, 1, MODES_CS) GEMV_CASE(M_, 2, MODES_CS) GEMV_CASE(M_, 4, MODES_CS)
+#define GEMV_CASES_MG(M_, G_)                                                                          \
+    GEMV_CASE(M_, 0, MODES_X | G_)                                                                     \
+    GEMV_CASE(M_, 1, MODES_N | G_) GEMV_CASE(M_, 2, MODES_N | G_) GEMV_CASE(M_, 4, MODES_N | G_)       \
+    GEMV_CASE(M_, 8, MODES_N | G_)                                                                     \
+    GEMV_CASE(M_, 1, MODES_NF | G_) GEMV_CASE(M_, 2, MODES_NF | G_) GEMV_CASE(M_, 4, MODES_NF | G_)    \
+    GEMV_CASE(M_, 8, MODES_NF | G_)                                                                    \
+    GEMV_CASE(M_, 1, MODES_S | G_) GEMV_CASE(M_, 2, MODES_S | G_) GEMV_CASE(M_, 4, MODES_S | G_)       \
+    GEMV_CASE(M_, 1, MODES_CS | G_) GEMV_CASE(M_, 2, MODES_CS | G_) GEMV_CASE(M_, 4, MODES_CS | G_)
+#define GEMV_CASES_M(M_) GEMV_CASES_MG(M_, 0) GEMV_CASES_MG(M_, MG)
 
 // Checks every job's prologue against the kernel's limits, lays the jobs'
 // tiles out in one grid and launches the instance for the jobs' prologue
@@ -56,7 +61,7 @@ extern "C" int l98k_upload_exp_table_gemv(const float *tab) {
 extern "C" int l98k_gemv(GemvBatch *b, int m, hipStream_t st) {
     if (m < 1 || m > MAX_CHUNK || b->n < 1 || b->n > MAX_GEMV_JOBS) return -1;
     const int M = m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8;
-    int tiles = 0, pj = 0, modes = 0;
+    int tiles = 0, pj = 0, modes = 0, grouped = 0;
     size_t lds = 0;
     for (int j = b->n; j < MAX_GEMV_JOBS; j++) b->tile0[j] = INT_MAX;
     for (int j = 0; j < b->n; j++) {
@@ -69,6 +74,7 @@ extern "C" int l98k_gemv(GemvBatch *b, int m, hipStream_t st) {
         b->tile0[j] = tiles;
         tiles += (J.rows + J.R - 1) / J.R;
         modes |= MB(J.pro.mode);
+        if (J.gs && J.gs < J.in_dim) grouped = MG;
         if (J.pro.mode != PRO_XQ) pj = pro_pj(J.in_dim) > pj ? pro_pj(J.in_dim) : pj;
     }
     for (int j = 0; j < b->n; j++) {
@@ -79,8 +85,10 @@ extern "C" int l98k_gemv(GemvBatch *b, int m, hipStream_t st) {
     if (lds > gemv_lds_limit()) return -1;
     if (modes == MODES_X) pj = 0;
     else if (modes == MB(PRO_COMBINE)) modes = MODES_CS;
-    else if (modes != MODES_N && modes != MODES_S && modes != MODES_CS) return -1;
-    switch (M * 1000 + pj * 100 + modes) {
+    else if (modes == MB(PRO_FOLD)) modes = MODES_NF;
+    else if (modes != MODES_N && modes != MODES_NF && modes != MODES_S && modes != MODES_CS) return -1;
+    modes |= grouped;
+    switch (M * 100000 + pj * 1000 + modes) {
         GEMV_CASES_M(1)
         GEMV_CASES_M(2)
         GEMV_CASES_M(4)

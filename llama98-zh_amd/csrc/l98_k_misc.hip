@@ -18,12 +18,12 @@ __global__ void k_embed(const int8_t *__restrict__ q, const float *__restrict__ 
         x[(size_t)t * d + i] = (float)row[i] * sr[i / gs];
 }
 
-template <int PJ>
+template <int PJ, bool NORM, bool TOK>
 __global__ __launch_bounds__(64) void k_rmsnorm(float *__restrict__ x, int x_stride,
                                                 const float *__restrict__ a, const float *__restrict__ b,
                                                 const float *__restrict__ w, int n, float eps,
                                                 float *__restrict__ out, int out_stride,
-                                                int8_t *__restrict__ xq, float *__restrict__ xqs, int tok) {
+                                                int8_t *__restrict__ xq, float *__restrict__ xqs) {
     __shared__ __align__(16) float sq[ps_row_floats<4 * PJ>()];
     __shared__ PsRec rec[128];
     __shared__ float s_inv;
@@ -53,9 +53,8 @@ __global__ __launch_bounds__(64) void k_rmsnorm(float *__restrict__ x, int x_str
             if (lane + 64 * j < nf) xr[lane + 64 * j] = v[j];
         }
     }
-    norm_row<PJ>(v, wn, n, eps, sq, rec, &s_inv, out ? out + (size_t)row * out_stride : nullptr,
-                 xq ? xq + (size_t)row * n : nullptr, xqs ? xqs + (size_t)row * (n >> 5) : nullptr, w != nullptr,
-                 tok != 0);
+    norm_row<PJ, NORM, TOK>(v, wn, n, eps, sq, rec, &s_inv, out ? out + (size_t)row * out_stride : nullptr,
+                            xq ? xq + (size_t)row * n : nullptr, xqs ? xqs + (size_t)row * (n >> 5) : nullptr);
 }
 
 // MTP input rows (lz_mtp_draft_step / lz_mtp_prefill, src/forward_mtp.c:
@@ -284,11 +283,21 @@ extern "C" int l98k_rmsnorm_ex(float *x, int x_stride, const float *a, const flo
     if (n < 32 || n > 256 * 8 || (n & 31) || (x_stride & 3) || (out && (out_stride & 3)) || rows < 1 ||
         (xq && !xqs))
         return -1;
-#define NORM_LAUNCH(PJ)                                                                          \
-    if (n <= 256 * PJ) {                                                                         \
-        hipLaunchKernelGGL(k_rmsnorm<PJ>, dim3(rows), dim3(64), 0, st, x, x_stride, a, b, w, n, \
-                           eps, out, out_stride, xq, xqs, tok);                                  \
-        return (int)hipGetLastError();                                                           \
+#define NORM_LAUNCH(PJ)                                                                                   \
+    if (n <= 256 * PJ) {                                                                                  \
+        if (w && !tok)                                                                                    \
+            hipLaunchKernelGGL((k_rmsnorm<PJ, true, false>), dim3(rows), dim3(64), 0, st, x, x_stride, a, b, w, \
+                               n, eps, out, out_stride, xq, xqs);                                         \
+        else if (w)                                                                                       \
+            hipLaunchKernelGGL((k_rmsnorm<PJ, true, true>), dim3(rows), dim3(64), 0, st, x, x_stride, a, b, w, \
+                               n, eps, out, out_stride, xq, xqs);                                         \
+        else if (!tok)                                                                                    \
+            hipLaunchKernelGGL((k_rmsnorm<PJ, false, false>), dim3(rows), dim3(64), 0, st, x, x_stride, a, b, \
+                               w, n, eps, out, out_stride, xq, xqs);                                      \
+        else                                                                                              \
+            hipLaunchKernelGGL((k_rmsnorm<PJ, false, true>), dim3(rows), dim3(64), 0, st, x, x_stride, a, b, \
+                               w, n, eps, out, out_stride, xq, xqs);                                      \
+        return (int)hipGetLastError();                                                                    \
     }
     NORM_CASES(NORM_LAUNCH)
 #undef NORM_LAUNCH

@@ -6,7 +6,7 @@
 // Grouped expert GEMV: block -> (projection jb, group gi, tile).  Group gi
 // is one distinct expert of the chunk with its member (token, slot) pairs;
 // its weight rows stream once for all members.  Output row = pair.
-template <int M, int PJ>
+template <int M, int PJ, int G>
 __global__ __launch_bounds__(GEMV_THREADS) void k_expert_gemv(ExpertJob j0, ExpertJob j1,
                                                               const MoeGroups *__restrict__ grp,
                                                               int max_groups, int in_dim, int out_rows, int R,
@@ -37,8 +37,8 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_expert_gemv(ExpertJob j0, Expe
         if (threadIdx.x == t) s_orow[t] = mem;
     }
     const int row0 = tile * R;
-    const int nws = (J.gs > 0 && J.gs < in_dim) ? in_dim / J.gs : 1;
-    gemv_tile<M, PJ, MODES_S>(J.q + ((size_t)e * out_rows + row0) * in_dim, J.s + (size_t)e * out_rows * nws,
+    const int nws = (G && J.gs > 0 && J.gs < in_dim) ? in_dim / J.gs : 1;
+    gemv_tile<M, PJ, MODES_S | G>(J.q + ((size_t)e * out_rows + row0) * in_dim, J.s + (size_t)e * out_rows * nws,
                              imin(R, out_rows - row0), R, in_dim, J.pro, J.xq, J.xqs, xrow, s_orow, nm, false, J.out,
                              out_rows, row0, nullptr, 0, smem, s_inv, tab, J.gs);
 }
@@ -280,7 +280,7 @@ __device__ __forceinline__ int route_group(const RouteLds &R, const RouteSet &rs
 // pair.  Block 0 also publishes the routing (sel_idx, sel_w, the group
 // table and the distinct-expert tally) for the down projection and the
 // combine.
-template <int M, int PJ>
+template <int M, int PJ, int G>
 __global__ __launch_bounds__(GEMV_THREADS) void k_moe_up(ExpertJob j0, ExpertJob j1, const float *__restrict__ logits,
                                                          const float *__restrict__ bias, int E, int topk, int nt,
                                                          int *__restrict__ sel_idx, float *__restrict__ sel_w,
@@ -331,8 +331,8 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_up(ExpertJob j0, ExpertJob
         if (threadIdx.x == t) s_orow[t] = mem;
     }
     const int row0 = tile * R;
-    const int nws = (J.gs > 0 && J.gs < in_dim) ? in_dim / J.gs : 1;
-    gemv_tile<M, PJ, MODES_Q>(J.q + ((size_t)e * out_rows + row0) * in_dim, J.s + (size_t)e * out_rows * nws,
+    const int nws = (G && J.gs > 0 && J.gs < in_dim) ? in_dim / J.gs : 1;
+    gemv_tile<M, PJ, MODES_Q | G>(J.q + ((size_t)e * out_rows + row0) * in_dim, J.s + (size_t)e * out_rows * nws,
                              imin(R, out_rows - row0), R, in_dim, J.pro, J.xq, J.xqs, xrow, s_orow, nm, false, J.out,
                              out_rows, row0, nullptr, 0, smem, s_inv, tab, J.gs);
 }
@@ -346,20 +346,25 @@ extern "C" int l98k_upload_exp_table_moe(const float *tab) {
 // Member slots of a grouped expert launch: a power of two >= nt.
 static int expert_m(int nt) { return nt <= 1 ? 1 : nt <= 2 ? 2 : nt <= 4 ? 4 : 8; }
 
-#define EXPERT_CASE(KERNEL, M_, PJ_, ...)                                                \
-    case M_ * 16 + PJ_:                                                                  \
-        ALLOW_BIG_LDS((KERNEL<M_, PJ_>));                                                \
-        hipLaunchKernelGGL((KERNEL<M_, PJ_>), __VA_ARGS__);                              \
+// Instances: member slots M, prologue width PJ, and G = MG for weights with
+// grouped scales (0: one scale per row).
+#define EXPERT_CASE(KERNEL, M_, PJ_, G_, ...)                                            \
+    case ((G_) != 0 ? 256 : 0) + M_ * 16 + PJ_:                                                 \
+        ALLOW_BIG_LDS((KERNEL<M_, PJ_, G_>));                                            \
+        hipLaunchKernelGGL((KERNEL<M_, PJ_, G_>), __VA_ARGS__);                          \
         break;
-#define EXPERT_DISPATCH(KERNEL, M, PJ, ...)                                              \
+#define EXPERT_CASES_G(KERNEL, G_, ...)                                                  \
+    EXPERT_CASE(KERNEL, 1, 1, G_, __VA_ARGS__) EXPERT_CASE(KERNEL, 1, 2, G_, __VA_ARGS__)  \
+    EXPERT_CASE(KERNEL, 1, 4, G_, __VA_ARGS__) EXPERT_CASE(KERNEL, 2, 1, G_, __VA_ARGS__)  \
+    EXPERT_CASE(KERNEL, 2, 2, G_, __VA_ARGS__) EXPERT_CASE(KERNEL, 2, 4, G_, __VA_ARGS__)  \
+    EXPERT_CASE(KERNEL, 4, 1, G_, __VA_ARGS__) EXPERT_CASE(KERNEL, 4, 2, G_, __VA_ARGS__)  \
+    EXPERT_CASE(KERNEL, 4, 4, G_, __VA_ARGS__) EXPERT_CASE(KERNEL, 8, 1, G_, __VA_ARGS__)  \
+    EXPERT_CASE(KERNEL, 8, 2, G_, __VA_ARGS__) EXPERT_CASE(KERNEL, 8, 4, G_, __VA_ARGS__)
+#define EXPERT_DISPATCH(KERNEL, M, PJ, GROUPED, ...)                                     \
     do {                                                                                 \
-        switch (M * 16 + PJ) {                                                           \
-            EXPERT_CASE(KERNEL, 1, 1, __VA_ARGS__) EXPERT_CASE(KERNEL, 1, 2, __VA_ARGS__)  \
-            EXPERT_CASE(KERNEL, 1, 4, __VA_ARGS__) EXPERT_CASE(KERNEL, 2, 1, __VA_ARGS__)  \
-            EXPERT_CASE(KERNEL, 2, 2, __VA_ARGS__) EXPERT_CASE(KERNEL, 2, 4, __VA_ARGS__)  \
-            EXPERT_CASE(KERNEL, 4, 1, __VA_ARGS__) EXPERT_CASE(KERNEL, 4, 2, __VA_ARGS__)  \
-            EXPERT_CASE(KERNEL, 4, 4, __VA_ARGS__) EXPERT_CASE(KERNEL, 8, 1, __VA_ARGS__)  \
-            EXPERT_CASE(KERNEL, 8, 2, __VA_ARGS__) EXPERT_CASE(KERNEL, 8, 4, __VA_ARGS__)  \
+        switch ((GROUPED ? 256 : 0) + M * 16 + PJ) {                                     \
+            EXPERT_CASES_G(KERNEL, 0, __VA_ARGS__)                                       \
+            EXPERT_CASES_G(KERNEL, MG, __VA_ARGS__)                                      \
         default: return -1;                                                              \
         }                                                                                \
     } while (0)
@@ -387,7 +392,9 @@ extern "C" int l98k_expert_gemv(const ExpertJob *jobs, int n_jobs, const MoeGrou
     const int pj = pro_pj(in_dim);
     const dim3 grid(tiles, max_groups, n_jobs), blk(GEMV_THREADS);
     const ExpertJob &a = jobs[0], &b2 = n_jobs > 1 ? jobs[1] : jobs[0];
-    EXPERT_DISPATCH(k_expert_gemv, M, pj, grid, blk, lds, st, a, b2, grp, max_groups, in_dim, out_rows, R, tiles);
+    const bool grouped = (a.gs && a.gs < in_dim) || (b2.gs && b2.gs < in_dim);
+    EXPERT_DISPATCH(k_expert_gemv, M, pj, grouped, grid, blk, lds, st, a, b2, grp, max_groups, in_dim, out_rows, R,
+                    tiles);
     return (int)hipGetLastError();
 }
 
@@ -406,8 +413,9 @@ extern "C" int l98k_moe_up(const ExpertJob *jobs, int n_jobs, const float *logit
     const int pj = pro_pj(in_dim);
     const dim3 grid(tiles, max_groups, n_jobs), blk(GEMV_THREADS);
     const ExpertJob &a = jobs[0], &b2 = n_jobs > 1 ? jobs[1] : jobs[0];
-    EXPERT_DISPATCH(k_moe_up, M, pj, grid, blk, lds, st, a, b2, logits, bias, E, topk, nt, sel_idx, sel_w, grp, tally,
-                    max_groups, in_dim, out_rows, R, tiles);
+    const bool grouped = (a.gs && a.gs < in_dim) || (b2.gs && b2.gs < in_dim);
+    EXPERT_DISPATCH(k_moe_up, M, pj, grouped, grid, blk, lds, st, a, b2, logits, bias, E, topk, nt, sel_idx, sel_w, grp,
+                    tally, max_groups, in_dim, out_rows, R, tiles);
     return (int)hipGetLastError();
 }
 
