@@ -70,7 +70,8 @@ class L98SynthConfig(C.Structure):
         "moe_inter", "shared_w", "mtp_inter")] + [
         ("w_std", C.c_float), ("router_std", C.c_float), ("bias_std", C.c_float), ("resid_std", C.c_float),
         ("mtp_echo", C.c_int), ("use_subn", C.c_int), ("hadamard_o", C.c_int), ("hadamard_down", C.c_int),
-        ("bin_version", C.c_int), ("gs", C.c_int), ("scale_layout", C.c_int), ("bf16_small", C.c_int)]
+        ("bin_version", C.c_int), ("gs", C.c_int), ("scale_layout", C.c_int), ("bf16_small", C.c_int),
+        ("mtp_n_draft", C.c_int)]
 
 
 _P = C.c_void_p

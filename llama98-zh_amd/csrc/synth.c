@@ -148,6 +148,15 @@ int l98_synth_config(int id, L98SynthConfig *c) {
         c->scale_layout = id == 14 ? 2 : 0;
         c->bf16_small = id == 14 ? 1 : 0;
         return 0;
+    case 18: case 19: case 20: case 21:
+        if (l98_synth_config(id == 18 ? 10 : id == 19 ? 11 : id == 20 ? 0 : 12, c)) return 1;
+        c->bin_version = id == 20 ? 7 : 6;
+        c->mtp_n_draft = id == 18 ? 4 : id == 19 ? 6 : 3;
+        if (id == 20) {
+            c->gs = 64;
+            c->bf16_small = 1;
+        }
+        return 0;
     case 10: case 11: case 12:
         c->vocab = 512; c->hidden = 64; c->n_layers = 4; c->seq_len = 160;
         c->n_heads = 2; c->n_kv_heads = 1; c->head_dim = 32;
@@ -239,7 +248,7 @@ static void put_u32(Writer *w, uint32_t v) { put_bytes(w, &v, 4); }
 static void put_i32(Writer *w, int32_t v) { put_bytes(w, &v, 4); }
 static void put_f32(Writer *w, float v) { put_bytes(w, &v, 4); }
 
-typedef enum { INIT_NORMAL, INIT_UNIFORM, INIT_CONST, INIT_ALOG, INIT_DTBIAS, INIT_EYE } InitKind;
+typedef enum { INIT_NORMAL, INIT_UNIFORM, INIT_CONST, INIT_ALOG, INIT_DTBIAS, INIT_EYE, INIT_EYE2 } InitKind;
 
 typedef struct {
     uint64_t seed;
@@ -269,6 +278,9 @@ static float init_value(const Job *j, uint64_t *st, int r, int c) {
     case INIT_EYE:              /* left square block I, right block N(0, a) */
         if (c >= j->rows) return (float)((double)j->a * l98_synth_normal(st));
         return r == c ? 1.0f : 0.0f;
+    case INIT_EYE2:             /* two square blocks I, then N(0, a) */
+        if (c >= 2 * j->rows) return (float)((double)j->a * l98_synth_normal(st));
+        return r == c % j->rows ? 1.0f : 0.0f;
     case INIT_NORMAL:
         return (float)((double)j->b + (double)j->a * l98_synth_normal(st));
     case INIT_UNIFORM:
@@ -408,6 +420,14 @@ static void emit_tensor(Writer *w, int rows, int cols, InitKind kind, float a,
     free(base.q); free(base.scale); free(base.f); free(base.s16); free(base.u8);
 }
 
+/* A tensor of no elements (a [vocab][0] Markov tensor): dtype and count only. */
+static void empty_tensor(Writer *w) {
+    uint8_t dt = w->bf16 ? FMT_BF16 : FMT_F32;
+    w->tensor_id++;
+    put_bytes(w, &dt, 1);
+    put_u32(w, 0u);
+}
+
 static void matrix(Writer *w, int rows, int cols, float std) {
     emit_tensor(w, rows, cols, INIT_NORMAL, std, 0.0f, 1);
 }
@@ -435,7 +455,8 @@ int l98_synth_write(const char *dir, const L98SynthConfig *c, uint64_t seed,
     snprintf(path, sizeof(path), "%s/model.bin", dir);
     const int ver = c->bin_version ? c->bin_version : 5;
     if (ver < 4 || ver > 9 || (c->gs && (c->gs % 32)) || c->scale_layout < 0 || c->scale_layout > 2 ||
-        (ver < 6 && c->scale_layout != 0) || (ver == 4 && c->use_subn)) {
+        (ver < 6 && c->scale_layout != 0) || (ver == 4 && c->use_subn) ||
+        (c->mtp_n_draft > 1 && ver < 6) || c->mtp_n_draft > 6) {
         if (err && errlen > 0) snprintf(err, (size_t)errlen, "bad format options");
         return 1;
     }
@@ -508,7 +529,8 @@ int l98_synth_write(const char *dir, const L98SynthConfig *c, uint64_t seed,
         put_i32(&w, c->n_layers);
         for (int i = 0; i < MAX_LAYERS; i++) put_i32(&w, i < c->n_layers ? i : 0);   /* app_layer */
         for (int i = 0; i < MAX_LAYERS; i++) put_i32(&w, 0);                        /* app_loop */
-        put_i32(&w, 1); put_i32(&w, 0); put_i32(&w, 0);    /* mtp_n_draft, embed_hadamard, embed_signs_seed */
+        put_i32(&w, c->mtp_n_draft > 1 ? c->mtp_n_draft : 1);   /* mtp_n_draft */
+        put_i32(&w, 0); put_i32(&w, 0);                /* embed_hadamard, embed_signs_seed */
         put_i32(&w, c->scale_layout);
     }
     if (ver >= 7) put_i32(&w, 0);                      /* loop_input_mix */
@@ -613,11 +635,23 @@ int l98_synth_write(const char *dir, const L98SynthConfig *c, uint64_t seed,
     if (c->mtp_echo) zero_matrix(&w, d, c->mtp_inter); /* down_proj */
     else matrix(&w, d, c->mtp_inter, ws);
     if (c->use_subn) vec_norm(&w, c->mtp_inter, 0.0f, ws);   /* down_proj.norm */
-    if (c->mtp_echo) emit_tensor(&w, d, 2 * d, INIT_EYE, ws, 0.0f, 1);     /* mtp.fc = [I | N(0, ws)] */
-    else matrix(&w, d, 2 * d, ws);                     /* mtp.fc */
+    const int dspark = c->mtp_n_draft > 1;
+    if (!dspark) {
+        if (c->mtp_echo) emit_tensor(&w, d, 2 * d, INIT_EYE, ws, 0.0f, 1);   /* mtp.fc = [I | N(0, ws)] */
+        else matrix(&w, d, 2 * d, ws);                 /* mtp.fc */
+    }
     vec_norm(&w, d, 0.0f, ws);                         /* mtp.norm */
     vec_norm(&w, d, 0.0f, ws);                         /* pre_fc_norm_hidden */
     vec_norm(&w, d, 0.0f, ws);                         /* pre_fc_norm_embedding */
+    if (dspark) {
+        /* main_proj over [norm(h) | norm(emb or mask) | depth row] */
+        if (c->mtp_echo) emit_tensor(&w, d, 3 * d, INIT_EYE2, ws, 0.0f, 1);
+        else matrix(&w, d, 3 * d, ws);
+        matrix(&w, c->mtp_n_draft, d, 1.0f);           /* depth_embed */
+        emit_tensor(&w, 1, d, INIT_NORMAL, 1.0f, 0.0f, 0);   /* mask_embed */
+        empty_tensor(&w);                              /* markov_embed [vocab][0] */
+        empty_tensor(&w);                              /* markov_proj [vocab][0] */
+    }
     }
 
     if (fclose(w.f) != 0) w.failed = 1;

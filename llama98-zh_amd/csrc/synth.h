@@ -55,6 +55,13 @@ typedef struct {
                                    per row and a u8 per group (base * u / 255) */
     int bf16_small;             /* 1: the F32 tensors (norms, conv taps, A_log,
                                    dt_bias, router bias) stored as BF16 */
+    int mtp_n_draft;            /* DSpark draft slots (version >= 6; 0 or 1: the
+                                   fc head).  > 1 writes main_proj [d][3d],
+                                   depth_embed [n_draft][d], mask_embed [d] and
+                                   the two Markov tensors [vocab][0] (a model.bin
+                                   carries no Markov rank, so they are empty) in
+                                   place of fc; with mtp_echo, main_proj =
+                                   [I | I | N(0, w_std)] */
 } L98SynthConfig;
 
 /* Named configurations:
@@ -78,6 +85,11 @@ typedef struct {
  *  15  tiny's shapes as a version-4 file (no MTP head): groups of 64
  *  16  micro's shapes as a version-7 file, per-row groups, f32 scales
  *  17  micro's shapes as a version-8 file, groups of 32, scale layout 2
+ *  18  micro's shapes with a DSpark head of 4 slots (version 6)
+ *  19  echo's shapes with a DSpark head of 6 slots (version 6), echoing
+ *  20  tiny's shapes with a DSpark head of 3 slots (version 7), groups of
+ *              64, BF16 small tensors
+ *  21  micro-subln's shapes with a DSpark head of 3 slots (version 6)
  * Returns 0 on success, 1 for an unknown id. */
 int l98_synth_config(int id, L98SynthConfig *out);
 

@@ -494,14 +494,19 @@ typedef struct {
     int mtp_inter;
     int use_subn, hadamard_o, hadamard_down;
     int version, scale_layout, has_mtp;
+    int n_draft;                                 /* mtp_n_draft: > 1 is a DSpark head */
     QMat embed;
     float *final_norm;
     OLayer *L;
     OLayer mtp;                                  /* attention block + dense FFN */
     QMat mtp_gate, mtp_up, mtp_down, mtp_fc;
     float *mtp_norm, *mtp_pre_h, *mtp_pre_e;
+    QMat mtp_main;                               /* DSpark main_proj [d][3d] */
+    float *mtp_depth, *mtp_mask;                 /* depth_embed rows [n_draft][d], mask_embed [d] */
     float *rope_cs;                              /* [seq_len][rot/2][2] */
 } OModel;
+
+#define SPEC_K_MAX_REF 6                         /* LZ_SPEC_K_MAX, src/ops.h:2098 */
 
 typedef struct { FILE *f; int bad; int layout; } Rd;
 static void rd(Rd *r, void *p, size_t n) {
@@ -532,11 +537,8 @@ static float f16_to_f32(unsigned h) {
 
 /* An F32 tensor of n elements, stored as f32 or as BF16 (dtype 6: the high
  * half of each f32, widened by <<16 as lz_t_f32 does, src/ops_epi.c:1210). */
-static float *rd_f32v(Rd *r, int n) {
-    uint8_t dt = 0xFF;
-    uint32_t cnt = 0;
+static float *rd_f32_body(Rd *r, int n, uint8_t dt, uint32_t cnt) {
     float *p;
-    rd(r, &dt, 1); rd(r, &cnt, 4);
     if ((dt != 0 && dt != 6) || (int)cnt != n) { r->bad = 1; return NULL; }
     p = (float *)malloc(sizeof(float) * (size_t)n);
     if (!p) { r->bad = 1; return NULL; }
@@ -555,6 +557,12 @@ static float *rd_f32v(Rd *r, int n) {
     }
     return p;
 }
+static float *rd_f32v(Rd *r, int n) {
+    uint8_t dt = 0xFF;
+    uint32_t cnt = 0;
+    rd(r, &dt, 1); rd(r, &cnt, 4);
+    return rd_f32_body(r, n, dt, cnt);
+}
 
 /* layout-2 decode (src/compat.c:340-345): base * (u / 255), each step
  * rounded to float. */
@@ -565,15 +573,16 @@ static float u8_decode(float base, float u) {
     return p;
 }
 
+static void free_q(QMat *m) { free(m->q); free(m->s); }
+
 /* A Q8_0 tensor: u32 gs (a multiple of 32 dividing the row), the codes,
  * then the scale plane in the file's layout (read_scale_plane,
  * src/model.c:3510-3554): 0 f32 per group; 1 binary16 per group; 2 a
  * binary16 base per row, then a u8 per group decoded as base * (u / 255). */
-static void rd_q8(Rd *r, QMat *m, int rows, int cols) {
-    uint8_t dt = 0xFF;
-    uint32_t cnt = 0, gs = 0;
+static void rd_q8_body(Rd *r, QMat *m, int rows, int cols, uint8_t dt, uint32_t cnt) {
+    uint32_t gs = 0;
     size_t ng;
-    rd(r, &dt, 1); rd(r, &cnt, 4); rd(r, &gs, 4);
+    rd(r, &gs, 4);
     m->rows = rows; m->cols = cols; m->gs = (int)gs; m->q = NULL; m->s = NULL;
     if (dt != 1 || cnt != (uint32_t)rows * (uint32_t)cols || gs == 0 || gs % 32 || (uint32_t)cols % gs) {
         r->bad = 1; return;
@@ -602,8 +611,29 @@ static void rd_q8(Rd *r, QMat *m, int rows, int cols) {
         free(h); free(u);
     }
 }
-
-static void free_q(QMat *m) { free(m->q); free(m->s); }
+static void rd_q8(Rd *r, QMat *m, int rows, int cols) {
+    uint8_t dt = 0xFF;
+    uint32_t cnt = 0;
+    rd(r, &dt, 1); rd(r, &cnt, 4);
+    rd_q8_body(r, m, rows, cols, dt, cnt);
+}
+/* A table of rows read as lz_t_row_f32 reads it (src/ops_epi.c:1260-1290):
+ * a Q8_0 row is its codes times their group's scale, an F32 / BF16 row its
+ * values.  Returns rows * cols floats. */
+static float *rd_rows_f32(Rd *r, int rows, int cols) {
+    uint8_t dt = 0xFF;
+    uint32_t cnt = 0;
+    float *p;
+    QMat q;
+    rd(r, &dt, 1); rd(r, &cnt, 4);
+    if (dt != 1) return rd_f32_body(r, rows * cols, dt, cnt);
+    rd_q8_body(r, &q, rows, cols, dt, cnt);
+    p = (float *)malloc(sizeof(float) * (size_t)rows * cols);
+    if (r->bad || !p) { r->bad = 1; free_q(&q); free(p); return NULL; }
+    for (size_t i = 0; i < (size_t)rows * cols; i++) p[i] = (float)q.q[i] * q.s[i / (size_t)q.gs];
+    free_q(&q);
+    return p;
+}
 
 /* Cos/sin table of lz_rope_build_table, rope scaling type 0
  * (src/forward_rope.c:75-210).  The float powf/sinf/cosf restatement is the
@@ -649,6 +679,7 @@ ORA_API void ora_close(void *h) {
     free(m->mtp.fn_gate); free(m->mtp.fn_up); free(m->mtp.fn_down);
     free_q(&m->mtp_gate); free_q(&m->mtp_up); free_q(&m->mtp_down); free_q(&m->mtp_fc);
     free(m->mtp_norm); free(m->mtp_pre_h); free(m->mtp_pre_e);
+    free_q(&m->mtp_main); free(m->mtp_depth); free(m->mtp_mask);
     free(m->rope_cs);
     free(m);
 }
@@ -693,9 +724,11 @@ ORA_API void *ora_open(const char *dir, char *err, int errlen) {
      * v5 carries the rest of the tail and the 522 appended words; v6 the
      * application table, mtp_n_draft, the rotated-vocabulary words and
      * the scale layout; v7 / v8 / v9 one word each.  The path restated
-     * here has the identity schedule, at most one draft slot, no rotated
-     * vocabulary and none of the v7-v9 mechanisms. */
+     * here has the identity schedule, no rotated vocabulary and none of the
+     * v7-v9 mechanisms; mtp_n_draft > 1 (at most LZ_SPEC_K_MAX, alloc_mtp
+     * src/model.c:2905-2909) is a DSpark head. */
     m->has_mtp = 0;
+    m->n_draft = 1;
     m->hadamard_o = m->hadamard_down = -1;
     if (m->version >= 5) {
         m->has_mtp = rd_i32(&r); m->mtp_inter = rd_i32(&r);
@@ -709,7 +742,8 @@ ORA_API void *ora_open(const char *dir, char *err, int errlen) {
         int exec_len = rd_i32(&r), bad = exec_len != m->n_layers;
         for (int i = 0; i < 128; i++) bad |= rd_i32(&r) != (i < m->n_layers ? i : 0);   /* app_layer */
         for (int i = 0; i < 128; i++) bad |= rd_i32(&r) != 0;                          /* app_loop */
-        bad |= rd_i32(&r) > 1;                                                          /* mtp_n_draft */
+        m->n_draft = rd_i32(&r);                                                        /* mtp_n_draft */
+        bad |= m->n_draft > SPEC_K_MAX_REF;
         bad |= rd_i32(&r) != 0;                                                         /* embed_hadamard */
         (void)rd_i32(&r);                                                               /* embed_signs_seed */
         r.layout = rd_i32(&r);
@@ -721,6 +755,8 @@ ORA_API void *ora_open(const char *dir, char *err, int errlen) {
     }
     m->scale_layout = r.layout;
     if (m->has_mtp != 0 && m->has_mtp != 1) r.bad = 1;
+    if (m->n_draft < 1) m->n_draft = 1;
+    if (m->n_draft > 1 && !m->has_mtp) r.bad = 1;
     /* resolve_hadamard (src/model.c:139-182): -1 derives (hadamard_o: the
      * whole lin_value_dim on a dense model when it is a power of two, else
      * 0; hadamard_down: the largest power of two <= 512 dividing
@@ -836,10 +872,22 @@ ORA_API void *ora_open(const char *dir, char *err, int errlen) {
     rd_q8(&r, &m->mtp_up, m->mtp_inter, d);
     rd_q8(&r, &m->mtp_down, d, m->mtp_inter);
     if (m->use_subn) m->mtp.fn_down = rd_f32v(&r, m->mtp_inter);
-    rd_q8(&r, &m->mtp_fc, d, 2 * d);
+    /* MTP_SPECS (src/model.c:2529-2552): fc for one draft slot, or the
+     * DSpark main_proj / depth_embed / mask_embed / markov_embed /
+     * markov_proj after the three norms.  A model.bin holds no Markov rank
+     * (only config.json names it, src/model.c:539), so the two Markov
+     * tensors are [vocab][0]: empty, and the correction adds zero. */
+    if (m->n_draft <= 1) rd_q8(&r, &m->mtp_fc, d, 2 * d);
     m->mtp_norm = rd_f32v(&r, d);
     m->mtp_pre_h = rd_f32v(&r, d);
     m->mtp_pre_e = rd_f32v(&r, d);
+    if (m->n_draft > 1) {
+        rd_q8(&r, &m->mtp_main, d, 3 * d);
+        m->mtp_depth = rd_rows_f32(&r, m->n_draft, d);
+        m->mtp_mask = rd_f32v(&r, d);
+        free(rd_f32v(&r, 0));                   /* markov_embed */
+        free(rd_f32v(&r, 0));                   /* markov_proj */
+    }
     }
     {
         char extra;
@@ -857,13 +905,13 @@ ORA_API void *ora_open(const char *dir, char *err, int errlen) {
 
 ORA_API int ora_config(void *h, int *out, int n) {
     OModel *m = (OModel *)h;
-    int v[29] = {m->vocab, m->d, m->n_layers, m->seq_len, m->nh, m->nkv, m->hd,
+    int v[30] = {m->vocab, m->d, m->n_layers, m->seq_len, m->nh, m->nkv, m->hd,
                  m->nk, m->nv, m->kd, m->vd, m->K, m->n_lin, m->n_full,
                  m->gate_rank, m->n_experts, m->topk, m->latent, m->moe_inter,
                  m->shared_w, m->mtp_inter, m->q_dim, m->kv_dim, m->conv_dim,
-                 m->version, m->scale_layout, m->has_mtp, m->embed.gs, m->use_subn};
-    for (int i = 0; i < n && i < 29; i++) out[i] = v[i];
-    return 29;
+                 m->version, m->scale_layout, m->has_mtp, m->embed.gs, m->use_subn, m->n_draft};
+    for (int i = 0; i < n && i < 30; i++) out[i] = v[i];
+    return 30;
 }
 
 ORA_API const float *ora_rope_table(void *h) { return ((OModel *)h)->rope_cs; }
@@ -891,6 +939,7 @@ typedef struct {
     float *x, *xb, *xb2;                         /* [MAXB][d] */
     int8_t *xq; float *xqs;
     float *logits, *mtp_logits, *mtp_hidden, *mtp_chain, *mtp_draft, *mtp_draft_q;
+    float *mtp_kdraft;                           /* DSpark slot logits [SPEC_K_EXT][V] */
     float *target_p;
     int lin_index[128], full_index[128];
     /* scratch */
@@ -904,7 +953,7 @@ ORA_API void ora_state_free(void *h) {
     free(s->kq); free(s->vq); free(s->ks); free(s->vs);
     free(s->x); free(s->xb); free(s->xb2); free(s->xq); free(s->xqs);
     free(s->logits); free(s->mtp_logits); free(s->mtp_hidden); free(s->mtp_chain);
-    free(s->mtp_draft); free(s->mtp_draft_q); free(s->target_p);
+    free(s->mtp_draft); free(s->mtp_draft_q); free(s->target_p); free(s->mtp_kdraft);
     free(s->t0); free(s->t1); free(s->t2); free(s->t3); free(s->t4); free(s->t5);
     free(s->att);
     free(s);
@@ -957,7 +1006,7 @@ ORA_API void *ora_state_new(void *hm, int seq_len, int spec_k_max) {
     s->ks = (float *)calloc((size_t)s->planes * s->seq_len * m->kv_dim / 32, sizeof(float));
     s->vs = (float *)calloc((size_t)s->planes * s->seq_len * m->kv_dim / 32, sizeof(float));
     wide = m->d;
-    if (2 * m->d > wide) wide = 2 * m->d;
+    if (3 * m->d > wide) wide = 3 * m->d;
     if (m->qg_dim > wide) wide = m->qg_dim;
     if (m->conv_dim > wide) wide = m->conv_dim;
     if (m->shared_w > wide) wide = m->shared_w;
@@ -974,6 +1023,7 @@ ORA_API void *ora_state_new(void *hm, int seq_len, int spec_k_max) {
     s->mtp_chain = (float *)calloc((size_t)m->d, sizeof(float));
     s->mtp_draft = (float *)calloc((size_t)m->vocab, sizeof(float));
     s->mtp_draft_q = (float *)calloc((size_t)SPEC_K_EXT * m->vocab, sizeof(float));
+    s->mtp_kdraft = (float *)calloc((size_t)SPEC_K_EXT * m->vocab, sizeof(float));
     s->target_p = (float *)calloc((size_t)m->vocab, sizeof(float));
     s->t0 = (float *)calloc((size_t)MAXB * wide * 4, sizeof(float));
     s->t1 = (float *)calloc((size_t)MAXB * wide * 4, sizeof(float));
@@ -1526,7 +1576,7 @@ ORA_API float *ora_mtp_draft_step(void *hs, int tok, int pos) {
     const int d = m->d;
     float *emb = s->t5, *concat = s->x, *mx = s->xb2 + 0;
     float mtp_x[4096];
-    if (!m->has_mtp || tok < 0 || tok >= m->vocab || pos < 0 || pos >= s->seq_len) return NULL;
+    if (!m->has_mtp || m->n_draft > 1 || tok < 0 || tok >= m->vocab || pos < 0 || pos >= s->seq_len) return NULL;
     (void)mx;
     embed_row(m, tok, emb);
     o_rmsnorm(concat, emb, m->mtp_pre_e, d, m->eps);
@@ -1558,7 +1608,7 @@ ORA_API int ora_mtp_prefill(void *hs, const float *h_all, const int *next, int n
     float *concat = (float *)malloc(sizeof(float) * 2 * (size_t)d);
     float *mx = (float *)malloc(sizeof(float) * (size_t)MAXB * d);
     float emb[4096];
-    if (!m->has_mtp || !h_all || !next || n < 1) { free(concat); free(mx); return 1; }
+    if (!m->has_mtp || m->n_draft > 1 || !h_all || !next || n < 1) { free(concat); free(mx); return 1; }
     while (done < n) {
         int k = n - done;
         if (k > s->nt_cap) k = s->nt_cap;
@@ -1806,6 +1856,194 @@ static int sample_from_dist(const float *p, int vocab, uint64_t *rng) {
     return vocab - 1;
 }
 
+/* mtp_attn_t1, src/forward_mtp.c:191-376, float arm with Q8 KV: one
+ * token at position 0 of the MTP plane with no history.  Softmax over the
+ * single score is exactly 1, so K, Q, RoPE and the scores are not
+ * computed; V is quantized into the plane's row 0 and read back through
+ * wsum_q8_row's arithmetic (src/forward_attn.c:17-21) with weight 1, then
+ * gated.  in: s->xb (one row); out: s->xb2. */
+static void attn_t1(OState *s, const OLayer *L) {
+    const OModel *m = s->m;
+    const int d = m->d, hd = m->hd, nh = m->nh, nkv = m->nkv, kvd = m->kv_dim, qd = m->q_dim;
+    const int kv_mul = nh / nkv;
+    float *qg = s->t0, *vt = s->t2, *ao = s->t4;
+    int8_t *vrow = s->vq + (size_t)m->n_full * s->seq_len * kvd;
+    float *vsrow = s->vs + (size_t)m->n_full * s->seq_len * kvd / 32;
+    if (m->use_subn) {                            /* q and v, each its own norm (:226-235) */
+        subn_proj(s, s->xb, L->sn_q, &L->q, qg, 1, 0, s->xb2);
+        subn_proj(s, s->xb, L->sn_v, &L->v, vt, 1, 0, s->xb2);
+    } else {                                      /* one shared quantization (:236-240) */
+        quant_rows(s, s->xb, d, 1);
+        mm(s, qg, &L->q, 1);
+        mm(s, vt, &L->v, 1);
+    }
+    o_quantize_q8(vt, kvd, vrow, vsrow);          /* the V write at slot 0 (:250-251) */
+    for (int h = 0; h < nh; h++) {
+        const int kvh = h / kv_mul;
+        const int8_t *vr = vrow + (size_t)kvh * hd;
+        const float *vsr = vsrow + (size_t)kvh * hd / 32;
+        const float *gate = qg + (size_t)h * 2 * hd + hd;
+        float *out = ao + (size_t)h * hd;
+        for (int e = 0; e < hd; e++) {
+            out[e] = 0.0f;
+            out[e] += 1.0f * (float)vr[e] * vsr[e >> 5];
+        }
+        for (int e = 0; e < hd; e++) out[e] *= o_sigmoid(gate[e]);   /* (:355-356) */
+    }
+    if (m->use_subn) o_rmsnorm(ao, ao, L->sn_o, qd, m->eps);        /* (:359-362) */
+    quant_rows(s, ao, qd, 1);
+    mm(s, s->xb2, &L->o, 1);
+}
+
+/* lz_mtp_draft_batch, src/forward_mtp.c:385-505: k slots from the same
+ * anchor hidden state (s->mtp_chain), each through main_proj over
+ * [norm(h) | norm(emb) | depth row], the MTP block at position 0 (attn_t1),
+ * the dense FFN, the exit norm and the tied lm_head, into row `slot` of
+ * s->mtp_kdraft.  Slot 0's emb is next_token's embedding row, every later
+ * slot's the shared mask_embed.  The chain is not changed. */
+ORA_API float *ora_mtp_draft_batch(void *hs, int next_token, int k) {
+    OState *s = (OState *)hs;
+    OModel *m = s->m;
+    const int d = m->d;
+    float *concat = s->t5, *emb = s->t3, *hn, mtp_x[4096], ex[4096];
+    if (!m->has_mtp || m->n_draft <= 1 || next_token < 0 || next_token >= m->vocab || k <= 0 || k > m->n_draft)
+        return NULL;
+    hn = concat;
+    o_rmsnorm(hn, s->mtp_chain, m->mtp_pre_h, d, m->eps);          /* (:404-406) */
+    for (int slot = 0; slot < k; slot++) {
+        if (slot == 0) embed_row(m, next_token, emb);
+        else memcpy(emb, m->mtp_mask, sizeof(float) * (size_t)d);
+        o_rmsnorm(concat + d, emb, m->mtp_pre_e, d, m->eps);      /* (:429-431) */
+        memcpy(concat + 2 * d, m->mtp_depth + (size_t)slot * d, sizeof(float) * (size_t)d);
+        o_quantize_q8(concat, 3 * d, s->xq, s->xqs);               /* lz_matmul_w (:438-439) */
+        o_matmul_q8g(mtp_x, s->xq, s->xqs, m->mtp_main.q, m->mtp_main.s, 3 * d, d, 1, m->mtp_main.gs, NULL);
+        if (m->use_subn) memcpy(s->xb, mtp_x, sizeof(float) * (size_t)d);
+        else o_rmsnorm(s->xb, mtp_x, m->mtp.in_norm, d, m->eps);
+        attn_t1(s, &m->mtp);
+        for (int i = 0; i < d; i++) mtp_x[i] += s->xb2[i];
+        if (m->use_subn) memcpy(s->xb, mtp_x, sizeof(float) * (size_t)d);
+        else o_rmsnorm(s->xb, mtp_x, m->mtp.post_norm, d, m->eps);
+        dense_ffn(s, &m->mtp, &m->mtp_gate, &m->mtp_up, &m->mtp_down, 1);
+        for (int i = 0; i < d; i++) mtp_x[i] += s->xb2[i];
+        o_rmsnorm(ex, mtp_x, m->mtp_norm, d, m->eps);               /* (:497-505) */
+        o_quantize_q8(ex, d, s->xq, s->xqs);
+        o_matmul_q8g(s->mtp_kdraft + (size_t)slot * m->vocab, s->xq, s->xqs, m->embed.q, m->embed.s, d, m->vocab,
+                     1, m->embed.gs, NULL);
+    }
+    return s->mtp_kdraft;
+}
+
+/* lz_mtp_markov_correct, src/forward_mtp.c:510-531: logits +=
+ * markov_proj(markov_embed[x_prev]).  The rank is 0 for every model.bin
+ * (the Markov tensors are [vocab][0]), so the projection is a row of zeros
+ * (lz_matmul over no inputs) and the update adds +0 to each entry. */
+ORA_API void ora_mtp_markov_correct(void *hs, int x_prev, float *logits) {
+    OState *s = (OState *)hs;
+    const OModel *m = s->m;
+    if (!m->has_mtp || m->n_draft <= 1 || x_prev < 0 || x_prev >= m->vocab) return;
+    for (int v = 0; v < m->vocab; v++) logits[v] += 0.0f;
+}
+
+/* lz_spec_round_dspark (greedy, no penalties), src/generate.c:1000-1133:
+ * one draft batch, each slot corrected and argmax'd in order (p_min cut),
+ * the verify, acceptance, ring rollback and the chain reseed; no MTP
+ * position advance and no catch-up. */
+ORA_API int ora_spec_round_dspark(void *hs, int anchor, int anchor_pos, int k, float p_min, int n_min,
+                                  int brk, int *out, int *out_n_accept, int *out_new_pos, int *out_k_eff) {
+    OState *s = (OState *)hs;
+    const OModel *m = s->m;
+    const int V = m->vocab;
+    int draft[SPEC_K_EXT], vt[SPEC_K_EXT + 1], targ[SPEC_K_EXT];
+    int k_eff = 0, n_accept, bonus, base;
+    float *bl;
+    if (k < 1 || k > SPEC_K_EXT || k > s->depth - 1 || k > m->n_draft) return -1;
+    bl = ora_mtp_draft_batch(s, anchor, k);
+    if (!bl) return -2;
+    for (int i = 0; i < k; i++) {
+        int x_prev = i == 0 ? anchor : draft[i - 1], idx;
+        float p1, *row = bl + (size_t)i * V;
+        ora_mtp_markov_correct(s, x_prev, row);
+        idx = o_argmax_p1(row, V, &p1);
+        if (p1 < p_min) break;
+        draft[i] = idx;
+        k_eff = i + 1;
+    }
+    if (k_eff < n_min) {
+        out[0] = anchor;
+        *out_n_accept = 0; *out_new_pos = anchor_pos; *out_k_eff = k_eff;
+        return 0;
+    }
+    base = s->ssm_slot;
+    vt[0] = anchor;
+    for (int i = 0; i < k_eff; i++) vt[i + 1] = draft[i];
+    if (ora_forward_verify(s, vt, k_eff + 1, anchor_pos + 1)) return -2;
+    for (int i = 0; i < k_eff; i++) targ[i] = o_argmax(s->mtp_logits + (size_t)i * V, V);
+    bonus = o_argmax(s->mtp_logits + (size_t)k_eff * V, V);
+    n_accept = o_spec_accept(draft, targ, k_eff, bonus, out);
+    if (n_accept < k_eff && !brk) s->ssm_slot = (base + n_accept + 1) % s->depth;
+    memcpy(s->mtp_chain, s->mtp_hidden + (size_t)n_accept * m->d, sizeof(float) * (size_t)m->d);
+    *out_n_accept = n_accept;
+    *out_new_pos = anchor_pos + 1 + n_accept;
+    *out_k_eff = k_eff;
+    return n_accept + 1;
+}
+
+/* lz_spec_round_dspark_temp (penalties off), src/generate.c:1382-1505. */
+ORA_API int ora_spec_round_dspark_temp(void *hs, int anchor, int anchor_pos, int k, float p_min, int n_min,
+                                       float temp, float topp, uint64_t *rng, int brk, int *out,
+                                       int *out_n_accept, int *out_new_pos, int *out_k_eff) {
+    OState *s = (OState *)hs;
+    const OModel *m = s->m;
+    const int V = m->vocab;
+    int draft[SPEC_K_EXT], vt[SPEC_K_EXT + 1];
+    int k_eff = 0, n_accept, base;
+    float *bl;
+    if (k < 1 || k > SPEC_K_EXT || k > s->depth - 1 || k > m->n_draft) return -1;
+    bl = ora_mtp_draft_batch(s, anchor, k);
+    if (!bl) return -2;
+    for (int i = 0; i < k; i++) {
+        int x_prev = i == 0 ? anchor : draft[i - 1], idx;
+        float *row = bl + (size_t)i * V;
+        ora_mtp_markov_correct(s, x_prev, row);
+        idx = o_sample_temp_q(row, V, temp, rng);
+        if (row[idx] < p_min) break;
+        draft[i] = idx;
+        memcpy(s->mtp_draft_q + (size_t)i * V, row, sizeof(float) * (size_t)V);
+        k_eff = i + 1;
+    }
+    if (k_eff < n_min) {
+        out[0] = anchor;
+        *out_n_accept = 0; *out_new_pos = anchor_pos; *out_k_eff = k_eff;
+        return 0;
+    }
+    base = s->ssm_slot;
+    vt[0] = anchor;
+    for (int i = 0; i < k_eff; i++) vt[i + 1] = draft[i];
+    if (ora_forward_verify(s, vt, k_eff + 1, anchor_pos + 1)) return -2;
+    n_accept = k_eff;
+    for (int i = 0; i < k_eff; i++) {
+        float *row = s->mtp_logits + (size_t)i * V;
+        float u;
+        int acc, tok;
+        o_target_dist(row, V, temp, topp, s->target_p);
+        u = o_random_f32(rng);
+        tok = o_spec_accept_temp(s->target_p, s->mtp_draft_q + (size_t)i * V, draft[i], V, u, rng, &acc);
+        out[i] = tok;
+        if (!acc) { n_accept = i; break; }
+    }
+    if (n_accept == k_eff) {
+        float *row = s->mtp_logits + (size_t)k_eff * V;
+        o_target_dist(row, V, temp, topp, s->target_p);
+        out[k_eff] = sample_from_dist(s->target_p, V, rng);
+    }
+    if (n_accept < k_eff && !brk) s->ssm_slot = (base + n_accept + 1) % s->depth;
+    memcpy(s->mtp_chain, s->mtp_hidden + (size_t)n_accept * m->d, sizeof(float) * (size_t)m->d);
+    *out_n_accept = n_accept;
+    *out_new_pos = anchor_pos + 1 + n_accept;
+    *out_k_eff = k_eff;
+    return n_accept + 1;
+}
+
 /* lz_spec_round (greedy, no penalties), src/generate.c:694-994. */
 ORA_API int ora_spec_round(void *hs, int anchor, int anchor_pos, int k, float p_min, int n_min,
                            int brk, int skipc, int *out, int *out_n_accept, int *out_new_pos,
@@ -1915,8 +2153,12 @@ ORA_API int ora_session_start(void *hs, const int *prompt, int n_prompt) {
     if (n_prompt < 2) return 1;
     h = (float *)malloc(sizeof(float) * (size_t)(n_prompt - 1) * s->m->d);
     rc = ora_forward_batch_capture(s, prompt, n_prompt - 1, 0, h);
-    if (!rc && s->m->has_mtp) rc = ora_mtp_prefill(s, h, prompt + 1, n_prompt - 1, s->mtp_pos);
-    s->mtp_pos = n_prompt - 1;
+    /* A DSpark head has no fc for lz_mtp_prefill to project through, and no
+     * DSpark step reads the MTP KV rows: its session is the body prefill. */
+    if (!rc && s->m->has_mtp && s->m->n_draft <= 1) {
+        rc = ora_mtp_prefill(s, h, prompt + 1, n_prompt - 1, s->mtp_pos);
+        s->mtp_pos = n_prompt - 1;
+    }
     free(h);
     return rc;
 }
@@ -1952,7 +2194,13 @@ ORA_API int ora_generate_ex(void *hs, const int *prompt, int n_prompt, int k, in
             n++;
             if (n >= n_new) break;
         }
-        if (temp > 0.0f)
+        if (m->n_draft > 1 && temp > 0.0f)       /* src/generate.c:1929-1946 */
+            ne = ora_spec_round_dspark_temp(s, anchor, anchor_pos, k, p_min, n_min, temp, topp, &rng, brk, out,
+                                            &n_accept, &new_pos, &k_eff);
+        else if (m->n_draft > 1)
+            ne = ora_spec_round_dspark(s, anchor, anchor_pos, k, p_min, n_min, brk, out, &n_accept, &new_pos,
+                                       &k_eff);
+        else if (temp > 0.0f)
             ne = ora_spec_round_temp(s, anchor, anchor_pos, k, p_min, n_min, temp, topp, &rng, brk,
                                      skipc, out, &n_accept, &new_pos, &k_eff);
         else
@@ -2004,6 +2252,7 @@ ORA_API const float *ora_mtp_logits(void *hs) { return ((OState *)hs)->mtp_logit
 ORA_API const float *ora_mtp_hidden(void *hs) { return ((OState *)hs)->mtp_hidden; }
 ORA_API const float *ora_mtp_chain(void *hs) { return ((OState *)hs)->mtp_chain; }
 ORA_API const float *ora_draft_logits(void *hs) { return ((OState *)hs)->mtp_draft; }
+ORA_API const float *ora_kdraft_logits(void *hs) { return ((OState *)hs)->mtp_kdraft; }
 ORA_API const float *ora_logits(void *hs) { return ((OState *)hs)->logits; }
 ORA_API void ora_kv_plane(void *hs, int plane, int rows, int8_t *kq, float *ks, int8_t *vq, float *vs) {
     OState *s = (OState *)hs;

@@ -8,6 +8,13 @@
  *   lz_forward_batch_capture(prompt[0..n-2]) -> lz_mtp_prefill -> mtp_pos=n-1
  *   lz_forward_capture(prompt[n-1]) -> anchor = sample(logits)
  *   loop lz_spec_round / lz_spec_round_temp.
+ * A DSpark model (config.mtp_n_draft > 1) runs lz_spec_round_dspark /
+ * lz_spec_round_dspark_temp, as the driver dispatches (src/generate.c:
+ * 1929-1946), and its session start skips lz_mtp_prefill: that function
+ * projects through mtp.fc (src/forward_mtp.c:590), which a DSpark head does
+ * not bind (src/model.c:2531-2532), so the driver's default prompt pass
+ * faults on such a model; its MTP-prefill skip knob gives the body-only
+ * prefill used here, and no DSpark step reads the MTP KV rows.
  *
  * Usage:
  *   l98ref_* gen MODEL_DIR PROMPT_FILE K N_NEW TEMP TOPP SEED OUT_PREFIX [opts]
@@ -105,6 +112,7 @@ static void select_mode(void) {
  * *token = prompt[n-1], *pos = n-1 (have_seed = 0). */
 static int session_start(const LZModel *m, LZRunState *s, const int *prompt,
                          int n_prompt, double *t_prefill_us) {
+    const int dspark = m->config.mtp_n_draft > 1;
     int dim = m->config.hidden_size;
     float *h_all;
     double t0 = now_us();
@@ -113,8 +121,10 @@ static int session_start(const LZModel *m, LZRunState *s, const int *prompt,
     h_all = (float *)malloc(sizeof(float) * (size_t)(n_prompt - 1) * dim);
     if (!h_all) return 1;
     if (!lz_forward_batch_capture(m, s, prompt, n_prompt - 1, 0, h_all)) { free(h_all); return 1; }
-    if (lz_mtp_prefill(m, s, h_all, prompt + 1, n_prompt - 1, s->mtp_pos) != 0) { free(h_all); return 1; }
-    s->mtp_pos = n_prompt - 1;
+    if (!dspark) {
+        if (lz_mtp_prefill(m, s, h_all, prompt + 1, n_prompt - 1, s->mtp_pos) != 0) { free(h_all); return 1; }
+        s->mtp_pos = n_prompt - 1;
+    }
     free(h_all);
     if (t_prefill_us) *t_prefill_us = now_us() - t0;
     return 0;
@@ -243,7 +253,13 @@ static int cmd_gen(int argc, char **argv) {
             toks[n_tok++] = anchor;
             if (n_tok >= n_new) break;
         }
-        if (temp > 0.0f)
+        if (m.config.mtp_n_draft > 1 && temp > 0.0f)
+            n_emit = lz_spec_round_dspark_temp(&m, &s, anchor, anchor_pos, k, p_min, n_min, &samp,
+                                               brk, out_t, &n_accept, &new_pos, &k_eff, err, sizeof err);
+        else if (m.config.mtp_n_draft > 1)
+            n_emit = lz_spec_round_dspark(&m, &s, anchor, anchor_pos, k, p_min, n_min, &samp,
+                                          brk, out_t, &n_accept, &new_pos, &k_eff, err, sizeof err);
+        else if (temp > 0.0f)
             n_emit = lz_spec_round_temp(&m, &s, anchor, anchor_pos, k, p_min, n_min, &samp,
                                         brk, skipc, out_t, &n_accept, &new_pos, &k_eff,
                                         err, sizeof err);
@@ -264,7 +280,10 @@ static int cmd_gen(int argc, char **argv) {
             dump(prefix, tag, s.mtp_verify_hidden,
                  sizeof(float) * (size_t)(k_eff + 1) * m.config.hidden_size);
             snprintf(tag, sizeof tag, "draft%d", rounds);
-            dump(prefix, tag, s.mtp_draft_logits, sizeof(float) * (size_t)m.config.vocab_size);
+            if (m.config.mtp_n_draft > 1)       /* every slot's (corrected) logits */
+                dump(prefix, tag, s.mtp_kdraft_logits, sizeof(float) * (size_t)k * m.config.vocab_size);
+            else
+                dump(prefix, tag, s.mtp_draft_logits, sizeof(float) * (size_t)m.config.vocab_size);
         }
         rounds++;
         have_seed = (n_emit > 0);

@@ -50,3 +50,25 @@ def micro_subln(pkg, model_root):
 @pytest.fixture(scope="session")
 def subln(pkg, model_root):
     return pkg.ensure_model(os.path.join(model_root, "subln"), 5, seed=1234)
+
+
+# DSpark heads (mtp_n_draft > 1): micro, echo, tiny (v7, groups of 64, BF16)
+# and micro-subln shapes
+@pytest.fixture(scope="session")
+def ds_micro(pkg, model_root):
+    return pkg.ensure_model(os.path.join(model_root, "ds_micro"), 18, seed=1234)
+
+
+@pytest.fixture(scope="session")
+def ds_echo(pkg, model_root):
+    return pkg.ensure_model(os.path.join(model_root, "ds_echo"), 19, seed=1234)
+
+
+@pytest.fixture(scope="session")
+def ds_tiny(pkg, model_root):
+    return pkg.ensure_model(os.path.join(model_root, "ds_tiny"), 20, seed=1234)
+
+
+@pytest.fixture(scope="session")
+def ds_subln(pkg, model_root):
+    return pkg.ensure_model(os.path.join(model_root, "ds_subln"), 21, seed=1234)

@@ -70,6 +70,19 @@ CASES = [
     ("gen_fmt14_v6_k2_temp", "fmt14", 14, 8192, 48, 2, 32, 0.8, 0.95, 7),
     ("gen_fmt16_v7_k2_greedy", "fmt16", 16, 512, 24, 2, 40, 0.0, 1.0, 1, {"dump": 4}),
     ("gen_fmt17_v8_k3_greedy", "fmt17", 17, 512, 24, 3, 40, 0.0, 1.0, 1, {"dump": 4}),
+    # DSpark heads (mtp_n_draft > 1, lz_spec_round_dspark / _temp); the echo
+    # one (config 19) accepts 0..k drafts.
+    ("gen_ds_micro_k4_greedy", "ds_micro", 18, 512, 24, 4, 40, 0.0, 1.0, 1, {"dump": 4}),
+    ("gen_ds_micro_k4_temp", "ds_micro", 18, 512, 24, 4, 40, 0.8, 0.95, 7),
+    ("gen_ds_echo_k4_greedy", "ds_echo", 19, 64, 24, 4, 100, 0.0, 1.0, 1, {"prompt_seed": 11, "dump": 6}),
+    ("gen_ds_echo_k6_greedy", "ds_echo", 19, 64, 24, 6, 100, 0.0, 1.0, 1, {"prompt_seed": 11}),
+    ("gen_ds_echo_k3_temp", "ds_echo", 19, 64, 24, 3, 100, 0.8, 0.95, 7, {"prompt_seed": 11}),
+    ("gen_ds_echo_k4_pmin_nmin", "ds_echo", 19, 64, 24, 4, 100, 0.0, 1.0, 1,
+     {"prompt_seed": 11, "p_min": 0.025, "n_min": 2}),
+    ("gen_ds_echo_k4_brk", "ds_echo", 19, 64, 24, 4, 100, 0.0, 1.0, 1, {"prompt_seed": 11, "brk": 1}),
+    ("gen_ds_tiny_k3_greedy", "ds_tiny", 20, 8192, 48, 3, 40, 0.0, 1.0, 1, {"dump": 4}),
+    ("gen_ds_subln_k3_greedy", "ds_subln", 21, 512, 24, 3, 40, 0.0, 1.0, 1, {"dump": 4}),
+    ("gen_ds_subln_k2_temp", "ds_subln", 21, 512, 24, 2, 40, 0.8, 0.95, 7),
 ]
 # Prefill + one capture (the harness's capture command; needs no MTP head):
 # (fixture, model dir name, generator config id, vocab, n_prompt)

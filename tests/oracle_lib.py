@@ -59,6 +59,11 @@ def lib():
             "ora_logits": (_FP, [_P]),
             "ora_kv_plane": (None, [_P, C.c_int, C.c_int, _P, _FP, _P, _FP]),
             "ora_set_tap": (None, [C.c_char_p]),
+            "ora_mtp_draft_batch": (_FP, [_P, C.c_int, C.c_int]),
+            "ora_mtp_markov_correct": (None, [_P, C.c_int, _FP]),
+            "ora_kdraft_logits": (_FP, [_P]),
+            "ora_spec_round_dspark": (C.c_int, [_P, C.c_int, C.c_int, C.c_int, C.c_float, C.c_int, C.c_int,
+                                                _IP, _IP, _IP, _IP]),
             "o_exp": (C.c_float, [C.c_float]),
             "o_rsqrt": (C.c_float, [C.c_float]),
             "o_sigmoid": (C.c_float, [C.c_float]),
@@ -109,11 +114,12 @@ class Oracle:
         if not self.m:
             raise RuntimeError("ora_open: " + err.value.decode())
         self.s = L.ora_state_new(self.m, 0, spec_k_max)
-        cfg = (C.c_int * 24)()
-        L.ora_config(self.m, cfg, 24)
+        cfg = (C.c_int * 30)()
+        L.ora_config(self.m, cfg, 30)
         (self.V, self.d, self.n_layers, self.seq_len, self.nh, self.nkv, self.hd, self.nk, self.nv, self.kd,
          self.vd, self.K, self.n_lin, self.n_full, self.gate_rank, self.E, self.topk, self.latent,
-         self.moe_inter, self.shared_w, self.mtp_inter, self.q_dim, self.kv_dim, self.conv_dim) = list(cfg)
+         self.moe_inter, self.shared_w, self.mtp_inter, self.q_dim, self.kv_dim, self.conv_dim) = list(cfg)[:24]
+        self.n_draft = cfg[29]
 
     def close(self):
         L = lib()
@@ -184,6 +190,21 @@ class Oracle:
         na, npos, ke = C.c_int(), C.c_int(), C.c_int()
         r = lib().ora_spec_round(self.s, int(anchor), int(anchor_pos), int(k), float(p_min), int(n_min),
                                  brk, skipc, ip(out), C.byref(na), C.byref(npos), C.byref(ke))
+        return r, out, na.value, npos.value, ke.value
+
+    def draft_batch(self, token, k):
+        """DSpark base logits of k slots from the current chain, [k][V]."""
+        p = lib().ora_mtp_draft_batch(self.s, int(token), int(k))
+        return None if not p else np.ctypeslib.as_array(p, shape=(k, self.V)).copy()
+
+    def kdraft_logits(self, k):
+        return np.ctypeslib.as_array(lib().ora_kdraft_logits(self.s), shape=(k, self.V)).copy()
+
+    def spec_round_dspark(self, anchor, anchor_pos, k, p_min=0.0, n_min=0, brk=0):
+        out = np.zeros(8, np.int32)
+        na, npos, ke = C.c_int(), C.c_int(), C.c_int()
+        r = lib().ora_spec_round_dspark(self.s, int(anchor), int(anchor_pos), int(k), float(p_min), int(n_min),
+                                        brk, ip(out), C.byref(na), C.byref(npos), C.byref(ke))
         return r, out, na.value, npos.value, ke.value
 
     def generate(self, prompt, k, n_new, temp=0.0, topp=1.0, seed=1, brk=0, skipc=0, p_min=0.0, n_min=0):

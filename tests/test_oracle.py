@@ -432,6 +432,55 @@ def test_generation_identical_to_reference_engine(pkg, request, tmp_path, name, 
     assert rng == r["rng"]
 
 
+DSPARK_CASES = [("ds_echo", 64, 4, 0.0, 1.0, 0.0, 0, 0), ("ds_echo", 64, 6, 0.0, 1.0, 0.0, 0, 1),
+                ("ds_echo", 64, 3, 0.8, 0.95, 0.0, 0, 0), ("ds_echo", 64, 4, 0.0, 1.0, 0.025, 2, 0),
+                ("ds_echo", 64, 4, 0.7, 1.0, 0.05, 2, 0), ("ds_micro", 512, 4, 0.8, 0.95, 0.0, 0, 0),
+                ("ds_tiny", 8192, 3, 0.0, 1.0, 0.0, 0, 0), ("ds_subln", 512, 2, 0.8, 0.95, 0.0, 0, 0)]
+
+
+@pytest.mark.parametrize("name,V,k,temp,topp,p_min,n_min,brk", DSPARK_CASES)
+def test_dspark_generation_identical_to_reference_engine(pkg, request, tmp_path, name, V, k, temp, topp, p_min,
+                                                         n_min, brk):
+    """DSpark heads (mtp_n_draft > 1) through lz_spec_round_dspark and
+    lz_spec_round_dspark_temp: tokens, k_eff, n_accept and the RNG state
+    against the reference engine, greedy and at temperature, with p_min /
+    n_min cuts and the broken rollback; the echo head accepts 0..k drafts."""
+    if not OL.have_reference():
+        pytest.skip("reference build absent; the DSpark golden fixtures cover this")
+    model = request.getfixturevalue(name)
+    prompt = pkg.prompt_tokens(31, 40, V)
+    kw = dict(p_min=p_min, n_min=n_min, brk=brk)
+    toks, ke, na, rng = gen_case(model, prompt, k, 48, temp, topp, seed=11, **kw)
+    extra = ("--pmin", repr(p_min), "--nmin", str(n_min)) + (("--break-rollback",) if brk else ())
+    r = OL.reference_generate(model, prompt, k, 48, temp, topp, seed=11, tmpdir=str(tmp_path), extra=extra)
+    n = min(len(toks), len(r["tokens"]))
+    assert n >= 48 and np.array_equal(toks[:n], r["tokens"][:n])
+    assert np.array_equal(ke, r["k_eff"]) and np.array_equal(na, r["n_accept"]) and rng == r["rng"]
+    if name == "ds_echo" and temp == 0.0 and p_min == 0.0:
+        assert max(na) >= 2 and min(na) == 0           # partial and zero acceptance both occur
+
+
+def test_dspark_draft_batch_slots(pkg, ds_micro):
+    """Slot independence of lz_mtp_draft_batch: a batch of k slots equals
+    the first k rows of a batch of n_draft slots, slots 1.. read the mask
+    row whatever the anchor, and the batch leaves the chain unchanged."""
+    o = Oracle(ds_micro)
+    try:
+        prompt = pkg.prompt_tokens(4, 30, 512)
+        assert o.session_start(prompt) == 0
+        o.forward_capture(prompt[-1], 29)
+        ch = o.chain()
+        full = o.draft_batch(17, o.n_draft)
+        assert np.array_equal(bits(o.chain()), bits(ch))
+        for k in range(1, o.n_draft):
+            assert np.array_equal(bits(o.draft_batch(17, k)), bits(full[:k]))
+        other = o.draft_batch(300, o.n_draft)
+        assert not np.array_equal(bits(other[0]), bits(full[0]))
+        assert o.draft_batch(17, o.n_draft + 1) is None and o.draft_step(17, 30) is None
+    finally:
+        o.close()
+
+
 def test_rollback_knob_changes_output(pkg, tiny, tmp_path):
     """debug_break_rollback must change a greedy run with rejections (so the
     ring rollback is exercised), in the oracle and in the reference alike."""
@@ -617,7 +666,8 @@ def test_load_config_reads_the_header(pkg, model_root, micro):
 def _greedy_rounds_oracle(model, prompt, k, n_rounds):
     """The harness's greedy loop (oracle/ref_harness.c cmd_gen) driven round
     by round on the oracle: the capture logits, then each round's verify
-    logits, verify hidden rows and last draft logits."""
+    logits, verify hidden rows and last draft logits (a DSpark head: every
+    slot's logits of the round's draft batch)."""
     o = Oracle(model)
     out = {}
     try:
@@ -628,11 +678,17 @@ def _greedy_rounds_oracle(model, prompt, k, n_rounds):
         anchor, anchor_pos = int(np.argmax(lg)), n - 1
         L = OL.lib()
         for r in range(n_rounds):
-            rc, toks, na, npos, ke = o.spec_round(anchor, anchor_pos, k)
+            if o.n_draft > 1:
+                rc, toks, na, npos, ke = o.spec_round_dspark(anchor, anchor_pos, k)
+            else:
+                rc, toks, na, npos, ke = o.spec_round(anchor, anchor_pos, k)
             assert rc > 0
             out[f"verify{r}"] = np.ctypeslib.as_array(L.ora_mtp_logits(o.s), shape=(8, o.V))[:ke + 1].copy()
             out[f"vhidden{r}"] = np.ctypeslib.as_array(L.ora_mtp_hidden(o.s), shape=(8, o.d))[:ke + 1].copy()
-            out[f"draft{r}"] = np.ctypeslib.as_array(L.ora_draft_logits(o.s), shape=(o.V,)).copy()
+            if o.n_draft > 1:
+                out[f"draft{r}"] = o.kdraft_logits(k)
+            else:
+                out[f"draft{r}"] = np.ctypeslib.as_array(L.ora_draft_logits(o.s), shape=(o.V,)).copy()
             anchor, anchor_pos = int(toks[na]), npos
     finally:
         o.close()
@@ -641,7 +697,9 @@ def _greedy_rounds_oracle(model, prompt, k, n_rounds):
 
 @pytest.mark.parametrize("name,vocab,k", [("micro", 512, 3), ("echo", 64, 3), ("tiny", 8192, 2),
                                           ("micro_subln", 512, 3), ("subln", 8192, 3), ("subln", 8192, 1),
-                                          ("fmt13", 512, 3), ("fmt14", 8192, 2)])
+                                          ("fmt13", 512, 3), ("fmt14", 8192, 2), ("fmt18", 512, 4),
+                                          ("fmt19", 64, 6), ("fmt19", 64, 2), ("fmt20", 8192, 3),
+                                          ("fmt21", 512, 3)])
 def test_rounds_bitwise_vs_reference(pkg, request, model_root, tmp_path, name, vocab, k):
     """The capture, every round's verify logits and hidden rows and the last
     draft step's logits equal the reference engine's bit for bit, round
@@ -651,7 +709,10 @@ def test_rounds_bitwise_vs_reference(pkg, request, model_root, tmp_path, name, v
     from rolled-back and caught-up state.  subln / micro_subln have
     use_subn = 1: per-projection input norms, no pre-layer norms, the
     block-Hadamard quantization of the KDA o_proj and MTP down_proj inputs,
-    per-token scales on the MTP FFN gate/up inputs."""
+    per-token scales on the MTP FFN gate/up inputs.  fmt18-21 carry DSpark
+    heads (configs 18-21: micro, echo, tiny v7 with groups of 64 and BF16,
+    micro-subln): lz_spec_round_dspark's draft batch, verify and acceptance;
+    the echo one accepts 0 to k drafts."""
     if not OL.have_reference():
         pytest.skip("reference build absent; the SubLN golden fixtures cover this")
     if name.startswith("fmt"):
