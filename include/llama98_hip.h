@@ -61,6 +61,8 @@ typedef struct {
     float rms_norm_eps, rope_theta;
     int layer_types[128];
     int use_subn, hadamard_o, hadamard_down;   /* SubLN (src/model.h: use_subn, hadamard_o/_down) */
+    int mtp_n_draft, mtp_markov_rank;          /* DSpark (src/model.h:359-375): > 1 draft slots; a
+                                                  model.bin carries no Markov rank (0) */
 } LZModelConfig;
 
 /* Caller-allocated, as in the reference: LZModel m; lz_open(&m, dir, ...). */
@@ -82,6 +84,8 @@ typedef struct {
     float *mtp_verify_hidden;      /* (L98_SPEC_K_GPU+1) x hidden: lz_forward_verify */
     float *mtp_chain;              /* hidden: after capture / draft / round */
     float *mtp_draft_logits;       /* vocab: lz_mtp_draft_step */
+    float *mtp_kdraft_logits;      /* LZ_SPEC_K_MAX x vocab: lz_mtp_draft_batch (DSpark models; NULL
+                                      otherwise, src/forward.h:866) */
     long long bytes_device;
     void *impl;
 } LZRunState;
@@ -148,9 +152,20 @@ float *lz_forward_batch_capture(const LZModel *m, LZRunState *s, const int *toke
  * into s->mtp_logits and hidden into s->mtp_verify_hidden; advances the ring
  * by n.  Returns 0, or 1 on failure. */
 int lz_forward_verify(const LZModel *m, LZRunState *s, const int *tokens, int n, int pos0);
-/* One MTP draft step; returns s->mtp_draft_logits, or NULL. */
+/* One MTP draft step; returns s->mtp_draft_logits, or NULL (also on a
+ * DSpark head, which binds no fc). */
 float *lz_mtp_draft_step(const LZModel *m, LZRunState *s, int next_token, int pos);
-/* MTP KV rows from (hidden, next token) pairs.  Returns 0, or 1. */
+/* DSpark (mtp_n_draft > 1): lz_mtp_draft_batch (src/forward.h:2033, body
+ * src/forward_mtp.c:385-505): k <= mtp_n_draft independent slots from
+ * s->mtp_chain, slot 0 fed next_token, the rest the mask row; their base
+ * logits into s->mtp_kdraft_logits (returned), or NULL.  The chain is not
+ * changed.  lz_mtp_markov_correct (src/forward.h:2046, body
+ * src/forward_mtp.c:510-531) adds markov_proj(markov_embed[x_prev]) to
+ * logits in place: the rank of a model.bin head is 0, so it adds zeros. */
+float *lz_mtp_draft_batch(const LZModel *m, LZRunState *s, int next_token, int k);
+void lz_mtp_markov_correct(const LZModel *m, LZRunState *s, int x_prev, float *logits);
+/* MTP KV rows from (hidden, next token) pairs.  Returns 0, or 1 (also on a
+ * DSpark head). */
 int lz_mtp_prefill(const LZModel *m, LZRunState *s, const float *h_body_all,
                    const int *next_tokens, int n, int pos0);
 int lz_mtp_catchup(const LZModel *m, LZRunState *s, const float *h_body_all,
@@ -171,6 +186,20 @@ int lz_spec_round_temp(const LZModel *m, LZRunState *s, int anchor, int anchor_p
                        float p_min, int n_min, LZSampler *samp, int debug_break_rollback,
                        int debug_skip_catchup, int *out, int *out_n_accept, int *out_new_pos,
                        int *out_k_eff, char *errbuf, int errlen);
+/* DSpark rounds (src/llama_zh.h:629-660; src/generate.c:1000-1133 and
+ * 1382-1505): one draft batch, each slot corrected and argmax'd (greedy) or
+ * sampled (temperature) in order with the p_min cut, the verify,
+ * acceptance, ring rollback and the chain reseed; no catch-up and no
+ * mtp_pos advance.  k <= mtp_n_draft.  lz_spec_round / lz_spec_round_temp
+ * refuse a DSpark head, these refuse a one-slot head. */
+int lz_spec_round_dspark(const LZModel *m, LZRunState *s, int anchor, int anchor_pos, int k,
+                         float p_min, int n_min, const LZSampler *samp, int debug_break_rollback,
+                         int *out, int *out_n_accept, int *out_new_pos, int *out_k_eff,
+                         char *errbuf, int errlen);
+int lz_spec_round_dspark_temp(const LZModel *m, LZRunState *s, int anchor, int anchor_pos, int k,
+                              float p_min, int n_min, LZSampler *samp, int debug_break_rollback,
+                              int *out, int *out_n_accept, int *out_new_pos, int *out_k_eff,
+                              char *errbuf, int errlen);
 
 /* ---- sampler (src/sampler.h:200-230) ---- */
 void lz_sample_defaults(LZSampleParams *p);

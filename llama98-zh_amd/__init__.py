@@ -36,7 +36,8 @@ class LZModelConfig(C.Structure):
         "kda_gate_rank", "num_experts", "num_experts_per_token", "moe_latent_dim",
         "moe_intermediate_size", "moe_shared_width", "mtp_intermediate_size", "mtp_n_layers")] + [
         ("rms_norm_eps", C.c_float), ("rope_theta", C.c_float), ("layer_types", C.c_int * 128),
-        ("use_subn", C.c_int), ("hadamard_o", C.c_int), ("hadamard_down", C.c_int)]
+        ("use_subn", C.c_int), ("hadamard_o", C.c_int), ("hadamard_down", C.c_int),
+        ("mtp_n_draft", C.c_int), ("mtp_markov_rank", C.c_int)]
 
 
 class LZModel(C.Structure):
@@ -48,7 +49,7 @@ class LZRunState(C.Structure):
                 ("mtp_pos", C.c_int), ("nt_cap", C.c_int),
                 ("logits", C.POINTER(C.c_float)), ("mtp_logits", C.POINTER(C.c_float)),
                 ("mtp_verify_hidden", C.POINTER(C.c_float)), ("mtp_chain", C.POINTER(C.c_float)),
-                ("mtp_draft_logits", C.POINTER(C.c_float)),
+                ("mtp_draft_logits", C.POINTER(C.c_float)), ("mtp_kdraft_logits", C.POINTER(C.c_float)),
                 ("bytes_device", C.c_longlong), ("impl", C.c_void_p)]
 
 
@@ -93,6 +94,8 @@ HIP_API = [
     ("lz_forward_verify", C.c_int, [C.POINTER(LZModel), C.POINTER(LZRunState), _IP, C.c_int, C.c_int]),
     ("lz_mtp_draft_step", _FP, [C.POINTER(LZModel), C.POINTER(LZRunState), C.c_int, C.c_int]),
     ("lz_mtp_prefill", C.c_int, [C.POINTER(LZModel), C.POINTER(LZRunState), _FP, _IP, C.c_int, C.c_int]),
+    ("lz_mtp_draft_batch", _FP, [C.POINTER(LZModel), C.POINTER(LZRunState), C.c_int, C.c_int]),
+    ("lz_mtp_markov_correct", None, [C.POINTER(LZModel), C.POINTER(LZRunState), C.c_int, _FP]),
     ("lz_mtp_catchup", C.c_int, [C.POINTER(LZModel), C.POINTER(LZRunState), _FP, _IP, C.c_int, C.c_int]),
     ("lz_spec_accept", C.c_int, [_IP, _IP, C.c_int, C.c_int, _IP]),
     ("lz_spec_accept_temp", C.c_int, [_FP, _FP, C.c_int, C.c_int, C.c_float, C.POINTER(C.c_uint64), _IP]),
@@ -104,6 +107,12 @@ HIP_API = [
     ("lz_spec_round_temp", C.c_int, [C.POINTER(LZModel), C.POINTER(LZRunState), C.c_int, C.c_int, C.c_int,
                                      C.c_float, C.c_int, C.POINTER(LZSampler), C.c_int, C.c_int, _IP, _IP, _IP,
                                      _IP, C.c_char_p, C.c_int]),
+    ("lz_spec_round_dspark", C.c_int, [C.POINTER(LZModel), C.POINTER(LZRunState), C.c_int, C.c_int, C.c_int,
+                                       C.c_float, C.c_int, C.POINTER(LZSampler), C.c_int, _IP, _IP, _IP, _IP,
+                                       C.c_char_p, C.c_int]),
+    ("lz_spec_round_dspark_temp", C.c_int, [C.POINTER(LZModel), C.POINTER(LZRunState), C.c_int, C.c_int,
+                                            C.c_int, C.c_float, C.c_int, C.POINTER(LZSampler), C.c_int, _IP, _IP,
+                                            _IP, _IP, C.c_char_p, C.c_int]),
     ("lz_sample_defaults", None, [C.POINTER(LZSampleParams)]),
     ("lz_sampler_init", C.c_int, [C.POINTER(LZSampler), C.c_int, C.POINTER(LZSampleParams), C.c_uint64]),
     ("lz_sampler_free", None, [C.POINTER(LZSampler)]),
@@ -307,14 +316,30 @@ class Engine:
         nt = np.ascontiguousarray(next_tokens, np.int32)
         return self.lib.lz_mtp_prefill(C.byref(self.m), C.byref(self.s), _fp(h), _ip(nt), len(nt), int(pos0))
 
+    @property
+    def dspark(self):
+        return self.m.config.mtp_n_draft > 1
+
     def spec_round(self, anchor, anchor_pos, k, p_min=0.0, n_min=0, brk=0, skipc=0):
+        """lz_spec_round, or lz_spec_round_dspark on a DSpark head (the
+        driver's dispatch, src/generate.c:1929-1946)."""
         out = np.zeros(L98_SPEC_K_GPU + 1, np.int32)
         na, npos, ke = C.c_int(), C.c_int(), C.c_int()
         err = C.create_string_buffer(256)
-        r = self.lib.lz_spec_round(C.byref(self.m), C.byref(self.s), int(anchor), int(anchor_pos), int(k),
-                                   float(p_min), int(n_min), None, brk, skipc, _ip(out), C.byref(na),
-                                   C.byref(npos), C.byref(ke), err, 256)
+        if self.dspark:
+            r = self.lib.lz_spec_round_dspark(C.byref(self.m), C.byref(self.s), int(anchor), int(anchor_pos),
+                                              int(k), float(p_min), int(n_min), None, brk, _ip(out), C.byref(na),
+                                              C.byref(npos), C.byref(ke), err, 256)
+        else:
+            r = self.lib.lz_spec_round(C.byref(self.m), C.byref(self.s), int(anchor), int(anchor_pos), int(k),
+                                       float(p_min), int(n_min), None, brk, skipc, _ip(out), C.byref(na),
+                                       C.byref(npos), C.byref(ke), err, 256)
         return r, out, na.value, npos.value, ke.value
+
+    def draft_batch(self, token, k):
+        """lz_mtp_draft_batch: the k DSpark slots' logits, [k][V]."""
+        p = self.lib.lz_mtp_draft_batch(C.byref(self.m), C.byref(self.s), int(token), int(k))
+        return None if not p else np.ctypeslib.as_array(p, shape=(k, self.V)).copy()
 
     def session_start(self, prompt):
         prompt = np.ascontiguousarray(prompt, np.int32)
@@ -411,15 +436,19 @@ class Engine:
         reference harness's --dump-rounds writes: "capture<r>" logits of each
         capture and, after each round r that emitted, "verify<r>" and
         "vhidden<r>" (the state's mtp_logits / mtp_verify_hidden rows) and
-        "draft<r>" (mtp_draft_logits).  Returns (tokens, k_eff per round,
-        n_accept per round)."""
+        "draft<r>" (mtp_draft_logits; a DSpark head's k slot rows,
+        mtp_kdraft_logits).  A DSpark head's session is the body prefill
+        alone (it has no fc for lz_mtp_prefill) and its rounds are
+        lz_spec_round_dspark.  Returns (tokens, k_eff per round, n_accept
+        per round)."""
         prompt = np.ascontiguousarray(prompt, np.int32)
         n_prompt = len(prompt)
         self.reset()
         h = self.batch_capture(prompt[:-1], 0)
-        if h is None or self.mtp_prefill(h, prompt[1:], self.s.mtp_pos) != 0:
+        if h is None or (not self.dspark and self.mtp_prefill(h, prompt[1:], self.s.mtp_pos) != 0):
             raise RuntimeError("prefill failed")
-        self.s.mtp_pos = n_prompt - 1
+        if not self.dspark:
+            self.s.mtp_pos = n_prompt - 1
         toks, ke, na = [], [], []
         token, pos, have_seed = int(prompt[-1]), n_prompt - 1, False
         while len(toks) < n_new:
@@ -444,7 +473,10 @@ class Engine:
                 on_round(f"verify{rnd}", np.ctypeslib.as_array(self.s.mtp_logits, shape=(k_eff + 1, self.V)).copy())
                 on_round(f"vhidden{rnd}",
                          np.ctypeslib.as_array(self.s.mtp_verify_hidden, shape=(k_eff + 1, self.d)).copy())
-                on_round(f"draft{rnd}", np.ctypeslib.as_array(self.s.mtp_draft_logits, shape=(self.V,)).copy())
+                if self.dspark:
+                    on_round(f"draft{rnd}", np.ctypeslib.as_array(self.s.mtp_kdraft_logits, shape=(k, self.V)).copy())
+                else:
+                    on_round(f"draft{rnd}", np.ctypeslib.as_array(self.s.mtp_draft_logits, shape=(self.V,)).copy())
             ke.append(k_eff)
             na.append(n_acc if r > 0 else -1)
             have_seed = r > 0

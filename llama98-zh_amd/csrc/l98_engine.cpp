@@ -140,6 +140,11 @@ struct DModel {
     DLayer mtp;
     DMat mtp_gate, mtp_up, mtp_down, mtp_fc;
     float *mtp_norm = nullptr, *mtp_pre_h = nullptr, *mtp_pre_e = nullptr;
+    // a DSpark head (mtp_n_draft > 1) in place of fc: main_proj [d][3d],
+    // depth_embed rows [n_draft][d] and mask_embed [d] as f32
+    int n_draft = 1;
+    DMat mtp_main;
+    float *mtp_depth = nullptr, *mtp_mask = nullptr;
     float *rope_cs = nullptr;
     int lin_index[128], full_index[128];
     struct DWide *wide = nullptr;       // scratch of the many-row forwards (first use)
@@ -263,6 +268,26 @@ HostTensor rd_f32(Bin &b, int n) {
     return t;
 }
 
+// A table read as lz_t_row_f32 reads its rows (src/ops_epi.c:1260-1290): a
+// Q8_0 row is its codes times their group's scale, an F32 / BF16 row its
+// values; rows * cols f32 in `own`.
+HostTensor rd_rows_f32(Bin &b, int rows, int cols, int layout) {
+    HostTensor t;
+    if (b.off < b.n && b.p[b.off] == 1) {
+        HostTensor q = rd_q8(b, rows, cols, layout);
+        if (b.bad) return t;
+        t.own = std::make_shared<std::vector<float>>((size_t)rows * cols);
+        for (size_t i = 0; i < (size_t)rows * cols; i++) (*t.own)[i] = (float)q.q[i] * q.s[i / (size_t)q.gs];
+    } else {
+        HostTensor f = rd_f32(b, rows * cols);
+        if (b.bad) return t;
+        t.own = std::make_shared<std::vector<float>>(f.s, f.s + (size_t)rows * cols);
+    }
+    t.s = t.own->data();
+    t.rows = 1; t.cols = rows * cols;
+    return t;
+}
+
 void *arena_take(DModel *m, size_t bytes) {
     size_t a = (m->arena_used + 255) & ~(size_t)255;
     if (a + bytes > m->arena_size) return nullptr;
@@ -329,6 +354,7 @@ struct HostLayer {
     std::vector<HostTensor> w1, w2, w3;
     HostTensor sn_q, sn_k, sn_v, sn_o, kn_q, kn_k, kn_v, kn_g, kn_o;
     HostTensor mn_gate, mn_down, mn_up, mn_sg, mn_su, mn_sd, fn_gate, fn_up, fn_down;
+    HostTensor ds_main, ds_depth, ds_mask;     // the MTP holder's DSpark tensors
 };
 
 // Parses the version-5 model.bin (reference loader order: header
@@ -364,11 +390,14 @@ int parse_model(Bin &b, LZModelConfig &c, HostTensor &embed, HostTensor &fnorm,
     // their "off" defaults, the hadamard blocks -1 = derived); v5 carries the
     // rest of the tail and the 522 appended words; v6 the application table,
     // mtp_n_draft, the rotated-vocabulary words and the scale layout; v7, v8,
-    // v9 one word each.  This path takes the identity schedule, at most one
-    // draft slot, no rotated vocabulary, and none of the v7-v9 mechanisms.
+    // v9 one word each.  This path takes the identity schedule, no rotated
+    // vocabulary and none of the v7-v9 mechanisms; mtp_n_draft > 1 (at most
+    // LZ_SPEC_K_MAX, alloc_mtp src/model.c:2905-2909) is a DSpark head.
     int rope_type = 0, mla_q = 0, mla_o = 0, kv_share = 0, sink = 0, gr = 0, ced_split = 0, ced_kv = 0;
     bool csa2 = false;
     c.mtp_n_layers = 0;
+    c.mtp_n_draft = 1;
+    c.mtp_markov_rank = 0;          // config.json only (src/model.c:539); a model.bin has none
     c.hadamard_o = c.hadamard_down = -1;
     if (ver >= 5) {
         c.mtp_n_layers = b.i32(); c.mtp_intermediate_size = b.i32();
@@ -388,7 +417,9 @@ int parse_model(Bin &b, LZModelConfig &c, HostTensor &embed, HostTensor &fnorm,
         schedule_ok = b.i32() == c.n_layers;                                      // exec_len
         for (int i = 0; i < 128; i++) schedule_ok &= b.i32() == (i < c.n_layers ? i : 0);   // app_layer
         for (int i = 0; i < 128; i++) schedule_ok &= b.i32() == 0;               // app_loop
-        draft_ok = b.i32() <= 1;                                                 // mtp_n_draft
+        c.mtp_n_draft = b.i32();                                                 // mtp_n_draft
+        if (c.mtp_n_draft < 1) c.mtp_n_draft = 1;
+        draft_ok = c.mtp_n_draft <= LZ_SPEC_K_MAX;
         rot_ok = b.i32() == 0;                                                   // embed_hadamard
         (void)b.i32();                                                           // embed_signs_seed
         layout_out = b.i32();                                                    // scale_layout
@@ -397,6 +428,7 @@ int parse_model(Bin &b, LZModelConfig &c, HostTensor &embed, HostTensor &fnorm,
         if (ver >= 9) (void)b.i32();                                             // loop_input_mix_from
     }
     if (b.bad) { set_err(err, errlen, "truncated header"); return LZ_ERR_BIN_OPEN; }
+    if (c.mtp_n_draft > 1 && c.mtp_n_layers != 1) draft_ok = false;
     if (!schedule_ok || !draft_ok || !rot_ok || !mix_ok || layout_out < 0 || layout_out > 2 || mla_q || mla_o ||
         kv_share || sink || gr || ced_split || ced_kv || csa2) {
         set_err(err, errlen, "model.bin v%d: a mechanism outside the implemented spec path "
@@ -436,7 +468,8 @@ int parse_model(Bin &b, LZModelConfig &c, HostTensor &embed, HostTensor &fnorm,
                         c.moe_latent_dim > 2048)) ||
         rope_type != 0 || c.mtp_n_layers > 1 || c.mtp_n_layers < 0 || c.num_experts > MAX_EXPERTS ||
         c.num_experts_per_token > MAX_TOPK || c.lin_n_k_heads != c.lin_n_v_heads ||
-        c.rotary_dim != c.head_dim || c.hidden_size % 32 || c.n_layers > 128) {
+        c.rotary_dim != c.head_dim || c.hidden_size % 32 || c.n_layers > 128 ||
+        (c.mtp_n_draft > 1 && (3 * c.hidden_size > 4096 || c.attn_kv_dim > 2048))) {
         set_err(err, errlen, "model variant outside the implemented spec path");
         return LZ_ERR_BIN_VERSION;
     }
@@ -524,10 +557,22 @@ int parse_model(Bin &b, LZModelConfig &c, HostTensor &embed, HostTensor &fnorm,
     mu = rd_q8(b, c.mtp_intermediate_size, d, layout_out);
     md = rd_q8(b, d, c.mtp_intermediate_size, layout_out);
     if (c.use_subn) mtp.fn_down = rd_f32(b, c.mtp_intermediate_size);
-    fc = rd_q8(b, d, 2 * d, layout_out);
+    // MTP_SPECS (src/model.c:2529-2552): fc for one draft slot; a DSpark
+    // head's main_proj, depth_embed, mask_embed and the two Markov tensors
+    // after the three norms.  A model.bin names no Markov rank, so those
+    // are [vocab][0]: empty.
+    const bool dspark = c.mtp_n_draft > 1;
+    if (!dspark) fc = rd_q8(b, d, 2 * d, layout_out);
     mn = rd_f32(b, d);
     mph = rd_f32(b, d);
     mpe = rd_f32(b, d);
+    if (dspark) {
+        mtp.ds_main = rd_q8(b, d, 3 * d, layout_out);
+        mtp.ds_depth = rd_rows_f32(b, c.mtp_n_draft, d, layout_out);
+        mtp.ds_mask = rd_f32(b, d);
+        (void)rd_f32(b, 0);                 // markov_embed
+        (void)rd_f32(b, 0);                 // markov_proj
+    }
     if (b.bad || b.off != b.n) { set_err(err, errlen, "model.bin layout mismatch"); return LZ_ERR_BIN_OPEN; }
     return 0;
 }
@@ -591,7 +636,14 @@ void upload_all(Uploader &u, DModel *m, const HostTensor &embed, const HostTenso
         M.sn_q = u.vec(hm.sn_q); M.sn_k = u.vec(hm.sn_k); M.sn_v = u.vec(hm.sn_v); M.sn_o = u.vec(hm.sn_o);
         M.fn_gate = u.vec(hm.fn_gate); M.fn_up = u.vec(hm.fn_up); M.fn_down = u.vec(hm.fn_down);
     }
-    m->mtp_gate = u.mat(mg); m->mtp_up = u.mat(mu); m->mtp_down = u.mat(md); m->mtp_fc = u.mat(fc);
+    m->mtp_gate = u.mat(mg); m->mtp_up = u.mat(mu); m->mtp_down = u.mat(md);
+    if (c.mtp_n_draft > 1) {
+        m->mtp_main = u.mat(hm.ds_main);
+        m->mtp_depth = u.vec(hm.ds_depth);
+        m->mtp_mask = u.vec(hm.ds_mask);
+    } else {
+        m->mtp_fc = u.mat(fc);
+    }
     m->mtp_norm = u.vec(mn); m->mtp_pre_h = u.vec(mph); m->mtp_pre_e = u.vec(mpe);
     }
     {
@@ -637,6 +689,7 @@ extern "C" int lz_open(LZModel *m, const char *dir, char *errbuf, int errlen) {
     int rc = parse_model(b, dm->c, embed, fnorm, HL, hm, mg, mu, md, fc, mn, mph, mpe, errbuf, errlen, ver, layout);
     dm->version = ver;
     dm->has_mtp = dm->c.mtp_n_layers > 0;
+    dm->n_draft = dm->c.mtp_n_draft;
     if (rc == 0 && ensure_tables() != 0) { set_err(errbuf, errlen, "HIP device not usable"); rc = 1; }
     if (rc == 0) {
         Uploader cnt{dm, true};
@@ -787,7 +840,7 @@ bool carve(DState *s) {
     int wide = d;
     int dims[] = {2 * d, c.attn_qgate_dim, c.lin_conv_dim, c.moe_shared_width, c.mtp_intermediate_size,
                   c.lin_n_v_heads * c.lin_k_head_dim, c.moe_intermediate_size, c.lin_value_dim,
-                  c.attn_q_dim, c.moe_latent_dim};
+                  c.attn_q_dim, c.moe_latent_dim, c.mtp_n_draft > 1 ? 3 * d : 0};
     for (int v : dims) wide = v > wide ? v : wide;
     const int pairs = B * c.num_experts_per_token;
     auto F = [&](size_t n) { return (float *)st_take(s, n * sizeof(float)); };
@@ -1128,6 +1181,41 @@ int forward_chunk(DState *s, const int *toks, int nt, const int *ctl_pos, int po
     return 0;
 }
 
+// The MTP block's dense FFN and head for nt rows: the attention output
+// s->blk is added to the residual rows s->mtp_x, then the FFN
+// (dense_ffn_step, src/forward_kda.c:1102-1240), the exit norm (its rows ->
+// chain_out when given) and the tied lm_head (logits rows -> out_logits).
+int mtp_ffn_head(DState *s, int nt, float *chain_out, float *out_logits) {
+    const DModel *m = s->m;
+    const LZModelConfig &c = m->c;
+    const int d = c.hidden_size, I = c.mtp_intermediate_size;
+    const float eps = c.rms_norm_eps;
+    float *mx = s->mtp_x2;
+    if (c.use_subn) {
+        // SubLN: the residual folds in place; gate / up normalize it with
+        // their own weights, one scale per row; the SwiGLU output takes
+        // down's own norm, then the block-Hadamard quantization
+        const float *fnw = m->mtp.fn_down;
+        const bool had = c.hadamard_down > 1;
+        mx = s->mtp_x;
+        CK(l98k_rmsnorm_ex(mx, d, s->blk, nullptr, m->mtp.fn_gate, d, eps, nt, nullptr, 0, s->xq, s->xqs, 1, s->st));
+        CK(l98k_rmsnorm_ex(mx, d, nullptr, nullptr, m->mtp.fn_up, d, eps, nt, nullptr, 0, s->xq3, s->xqs3, 1, s->st));
+        CK(gemv(s, {JX(m->mtp_gate, s->hb, I, s->xq, s->xqs), JX(m->mtp_up, s->hb2, I, s->xq3, s->xqs3)}, nt));
+        CK(l98k_wide_pro_f(1, s->hb, s->hb2, I, nullptr, nullptr, 0, I, nt, s->sub_a, s->st));
+        CK(l98k_rmsnorm_ex(s->sub_a, I, nullptr, nullptr, fnw, I, eps, nt, had ? s->sub_b : nullptr, I,
+                           had ? nullptr : s->xq, s->xqs, 0, s->st));
+        if (had) CK(l98k_subn_quant(s->sub_b, nt, I, c.hadamard_down, 32, s->xq, s->xqs, s->st));
+        CK(gemv(s, {JX(m->mtp_down, s->ffn_out, d, s->xq, s->xqs)}, nt));
+    } else {
+        const Prologue post = PN(s->mtp_x, d, s->blk, nullptr, m->mtp.post_norm, eps, s->mtp_x2, nullptr, 0);
+        CK(gemv(s, {J(m->mtp_gate, s->hb, I, post), J(m->mtp_up, s->hb2, I, post)}, nt));
+        CK(gemv(s, {J(m->mtp_down, s->ffn_out, d, PS(s->hb, s->hb2, I))}, nt));
+    }
+    CK(l98k_rmsnorm(mx, d, s->ffn_out, nullptr, m->mtp_norm, d, eps, nt, chain_out, d, s->xq, s->xqs, s->st));
+    CK(gemv(s, {JX(m->embed, out_logits, c.vocab_size, s->xq, s->xqs)}, nt));
+    return 0;
+}
+
 // lz_mtp_draft_step on device: input token at toks[0], position
 // *ctl_pos + pos_off; logits -> out_logits; argmax (lz_argmax_p1 order) ->
 // out_tok (device) when given.
@@ -1135,38 +1223,49 @@ int draft_step(DState *s, const int *toks, const int *ctl_pos, int pos_off, int 
                float *out_logits, int *out_tok) {
     const DModel *m = s->m;
     const LZModelConfig &c = m->c;
-    const int d = c.hidden_size, I = c.mtp_intermediate_size;
+    const int d = c.hidden_size;
     const float eps = c.rms_norm_eps;
     CK(l98k_mtp_pre(m->embed.q, m->embed.s, m->embed.gs, toks, s->chain, d, m->mtp_pre_e, m->mtp_pre_h, eps, 1, s->xq,
                     s->xqs, s->st));
     CK(gemv(s, {JX(m->mtp_fc, s->mtp_x, d, s->xq, s->xqs)}, 1));
     CK(attn_block(s, m->mtp, PN(s->mtp_x, d, nullptr, nullptr, m->mtp.in_norm, eps, nullptr, nullptr, 0),
                   s->planes - 1, ctl_pos, pos_off, 1, max_pos, false));
-    float *mx = s->mtp_x2;
-    if (c.use_subn) {
-        // dense FFN, SubLN (src/forward_kda.c:1102-1240): the residual folds
-        // in place; gate / up normalize it with their own weights, one scale
-        // per row; the SwiGLU output takes down's own norm, then the
-        // block-Hadamard quantization
-        const float *fnw = m->mtp.fn_down;
-        const bool had = c.hadamard_down > 1;
-        mx = s->mtp_x;
-        CK(l98k_rmsnorm_ex(mx, d, s->blk, nullptr, m->mtp.fn_gate, d, eps, 1, nullptr, 0, s->xq, s->xqs, 1, s->st));
-        CK(l98k_rmsnorm_ex(mx, d, nullptr, nullptr, m->mtp.fn_up, d, eps, 1, nullptr, 0, s->xq3, s->xqs3, 1, s->st));
-        CK(gemv(s, {JX(m->mtp_gate, s->hb, I, s->xq, s->xqs), JX(m->mtp_up, s->hb2, I, s->xq3, s->xqs3)}, 1));
-        CK(l98k_wide_pro_f(1, s->hb, s->hb2, I, nullptr, nullptr, 0, I, 1, s->sub_a, s->st));
-        CK(l98k_rmsnorm_ex(s->sub_a, I, nullptr, nullptr, fnw, I, eps, 1, had ? s->sub_b : nullptr, I,
-                           had ? nullptr : s->xq, s->xqs, 0, s->st));
-        if (had) CK(l98k_subn_quant(s->sub_b, 1, I, c.hadamard_down, 32, s->xq, s->xqs, s->st));
-        CK(gemv(s, {JX(m->mtp_down, s->ffn_out, d, s->xq, s->xqs)}, 1));
-    } else {
-        const Prologue post = PN(s->mtp_x, d, s->blk, nullptr, m->mtp.post_norm, eps, s->mtp_x2, nullptr, 0);
-        CK(gemv(s, {J(m->mtp_gate, s->hb, I, post), J(m->mtp_up, s->hb2, I, post)}, 1));
-        CK(gemv(s, {J(m->mtp_down, s->ffn_out, d, PS(s->hb, s->hb2, I))}, 1));
-    }
-    CK(l98k_rmsnorm(mx, d, s->ffn_out, nullptr, m->mtp_norm, d, eps, 1, s->chain, d, s->xq, s->xqs, s->st));
-    CK(gemv(s, {JX(m->embed, out_logits, c.vocab_size, s->xq, s->xqs)}, 1));
+    CK(mtp_ffn_head(s, 1, s->chain, out_logits));
     if (out_tok) CK(l98k_argmax(out_logits, c.vocab_size, 1, 1, out_tok, s->amax_part, s->amax_cnt, s->st));
+    return 0;
+}
+
+// lz_mtp_draft_batch on device (src/forward_mtp.c:385-505): the k DSpark
+// slots as k rows of one pass.  Row r's main_proj input is [norm(chain) |
+// norm(emb(toks[0]) for r = 0, else mask) | depth row r]; the MTP block
+// runs at position 0 with no history (mtp_attn_t1), then the FFN, exit norm
+// and lm_head.  logits rows -> out_logits; their lz_argmax_p1 indices ->
+// out_tok[0..k) when given.  The chain is read, not written.
+int dspark_draft(DState *s, const int *toks, int k, float *out_logits, int *out_tok) {
+    const DModel *m = s->m;
+    const LZModelConfig &c = m->c;
+    const int d = c.hidden_size;
+    const float eps = c.rms_norm_eps;
+    const DLayer &L = m->mtp;
+    const bool sub = c.use_subn != 0;
+    CK(l98k_dspark_pre(m->embed.q, m->embed.s, m->embed.gs, toks, s->chain, m->mtp_mask, m->mtp_depth, d,
+                       m->mtp_pre_e, m->mtp_pre_h, eps, k, s->xq, s->xqs, s->st));
+    CK(gemv(s, {JX(m->mtp_main, s->mtp_x, d, s->xq, s->xqs)}, k));
+    // q (its gate half is all the T=1 attention reads) and v, sharing the
+    // input norm, or SubLN's own norm each (src/forward_mtp.c:226-240)
+    const Prologue in = PN(s->mtp_x, d, nullptr, nullptr, L.in_norm, eps, nullptr, nullptr, 0);
+    CK(gemv(s, {J(L.q, s->qg, c.attn_qgate_dim, sub ? PW(in, L.sn_q) : in),
+                J(L.v, s->vp, c.attn_kv_dim, sub ? PW(in, L.sn_v) : in)}, k));
+    const size_t off = (size_t)(s->planes - 1) * s->seq_len * c.attn_kv_dim;      // the MTP plane, row 0
+    CK(l98k_attn_t1(s->qg, c.attn_qgate_dim, s->vp, c.attn_kv_dim, c.n_heads, c.n_kv_heads, c.head_dim,
+                    c.attn_q_dim, k, s->vq + off, s->vs + off / 32, sub ? s->sub_a : nullptr, s->xq2, s->xqs2,
+                    s->st));
+    if (sub)
+        CK(l98k_rmsnorm_ex(s->sub_a, c.attn_q_dim, nullptr, nullptr, L.sn_o, c.attn_q_dim, eps, k, nullptr, 0,
+                           s->xq2, s->xqs2, 0, s->st));
+    CK(gemv(s, {JX(L.o, s->blk, d, s->xq2, s->xqs2)}, k));
+    CK(mtp_ffn_head(s, k, nullptr, out_logits));
+    if (out_tok) CK(l98k_argmax(out_logits, c.vocab_size, k, 1, out_tok, s->amax_part, s->amax_cnt, s->st));
     return 0;
 }
 
@@ -1501,6 +1600,8 @@ extern "C" int lz_state_alloc(LZRunState *s, const LZModel *mm, int seq_len, int
     s->mtp_verify_hidden = (float *)calloc((size_t)(L98_SPEC_K_GPU + 1) * c.hidden_size, sizeof(float));
     s->mtp_chain = (float *)calloc((size_t)c.hidden_size, sizeof(float));
     s->mtp_draft_logits = (float *)calloc((size_t)c.vocab_size, sizeof(float));
+    s->mtp_kdraft_logits = c.mtp_n_draft > 1 ? (float *)calloc((size_t)LZ_SPEC_K_MAX * c.vocab_size, sizeof(float))
+                                             : nullptr;
     lz_state_reset(s, mm);
     return 0;
 }
@@ -1523,7 +1624,7 @@ extern "C" void lz_state_free(LZRunState *s) {
         delete d;
     }
     free(s->logits); free(s->mtp_logits); free(s->mtp_verify_hidden);
-    free(s->mtp_chain); free(s->mtp_draft_logits);
+    free(s->mtp_chain); free(s->mtp_draft_logits); free(s->mtp_kdraft_logits);
     memset(s, 0, sizeof(*s));
 }
 
@@ -1677,8 +1778,10 @@ extern "C" int lz_forward_verify(const LZModel *mm, LZRunState *s, const int *to
     return 0;
 }
 
+// A DSpark head (mtp_n_draft > 1) binds no mtp.fc (src/model.c:2531-2532):
+// lz_mtp_draft_step, lz_mtp_prefill and lz_mtp_catchup refuse it.
 extern "C" float *lz_mtp_draft_step(const LZModel *mm, LZRunState *s, int next_token, int pos) {
-    if (!mm || !s || !s->impl || !Mo(mm)->has_mtp) return nullptr;
+    if (!mm || !s || !s->impl || !Mo(mm)->has_mtp || Mo(mm)->n_draft > 1) return nullptr;
     DState *d = S(s);
     const LZModelConfig &c = d->m->c;
     if (next_token < 0 || next_token >= c.vocab_size || pos < 0 || pos >= d->seq_len) return nullptr;
@@ -1698,9 +1801,43 @@ extern "C" float *lz_mtp_draft_step(const LZModel *mm, LZRunState *s, int next_t
     return s->mtp_draft_logits;
 }
 
+// lz_mtp_draft_batch (src/forward_mtp.c:385-505): the k DSpark slots'
+// base logits from s->mtp_chain, into s->mtp_kdraft_logits.
+extern "C" float *lz_mtp_draft_batch(const LZModel *mm, LZRunState *s, int next_token, int k) {
+    if (!mm || !s || !s->impl || !Mo(mm)->has_mtp || Mo(mm)->n_draft <= 1 || !s->mtp_kdraft_logits) return nullptr;
+    DState *d = S(s);
+    const LZModelConfig &c = d->m->c;
+    if (next_token < 0 || next_token >= c.vocab_size || k <= 0 || k > c.mtp_n_draft) return nullptr;
+    if (!knobs_ok(c.num_experts_per_token, nullptr, 0)) return nullptr;
+    const timespec t0 = now_ts();
+    DevCtl h = ctl_from(s);
+    h.tok[0] = next_token;
+    if (ctl_put(d, h) || chain_put(d, s) || dspark_draft(d, d->ctl->tok, k, d->draft_logits, nullptr) ||
+        hipMemcpyAsync(s->mtp_kdraft_logits, d->draft_logits, sizeof(float) * (size_t)k * c.vocab_size,
+                       hipMemcpyDeviceToHost, d->st) ||
+        hipStreamSynchronize(d->st))
+        return nullptr;
+    lz_debug_us_draft += us_since(t0);
+    return s->mtp_kdraft_logits;
+}
+
+// lz_mtp_markov_correct (src/forward_mtp.c:510-531): logits +=
+// markov_proj(markov_embed[x_prev]).  A model.bin head's Markov rank is 0
+// (its two tensors are [vocab][0]), so the projection is a row of zeros and
+// the update adds +0 to each entry, as the reference's lz_matmul over no
+// inputs does.
+extern "C" void lz_mtp_markov_correct(const LZModel *mm, LZRunState *s, int x_prev, float *logits) {
+    (void)s;
+    if (!mm || !mm->impl || !Mo(mm)->has_mtp || Mo(mm)->n_draft <= 1 || !logits) return;
+    const LZModelConfig &c = Mo(mm)->c;
+    if (x_prev < 0 || x_prev >= c.vocab_size) return;
+    for (int v = 0; v < c.vocab_size; v++) logits[v] += 0.0f;
+}
+
 extern "C" int lz_mtp_prefill(const LZModel *mm, LZRunState *s, const float *h_body_all,
                               const int *next_tokens, int n, int pos0) {
-    if (!mm || !s || !s->impl || !h_body_all || !next_tokens || n < 1 || !Mo(mm)->has_mtp) return 1;
+    if (!mm || !s || !s->impl || !h_body_all || !next_tokens || n < 1 || !Mo(mm)->has_mtp || Mo(mm)->n_draft > 1)
+        return 1;
     DState *d = S(s);
     const LZModelConfig &c = d->m->c;
     if (!tok_ok(c, next_tokens, n) || pos0 < 0 || pos0 + n > d->seq_len || n > d->cap_rows) return 1;
@@ -1930,10 +2067,12 @@ namespace {
 // sequence is graph-capturable.
 int enqueue_verify_accept(DState *d, int k_eff, int max_pos, int brk, bool catchup, hipEvent_t mark = nullptr) {
     const LZModelConfig &c = d->m->c;
+    const bool dspark = d->m->n_draft > 1;     // no catch-up, mtp_pos kept (src/generate.c:1117-1133)
     CK(forward_chunk(d, d->ctl->tok, k_eff + 1, &d->ctl->anchor_pos, 1, max_pos, d->vhidden, true,
                      d->mtp_logits, false));
     CK(l98k_argmax(d->mtp_logits, c.vocab_size, k_eff + 1, 0, d->ctl->targ, d->amax_part, d->amax_cnt, d->st));
-    CK(l98k_accept(d->ctl, d->vhidden, c.hidden_size, d->chain, d->depth, brk, d->st));
+    CK(l98k_accept(d->ctl, d->vhidden, c.hidden_size, d->chain, d->depth, (brk ? 1 : 0) | (dspark ? 2 : 0), d->st));
+    if (dspark) catchup = false;
     if (mark) CK(hipEventRecord(mark, d->st));
     if (catchup && k_eff > 1)
         CK(mtp_prefill_dev(d, d->vhidden, d->ctl->catch_tok, k_eff - 1, &d->ctl->catch_pos, 0));
@@ -1943,6 +2082,10 @@ int enqueue_verify_accept(DState *d, int k_eff, int max_pos, int brk, bool catch
 
 int enqueue_greedy_round(DState *d, int k, int max_pos, int brk, bool catchup) {
     const LZModelConfig &c = d->m->c;
+    if (d->m->n_draft > 1) {      // lz_spec_round_dspark: one draft batch of k slots
+        CK(dspark_draft(d, d->ctl->tok, k, d->draft_logits, d->ctl->tok + 1));
+        return enqueue_verify_accept(d, k, max_pos, brk, false);
+    }
     for (int i = 0; i < k; i++)
         CK(draft_step(d, d->ctl->tok + i, &d->ctl->mtp_pos, i, max_pos, d->draft_logits + (size_t)i * c.vocab_size,
                       d->ctl->tok + 1 + i));
@@ -1963,6 +2106,8 @@ extern "C" int lz_spec_round(const LZModel *mm, LZRunState *s, int anchor, int a
     if (!mm || !s || !out || !out_n_accept || !out_new_pos || !out_k_eff || !s->impl)
         return errset(errbuf, errlen, LZ_ERR_NULL_ARG, "null argument");
     if (!Mo(mm)->has_mtp) return errset(errbuf, errlen, LZ_ERR_SPEC_NO_HEAD, "model has no MTP head");
+    if (Mo(mm)->n_draft > 1)
+        return errset(errbuf, errlen, LZ_ERR_FORWARD, "a DSpark head (mtp_n_draft > 1) runs lz_spec_round_dspark");
     if (k < 1 || k > LZ_SPEC_K_MAX || k > s->ssm_ring_depth - 1) {
         set_err(errbuf, errlen, "spec_k %d out of range 1..%d", k,
                 k > LZ_SPEC_K_MAX ? LZ_SPEC_K_MAX : s->ssm_ring_depth - 1);
@@ -2146,16 +2291,109 @@ int dev_sample_ex(DState *d, const float *row, int V, float temp, float topp, lz
 
 }  // namespace
 
+// lz_spec_round_dspark (greedy, penalties off), src/generate.c:1000-1133:
+// one draft batch of k slots, each slot's Markov correction (a zero row)
+// and lz_argmax_p1 in slot order with the p_min cut, the verify, acceptance,
+// ring rollback and the chain reseed.  No catch-up, mtp_pos unchanged.  With
+// p_min = 0 and n_min <= k the round stays on the device as one sequence.
+extern "C" int lz_spec_round_dspark(const LZModel *mm, LZRunState *s, int anchor, int anchor_pos, int k,
+                                    float p_min, int n_min, const LZSampler *samp, int brk, int *out,
+                                    int *out_n_accept, int *out_new_pos, int *out_k_eff, char *errbuf,
+                                    int errlen) {
+    if (!mm || !s || !out || !out_n_accept || !out_new_pos || !out_k_eff || !s->impl)
+        return errset(errbuf, errlen, LZ_ERR_NULL_ARG, "null argument");
+    if (!Mo(mm)->has_mtp) return errset(errbuf, errlen, LZ_ERR_SPEC_NO_HEAD, "model has no MTP head");
+    const int nd = Mo(mm)->n_draft;
+    if (k < 1 || k > LZ_SPEC_K_MAX || k > s->ssm_ring_depth - 1 || k > nd) {
+        const int lim = k > LZ_SPEC_K_MAX ? LZ_SPEC_K_MAX : k > s->ssm_ring_depth - 1 ? s->ssm_ring_depth - 1 : nd;
+        set_err(errbuf, errlen, "spec_k %d out of range 1..%d", k, lim);
+        return -LZ_ERR_SPEC_K_RANGE;
+    }
+    if (nd <= 1 || !s->mtp_kdraft_logits) return errset(errbuf, errlen, LZ_ERR_FORWARD, "not a DSpark head");
+    if (penalties_on(samp)) return errset(errbuf, errlen, LZ_ERR_NULL_ARG, "sampler penalties are not on this path");
+    DState *d = S(s);
+    const LZModelConfig &c = d->m->c;
+    const int V = c.vocab_size;
+    if (!knobs_ok(c.num_experts_per_token, errbuf, errlen)) return -LZ_ERR_FORWARD;
+    if (anchor < 0 || anchor >= V || anchor_pos + 1 + k >= d->seq_len)
+        return errset(errbuf, errlen, LZ_ERR_FORWARD, "forward failed (token/position out of range)");
+    const int max_pos = d->seq_len - 1;
+    DevCtl h = ctl_from(s);
+    h.anchor = anchor;
+    h.anchor_pos = anchor_pos;
+    h.tok[0] = anchor;
+    h.k_eff = k;
+    if (ctl_put(d, h) || chain_put(d, s) || hipEventRecord(d->ph[0], d->st)) return -LZ_ERR_FORWARD;
+    if (dspark_draft(d, d->ctl->tok, k, d->draft_logits, d->ctl->tok + 1)) return -LZ_ERR_FORWARD;
+    int k_eff = k;
+    if (p_min > 0.0f || k < n_min) {
+        // the cut needs each slot's top-1 probability (lz_argmax_p1's online
+        // softmax) on the host copy of the rows
+        if (hipMemcpyAsync(s->mtp_kdraft_logits, d->draft_logits, sizeof(float) * (size_t)k * V,
+                           hipMemcpyDeviceToHost, d->st) || hipStreamSynchronize(d->st))
+            return -LZ_ERR_FORWARD;
+        k_eff = 0;
+        int prev = anchor;
+        for (int i = 0; i < k; i++) {
+            float *row = s->mtp_kdraft_logits + (size_t)i * V, p1;
+            lz_mtp_markov_correct(mm, s, prev, row);
+            prev = lz_argmax_p1(row, V, &p1);
+            if (p1 < p_min) break;
+            k_eff = i + 1;
+        }
+        if (k_eff < n_min) {     // discard; the draft batch left the chain as it was
+            out[0] = anchor; *out_n_accept = 0; *out_new_pos = anchor_pos; *out_k_eff = k_eff;
+            return 0;
+        }
+        const int ke = k_eff;
+        if (hipMemcpyAsync(&d->ctl->k_eff, &ke, sizeof(int), hipMemcpyHostToDevice, d->st)) return -LZ_ERR_FORWARD;
+    }
+    if (hipEventRecord(d->ph[1], d->st) || enqueue_verify_accept(d, k_eff, max_pos, brk, false) ||
+        hipEventRecord(d->ph[2], d->st))
+        return -LZ_ERR_FORWARD;
+    if (hipMemcpyAsync(s->mtp_chain, d->chain, sizeof(float) * c.hidden_size, hipMemcpyDeviceToHost, d->st) ||
+        hipMemcpyAsync(s->mtp_logits, d->mtp_logits, sizeof(float) * (size_t)(k_eff + 1) * V,
+                       hipMemcpyDeviceToHost, d->st) ||
+        hipMemcpyAsync(s->mtp_verify_hidden, d->vhidden, sizeof(float) * (size_t)(k_eff + 1) * c.hidden_size,
+                       hipMemcpyDeviceToHost, d->st) ||
+        (p_min <= 0.0f && k >= n_min &&
+         hipMemcpyAsync(s->mtp_kdraft_logits, d->draft_logits, sizeof(float) * (size_t)k * V, hipMemcpyDeviceToHost,
+                        d->st)))
+        return -LZ_ERR_FORWARD;
+    if (ctl_get(d, &h)) return -LZ_ERR_FORWARD;
+    const int n_accept = h.n_accept;
+    for (int i = 0; i <= n_accept; i++) out[i] = h.out[i];
+    s->ssm_slot = h.ssm_slot;
+    *out_n_accept = n_accept;
+    *out_new_pos = anchor_pos + 1 + n_accept;
+    *out_k_eff = k_eff;
+    {
+        float ms[2] = {0, 0};
+        for (int i = 0; i < 2; i++) (void)hipEventElapsedTime(&ms[i], d->ph[i], d->ph[i + 1]);
+        lz_debug_us_draft += (long long)(ms[0] * 1000.0f);
+        lz_debug_us_verify += (long long)(ms[1] * 1000.0f);
+        lz_debug_n_chunks++;
+        lz_debug_n_lmhead++;
+        if (n_accept < k_eff) lz_debug_n_ring_rollback++;
+    }
+    return n_accept + 1;
+}
+
 namespace {
 // lz_spec_round_temp with the draft width bounded by k_cap: LZ_SPEC_K_MAX
 // for the reference entry point, L98_SPEC_K_GPU for this library's own
-// generation loop.
+// generation loop.  A DSpark head (mtp_n_draft > 1) takes
+// lz_spec_round_dspark_temp's form (src/generate.c:1382-1505): one draft
+// batch of k <= mtp_n_draft slots, each slot's corrected row sampled in
+// turn, no catch-up and no mtp_pos advance.
 int spec_round_temp(const LZModel *mm, LZRunState *s, int anchor, int anchor_pos, int k, float p_min, int n_min,
                     LZSampler *samp, int brk, int skipc, int *out, int *out_n_accept, int *out_new_pos,
                     int *out_k_eff, char *errbuf, int errlen, int k_cap) {
     if (!mm || !s || !samp || !out || !out_n_accept || !out_new_pos || !out_k_eff || !s->impl)
         return errset(errbuf, errlen, LZ_ERR_NULL_ARG, "null argument");
     if (!Mo(mm)->has_mtp) return errset(errbuf, errlen, LZ_ERR_SPEC_NO_HEAD, "model has no MTP head");
+    const bool ds = Mo(mm)->n_draft > 1;
+    if (ds && Mo(mm)->n_draft < k_cap) k_cap = Mo(mm)->n_draft;
     if (k < 1 || k > k_cap || k > s->ssm_ring_depth - 1) {
         set_err(errbuf, errlen, "spec_k %d out of range 1..%d", k, k > k_cap ? k_cap : s->ssm_ring_depth - 1);
         return -LZ_ERR_SPEC_K_RANGE;
@@ -2167,7 +2405,7 @@ int spec_round_temp(const LZModel *mm, LZRunState *s, int anchor, int anchor_pos
     const int V = c.vocab_size;
     if (!knobs_ok(c.num_experts_per_token, errbuf, errlen)) return -LZ_ERR_FORWARD;
     timespec t0 = now_ts();
-    if (anchor < 0 || anchor >= V || anchor_pos + 1 + k >= d->seq_len || s->mtp_pos + k > d->seq_len)
+    if (anchor < 0 || anchor >= V || anchor_pos + 1 + k >= d->seq_len || (!ds && s->mtp_pos + k > d->seq_len))
         return errset(errbuf, errlen, LZ_ERR_FORWARD, "forward failed (token/position out of range)");
     const float temp = samp->p.temperature, topp = samp->p.topp;
     DevCtl h = ctl_from(s);
@@ -2178,16 +2416,19 @@ int spec_round_temp(const LZModel *mm, LZRunState *s, int anchor, int anchor_pos
         return -LZ_ERR_FORWARD;
     int draft[L98_SPEC_K_GPU], k_eff = 0;
     const float inv = 1.0f / temp;
+    // the DSpark rows' Markov correction adds a zero row: nothing to apply
+    if (ds && dspark_draft(d, d->ctl->tok, k, d->draft_logits, nullptr)) return -LZ_ERR_FORWARD;
     for (int i = 0; i < k; i++) {
-        if (draft_step(d, d->ctl->tok + i, &d->ctl->mtp_pos, i, s->mtp_pos + k, d->draft_logits, nullptr))
+        if (!ds && draft_step(d, d->ctl->tok + i, &d->ctl->mtp_pos, i, s->mtp_pos + k, d->draft_logits, nullptr))
             return -LZ_ERR_FORWARD;
+        const float *row = d->draft_logits + (ds ? (size_t)i * V : 0);
         // lz_sample_temp_q (src/sampler.c:736-747): q = softmax(logits/T),
         // then the multinomial draw; the draw also becomes the next draft
         // step's input token
         float *qi = d->smp_q + (size_t)i * V;
         int idx = 0;
         float qidx = 0.0f;
-        if (l98k_smp_softmax(d->draft_logits, V, inv, qi, 0.0f, nullptr, nullptr, nullptr, d->st) ||
+        if (l98k_smp_softmax(row, V, inv, qi, 0.0f, nullptr, nullptr, nullptr, d->st) ||
             l98k_smp_draw(qi, V, d->smp_rng, d->smp_out, d->smp_outf, d->ctl->tok + 1 + i, d->st) ||
             hipMemcpyAsync(&idx, d->smp_out, sizeof(int), hipMemcpyDeviceToHost, d->st) ||
             hipMemcpyAsync(&qidx, d->smp_outf, sizeof(float), hipMemcpyDeviceToHost, d->st) ||
@@ -2246,6 +2487,12 @@ int spec_round_temp(const LZModel *mm, LZRunState *s, int anchor, int anchor_pos
     *out_n_accept = n_accept;
     *out_new_pos = anchor_pos + 1 + n_accept;
     *out_k_eff = k_eff;
+    if (ds) {
+        if (hipMemcpyAsync(s->mtp_chain, d->chain, sizeof(float) * c.hidden_size, hipMemcpyDeviceToHost, d->st) ||
+            hipStreamSynchronize(d->st))
+            return -LZ_ERR_FORWARD;
+        return n_accept + 1;
+    }
     if (n_accept > 1 && !skipc) {
         t0 = now_ts();
         DevCtl h2 = h;
@@ -2270,7 +2517,24 @@ extern "C" int lz_spec_round_temp(const LZModel *mm, LZRunState *s, int anchor, 
                                   float p_min, int n_min, LZSampler *samp, int brk, int skipc,
                                   int *out, int *out_n_accept, int *out_new_pos, int *out_k_eff,
                                   char *errbuf, int errlen) {
+    if (mm && mm->impl && Mo(mm)->n_draft > 1)
+        return errset(errbuf, errlen, LZ_ERR_FORWARD, "a DSpark head (mtp_n_draft > 1) runs lz_spec_round_dspark_temp");
     return spec_round_temp(mm, s, anchor, anchor_pos, k, p_min, n_min, samp, brk, skipc, out, out_n_accept,
+                           out_new_pos, out_k_eff, errbuf, errlen, LZ_SPEC_K_MAX);
+}
+
+// lz_spec_round_dspark_temp (penalties off), src/generate.c:1382-1505.
+extern "C" int lz_spec_round_dspark_temp(const LZModel *mm, LZRunState *s, int anchor, int anchor_pos, int k,
+                                         float p_min, int n_min, LZSampler *samp, int brk, int *out,
+                                         int *out_n_accept, int *out_new_pos, int *out_k_eff, char *errbuf,
+                                         int errlen) {
+    if (mm && mm->impl && Mo(mm)->has_mtp && Mo(mm)->n_draft <= 1)
+        return errset(errbuf, errlen, LZ_ERR_FORWARD, "not a DSpark head");
+    if (mm && mm->impl && Mo(mm)->n_draft > 1 && k > Mo(mm)->n_draft && k <= LZ_SPEC_K_MAX) {
+        set_err(errbuf, errlen, "spec_k %d out of range 1..%d", k, Mo(mm)->n_draft);
+        return -LZ_ERR_SPEC_K_RANGE;
+    }
+    return spec_round_temp(mm, s, anchor, anchor_pos, k, p_min, n_min, samp, brk, 1, out, out_n_accept,
                            out_new_pos, out_k_eff, errbuf, errlen, LZ_SPEC_K_MAX);
 }
 
@@ -2427,15 +2691,18 @@ extern "C" int l98_session_start(const LZModel *mm, LZRunState *s, const int *pr
     // prefill + MTP prefill (src/generate.c:2806-2960)
     lz_state_reset(s, mm);
     if (batch_capture_dev(d, s, prompt, n_prompt - 1, 0)) return -LZ_ERR_FORWARD;
-    {
+    // A DSpark head has no fc for the MTP prefill to project through, and
+    // none of its steps reads the MTP KV rows: its session is the body
+    // prefill alone (the driver's MTP-prefill skip, src/generate.c:2817-2830).
+    if (d->m->n_draft <= 1) {
         DevCtl h = ctl_from(s);
         h.pos_scratch = 0;
         if (ctl_put(d, h) ||
             hipMemcpyAsync(d->tokbuf, prompt + 1, sizeof(int) * (size_t)(n_prompt - 1), hipMemcpyHostToDevice, d->st) ||
             mtp_prefill_dev(d, d->hcap, d->tokbuf, n_prompt - 1, &d->ctl->pos_scratch, 0))
             return -LZ_ERR_FORWARD;
+        s->mtp_pos = n_prompt - 1;
     }
-    s->mtp_pos = n_prompt - 1;
     // first anchor from a capture forward
     float *lg = lz_forward_capture(mm, s, prompt[n_prompt - 1], n_prompt - 1);
     if (!lg) return -LZ_ERR_FORWARD;
@@ -2475,6 +2742,7 @@ extern "C" int l98_greedy_rounds_ex(const LZModel *mm, LZRunState *s, int k, int
     if (!mm || !s || !s->impl || n_rounds < 1) return -LZ_ERR_NULL_ARG;
     if (!Mo(mm)->has_mtp) return -LZ_ERR_SPEC_NO_HEAD;
     if (k < 1 || k > L98_SPEC_K_GPU || k > s->ssm_ring_depth - 1) return -LZ_ERR_SPEC_K_RANGE;
+    if (Mo(mm)->n_draft > 1 && k > Mo(mm)->n_draft) return -LZ_ERR_SPEC_K_RANGE;     // DSpark: k <= mtp_n_draft
     DState *d = S(s);
     if (n_rounds > d->hist_cap) return -LZ_ERR_NULL_ARG;
     const int max_pos = d->seq_len - 1;
@@ -2649,6 +2917,7 @@ extern "C" int l98_greedy_rounds_batch(const LZModel *mm, LZRunState **states, i
         LZRunState *s = states[i];
         DState *d = S(s);
         if (k < 1 || k > L98_SPEC_K_GPU || k > s->ssm_ring_depth - 1) return -LZ_ERR_SPEC_K_RANGE;
+        if (Mo(mm)->n_draft > 1 && k > Mo(mm)->n_draft) return -LZ_ERR_SPEC_K_RANGE;
         if (n_rounds > d->hist_cap) return -LZ_ERR_NULL_ARG;
         DevCtl h;
         if (ctl_get(d, &h)) return -LZ_ERR_FORWARD;
@@ -2710,6 +2979,7 @@ extern "C" int l98_generate(const LZModel *mm, LZRunState *s, const int *prompt,
                             int *n_accept_out, int *n_rounds) {
     if (!mm || !s || !s->impl || !prompt || n_prompt < 2 || !tokens) return -LZ_ERR_NULL_ARG;
     if (k < 1 || k > L98_SPEC_K_GPU || k > s->ssm_ring_depth - 1) return -LZ_ERR_SPEC_K_RANGE;
+    if (Mo(mm)->n_draft > 1 && k > Mo(mm)->n_draft) return -LZ_ERR_SPEC_K_RANGE;     // DSpark: k <= mtp_n_draft
     DState *d = S(s);
     if (n_prompt + n_new + 2 * (k + 1) >= d->seq_len) return -LZ_ERR_FORWARD;
     int anchor = l98_session_start(mm, s, prompt, n_prompt, samp);

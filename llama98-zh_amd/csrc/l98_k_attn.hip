@@ -506,10 +506,76 @@ __global__ __launch_bounds__(AV_THREADS) void k_attn_av_items(AttnArgs b, const 
     attn_av_body<CH>(a, att + (size_t)item * att_item, att_stride, sc, blockIdx.x, t);
 }
 
+// mtp_attn_t1 (src/forward_mtp.c:191-376, Q8 KV float arm): attention of
+// a DSpark slot at position 0 of the MTP plane with no history, one block
+// per slot row r.  The softmax over the single score is exactly 1, so K,
+// Q, RoPE and the scores never enter: V is quantized per 32 (the plane's
+// row 0 keeps the last slot's, as the reference's slots overwrite it in
+// turn), each output element is 0 + (1 * q) * scale (wsum_q8_row,
+// src/forward_attn.c:17-21, with weight 1), times sigmoid of its gate, then
+// the o_proj input: the float row (out, SubLN's own norm follows) or its
+// per-32 quantization (oq, oqs).
+__global__ __launch_bounds__(256) void k_attn_t1(const float *__restrict__ qg, int qg_dim,
+                                                 const float *__restrict__ vp, int kv_dim, int nh, int nkv, int hd,
+                                                 int q_dim, int rows, int8_t *__restrict__ vc0,
+                                                 float *__restrict__ vs0, float *__restrict__ out,
+                                                 int8_t *__restrict__ oq, float *__restrict__ oqs) {
+    EXP_TAB_LOAD(tab);
+    __shared__ int8_t s_vq[2048];
+    __shared__ float s_vs[64];
+    const int r = blockIdx.x, tid = threadIdx.x, kv_mul = nh / nkv;
+    const bool last = r == rows - 1;
+    for (int b = 0; b < kv_dim; b += 256) {
+        const int i = b + tid;
+        const float x = vp[(size_t)r * kv_dim + (i < kv_dim ? i : kv_dim - 1)];
+        int8_t q;
+        float sg = 0.0f;
+        d_quant_group32(x, &q, &sg);
+        if (i < kv_dim) {
+            s_vq[i] = q;
+            if (last) vc0[i] = q;
+            if ((i & 31) == 0) {
+                s_vs[i >> 5] = sg;
+                if (last) vs0[i >> 5] = sg;
+            }
+        }
+    }
+    EXP_TAB_PUT(tab);
+    __syncthreads();
+    for (int b = 0; b < q_dim; b += 256) {
+        const int j = b + tid, jc = j < q_dim ? j : q_dim - 1;
+        const int h = jc / hd, e = jc - h * hd, src = (h / kv_mul) * hd + e;
+        float o = 0.0f + (1.0f * (float)s_vq[src]) * s_vs[src >> 5];
+        o *= d_sigmoid(qg[(size_t)r * qg_dim + (size_t)h * 2 * hd + hd + e], tab);
+        if (out) {
+            if (j < q_dim) out[(size_t)r * q_dim + j] = o;
+            continue;
+        }
+        int8_t q;
+        float sg = 0.0f;
+        d_quant_group32(o, &q, &sg);
+        if (j < q_dim) {
+            oq[(size_t)r * q_dim + j] = q;
+            if ((j & 31) == 0) oqs[(size_t)r * (q_dim >> 5) + (j >> 5)] = sg;
+        }
+    }
+}
+
 // ---------------------------------------------------------- host glue ---
 
 extern "C" int l98k_upload_exp_table_attn(const float *tab) {
     return (int)hipMemcpyToSymbol(HIP_SYMBOL(c_exp_tab), tab, 32 * sizeof(float));
+}
+
+extern "C" int l98k_attn_t1(const float *qg, int qg_dim, const float *vp, int kv_dim, int nh, int nkv, int hd,
+                            int q_dim, int rows, int8_t *vc0, float *vs0, float *out, int8_t *oq, float *oqs,
+                            hipStream_t st) {
+    if (rows < 1 || kv_dim > 2048 || (kv_dim & 31) || (q_dim & 31) || (hd & 31) || nkv < 1 || nh % nkv ||
+        q_dim != nh * hd || kv_dim != nkv * hd || qg_dim != 2 * q_dim || (!out && (!oq || !oqs)))
+        return -1;
+    hipLaunchKernelGGL(k_attn_t1, dim3(rows), dim3(256), 0, st, qg, qg_dim, vp, kv_dim, nh, nkv, hd, q_dim, rows,
+                       vc0, vs0, out, oq, oqs);
+    return (int)hipGetLastError();
 }
 
 extern "C" int l98k_attn_prep(const AttnArgs *a, int nt, hipStream_t st) {

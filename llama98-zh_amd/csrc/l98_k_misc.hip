@@ -96,6 +96,52 @@ __global__ __launch_bounds__(64) void k_mtp_pre(const int8_t *__restrict__ emb_q
                  xqs + (size_t)r * (2 * d >> 5) + (size_t)half * (d >> 5));
 }
 
+// The DSpark draft batch's main_proj input (lz_mtp_draft_batch,
+// src/forward_mtp.c:404-439): row r (slot r) is [rmsnorm(chain, pre_h) |
+// rmsnorm(e_r, pre_e) | depth row r], e_0 the embedding row of the anchor
+// token, e_r (r > 0) the shared mask row, then its per-32 quantization.
+// blockIdx.y picks the third; d % 32 == 0, so the thirds quantize
+// independently.
+template <int PJ>
+__global__ __launch_bounds__(64) void k_dspark_pre(const int8_t *__restrict__ emb_q, const float *__restrict__ emb_s,
+                                                   const int *__restrict__ tok, const float *__restrict__ chain,
+                                                   const float *__restrict__ mask, const float *__restrict__ depth,
+                                                   int d, int gs, const float *__restrict__ w_e,
+                                                   const float *__restrict__ w_h, float eps,
+                                                   int8_t *__restrict__ xq, float *__restrict__ xqs) {
+    __shared__ __align__(16) float sq[ps_row_floats<4 * PJ>()];
+    __shared__ PsRec rec[128];
+    __shared__ float s_inv;
+    const int r = blockIdx.x, third = blockIdx.y, lane = threadIdx.x, nf = d >> 2;
+    float4 v[PJ], wn[PJ];
+    const float *src = third == 0 ? chain : third == 2 ? depth + (size_t)r * d : mask;
+    if (third == 1 && r == 0) {
+        const uint32_t *er = reinterpret_cast<const uint32_t *>(emb_q + (size_t)tok[0] * d);
+        const float *sr = emb_s + (size_t)tok[0] * (d / gs);
+#pragma unroll
+        for (int j = 0; j < PJ; j++) {
+            const int fe = imin(lane + 64 * j, nf - 1);
+            const uint32_t q = er[fe];
+            const float sc = sr[4 * fe / gs];
+            v[j] = make_float4((float)(int8_t)(q & 0xFF) * sc, (float)(int8_t)((q >> 8) & 0xFF) * sc,
+                               (float)(int8_t)((q >> 16) & 0xFF) * sc, (float)(int8_t)(q >> 24) * sc);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < PJ; j++) v[j] = reinterpret_cast<const float4 *>(src)[imin(lane + 64 * j, nf - 1)];
+    }
+    int8_t *q = xq + (size_t)r * 3 * d + (size_t)third * d;
+    float *qs = xqs + (size_t)r * (3 * d >> 5) + (size_t)third * (d >> 5);
+    if (third == 2) {
+        norm_row<PJ, false>(v, wn, d, eps, sq, rec, &s_inv, nullptr, q, qs);
+        return;
+    }
+    const float4 *wn4 = reinterpret_cast<const float4 *>(third == 0 ? w_h : w_e);
+#pragma unroll
+    for (int j = 0; j < PJ; j++) wn[j] = wn4[imin(lane + 64 * j, nf - 1)];
+    norm_row<PJ>(v, wn, d, eps, sq, rec, &s_inv, nullptr, q, qs);
+}
+
 // Index-order sums of non-negative rows (wave_sum_nonneg, the sum the
 // RMSNorm kernels use), one 64-lane block per row: the library's check of
 // that routine on arbitrary inputs.
@@ -189,8 +235,11 @@ __global__ __launch_bounds__(256) void k_argmax(const float *__restrict__ x, int
 // the device-side bookkeeping of lz_spec_round (src/generate.c:802-993):
 // ring rollback, mtp_chain reseed from the accepted row, catch-up count,
 // next anchor and positions.
+// flags: bit 0 debug_break_rollback; bit 1 a DSpark round (no catch-up rows,
+// mtp_pos unchanged: src/generate.c:1117-1133).
 __global__ void k_accept(DevCtl *ctl, const float *__restrict__ vhidden, int d,
-                         float *__restrict__ chain, int depth, int brk) {
+                         float *__restrict__ chain, int depth, int flags) {
+    const bool brk = (flags & 1) != 0, dspark = (flags & 2) != 0;
     __shared__ int s_n;
     if (threadIdx.x == 0) {
         int k_eff = ctl->k_eff;
@@ -207,13 +256,13 @@ __global__ void k_accept(DevCtl *ctl, const float *__restrict__ vhidden, int d,
         ctl->ssm_slot = slot;
         ctl->new_pos = ctl->anchor_pos + 1 + n;
         // catch-up pairs (verify_hidden[j], out[j]) j < n-1 at mtp_pos+1+j
-        ctl->catch_n = n > 1 ? n - 1 : 0;
+        ctl->catch_n = n > 1 && !dspark ? n - 1 : 0;
         ctl->catch_pos = ctl->mtp_pos + 1;
         // Catch-up always runs k-1 rows so a round has a fixed shape; rows
         // j >= catch_n land at MTP positions >= the next round's mtp_pos,
         // which that round's draft steps overwrite before any read.
         for (int j = 0; j < 8; j++) ctl->catch_tok[j] = j < ctl->catch_n ? ctl->out[j] : ctl->out[0];
-        ctl->mtp_pos_next = ctl->mtp_pos + n;
+        ctl->mtp_pos_next = dspark ? ctl->mtp_pos : ctl->mtp_pos + n;
         s_n = n;
     }
     __syncthreads();
@@ -327,6 +376,22 @@ extern "C" int l98k_mtp_pre(const int8_t *emb_q, const float *emb_s, int gs, con
     return -1;
 }
 
+extern "C" int l98k_dspark_pre(const int8_t *emb_q, const float *emb_s, int gs, const int *tok, const float *chain,
+                               const float *mask, const float *depth, int d, const float *w_e, const float *w_h,
+                               float eps, int rows, int8_t *xq, float *xqs, hipStream_t st) {
+    if (gs <= 0) gs = d;
+    if (d < 32 || d > 256 * 8 || (d & 31) || rows < 1 || (gs & 31) || d % gs) return -1;
+#define DSPARK_LAUNCH(PJ)                                                                                 \
+    if (d <= 256 * PJ) {                                                                                  \
+        hipLaunchKernelGGL(k_dspark_pre<PJ>, dim3(rows, 3), dim3(64), 0, st, emb_q, emb_s, tok, chain, mask, \
+                           depth, d, gs, w_e, w_h, eps, xq, xqs);                                         \
+        return (int)hipGetLastError();                                                                    \
+    }
+    NORM_CASES(DSPARK_LAUNCH)
+#undef DSPARK_LAUNCH
+    return -1;
+}
+
 extern "C" int l98k_argmax(const float *x, int n, int rows, int mode, int *out,
                            unsigned long long *partial, unsigned *counter, hipStream_t st) {
     if (rows < 1 || rows > LZ_ARGMAX_ROWS || n < 1) return -1;
@@ -336,8 +401,8 @@ extern "C" int l98k_argmax(const float *x, int n, int rows, int mode, int *out,
 }
 
 extern "C" int l98k_accept(DevCtl *ctl, const float *vhidden, int d, float *chain, int depth,
-                           int brk, hipStream_t st) {
-    hipLaunchKernelGGL(k_accept, dim3(1), dim3(256), 0, st, ctl, vhidden, d, chain, depth, brk);
+                           int flags, hipStream_t st) {
+    hipLaunchKernelGGL(k_accept, dim3(1), dim3(256), 0, st, ctl, vhidden, d, chain, depth, flags);
     return (int)hipGetLastError();
 }
 

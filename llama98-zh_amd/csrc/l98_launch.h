@@ -78,6 +78,10 @@ int l98k_rmsnorm(float *x, int x_stride, const float *a, const float *b, const f
 int l98k_rmsnorm_ex(float *x, int x_stride, const float *a, const float *b, const float *w, int n, float eps,
                     int rows, float *out, int out_stride, int8_t *xq, float *xqs, int tok, hipStream_t st);
 // MTP input rows: [norm_e(embed(tok)) | norm_h(h)] quantized per 32 into xq [rows][2d].
+// DSpark main_proj input rows: [norm(chain) | norm(emb(tok[0]) or mask) | depth row], quantized per 32
+int l98k_dspark_pre(const int8_t *emb_q, const float *emb_s, int gs, const int *tok, const float *chain,
+                    const float *mask, const float *depth, int d, const float *w_e, const float *w_h, float eps,
+                    int rows, int8_t *xq, float *xqs, hipStream_t st);
 int l98k_mtp_pre(const int8_t *emb_q, const float *emb_s, int gs, const int *toks, const float *h, int d,
                  const float *w_e, const float *w_h, float eps, int rows, int8_t *xq, float *xqs,
                  hipStream_t st);
@@ -89,6 +93,11 @@ int l98k_kda_step(const KdaStepArgs *a, int kd, int K, hipStream_t st);
 int l98k_kda_items(const KdaStepArgs *a, const KdaItem *items, int n_items, size_t state_off, size_t conv_off,
                    int kd, int K, hipStream_t st);
 int l98k_attn_prep(const AttnArgs *a, int nt, hipStream_t st);
+// DSpark slot attention (mtp_attn_t1): rows slot rows of qg [rows][qg_dim]
+// and vp [rows][kv_dim]; the last row's V quantization also goes to the MTP
+// plane's row 0 (vc0, vs0); output float rows (out) or quantized (oq, oqs).
+int l98k_attn_t1(const float *qg, int qg_dim, const float *vp, int kv_dim, int nh, int nkv, int hd, int q_dim,
+                 int rows, int8_t *vc0, float *vs0, float *out, int8_t *oq, float *oqs, hipStream_t st);
 // Attention of several sessions' rows in one launch per kernel (items in
 // device memory); att: n_items blocks of att_item floats.
 int l98k_attn_items(const AttnArgs *a, const AttnItem *items, int n_items, int plane, int max_len, float *att,
@@ -123,7 +132,8 @@ int l98k_fwht_f32(float *v, int rows, int n, int blk, int rot, hipStream_t st);
 int l98k_subn_quant(const float *x, int rows, int n, int blk, int gw, int8_t *q, float *s, hipStream_t st);
 int l98k_argmax(const float *x, int n, int rows, int mode, int *out, unsigned long long *partial,
                 unsigned *counter, hipStream_t st);
-int l98k_accept(DevCtl *ctl, const float *vhidden, int d, float *chain, int depth, int brk, hipStream_t st);
+// flags: 1 debug_break_rollback, 2 a DSpark round (no catch-up, mtp_pos kept)
+int l98k_accept(DevCtl *ctl, const float *vhidden, int d, float *chain, int depth, int flags, hipStream_t st);
 int l98k_set_tokens(DevCtl *ctl, int op, RoundRec *hist, int hist_cap, hipStream_t st);
 }
 

@@ -21,8 +21,7 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
-FIXTURES = sorted(f for f in os.listdir(GOLDEN) if f.startswith("gen_") and f.endswith(".json")
-                  and not f.startswith("gen_ds_"))
+FIXTURES = sorted(f for f in os.listdir(GOLDEN) if f.startswith("gen_") and f.endswith(".json"))
 
 
 def load(pkg, model_root, fname):
