@@ -257,6 +257,43 @@ def bench_ksweep(args, pkg):
     eng.close()
 
 
+def bench_dspark(args, pkg):
+    """A DSpark head (mtp_n_draft = 6) on configs[1]'s shapes (synthetic
+    config 22): greedy rounds at k = 1..6, each one HIP graph launch whose
+    k drafts are one k-row pass (lz_mtp_draft_batch) instead of k chained
+    draft steps; the draft batch alone is timed too.  Prints one JSON line."""
+    import numpy as np
+    mdir = os.path.join(args.model_dir, "base_dspark")
+    pkg.ensure_model(mdir, 22, seed=1234)
+    eng = pkg.Engine(mdir, spec_k_max=pkg.L98_SPEC_K_GPU)
+    prompt = pkg.prompt_tokens(0, args.prompt, eng.V)
+    rows = []
+    n_rounds = min(args.steps, 64)          # rounds that fit the 1280-row state at k = 6 after the prompt
+    for k in range(1, 7):
+        eng.session_start(prompt)
+        eng.greedy_rounds(k, args.warmup)
+        _, na, ms = eng.greedy_rounds(k, n_rounds, detail=False)
+        emitted = int(np.sum(na)) + len(na)
+        lg = eng.forward_capture(int(prompt[-1]), len(prompt) - 1)
+        t0 = time.perf_counter()
+        for _ in range(20):
+            eng.draft_batch(int(np.argmax(lg)), k)
+        batch_ms = (time.perf_counter() - t0) * 1e3 / 20
+        rows.append({"k": k, "round_ms": round(ms / n_rounds, 4), "tok_s": round(emitted / (ms * 1e-3), 1),
+                     "alpha": round(float(np.sum(na)) / (k * len(na)), 4),
+                     "draft_batch_ms_host": round(batch_ms, 4)})
+    out = {"metric": "DSpark greedy spec decode tok/s per draft width (configs[1] shapes, 6-slot head)",
+           "value": rows[2]["tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": n_rounds, "warmup": args.warmup,
+           "ms_per_step": rows[2]["round_ms"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+           "dtype": "int8xint8->int32, fp32 epilogue/state",
+           "data": "synthetic (seeded random-init weights; random prompt)",
+           "config": {"workload": f"configs[1] shapes + DSpark head (mtp_n_draft 6, model.bin v6), "
+                                  f"{args.prompt}-token prompt, greedy rounds at k = 1..6; value at k = 3"},
+           "sweep": rows}
+    print(json.dumps(out))
+    eng.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -269,6 +306,7 @@ def main():
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--sessions", type=int, default=32, help="configs[4]: concurrent sessions")
+    ap.add_argument("--dspark", action="store_true", help="a DSpark head on configs[1]'s shapes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs the single-sequence path on one GPU; --gpus {args.gpus} "
@@ -282,6 +320,9 @@ def main():
         return
     if args.config == 2:
         bench_ksweep(args, pkg)
+        return
+    if args.dspark:
+        bench_dspark(args, pkg)
         return
     name = {0: "tiny", 1: "base", 3: "large"}.get(args.config, f"c{args.config}")
     mdir = os.path.join(args.model_dir, name)

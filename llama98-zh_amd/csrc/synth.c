@@ -148,6 +148,11 @@ int l98_synth_config(int id, L98SynthConfig *c) {
         c->scale_layout = id == 14 ? 2 : 0;
         c->bf16_small = id == 14 ? 1 : 0;
         return 0;
+    case 22:
+        if (l98_synth_config(1, c)) return 1;
+        c->bin_version = 6;
+        c->mtp_n_draft = 6;
+        return 0;
     case 18: case 19: case 20: case 21:
         if (l98_synth_config(id == 18 ? 10 : id == 19 ? 11 : id == 20 ? 0 : 12, c)) return 1;
         c->bin_version = id == 20 ? 7 : 6;

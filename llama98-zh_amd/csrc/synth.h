@@ -90,6 +90,7 @@ typedef struct {
  *  20  tiny's shapes with a DSpark head of 3 slots (version 7), groups of
  *              64, BF16 small tensors
  *  21  micro-subln's shapes with a DSpark head of 3 slots (version 6)
+ *  22  base's shapes with a DSpark head of 6 slots (version 6)
  * Returns 0 on success, 1 for an unknown id. */
 int l98_synth_config(int id, L98SynthConfig *out);
 

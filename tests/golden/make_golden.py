@@ -83,6 +83,7 @@ CASES = [
     ("gen_ds_tiny_k3_greedy", "ds_tiny", 20, 8192, 48, 3, 40, 0.0, 1.0, 1, {"dump": 4}),
     ("gen_ds_subln_k3_greedy", "ds_subln", 21, 512, 24, 3, 40, 0.0, 1.0, 1, {"dump": 4}),
     ("gen_ds_subln_k2_temp", "ds_subln", 21, 512, 24, 2, 40, 0.8, 0.95, 7),
+    ("gen_ds_base_k3_greedy", "base_dspark", 22, 65536, 64, 3, 32, 0.0, 1.0, 1, {"dump": 3}),
 ]
 # Prefill + one capture (the harness's capture command; needs no MTP head):
 # (fixture, model dir name, generator config id, vocab, n_prompt)
