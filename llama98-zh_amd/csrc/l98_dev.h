@@ -52,17 +52,16 @@ typedef struct {
     int rows;
     int in_dim;
     int out_stride;
-    int tile0;               // first tile of this job in the launch grid (set by the launcher)
+    int tiles;               // tiles of this job: blocks (0..tiles-1, job) of the launch grid (set by the launcher)
     int R;                   // rows per tile (set by the launcher)
     int gs;                  // weight scale group (a multiple of 32 dividing in_dim; 0: the row)
     Prologue pro;
 } GemvJob;
 
-// A fused GEMV launch.  The jobs' first tiles lead the struct so a block
-// finds its job with one scalar load of tile0[].
+// A fused GEMV launch: block (x, y) is tile x of job y, so a block's job is
+// known at entry and its fields load with the kernel's first scalar loads.
 typedef struct {
     int n;
-    int tile0[MAX_GEMV_JOBS];    // first tile of each job (set by the launcher); unused entries past n
     int pad[3];
     GemvJob job[MAX_GEMV_JOBS];
 } GemvBatch;

@@ -800,8 +800,6 @@ struct DState {
     MoeGroups *grp;
     DevCtl *ctl;
     int *tokbuf;
-    unsigned long long *amax_part;          // argmax block partials [rows][ARGMAX_BLOCKS]
-    unsigned *amax_cnt;                     // argmax per-row block counters (self-resetting)
     DevCtl *ctl_pinned = nullptr;
     int cap_rows = 0;                       // rows of hcap / tokbuf
     RoundRec *hist = nullptr;               // device round records
@@ -880,8 +878,6 @@ bool carve(DState *s) {
     s->grp = (MoeGroups *)st_take(s, sizeof(MoeGroups));
     s->ctl = (DevCtl *)st_take(s, sizeof(DevCtl));
     s->tokbuf = (int *)st_take(s, sizeof(int) * (size_t)s->cap_rows);
-    s->amax_part = (unsigned long long *)st_take(s, sizeof(unsigned long long) * (L98_SPEC_K_GPU + 1) * 64);
-    s->amax_cnt = (unsigned *)st_take(s, sizeof(unsigned) * (L98_SPEC_K_GPU + 1));
     s->hist_cap = s->seq_len;
     s->hist = (RoundRec *)st_take(s, sizeof(RoundRec) * (size_t)s->hist_cap);
     return true;
@@ -1231,7 +1227,7 @@ int draft_step(DState *s, const int *toks, const int *ctl_pos, int pos_off, int 
     CK(attn_block(s, m->mtp, PN(s->mtp_x, d, nullptr, nullptr, m->mtp.in_norm, eps, nullptr, nullptr, 0),
                   s->planes - 1, ctl_pos, pos_off, 1, max_pos, false));
     CK(mtp_ffn_head(s, 1, s->chain, out_logits));
-    if (out_tok) CK(l98k_argmax(out_logits, c.vocab_size, 1, 1, out_tok, s->amax_part, s->amax_cnt, s->st));
+    if (out_tok) CK(l98k_argmax(out_logits, c.vocab_size, 1, 1, out_tok, s->st));
     return 0;
 }
 
@@ -1265,7 +1261,7 @@ int dspark_draft(DState *s, const int *toks, int k, float *out_logits, int *out_
                            s->xq2, s->xqs2, 0, s->st));
     CK(gemv(s, {JX(L.o, s->blk, d, s->xq2, s->xqs2)}, k));
     CK(mtp_ffn_head(s, k, nullptr, out_logits));
-    if (out_tok) CK(l98k_argmax(out_logits, c.vocab_size, k, 1, out_tok, s->amax_part, s->amax_cnt, s->st));
+    if (out_tok) CK(l98k_argmax(out_logits, c.vocab_size, k, 1, out_tok, s->st));
     return 0;
 }
 
@@ -2070,7 +2066,7 @@ int enqueue_verify_accept(DState *d, int k_eff, int max_pos, int brk, bool catch
     const bool dspark = d->m->n_draft > 1;     // no catch-up, mtp_pos kept (src/generate.c:1117-1133)
     CK(forward_chunk(d, d->ctl->tok, k_eff + 1, &d->ctl->anchor_pos, 1, max_pos, d->vhidden, true,
                      d->mtp_logits, false));
-    CK(l98k_argmax(d->mtp_logits, c.vocab_size, k_eff + 1, 0, d->ctl->targ, d->amax_part, d->amax_cnt, d->st));
+    CK(l98k_argmax(d->mtp_logits, c.vocab_size, k_eff + 1, 0, d->ctl->targ, d->st));
     CK(l98k_accept(d->ctl, d->vhidden, c.hidden_size, d->chain, d->depth, (brk ? 1 : 0) | (dspark ? 2 : 0), d->st));
     if (dspark) catchup = false;
     if (mark) CK(hipEventRecord(mark, d->st));
@@ -2641,14 +2637,9 @@ extern "C" int l98_gemm_q8(const int8_t *w, const float *ws, int N, int K, const
 
 extern "C" int l98_argmax_rows(const float *x, int rows, int n, int mode, int *out) {
     if (!x || !out || rows < 1 || rows > MAX_CHUNK || n < 1 || (mode != 0 && mode != 1)) return 1;
-    DevBuf dx, dpart, dcnt, dout;
-    if (!dx.get(x, sizeof(float) * (size_t)rows * n) || !dpart.get(nullptr, sizeof(unsigned long long) * rows * 64) ||
-        !dcnt.get(nullptr, sizeof(unsigned) * rows) || !dout.get(nullptr, sizeof(int) * rows))
-        return 1;
-    if (hipMemset(dcnt.p, 0, sizeof(unsigned) * rows) != hipSuccess) return 1;
-    if (l98k_argmax((const float *)dx.p, n, rows, mode, (int *)dout.p, (unsigned long long *)dpart.p,
-                    (unsigned *)dcnt.p, nullptr))
-        return 1;
+    DevBuf dx, dout;
+    if (!dx.get(x, sizeof(float) * (size_t)rows * n) || !dout.get(nullptr, sizeof(int) * rows)) return 1;
+    if (l98k_argmax((const float *)dx.p, n, rows, mode, (int *)dout.p, nullptr)) return 1;
     return dout.put(out, sizeof(int) * rows) ? 0 : 1;
 }
 

@@ -5,28 +5,25 @@
 #include <climits>
 
 // One launch over b.n jobs; m <= M live token rows (M a power of two).
+// Block (x, y) is tile x of job y: the job index is the workgroup id, so
+// the job's fields are read with the kernel's first batch of scalar loads
+// (no dependent lookup); tiles past a job's last exit at once.
 template <int M, int PJ, int MODES>
 __global__ __launch_bounds__(GEMV_THREADS) void k_gemv_q8(GemvBatch batch, int m) {
     extern __shared__ __align__(16) char smem[];
     __shared__ int s_row[M];
     __shared__ float s_inv[M], tab[32];
-    const int blk = blockIdx.x;
-    // tile0[] ascends and its entries past n hold INT_MAX (the launcher), so
-    // the job is the last one whose first tile is <= blk; the whole job is
-    // then read at once (one batch of scalar loads, not one per use)
-    int j = 0;
-#pragma unroll
-    for (int i = 1; i < MAX_GEMV_JOBS; i++) j = blk >= batch.tile0[i] ? i : j;
-    j = __builtin_amdgcn_readfirstlane(j);
-    const GemvJob job = batch.job[j];
-    const int row0 = (blk - job.tile0) * job.R;
+    const GemvJob job = batch.job[blockIdx.y];
+    if ((int)blockIdx.x >= job.tiles) return;
+    const int row0 = blockIdx.x * job.R;
     const int rows_here = imin(job.R, job.rows - row0);
     if (threadIdx.x < M) s_row[threadIdx.x] = threadIdx.x < m ? threadIdx.x : 0;
     int xrow[M];
 #pragma unroll
     for (int t = 0; t < M; t++) xrow[t] = t < m ? t : 0;
     gemv_tile<M, PJ, MODES>(job.w + (size_t)row0 * job.in_dim, job.ws, rows_here, job.R, job.in_dim, job.pro, job.xq,
-                            job.xqs, xrow, s_row, m, blk == 0, job.out, job.out_stride, row0, job.acc_out, job.rows,
+                            job.xqs, xrow, s_row, m, blockIdx.x == 0 && blockIdx.y == 0, job.out, job.out_stride,
+                            row0, job.acc_out, job.rows,
                             smem, s_inv, tab, job.gs);
 }
 
@@ -43,7 +40,7 @@ extern "C" int l98k_upload_exp_table_gemv(const float *tab) {
 #define GEMV_CASE(M_, PJ_, MODES_)                                                                         \
     case (M_) * 100000 + (PJ_) * 1000 + (MODES_):                                                            \
         ALLOW_BIG_LDS((k_gemv_q8<M_, PJ_, MODES_>));                                                      \
-        hipLaunchKernelGGL((k_gemv_q8<M_, PJ_, MODES_>), dim3(tiles), dim3(GEMV_THREADS), lds, st, *b, m); \
+        hipLaunchKernelGGL((k_gemv_q8<M_, PJ_, MODES_>), dim3(tiles, b->n), dim3(GEMV_THREADS), lds, st, *b, m); \
         break;
 #define GEMV_CASES_MG(M_, G_)                                                                          \
     GEMV_CASE(M_, 0, MODES_X | G_)                                                                     \
@@ -61,18 +58,16 @@ extern "C" int l98k_upload_exp_table_gemv(const float *tab) {
 extern "C" int l98k_gemv(GemvBatch *b, int m, hipStream_t st) {
     if (m < 1 || m > MAX_CHUNK || b->n < 1 || b->n > MAX_GEMV_JOBS) return -1;
     const int M = m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8;
-    int tiles = 0, pj = 0, modes = 0, grouped = 0;
+    int tiles = 0, pj = 0, modes = 0, grouped = 0;       // tiles: the largest job's
     size_t lds = 0;
-    for (int j = b->n; j < MAX_GEMV_JOBS; j++) b->tile0[j] = INT_MAX;
     for (int j = 0; j < b->n; j++) {
         GemvJob &J = b->job[j];
         if (J.in_dim < 32 || (J.in_dim & 31) || J.in_dim > GEMV_MAX_IN || J.rows < 1 ||
             !prologue_ok(J.pro, J.in_dim, J.xq, J.xqs) || (J.gs && ((J.gs & 31) || J.in_dim % J.gs)))
             return -1;
         J.R = gemv_rows_per_tile(J.in_dim, M);
-        J.tile0 = tiles;
-        b->tile0[j] = tiles;
-        tiles += (J.rows + J.R - 1) / J.R;
+        J.tiles = (J.rows + J.R - 1) / J.R;
+        tiles = J.tiles > tiles ? J.tiles : tiles;
         modes |= MB(J.pro.mode);
         if (J.gs && J.gs < J.in_dim) grouped = MG;
         if (J.pro.mode != PRO_XQ) pj = pro_pj(J.in_dim) > pj ? pro_pj(J.in_dim) : pj;

@@ -167,67 +167,66 @@ extern "C" int l98k_row_sums(const float *x, int rows, int n, float *out, hipStr
 
 // -------------------------------------------------------- argmax / ctl ---
 
-#define ARGMAX_BLOCKS 64
 #define LZ_ARGMAX_ROWS 8
+#define ARGMAX_THREADS 1024
 
-// Per row argmax, ARGMAX_BLOCKS blocks per row; the last block to finish a
-// row reduces the partials and resets the row's counter (so the kernel can
-// be replayed from a graph).  mode 0: order-preserving key, first index wins
-// (sample_argmax, src/sampler.c:121-137).  mode 1: float '>' compare, first
-// index wins (lz_argmax_p1's scan, src/sampler.c:139-155).
-__global__ __launch_bounds__(256) void k_argmax(const float *__restrict__ x, int n, int mode,
-                                                unsigned long long *__restrict__ partial,
-                                                unsigned *__restrict__ counter, int *__restrict__ out) {
-    const int row = blockIdx.y, nb = gridDim.x;
+// Per row argmax, one block of 1024 lanes per row: every lane scans a
+// strided share of the row with its loads in flight, then a block max of
+// the packed (key, ~index) words.  One block per row needs no hand-over
+// between blocks (a device-scope fence on this chip writes back and
+// invalidates every cache, which costs more than the row's read).  mode 0:
+// order-preserving key, first index wins (sample_argmax,
+// src/sampler.c:121-137).  mode 1: float '>' compare, first index wins
+// (lz_argmax_p1's scan, src/sampler.c:139-155).
+__global__ __launch_bounds__(ARGMAX_THREADS) void k_argmax(const float *__restrict__ x, int n, int mode,
+                                                           int *__restrict__ out) {
+    const int row = blockIdx.x, tid = threadIdx.x;
     const float *r = x + (size_t)row * n;
-    const int seg = (n + nb - 1) / nb;
-    const int lo = blockIdx.x * seg, hi = lo + seg < n ? lo + seg : n;
     unsigned long long best = 0;
-    for (int i = lo + threadIdx.x; i < hi; i += blockDim.x) {
-        float v = r[i];
+    auto fold = [&](float v, int i) {
         uint32_t k;
         if (mode == 0) k = d_fkey(v);
         else k = (v != v) ? 0u : d_fkey(v == 0.0f ? 0.0f : v);
-        unsigned long long cand = ((unsigned long long)k << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)i);
+        const unsigned long long cand = ((unsigned long long)k << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)i);
         best = cand > best ? cand : best;
+    };
+    if ((n & 3) == 0 && ((uintptr_t)r & 15) == 0) {
+        // float4 f = tid + 1024 * u: eight loads in flight per round
+        const float4 *r4 = reinterpret_cast<const float4 *>(r);
+        const int n4 = n >> 2;
+        for (int base = 0; base < n4; base += 8 * ARGMAX_THREADS) {
+            float4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v[u] = r4[imin(base + u * ARGMAX_THREADS + tid, n4 - 1)];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int f = base + u * ARGMAX_THREADS + tid;
+                if (f < n4) {
+                    fold(v[u].x, 4 * f);
+                    fold(v[u].y, 4 * f + 1);
+                    fold(v[u].z, 4 * f + 2);
+                    fold(v[u].w, 4 * f + 3);
+                }
+            }
+        }
+    } else {
+        for (int i = tid; i < n; i += ARGMAX_THREADS) fold(r[i], i);
     }
     best = wave_max_u64(best);
-    __shared__ unsigned long long sb[4];
-    __shared__ bool s_last;
-    if ((threadIdx.x & 63) == 0) sb[threadIdx.x >> 6] = best;
+    __shared__ unsigned long long sb[ARGMAX_THREADS / 64];
+    if ((tid & 63) == 0) sb[tid >> 6] = best;
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (tid == 0) {
         unsigned long long b = 0;
-        for (int i = 0; i < (int)(blockDim.x >> 6); i++) b = sb[i] > b ? sb[i] : b;
-        partial[(size_t)row * nb + blockIdx.x] = b;
-        __threadfence();
-        unsigned prev = atomicAdd(&counter[row], 1u);
-        s_last = (prev == (unsigned)nb - 1);
-    }
-    __syncthreads();
-    if (s_last) {
-        __threadfence();
-        unsigned long long b = 0;
-        for (int i = threadIdx.x; i < nb; i += blockDim.x) {
-            unsigned long long p = __atomic_load_n(&partial[(size_t)row * nb + i], __ATOMIC_RELAXED);
-            b = p > b ? p : b;
+        for (int i = 0; i < ARGMAX_THREADS / 64; i++) b = sb[i] > b ? sb[i] : b;
+        int idx = (int)(0xFFFFFFFFu - (uint32_t)(b & 0xFFFFFFFFu));
+        // lz_argmax_p1 starts from element 0 and takes only v > best: a NaN
+        // there is never beaten, so the row's answer is 0.
+        if (mode == 1) {
+            const float r0 = r[0];
+            if (r0 != r0) idx = 0;
         }
-        b = wave_max_u64(b);
-        if ((threadIdx.x & 63) == 0) sb[threadIdx.x >> 6] = b;
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            unsigned long long bb = 0;
-            for (int i = 0; i < (int)(blockDim.x >> 6); i++) bb = sb[i] > bb ? sb[i] : bb;
-            int idx = (int)(0xFFFFFFFFu - (uint32_t)(bb & 0xFFFFFFFFu));
-            // lz_argmax_p1 starts from element 0 and takes only v > best:
-            // a NaN there is never beaten, so the row's answer is 0.
-            if (mode == 1) {
-                const float r0 = r[0];
-                if (r0 != r0) idx = 0;
-            }
-            out[row] = idx;
-            counter[row] = 0;
-        }
+        out[row] = idx;
     }
 }
 
@@ -392,11 +391,9 @@ extern "C" int l98k_dspark_pre(const int8_t *emb_q, const float *emb_s, int gs, 
     return -1;
 }
 
-extern "C" int l98k_argmax(const float *x, int n, int rows, int mode, int *out,
-                           unsigned long long *partial, unsigned *counter, hipStream_t st) {
+extern "C" int l98k_argmax(const float *x, int n, int rows, int mode, int *out, hipStream_t st) {
     if (rows < 1 || rows > LZ_ARGMAX_ROWS || n < 1) return -1;
-    hipLaunchKernelGGL(k_argmax, dim3(ARGMAX_BLOCKS, rows), dim3(256), 0, st, x, n, mode, partial,
-                       counter, out);
+    hipLaunchKernelGGL(k_argmax, dim3(rows), dim3(ARGMAX_THREADS), 0, st, x, n, mode, out);
     return (int)hipGetLastError();
 }
 

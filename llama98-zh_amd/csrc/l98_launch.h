@@ -130,8 +130,9 @@ int l98k_row_sums(const float *x, int rows, int n, float *out, hipStream_t st);
 int l98k_fwht_i32(const int32_t *x, int32_t *y, int rows, int n, int blk, hipStream_t st);
 int l98k_fwht_f32(float *v, int rows, int n, int blk, int rot, hipStream_t st);
 int l98k_subn_quant(const float *x, int rows, int n, int blk, int gw, int8_t *q, float *s, hipStream_t st);
-int l98k_argmax(const float *x, int n, int rows, int mode, int *out, unsigned long long *partial,
-                unsigned *counter, hipStream_t st);
+// Per row argmax of rows x n floats, one block per row (mode 0:
+// sample_argmax's key order, 1: lz_argmax_p1's compare).
+int l98k_argmax(const float *x, int n, int rows, int mode, int *out, hipStream_t st);
 // flags: 1 debug_break_rollback, 2 a DSpark round (no catch-up, mtp_pos kept)
 int l98k_accept(DevCtl *ctl, const float *vhidden, int d, float *chain, int depth, int flags, hipStream_t st);
 int l98k_set_tokens(DevCtl *ctl, int op, RoundRec *hist, int hist_cap, hipStream_t st);
