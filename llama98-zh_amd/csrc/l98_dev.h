@@ -142,6 +142,9 @@ typedef struct {
     int nv, key, value, rank, depth, advance, nt;
     float scale, eps;
     int fb_gs;                          // f_b scale group (0: the row)
+    int hist_rows;                      // conv history from the rows before row 0, not the ring (split prefill)
+    float *rec;                         // split prefill: token records [n][nv][5*kd + 4]
+    float *orow;                        // split prefill: recurrence outputs [n][value]
 } KdaStepArgs;
 
 typedef struct {

@@ -1317,6 +1317,7 @@ struct DWide {
     int *ng, *gexp, *goff, *gcnt, *list, *pair_token;
     int *toks;
     float *att;
+    float *kda_rec, *kda_o;   // split KDA prefill: token records [R][nv][5*kd + 4], recurrence outputs [R][value]
     float *logits = nullptr;  // rows x vocab, sized on demand
     int logits_rows = 0;
     KdaItem *kitems;          // per-session tables of the item launches [WIDE_MAX]
@@ -1364,7 +1365,9 @@ DWide *wide_get(const DModel *cm) {
                  ong = take(4), oge = take(4 * MAX_EXPERTS), ogo = take(4 * MAX_EXPERTS), ogc = take(4 * MAX_EXPERTS),
                  oli = take(4 * pairs), opt = take(4 * pairs), otk = take(4 * R),
                  oki = take(sizeof(KdaItem) * R), oai = take(sizeof(AttnItem) * R),
-                 oat = take(4 * (size_t)MAX_CHUNK * c.n_heads * (size_t)((c.seq_len + 3) & ~3));
+                 oat = take(4 * (size_t)MAX_CHUNK * c.n_heads * (size_t)((c.seq_len + 3) & ~3)),
+                 okr = take(4 * R * c.lin_n_v_heads * (size_t)(5 * c.lin_k_head_dim + 4)),
+                 oko = take(4 * R * c.lin_value_dim);
     if (hipMalloc((void **)&w->arena, off) != hipSuccess) { delete w; return nullptr; }
     char *a = w->arena;
     w->cap = WIDE_MAX;
@@ -1382,6 +1385,7 @@ DWide *wide_get(const DModel *cm) {
     w->ng = (int *)(a + ong); w->gexp = (int *)(a + oge); w->goff = (int *)(a + ogo); w->gcnt = (int *)(a + ogc);
     w->list = (int *)(a + oli); w->pair_token = (int *)(a + opt); w->toks = (int *)(a + otk);
     w->att = (float *)(a + oat);
+    w->kda_rec = (float *)(a + okr); w->kda_o = (float *)(a + oko);
     w->kitems = (KdaItem *)(a + oki);
     w->aitems = (AttnItem *)(a + oai);
     m->wide = w;
@@ -1515,8 +1519,27 @@ int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, 
             a.nv = nv; a.key = key; a.value = value; a.rank = rank;
             a.advance = advance ? 1 : 0;
             a.scale = ssm_scale(kd); a.eps = eps;
-            CK(l98k_kda_items(&a, w->kitems, n_items, (size_t)li * nv * kd * c.lin_v_head_dim,
-                              (size_t)li * c.lin_conv_dim * hist, kd, c.conv_kernel, st));
+            if (n_items == 1 && items[0].n > MAX_CHUNK && !advance) {
+                // one session's prefill: the state-free work of every row at
+                // once, the recurrence, then the gated norm of every row
+                const DState *s = items[0].d;
+                a.state = s->kda + (size_t)li * nv * kd * c.lin_v_head_dim;
+                a.conv_ring = s->conv + (size_t)li * c.lin_conv_dim * hist;
+                a.ctl_slot = &s->ctl->slot_base;
+                a.slot_stride = s->kda_slot;
+                a.conv_slot_stride = s->conv_slot;
+                a.depth = s->depth;
+                const size_t r0 = (size_t)items[0].row0;
+                a.pq += r0 * key; a.pk += r0 * key; a.pv += r0 * value; a.pfa += r0 * rank;
+                a.bvec += r0 * nv; a.gz += r0 * value;
+                a.xq += r0 * value; a.xqs += r0 * (value / 32);
+                a.rec = w->kda_rec;
+                a.orow = w->kda_o;
+                CK(l98k_kda_split(&a, items[0].n, kd, c.conv_kernel, st));
+            } else {
+                CK(l98k_kda_items(&a, w->kitems, n_items, (size_t)li * nv * kd * c.lin_v_head_dim,
+                                  (size_t)li * c.lin_conv_dim * hist, kd, c.conv_kernel, st));
+            }
             CK(mf(L.ko, w->xq2, w->xqs2, R, w->blk, d, st));
         }
         CK(l98k_rmsnorm(w->x, d, w->blk, nullptr, L.post_norm, d, eps, R, nullptr, 0, w->xq, w->xqs, st));

@@ -41,11 +41,111 @@ __device__ __forceinline__ float dpp_quad_bcast3(float v) {      // every lane <
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xFF, 0xF, 0xF, false));
 }
 
-template <int KD, int K, int NT>
+// One token of the recurrence on the lane quads: c = kn.g, q = qn.g*scale,
+// g and b = kn are LDS rows of the token (the lane reads its rows row0 ..
+// row0 + kd/4), vt its v for the lane's column.  Every LDS read is issued at
+// the top (one wait, not one per use).  Returns o on every lane of the quad
+// and leaves S' in S.
+template <int KD>
+__device__ __forceinline__ float kda_token(float (&S)[KD / 4], const float *sc, const float *sa, const float *sg,
+                                           const float *sb, const float *pv, const float *pbeta,
+                                           const float *pkq, int row0) {
+    constexpr int RPL = KD / 4;
+    float4 c4[RPL / 4], a4[RPL / 4], g4[RPL / 4], b4[RPL / 4];
+#pragma unroll
+    for (int i = 0; i < RPL / 4; i++) {
+        c4[i] = *reinterpret_cast<const float4 *>(&sc[row0 + 4 * i]);
+        a4[i] = *reinterpret_cast<const float4 *>(&sa[row0 + 4 * i]);
+        g4[i] = *reinterpret_cast<const float4 *>(&sg[row0 + 4 * i]);
+        b4[i] = *reinterpret_cast<const float4 *>(&sb[row0 + 4 * i]);
+    }
+    const float vt = *pv, bt = *pbeta, kqt = *pkq;
+    __builtin_amdgcn_sched_barrier(0);
+    float pu[RPL], pw[RPL];
+#pragma unroll
+    for (int i = 0; i < RPL / 4; i++) {
+        pu[4 * i] = S[4 * i] * c4[i].x; pu[4 * i + 1] = S[4 * i + 1] * c4[i].y;
+        pu[4 * i + 2] = S[4 * i + 2] * c4[i].z; pu[4 * i + 3] = S[4 * i + 3] * c4[i].w;
+        pw[4 * i] = S[4 * i] * a4[i].x; pw[4 * i + 1] = S[4 * i + 1] * a4[i].y;
+        pw[4 * i + 2] = S[4 * i + 2] * a4[i].z; pw[4 * i + 3] = S[4 * i + 3] * a4[i].w;
+    }
+    float u = 0.0f, w = 0.0f;
+#pragma unroll
+    for (int ph = 0; ph < 4; ph++) {
+        if (ph) { u = dpp_quad_shr1(u); w = dpp_quad_shr1(w); }
+#pragma unroll
+        for (int i = 0; i < RPL; i++) { u += pu[i]; w += pw[i]; }
+    }
+    u = dpp_quad_bcast3(u);
+    w = dpp_quad_bcast3(w);
+    const float ut = (vt - 1.0f * u) * bt;
+    const float o = 1.0f * w + ut * kqt;
+#pragma unroll
+    for (int i = 0; i < RPL / 4; i++) {
+        S[4 * i] = S[4 * i] * g4[i].x + b4[i].x * ut;
+        S[4 * i + 1] = S[4 * i + 1] * g4[i].y + b4[i].y * ut;
+        S[4 * i + 2] = S[4 * i + 2] * g4[i].z + b4[i].z * ut;
+        S[4 * i + 3] = S[4 * i + 3] * g4[i].w + b4[i].w * ut;
+    }
+    return o;
+}
+
+// The per-head gated RMSNorm of the recurrence outputs s_o[t][0..vd) with
+// the silu'd output gate s_z (src/ops_norm.c:749-793: the sum of o^2 in
+// index order, inv = rsqrt(ss/vd + eps), ((o*inv)*w)*z), then the per-32
+// quantization of the rows for o_proj (src/forward_kda.c:1000-1043).  s_sq,
+// s_y: LDS rows the tail may overwrite.  All 4*kd threads of the block.
+template <int KD, int NT>
+__device__ __forceinline__ void kda_gated_tail(const KdaStepArgs &a, int h, int nt, int j, float onw,
+                                               float (*s_o)[KD], const float (*s_z)[KD], float (*s_sq)[KD],
+                                               float (*s_y)[KD], float *s_oinv) {
+    constexpr int VD = KD, NTHR = 4 * KD;
+    constexpr int NO4 = (NT * VD / 4 + NTHR - 1) / NTHR;                // float4 of the output per thread
+    const int tid = threadIdx.x, value = a.value;
+    const bool chan = tid < KD;
+    if (chan) {
+#pragma unroll
+        for (int t = 0; t < NT; t++)
+            if (t < nt) s_sq[t][j] = s_o[t][j] * s_o[t][j];
+    }
+    __syncthreads();
+    if (tid < nt) s_oinv[tid] = d_rsqrt(d_ss_over_n(serial_sum_n<VD>(s_sq[tid]), VD) + a.eps);
+    __syncthreads();
+    float yv[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        const int tc = imin(t, nt - 1);
+        yv[t] = s_o[tc][j] * s_oinv[tc] * onw * s_z[t][j];
+    }
+    if (chan) {
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            if (t < nt) {
+                if (a.normed_out) a.normed_out[(size_t)t * value + h * VD + j] = yv[t];
+                s_y[t][j] = yv[t];
+            }
+        }
+    }
+    __syncthreads();
+    const int no4 = nt * VD / 4;
+#pragma unroll
+    for (int u = 0; u < NO4; u++) {
+        const int f = u * NTHR + tid;
+        const int fc = imin(f, no4 - 1);
+        const int t = (4 * fc) / VD, c = 4 * fc - t * VD;
+        float sg;
+        const uint32_t q = quant_octet(*reinterpret_cast<const float4 *>(&s_y[t][c]), &sg);
+        if (f < no4) {
+            reinterpret_cast<uint32_t *>(a.xq + (size_t)t * value + h * VD)[c >> 2] = q;
+            if (!(c & 31)) a.xqs[(size_t)t * (value >> 5) + ((h * VD + c) >> 5)] = sg;
+        }
+    }
+}
+
+template <int KD, int K, int NT, bool PRE = false>
 __device__ __forceinline__ void kda_step_body(const KdaStepArgs &a, int h) {
     constexpr int VD = KD, HIST = K - 1, NTHR = 4 * KD, RPL = KD / 4;
     constexpr int NF4 = (NT * KDA_MAX_RANK / 4 + NTHR - 1) / NTHR;      // float4 of the gate input per thread
-    constexpr int NO4 = (NT * VD / 4 + NTHR - 1) / NTHR;                // float4 of the output per thread
     EXP_TAB_LOAD(tab);
     __shared__ __align__(16) float s_a[MAX_CHUNK][KD];   // q, then q.g*invq*scale (qcw), then y
     __shared__ __align__(16) float s_b[MAX_CHUNK][KD];   // k, then k*invk (kn)
@@ -59,11 +159,10 @@ __device__ __forceinline__ void kda_step_body(const KdaStepArgs &a, int h) {
         s_oinv[MAX_CHUNK];
     __shared__ __align__(16) float s_z[MAX_CHUNK][KD];   // silu of the output gate input
     const int tid = threadIdx.x;
-    const bool chan = tid < KD;
     // Channel phases: thread group grp = tid / kd takes row type grp (0: q,
     // 1: k, 2: v, 3: the output gate input) of channel j for every token, and
     // the gate rows of tokens grp, grp + 4, ...; the later phases use the
-    // first group (chan: tid < kd, j = tid).
+    // first group (tid < kd, j = tid).
     const int grp = tid / KD, j = tid - grp * KD;
     const int col = tid >> 2, quarter = tid & 3, row0 = quarter * RPL;
     const int nt = a.nt, key = a.key, value = a.value, rank = a.rank;
@@ -91,7 +190,11 @@ __device__ __forceinline__ void kda_step_body(const KdaStepArgs &a, int h) {
     float wc[K], hc[HIST > 0 ? HIST : 1];
 #pragma unroll
     for (int i = 0; i < K; i++) wc[i] = a.conv_w[(size_t)cch * K + i];
-    {
+    if (PRE && a.hist_rows) {
+        // the inputs of the HIST rows before row 0 (earlier rows of the same prefill)
+#pragma unroll
+        for (int i = 0; i < HIST; i++) hc[i] = xsrc[(ptrdiff_t)(i - HIST) * xstride + h * KD + j];
+    } else {
         const float *r0 = a.conv_ring + (size_t)base * a.conv_slot_stride;
 #pragma unroll
         for (int i = 0; i < HIST; i++) hc[i] = r0[(size_t)cch * HIST + i];
@@ -111,7 +214,7 @@ __device__ __forceinline__ void kda_step_body(const KdaStepArgs &a, int h) {
     const float onw = a.o_norm[j];
     const float alog = a.a_log[h];
     float S[RPL];
-    {
+    if constexpr (!PRE) {
         const float4 *src = reinterpret_cast<const float4 *>(a.state + (size_t)base * a.slot_stride + head_off +
                                                              (size_t)col * KD + row0);
 #pragma unroll
@@ -152,8 +255,9 @@ __device__ __forceinline__ void kda_step_body(const KdaStepArgs &a, int h) {
         else if (grp == 2) { s_v[t][j] = y; }
         else s_z[t][j] = y;
     }
-    // ring: the history after token t is seq[t+1 .. t+HIST]
-    if (grp < 3) {
+    // ring: the history after token t is seq[t+1 .. t+HIST] (the split
+    // prefill writes it after its last row instead)
+    if (!PRE && grp < 3) {
         int so_t = so0;
 #pragma unroll
         for (int t = 0; t < NT; t++) {
@@ -291,48 +395,25 @@ __device__ __forceinline__ void kda_step_body(const KdaStepArgs &a, int h) {
         s_kq[tid] = kq;
     }
     __syncthreads();
-    // ---- the token-serial recurrence on the lane quads.  Every LDS read of
-    // a token is issued at the top of its step (one wait, not one per use);
-    // the state slot advances without a division.
+    if constexpr (PRE) {
+        // the rows' token records for the split prefill's recurrence launch:
+        // [kn.g | qn.g | g | kn | v] of the head, then beta, k.q, 0, 0
+        constexpr int Q4 = KD / 4, RS4 = 5 * Q4 + 1;
+        for (int f = tid; f < nt * RS4; f += NTHR) {
+            const int t = f / RS4, e = f - t * RS4, seg = e / Q4, k4 = e - seg * Q4;
+            const float(*arr)[KD] = seg == 0 ? s_c : seg == 1 ? s_a : seg == 2 ? s_g : seg == 3 ? s_b : s_v;
+            const float4 val = seg < 5 ? reinterpret_cast<const float4 *>(arr[t])[k4]
+                                       : make_float4(s_beta[t], s_kq[t], 0.0f, 0.0f);
+            reinterpret_cast<float4 *>(a.rec + (size_t)t * a.nv * (4 * RS4) + (size_t)h * (4 * RS4))[e] = val;
+        }
+        return;
+    }
+    // ---- the token-serial recurrence on the lane quads; the state slot
+    // advances without a division
     int so_t = so0;
 #pragma unroll 1
     for (int t = 0; t < nt; t++) {
-        float4 c4[RPL / 4], a4[RPL / 4], g4[RPL / 4], b4[RPL / 4];
-#pragma unroll
-        for (int i = 0; i < RPL / 4; i++) {
-            c4[i] = *reinterpret_cast<const float4 *>(&s_c[t][row0 + 4 * i]);
-            a4[i] = *reinterpret_cast<const float4 *>(&s_a[t][row0 + 4 * i]);
-            g4[i] = *reinterpret_cast<const float4 *>(&s_g[t][row0 + 4 * i]);
-            b4[i] = *reinterpret_cast<const float4 *>(&s_b[t][row0 + 4 * i]);
-        }
-        const float vt = s_v[t][col], bt = s_beta[t], kqt = s_kq[t];
-        __builtin_amdgcn_sched_barrier(0);
-        float pu[RPL], pw[RPL];
-#pragma unroll
-        for (int i = 0; i < RPL / 4; i++) {
-            pu[4 * i] = S[4 * i] * c4[i].x; pu[4 * i + 1] = S[4 * i + 1] * c4[i].y;
-            pu[4 * i + 2] = S[4 * i + 2] * c4[i].z; pu[4 * i + 3] = S[4 * i + 3] * c4[i].w;
-            pw[4 * i] = S[4 * i] * a4[i].x; pw[4 * i + 1] = S[4 * i + 1] * a4[i].y;
-            pw[4 * i + 2] = S[4 * i + 2] * a4[i].z; pw[4 * i + 3] = S[4 * i + 3] * a4[i].w;
-        }
-        float u = 0.0f, w = 0.0f;
-#pragma unroll
-        for (int ph = 0; ph < 4; ph++) {
-            if (ph) { u = dpp_quad_shr1(u); w = dpp_quad_shr1(w); }
-#pragma unroll
-            for (int i = 0; i < RPL; i++) { u += pu[i]; w += pw[i]; }
-        }
-        u = dpp_quad_bcast3(u);
-        w = dpp_quad_bcast3(w);
-        const float ut = (vt - 1.0f * u) * bt;
-        const float o = 1.0f * w + ut * kqt;
-#pragma unroll
-        for (int i = 0; i < RPL / 4; i++) {
-            S[4 * i] = S[4 * i] * g4[i].x + b4[i].x * ut;
-            S[4 * i + 1] = S[4 * i + 1] * g4[i].y + b4[i].y * ut;
-            S[4 * i + 2] = S[4 * i + 2] * g4[i].z + b4[i].z * ut;
-            S[4 * i + 3] = S[4 * i + 3] * g4[i].w + b4[i].w * ut;
-        }
+        const float o = kda_token<KD>(S, s_c[t], s_a[t], s_g[t], s_b[t], &s_v[t][col], &s_beta[t], &s_kq[t], row0);
         if (a.advance || t == nt - 1) {
             // slot (base + t) % depth + 1 (wrapping) when advancing, else base
             const int so = a.advance ? so_t : base;
@@ -348,45 +429,7 @@ __device__ __forceinline__ void kda_step_body(const KdaStepArgs &a, int h) {
         }
     }
     __syncthreads();
-    if (chan) {
-#pragma unroll
-        for (int t = 0; t < NT; t++)
-            if (t < nt) s_c[t][j] = s_d[t][j] * s_d[t][j];
-    }
-    __syncthreads();
-    if (tid < nt) s_oinv[tid] = d_rsqrt(d_ss_over_n(serial_sum_n<VD>(s_c[tid]), VD) + a.eps);
-    __syncthreads();
-    // gated RMSNorm over the head: ((o*inv)*w)*silu(g)  (src/ops_norm.c:749-793)
-    float yv[NT];
-#pragma unroll
-    for (int t = 0; t < NT; t++) {
-        const int tc = imin(t, nt - 1);
-        yv[t] = s_d[tc][j] * s_oinv[tc] * onw * s_z[t][j];
-    }
-    if (chan) {
-#pragma unroll
-        for (int t = 0; t < NT; t++) {
-            if (t < nt) {
-                if (a.normed_out) a.normed_out[(size_t)t * value + h * VD + j] = yv[t];
-                s_a[t][j] = yv[t];
-            }
-        }
-    }
-    __syncthreads();
-    // per-32 quantization of the output rows, four values per thread
-    const int no4 = nt * VD / 4;
-#pragma unroll
-    for (int u = 0; u < NO4; u++) {
-        const int f = u * NTHR + tid;
-        const int fc = imin(f, no4 - 1);
-        const int t = (4 * fc) / VD, c = 4 * fc - t * VD;
-        float sg;
-        const uint32_t q = quant_octet(*reinterpret_cast<const float4 *>(&s_a[t][c]), &sg);
-        if (f < no4) {
-            reinterpret_cast<uint32_t *>(a.xq + (size_t)t * value + h * VD)[c >> 2] = q;
-            if (!(c & 31)) a.xqs[(size_t)t * (value >> 5) + ((h * VD + c) >> 5)] = sg;
-        }
-    }
+    kda_gated_tail<KD, NT>(a, h, nt, j, onw, s_d, s_z, s_c, s_a, s_oinv);
 }
 
 template <int KD, int K, int NT>
@@ -426,6 +469,153 @@ __global__ __launch_bounds__(4 * KD) void k_kda_items(KdaStepArgs b, const KdaIt
         a.normed_out = b.normed_out ? b.normed_out + (size_t)r * b.value : nullptr;
         if (c0) __syncthreads();
         kda_step_body<KD, K, MAX_CHUNK>(a, blockIdx.x);
+    }
+}
+
+// One session's prefill rows (n > MAX_CHUNK, no ring advance) in three
+// launches, the same arithmetic as k_kda_items' sub-chunks:
+//   k_kda_pre  - every (MAX_CHUNK-row block, head) at once: the conv (history
+//                from the ring for the first rows, else from the rows before),
+//                the gate rows, the l2 norms, beta and k.q, i.e. everything
+//                that does not read the state, stored as one record per
+//                (row, head): [kn.g | qn.g*scale... | g | kn | v | beta, k.q];
+//   k_kda_rec  - one block per head: the token-serial recurrence over all n
+//                rows from the records, staged through LDS one block of rows
+//                ahead (the next block's records are in flight while the
+//                current block's tokens run); o to orow, the final state to
+//                the base slot;
+//   k_kda_post - every (row block, head) at once: the gated norm and the
+//                quantization for o_proj, and the conv history after the last
+//                row into the base slot (after every read of it).
+template <int KD, int K>
+__global__ __launch_bounds__(4 * KD) void k_kda_pre(KdaStepArgs b, int n) {
+    const int r = blockIdx.x * MAX_CHUNK;
+    KdaStepArgs a = b;
+    a.nt = imin(MAX_CHUNK, n - r);
+    a.hist_rows = r > 0;
+    a.pq = b.pq + (size_t)r * b.key;
+    a.pk = b.pk + (size_t)r * b.key;
+    a.pv = b.pv + (size_t)r * b.value;
+    a.pfa = b.pfa + (size_t)r * b.rank;
+    a.bvec = b.bvec + (size_t)r * b.nv;
+    a.gz = b.gz + (size_t)r * b.value;
+    a.rec = b.rec + (size_t)r * b.nv * (5 * KD + 4);
+    kda_step_body<KD, K, MAX_CHUNK, true>(a, blockIdx.y);
+}
+
+// A stage of k_kda_rec: the records of rows s0 .. s0 + MAX_CHUNK - 1 (those
+// below n) of one head, RS4 float4 each, spread over the block's threads
+// (three float4 per thread for every kd here; indices past the stage clamp
+// to its last float4); fetched into registers, later stored to the stage's
+// LDS buffer.
+template <int KD>
+struct RecStage {
+    static constexpr int RS4 = (5 * KD + 4) / 4, NTHR = 4 * KD;
+    static_assert(MAX_CHUNK * RS4 <= 3 * NTHR && MAX_CHUNK * RS4 > 2 * NTHR, "three float4 per thread");
+    float4 v0, v1, v2;
+    __device__ __forceinline__ int idx(int u, int m) const { return imin(u * NTHR + (int)threadIdx.x, m - 1); }
+    __device__ __forceinline__ float4 ld(const float *src, size_t rstride, int s0, int f) const {
+        const int t = f / RS4;
+        return reinterpret_cast<const float4 *>(src + (size_t)(s0 + t) * rstride)[f - t * RS4];
+    }
+    __device__ __forceinline__ void fetch(const float *src, size_t rstride, int s0, int n) {
+        const int m = imin(MAX_CHUNK, n - s0) * RS4;
+        v0 = ld(src, rstride, s0, idx(0, m));
+        v1 = ld(src, rstride, s0, idx(1, m));
+        v2 = ld(src, rstride, s0, idx(2, m));
+    }
+    __device__ __forceinline__ void put(float (*buf)[5 * KD + 4], int s0, int n) const {
+        const int m = imin(MAX_CHUNK, n - s0) * RS4;
+        const int f0 = idx(0, m), f1 = idx(1, m), f2 = idx(2, m);      // clamped lanes rewrite the last value
+        reinterpret_cast<float4 *>(buf[f0 / RS4])[f0 % RS4] = v0;
+        reinterpret_cast<float4 *>(buf[f1 / RS4])[f1 % RS4] = v1;
+        reinterpret_cast<float4 *>(buf[f2 / RS4])[f2 % RS4] = v2;
+    }
+};
+
+template <int KD>
+__global__ __launch_bounds__(4 * KD) void k_kda_rec(KdaStepArgs a, int n) {
+    constexpr int RPL = KD / 4, RS = 5 * KD + 4, T = MAX_CHUNK;
+    __shared__ __align__(16) float s_rec[2][T][RS];
+    const int h = blockIdx.x, tid = threadIdx.x, col = tid >> 2, row0 = (tid & 3) * RPL;
+    float *sp = a.state + (size_t)(*a.ctl_slot) * a.slot_stride + (size_t)h * KD * KD + (size_t)col * KD + row0;
+    float S[RPL];
+#pragma unroll
+    for (int i = 0; i < RPL / 4; i++) {
+        const float4 q = reinterpret_cast<const float4 *>(sp)[i];
+        S[4 * i] = q.x; S[4 * i + 1] = q.y; S[4 * i + 2] = q.z; S[4 * i + 3] = q.w;
+    }
+    const size_t rstride = (size_t)a.nv * RS;
+    const float *src = a.rec + (size_t)h * RS;
+    RecStage<KD> nb;
+    nb.fetch(src, rstride, 0, n);
+    nb.put(s_rec[0], 0, n);
+    __syncthreads();
+    const int nst = (n + T - 1) / T;
+#pragma unroll 1
+    for (int sk = 0; sk < nst; sk++) {
+        // the next stage's records are in flight while this stage runs (the
+        // last stage refetches itself into the idle buffer)
+        const int sb = sk & 1, s0 = sk * T, nt = imin(T, n - s0), sn = sk + 1 < nst ? s0 + T : s0;
+        nb.fetch(src, rstride, sn, n);
+#pragma unroll 1
+        for (int t = 0; t < nt; t++) {
+            const float *rc = s_rec[sb][t];
+            const float o = kda_token<KD>(S, rc, rc + KD, rc + 2 * KD, rc + 3 * KD, rc + 4 * KD + col, rc + 5 * KD,
+                                          rc + 5 * KD + 1, row0);
+            if ((tid & 3) == 0) {
+                const size_t oi = (size_t)(s0 + t) * a.value + (size_t)h * KD + col;
+                a.orow[oi] = o;
+                if (a.raw_out) a.raw_out[oi] = o;
+            }
+        }
+        nb.put(s_rec[sb ^ 1], sn, n);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < RPL / 4; i++)
+        reinterpret_cast<float4 *>(sp)[i] = make_float4(S[4 * i], S[4 * i + 1], S[4 * i + 2], S[4 * i + 3]);
+}
+
+template <int KD, int K>
+__global__ __launch_bounds__(4 * KD) void k_kda_post(KdaStepArgs b, int n) {
+    constexpr int VD = KD, HIST = K - 1, NT = MAX_CHUNK;
+    EXP_TAB_LOAD(tab);
+    __shared__ __align__(16) float s_o[NT][KD];
+    __shared__ __align__(16) float s_z[NT][KD];
+    __shared__ __align__(16) float s_sq[NT][KD];
+    __shared__ __align__(16) float s_y[NT][KD];
+    __shared__ float s_oinv[NT];
+    const int h = blockIdx.y, r = blockIdx.x * NT, nt = imin(NT, n - r), tid = threadIdx.x;
+    const int grp = tid / KD, j = tid - grp * KD;
+    float ov[NT / 4], zv[NT / 4];
+#pragma unroll
+    for (int i = 0; i < NT / 4; i++) {
+        const size_t ri = (size_t)(r + imin(4 * i + grp, nt - 1)) * b.value + (size_t)h * VD + j;
+        ov[i] = b.orow[ri];
+        zv[i] = b.gz[ri];
+    }
+    const float onw = b.o_norm[j];
+    EXP_TAB_PUT(tab);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < NT / 4; i++) {
+        s_o[4 * i + grp][j] = ov[i];
+        s_z[4 * i + grp][j] = d_silu(zv[i], tab);
+    }
+    __syncthreads();
+    KdaStepArgs a = b;
+    a.xq = b.xq + (size_t)r * b.value;
+    a.xqs = b.xqs + (size_t)r * (b.value >> 5);
+    a.normed_out = b.normed_out ? b.normed_out + (size_t)r * b.value : nullptr;
+    kda_gated_tail<KD, NT>(a, h, nt, j, onw, s_o, s_z, s_sq, s_y, s_oinv);
+    if (r + nt == n && grp < 3) {
+        const int cch = grp == 0 ? h * KD + j : grp == 1 ? b.key + h * KD + j : 2 * b.key + h * VD + j;
+        const float *xsrc = grp == 0 ? b.pq : grp == 1 ? b.pk : b.pv;
+        const int xstride = grp < 2 ? b.key : b.value;
+        float *r1 = b.conv_ring + (size_t)(*b.ctl_slot) * b.conv_slot_stride;
+#pragma unroll
+        for (int i = 0; i < HIST; i++) r1[(size_t)cch * HIST + i] = xsrc[(size_t)(n - HIST + i) * xstride + h * KD + j];
     }
 }
 
@@ -487,5 +677,32 @@ extern "C" int l98k_kda_items(const KdaStepArgs *a, const KdaItem *items, int n_
     default: return -1;
     }
 #undef KDA_ITEMS
+    return (int)hipGetLastError();
+}
+
+extern "C" int l98k_kda_split(const KdaStepArgs *a, int n, int kd, int K, hipStream_t st) {
+    if (n <= MAX_CHUNK || a->advance || !a->rec || !a->orow || a->rank < 32 || (a->rank & 31) ||
+        a->rank > KDA_MAX_RANK || a->key != a->nv * kd || a->value != a->nv * kd || K < 2 || K > 4)
+        return -1;
+    const dim3 rows((n + MAX_CHUNK - 1) / MAX_CHUNK, a->nv);
+#define KDA_SPLIT(KD_, K_)                                                                            \
+    do {                                                                                              \
+        hipLaunchKernelGGL((k_kda_pre<KD_, K_>), rows, dim3(4 * (KD_)), 0, st, *a, n);               \
+        hipLaunchKernelGGL((k_kda_rec<KD_>), dim3(a->nv), dim3(4 * (KD_)), 0, st, *a, n);            \
+        hipLaunchKernelGGL((k_kda_post<KD_, K_>), rows, dim3(4 * (KD_)), 0, st, *a, n);              \
+    } while (0)
+    switch (kd * 8 + K) {
+    case 64 * 8 + 4: KDA_SPLIT(64, 4); break;
+    case 64 * 8 + 3: KDA_SPLIT(64, 3); break;
+    case 64 * 8 + 2: KDA_SPLIT(64, 2); break;
+    case 128 * 8 + 4: KDA_SPLIT(128, 4); break;
+    case 128 * 8 + 3: KDA_SPLIT(128, 3); break;
+    case 128 * 8 + 2: KDA_SPLIT(128, 2); break;
+    case 32 * 8 + 4: KDA_SPLIT(32, 4); break;
+    case 32 * 8 + 3: KDA_SPLIT(32, 3); break;
+    case 32 * 8 + 2: KDA_SPLIT(32, 2); break;
+    default: return -1;
+    }
+#undef KDA_SPLIT
     return (int)hipGetLastError();
 }

@@ -92,6 +92,12 @@ int l98k_kda_step(const KdaStepArgs *a, int kd, int K, hipStream_t st);
 // memory; state_off / conv_off: the layer's offsets inside each ring slot).
 int l98k_kda_items(const KdaStepArgs *a, const KdaItem *items, int n_items, size_t state_off, size_t conv_off,
                    int kd, int K, hipStream_t st);
+// One session's prefill of n > MAX_CHUNK rows (no ring advance) as three
+// launches: the state-free work of every row and head at once, the
+// recurrence (one block per head), the gated norm and quantization of every
+// row and head at once.  a->rec and a->orow: scratch of n * nv * (5*kd + 4)
+// and n * value floats; a->state / conv_ring / ctl_slot as for one session.
+int l98k_kda_split(const KdaStepArgs *a, int n, int kd, int K, hipStream_t st);
 int l98k_attn_prep(const AttnArgs *a, int nt, hipStream_t st);
 // DSpark slot attention (mtp_attn_t1): rows slot rows of qg [rows][qg_dim]
 // and vp [rows][kv_dim]; the last row's V quantization also goes to the MTP
