@@ -168,8 +168,8 @@ typedef struct {
 typedef struct {
     int8_t *kq, *vq;                    // the session's KV planes, plane 0 base [planes][seq][kv_dim]
     float *ks, *vs;                     // their scales [planes][seq][kv_dim/32]
-    const int *ctl_pos;                 // position of the item's first row
-    int row0, n, seq_len, pad;
+    const int *ctl_pos;                 // position of the item's first row = *ctl_pos + pos_off
+    int row0, n, seq_len, pos_off;
 } AttnItem;
 
 // One session's rows of a many-session KDA launch (l98k_kda_items).

@@ -1420,11 +1420,17 @@ int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, 
     const float eps = c.rms_norm_eps;
     if (R < 1 || R > w->cap || n_items < 1 || n_items > w->cap) return 1;
     // the sessions' tables for the item launches
+    // Attention runs as one item launch per kernel: over the sessions'
+    // verify rows, or over one session's prefill rows cut into MAX_CHUNK-row
+    // items (prefill_items: their K and V rows go to the cache first, in one
+    // launch), else chunk by chunk.
     bool attn_items = n_items > 1;
+    const bool prefill_items = n_items == 1 && items[0].n > MAX_CHUNK && !advance;
+    int n_attn = n_items;
     int max_len = 1;
     {
         std::vector<KdaItem> ki((size_t)n_items);
-        std::vector<AttnItem> ai((size_t)n_items);
+        std::vector<AttnItem> ai;
         for (int i = 0; i < n_items; i++) {
             const WideItem &I = items[i];
             DState *s = I.d;
@@ -1432,19 +1438,29 @@ int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, 
             attn_items = attn_items && I.n <= MAX_CHUNK;
             max_len = I.pos0 + I.n > max_len ? I.pos0 + I.n : max_len;
             ki[i] = KdaItem{s->kda, s->conv, &s->ctl->slot_base, s->kda_slot, s->conv_slot, I.row0, I.n, s->depth, 0};
-            ai[i] = AttnItem{s->kq, s->vq, s->ks, s->vs, &s->ctl->pos_scratch, I.row0, I.n, s->seq_len, 0};
+            if (prefill_items) {
+                for (int c0 = 0; c0 < I.n; c0 += MAX_CHUNK)
+                    ai.push_back(AttnItem{s->kq, s->vq, s->ks, s->vs, &s->ctl->pos_scratch, I.row0 + c0,
+                                          I.n - c0 < MAX_CHUNK ? I.n - c0 : MAX_CHUNK, s->seq_len, c0});
+            } else {
+                ai.push_back(AttnItem{s->kq, s->vq, s->ks, s->vs, &s->ctl->pos_scratch, I.row0, I.n, s->seq_len, 0});
+            }
+        }
+        if (prefill_items) {
+            attn_items = true;
+            n_attn = (int)ai.size();
         }
         CK(hipMemcpyAsync(w->kitems, ki.data(), sizeof(KdaItem) * ki.size(), hipMemcpyHostToDevice, st));
         CK(hipMemcpyAsync(w->aitems, ai.data(), sizeof(AttnItem) * ai.size(), hipMemcpyHostToDevice, st));
     }
     const size_t att_item = (size_t)MAX_CHUNK * c.n_heads * (size_t)((max_len + 3) & ~3);
-    if (attn_items && w->att_items_floats < att_item * n_items) {
+    if (attn_items && w->att_items_floats < att_item * n_attn) {
         CK(hipStreamSynchronize(st));
         if (w->att_items) (void)hipFree(w->att_items);
         w->att_items = nullptr;
         w->att_items_floats = 0;
-        CK(hipMalloc((void **)&w->att_items, sizeof(float) * att_item * n_items));
-        w->att_items_floats = att_item * n_items;
+        CK(hipMalloc((void **)&w->att_items, sizeof(float) * att_item * n_attn));
+        w->att_items_floats = att_item * n_attn;
     }
     CK(l98k_embed(m->embed.q, m->embed.s, w->toks, d, m->embed.gs, R, w->x, st));
     const float *ra = nullptr, *rb = nullptr;
@@ -1470,7 +1486,21 @@ int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, 
                 a.kv_only = 0;
                 a.eps = eps;
                 a.attn_scale = ssm_scale(c.head_dim);
-                CK(l98k_attn_items(&a, w->aitems, n_items, plane, max_len, w->att_items, att_item, st));
+                if (prefill_items) {
+                    // every prefill row's K and V into the cache, so each item
+                    // finds the earlier items' rows there
+                    const WideItem &I = items[0];
+                    const DState *s = I.d;
+                    AttnArgs p = a;
+                    p.kv_only = 1;
+                    p.kp = w->kp + (size_t)I.row0 * kvd; p.vp = w->vp + (size_t)I.row0 * kvd;
+                    const size_t off = (size_t)plane * s->seq_len * kvd;
+                    p.kcache = s->kq + off; p.vcache = s->vq + off;
+                    p.kscale = s->ks + off / 32; p.vscale = s->vs + off / 32;
+                    p.ctl_pos = &s->ctl->pos_scratch; p.pos_off = 0;
+                    CK(l98k_attn_prep(&p, I.n, st));
+                }
+                CK(l98k_attn_items(&a, w->aitems, n_attn, plane, max_len, w->att_items, att_item, st));
             }
             for (int it = 0; it < n_items && !attn_items; it++) {
                 const WideItem &I = items[it];

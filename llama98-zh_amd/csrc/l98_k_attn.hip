@@ -223,10 +223,12 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a, float *__restri
     attn_scores_body(a, att, att_stride, blockIdx.x, blockIdx.y, blockIdx.z);
 }
 
-// One launch over several sessions' rows (the session batch's verify):
-// item i is a session's rows [row0, row0 + n) (n <= MAX_CHUNK) against its
-// own KV plane, positions *ctl_pos + t; the launch's AttnArgs carry the
-// layer's weights and the row buffers at row 0.  Block z = (item, token).
+// One launch over several sessions' rows (the session batch's verify), or
+// over one session's prefill rows cut into MAX_CHUNK-row items whose K and V
+// rows are all in the cache before the launch: item i is rows [row0, row0 +
+// n) (n <= MAX_CHUNK) against its KV plane, positions *ctl_pos + pos_off +
+// t; the launch's AttnArgs carry the layer's weights and the row buffers at
+// row 0.  Block z = (item, token).
 __device__ __forceinline__ AttnArgs attn_item_args(const AttnArgs &b, const AttnItem &it, int plane) {
     AttnArgs a = b;
     const size_t off = (size_t)plane * it.seq_len * b.kv_dim;
@@ -242,7 +244,7 @@ __device__ __forceinline__ AttnArgs attn_item_args(const AttnArgs &b, const Attn
     a.oq = b.oq + (size_t)it.row0 * b.q_dim;
     a.oqs = b.oqs + (size_t)it.row0 * (b.q_dim >> 5);
     a.ctl_pos = it.ctl_pos;
-    a.pos_off = 0;
+    a.pos_off = it.pos_off;
     return a;
 }
 
