@@ -1268,7 +1268,7 @@ int dspark_draft(DState *s, const int *toks, int k, float *out_logits, int *out_
 // MTP prefill/catch-up: K/V rows of the MTP plane from (hidden, next token)
 // pairs, chunked by MAX_CHUNK.  h: device rows [n][d]; toks: device ids;
 // positions *ctl_pos + pos_off + j.
-int mtp_prefill_dev(DState *s, const float *h, const int *toks, int n, const int *ctl_pos, int pos_off) {
+int mtp_prefill_chunked(DState *s, const float *h, const int *toks, int n, const int *ctl_pos, int pos_off) {
     const DModel *m = s->m;
     const LZModelConfig &c = m->c;
     const int d = c.hidden_size;
@@ -1318,6 +1318,8 @@ struct DWide {
     int *toks;
     float *att;
     float *kda_rec, *kda_o;   // split KDA prefill: token records [R][nv][5*kd + 4], recurrence outputs [R][value]
+    int8_t *mq;               // MTP prefill: main_proj input rows [R][2d] quantized
+    float *mqs;
     float *logits = nullptr;  // rows x vocab, sized on demand
     int logits_rows = 0;
     KdaItem *kitems;          // per-session tables of the item launches [WIDE_MAX]
@@ -1367,7 +1369,7 @@ DWide *wide_get(const DModel *cm) {
                  oki = take(sizeof(KdaItem) * R), oai = take(sizeof(AttnItem) * R),
                  oat = take(4 * (size_t)MAX_CHUNK * c.n_heads * (size_t)((c.seq_len + 3) & ~3)),
                  okr = take(4 * R * c.lin_n_v_heads * (size_t)(5 * c.lin_k_head_dim + 4)),
-                 oko = take(4 * R * c.lin_value_dim);
+                 oko = take(4 * R * c.lin_value_dim), omq = take(R * 2 * d), omqs = take(4 * R * 2 * d / 32);
     if (hipMalloc((void **)&w->arena, off) != hipSuccess) { delete w; return nullptr; }
     char *a = w->arena;
     w->cap = WIDE_MAX;
@@ -1386,6 +1388,7 @@ DWide *wide_get(const DModel *cm) {
     w->list = (int *)(a + oli); w->pair_token = (int *)(a + opt); w->toks = (int *)(a + otk);
     w->att = (float *)(a + oat);
     w->kda_rec = (float *)(a + okr); w->kda_o = (float *)(a + oko);
+    w->mq = (int8_t *)(a + omq); w->mqs = (float *)(a + omqs);
     w->kitems = (KdaItem *)(a + oki);
     w->aitems = (AttnItem *)(a + oai);
     m->wide = w;
@@ -1600,6 +1603,50 @@ int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, 
     CK(l98k_rmsnorm(w->x, d, ra, rb, m->final_norm, d, eps, R, capture, d, logits ? w->xq : nullptr, w->xqs, st));
     if (logits) CK(mf(m->embed, w->xq, w->xqs, R, logits, c.vocab_size, st));
     return 0;
+}
+
+// The MTP prefill over many rows (lz_mtp_prefill, src/forward_mtp.c:561-627)
+// with mtp_prefill_chunked's arithmetic: the main_proj input rows, fc, the
+// MTP block's input norm and K / V projections as matrix-core GEMMs, then
+// the K / V rows into the MTP plane, WIDE_MAX rows per pass.
+int mtp_prefill_wide(DState *s, DWide *w, const float *h, const int *toks, int n, const int *ctl_pos, int pos_off) {
+    const DModel *m = s->m;
+    const LZModelConfig &c = m->c;
+    const int d = c.hidden_size, kvd = c.attn_kv_dim;
+    const float eps = c.rms_norm_eps;
+    hipStream_t st = s->st;
+    for (int done = 0; done < n;) {
+        const int R = n - done < w->cap ? n - done : w->cap;
+        CK(l98k_mtp_pre(m->embed.q, m->embed.s, m->embed.gs, toks + done, h + (size_t)done * d, d, m->mtp_pre_e,
+                        m->mtp_pre_h, eps, R, w->mq, w->mqs, st));
+        CK(mf(m->mtp_fc, w->mq, w->mqs, R, w->blk, d, st));
+        CK(l98k_rmsnorm(w->blk, d, nullptr, nullptr, m->mtp.in_norm, d, eps, R, nullptr, 0, w->xq, w->xqs, st));
+        CK(mf(m->mtp.k, w->xq, w->xqs, R, w->kp, kvd, st));
+        CK(mf(m->mtp.v, w->xq, w->xqs, R, w->vp, kvd, st));
+        AttnArgs a{};
+        a.kp = w->kp; a.vp = w->vp;
+        a.k_norm = m->mtp.k_norm; a.rope_cs = m->rope_cs;
+        const size_t off = (size_t)(s->planes - 1) * s->seq_len * kvd;
+        a.kcache = s->kq + off; a.vcache = s->vq + off;
+        a.kscale = s->ks + off / 32; a.vscale = s->vs + off / 32;
+        a.ctl_pos = ctl_pos; a.pos_off = pos_off + done;
+        a.nh = c.n_heads; a.nkv = c.n_kv_heads; a.hd = c.head_dim; a.rot = c.rotary_dim;
+        a.q_dim = c.attn_q_dim; a.qg_dim = c.attn_qgate_dim; a.kv_dim = kvd;
+        a.kv_only = 1;
+        a.eps = eps;
+        CK(l98k_attn_prep(&a, R, st));
+        done += R;
+    }
+    return 0;
+}
+
+// The MTP prefill / catch-up of n rows: the many-row form for a prefill (n
+// >= WIDE_MIN, a model the many-row forward carries), else MAX_CHUNK rows at
+// a time.
+int mtp_prefill_dev(DState *s, const float *h, const int *toks, int n, const int *ctl_pos, int pos_off) {
+    DWide *w = n >= WIDE_MIN ? wide_get(s->m) : nullptr;
+    if (w) return mtp_prefill_wide(s, w, h, toks, n, ctl_pos, pos_off);
+    return mtp_prefill_chunked(s, h, toks, n, ctl_pos, pos_off);
 }
 
 }  // namespace
