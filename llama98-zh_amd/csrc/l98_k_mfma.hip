@@ -17,6 +17,13 @@
 // A[l % 16][8 (l / 16) .. +8) and B[8 (l / 16) .. +8)[l % 16] as eight
 // bytes each, and receives D[4 (l / 16) + v][l % 16] in result register v.
 // A is the weight tile (rows), B the activation tile (tokens).
+//
+// A block computes 64 weight rows x 64 token columns (a wave per 16
+// columns).  K goes through LDS in stages of MF_KC bytes (eight groups),
+// double-buffered: each thread loads its 16-byte pieces of the next stage
+// (coalesced: 16 threads per 256-byte row) while the block's MFMAs run on
+// the current one, so a stage costs one memory round trip overlapped with
+// compute instead of one per group batch.
 #include "l98_devmath.h"
 
 typedef int v4i_t __attribute__((ext_vector_type(4)));
@@ -24,7 +31,8 @@ typedef int v4i_t __attribute__((ext_vector_type(4)));
 #define MF_THREADS 256
 #define MF_ROWS 64        // weight rows per block (four 16-row MFMA tiles per wave)
 #define MF_COLS 64        // token columns per block (16 per wave)
-#define MF_GU 4           // groups whose operands are loaded ahead of their MFMAs
+#define MF_KC 256         // K bytes (eight groups) per LDS stage
+#define MF_LDS_ROW (MF_KC + 16)   // padded stage row: the lanes' 8-byte operand reads spread over the banks
 
 // Columns of a launch: dense (column t is activation row t and output row
 // t, t < M) or grouped (block z is group g: expert gexp[g], columns
@@ -37,12 +45,49 @@ struct MfCols {
 
 __device__ __forceinline__ long ld8(const int8_t *p) { return *reinterpret_cast<const long *>(p); }
 
+// One LDS stage of k_mfma_q8 in a thread's registers: its four 16-byte
+// pieces of weight rows and of activation columns, and its B column's eight
+// group scales (named members, so they stay in registers across the stage
+// loop).
+static_assert(MF_KC == 256, "MfStage holds eight group scales");
+struct MfStage {
+    int4 w0, w1, w2, w3, x0, x1, x2, x3;
+    float s0, s1, s2, s3, s4, s5, s6, s7;
+    __device__ __forceinline__ void load(const int8_t *const (&wl)[4], const int8_t *const (&xl)[4],
+                                         const float *xsp, int st, int pc, int K, int nb) {
+        const int off = imin(st * MF_KC + 16 * pc, K - 16);
+        w0 = *reinterpret_cast<const int4 *>(wl[0] + off);
+        w1 = *reinterpret_cast<const int4 *>(wl[1] + off);
+        w2 = *reinterpret_cast<const int4 *>(wl[2] + off);
+        w3 = *reinterpret_cast<const int4 *>(wl[3] + off);
+        x0 = *reinterpret_cast<const int4 *>(xl[0] + off);
+        x1 = *reinterpret_cast<const int4 *>(xl[1] + off);
+        x2 = *reinterpret_cast<const int4 *>(xl[2] + off);
+        x3 = *reinterpret_cast<const int4 *>(xl[3] + off);
+        const int g0 = st * (MF_KC / 32), gl = nb - 1;
+        s0 = xsp[imin(g0, gl)]; s1 = xsp[imin(g0 + 1, gl)]; s2 = xsp[imin(g0 + 2, gl)]; s3 = xsp[imin(g0 + 3, gl)];
+        s4 = xsp[imin(g0 + 4, gl)]; s5 = xsp[imin(g0 + 5, gl)]; s6 = xsp[imin(g0 + 6, gl)]; s7 = xsp[imin(g0 + 7, gl)];
+    }
+    __device__ __forceinline__ void put(int8_t (*sw)[MF_LDS_ROW], int8_t (*sx)[MF_LDS_ROW], int rr, int pc) const {
+        *reinterpret_cast<int4 *>(&sw[rr][16 * pc]) = w0;
+        *reinterpret_cast<int4 *>(&sw[rr + 16][16 * pc]) = w1;
+        *reinterpret_cast<int4 *>(&sw[rr + 32][16 * pc]) = w2;
+        *reinterpret_cast<int4 *>(&sw[rr + 48][16 * pc]) = w3;
+        *reinterpret_cast<int4 *>(&sx[rr][16 * pc]) = x0;
+        *reinterpret_cast<int4 *>(&sx[rr + 16][16 * pc]) = x1;
+        *reinterpret_cast<int4 *>(&sx[rr + 32][16 * pc]) = x2;
+        *reinterpret_cast<int4 *>(&sx[rr + 48][16 * pc]) = x3;
+    }
+};
+
 __global__ __launch_bounds__(MF_THREADS) void k_mfma_q8(const int8_t *__restrict__ W, const float *__restrict__ ws,
                                                          int N, int K, size_t w_group_stride,
                                                          const int8_t *__restrict__ X, const float *__restrict__ Xs,
                                                          int M, MfCols cols, float *__restrict__ out,
                                                          int out_stride) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    __shared__ __align__(16) int8_t s_w[2][MF_ROWS][MF_LDS_ROW];
+    __shared__ __align__(16) int8_t s_x[2][MF_COLS][MF_LDS_ROW];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int n0 = blockIdx.x * MF_ROWS, c0 = blockIdx.y * MF_COLS;
     const int nb = K >> 5;
     int ncols = M, cbase = 0;
@@ -67,58 +112,66 @@ __global__ __launch_bounds__(MF_THREADS) void k_mfma_q8(const int8_t *__restrict
         xrow = cols.xmap ? cols.xmap[orow] : orow;
     }
     const int kq = 8 * (lane >> 4);
-    const int8_t *xp = X + (size_t)xrow * K + kq;
     const float *xsp = Xs + (size_t)xrow * nb;
-    const int8_t *wp[4];
+    // Stage loads: thread t takes the 16-byte piece pc of weight rows and
+    // activation columns rr + 16 j of the block (j < 4): every row's
+    // MF_KC-byte stage is read by 16 consecutive threads.  Rows past N and
+    // columns past ncols repeat the last; pieces past K repeat the row's
+    // last piece (their groups are not used).
+    const int pc = tid & 15, rr = tid >> 4;
+    const int8_t *wl[4], *xl[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int r = n0 + 16 * i + (lane & 15);
-        wp[i] = Wg + (size_t)(r < N ? r : N - 1) * K + kq;
+    for (int j = 0; j < 4; j++) {
+        const int r = n0 + rr + 16 * j;
+        wl[j] = Wg + (size_t)(r < N ? r : N - 1) * K;
+        const int c = imin(c0 + rr + 16 * j, ncols - 1);
+        int xr = c;
+        if (cols.list) {
+            const int o = cols.list[cbase + c];
+            xr = cols.xmap ? cols.xmap[o] : o;
+        }
+        xl[j] = X + (size_t)xr * K;
     }
+    const int nst = (K + MF_KC - 1) / MF_KC;
+    MfStage nx;
     float f[4][4];
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int v = 0; v < 4; v++) f[i][v] = 0.0f;
     const v4i_t zero = {0, 0, 0, 0};
-    int g = 0;
-    for (; g + MF_GU <= nb; g += MF_GU) {
-        long a[MF_GU][4], b[MF_GU];
-        float s[MF_GU];
-#pragma unroll
-        for (int u = 0; u < MF_GU; u++) {
-#pragma unroll
-            for (int i = 0; i < 4; i++) a[u][i] = ld8(wp[i] + 32 * (g + u));
-            b[u] = ld8(xp + 32 * (g + u));
-            s[u] = xsp[g + u];
-        }
-#pragma unroll
-        for (int u = 0; u < MF_GU; u++) {
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const v4i_t d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[u][i], b[u], zero, 0, 0, 0);
-#pragma unroll
-                for (int v = 0; v < 4; v++) f[i][v] += (float)d[v] * s[u];
-            }
-        }
-    }
     // one group (K == 32): f holds the exact group sum (|acc| < 2^24) for
     // epi_one_group's association
     const bool one = nb == 1;
     float s0 = 0.0f;
-    for (; g < nb; g++) {
-        long a[4];
+    nx.load(wl, xl, xsp, 0, pc, K, nb);
+    nx.put(s_w[0], s_x[0], rr, pc);
+    __syncthreads();
+#pragma unroll 1
+    for (int st = 0; st < nst; st++) {
+        const int buf = st & 1;
+        const float sc[MF_KC / 32] = {nx.s0, nx.s1, nx.s2, nx.s3, nx.s4, nx.s5, nx.s6, nx.s7};
+        // the next stage's loads are in flight during this stage's MFMAs (the
+        // last stage reloads itself into the idle buffer)
+        nx.load(wl, xl, xsp, st + 1 < nst ? st + 1 : st, pc, K, nb);
 #pragma unroll
-        for (int i = 0; i < 4; i++) a[i] = ld8(wp[i] + 32 * g);
-        const long b = ld8(xp + 32 * g);
-        const float s = xsp[g];
-        s0 = s;
+        for (int gl = 0; gl < MF_KC / 32; gl++) {
+            if (st * (MF_KC / 32) + gl >= nb) break;          // uniform
+            long a[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const v4i_t d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[i], b, zero, 0, 0, 0);
+            for (int i = 0; i < 4; i++) a[i] = *reinterpret_cast<const long *>(&s_w[buf][16 * i + (lane & 15)][32 * gl + kq]);
+            const long b = *reinterpret_cast<const long *>(&s_x[buf][16 * wave + (lane & 15)][32 * gl + kq]);
+            const float s = sc[gl];
+            s0 = s;
 #pragma unroll
-            for (int v = 0; v < 4; v++) f[i][v] += one ? (float)d[v] : (float)d[v] * s;
+            for (int i = 0; i < 4; i++) {
+                const v4i_t d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[i], b, zero, 0, 0, 0);
+#pragma unroll
+                for (int v = 0; v < 4; v++) f[i][v] += one ? (float)d[v] : (float)d[v] * s;
+            }
         }
+        nx.put(s_w[buf ^ 1], s_x[buf ^ 1], rr, pc);
+        __syncthreads();
     }
     if (cl >= ncols) return;
     float *op = out + (size_t)orow * out_stride;

@@ -23,7 +23,8 @@ def case(rng, N, K, M):
 
 
 @pytest.mark.parametrize("N,K,M", [(64, 32, 1), (100, 96, 70), (1024, 1024, 512), (2048, 1024, 33),
-                                   (16, 64, 128), (8192, 256, 128), (768, 512, 65), (4096, 4096, 8)])
+                                   (16, 64, 128), (8192, 256, 128), (768, 512, 65), (4096, 4096, 8),
+                                   (256, 768, 100), (130, 2080, 64)])
 def test_mfma_gemm_bit_exact(pkg, N, K, M):
     rng = np.random.default_rng(N * 7 + K + M)
     w, ws, x, xs = case(rng, N, K, M)
