@@ -88,7 +88,7 @@ __global__ __launch_bounds__(MF_THREADS) void k_mfma_q8(const int8_t *__restrict
     __shared__ __align__(16) int8_t s_w[2][MF_ROWS][MF_LDS_ROW];
     __shared__ __align__(16) int8_t s_x[2][MF_COLS][MF_LDS_ROW];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int n0 = blockIdx.x * MF_ROWS, c0 = blockIdx.y * MF_COLS;
+    const int n0 = blockIdx.x * MF_ROWS;
     const int nb = K >> 5;
     int ncols = M, cbase = 0;
     const int8_t *Wg = W;
@@ -102,89 +102,96 @@ __global__ __launch_bounds__(MF_THREADS) void k_mfma_q8(const int8_t *__restrict
         Wg = W + (size_t)e * w_group_stride;
         wsg = ws + (size_t)e * N;
     }
-    if (c0 >= ncols) return;
-    // this lane's B column and its activation / output rows
-    const int cl = c0 + 16 * wave + (lane & 15);
-    const int cc = cl < ncols ? cl : ncols - 1;
-    int orow = cc, xrow = cc;
-    if (cols.list) {
-        orow = cols.list[cbase + cc];
-        xrow = cols.xmap ? cols.xmap[orow] : orow;
-    }
-    const int kq = 8 * (lane >> 4);
-    const float *xsp = Xs + (size_t)xrow * nb;
-    // Stage loads: thread t takes the 16-byte piece pc of weight rows and
-    // activation columns rr + 16 j of the block (j < 4): every row's
-    // MF_KC-byte stage is read by 16 consecutive threads.  Rows past N and
-    // columns past ncols repeat the last; pieces past K repeat the row's
-    // last piece (their groups are not used).
-    const int pc = tid & 15, rr = tid >> 4;
-    const int8_t *wl[4], *xl[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int r = n0 + rr + 16 * j;
-        wl[j] = Wg + (size_t)(r < N ? r : N - 1) * K;
-        const int c = imin(c0 + rr + 16 * j, ncols - 1);
-        int xr = c;
-        if (cols.list) {
-            const int o = cols.list[cbase + c];
-            xr = cols.xmap ? cols.xmap[o] : o;
-        }
-        xl[j] = X + (size_t)xr * K;
-    }
-    const int nst = (K + MF_KC - 1) / MF_KC;
-    MfStage nx;
-    float f[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int v = 0; v < 4; v++) f[i][v] = 0.0f;
-    const v4i_t zero = {0, 0, 0, 0};
-    // one group (K == 32): f holds the exact group sum (|acc| < 2^24) for
-    // epi_one_group's association
-    const bool one = nb == 1;
-    float s0 = 0.0f;
-    nx.load(wl, xl, xsp, 0, pc, K, nb);
-    nx.put(s_w[0], s_x[0], rr, pc);
-    __syncthreads();
+    // column tiles blockIdx.y, + gridDim.y, ... (a grouped launch has one
+    // block row per group, which walks the group's tiles)
 #pragma unroll 1
-    for (int st = 0; st < nst; st++) {
-        const int buf = st & 1;
-        const float sc[MF_KC / 32] = {nx.s0, nx.s1, nx.s2, nx.s3, nx.s4, nx.s5, nx.s6, nx.s7};
-        // the next stage's loads are in flight during this stage's MFMAs (the
-        // last stage reloads itself into the idle buffer)
-        nx.load(wl, xl, xsp, st + 1 < nst ? st + 1 : st, pc, K, nb);
+    for (int c0 = blockIdx.y * MF_COLS; c0 < ncols; c0 += gridDim.y * MF_COLS) {
+        // this lane's B column and its activation / output rows
+        const int cl = c0 + 16 * wave + (lane & 15);
+        const int cc = cl < ncols ? cl : ncols - 1;
+        int orow = cc, xrow = cc;
+        if (cols.list) {
+            orow = cols.list[cbase + cc];
+            xrow = cols.xmap ? cols.xmap[orow] : orow;
+        }
+        const int kq = 8 * (lane >> 4);
+        const float *xsp = Xs + (size_t)xrow * nb;
+        // Stage loads: thread t takes the 16-byte piece pc of weight rows and
+        // activation columns rr + 16 j of the block (j < 4): every row's
+        // MF_KC-byte stage is read by 16 consecutive threads.  Rows past N and
+        // columns past ncols repeat the last; pieces past K repeat the row's
+        // last piece (their groups are not used).
+        const int pc = tid & 15, rr = tid >> 4;
+        const int8_t *wl[4], *xl[4];
 #pragma unroll
-        for (int gl = 0; gl < MF_KC / 32; gl++) {
-            if (st * (MF_KC / 32) + gl >= nb) break;          // uniform
-            long a[4];
+        for (int j = 0; j < 4; j++) {
+            const int r = n0 + rr + 16 * j;
+            wl[j] = Wg + (size_t)(r < N ? r : N - 1) * K;
+            const int c = imin(c0 + rr + 16 * j, ncols - 1);
+            int xr = c;
+            if (cols.list) {
+                const int o = cols.list[cbase + c];
+                xr = cols.xmap ? cols.xmap[o] : o;
+            }
+            xl[j] = X + (size_t)xr * K;
+        }
+        const int nst = (K + MF_KC - 1) / MF_KC;
+        MfStage nx;
+        float f[4][4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) a[i] = *reinterpret_cast<const long *>(&s_w[buf][16 * i + (lane & 15)][32 * gl + kq]);
-            const long b = *reinterpret_cast<const long *>(&s_x[buf][16 * wave + (lane & 15)][32 * gl + kq]);
-            const float s = sc[gl];
-            s0 = s;
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) f[i][v] = 0.0f;
+        const v4i_t zero = {0, 0, 0, 0};
+        // one group (K == 32): f holds the exact group sum (|acc| < 2^24) for
+        // epi_one_group's association
+        const bool one = nb == 1;
+        float s0 = 0.0f;
+        nx.load(wl, xl, xsp, 0, pc, K, nb);
+        nx.put(s_w[0], s_x[0], rr, pc);
+        __syncthreads();
+#pragma unroll 1
+        for (int st = 0; st < nst; st++) {
+            const int buf = st & 1;
+            const float sc[MF_KC / 32] = {nx.s0, nx.s1, nx.s2, nx.s3, nx.s4, nx.s5, nx.s6, nx.s7};
+            // the next stage's loads are in flight during this stage's MFMAs (the
+            // last stage reloads itself into the idle buffer)
+            nx.load(wl, xl, xsp, st + 1 < nst ? st + 1 : st, pc, K, nb);
+#pragma unroll
+            for (int gl = 0; gl < MF_KC / 32; gl++) {
+                if (st * (MF_KC / 32) + gl >= nb) break;          // uniform
+                long a[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) a[i] = *reinterpret_cast<const long *>(&s_w[buf][16 * i + (lane & 15)][32 * gl + kq]);
+                const long b = *reinterpret_cast<const long *>(&s_x[buf][16 * wave + (lane & 15)][32 * gl + kq]);
+                const float s = sc[gl];
+                s0 = s;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const v4i_t d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[i], b, zero, 0, 0, 0);
+#pragma unroll
+                    for (int v = 0; v < 4; v++) f[i][v] += one ? (float)d[v] : (float)d[v] * s;
+                }
+            }
+            nx.put(s_w[buf ^ 1], s_x[buf ^ 1], rr, pc);
+            __syncthreads();
+        }
+        // (after the last stage's barrier no wave reads this tile's LDS, so the
+        // next tile may refill it)
+        if (cl < ncols) {
+            float *op = out + (size_t)orow * out_stride;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const v4i_t d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[i], b, zero, 0, 0, 0);
 #pragma unroll
-                for (int v = 0; v < 4; v++) f[i][v] += one ? (float)d[v] : (float)d[v] * s;
-            }
-        }
-        nx.put(s_w[buf ^ 1], s_x[buf ^ 1], rr, pc);
-        __syncthreads();
-    }
-    if (cl >= ncols) return;
-    float *op = out + (size_t)orow * out_stride;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-#pragma unroll
-        for (int v = 0; v < 4; v++) {
-            const int n = n0 + 16 * i + 4 * (lane >> 4) + v;
-            if (n < N) {
-                float sum = 0.0f;
-                if (one) sum = epi_one_group((int)f[i][v], s0, wsg[n]);
-                else sum += f[i][v] * wsg[n];
-                op[n] = sum;
+                for (int v = 0; v < 4; v++) {
+                    const int n = n0 + 16 * i + 4 * (lane >> 4) + v;
+                    if (n < N) {
+                        float sum = 0.0f;
+                        if (one) sum = epi_one_group((int)f[i][v], s0, wsg[n]);
+                        else sum += f[i][v] * wsg[n];
+                        op[n] = sum;
+                    }
+                }
             }
         }
     }
@@ -273,8 +280,7 @@ extern "C" int l98k_mfma_gemm_grouped(const int8_t *bank, const float *bank_s, i
                                       int max_cols, float *out, int out_stride, hipStream_t st) {
     if (N < 1 || K < 32 || (K & 31) || max_groups < 1 || max_cols < 1 || out_stride < N) return -1;
     MfCols c{gexp, goff, gcnt, list, xmap, ng};
-    hipLaunchKernelGGL(k_mfma_q8,
-                       dim3((N + MF_ROWS - 1) / MF_ROWS, (max_cols + MF_COLS - 1) / MF_COLS, max_groups),
+    hipLaunchKernelGGL(k_mfma_q8, dim3((N + MF_ROWS - 1) / MF_ROWS, 1, max_groups),
                        dim3(MF_THREADS), 0, st, bank, bank_s, N, K, (size_t)N * K, X, Xs, 0, c, out, out_stride);
     return (int)hipGetLastError();
 }
