@@ -18,8 +18,9 @@
 // bytes each, and receives D[4 (l / 16) + v][l % 16] in result register v.
 // A is the weight tile (rows), B the activation tile (tokens).
 //
-// A block computes 64 weight rows x 64 token columns (a wave per 16
-// columns).  K goes through LDS in stages of MF_KC bytes (eight groups),
+// A block computes MF_ROWS = 16 MF_RT weight rows x 64 token columns (a
+// wave per 16 columns, MF_RT 16-row MFMA tiles each; two tiles keep a
+// wave's per-group fp32 fold short and give a 1024-row GEMM a block per CU).  K goes through LDS in stages of MF_KC bytes (eight groups),
 // double-buffered: each thread loads its 16-byte pieces of the next stage
 // (coalesced: 16 threads per 256-byte row) while the block's MFMAs run on
 // the current one, so a stage costs one memory round trip overlapped with
@@ -29,7 +30,8 @@
 typedef int v4i_t __attribute__((ext_vector_type(4)));
 
 #define MF_THREADS 256
-#define MF_ROWS 64        // weight rows per block (four 16-row MFMA tiles per wave)
+#define MF_RT 2           // 16-row MFMA tiles per wave
+#define MF_ROWS (16 * MF_RT)  // weight rows per block
 #define MF_COLS 64        // token columns per block (16 per wave)
 #define MF_KC 256         // K bytes (eight groups) per LDS stage
 #define MF_LDS_ROW (MF_KC + 16)   // padded stage row: the lanes' 8-byte operand reads spread over the banks
@@ -45,41 +47,82 @@ struct MfCols {
 
 __device__ __forceinline__ long ld8(const int8_t *p) { return *reinterpret_cast<const long *>(p); }
 
-// One LDS stage of k_mfma_q8 in a thread's registers: its four 16-byte
-// pieces of weight rows and of activation columns, and its B column's eight
-// group scales (named members, so they stay in registers across the stage
-// loop).
-static_assert(MF_KC == 256, "MfStage holds eight group scales");
-struct MfStage {
-    int4 w0, w1, w2, w3, x0, x1, x2, x3;
-    float s0, s1, s2, s3, s4, s5, s6, s7;
-    __device__ __forceinline__ void load(const int8_t *const (&wl)[4], const int8_t *const (&xl)[4],
-                                         const float *xsp, int st, int pc, int K, int nb) {
-        const int off = imin(st * MF_KC + 16 * pc, K - 16);
-        w0 = *reinterpret_cast<const int4 *>(wl[0] + off);
-        w1 = *reinterpret_cast<const int4 *>(wl[1] + off);
-        w2 = *reinterpret_cast<const int4 *>(wl[2] + off);
-        w3 = *reinterpret_cast<const int4 *>(wl[3] + off);
-        x0 = *reinterpret_cast<const int4 *>(xl[0] + off);
-        x1 = *reinterpret_cast<const int4 *>(xl[1] + off);
-        x2 = *reinterpret_cast<const int4 *>(xl[2] + off);
-        x3 = *reinterpret_cast<const int4 *>(xl[3] + off);
-        const int g0 = st * (MF_KC / 32), gl = nb - 1;
-        s0 = xsp[imin(g0, gl)]; s1 = xsp[imin(g0 + 1, gl)]; s2 = xsp[imin(g0 + 2, gl)]; s3 = xsp[imin(g0 + 3, gl)];
-        s4 = xsp[imin(g0 + 4, gl)]; s5 = xsp[imin(g0 + 5, gl)]; s6 = xsp[imin(g0 + 6, gl)]; s7 = xsp[imin(g0 + 7, gl)];
-    }
-    __device__ __forceinline__ void put(int8_t (*sw)[MF_LDS_ROW], int8_t (*sx)[MF_LDS_ROW], int rr, int pc) const {
-        *reinterpret_cast<int4 *>(&sw[rr][16 * pc]) = w0;
-        *reinterpret_cast<int4 *>(&sw[rr + 16][16 * pc]) = w1;
-        *reinterpret_cast<int4 *>(&sw[rr + 32][16 * pc]) = w2;
-        *reinterpret_cast<int4 *>(&sw[rr + 48][16 * pc]) = w3;
-        *reinterpret_cast<int4 *>(&sx[rr][16 * pc]) = x0;
-        *reinterpret_cast<int4 *>(&sx[rr + 16][16 * pc]) = x1;
-        *reinterpret_cast<int4 *>(&sx[rr + 32][16 * pc]) = x2;
-        *reinterpret_cast<int4 *>(&sx[rr + 48][16 * pc]) = x3;
-    }
-};
+// One LDS stage of k_mfma_q8 in a thread's registers (set R: Aw0 .. At1):
+// its four 16-byte pieces of weight rows and of activation
+// columns, and two of the block's 64 x 8 activation group scales (column
+// tid / 4, groups 2 (tid % 4) and the next).  Plain locals (a struct would
+// be kept in scratch memory across the scheduling barriers that hold the
+// loads' issue in place).
+static_assert(MF_KC == 256 && MF_THREADS == 256, "a stage: eight group scales per column, two per thread");
+#define MF_STAGE_LOAD(R, st_)                                                                  \
+    do {                                                                                       \
+        const int off_ = imin((st_) * MF_KC + 16 * pc, K - 16);                                \
+        R##w0 = *reinterpret_cast<const int4 *>(wl0 + off_);                                   \
+        R##w1 = *reinterpret_cast<const int4 *>(wl1 + off_);                                   \
+        if constexpr (MF_RT == 4) {                                                            \
+            R##w2 = *reinterpret_cast<const int4 *>(wl2 + off_);                               \
+            R##w3 = *reinterpret_cast<const int4 *>(wl3 + off_);                               \
+        }                                                                                      \
+        R##x0 = *reinterpret_cast<const int4 *>(xl0 + off_);                                   \
+        R##x1 = *reinterpret_cast<const int4 *>(xl1 + off_);                                   \
+        R##x2 = *reinterpret_cast<const int4 *>(xl2 + off_);                                   \
+        R##x3 = *reinterpret_cast<const int4 *>(xl3 + off_);                                   \
+        const int g_ = (st_) * (MF_KC / 32) + 2 * (tid & 3);                                   \
+        R##t0 = xsl[imin(g_, nb - 1)];                                                         \
+        R##t1 = xsl[imin(g_ + 1, nb - 1)];                                                     \
+    } while (0)
+#define MF_STAGE_PUT(R, b_)                                                                    \
+    do {                                                                                       \
+        *reinterpret_cast<int4 *>(&s_w[b_][rr][16 * pc]) = R##w0;                              \
+        *reinterpret_cast<int4 *>(&s_w[b_][rr + 16][16 * pc]) = R##w1;                         \
+        if constexpr (MF_RT == 4) {                                                            \
+            *reinterpret_cast<int4 *>(&s_w[b_][rr + 32][16 * pc]) = R##w2;                     \
+            *reinterpret_cast<int4 *>(&s_w[b_][rr + 48][16 * pc]) = R##w3;                     \
+        }                                                                                      \
+        *reinterpret_cast<int4 *>(&s_x[b_][rr][16 * pc]) = R##x0;                              \
+        *reinterpret_cast<int4 *>(&s_x[b_][rr + 16][16 * pc]) = R##x1;                         \
+        *reinterpret_cast<int4 *>(&s_x[b_][rr + 32][16 * pc]) = R##x2;                         \
+        *reinterpret_cast<int4 *>(&s_x[b_][rr + 48][16 * pc]) = R##x3;                         \
+        *reinterpret_cast<float2 *>(&s_xs[b_][tid >> 2][2 * (tid & 3)]) = make_float2(R##t0, R##t1); \
+    } while (0)
 
+__device__ __forceinline__ void mf_fold(float (&f)[4], v4i_t d, float s, bool one) {
+    f[0] += one ? (float)d[0] : (float)d[0] * s;
+    f[1] += one ? (float)d[1] : (float)d[1] * s;
+    f[2] += one ? (float)d[2] : (float)d[2] * s;
+    f[3] += one ? (float)d[3] : (float)d[3] * s;
+}
+template <bool FULL>
+__device__ __forceinline__ void mf_stage(float (&f)[MF_RT][4], const int8_t (*sw)[MF_LDS_ROW],
+                                         const int8_t (*sx)[MF_LDS_ROW], const float *sc, int ng, bool one,
+                                         int wave, int lane, int kq) {
+    const v4i_t zero = {0, 0, 0, 0};
+#pragma unroll
+    for (int gl = 0; gl < MF_KC / 32; gl++) {
+        if (!FULL && gl >= ng) break;                  // uniform
+        const long b = *reinterpret_cast<const long *>(&sx[16 * wave + (lane & 15)][32 * gl + kq]);
+        const long a0 = *reinterpret_cast<const long *>(&sw[(lane & 15)][32 * gl + kq]);
+        const long a1 = *reinterpret_cast<const long *>(&sw[16 + (lane & 15)][32 * gl + kq]);
+        const v4i_t d0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, b, zero, 0, 0, 0);
+        const v4i_t d1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, b, zero, 0, 0, 0);
+        const float s = sc[gl];
+        if constexpr (MF_RT == 4) {
+            const long a2 = *reinterpret_cast<const long *>(&sw[32 + (lane & 15)][32 * gl + kq]);
+            const long a3 = *reinterpret_cast<const long *>(&sw[48 + (lane & 15)][32 * gl + kq]);
+            const v4i_t d2 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a2, b, zero, 0, 0, 0);
+            const v4i_t d3 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a3, b, zero, 0, 0, 0);
+            mf_fold(f[0], d0, s, one);
+            mf_fold(f[1], d1, s, one);
+            mf_fold(f[MF_RT - 2], d2, s, one);
+            mf_fold(f[MF_RT - 1], d3, s, one);
+        } else {
+            mf_fold(f[0], d0, s, one);
+            mf_fold(f[1], d1, s, one);
+        }
+    }
+}
+
+template <bool FULLK>
 __global__ __launch_bounds__(MF_THREADS) void k_mfma_q8(const int8_t *__restrict__ W, const float *__restrict__ ws,
                                                          int N, int K, size_t w_group_stride,
                                                          const int8_t *__restrict__ X, const float *__restrict__ Xs,
@@ -87,6 +130,7 @@ __global__ __launch_bounds__(MF_THREADS) void k_mfma_q8(const int8_t *__restrict
                                                          int out_stride) {
     __shared__ __align__(16) int8_t s_w[2][MF_ROWS][MF_LDS_ROW];
     __shared__ __align__(16) int8_t s_x[2][MF_COLS][MF_LDS_ROW];
+    __shared__ __align__(16) float s_xs[2][MF_COLS][MF_KC / 32];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int n0 = blockIdx.x * MF_ROWS;
     const int nb = K >> 5;
@@ -106,74 +150,75 @@ __global__ __launch_bounds__(MF_THREADS) void k_mfma_q8(const int8_t *__restrict
     // block row per group, which walks the group's tiles)
 #pragma unroll 1
     for (int c0 = blockIdx.y * MF_COLS; c0 < ncols; c0 += gridDim.y * MF_COLS) {
-        // this lane's B column and its activation / output rows
+        // this lane's B column and its output row
         const int cl = c0 + 16 * wave + (lane & 15);
         const int cc = cl < ncols ? cl : ncols - 1;
-        int orow = cc, xrow = cc;
-        if (cols.list) {
-            orow = cols.list[cbase + cc];
-            xrow = cols.xmap ? cols.xmap[orow] : orow;
-        }
+        const int orow = cols.list ? cols.list[cbase + cc] : cc;
         const int kq = 8 * (lane >> 4);
-        const float *xsp = Xs + (size_t)xrow * nb;
-        // Stage loads: thread t takes the 16-byte piece pc of weight rows and
-        // activation columns rr + 16 j of the block (j < 4): every row's
+        // Stage loads: thread t takes the 16-byte piece pc of weight rows
+        // rr + 16 j (j < MF_RT) and activation columns rr + 16 j (j < 4) of
+        // the block: every row's
         // MF_KC-byte stage is read by 16 consecutive threads.  Rows past N and
         // columns past ncols repeat the last; pieces past K repeat the row's
         // last piece (their groups are not used).
         const int pc = tid & 15, rr = tid >> 4;
-        const int8_t *wl[4], *xl[4];
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int r = n0 + rr + 16 * j;
-            wl[j] = Wg + (size_t)(r < N ? r : N - 1) * K;
+        auto wrow = [&](int j) { const int r = n0 + rr + 16 * j; return Wg + (size_t)(r < N ? r : N - 1) * K; };
+        auto xcol = [&](int j) {
             const int c = imin(c0 + rr + 16 * j, ncols - 1);
             int xr = c;
             if (cols.list) {
                 const int o = cols.list[cbase + c];
                 xr = cols.xmap ? cols.xmap[o] : o;
             }
-            xl[j] = X + (size_t)xr * K;
+            return X + (size_t)xr * K;
+        };
+        const int8_t *wl0 = wrow(0), *wl1 = wrow(1), *wl2 = wrow(MF_RT - 2), *wl3 = wrow(MF_RT - 1);
+        const int8_t *xl0 = xcol(0), *xl1 = xcol(1), *xl2 = xcol(2), *xl3 = xcol(3);
+        // the activation scales this thread stages: column tid / 4
+        const float *xsl;
+        {
+            const int c = imin(c0 + (tid >> 2), ncols - 1);
+            int xr = c;
+            if (cols.list) {
+                const int o = cols.list[cbase + c];
+                xr = cols.xmap ? cols.xmap[o] : o;
+            }
+            xsl = Xs + (size_t)xr * nb;
         }
         const int nst = (K + MF_KC - 1) / MF_KC;
-        MfStage nx;
-        float f[4][4];
+        int4 Aw0, Aw1, Aw2 = {}, Aw3 = {}, Ax0, Ax1, Ax2, Ax3;
+        float At0, At1;
+        float f[MF_RT][4];
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+        for (int i = 0; i < MF_RT; i++)
 #pragma unroll
             for (int v = 0; v < 4; v++) f[i][v] = 0.0f;
-        const v4i_t zero = {0, 0, 0, 0};
         // one group (K == 32): f holds the exact group sum (|acc| < 2^24) for
         // epi_one_group's association
         const bool one = nb == 1;
         float s0 = 0.0f;
-        nx.load(wl, xl, xsp, 0, pc, K, nb);
-        nx.put(s_w[0], s_x[0], rr, pc);
+        MF_STAGE_LOAD(A, 0);
+        MF_STAGE_PUT(A, 0);
         __syncthreads();
 #pragma unroll 1
         for (int st = 0; st < nst; st++) {
             const int buf = st & 1;
-            const float sc[MF_KC / 32] = {nx.s0, nx.s1, nx.s2, nx.s3, nx.s4, nx.s5, nx.s6, nx.s7};
+            const float *sc = s_xs[buf][16 * wave + (lane & 15)];
             // the next stage's loads are in flight during this stage's MFMAs (the
-            // last stage reloads itself into the idle buffer)
-            nx.load(wl, xl, xsp, st + 1 < nst ? st + 1 : st, pc, K, nb);
-#pragma unroll
-            for (int gl = 0; gl < MF_KC / 32; gl++) {
-                if (st * (MF_KC / 32) + gl >= nb) break;          // uniform
-                long a[4];
-#pragma unroll
-                for (int i = 0; i < 4; i++) a[i] = *reinterpret_cast<const long *>(&s_w[buf][16 * i + (lane & 15)][32 * gl + kq]);
-                const long b = *reinterpret_cast<const long *>(&s_x[buf][16 * wave + (lane & 15)][32 * gl + kq]);
-                const float s = sc[gl];
-                s0 = s;
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const v4i_t d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[i], b, zero, 0, 0, 0);
-#pragma unroll
-                    for (int v = 0; v < 4; v++) f[i][v] += one ? (float)d[v] : (float)d[v] * s;
-                }
+            // last stage reloads itself into the idle buffer); the scheduling
+            // barrier keeps their issue ahead of the MFMAs.  FULLK: every stage
+            // holds eight groups and the stage is one basic block (with a
+            // branch between them the compiler sinks the loads to their LDS
+            // stores).
+            MF_STAGE_LOAD(A, st + 1 < nst ? st + 1 : st);
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (FULLK) {
+                mf_stage<true>(f, s_w[buf], s_x[buf], sc, MF_KC / 32, false, wave, lane, kq);
+            } else {
+                mf_stage<false>(f, s_w[buf], s_x[buf], sc, nb - st * (MF_KC / 32), one, wave, lane, kq);
+                if (one) s0 = sc[0];
             }
-            nx.put(s_w[buf ^ 1], s_x[buf ^ 1], rr, pc);
+            MF_STAGE_PUT(A, buf ^ 1);
             __syncthreads();
         }
         // (after the last stage's barrier no wave reads this tile's LDS, so the
@@ -181,7 +226,7 @@ __global__ __launch_bounds__(MF_THREADS) void k_mfma_q8(const int8_t *__restrict
         if (cl < ncols) {
             float *op = out + (size_t)orow * out_stride;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
+            for (int i = 0; i < MF_RT; i++) {
 #pragma unroll
                 for (int v = 0; v < 4; v++) {
                     const int n = n0 + 16 * i + 4 * (lane >> 4) + v;
@@ -196,6 +241,9 @@ __global__ __launch_bounds__(MF_THREADS) void k_mfma_q8(const int8_t *__restrict
         }
     }
 }
+
+#undef MF_STAGE_LOAD
+#undef MF_STAGE_PUT
 
 // ------------------------------------------------------ wide producers ---
 //
@@ -267,8 +315,13 @@ extern "C" int l98k_mfma_gemm(const int8_t *W, const float *ws, int N, int K, co
                               float *out, int out_stride, hipStream_t st) {
     if (N < 1 || M < 1 || K < 32 || (K & 31) || out_stride < N) return -1;
     MfCols c{};
-    hipLaunchKernelGGL(k_mfma_q8, dim3((N + MF_ROWS - 1) / MF_ROWS, (M + MF_COLS - 1) / MF_COLS, 1),
-                       dim3(MF_THREADS), 0, st, W, ws, N, K, (size_t)0, X, Xs, M, c, out, out_stride);
+    const dim3 grid((N + MF_ROWS - 1) / MF_ROWS, (M + MF_COLS - 1) / MF_COLS, 1);
+    if (K % MF_KC == 0)
+        hipLaunchKernelGGL(k_mfma_q8<true>, grid, dim3(MF_THREADS), 0, st, W, ws, N, K, (size_t)0, X, Xs, M, c, out,
+                           out_stride);
+    else
+        hipLaunchKernelGGL(k_mfma_q8<false>, grid, dim3(MF_THREADS), 0, st, W, ws, N, K, (size_t)0, X, Xs, M, c, out,
+                           out_stride);
     return (int)hipGetLastError();
 }
 
@@ -280,8 +333,13 @@ extern "C" int l98k_mfma_gemm_grouped(const int8_t *bank, const float *bank_s, i
                                       int max_cols, float *out, int out_stride, hipStream_t st) {
     if (N < 1 || K < 32 || (K & 31) || max_groups < 1 || max_cols < 1 || out_stride < N) return -1;
     MfCols c{gexp, goff, gcnt, list, xmap, ng};
-    hipLaunchKernelGGL(k_mfma_q8, dim3((N + MF_ROWS - 1) / MF_ROWS, 1, max_groups),
-                       dim3(MF_THREADS), 0, st, bank, bank_s, N, K, (size_t)N * K, X, Xs, 0, c, out, out_stride);
+    const dim3 grid((N + MF_ROWS - 1) / MF_ROWS, 1, max_groups);
+    if (K % MF_KC == 0)
+        hipLaunchKernelGGL(k_mfma_q8<true>, grid, dim3(MF_THREADS), 0, st, bank, bank_s, N, K, (size_t)N * K, X, Xs, 0,
+                           c, out, out_stride);
+    else
+        hipLaunchKernelGGL(k_mfma_q8<false>, grid, dim3(MF_THREADS), 0, st, bank, bank_s, N, K, (size_t)N * K, X, Xs,
+                           0, c, out, out_stride);
     return (int)hipGetLastError();
 }
 
