@@ -30,7 +30,7 @@
 typedef int v4i_t __attribute__((ext_vector_type(4)));
 
 #define MF_THREADS 256
-#define MF_RT 2           // 16-row MFMA tiles per wave
+#define MF_RT 1           // 16-row MFMA tiles per wave
 #define MF_ROWS (16 * MF_RT)  // weight rows per block
 #define MF_COLS 64        // token columns per block (16 per wave)
 #define MF_KC 256         // K bytes (eight groups) per LDS stage
@@ -58,7 +58,7 @@ static_assert(MF_KC == 256 && MF_THREADS == 256, "a stage: eight group scales pe
     do {                                                                                       \
         const int off_ = imin((st_) * MF_KC + 16 * pc, K - 16);                                \
         R##w0 = *reinterpret_cast<const int4 *>(wl0 + off_);                                   \
-        R##w1 = *reinterpret_cast<const int4 *>(wl1 + off_);                                   \
+        if constexpr (MF_RT >= 2) R##w1 = *reinterpret_cast<const int4 *>(wl1 + off_);         \
         if constexpr (MF_RT == 4) {                                                            \
             R##w2 = *reinterpret_cast<const int4 *>(wl2 + off_);                               \
             R##w3 = *reinterpret_cast<const int4 *>(wl3 + off_);                               \
@@ -74,7 +74,7 @@ static_assert(MF_KC == 256 && MF_THREADS == 256, "a stage: eight group scales pe
 #define MF_STAGE_PUT(R, b_)                                                                    \
     do {                                                                                       \
         *reinterpret_cast<int4 *>(&s_w[b_][rr][16 * pc]) = R##w0;                              \
-        *reinterpret_cast<int4 *>(&s_w[b_][rr + 16][16 * pc]) = R##w1;                         \
+        if constexpr (MF_RT >= 2) *reinterpret_cast<int4 *>(&s_w[b_][rr + 16][16 * pc]) = R##w1; \
         if constexpr (MF_RT == 4) {                                                            \
             *reinterpret_cast<int4 *>(&s_w[b_][rr + 32][16 * pc]) = R##w2;                     \
             *reinterpret_cast<int4 *>(&s_w[b_][rr + 48][16 * pc]) = R##w3;                     \
@@ -102,10 +102,14 @@ __device__ __forceinline__ void mf_stage(float (&f)[MF_RT][4], const int8_t (*sw
         if (!FULL && gl >= ng) break;                  // uniform
         const long b = *reinterpret_cast<const long *>(&sx[16 * wave + (lane & 15)][32 * gl + kq]);
         const long a0 = *reinterpret_cast<const long *>(&sw[(lane & 15)][32 * gl + kq]);
-        const long a1 = *reinterpret_cast<const long *>(&sw[16 + (lane & 15)][32 * gl + kq]);
         const v4i_t d0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, b, zero, 0, 0, 0);
-        const v4i_t d1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, b, zero, 0, 0, 0);
         const float s = sc[gl];
+        if constexpr (MF_RT == 1) {
+            mf_fold(f[0], d0, s, one);
+            continue;
+        }
+        const long a1 = *reinterpret_cast<const long *>(&sw[16 + (lane & 15)][32 * gl + kq]);
+        const v4i_t d1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, b, zero, 0, 0, 0);
         if constexpr (MF_RT == 4) {
             const long a2 = *reinterpret_cast<const long *>(&sw[32 + (lane & 15)][32 * gl + kq]);
             const long a3 = *reinterpret_cast<const long *>(&sw[48 + (lane & 15)][32 * gl + kq]);
@@ -117,7 +121,7 @@ __device__ __forceinline__ void mf_stage(float (&f)[MF_RT][4], const int8_t (*sw
             mf_fold(f[MF_RT - 1], d3, s, one);
         } else {
             mf_fold(f[0], d0, s, one);
-            mf_fold(f[1], d1, s, one);
+            mf_fold(f[MF_RT - 1], d1, s, one);
         }
     }
 }
@@ -172,7 +176,8 @@ __global__ __launch_bounds__(MF_THREADS) void k_mfma_q8(const int8_t *__restrict
             }
             return X + (size_t)xr * K;
         };
-        const int8_t *wl0 = wrow(0), *wl1 = wrow(1), *wl2 = wrow(MF_RT - 2), *wl3 = wrow(MF_RT - 1);
+        const int8_t *wl0 = wrow(0), *wl1 = wrow(imin(1, MF_RT - 1)), *wl2 = wrow(imax(0, MF_RT - 2)),
+                     *wl3 = wrow(MF_RT - 1);
         const int8_t *xl0 = xcol(0), *xl1 = xcol(1), *xl2 = xcol(2), *xl3 = xcol(3);
         // the activation scales this thread stages: column tid / 4
         const float *xsl;
@@ -186,7 +191,7 @@ __global__ __launch_bounds__(MF_THREADS) void k_mfma_q8(const int8_t *__restrict
             xsl = Xs + (size_t)xr * nb;
         }
         const int nst = (K + MF_KC - 1) / MF_KC;
-        int4 Aw0, Aw1, Aw2 = {}, Aw3 = {}, Ax0, Ax1, Ax2, Ax3;
+        int4 Aw0, Aw1 = {}, Aw2 = {}, Aw3 = {}, Ax0, Ax1, Ax2, Ax3;
         float At0, At1;
         float f[MF_RT][4];
 #pragma unroll
