@@ -9,7 +9,10 @@ Prints, as markdown:
     including the next (the last complete round), grouped by kernel;
   * the tied lm_head GEMV launches (k_gemv_q8 dispatches whose grid covers
     `vocab` rows), whose mean duration is the figure bench.py's roofline
-    uses.
+    uses;
+  * the prompt's many-row path: the dispatches from the last many-row
+    k_embed to the last many-row kernel (k_mfma_q8, k_kda_post, k_attn_prep)
+    before the first k_accept, i.e. the session's prefill and MTP prefill.
 """
 import argparse
 import collections
@@ -21,7 +24,7 @@ def load(path):
     with open(path, newline="") as f:
         for r in csv.DictReader(f):
             rows.append((r["Kernel_Name"], int(r["Start_Timestamp"]), int(r["End_Timestamp"]),
-                         int(r["Grid_Size_X"]), int(r["Workgroup_Size_X"])))
+                         int(r["Grid_Size_X"]), int(r["Workgroup_Size_X"]), int(r.get("Grid_Size_Y") or 1)))
     rows.sort(key=lambda r: r[1])
     return rows
 
@@ -50,22 +53,36 @@ def main():
     a = ap.parse_args()
     rows = load(a.trace)
     whole = collections.defaultdict(list)
-    for n, s, e, g, w in rows:
+    for n, s, e, g, w, *_ in rows:
         whole[short(n)].append(e - s)
     print(table(whole, "Whole run", "all dispatches"))
     acc = [i for i, r in enumerate(rows) if short(r[0]) == "k_accept"]
     if len(acc) >= 2:
         seg = rows[acc[-2] + 1:acc[-1] + 1]
         grp = collections.defaultdict(list)
-        for n, s, e, g, w in seg:
+        for n, s, e, g, w, *_ in seg:
             grp[short(n)].append(e - s)
         span = seg[-1][2] - seg[0][1]
         print()
         print(table(grp, f"One round (last complete round; span {span / 1e3:.1f} us without graph replay)",
                     "round"))
+    first_acc = acc[0] if acc else len(rows)
+    # the last many-row embedding (a grid of at least 16 token rows in y) before it
+    emb = [i for i, r in enumerate(rows[:first_acc]) if short(r[0]) == "k_embed" and r[5] >= 16]
+    emb = emb[-1:]
+    wide = [i for i, r in enumerate(rows[:first_acc])
+            if short(r[0]).startswith(("k_mfma_q8", "k_kda_post", "k_attn_prep"))]
+    if emb and wide and wide[-1] > emb[0]:
+        seg = rows[emb[0]:wide[-1] + 1]
+        grp = collections.defaultdict(list)
+        for n, s, e, g, w, *_ in seg:
+            grp[short(n)].append(e - s)
+        span = seg[-1][2] - seg[0][1]
+        print()
+        print(table(grp, f"Prompt prefill and MTP prefill (span {span / 1e3:.1f} us)", "prefill"))
     tiles = (a.vocab + a.gemv_rows_per_block - 1) // a.gemv_rows_per_block
     lm = collections.defaultdict(list)
-    for n, s, e, g, w in rows:
+    for n, s, e, g, w, *_ in rows:
         if short(n).startswith("k_gemv_q8") and w > 0 and g // w == tiles:
             lm[short(n)].append(e - s)
     if lm:
