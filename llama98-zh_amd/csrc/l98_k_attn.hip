@@ -82,12 +82,16 @@ __global__ __launch_bounds__(64) void k_attn_prep(AttnArgs a) {
     }
 }
 
-// Attention of the chunk's tokens against the Q8 KV cache, in two kernels
-// (attn_score_loop Q8 branch, src/forward_attn.c:206-660; score_q8_row
-// :30-41; lz_softmax src/ops_norm.c:903-990; wsum_q8_row :17-21).
+// Attention of the chunk's tokens against the Q8 KV cache (attn_score_loop
+// Q8 branch, src/forward_attn.c:206-660; score_q8_row :30-41; lz_softmax
+// src/ops_norm.c:903-990; wsum_q8_row :17-21).  A session's chunk (<= 8
+// rows) runs as one launch, k_attn_fused: block (q head, token) computes its
+// own scores (see attn_av_body), then the softmax and value sum.  The
+// many-item launch (the session batch's verify rows, a prefill's rows) has
+// two kernels:
 //
-// k_attn_scores: one block per (64-position slice, kv head, token).  The
-// block prepares what it needs itself: the kv_mul q heads of the token
+// k_attn_scores_items: one block per (64-position slice, kv head, token).
+// The block prepares what it needs itself: the kv_mul q heads of the token
 // (RMSNorm(1+w), NeoX rotary: src/forward_attn.c:878-960, src/ops_rope.c:
 // 21-67) and, for positions of the chunk's own tokens, the K rows from the
 // K projection (norm, rotary, per-32 quantization); every other K row comes
@@ -219,10 +223,6 @@ __device__ __forceinline__ void attn_scores_body(const AttnArgs &a, float *__res
     }
 }
 
-__global__ __launch_bounds__(256) void k_attn_scores(AttnArgs a, float *__restrict__ att, int att_stride) {
-    attn_scores_body(a, att, att_stride, blockIdx.x, blockIdx.y, blockIdx.z);
-}
-
 // One launch over several sessions' rows (the session batch's verify), or
 // over one session's prefill rows cut into MAX_CHUNK-row items whose K and V
 // rows are all in the cache before the launch: item i is rows [row0, row0 +
@@ -258,7 +258,7 @@ __global__ __launch_bounds__(256) void k_attn_scores_items(AttnArgs b, const Att
     attn_scores_body(a, att + (size_t)item * att_item, att_stride, blockIdx.x, blockIdx.y, t);
 }
 
-// k_attn_av: one block of 8 waves per (q head, token).  Softmax over the
+// k_attn_av_items: one block of 8 waves per (q head, token).  Softmax over the
 // token's scores (max, exp, the serial loop's sum - taken by the exact wave
 // sum up to 2048 positions -, scale), then the value sum
 // out[d] = sum_p a[p] * v[p][d] * vs[p][d/32] walked in position order by
@@ -360,7 +360,16 @@ __device__ __forceinline__ void av_stage_any(const int8_t *__restrict__ vc, cons
         av_stage<false>(vc, vs, kv_dim, kvh, hd, p0, n, s_v, s_vs, arow, L, s_a);
 }
 
-template <int CH>
+// FUSED (the chunk path of one session, k_attn_fused): the block first does
+// the scores kernel's work for its own (q head, token) over every position,
+// into LDS: its q head and the chunk's new K rows 0..t of its kv head
+// (RMSNorm(1+w), NeoX rotary, K quantized per 32) and those rows' V
+// quantized per 32; positions before the chunk read K from the cache, the
+// chunk's positions the block's own rows; token t's K and V rows go to the
+// cache from the kv head's first q head's block.  The staged V rows of the
+// chunk's positions are then replaced by the block's own (the cache rows may
+// still be in flight from other blocks of the launch).
+template <int CH, bool FUSED = false>
 __device__ __forceinline__ void attn_av_body(const AttnArgs &a, const float *__restrict__ att, int att_stride, int sc,
                                              int h, int t) {
     EXP_TAB_LOAD(tab);
@@ -368,9 +377,12 @@ __device__ __forceinline__ void attn_av_body(const AttnArgs &a, const float *__r
     __shared__ uint32_t s_red[AV_THREADS / 64];
     __shared__ float s_inv;
     __shared__ PsRec s_rec[128];
+    constexpr int NEWR = FUSED ? MAX_CHUNK : 1;
+    __shared__ __align__(16) int8_t s_knew[NEWR * ATT_MAX_HD], s_vnew[NEWR * ATT_MAX_HD];
+    __shared__ float s_ksn[NEWR * (ATT_MAX_HD / 32)], s_vsn[NEWR * (ATT_MAX_HD / 32)], s_vin[NEWR + 1];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int hd = a.hd, nb = hd >> 5, kv_mul = a.nh / a.nkv, kvh = h / kv_mul;
-    const int pos_t = *a.ctl_pos + a.pos_off + t, L = pos_t + 1;
+    const int pos0 = *a.ctl_pos + a.pos_off, pos_t = pos0 + t, L = pos_t + 1;
     const int Lp = (att_stride + 3) & ~3;
     float *s_a = reinterpret_cast<float *>(smem);                                   // [Lp]
     constexpr int AV_CH = CH, AV_PAD = CH + 4;
@@ -378,14 +390,112 @@ __device__ __forceinline__ void attn_av_body(const AttnArgs &a, const float *__r
     int8_t *s_v = reinterpret_cast<int8_t *>(prod + 2 * hd * AV_PAD);               // [sc][hd]
     float *s_vs = reinterpret_cast<float *>(s_v + (size_t)sc * hd);                  // [sc][nb]
     float *s_e = s_vs + (size_t)sc * nb;                                             // [AV_ESUM_FLOATS]
-    const float *arow = att + ((size_t)t * a.nh + h) * att_stride;
+    const float *arow = FUSED ? nullptr : att + ((size_t)t * a.nh + h) * att_stride;
     const int cpr = hd >> 4;
+    // the chunk's rows among V positions [sp0, sp0 + nsc): the block's own
+    // quantized rows replace the staged ones
+    auto patch_new = [&](int sp0, int nsc) {
+        const int lo = imax(pos0, sp0), hi = imin(L, sp0 + nsc);
+        for (int f = tid; f < (hi - lo) * hd; f += AV_THREADS) {
+            const int r = f / hd, i = f - r * hd;
+            s_v[(size_t)(lo + r - sp0) * hd + i] = s_vnew[(lo + r - pos0) * hd + i];
+        }
+        for (int f = tid; f < (hi - lo) * nb; f += AV_THREADS) {
+            const int r = f / nb, g = f - r * nb;
+            s_vs[(size_t)(lo + r - sp0) * nb + g] = s_vsn[(lo + r - pos0) * nb + g];
+        }
+    };
+    if constexpr (FUSED) {
+        // vectors: 0 = the q head, 1 + r = the chunk's K row r (r <= t);
+        // prepared in the product buffer, which the value pass uses later
+        float *s_x = prod, *s_sq = prod + (1 + MAX_CHUNK) * ATT_MAX_HD;
+        const int nvec = 2 + t, half = a.rot >> 1;
+        for (int f = tid; f < nvec * hd; f += AV_THREADS) {
+            const int v = f / hd, i = f - v * hd;
+            const float x = v == 0 ? a.qg[(size_t)t * a.qg_dim + (size_t)h * 2 * hd + i]
+                                   : a.kp[(size_t)(v - 1) * a.kv_dim + kvh * hd + i];
+            s_x[v * hd + i] = x;
+            s_sq[v * (hd + 4) + i] = x * x;
+        }
+        __syncthreads();
+        if (tid < nvec) s_vin[tid] = d_rsqrt(d_ss_over_n(serial_sum(s_sq + tid * (hd + 4), hd), hd) + a.eps);
+        __syncthreads();
+        for (int f = tid; f < nvec * hd; f += AV_THREADS) {
+            const int v = f / hd, i = f - v * hd;
+            const float w = v == 0 ? a.q_norm[i] : a.k_norm[i];
+            s_x[v * hd + i] = s_x[v * hd + i] * s_vin[v] * (1.0f + w);
+        }
+        __syncthreads();
+        for (int f = tid; f < nvec * half; f += AV_THREADS) {
+            const int v = f / half, i = f - v * half;
+            const int pos = v == 0 ? pos_t : pos0 + v - 1;
+            const float c = a.rope_cs[((size_t)pos * half + i) * 2], sn = a.rope_cs[((size_t)pos * half + i) * 2 + 1];
+            const float x0 = s_x[v * hd + i], x1 = s_x[v * hd + i + half];
+            s_x[v * hd + i] = x0 * c - x1 * sn;
+            s_x[v * hd + i + half] = x1 * c + x0 * sn;
+        }
+        __syncthreads();
+        // K rows 0..t and their V rows per 32 (32-lane groups: hd % 32 == 0)
+        const bool writer = h == kvh * kv_mul;
+        for (int base = 0; base < (t + 1) * hd; base += AV_THREADS) {
+            const int nk = (t + 1) * hd, f = base + tid;
+            const int fc = imin(f, nk - 1), r = fc / hd, i = fc - r * hd;
+            int8_t qk, qv;
+            float sk, sv;
+            d_quant_group32(s_x[(1 + r) * hd + i], &qk, &sk);
+            d_quant_group32(a.vp[(size_t)r * a.kv_dim + kvh * hd + i], &qv, &sv);
+            if (f < nk) {
+                s_knew[r * hd + i] = qk;
+                s_vnew[r * hd + i] = qv;
+                if ((i & 31) == 0) { s_ksn[r * nb + (i >> 5)] = sk; s_vsn[r * nb + (i >> 5)] = sv; }
+                if (writer && r == t) {
+                    const size_t row = (size_t)pos_t * a.kv_dim + kvh * hd + i;
+                    a.kcache[row] = qk;
+                    a.vcache[row] = qv;
+                    if ((i & 31) == 0) {
+                        const size_t srow = (size_t)pos_t * (a.kv_dim >> 5) + kvh * nb + (i >> 5);
+                        a.kscale[srow] = sk;
+                        a.vscale[srow] = sv;
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        // scores: each 32-group's products summed in order, then the groups,
+        // times attn_scale (score_q8_row)
+        const float scale = a.attn_scale;
+        auto score = [&](const int8_t *kr, const float *ks) {
+            float sum = 0.0f;
+            for (int dd = 0; dd < hd; dd += 32) {
+                const int4 k0 = *reinterpret_cast<const int4 *>(kr + dd);
+                const int4 k1 = *reinterpret_cast<const int4 *>(kr + dd + 16);
+                const int8_t *kb0 = reinterpret_cast<const int8_t *>(&k0);
+                const int8_t *kb1 = reinterpret_cast<const int8_t *>(&k1);
+                float acc = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 16; e++) acc += s_x[dd + e] * (float)kb0[e];
+#pragma unroll
+                for (int e = 0; e < 16; e++) acc += s_x[dd + 16 + e] * (float)kb1[e];
+                sum += acc * ks[dd >> 5];
+            }
+            return sum * scale;
+        };
+        for (int p = tid; p < L; p += AV_THREADS) {
+            if (p < pos0)
+                s_a[p] = score(a.kcache + (size_t)p * a.kv_dim + kvh * hd,
+                               a.kscale + (size_t)p * (a.kv_dim >> 5) + kvh * nb);
+            else
+                s_a[p] = score(s_knew + (p - pos0) * hd, s_ksn + (p - pos0) * nb);
+        }
+    }
     // scores and the first V stage -> LDS, their loads in one batch (score
     // rows past AV_SCORE_MAX * AV_THREADS positions: the rest after)
     av_stage_any(a.vcache, a.vscale, a.kv_dim, kvh, hd, 0, imin(sc, L), s_v, s_vs, arow, L, s_a);
-    for (int p = AV_SCORE_MAX * AV_THREADS + tid; p < L; p += AV_THREADS) s_a[p] = arow[p];
+    if constexpr (!FUSED)
+        for (int p = AV_SCORE_MAX * AV_THREADS + tid; p < L; p += AV_THREADS) s_a[p] = arow[p];
     EXP_TAB_PUT(tab);
     __syncthreads();
+    if constexpr (FUSED) patch_new(0, imin(sc, L));    // (the softmax's barriers come before any read)
     // softmax: max (order-preserving key), exp, serial sum, scale
     uint32_t best = 0;
     for (int p = tid; p < L; p += AV_THREADS) best = umax(best, d_fkey(s_a[p]));
@@ -453,6 +563,10 @@ __device__ __forceinline__ void attn_av_body(const AttnArgs &a, const float *__r
             __syncthreads();
             av_stage_any(a.vcache, a.vscale, a.kv_dim, kvh, hd, sp0, nsc, s_v, s_vs, nullptr, 0, nullptr);
             __syncthreads();
+            if constexpr (FUSED) {
+                patch_new(sp0, nsc);
+                __syncthreads();
+            }
         }
         const int nch = (nsc + AV_CH - 1) / AV_CH;
         if (!cons) produce(sp0, sp0, nsc, 0);
@@ -491,10 +605,11 @@ __device__ __forceinline__ void attn_av_body(const AttnArgs &a, const float *__r
     }
 }
 
+// The chunk path of one session in one launch: block (q head, token) does
+// its own scores (see attn_av_body, FUSED), then the softmax and value sum.
 template <int CH>
-__global__ __launch_bounds__(AV_THREADS) void k_attn_av(AttnArgs a, const float *__restrict__ att, int att_stride,
-                                                 int sc) {
-    attn_av_body<CH>(a, att, att_stride, sc, blockIdx.x, blockIdx.y);
+__global__ __launch_bounds__(AV_THREADS) void k_attn_fused(AttnArgs a, int att_stride, int sc) {
+    attn_av_body<CH, true>(a, nullptr, att_stride, sc, blockIdx.x, blockIdx.y);
 }
 
 template <int CH>
@@ -625,8 +740,6 @@ static void av_allow_lds() {
     static bool attr_set = false;
     if (attr_set) return;
     const int lim = lds_limit() - 4096;
-    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k_attn_av<128>), hipFuncAttributeMaxDynamicSharedMemorySize, lim);
-    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k_attn_av<64>), hipFuncAttributeMaxDynamicSharedMemorySize, lim);
     (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k_attn_av_items<128>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, lim);
     (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k_attn_av_items<64>),
@@ -674,16 +787,14 @@ extern "C" int l98k_attn(const AttnArgs *a, int nt, int max_len, float *att, hip
     const int kv_mul = a->nh / a->nkv;
     if (kv_mul + MAX_CHUNK > ATT_MAX_VEC) return -1;
     const int att_stride = (max_len + 3) & ~3;
-    const int slices = (max_len + ATT_SLICE - 1) / ATT_SLICE;
-    hipLaunchKernelGGL(k_attn_scores, dim3(slices, a->nkv, nt), dim3(256), 0, st, *a, att, att_stride);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return (int)e;
-    // value-sum kernel: scores, the product double buffer, then as many
-    // staged V positions (a multiple of the chunk) as the LDS limit leaves;
-    // 128-position chunks when a whole chunk of V still fits beside them
+    // one launch: each (q head, token) block does its own scores, then the
+    // softmax and the value sum (scores row, the product double buffer, then
+    // as many staged V positions, a multiple of the chunk, as the LDS limit
+    // leaves beside the kernel's static LDS; 128-position chunks when a whole
+    // chunk of V still fits)
     const int hd = a->hd;
     const size_t per_pos = (size_t)hd + (size_t)(hd >> 5) * sizeof(float);
-    const int lim = lds_limit() - 4096;          // the kernel's static LDS (exp table, reductions, sum records) fits in the rest
+    const int lim = lds_limit() - 8192;
     auto plan = [&](int ch, int *sc_out, size_t *lds_out) {
         const size_t fixed = ((size_t)att_stride + 2 * (size_t)hd * (ch + 4) + AV_ESUM_FLOATS) * sizeof(float);
         if (fixed + (size_t)ch * per_pos > (size_t)lim) return false;
@@ -698,18 +809,18 @@ extern "C" int l98k_attn(const AttnArgs *a, int nt, int max_len, float *att, hip
     };
     static bool attr_set = false;
     if (!attr_set) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k_attn_av<128>),
+        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k_attn_fused<128>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, lim);
-        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k_attn_av<64>),
+        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k_attn_fused<64>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, lim);
         attr_set = true;
     }
     int sc = 0;
     size_t lds = 0;
     if (plan(128, &sc, &lds))
-        hipLaunchKernelGGL(k_attn_av<128>, dim3(a->nh, nt), dim3(AV_THREADS), lds, st, *a, att, att_stride, sc);
+        hipLaunchKernelGGL(k_attn_fused<128>, dim3(a->nh, nt), dim3(AV_THREADS), lds, st, *a, att_stride, sc);
     else if (plan(64, &sc, &lds))
-        hipLaunchKernelGGL(k_attn_av<64>, dim3(a->nh, nt), dim3(AV_THREADS), lds, st, *a, att, att_stride, sc);
+        hipLaunchKernelGGL(k_attn_fused<64>, dim3(a->nh, nt), dim3(AV_THREADS), lds, st, *a, att_stride, sc);
     else
         return -1;
     return (int)hipGetLastError();
