@@ -623,6 +623,101 @@ __global__ __launch_bounds__(AV_THREADS) void k_attn_av_items(AttnArgs b, const 
     attn_av_body<CH>(a, att + (size_t)item * att_item, att_stride, sc, blockIdx.x, t);
 }
 
+// k_attn_av_rows: the softmax and value sums of an item launch whose rows
+// all lie below position 512, for 64-wide heads: one block per (q head,
+// item), wave t = the item's token t, lane = output element d.  The item's
+// V rows are staged once for its eight tokens, transposed ([d][position],
+// and the scales [group][position]), so a lane reads four positions' bytes
+// in one access; each wave takes its token's softmax (max, exp, the exact
+// wave sum of the serial loop, scale), then lane d adds (a[p] * v[p][d]) *
+// vs[p][d/32] over positions p = 0 .. pos in order - the arithmetic of
+// attn_av_body, per token.  Then the gate and the per-32 quantization.
+#define AVR_L 512
+#define AVR_HD 64
+__global__ __launch_bounds__(512) void k_attn_av_rows(AttnArgs b, const AttnItem *__restrict__ items, int plane,
+                                                      const float *__restrict__ att, int att_stride, size_t att_item) {
+    EXP_TAB_LOAD(tab);
+    __shared__ __align__(16) int8_t s_vt[AVR_HD][AVR_L];          // V transposed
+    __shared__ __align__(16) float s_vst[AVR_HD / 32][AVR_L];     // its scales, transposed
+    __shared__ __align__(16) float s_a[MAX_CHUNK][AVR_L];         // scores, then probabilities
+    __shared__ __align__(16) float s_e[MAX_CHUNK][64 * (8 + 4)];  // exps in the exact sum's layout (8 per lane)
+    __shared__ PsRec s_rec[MAX_CHUNK][128];
+    const int h = blockIdx.x, item = blockIdx.y;
+    const AttnItem it = items[item];
+    const AttnArgs a = attn_item_args(b, it, plane);
+    const float *arows = att + (size_t)item * att_item;
+    const int tid = threadIdx.x, t = tid >> 6, lane = tid & 63;
+    const int kv_mul = a.nh / a.nkv, kvh = h / kv_mul, nb = AVR_HD / 32;
+    const int pos0 = *a.ctl_pos + a.pos_off, n = it.n, Lmax = pos0 + n;
+    const bool live = t < n;
+    const int L = pos0 + imin(t, n - 1) + 1;
+    // stage: V rows [0, Lmax) of the kv head (4 int4 per row), their scales,
+    // and each wave's score row
+    for (int f = tid; f < Lmax * 4; f += 512) {
+        const int p = f >> 2, c = f & 3;
+        const int4 v4 = *reinterpret_cast<const int4 *>(a.vcache + (size_t)p * a.kv_dim + kvh * AVR_HD + 16 * c);
+        const int w4[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+        for (int k = 0; k < 16; k++) s_vt[16 * c + k][p] = (int8_t)((w4[k >> 2] >> (8 * (k & 3))) & 0xFF);
+    }
+    for (int f = tid; f < Lmax * nb; f += 512) {
+        const int p = f / nb, g = f - p * nb;
+        s_vst[g][p] = a.vscale[(size_t)p * (a.kv_dim >> 5) + kvh * nb + g];
+    }
+    if (live)
+        for (int p = lane; p < L; p += 64) s_a[t][p] = arows[((size_t)t * a.nh + h) * att_stride + p];
+    EXP_TAB_PUT(tab);
+    __syncthreads();
+    // softmax of the wave's token: max (order-preserving key), exp, the
+    // serial loop's sum, scale
+    if (live) {
+        uint32_t best = 0;
+        for (int p = lane; p < L; p += 64) best = umax(best, d_fkey(s_a[t][p]));
+        for (int o = 32; o > 0; o >>= 1) best = umax(best, (uint32_t)__shfl_xor((int)best, o));
+        const float mx = d_unkey(best);
+        for (int p = lane; p < L; p += 64) {
+            const float e = d_exp(s_a[t][p] - mx, tab);
+            s_a[t][p] = e;
+            s_e[t][(p >> 3) * 12 + (p & 7)] = e;
+        }
+        // positions L .. of the padded row read as 0 inside the exact sum
+        __builtin_amdgcn_s_waitcnt(0xC07F);           // lgkmcnt(0): the wave's exps are in LDS
+        __builtin_amdgcn_wave_barrier();
+        const float sum = wave_sum_nonneg<8>(s_e[t], L, s_rec[t]);
+        const float inv = (sum > 0.0f) ? 1.0f / sum : 0.0f;
+        for (int p = lane; p < L; p += 64) s_a[t][p] *= inv;
+    }
+    __syncthreads();
+    if (!live) return;
+    // value sum, four positions per step (the adds stay in position order)
+    const int d = lane, g = d >> 5;
+    float o = 0.0f;
+    const int L4 = L & ~3;
+    for (int p = 0; p < L4; p += 4) {
+        const float4 ap = *reinterpret_cast<const float4 *>(&s_a[t][p]);
+        const uint32_t vb = *reinterpret_cast<const uint32_t *>(&s_vt[d][p]);
+        const float4 vs = *reinterpret_cast<const float4 *>(&s_vst[g][p]);
+        const float p0 = ap.x * (float)(int8_t)(vb & 0xFF) * vs.x;
+        const float p1 = ap.y * (float)(int8_t)((vb >> 8) & 0xFF) * vs.y;
+        const float p2 = ap.z * (float)(int8_t)((vb >> 16) & 0xFF) * vs.z;
+        const float p3 = ap.w * (float)(int8_t)(vb >> 24) * vs.w;
+        o += p0;
+        o += p1;
+        o += p2;
+        o += p3;
+    }
+    for (int p = L4; p < L; p++) o += s_a[t][p] * (float)s_vt[d][p] * s_vst[g][p];
+    const float gate = a.qg[(size_t)t * a.qg_dim + (size_t)h * 2 * AVR_HD + AVR_HD + d];
+    o *= d_sigmoid(gate, tab);
+    const int col = h * AVR_HD + d;
+    if (a.out) a.out[(size_t)t * a.q_dim + col] = o;
+    int8_t q;
+    float sg;
+    d_quant_group32(o, &q, &sg);
+    a.oq[(size_t)t * a.q_dim + col] = q;
+    if ((d & 31) == 0) a.oqs[(size_t)t * (a.q_dim >> 5) + (col >> 5)] = sg;
+}
+
 // mtp_attn_t1 (src/forward_mtp.c:191-376, Q8 KV float arm): attention of
 // a DSpark slot at position 0 of the MTP plane with no history, one block
 // per slot row r.  The softmax over the single score is exactly 1, so K,
@@ -765,6 +860,11 @@ extern "C" int l98k_attn_items(const AttnArgs *a, const AttnItem *items, int n_i
                        plane, att, att_stride, att_item);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
+    if (a->hd == AVR_HD && max_len <= AVR_L) {
+        hipLaunchKernelGGL(k_attn_av_rows, dim3(a->nh, n_items), dim3(512), 0, st, *a, items, plane, att, att_stride,
+                           att_item);
+        return (int)hipGetLastError();
+    }
     av_allow_lds();
     int ch = 0, sc = 0;
     size_t lds = 0;
