@@ -1503,7 +1503,8 @@ int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, 
                     p.ctl_pos = &s->ctl->pos_scratch; p.pos_off = 0;
                     CK(l98k_attn_prep(&p, I.n, st));
                 }
-                CK(l98k_attn_items(&a, w->aitems, n_attn, plane, max_len, w->att_items, att_item, st));
+                CK(l98k_attn_items(&a, w->aitems, n_attn, plane, max_len, w->att_items, att_item,
+                                   prefill_items ? 1 : 0, st));
             }
             for (int it = 0; it < n_items && !attn_items; it++) {
                 const WideItem &I = items[it];

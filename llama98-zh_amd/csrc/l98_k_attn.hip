@@ -635,13 +635,15 @@ __global__ __launch_bounds__(AV_THREADS) void k_attn_av_items(AttnArgs b, const 
 #define AVR_L 512
 #define AVR_HD 64
 __global__ __launch_bounds__(512) void k_attn_av_rows(AttnArgs b, const AttnItem *__restrict__ items, int plane,
-                                                      const float *__restrict__ att, int att_stride, size_t att_item) {
+                                                      const float *__restrict__ att, int att_stride, size_t att_item,
+                                                      int own_scores) {
     EXP_TAB_LOAD(tab);
     __shared__ __align__(16) int8_t s_vt[AVR_HD][AVR_L];          // V transposed
     __shared__ __align__(16) float s_vst[AVR_HD / 32][AVR_L];     // its scales, transposed
     __shared__ __align__(16) float s_a[MAX_CHUNK][AVR_L];         // scores, then probabilities
     __shared__ __align__(16) float s_e[MAX_CHUNK][64 * (8 + 4)];  // exps in the exact sum's layout (8 per lane)
     __shared__ PsRec s_rec[MAX_CHUNK][128];
+    __shared__ __align__(16) float s_q[MAX_CHUNK][AVR_HD];        // own_scores: the prepared q heads
     const int h = blockIdx.x, item = blockIdx.y;
     const AttnItem it = items[item];
     const AttnArgs a = attn_item_args(b, it, plane);
@@ -664,8 +666,53 @@ __global__ __launch_bounds__(512) void k_attn_av_rows(AttnArgs b, const AttnItem
         const int p = f / nb, g = f - p * nb;
         s_vst[g][p] = a.vscale[(size_t)p * (a.kv_dim >> 5) + kvh * nb + g];
     }
-    if (live)
+    if (live && !own_scores)
         for (int p = lane; p < L; p += 64) s_a[t][p] = arows[((size_t)t * a.nh + h) * att_stride + p];
+    if (live && own_scores) {
+        // every K row is in the cache: the wave prepares its token's q head
+        // (RMSNorm(1+w) with the serial sum, NeoX rotary) and computes the
+        // scores itself, as k_attn_scores_items does
+        const int pos_t = L - 1, half = a.rot >> 1;
+        const float x = a.qg[(size_t)t * a.qg_dim + (size_t)h * 2 * AVR_HD + lane];
+        s_e[t][lane] = x * x;
+        __builtin_amdgcn_s_waitcnt(0xC07F);           // lgkmcnt(0): the squares are in LDS
+        __builtin_amdgcn_wave_barrier();
+        const float inv = d_rsqrt(d_ss_over_n(serial_sum(s_e[t], AVR_HD), AVR_HD) + a.eps);
+        const float y = x * inv * (1.0f + a.q_norm[lane]);
+        const float yo = __shfl(y, lane < half ? lane + half : lane - half);     // the rotary partner
+        float r = y;
+        if (lane < half) {
+            const float c = a.rope_cs[((size_t)pos_t * half + lane) * 2], sn = a.rope_cs[((size_t)pos_t * half + lane) * 2 + 1];
+            r = y * c - yo * sn;
+        } else if (lane < 2 * half) {
+            const int i = lane - half;
+            const float c = a.rope_cs[((size_t)pos_t * half + i) * 2], sn = a.rope_cs[((size_t)pos_t * half + i) * 2 + 1];
+            r = y * c + yo * sn;
+        }
+        s_q[t][lane] = r;
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_wave_barrier();
+        const float scale = a.attn_scale;
+        for (int p = lane; p < L; p += 64) {
+            const int8_t *kr = a.kcache + (size_t)p * a.kv_dim + kvh * AVR_HD;
+            const float *ks = a.kscale + (size_t)p * (a.kv_dim >> 5) + kvh * nb;
+            float sum = 0.0f;
+#pragma unroll
+            for (int dd = 0; dd < AVR_HD; dd += 32) {
+                const int4 k0 = *reinterpret_cast<const int4 *>(kr + dd);
+                const int4 k1 = *reinterpret_cast<const int4 *>(kr + dd + 16);
+                const int8_t *kb0 = reinterpret_cast<const int8_t *>(&k0);
+                const int8_t *kb1 = reinterpret_cast<const int8_t *>(&k1);
+                float acc = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 16; e++) acc += s_q[t][dd + e] * (float)kb0[e];
+#pragma unroll
+                for (int e = 0; e < 16; e++) acc += s_q[t][dd + 16 + e] * (float)kb1[e];
+                sum += acc * ks[dd >> 5];
+            }
+            s_a[t][p] = sum * scale;
+        }
+    }
     EXP_TAB_PUT(tab);
     __syncthreads();
     // softmax of the wave's token: max (order-preserving key), exp, the
@@ -848,21 +895,28 @@ static void av_allow_lds() {
 // buffers at row 0.  max_len: the longest item's last position + 1; att:
 // n_items scratch blocks of att_item floats.
 extern "C" int l98k_attn_items(const AttnArgs *a, const AttnItem *items, int n_items, int plane, int max_len,
-                               float *att, size_t att_item, hipStream_t st) {
+                               float *att, size_t att_item, int kv_cached, hipStream_t st) {
     if (a->nkv < 1 || a->nh % a->nkv || (a->hd & 31) || 256 % a->hd || a->hd > ATT_MAX_HD || a->rot > a->hd ||
         (a->rot & 1) || n_items < 1 || max_len < 1 || !a->oq || !a->oqs || !att || a->kv_only)
         return -1;
     if (a->nh / a->nkv + MAX_CHUNK > ATT_MAX_VEC) return -1;
     const int att_stride = (max_len + 3) & ~3;
     if ((size_t)MAX_CHUNK * a->nh * att_stride > att_item) return -1;
+    const bool rows = a->hd == AVR_HD && max_len <= AVR_L;
+    if (rows && kv_cached) {
+        // every row's K is in the cache: the value-sum blocks take their scores
+        hipLaunchKernelGGL(k_attn_av_rows, dim3(a->nh, n_items), dim3(512), 0, st, *a, items, plane, att, att_stride,
+                           att_item, 1);
+        return (int)hipGetLastError();
+    }
     const int slices = (max_len + ATT_SLICE - 1) / ATT_SLICE;
     hipLaunchKernelGGL(k_attn_scores_items, dim3(slices, a->nkv, n_items * MAX_CHUNK), dim3(256), 0, st, *a, items,
                        plane, att, att_stride, att_item);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
-    if (a->hd == AVR_HD && max_len <= AVR_L) {
+    if (rows) {
         hipLaunchKernelGGL(k_attn_av_rows, dim3(a->nh, n_items), dim3(512), 0, st, *a, items, plane, att, att_stride,
-                           att_item);
+                           att_item, 0);
         return (int)hipGetLastError();
     }
     av_allow_lds();

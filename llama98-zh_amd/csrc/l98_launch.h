@@ -105,9 +105,10 @@ int l98k_attn_prep(const AttnArgs *a, int nt, hipStream_t st);
 int l98k_attn_t1(const float *qg, int qg_dim, const float *vp, int kv_dim, int nh, int nkv, int hd, int q_dim,
                  int rows, int8_t *vc0, float *vs0, float *out, int8_t *oq, float *oqs, hipStream_t st);
 // Attention of several sessions' rows in one launch per kernel (items in
-// device memory); att: n_items blocks of att_item floats.
+// device memory); att: n_items blocks of att_item floats.  kv_cached: every
+// row's K and V are already in the cache (a prefill after its K/V launch).
 int l98k_attn_items(const AttnArgs *a, const AttnItem *items, int n_items, int plane, int max_len, float *att,
-                    size_t att_item, hipStream_t st);
+                    size_t att_item, int kv_cached, hipStream_t st);
 // Attention of nt tokens (positions *ctl_pos + pos_off + t) against the KV
 // plane: scores with the q/k preparation and the chunk's own K/V cache rows,
 // then softmax, value sum, output gate and quantization into oq / oqs.
