@@ -1326,21 +1326,24 @@ struct DWide {
     AttnItem *aitems;
     float *att_items = nullptr;   // attention scratch of an item launch, sized on demand
     size_t att_items_floats = 0;
+    // the second half of a split prefill chunk (see batch_capture_dev): its
+    // own scratch, a second stream, and one event per layer plus two
+    DWide *peer = nullptr;
+    hipStream_t st2 = nullptr;
+    std::vector<hipEvent_t> ev;
 };
 
 namespace {
 
 #define WIDE_MAX 512          // rows of one wide forward
 #define WIDE_MIN 16           // prefills shorter than this take the chunked path
+#define WIDE_SPLIT 64         // wide prefill chunks of at least this many rows run as two halves
 
 // nullptr (the callers take the chunked path) for a SubLN model, whose
 // per-projection norms this many-row forward does not carry, and for a
 // model with grouped weight scales (its matrix-core epilogue takes one
 // scale per row).
-DWide *wide_get(const DModel *cm) {
-    DModel *m = const_cast<DModel *>(cm);
-    if (m->c.use_subn || m->grouped) return nullptr;
-    if (m->wide) return m->wide;
+DWide *wide_alloc(const DModel *m) {
     const LZModelConfig &c = m->c;
     const size_t R = WIDE_MAX, d = c.hidden_size, pairs = R * c.num_experts_per_token;
     size_t wide = d;
@@ -1391,16 +1394,54 @@ DWide *wide_get(const DModel *cm) {
     w->mq = (int8_t *)(a + omq); w->mqs = (float *)(a + omqs);
     w->kitems = (KdaItem *)(a + oki);
     w->aitems = (AttnItem *)(a + oai);
-    m->wide = w;
     return w;
 }
 
+void wide_release(DWide *w) {
+    if (!w) return;
+    if (w->arena) (void)hipFree(w->arena);
+    if (w->logits) (void)hipFree(w->logits);
+    if (w->att_items) (void)hipFree(w->att_items);
+    delete w;
+}
+
+DWide *wide_get(const DModel *cm) {
+    DModel *m = const_cast<DModel *>(cm);
+    if (m->c.use_subn || m->grouped) return nullptr;
+    if (!m->wide) m->wide = wide_alloc(m);
+    return m->wide;
+}
+
+// The pair for a split prefill chunk: w's peer scratch, a second stream
+// (default priority) and the events; false when any of it cannot be made.
+bool wide_pair(DModel *m, DWide *w) {
+    if (w->peer) return true;
+    DWide *p = wide_alloc(m);
+    if (!p) return false;
+    std::vector<hipEvent_t> ev((size_t)m->c.n_layers + 2, nullptr);
+    bool ok = hipStreamCreateWithFlags(&w->st2, hipStreamNonBlocking) == hipSuccess;
+    for (auto &e : ev) ok = ok && hipEventCreateWithFlags(&e, hipEventDisableTiming) == hipSuccess;
+    if (!ok) {
+        for (auto &e : ev)
+            if (e) (void)hipEventDestroy(e);
+        if (w->st2) (void)hipStreamDestroy(w->st2);
+        w->st2 = nullptr;
+        wide_release(p);
+        return false;
+    }
+    w->peer = p;
+    w->ev = ev;
+    return true;
+}
+
 void wide_free(DModel *m) {
-    if (!m->wide) return;
-    if (m->wide->arena) (void)hipFree(m->wide->arena);
-    if (m->wide->logits) (void)hipFree(m->wide->logits);
-    if (m->wide->att_items) (void)hipFree(m->wide->att_items);
-    delete m->wide;
+    DWide *w = m->wide;
+    if (!w) return;
+    if (w->st2) (void)hipStreamSynchronize(w->st2);
+    for (auto &e : w->ev) (void)hipEventDestroy(e);
+    if (w->st2) (void)hipStreamDestroy(w->st2);
+    wide_release(w->peer);
+    wide_release(w);
     m->wide = nullptr;
 }
 
@@ -1416,7 +1457,8 @@ int mf(const DMat &W, const int8_t *xq, const float *xqs, int R, float *out, int
 // launch goes on stream st; the sessions' control blocks must hold their
 // slot bases and positions (pos_scratch = the item's pos0) before.
 int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, int R, bool advance, float *capture,
-                 float *logits, hipStream_t st) {
+                 float *logits, hipStream_t st, int pos_base = 0, hipEvent_t *wait_ev = nullptr,
+                 hipEvent_t *rec_ev = nullptr) {
     const LZModelConfig &c = m->c;
     const int d = c.hidden_size, E = c.num_experts, topk = c.num_experts_per_token;
     const int lat = c.moe_latent_dim, inter = c.moe_intermediate_size, sw = c.moe_shared_width;
@@ -1429,6 +1471,7 @@ int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, 
     // launch), else chunk by chunk.
     bool attn_items = n_items > 1;
     const bool prefill_items = n_items == 1 && items[0].n > MAX_CHUNK && !advance;
+    if ((pos_base || wait_ev || rec_ev) && !prefill_items) return 1;   // only a prefill chunk is split
     int n_attn = n_items;
     int max_len = 1;
     {
@@ -1444,7 +1487,7 @@ int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, 
             if (prefill_items) {
                 for (int c0 = 0; c0 < I.n; c0 += MAX_CHUNK)
                     ai.push_back(AttnItem{s->kq, s->vq, s->ks, s->vs, &s->ctl->pos_scratch, I.row0 + c0,
-                                          I.n - c0 < MAX_CHUNK ? I.n - c0 : MAX_CHUNK, s->seq_len, c0});
+                                          I.n - c0 < MAX_CHUNK ? I.n - c0 : MAX_CHUNK, s->seq_len, pos_base + c0});
             } else {
                 ai.push_back(AttnItem{s->kq, s->vq, s->ks, s->vs, &s->ctl->pos_scratch, I.row0, I.n, s->seq_len, 0});
             }
@@ -1500,11 +1543,14 @@ int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, 
                     const size_t off = (size_t)plane * s->seq_len * kvd;
                     p.kcache = s->kq + off; p.vcache = s->vq + off;
                     p.kscale = s->ks + off / 32; p.vscale = s->vs + off / 32;
-                    p.ctl_pos = &s->ctl->pos_scratch; p.pos_off = 0;
+                    p.ctl_pos = &s->ctl->pos_scratch; p.pos_off = pos_base;
                     CK(l98k_attn_prep(&p, I.n, st));
                 }
+                // (a split chunk's second half reads the first half's K and V rows)
+                if (wait_ev) CK(hipStreamWaitEvent(st, wait_ev[l], 0));
                 CK(l98k_attn_items(&a, w->aitems, n_attn, plane, max_len, w->att_items, att_item,
                                    prefill_items ? 1 : 0, st));
+                if (rec_ev) CK(hipEventRecord(rec_ev[l], st));
             }
             for (int it = 0; it < n_items && !attn_items; it++) {
                 const WideItem &I = items[it];
@@ -1569,7 +1615,11 @@ int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, 
                 a.xq += r0 * value; a.xqs += r0 * (value / 32);
                 a.rec = w->kda_rec;
                 a.orow = w->kda_o;
+                // (a split chunk's second half starts from the state and conv
+                // history the first half leaves)
+                if (wait_ev) CK(hipStreamWaitEvent(st, wait_ev[l], 0));
                 CK(l98k_kda_split(&a, items[0].n, kd, c.conv_kernel, st));
+                if (rec_ev) CK(hipEventRecord(rec_ev[l], st));
             } else {
                 CK(l98k_kda_items(&a, w->kitems, n_items, (size_t)li * nv * kd * c.lin_v_head_dim,
                                   (size_t)li * c.lin_conv_dim * hist, kd, c.conv_kernel, st));
@@ -1810,14 +1860,39 @@ int batch_capture_dev(DState *d, LZRunState *s, const int *tokens, int n, int po
     DWide *w = n >= WIDE_MIN ? wide_get(d->m) : nullptr;
     if (w) {
         // wide chunks of up to WIDE_MAX rows: each one's positions start at
-        // pos_scratch, which the chunk's own control write moves along
+        // pos_scratch, which the chunk's own control write moves along.  A
+        // chunk of at least WIDE_SPLIT rows runs as two halves on two streams:
+        // the second half's layer l waits, before its KDA recurrence or
+        // attention, for the first half's (state, conv history and K/V rows
+        // of the rows before it), so each half's serial recurrence overlaps
+        // the other half's other work.
+        DModel *dm = const_cast<DModel *>(d->m);
         for (int done = 0; done < n;) {
             const int k = n - done < w->cap ? n - done : w->cap;
             h.pos_scratch = pos0 + done;
             CK(ctl_put(d, h));
-            CK(hipMemcpyAsync(w->toks, d->tokbuf + done, sizeof(int) * (size_t)k, hipMemcpyDeviceToDevice, d->st));
-            const WideItem item{d, 0, k, pos0 + done};
-            CK(wide_forward(d->m, w, &item, 1, k, false, d->hcap + (size_t)done * c.hidden_size, nullptr, d->st));
+            const int k0 = ((k + 1) / 2 + MAX_CHUNK - 1) & ~(MAX_CHUNK - 1), k1 = k - k0;
+            if (k >= WIDE_SPLIT && k1 > MAX_CHUNK && wide_pair(dm, w)) {
+                DWide *w2 = w->peer;
+                hipEvent_t *ev = w->ev.data();
+                const int L = c.n_layers;
+                CK(hipMemcpyAsync(w->toks, d->tokbuf + done, sizeof(int) * (size_t)k0, hipMemcpyDeviceToDevice, d->st));
+                CK(hipMemcpyAsync(w2->toks, d->tokbuf + done + k0, sizeof(int) * (size_t)k1, hipMemcpyDeviceToDevice,
+                                  d->st));
+                CK(hipEventRecord(ev[L], d->st));                     // the second stream starts after these
+                CK(hipStreamWaitEvent(w->st2, ev[L], 0));
+                const WideItem i0{d, 0, k0, pos0 + done}, i1{d, 0, k1, pos0 + done + k0};
+                CK(wide_forward(d->m, w, &i0, 1, k0, false, d->hcap + (size_t)done * c.hidden_size, nullptr, d->st, 0,
+                                nullptr, ev));
+                CK(wide_forward(d->m, w2, &i1, 1, k1, false, d->hcap + (size_t)(done + k0) * c.hidden_size, nullptr,
+                                w->st2, k0, ev, nullptr));
+                CK(hipEventRecord(ev[L + 1], w->st2));                // and the first one continues after it
+                CK(hipStreamWaitEvent(d->st, ev[L + 1], 0));
+            } else {
+                CK(hipMemcpyAsync(w->toks, d->tokbuf + done, sizeof(int) * (size_t)k, hipMemcpyDeviceToDevice, d->st));
+                const WideItem item{d, 0, k, pos0 + done};
+                CK(wide_forward(d->m, w, &item, 1, k, false, d->hcap + (size_t)done * c.hidden_size, nullptr, d->st));
+            }
             done += k;
             lz_debug_n_chunks++;
         }
