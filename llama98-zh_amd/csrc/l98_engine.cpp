@@ -1326,10 +1326,10 @@ struct DWide {
     AttnItem *aitems;
     float *att_items = nullptr;   // attention scratch of an item launch, sized on demand
     size_t att_items_floats = 0;
-    // the second half of a split prefill chunk (see batch_capture_dev): its
-    // own scratch, a second stream, and one event per layer plus two
-    DWide *peer = nullptr;
-    hipStream_t st2 = nullptr;
+    // the later parts of a split prefill chunk (see batch_capture_dev): each
+    // its own scratch and stream, and per part one event per layer plus two
+    std::vector<DWide *> peer;
+    std::vector<hipStream_t> pst;
     std::vector<hipEvent_t> ev;
 };
 
@@ -1337,7 +1337,9 @@ namespace {
 
 #define WIDE_MAX 512          // rows of one wide forward
 #define WIDE_MIN 16           // prefills shorter than this take the chunked path
-#define WIDE_SPLIT 64         // wide prefill chunks of at least this many rows run as two halves
+#define WIDE_SPLIT 64         // wide prefill chunks of at least this many rows run in parts
+#define WIDE_PARTS 2          // parts of a split chunk, each on its own stream (3 and 4 parts measured
+                              // slower: the host's launch enqueue outgrows the device time)
 
 // nullptr (the callers take the chunked path) for a SubLN model, whose
 // per-projection norms this many-row forward does not carry, and for a
@@ -1412,24 +1414,32 @@ DWide *wide_get(const DModel *cm) {
     return m->wide;
 }
 
-// The pair for a split prefill chunk: w's peer scratch, a second stream
-// (default priority) and the events; false when any of it cannot be made.
-bool wide_pair(DModel *m, DWide *w) {
-    if (w->peer) return true;
-    DWide *p = wide_alloc(m);
-    if (!p) return false;
-    std::vector<hipEvent_t> ev((size_t)m->c.n_layers + 2, nullptr);
-    bool ok = hipStreamCreateWithFlags(&w->st2, hipStreamNonBlocking) == hipSuccess;
+// The parts of a split prefill chunk: WIDE_PARTS - 1 peer scratches and
+// streams (default priority) and WIDE_PARTS x (n_layers + 2) events; false
+// when any of it cannot be made.
+bool wide_parts(DModel *m, DWide *w) {
+    if (!w->peer.empty()) return true;
+    std::vector<DWide *> peer;
+    std::vector<hipStream_t> pst;
+    std::vector<hipEvent_t> ev((size_t)WIDE_PARTS * (m->c.n_layers + 2), nullptr);
+    bool ok = true;
+    for (int p = 1; p < WIDE_PARTS && ok; p++) {
+        DWide *q = wide_alloc(m);
+        hipStream_t sq = nullptr;
+        ok = q && hipStreamCreateWithFlags(&sq, hipStreamNonBlocking) == hipSuccess;
+        if (q) peer.push_back(q);
+        if (sq) pst.push_back(sq);
+    }
     for (auto &e : ev) ok = ok && hipEventCreateWithFlags(&e, hipEventDisableTiming) == hipSuccess;
     if (!ok) {
         for (auto &e : ev)
             if (e) (void)hipEventDestroy(e);
-        if (w->st2) (void)hipStreamDestroy(w->st2);
-        w->st2 = nullptr;
-        wide_release(p);
+        for (auto sq : pst) (void)hipStreamDestroy(sq);
+        for (auto q : peer) wide_release(q);
         return false;
     }
-    w->peer = p;
+    w->peer = peer;
+    w->pst = pst;
     w->ev = ev;
     return true;
 }
@@ -1437,10 +1447,10 @@ bool wide_pair(DModel *m, DWide *w) {
 void wide_free(DModel *m) {
     DWide *w = m->wide;
     if (!w) return;
-    if (w->st2) (void)hipStreamSynchronize(w->st2);
+    for (auto sq : w->pst) (void)hipStreamSynchronize(sq);
     for (auto &e : w->ev) (void)hipEventDestroy(e);
-    if (w->st2) (void)hipStreamDestroy(w->st2);
-    wide_release(w->peer);
+    for (auto sq : w->pst) (void)hipStreamDestroy(sq);
+    for (auto q : w->peer) wide_release(q);
     wide_release(w);
     m->wide = nullptr;
 }
@@ -1861,33 +1871,35 @@ int batch_capture_dev(DState *d, LZRunState *s, const int *tokens, int n, int po
     if (w) {
         // wide chunks of up to WIDE_MAX rows: each one's positions start at
         // pos_scratch, which the chunk's own control write moves along.  A
-        // chunk of at least WIDE_SPLIT rows runs as two halves on two streams:
-        // the second half's layer l waits, before its KDA recurrence or
-        // attention, for the first half's (state, conv history and K/V rows
-        // of the rows before it), so each half's serial recurrence overlaps
-        // the other half's other work.
+        // chunk of at least WIDE_SPLIT rows runs as WIDE_PARTS parts, each on
+        // its own stream with its own scratch: part p's layer l waits, before
+        // its KDA recurrence or attention, for part p - 1's (the state, conv
+        // history and K/V rows of the rows before it), so each part's serial
+        // recurrence overlaps the other parts' remaining work.
         DModel *dm = const_cast<DModel *>(d->m);
         for (int done = 0; done < n;) {
             const int k = n - done < w->cap ? n - done : w->cap;
             h.pos_scratch = pos0 + done;
             CK(ctl_put(d, h));
-            const int k0 = ((k + 1) / 2 + MAX_CHUNK - 1) & ~(MAX_CHUNK - 1), k1 = k - k0;
-            if (k >= WIDE_SPLIT && k1 > MAX_CHUNK && wide_pair(dm, w)) {
-                DWide *w2 = w->peer;
-                hipEvent_t *ev = w->ev.data();
-                const int L = c.n_layers;
-                CK(hipMemcpyAsync(w->toks, d->tokbuf + done, sizeof(int) * (size_t)k0, hipMemcpyDeviceToDevice, d->st));
-                CK(hipMemcpyAsync(w2->toks, d->tokbuf + done + k0, sizeof(int) * (size_t)k1, hipMemcpyDeviceToDevice,
-                                  d->st));
-                CK(hipEventRecord(ev[L], d->st));                     // the second stream starts after these
-                CK(hipStreamWaitEvent(w->st2, ev[L], 0));
-                const WideItem i0{d, 0, k0, pos0 + done}, i1{d, 0, k1, pos0 + done + k0};
-                CK(wide_forward(d->m, w, &i0, 1, k0, false, d->hcap + (size_t)done * c.hidden_size, nullptr, d->st, 0,
-                                nullptr, ev));
-                CK(wide_forward(d->m, w2, &i1, 1, k1, false, d->hcap + (size_t)(done + k0) * c.hidden_size, nullptr,
-                                w->st2, k0, ev, nullptr));
-                CK(hipEventRecord(ev[L + 1], w->st2));                // and the first one continues after it
-                CK(hipStreamWaitEvent(d->st, ev[L + 1], 0));
+            const int kp = ((k + WIDE_PARTS - 1) / WIDE_PARTS + MAX_CHUNK - 1) & ~(MAX_CHUNK - 1);
+            if (k >= WIDE_SPLIT && k - (WIDE_PARTS - 1) * kp > MAX_CHUNK && wide_parts(dm, w)) {
+                const int L = c.n_layers, E = L + 2;
+                hipEvent_t *ev = w->ev.data();             // part p: ev[p * E + l], start E - 2, end E - 1
+                CK(hipEventRecord(ev[E - 2], d->st));      // the other streams start after the control write
+                for (int p = 0; p < WIDE_PARTS; p++) {
+                    DWide *wp = p ? w->peer[p - 1] : w;
+                    hipStream_t sp = p ? w->pst[p - 1] : d->st;
+                    const int r0 = p * kp, kr = p + 1 < WIDE_PARTS ? kp : k - r0;
+                    if (p) CK(hipStreamWaitEvent(sp, ev[E - 2], 0));
+                    CK(hipMemcpyAsync(wp->toks, d->tokbuf + done + r0, sizeof(int) * (size_t)kr,
+                                      hipMemcpyDeviceToDevice, sp));
+                    const WideItem item{d, 0, kr, pos0 + done + r0};
+                    CK(wide_forward(d->m, wp, &item, 1, kr, false, d->hcap + (size_t)(done + r0) * c.hidden_size,
+                                    nullptr, sp, r0, p ? ev + (size_t)(p - 1) * E : nullptr,
+                                    p + 1 < WIDE_PARTS ? ev + (size_t)p * E : nullptr));
+                    if (p) CK(hipEventRecord(ev[(size_t)p * E + E - 1], sp));
+                }
+                for (int p = 1; p < WIDE_PARTS; p++) CK(hipStreamWaitEvent(d->st, ev[(size_t)p * E + E - 1], 0));
             } else {
                 CK(hipMemcpyAsync(w->toks, d->tokbuf + done, sizeof(int) * (size_t)k, hipMemcpyDeviceToDevice, d->st));
                 const WideItem item{d, 0, k, pos0 + done};
