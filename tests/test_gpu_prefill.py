@@ -78,3 +78,38 @@ def test_configs3_prompt_chunking_invariant(pkg, model_root):
     finally:
         eng.free_session(other)
         eng.close()
+
+
+@pytest.mark.parametrize("n", [63, 64, 65, 97, 130, 600])
+def test_split_prefill_matches_chunked(pkg, server, n):
+    """A wide prefill chunk of 64 or more rows runs in two parts on two
+    streams (the second part's layers wait for the first part's KDA
+    recurrence and attention); rows and the next verify's logits equal the
+    8-row chunked path bit for bit, at part sizes around the split's
+    threshold and rounding, and over two wide chunks (600 rows)."""
+    print(f"[case] split prefill n={n}", flush=True)
+    prompt = pkg.prompt_tokens(9, n, 8192)
+    eng = pkg.Engine(server)
+    other = eng.add_session()
+    try:
+        eng.reset()
+        h_wide = eng.batch_capture(prompt, 0)
+        assert h_wide is not None
+        lib, d = eng.lib, eng.d
+        lib.lz_state_reset(C.byref(other), C.byref(eng.m))
+        h_small = np.zeros((n, d), np.float32)
+        for p0 in range(0, n, 15):                         # below the wide path's threshold
+            t = np.ascontiguousarray(prompt[p0:p0 + 15], np.int32)
+            buf = np.zeros((len(t), d), np.float32)
+            assert lib.lz_forward_batch_capture(C.byref(eng.m), C.byref(other), t.ctypes.data_as(C.POINTER(C.c_int)),
+                                                len(t), p0, buf.ctypes.data_as(C.POINTER(C.c_float)))
+            h_small[p0:p0 + len(t)] = buf
+        assert same_bits(h_wide, h_small), "hidden rows: " + diff_report(h_wide, h_small)
+        toks = np.array([3, 1000, 77, 8191], np.int32)
+        v_wide = eng.verify(toks, n)
+        assert lib.lz_forward_verify(C.byref(eng.m), C.byref(other), toks.ctypes.data_as(C.POINTER(C.c_int)), 4, n) == 0
+        lg = np.ctypeslib.as_array(other.mtp_logits, shape=(pkg.L98_SPEC_K_GPU + 1, eng.V))[:4]
+        assert same_bits(v_wide[0], lg), "verify logits after the two prefills: " + diff_report(v_wide[0], lg)
+    finally:
+        eng.free_session(other)
+        eng.close()
