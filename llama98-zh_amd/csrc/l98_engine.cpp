@@ -1468,12 +1468,16 @@ int mf(const DMat &W, const int8_t *xq, const float *xqs, int R, float *out, int
 // slot bases and positions (pos_scratch = the item's pos0) before.
 int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, int R, bool advance, float *capture,
                  float *logits, hipStream_t st, int pos_base = 0, hipEvent_t *wait_ev = nullptr,
-                 hipEvent_t *rec_ev = nullptr) {
+                 hipEvent_t *rec_ev = nullptr, int l0 = 0, int l1 = -1) {
     const LZModelConfig &c = m->c;
     const int d = c.hidden_size, E = c.num_experts, topk = c.num_experts_per_token;
     const int lat = c.moe_latent_dim, inter = c.moe_intermediate_size, sw = c.moe_shared_width;
     const float eps = c.rms_norm_eps;
-    if (R < 1 || R > w->cap || n_items < 1 || n_items > w->cap) return 1;
+    if (l1 < 0) l1 = c.n_layers;
+    if (R < 1 || R > w->cap || n_items < 1 || n_items > w->cap || l0 < 0 || l0 >= l1 || l1 > c.n_layers) return 1;
+    // Layers [l0, l1) only (a split prefill enqueues its parts layer by layer,
+    // in turn): the tables, the attention scratch and the embedding come with
+    // layer 0, the final norm with the last layer.
     // the sessions' tables for the item launches
     // Attention runs as one item launch per kernel: over the sessions'
     // verify rows, or over one session's prefill rows cut into MAX_CHUNK-row
@@ -1506,11 +1510,13 @@ int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, 
             attn_items = true;
             n_attn = (int)ai.size();
         }
-        CK(hipMemcpyAsync(w->kitems, ki.data(), sizeof(KdaItem) * ki.size(), hipMemcpyHostToDevice, st));
-        CK(hipMemcpyAsync(w->aitems, ai.data(), sizeof(AttnItem) * ai.size(), hipMemcpyHostToDevice, st));
+        if (l0 == 0) {
+            CK(hipMemcpyAsync(w->kitems, ki.data(), sizeof(KdaItem) * ki.size(), hipMemcpyHostToDevice, st));
+            CK(hipMemcpyAsync(w->aitems, ai.data(), sizeof(AttnItem) * ai.size(), hipMemcpyHostToDevice, st));
+        }
     }
     const size_t att_item = (size_t)MAX_CHUNK * c.n_heads * (size_t)((max_len + 3) & ~3);
-    if (attn_items && w->att_items_floats < att_item * n_attn) {
+    if (l0 == 0 && attn_items && w->att_items_floats < att_item * n_attn) {
         CK(hipStreamSynchronize(st));
         if (w->att_items) (void)hipFree(w->att_items);
         w->att_items = nullptr;
@@ -1518,9 +1524,10 @@ int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, 
         CK(hipMalloc((void **)&w->att_items, sizeof(float) * att_item * n_attn));
         w->att_items_floats = att_item * n_attn;
     }
-    CK(l98k_embed(m->embed.q, m->embed.s, w->toks, d, m->embed.gs, R, w->x, st));
-    const float *ra = nullptr, *rb = nullptr;
-    for (int l = 0; l < c.n_layers; l++) {
+    if (l0 == 0) CK(l98k_embed(m->embed.q, m->embed.s, w->toks, d, m->embed.gs, R, w->x, st));
+    // every layer leaves its two residual addends in up_out and sd_out
+    const float *ra = l0 ? w->up_out : nullptr, *rb = l0 ? w->sd_out : nullptr;
+    for (int l = l0; l < l1; l++) {
         const DLayer &L = m->L[l];
         CK(l98k_rmsnorm(w->x, d, ra, rb, L.in_norm, d, eps, R, nullptr, 0, w->xq, w->xqs, st));
         if (L.type == 1) {
@@ -1661,6 +1668,7 @@ int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, 
         ra = w->up_out;
         rb = w->sd_out;
     }
+    if (l1 < c.n_layers) return 0;
     CK(l98k_rmsnorm(w->x, d, ra, rb, m->final_norm, d, eps, R, capture, d, logits ? w->xq : nullptr, w->xqs, st));
     if (logits) CK(mf(m->embed, w->xq, w->xqs, R, logits, c.vocab_size, st));
     return 0;
@@ -1886,18 +1894,26 @@ int batch_capture_dev(DState *d, LZRunState *s, const int *tokens, int n, int po
                 const int L = c.n_layers, E = L + 2;
                 hipEvent_t *ev = w->ev.data();             // part p: ev[p * E + l], start E - 2, end E - 1
                 CK(hipEventRecord(ev[E - 2], d->st));      // the other streams start after the control write
-                for (int p = 0; p < WIDE_PARTS; p++) {
-                    DWide *wp = p ? w->peer[p - 1] : w;
-                    hipStream_t sp = p ? w->pst[p - 1] : d->st;
-                    const int r0 = p * kp, kr = p + 1 < WIDE_PARTS ? kp : k - r0;
-                    if (p) CK(hipStreamWaitEvent(sp, ev[E - 2], 0));
-                    CK(hipMemcpyAsync(wp->toks, d->tokbuf + done + r0, sizeof(int) * (size_t)kr,
-                                      hipMemcpyDeviceToDevice, sp));
-                    const WideItem item{d, 0, kr, pos0 + done + r0};
-                    CK(wide_forward(d->m, wp, &item, 1, kr, false, d->hcap + (size_t)(done + r0) * c.hidden_size,
-                                    nullptr, sp, r0, p ? ev + (size_t)(p - 1) * E : nullptr,
-                                    p + 1 < WIDE_PARTS ? ev + (size_t)p * E : nullptr));
-                    if (p) CK(hipEventRecord(ev[(size_t)p * E + E - 1], sp));
+                // the parts' layers are enqueued in turn (layer 0 of every
+                // part, then layer 1, ...), so every stream has work from the
+                // start and each wait follows the record it waits for
+                for (int l = 0; l < L; l++) {
+                    for (int p = 0; p < WIDE_PARTS; p++) {
+                        DWide *wp = p ? w->peer[p - 1] : w;
+                        hipStream_t sp = p ? w->pst[p - 1] : d->st;
+                        const int r0 = p * kp, kr = p + 1 < WIDE_PARTS ? kp : k - r0;
+                        if (l == 0) {
+                            if (p) CK(hipStreamWaitEvent(sp, ev[E - 2], 0));
+                            CK(hipMemcpyAsync(wp->toks, d->tokbuf + done + r0, sizeof(int) * (size_t)kr,
+                                              hipMemcpyDeviceToDevice, sp));
+                        }
+                        const WideItem item{d, 0, kr, pos0 + done + r0};
+                        CK(wide_forward(d->m, wp, &item, 1, kr, false,
+                                        d->hcap + (size_t)(done + r0) * c.hidden_size, nullptr, sp, r0,
+                                        p ? ev + (size_t)(p - 1) * E : nullptr,
+                                        p + 1 < WIDE_PARTS ? ev + (size_t)p * E : nullptr, l, l + 1));
+                        if (p && l == L - 1) CK(hipEventRecord(ev[(size_t)p * E + E - 1], sp));
+                    }
                 }
                 for (int p = 1; p < WIDE_PARTS; p++) CK(hipStreamWaitEvent(d->st, ev[(size_t)p * E + E - 1], 0));
             } else {

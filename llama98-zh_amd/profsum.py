@@ -10,9 +10,10 @@ Prints, as markdown:
   * the tied lm_head GEMV launches (k_gemv_q8 dispatches whose grid covers
     `vocab` rows), whose mean duration is the figure bench.py's roofline
     uses;
-  * the prompt's many-row path: the dispatches from the last many-row
-    k_embed to the last many-row kernel (k_mfma_q8, k_kda_post, k_attn_prep)
-    before the first k_accept, i.e. the session's prefill and MTP prefill.
+  * the prompt's many-row path: the dispatches from the last run of
+    many-row k_embed dispatches (one per part of a split chunk) to the last
+    many-row kernel (k_mfma_q8, k_kda_post, k_attn_prep) before the first
+    k_accept, i.e. the session's prefill and MTP prefill.
 """
 import argparse
 import collections
@@ -67,8 +68,13 @@ def main():
         print(table(grp, f"One round (last complete round; span {span / 1e3:.1f} us without graph replay)",
                     "round"))
     first_acc = acc[0] if acc else len(rows)
-    # the last many-row embedding (a grid of at least 16 token rows in y) before it
+    # the many-row embeddings (a grid of at least 16 token rows in y) before
+    # it; a prefill whose chunk runs in parts on several streams has one per
+    # part, close together: take the first of the last such run (embeddings
+    # less than 1 ms apart)
     emb = [i for i, r in enumerate(rows[:first_acc]) if short(r[0]) == "k_embed" and r[5] >= 16]
+    while len(emb) >= 2 and rows[emb[-1]][1] - rows[emb[-2]][1] < 1_000_000:
+        emb = emb[:-2] + emb[-2:-1]
     emb = emb[-1:]
     wide = [i for i, r in enumerate(rows[:first_acc])
             if short(r[0]).startswith(("k_mfma_q8", "k_kda_post", "k_attn_prep"))]
