@@ -1338,8 +1338,9 @@ namespace {
 #define WIDE_MAX 512          // rows of one wide forward
 #define WIDE_MIN 16           // prefills shorter than this take the chunked path
 #define WIDE_SPLIT 64         // wide prefill chunks of at least this many rows run in parts
-#define WIDE_PARTS 2          // parts of a split chunk, each on its own stream (3 and 4 parts measured
-                              // slower: the host's launch enqueue outgrows the device time)
+#define WIDE_PARTS 3          // parts of a split chunk, each on its own stream (measured: 2 parts
+                              // 10.1 ms, 3 parts 9.7 ms, 4 parts 15.0 ms for a 512-row prefill; four
+                              // streams oversubscribe the process's four hardware queues)
 
 // nullptr (the callers take the chunked path) for a SubLN model, whose
 // per-projection norms this many-row forward does not carry, and for a
