@@ -1461,6 +1461,26 @@ int mf(const DMat &W, const int8_t *xq, const float *xqs, int R, float *out, int
     return l98k_mfma_gemm(W.q, W.s, W.rows, W.cols, xq, xqs, R, out, out_stride, st);
 }
 
+// Several weight matrices (same input width) over the same rows, one launch.
+struct MfOut {
+    const DMat *W;
+    float *out;
+    int out_stride;
+};
+int mf_multi(std::initializer_list<MfOut> jobs, const int8_t *xq, const float *xqs, int R, hipStream_t st) {
+    const int8_t *W[6];
+    const float *ws[6];
+    float *out[6];
+    int N[6], os[6], n = 0, K = 0;
+    for (const MfOut &j : jobs) {
+        if (n == 6 || (n && j.W->cols != K)) return 1;
+        K = j.W->cols;
+        W[n] = j.W->q; ws[n] = j.W->s; N[n] = j.W->rows; out[n] = j.out; os[n] = j.out_stride;
+        n++;
+    }
+    return l98k_mfma_gemm_multi(n, W, ws, N, out, os, K, xq, xqs, R, st);
+}
+
 // The trunk over R rows of w->toks (device ids), grouped into sessions by
 // items (row order).  advance: KDA ring advance per token (verify) or not
 // (prefill).  capture: device rows [R][d] of the final-normed hidden, or
@@ -1533,9 +1553,7 @@ int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, 
         CK(l98k_rmsnorm(w->x, d, ra, rb, L.in_norm, d, eps, R, nullptr, 0, w->xq, w->xqs, st));
         if (L.type == 1) {
             const int qgd = c.attn_qgate_dim, kvd = c.attn_kv_dim, qd = c.attn_q_dim;
-            CK(mf(L.q, w->xq, w->xqs, R, w->qg, qgd, st));
-            CK(mf(L.k, w->xq, w->xqs, R, w->kp, kvd, st));
-            CK(mf(L.v, w->xq, w->xqs, R, w->vp, kvd, st));
+            CK(mf_multi({{&L.q, w->qg, qgd}, {&L.k, w->kp, kvd}, {&L.v, w->vp, kvd}}, w->xq, w->xqs, R, st));
             const int plane = m->full_index[l];
             if (attn_items) {
                 // every session's rows in one launch per kernel
@@ -1598,12 +1616,9 @@ int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, 
         } else {
             const int key = c.lin_key_dim, value = c.lin_value_dim, nv = c.lin_n_v_heads, kd = c.lin_k_head_dim;
             const int rank = c.kda_gate_rank, hist = c.conv_kernel - 1;
-            CK(mf(L.kq, w->xq, w->xqs, R, w->pq, key, st));
-            CK(mf(L.kk, w->xq, w->xqs, R, w->pk, key, st));
-            CK(mf(L.kv, w->xq, w->xqs, R, w->pv, value, st));
-            CK(mf(L.fa, w->xq, w->xqs, R, w->pfa, rank, st));
-            CK(mf(L.kb, w->xq, w->xqs, R, w->pb, nv, st));
-            CK(mf(L.kg, w->xq, w->xqs, R, w->pg, value, st));
+            CK(mf_multi({{&L.kq, w->pq, key}, {&L.kk, w->pk, key}, {&L.kv, w->pv, value}, {&L.fa, w->pfa, rank},
+                         {&L.kb, w->pb, nv}, {&L.kg, w->pg, value}},
+                        w->xq, w->xqs, R, st));
             const int li = m->lin_index[l];
             // every session's rows in one launch (a prefill's rows in
             // sub-chunks inside its blocks)
@@ -1646,10 +1661,8 @@ int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, 
         }
         CK(l98k_rmsnorm(w->x, d, w->blk, nullptr, L.post_norm, d, eps, R, nullptr, 0, w->xq, w->xqs, st));
         // latent MoE (src/forward_moe.c:220-553) with the shared expert
-        CK(mf(L.router, w->xq, w->xqs, R, w->rl, E, st));
-        CK(mf(L.down, w->xq, w->xqs, R, w->latx, lat, st));
-        CK(mf(L.sg, w->xq, w->xqs, R, w->sgo, sw, st));
-        CK(mf(L.su, w->xq, w->xqs, R, w->suo, sw, st));
+        CK(mf_multi({{&L.router, w->rl, E}, {&L.down, w->latx, lat}, {&L.sg, w->sgo, sw}, {&L.su, w->suo, sw}},
+                    w->xq, w->xqs, R, st));
         const int pairs = R * topk;
         CK(l98k_moe_route_wide(w->rl, L.bias, E, topk, R, w->sel_idx, w->sel_w, st));
         CK(l98k_moe_group(w->sel_idx, pairs, topk, E, w->ng, w->gexp, w->goff, w->gcnt, w->list, w->pair_token, st));
@@ -1691,8 +1704,7 @@ int mtp_prefill_wide(DState *s, DWide *w, const float *h, const int *toks, int n
                         m->mtp_pre_h, eps, R, w->mq, w->mqs, st));
         CK(mf(m->mtp_fc, w->mq, w->mqs, R, w->blk, d, st));
         CK(l98k_rmsnorm(w->blk, d, nullptr, nullptr, m->mtp.in_norm, d, eps, R, nullptr, 0, w->xq, w->xqs, st));
-        CK(mf(m->mtp.k, w->xq, w->xqs, R, w->kp, kvd, st));
-        CK(mf(m->mtp.v, w->xq, w->xqs, R, w->vp, kvd, st));
+        CK(mf_multi({{&m->mtp.k, w->kp, kvd}, {&m->mtp.v, w->vp, kvd}}, w->xq, w->xqs, R, st));
         AttnArgs a{};
         a.kp = w->kp; a.vp = w->vp;
         a.k_norm = m->mtp.k_norm; a.rope_cs = m->rope_cs;

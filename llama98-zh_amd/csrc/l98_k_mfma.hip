@@ -40,6 +40,21 @@ typedef int v4i_t __attribute__((ext_vector_type(4)));
 // t, t < M) or grouped (block z is group g: expert gexp[g], columns
 // list[goff[g] .. goff[g] + gcnt[g]), activation row xmap[col] or col,
 // output row col).
+// Dense GEMMs of one input sharing a launch: job j covers block rows
+// [blk0, next job's blk0) of the grid's x; n == 0: the launch's own W / ws /
+// N / out.
+#define MF_MAX_JOBS 6
+struct MfJob {
+    const int8_t *W;
+    const float *ws;
+    float *out;
+    int N, out_stride, blk0, pad;
+};
+struct MfJobs {
+    MfJob j[MF_MAX_JOBS];
+    int n, pad[3];
+};
+
 struct MfCols {
     const int *gexp, *goff, *gcnt, *list, *xmap;
     const int *ng;           // groups actually present (device)
@@ -127,16 +142,34 @@ __device__ __forceinline__ void mf_stage(float (&f)[MF_RT][4], const int8_t (*sw
 }
 
 template <bool FULLK>
-__global__ __launch_bounds__(MF_THREADS) void k_mfma_q8(const int8_t *__restrict__ W, const float *__restrict__ ws,
-                                                         int N, int K, size_t w_group_stride,
+__global__ __launch_bounds__(MF_THREADS) void k_mfma_q8(const int8_t *__restrict__ W0, const float *__restrict__ ws0,
+                                                         int N0, int K, size_t w_group_stride,
                                                          const int8_t *__restrict__ X, const float *__restrict__ Xs,
-                                                         int M, MfCols cols, float *__restrict__ out,
-                                                         int out_stride) {
+                                                         int M, MfCols cols, float *__restrict__ out0,
+                                                         int out_stride0, MfJobs jobs) {
     __shared__ __align__(16) int8_t s_w[2][MF_ROWS][MF_LDS_ROW];
     __shared__ __align__(16) int8_t s_x[2][MF_COLS][MF_LDS_ROW];
     __shared__ __align__(16) float s_xs[2][MF_COLS][MF_KC / 32];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int n0 = blockIdx.x * MF_ROWS;
+    const int8_t *W = W0;
+    const float *ws = ws0;
+    float *out = out0;
+    int N = N0, out_stride = out_stride0, bx = blockIdx.x;
+    if (jobs.n) {
+        // the job whose block rows hold this block (the index is uniform)
+        int ji = 0;
+#pragma unroll
+        for (int k = 1; k < MF_MAX_JOBS; k++)
+            if (k < jobs.n && bx >= jobs.j[k].blk0) ji = k;
+        const MfJob jb = jobs.j[ji];
+        W = jb.W;
+        ws = jb.ws;
+        out = jb.out;
+        N = jb.N;
+        out_stride = jb.out_stride;
+        bx -= jb.blk0;
+    }
+    const int n0 = bx * MF_ROWS;
     const int nb = K >> 5;
     int ncols = M, cbase = 0;
     const int8_t *Wg = W;
@@ -323,10 +356,36 @@ extern "C" int l98k_mfma_gemm(const int8_t *W, const float *ws, int N, int K, co
     const dim3 grid((N + MF_ROWS - 1) / MF_ROWS, (M + MF_COLS - 1) / MF_COLS, 1);
     if (K % MF_KC == 0)
         hipLaunchKernelGGL(k_mfma_q8<true>, grid, dim3(MF_THREADS), 0, st, W, ws, N, K, (size_t)0, X, Xs, M, c, out,
-                           out_stride);
+                           out_stride, MfJobs{});
     else
         hipLaunchKernelGGL(k_mfma_q8<false>, grid, dim3(MF_THREADS), 0, st, W, ws, N, K, (size_t)0, X, Xs, M, c, out,
-                           out_stride);
+                           out_stride, MfJobs{});
+    return (int)hipGetLastError();
+}
+
+// Several dense GEMMs over the same activation rows (X, Xs: M rows of K) in
+// one launch: job j multiplies W[j] (N[j] x K, scales ws[j]) into out[j]
+// (row stride out_stride[j]).  The blocks of job j follow those of job j - 1.
+extern "C" int l98k_mfma_gemm_multi(int n_jobs, const int8_t *const *W, const float *const *ws, const int *N,
+                                    float *const *out, const int *out_stride, int K, const int8_t *X,
+                                    const float *Xs, int M, hipStream_t st) {
+    if (n_jobs < 1 || n_jobs > MF_MAX_JOBS || M < 1 || K < 32 || (K & 31)) return -1;
+    MfJobs jobs{};
+    int blocks = 0;
+    for (int j = 0; j < n_jobs; j++) {
+        if (N[j] < 1 || out_stride[j] < N[j]) return -1;
+        jobs.j[j] = MfJob{W[j], ws[j], out[j], N[j], out_stride[j], blocks, 0};
+        blocks += (N[j] + MF_ROWS - 1) / MF_ROWS;
+    }
+    jobs.n = n_jobs;
+    MfCols c{};
+    const dim3 grid(blocks, (M + MF_COLS - 1) / MF_COLS, 1);
+    if (K % MF_KC == 0)
+        hipLaunchKernelGGL(k_mfma_q8<true>, grid, dim3(MF_THREADS), 0, st, W[0], ws[0], N[0], K, (size_t)0, X, Xs, M, c,
+                           out[0], out_stride[0], jobs);
+    else
+        hipLaunchKernelGGL(k_mfma_q8<false>, grid, dim3(MF_THREADS), 0, st, W[0], ws[0], N[0], K, (size_t)0, X, Xs, M,
+                           c, out[0], out_stride[0], jobs);
     return (int)hipGetLastError();
 }
 
@@ -341,10 +400,10 @@ extern "C" int l98k_mfma_gemm_grouped(const int8_t *bank, const float *bank_s, i
     const dim3 grid((N + MF_ROWS - 1) / MF_ROWS, 1, max_groups);
     if (K % MF_KC == 0)
         hipLaunchKernelGGL(k_mfma_q8<true>, grid, dim3(MF_THREADS), 0, st, bank, bank_s, N, K, (size_t)N * K, X, Xs, 0,
-                           c, out, out_stride);
+                           c, out, out_stride, MfJobs{});
     else
         hipLaunchKernelGGL(k_mfma_q8<false>, grid, dim3(MF_THREADS), 0, st, bank, bank_s, N, K, (size_t)N * K, X, Xs,
-                           0, c, out, out_stride);
+                           0, c, out, out_stride, MfJobs{});
     return (int)hipGetLastError();
 }
 
