@@ -1461,24 +1461,28 @@ int mf(const DMat &W, const int8_t *xq, const float *xqs, int R, float *out, int
     return l98k_mfma_gemm(W.q, W.s, W.rows, W.cols, xq, xqs, R, out, out_stride, st);
 }
 
-// Several weight matrices (same input width) over the same rows, one launch.
+// Several weight matrices over the same rows, one launch: each job's input
+// (xq, xqs) defaults to the call's.
 struct MfOut {
     const DMat *W;
     float *out;
     int out_stride;
+    const int8_t *xq = nullptr;
+    const float *xqs = nullptr;
 };
 int mf_multi(std::initializer_list<MfOut> jobs, const int8_t *xq, const float *xqs, int R, hipStream_t st) {
-    const int8_t *W[6];
-    const float *ws[6];
+    const int8_t *W[6], *X[6];
+    const float *ws[6], *Xs[6];
     float *out[6];
-    int N[6], os[6], n = 0, K = 0;
+    int N[6], os[6], K[6], n = 0;
     for (const MfOut &j : jobs) {
-        if (n == 6 || (n && j.W->cols != K)) return 1;
-        K = j.W->cols;
-        W[n] = j.W->q; ws[n] = j.W->s; N[n] = j.W->rows; out[n] = j.out; os[n] = j.out_stride;
+        if (n == 6) return 1;
+        W[n] = j.W->q; ws[n] = j.W->s; N[n] = j.W->rows; K[n] = j.W->cols; out[n] = j.out; os[n] = j.out_stride;
+        X[n] = j.xq ? j.xq : xq;
+        Xs[n] = j.xq ? j.xqs : xqs;
         n++;
     }
-    return l98k_mfma_gemm_multi(n, W, ws, N, out, os, K, xq, xqs, R, st);
+    return l98k_mfma_gemm_multi(n, W, ws, N, out, os, K, X, Xs, R, st);
 }
 
 // The trunk over R rows of w->toks (device ids), grouped into sessions by
@@ -1676,9 +1680,9 @@ int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, 
         CK(l98k_mfma_gemm_grouped(L.w2.q, L.w2.s, lat, inter, w->hq, w->hqs, w->ng, maxg, w->gexp, w->goff, w->gcnt,
                                   w->list, nullptr, R, w->h2, lat, st));
         CK(l98k_wide_pro(2, w->h2, nullptr, lat, w->sel_idx, w->sel_w, topk, lat, R, w->cq, w->cqs, st));
-        CK(mf(L.up, w->cq, w->cqs, R, w->up_out, d, st));
         CK(l98k_wide_pro(1, w->sgo, w->suo, sw, nullptr, nullptr, 0, sw, R, w->shq, w->shqs, st));
-        CK(mf(L.sd, w->shq, w->shqs, R, w->sd_out, d, st));
+        CK(mf_multi({{&L.up, w->up_out, d, w->cq, w->cqs}, {&L.sd, w->sd_out, d, w->shq, w->shqs}}, nullptr, nullptr,
+                    R, st));
         ra = w->up_out;
         rb = w->sd_out;
     }

@@ -40,15 +40,17 @@ typedef int v4i_t __attribute__((ext_vector_type(4)));
 // t, t < M) or grouped (block z is group g: expert gexp[g], columns
 // list[goff[g] .. goff[g] + gcnt[g]), activation row xmap[col] or col,
 // output row col).
-// Dense GEMMs of one input sharing a launch: job j covers block rows
-// [blk0, next job's blk0) of the grid's x; n == 0: the launch's own W / ws /
-// N / out.
+// Dense GEMMs over the same rows sharing a launch: job j covers block rows
+// [blk0, next job's blk0) of the grid's x, with its own weights, input (X,
+// Xs, K) and output; n == 0: the launch's own arguments.
 #define MF_MAX_JOBS 6
 struct MfJob {
     const int8_t *W;
     const float *ws;
     float *out;
-    int N, out_stride, blk0, pad;
+    const int8_t *X;
+    const float *Xs;
+    int N, out_stride, blk0, K;
 };
 struct MfJobs {
     MfJob j[MF_MAX_JOBS];
@@ -143,8 +145,8 @@ __device__ __forceinline__ void mf_stage(float (&f)[MF_RT][4], const int8_t (*sw
 
 template <bool FULLK>
 __global__ __launch_bounds__(MF_THREADS) void k_mfma_q8(const int8_t *__restrict__ W0, const float *__restrict__ ws0,
-                                                         int N0, int K, size_t w_group_stride,
-                                                         const int8_t *__restrict__ X, const float *__restrict__ Xs,
+                                                         int N0, int K0, size_t w_group_stride,
+                                                         const int8_t *__restrict__ X0, const float *__restrict__ Xs0,
                                                          int M, MfCols cols, float *__restrict__ out0,
                                                          int out_stride0, MfJobs jobs) {
     __shared__ __align__(16) int8_t s_w[2][MF_ROWS][MF_LDS_ROW];
@@ -154,7 +156,9 @@ __global__ __launch_bounds__(MF_THREADS) void k_mfma_q8(const int8_t *__restrict
     const int8_t *W = W0;
     const float *ws = ws0;
     float *out = out0;
-    int N = N0, out_stride = out_stride0, bx = blockIdx.x;
+    const int8_t *X = X0;
+    const float *Xs = Xs0;
+    int N = N0, K = K0, out_stride = out_stride0, bx = blockIdx.x;
     if (jobs.n) {
         // the job whose block rows hold this block (the index is uniform)
         int ji = 0;
@@ -165,6 +169,9 @@ __global__ __launch_bounds__(MF_THREADS) void k_mfma_q8(const int8_t *__restrict
         W = jb.W;
         ws = jb.ws;
         out = jb.out;
+        X = jb.X;
+        Xs = jb.Xs;
+        K = jb.K;
         N = jb.N;
         out_stride = jb.out_stride;
         bx -= jb.blk0;
@@ -363,29 +370,32 @@ extern "C" int l98k_mfma_gemm(const int8_t *W, const float *ws, int N, int K, co
     return (int)hipGetLastError();
 }
 
-// Several dense GEMMs over the same activation rows (X, Xs: M rows of K) in
-// one launch: job j multiplies W[j] (N[j] x K, scales ws[j]) into out[j]
-// (row stride out_stride[j]).  The blocks of job j follow those of job j - 1.
+// Several dense GEMMs over the same M rows in one launch: job j multiplies
+// W[j] (N[j] x K[j], scales ws[j]) over the rows of X[j] / Xs[j] into out[j]
+// (row stride out_stride[j]).  The blocks of job j follow those of job
+// j - 1.  The full-stage instance needs every K a multiple of 256.
 extern "C" int l98k_mfma_gemm_multi(int n_jobs, const int8_t *const *W, const float *const *ws, const int *N,
-                                    float *const *out, const int *out_stride, int K, const int8_t *X,
-                                    const float *Xs, int M, hipStream_t st) {
-    if (n_jobs < 1 || n_jobs > MF_MAX_JOBS || M < 1 || K < 32 || (K & 31)) return -1;
+                                    float *const *out, const int *out_stride, const int *K,
+                                    const int8_t *const *X, const float *const *Xs, int M, hipStream_t st) {
+    if (n_jobs < 1 || n_jobs > MF_MAX_JOBS || M < 1) return -1;
     MfJobs jobs{};
     int blocks = 0;
+    bool full = true;
     for (int j = 0; j < n_jobs; j++) {
-        if (N[j] < 1 || out_stride[j] < N[j]) return -1;
-        jobs.j[j] = MfJob{W[j], ws[j], out[j], N[j], out_stride[j], blocks, 0};
+        if (N[j] < 1 || out_stride[j] < N[j] || K[j] < 32 || (K[j] & 31)) return -1;
+        full = full && K[j] % MF_KC == 0;
+        jobs.j[j] = MfJob{W[j], ws[j], out[j], X[j], Xs[j], N[j], out_stride[j], blocks, K[j]};
         blocks += (N[j] + MF_ROWS - 1) / MF_ROWS;
     }
     jobs.n = n_jobs;
     MfCols c{};
     const dim3 grid(blocks, (M + MF_COLS - 1) / MF_COLS, 1);
-    if (K % MF_KC == 0)
-        hipLaunchKernelGGL(k_mfma_q8<true>, grid, dim3(MF_THREADS), 0, st, W[0], ws[0], N[0], K, (size_t)0, X, Xs, M, c,
-                           out[0], out_stride[0], jobs);
+    if (full)
+        hipLaunchKernelGGL(k_mfma_q8<true>, grid, dim3(MF_THREADS), 0, st, W[0], ws[0], N[0], K[0], (size_t)0, X[0],
+                           Xs[0], M, c, out[0], out_stride[0], jobs);
     else
-        hipLaunchKernelGGL(k_mfma_q8<false>, grid, dim3(MF_THREADS), 0, st, W[0], ws[0], N[0], K, (size_t)0, X, Xs, M,
-                           c, out[0], out_stride[0], jobs);
+        hipLaunchKernelGGL(k_mfma_q8<false>, grid, dim3(MF_THREADS), 0, st, W[0], ws[0], N[0], K[0], (size_t)0, X[0],
+                           Xs[0], M, c, out[0], out_stride[0], jobs);
     return (int)hipGetLastError();
 }
 

@@ -21,9 +21,11 @@ int l98k_upload_exp_table_mfma(const float *tab);
 // token rows, bit-identical to the GEMV path per token.
 int l98k_mfma_gemm(const int8_t *W, const float *ws, int N, int K, const int8_t *X, const float *Xs, int M, float *out,
                    int out_stride, hipStream_t st);
-// Up to six dense GEMMs over the same activation rows in one launch.
+// Up to six dense GEMMs over the same M rows in one launch (each its own
+// weights, input rows of width K[j] and output).
 int l98k_mfma_gemm_multi(int n_jobs, const int8_t *const *W, const float *const *ws, const int *N, float *const *out,
-                         const int *out_stride, int K, const int8_t *X, const float *Xs, int M, hipStream_t st);
+                         const int *out_stride, const int *K, const int8_t *const *X, const float *const *Xs, int M,
+                         hipStream_t st);
 // Grouped over experts: group g < *ng multiplies expert gexp[g]'s bank rows
 // with its columns list[goff[g] .. + gcnt[g]] (activation row xmap[col] or
 // col, output row col).
