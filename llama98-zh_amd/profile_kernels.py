@@ -17,6 +17,12 @@ Meant to run under
     rocprofv3 --pmc WRITE_SIZE --output-format csv -d OUT -o pmc -- python3 llama98-zh_amd/profile_kernels.py
 
 and summarized by llama98-zh_amd/pmcsum.py.
+
+With --prefill it runs two 512-token session starts instead (the prefill's
+matrix-core GEMMs, k_mfma_q8, for the MFMA counters:
+    rocprofv3 --pmc SQ_INSTS_VALU_MFMA_MOPS_I8 SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE \
+        --output-format csv -d OUT -o pmc -- python3 llama98-zh_amd/profile_kernels.py --prefill
+).
 """
 import argparse
 import os
@@ -31,12 +37,20 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--iters", type=int, default=20)
     ap.add_argument("--model-dir", default=os.path.join(tempfile.gettempdir(), "l98_models"))
+    ap.add_argument("--prefill", action="store_true", help="two 512-token session starts")
     args = ap.parse_args()
     import __graft_entry__
     pkg = __graft_entry__.load_package()
     mdir = os.path.join(args.model_dir, "base")
     pkg.ensure_model(mdir, 1, seed=1234)
     eng = pkg.Engine(mdir)
+    if args.prefill:
+        for r in range(2):
+            eng.reset()
+            eng.session_start(pkg.prompt_tokens(0, 512, eng.V))
+            print(f"prefill {r} done", flush=True)
+        eng.close()
+        return
     eng.session_start(pkg.prompt_tokens(0, 32, eng.V))
     for which, name in ((0, "lm_head"), (4, "kda input"), (5, "attention input"), (6, "moe input"), (2, "copy")):
         ms = eng.time_kernel(which, 4, args.iters)
