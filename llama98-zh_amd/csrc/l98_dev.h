@@ -60,9 +60,14 @@ typedef struct {
 
 // A fused GEMV launch: block (x, y) is tile x of job y, so a block's job is
 // known at entry and its fields load with the kernel's first scalar loads.
+// amax_part (one job only): the launch also stores, per tile and output
+// row t, the packed argmax candidate of the tile's rows (amax_mode 0:
+// sample_argmax's key order, 1: lz_argmax_p1's) at amax_part[t * tiles +
+// tile] (amax_cap entries; tiles * m needed), for l98k_argmax_part.
 typedef struct {
     int n;
-    int pad[3];
+    int amax_mode, amax_cap, pad;
+    unsigned long long *amax_part;
     GemvJob job[MAX_GEMV_JOBS];
 } GemvBatch;
 

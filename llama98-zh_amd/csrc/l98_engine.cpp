@@ -800,6 +800,13 @@ struct DState {
     MoeGroups *grp;
     DevCtl *ctl;
     int *tokbuf;
+    // the lm_head GEMV's argmax epilogue: per-tile candidates;
+    // amax_tok / amax_mode: the next lm_head's argmax target (taken and
+    // cleared by lm_head_gemv)
+    unsigned long long *amax_part = nullptr;
+    int amax_cap = 0;
+    int *amax_tok = nullptr;
+    int amax_mode = 0;
     DevCtl *ctl_pinned = nullptr;
     int cap_rows = 0;                       // rows of hcap / tokbuf
     RoundRec *hist = nullptr;               // device round records
@@ -878,6 +885,12 @@ bool carve(DState *s) {
     s->grp = (MoeGroups *)st_take(s, sizeof(MoeGroups));
     s->ctl = (DevCtl *)st_take(s, sizeof(DevCtl));
     s->tokbuf = (int *)st_take(s, sizeof(int) * (size_t)s->cap_rows);
+    s->amax_cap = 0;
+    for (int m = 1; m <= MAX_CHUNK; m *= 2) {
+        const int need = l98k_gemv_tiles(c.vocab_size, d, m) * m;
+        s->amax_cap = need > s->amax_cap ? need : s->amax_cap;
+    }
+    s->amax_part = (unsigned long long *)st_take(s, sizeof(unsigned long long) * (size_t)s->amax_cap);
     s->hist_cap = s->seq_len;
     s->hist = (RoundRec *)st_take(s, sizeof(RoundRec) * (size_t)s->hist_cap);
     return true;
@@ -897,6 +910,27 @@ int gemv(DState *s, std::initializer_list<GemvJob> jobs, int mtok) {
         if (o.pro.mode == PRO_XQ && !o.xq) { o.xq = s->xq; o.xqs = s->xqs; }
     }
     return l98k_gemv(&b, mtok, s->st);
+}
+
+// The tied lm_head GEMV of job j over mtok rows.  When s->amax_tok is set
+// (then cleared), the rows' argmaxes (mode s->amax_mode) go there: the GEMV
+// keeps each tile's candidates and l98k_argmax_part reduces those, so the
+// argmax reads 8 bytes per tile and row instead of the logits.
+int lm_head_gemv(DState *s, const GemvJob &j, int mtok) {
+    GemvBatch b{};
+    b.n = 1;
+    b.job[0] = j;
+    int *tok = s->amax_tok;
+    s->amax_tok = nullptr;
+    if (tok) {
+        b.amax_mode = s->amax_mode;
+        b.amax_part = s->amax_part;
+        b.amax_cap = s->amax_cap;
+    }
+    CK(l98k_gemv(&b, mtok, s->st));
+    if (tok)
+        CK(l98k_argmax_part(s->amax_part, b.job[0].tiles, j.out, j.out_stride, mtok, s->amax_mode, tok, s->st));
+    return 0;
 }
 
 // GEMV job prologues (how a tile builds its int8 activation rows).
@@ -1169,7 +1203,7 @@ int forward_chunk(DState *s, const int *toks, int nt, const int *ctl_pos, int po
     CK(l98k_rmsnorm(xb[cur], d, ra, rb, m->final_norm, d, eps, nt, capture, d,
                     want_logits ? s->xq : nullptr, s->xqs, s->st));
     if (all_logits) {
-        CK(gemv(s, {JX(m->embed, logits_out, c.vocab_size, s->xq, s->xqs)}, nt));
+        CK(lm_head_gemv(s, JX(m->embed, logits_out, c.vocab_size, s->xq, s->xqs), nt));
     } else if (!skip_logits) {
         CK(gemv(s, {JX(m->embed, s->logits, c.vocab_size, s->xq + (size_t)(nt - 1) * d,
                        s->xqs + (size_t)(nt - 1) * (d / 32))}, 1));
@@ -1208,7 +1242,7 @@ int mtp_ffn_head(DState *s, int nt, float *chain_out, float *out_logits) {
         CK(gemv(s, {J(m->mtp_down, s->ffn_out, d, PS(s->hb, s->hb2, I))}, nt));
     }
     CK(l98k_rmsnorm(mx, d, s->ffn_out, nullptr, m->mtp_norm, d, eps, nt, chain_out, d, s->xq, s->xqs, s->st));
-    CK(gemv(s, {JX(m->embed, out_logits, c.vocab_size, s->xq, s->xqs)}, nt));
+    CK(lm_head_gemv(s, JX(m->embed, out_logits, c.vocab_size, s->xq, s->xqs), nt));
     return 0;
 }
 
@@ -1226,8 +1260,9 @@ int draft_step(DState *s, const int *toks, const int *ctl_pos, int pos_off, int 
     CK(gemv(s, {JX(m->mtp_fc, s->mtp_x, d, s->xq, s->xqs)}, 1));
     CK(attn_block(s, m->mtp, PN(s->mtp_x, d, nullptr, nullptr, m->mtp.in_norm, eps, nullptr, nullptr, 0),
                   s->planes - 1, ctl_pos, pos_off, 1, max_pos, false));
+    s->amax_tok = out_tok;       // argmax in the lm_head's epilogue
+    s->amax_mode = 1;
     CK(mtp_ffn_head(s, 1, s->chain, out_logits));
-    if (out_tok) CK(l98k_argmax(out_logits, c.vocab_size, 1, 1, out_tok, s->st));
     return 0;
 }
 
@@ -1260,8 +1295,9 @@ int dspark_draft(DState *s, const int *toks, int k, float *out_logits, int *out_
         CK(l98k_rmsnorm_ex(s->sub_a, c.attn_q_dim, nullptr, nullptr, L.sn_o, c.attn_q_dim, eps, k, nullptr, 0,
                            s->xq2, s->xqs2, 0, s->st));
     CK(gemv(s, {JX(L.o, s->blk, d, s->xq2, s->xqs2)}, k));
+    s->amax_tok = out_tok;       // argmax in the lm_head's epilogue
+    s->amax_mode = 1;
     CK(mtp_ffn_head(s, k, nullptr, out_logits));
-    if (out_tok) CK(l98k_argmax(out_logits, c.vocab_size, k, 1, out_tok, s->st));
     return 0;
 }
 
@@ -2285,9 +2321,10 @@ namespace {
 int enqueue_verify_accept(DState *d, int k_eff, int max_pos, int brk, bool catchup, hipEvent_t mark = nullptr) {
     const LZModelConfig &c = d->m->c;
     const bool dspark = d->m->n_draft > 1;     // no catch-up, mtp_pos kept (src/generate.c:1117-1133)
+    d->amax_tok = d->ctl->targ;  // the verify rows' argmaxes in the lm_head's epilogue
+    d->amax_mode = 0;
     CK(forward_chunk(d, d->ctl->tok, k_eff + 1, &d->ctl->anchor_pos, 1, max_pos, d->vhidden, true,
                      d->mtp_logits, false));
-    CK(l98k_argmax(d->mtp_logits, c.vocab_size, k_eff + 1, 0, d->ctl->targ, d->st));
     CK(l98k_accept(d->ctl, d->vhidden, c.hidden_size, d->chain, d->depth, (brk ? 1 : 0) | (dspark ? 2 : 0), d->st));
     if (dspark) catchup = false;
     if (mark) CK(hipEventRecord(mark, d->st));

@@ -103,6 +103,17 @@ __device__ __forceinline__ void quant_rows(const float4 (&v)[RW][PJN], int wave,
 // Instance flag: the jobs' weights have grouped scales (more than one per
 // row); instances without it keep one scale per row in a register.
 #define MG (1 << 7)
+// Instance flag: the launch's argmax epilogue (GemvBatch.amax_out).
+#define MA (1 << 8)
+
+// The packed argmax candidate of output value v at index i: the float key
+// above the complemented index, so the larger value wins and, among equal
+// keys, the lower index.  mode 0: sample_argmax's key (src/sampler.c:121);
+// 1: lz_argmax_p1's compare (NaN never wins, -0 ties +0).
+__device__ __forceinline__ unsigned long long amax_cand(float v, int i, int mode) {
+    const uint32_t k = mode == 0 ? d_fkey(v) : (v != v) ? 0u : d_fkey(v == 0.0f ? 0.0f : v);
+    return ((unsigned long long)k << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)i);
+}
 // The activation loads of a prologue go out before the tile's weight loads:
 // the empty asm with a memory clobber keeps every earlier load above it
 // (no pass may sink one into a later conditional use, behind the weights,
@@ -446,7 +457,8 @@ __device__ __forceinline__ void gemv_tile(const int8_t *__restrict__ wt, const f
                                           const float *__restrict__ xqs, const int (&xrow)[M], const int *s_orow,
                                           int nm, bool writer, float *__restrict__ out, size_t out_stride,
                                           int row0, int32_t *__restrict__ acc_out, int acc_rows, char *smem,
-                                          float *s_inv, float *tab, int gs = 0) {
+                                          float *s_inv, float *tab, int gs = 0,
+                                          unsigned long long *s_am = nullptr, int amax_mode = 0) {
     // scales per row (ws holds [rows][nws]): one unless the instance is
     // compiled for grouped scales
     constexpr bool GROUPED = (MODES & MG) != 0;
@@ -475,6 +487,7 @@ __device__ __forceinline__ void gemv_tile(const int8_t *__restrict__ wt, const f
         if (GROUPED && nws > 1) o = tile_epilogue_g(pp, sxs + et * nb, nb, gs >> 5, ws + (size_t)(row0 + er) * nws);
         else o = tile_epilogue(pp, sxs + et * nb, nb, wsv);
         out[(size_t)s_orow[et] * out_stride + row0 + er] = o;
+        if (MODES & MA) atomicMax(&s_am[et], amax_cand(o, row0 + er, amax_mode));
         if (acc_out)
             for (int g = 0; g < nb; g++) acc_out[((size_t)et * acc_rows + row0 + er) * nb + g] = pp[g];
     }

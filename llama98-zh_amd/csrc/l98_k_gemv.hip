@@ -4,6 +4,15 @@
 #include "l98_gemv.h"
 #include <climits>
 
+// The argmax epilogue (instances with MA; one job): each block stores its
+// tile's per-row maxima (exact 64-bit candidates) for l98k_argmax_part.
+template <int M>
+__device__ __forceinline__ void amax_store(const GemvBatch &b, const GemvJob &job, int m,
+                                           const unsigned long long *s_am) {
+    __syncthreads();
+    if ((int)threadIdx.x < m) b.amax_part[(size_t)threadIdx.x * job.tiles + blockIdx.x] = s_am[threadIdx.x];
+}
+
 // One launch over b.n jobs; m <= M live token rows (M a power of two).
 // Block (x, y) is tile x of job y: the job index is the workgroup id, so
 // the job's fields are read with the kernel's first batch of scalar loads
@@ -13,8 +22,10 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv_q8(GemvBatch batch, int m
     extern __shared__ __align__(16) char smem[];
     __shared__ int s_row[M];
     __shared__ float s_inv[M], tab[32];
+    __shared__ unsigned long long s_am[(MODES & MA) ? M : 1];
     const GemvJob job = batch.job[blockIdx.y];
     if ((int)blockIdx.x >= job.tiles) return;
+    if ((MODES & MA) && threadIdx.x < M) s_am[threadIdx.x] = 0;
     const int row0 = blockIdx.x * job.R;
     const int rows_here = imin(job.R, job.rows - row0);
     if (threadIdx.x < M) s_row[threadIdx.x] = threadIdx.x < m ? threadIdx.x : 0;
@@ -24,7 +35,8 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_gemv_q8(GemvBatch batch, int m
     gemv_tile<M, PJ, MODES>(job.w + (size_t)row0 * job.in_dim, job.ws, rows_here, job.R, job.in_dim, job.pro, job.xq,
                             job.xqs, xrow, s_row, m, blockIdx.x == 0 && blockIdx.y == 0, job.out, job.out_stride,
                             row0, job.acc_out, job.rows,
-                            smem, s_inv, tab, job.gs);
+                            smem, s_inv, tab, job.gs, s_am, batch.amax_mode);
+    if (MODES & MA) amax_store<M>(batch, job, m, s_am);
 }
 
 // ---------------------------------------------------------- host glue ---
@@ -36,7 +48,8 @@ extern "C" int l98k_upload_exp_table_gemv(const float *tab) {
 // Instances: token slots M in {1, 2, 4, 8}; prologue sets: pre-quantized
 // (PJ 0), RMSNorm (PJ 1..8), RMSNorm with fold-only jobs (PJ 1..8),
 // SiLU-mul (PJ 1..4), combine + SiLU-mul (PJ 1..4); each with one scale per
-// weight row or with grouped scales (MG).
+// weight row or with grouped scales (MG); pre-quantized with the argmax
+// epilogue (MA).
 #define GEMV_CASE(M_, PJ_, MODES_)                                                                         \
     case (M_) * 100000 + (PJ_) * 1000 + (MODES_):                                                            \
         ALLOW_BIG_LDS((k_gemv_q8<M_, PJ_, MODES_>));                                                      \
@@ -50,7 +63,8 @@ extern "C" int l98k_upload_exp_table_gemv(const float *tab) {
     GEMV_CASE(M_, 8, MODES_NF | G_)                                                                    \
     GEMV_CASE(M_, 1, MODES_S | G_) GEMV_CASE(M_, 2, MODES_S | G_) GEMV_CASE(M_, 4, MODES_S | G_)       \
     GEMV_CASE(M_, 1, MODES_CS | G_) GEMV_CASE(M_, 2, MODES_CS | G_) GEMV_CASE(M_, 4, MODES_CS | G_)
-#define GEMV_CASES_M(M_) GEMV_CASES_MG(M_, 0) GEMV_CASES_MG(M_, MG)
+#define GEMV_CASES_M(M_)                                                                              \
+    GEMV_CASES_MG(M_, 0) GEMV_CASES_MG(M_, MG) GEMV_CASE(M_, 0, MODES_X | MA) GEMV_CASE(M_, 0, MODES_X | MG | MA)
 
 // Checks every job's prologue against the kernel's limits, lays the jobs'
 // tiles out in one grid and launches the instance for the jobs' prologue
@@ -82,6 +96,13 @@ extern "C" int l98k_gemv(GemvBatch *b, int m, hipStream_t st) {
     else if (modes == MB(PRO_COMBINE)) modes = MODES_CS;
     else if (modes == MB(PRO_FOLD)) modes = MODES_NF;
     else if (modes != MODES_N && modes != MODES_NF && modes != MODES_S && modes != MODES_CS) return -1;
+    if (b->amax_part) {
+        // the argmax epilogue: one pre-quantized job, partials for every tile
+        if (b->n != 1 || modes != MODES_X || (b->amax_mode != 0 && b->amax_mode != 1) ||
+            (size_t)tiles * (size_t)m > (size_t)b->amax_cap)
+            return -1;
+        modes |= MA;
+    }
     modes |= grouped;
     switch (M * 100000 + pj * 1000 + modes) {
         GEMV_CASES_M(1)

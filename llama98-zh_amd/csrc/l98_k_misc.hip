@@ -230,6 +230,38 @@ __global__ __launch_bounds__(ARGMAX_THREADS) void k_argmax(const float *__restri
     }
 }
 
+// The argmax of rows whose GEMV stored per-tile candidates (the lm_head's
+// argmax epilogue): row r's candidates part[r * tiles .. + tiles) are the
+// packed (key, complemented index) maxima of each tile, so their maximum is
+// k_argmax's result over the row (x: the rows, for mode 1's NaN-at-0 rule).
+__global__ __launch_bounds__(256) void k_argmax_part(const unsigned long long *__restrict__ part, int tiles,
+                                                     const float *__restrict__ x, int n, int mode,
+                                                     int *__restrict__ out) {
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const unsigned long long *p = part + (size_t)row * tiles;
+    unsigned long long v[8], best = 0;
+    for (int base = 0; base < tiles; base += 8 * 256) {
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = p[imin(base + u * 256 + tid, tiles - 1)];
+#pragma unroll
+        for (int u = 0; u < 8; u++) best = v[u] > best ? v[u] : best;
+    }
+    best = wave_max_u64(best);
+    __shared__ unsigned long long sb[4];
+    if ((tid & 63) == 0) sb[tid >> 6] = best;
+    __syncthreads();
+    if (tid == 0) {
+        unsigned long long b = 0;
+        for (int i = 0; i < 4; i++) b = sb[i] > b ? sb[i] : b;
+        int idx = (int)(0xFFFFFFFFu - (uint32_t)(b & 0xFFFFFFFFu));
+        if (mode == 1) {
+            const float r0 = x[(size_t)row * n];
+            if (r0 != r0) idx = 0;
+        }
+        out[row] = idx;
+    }
+}
+
 // Acceptance of a greedy round (lz_spec_accept, src/generate.c:232-243) and
 // the device-side bookkeeping of lz_spec_round (src/generate.c:802-993):
 // ring rollback, mtp_chain reseed from the accepted row, catch-up count,
@@ -394,6 +426,13 @@ extern "C" int l98k_dspark_pre(const int8_t *emb_q, const float *emb_s, int gs, 
 extern "C" int l98k_argmax(const float *x, int n, int rows, int mode, int *out, hipStream_t st) {
     if (rows < 1 || rows > LZ_ARGMAX_ROWS || n < 1) return -1;
     hipLaunchKernelGGL(k_argmax, dim3(rows), dim3(ARGMAX_THREADS), 0, st, x, n, mode, out);
+    return (int)hipGetLastError();
+}
+
+extern "C" int l98k_argmax_part(const unsigned long long *part, int tiles, const float *x, int n, int rows, int mode,
+                                int *out, hipStream_t st) {
+    if (rows < 1 || rows > LZ_ARGMAX_ROWS || tiles < 1 || n < 1) return -1;
+    hipLaunchKernelGGL(k_argmax_part, dim3(rows), dim3(256), 0, st, part, tiles, x, n, mode, out);
     return (int)hipGetLastError();
 }
 

@@ -68,6 +68,9 @@ int l98k_smp_xprefix(const float *x, int rows, int n, int mode, const float *c, 
 // Fused GEMV of b->n jobs over m <= MAX_CHUNK activation rows; each job's
 // prologue builds its int8 input rows.
 int l98k_gemv(GemvBatch *b, int m, hipStream_t st);
+// Tiles of a GEMV over `rows` rows of in_dim with m token rows (the grid of
+// l98k_gemv; an argmax epilogue needs tiles * m partial entries).
+int l98k_gemv_tiles(int rows, int in_dim, int m);
 // 1 when a GEMV with an RMSNorm prologue over m rows of in_dim fits the kernel.
 int l98k_gemv_norm_fits(int in_dim, int m);
 // Grouped expert GEMV: n_jobs (<= 2) projections over the groups in grp.
@@ -145,6 +148,10 @@ int l98k_subn_quant(const float *x, int rows, int n, int blk, int gw, int8_t *q,
 // Per row argmax of rows x n floats, one block per row (mode 0:
 // sample_argmax's key order, 1: lz_argmax_p1's compare).
 int l98k_argmax(const float *x, int n, int rows, int mode, int *out, hipStream_t st);
+// The same from a GEMV's argmax-epilogue candidates (GemvBatch.amax_part,
+// tiles per row; x: the GEMV's output rows of n, read for mode 1's rule).
+int l98k_argmax_part(const unsigned long long *part, int tiles, const float *x, int n, int rows, int mode, int *out,
+                     hipStream_t st);
 // flags: 1 debug_break_rollback, 2 a DSpark round (no catch-up, mtp_pos kept)
 int l98k_accept(DevCtl *ctl, const float *vhidden, int d, float *chain, int depth, int flags, hipStream_t st);
 int l98k_set_tokens(DevCtl *ctl, int op, RoundRec *hist, int hist_cap, hipStream_t st);
