@@ -139,6 +139,7 @@ HIP_API = [
     ("l98_prefix_query", C.c_int, [_FP, C.c_int, C.c_int, C.c_int, _FP, _IP, _FP]),
     ("l98_moe_route", C.c_int, [_FP, _FP, C.c_int, C.c_int, C.c_int, _IP, _FP]),
     ("l98_argmax_rows", C.c_int, [_FP, C.c_int, C.c_int, C.c_int, _IP]),
+    ("l98_gemv_argmax", C.c_int, [C.c_void_p, _FP, C.c_int, C.c_int, C.c_void_p, _FP, C.c_int, C.c_int, _FP, _IP]),
     ("l98_gemm_q8", C.c_int, [C.c_void_p, _FP, C.c_int, C.c_int, C.c_void_p, _FP, C.c_int, _FP]),
     ("l98_device_name", C.c_char_p, []),
     ("l98_last_loop_seconds", C.c_double, []),

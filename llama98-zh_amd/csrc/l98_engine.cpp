@@ -2901,6 +2901,40 @@ extern "C" int l98_argmax_rows(const float *x, int rows, int n, int mode, int *o
     return dout.put(out, sizeof(int) * rows) ? 0 : 1;
 }
 
+// The lm_head path's argmax: an int8 GEMV (one scale per weight row) over M
+// pre-quantized rows with the argmax epilogue, then l98k_argmax_part;
+// logits [M][N] and the rows' argmaxes (mode 0 or 1) come back.
+extern "C" int l98_gemv_argmax(const int8_t *w, const float *ws, int N, int K, const int8_t *xq, const float *xqs,
+                               int M, int mode, float *logits, int *out) {
+    if (!w || !ws || !xq || !xqs || !logits || !out || N < 1 || K < 32 || (K & 31) || M < 1 || M > MAX_CHUNK ||
+        (mode != 0 && mode != 1))
+        return 1;
+    int cap = 0;
+    for (int m = 1; m <= MAX_CHUNK; m *= 2) {
+        const int need = l98k_gemv_tiles(N, K, m) * m;
+        cap = need > cap ? need : cap;
+    }
+    DevBuf dw, dws, dx, dxs, dl, dp, dout;
+    if (!dw.get(w, (size_t)N * K) || !dws.get(ws, sizeof(float) * N) || !dx.get(xq, (size_t)M * K) ||
+        !dxs.get(xqs, sizeof(float) * (size_t)M * (K / 32)) || !dl.get(nullptr, sizeof(float) * (size_t)M * N) ||
+        !dp.get(nullptr, sizeof(unsigned long long) * (size_t)cap) || !dout.get(nullptr, sizeof(int) * M))
+        return 1;
+    GemvBatch b{};
+    b.n = 1;
+    GemvJob &j = b.job[0];
+    j.w = (const int8_t *)dw.p; j.ws = (const float *)dws.p; j.out = (float *)dl.p;
+    j.xq = (const int8_t *)dx.p; j.xqs = (const float *)dxs.p;
+    j.rows = N; j.in_dim = K; j.out_stride = N; j.gs = 0;
+    j.pro.mode = PRO_XQ;
+    b.amax_mode = mode;
+    b.amax_part = (unsigned long long *)dp.p;
+    b.amax_cap = cap;
+    if (l98k_gemv(&b, M, nullptr) ||
+        l98k_argmax_part(b.amax_part, j.tiles, j.out, N, M, mode, (int *)dout.p, nullptr))
+        return 1;
+    return dl.put(logits, sizeof(float) * (size_t)M * N) && dout.put(out, sizeof(int) * M) ? 0 : 1;
+}
+
 extern "C" int l98_prefix_query(const float *x, int rows, int n, int mode, const float *c, int *out, float *outv) {
     if (!x || !out || !outv || rows < 1 || n < 1 || mode < 0 || mode > 2 || (mode && !c)) return 1;
     float *dx = nullptr, *dc = nullptr, *dv = nullptr;

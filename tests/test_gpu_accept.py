@@ -47,6 +47,45 @@ def test_device_argmax_matches_oracle(pkg, n):
             assert out[r] == want, (mode, r, out[r], want)
 
 
+@pytest.mark.parametrize("M", [1, 4, 8])
+def test_gemv_argmax_epilogue_matches_oracle(pkg, M):
+    # The rounds' argmax: per-tile candidates from the lm_head GEMV's
+    # epilogue, reduced by l98k_argmax_part.  Row scales plant the special
+    # values in whole logit columns: NaN at index 0 and elsewhere, +inf ties,
+    # a band of zeros (0 scale, and -0 scale), and a maximum in the last row.
+    lib = pkg.hip_lib()
+    L = OL.lib()
+    N, K = 65536 + 40, 1024
+    rng = np.random.default_rng(M)
+    w = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    xq = rng.integers(-127, 128, (M, K), dtype=np.int8)
+    xqs = (rng.random((M, K // 32)) * 0.01 + 1e-4).astype(np.float32)
+    ws = (rng.random(N) * 0.01).astype(np.float32)
+    ws[0] = np.nan
+    ws[777] = np.nan
+    ws[100:140] = 0.0
+    ws[140:160] = -0.0
+    ws[3000] = ws[5000] = np.inf
+    ws[N - 1] = 1e30
+    for mode in (0, 1):
+        for plant in (True, False):
+            s = ws.copy()
+            if not plant:                                # finite rows only: ties by value
+                s[[0, 777, 3000, 5000, N - 1]] = 0.0
+            logits = np.zeros((M, N), np.float32)
+            out = np.zeros(M, np.int32)
+            assert lib.l98_gemv_argmax(w.ctypes.data, fp(s), N, K, xq.ctypes.data, fp(xqs), M, mode,
+                                       fp(logits), ip(out)) == 0
+            for r in range(M):
+                row = np.ascontiguousarray(logits[r])
+                if mode == 0:
+                    want = L.o_argmax(fp(row), N)
+                else:
+                    p = C.c_float()
+                    want = L.o_argmax_p1(fp(row), N, C.byref(p))
+                assert out[r] == want, (mode, plant, r, out[r], want)
+
+
 def test_library_spec_accept_exhaustive(pkg):
     """lz_spec_accept of the library (src/generate.c:232-243) against the
     oracle's and the definition, over every draft/target pair on 3 symbols
