@@ -168,13 +168,14 @@ def cpu_baseline(model_dir, vocab, k, n_prompt):
                 "prefill_s": round(float(d["prefill_us"][0]) * 1e-6, 2),
                 "verify_ms": round(float(d["verify_us_median"][0]) * 1e-3, 3), "tier": d["kernel"][0]}
     ship, ora = summary(res["ship"]), summary(res["oracle"])
+    ora["tokens"] = [int(t) for t in res["oracle"]["tokens"]]
     return {"value": ship["tok_s"], "unit": "tok/s", "cores": 1, "kind": "reference",
             "sample": f"reference shipping build (lz_spec_round, tier {ship['tier']}, gcc -O2 AVX2) on 1 core of "
                       f"{os.cpu_count()} ({cpu}): {n_prompt}-token prompt prefilled ({ship['prefill_s']} s), then "
                       f"{ship['tokens']} tokens in {ship['rounds']} rounds at k={k} on the same model; its verify "
                       f"forward of M={k + 1} rows alone: {ship['verify_ms']} ms",
             "round_ms": ship["round_ms"], "verify_ms": ship["verify_ms"], "prefill_s": ship["prefill_s"],
-            "oracle_mode": ora}
+            "oracle_mode": ora, "ship_tokens": [int(t) for t in res["ship"]["tokens"]]}
 
 
 def bench_server(args, pkg):
@@ -389,7 +390,15 @@ def main():
         t_ms = eng.time_kernel(1, ks + 1, 10)
         vb = round_bytes(cfg, ks, ctx_now, int(experts.mean()))[1]
         sweep.append({"k": ks, "M": ks + 1, "ms": round(t_ms, 4), "GB/s": round(vb / (t_ms * 1e-3) / 1e9, 1)})
+    # the launch floor: per launch of 64 dependent launches in one graph
+    floor = {"graph_empty_1block_us": round(eng.time_kernel(7, M, 20) * 1e3, 3),
+             "graph_empty_256blocks_us": round(eng.time_kernel(8, M, 20) * 1e3, 3),
+             "graph_handoff_256blocks_us": round(eng.time_kernel(9, M, 20) * 1e3, 3),
+             "stream_empty_256blocks_us": round(eng.time_kernel(10, M, 20) * 1e3, 3),
+             "note": "chains of 64 dependent launches; handoff: every block reads the M x hidden floats the "
+                     "previous launch wrote"}
     cpu = None if args.no_cpu else cpu_baseline(mdir, cfg.vocab_size, k, len(prompt))
+    parity = bench_parity(eng, prompt, k, cpu)
     out = {
         "metric": "accepted tok/s @bs1 k=3; verify-step HBM GB/s as % of MI355X peak",
         "value": round(value, 3),
@@ -433,10 +442,36 @@ def main():
                   "roofline_tok_s": round(roof_toks, 1),
                   "frac_of_roofline": round(value / roof_toks, 4),
                   "mean_distinct_experts": round(float(experts.mean()), 2)},
+        "launch_floor": floor,
         "cpu_baseline": cpu,
+        "parity": parity,
     }
     print(json.dumps(out))
     eng.close()
+
+
+def bench_parity(eng, prompt, k, cpu):
+    """The benched workload's own output against the reference: a fresh
+    session on the same prompt, greedy rounds at the same k on the device
+    (the timed path), and its first tokens compared with the tokens the
+    reference engine's float-oracle build emitted in the CPU baseline's run
+    (same model, prompt and k).  None when the CPU leg did not run."""
+    import numpy as np
+    if not cpu or "tokens" not in cpu.get("oracle_mode", {}):
+        return None
+    want = [int(t) for t in cpu["oracle_mode"]["tokens"]]
+    first = eng.session_start(prompt)
+    toks = [int(first)]
+    while len(toks) < len(want):
+        t, _, _ = eng.greedy_rounds(k, 1)
+        toks.extend(int(x) for x in t)
+    got = toks[:len(want)]
+    bad = [i for i in range(len(want)) if got[i] != want[i]]
+    return {"reference": "oracle/_ref/l98ref_oracle (the reference engine built from its sources, float-oracle "
+                         "mode), same model, prompt and k",
+            "tokens_compared": len(want), "identical": not bad, "first_divergence": bad[0] if bad else None,
+            "gpu_tokens": got, "reference_tokens": want,
+            "shipping_build_tokens": [int(t) for t in cpu.get("ship_tokens", [])]}
 
 
 if __name__ == "__main__":

@@ -63,6 +63,8 @@ typedef struct {
     int use_subn, hadamard_o, hadamard_down;   /* SubLN (src/model.h: use_subn, hadamard_o/_down) */
     int mtp_n_draft, mtp_markov_rank;          /* DSpark (src/model.h:359-375): > 1 draft slots; a
                                                   model.bin carries no Markov rank (0) */
+    int kda_has_gate_lower_bound;              /* src/model.h:264-265: the KDA gate is */
+    float kda_gate_lower_bound;                /* lb * sigmoid(exp(A_log) * pre) when set */
 } LZModelConfig;
 
 /* Caller-allocated, as in the reference: LZModel m; lz_open(&m, dir, ...). */
@@ -288,7 +290,13 @@ int l98_greedy_rounds_batch(const LZModel *m, LZRunState **states, int n_seq, in
  * int8 bytes (calibration for byte counters); 3: the lm_head GEMV after a
  * cache-evicting 512 MiB copy each time (only the GEMV timed); 4, 5, 6: the
  * RMSNorm-prologue GEMV of every KDA layer's, attention layer's and layer's
- * MoE input projections in order, back to back (mean per launch).
+ * MoE input projections in order, back to back (mean per launch); 7-10:
+ * the launch floor, per launch of a chain of 64 dependent launches: 7 an
+ * empty kernel of 1 block, 8 of 256 blocks, 9 a kernel of 256 blocks each
+ * reading the mrows x hidden floats the previous launch wrote (7-9 captured
+ * as one HIP graph and replayed), 10 mode 8 launched without a graph, 11
+ * mode 9 plus a last-block reduction per 8 blocks (device-scope release,
+ * counter, acquire, the group's partials read back), as a graph.
  * Returns 0 (1 on a bad argument or a device error). */
 int l98_time_kernel(const LZModel *m, LZRunState *s, int which, int mrows, int iters, float *avg_ms);
 /* For each of `rows` rows of n (<= 2048) non-negative floats (host

@@ -37,7 +37,8 @@ class LZModelConfig(C.Structure):
         "moe_intermediate_size", "moe_shared_width", "mtp_intermediate_size", "mtp_n_layers")] + [
         ("rms_norm_eps", C.c_float), ("rope_theta", C.c_float), ("layer_types", C.c_int * 128),
         ("use_subn", C.c_int), ("hadamard_o", C.c_int), ("hadamard_down", C.c_int),
-        ("mtp_n_draft", C.c_int), ("mtp_markov_rank", C.c_int)]
+        ("mtp_n_draft", C.c_int), ("mtp_markov_rank", C.c_int),
+        ("kda_has_gate_lower_bound", C.c_int), ("kda_gate_lower_bound", C.c_float)]
 
 
 class LZModel(C.Structure):
@@ -69,7 +70,8 @@ class L98SynthConfig(C.Structure):
         "vocab", "hidden", "n_layers", "seq_len", "attn_period", "n_heads", "n_kv_heads", "head_dim",
         "kda_heads", "kd", "vd", "conv_kernel", "gate_rank", "n_experts", "topk", "latent",
         "moe_inter", "shared_w", "mtp_inter")] + [
-        ("w_std", C.c_float), ("router_std", C.c_float), ("bias_std", C.c_float), ("resid_std", C.c_float),
+        ("w_std", C.c_float), ("router_std", C.c_float), ("bias_std", C.c_float), ("gate_lb", C.c_float),
+        ("resid_std", C.c_float),
         ("mtp_echo", C.c_int), ("use_subn", C.c_int), ("hadamard_o", C.c_int), ("hadamard_down", C.c_int),
         ("bin_version", C.c_int), ("gs", C.c_int), ("scale_layout", C.c_int), ("bf16_small", C.c_int),
         ("mtp_n_draft", C.c_int)]

@@ -146,6 +146,8 @@ typedef struct {
     float *xqs;
     int nv, key, value, rank, depth, advance, nt;
     float scale, eps;
+    float gate_lb;                      // gate lower bound (has_lb): g = lb * sigmoid(exp(A_log) * pre)
+    int has_lb;                         // 0: g = -exp(A_log) * softplus(pre)
     int fb_gs;                          // f_b scale group (0: the row)
     int hist_rows;                      // conv history from the rows before row 0, not the ring (split prefill)
     float *rec;                         // split prefill: token records [n][nv][5*kd + 4]

@@ -380,7 +380,7 @@ int parse_model(Bin &b, LZModelConfig &c, HostTensor &embed, HostTensor &fnorm,
     c.rotary_dim = b.i32();
     for (int i = 0; i < 128; i++) c.layer_types[i] = b.i32();
     c.kda_gate_rank = b.i32();
-    int has_lb = b.i32(); (void)b.f32();
+    c.kda_has_gate_lower_bound = b.i32() != 0; c.kda_gate_lower_bound = b.f32();
     c.num_experts = b.i32(); c.num_experts_per_token = b.i32(); int n_shared = b.i32();
     c.moe_intermediate_size = b.i32(); c.moe_latent_dim = b.i32();
     int first_dense = b.i32(), renorm = b.i32(), sig = b.i32(), lat_norm = b.i32();
@@ -461,7 +461,7 @@ int parse_model(Bin &b, LZModelConfig &c, HostTensor &embed, HostTensor &fnorm,
     // full attention, sigmoid latent MoE with a shared expert, one MTP layer;
     // SubLN (use_subn) on that MoE variant, whose scales are per 32 elements
     // (the default subn scale on a model with experts).
-    if (has_lb || n_shared != 1 || first_dense != 0 || !renorm || !sig || lat_norm ||
+    if (n_shared != 1 || first_dense != 0 || !renorm || !sig || lat_norm ||
         (c.use_subn != 0 && c.use_subn != 1) ||
         (c.use_subn && (c.num_experts < 1 || c.hidden_size > 2048 || c.lin_value_dim > 2048 ||
                         c.attn_q_dim > 2048 || c.mtp_intermediate_size > 2048 || c.moe_shared_width > 2048 ||
@@ -1104,6 +1104,7 @@ int kda_block(DState *s, const DLayer &L, const Prologue &in, int li, int nt, in
     a.xq = s->xq2; a.xqs = s->xqs2;
     a.normed_out = sub ? s->sub_a : nullptr;
     a.nv = nv; a.key = key; a.value = value; a.rank = c.kda_gate_rank;
+    a.has_lb = c.kda_has_gate_lower_bound; a.gate_lb = c.kda_gate_lower_bound;
     a.depth = s->depth; a.advance = advance; a.nt = nt;
     a.scale = ssm_scale(kd); a.eps = c.rms_norm_eps;
     CK(l98k_kda_step(&a, kd, c.conv_kernel, s->st));
@@ -1670,6 +1671,7 @@ int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, 
             a.a_log = L.a_log; a.dt_bias = L.dt_bias; a.o_norm = L.o_norm;
             a.xq = w->xq2; a.xqs = w->xqs2;
             a.nv = nv; a.key = key; a.value = value; a.rank = rank;
+            a.has_lb = c.kda_has_gate_lower_bound; a.gate_lb = c.kda_gate_lower_bound;
             a.advance = advance ? 1 : 0;
             a.scale = ssm_scale(kd); a.eps = eps;
             if (n_items == 1 && items[0].n > MAX_CHUNK && !advance) {
@@ -3347,6 +3349,51 @@ extern "C" int l98_time_kernel(const LZModel *mm, LZRunState *s, int which, int 
     DState *d = S(s);
     const DModel *m = d->m;
     const LZModelConfig &c = m->c;
+    if (which >= 7 && which <= 11) {
+        // launch floor: a chain of CHAIN dependent launches (7: empty
+        // kernel, 1 block; 8: empty, 256 blocks; 9: 256 blocks each reading
+        // the mrows x hidden floats the previous launch wrote; 11: mode 9
+        // plus a last-block reduction per 8 blocks (release, counter,
+        // acquire, the group's partials read back); all captured once as a
+        // HIP graph and replayed; 10: mode 8 launched on the stream without
+        // a graph); avg_ms is per launch
+        const int CHAIN = 64, n = mrows * c.hidden_size;
+        const int grid = which == 7 ? 1 : 256, kind = which == 9 ? 1 : which == 11 ? 2 : 0;
+        if (n < 256 || n > 8192) return 1;
+        float *buf = nullptr;
+        // two n-float buffers, then (mode 11) grid x 256 partials and the counters
+        const size_t nbuf = 2 * (size_t)n + (size_t)grid * 256 + grid;
+        if (hipMalloc(&buf, nbuf * sizeof(float)) != hipSuccess) return 1;
+        int rc = hipMemsetAsync(buf, 0, nbuf * sizeof(float), d->st) != hipSuccess;
+        hipGraph_t g = nullptr;
+        hipGraphExec_t ge = nullptr;
+        auto chain = [&]() { return l98k_launch_chain(kind, CHAIN, grid, buf, buf + n, n, d->st); };
+        if (!rc && which != 10) {
+            if (hipStreamBeginCapture(d->st, hipStreamCaptureModeThreadLocal) != hipSuccess) rc = 1;
+            else {
+                const int crc = chain();
+                if (hipStreamEndCapture(d->st, &g) != hipSuccess || crc) rc = 1;
+                else if (hipGraphInstantiate(&ge, g, nullptr, nullptr, 0) != hipSuccess) rc = 1;
+            }
+        }
+        auto once = [&]() { return which == 10 ? chain() : (int)(hipGraphLaunch(ge, d->st) != hipSuccess); };
+        float ms = 0.0f;
+        if (!rc) rc = once();
+        if (!rc) {
+            (void)hipEventRecord(d->ev0, d->st);
+            for (int i = 0; i < iters && !rc; i++) rc = once();
+            (void)hipEventRecord(d->ev1, d->st);
+            if (!rc && hipEventSynchronize(d->ev1) != hipSuccess) rc = 1;
+            if (!rc) (void)hipEventElapsedTime(&ms, d->ev0, d->ev1);
+        }
+        (void)hipStreamSynchronize(d->st);
+        if (ge) (void)hipGraphExecDestroy(ge);
+        if (g) (void)hipGraphDestroy(g);
+        (void)hipFree(buf);
+        if (rc) return 1;
+        *avg_ms = ms / (float)iters / (float)CHAIN;
+        return 0;
+    }
     if (which < 0 || which > 6) return 1;
     std::vector<int> layers;                    // the layers modes 4-6 run, in order
     for (int l = 0; l < c.n_layers; l++)

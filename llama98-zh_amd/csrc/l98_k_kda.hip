@@ -343,8 +343,9 @@ __device__ __forceinline__ void kda_step_body(const KdaStepArgs &a, int h) {
             } else {
                 pre += dot * fbs;
             }
+            // kda_gate_build_float, src/forward_kda.c:285-293
             const float p = pre + dtb;
-            const float gg = -decay * d_softplus(p, tab);
+            const float gg = a.has_lb ? a.gate_lb * d_sigmoid(decay * p, tab) : -decay * d_softplus(p, tab);
             s_g[t][j] = d_exp(gg, tab);
         }
     }

@@ -447,3 +447,71 @@ extern "C" int l98k_set_tokens(DevCtl *ctl, int op, RoundRec *hist, int hist_cap
     return (int)hipGetLastError();
 }
 
+
+// Launch-floor probes (l98_time_kernel modes 7-10): an empty kernel, and a
+// handoff kernel whose every block reads the n floats the previous launch
+// wrote (as a GEMV's blocks read the activation rows their producer wrote
+// on other XCDs) while block 0 writes the next buffer.
+__global__ void k_nop() {}
+
+// n <= 8192: every load of a thread is issued before the first use.
+__global__ __launch_bounds__(256) void k_handoff(const float *__restrict__ in, float *__restrict__ out, int n) {
+    float4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+        const int i = (u * 256 + (int)threadIdx.x) * 4;
+        v[u] = i < n ? *reinterpret_cast<const float4 *>(in + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 8; u++) acc += v[u].x + v[u].y + v[u].z + v[u].w;
+    if (blockIdx.x == 0)
+        for (int i = (int)threadIdx.x; i < n; i += 256) out[i] = in[i] + (acc == 12345.0f ? 1.0f : 0.0f);
+}
+
+// The handoff kernel plus a last-block reduction: blocks come in groups of
+// 8; each writes 256 floats of partials, then a device-scope release and a
+// counter increment; the group's last block (acquire) reads its group's
+// 2048 partials and writes one value per thread.
+__global__ __launch_bounds__(256) void k_lastblock(const float *__restrict__ in, float *__restrict__ out, int n,
+                                                   float *__restrict__ part, unsigned int *__restrict__ cnt) {
+    float4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+        const int i = (u * 256 + (int)threadIdx.x) * 4;
+        v[u] = i < n ? *reinterpret_cast<const float4 *>(in + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 8; u++) acc += v[u].x + v[u].y + v[u].z + v[u].w;
+    part[blockIdx.x * 256 + threadIdx.x] = acc;
+    __shared__ unsigned int s_old;
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) s_old = atomicAdd(&cnt[blockIdx.x >> 3], 1u);
+    __syncthreads();
+    if ((s_old & 7u) != 7u) return;
+    __threadfence();
+    const int g0 = (int)(blockIdx.x & ~7u) * 256;
+    float r = 0.0f;
+#pragma unroll
+    for (int b = 0; b < 8; b++) r += part[g0 + b * 256 + threadIdx.x];
+    if ((int)threadIdx.x < n) out[(blockIdx.x >> 3) * 256 + threadIdx.x] = in[threadIdx.x] + (r == 12345.0f ? 1.0f : 0.0f);
+}
+
+extern "C" int l98k_launch_chain(int kind, int launches, int grid, float *a, float *b, int n, hipStream_t st) {
+    if (launches < 1 || grid < 1 || grid > 65536 || (kind >= 1 && (!a || !b || n < 256 || n > 8192 || (n & 3))) ||
+        (kind == 2 && (grid & 7)))
+        return -1;
+    for (int i = 0; i < launches; i++) {
+        float *src = (i & 1) ? b : a, *dst = (i & 1) ? a : b;
+        if (kind == 0) hipLaunchKernelGGL(k_nop, dim3(grid), dim3(256), 0, st);
+        else if (kind == 1) hipLaunchKernelGGL(k_handoff, dim3(grid), dim3(256), 0, st, src, dst, n);
+        else
+            // partials and counters past the two n-float buffers (the caller
+            // sizes the buffer for them)
+            hipLaunchKernelGGL(k_lastblock, dim3(grid), dim3(256), 0, st, src, dst, n, b + n,
+                               reinterpret_cast<unsigned int *>(b + n + (size_t)grid * 256));
+    }
+    return (int)hipGetLastError();
+}

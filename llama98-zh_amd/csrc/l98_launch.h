@@ -155,6 +155,12 @@ int l98k_argmax_part(const unsigned long long *part, int tiles, const float *x, 
 // flags: 1 debug_break_rollback, 2 a DSpark round (no catch-up, mtp_pos kept)
 int l98k_accept(DevCtl *ctl, const float *vhidden, int d, float *chain, int depth, int flags, hipStream_t st);
 int l98k_set_tokens(DevCtl *ctl, int op, RoundRec *hist, int hist_cap, hipStream_t st);
+// Launch-floor probes: `launches` dependent launches of an empty kernel
+// (kind 0) or of a kernel whose `grid` blocks each read the n floats the
+// previous launch wrote (kind 1, buffers a and b alternating; 256 <= n <=
+// 8192), or kind 1 plus a last-block reduction per 8 blocks (kind 2: b is
+// followed by grid x 256 floats of partials and grid counters).
+int l98k_launch_chain(int kind, int launches, int grid, float *a, float *b, int n, hipStream_t st);
 }
 
 #endif

@@ -148,6 +148,16 @@ int l98_synth_config(int id, L98SynthConfig *c) {
         c->scale_layout = id == 14 ? 2 : 0;
         c->bf16_small = id == 14 ? 1 : 0;
         return 0;
+    case 23:                          /* configs[4]: configs[3]'s model, skewed router */
+        if (l98_synth_config(3, c)) return 1;
+        c->seq_len = 2304;
+        c->router_std = 0.022097087f;     /* 1/sqrt(2048): unit-variance logits */
+        c->bias_std = 0.5f;
+        return 0;
+    case 24: case 25:                 /* the KDA gate's lower-bound arm (K3's -5) */
+        if (l98_synth_config(id == 24 ? 0 : 10, c)) return 1;
+        c->gate_lb = -5.0f;
+        return 0;
     case 22:
         if (l98_synth_config(1, c)) return 1;
         c->bin_version = 6;
@@ -508,7 +518,7 @@ int l98_synth_write(const char *dir, const L98SynthConfig *c, uint64_t seed,
     put_i32(&w, key); put_i32(&w, value); put_i32(&w, 2 * key + value);
     put_i32(&w, hd);                                   /* rotary_dim */
     for (int i = 0; i < MAX_LAYERS; i++) put_i32(&w, types[i]);
-    put_i32(&w, c->gate_rank); put_i32(&w, 0); put_f32(&w, 0.0f);
+    put_i32(&w, c->gate_rank); put_i32(&w, c->gate_lb != 0.0f); put_f32(&w, c->gate_lb);
     put_i32(&w, c->n_experts); put_i32(&w, c->topk); put_i32(&w, 1);
     put_i32(&w, c->moe_inter); put_i32(&w, c->latent);
     put_i32(&w, 0);                                    /* first_k_dense_replace */

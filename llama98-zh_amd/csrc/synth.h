@@ -30,6 +30,8 @@ typedef struct {
     float w_std;                /* N(0, w_std) for every matrix except the router */
     float router_std;           /* router weight std (0: use w_std) */
     float bias_std;             /* router selection bias std */
+    float gate_lb;              /* KDA gate lower bound (kda_gate_lower_bound; 0:
+                                   none, the softplus gate) */
     float resid_std;            /* std of the matrices that write the residual stream
                                    (attention / KDA o_proj, routed up_proj, shared
                                    down_proj); 0: use w_std */

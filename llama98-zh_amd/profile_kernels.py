@@ -18,6 +18,14 @@ Meant to run under
 
 and summarized by llama98-zh_amd/pmcsum.py.
 
+With --launch-floor it times the launch floor instead (l98_time_kernel
+modes 7-10: chains of 64 dependent launches of an empty kernel of 1 and 256
+blocks and of a 256-block kernel whose blocks read the M x hidden floats the
+previous launch wrote, as a HIP graph and, for the empty 256-block kernel,
+launched on the stream without a graph), printing microseconds per launch;
+under `rocprofv3 --kernel-trace --stats` the probes' dispatches show as
+k_nop and k_handoff.
+
 With --prefill it runs two 512-token session starts instead (the prefill's
 matrix-core GEMMs, k_mfma_q8, for the MFMA counters:
     rocprofv3 --pmc SQ_INSTS_VALU_MFMA_MOPS_I8 SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE \
@@ -38,6 +46,7 @@ def main():
     ap.add_argument("--iters", type=int, default=20)
     ap.add_argument("--model-dir", default=os.path.join(tempfile.gettempdir(), "l98_models"))
     ap.add_argument("--prefill", action="store_true", help="two 512-token session starts")
+    ap.add_argument("--launch-floor", action="store_true", help="dependent-launch chains (modes 7-10)")
     args = ap.parse_args()
     import __graft_entry__
     pkg = __graft_entry__.load_package()
@@ -52,6 +61,15 @@ def main():
         eng.close()
         return
     eng.session_start(pkg.prompt_tokens(0, 32, eng.V))
+    if args.launch_floor:
+        for which, name in ((7, "graph, empty kernel, 1 block"), (8, "graph, empty kernel, 256 blocks"),
+                            (9, "graph, 256 blocks reading the previous launch's 4 x hidden floats"),
+                            (10, "stream, empty kernel, 256 blocks"),
+                            (11, "graph, mode 9 plus a last-block reduction per 8 blocks")):
+            us = eng.time_kernel(which, 4, args.iters) * 1e3
+            print(f"mode {which} ({name}): {us:.3f} us/launch", flush=True)
+        eng.close()
+        return
     for which, name in ((0, "lm_head"), (4, "kda input"), (5, "attention input"), (6, "moe input"), (2, "copy")):
         ms = eng.time_kernel(which, 4, args.iters)
         print(f"mode {which} ({name}, M=4): {ms * 1e3:.2f} us/launch", flush=True)

@@ -491,6 +491,8 @@ typedef struct {
     int q_dim, qg_dim, kv_dim, key, value, conv_dim, rot;
     int types[128];
     int gate_rank, n_experts, topk, moe_inter, latent, shared_w;
+    int has_lb;                                  /* kda_has_gate_lower_bound */
+    float gate_lb;                               /* kda_gate_lower_bound */
     int mtp_inter;
     int use_subn, hadamard_o, hadamard_down;
     int version, scale_layout, has_mtp;
@@ -714,7 +716,7 @@ ORA_API void *ora_open(const char *dir, char *err, int errlen) {
     m->key = rd_i32(&r); m->value = rd_i32(&r); m->conv_dim = rd_i32(&r);
     m->rot = rd_i32(&r);
     for (int i = 0; i < 128; i++) m->types[i] = rd_i32(&r);
-    m->gate_rank = rd_i32(&r); (void)rd_i32(&r); (void)rd_f32(&r);
+    m->gate_rank = rd_i32(&r); m->has_lb = rd_i32(&r); m->gate_lb = rd_f32(&r);
     m->n_experts = rd_i32(&r); m->topk = rd_i32(&r); (void)rd_i32(&r);
     m->moe_inter = rd_i32(&r); m->latent = rd_i32(&r);
     (void)rd_i32(&r); (void)rd_i32(&r); (void)rd_i32(&r); (void)rd_i32(&r);
@@ -1181,14 +1183,16 @@ static void forward_kda(OState *s, const OLayer *L, int li, int nt, int advance,
         o_matmul_q8g(gate + (size_t)t * nvk, s->xq, s->xqs, L->fb.q, L->fb.s,
                      m->gate_rank, nvk, 1, L->fb.gs, NULL);
     }
-    /* decay gate (:277-300, :840-850) */
+    /* decay gate (kda_gate_build_float, src/forward_kda.c:277-300, :840-850):
+     * with a lower bound lb the gate is lb * sigmoid(exp(A_log) * pre),
+     * without one -exp(A_log) * softplus(pre) */
     for (int h = 0; h < nv; h++) decay[h] = o_exp(L->a_log[h]);
     for (int t = 0; t < nt; t++)
         for (int h = 0; h < nv; h++)
             for (int i = 0; i < kd; i++) {
                 int idx = h * kd + i;
                 float pre = gate[(size_t)t * nvk + idx] + L->dt_bias[idx];
-                float gg = -decay[h] * o_softplus(pre);
+                float gg = m->has_lb ? m->gate_lb * o_sigmoid(decay[h] * pre) : -decay[h] * o_softplus(pre);
                 gate[(size_t)t * nvk + idx] = o_exp(gg);
             }
     tap("kgate", layer, gate, nvk);

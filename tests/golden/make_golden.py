@@ -84,6 +84,21 @@ CASES = [
     ("gen_ds_subln_k3_greedy", "ds_subln", 21, 512, 24, 3, 40, 0.0, 1.0, 1, {"dump": 4}),
     ("gen_ds_subln_k2_temp", "ds_subln", 21, 512, 24, 2, 40, 0.8, 0.95, 7),
     ("gen_ds_base_k3_greedy", "base_dspark", 22, 65536, 64, 3, 32, 0.0, 1.0, 1, {"dump": 3}),
+    # The KDA gate's lower-bound arm (kda_has_gate_lower_bound, lb = -5).
+    ("gen_lb_k3_greedy", "lb", 24, 8192, 64, 3, 96, 0.0, 1.0, 1, {"dump": 4}),
+    ("gen_lb_k2_temp", "lb", 24, 8192, 64, 2, 48, 0.8, 0.95, 7),
+    ("gen_lb_micro_k3_greedy", "lb_micro", 25, 512, 24, 3, 48, 0.0, 1.0, 1, {"dump": 6}),
+    # BASELINE.json's configs as stated (numbered from 0): configs[1] with its
+    # 512-token prompt and 512 new tokens (the benchmarked workload);
+    # configs[2] at temperature on configs[1]'s model and prompt, k = 1 and 4;
+    # configs[3] with its 4096-token prompt and 512 new tokens; configs[4]'s
+    # model (configs[3]'s shapes, unit-variance router logits, per-expert
+    # bias N(0, 0.5)) at a short context.
+    ("gen_base_p512_k3_greedy", "base", 1, 65536, 512, 3, 512, 0.0, 1.0, 1, {"dump": 4}),
+    ("gen_base_p512_k1_temp", "base", 1, 65536, 512, 1, 128, 0.8, 0.95, 7),
+    ("gen_base_p512_k4_temp", "base", 1, 65536, 512, 4, 128, 0.8, 0.95, 7),
+    ("gen_large_p4096_k3_greedy", "large", 3, 131072, 4096, 3, 512, 0.0, 1.0, 1, {"dump": 2}),
+    ("gen_xlserver_k3_greedy", "xlserver", 23, 131072, 48, 3, 32, 0.0, 1.0, 1, {"dump": 2}),
 ]
 # Prefill + one capture (the harness's capture command; needs no MTP head):
 # (fixture, model dir name, generator config id, vocab, n_prompt)
@@ -91,6 +106,13 @@ CAPTURES = [
     ("cap_fmt15_v4", "fmt15", 15, 8192, 40),       # version 4: no MTP head, groups of 64
     ("cap_fmt14_v6", "fmt14", 14, 8192, 40),
     ("cap_fmt13_v9", "fmt13", 13, 512, 40),
+]
+# Draft widths past the reference's cap (LZ_SPEC_K_MAX = 6): written by the
+# CPU restatement (oracle/l98_oracle.c, pinned against the reference on every
+# fixture above) extended to an 8-slot ring, as ora_*.json.
+# (fixture, model dir name, generator config id, vocab, n_prompt, k, n_new, temp, topp, sampler seed)
+ORACLE_CASES = [
+    ("ora_base_p512_k7_temp", "base", 1, 65536, 512, 7, 128, 0.8, 0.95, 7),    # configs[2] at k = 7
 ]
 MODEL_SEED = 1234
 PROMPT_SEED = 0
@@ -182,6 +204,37 @@ def main_captures():
         print(name, flush=True)
 
 
+def main_oracle():
+    import __graft_entry__
+    from oracle_lib import Oracle
+    pkg = __graft_entry__.load_package()
+    root = os.environ.get("L98_MODEL_DIR") or os.path.join(tempfile.gettempdir(), "l98_models")
+    only = set(sys.argv[1:])
+    for name, mdir, cid, V, n_prompt, k, n_new, temp, topp, seed in ORACLE_CASES:
+        if only and name not in only:
+            continue
+        model = pkg.ensure_model(os.path.join(root, mdir), cid, seed=MODEL_SEED)
+        h = hashlib.sha256()
+        with open(os.path.join(model, "model.bin"), "rb") as f:
+            for blk in iter(lambda: f.read(1 << 24), b""):
+                h.update(blk)
+        prompt = pkg.prompt_tokens(PROMPT_SEED, n_prompt, V)
+        o = Oracle(model, spec_k_max=k)
+        try:
+            toks, ke, na, rng = o.generate(prompt, k, n_new, temp, topp, seed)
+        finally:
+            o.close()
+        out = {"model": mdir, "config_id": cid, "model_seed": MODEL_SEED, "model_sha256": h.hexdigest(),
+               "vocab": V, "prompt_seed": PROMPT_SEED, "n_prompt": n_prompt, "k": k, "n_new": n_new, "temp": temp,
+               "topp": topp, "sampler_seed": seed, "tokens": [int(t) for t in toks],
+               "k_eff": [int(t) for t in ke], "n_accept": [int(t) for t in na], "rng": int(rng),
+               "source": "oracle/l98_oracle.c ora_generate_ex (the CPU restatement; k past the reference's cap)"}
+        with open(os.path.join(HERE, name + ".json"), "w") as f:
+            json.dump(out, f, indent=1)
+        print(name, len(out["tokens"]), "tokens", flush=True)
+
+
 if __name__ == "__main__":
     main()
     main_captures()
+    main_oracle()

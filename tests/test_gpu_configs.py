@@ -1,0 +1,130 @@
+"""BASELINE.json's configs as stated (numbered from 0), on the GPU, beyond
+the reference fixtures that test_gpu_golden.py replays:
+
+  * 32 sessions of configs[3]'s model with the skewed router
+    (unit-variance logits, per-expert bias N(0, 0.5); synthetic config 23),
+    contexts uniform in [256, 2048], k = 3: the batched verify of 128 rows
+    (grouped MFMA expert GEMMs over top-8 routing on 128 experts) equals the
+    same sessions verified one by one, bit for bit;
+  * configs[2] at k = 7 on configs[1]'s model (the reference caps k at 6, so
+    the expected tokens come from the CPU restatement extended to an 8-slot
+    ring: tests/golden/ora_base_p512_k7_temp.json), plus the width
+    invariants: greedy decoding at k = 7 emits the reference's k = 3
+    tokens, and an M = 8 verify equals eight single steps."""
+import ctypes as C
+import json
+import os
+
+import numpy as np
+import pytest
+
+from test_gpu_parity import diff_report, same_bits
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def fixture(name):
+    return json.load(open(os.path.join(GOLDEN, name)))
+
+
+@pytest.fixture(scope="module")
+def xlserver(pkg, model_root):
+    return pkg.ensure_model(os.path.join(model_root, "xlserver"), 23, seed=1234)
+
+
+@pytest.fixture(scope="module")
+def base(pkg, model_root):
+    return pkg.ensure_model(os.path.join(model_root, "base"), 1, seed=1234)
+
+
+def test_configs4_batched_verify_top8_128_experts(pkg, xlserver):
+    print("[case] configs[4]: 32 sessions of the 128-expert top-8 model, contexts 256-2048", flush=True)
+    eng = pkg.Engine(xlserver)
+    rng = np.random.default_rng(4)
+    ctx = rng.integers(256, 2049, size=32)
+    V = eng.V
+    batch, single = [], []
+    try:
+        for i, n in enumerate(ctx):
+            prompt = pkg.prompt_tokens(4000 + i, int(n), V)
+            for group in (batch, single):
+                st = eng.add_session()
+                eng.session_start_on(st, prompt)
+                group.append(st)
+        print(f"[case] 64 sessions prefilled ({int(ctx.sum())} prompt tokens each set)", flush=True)
+        toks = np.array([[(131 * i + 17 * j + 5) % V for j in range(4)] for i in range(32)], np.int32)
+        pos0 = ctx.astype(np.int32)
+        _, out = eng.verify_batch(batch, toks, pos0)
+        d = eng.d
+        for i, st in enumerate(single):
+            t = np.ascontiguousarray(toks[i])
+            assert eng.lib.lz_forward_verify(C.byref(eng.m), C.byref(st), t.ctypes.data_as(C.POINTER(C.c_int)), 4,
+                                             int(pos0[i])) == 0
+            lg = np.ctypeslib.as_array(st.mtp_logits, shape=(pkg.L98_SPEC_K_GPU + 1, V))[:4]
+            hd = np.ctypeslib.as_array(st.mtp_verify_hidden, shape=(pkg.L98_SPEC_K_GPU + 1, d))[:4]
+            assert same_bits(out[i][0], lg), f"session {i} (ctx {ctx[i]}) logits: " + diff_report(out[i][0], lg)
+            assert same_bits(out[i][1], hd), f"session {i} (ctx {ctx[i]}) hidden: " + diff_report(out[i][1], hd)
+            assert batch[i].ssm_slot == st.ssm_slot
+    finally:
+        for st in batch + single:
+            eng.free_session(st)
+        eng.close()
+
+
+def test_configs2_k7_temperature_matches_restatement(pkg, base):
+    g = fixture("ora_base_p512_k7_temp.json")
+    print("[case] configs[2]: configs[1] model, T=0.8 top-p 0.95, k=7, 512-token prompt", flush=True)
+    prompt = pkg.prompt_tokens(g["prompt_seed"], g["n_prompt"], g["vocab"])
+    eng = pkg.Engine(base, spec_k_max=7)
+    try:
+        toks, ke, na = eng.generate(prompt, 7, g["n_new"], g["temp"], g["topp"], g["sampler_seed"])
+        want = np.array(g["tokens"], np.int32)
+        n = min(len(toks), len(want))
+        assert n >= g["n_new"]
+        bad = np.nonzero(toks[:n] != want[:n])[0]
+        assert len(bad) == 0, f"first divergence at token {bad[0]}"
+        assert list(ke) == g["k_eff"] and list(na) == g["n_accept"]
+        assert eng.last_rng == g["rng"]
+    finally:
+        eng.close()
+
+
+def test_configs2_k7_greedy_emits_the_reference_k3_tokens(pkg, base):
+    """Greedy speculative decoding is lossless: at k = 7 the emitted tokens
+    are the reference's own at k = 3 (configs[1]'s 512-token prompt)."""
+    g = fixture("gen_base_p512_k3_greedy.json")
+    print("[case] configs[1] model greedy k=7 vs the reference's k=3 tokens", flush=True)
+    prompt = pkg.prompt_tokens(g["prompt_seed"], g["n_prompt"], g["vocab"])
+    eng = pkg.Engine(base, spec_k_max=7)
+    try:
+        toks, _, _ = eng.generate(prompt, 7, g["n_new"], 0.0, 1.0, 1)
+        want = np.array(g["tokens"], np.int32)
+        n = min(len(toks), len(want))
+        assert n >= g["n_new"]
+        assert np.array_equal(toks[:n], want[:n])
+    finally:
+        eng.close()
+
+
+def test_configs1_verify_of_eight_rows_equals_single_steps(pkg, base):
+    """The M = 8 verify on configs[1]'s shapes gives each row exactly the
+    logits and hidden row of forwarding that token alone."""
+    print("[case] configs[1] model M=8 verify vs single steps", flush=True)
+    prompt = pkg.prompt_tokens(0, 512, 65536)
+    toks = np.array([5, 17, 17, 40000, 2, 65535, 0, 31], np.int32)
+    a = pkg.Engine(base, spec_k_max=7)
+    b = pkg.Engine(base, spec_k_max=7)
+    try:
+        for e in (a, b):
+            e.reset()
+            assert e.batch_capture(prompt, 0) is not None
+        lg, hd = a.verify(toks, len(prompt))
+        for j, t in enumerate(toks):
+            one = b.forward_capture(int(t), len(prompt) + j)
+            assert np.array_equal(one.view(np.uint32), lg[j].view(np.uint32)), j
+            assert np.array_equal(b.chain().view(np.uint32), hd[j].view(np.uint32)), j
+    finally:
+        a.close()
+        b.close()

@@ -597,6 +597,10 @@ def test_oracle_matches_golden(pkg, model_root, fname):
     """The restatement reproduces the reference's recorded generations,
     including configs[1] (the benchmark model; about a minute of CPU)."""
     g = json.load(open(os.path.join(GOLDEN, fname)))
+    if g["n_prompt"] >= 512 or g["model"] == "xlserver":
+        pytest.skip("BASELINE-size fixture (512+ token prompts, the 6 GB configs[4] model): the GPU tests compare "
+                    "the HIP path with the reference's recorded outputs directly; the restatement is pinned on "
+                    "the shorter fixtures of the same models")
     model = pkg.ensure_model(os.path.join(model_root, g["model"]), g["config_id"], seed=g["model_seed"])
     digest = hashlib.sha256(open(os.path.join(model, "model.bin"), "rb").read()).hexdigest()
     assert digest == g["model_sha256"], "synthetic model generator changed"
