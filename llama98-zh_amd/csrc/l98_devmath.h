@@ -101,6 +101,20 @@ __device__ __forceinline__ int d_q8_round(float v) {
     return (int)(u_from_f(t) & 0x007FFFFFu) - 0x00400000;
 }
 
+// q8_group_scale's decisions as selects (straight-line code): amax > 0
+// with s = amax * (1/127) >= 1e-30 gives s and inv = 127 / amax; zero, NaN
+// and tiny groups give s = 1, inv = 0.  The reference's fallback of
+// dividing by s when 127 / amax overflows is unreachable: s >= 1e-30
+// means amax > 1.2e-28, so 127 / amax < 1.1e30 is finite.
+__device__ __forceinline__ void q8_scale_inv(float amax, float *sg, float *inv) {
+    const float INV127 = 1.0f / 127.0f;
+    const float sg0 = amax * INV127;
+    const float inv0 = 127.0f / amax;
+    const bool live = amax > 0.0f && !(sg0 < 1.0e-30f);
+    *sg = live ? sg0 : 1.0f;
+    *inv = live ? inv0 : 0.0f;
+}
+
 // sum of squares / n for power-of-two n is a multiply (src/ops_norm.c:161-170)
 __device__ __forceinline__ float d_ss_over_n(float ss, int n) {
     if ((n & (n - 1)) == 0) {
@@ -139,20 +153,11 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 // 32-lane half wave (lane & 31 = element).  Writes q[lane] and, from lane
 // 0 of the half, the scale.  src/ops_quant.c:1633-1670, 2152-2286.
 __device__ __forceinline__ void d_quant_group32(float x, int8_t *q, float *s) {
-    const float INV127 = 1.0f / 127.0f;
     uint32_t a = u_from_f(x) & 0x7FFFFFFFu;
     float amax = wave_max_u(a, 32);
     float sg, inv;
-    bool fast;
-    if (amax > 0.0f) {
-        sg = amax * INV127;
-        inv = 127.0f / amax;
-        fast = (inv <= 3.40282347e+38f);
-        if (sg < 1.0e-30f) { sg = 1.0f; inv = 0.0f; fast = true; }
-    } else {
-        sg = 1.0f; inv = 0.0f; fast = true;
-    }
-    int qi = fast ? d_q8_round(x * inv) : d_q8_round(x / sg);
+    q8_scale_inv(amax, &sg, &inv);
+    int qi = d_q8_round(x * inv);
     qi = qi > 127 ? 127 : qi;
     qi = qi < -127 ? -127 : qi;
     *q = (int8_t)qi;
@@ -450,25 +455,9 @@ __device__ __forceinline__ uint32_t abs_bits4(float4 v) {
 // The element loop of the quantization for a group whose amax is given
 // (q8_group_scale's decisions, then the rounding of each element).
 __device__ __forceinline__ uint32_t quant4_amax(float4 v, float amax, float *sg_out) {
-    const float INV127 = 1.0f / 127.0f;
     float sg, inv;
-    bool fast;
-    if (amax > 0.0f) {
-        sg = amax * INV127;
-        inv = 127.0f / amax;
-        fast = (inv <= 3.40282347e+38f);
-        if (sg < 1.0e-30f) { sg = 1.0f; inv = 0.0f; fast = true; }
-    } else {
-        sg = 1.0f; inv = 0.0f; fast = true;
-    }
-    float e[4] = {v.x, v.y, v.z, v.w};
-    if (fast) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) e[i] = e[i] * inv;
-    } else {                             // 127/amax overflowed: divide by the scale instead
-#pragma unroll
-        for (int i = 0; i < 4; i++) e[i] = e[i] / sg;
-    }
+    q8_scale_inv(amax, &sg, &inv);
+    float e[4] = {v.x * inv, v.y * inv, v.z * inv, v.w * inv};
     uint32_t packed = 0;
 #pragma unroll
     for (int i = 0; i < 4; i++) {

@@ -454,14 +454,13 @@ extern "C" int l98k_set_tokens(DevCtl *ctl, int op, RoundRec *hist, int hist_cap
 // on other XCDs) while block 0 writes the next buffer.
 __global__ void k_nop() {}
 
-// n <= 8192: every load of a thread is issued before the first use.
+// n <= 8192: every load of a thread is issued before the first use
+// (addresses clamped, no branches).
 __global__ __launch_bounds__(256) void k_handoff(const float *__restrict__ in, float *__restrict__ out, int n) {
     float4 v[8];
 #pragma unroll
-    for (int u = 0; u < 8; u++) {
-        const int i = (u * 256 + (int)threadIdx.x) * 4;
-        v[u] = i < n ? *reinterpret_cast<const float4 *>(in + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    }
+    for (int u = 0; u < 8; u++)
+        v[u] = *reinterpret_cast<const float4 *>(in + imin((u * 256 + (int)threadIdx.x) * 4, n - 4));
     float acc = 0.0f;
 #pragma unroll
     for (int u = 0; u < 8; u++) acc += v[u].x + v[u].y + v[u].z + v[u].w;
@@ -477,10 +476,8 @@ __global__ __launch_bounds__(256) void k_lastblock(const float *__restrict__ in,
                                                    float *__restrict__ part, unsigned int *__restrict__ cnt) {
     float4 v[8];
 #pragma unroll
-    for (int u = 0; u < 8; u++) {
-        const int i = (u * 256 + (int)threadIdx.x) * 4;
-        v[u] = i < n ? *reinterpret_cast<const float4 *>(in + i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    }
+    for (int u = 0; u < 8; u++)
+        v[u] = *reinterpret_cast<const float4 *>(in + imin((u * 256 + (int)threadIdx.x) * 4, n - 4));
     float acc = 0.0f;
 #pragma unroll
     for (int u = 0; u < 8; u++) acc += v[u].x + v[u].y + v[u].z + v[u].w;
@@ -513,5 +510,34 @@ extern "C" int l98k_launch_chain(int kind, int launches, int grid, float *a, flo
             hipLaunchKernelGGL(k_lastblock, dim3(grid), dim3(256), 0, st, src, dst, n, b + n,
                                reinterpret_cast<unsigned int *>(b + n + (size_t)grid * 256));
     }
+    return (int)hipGetLastError();
+}
+
+typedef int v4i_s __attribute__((ext_vector_type(4)));
+
+// Per-CU streaming probe: each block streams `chunks` 16-byte chunks of its
+// own region of w with non-temporal loads, J per thread in flight per
+// pass, and writes one word (so the loads are live).
+template <int J>
+__global__ void k_stream(const int4 *__restrict__ w, int chunks, int *__restrict__ out) {
+    const int4 *base = w + (size_t)blockIdx.x * chunks;
+    int acc = 0;
+    for (int c0 = 0; c0 < chunks; c0 += J * (int)blockDim.x) {
+        v4i_s q[J];
+#pragma unroll
+        for (int j = 0; j < J; j++) {
+            const int c = imin(c0 + j * (int)blockDim.x + (int)threadIdx.x, chunks - 1);
+            q[j] = __builtin_nontemporal_load(reinterpret_cast<const v4i_s *>(base) + c);
+        }
+#pragma unroll
+        for (int j = 0; j < J; j++) acc ^= q[j].x ^ q[j].y ^ q[j].z ^ q[j].w;
+    }
+    if (acc == 0x12345678) out[blockIdx.x] = acc;
+}
+
+extern "C" int l98k_stream(const void *w, int blocks, int threads, int chunks, int *out, hipStream_t st) {
+    if (blocks < 1 || (threads != 256 && threads != 512 && threads != 1024) || chunks < 1) return -1;
+    hipLaunchKernelGGL(k_stream<16>, dim3(blocks), dim3(threads), 0, st, reinterpret_cast<const int4 *>(w), chunks,
+                       out);
     return (int)hipGetLastError();
 }
