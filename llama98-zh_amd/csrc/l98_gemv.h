@@ -129,8 +129,8 @@ __device__ __forceinline__ unsigned long long amax_cand(float v, int i, int mode
     } while (0)
 
 template <int M, int PJ, int MODES, typename IssueW>
-__device__ __forceinline__ void build_rows(const Prologue &P, const int8_t *__restrict__ xq,
-                                           const float *__restrict__ xqs, int in_dim, const int (&xrow)[M], int nm,
+__device__ __forceinline__ void build_rows(const Prologue &P, const int8_t *xq,
+                                           const float *xqs, int in_dim, const int (&xrow)[M], int nm,
                                            bool writer, int8_t *sx, float *sxs, float *sq, float *s_inv,
                                            float *tab, IssueW issue_w) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -139,32 +139,40 @@ __device__ __forceinline__ void build_rows(const Prologue &P, const int8_t *__re
         // int4 chunk idx of the tile's rows: token idx / cpr, chunk idx % cpr;
         // the stores are unconditional (clamped: past the end they rewrite
         // the last chunk with its own value).
+        // (no __restrict__ on xq / xqs: the empty asm's memory clobber in
+        // PRO_ISSUE_W then keeps these loads above the weights', which a
+        // restrict-qualified read-only pointer would let the compiler sink
+        // to their LDS stores, each behind a wait for the whole tile)
         const int cpr = in_dim >> 4;
         const int total = M * cpr, stotal = M * nb;
-        int4 r[XQ_PER_THREAD];
-        float sc[XQ_PER_THREAD];
+        // loads per thread in the first batch: M rows of up to GEMV_MAX_IN
+        constexpr int XU = (M * (GEMV_MAX_IN / 16) + GEMV_THREADS - 1) / GEMV_THREADS < XQ_PER_THREAD
+                               ? (M * (GEMV_MAX_IN / 16) + GEMV_THREADS - 1) / GEMV_THREADS
+                               : XQ_PER_THREAD;
+        v4i r[XU];                       // a vector type: kept in registers (an int4 array went to scratch)
+        float sc[XU];
 #pragma unroll
-        for (int u = 0; u < XQ_PER_THREAD; u++) {
+        for (int u = 0; u < XU; u++) {
             const int idx = imin(u * GEMV_THREADS + tid, total - 1);
             const int t = idx / cpr, p = idx - t * cpr;
-            r[u] = *reinterpret_cast<const int4 *>(xq + (size_t)xrow[t < nm ? t : 0] * in_dim + p * 16);
+            r[u] = *reinterpret_cast<const v4i *>(xq + (size_t)xrow[t < nm ? t : 0] * in_dim + p * 16);
             const int si = imin(u * GEMV_THREADS + tid, stotal - 1);
             const int ts = si / nb;
             sc[u] = xqs[(size_t)xrow[ts < nm ? ts : 0] * nb + (si - ts * nb)];
         }
         PRO_ISSUE_W();
 #pragma unroll
-        for (int u = 0; u < XQ_PER_THREAD; u++) {
-            reinterpret_cast<int4 *>(sx)[imin(u * GEMV_THREADS + tid, total - 1)] = r[u];
+        for (int u = 0; u < XU; u++) {
+            reinterpret_cast<v4i *>(sx)[imin(u * GEMV_THREADS + tid, total - 1)] = r[u];
             sxs[imin(u * GEMV_THREADS + tid, stotal - 1)] = sc[u];
         }
-        for (int base = XQ_PER_THREAD * GEMV_THREADS; base < total; base += GEMV_THREADS) {
+        for (int base = XU * GEMV_THREADS; base < total; base += GEMV_THREADS) {
             const int idx = imin(base + tid, total - 1);
             const int t = idx / cpr, p = idx - t * cpr;
             reinterpret_cast<int4 *>(sx)[idx] =
                 *reinterpret_cast<const int4 *>(xq + (size_t)xrow[t < nm ? t : 0] * in_dim + p * 16);
         }
-        for (int base = XQ_PER_THREAD * GEMV_THREADS; base < stotal; base += GEMV_THREADS) {
+        for (int base = XU * GEMV_THREADS; base < stotal; base += GEMV_THREADS) {
             const int si = imin(base + tid, stotal - 1);
             const int ts = si / nb;
             sxs[si] = xqs[(size_t)xrow[ts < nm ? ts : 0] * nb + (si - ts * nb)];
@@ -453,8 +461,8 @@ __device__ __forceinline__ void tile_load(int4 (&wv)[GEMV_MAXJ], const int8_t *_
 // first.
 template <int M, int PJ, int MODES>
 __device__ __forceinline__ void gemv_tile(const int8_t *__restrict__ wt, const float *__restrict__ ws, int rows_here,
-                                          int R, int in_dim, const Prologue &P, const int8_t *__restrict__ xq,
-                                          const float *__restrict__ xqs, const int (&xrow)[M], const int *s_orow,
+                                          int R, int in_dim, const Prologue &P, const int8_t *xq,
+                                          const float *xqs, const int (&xrow)[M], const int *s_orow,
                                           int nm, bool writer, float *__restrict__ out, size_t out_stride,
                                           int row0, int32_t *__restrict__ acc_out, int acc_rows, char *smem,
                                           float *s_inv, float *tab, int gs = 0,
