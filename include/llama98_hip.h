@@ -299,6 +299,12 @@ int l98_greedy_rounds_batch(const LZModel *m, LZRunState **states, int n_seq, in
  * counter, acquire, the group's partials read back), as a graph.
  * Returns 0 (1 on a bad argument or a device error). */
 int l98_time_kernel(const LZModel *m, LZRunState *s, int which, int mrows, int iters, float *avg_ms);
+/* Per-CU streaming probe: 16 dependent launches of `blocks` blocks of
+ * `threads` (256, 512 or 1024) threads, each block streaming its own
+ * kb_per_block KiB (non-temporal 16-byte loads, 16 per thread in flight),
+ * each launch on a fresh region of a 1 GiB buffer.  *us_per_launch: the mean
+ * per launch.  Returns 0 (1 on a bad argument or a device error). */
+int l98_time_stream(LZRunState *s, int blocks, int threads, int kb_per_block, int iters, float *us_per_launch);
 /* For each of `rows` rows of n (<= 2048) non-negative floats (host
  * arrays), the float the serial loop s = 0; s += x[i] gives, computed on the
  * device by the parallel routine the RMSNorm kernels use for their sums of
@@ -351,10 +357,21 @@ int l98_moe_route(const float *logits, const float *bias, int nt, int E, int top
  * stays the answer).  A check of the kernel the rounds run; the reference
  * has no device.  Returns 0 (1 on a bad argument or a device error). */
 int l98_argmax_rows(const float *x, int rows, int n, int mode, int *out);
+/* The rounds' argmax path on host inputs: the tied lm_head GEMV's epilogue
+ * (per-tile packed maxima of N rows of K int8 weights with scales ws, one
+ * per row for gs = 0 or K, else K/gs per row in groups of gs) over M rows of
+ * per-32 quantized activations, then the reduction of the tile candidates;
+ * logits (M x N) and the argmax of each row (mode as l98_argmax_rows) come
+ * back.  A check of the kernels the rounds run (src/sampler.c:226-295); the
+ * reference has no device.  Returns 0 (1 on a bad argument or a device
+ * error). */
+int l98_gemv_argmax(const int8_t *w, const float *ws, int N, int K, int gs, const int8_t *xq, const float *xqs,
+                    int M, int mode, float *logits, int *out);
 /* lz_spec_accept_temp (src/generate.c:283-346) on host rows with no device
  * allocation: no counterpart in the reference; for callers that cannot call
- * hipMalloc (code under HIP graph capture, tight serving loops, harnesses
- * that forbid it).  The rows, the generator state and the result are staged
+ * hipMalloc (tight serving loops, harnesses that forbid it).  It copies
+ * synchronously and waits for its kernel, so it is not for code under HIP
+ * graph capture.  The rows, the generator state and the result are staged
  * in a static device array of 2 * L98_NOALLOC_MAX_VOCAB floats + 256 bytes
  * per GPU, held until the process ends; calls that overlap on one GPU race
  * on it.  Returns what lz_spec_accept_temp returns (the token, -1 on bad

@@ -130,6 +130,7 @@ HIP_API = [
     ("l98_greedy_rounds_ex", C.c_int, [C.POINTER(LZModel), C.POINTER(LZRunState), C.c_int, C.c_int, C.c_int,
                                        _IP, C.c_int, _IP, _IP, _IP, _FP]),
     ("l98_time_kernel", C.c_int, [C.POINTER(LZModel), C.POINTER(LZRunState), C.c_int, C.c_int, C.c_int, _FP]),
+    ("l98_time_stream", C.c_int, [C.POINTER(LZRunState), C.c_int, C.c_int, C.c_int, C.c_int, _FP]),
     ("l98_verify_batch", C.c_int, [C.POINTER(LZModel), C.POINTER(C.POINTER(LZRunState)), C.c_int, _IP, C.c_int,
                                    _IP, C.c_int, _FP]),
     ("l98_greedy_rounds_batch", C.c_int, [C.POINTER(LZModel), C.POINTER(C.POINTER(LZRunState)), C.c_int, C.c_int,
@@ -141,7 +142,8 @@ HIP_API = [
     ("l98_prefix_query", C.c_int, [_FP, C.c_int, C.c_int, C.c_int, _FP, _IP, _FP]),
     ("l98_moe_route", C.c_int, [_FP, _FP, C.c_int, C.c_int, C.c_int, _IP, _FP]),
     ("l98_argmax_rows", C.c_int, [_FP, C.c_int, C.c_int, C.c_int, _IP]),
-    ("l98_gemv_argmax", C.c_int, [C.c_void_p, _FP, C.c_int, C.c_int, C.c_void_p, _FP, C.c_int, C.c_int, _FP, _IP]),
+    ("l98_gemv_argmax", C.c_int, [C.c_void_p, _FP, C.c_int, C.c_int, C.c_int, C.c_void_p, _FP, C.c_int, C.c_int,
+                                  _FP, _IP]),
     ("l98_gemm_q8", C.c_int, [C.c_void_p, _FP, C.c_int, C.c_int, C.c_void_p, _FP, C.c_int, _FP]),
     ("l98_device_name", C.c_char_p, []),
     ("l98_last_loop_seconds", C.c_double, []),
@@ -373,6 +375,12 @@ class Engine:
         if self.lib.l98_time_kernel(C.byref(self.m), C.byref(self.s), which, mrows, iters, C.byref(ms)) != 0:
             raise RuntimeError("l98_time_kernel failed")
         return ms.value
+
+    def time_stream(self, blocks, threads, kb_per_block, iters=4):
+        us = C.c_float()
+        if self.lib.l98_time_stream(C.byref(self.s), blocks, threads, kb_per_block, iters, C.byref(us)) != 0:
+            raise RuntimeError("l98_time_stream failed")
+        return us.value
 
     def add_session(self, seq_len=0, spec_k_max=LZ_SPEC_K_MAX):
         """Another run state on the same model (an independent session)."""

@@ -912,6 +912,17 @@ int gemv(DState *s, std::initializer_list<GemvJob> jobs, int mtok) {
     return l98k_gemv(&b, mtok, s->st);
 }
 
+// Clears the pending argmax target when the function that set it returns,
+// so an error path between setting it and the lm_head leaves nothing behind
+// for an unrelated later lm_head GEMV.
+struct AmaxScope {
+    DState *s;
+    AmaxScope(DState *st, int *tok, int mode) : s(st) { s->amax_tok = tok; s->amax_mode = mode; }
+    ~AmaxScope() { s->amax_tok = nullptr; }
+    AmaxScope(const AmaxScope &) = delete;
+    AmaxScope &operator=(const AmaxScope &) = delete;
+};
+
 // The tied lm_head GEMV of job j over mtok rows.  When s->amax_tok is set
 // (then cleared), the rows' argmaxes (mode s->amax_mode) go there: the GEMV
 // keeps each tile's candidates and l98k_argmax_part reduces those, so the
@@ -1261,8 +1272,7 @@ int draft_step(DState *s, const int *toks, const int *ctl_pos, int pos_off, int 
     CK(gemv(s, {JX(m->mtp_fc, s->mtp_x, d, s->xq, s->xqs)}, 1));
     CK(attn_block(s, m->mtp, PN(s->mtp_x, d, nullptr, nullptr, m->mtp.in_norm, eps, nullptr, nullptr, 0),
                   s->planes - 1, ctl_pos, pos_off, 1, max_pos, false));
-    s->amax_tok = out_tok;       // argmax in the lm_head's epilogue
-    s->amax_mode = 1;
+    AmaxScope amax(s, out_tok, 1);   // argmax in the lm_head's epilogue
     CK(mtp_ffn_head(s, 1, s->chain, out_logits));
     return 0;
 }
@@ -1296,8 +1306,7 @@ int dspark_draft(DState *s, const int *toks, int k, float *out_logits, int *out_
         CK(l98k_rmsnorm_ex(s->sub_a, c.attn_q_dim, nullptr, nullptr, L.sn_o, c.attn_q_dim, eps, k, nullptr, 0,
                            s->xq2, s->xqs2, 0, s->st));
     CK(gemv(s, {JX(L.o, s->blk, d, s->xq2, s->xqs2)}, k));
-    s->amax_tok = out_tok;       // argmax in the lm_head's epilogue
-    s->amax_mode = 1;
+    AmaxScope amax(s, out_tok, 1);   // argmax in the lm_head's epilogue
     CK(mtp_ffn_head(s, k, nullptr, out_logits));
     return 0;
 }
@@ -1378,6 +1387,11 @@ namespace {
 #define WIDE_PARTS 3          // parts of a split chunk, each on its own stream (measured: 2 parts
                               // 10.1 ms, 3 parts 9.7 ms, 4 parts 15.0 ms for a 512-row prefill; four
                               // streams oversubscribe the process's four hardware queues)
+// Each part of a split chunk must exceed MAX_CHUNK rows: a part's rows run as
+// prefill items (wide_forward refuses a split part of MAX_CHUNK rows or
+// fewer), and the split is taken only when the last part also exceeds it.
+static_assert(((WIDE_SPLIT / WIDE_PARTS + MAX_CHUNK - 1) & ~(MAX_CHUNK - 1)) > MAX_CHUNK,
+              "the parts of the smallest split chunk must exceed MAX_CHUNK rows");
 
 // nullptr (the callers take the chunked path) for a SubLN model, whose
 // per-projection norms this many-row forward does not carry, and for a
@@ -2228,14 +2242,28 @@ extern "C" int lz_spec_accept_temp(const float *p, const float *q, int x, int vo
         return -1;
     }
     // the host rows go to the device and through the round's acceptance
-    // kernel (with this u); the generator state comes back
-    float *dp = nullptr, *dq = nullptr;
-    unsigned long long *drng = nullptr;
-    int *dout = nullptr, res[2] = {-1, 0}, rc = 0;
-    if (hipMalloc(&dp, sizeof(float) * (size_t)vocab) != hipSuccess ||
-        hipMalloc(&dq, sizeof(float) * (size_t)vocab) != hipSuccess ||
-        hipMalloc(&drng, sizeof(*drng)) != hipSuccess || hipMalloc(&dout, sizeof(res)) != hipSuccess)
-        rc = 1;
+    // kernel (with this u); the generator state comes back.  The staging
+    // (both rows, the generator state, the result) persists per device and
+    // grows only when a larger vocabulary arrives, so a call allocates
+    // nothing once a vocabulary has been seen (the reference's function is
+    // not reentrant either; the lock keeps concurrent callers apart).
+    static std::mutex mu;
+    static char *stage[64] = {};
+    static size_t cap[64] = {};
+    std::lock_guard<std::mutex> lock(mu);
+    int dev = 0, res[2] = {-1, 0}, rc = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) rc = 1;
+    const size_t need = 2 * sizeof(float) * (size_t)vocab + 256;
+    if (!rc && cap[dev] < need) {
+        if (stage[dev]) (void)hipFree(stage[dev]);
+        stage[dev] = nullptr;
+        cap[dev] = 0;
+        if (hipMalloc(&stage[dev], need) != hipSuccess) rc = 1;
+        else cap[dev] = need;
+    }
+    float *dp = rc ? nullptr : reinterpret_cast<float *>(stage[dev]), *dq = dp ? dp + vocab : nullptr;
+    unsigned long long *drng = dq ? reinterpret_cast<unsigned long long *>(dq + vocab) : nullptr;
+    int *dout = drng ? reinterpret_cast<int *>(drng + 1) : nullptr;
     if (!rc && (hipMemcpy(dp, p, sizeof(float) * (size_t)vocab, hipMemcpyHostToDevice) != hipSuccess ||
                 hipMemcpy(dq, q, sizeof(float) * (size_t)vocab, hipMemcpyHostToDevice) != hipSuccess ||
                 hipMemcpy(drng, rng, sizeof(*drng), hipMemcpyHostToDevice) != hipSuccess))
@@ -2244,8 +2272,6 @@ extern "C" int lz_spec_accept_temp(const float *p, const float *q, int x, int vo
     if (!rc && (hipMemcpy(res, dout, sizeof(res), hipMemcpyDeviceToHost) != hipSuccess ||
                 hipMemcpy(rng, drng, sizeof(*drng), hipMemcpyDeviceToHost) != hipSuccess))
         rc = 1;
-    for (void *m : {(void *)dp, (void *)dq, (void *)drng, (void *)dout})
-        if (m) (void)hipFree(m);
     if (rc) {
         if (out_accepted) *out_accepted = 0;
         return -1;
@@ -2323,10 +2349,11 @@ namespace {
 int enqueue_verify_accept(DState *d, int k_eff, int max_pos, int brk, bool catchup, hipEvent_t mark = nullptr) {
     const LZModelConfig &c = d->m->c;
     const bool dspark = d->m->n_draft > 1;     // no catch-up, mtp_pos kept (src/generate.c:1117-1133)
-    d->amax_tok = d->ctl->targ;  // the verify rows' argmaxes in the lm_head's epilogue
-    d->amax_mode = 0;
-    CK(forward_chunk(d, d->ctl->tok, k_eff + 1, &d->ctl->anchor_pos, 1, max_pos, d->vhidden, true,
-                     d->mtp_logits, false));
+    {
+        AmaxScope amax(d, d->ctl->targ, 0);   // the verify rows' argmaxes in the lm_head's epilogue
+        CK(forward_chunk(d, d->ctl->tok, k_eff + 1, &d->ctl->anchor_pos, 1, max_pos, d->vhidden, true,
+                         d->mtp_logits, false));
+    }
     CK(l98k_accept(d->ctl, d->vhidden, c.hidden_size, d->chain, d->depth, (brk ? 1 : 0) | (dspark ? 2 : 0), d->st));
     if (dspark) catchup = false;
     if (mark) CK(hipEventRecord(mark, d->st));
@@ -2903,21 +2930,24 @@ extern "C" int l98_argmax_rows(const float *x, int rows, int n, int mode, int *o
     return dout.put(out, sizeof(int) * rows) ? 0 : 1;
 }
 
-// The lm_head path's argmax: an int8 GEMV (one scale per weight row) over M
+// The lm_head path's argmax: an int8 GEMV (one scale per weight row, or
+// groups of gs) over M
 // pre-quantized rows with the argmax epilogue, then l98k_argmax_part;
 // logits [M][N] and the rows' argmaxes (mode 0 or 1) come back.
-extern "C" int l98_gemv_argmax(const int8_t *w, const float *ws, int N, int K, const int8_t *xq, const float *xqs,
-                               int M, int mode, float *logits, int *out) {
+extern "C" int l98_gemv_argmax(const int8_t *w, const float *ws, int N, int K, int gs, const int8_t *xq,
+                               const float *xqs, int M, int mode, float *logits, int *out) {
     if (!w || !ws || !xq || !xqs || !logits || !out || N < 1 || K < 32 || (K & 31) || M < 1 || M > MAX_CHUNK ||
-        (mode != 0 && mode != 1))
+        (mode != 0 && mode != 1) || gs < 0 || (gs && ((gs & 31) || K % gs)))
         return 1;
+    if (gs == K) gs = 0;
+    const size_t nws = gs ? (size_t)(K / gs) : 1;
     int cap = 0;
     for (int m = 1; m <= MAX_CHUNK; m *= 2) {
         const int need = l98k_gemv_tiles(N, K, m) * m;
         cap = need > cap ? need : cap;
     }
     DevBuf dw, dws, dx, dxs, dl, dp, dout;
-    if (!dw.get(w, (size_t)N * K) || !dws.get(ws, sizeof(float) * N) || !dx.get(xq, (size_t)M * K) ||
+    if (!dw.get(w, (size_t)N * K) || !dws.get(ws, sizeof(float) * N * nws) || !dx.get(xq, (size_t)M * K) ||
         !dxs.get(xqs, sizeof(float) * (size_t)M * (K / 32)) || !dl.get(nullptr, sizeof(float) * (size_t)M * N) ||
         !dp.get(nullptr, sizeof(unsigned long long) * (size_t)cap) || !dout.get(nullptr, sizeof(int) * M))
         return 1;
@@ -2926,7 +2956,7 @@ extern "C" int l98_gemv_argmax(const int8_t *w, const float *ws, int N, int K, c
     GemvJob &j = b.job[0];
     j.w = (const int8_t *)dw.p; j.ws = (const float *)dws.p; j.out = (float *)dl.p;
     j.xq = (const int8_t *)dx.p; j.xqs = (const float *)dxs.p;
-    j.rows = N; j.in_dim = K; j.out_stride = N; j.gs = 0;
+    j.rows = N; j.in_dim = K; j.out_stride = N; j.gs = gs;
     j.pro.mode = PRO_XQ;
     b.amax_mode = mode;
     b.amax_part = (unsigned long long *)dp.p;
@@ -3343,6 +3373,38 @@ extern "C" int l98_generate(const LZModel *mm, LZRunState *s, const int *prompt,
 //   6  the same for every layer's MoE input (router, latent down, shared
 //      gate and up).  4-6 read the state's residual rows and write only
 //      scratch rows, so the session stays usable.
+// Streaming probe: 16 dependent launches of `blocks` blocks of `threads`
+// threads, each block streaming its own kb_per_block KiB with all loads of a
+// pass in flight, each launch on a fresh region of a 1 GiB buffer (beyond
+// the last-level cache); *us_per_launch is the mean per launch.
+extern "C" int l98_time_stream(LZRunState *s, int blocks, int threads, int kb_per_block, int iters,
+                               float *us_per_launch) {
+    if (!s || !s->impl || blocks < 1 || kb_per_block < 1 || iters < 1 || !us_per_launch) return 1;
+    DState *d = S(s);
+    const size_t per = (size_t)kb_per_block << 10, span = per * (size_t)blocks, total = (size_t)1 << 30;
+    if (span > total / 16) return 1;
+    char *buf = nullptr;
+    if (hipMalloc(&buf, total + 4096) != hipSuccess) return 1;
+    int rc = hipMemsetAsync(buf, 1, total, d->st) != hipSuccess;
+    int *out = reinterpret_cast<int *>(buf + total);
+    float ms = 0.0f;
+    if (!rc) rc = l98k_stream(buf, blocks, threads, (int)(per / 16), out, d->st);
+    if (!rc) {
+        (void)hipEventRecord(d->ev0, d->st);
+        for (int it = 0; it < iters && !rc; it++)
+            for (int i = 0; i < 16 && !rc; i++)
+                rc = l98k_stream(buf + (size_t)i * (total / 16), blocks, threads, (int)(per / 16), out, d->st);
+        (void)hipEventRecord(d->ev1, d->st);
+        if (!rc && hipEventSynchronize(d->ev1) != hipSuccess) rc = 1;
+        if (!rc) (void)hipEventElapsedTime(&ms, d->ev0, d->ev1);
+    }
+    (void)hipStreamSynchronize(d->st);
+    (void)hipFree(buf);
+    if (rc) return 1;
+    *us_per_launch = ms * 1e3f / (float)(16 * iters);
+    return 0;
+}
+
 extern "C" int l98_time_kernel(const LZModel *mm, LZRunState *s, int which, int mrows, int iters,
                                float *avg_ms) {
     if (!mm || !s || !s->impl || iters < 1 || mrows < 1 || mrows > MAX_CHUNK || !avg_ms) return 1;

@@ -161,6 +161,9 @@ int l98k_set_tokens(DevCtl *ctl, int op, RoundRec *hist, int hist_cap, hipStream
 // 8192), or kind 1 plus a last-block reduction per 8 blocks (kind 2: b is
 // followed by grid x 256 floats of partials and grid counters).
 int l98k_launch_chain(int kind, int launches, int grid, float *a, float *b, int n, hipStream_t st);
+// Streaming probe: `blocks` blocks of `threads` threads, each streaming its
+// own `chunks` 16-byte chunks of w.
+int l98k_stream(const void *w, int blocks, int threads, int chunks, int *out, hipStream_t st);
 }
 
 #endif

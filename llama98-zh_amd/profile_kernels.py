@@ -68,6 +68,15 @@ def main():
                             (11, "graph, mode 9 plus a last-block reduction per 8 blocks")):
             us = eng.time_kernel(which, 4, args.iters) * 1e3
             print(f"mode {which} ({name}): {us:.3f} us/launch", flush=True)
+        # per-CU streaming: the same bytes per launch over few fat blocks or
+        # many thin ones
+        for blocks, threads, kb in ((16, 1024, 384), (24, 1024, 384), (32, 1024, 192), (64, 1024, 96),
+                                    (64, 256, 96), (128, 256, 48), (256, 256, 24), (256, 256, 32),
+                                    (256, 1024, 256), (2048, 256, 32)):
+            us = eng.time_stream(blocks, threads, kb)
+            print(f"stream {blocks} blocks x {threads} threads x {kb} KiB: {us:.3f} us/launch, "
+                  f"{blocks * kb * 1024 / (us * 1e-6) / 1e9:.0f} GB/s, "
+                  f"{kb * 1024 / (us * 1e-6) / 1e9:.1f} GB/s per block", flush=True)
         eng.close()
         return
     for which, name in ((0, "lm_head"), (4, "kda input"), (5, "attention input"), (6, "moe input"), (2, "copy")):

@@ -47,26 +47,30 @@ def test_device_argmax_matches_oracle(pkg, n):
             assert out[r] == want, (mode, r, out[r], want)
 
 
-@pytest.mark.parametrize("M", [1, 4, 8])
-def test_gemv_argmax_epilogue_matches_oracle(pkg, M):
+@pytest.mark.parametrize("M,gs", [(1, 0), (2, 0), (3, 0), (4, 0), (8, 0), (1, 64), (4, 64), (1, 128), (4, 128)])
+def test_gemv_argmax_epilogue_matches_oracle(pkg, M, gs):
     # The rounds' argmax: per-tile candidates from the lm_head GEMV's
-    # epilogue, reduced by l98k_argmax_part.  Row scales plant the special
-    # values in whole logit columns: NaN at index 0 and elsewhere, +inf ties,
-    # a band of zeros (0 scale, and -0 scale), and a maximum in the last row.
+    # epilogue, reduced by l98k_argmax_part, with one scale per weight row
+    # (gs = 0) or grouped scales (the instances a model.bin with Q8_0 groups
+    # of 64 or 128 runs).  Row scales plant the special values in whole logit
+    # columns: NaN at index 0 and elsewhere, +inf ties, a band of zeros (0
+    # scale, and -0 scale), and a maximum in the last row.
     lib = pkg.hip_lib()
     L = OL.lib()
     N, K = 65536 + 40, 1024
-    rng = np.random.default_rng(M)
+    nws = K // gs if gs else 1
+    rng = np.random.default_rng(M + gs)
     w = rng.integers(-127, 128, (N, K), dtype=np.int8)
     xq = rng.integers(-127, 128, (M, K), dtype=np.int8)
     xqs = (rng.random((M, K // 32)) * 0.01 + 1e-4).astype(np.float32)
-    ws = (rng.random(N) * 0.01).astype(np.float32)
+    ws = (rng.random((N, nws)) * 0.01).astype(np.float32)
     ws[0] = np.nan
     ws[777] = np.nan
     ws[100:140] = 0.0
     ws[140:160] = -0.0
     ws[3000] = ws[5000] = np.inf
     ws[N - 1] = 1e30
+    print(f"[case] gemv argmax M={M} gs={gs}", flush=True)
     for mode in (0, 1):
         for plant in (True, False):
             s = ws.copy()
@@ -74,8 +78,8 @@ def test_gemv_argmax_epilogue_matches_oracle(pkg, M):
                 s[[0, 777, 3000, 5000, N - 1]] = 0.0
             logits = np.zeros((M, N), np.float32)
             out = np.zeros(M, np.int32)
-            assert lib.l98_gemv_argmax(w.ctypes.data, fp(s), N, K, xq.ctypes.data, fp(xqs), M, mode,
-                                       fp(logits), ip(out)) == 0
+            assert lib.l98_gemv_argmax(w.ctypes.data, fp(np.ascontiguousarray(s)), N, K, gs, xq.ctypes.data,
+                                       fp(xqs), M, mode, fp(logits), ip(out)) == 0
             for r in range(M):
                 row = np.ascontiguousarray(logits[r])
                 if mode == 0:

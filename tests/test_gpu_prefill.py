@@ -82,11 +82,11 @@ def test_configs3_prompt_chunking_invariant(pkg, model_root):
 
 @pytest.mark.parametrize("n", [63, 64, 65, 97, 130, 600])
 def test_split_prefill_matches_chunked(pkg, server, n):
-    """A wide prefill chunk of 64 or more rows runs in two parts on two
-    streams (the second part's layers wait for the first part's KDA
-    recurrence and attention); rows and the next verify's logits equal the
-    8-row chunked path bit for bit, at part sizes around the split's
-    threshold and rounding, and over two wide chunks (600 rows)."""
+    """A wide prefill chunk of 64 or more rows runs in three parts, each on
+    its own stream (part p's layers wait for part p - 1's KDA recurrence and
+    attention), when every part exceeds 8 rows; rows and the next verify's
+    logits equal the 8-row chunked path bit for bit, at part sizes around the
+    split's threshold and rounding, and over two wide chunks (600 rows)."""
     print(f"[case] split prefill n={n}", flush=True)
     prompt = pkg.prompt_tokens(9, n, 8192)
     eng = pkg.Engine(server)
