@@ -253,6 +253,11 @@ int l98_generate(const LZModel *m, LZRunState *s, const int *prompt, int n_promp
  * device round state.  Returns the first emitted token, or -LZErr. */
 int l98_session_start(const LZModel *m, LZRunState *s, const int *prompt, int n_prompt,
                       const LZSampler *samp);
+/* The sampler of the session l98_session_start began (its parameters and
+ * the generator state after the first token's draw), for a caller that
+ * drives the session's rounds itself (lz_spec_round_temp).  Returns 0, or
+ * 1 on a null argument. */
+int l98_session_sampler(const LZRunState *s, LZSampler *out);
 /* n greedy rounds after l98_session_start (or a previous call), back to back
  * on the device: every scalar of a round (positions, ring slot, drafts,
  * acceptance) stays in device memory, and with use_graph each round is one
@@ -357,6 +362,12 @@ int l98_moe_route(const float *logits, const float *bias, int nt, int E, int top
  * stays the answer).  A check of the kernel the rounds run; the reference
  * has no device.  Returns 0 (1 on a bad argument or a device error). */
 int l98_argmax_rows(const float *x, int rows, int n, int mode, int *out);
+/* The top-p candidates' order on host keys: a stable descending sort of n
+ * (<= 2^20) keys below 2^30 (the bits of probabilities in [0, 1]) with
+ * their indices, by the library's radix sort, as select_all orders the
+ * candidates (src/sampler.c:526-538: descending, equal keys in index
+ * order).  Returns 0 (1 on a bad argument or a device error). */
+int l98_sort_desc(const uint32_t *keys, int n, uint32_t *keys_out, int *idx_out);
 /* The rounds' argmax path on host inputs: the tied lm_head GEMV's epilogue
  * (per-tile packed maxima of N rows of K int8 weights with scales ws, one
  * per row for gs = 0 or K, else K/gs per row in groups of gs) over M rows of

@@ -123,6 +123,7 @@ HIP_API = [
     ("lz_argmax_p1", C.c_int, [_FP, C.c_int, _FP]),
     ("l98_generate", C.c_int, [C.POINTER(LZModel), C.POINTER(LZRunState), _IP, C.c_int, C.c_int, C.c_int,
                                C.POINTER(LZSampler), _IP, C.c_int, _IP, _IP, _IP]),
+    ("l98_session_sampler", C.c_int, [C.POINTER(LZRunState), C.POINTER(LZSampler)]),
     ("l98_session_start", C.c_int, [C.POINTER(LZModel), C.POINTER(LZRunState), _IP, C.c_int,
                                     C.POINTER(LZSampler)]),
     ("l98_greedy_rounds", C.c_int, [C.POINTER(LZModel), C.POINTER(LZRunState), C.c_int, C.c_int, C.c_int, _IP,
@@ -142,6 +143,7 @@ HIP_API = [
     ("l98_prefix_query", C.c_int, [_FP, C.c_int, C.c_int, C.c_int, _FP, _IP, _FP]),
     ("l98_moe_route", C.c_int, [_FP, _FP, C.c_int, C.c_int, C.c_int, _IP, _FP]),
     ("l98_argmax_rows", C.c_int, [_FP, C.c_int, C.c_int, C.c_int, _IP]),
+    ("l98_sort_desc", C.c_int, [C.c_void_p, C.c_int, C.c_void_p, _IP]),
     ("l98_gemv_argmax", C.c_int, [C.c_void_p, _FP, C.c_int, C.c_int, C.c_int, C.c_void_p, _FP, C.c_int, C.c_int,
                                   _FP, _IP]),
     ("l98_gemm_q8", C.c_int, [C.c_void_p, _FP, C.c_int, C.c_int, C.c_void_p, _FP, C.c_int, _FP]),
@@ -495,6 +497,44 @@ class Engine:
                 toks.extend(int(t) for t in out[:n_acc + 1])
             pos = new_pos + 1
             token = int(out[n_acc])
+        return np.array(toks, np.int32), np.array(ke, np.int32), np.array(na, np.int32)
+
+    def generate_host_temp(self, prompt, k, n_new, temp, topp, seed):
+        """Temperature generation driven from the host through the reference
+        entry point lz_spec_round_temp, round by round (l98_session_start for
+        the prefill and the first draw, then the session's sampler).  Returns
+        (tokens, k_eff per round, n_accept per round); last_rng is the
+        generator state after the run."""
+        prompt = np.ascontiguousarray(prompt, np.int32)
+        p = LZSampleParams()
+        self.lib.lz_sample_defaults(C.byref(p))
+        p.temperature, p.topp, p.topk, p.minp = temp, topp, 0, 0.0
+        p.presence_penalty, p.frequency_penalty, p.repetition_penalty, p.repeat_last_n = 0.0, 0.0, 1.0, 0
+        samp = LZSampler()
+        self.lib.lz_sampler_init(C.byref(samp), self.V, C.byref(p), seed)
+        anchor = self.lib.l98_session_start(C.byref(self.m), C.byref(self.s), _ip(prompt), len(prompt),
+                                            C.byref(samp))
+        if anchor < 0:
+            raise RuntimeError(f"l98_session_start failed: {anchor}")
+        assert self.lib.l98_session_sampler(C.byref(self.s), C.byref(samp)) == 0
+        toks, ke, na = [anchor], [], []
+        anchor_pos = len(prompt) - 1
+        out = np.zeros(L98_SPEC_K_GPU + 1, np.int32)
+        n_acc, npos, k_eff = C.c_int(), C.c_int(), C.c_int()
+        err = C.create_string_buffer(256)
+        while len(toks) < n_new:
+            r = self.lib.lz_spec_round_temp(C.byref(self.m), C.byref(self.s), int(anchor), int(anchor_pos), int(k),
+                                            0.0, 0, C.byref(samp), 0, 0, _ip(out),
+                                            C.byref(n_acc), C.byref(npos), C.byref(k_eff), err, 256)
+            if r < 0:
+                raise RuntimeError(f"lz_spec_round_temp failed: {r} {err.value.decode()}")
+            if r == 0:
+                raise RuntimeError("a discarded round (p_min and n_min are 0 here)")
+            ke.append(k_eff.value)
+            na.append(n_acc.value)
+            toks.extend(int(t) for t in out[:n_acc.value + 1])
+            anchor, anchor_pos = int(out[n_acc.value]), npos.value
+        self.last_rng = samp.rng_state
         return np.array(toks, np.int32), np.array(ke, np.int32), np.array(na, np.int32)
 
     def generate(self, prompt, k, n_new, temp=0.0, topp=1.0, seed=1):

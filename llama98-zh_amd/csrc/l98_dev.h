@@ -114,7 +114,8 @@ typedef struct {
     int catch_tok[16];       // catch-up tokens; rows past catch_n carry a valid stand-in id
     int round;               // rounds completed since the history was cleared
     int expert_tally;        // distinct experts streamed by the MoE layers since the last round record
-    int pad[14];
+    int smp_done;            // temperature round: a verify row rejected its draft (later rows do nothing)
+    int pad[13];
 } DevCtl;
 
 // One finished round as the host reads it back.

@@ -814,6 +814,8 @@ struct DState {
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     hipEvent_t ph[4] = {};                  // phase marks of a host-driven round (draft / verify / catch-up)
     hipGraphExec_t round_graph[L98_SPEC_K_GPU + 1] = {};
+    hipGraphExec_t temp_graph[L98_SPEC_K_GPU + 1] = {};   // device temperature rounds, per k
+    float temp_graph_t[L98_SPEC_K_GPU + 1] = {}, temp_graph_p[L98_SPEC_K_GPU + 1] = {};   // their T and top-p
     LZSampler session_samp{};               // the sampler of the current session (l98_session_start)
     bool session_greedy = true;
     // temperature sampling scratch (allocated on first use)
@@ -821,7 +823,7 @@ struct DState {
     float *smp_q = nullptr;                 // [L98_SPEC_K_GPU][V] draft distributions of a round
     float *smp_p = nullptr, *smp_probs = nullptr;
     uint32_t *smp_keys = nullptr, *smp_skeys = nullptr;
-    int *smp_vals = nullptr, *smp_svals = nullptr;
+    int *smp_svals = nullptr;
     void *smp_tmp = nullptr;
     size_t smp_tmp_bytes = 0;
     unsigned long long *smp_rng = nullptr;
@@ -1854,6 +1856,8 @@ extern "C" void lz_state_free(LZRunState *s) {
             if (e) (void)hipEventDestroy(e);
         for (auto &g : d->round_graph)
             if (g) (void)hipGraphExecDestroy(g);
+        for (auto &g : d->temp_graph)
+            if (g) (void)hipGraphExecDestroy(g);
         if (d->st) (void)hipStreamDestroy(d->st);
         delete d;
     }
@@ -2507,12 +2511,11 @@ namespace {
 bool smp_ensure(DState *d) {
     if (d->smp_arena) return true;
     const size_t V = (size_t)d->m->c.vocab_size;
-    size_t tmp = 0;
-    if (l98k_smp_sort_desc(nullptr, nullptr, nullptr, nullptr, (int)V, nullptr, &tmp, d->st)) return false;
+    const size_t tmp = l98k_smp_sort_tmp_bytes((int)V);
     size_t off = 0;
     auto take = [&](size_t bytes) { size_t a = off; off = (off + bytes + 255) & ~(size_t)255; return a; };
     const size_t oq = take(sizeof(float) * V * L98_SPEC_K_GPU), op = take(sizeof(float) * V),
-                 opr = take(sizeof(float) * V), ok = take(4 * V), osk = take(4 * V), ov = take(4 * V),
+                 opr = take(sizeof(float) * V), ok = take(4 * V), osk = take(4 * V),
                  osv = take(4 * V), ot = take(tmp), orng = take(8), oo = take(64), oof = take(64);
     char *a = nullptr;
     if (hipMalloc(&a, off) != hipSuccess) return false;
@@ -2522,7 +2525,6 @@ bool smp_ensure(DState *d) {
     d->smp_probs = (float *)(a + opr);
     d->smp_keys = (uint32_t *)(a + ok);
     d->smp_skeys = (uint32_t *)(a + osk);
-    d->smp_vals = (int *)(a + ov);
     d->smp_svals = (int *)(a + osv);
     d->smp_tmp = a + ot;
     d->smp_tmp_bytes = tmp;
@@ -2536,15 +2538,16 @@ bool smp_ensure(DState *d) {
 // logits row into d->smp_p: softmax(row / T), then with top-p the
 // candidates >= (1 - top_p) / (V - 1) sorted by probability (stable), the
 // prefix up to the first cumulative mass >= top_p renormalized.
-int dev_target_dist(DState *d, const float *row, int V, float temp, float topp) {
+// skip: a device flag (null: never) that turns every launch into a no-op.
+int dev_target_dist(DState *d, const float *row, int V, float temp, float topp, const int *skip = nullptr) {
     const float inv = 1.0f / temp;
-    if (!topp_active(topp)) return l98k_smp_softmax(row, V, inv, d->smp_p, 0.0f, nullptr, nullptr, nullptr, d->st);
+    if (!topp_active(topp)) return l98k_smp_softmax(row, V, inv, d->smp_p, 0.0f, nullptr, nullptr, skip, d->st);
     const float cutoff = (V > 1) ? (1.0f - topp) / (float)(V - 1) : 0.0f;
-    size_t tb = d->smp_tmp_bytes;
-    if (l98k_smp_softmax(row, V, inv, d->smp_probs, cutoff, d->smp_keys, d->smp_vals, d->smp_out + 8, d->st) ||
-        l98k_smp_sort_desc(d->smp_keys, d->smp_skeys, d->smp_vals, d->smp_svals, V, d->smp_tmp, &tb, d->st))
+    if (l98k_smp_softmax(row, V, inv, d->smp_probs, cutoff, d->smp_keys, d->smp_out + 8, skip, d->st) ||
+        l98k_smp_sort_desc(d->smp_keys, d->smp_skeys, d->smp_svals, V, d->smp_tmp, skip, d->st))
         return 1;
-    return l98k_smp_topp_dist(d->smp_probs, V, d->smp_skeys, d->smp_svals, d->smp_out + 8, topp, d->smp_p, d->st);
+    return l98k_smp_topp_dist(d->smp_probs, V, d->smp_skeys, d->smp_svals, d->smp_out + 8, topp, d->smp_p, skip,
+                              d->st);
 }
 
 // lz_sample_ex for temperature > 0 (src/sampler.c:794-840) on a device
@@ -2555,13 +2558,12 @@ int dev_sample_ex(DState *d, const float *row, int V, float temp, float topp, lz
     if (hipMemcpyAsync(d->smp_rng, rng, sizeof(lz_u64), hipMemcpyHostToDevice, d->st)) return 1;
     if (!topp_active(topp)) {
         if (l98k_smp_softmax(row, V, inv, d->smp_probs, 0.0f, nullptr, nullptr, nullptr, d->st) ||
-            l98k_smp_draw(d->smp_probs, V, d->smp_rng, d->smp_out, nullptr, nullptr, d->st))
+            l98k_smp_draw(d->smp_probs, V, d->smp_rng, d->smp_out, nullptr, nullptr, nullptr, d->st))
             return 1;
     } else {
         const float cutoff = (V > 1) ? (1.0f - topp) / (float)(V - 1) : 0.0f;
-        size_t tb = d->smp_tmp_bytes;
-        if (l98k_smp_softmax(row, V, inv, d->smp_probs, cutoff, d->smp_keys, d->smp_vals, d->smp_out + 8, d->st) ||
-            l98k_smp_sort_desc(d->smp_keys, d->smp_skeys, d->smp_vals, d->smp_svals, V, d->smp_tmp, &tb, d->st) ||
+        if (l98k_smp_softmax(row, V, inv, d->smp_probs, cutoff, d->smp_keys, d->smp_out + 8, nullptr, d->st) ||
+            l98k_smp_sort_desc(d->smp_keys, d->smp_skeys, d->smp_svals, V, d->smp_tmp, nullptr, d->st) ||
             l98k_smp_sample_topp(d->smp_probs, V, d->smp_skeys, d->smp_svals, d->smp_out + 8, topp, d->smp_rng,
                                  d->smp_out, d->st))
             return 1;
@@ -2569,6 +2571,45 @@ int dev_sample_ex(DState *d, const float *row, int V, float temp, float topp, lz
     if (hipMemcpyAsync(tok, d->smp_out, sizeof(int), hipMemcpyDeviceToHost, d->st) ||
         hipMemcpyAsync(rng, d->smp_rng, sizeof(lz_u64), hipMemcpyDeviceToHost, d->st) || hipStreamSynchronize(d->st))
         return 1;
+    return 0;
+}
+
+// One temperature round on the device: lz_spec_round_temp with p_min = 0,
+// n_min = 0 and the one-slot head (src/generate.c:1234-1377).  k chained
+// draft steps, each q_i = softmax(logits/T) and a draw into ctl->tok[1+i]
+// (lz_sample_temp_q, src/sampler.c:736-747); the (k+1)-row verify; per
+// row i the target distribution (lz_target_dist) and the acceptance test
+// with residual resampling, which on a rejection records n_accept = i and
+// sets ctl->smp_done, after which every sampling launch of the round does
+// nothing (the reference's loop stops there, drawing nothing more); the
+// bonus draw from row k when no row rejected; then the ring rollback, chain
+// reseed, catch-up and round record of the greedy round.  Every scalar
+// lives in ctl and the generator state in device memory, so the sequence
+// is graph-capturable.
+int enqueue_temp_round(DState *d, int k, int max_pos, float temp, float topp) {
+    const LZModelConfig &c = d->m->c;
+    const int V = c.vocab_size;
+    const float inv = 1.0f / temp;
+    for (int i = 0; i < k; i++) {
+        float *qi = d->smp_q + (size_t)i * V;
+        CK(draft_step(d, d->ctl->tok + i, &d->ctl->mtp_pos, i, max_pos, d->draft_logits, nullptr));
+        CK(l98k_smp_softmax(d->draft_logits, V, inv, qi, 0.0f, nullptr, nullptr, nullptr, d->st));
+        CK(l98k_smp_draw(qi, V, d->smp_rng, d->smp_out, d->smp_outf, d->ctl->tok + 1 + i, nullptr, d->st));
+    }
+    CK(forward_chunk(d, d->ctl->tok, k + 1, &d->ctl->anchor_pos, 1, max_pos, d->vhidden, true, d->mtp_logits,
+                     false));
+    CK(l98k_set_tokens(d->ctl, 2, nullptr, 0, d->st));
+    const int *done = &d->ctl->smp_done;
+    for (int i = 0; i < k; i++) {
+        CK(dev_target_dist(d, d->mtp_logits + (size_t)i * V, V, temp, topp, done));
+        CK(l98k_smp_accept_row(d->smp_p, d->smp_q + (size_t)i * V, V, d->ctl->tok + 1 + i, d->smp_rng,
+                               d->ctl->out + i, &d->ctl->n_accept, &d->ctl->smp_done, i, d->st));
+    }
+    CK(dev_target_dist(d, d->mtp_logits + (size_t)k * V, V, temp, topp, done));
+    CK(l98k_smp_draw(d->smp_p, V, d->smp_rng, d->smp_out, nullptr, d->ctl->out + k, done, d->st));
+    CK(l98k_accept(d->ctl, d->vhidden, c.hidden_size, d->chain, d->depth, 4, d->st));
+    if (k > 1) CK(mtp_prefill_dev(d, d->vhidden, d->ctl->catch_tok, k - 1, &d->ctl->catch_pos, 0));
+    CK(l98k_set_tokens(d->ctl, 1, d->hist, d->hist_cap, d->st));
     return 0;
 }
 
@@ -2712,7 +2753,7 @@ int spec_round_temp(const LZModel *mm, LZRunState *s, int anchor, int anchor_pos
         int idx = 0;
         float qidx = 0.0f;
         if (l98k_smp_softmax(row, V, inv, qi, 0.0f, nullptr, nullptr, nullptr, d->st) ||
-            l98k_smp_draw(qi, V, d->smp_rng, d->smp_out, d->smp_outf, d->ctl->tok + 1 + i, d->st) ||
+            l98k_smp_draw(qi, V, d->smp_rng, d->smp_out, d->smp_outf, d->ctl->tok + 1 + i, nullptr, d->st) ||
             hipMemcpyAsync(&idx, d->smp_out, sizeof(int), hipMemcpyDeviceToHost, d->st) ||
             hipMemcpyAsync(&qidx, d->smp_outf, sizeof(float), hipMemcpyDeviceToHost, d->st) ||
             hipStreamSynchronize(d->st))
@@ -2752,7 +2793,7 @@ int spec_round_temp(const LZModel *mm, LZRunState *s, int anchor, int anchor_pos
     }
     if (n_accept == k_eff) {
         if (dev_target_dist(d, d->mtp_logits + (size_t)k_eff * V, V, temp, topp) ||
-            l98k_smp_draw(d->smp_p, V, d->smp_rng, d->smp_out, nullptr, nullptr, d->st) ||
+            l98k_smp_draw(d->smp_p, V, d->smp_rng, d->smp_out, nullptr, nullptr, nullptr, d->st) ||
             hipMemcpyAsync(out + k_eff, d->smp_out, sizeof(int), hipMemcpyDeviceToHost, d->st))
             return -LZ_ERR_FORWARD;
     }
@@ -2922,6 +2963,18 @@ extern "C" int l98_gemm_q8(const int8_t *w, const float *ws, int N, int K, const
     return dout.put(out, sizeof(float) * (size_t)M * N) ? 0 : 1;
 }
 
+extern "C" int l98_sort_desc(const uint32_t *keys, int n, uint32_t *keys_out, int *idx_out) {
+    if (!keys || !keys_out || !idx_out || n < 1 || n > (1 << 20)) return 1;
+    for (int i = 0; i < n; i++)
+        if (keys[i] >= (1u << 30)) return 1;
+    DevBuf dk, dko, dio, dt;
+    if (!dk.get(keys, sizeof(uint32_t) * (size_t)n) || !dko.get(nullptr, sizeof(uint32_t) * (size_t)n) ||
+        !dio.get(nullptr, sizeof(int) * (size_t)n) || !dt.get(nullptr, l98k_smp_sort_tmp_bytes(n)))
+        return 1;
+    if (l98k_smp_sort_desc((uint32_t *)dk.p, (uint32_t *)dko.p, (int *)dio.p, n, dt.p, nullptr, nullptr)) return 1;
+    return dko.put(keys_out, sizeof(uint32_t) * (size_t)n) && dio.put(idx_out, sizeof(int) * (size_t)n) ? 0 : 1;
+}
+
 extern "C" int l98_argmax_rows(const float *x, int rows, int n, int mode, int *out) {
     if (!x || !out || rows < 1 || rows > MAX_CHUNK || n < 1 || (mode != 0 && mode != 1)) return 1;
     DevBuf dx, dout;
@@ -3032,6 +3085,12 @@ extern "C" int l98_session_start(const LZModel *mm, LZRunState *s, const int *pr
     h.tok[0] = anchor;
     if (ctl_put(d, h) || hipStreamSynchronize(d->st)) return -LZ_ERR_FORWARD;
     return anchor;
+}
+
+extern "C" int l98_session_sampler(const LZRunState *s, LZSampler *out) {
+    if (!s || !s->impl || !out) return 1;
+    *out = S(const_cast<LZRunState *>(s))->session_samp;
+    return 0;
 }
 
 // Rounds that stay inside the state whatever they accept: a round's verify
@@ -3289,6 +3348,79 @@ extern "C" int l98_greedy_rounds_batch(const LZModel *mm, LZRunState **states, i
     return total;
 }
 
+// n temperature rounds on the device, one HIP graph launch each (captured
+// per k, and again when T or top-p change), with the generator state in
+// device memory from *rng and back into it.  Returns the tokens emitted
+// (their ids in tokens[0 .. cap)), or -LZErr; k_eff / n_accept per round.
+static int temp_rounds_dev(const LZModel *mm, LZRunState *s, int k, int n_rounds, float temp, float topp,
+                           lz_u64 *rng, int *tokens, int cap, int *k_eff_out, int *n_accept_out) {
+    DState *d = S(s);
+    if (n_rounds < 1 || n_rounds > d->hist_cap || Mo(mm)->n_draft > 1) return -LZ_ERR_NULL_ARG;
+    const int max_pos = d->seq_len - 1;
+    if (!smp_ensure(d)) return -LZ_ERR_FORWARD;
+    {
+        DevCtl h;
+        if (ctl_get(d, &h)) return -LZ_ERR_FORWARD;
+        if (n_rounds > rounds_that_fit(d, h, k)) return -LZ_ERR_FORWARD;
+        h.round = 0;
+        h.expert_tally = 0;
+        h.k_eff = k;
+        if (ctl_put(d, h)) return -LZ_ERR_FORWARD;
+    }
+    if (d->temp_graph[k] && (d->temp_graph_t[k] != temp || d->temp_graph_p[k] != topp)) {
+        (void)hipGraphExecDestroy(d->temp_graph[k]);
+        d->temp_graph[k] = nullptr;
+    }
+    if (!d->temp_graph[k]) {
+        hipGraph_t g = nullptr;
+        if (hipStreamBeginCapture(d->st, hipStreamCaptureModeThreadLocal) != hipSuccess) return -LZ_ERR_FORWARD;
+        int rc = enqueue_temp_round(d, k, max_pos, temp, topp);
+        if (hipStreamEndCapture(d->st, &g) != hipSuccess || rc) return -LZ_ERR_FORWARD;
+        if (hipGraphInstantiate(&d->temp_graph[k], g, nullptr, nullptr, 0) != hipSuccess) {
+            (void)hipGraphDestroy(g);
+            return -LZ_ERR_FORWARD;
+        }
+        (void)hipGraphDestroy(g);
+        d->temp_graph_t[k] = temp;
+        d->temp_graph_p[k] = topp;
+    }
+    if (hipMemcpyAsync(d->smp_rng, rng, sizeof(lz_u64), hipMemcpyHostToDevice, d->st) != hipSuccess)
+        return -LZ_ERR_FORWARD;
+    (void)hipEventRecord(d->ev0, d->st);
+    for (int r = 0; r < n_rounds; r++)
+        if (hipGraphLaunch(d->temp_graph[k], d->st) != hipSuccess) return -LZ_ERR_FORWARD;
+    (void)hipEventRecord(d->ev1, d->st);
+    if (hipMemcpyAsync(rng, d->smp_rng, sizeof(lz_u64), hipMemcpyDeviceToHost, d->st) != hipSuccess ||
+        hipStreamSynchronize(d->st) != hipSuccess)
+        return -LZ_ERR_FORWARD;
+    float ms = 0.0f;
+    (void)hipEventElapsedTime(&ms, d->ev0, d->ev1);
+    g_last_loop_s = ms * 1e-3;
+    std::vector<RoundRec> rec((size_t)n_rounds);
+    if (hipMemcpy(rec.data(), d->hist, sizeof(RoundRec) * rec.size(), hipMemcpyDeviceToHost) != hipSuccess)
+        return -LZ_ERR_FORWARD;
+    int n = 0;
+    for (int r = 0; r < n_rounds; r++) {
+        if (rec[r].n_accept < rec[r].k_eff) lz_debug_n_ring_rollback++;
+        if (rec[r].n_accept > 1) lz_debug_n_catchup++;
+        lz_debug_n_chunks++;
+        lz_debug_n_lmhead++;
+        if (k_eff_out) k_eff_out[r] = rec[r].k_eff;
+        if (n_accept_out) n_accept_out[r] = rec[r].n_accept;
+        for (int j = 0; j <= rec[r].n_accept; j++) {
+            if (tokens && n < cap) tokens[n] = rec[r].out[j];
+            n++;
+        }
+    }
+    DevCtl h;
+    if (ctl_get(d, &h)) return -LZ_ERR_FORWARD;
+    s->ssm_slot = h.slot_base;
+    s->mtp_pos = h.mtp_pos;
+    if (hipMemcpy(s->mtp_chain, d->chain, sizeof(float) * d->m->c.hidden_size, hipMemcpyDeviceToHost) != hipSuccess)
+        return -LZ_ERR_FORWARD;
+    return n;
+}
+
 extern "C" int l98_generate(const LZModel *mm, LZRunState *s, const int *prompt, int n_prompt, int k,
                             int n_new, LZSampler *samp, int *tokens, int cap, int *k_eff_out,
                             int *n_accept_out, int *n_rounds) {
@@ -3302,6 +3434,37 @@ extern "C" int l98_generate(const LZModel *mm, LZRunState *s, const int *prompt,
     int n = 0, rounds = 0;
     if (n < cap) tokens[n] = anchor;
     n++;
+    if (!d->session_greedy && Mo(mm)->n_draft <= 1) {
+        // temperature rounds on the device, in batches that cannot pass
+        // n_new (as the greedy loop below); the generator state comes back
+        // after each batch
+        LZSampler &local = d->session_samp;
+        std::vector<int> ke((size_t)n_new + 8), nac((size_t)n_new + 8);
+        while (n < n_new) {
+            int batch = (n_new - n) / (k + 1);
+            if (batch < 1) batch = 1;
+            if (batch > 64) batch = 64;
+            DevCtl h;
+            if (ctl_get(d, &h)) return -LZ_ERR_FORWARD;
+            const int fit = rounds_that_fit(d, h, k);
+            if (fit < 1) return -LZ_ERR_FORWARD;
+            if (batch > fit) batch = fit;
+            std::vector<int> tk((size_t)batch * (k + 1));
+            int got = temp_rounds_dev(mm, s, k, batch, local.p.temperature, local.p.topp, &local.rng_state, tk.data(),
+                                      (int)tk.size(), ke.data(), nac.data());
+            if (got < 0) return got;
+            int pos = 0;
+            for (int r = 0; r < batch; r++) {
+                if (k_eff_out) k_eff_out[rounds] = ke[r];
+                if (n_accept_out) n_accept_out[rounds] = nac[r];
+                rounds++;
+                for (int i = 0; i <= nac[r]; i++, pos++) { if (n < cap) tokens[n] = tk[pos]; n++; }
+            }
+        }
+        if (n_rounds) *n_rounds = rounds;
+        if (samp) samp->rng_state = local.rng_state;
+        return n;
+    }
     if (!d->session_greedy) {
         LZSampler &local = d->session_samp;
         int anchor_pos = n_prompt - 1;

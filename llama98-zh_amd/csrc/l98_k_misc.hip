@@ -270,16 +270,23 @@ __global__ __launch_bounds__(256) void k_argmax_part(const unsigned long long *_
 // mtp_pos unchanged: src/generate.c:1117-1133).
 __global__ void k_accept(DevCtl *ctl, const float *__restrict__ vhidden, int d,
                          float *__restrict__ chain, int depth, int flags) {
-    const bool brk = (flags & 1) != 0, dspark = (flags & 2) != 0;
+    // flags: 1 the rollback break, 2 a DSpark round (no catch-up), 4 a
+    // temperature round (n_accept and out[] already written by its
+    // acceptance launches)
+    const bool brk = (flags & 1) != 0, dspark = (flags & 2) != 0, sampled = (flags & 4) != 0;
     __shared__ int s_n;
     if (threadIdx.x == 0) {
         int k_eff = ctl->k_eff;
         int n = k_eff;
-        for (int i = 0; i < k_eff; i++) {
-            ctl->out[i] = ctl->targ[i];
-            if (ctl->tok[1 + i] != ctl->targ[i]) { n = i; break; }
+        if (sampled) {
+            n = ctl->n_accept;
+        } else {
+            for (int i = 0; i < k_eff; i++) {
+                ctl->out[i] = ctl->targ[i];
+                if (ctl->tok[1 + i] != ctl->targ[i]) { n = i; break; }
+            }
+            if (n == k_eff) ctl->out[k_eff] = ctl->targ[k_eff];
         }
-        if (n == k_eff) ctl->out[k_eff] = ctl->targ[k_eff];
         ctl->n_accept = n;
         int base = ctl->slot_base;
         int slot = (base + k_eff + 1) % depth;           // what the verify left
@@ -305,11 +312,15 @@ __global__ void k_accept(DevCtl *ctl, const float *__restrict__ vhidden, int d,
 // record the finished round in hist and advance to the next one as the
 // generation driver does with have_seed (src/generate.c:1850-1866,
 // 2096-2104): anchor = out[n_accept] at position new_pos, mtp_pos and the
-// ring slot carried over.
+// ring slot carried over.  op 2: a temperature round's acceptance starts
+// (n_accept = k_eff until a row rejects, no row decided).
 __global__ void k_set_tokens(DevCtl *ctl, int op, RoundRec *hist, int hist_cap) {
     if (threadIdx.x != 0) return;
     if (op == 0) {
         ctl->tok[0] = ctl->anchor;
+    } else if (op == 2) {
+        ctl->n_accept = ctl->k_eff;
+        ctl->smp_done = 0;
     } else if (op == 1) {
         if (hist && ctl->round < hist_cap) {
             RoundRec *r = hist + ctl->round;

@@ -15,10 +15,19 @@
 // prefix queries: after one walk over the special elements, every element's
 // exact prefix is s_after(its run's special) + (grid steps since) * ulp, so
 // "the first index whose prefix passes the coin" is a parallel minimum.
+// The top-p candidates are ordered by a stable descending LSD radix sort of
+// this file's own (three passes of 10-bit digits: a candidate key, the bits
+// of a probability in [0, 1], is below 2^30).
+//
+// The kernels a device-resident temperature round runs take `skip`, a
+// device flag (the round's "decided" word): when it is set the launch does
+// nothing, so the acceptance rows after the first rejection consume no
+// random numbers, as the reference's loop stops there.
 #include <cstring>
-#include <rocprim/device/device_radix_sort.hpp>
 
 #include "l98_devmath.h"
+
+__device__ __forceinline__ uint32_t umin_u32(uint32_t a, uint32_t b) { return a < b ? a : b; }
 
 #define SMP_THREADS 1024
 #define SMP_WAVES (SMP_THREADS / 64)
@@ -366,10 +375,11 @@ __device__ __forceinline__ int blk_argmax(const float *x, int n, SmpLds &L) {
 // the descending sort, and their count.
 __global__ __launch_bounds__(SMP_THREADS) void k_smp_softmax(const float *__restrict__ logits, int n, float inv_t,
                                                              float *__restrict__ probs, float cutoff,
-                                                             uint32_t *__restrict__ keys, int *__restrict__ vals,
-                                                             int *__restrict__ n_cand) {
+                                                             uint32_t *__restrict__ keys,
+                                                             int *__restrict__ n_cand, const int *__restrict__ skip) {
     __shared__ SmpLds L;
     __shared__ float tab[32];
+    if (skip && *skip) return;
     const int tid = threadIdx.x;
     if (tid < 32) tab[tid] = c_exp_tab[tid];
     uint32_t mk = 0u;
@@ -390,9 +400,9 @@ __global__ __launch_bounds__(SMP_THREADS) void k_smp_softmax(const float *__rest
         const float p = probs[i] * inv;
         probs[i] = p;
         if (keys) {
+            // a probability is at most 1 (e <= sum), so a key is below 2^30
             const bool c = p >= cutoff;
-            keys[i] = c ? __float_as_uint(p) : 0u;
-            vals[i] = i;
+            keys[i] = c ? umin_u32(__float_as_uint(p), 0x3F800000u) : 0u;
             cnt += c ? 1u : 0u;
         }
     }
@@ -408,8 +418,10 @@ __global__ __launch_bounds__(SMP_THREADS) void k_smp_softmax(const float *__rest
 // to *out_tok (and to *ctl_tok when given) and p[index] to *out_p.
 __global__ __launch_bounds__(SMP_THREADS) void k_smp_draw(const float *__restrict__ p, int n,
                                                           unsigned long long *__restrict__ rng, int *__restrict__ out_tok,
-                                                          float *__restrict__ out_p, int *__restrict__ ctl_tok) {
+                                                          float *__restrict__ out_p, int *__restrict__ ctl_tok,
+                                                          const int *__restrict__ skip) {
     __shared__ SmpLds L;
+    if (skip && *skip) return;
     if (threadIdx.x == 0) L.fv = d_random_f32(rng);
     __syncthreads();
     xprefix(GetArr{p, n}, n, XP_FIRST_GT, L.fv, L);
@@ -430,8 +442,9 @@ __global__ __launch_bounds__(SMP_THREADS) void k_smp_topp_dist(const float *__re
                                                                const uint32_t *__restrict__ skeys,
                                                                const int *__restrict__ svals,
                                                                const int *__restrict__ n_cand, float topp,
-                                                               float *__restrict__ p_out) {
+                                                               float *__restrict__ p_out, const int *__restrict__ skip) {
     __shared__ SmpLds L;
+    if (skip && *skip) return;
     const int tid = threadIdx.x, nc = *n_cand;
     for (int i = tid; i < n; i += SMP_THREADS) p_out[i] = 0.0f;
     if (nc <= 0) {
@@ -451,12 +464,23 @@ __global__ __launch_bounds__(SMP_THREADS) void k_smp_topp_dist(const float *__re
 // p[x]/q[x]); otherwise the residual draw over max(p - q, 0) (argmax of p
 // when its mass is 0; the last positive index when no cdf passes the coin).
 // out[0] = token, out[1] = accepted.
+// In a device-resident round (done != null): the draft token is read from
+// x_dev, the emitted token goes to *ctl_out, and a rejection sets
+// *ctl_n = row and *done.
 __global__ __launch_bounds__(SMP_THREADS) void k_smp_accept(const float *__restrict__ p, const float *__restrict__ q,
-                                                            int n, int x, float u_in, int have_u,
-                                                            unsigned long long *__restrict__ rng,
-                                                            int *__restrict__ out) {
+                                                            int n, int x_in, const int *__restrict__ x_dev, float u_in,
+                                                            int have_u, unsigned long long *__restrict__ rng,
+                                                            int *__restrict__ out, int *__restrict__ ctl_out,
+                                                            int *__restrict__ ctl_n, int *__restrict__ done, int row) {
     __shared__ SmpLds L;
+    if (done && *done) return;
     const int tid = threadIdx.x;
+    const int x = x_dev ? *x_dev : x_in;
+    auto emit = [&](int tok, int acc) {
+        if (out) { out[0] = tok; out[1] = acc; }
+        if (ctl_out) *ctl_out = tok;
+        if (done && !acc) { *ctl_n = row; *done = 1; }
+    };
     if (tid == 0) {
         const float qx = q[x];
         float ratio;
@@ -467,14 +491,14 @@ __global__ __launch_bounds__(SMP_THREADS) void k_smp_accept(const float *__restr
     }
     __syncthreads();
     if (L.iv) {
-        if (tid == 0) { out[0] = x; out[1] = 1; }
+        if (tid == 0) emit(x, 1);
         return;
     }
     xprefix(GetResid{p, q, n}, n, XP_TOTAL, 0.0f, L);
     const float total = L.fres;
     if (total <= 0.0f) {
         const int a = blk_argmax(p, n, L);
-        if (tid == 0) { out[0] = a; out[1] = 0; }
+        if (tid == 0) emit(a, 0);
         return;
     }
     int lp = -1;
@@ -483,7 +507,7 @@ __global__ __launch_bounds__(SMP_THREADS) void k_smp_accept(const float *__restr
     if (tid == 0) L.fv = d_random_f32(rng) * total;
     __syncthreads();
     xprefix(GetResid{p, q, n}, n, XP_FIRST_GT, L.fv, L);
-    if (tid == 0) { out[0] = L.result >= 0 ? L.result : last_pos; out[1] = 0; }
+    if (tid == 0) emit(L.result >= 0 ? L.result : last_pos, 0);
 }
 
 // lz_sample_ex with top-p after the candidate sort: r = coin * kept mass,
@@ -525,6 +549,142 @@ __global__ __launch_bounds__(SMP_THREADS) void k_smp_xprefix(const float *__rest
     if (threadIdx.x == 0) { out[r] = L.result; outv[r] = L.fres; }
 }
 
+// ------------------------------------------------------ radix sort ---
+//
+// Stable descending sort of (key, index) pairs, keys below 2^30: three LSD
+// passes of 10-bit digits over tiles of RS_TILE elements (one per thread,
+// so a tile's elements are in index order across waves and lanes).  A pass
+// is (1) k_rs_count: each tile's digit counts -> hist[digit][tile]; (2)
+// k_rs_scan: the exclusive prefix of hist in (digit, tile) order, by one
+// block; (3) k_rs_scatter: each element to hist[digit][tile] + the count of
+// equal digits before it in its tile (lanes of the same digit found with 10
+// ballots, then the waves before it).  Digits are taken as 1023 - digit, so
+// the order is descending; every pass keeps the order of equal digits, so
+// equal keys keep index order.
+#define RS_TILE 1024
+#define RS_BITS 10
+#define RS_DIG (1 << RS_BITS)
+#define RS_PASSES 3
+
+__device__ __forceinline__ int rs_digit(uint32_t key, int shift) {
+    return (RS_DIG - 1) - (int)((key >> shift) & (RS_DIG - 1));
+}
+
+__global__ __launch_bounds__(RS_TILE) void k_rs_count(const uint32_t *__restrict__ keys, int n, int shift,
+                                                      int *__restrict__ hist, int ntiles,
+                                                      const int *__restrict__ skip) {
+    __shared__ int cnt[RS_DIG];
+    if (skip && *skip) return;
+    const int tid = threadIdx.x, i = blockIdx.x * RS_TILE + tid;
+    cnt[tid] = 0;
+    __syncthreads();
+    if (i < n) atomicAdd(&cnt[rs_digit(keys[i], shift)], 1);
+    __syncthreads();
+    hist[(size_t)tid * ntiles + blockIdx.x] = cnt[tid];
+}
+
+// Exclusive prefix, in place, of the RS_DIG x ntiles counts in (digit,
+// tile) order: thread t takes digit t's row of ntiles counts (its loads
+// eight 16-byte vectors at a time when ntiles % 4 == 0).
+__global__ __launch_bounds__(RS_TILE) void k_rs_scan(int *__restrict__ hist, int ntiles, const int *__restrict__ skip) {
+    __shared__ int wsum[RS_TILE / 64];
+    if (skip && *skip) return;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    int *row = hist + (size_t)tid * ntiles;
+    int sum = 0;
+    if ((ntiles & 3) == 0) {
+        const int4 *r4 = reinterpret_cast<const int4 *>(row);
+        const int n4 = ntiles >> 2;
+        for (int i0 = 0; i0 < n4; i0 += 8) {
+            int4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v[u] = r4[imin(i0 + u, n4 - 1)];
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (i0 + u < n4) sum += v[u].x + v[u].y + v[u].z + v[u].w;
+        }
+    } else {
+        for (int i = 0; i < ntiles; i++) sum += row[i];
+    }
+    const int incl = (int)wave_scan_u32((uint32_t)sum);
+    if (lane == 63) wsum[w] = incl;
+    __syncthreads();
+    if (w == 0) {
+        int v = lane < RS_TILE / 64 ? wsum[lane] : 0;
+        v = (int)wave_scan_u32((uint32_t)v);
+        if (lane < RS_TILE / 64) wsum[lane] = v;
+    }
+    __syncthreads();
+    int run = (w ? wsum[w - 1] : 0) + incl - sum;
+    if ((ntiles & 3) == 0) {
+        int4 *r4 = reinterpret_cast<int4 *>(row);
+        const int n4 = ntiles >> 2;
+        for (int i0 = 0; i0 < n4; i0 += 8) {
+            int4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v[u] = r4[imin(i0 + u, n4 - 1)];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                if (i0 + u < n4) {
+                    int4 o;
+                    o.x = run; run += v[u].x;
+                    o.y = run; run += v[u].y;
+                    o.z = run; run += v[u].z;
+                    o.w = run; run += v[u].w;
+                    r4[i0 + u] = o;
+                }
+            }
+        }
+    } else {
+        for (int i = 0; i < ntiles; i++) {
+            const int c = row[i];
+            row[i] = run;
+            run += c;
+        }
+    }
+}
+
+__global__ __launch_bounds__(RS_TILE) void k_rs_scatter(const uint32_t *__restrict__ keys, const int *__restrict__ vals,
+                                                        uint32_t *__restrict__ keys_out, int *__restrict__ vals_out,
+                                                        int n, int shift, const int *__restrict__ hist, int ntiles,
+                                                        const int *__restrict__ skip) {
+    __shared__ unsigned short wcnt[RS_TILE / 64][RS_DIG];   // per wave: elements of each digit
+    if (skip && *skip) return;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, i = blockIdx.x * RS_TILE + tid;
+    const bool valid = i < n;
+    const uint32_t key = valid ? keys[i] : 0u;
+    const int val = valid ? (vals ? vals[i] : i) : 0;
+    const int dg = rs_digit(key, shift);
+    for (int j = tid; j < (RS_TILE / 64) * RS_DIG; j += RS_TILE) (&wcnt[0][0])[j] = 0;
+    // the lanes of this wave holding the same digit
+    unsigned long long peers = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < RS_BITS; b++) {
+        const unsigned long long bb = __ballot((dg >> b) & 1);
+        peers &= ((dg >> b) & 1) ? bb : ~bb;
+    }
+    const int rank = __popcll(peers & ((1ull << lane) - 1ull));
+    __syncthreads();
+    if (valid && rank == 0) wcnt[w][dg] = (unsigned short)__popcll(peers);
+    __syncthreads();
+    // thread t: digit t's running count over the waves, exclusive
+    {
+        int run = 0;
+#pragma unroll
+        for (int ww = 0; ww < RS_TILE / 64; ww++) {
+            const int c = wcnt[ww][tid];
+            wcnt[ww][tid] = (unsigned short)run;
+            run += c;
+        }
+    }
+    __syncthreads();
+    if (valid) {
+        const int pos = hist[(size_t)dg * ntiles + blockIdx.x] + wcnt[w][dg] + rank;
+        keys_out[pos] = key;
+        vals_out[pos] = val;
+    }
+}
+
 // ---------------------------------------------------------- host glue ---
 
 extern "C" int l98k_upload_exp_table_smp(const float *tab) {
@@ -532,38 +692,71 @@ extern "C" int l98k_upload_exp_table_smp(const float *tab) {
 }
 
 extern "C" int l98k_smp_softmax(const float *logits, int n, float inv_t, float *probs, float cutoff, uint32_t *keys,
-                                int *vals, int *n_cand, hipStream_t st) {
+                                int *n_cand, const int *skip, hipStream_t st) {
     if (n < 1) return -1;
-    hipLaunchKernelGGL(k_smp_softmax, dim3(1), dim3(SMP_THREADS), 0, st, logits, n, inv_t, probs, cutoff, keys, vals,
-                       n_cand);
+    hipLaunchKernelGGL(k_smp_softmax, dim3(1), dim3(SMP_THREADS), 0, st, logits, n, inv_t, probs, cutoff, keys, n_cand,
+                       skip);
     return (int)hipGetLastError();
 }
 
 extern "C" int l98k_smp_draw(const float *p, int n, unsigned long long *rng, int *out_tok, float *out_p, int *ctl_tok,
-                             hipStream_t st) {
+                             const int *skip, hipStream_t st) {
     if (n < 1) return -1;
-    hipLaunchKernelGGL(k_smp_draw, dim3(1), dim3(SMP_THREADS), 0, st, p, n, rng, out_tok, out_p, ctl_tok);
+    hipLaunchKernelGGL(k_smp_draw, dim3(1), dim3(SMP_THREADS), 0, st, p, n, rng, out_tok, out_p, ctl_tok, skip);
     return (int)hipGetLastError();
 }
 
-// Stable descending sort of (key, index) pairs; tmp == nullptr queries the
-// scratch size into *tmp_bytes.
-extern "C" int l98k_smp_sort_desc(const uint32_t *keys, uint32_t *keys_out, const int *vals, int *vals_out, int n,
-                                  void *tmp, size_t *tmp_bytes, hipStream_t st) {
-    return (int)rocprim::radix_sort_pairs_desc(tmp, *tmp_bytes, keys, keys_out, vals, vals_out, (unsigned)n, 0, 32, st);
+extern "C" size_t l98k_smp_sort_tmp_bytes(int n) {
+    const size_t ntiles = ((size_t)n + RS_TILE - 1) / RS_TILE;
+    return sizeof(int) * RS_DIG * ntiles + 2 * sizeof(int) * (size_t)n;
+}
+
+// Stable descending sort of n keys (below 2^30) with their indices 0..n-1:
+// keys_out, vals_out.  keys is overwritten (a pass's buffer); tmp holds
+// l98k_smp_sort_tmp_bytes(n) bytes.
+extern "C" int l98k_smp_sort_desc(uint32_t *keys, uint32_t *keys_out, int *vals_out, int n, void *tmp,
+                                  const int *skip, hipStream_t st) {
+    if (n < 1 || n > RS_DIG * RS_TILE || !tmp) return -1;
+    const int ntiles = (n + RS_TILE - 1) / RS_TILE;
+    int *hist = reinterpret_cast<int *>(tmp);
+    int *vtmp = hist + (size_t)RS_DIG * ntiles;
+    // pass 0: keys -> keys_out (indices implicit) -> vals_out; pass 1:
+    // keys_out -> keys, vals_out -> vtmp; pass 2: keys -> keys_out, vtmp ->
+    // vals_out
+    const uint32_t *kin[RS_PASSES] = {keys, keys_out, keys};
+    uint32_t *kout[RS_PASSES] = {keys_out, keys, keys_out};
+    const int *vin[RS_PASSES] = {nullptr, vals_out, vtmp};
+    int *vout[RS_PASSES] = {vals_out, vtmp, vals_out};
+    for (int pass = 0; pass < RS_PASSES; pass++) {
+        const int shift = pass * RS_BITS;
+        hipLaunchKernelGGL(k_rs_count, dim3(ntiles), dim3(RS_TILE), 0, st, kin[pass], n, shift, hist, ntiles, skip);
+        hipLaunchKernelGGL(k_rs_scan, dim3(1), dim3(RS_TILE), 0, st, hist, ntiles, skip);
+        hipLaunchKernelGGL(k_rs_scatter, dim3(ntiles), dim3(RS_TILE), 0, st, kin[pass], vin[pass], kout[pass],
+                           vout[pass], n, shift, hist, ntiles, skip);
+    }
+    return (int)hipGetLastError();
 }
 
 extern "C" int l98k_smp_topp_dist(const float *probs, int n, const uint32_t *skeys, const int *svals,
-                                  const int *n_cand, float topp, float *p_out, hipStream_t st) {
+                                  const int *n_cand, float topp, float *p_out, const int *skip, hipStream_t st) {
     hipLaunchKernelGGL(k_smp_topp_dist, dim3(1), dim3(SMP_THREADS), 0, st, probs, n, skeys, svals, n_cand, topp,
-                       p_out);
+                       p_out, skip);
     return (int)hipGetLastError();
 }
 
 extern "C" int l98k_smp_accept(const float *p, const float *q, int n, int x, const float *u, unsigned long long *rng,
                                int *out, hipStream_t st) {
     if (n < 1 || x < 0 || x >= n) return -1;
-    hipLaunchKernelGGL(k_smp_accept, dim3(1), dim3(SMP_THREADS), 0, st, p, q, n, x, u ? *u : 0.0f, u ? 1 : 0, rng, out);
+    hipLaunchKernelGGL(k_smp_accept, dim3(1), dim3(SMP_THREADS), 0, st, p, q, n, x, nullptr, u ? *u : 0.0f, u ? 1 : 0,
+                       rng, out, nullptr, nullptr, nullptr, 0);
+    return (int)hipGetLastError();
+}
+
+extern "C" int l98k_smp_accept_row(const float *p, const float *q, int n, const int *x_dev, unsigned long long *rng,
+                                   int *ctl_out, int *ctl_n, int *done, int row, hipStream_t st) {
+    if (n < 1 || !x_dev || !ctl_out || !ctl_n || !done) return -1;
+    hipLaunchKernelGGL(k_smp_accept, dim3(1), dim3(SMP_THREADS), 0, st, p, q, n, 0, x_dev, 0.0f, 0, rng, nullptr,
+                       ctl_out, ctl_n, done, row);
     return (int)hipGetLastError();
 }
 

@@ -41,23 +41,34 @@ int l98k_wide_pro(int mode, const float *src, const float *src2, int src_stride,
 int l98k_wide_pro_f(int mode, const float *src, const float *src2, int src_stride, const int *sel_idx,
                     const float *sel_w, int topk, int n, int rows, float *fout, hipStream_t st);
 // Temperature sampling (one block per call; l98_k_sample.hip).
-// probs = softmax(logits * inv_t); with keys: the top-p candidate keys and
-// indices for l98k_smp_sort_desc and their count.
-int l98k_smp_softmax(const float *logits, int n, float inv_t, float *probs, float cutoff, uint32_t *keys, int *vals,
-                     int *n_cand, hipStream_t st);
+// The launches that take `skip` (a device flag) do nothing when it is set
+// (null: never).
+// probs = softmax(logits * inv_t); with keys: the top-p candidate keys for
+// l98k_smp_sort_desc and their count.
+int l98k_smp_softmax(const float *logits, int n, float inv_t, float *probs, float cutoff, uint32_t *keys,
+                     int *n_cand, const int *skip, hipStream_t st);
 // A draw from p by the cdf (rng advanced on the device); ctl_tok optional.
 int l98k_smp_draw(const float *p, int n, unsigned long long *rng, int *out_tok, float *out_p, int *ctl_tok,
-                  hipStream_t st);
-// Stable descending (key, index) sort; tmp == nullptr sizes the scratch.
-int l98k_smp_sort_desc(const uint32_t *keys, uint32_t *keys_out, const int *vals, int *vals_out, int n, void *tmp,
-                       size_t *tmp_bytes, hipStream_t st);
+                  const int *skip, hipStream_t st);
+// Scratch bytes of l98k_smp_sort_desc for n keys.
+size_t l98k_smp_sort_tmp_bytes(int n);
+// Stable descending sort of n keys (below 2^30) with their indices: a
+// radix sort of this library's own, three passes of three launches; keys
+// is overwritten.
+int l98k_smp_sort_desc(uint32_t *keys, uint32_t *keys_out, int *vals_out, int n, void *tmp, const int *skip,
+                       hipStream_t st);
 // Top-p target distribution from the softmax and the sorted candidates.
 int l98k_smp_topp_dist(const float *probs, int n, const uint32_t *skeys, const int *svals, const int *n_cand,
-                       float topp, float *p_out, hipStream_t st);
+                       float topp, float *p_out, const int *skip, hipStream_t st);
 // Speculative acceptance of draft x with residual resampling (u given, or
 // drawn when u is null): out[0] token, out[1] accepted.
 int l98k_smp_accept(const float *p, const float *q, int n, int x, const float *u, unsigned long long *rng, int *out,
                     hipStream_t st);
+// The same for row `row` of a device-resident round: the draft token from
+// x_dev, the emitted token to *ctl_out; a rejection sets *ctl_n = row and
+// *done (nothing runs once *done is set).
+int l98k_smp_accept_row(const float *p, const float *q, int n, const int *x_dev, unsigned long long *rng,
+                        int *ctl_out, int *ctl_n, int *done, int row, hipStream_t st);
 // lz_sample_ex's top-p draw after the candidate sort.
 int l98k_smp_sample_topp(const float *probs, int n, const uint32_t *skeys, const int *svals, const int *n_cand,
                          float topp, unsigned long long *rng, int *out_tok, hipStream_t st);
