@@ -355,6 +355,33 @@ __device__ __forceinline__ void tile_dot(const int4 (&wv)[GEMV_MAXJ], const int8
     const bool reuse = m64 == 0;
     int r = c0 / cpr, p = c0 - r * cpr;
     int4 xv[M];
+    if (reuse && (cmax & (GEMV_WAVE_BYTES / 16 - 1)) == 0) {
+        // every lane's chunks share one in-row offset and this wave's 8 KiB
+        // quarter is all live (or all past the tile's rows): straight-line
+        // code, the token rows' dot products interleaved
+        if (wave * (GEMV_WAVE_BYTES / 16) >= cmax) return;
+#pragma unroll
+        for (int t = 0; t < M; t++) xv[t] = sx4[t * cpr + p];
+#pragma unroll
+        for (int j = 0; j < GEMV_MAXJ; j++) {
+            int a[M];
+#pragma unroll
+            for (int t = 0; t < M; t++) a[t] = __builtin_amdgcn_sdot4(wv[j].x, xv[t].x, 0, false);
+#pragma unroll
+            for (int t = 0; t < M; t++) a[t] = __builtin_amdgcn_sdot4(wv[j].y, xv[t].y, a[t], false);
+#pragma unroll
+            for (int t = 0; t < M; t++) a[t] = __builtin_amdgcn_sdot4(wv[j].z, xv[t].z, a[t], false);
+#pragma unroll
+            for (int t = 0; t < M; t++) a[t] = __builtin_amdgcn_sdot4(wv[j].w, xv[t].w, a[t], false);
+            int *dst = part + (r + j * q64) * M * pstride + (p >> 1);
+#pragma unroll
+            for (int t = 0; t < M; t++) {
+                a[t] += __builtin_amdgcn_update_dpp(0, a[t], 0xB1, 0xF, 0xF, false);     // lane ^ 1
+                dst[t * pstride] = a[t];
+            }
+        }
+        return;
+    }
     if (reuse) {
 #pragma unroll
         for (int t = 0; t < M; t++) xv[t] = sx4[t * cpr + p];
