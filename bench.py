@@ -107,18 +107,76 @@ def norm_gemv_shapes(cfg, M):
             ("moe input", 6, cfg.n_layers, b(moe_rows, 1))]
 
 
+def kda_step_bytes(cfg, M):
+    """Algorithmic bytes of one KDA layer's token step over M verify rows
+    (k_kda_step): the fp32 state read from its ring slot and written to the
+    M slots after it, the conv history read and written per row, the taps,
+    the f_b gate projection, A_log / dt_bias / output norm, the projected q,
+    k, v, gate-input, f_a and b rows read, and the quantized output rows."""
+    nv, kd, vd, K = cfg.lin_n_v_heads, cfg.lin_k_head_dim, cfg.lin_v_head_dim, cfg.conv_kernel
+    key, value, conv, rank = cfg.lin_key_dim, cfg.lin_value_dim, cfg.lin_conv_dim, cfg.kda_gate_rank
+    state = 4 * nv * kd * vd
+    hist = 4 * conv * (K - 1)
+    return (state * (1 + M) + hist * (1 + M) + 4 * conv * K + (nv * kd * rank + 4 * nv * kd)
+            + 4 * nv + 4 * nv * kd + 4 * vd
+            + 4 * M * (2 * key + 2 * value + rank + nv) + M * value + 4 * M * value // 32)
+
+
+def moe_bytes(cfg, M, experts):
+    """Algorithmic bytes of the routed experts of one MoE layer over M verify
+    rows with `experts` distinct experts: k_moe_up (routing from the router
+    logits, w1 and w3 of each distinct expert, the latent rows in, the
+    (token, slot) pairs' h1 / h3 out) and k_expert_gemv (w2 of each distinct
+    expert, h1 / h3 in, the pairs' latent rows out)."""
+    lat, inter, E, topk = cfg.moe_latent_dim, cfg.moe_intermediate_size, cfg.num_experts, cfg.num_experts_per_token
+    pairs = M * topk
+    up = experts * 2 * inter * (lat + 4) + 4 * M * E + 4 * E + 4 * M * lat + 2 * 4 * pairs * inter
+    down = experts * lat * (inter + 4) + 2 * 4 * pairs * inter + 4 * pairs * lat
+    return up, down
+
+
+def sources_sha(paths):
+    """sha256 of the named source files' bytes, in order (ties a committed
+    counter summary to the kernel code it measured)."""
+    import hashlib
+    h = hashlib.sha256()
+    for p in paths:
+        with open(os.path.join(ROOT, p), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()
+
+
+# the kernel sources the traffic summary's figures depend on
+TRAFFIC_SOURCES = ["llama98-zh_amd/csrc/l98_gemv.h", "llama98-zh_amd/csrc/l98_k_gemv.hip",
+                   "llama98-zh_amd/csrc/l98_devmath.h", "llama98-zh_amd/csrc/l98_k_kda.hip",
+                   "llama98-zh_amd/csrc/l98_k_moe.hip"]
+TRAFFIC_PROFILE = os.path.join("profiles", "traffic_configs1_m4.md")
+
+
 def measured_traffic(config, k):
     """HBM bytes per round of the RMSNorm-prologue GEMV launches (and per
     lm_head launch) from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
     summary (copy-calibrated), for the configs[1], k = 3 workload it was
     measured on; None otherwise."""
-    path = os.path.join(ROOT, "profiles", "norm_gemv_and_lm_head_traffic_configs1_m4.md")
+    path = os.path.join(ROOT, TRAFFIC_PROFILE)
     out = {}
     if config != 1 or k != 3 or not os.path.exists(path):
         return out
+    vals = {}
     for line in open(path):
-        if ":" in line and line.split(":")[0] in ("norm_gemv_traffic_bytes_per_round", "lm_head_traffic_bytes_per_launch"):
-            out[line.split(":")[0]] = int(line.split(":")[1])
+        if ":" in line and not line.startswith(("|", "#", " ")):
+            key, val = line.split(":", 1)
+            vals[key.strip()] = val.strip()
+    if vals.get("kernel_sources_sha256") != sources_sha(TRAFFIC_SOURCES):
+        out["traffic_source"] = f"{TRAFFIC_PROFILE} is stale (the kernel sources changed since it was measured)"
+        return out
+    out["traffic_source"] = f"{TRAFFIC_PROFILE} (kernel sources sha256 {vals['kernel_sources_sha256'][:16]})"
+    for key in ("norm_gemv_traffic_bytes_per_round", "lm_head_traffic_bytes_per_launch"):
+        if key in vals:
+            out[key] = int(vals[key])
+    for key in ("norm_gemv_rocprof_us_per_round", "norm_gemv_rocprof_frac"):
+        if key in vals:
+            out[key] = float(vals[key])
     return out
 
 
@@ -179,13 +237,15 @@ def cpu_baseline(model_dir, vocab, k, n_prompt):
 
 
 def bench_server(args, pkg):
-    """n_seq sessions of the server model with ragged contexts
-    (uniform in [256, 2048], seed 0), k = 3.  Times the batched verify of
-    k+1 tokens per session (all sessions in flight together, one stream
-    each) and the batched greedy rounds; prints one JSON line."""
+    """n_seq sessions of configs[3]'s model (128 experts top-8)
+    with the skewed router (unit-variance logits plus a per-expert bias
+    N(0, 0.5); synthetic config 23) and ragged contexts (uniform in
+    [256, 2048], seed 0), k = 3.  Times the batched verify of k+1 tokens
+    per session (all sessions in flight together, one stream each) and the
+    batched greedy rounds; prints one JSON line."""
     import numpy as np
-    mdir = os.path.join(args.model_dir, "server")
-    pkg.ensure_model(mdir, 4, seed=1234)
+    mdir = os.path.join(args.model_dir, "xlserver")
+    pkg.ensure_model(mdir, 23, seed=1234)
     eng = pkg.Engine(mdir)
     k, n_seq = args.k, args.sessions
     rng = np.random.default_rng(0)
@@ -214,7 +274,8 @@ def bench_server(args, pkg):
         "ms_per_step": round(step_ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "int8xint8->int32, fp32 epilogue/state",
         "data": "synthetic (seeded random-init weights, router N(0,1) logits + N(0,0.5) expert bias; random prompts)",
-        "config": {"workload": f"configs[4] server batch: {n_seq} sessions of the configs[0]-shape model, k={k}, "
+        "config": {"workload": f"configs[4] server batch: {n_seq} sessions of the configs[3] model (d=2048, L=32, "
+                               f"128 experts top-8, skewed router), k={k}, "
                                f"contexts {int(ctx.min())}-{int(ctx.max())}", "sessions": n_seq, "k": k},
         "rounds": {"rounds": nr, "wall_ms": round(r_ms, 3), "tokens": emitted,
                    "tok_s": round(emitted / (r_ms * 1e-3), 1)},
@@ -226,33 +287,40 @@ def bench_server(args, pkg):
 
 
 def bench_ksweep(args, pkg):
-    """the configs[0] model at temperature 0.8, top-p 0.95, a
+    """configs[1]'s model at temperature 0.8, top-p 0.95, a
     fixed sampler seed, draft widths k in {1, 2, 4, 7} (k = 7 through the
-    library's own generation loop: the reference caps k at 6); per k the
-    generation's tok/s and acceptance, and the verify forward of M = k+1
-    rows timed alone.  Prints one JSON line."""
+    library's own generation loop: the reference caps k at 6), after
+    configs[1]'s 512-token prompt; per k the generation's tok/s and
+    acceptance (prefill excluded), and the verify forward of M = k+1 rows
+    timed alone.  Prints one JSON line."""
     import numpy as np
-    mdir = os.path.join(args.model_dir, "tiny")
-    pkg.ensure_model(mdir, 0, seed=1234)
+    mdir = os.path.join(args.model_dir, "base")
+    pkg.ensure_model(mdir, 1, seed=1234)
     eng = pkg.Engine(mdir, spec_k_max=pkg.L98_SPEC_K_GPU)
-    prompt = pkg.prompt_tokens(0, 64, eng.V)
+    prompt = pkg.prompt_tokens(0, args.prompt, eng.V)
     rows = []
+    n_new = 256
     for k in (1, 2, 4, 7):
-        eng.generate(prompt, k, 16, 0.8, 0.95, 7)                 # warm
+        eng.generate(prompt, k, 16, 0.8, 0.95, 7)                 # warm: code load, the per-k graphs
         t0 = time.perf_counter()
-        toks, ke, na = eng.generate(prompt, k, 128, 0.8, 0.95, 7)
+        eng.session_start(prompt)
+        prefill = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        toks, ke, na = eng.generate(prompt, k, n_new, 0.8, 0.95, 7)
         wall = time.perf_counter() - t0
         ver_ms = eng.time_kernel(1, k + 1, 20)
         rows.append({"k": k, "M": k + 1, "tokens": int(len(toks)), "rounds": int(len(na)),
                      "alpha": round(float(np.clip(na, 0, None).sum()) / max(1, int(np.sum(ke))), 4),
-                     "tok_s": round(len(toks) / wall, 1), "verify_ms": round(ver_ms, 4)})
+                     "tok_s": round(len(toks) / (wall - prefill), 1), "wall_s_with_prefill": round(wall, 4),
+                     "prefill_s": round(prefill, 4), "verify_ms": round(ver_ms, 4)})
     out = {"metric": "temperature spec decode tok/s and verify ms per draft width (configs[2])",
-           "value": rows[-1]["tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": 128, "warmup": 16,
+           "value": rows[-1]["tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": n_new, "warmup": 16,
            "ms_per_step": rows[-1]["verify_ms"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
            "dtype": "int8xint8->int32, fp32 epilogue/state",
-           "data": "synthetic (seeded random-init weights; 64-token random prompt; sampler seed 7)",
-           "config": {"workload": "configs[2]: configs[0] model, T=0.8 top-p 0.95, k in {1,2,4,7}, "
-                                  "generation of 128 tokens per k (prefill included), verify timed alone"},
+           "data": f"synthetic (seeded random-init weights; {len(prompt)}-token random prompt; sampler seed 7)",
+           "config": {"workload": f"configs[2]: configs[1] model, T=0.8 top-p 0.95, k in {{1,2,4,7}}, "
+                                  f"generation of {n_new} tokens per k after a {len(prompt)}-token prompt "
+                                  f"(tok/s with the prefill, timed alone, taken out), verify timed alone"},
            "sweep": rows}
     print(json.dumps(out))
     eng.close()
@@ -422,7 +490,12 @@ def main():
                      "achieved": round(ng_bw / 1e9, 1), "peak": 8000.0, "unit": "GB/s",
                      "frac": round(ng_bw / HBM_PEAK, 4),
                      "traffic": traffic.get("norm_gemv_traffic_bytes_per_round"),
+                     "traffic_source": traffic.get("traffic_source"),
+                     "frac_rocprof": traffic.get("norm_gemv_rocprof_frac"),
                      "bytes_per_round": int(ng_bytes), "us_per_round": round(ng_s * 1e6, 1),
+                     "timing": "each launch shape's layers back to back, HIP events on the state's stream "
+                               "(l98_time_kernel modes 4-6); frac_rocprof: the same launches' rocprofv3 mean "
+                               "durations from the traffic summary",
                      "launches": ng_rows},
         "lm_head": {"kernel": f"k_gemv_q8<{M}, 0, pre-quantized> (tied lm_head, {V}x{d} int8)",
                     "bytes_per_launch": lm_bytes, "launch_ms": round(lm_ms, 5),

@@ -11,12 +11,20 @@ of (l98_time_kernel modes):
   2  a device copy of the lm_head's vocab x hidden int8 bytes, the
      calibration kernel (its FETCH_SIZE and WRITE_SIZE per dispatch stand
      for a known byte count).
-Meant to run under
+then 8 greedy rounds at k = 3 launched kernel by kernel (the verify's
+KDA steps and routed experts) and prints one "SHAPES {json}" line: the
+algorithmic bytes per launch of each kernel (bench.py's formulas), the
+rounds' mean distinct experts per layer, the hipEvent timings above and the
+sha256 of the kernel sources.  Meant to run under
 
     rocprofv3 --pmc FETCH_SIZE --output-format csv -d OUT -o pmc -- python3 llama98-zh_amd/profile_kernels.py
     rocprofv3 --pmc WRITE_SIZE --output-format csv -d OUT -o pmc -- python3 llama98-zh_amd/profile_kernels.py
 
-and summarized by llama98-zh_amd/pmcsum.py.
+and, for the rocprof durations,
+
+    rocprofv3 --kernel-trace --stats --output-format csv -d OUT -o tr -- python3 llama98-zh_amd/profile_kernels.py
+
+all three summarized by llama98-zh_amd/trafficsum.py.
 
 With --launch-floor it times the launch floor instead (l98_time_kernel
 modes 7-10: chains of 64 dependent launches of an empty kernel of 1 and 256
@@ -79,10 +87,38 @@ def main():
                   f"{kb * 1024 / (us * 1e-6) / 1e9:.1f} GB/s per block", flush=True)
         eng.close()
         return
+    import json
+    import numpy as np
+    import bench
+    cfg = eng.cfg
+    M = 4
+    timing = {}
     for which, name in ((0, "lm_head"), (4, "kda input"), (5, "attention input"), (6, "moe input"), (2, "copy")):
-        ms = eng.time_kernel(which, 4, args.iters)
-        print(f"mode {which} ({name}, M=4): {ms * 1e3:.2f} us/launch", flush=True)
-    print(f"copy bytes {eng.V * eng.d}", flush=True)
+        ms = eng.time_kernel(which, M, args.iters)
+        timing[name] = ms * 1e3
+        print(f"mode {which} ({name}, M={M}): {ms * 1e3:.3f} us/launch (hipEvent, back to back)", flush=True)
+    # greedy rounds at k = 3 launched kernel by kernel (the verify's KDA steps,
+    # routed experts, attention, o_proj and tail GEMVs), with the distinct
+    # experts each round's verify streamed
+    eng.session_start(pkg.prompt_tokens(0, 64, eng.V))
+    rounds = 8
+    _, _, _, experts, _ = eng.greedy_rounds(3, rounds, use_graph=False, detail=True)
+    mean_experts = float(np.mean(experts)) / cfg.n_layers
+    up, down = bench.moe_bytes(cfg, M, mean_experts)
+    V, d = cfg.vocab_size, cfg.hidden_size
+    shapes = {
+        "M": M, "rounds": rounds, "copy_bytes": V * d, "n_layers": cfg.n_layers,
+        "n_kda_layers": cfg.n_linear_layers,
+        "kda_instance": f"k_kda_step<{cfg.lin_k_head_dim}, {cfg.conv_kernel}, {M}>",
+        "norm_gemv": [{"launch": n, "mode": mo, "per_round": pr, "bytes": b}
+                      for n, mo, pr, b in bench.norm_gemv_shapes(cfg, M)],
+        "lm_head_bytes": V * d + 4 * V + M * d + 4 * M * d // 32 + 4 * M * V,
+        "kda_step_bytes": bench.kda_step_bytes(cfg, M),
+        "moe_up_bytes": up, "expert_gemv_bytes": down, "mean_distinct_experts_per_layer": mean_experts,
+        "hipevent_us": timing,
+        "kernel_sources_sha256": bench.sources_sha(bench.TRAFFIC_SOURCES),
+    }
+    print("SHAPES " + json.dumps(shapes), flush=True)
     eng.close()
 
 
