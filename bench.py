@@ -264,10 +264,14 @@ def bench_server(args, pkg):
     ms = [eng.verify_batch(states, toks, pos0, copy_out=False)[0] for _ in range(args.steps)]
     step_ms = float(np.mean(ms))
     value = n_seq * (k + 1) / (step_ms * 1e-3)
-    # batched greedy rounds (rounds continue from each session's prefill)
+    # batched greedy rounds (rounds continue from each session's prefill;
+    # each session's round is a HIP graph launch, so --no-graph leaves them out)
     nr = min(args.steps, 32)
-    r_ms, outs = eng.greedy_rounds_batch(states, k, nr)
-    emitted = sum(len(o) for o in outs)
+    rounds = None
+    if not args.no_graph:
+        r_ms, outs = eng.greedy_rounds_batch(states, k, nr)
+        emitted = sum(len(o) for o in outs)
+        rounds = {"rounds": nr, "wall_ms": round(r_ms, 3), "tokens": emitted, "tok_s": round(emitted / (r_ms * 1e-3), 1)}
     out = {
         "metric": f"batched verify tok/s ({n_seq} sessions x k+1={k + 1} tokens, ragged contexts 256-2048)",
         "value": round(value, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -277,8 +281,7 @@ def bench_server(args, pkg):
         "config": {"workload": f"configs[4] server batch: {n_seq} sessions of the configs[3] model (d=2048, L=32, "
                                f"128 experts top-8, skewed router), k={k}, "
                                f"contexts {int(ctx.min())}-{int(ctx.max())}", "sessions": n_seq, "k": k},
-        "rounds": {"rounds": nr, "wall_ms": round(r_ms, 3), "tokens": emitted,
-                   "tok_s": round(emitted / (r_ms * 1e-3), 1)},
+        "rounds": rounds,
     }
     print(json.dumps(out))
     for st in states:

@@ -1374,6 +1374,10 @@ struct DWide {
     AttnItem *aitems;
     float *att_items = nullptr;   // attention scratch of an item launch, sized on demand
     size_t att_items_floats = 0;
+    // a session batch's control blocks and their destinations, staged in
+    // pinned memory and copied with one transfer (sized on demand)
+    char *ctl_host = nullptr, *ctl_dev = nullptr;
+    int ctl_cap = 0;
     // the later parts of a split prefill chunk (see batch_capture_dev): each
     // its own scratch and stream, and per part one event per layer plus two
     std::vector<DWide *> peer;
@@ -1458,6 +1462,8 @@ void wide_release(DWide *w) {
     if (w->arena) (void)hipFree(w->arena);
     if (w->logits) (void)hipFree(w->logits);
     if (w->att_items) (void)hipFree(w->att_items);
+    if (w->ctl_host) (void)hipHostFree(w->ctl_host);
+    if (w->ctl_dev) (void)hipFree(w->ctl_dev);
     delete w;
 }
 
@@ -1565,7 +1571,7 @@ int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, 
     const bool prefill_items = n_items == 1 && items[0].n > MAX_CHUNK && !advance;
     if ((pos_base || wait_ev || rec_ev) && !prefill_items) return 1;   // only a prefill chunk is split
     int n_attn = n_items;
-    int max_len = 1;
+    int max_len = 1, max_rows = 1;          // the attention items' longest row span and most rows
     {
         std::vector<KdaItem> ki((size_t)n_items);
         std::vector<AttnItem> ai;
@@ -1588,6 +1594,7 @@ int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, 
             attn_items = true;
             n_attn = (int)ai.size();
         }
+        for (const AttnItem &x : ai) max_rows = x.n > max_rows ? x.n : max_rows;
         if (l0 == 0) {
             CK(hipMemcpyAsync(w->kitems, ki.data(), sizeof(KdaItem) * ki.size(), hipMemcpyHostToDevice, st));
             CK(hipMemcpyAsync(w->aitems, ai.data(), sizeof(AttnItem) * ai.size(), hipMemcpyHostToDevice, st));
@@ -1641,7 +1648,7 @@ int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, 
                 }
                 // (a split chunk's second half reads the first half's K and V rows)
                 if (wait_ev) CK(hipStreamWaitEvent(st, wait_ev[l], 0));
-                CK(l98k_attn_items(&a, w->aitems, n_attn, plane, max_len, w->att_items, att_item,
+                CK(l98k_attn_items(&a, w->aitems, n_attn, plane, max_len, max_rows, w->att_items, att_item,
                                    prefill_items ? 1 : 0, st));
                 if (rec_ev) CK(hipEventRecord(rec_ev[l], st));
             }
@@ -3227,14 +3234,32 @@ extern "C" int l98_verify_batch(const LZModel *mm, LZRunState **states, int n_se
         // session's stream: one launch per op over all R rows
         hipStream_t st = S(states[0])->st;
         std::vector<WideItem> items((size_t)n_seq);
-        std::vector<DevCtl> hs((size_t)n_seq);
+        // the control blocks go up as one transfer of [n DevCtl][n
+        // destinations] from pinned memory, then one launch puts each in place
+        const size_t cbytes = (sizeof(DevCtl) + sizeof(DevCtl *)) * (size_t)n_seq;
+        if (w->ctl_cap < n_seq) {
+            if (w->ctl_host) (void)hipHostFree(w->ctl_host);
+            if (w->ctl_dev) (void)hipFree(w->ctl_dev);
+            w->ctl_host = w->ctl_dev = nullptr;
+            w->ctl_cap = 0;
+            if (hipHostMalloc((void **)&w->ctl_host, cbytes, hipHostMallocDefault) != hipSuccess ||
+                hipMalloc((void **)&w->ctl_dev, cbytes) != hipSuccess)
+                return 1;
+            w->ctl_cap = n_seq;
+        }
+        DevCtl *hs = reinterpret_cast<DevCtl *>(w->ctl_host);
+        DevCtl **dst = reinterpret_cast<DevCtl **>(w->ctl_host + sizeof(DevCtl) * (size_t)n_seq);
         for (int i = 0; i < n_seq; i++) {
             DState *d = S(states[i]);
             hs[i] = ctl_from(states[i]);
             hs[i].pos_scratch = pos0[i];
-            if (hipMemcpyAsync(d->ctl, &hs[i], sizeof(DevCtl), hipMemcpyHostToDevice, st)) return 1;
+            dst[i] = d->ctl;
             items[i] = WideItem{d, i * n_tok, n_tok, pos0[i]};
         }
+        if (hipMemcpyAsync(w->ctl_dev, w->ctl_host, cbytes, hipMemcpyHostToDevice, st) ||
+            l98k_put_ctl(reinterpret_cast<const DevCtl *>(w->ctl_dev),
+                         reinterpret_cast<DevCtl *const *>(w->ctl_dev + sizeof(DevCtl) * (size_t)n_seq), n_seq, st))
+            return 1;
         if (hipMemcpyAsync(w->toks, tokens, sizeof(int) * (size_t)R, hipMemcpyHostToDevice, st) ||
             wide_forward(Mo(mm), w, items.data(), n_seq, R, true, w->hcap, w->logits, st))
             return 1;

@@ -10,13 +10,10 @@
 // first rot dims, then q to qh or k quantized per 32 into the KV plane at
 // slot pos; the last nkv blocks of a token quantize v heads.
 // (attn_impl src/forward_attn.c:878-960; lz_rope src/ops_rope.c:21-67.)
-__global__ __launch_bounds__(64) void k_attn_prep(AttnArgs a) {
+__device__ __forceinline__ void attn_prep_body(const AttnArgs &a, int t, int hh) {
     __shared__ __align__(16) float sh[256], sq[256];
     __shared__ float s_inv;
     const int nq = a.kv_only ? 0 : a.nh;
-    const int per_tok = nq + 2 * a.nkv;
-    const int t = blockIdx.x / per_tok;
-    const int hh = blockIdx.x - t * per_tok;
     const int lane = threadIdx.x;
     const int hd = a.hd, half = a.rot >> 1;
     const int pos = *a.ctl_pos + a.pos_off + t;
@@ -80,6 +77,12 @@ __global__ __launch_bounds__(64) void k_attn_prep(AttnArgs a) {
             }
         }
     }
+}
+
+__global__ __launch_bounds__(64) void k_attn_prep(AttnArgs a) {
+    const int per_tok = (a.kv_only ? 0 : a.nh) + 2 * a.nkv;
+    const int t = blockIdx.x / per_tok;
+    attn_prep_body(a, t, blockIdx.x - t * per_tok);
 }
 
 // Attention of the chunk's tokens against the Q8 KV cache (attn_score_loop
@@ -765,6 +768,302 @@ __global__ __launch_bounds__(512) void k_attn_av_rows(AttnArgs b, const AttnItem
     if ((d & 31) == 0) a.oqs[(size_t)t * (a.q_dim >> 5) + (col >> 5)] = sg;
 }
 
+// k_attn_rows<HD, WPT>: the softmax and value sums of an item launch whose
+// K and V rows are all in the cache, 64- or 128-wide heads, positions up to
+// what the block's LDS holds (the launch checks): one block of 8 waves per
+// (q head, item), WPT waves per token (2 when every item has at most 4
+// rows), so the block holds TPB = 8 / WPT tokens; wave w takes token
+// w / WPT as its part w % WPT.
+//   1. each token's part-0 wave prepares its q head (RMSNorm(1+w) with the
+//      serial sum, NeoX rotary), as attn_prep_body does;
+//   2. the kv head's K rows are staged in chunks of AR_CH positions, once
+//      for every token of the block; each wave computes its token's scores
+//      for its positions of the chunk (the 32-group products in order, then
+//      the groups, times attn_scale), two positions interleaved when it has
+//      two;
+//   3. each token's part-0 wave takes the softmax (max by order-preserving
+//      key, exp, the serial loop's sum, scale);
+//   4. the V rows are staged in chunks of AR_CH positions, transposed
+//      ([d][position], scales [group][position]), and lane l of part r adds
+//      (a[p] * v[p][d]) * vs[p][d/32] for its elements d = u*64 + l
+//      (u = r, r + WPT, ...) over the positions in order, four per LDS read,
+//      the next four's reads issued before the current four's adds;
+//   5. the sigmoid output gate and the per-32 quantization.
+// The arithmetic is attn_av_body's and attn_scores_body's, so the bits are.
+// LDS: the staging area (STAGE bytes), then the score rows [TPB][lp] floats
+// (dynamic).
+#define AR_CH 128
+#define AR_STATIC_MARGIN (5 * 1024)     // the kernel's static LDS (q heads, exp table) and slack
+#define AR_THREADS (MAX_CHUNK * 64)
+#define GLOBAL __attribute__((address_space(1)))     // the cache planes: global loads, not flat
+typedef int v4i_a __attribute__((ext_vector_type(4)));
+template <int HD>
+struct ArPlan {
+    static constexpr int NDP = HD / 64, NB = HD / 32, CPR = HD / 16, KS = HD + 16, VS = AR_CH + 4;
+    static constexpr int K_BYTES = AR_CH * KS + AR_CH * NB * 4;
+    static constexpr int V_BYTES = HD * VS + NB * AR_CH * 4;
+    static constexpr int Q_BYTES = MAX_CHUNK * HD * 4;
+    static constexpr int m2(int x, int y) { return x > y ? x : y; }
+    static constexpr int STAGE = (m2(m2(K_BYTES, V_BYTES), Q_BYTES) + 15) & ~15;
+    static_assert(AR_CH * CPR % AR_THREADS == 0 && AR_CH * NB <= AR_THREADS && (HD * VS) % 16 == 0,
+                  "chunk staging layout");
+};
+
+template <int HD, int WPT>
+__global__ __launch_bounds__(AR_THREADS) void k_attn_rows(AttnArgs b, const AttnItem *__restrict__ items,
+                                                          int plane, int lp) {
+    using P = ArPlan<HD>;
+    constexpr int NDP = P::NDP, NB = P::NB, CPR = P::CPR, KS = P::KS, VS = P::VS, NTHR = AR_THREADS;
+    constexpr int TPB = MAX_CHUNK / WPT, JP = AR_CH / (64 * WPT);      // tokens per block, positions per lane
+    EXP_TAB_LOAD(tab);
+    extern __shared__ __align__(16) char smem[];
+    __shared__ __align__(16) float s_q[TPB][HD];                 // the prepared q heads
+    char *stage = smem;
+    float *s_a = reinterpret_cast<float *>(smem + P::STAGE);      // [TPB][lp]
+    const int h = blockIdx.x, item = blockIdx.y;
+    const AttnItem it = items[item];
+    const AttnArgs a = attn_item_args(b, it, plane);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, t = wave / WPT, part = wave - t * WPT;
+    const int kv_mul = a.nh / a.nkv, kvh = h / kv_mul;
+    const int pos0 = *a.ctl_pos + a.pos_off, n = it.n, Lmax = pos0 + n;
+    const bool live = t < n, lead = live && part == 0;
+    const int L = pos0 + imin(t, n - 1) + 1;
+    float *arow = s_a + (size_t)t * lp;
+    // 1. q heads: squares in the staging area, the serial sum, RMSNorm(1+w),
+    //    rotary (partners through s_q)
+    if (lead) {
+        float *sq = reinterpret_cast<float *>(stage) + t * HD;
+        const int half = a.rot >> 1, pos_t = L - 1;
+        float x[NDP], y[NDP];
+#pragma unroll
+        for (int u = 0; u < NDP; u++) {
+            x[u] = a.qg[(size_t)t * a.qg_dim + (size_t)h * 2 * HD + u * 64 + lane];
+            sq[u * 64 + lane] = x[u] * x[u];
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);           // lgkmcnt(0): the squares are in LDS
+        __builtin_amdgcn_wave_barrier();
+        const float inv = d_rsqrt(d_ss_over_n(serial_sum(sq, HD), HD) + a.eps);
+#pragma unroll
+        for (int u = 0; u < NDP; u++) {
+            y[u] = x[u] * inv * (1.0f + a.q_norm[u * 64 + lane]);
+            s_q[t][u * 64 + lane] = y[u];
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_wave_barrier();
+        float r[NDP];
+#pragma unroll
+        for (int u = 0; u < NDP; u++) {
+            const int i = u * 64 + lane;
+            r[u] = y[u];
+            if (i < half) {
+                const float c = a.rope_cs[((size_t)pos_t * half + i) * 2], sn = a.rope_cs[((size_t)pos_t * half + i) * 2 + 1];
+                r[u] = y[u] * c - s_q[t][i + half] * sn;
+            } else if (i < 2 * half) {
+                const int j = i - half;
+                const float c = a.rope_cs[((size_t)pos_t * half + j) * 2], sn = a.rope_cs[((size_t)pos_t * half + j) * 2 + 1];
+                r[u] = y[u] * c + s_q[t][j] * sn;
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int u = 0; u < NDP; u++) s_q[t][u * 64 + lane] = r[u];
+    }
+    EXP_TAB_PUT(tab);
+    __syncthreads();
+    // 2. scores, chunk by chunk of K rows
+    {
+        int8_t *s_k = reinterpret_cast<int8_t *>(stage);                              // [AR_CH][KS]
+        float *s_ks = reinterpret_cast<float *>(stage + AR_CH * KS);                   // [AR_CH][NB]
+        const int8_t *kbase = a.kcache + kvh * HD;
+        const float *ksbase = a.kscale + kvh * NB;
+        const size_t kst = (size_t)a.kv_dim, sst = (size_t)(a.kv_dim >> 5);
+        const float scale = a.attn_scale;
+        for (int c0 = 0; c0 < Lmax; c0 += AR_CH) {
+            const int nc = imin(AR_CH, Lmax - c0), total = nc * CPR, stotal = nc * NB;
+            constexpr int KU = AR_CH * CPR / NTHR;
+            int4 kr[KU];
+#pragma unroll
+            for (int u = 0; u < KU; u++) {
+                const int f = imin(u * NTHR + tid, total - 1), p = f / CPR, c = f - p * CPR;
+                const v4i_a q = *(const GLOBAL v4i_a *)(kbase + (size_t)(c0 + p) * kst + c * 16);
+                kr[u] = make_int4(q.x, q.y, q.z, q.w);
+            }
+            const int sf = imin(tid, stotal - 1), sp = sf / NB, sg = sf - sp * NB;
+            const float ksv = ((const GLOBAL float *)ksbase)[(size_t)(c0 + sp) * sst + sg];
+#pragma unroll
+            for (int u = 0; u < KU; u++) {
+                const int f = u * NTHR + tid, p = f / CPR, c = f - p * CPR;
+                if (f < total) *reinterpret_cast<int4 *>(s_k + p * KS + c * 16) = kr[u];
+            }
+            if (tid < stotal) s_ks[sp * NB + sg] = ksv;
+            __syncthreads();
+            // the wave's positions part*64 + lane + j*64*WPT; a position past
+            // the token's end computes on row 0 and stores nothing
+            const int lim = __builtin_amdgcn_readfirstlane(imin(nc, L - c0));
+            if (live && part * 64 < lim) {
+                int pl[JP];
+                bool ok[JP];
+#pragma unroll
+                for (int j = 0; j < JP; j++) {
+                    const int q = (j * WPT + part) * 64 + lane;
+                    ok[j] = q < lim;
+                    pl[j] = ok[j] ? q : 0;
+                }
+                const float *qq = s_q[t];
+                float sum[JP];
+#pragma unroll
+                for (int j = 0; j < JP; j++) sum[j] = 0.0f;
+#pragma unroll
+                for (int dd = 0; dd < HD; dd += 32) {
+                    int4 k0[JP], k1[JP];
+#pragma unroll
+                    for (int j = 0; j < JP; j++) {
+                        k0[j] = *reinterpret_cast<const int4 *>(s_k + pl[j] * KS + dd);
+                        k1[j] = *reinterpret_cast<const int4 *>(s_k + pl[j] * KS + dd + 16);
+                    }
+                    float acc[JP];
+#pragma unroll
+                    for (int j = 0; j < JP; j++) acc[j] = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 16; e++) {
+                        const float qe = qq[dd + e];
+#pragma unroll
+                        for (int j = 0; j < JP; j++) acc[j] += qe * (float)reinterpret_cast<const int8_t *>(&k0[j])[e];
+                    }
+#pragma unroll
+                    for (int e = 0; e < 16; e++) {
+                        const float qe = qq[dd + 16 + e];
+#pragma unroll
+                        for (int j = 0; j < JP; j++) acc[j] += qe * (float)reinterpret_cast<const int8_t *>(&k1[j])[e];
+                    }
+#pragma unroll
+                    for (int j = 0; j < JP; j++) sum[j] += acc[j] * s_ks[pl[j] * NB + (dd >> 5)];
+                }
+#pragma unroll
+                for (int j = 0; j < JP; j++)
+                    if (ok[j]) arow[c0 + pl[j]] = sum[j] * scale;
+            }
+            __syncthreads();
+        }
+    }
+    // 3. softmax of each token, by its part-0 wave: max by order-preserving
+    //    key, exp, the serial loop's sum over the score row, scale (every
+    //    token at once; the exact wave sum's tables would take the
+    //    registers that let two blocks share a CU)
+    if (lead) {
+        uint32_t best = 0;
+        for (int p = lane; p < L; p += 64) best = umax(best, d_fkey(arow[p]));
+        for (int o = 32; o > 0; o >>= 1) best = umax(best, (uint32_t)__shfl_xor((int)best, o));
+        const float mx = d_unkey(best);
+        for (int p = lane; p < L; p += 64) arow[p] = d_exp(arow[p] - mx, tab);
+        __builtin_amdgcn_s_waitcnt(0xC07F);           // lgkmcnt(0): the wave's exps are in LDS
+        __builtin_amdgcn_wave_barrier();
+        const float sum = serial_sum(arow, L);
+        const float inv = (sum > 0.0f) ? 1.0f / sum : 0.0f;
+        for (int p = lane; p < L; p += 64) arow[p] *= inv;
+    }
+    __syncthreads();
+    // 4. value sums, chunk by chunk of V rows (transposed); the wave's
+    //    elements u = part, part + WPT, ... (NU of them)
+    constexpr int NU = NDP >= WPT ? NDP / WPT : 1;
+    const bool vwork = live && part < NDP;
+    float o[NU];
+#pragma unroll
+    for (int i = 0; i < NU; i++) o[i] = 0.0f;
+    {
+        int8_t *s_vt = reinterpret_cast<int8_t *>(stage);                              // [HD][VS]
+        float *s_vst = reinterpret_cast<float *>(stage + HD * VS);                      // [NB][AR_CH]
+        const int8_t *vbase = a.vcache + kvh * HD;
+        const float *vsbase = a.vscale + kvh * NB;
+        const size_t vst = (size_t)a.kv_dim, sst = (size_t)(a.kv_dim >> 5);
+        for (int c0 = 0; c0 < Lmax; c0 += AR_CH) {
+            const int nc = imin(AR_CH, Lmax - c0), total = nc * CPR, stotal = nc * NB;
+            constexpr int KU = AR_CH * CPR / NTHR;
+            int4 vr[KU];
+#pragma unroll
+            for (int u = 0; u < KU; u++) {
+                const int f = imin(u * NTHR + tid, total - 1), p = f / CPR, c = f - p * CPR;
+                const v4i_a q = *(const GLOBAL v4i_a *)(vbase + (size_t)(c0 + p) * vst + c * 16);
+                vr[u] = make_int4(q.x, q.y, q.z, q.w);
+            }
+            const int sf = imin(tid, stotal - 1), sp = sf / NB, sg = sf - sp * NB;
+            const float vsv = ((const GLOBAL float *)vsbase)[(size_t)(c0 + sp) * sst + sg];
+#pragma unroll
+            for (int u = 0; u < KU; u++) {
+                const int f = u * NTHR + tid, p = f / CPR, c = f - p * CPR;
+                if (f < total) {
+                    const int w4[4] = {vr[u].x, vr[u].y, vr[u].z, vr[u].w};
+#pragma unroll
+                    for (int k = 0; k < 16; k++) s_vt[(16 * c + k) * VS + p] = (int8_t)((w4[k >> 2] >> (8 * (k & 3))) & 0xFF);
+                }
+            }
+            if (tid < stotal) s_vst[sg * AR_CH + sp] = vsv;
+            __syncthreads();
+            const int pe = __builtin_amdgcn_readfirstlane(imin(nc, L - c0));
+            if (vwork && pe > 0) {
+                const int pe4 = pe & ~3;
+                const float *ar = arow + c0;
+                const int8_t *vt[NU];
+                const float *vsr[NU];
+#pragma unroll
+                for (int i = 0; i < NU; i++) {
+                    const int d = (i * WPT + part) * 64 + lane;
+                    vt[i] = s_vt + d * VS;
+                    vsr[i] = s_vst + (d >> 5) * AR_CH;
+                }
+#pragma unroll 4
+                for (int p = 0; p < pe4; p += 4) {
+                    const float4 ap = *reinterpret_cast<const float4 *>(ar + p);
+#pragma unroll
+                    for (int i = 0; i < NU; i++) {
+                        const uint32_t vb = *reinterpret_cast<const uint32_t *>(vt[i] + p);
+                        const float4 vs = *reinterpret_cast<const float4 *>(vsr[i] + p);
+                        const float p0 = ap.x * (float)(int8_t)(vb & 0xFF) * vs.x;
+                        const float p1 = ap.y * (float)(int8_t)((vb >> 8) & 0xFF) * vs.y;
+                        const float p2 = ap.z * (float)(int8_t)((vb >> 16) & 0xFF) * vs.z;
+                        const float p3 = ap.w * (float)(int8_t)(vb >> 24) * vs.w;
+                        o[i] += p0;
+                        o[i] += p1;
+                        o[i] += p2;
+                        o[i] += p3;
+                    }
+                }
+                for (int p = pe4; p < pe; p++)
+#pragma unroll
+                    for (int i = 0; i < NU; i++) o[i] += ar[p] * (float)vt[i][p] * vsr[i][p];
+            }
+            __syncthreads();
+        }
+    }
+    if (!vwork) return;
+    // 5. gate, quantization
+#pragma unroll
+    for (int i = 0; i < NU; i++) {
+        const int d = (i * WPT + part) * 64 + lane;
+        const float gate = a.qg[(size_t)t * a.qg_dim + (size_t)h * 2 * HD + HD + d];
+        const float y = o[i] * d_sigmoid(gate, tab);
+        const int col = h * HD + d;
+        if (a.out) a.out[(size_t)t * a.q_dim + col] = y;
+        int8_t q;
+        float sg;
+        d_quant_group32(y, &q, &sg);
+        a.oq[(size_t)t * a.q_dim + col] = q;
+        if ((d & 31) == 0) a.oqs[(size_t)t * (a.q_dim >> 5) + (col >> 5)] = sg;
+    }
+}
+
+// k_attn_prep_items: every item's new K and V rows quantized into its
+// cache plane (attn_prep_body without the q heads), one 64-lane block per
+// (k or v head, token, item); tokens past an item's n return.
+__global__ __launch_bounds__(64) void k_attn_prep_items(AttnArgs b, const AttnItem *__restrict__ items, int plane) {
+    const AttnItem it = items[blockIdx.z];
+    if ((int)blockIdx.y >= it.n) return;
+    AttnArgs a = attn_item_args(b, it, plane);
+    a.kv_only = 1;
+    attn_prep_body(a, blockIdx.y, blockIdx.x);
+}
+
 // mtp_attn_t1 (src/forward_mtp.c:191-376, Q8 KV float arm): attention of
 // a DSpark slot at position 0 of the MTP plane with no history, one block
 // per slot row r.  The softmax over the single score is exactly 1, so K,
@@ -895,7 +1194,7 @@ static void av_allow_lds() {
 // buffers at row 0.  max_len: the longest item's last position + 1; att:
 // n_items scratch blocks of att_item floats.
 extern "C" int l98k_attn_items(const AttnArgs *a, const AttnItem *items, int n_items, int plane, int max_len,
-                               float *att, size_t att_item, int kv_cached, hipStream_t st) {
+                               int nmax, float *att, size_t att_item, int kv_cached, hipStream_t st) {
     if (a->nkv < 1 || a->nh % a->nkv || (a->hd & 31) || 256 % a->hd || a->hd > ATT_MAX_HD || a->rot > a->hd ||
         (a->rot & 1) || n_items < 1 || max_len < 1 || !a->oq || !a->oqs || !att || a->kv_only)
         return -1;
@@ -907,6 +1206,45 @@ extern "C" int l98k_attn_items(const AttnArgs *a, const AttnItem *items, int n_i
         // every row's K is in the cache: the value-sum blocks take their scores
         hipLaunchKernelGGL(k_attn_av_rows, dim3(a->nh, n_items), dim3(512), 0, st, *a, items, plane, att, att_stride,
                            att_item, 1);
+        return (int)hipGetLastError();
+    }
+    // 64- or 128-wide heads past the rows kernel's reach: the new K and V
+    // rows into the caches first (unless they are there), then one block per
+    // (q head, item) with the score rows in LDS, two waves per token when
+    // every item has at most half a chunk of rows
+    const int wpt = nmax <= MAX_CHUNK / 2 ? 2 : 1;
+    const size_t ar_lds = (size_t)(a->hd == 128 ? ArPlan<128>::STAGE : ArPlan<64>::STAGE) +
+                          (size_t)(MAX_CHUNK / wpt) * att_stride * sizeof(float);
+    if (!rows && (a->hd == 64 || a->hd == 128) && nmax >= 1 && nmax <= MAX_CHUNK &&
+        ar_lds <= (size_t)(lds_limit() - AR_STATIC_MARGIN)) {
+        if (!kv_cached) {
+            hipLaunchKernelGGL(k_attn_prep_items, dim3(2 * a->nkv, MAX_CHUNK, n_items), dim3(64), 0, st, *a, items,
+                               plane);
+            hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return (int)e;
+        }
+        static bool ar_attr = false;
+        if (!ar_attr) {
+            const int lim = lds_limit() - AR_STATIC_MARGIN;
+            (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k_attn_rows<128, 1>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, lim);
+            (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k_attn_rows<128, 2>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, lim);
+            (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k_attn_rows<64, 1>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, lim);
+            (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k_attn_rows<64, 2>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, lim);
+            ar_attr = true;
+        }
+        const dim3 grid(a->nh, n_items), blk(AR_THREADS);
+        if (a->hd == 128 && wpt == 2)
+            hipLaunchKernelGGL((k_attn_rows<128, 2>), grid, blk, ar_lds, st, *a, items, plane, att_stride);
+        else if (a->hd == 128)
+            hipLaunchKernelGGL((k_attn_rows<128, 1>), grid, blk, ar_lds, st, *a, items, plane, att_stride);
+        else if (wpt == 2)
+            hipLaunchKernelGGL((k_attn_rows<64, 2>), grid, blk, ar_lds, st, *a, items, plane, att_stride);
+        else
+            hipLaunchKernelGGL((k_attn_rows<64, 1>), grid, blk, ar_lds, st, *a, items, plane, att_stride);
         return (int)hipGetLastError();
     }
     const int slices = (max_len + ATT_SLICE - 1) / ATT_SLICE;

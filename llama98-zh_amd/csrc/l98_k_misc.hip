@@ -552,3 +552,17 @@ extern "C" int l98k_stream(const void *w, int blocks, int threads, int chunks, i
                        out);
     return (int)hipGetLastError();
 }
+
+// Control block i of a staging array copied to its session's (block i), so
+// a session batch's blocks go up as one host transfer.
+__global__ __launch_bounds__(128) void k_put_ctl(const DevCtl *__restrict__ src, DevCtl *const *__restrict__ dst) {
+    const int *s = reinterpret_cast<const int *>(src + blockIdx.x);
+    int *d = reinterpret_cast<int *>(dst[blockIdx.x]);
+    for (int j = threadIdx.x; j < (int)(sizeof(DevCtl) / sizeof(int)); j += 128) d[j] = s[j];
+}
+
+extern "C" int l98k_put_ctl(const DevCtl *src, DevCtl *const *dst, int n, hipStream_t st) {
+    if (n < 1) return -1;
+    hipLaunchKernelGGL(k_put_ctl, dim3(n), dim3(128), 0, st, src, dst);
+    return (int)hipGetLastError();
+}
