@@ -371,15 +371,20 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--k", type=int, default=3)
+    ap.add_argument("--k", type=int, default=None, help="draft width (default: the config's own, 1 for configs[0], else 3)")
     ap.add_argument("--config", type=int, default=1)
-    ap.add_argument("--prompt", type=int, default=512)
+    ap.add_argument("--prompt", type=int, default=None,
+                    help="prompt tokens (default: the config's own, 64 / 512 / 512 / 4096 for configs[0..3])")
     ap.add_argument("--model-dir", default=os.path.join(tempfile.gettempdir(), "l98_models"))
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--sessions", type=int, default=32, help="configs[4]: concurrent sessions")
     ap.add_argument("--dspark", action="store_true", help="a DSpark head on configs[1]'s shapes")
     args = ap.parse_args()
+    if args.prompt is None:
+        args.prompt = {0: 64, 3: 4096}.get(args.config, 512)
+    if args.k is None:
+        args.k = 1 if args.config == 0 else 3
     if args.gpus != 1:
         print(f"bench.py: this build runs the single-sequence path on one GPU; --gpus {args.gpus} "
               f"is not supported (see DESIGN.md for how the path would shard)", file=sys.stderr)

@@ -150,17 +150,47 @@ __device__ __forceinline__ float d_random_f32(unsigned long long *st) {
 #define XP_FIRST_GE 2                    // L.result = first i with prefix_i >= c (-1 if none), L.fres = that prefix
                                          // (the total when there is none)
 
+// An element is also special when the guessed sums around it come within
+// 2^-10 of a binade edge: the serial loop's rounding drift (a row of
+// probabilities that sums to about 1 ends a few ulps of 1 away from any
+// accurate sum) can put its real sum on the other side of the edge, and a
+// run the walk adds as one must not cross one.
+__device__ __forceinline__ bool xp_near(float A, float An) {
+    return f_binade(A * (1.0f - 0x1p-10f)) != f_binade(An * (1.0f + 0x1p-10f));
+}
+
 // The serial loop s = 0; s += x[i] over x[0..n) (non-negative values,
 // get(i) returns x[i], and 0 for i >= n), answered for `mode` by the whole
 // block.  Thread t owns elements [t*CH, (t+1)*CH).  Contains barriers.
+// Each pass reads the thread's elements XP_BATCH at a time, every load of a
+// batch issued before the first use.
+#define XP_BATCH 8
+template <class G, class F>
+__device__ __forceinline__ void xp_walk(const G &get, int i0, int CH, const bool &stop, F f) {
+    for (int k0 = 0; k0 < CH && !stop; k0 += XP_BATCH) {
+        float v[XP_BATCH];
+#pragma unroll
+        for (int u = 0; u < XP_BATCH; u++) v[u] = get.clamped(i0 + k0 + u);     // past the chunk: ignored
+#pragma unroll
+        for (int u = 0; u < XP_BATCH; u++)
+            if (k0 + u < CH && !stop) f(k0 + u, v[u]);
+    }
+}
+
 template <class G>
 __device__ __forceinline__ void xprefix(const G &get, int n, int mode, float c, SmpLds &L) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    if (n < 1) {                          // an empty row: no index passes, the sum is 0
+        if (tid == 0) { L.result = -1; L.fres = 0.0f; }
+        __syncthreads();
+        return;
+    }
     const int CH = (n + SMP_THREADS - 1) / SMP_THREADS;
     const int i0 = tid * CH;
+    const bool never = false;
     // approximate prefix (the binade guesses)
     float T = 0.0f;
-    for (int k = 0; k < CH; k++) T += get(i0 + k);
+    xp_walk(get, i0, CH, never, [&](int, float x) { T += x; });
     const float incl = blk_incl_f32(T, L);
     L.incl[tid] = incl;
     if (tid == 0) { L.K = 0; L.fail = 0; }
@@ -172,13 +202,12 @@ __device__ __forceinline__ void xprefix(const G &get, int n, int mode, float c, 
     {
         float A = off;
         int E0 = f_binade(off);
-        for (int k = 0; k < CH; k++) {
+        xp_walk(get, i0, CH, never, [&](int k, float x) {
             const int i = i0 + k;
-            const float x = get(i);
             const float An = (k == CH - 1) ? incl : A + x;
             const int E1 = f_binade(An);
             uint32_t q;
-            const uint32_t plain = ps_classify(x, E0, E1, &q);
+            const uint32_t plain = ps_classify(x, E0, xp_near(A, An) ? -1 : E1, &q);
             if (!plain) {
                 const int slot = atomicAdd(&L.K, 1);
                 if (slot < SMP_RMAX) {
@@ -194,7 +223,7 @@ __device__ __forceinline__ void xprefix(const G &get, int n, int mode, float c, 
             qs += q;
             A = An;
             E0 = E1;
-        }
+        });
     }
     L.cnt_ex[tid] = blk_excl_u32(cnt, L);
     unsigned long long qtot;
@@ -302,13 +331,13 @@ __device__ __forceinline__ void xprefix(const G &get, int n, int mode, float c, 
         int E0 = f_binade(off);
         uint32_t rk = L.cnt_ex[tid];
         unsigned long long qp = L.q_ex[tid];
-        for (int k = 0; k < CH; k++) {
+        bool found = false;
+        xp_walk(get, i0, CH, found, [&](int k, float x) {
             const int i = i0 + k;
-            const float x = get(i);
             const float An = (k == CH - 1) ? incl : A + x;
             const int E1 = f_binade(An);
             uint32_t q;
-            const uint32_t plain = ps_classify(x, E0, E1, &q);
+            const uint32_t plain = ps_classify(x, E0, xp_near(A, An) ? -1 : E1, &q);
             float pref;
             if (!plain) {
                 rk++;
@@ -321,10 +350,10 @@ __device__ __forceinline__ void xprefix(const G &get, int n, int mode, float c, 
                 pref = L.sA[rk] + (float)run * __builtin_amdgcn_ldexpf(1.0f, eb - 150);
             }
             const bool hit = i < n && (mode == XP_FIRST_GT ? c < pref : pref >= c);
-            if (hit) { best = i; bestv = pref; break; }
+            if (hit) { best = i; bestv = pref; found = true; }
             A = An;
             E0 = E1;
-        }
+        });
     }
     const int first = blk_min_i32(best, L);
     if (best == first && first != 0x7FFFFFFF) L.fres = bestv;
@@ -335,10 +364,17 @@ __device__ __forceinline__ void xprefix(const G &get, int n, int mode, float c, 
     __syncthreads();
 }
 
+// Row accessors: operator() reads element i (0 past n); clamped(i) reads
+// it with the index clamped into the row and selects 0 past n, a load with
+// no branch, so a thread's loads can all be in flight together.
 struct GetArr {
     const float *x;
     int n;
     __device__ float operator()(int i) const { return i < n ? x[i] : 0.0f; }
+    __device__ float clamped(int i) const {
+        const float v = x[imin(i, n - 1)];
+        return i < n ? v : 0.0f;
+    }
 };
 struct GetResid {                        // max(p - q, 0) (sample_residual's dd > 0 terms)
     const float *p, *q;
@@ -348,11 +384,20 @@ struct GetResid {                        // max(p - q, 0) (sample_residual's dd 
         const float dd = p[i] - q[i];
         return dd > 0.0f ? dd : 0.0f;
     }
+    __device__ float clamped(int i) const {
+        const int ic = imin(i, n - 1);
+        const float dd = p[ic] - q[ic];
+        return i < n && dd > 0.0f ? dd : 0.0f;
+    }
 };
 struct GetKeys {                         // probabilities from sorted order-preserving keys
     const uint32_t *k;
     int n;
     __device__ float operator()(int i) const { return i < n ? __uint_as_float(k[i]) : 0.0f; }
+    __device__ float clamped(int i) const {
+        const float v = __uint_as_float(k[imin(i, n - 1)]);
+        return i < n ? v : 0.0f;
+    }
 };
 
 // first index of the largest value (order-preserving key, strict >)

@@ -2,6 +2,12 @@
 
     rocprofv3 --kernel-trace --stats --output-format csv -d OUT -o prof -- python3 bench.py --no-graph ...
     python3 llama98-zh_amd/profsum.py OUT/prof_kernel_trace.csv [--vocab V]
+    python3 llama98-zh_amd/profsum.py OUT/prof_kernel_trace.csv --verify-batches N
+
+With --verify-batches N (a trace of `bench.py --config 4 --no-graph`, whose
+last N dispatch runs are the batched verifies), prints instead the whole
+run and the mean of the last N batched verifies, each starting at its
+many-row k_embed (the batch's token rows in one launch).
 
 Prints, as markdown:
   * every kernel of the whole run (calls, total, mean, min, max);
@@ -51,12 +57,34 @@ def main():
     ap.add_argument("--vocab", type=int, default=65536)
     ap.add_argument("--gemv-rows-per-block", type=int, default=32,
                     help="rows per GEMV tile at the lm_head's input width")
+    ap.add_argument("--verify-batches", type=int, default=0, help="summarize the last N batched verifies")
     a = ap.parse_args()
     rows = load(a.trace)
     whole = collections.defaultdict(list)
     for n, s, e, g, w, *_ in rows:
         whole[short(n)].append(e - s)
     print(table(whole, "Whole run", "all dispatches"))
+    if a.verify_batches:
+        emb = [i for i, r in enumerate(rows) if short(r[0]) == "k_embed" and r[5] >= 16]
+        nb = min(a.verify_batches, len(emb))
+        seg = rows[emb[-nb]:]
+        grp = collections.defaultdict(list)
+        for n, s, e, g, w, *_ in seg:
+            grp[short(n)].append(e - s)
+        span = (seg[-1][2] - seg[0][1]) / nb
+        per = {k: [x / nb for x in v] for k, v in grp.items()}
+        print()
+        print(f"### Batched verify: the last {nb} (per verify: calls / {nb}, total / {nb}; span {span / 1e3:.1f} us "
+              f"per verify, kernels launched one by one under the tracer)")
+        print()
+        print("| kernel | calls | total us | mean us | % |")
+        print("|---|---:|---:|---:|---:|")
+        tot = sum(sum(v) for v in grp.values())
+        for k, v in sorted(grp.items(), key=lambda kv: -sum(kv[1])):
+            print(f"| `{k}` | {len(v) / nb:g} | {sum(v) / nb / 1e3:.1f} | {sum(v) / len(v) / 1e3:.2f} | "
+                  f"{100 * sum(v) / tot:.1f} |")
+        print(f"| **verify** | {sum(len(v) for v in grp.values()) / nb:g} | {tot / nb / 1e3:.1f} | | |")
+        return
     acc = [i for i, r in enumerate(rows) if short(r[0]) == "k_accept"]
     if len(acc) >= 2:
         seg = rows[acc[-2] + 1:acc[-1] + 1]
