@@ -284,11 +284,25 @@ int l98_greedy_rounds_ex(const LZModel *m, LZRunState *s, int k, int n_rounds, i
 int l98_verify_batch(const LZModel *m, LZRunState **states, int n_seq, const int *tokens, int n_tok,
                      const int *pos0, int copy_out, float *wall_ms);
 /* l98_greedy_rounds for n_seq sessions started with l98_session_start:
- * n_rounds rounds each (one HIP graph launch per round and session).
- * tokens[i*cap ..] receives session i's emitted ids, n_out[i] their count.
- * Returns the total tokens emitted, or -LZErr. */
+ * n_rounds rounds each.  tokens[i*cap ..] receives session i's emitted ids,
+ * n_out[i] their count.  Returns the total tokens emitted, or -LZErr.
+ * The rounds run batched across the sessions when the model allows it (a
+ * one-slot MTP head, no SubLN, one scale per weight row, (k+1)*n_seq <= 512
+ * rows): each draft step is one many-row pass over every session's row, the
+ * verify one many-row forward, then every session's acceptance, catch-up
+ * and round record in one launch each; otherwise each session's round graph
+ * is replayed on its own stream.  Either way each session emits exactly what
+ * it emits alone. */
 int l98_greedy_rounds_batch(const LZModel *m, LZRunState **states, int n_seq, int k, int n_rounds, int *tokens,
                             int cap, int *n_out, float *wall_ms);
+/* l98_greedy_rounds_batch with the path chosen: mode 0 as above, mode 1
+ * each session's own round graph (the reference for the batched path's
+ * tests). */
+int l98_greedy_rounds_batch_ex(const LZModel *m, LZRunState **states, int n_seq, int k, int n_rounds, int *tokens,
+                               int cap, int *n_out, float *wall_ms, int mode);
+/* 1 when l98_greedy_rounds_batch runs n_seq sessions of this model at
+ * draft width k as batched rounds, else 0. */
+int l98_batched_rounds_ok(const LZModel *m, int n_seq, int k);
 /* Mean duration of `iters` launches, hipEvent-timed on the state's stream.
  * which = 0: the tied lm_head GEMV with mrows token rows, back to back;
  * 1: the verify forward of mrows tokens; 2: a device copy of the lm_head's

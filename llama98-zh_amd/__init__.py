@@ -136,6 +136,9 @@ HIP_API = [
                                    _IP, C.c_int, _FP]),
     ("l98_greedy_rounds_batch", C.c_int, [C.POINTER(LZModel), C.POINTER(C.POINTER(LZRunState)), C.c_int, C.c_int,
                                           C.c_int, _IP, C.c_int, _IP, _FP]),
+    ("l98_greedy_rounds_batch_ex", C.c_int, [C.POINTER(LZModel), C.POINTER(C.POINTER(LZRunState)), C.c_int,
+                                             C.c_int, C.c_int, _IP, C.c_int, _IP, _FP, C.c_int]),
+    ("l98_batched_rounds_ok", C.c_int, [C.POINTER(LZModel), C.c_int, C.c_int]),
     ("l98_row_sums", C.c_int, [_FP, C.c_int, C.c_int, _FP]),
     ("l98_fwht_i32", C.c_int, [_IP, _IP, C.c_int, C.c_int, C.c_int]),
     ("l98_fwht_f32", C.c_int, [_FP, C.c_int, C.c_int, C.c_int, C.c_int]),
@@ -428,14 +431,16 @@ class Engine:
             out.append((lg, hd))
         return ms.value, out
 
-    def greedy_rounds_batch(self, states, k, n_rounds):
-        """l98_greedy_rounds_batch; returns (wall_ms, [tokens per session])."""
+    def greedy_rounds_batch(self, states, k, n_rounds, mode=0):
+        """l98_greedy_rounds_batch_ex (mode 0: batched when the model allows,
+        1: each session's own round graph); returns (wall_ms, [tokens per
+        session])."""
         cap = n_rounds * (k + 1)
         toks = np.zeros((len(states), cap), np.int32)
         n_out = np.zeros(len(states), np.int32)
         ms = C.c_float()
-        n = self.lib.l98_greedy_rounds_batch(C.byref(self.m), self._state_ptrs(states), len(states), k, n_rounds,
-                                             _ip(toks), cap, _ip(n_out), C.byref(ms))
+        n = self.lib.l98_greedy_rounds_batch_ex(C.byref(self.m), self._state_ptrs(states), len(states), k, n_rounds,
+                                                _ip(toks), cap, _ip(n_out), C.byref(ms), mode)
         if n < 0:
             raise RuntimeError(f"l98_greedy_rounds_batch failed: {n}")
         return ms.value, [toks[i, :n_out[i]].copy() for i in range(len(states))]

@@ -172,6 +172,15 @@ typedef struct {
     float eps, attn_scale;
 } AttnArgs;
 
+// One session of a batched round (l98k_batch_round): its control block,
+// draft chain, round history and KDA ring depth.
+typedef struct {
+    DevCtl *ctl;
+    float *chain;
+    RoundRec *hist;
+    int hist_cap, depth;
+} BatchSess;
+
 // One session's rows of a many-session attention launch (l98k_attn_items).
 typedef struct {
     int8_t *kq, *vq;                    // the session's KV planes, plane 0 base [planes][seq][kv_dim]

@@ -3308,10 +3308,181 @@ extern "C" int l98_verify_batch(const LZModel *mm, LZRunState **states, int n_se
     return 0;
 }
 
-extern "C" int l98_greedy_rounds_batch(const LZModel *mm, LZRunState **states, int n_seq, int k, int n_rounds,
-                                       int *tokens, int cap, int *n_out, float *wall_ms) {
-    if (!batch_ok(mm, states, n_seq) || n_rounds < 1 || !n_out) return -LZ_ERR_NULL_ARG;
+namespace {
+
+// ----------------------------------------------- batched session rounds ---
+//
+// n sessions' greedy rounds as many-row passes over their rows, on the first
+// session's stream, with draft_step's, enqueue_verify_accept's and
+// mtp_prefill_chunked's arithmetic through the many-row kernels (the MFMA
+// GEMMs, the RMSNorm rows, the SiLU-mul rows and the item attention give the
+// GEMV path's bits):
+//   * draft step j: one row per session (its tok[j] and chain), the MTP
+//     block at its position mtp_pos + j (one attention item per session), the
+//     FFN, the exit norm (the new chain rows) and the tied lm_head, argmax
+//     p1 per row into tok[j + 1];
+//   * the verify: wide_forward over the sessions' K1 = k + 1 rows each at
+//     anchor_pos, argmax per row as targ;
+//   * acceptance with ring rollback and the chain reseed per session, the
+//     catch-up of k - 1 rows per session (K and V into the MTP plane at
+//     catch_pos), the round record and the advance.
+struct RoundBatch {
+    char *mem = nullptr;             // device tables
+    BatchSess *bs = nullptr;
+    AttnItem *draft_items = nullptr; // [k][n]: row r, position mtp_pos + j
+    AttnItem *catch_items = nullptr; // [n]: rows r*(k-1) .., position catch_pos
+    int *am = nullptr;               // argmaxes [n * K1]
+    ~RoundBatch() { if (mem) (void)hipFree(mem); }
+};
+
+int wide_draft_step(const DModel *m, DWide *w, const RoundBatch &rb, int n, int j, int max_len, hipStream_t st) {
+    const LZModelConfig &c = m->c;
+    const int d = c.hidden_size, I = c.mtp_intermediate_size, V = c.vocab_size;
+    const int qgd = c.attn_qgate_dim, kvd = c.attn_kv_dim, qd = c.attn_q_dim;
+    const float eps = c.rms_norm_eps;
+    const DLayer &L = m->mtp;
+    CK(l98k_batch_round(0, rb.bs, n, j, 1, 0, d, nullptr, nullptr, w->toks, w->hcap, st));
+    CK(l98k_mtp_pre(m->embed.q, m->embed.s, m->embed.gs, w->toks, w->hcap, d, m->mtp_pre_e, m->mtp_pre_h, eps, n,
+                    w->mq, w->mqs, st));
+    CK(mf(m->mtp_fc, w->mq, w->mqs, n, w->x, d, st));
+    CK(l98k_rmsnorm(w->x, d, nullptr, nullptr, L.in_norm, d, eps, n, nullptr, 0, w->xq, w->xqs, st));
+    CK(mf_multi({{&L.q, w->qg, qgd}, {&L.k, w->kp, kvd}, {&L.v, w->vp, kvd}}, w->xq, w->xqs, n, st));
+    AttnArgs a{};
+    a.qg = w->qg; a.kp = w->kp; a.vp = w->vp;
+    a.q_norm = L.q_norm; a.k_norm = L.k_norm; a.rope_cs = m->rope_cs;
+    a.qh = w->qh;
+    a.oq = w->xq2; a.oqs = w->xqs2;
+    a.nh = c.n_heads; a.nkv = c.n_kv_heads; a.hd = c.head_dim; a.rot = c.rotary_dim;
+    a.q_dim = qd; a.qg_dim = qgd; a.kv_dim = kvd;
+    a.eps = eps;
+    a.attn_scale = ssm_scale(c.head_dim);
+    const size_t att_item = (size_t)MAX_CHUNK * c.n_heads * (size_t)((max_len + 3) & ~3);
+    CK(l98k_attn_items(&a, rb.draft_items + (size_t)j * n, n, c.n_full_layers, max_len, 1, w->att_items, att_item, 0,
+                       st));
+    CK(mf(L.o, w->xq2, w->xqs2, n, w->blk, d, st));
+    // the FFN (dense_ffn_step): the residual folds in place, post-norm, gate
+    // / up, SiLU-mul, down, then the exit norm (the chain rows) and the head
+    CK(l98k_rmsnorm(w->x, d, w->blk, nullptr, L.post_norm, d, eps, n, nullptr, 0, w->xq, w->xqs, st));
+    CK(mf_multi({{&m->mtp_gate, w->h1, I}, {&m->mtp_up, w->h3, I}}, w->xq, w->xqs, n, st));
+    CK(l98k_wide_pro(1, w->h1, w->h3, I, nullptr, nullptr, 0, I, n, w->hq, w->hqs, st));
+    CK(mf(m->mtp_down, w->hq, w->hqs, n, w->blk, d, st));
+    CK(l98k_rmsnorm(w->x, d, w->blk, nullptr, m->mtp_norm, d, eps, n, w->hcap, d, w->xq, w->xqs, st));
+    CK(mf(m->embed, w->xq, w->xqs, n, w->logits, V, st));
+    CK(l98k_argmax(w->logits, V, n, 1, rb.am, st));
+    return l98k_batch_round(1, rb.bs, n, j, 1, 0, d, rb.am, w->hcap, nullptr, nullptr, st);
+}
+
+// The catch-up of k - 1 rows per session after the acceptance: the rows'
+// main_proj input from (verify hidden row j, catch_tok[j]), fc, the MTP
+// block's input norm and K / V into each session's MTP plane at catch_pos + j.
+int wide_catchup(const DModel *m, DWide *w, const RoundBatch &rb, int n, int k, hipStream_t st) {
+    const LZModelConfig &c = m->c;
+    const int d = c.hidden_size, kvd = c.attn_kv_dim, nc = k - 1, R = n * nc;
+    const float eps = c.rms_norm_eps;
+    CK(l98k_batch_round(4, rb.bs, n, 0, k + 1, nc, d, nullptr, w->hcap, w->toks, w->blk, st));
+    CK(l98k_mtp_pre(m->embed.q, m->embed.s, m->embed.gs, w->toks, w->blk, d, m->mtp_pre_e, m->mtp_pre_h, eps, R,
+                    w->mq, w->mqs, st));
+    CK(mf(m->mtp_fc, w->mq, w->mqs, R, w->x, d, st));
+    CK(l98k_rmsnorm(w->x, d, nullptr, nullptr, m->mtp.in_norm, d, eps, R, nullptr, 0, w->xq, w->xqs, st));
+    CK(mf_multi({{&m->mtp.k, w->kp, kvd}, {&m->mtp.v, w->vp, kvd}}, w->xq, w->xqs, R, st));
+    AttnArgs a{};
+    a.kp = w->kp; a.vp = w->vp;
+    a.k_norm = m->mtp.k_norm; a.rope_cs = m->rope_cs;
+    a.nh = c.n_heads; a.nkv = c.n_kv_heads; a.hd = c.head_dim; a.rot = c.rotary_dim;
+    a.q_dim = c.attn_q_dim; a.qg_dim = c.attn_qgate_dim; a.kv_dim = kvd;
+    a.kv_only = 1;
+    a.eps = eps;
+    return l98k_attn_prep_items(&a, rb.catch_items, n, c.n_full_layers, st);
+}
+
+// Whether a batch of sessions can take the batched rounds: the many-row
+// forward carries the model (no SubLN, no grouped scales), a one-slot MTP
+// head, every row fits one many-row pass, and the FFN rows fit the expert
+// buffers they borrow.
+bool batched_rounds_ok(const DModel *m, int n_seq, int k) {
+    const LZModelConfig &c = m->c;
+    if (m->n_draft > 1 || c.use_subn || n_seq < 1 || k < 1) return false;
+    if ((size_t)n_seq * (k + 1) > WIDE_MAX || (size_t)n_seq * (k - 1 > 0 ? k - 1 : 1) > WIDE_MAX) return false;
+    const size_t pairs = (size_t)WIDE_MAX * c.num_experts_per_token;
+    return (size_t)n_seq * c.mtp_intermediate_size <= pairs * c.moe_intermediate_size;
+}
+
+int greedy_rounds_batched(const LZModel *mm, LZRunState **states, int n_seq, int k, int n_rounds, float *wall_ms) {
+    const DModel *m = Mo(mm);
+    const LZModelConfig &c = m->c;
+    const int K1 = k + 1, R = n_seq * K1, V = c.vocab_size;
+    DWide *w = wide_get(m);
+    if (!w || !batched_rounds_ok(m, n_seq, k)) return 1;
+    hipStream_t st = S(states[0])->st;
+    int max_len = 1;
+    for (int i = 0; i < n_seq; i++) max_len = S(states[i])->seq_len > max_len ? S(states[i])->seq_len : max_len;
+    // scratch sized once, before the timed loop
+    if (w->logits_rows < R) {
+        if (w->logits) (void)hipFree(w->logits);
+        w->logits = nullptr;
+        w->logits_rows = 0;
+        if (hipMalloc((void **)&w->logits, sizeof(float) * (size_t)R * V) != hipSuccess) return 1;
+        w->logits_rows = R;
+    }
+    const size_t att_item = (size_t)MAX_CHUNK * c.n_heads * (size_t)((max_len + 3) & ~3);
+    if (w->att_items_floats < att_item * n_seq) {
+        if (w->att_items) (void)hipFree(w->att_items);
+        w->att_items = nullptr;
+        w->att_items_floats = 0;
+        if (hipMalloc((void **)&w->att_items, sizeof(float) * att_item * n_seq) != hipSuccess) return 1;
+        w->att_items_floats = att_item * n_seq;
+    }
+    RoundBatch rb;
+    const size_t o_bs = 0, o_di = (sizeof(BatchSess) * n_seq + 255) & ~(size_t)255,
+                 o_ci = o_di + ((sizeof(AttnItem) * (size_t)k * n_seq + 255) & ~(size_t)255),
+                 o_am = o_ci + ((sizeof(AttnItem) * n_seq + 255) & ~(size_t)255), bytes = o_am + sizeof(int) * R;
+    if (hipMalloc((void **)&rb.mem, bytes) != hipSuccess) return 1;
+    rb.bs = (BatchSess *)(rb.mem + o_bs);
+    rb.draft_items = (AttnItem *)(rb.mem + o_di);
+    rb.catch_items = (AttnItem *)(rb.mem + o_ci);
+    rb.am = (int *)(rb.mem + o_am);
+    std::vector<BatchSess> hb((size_t)n_seq);
+    std::vector<AttnItem> hd((size_t)k * n_seq), hc((size_t)n_seq);
+    std::vector<WideItem> items((size_t)n_seq);
+    for (int i = 0; i < n_seq; i++) {
+        DState *d = S(states[i]);
+        hb[i] = BatchSess{d->ctl, d->chain, d->hist, d->hist_cap, d->depth};
+        for (int j = 0; j < k; j++)
+            hd[(size_t)j * n_seq + i] = AttnItem{d->kq, d->vq, d->ks, d->vs, &d->ctl->mtp_pos, i, 1, d->seq_len, j};
+        hc[i] = AttnItem{d->kq, d->vq, d->ks, d->vs, &d->ctl->catch_pos, i * (k - 1), k - 1, d->seq_len, 0};
+        // positions come from each control block; pos0 only bounds the rows' reach
+        items[i] = WideItem{d, i * K1, K1, d->seq_len - K1};
+    }
+    if (hipMemcpy(rb.bs, hb.data(), sizeof(BatchSess) * n_seq, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(rb.draft_items, hd.data(), sizeof(AttnItem) * hd.size(), hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(rb.catch_items, hc.data(), sizeof(AttnItem) * n_seq, hipMemcpyHostToDevice) != hipSuccess)
+        return 1;
+    const double t0 = now_ms();
+    for (int r = 0; r < n_rounds; r++) {
+        for (int j = 0; j < k; j++) CK(wide_draft_step(m, w, rb, n_seq, j, max_len, st));
+        CK(l98k_batch_round(2, rb.bs, n_seq, 0, K1, 0, c.hidden_size, nullptr, nullptr, w->toks, nullptr, st));
+        CK(wide_forward(m, w, items.data(), n_seq, R, true, w->hcap, w->logits, st));
+        CK(l98k_argmax(w->logits, V, R, 0, rb.am, st));
+        CK(l98k_batch_round(3, rb.bs, n_seq, 0, K1, 0, c.hidden_size, rb.am, w->hcap, nullptr, nullptr, st));
+        if (k > 1) CK(wide_catchup(m, w, rb, n_seq, k, st));
+        CK(l98k_batch_round(5, rb.bs, n_seq, 0, K1, 0, c.hidden_size, nullptr, nullptr, nullptr, nullptr, st));
+    }
+    if (hipStreamSynchronize(st) != hipSuccess) return 1;
+    if (wall_ms) *wall_ms = (float)(now_ms() - t0);
+    lz_debug_n_chunks += n_rounds;
+    lz_debug_n_lmhead += n_rounds;
+    return 0;
+}
+
+}  // namespace
+
+extern "C" int l98_greedy_rounds_batch_ex(const LZModel *mm, LZRunState **states, int n_seq, int k, int n_rounds,
+                                          int *tokens, int cap, int *n_out, float *wall_ms, int mode) {
+    if (!batch_ok(mm, states, n_seq) || n_rounds < 1 || !n_out || mode < 0 || mode > 1) return -LZ_ERR_NULL_ARG;
     if (!Mo(mm)->has_mtp) return -LZ_ERR_SPEC_NO_HEAD;
+    // mode 0: the batched rounds when the model and the batch allow them;
+    // mode 1: each session's own round graph on its own stream
+    const bool batched = mode == 0 && batched_rounds_ok(Mo(mm), n_seq, k) && wide_get(Mo(mm)) != nullptr;
     for (int i = 0; i < n_seq; i++) {
         LZRunState *s = states[i];
         DState *d = S(s);
@@ -3325,7 +3496,7 @@ extern "C" int l98_greedy_rounds_batch(const LZModel *mm, LZRunState **states, i
         h.expert_tally = 0;
         h.k_eff = k;
         if (ctl_put(d, h)) return -LZ_ERR_FORWARD;
-        if (!d->round_graph[k]) {
+        if (!batched && !d->round_graph[k]) {
             hipGraph_t g = nullptr;
             if (hipStreamBeginCapture(d->st, hipStreamCaptureModeThreadLocal) != hipSuccess) return -LZ_ERR_FORWARD;
             int rc = enqueue_greedy_round(d, k, d->seq_len - 1, 0, true);
@@ -3338,15 +3509,19 @@ extern "C" int l98_greedy_rounds_batch(const LZModel *mm, LZRunState **states, i
         }
         if (hipStreamSynchronize(d->st) != hipSuccess) return -LZ_ERR_FORWARD;
     }
-    const double t0 = now_ms();
-    for (int r = 0; r < n_rounds; r++)
-        for (int i = 0; i < n_seq; i++) {
-            DState *d = S(states[i]);
-            if (hipGraphLaunch(d->round_graph[k], d->st) != hipSuccess) return -LZ_ERR_FORWARD;
-        }
-    for (int i = 0; i < n_seq; i++)
-        if (hipStreamSynchronize(S(states[i])->st) != hipSuccess) return -LZ_ERR_FORWARD;
-    if (wall_ms) *wall_ms = (float)(now_ms() - t0);
+    if (batched) {
+        if (greedy_rounds_batched(mm, states, n_seq, k, n_rounds, wall_ms)) return -LZ_ERR_FORWARD;
+    } else {
+        const double t0 = now_ms();
+        for (int r = 0; r < n_rounds; r++)
+            for (int i = 0; i < n_seq; i++) {
+                DState *d = S(states[i]);
+                if (hipGraphLaunch(d->round_graph[k], d->st) != hipSuccess) return -LZ_ERR_FORWARD;
+            }
+        for (int i = 0; i < n_seq; i++)
+            if (hipStreamSynchronize(S(states[i])->st) != hipSuccess) return -LZ_ERR_FORWARD;
+        if (wall_ms) *wall_ms = (float)(now_ms() - t0);
+    }
     int total = 0;
     std::vector<RoundRec> rec((size_t)n_rounds);
     for (int i = 0; i < n_seq; i++) {
@@ -3371,6 +3546,16 @@ extern "C" int l98_greedy_rounds_batch(const LZModel *mm, LZRunState **states, i
             return -LZ_ERR_FORWARD;
     }
     return total;
+}
+
+extern "C" int l98_batched_rounds_ok(const LZModel *mm, int n_seq, int k) {
+    if (!mm || !mm->impl) return 0;
+    return batched_rounds_ok(Mo(mm), n_seq, k) && wide_get(Mo(mm)) != nullptr ? 1 : 0;
+}
+
+extern "C" int l98_greedy_rounds_batch(const LZModel *mm, LZRunState **states, int n_seq, int k, int n_rounds,
+                                       int *tokens, int cap, int *n_out, float *wall_ms) {
+    return l98_greedy_rounds_batch_ex(mm, states, n_seq, k, n_rounds, tokens, cap, n_out, wall_ms, 0);
 }
 
 // n temperature rounds on the device, one HIP graph launch each (captured

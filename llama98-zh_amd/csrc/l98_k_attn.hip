@@ -1270,6 +1270,14 @@ extern "C" int l98k_attn_items(const AttnArgs *a, const AttnItem *items, int n_i
     return (int)hipGetLastError();
 }
 
+// The K and V rows of every item's tokens into its session's cache plane
+// (a batch of sessions' MTP catch-up rows).
+extern "C" int l98k_attn_prep_items(const AttnArgs *a, const AttnItem *items, int n_items, int plane, hipStream_t st) {
+    if (a->hd > 256 || (a->hd & 31) || a->rot > a->hd || n_items < 1 || n_items > 65535) return -1;
+    hipLaunchKernelGGL(k_attn_prep_items, dim3(2 * a->nkv, MAX_CHUNK, n_items), dim3(64), 0, st, *a, items, plane);
+    return (int)hipGetLastError();
+}
+
 extern "C" int l98k_attn(const AttnArgs *a, int nt, int max_len, float *att, hipStream_t st) {
     // hd divides 256: the new K rows' quantization takes 32-lane groups of
     // a 256-thread block

@@ -268,8 +268,8 @@ __global__ __launch_bounds__(256) void k_argmax_part(const unsigned long long *_
 // next anchor and positions.
 // flags: bit 0 debug_break_rollback; bit 1 a DSpark round (no catch-up rows,
 // mtp_pos unchanged: src/generate.c:1117-1133).
-__global__ void k_accept(DevCtl *ctl, const float *__restrict__ vhidden, int d,
-                         float *__restrict__ chain, int depth, int flags) {
+__device__ __forceinline__ void accept_body(DevCtl *ctl, const float *__restrict__ vhidden, int d,
+                                            float *__restrict__ chain, int depth, int flags) {
     // flags: 1 the rollback break, 2 a DSpark round (no catch-up), 4 a
     // temperature round (n_accept and out[] already written by its
     // acceptance launches)
@@ -308,6 +308,31 @@ __global__ void k_accept(DevCtl *ctl, const float *__restrict__ vhidden, int d,
     for (int i = threadIdx.x; i < d; i += blockDim.x) chain[i] = vhidden[(size_t)n * d + i];
 }
 
+__global__ void k_accept(DevCtl *ctl, const float *__restrict__ vhidden, int d,
+                         float *__restrict__ chain, int depth, int flags) {
+    accept_body(ctl, vhidden, d, chain, depth, flags);
+}
+
+// The finished round into hist; the next round's anchor (op 1 below).
+__device__ __forceinline__ void next_round(DevCtl *ctl, RoundRec *hist, int hist_cap) {
+    if (hist && ctl->round < hist_cap) {
+        RoundRec *r = hist + ctl->round;
+        r->n_accept = ctl->n_accept;
+        r->k_eff = ctl->k_eff;
+        r->new_pos = ctl->new_pos;
+        r->ssm_slot = ctl->ssm_slot;
+        r->experts = ctl->expert_tally;
+        for (int j = 0; j < 8; j++) r->out[j] = ctl->out[j];
+    }
+    ctl->expert_tally = 0;
+    ctl->round++;
+    ctl->anchor = ctl->out[ctl->n_accept];
+    ctl->anchor_pos = ctl->new_pos;
+    ctl->mtp_pos = ctl->mtp_pos_next;
+    ctl->slot_base = ctl->ssm_slot;
+    ctl->tok[0] = ctl->anchor;
+}
+
 // Round bookkeeping on the device.  op 0: draft input 0 = anchor.  op 1:
 // record the finished round in hist and advance to the next one as the
 // generation driver does with have_seed (src/generate.c:1850-1866,
@@ -322,23 +347,66 @@ __global__ void k_set_tokens(DevCtl *ctl, int op, RoundRec *hist, int hist_cap) 
         ctl->n_accept = ctl->k_eff;
         ctl->smp_done = 0;
     } else if (op == 1) {
-        if (hist && ctl->round < hist_cap) {
-            RoundRec *r = hist + ctl->round;
-            r->n_accept = ctl->n_accept;
-            r->k_eff = ctl->k_eff;
-            r->new_pos = ctl->new_pos;
-            r->ssm_slot = ctl->ssm_slot;
-            r->experts = ctl->expert_tally;
-            for (int j = 0; j < 8; j++) r->out[j] = ctl->out[j];
-        }
-        ctl->expert_tally = 0;
-        ctl->round++;
-        ctl->anchor = ctl->out[ctl->n_accept];
-        ctl->anchor_pos = ctl->new_pos;
-        ctl->mtp_pos = ctl->mtp_pos_next;
-        ctl->slot_base = ctl->ssm_slot;
-        ctl->tok[0] = ctl->anchor;
+        next_round(ctl, hist, hist_cap);
     }
+}
+
+// ------------------------------------------------- session batch rounds ---
+//
+// A batch of sessions' greedy rounds as many-row passes: block r works for
+// session r (its BatchSess entry).  Draft step j reads each session's input
+// token tok[j] and chain into rows (k_batch_draft_in) and writes the rows'
+// argmaxes and exit-norm rows back (k_batch_draft_out); the verify's token
+// rows come from tok[0..K1), at positions anchor_pos + 1 + t (the first of
+// them into pos_scratch, k_batch_verify_in); k_batch_accept takes each session's K1 argmaxes as
+// targ and runs k_accept's acceptance on its hidden rows; the catch-up rows
+// are (hidden row j, catch_tok[j]) for j < k-1 (k_batch_catch_in); then
+// each session's round record and advance (k_batch_next).
+
+__global__ __launch_bounds__(256) void k_batch_draft_in(const BatchSess *__restrict__ bs, int j, int d,
+                                                        int *__restrict__ toks, float *__restrict__ h) {
+    const BatchSess b = bs[blockIdx.x];
+    if (threadIdx.x == 0) toks[blockIdx.x] = b.ctl->tok[j];
+    for (int i = threadIdx.x; i < d; i += 256) h[(size_t)blockIdx.x * d + i] = b.chain[i];
+}
+
+__global__ __launch_bounds__(256) void k_batch_draft_out(const BatchSess *__restrict__ bs, int j, int d,
+                                                         const int *__restrict__ am, const float *__restrict__ h) {
+    const BatchSess b = bs[blockIdx.x];
+    if (threadIdx.x == 0) b.ctl->tok[j + 1] = am[blockIdx.x];
+    for (int i = threadIdx.x; i < d; i += 256) b.chain[i] = h[(size_t)blockIdx.x * d + i];
+}
+
+__global__ __launch_bounds__(64) void k_batch_verify_in(const BatchSess *__restrict__ bs, int K1,
+                                                        int *__restrict__ toks) {
+    const BatchSess b = bs[blockIdx.x];
+    if ((int)threadIdx.x < K1) toks[blockIdx.x * K1 + threadIdx.x] = b.ctl->tok[threadIdx.x];
+    if (threadIdx.x == 0) b.ctl->pos_scratch = b.ctl->anchor_pos + 1;      // the anchor's row follows anchor_pos
+}
+
+__global__ __launch_bounds__(256) void k_batch_accept(const BatchSess *__restrict__ bs, int K1, const int *__restrict__ am,
+                                                      const float *__restrict__ vh, int d) {
+    const BatchSess b = bs[blockIdx.x];
+    if ((int)threadIdx.x < K1) b.ctl->targ[threadIdx.x] = am[blockIdx.x * K1 + threadIdx.x];
+    __syncthreads();
+    accept_body(b.ctl, vh + (size_t)blockIdx.x * K1 * d, d, b.chain, b.depth, 0);
+}
+
+__global__ __launch_bounds__(256) void k_batch_catch_in(const BatchSess *__restrict__ bs, int K1, int nc, int d,
+                                                        const float *__restrict__ vh, int *__restrict__ toks,
+                                                        float *__restrict__ h) {
+    const BatchSess b = bs[blockIdx.x];
+    if ((int)threadIdx.x < nc) toks[blockIdx.x * nc + threadIdx.x] = b.ctl->catch_tok[threadIdx.x];
+    for (int f = threadIdx.x; f < nc * d; f += 256) {
+        const int j = f / d, i = f - j * d;
+        h[((size_t)blockIdx.x * nc + j) * d + i] = vh[((size_t)blockIdx.x * K1 + j) * d + i];
+    }
+}
+
+__global__ void k_batch_next(const BatchSess *__restrict__ bs) {
+    if (threadIdx.x != 0) return;
+    const BatchSess b = bs[blockIdx.x];
+    next_round(b.ctl, b.hist, b.hist_cap);
 }
 
 // ---------------------------------------------------------- host glue ---
@@ -435,7 +503,7 @@ extern "C" int l98k_dspark_pre(const int8_t *emb_q, const float *emb_s, int gs, 
 }
 
 extern "C" int l98k_argmax(const float *x, int n, int rows, int mode, int *out, hipStream_t st) {
-    if (rows < 1 || rows > LZ_ARGMAX_ROWS || n < 1) return -1;
+    if (rows < 1 || rows > 65535 || n < 1) return -1;
     hipLaunchKernelGGL(k_argmax, dim3(rows), dim3(ARGMAX_THREADS), 0, st, x, n, mode, out);
     return (int)hipGetLastError();
 }
@@ -564,5 +632,20 @@ __global__ __launch_bounds__(128) void k_put_ctl(const DevCtl *__restrict__ src,
 extern "C" int l98k_put_ctl(const DevCtl *src, DevCtl *const *dst, int n, hipStream_t st) {
     if (n < 1) return -1;
     hipLaunchKernelGGL(k_put_ctl, dim3(n), dim3(128), 0, st, src, dst);
+    return (int)hipGetLastError();
+}
+
+extern "C" int l98k_batch_round(int op, const BatchSess *bs, int n, int j, int K1, int nc, int d, const int *am,
+                                const float *rows, int *toks, float *h, hipStream_t st) {
+    if (n < 1 || K1 < 1 || K1 > 16 || nc < 0 || nc > 8) return -1;
+    switch (op) {
+    case 0: hipLaunchKernelGGL(k_batch_draft_in, dim3(n), dim3(256), 0, st, bs, j, d, toks, h); break;
+    case 1: hipLaunchKernelGGL(k_batch_draft_out, dim3(n), dim3(256), 0, st, bs, j, d, am, rows); break;
+    case 2: hipLaunchKernelGGL(k_batch_verify_in, dim3(n), dim3(64), 0, st, bs, K1, toks); break;
+    case 3: hipLaunchKernelGGL(k_batch_accept, dim3(n), dim3(256), 0, st, bs, K1, am, rows, d); break;
+    case 4: hipLaunchKernelGGL(k_batch_catch_in, dim3(n), dim3(256), 0, st, bs, K1, nc, d, rows, toks, h); break;
+    case 5: hipLaunchKernelGGL(k_batch_next, dim3(n), dim3(64), 0, st, bs); break;
+    default: return -1;
+    }
     return (int)hipGetLastError();
 }

@@ -126,6 +126,7 @@ int l98k_attn_t1(const float *qg, int qg_dim, const float *vp, int kv_dim, int n
 // Attention of several sessions' rows in one launch per kernel (items in
 // device memory); att: n_items blocks of att_item floats.  kv_cached: every
 // row's K and V are already in the cache (a prefill after its K/V launch).
+int l98k_attn_prep_items(const AttnArgs *a, const AttnItem *items, int n_items, int plane, hipStream_t st);
 int l98k_attn_items(const AttnArgs *a, const AttnItem *items, int n_items, int plane, int max_len, int nmax,
                     float *att, size_t att_item, int kv_cached, hipStream_t st);
 // Attention of nt tokens (positions *ctl_pos + pos_off + t) against the KV
@@ -167,6 +168,11 @@ int l98k_argmax_part(const unsigned long long *part, int tiles, const float *x, 
 int l98k_accept(DevCtl *ctl, const float *vhidden, int d, float *chain, int depth, int flags, hipStream_t st);
 int l98k_set_tokens(DevCtl *ctl, int op, RoundRec *hist, int hist_cap, hipStream_t st);
 int l98k_put_ctl(const DevCtl *src, DevCtl *const *dst, int n, hipStream_t st);
+// Session-batch round control (op 0 draft rows in, 1 draft argmaxes and
+// chains out, 2 verify rows in, 3 acceptance, 4 catch-up rows in, 5 round
+// record and advance), block r for session r.
+int l98k_batch_round(int op, const BatchSess *bs, int n, int j, int K1, int nc, int d, const int *am,
+                     const float *rows, int *toks, float *h, hipStream_t st);
 // Launch-floor probes: `launches` dependent launches of an empty kernel
 // (kind 0) or of a kernel whose `grid` blocks each read the n floats the
 // previous launch wrote (kind 1, buffers a and b alternating; 256 <= n <=

@@ -109,3 +109,53 @@ def test_verify_batch_32_sessions_ragged_contexts(pkg, server):
         for st in batch + single:
             eng.free_session(st)
         eng.close()
+
+
+@pytest.fixture(scope="module")
+def echo_model(pkg, model_root):
+    import os
+    return pkg.ensure_model(os.path.join(model_root, "echo"), 11, seed=1234)
+
+
+@pytest.mark.parametrize("which", ["server", "echo"])
+def test_batched_rounds_match_per_session_graphs(pkg, server, echo_model, which):
+    """The batched rounds (each draft step one many-row pass over the
+    sessions, one many-row verify, the acceptance and catch-up as one launch
+    each) emit exactly what each session's own round graph emits; on the echo
+    model, whose drafts are accepted, that covers the acceptance, the ring
+    rollback and the catch-up.  The first session's tokens are also checked
+    against the CPU restatement's generation."""
+    model = server if which == "server" else echo_model
+    print(f"[case] batched rounds vs per-session graphs, {which} model", flush=True)
+    lens = [24, 41, 30, 52, 19, 33]
+    k, n_rounds = 3, 10
+    engs = [pkg.Engine(model), pkg.Engine(model)]
+    V = engs[0].V
+    assert engs[0].lib.l98_batched_rounds_ok(pkg.C.byref(engs[0].m), len(lens), k) == 1
+    groups = [[], []]
+    try:
+        outs, firsts = [], []
+        for g, eng in enumerate(engs):
+            for i, n in enumerate(lens):
+                st = eng.add_session()
+                f = eng.session_start_on(st, pkg.prompt_tokens(300 + i, n, V))
+                if g == 0:
+                    firsts.append(f)
+                groups[g].append(st)
+            outs.append(eng.greedy_rounds_batch(groups[g], k, n_rounds, mode=g)[1])
+        accepted = 0
+        for i in range(len(lens)):
+            assert np.array_equal(outs[0][i], outs[1][i]), (i, outs[0][i], outs[1][i])
+            accepted += len(outs[0][i]) - n_rounds
+        if which == "echo":
+            assert accepted > 0
+        prompt = pkg.prompt_tokens(300, lens[0], V)
+        want = Oracle(model).generate(prompt, k, len(outs[0][0]) + 1)[0]
+        got = np.concatenate([[firsts[0]], outs[0][0]])
+        m = min(len(got), len(want))
+        assert m > n_rounds and np.array_equal(got[:m], want[:m])
+    finally:
+        for g, eng in enumerate(engs):
+            for st in groups[g]:
+                eng.free_session(st)
+            eng.close()

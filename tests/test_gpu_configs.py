@@ -128,3 +128,31 @@ def test_configs1_verify_of_eight_rows_equals_single_steps(pkg, base):
     finally:
         a.close()
         b.close()
+
+
+def test_configs4_batched_rounds_match_per_session_graphs(pkg, xlserver):
+    """configs[4]'s 32 sessions through the batched rounds (every draft step
+    one 32-row pass, one 128-row verify) emit what each session's own round
+    graph emits."""
+    print("[case] configs[4]: batched rounds vs per-session round graphs, 32 sessions", flush=True)
+    k, n_rounds = 3, 4
+    rng = np.random.default_rng(5)
+    ctx = rng.integers(256, 2049, size=32)
+    engs = [pkg.Engine(xlserver), pkg.Engine(xlserver)]
+    assert engs[0].lib.l98_batched_rounds_ok(C.byref(engs[0].m), 32, k) == 1
+    groups = [[], []]
+    try:
+        outs = []
+        for g, eng in enumerate(engs):
+            for i, n in enumerate(ctx):
+                st = eng.add_session()
+                eng.session_start_on(st, pkg.prompt_tokens(5000 + i, int(n), eng.V))
+                groups[g].append(st)
+            outs.append(eng.greedy_rounds_batch(groups[g], k, n_rounds, mode=g)[1])
+        for i in range(32):
+            assert np.array_equal(outs[0][i], outs[1][i]), (i, outs[0][i], outs[1][i])
+    finally:
+        for g, eng in enumerate(engs):
+            for st in groups[g]:
+                eng.free_session(st)
+            eng.close()
