@@ -165,8 +165,25 @@ __device__ __forceinline__ bool xp_near(float A, float An) {
 // Each pass reads the thread's elements XP_BATCH at a time, every load of a
 // batch issued before the first use.
 #define XP_BATCH 8
+// vec: the row is 16-byte aligned and CH a multiple of 4, so a batch is
+// four 16-byte loads per thread (XP_BATCH * 2 elements)
 template <class G, class F>
-__device__ __forceinline__ void xp_walk(const G &get, int i0, int CH, const bool &stop, F f) {
+__device__ __forceinline__ void xp_walk(const G &get, int i0, int CH, bool vec, const bool &stop, F f) {
+    if (vec) {
+        constexpr int B = 2 * XP_BATCH;
+        for (int k0 = 0; k0 < CH && !stop; k0 += B) {
+            float4 v[B / 4];
+#pragma unroll
+            for (int u = 0; u < B / 4; u++) v[u] = get.clamped4(i0 + k0 + 4 * u);  // past the chunk: ignored
+#pragma unroll
+            for (int u = 0; u < B; u++) {
+                const float x = (u & 3) == 0 ? v[u >> 2].x : (u & 3) == 1 ? v[u >> 2].y : (u & 3) == 2 ? v[u >> 2].z
+                                                                                                    : v[u >> 2].w;
+                if (k0 + u < CH && !stop) f(k0 + u, x);
+            }
+        }
+        return;
+    }
     for (int k0 = 0; k0 < CH && !stop; k0 += XP_BATCH) {
         float v[XP_BATCH];
 #pragma unroll
@@ -185,12 +202,14 @@ __device__ __forceinline__ void xprefix(const G &get, int n, int mode, float c, 
         __syncthreads();
         return;
     }
-    const int CH = (n + SMP_THREADS - 1) / SMP_THREADS;
+    // a multiple of 4 (threads past the row hold zeros, which leave every
+    // prefix as it is)
+    const int CH = (((n + SMP_THREADS - 1) / SMP_THREADS) + 3) & ~3;
     const int i0 = tid * CH;
-    const bool never = false;
+    const bool never = false, vec = get.aligned();
     // approximate prefix (the binade guesses)
     float T = 0.0f;
-    xp_walk(get, i0, CH, never, [&](int, float x) { T += x; });
+    xp_walk(get, i0, CH, vec, never, [&](int, float x) { T += x; });
     const float incl = blk_incl_f32(T, L);
     L.incl[tid] = incl;
     if (tid == 0) { L.K = 0; L.fail = 0; }
@@ -202,7 +221,7 @@ __device__ __forceinline__ void xprefix(const G &get, int n, int mode, float c, 
     {
         float A = off;
         int E0 = f_binade(off);
-        xp_walk(get, i0, CH, never, [&](int k, float x) {
+        xp_walk(get, i0, CH, vec, never, [&](int k, float x) {
             const int i = i0 + k;
             const float An = (k == CH - 1) ? incl : A + x;
             const int E1 = f_binade(An);
@@ -332,7 +351,7 @@ __device__ __forceinline__ void xprefix(const G &get, int n, int mode, float c, 
         uint32_t rk = L.cnt_ex[tid];
         unsigned long long qp = L.q_ex[tid];
         bool found = false;
-        xp_walk(get, i0, CH, found, [&](int k, float x) {
+        xp_walk(get, i0, CH, vec, found, [&](int k, float x) {
             const int i = i0 + k;
             const float An = (k == CH - 1) ? incl : A + x;
             const int E1 = f_binade(An);
@@ -367,6 +386,8 @@ __device__ __forceinline__ void xprefix(const G &get, int n, int mode, float c, 
 // Row accessors: operator() reads element i (0 past n); clamped(i) reads
 // it with the index clamped into the row and selects 0 past n, a load with
 // no branch, so a thread's loads can all be in flight together.
+// clamped4(i), i a multiple of 4: elements i .. i+3 (0 past n), one 16-byte
+// load inside the row; aligned(): the row's base allows those loads.
 struct GetArr {
     const float *x;
     int n;
@@ -375,6 +396,11 @@ struct GetArr {
         const float v = x[imin(i, n - 1)];
         return i < n ? v : 0.0f;
     }
+    __device__ float4 clamped4(int i) const {
+        if (i + 3 < n) return *reinterpret_cast<const float4 *>(x + i);
+        return make_float4(clamped(i), clamped(i + 1), clamped(i + 2), clamped(i + 3));
+    }
+    __device__ bool aligned() const { return ((uintptr_t)x & 15) == 0; }
 };
 struct GetResid {                        // max(p - q, 0) (sample_residual's dd > 0 terms)
     const float *p, *q;
@@ -389,6 +415,16 @@ struct GetResid {                        // max(p - q, 0) (sample_residual's dd 
         const float dd = p[ic] - q[ic];
         return i < n && dd > 0.0f ? dd : 0.0f;
     }
+    __device__ float4 clamped4(int i) const {
+        if (i + 3 < n) {
+            const float4 a = *reinterpret_cast<const float4 *>(p + i), b = *reinterpret_cast<const float4 *>(q + i);
+            const float dx = a.x - b.x, dy = a.y - b.y, dz = a.z - b.z, dw = a.w - b.w;
+            return make_float4(dx > 0.0f ? dx : 0.0f, dy > 0.0f ? dy : 0.0f, dz > 0.0f ? dz : 0.0f,
+                               dw > 0.0f ? dw : 0.0f);
+        }
+        return make_float4(clamped(i), clamped(i + 1), clamped(i + 2), clamped(i + 3));
+    }
+    __device__ bool aligned() const { return (((uintptr_t)p | (uintptr_t)q) & 15) == 0; }
 };
 struct GetKeys {                         // probabilities from sorted order-preserving keys
     const uint32_t *k;
@@ -398,6 +434,14 @@ struct GetKeys {                         // probabilities from sorted order-pres
         const float v = __uint_as_float(k[imin(i, n - 1)]);
         return i < n ? v : 0.0f;
     }
+    __device__ float4 clamped4(int i) const {
+        if (i + 3 < n) {
+            const uint4 u = *reinterpret_cast<const uint4 *>(k + i);
+            return make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w));
+        }
+        return make_float4(clamped(i), clamped(i + 1), clamped(i + 2), clamped(i + 3));
+    }
+    __device__ bool aligned() const { return ((uintptr_t)k & 15) == 0; }
 };
 
 // first index of the largest value (order-preserving key, strict >)
@@ -428,6 +472,7 @@ __global__ __launch_bounds__(SMP_THREADS) void k_smp_softmax(const float *__rest
     const int tid = threadIdx.x;
     if (tid < 32) tab[tid] = c_exp_tab[tid];
     uint32_t mk = 0u;
+#pragma unroll 8
     for (int i = tid; i < n; i += SMP_THREADS) {
         const float s = logits[i] * inv_t;
         probs[i] = s;
@@ -435,12 +480,14 @@ __global__ __launch_bounds__(SMP_THREADS) void k_smp_softmax(const float *__rest
         mk = k > mk ? k : mk;
     }
     const float mx = d_unkey(blk_max_u32(mk, L));
+#pragma unroll 8
     for (int i = tid; i < n; i += SMP_THREADS) probs[i] = d_exp(probs[i] - mx, tab);
     __syncthreads();
     xprefix(GetArr{probs, n}, n, XP_TOTAL, 0.0f, L);
     const float sum = L.fres;
     const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
     uint32_t cnt = 0;
+#pragma unroll 8
     for (int i = tid; i < n; i += SMP_THREADS) {
         const float p = probs[i] * inv;
         probs[i] = p;
@@ -547,6 +594,7 @@ __global__ __launch_bounds__(SMP_THREADS) void k_smp_accept(const float *__restr
         return;
     }
     int lp = -1;
+#pragma unroll 8
     for (int i = tid; i < n; i += SMP_THREADS) if (p[i] - q[i] > 0.0f) lp = i;
     const int last_pos = (int)blk_max_u32((uint32_t)(lp + 1), L) - 1;
     if (tid == 0) L.fv = d_random_f32(rng) * total;
