@@ -1184,7 +1184,14 @@ int forward_chunk(DState *s, const int *toks, int nt, const int *ctl_pos, int po
     // other, since every block of that launch reads the input.
     float *xb[2] = {s->x, s->x2};
     int cur = 0;
-    const bool fused = l98k_gemv_norm_fits(d, nt) != 0;
+    // Every block of a fused launch normalizes all nt rows itself (reading
+    // the rows and their addends), so for several rows of d = 2048, or more
+    // than 4096 row elements, a norm kernel that quantizes the rows once,
+    // then GEMVs of pre-quantized rows, is faster (measured on the d = 2048
+    // verify: 4.25 -> 3.82 ms at 4 rows).  SubLN's per-projection norms only
+    // run fused.
+    const bool fused = l98k_gemv_norm_fits(d, nt) != 0 &&
+                       (c.use_subn || ((size_t)nt * d <= 4096 && (d <= 1024 || nt == 1)));
     if (c.use_subn && !fused) return -1;      // SubLN's per-projection norms run in the GEMV prologues
     CK(l98k_embed(m->embed.q, m->embed.s, toks, d, m->embed.gs, nt, xb[cur], s->st));
     const float *ra = nullptr, *rb = nullptr;     // pending residual of the previous block
