@@ -290,6 +290,113 @@ __global__ __launch_bounds__(MF_THREADS) void k_mfma_q8(const int8_t *__restrict
 #undef MF_STAGE_LOAD
 #undef MF_STAGE_PUT
 
+// The grouped form for small groups (expert GEMMs over a batched verify's
+// few pairs per expert): a block computes 64 weight rows x 16 token
+// columns (wave w: rows 16 w .. 16 w + 15, the same 16 columns), so each
+// block streams four times the weights of k_mfma_q8's 16-row tile and
+// stages only the 16 columns it uses; a group's column tiles spread over
+// the grid's y.  Same stages, MFMAs and fold per
+// (row, column) as k_mfma_q8, so the same bits.
+#define MFN_ROWS 64
+#define MFN_COLS 16
+template <bool FULLK>
+__global__ __launch_bounds__(MF_THREADS) void k_mfma_q8n(const int8_t *__restrict__ W, const float *__restrict__ ws,
+                                                          int N, int K, size_t w_group_stride,
+                                                          const int8_t *__restrict__ X, const float *__restrict__ Xs,
+                                                          MfCols cols, float *__restrict__ out, int out_stride) {
+    __shared__ __align__(16) int8_t s_w[2][MFN_ROWS][MF_LDS_ROW];
+    __shared__ __align__(16) int8_t s_x[2][MFN_COLS][MF_LDS_ROW];
+    __shared__ __align__(16) float s_xs[2][MFN_COLS][MF_KC / 32];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int g = blockIdx.z;
+    if (g >= *cols.ng) return;
+    const int ncols = cols.gcnt[g], cbase = cols.goff[g], e = cols.gexp[g];
+    const int8_t *Wg = W + (size_t)e * w_group_stride;
+    const float *wsg = ws + (size_t)e * N;
+    const int n0 = blockIdx.x * MFN_ROWS, nb = K >> 5;
+    const int pc = tid & 15, rr = tid >> 4;
+    auto wrow = [&](int j) { const int r = n0 + rr + 16 * j; return Wg + (size_t)(r < N ? r : N - 1) * K; };
+    const int8_t *wl0 = wrow(0), *wl1 = wrow(1), *wl2 = wrow(2), *wl3 = wrow(3);
+    const int kq = 8 * (lane >> 4);
+    // column tiles blockIdx.y, + gridDim.y, ... (the few large groups of a
+    // skewed routing spread over gridDim.y blocks; the others' extra blocks
+    // exit here)
+#pragma unroll 1
+    for (int c0 = blockIdx.y * MFN_COLS; c0 < ncols; c0 += gridDim.y * MFN_COLS) {
+        auto xrow = [&](int c) {
+            const int o = cols.list[cbase + imin(c0 + c, ncols - 1)];
+            return cols.xmap ? cols.xmap[o] : o;
+        };
+        const int8_t *xl0 = X + (size_t)xrow(rr) * K;                  // column rr's piece pc
+        const float *xsl = Xs + (size_t)xrow(tid >> 2) * nb;            // threads < 64: column tid / 4
+        const int cl = c0 + (lane & 15);
+        const int nst = (K + MF_KC - 1) / MF_KC;
+        int4 w0, w1, w2, w3, x0;
+        float t0 = 0.0f, t1 = 0.0f;
+        auto load = [&](int st) {
+            const int off = imin(st * MF_KC + 16 * pc, K - 16);
+            w0 = *reinterpret_cast<const int4 *>(wl0 + off);
+            w1 = *reinterpret_cast<const int4 *>(wl1 + off);
+            w2 = *reinterpret_cast<const int4 *>(wl2 + off);
+            w3 = *reinterpret_cast<const int4 *>(wl3 + off);
+            x0 = *reinterpret_cast<const int4 *>(xl0 + off);
+            if (tid < 64) {
+                const int gg = st * (MF_KC / 32) + 2 * (tid & 3);
+                t0 = xsl[imin(gg, nb - 1)];
+                t1 = xsl[imin(gg + 1, nb - 1)];
+            }
+        };
+        auto put = [&](int b) {
+            *reinterpret_cast<int4 *>(&s_w[b][rr][16 * pc]) = w0;
+            *reinterpret_cast<int4 *>(&s_w[b][rr + 16][16 * pc]) = w1;
+            *reinterpret_cast<int4 *>(&s_w[b][rr + 32][16 * pc]) = w2;
+            *reinterpret_cast<int4 *>(&s_w[b][rr + 48][16 * pc]) = w3;
+            *reinterpret_cast<int4 *>(&s_x[b][rr][16 * pc]) = x0;
+            if (tid < 64) *reinterpret_cast<float2 *>(&s_xs[b][tid >> 2][2 * (tid & 3)]) = make_float2(t0, t1);
+        };
+        float f[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        const bool one = nb == 1;
+        float s0 = 0.0f;
+        load(0);
+        put(0);
+        __syncthreads();
+#pragma unroll 1
+        for (int st = 0; st < nst; st++) {
+            const int buf = st & 1;
+            const float *sc = s_xs[buf][lane & 15];
+            load(st + 1 < nst ? st + 1 : st);
+            __builtin_amdgcn_sched_barrier(0);
+            const v4i_t zero = {0, 0, 0, 0};
+            const int ng = FULLK ? MF_KC / 32 : nb - st * (MF_KC / 32);
+#pragma unroll
+            for (int gl = 0; gl < MF_KC / 32; gl++) {
+                if (!FULLK && gl >= ng) break;                     // uniform
+                const long b = *reinterpret_cast<const long *>(&s_x[buf][lane & 15][32 * gl + kq]);
+                const long a = *reinterpret_cast<const long *>(&s_w[buf][16 * wave + (lane & 15)][32 * gl + kq]);
+                const v4i_t dd = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, zero, 0, 0, 0);
+                mf_fold(f, dd, sc[gl], one);
+            }
+            if (!FULLK && one) s0 = sc[0];
+            put(buf ^ 1);
+            __syncthreads();
+        }
+        if (cl < ncols) {
+            float *op = out + (size_t)cols.list[cbase + cl] * out_stride;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int n = n0 + 16 * wave + 4 * (lane >> 4) + v;
+                if (n < N) {
+                    float sum = 0.0f;
+                    if (one) sum = epi_one_group((int)f[v], s0, wsg[n]);
+                    else sum += f[v] * wsg[n];
+                    op[n] = sum;
+                }
+            }
+        }
+    }
+}
+
+
 // ------------------------------------------------------ wide producers ---
 //
 // The quantized GEMM inputs of many rows, one 64-lane block per row, with
@@ -401,12 +508,25 @@ extern "C" int l98k_mfma_gemm_multi(int n_jobs, const int8_t *const *W, const fl
 
 // Grouped (experts): group g (< *ng <= max_groups) multiplies bank rows of
 // expert gexp[g] with its columns list[goff[g] ..], at most max_cols each.
+// Groups of about 16 columns or fewer (mean_cols, the caller's estimate)
+// take the 64-row x 16-column tiles, larger ones the 16 x 64 tiles.
 extern "C" int l98k_mfma_gemm_grouped(const int8_t *bank, const float *bank_s, int N, int K, const int8_t *X,
                                       const float *Xs, const int *ng, int max_groups, const int *gexp,
                                       const int *goff, const int *gcnt, const int *list, const int *xmap,
-                                      int max_cols, float *out, int out_stride, hipStream_t st) {
+                                      int max_cols, int mean_cols, float *out, int out_stride, hipStream_t st) {
     if (N < 1 || K < 32 || (K & 31) || max_groups < 1 || max_cols < 1 || out_stride < N) return -1;
     MfCols c{gexp, goff, gcnt, list, xmap, ng};
+    if (mean_cols <= MFN_COLS) {
+        const int ys = max_cols > 3 * MFN_COLS ? 4 : (max_cols + MFN_COLS - 1) / MFN_COLS;
+        const dim3 gridn((N + MFN_ROWS - 1) / MFN_ROWS, ys, max_groups);
+        if (K % MF_KC == 0)
+            hipLaunchKernelGGL(k_mfma_q8n<true>, gridn, dim3(MF_THREADS), 0, st, bank, bank_s, N, K, (size_t)N * K, X,
+                               Xs, c, out, out_stride);
+        else
+            hipLaunchKernelGGL(k_mfma_q8n<false>, gridn, dim3(MF_THREADS), 0, st, bank, bank_s, N, K, (size_t)N * K,
+                               X, Xs, c, out, out_stride);
+        return (int)hipGetLastError();
+    }
     const dim3 grid((N + MF_ROWS - 1) / MF_ROWS, 1, max_groups);
     if (K % MF_KC == 0)
         hipLaunchKernelGGL(k_mfma_q8<true>, grid, dim3(MF_THREADS), 0, st, bank, bank_s, N, K, (size_t)N * K, X, Xs, 0,

@@ -28,10 +28,12 @@ int l98k_mfma_gemm_multi(int n_jobs, const int8_t *const *W, const float *const 
                          hipStream_t st);
 // Grouped over experts: group g < *ng multiplies expert gexp[g]'s bank rows
 // with its columns list[goff[g] .. + gcnt[g]] (activation row xmap[col] or
-// col, output row col).
+// col, output row col).  mean_cols, the host's estimate of the columns per
+// group, picks the tile shape (the same bits either way).
 int l98k_mfma_gemm_grouped(const int8_t *bank, const float *bank_s, int N, int K, const int8_t *X, const float *Xs,
                            const int *ng, int max_groups, const int *gexp, const int *goff, const int *gcnt,
-                           const int *list, const int *xmap, int max_cols, float *out, int out_stride, hipStream_t st);
+                           const int *list, const int *xmap, int max_cols, int mean_cols, float *out, int out_stride,
+                           hipStream_t st);
 // Quantized GEMM inputs of `rows` rows: mode 0 quantize, 1 silu(src)*src2,
 // 2 slot-ordered expert combine; the GEMV prologues' arithmetic.
 int l98k_wide_pro(int mode, const float *src, const float *src2, int src_stride, const int *sel_idx,
