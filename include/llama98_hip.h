@@ -303,6 +303,16 @@ int l98_greedy_rounds_batch_ex(const LZModel *m, LZRunState **states, int n_seq,
 /* 1 when l98_greedy_rounds_batch runs n_seq sessions of this model at
  * draft width k as batched rounds, else 0. */
 int l98_batched_rounds_ok(const LZModel *m, int n_seq, int k);
+/* The attention path of a session's chunk (verify, draft step, capture
+ * chunk): 0 chosen by the session's capacity (past 2048 positions two
+ * launches: the scores of every 64-position slice, kv head and token, then
+ * the softmax and value chains of every (q head, token, 32-wide output
+ * group); else one launch per (q head, token)); 1 always the one launch;
+ * 2 the two launches wherever their LDS fits.  Both give the same bits.
+ * Process-wide; applies to launches enqueued and graphs captured
+ * afterwards.  No counterpart in the reference (a tuning and test
+ * control). */
+void l98_set_attn_path(int mode);
 /* Mean duration of `iters` launches, hipEvent-timed on the state's stream.
  * which = 0: the tied lm_head GEMV with mrows token rows, back to back;
  * 1: the verify forward of mrows tokens; 2: a device copy of the lm_head's

@@ -139,6 +139,7 @@ HIP_API = [
     ("l98_greedy_rounds_batch_ex", C.c_int, [C.POINTER(LZModel), C.POINTER(C.POINTER(LZRunState)), C.c_int,
                                              C.c_int, C.c_int, _IP, C.c_int, _IP, _FP, C.c_int]),
     ("l98_batched_rounds_ok", C.c_int, [C.POINTER(LZModel), C.c_int, C.c_int]),
+    ("l98_set_attn_path", None, [C.c_int]),
     ("l98_row_sums", C.c_int, [_FP, C.c_int, C.c_int, _FP]),
     ("l98_fwht_i32", C.c_int, [_IP, _IP, C.c_int, C.c_int, C.c_int]),
     ("l98_fwht_f32", C.c_int, [_FP, C.c_int, C.c_int, C.c_int, C.c_int]),
@@ -188,6 +189,14 @@ def hip_lib(path=HIP_LIB):
             f.argtypes = args
         _hip = lib
     return _hip
+
+
+def set_attn_path(mode):
+    """The attention path of a session's chunk for launches and graph
+    captures from now on (l98_set_attn_path): 0 by the session's capacity,
+    1 one launch per (q head, token), 2 scores by position slice, then the
+    softmax and value chains per (q head, token, 32-wide group)."""
+    hip_lib().l98_set_attn_path(int(mode))
 
 
 def synth_lib():

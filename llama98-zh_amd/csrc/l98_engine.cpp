@@ -3561,6 +3561,8 @@ extern "C" int l98_batched_rounds_ok(const LZModel *mm, int n_seq, int k) {
     return batched_rounds_ok(Mo(mm), n_seq, k) && wide_get(Mo(mm)) != nullptr ? 1 : 0;
 }
 
+extern "C" void l98_set_attn_path(int mode) { l98k_set_attn_path(mode); }
+
 extern "C" int l98_greedy_rounds_batch(const LZModel *mm, LZRunState **states, int n_seq, int k, int n_rounds,
                                        int *tokens, int cap, int *n_out, float *wall_ms) {
     return l98_greedy_rounds_batch_ex(mm, states, n_seq, k, n_rounds, tokens, cap, n_out, wall_ms, 0);

@@ -626,6 +626,196 @@ __global__ __launch_bounds__(AV_THREADS) void k_attn_av_items(AttnArgs b, const 
     attn_av_body<CH>(a, att + (size_t)item * att_item, att_stride, sc, blockIdx.x, t);
 }
 
+// The chunk path of one session at long contexts, in two launches instead
+// of k_attn_fused's single block per (q head, token), which walks every
+// position's score, the softmax's serial sum and the value chains on one CU:
+//   k_attn_scores_chunk: one block per (64-position slice, kv head, token),
+//     attn_scores_body: the kv_mul q heads and the slice's new K rows
+//     prepared in the block, the scores into att, the new K and V rows into
+//     the cache by their own token's block;
+//   k_attn_avg<HD>: one block per (q head, token, 32-wide output group):
+//     the token's score row, the softmax (max by order-preserving key, exp,
+//     the serial loop's sum by the exact wave sum over segments of AG_SEG
+//     values, each segment's sum entering the next as its first element,
+//     scale), then the group's 32 value chains in position order: four
+//     producer waves form (a * v) * vs for AG_CH positions at a time into a
+//     double buffer while lanes 0-31 of wave 0 add the previous AG_CH, the
+//     producers' V loads running AG_NPF chunks ahead (the first ones issued
+//     before the softmax); then the gate and the group's quantization.
+// The arithmetic is attn_av_body's, so the bits are k_attn_fused's.
+#define AG_CH 128
+#define AG_PAD (AG_CH + 4)
+#define AG_NPF 4
+#define AG_THREADS 320
+#define AG_SEG 2047
+__global__ __launch_bounds__(256) void k_attn_scores_chunk(AttnArgs a, float *att, int att_stride) {
+    attn_scores_body(a, att, att_stride, blockIdx.x, blockIdx.y, blockIdx.z);
+}
+
+// Dynamic LDS of k_attn_avg: the product double buffer, the score row
+// (att_stride floats), the exact sum's segment rows.
+__host__ __device__ inline int ag_segments(int att_stride) { return (att_stride + AG_SEG - 1) / AG_SEG; }
+__host__ __device__ inline size_t ag_lds_bytes(int att_stride) {
+    return (2 * 32 * AG_PAD + (size_t)((att_stride + 3) & ~3) + (size_t)ag_segments(att_stride) * ps_row_floats<32>()) *
+           sizeof(float);
+}
+
+template <int HD>
+__global__ __launch_bounds__(AG_THREADS) void k_attn_avg(AttnArgs a, const float *__restrict__ att, int att_stride) {
+    EXP_TAB_LOAD(tab);
+    extern __shared__ __align__(16) char smem[];
+    __shared__ uint32_t s_red[AG_THREADS / 64];
+    __shared__ float s_inv;
+    __shared__ PsRec s_rec[128];
+    constexpr int NB = HD / 32, PSR = ps_row_floats<32>();
+    const int h = blockIdx.x, t = blockIdx.y, g = blockIdx.z;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int kvh = h / (a.nh / a.nkv);
+    const int L = *a.ctl_pos + a.pos_off + t + 1;
+    const int nch = (L + AG_CH - 1) / AG_CH, nseg = (L + AG_SEG - 1) / AG_SEG;
+    float *prod = reinterpret_cast<float *>(smem);                       // [2][32][AG_PAD]
+    float *s_a = prod + 2 * 32 * AG_PAD;                                  // [att_stride]
+    float *s_ps = s_a + ((att_stride + 3) & ~3);                          // [segments][PSR]
+    // producers: thread ptid takes position ptid / 2 of each chunk, bytes
+    // 16 (ptid % 2) .. +16 of the group
+    const bool prodw = wave >= 1;
+    const int ptid = tid - 64, pp = ptid >> 1, ph = ptid & 1;
+    const int8_t *vb = a.vcache + kvh * HD + 32 * g + 16 * ph;
+    const float *vsb = a.vscale + kvh * NB + g;
+    const size_t vst = (size_t)a.kv_dim, sst = (size_t)(a.kv_dim >> 5);
+    int4 r[AG_NPF];
+    float rs[AG_NPF];
+    // chunk c's piece into ring slot J (a constant after unrolling);
+    // positions past the row re-read its last one
+#define AG_LOAD(c_, J)                                                         \
+    do {                                                                       \
+        const int p_ = imin((c_) * AG_CH + pp, L - 1);                         \
+        r[J] = *reinterpret_cast<const int4 *>(vb + (size_t)p_ * vst);         \
+        rs[J] = vsb[(size_t)p_ * sst];                                         \
+    } while (0)
+    if (prodw) {
+#pragma unroll
+        for (int j = 0; j < AG_NPF; j++) AG_LOAD(j, j);
+    }
+    // the score row, its max by order-preserving key
+    const float *arow = att + ((size_t)t * a.nh + h) * att_stride;
+    uint32_t best = 0;
+    for (int p0 = 0; p0 < L; p0 += 4 * AG_THREADS) {
+        float x[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) x[u] = arow[imin(p0 + u * AG_THREADS + tid, L - 1)];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int p = p0 + u * AG_THREADS + tid;
+            if (p < L) {
+                s_a[p] = x[u];
+                best = umax(best, d_fkey(x[u]));
+            }
+        }
+    }
+    EXP_TAB_PUT(tab);
+    for (int o = 32; o > 0; o >>= 1) best = umax(best, (uint32_t)__shfl_xor((int)best, o));
+    if (lane == 0) s_red[wave] = best;
+    __syncthreads();
+    uint32_t bk = s_red[0];
+#pragma unroll
+    for (int w = 1; w < AG_THREADS / 64; w++) bk = umax(bk, s_red[w]);
+    const float mx = d_unkey(bk);
+    // exps, also into the segment rows (segment k: slot 0 the carried sum,
+    // slot 1 + i the value of position k * AG_SEG + i)
+    for (int p = tid; p < L; p += AG_THREADS) {
+        const float e = d_exp(s_a[p] - mx, tab);
+        s_a[p] = e;
+        const int k = p / AG_SEG, i = p - k * AG_SEG + 1;
+        s_ps[k * PSR + ps_slot<32>(i)] = e;
+    }
+    __syncthreads();
+    if (wave == 0) {                     // the serial loop's sum, bit for bit
+        float carry = 0.0f;
+        for (int k = 0; k < nseg; k++) {
+            float *row = s_ps + k * PSR;
+            if (lane == 0) row[0] = carry;
+            __builtin_amdgcn_s_waitcnt(0xC07F);       // lgkmcnt(0)
+            __builtin_amdgcn_wave_barrier();
+            carry = wave_sum_nonneg<32>(row, imin(AG_SEG, L - k * AG_SEG) + 1, s_rec);
+        }
+        if (lane == 0) s_inv = (carry > 0.0f) ? 1.0f / carry : 0.0f;
+    }
+    __syncthreads();
+    const float inv = s_inv;
+    for (int p = tid; p < L; p += AG_THREADS) s_a[p] *= inv;
+    __syncthreads();
+    // value chains
+    auto produce = [&](int c, int buf, int4 v4, float vsc) {
+        const int p = c * AG_CH + pp;
+        // past the row: a = 0, a product of +-0, which leaves the sum as it is
+        const float ap = p < L ? s_a[p] : 0.0f;
+        float *pb = prod + buf * 32 * AG_PAD + 16 * ph * AG_PAD + pp;
+        const int w4[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+        for (int i = 0; i < 16; i++) pb[i * AG_PAD] = ap * (float)(int8_t)((w4[i >> 2] >> (8 * (i & 3))) & 0xFF) * vsc;
+    };
+    const int d = lane & 31;
+    float o = 0.0f;
+    if (prodw) {
+        produce(0, 0, r[0], rs[0]);
+        AG_LOAD(AG_NPF, 0);
+    }
+    __syncthreads();
+#pragma unroll 1
+    for (int c0 = 0; c0 < nch; c0 += AG_NPF) {
+#pragma unroll
+        for (int j = 0; j < AG_NPF; j++) {
+            const int c = c0 + j;
+            if (c >= nch) break;                      // uniform
+            if (!prodw) {
+                // the chunk in quarters, each quarter's reads issued before
+                // the previous quarter's adds
+                const float4 *pr = reinterpret_cast<const float4 *>(prod + (c & 1) * 32 * AG_PAD + d * AG_PAD);
+                constexpr int QN = AG_CH / 16;
+                float4 q0[QN], q1[QN];
+#pragma unroll
+                for (int i = 0; i < QN; i++) q0[i] = pr[i];
+#pragma unroll
+                for (int qr = 0; qr < 4; qr += 2) {
+#pragma unroll
+                    for (int i = 0; i < QN; i++) q1[i] = pr[(qr + 1) * QN + i];
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int i = 0; i < QN; i++) { o += q0[i].x; o += q0[i].y; o += q0[i].z; o += q0[i].w; }
+                    if (qr + 2 < 4) {
+#pragma unroll
+                        for (int i = 0; i < QN; i++) q0[i] = pr[(qr + 2) * QN + i];
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int i = 0; i < QN; i++) { o += q1[i].x; o += q1[i].y; o += q1[i].z; o += q1[i].w; }
+                }
+            } else if (c + 1 < nch) {
+                const int jn = (j + 1) % AG_NPF;
+                produce(c + 1, (c + 1) & 1, r[jn], rs[jn]);
+                AG_LOAD(c + 1 + AG_NPF, jn);
+            }
+            __syncthreads();
+        }
+    }
+#undef AG_LOAD
+    if (prodw) return;
+    // gate, the group's quantization (lanes 32-63 repeat lanes 0-31 and store nothing)
+    const int dd = 32 * g + d;
+    const float gate = a.qg[(size_t)t * a.qg_dim + (size_t)h * 2 * HD + HD + dd];
+    o *= d_sigmoid(gate, tab);
+    const int col = h * HD + dd;
+    if (a.out && lane < 32) a.out[(size_t)t * a.q_dim + col] = o;
+    int8_t q;
+    float sg;
+    d_quant_group32(o, &q, &sg);
+    if (lane < 32) {
+        a.oq[(size_t)t * a.q_dim + col] = q;
+        if (lane == 0) a.oqs[(size_t)t * (a.q_dim >> 5) + (col >> 5)] = sg;
+    }
+}
+
 // k_attn_av_rows: the softmax and value sums of an item launch whose rows
 // all lie below position 512, for 64-wide heads: one block per (q head,
 // item), wave t = the item's token t, lane = output element d.  The item's
@@ -1278,6 +1468,13 @@ extern "C" int l98k_attn_prep_items(const AttnArgs *a, const AttnItem *items, in
     return (int)hipGetLastError();
 }
 
+// Which chunk path l98k_attn takes: 0 by the session's capacity (the two
+// launches past AG_AUTO_LEN positions), 1 always the one launch, 2 the two
+// launches wherever their LDS fits.
+#define AG_AUTO_LEN 2048
+static int g_attn_path = 0;
+extern "C" void l98k_set_attn_path(int mode) { g_attn_path = mode; }
+
 extern "C" int l98k_attn(const AttnArgs *a, int nt, int max_len, float *att, hipStream_t st) {
     // hd divides 256: the new K rows' quantization takes 32-lane groups of
     // a 256-thread block
@@ -1287,6 +1484,30 @@ extern "C" int l98k_attn(const AttnArgs *a, int nt, int max_len, float *att, hip
     const int kv_mul = a->nh / a->nkv;
     if (kv_mul + MAX_CHUNK > ATT_MAX_VEC) return -1;
     const int att_stride = (max_len + 3) & ~3;
+    // two launches: the scores of every (slice, kv head, token), then the
+    // softmax and value chains of every (q head, token, output group)
+    const size_t ag_lds = ag_lds_bytes(att_stride);
+    const bool ag_fits = (a->hd == 64 || a->hd == 128) && ag_lds <= (size_t)(lds_limit() - 8192);
+    if (ag_fits && (g_attn_path == 2 || (g_attn_path == 0 && max_len > AG_AUTO_LEN))) {
+        static bool ag_attr = false;
+        if (!ag_attr) {
+            const int lim = lds_limit() - 8192;
+            (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k_attn_avg<128>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, lim);
+            (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k_attn_avg<64>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, lim);
+            ag_attr = true;
+        }
+        const int slices = (max_len + ATT_SLICE - 1) / ATT_SLICE;
+        hipLaunchKernelGGL(k_attn_scores_chunk, dim3(slices, a->nkv, nt), dim3(256), 0, st, *a, att, att_stride);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return (int)e;
+        if (a->hd == 128)
+            hipLaunchKernelGGL(k_attn_avg<128>, dim3(a->nh, nt, 4), dim3(AG_THREADS), ag_lds, st, *a, att, att_stride);
+        else
+            hipLaunchKernelGGL(k_attn_avg<64>, dim3(a->nh, nt, 2), dim3(AG_THREADS), ag_lds, st, *a, att, att_stride);
+        return (int)hipGetLastError();
+    }
     // one launch: each (q head, token) block does its own scores, then the
     // softmax and the value sum (scores row, the product double buffer, then
     // as many staged V positions, a multiple of the chunk, as the LDS limit

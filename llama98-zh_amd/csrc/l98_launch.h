@@ -136,6 +136,8 @@ int l98k_attn_items(const AttnArgs *a, const AttnItem *items, int n_items, int p
 // then softmax, value sum, output gate and quantization into oq / oqs.
 // att: scratch [MAX_CHUNK][nh][round4(max_len)] floats.
 int l98k_attn(const AttnArgs *a, int nt, int max_len, float *att, hipStream_t st);
+// l98k_attn's chunk path: 0 by capacity, 1 one launch, 2 two launches.
+void l98k_set_attn_path(int mode);
 // Routing of nt tokens (computed in every block) and the routed experts'
 // first projections (n_jobs <= 2, e.g. w1 and w3 over the latent rows);
 // publishes sel_idx / sel_w / grp (and adds the distinct-expert count to
