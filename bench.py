@@ -380,6 +380,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--sessions", type=int, default=32, help="configs[4]: concurrent sessions")
     ap.add_argument("--dspark", action="store_true", help="a DSpark head on configs[1]'s shapes")
+    ap.add_argument("--attn-path", type=int, default=0,
+                    help="attention path of a session's chunk (l98_set_attn_path): 0 by capacity, 1 one launch, "
+                         "2 slice scores + grouped value chains")
     args = ap.parse_args()
     if args.prompt is None:
         args.prompt = {0: 64, 3: 4096}.get(args.config, 512)
@@ -392,6 +395,7 @@ def main():
 
     import __graft_entry__
     pkg = __graft_entry__.load_package()
+    pkg.set_attn_path(args.attn_path)
     if args.config == 4:
         bench_server(args, pkg)
         return

@@ -652,12 +652,17 @@ __global__ __launch_bounds__(256) void k_attn_scores_chunk(AttnArgs a, float *at
     attn_scores_body(a, att, att_stride, blockIdx.x, blockIdx.y, blockIdx.z);
 }
 
-// Dynamic LDS of k_attn_avg: the product double buffer, the score row
-// (att_stride floats), the exact sum's segment rows.
+// Dynamic LDS of k_attn_avg: the product double buffer, then the score
+// row in the exact sum's segment layout (segment k: slot 0 the carried sum,
+// then positions k * AG_SEG ..; the scores, the exps and the weights in
+// turn occupy the same slots).
 __host__ __device__ inline int ag_segments(int att_stride) { return (att_stride + AG_SEG - 1) / AG_SEG; }
 __host__ __device__ inline size_t ag_lds_bytes(int att_stride) {
-    return (2 * 32 * AG_PAD + (size_t)((att_stride + 3) & ~3) + (size_t)ag_segments(att_stride) * ps_row_floats<32>()) *
-           sizeof(float);
+    return (2 * 32 * AG_PAD + (size_t)ag_segments(att_stride) * ps_row_floats<32>()) * sizeof(float);
+}
+__device__ __forceinline__ int ag_slot(int p) {
+    const int k = p / AG_SEG;
+    return k * ps_row_floats<32>() + ps_slot<32>(p - k * AG_SEG + 1);
 }
 
 template <int HD>
@@ -674,8 +679,7 @@ __global__ __launch_bounds__(AG_THREADS) void k_attn_avg(AttnArgs a, const float
     const int L = *a.ctl_pos + a.pos_off + t + 1;
     const int nch = (L + AG_CH - 1) / AG_CH, nseg = (L + AG_SEG - 1) / AG_SEG;
     float *prod = reinterpret_cast<float *>(smem);                       // [2][32][AG_PAD]
-    float *s_a = prod + 2 * 32 * AG_PAD;                                  // [att_stride]
-    float *s_ps = s_a + ((att_stride + 3) & ~3);                          // [segments][PSR]
+    float *s_ps = prod + 2 * 32 * AG_PAD;                                 // [segments][PSR]
     // producers: thread ptid takes position ptid / 2 of each chunk, bytes
     // 16 (ptid % 2) .. +16 of the group
     const bool prodw = wave >= 1;
@@ -708,7 +712,7 @@ __global__ __launch_bounds__(AG_THREADS) void k_attn_avg(AttnArgs a, const float
         for (int u = 0; u < 4; u++) {
             const int p = p0 + u * AG_THREADS + tid;
             if (p < L) {
-                s_a[p] = x[u];
+                s_ps[ag_slot(p)] = x[u];
                 best = umax(best, d_fkey(x[u]));
             }
         }
@@ -721,13 +725,10 @@ __global__ __launch_bounds__(AG_THREADS) void k_attn_avg(AttnArgs a, const float
 #pragma unroll
     for (int w = 1; w < AG_THREADS / 64; w++) bk = umax(bk, s_red[w]);
     const float mx = d_unkey(bk);
-    // exps, also into the segment rows (segment k: slot 0 the carried sum,
-    // slot 1 + i the value of position k * AG_SEG + i)
+    // exps in place
     for (int p = tid; p < L; p += AG_THREADS) {
-        const float e = d_exp(s_a[p] - mx, tab);
-        s_a[p] = e;
-        const int k = p / AG_SEG, i = p - k * AG_SEG + 1;
-        s_ps[k * PSR + ps_slot<32>(i)] = e;
+        float *e = s_ps + ag_slot(p);
+        *e = d_exp(*e - mx, tab);
     }
     __syncthreads();
     if (wave == 0) {                     // the serial loop's sum, bit for bit
@@ -743,13 +744,13 @@ __global__ __launch_bounds__(AG_THREADS) void k_attn_avg(AttnArgs a, const float
     }
     __syncthreads();
     const float inv = s_inv;
-    for (int p = tid; p < L; p += AG_THREADS) s_a[p] *= inv;
+    for (int p = tid; p < L; p += AG_THREADS) s_ps[ag_slot(p)] *= inv;
     __syncthreads();
     // value chains
     auto produce = [&](int c, int buf, int4 v4, float vsc) {
         const int p = c * AG_CH + pp;
         // past the row: a = 0, a product of +-0, which leaves the sum as it is
-        const float ap = p < L ? s_a[p] : 0.0f;
+        const float ap = p < L ? s_ps[ag_slot(p)] : 0.0f;
         float *pb = prod + buf * 32 * AG_PAD + 16 * ph * AG_PAD + pp;
         const int w4[4] = {v4.x, v4.y, v4.z, v4.w};
 #pragma unroll
