@@ -290,82 +290,128 @@ __global__ __launch_bounds__(MF_THREADS) void k_mfma_q8(const int8_t *__restrict
 #undef MF_STAGE_LOAD
 #undef MF_STAGE_PUT
 
-// The grouped form for small groups (expert GEMMs over a batched verify's
-// few pairs per expert): a block computes 64 weight rows x 16 token
-// columns (wave w: rows 16 w .. 16 w + 15, the same 16 columns), so each
-// block streams four times the weights of k_mfma_q8's 16-row tile and
-// stages only the 16 columns it uses; a group's column tiles spread over
-// the grid's y.  Same stages, MFMAs and fold per
-// (row, column) as k_mfma_q8, so the same bits.
+// The narrow form: a block computes 64 weight rows x 16 token columns
+// (wave w: rows 16 w .. 16 w + 15 of the same 16 columns), so each block
+// streams four times the weights of k_mfma_q8's 16-row tile and stages
+// only the 16 columns it uses, and the loads run two stages ahead (register
+// sets A and B alternate) - for few columns per weight tile (the experts of
+// a batched verify, whose groups average a few pairs; dense GEMMs over the
+// batch's rows), where a stage's round trip, not the arithmetic, bounds the
+// block.  Dense (cols.list null: column t is activation and output row t,
+// t < M; jobs as in k_mfma_q8; a 1-D grid mapped onto the XCDs so that the
+// column tiles of a weight tile share an L2) or grouped (block z is group g; a group's
+// column tiles spread over the grid's y, whose extra blocks exit at once).
+// Same stages, MFMAs and fold per (row, column) as k_mfma_q8, so the same
+// bits.
 #define MFN_ROWS 64
 #define MFN_COLS 16
+#define MFN_DENSE_MAX 128      // dense GEMMs of at most this many rows take the narrow tiles
+#define MFN_STAGE_LOAD(R, st_)                                                                 \
+    do {                                                                                       \
+        const int off_ = imin((st_) * MF_KC + 16 * pc, K - 16);                                \
+        R##w0 = *reinterpret_cast<const int4 *>(wl0 + off_);                                   \
+        R##w1 = *reinterpret_cast<const int4 *>(wl1 + off_);                                   \
+        R##w2 = *reinterpret_cast<const int4 *>(wl2 + off_);                                   \
+        R##w3 = *reinterpret_cast<const int4 *>(wl3 + off_);                                   \
+        R##x0 = *reinterpret_cast<const int4 *>(xl0 + off_);                                   \
+        if (tid < 64) {                                                                        \
+            const int g_ = (st_) * (MF_KC / 32) + 2 * (tid & 3);                               \
+            R##t0 = xsl[imin(g_, nb - 1)];                                                     \
+            R##t1 = xsl[imin(g_ + 1, nb - 1)];                                                 \
+        }                                                                                      \
+    } while (0)
+#define MFN_STAGE_PUT(R, b_)                                                                   \
+    do {                                                                                       \
+        *reinterpret_cast<int4 *>(&s_w[b_][rr][16 * pc]) = R##w0;                              \
+        *reinterpret_cast<int4 *>(&s_w[b_][rr + 16][16 * pc]) = R##w1;                         \
+        *reinterpret_cast<int4 *>(&s_w[b_][rr + 32][16 * pc]) = R##w2;                         \
+        *reinterpret_cast<int4 *>(&s_w[b_][rr + 48][16 * pc]) = R##w3;                         \
+        *reinterpret_cast<int4 *>(&s_x[b_][rr][16 * pc]) = R##x0;                              \
+        if (tid < 64) *reinterpret_cast<float2 *>(&s_xs[b_][tid >> 2][2 * (tid & 3)]) = make_float2(R##t0, R##t1); \
+    } while (0)
 template <bool FULLK>
-__global__ __launch_bounds__(MF_THREADS) void k_mfma_q8n(const int8_t *__restrict__ W, const float *__restrict__ ws,
-                                                          int N, int K, size_t w_group_stride,
-                                                          const int8_t *__restrict__ X, const float *__restrict__ Xs,
-                                                          MfCols cols, float *__restrict__ out, int out_stride) {
+__global__ __launch_bounds__(MF_THREADS) void k_mfma_q8n(const int8_t *__restrict__ W0, const float *__restrict__ ws0,
+                                                          int N0, int K0, size_t w_group_stride,
+                                                          const int8_t *__restrict__ X0, const float *__restrict__ Xs0,
+                                                          int M, MfCols cols, float *__restrict__ out0,
+                                                          int out_stride0, MfJobs jobs) {
     __shared__ __align__(16) int8_t s_w[2][MFN_ROWS][MF_LDS_ROW];
     __shared__ __align__(16) int8_t s_x[2][MFN_COLS][MF_LDS_ROW];
     __shared__ __align__(16) float s_xs[2][MFN_COLS][MF_KC / 32];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int g = blockIdx.z;
-    if (g >= *cols.ng) return;
-    const int ncols = cols.gcnt[g], cbase = cols.goff[g], e = cols.gexp[g];
-    const int8_t *Wg = W + (size_t)e * w_group_stride;
-    const float *wsg = ws + (size_t)e * N;
-    const int n0 = blockIdx.x * MFN_ROWS, nb = K >> 5;
+    const int8_t *W = W0;
+    const float *ws = ws0;
+    float *out = out0;
+    const int8_t *X = X0;
+    const float *Xs = Xs0;
+    int N = N0, K = K0, out_stride = out_stride0, bx = blockIdx.x;
+    int cy = blockIdx.y, cys = gridDim.y;
+    if (!cols.list) {
+        // Dense: a 1-D grid of (row tiles rounded up to 8) x column tiles.
+        // Blocks go to the 8 XCDs in turn by linear index, so block L runs on
+        // XCD L % 8; give XCD x the row tiles x, x + 8, ... with all their
+        // column tiles one after another, so the column tiles that share a
+        // weight tile share that XCD's L2 (weights read from HBM once).
+        const int ny = (M + MFN_COLS - 1) / MFN_COLS, xcd = bx & 7, sl = bx >> 3, q = sl / ny;
+        bx = q * 8 + xcd;
+        cy = sl - q * ny;
+        cys = ny;
+        const int nrt = jobs.n ? jobs.j[jobs.n - 1].blk0 + (jobs.j[jobs.n - 1].N + MFN_ROWS - 1) / MFN_ROWS
+                               : (N0 + MFN_ROWS - 1) / MFN_ROWS;
+        if (bx >= nrt) return;
+    }
+    if (jobs.n) {
+        int ji = 0;
+#pragma unroll
+        for (int k = 1; k < MF_MAX_JOBS; k++)
+            if (k < jobs.n && bx >= jobs.j[k].blk0) ji = k;
+        const MfJob jb = jobs.j[ji];
+        W = jb.W;
+        ws = jb.ws;
+        out = jb.out;
+        X = jb.X;
+        Xs = jb.Xs;
+        K = jb.K;
+        N = jb.N;
+        out_stride = jb.out_stride;
+        bx -= jb.blk0;
+    }
+    int ncols = M, cbase = 0;
+    const int8_t *Wg = W;
+    const float *wsg = ws;
+    if (cols.list) {
+        const int g = blockIdx.z;
+        if (g >= *cols.ng) return;
+        ncols = cols.gcnt[g];
+        cbase = cols.goff[g];
+        const int e = cols.gexp[g];
+        Wg = W + (size_t)e * w_group_stride;
+        wsg = ws + (size_t)e * N;
+    }
+    const int n0 = bx * MFN_ROWS, nb = K >> 5;
     const int pc = tid & 15, rr = tid >> 4;
     auto wrow = [&](int j) { const int r = n0 + rr + 16 * j; return Wg + (size_t)(r < N ? r : N - 1) * K; };
     const int8_t *wl0 = wrow(0), *wl1 = wrow(1), *wl2 = wrow(2), *wl3 = wrow(3);
     const int kq = 8 * (lane >> 4);
-    // column tiles blockIdx.y, + gridDim.y, ... (the few large groups of a
-    // skewed routing spread over gridDim.y blocks; the others' extra blocks
-    // exit here)
+    const int nst = (K + MF_KC - 1) / MF_KC;
 #pragma unroll 1
-    for (int c0 = blockIdx.y * MFN_COLS; c0 < ncols; c0 += gridDim.y * MFN_COLS) {
+    for (int c0 = cy * MFN_COLS; c0 < ncols; c0 += cys * MFN_COLS) {
         auto xrow = [&](int c) {
-            const int o = cols.list[cbase + imin(c0 + c, ncols - 1)];
+            const int cc = imin(c0 + c, ncols - 1);
+            if (!cols.list) return cc;
+            const int o = cols.list[cbase + cc];
             return cols.xmap ? cols.xmap[o] : o;
         };
         const int8_t *xl0 = X + (size_t)xrow(rr) * K;                  // column rr's piece pc
         const float *xsl = Xs + (size_t)xrow(tid >> 2) * nb;            // threads < 64: column tid / 4
         const int cl = c0 + (lane & 15);
-        const int nst = (K + MF_KC - 1) / MF_KC;
-        int4 w0, w1, w2, w3, x0;
-        float t0 = 0.0f, t1 = 0.0f;
-        auto load = [&](int st) {
-            const int off = imin(st * MF_KC + 16 * pc, K - 16);
-            w0 = *reinterpret_cast<const int4 *>(wl0 + off);
-            w1 = *reinterpret_cast<const int4 *>(wl1 + off);
-            w2 = *reinterpret_cast<const int4 *>(wl2 + off);
-            w3 = *reinterpret_cast<const int4 *>(wl3 + off);
-            x0 = *reinterpret_cast<const int4 *>(xl0 + off);
-            if (tid < 64) {
-                const int gg = st * (MF_KC / 32) + 2 * (tid & 3);
-                t0 = xsl[imin(gg, nb - 1)];
-                t1 = xsl[imin(gg + 1, nb - 1)];
-            }
-        };
-        auto put = [&](int b) {
-            *reinterpret_cast<int4 *>(&s_w[b][rr][16 * pc]) = w0;
-            *reinterpret_cast<int4 *>(&s_w[b][rr + 16][16 * pc]) = w1;
-            *reinterpret_cast<int4 *>(&s_w[b][rr + 32][16 * pc]) = w2;
-            *reinterpret_cast<int4 *>(&s_w[b][rr + 48][16 * pc]) = w3;
-            *reinterpret_cast<int4 *>(&s_x[b][rr][16 * pc]) = x0;
-            if (tid < 64) *reinterpret_cast<float2 *>(&s_xs[b][tid >> 2][2 * (tid & 3)]) = make_float2(t0, t1);
-        };
+        int4 Aw0, Aw1, Aw2, Aw3, Ax0, Bw0, Bw1, Bw2, Bw3, Bx0;
+        float At0 = 0.0f, At1 = 0.0f, Bt0 = 0.0f, Bt1 = 0.0f;
         float f[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         const bool one = nb == 1;
         float s0 = 0.0f;
-        load(0);
-        put(0);
-        __syncthreads();
-#pragma unroll 1
-        for (int st = 0; st < nst; st++) {
-            const int buf = st & 1;
+        auto compute = [&](int buf, int st) {
             const float *sc = s_xs[buf][lane & 15];
-            load(st + 1 < nst ? st + 1 : st);
-            __builtin_amdgcn_sched_barrier(0);
             const v4i_t zero = {0, 0, 0, 0};
             const int ng = FULLK ? MF_KC / 32 : nb - st * (MF_KC / 32);
 #pragma unroll
@@ -377,11 +423,29 @@ __global__ __launch_bounds__(MF_THREADS) void k_mfma_q8n(const int8_t *__restric
                 mf_fold(f, dd, sc[gl], one);
             }
             if (!FULLK && one) s0 = sc[0];
-            put(buf ^ 1);
+        };
+        // stage st in buffer st % 2; the loads of stages st + 1 and st + 2
+        // in flight while it runs (stages past the last reload the last)
+        MFN_STAGE_LOAD(A, 0);
+        MFN_STAGE_PUT(A, 0);
+        __syncthreads();
+        MFN_STAGE_LOAD(A, imin(1, nst - 1));
+#pragma unroll 1
+        for (int st = 0; st < nst; st += 2) {
+            MFN_STAGE_LOAD(B, imin(st + 2, nst - 1));
+            __builtin_amdgcn_sched_barrier(0);
+            compute(0, st);
+            MFN_STAGE_PUT(A, 1);
+            __syncthreads();
+            if (st + 1 >= nst) break;                          // uniform
+            MFN_STAGE_LOAD(A, imin(st + 3, nst - 1));
+            __builtin_amdgcn_sched_barrier(0);
+            compute(1, st + 1);
+            MFN_STAGE_PUT(B, 0);
             __syncthreads();
         }
         if (cl < ncols) {
-            float *op = out + (size_t)cols.list[cbase + cl] * out_stride;
+            float *op = out + (size_t)(cols.list ? cols.list[cbase + cl] : cl) * out_stride;
 #pragma unroll
             for (int v = 0; v < 4; v++) {
                 const int n = n0 + 16 * wave + 4 * (lane >> 4) + v;
@@ -395,6 +459,8 @@ __global__ __launch_bounds__(MF_THREADS) void k_mfma_q8n(const int8_t *__restric
         }
     }
 }
+#undef MFN_STAGE_LOAD
+#undef MFN_STAGE_PUT
 
 
 // ------------------------------------------------------ wide producers ---
@@ -467,6 +533,17 @@ extern "C" int l98k_mfma_gemm(const int8_t *W, const float *ws, int N, int K, co
                               float *out, int out_stride, hipStream_t st) {
     if (N < 1 || M < 1 || K < 32 || (K & 31) || out_stride < N) return -1;
     MfCols c{};
+    if (M <= MFN_DENSE_MAX) {
+        const int nrt8 = ((N + MFN_ROWS - 1) / MFN_ROWS + 7) & ~7;
+        const dim3 gridn(nrt8 * ((M + MFN_COLS - 1) / MFN_COLS), 1, 1);
+        if (K % MF_KC == 0)
+            hipLaunchKernelGGL(k_mfma_q8n<true>, gridn, dim3(MF_THREADS), 0, st, W, ws, N, K, (size_t)0, X, Xs, M, c,
+                               out, out_stride, MfJobs{});
+        else
+            hipLaunchKernelGGL(k_mfma_q8n<false>, gridn, dim3(MF_THREADS), 0, st, W, ws, N, K, (size_t)0, X, Xs, M, c,
+                               out, out_stride, MfJobs{});
+        return (int)hipGetLastError();
+    }
     const dim3 grid((N + MF_ROWS - 1) / MF_ROWS, (M + MF_COLS - 1) / MF_COLS, 1);
     if (K % MF_KC == 0)
         hipLaunchKernelGGL(k_mfma_q8<true>, grid, dim3(MF_THREADS), 0, st, W, ws, N, K, (size_t)0, X, Xs, M, c, out,
@@ -485,6 +562,8 @@ extern "C" int l98k_mfma_gemm_multi(int n_jobs, const int8_t *const *W, const fl
                                     float *const *out, const int *out_stride, const int *K,
                                     const int8_t *const *X, const float *const *Xs, int M, hipStream_t st) {
     if (n_jobs < 1 || n_jobs > MF_MAX_JOBS || M < 1) return -1;
+    const bool narrow = M <= MFN_DENSE_MAX;
+    const int tile = narrow ? MFN_ROWS : MF_ROWS;
     MfJobs jobs{};
     int blocks = 0;
     bool full = true;
@@ -492,10 +571,20 @@ extern "C" int l98k_mfma_gemm_multi(int n_jobs, const int8_t *const *W, const fl
         if (N[j] < 1 || out_stride[j] < N[j] || K[j] < 32 || (K[j] & 31)) return -1;
         full = full && K[j] % MF_KC == 0;
         jobs.j[j] = MfJob{W[j], ws[j], out[j], X[j], Xs[j], N[j], out_stride[j], blocks, K[j]};
-        blocks += (N[j] + MF_ROWS - 1) / MF_ROWS;
+        blocks += (N[j] + tile - 1) / tile;
     }
     jobs.n = n_jobs;
     MfCols c{};
+    if (narrow) {
+        const dim3 gridn(((blocks + 7) & ~7) * ((M + MFN_COLS - 1) / MFN_COLS), 1, 1);
+        if (full)
+            hipLaunchKernelGGL(k_mfma_q8n<true>, gridn, dim3(MF_THREADS), 0, st, W[0], ws[0], N[0], K[0], (size_t)0,
+                               X[0], Xs[0], M, c, out[0], out_stride[0], jobs);
+        else
+            hipLaunchKernelGGL(k_mfma_q8n<false>, gridn, dim3(MF_THREADS), 0, st, W[0], ws[0], N[0], K[0], (size_t)0,
+                               X[0], Xs[0], M, c, out[0], out_stride[0], jobs);
+        return (int)hipGetLastError();
+    }
     const dim3 grid(blocks, (M + MF_COLS - 1) / MF_COLS, 1);
     if (full)
         hipLaunchKernelGGL(k_mfma_q8<true>, grid, dim3(MF_THREADS), 0, st, W[0], ws[0], N[0], K[0], (size_t)0, X[0],
@@ -521,10 +610,10 @@ extern "C" int l98k_mfma_gemm_grouped(const int8_t *bank, const float *bank_s, i
         const dim3 gridn((N + MFN_ROWS - 1) / MFN_ROWS, ys, max_groups);
         if (K % MF_KC == 0)
             hipLaunchKernelGGL(k_mfma_q8n<true>, gridn, dim3(MF_THREADS), 0, st, bank, bank_s, N, K, (size_t)N * K, X,
-                               Xs, c, out, out_stride);
+                               Xs, 0, c, out, out_stride, MfJobs{});
         else
             hipLaunchKernelGGL(k_mfma_q8n<false>, gridn, dim3(MF_THREADS), 0, st, bank, bank_s, N, K, (size_t)N * K,
-                               X, Xs, c, out, out_stride);
+                               X, Xs, 0, c, out, out_stride, MfJobs{});
         return (int)hipGetLastError();
     }
     const dim3 grid((N + MF_ROWS - 1) / MF_ROWS, 1, max_groups);
