@@ -888,7 +888,7 @@ bool carve(DState *s) {
     s->ctl = (DevCtl *)st_take(s, sizeof(DevCtl));
     s->tokbuf = (int *)st_take(s, sizeof(int) * (size_t)s->cap_rows);
     s->amax_cap = 0;
-    for (int m = 1; m <= MAX_CHUNK; m *= 2) {
+    for (int m = 1; m <= MAX_CHUNK; m++) {
         const int need = l98k_gemv_tiles(c.vocab_size, d, m) * m;
         s->amax_cap = need > s->amax_cap ? need : s->amax_cap;
     }
@@ -3010,7 +3010,7 @@ extern "C" int l98_gemv_argmax(const int8_t *w, const float *ws, int N, int K, i
     if (gs == K) gs = 0;
     const size_t nws = gs ? (size_t)(K / gs) : 1;
     int cap = 0;
-    for (int m = 1; m <= MAX_CHUNK; m *= 2) {
+    for (int m = 1; m <= MAX_CHUNK; m++) {
         const int need = l98k_gemv_tiles(N, K, m) * m;
         cap = need > cap ? need : cap;
     }

@@ -36,6 +36,9 @@ static inline int pro_pj(int in_dim) {
     return j <= 1 ? 1 : j <= 2 ? 2 : j <= 4 ? 4 : 8;
 }
 typedef int v4i __attribute__((ext_vector_type(4)));
+// Token slots of the instance that runs m rows: 1, 2, 4, 5, 6 or 8 (the
+// verify of k = 4 and 5 drafts has its own instance instead of paying for 8).
+static inline int gemv_slots(int m) { return m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : m <= 6 ? m : 8; }
 
 // LDS bytes of one tile: staged activations, their scales, and the larger of
 // the group sums and the RMSNorm squares (m rows in the exact sum's layout

@@ -13,7 +13,7 @@ __device__ __forceinline__ void amax_store(const GemvBatch &b, const GemvJob &jo
     if ((int)threadIdx.x < m) b.amax_part[(size_t)threadIdx.x * job.tiles + blockIdx.x] = s_am[threadIdx.x];
 }
 
-// One launch over b.n jobs; m <= M live token rows (M a power of two).
+// One launch over b.n jobs; m <= M live token rows.
 // Block (x, y) is tile x of job y: the job index is the workgroup id, so
 // the job's fields are read with the kernel's first batch of scalar loads
 // (no dependent lookup); tiles past a job's last exit at once.
@@ -45,7 +45,7 @@ extern "C" int l98k_upload_exp_table_gemv(const float *tab) {
     return (int)hipMemcpyToSymbol(HIP_SYMBOL(c_exp_tab), tab, 32 * sizeof(float));
 }
 
-// Instances: token slots M in {1, 2, 4, 8}; prologue sets: pre-quantized
+// Instances: token slots M in {1, 2, 4, 5, 6, 8}; prologue sets: pre-quantized
 // (PJ 0), RMSNorm (PJ 1..8), RMSNorm with fold-only jobs (PJ 1..8),
 // SiLU-mul (PJ 1..4), combine + SiLU-mul (PJ 1..4); each with one scale per
 // weight row or with grouped scales (MG); pre-quantized with the argmax
@@ -71,7 +71,7 @@ extern "C" int l98k_upload_exp_table_gemv(const float *tab) {
 // set (pre-quantized, RMSNorm, SiLU-mul, or combine + SiLU-mul).
 extern "C" int l98k_gemv(GemvBatch *b, int m, hipStream_t st) {
     if (m < 1 || m > MAX_CHUNK || b->n < 1 || b->n > MAX_GEMV_JOBS) return -1;
-    const int M = m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8;
+    const int M = gemv_slots(m);
     int tiles = 0, pj = 0, modes = 0, grouped = 0;       // tiles: the largest job's
     size_t lds = 0;
     for (int j = 0; j < b->n; j++) {
@@ -108,6 +108,8 @@ extern "C" int l98k_gemv(GemvBatch *b, int m, hipStream_t st) {
         GEMV_CASES_M(1)
         GEMV_CASES_M(2)
         GEMV_CASES_M(4)
+        GEMV_CASES_M(5)
+        GEMV_CASES_M(6)
         GEMV_CASES_M(8)
     default:
         return -1;
@@ -117,7 +119,7 @@ extern "C" int l98k_gemv(GemvBatch *b, int m, hipStream_t st) {
 
 // Tiles of a GEMV over `rows` rows of in_dim with m token rows.
 extern "C" int l98k_gemv_tiles(int rows, int in_dim, int m) {
-    const int R = gemv_rows_per_tile(in_dim, m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8);
+    const int R = gemv_rows_per_tile(in_dim, gemv_slots(m));
     return (rows + R - 1) / R;
 }
 
@@ -125,7 +127,7 @@ extern "C" int l98k_gemv_tiles(int rows, int in_dim, int m) {
 // fits the kernel's LDS.
 extern "C" int l98k_gemv_norm_fits(int in_dim, int m) {
     if (in_dim > PRO_MAX_IN || m < 1 || m > MAX_CHUNK) return 0;
-    const int M = m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8;
+    const int M = gemv_slots(m);
     return gemv_lds_bytes(M, in_dim, gemv_rows_per_tile(in_dim, M), 1, pro_pj(in_dim)) <= gemv_lds_limit();
 }
 

@@ -32,7 +32,7 @@
 //   * the per-head gated RMSNorm and the per-32 quantization for o_proj
 //     (src/forward_kda.c:1000-1043).
 // Work that does not depend on the state is done for all NT token slots at
-// once (NT a power of two >= nt; slots past nt repeat the last token and
+// once (NT in {1, 2, 4, 5, 6, 8}, >= nt; slots past nt repeat the last token and
 // store nothing), as straight-line code with independent work per token.
 __device__ __forceinline__ float dpp_quad_shr1(float v) {        // lane r <- lane r-1 (lane 0 keeps its own)
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x90, 0xF, 0xF, false));
@@ -630,7 +630,7 @@ extern "C" int l98k_kda_step(const KdaStepArgs *a, int kd, int K, hipStream_t st
     if (a->nt < 1 || a->nt > MAX_CHUNK || a->rank < 32 || (a->rank & 31) || a->rank > KDA_MAX_RANK ||
         a->key != a->nv * kd || a->value != a->nv * kd || K < 2 || K > 4)
         return -1;
-    const int nt = a->nt, NT = nt <= 1 ? 1 : nt <= 2 ? 2 : nt <= 4 ? 4 : 8;
+    const int nt = a->nt, NT = nt <= 1 ? 1 : nt <= 2 ? 2 : nt <= 4 ? 4 : nt <= 6 ? nt : 8;
     // conv width 4 (every synthetic config) has an instance per token bound;
     // other widths run the 8-slot instance
 #define KDA_STEP(KD_, K_, NT_) hipLaunchKernelGGL((k_kda_step<KD_, K_, NT_>), dim3(a->nv), dim3(4 * (KD_)), 0, st, *a)
@@ -639,6 +639,8 @@ extern "C" int l98k_kda_step(const KdaStepArgs *a, int kd, int K, hipStream_t st
     case 1: KDA_STEP(KD_, 4, 1); break;             \
     case 2: KDA_STEP(KD_, 4, 2); break;             \
     case 4: KDA_STEP(KD_, 4, 4); break;             \
+    case 5: KDA_STEP(KD_, 4, 5); break;             \
+    case 6: KDA_STEP(KD_, 4, 6); break;             \
     default: KDA_STEP(KD_, 4, 8); break;            \
     }
     switch (kd * 8 + K) {

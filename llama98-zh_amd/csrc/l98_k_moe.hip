@@ -343,8 +343,8 @@ extern "C" int l98k_upload_exp_table_moe(const float *tab) {
     return (int)hipMemcpyToSymbol(HIP_SYMBOL(c_exp_tab), tab, 32 * sizeof(float));
 }
 
-// Member slots of a grouped expert launch: a power of two >= nt.
-static int expert_m(int nt) { return nt <= 1 ? 1 : nt <= 2 ? 2 : nt <= 4 ? 4 : 8; }
+// Member slots of a grouped expert launch (>= nt): the GEMV's token slots.
+static int expert_m(int nt) { return gemv_slots(nt); }
 
 // Instances: member slots M, prologue width PJ, and G = MG for weights with
 // grouped scales (0: one scale per row).
@@ -358,7 +358,10 @@ static int expert_m(int nt) { return nt <= 1 ? 1 : nt <= 2 ? 2 : nt <= 4 ? 4 : 8
     EXPERT_CASE(KERNEL, 1, 4, G_, __VA_ARGS__) EXPERT_CASE(KERNEL, 2, 1, G_, __VA_ARGS__)  \
     EXPERT_CASE(KERNEL, 2, 2, G_, __VA_ARGS__) EXPERT_CASE(KERNEL, 2, 4, G_, __VA_ARGS__)  \
     EXPERT_CASE(KERNEL, 4, 1, G_, __VA_ARGS__) EXPERT_CASE(KERNEL, 4, 2, G_, __VA_ARGS__)  \
-    EXPERT_CASE(KERNEL, 4, 4, G_, __VA_ARGS__) EXPERT_CASE(KERNEL, 8, 1, G_, __VA_ARGS__)  \
+    EXPERT_CASE(KERNEL, 4, 4, G_, __VA_ARGS__) EXPERT_CASE(KERNEL, 5, 1, G_, __VA_ARGS__)  \
+    EXPERT_CASE(KERNEL, 5, 2, G_, __VA_ARGS__) EXPERT_CASE(KERNEL, 5, 4, G_, __VA_ARGS__)  \
+    EXPERT_CASE(KERNEL, 6, 1, G_, __VA_ARGS__) EXPERT_CASE(KERNEL, 6, 2, G_, __VA_ARGS__)  \
+    EXPERT_CASE(KERNEL, 6, 4, G_, __VA_ARGS__) EXPERT_CASE(KERNEL, 8, 1, G_, __VA_ARGS__)  \
     EXPERT_CASE(KERNEL, 8, 2, G_, __VA_ARGS__) EXPERT_CASE(KERNEL, 8, 4, G_, __VA_ARGS__)
 #define EXPERT_DISPATCH(KERNEL, M, PJ, GROUPED, ...)                                     \
     do {                                                                                 \
