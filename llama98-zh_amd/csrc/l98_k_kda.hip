@@ -10,8 +10,12 @@
 // channel tid % kd for every token, the gate rows go to the groups token by
 // token, and the later channel phases use the first group; the recurrence
 // uses a lane quad per state column: thread 4c + r holds rows
-// [r*kd/4, (r+1)*kd/4) of column c of the fp32 state S[kd][vd] (stored
-// column-major per head).
+// [r*kd/4, (r+1)*kd/4) of column c of the fp32 state S[kd][vd].  The ring
+// slot stores a head's state in that thread order: float4 i of thread t
+// (rows r*kd/4 + 4i .. + 3 of column c) at float4 index i * 4kd + t of the
+// head, so each load or store instruction of the block moves 4kd
+// consecutive float4s (the recurrence kernels are the state's only
+// readers and writers).
 // For the chunk's tokens, in one launch:
 //   * the depthwise causal conv + SiLU of the q, k and v channels along the
 //     ring (lz_causal_conv1d_step, src/ops_conv1d.c:26-87: taps summed in
@@ -215,11 +219,10 @@ __device__ __forceinline__ void kda_step_body(const KdaStepArgs &a, int h) {
     const float alog = a.a_log[h];
     float S[RPL];
     if constexpr (!PRE) {
-        const float4 *src = reinterpret_cast<const float4 *>(a.state + (size_t)base * a.slot_stride + head_off +
-                                                             (size_t)col * KD + row0);
+        const float4 *src = reinterpret_cast<const float4 *>(a.state + (size_t)base * a.slot_stride + head_off) + tid;
 #pragma unroll
         for (int i = 0; i < RPL / 4; i++) {
-            const float4 q = src[i];
+            const float4 q = src[i * NTHR];
             S[4 * i] = q.x; S[4 * i + 1] = q.y; S[4 * i + 2] = q.z; S[4 * i + 3] = q.w;
         }
     }
@@ -418,10 +421,10 @@ __device__ __forceinline__ void kda_step_body(const KdaStepArgs &a, int h) {
         if (a.advance || t == nt - 1) {
             // slot (base + t) % depth + 1 (wrapping) when advancing, else base
             const int so = a.advance ? so_t : base;
-            float4 *dst = reinterpret_cast<float4 *>(a.state + (size_t)so * a.slot_stride + head_off +
-                                                     (size_t)col * KD + row0);
+            float4 *dst = reinterpret_cast<float4 *>(a.state + (size_t)so * a.slot_stride + head_off) + tid;
 #pragma unroll
-            for (int i = 0; i < RPL / 4; i++) dst[i] = make_float4(S[4 * i], S[4 * i + 1], S[4 * i + 2], S[4 * i + 3]);
+            for (int i = 0; i < RPL / 4; i++)
+                dst[i * NTHR] = make_float4(S[4 * i], S[4 * i + 1], S[4 * i + 2], S[4 * i + 3]);
         }
         so_t = so_t + 1 == a.depth ? 0 : so_t + 1;
         if (quarter == 0) {
@@ -539,11 +542,11 @@ __global__ __launch_bounds__(4 * KD) void k_kda_rec(KdaStepArgs a, int n) {
     constexpr int RPL = KD / 4, RS = 5 * KD + 4, T = MAX_CHUNK;
     __shared__ __align__(16) float s_rec[2][T][RS];
     const int h = blockIdx.x, tid = threadIdx.x, col = tid >> 2, row0 = (tid & 3) * RPL;
-    float *sp = a.state + (size_t)(*a.ctl_slot) * a.slot_stride + (size_t)h * KD * KD + (size_t)col * KD + row0;
+    float4 *sp = reinterpret_cast<float4 *>(a.state + (size_t)(*a.ctl_slot) * a.slot_stride + (size_t)h * KD * KD) + tid;
     float S[RPL];
 #pragma unroll
     for (int i = 0; i < RPL / 4; i++) {
-        const float4 q = reinterpret_cast<const float4 *>(sp)[i];
+        const float4 q = sp[i * 4 * KD];
         S[4 * i] = q.x; S[4 * i + 1] = q.y; S[4 * i + 2] = q.z; S[4 * i + 3] = q.w;
     }
     const size_t rstride = (size_t)a.nv * RS;
@@ -574,8 +577,7 @@ __global__ __launch_bounds__(4 * KD) void k_kda_rec(KdaStepArgs a, int n) {
         __syncthreads();
     }
 #pragma unroll
-    for (int i = 0; i < RPL / 4; i++)
-        reinterpret_cast<float4 *>(sp)[i] = make_float4(S[4 * i], S[4 * i + 1], S[4 * i + 2], S[4 * i + 3]);
+    for (int i = 0; i < RPL / 4; i++) sp[i * 4 * KD] = make_float4(S[4 * i], S[4 * i + 1], S[4 * i + 2], S[4 * i + 3]);
 }
 
 template <int KD, int K>
