@@ -57,6 +57,88 @@ __global__ __launch_bounds__(64) void k_rmsnorm(float *__restrict__ x, int x_str
                             xq ? xq + (size_t)row * n : nullptr, xqs ? xqs + (size_t)row * (n >> 5) : nullptr);
 }
 
+// The same row operation (one scale per 32) with a 256-thread block per
+// row, for rows of more than 512 elements: thread t holds float4 t + 256 j
+// of the row, so the loads, the residual fold, the normalization and the
+// per-32 quantization (an aligned lane octet per group, as above) spread
+// over four waves, and wave 0 takes the index-order sum of the squares with
+// the one-wave kernel's exact wave sum (the same layout, so the same bits).
+template <int PJ, bool NORM>
+__global__ __launch_bounds__(256) void k_rmsnorm_b(float *__restrict__ x, int x_stride,
+                                                   const float *__restrict__ a, const float *__restrict__ b,
+                                                   const float *__restrict__ w, int n, float eps,
+                                                   float *__restrict__ out, int out_stride,
+                                                   int8_t *__restrict__ xq, float *__restrict__ xqs) {
+    constexpr int PB = PJ / 4, PC = 4 * PJ;           // float4 per thread; the sum's lane chunk
+    static_assert(PJ == 4 || PJ == 8, "rows of 513..2048 elements");
+    __shared__ __align__(16) float sq[ps_row_floats<PC>()];
+    __shared__ PsRec rec[128];
+    __shared__ float s_inv;
+    const int row = blockIdx.x, tid = threadIdx.x, nf = n >> 2;
+    float4 *xr = reinterpret_cast<float4 *>(x + (size_t)row * x_stride);
+    float4 v[PB], wn[PB];
+#pragma unroll
+    for (int j = 0; j < PB; j++) {
+        const int fc = imin(tid + 256 * j, nf - 1);
+        v[j] = xr[fc];
+        wn[j] = reinterpret_cast<const float4 *>(w ? w : x)[fc];
+    }
+    if (a) {
+        float4 av[PB];
+#pragma unroll
+        for (int j = 0; j < PB; j++) av[j] = reinterpret_cast<const float4 *>(a + (size_t)row * n)[imin(tid + 256 * j, nf - 1)];
+        if (b) {
+#pragma unroll
+            for (int j = 0; j < PB; j++) {
+                const float4 bv = reinterpret_cast<const float4 *>(b + (size_t)row * n)[imin(tid + 256 * j, nf - 1)];
+                av[j] = make_float4(av[j].x + bv.x, av[j].y + bv.y, av[j].z + bv.z, av[j].w + bv.w);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < PB; j++) {
+            v[j] = make_float4(v[j].x + av[j].x, v[j].y + av[j].y, v[j].z + av[j].z, v[j].w + av[j].w);
+            if (tid + 256 * j < nf) xr[tid + 256 * j] = v[j];
+        }
+    }
+    float inv = 1.0f;
+    if constexpr (NORM) {
+#pragma unroll
+        for (int j = 0; j < PB; j++) {
+            const int f = tid + 256 * j;
+            if (f < nf)
+                *reinterpret_cast<float4 *>(sq + ps_slot<PC>(4 * f)) =
+                    make_float4(v[j].x * v[j].x, v[j].y * v[j].y, v[j].z * v[j].z, v[j].w * v[j].w);
+        }
+        __syncthreads();
+        if (tid < 64) {
+            const float ss = wave_sum_nonneg<PC>(sq, n, rec);
+            if (tid == 0) s_inv = d_rsqrt(d_ss_over_n(ss, n) + eps);
+        }
+        __syncthreads();
+        inv = s_inv;
+    }
+    float *orow = out ? out + (size_t)row * out_stride : nullptr;
+    int8_t *qrow = xq ? xq + (size_t)row * n : nullptr;
+    float *srow = xq ? xqs + (size_t)row * (n >> 5) : nullptr;
+#pragma unroll
+    for (int j = 0; j < PB; j++) {
+        const int f = tid + 256 * j;
+        float4 o = v[j];
+        if constexpr (NORM)
+            o = make_float4(v[j].x * inv * (1.0f + wn[j].x), v[j].y * inv * (1.0f + wn[j].y),
+                            v[j].z * inv * (1.0f + wn[j].z), v[j].w * inv * (1.0f + wn[j].w));
+        if (orow && f < nf) reinterpret_cast<float4 *>(orow)[f] = o;
+        if (qrow) {
+            float sg;
+            const uint32_t q = quant_octet(o, &sg);
+            if (f < nf) {
+                reinterpret_cast<uint32_t *>(qrow)[f] = q;
+                if (!(f & 7)) srow[f >> 3] = sg;
+            }
+        }
+    }
+}
+
 // MTP input rows (lz_mtp_draft_step / lz_mtp_prefill, src/forward_mtp.c:
 // e = embed(tok); concat = [rmsnorm(e, pre_e) | rmsnorm(h, pre_h)], then the
 // per-32 quantization of concat for the fc projection).  blockIdx.y = 0: the
@@ -442,6 +524,22 @@ extern "C" int l98k_rmsnorm_ex(float *x, int x_stride, const float *a, const flo
     if (n < 32 || n > 256 * 8 || (n & 31) || (x_stride & 3) || (out && (out_stride & 3)) || rows < 1 ||
         (xq && !xqs))
         return -1;
+    if (!tok && n > 512) {
+        // rows of 513..2048 elements: a 256-thread block per row
+        if (n <= 1024 && w)
+            hipLaunchKernelGGL((k_rmsnorm_b<4, true>), dim3(rows), dim3(256), 0, st, x, x_stride, a, b, w, n, eps, out,
+                               out_stride, xq, xqs);
+        else if (n <= 1024)
+            hipLaunchKernelGGL((k_rmsnorm_b<4, false>), dim3(rows), dim3(256), 0, st, x, x_stride, a, b, w, n, eps, out,
+                               out_stride, xq, xqs);
+        else if (w)
+            hipLaunchKernelGGL((k_rmsnorm_b<8, true>), dim3(rows), dim3(256), 0, st, x, x_stride, a, b, w, n, eps, out,
+                               out_stride, xq, xqs);
+        else
+            hipLaunchKernelGGL((k_rmsnorm_b<8, false>), dim3(rows), dim3(256), 0, st, x, x_stride, a, b, w, n, eps, out,
+                               out_stride, xq, xqs);
+        return (int)hipGetLastError();
+    }
 #define NORM_LAUNCH(PJ)                                                                                   \
     if (n <= 256 * PJ) {                                                                                  \
         if (w && !tok)                                                                                    \
