@@ -1741,10 +1741,8 @@ int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, 
         CK(l98k_wide_pro(0, w->latx, nullptr, lat, nullptr, nullptr, 0, lat, R, w->latq, w->latqs, st));
         const int maxg = pairs < E ? pairs : E;
         const int mean_cols = (pairs + maxg - 1) / maxg;
-        CK(l98k_mfma_gemm_grouped(L.w1.q, L.w1.s, inter, lat, w->latq, w->latqs, w->ng, maxg, w->gexp, w->goff,
-                                  w->gcnt, w->list, w->pair_token, R, mean_cols, w->h1, inter, st));
-        CK(l98k_mfma_gemm_grouped(L.w3.q, L.w3.s, inter, lat, w->latq, w->latqs, w->ng, maxg, w->gexp, w->goff,
-                                  w->gcnt, w->list, w->pair_token, R, mean_cols, w->h3, inter, st));
+        CK(l98k_mfma_gemm_grouped2(L.w1.q, L.w1.s, w->h1, L.w3.q, L.w3.s, w->h3, inter, lat, w->latq, w->latqs, w->ng,
+                                   maxg, w->gexp, w->goff, w->gcnt, w->list, w->pair_token, R, mean_cols, inter, st));
         CK(l98k_wide_pro(1, w->h1, w->h3, inter, nullptr, nullptr, 0, inter, pairs, w->hq, w->hqs, st));
         CK(l98k_mfma_gemm_grouped(L.w2.q, L.w2.s, lat, inter, w->hq, w->hqs, w->ng, maxg, w->gexp, w->goff, w->gcnt,
                                   w->list, nullptr, R, mean_cols, w->h2, lat, st));

@@ -626,6 +626,40 @@ extern "C" int l98k_mfma_gemm_grouped(const int8_t *bank, const float *bank_s, i
     return (int)hipGetLastError();
 }
 
+// Two grouped GEMMs over the same columns and groups (an expert's w1 and w3
+// banks, both N x K): on the narrow tiles one launch whose first half of
+// block columns runs bank 1 and the second half bank 3 (jobs); otherwise
+// two launches.
+extern "C" int l98k_mfma_gemm_grouped2(const int8_t *bank1, const float *bank1_s, float *out1, const int8_t *bank3,
+                                       const float *bank3_s, float *out3, int N, int K, const int8_t *X,
+                                       const float *Xs, const int *ng, int max_groups, const int *gexp,
+                                       const int *goff, const int *gcnt, const int *list, const int *xmap,
+                                       int max_cols, int mean_cols, int out_stride, hipStream_t st) {
+    if (N < 1 || K < 32 || (K & 31) || max_groups < 1 || max_cols < 1 || out_stride < N) return -1;
+    if (mean_cols > MFN_COLS) {
+        const int rc = l98k_mfma_gemm_grouped(bank1, bank1_s, N, K, X, Xs, ng, max_groups, gexp, goff, gcnt, list, xmap,
+                                              max_cols, mean_cols, out1, out_stride, st);
+        if (rc) return rc;
+        return l98k_mfma_gemm_grouped(bank3, bank3_s, N, K, X, Xs, ng, max_groups, gexp, goff, gcnt, list, xmap,
+                                      max_cols, mean_cols, out3, out_stride, st);
+    }
+    MfCols c{gexp, goff, gcnt, list, xmap, ng};
+    const int nrt = (N + MFN_ROWS - 1) / MFN_ROWS;
+    MfJobs jobs{};
+    jobs.j[0] = MfJob{bank1, bank1_s, out1, X, Xs, N, out_stride, 0, K};
+    jobs.j[1] = MfJob{bank3, bank3_s, out3, X, Xs, N, out_stride, nrt, K};
+    jobs.n = 2;
+    const int ys = max_cols > 3 * MFN_COLS ? 4 : (max_cols + MFN_COLS - 1) / MFN_COLS;
+    const dim3 gridn(2 * nrt, ys, max_groups);
+    if (K % MF_KC == 0)
+        hipLaunchKernelGGL(k_mfma_q8n<true>, gridn, dim3(MF_THREADS), 0, st, bank1, bank1_s, N, K, (size_t)N * K, X, Xs,
+                           0, c, out1, out_stride, jobs);
+    else
+        hipLaunchKernelGGL(k_mfma_q8n<false>, gridn, dim3(MF_THREADS), 0, st, bank1, bank1_s, N, K, (size_t)N * K, X, Xs,
+                           0, c, out1, out_stride, jobs);
+    return (int)hipGetLastError();
+}
+
 extern "C" int l98k_wide_pro(int mode, const float *src, const float *src2, int src_stride, const int *sel_idx,
                              const float *sel_w, int topk, int n, int rows, int8_t *xq, float *xqs, hipStream_t st) {
     if (rows < 1 || n < 32 || (n & 31) || n > 4 * 64 * WP_MAXJ || mode < 0 || mode > 2) return -1;

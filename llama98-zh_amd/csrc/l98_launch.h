@@ -34,6 +34,13 @@ int l98k_mfma_gemm_grouped(const int8_t *bank, const float *bank_s, int N, int K
                            const int *ng, int max_groups, const int *gexp, const int *goff, const int *gcnt,
                            const int *list, const int *xmap, int max_cols, int mean_cols, float *out, int out_stride,
                            hipStream_t st);
+// Two grouped GEMMs over the same columns and groups (w1 and w3), one
+// launch where the tiles allow.
+int l98k_mfma_gemm_grouped2(const int8_t *bank1, const float *bank1_s, float *out1, const int8_t *bank3,
+                            const float *bank3_s, float *out3, int N, int K, const int8_t *X, const float *Xs,
+                            const int *ng, int max_groups, const int *gexp, const int *goff, const int *gcnt,
+                            const int *list, const int *xmap, int max_cols, int mean_cols, int out_stride,
+                            hipStream_t st);
 // Quantized GEMM inputs of `rows` rows: mode 0 quantize, 1 silu(src)*src2,
 // 2 slot-ordered expert combine; the GEMV prologues' arithmetic.
 int l98k_wide_pro(int mode, const float *src, const float *src2, int src_stride, const int *sel_idx,
