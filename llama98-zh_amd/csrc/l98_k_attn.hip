@@ -107,11 +107,14 @@ __global__ __launch_bounds__(64) void k_attn_prep(AttnArgs a) {
 #define ATT_MAX_HD 128
 #define ATT_MAX_VEC 24                  // kv_mul q heads + up to MAX_CHUNK new K rows
 
+// NV: the vectors the block prepares at most (kv_mul + MAX_CHUNK); the
+// kernels take 12 when kv_mul <= 4, so more blocks share a CU's LDS.
+template <int NV = ATT_MAX_VEC>
 __device__ __forceinline__ void attn_scores_body(const AttnArgs &a, float *__restrict__ att, int att_stride, int slice,
                                                  int kvh, int t) {
-    __shared__ __align__(16) float s_x[ATT_MAX_VEC * ATT_MAX_HD];     // vectors being prepared
-    __shared__ __align__(16) float s_sq[ATT_MAX_VEC * (ATT_MAX_HD + 4)];
-    __shared__ float s_inv[ATT_MAX_VEC];
+    __shared__ __align__(16) float s_x[NV * ATT_MAX_HD];     // vectors being prepared
+    __shared__ __align__(16) float s_sq[NV * (ATT_MAX_HD + 4)];
+    __shared__ float s_inv[NV];
     __shared__ __align__(16) int8_t s_k[ATT_SLICE * (ATT_MAX_HD + 16)];   // K rows, padded
     __shared__ float s_ks[ATT_SLICE * (ATT_MAX_HD / 32)];
     const int tid = threadIdx.x;
@@ -172,7 +175,7 @@ __device__ __forceinline__ void attn_scores_body(const AttnArgs &a, float *__res
     // 4. new K rows: per-32 quantization into the slice (and the cache, by the
     //    token's own block); its V row goes to the cache too.  Groups are 32
     //    consecutive lanes (hd % 32 == 0, 256 % hd == 0 or hd % 256 == 0).
-    for (int base = 0; base < ATT_MAX_VEC * ATT_MAX_HD; base += 256) {
+    for (int base = 0; base < NV * ATT_MAX_HD; base += 256) {
         const int f = base + tid;
         const int nk = n_new * hd;
         if (base >= nk) break;                       // uniform over the block
@@ -648,8 +651,9 @@ __global__ __launch_bounds__(AV_THREADS) void k_attn_av_items(AttnArgs b, const 
 #define AG_NPF 4
 #define AG_THREADS 320
 #define AG_SEG 2047
+template <int NV>
 __global__ __launch_bounds__(256) void k_attn_scores_chunk(AttnArgs a, float *att, int att_stride) {
-    attn_scores_body(a, att, att_stride, blockIdx.x, blockIdx.y, blockIdx.z);
+    attn_scores_body<NV>(a, att, att_stride, blockIdx.x, blockIdx.y, blockIdx.z);
 }
 
 // Dynamic LDS of k_attn_avg: the product double buffer, then the score
@@ -704,12 +708,13 @@ __global__ __launch_bounds__(AG_THREADS) void k_attn_avg(AttnArgs a, const float
     // the score row, its max by order-preserving key
     const float *arow = att + ((size_t)t * a.nh + h) * att_stride;
     uint32_t best = 0;
-    for (int p0 = 0; p0 < L; p0 += 4 * AG_THREADS) {
-        float x[4];
+    // (16 loads per thread in flight at once: one batch up to 5,120 positions)
+    for (int p0 = 0; p0 < L; p0 += 16 * AG_THREADS) {
+        float x[16];
 #pragma unroll
-        for (int u = 0; u < 4; u++) x[u] = arow[imin(p0 + u * AG_THREADS + tid, L - 1)];
+        for (int u = 0; u < 16; u++) x[u] = arow[imin(p0 + u * AG_THREADS + tid, L - 1)];
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
+        for (int u = 0; u < 16; u++) {
             const int p = p0 + u * AG_THREADS + tid;
             if (p < L) {
                 s_ps[ag_slot(p)] = x[u];
@@ -1500,7 +1505,11 @@ extern "C" int l98k_attn(const AttnArgs *a, int nt, int max_len, float *att, hip
             ag_attr = true;
         }
         const int slices = (max_len + ATT_SLICE - 1) / ATT_SLICE;
-        hipLaunchKernelGGL(k_attn_scores_chunk, dim3(slices, a->nkv, nt), dim3(256), 0, st, *a, att, att_stride);
+        if (kv_mul + MAX_CHUNK <= 12)
+            hipLaunchKernelGGL(k_attn_scores_chunk<12>, dim3(slices, a->nkv, nt), dim3(256), 0, st, *a, att, att_stride);
+        else
+            hipLaunchKernelGGL(k_attn_scores_chunk<ATT_MAX_VEC>, dim3(slices, a->nkv, nt), dim3(256), 0, st, *a, att,
+                               att_stride);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return (int)e;
         if (a->hd == 128)
