@@ -3241,8 +3241,9 @@ extern "C" int l98_verify_batch(const LZModel *mm, LZRunState **states, int n_se
         hipStream_t st = S(states[0])->st;
         std::vector<WideItem> items((size_t)n_seq);
         // the control blocks go up as one transfer of [n DevCtl][n
-        // destinations] from pinned memory, then one launch puts each in place
-        const size_t cbytes = (sizeof(DevCtl) + sizeof(DevCtl *)) * (size_t)n_seq;
+        // destinations][n logits destinations][n hidden destinations] from
+        // pinned memory, then one launch puts each in place
+        const size_t cbytes = (sizeof(DevCtl) + sizeof(DevCtl *) + 2 * sizeof(float *)) * (size_t)n_seq;
         if (w->ctl_cap < n_seq) {
             if (w->ctl_host) (void)hipHostFree(w->ctl_host);
             if (w->ctl_dev) (void)hipFree(w->ctl_dev);
@@ -3255,11 +3256,14 @@ extern "C" int l98_verify_batch(const LZModel *mm, LZRunState **states, int n_se
         }
         DevCtl *hs = reinterpret_cast<DevCtl *>(w->ctl_host);
         DevCtl **dst = reinterpret_cast<DevCtl **>(w->ctl_host + sizeof(DevCtl) * (size_t)n_seq);
+        float **ldst = reinterpret_cast<float **>(dst + n_seq), **hdst = ldst + n_seq;
         for (int i = 0; i < n_seq; i++) {
             DState *d = S(states[i]);
             hs[i] = ctl_from(states[i]);
             hs[i].pos_scratch = pos0[i];
             dst[i] = d->ctl;
+            ldst[i] = d->mtp_logits;
+            hdst[i] = d->vhidden;
             items[i] = WideItem{d, i * n_tok, n_tok, pos0[i]};
         }
         if (hipMemcpyAsync(w->ctl_dev, w->ctl_host, cbytes, hipMemcpyHostToDevice, st) ||
@@ -3269,13 +3273,14 @@ extern "C" int l98_verify_batch(const LZModel *mm, LZRunState **states, int n_se
         if (hipMemcpyAsync(w->toks, tokens, sizeof(int) * (size_t)R, hipMemcpyHostToDevice, st) ||
             wide_forward(Mo(mm), w, items.data(), n_seq, R, true, w->hcap, w->logits, st))
             return 1;
+        // every session's verify logits and hidden rows into its own buffers
+        float *const *ldev = reinterpret_cast<float *const *>(w->ctl_dev + (sizeof(DevCtl) + sizeof(DevCtl *)) *
+                                                                               (size_t)n_seq);
+        if (l98k_scatter_rows(w->logits, (size_t)n_tok * c.vocab_size, ldev, n_seq, st) ||
+            l98k_scatter_rows(w->hcap, (size_t)n_tok * c.hidden_size, ldev + n_seq, n_seq, st))
+            return 1;
         for (int i = 0; i < n_seq; i++) {
             DState *d = S(states[i]);
-            if (hipMemcpyAsync(d->mtp_logits, w->logits + (size_t)i * n_tok * c.vocab_size,
-                               sizeof(float) * (size_t)n_tok * c.vocab_size, hipMemcpyDeviceToDevice, st) ||
-                hipMemcpyAsync(d->vhidden, w->hcap + (size_t)i * n_tok * c.hidden_size,
-                               sizeof(float) * (size_t)n_tok * c.hidden_size, hipMemcpyDeviceToDevice, st))
-                return 1;
             states[i]->ssm_slot = (states[i]->ssm_slot + n_tok) % d->depth;
         }
         if (hipStreamSynchronize(st) != hipSuccess) return 1;

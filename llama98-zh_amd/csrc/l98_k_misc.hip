@@ -733,6 +733,26 @@ extern "C" int l98k_put_ctl(const DevCtl *src, DevCtl *const *dst, int n, hipStr
     return (int)hipGetLastError();
 }
 
+// Item i's `per` floats (per % 4 == 0) from src + i * per to dst[i]: a
+// session batch's logits and hidden rows into each session's own buffers in
+// one launch (grid: (slices, n)).
+__global__ __launch_bounds__(256) void k_scatter_rows(const float4 *__restrict__ src, size_t per4,
+                                                      float *const *__restrict__ dst) {
+    const float4 *s = src + (size_t)blockIdx.y * per4;
+    float4 *d = reinterpret_cast<float4 *>(dst[blockIdx.y]);
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < per4; i += (size_t)gridDim.x * 256) d[i] = s[i];
+}
+
+extern "C" int l98k_scatter_rows(const float *src, size_t per, float *const *dst, int n, hipStream_t st) {
+    if (n < 1 || n > 65535 || (per & 3) || per == 0) return -1;
+    const size_t per4 = per >> 2;
+    size_t slices = (per4 + 4 * 256 - 1) / (4 * 256);
+    if (slices > 256) slices = 256;
+    hipLaunchKernelGGL(k_scatter_rows, dim3((unsigned)slices, n), dim3(256), 0, st,
+                       reinterpret_cast<const float4 *>(src), per4, dst);
+    return (int)hipGetLastError();
+}
+
 extern "C" int l98k_batch_round(int op, const BatchSess *bs, int n, int j, int K1, int nc, int d, const int *am,
                                 const float *rows, int *toks, float *h, hipStream_t st) {
     if (n < 1 || K1 < 1 || K1 > 16 || nc < 0 || nc > 8) return -1;

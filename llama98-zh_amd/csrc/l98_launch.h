@@ -179,6 +179,9 @@ int l98k_argmax_part(const unsigned long long *part, int tiles, const float *x, 
 int l98k_accept(DevCtl *ctl, const float *vhidden, int d, float *chain, int depth, int flags, hipStream_t st);
 int l98k_set_tokens(DevCtl *ctl, int op, RoundRec *hist, int hist_cap, hipStream_t st);
 int l98k_put_ctl(const DevCtl *src, DevCtl *const *dst, int n, hipStream_t st);
+// Item i's per floats (per % 4 == 0) from src + i * per to dst[i] (device
+// table), one launch.
+int l98k_scatter_rows(const float *src, size_t per, float *const *dst, int n, hipStream_t st);
 // Session-batch round control (op 0 draft rows in, 1 draft argmaxes and
 // chains out, 2 verify rows in, 3 acceptance, 4 catch-up rows in, 5 round
 // record and advance), block r for session r.
