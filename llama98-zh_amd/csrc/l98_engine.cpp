@@ -1746,8 +1746,9 @@ int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, 
         CK(l98k_wide_pro(1, w->h1, w->h3, inter, nullptr, nullptr, 0, inter, pairs, w->hq, w->hqs, st));
         CK(l98k_mfma_gemm_grouped(L.w2.q, L.w2.s, lat, inter, w->hq, w->hqs, w->ng, maxg, w->gexp, w->goff, w->gcnt,
                                   w->list, nullptr, R, mean_cols, w->h2, lat, st));
-        CK(l98k_wide_pro(2, w->h2, nullptr, lat, w->sel_idx, w->sel_w, topk, lat, R, w->cq, w->cqs, st));
-        CK(l98k_wide_pro(1, w->sgo, w->suo, sw, nullptr, nullptr, 0, sw, R, w->shq, w->shqs, st));
+        // the shared expert's SiLU-mul rows and the routed experts' combine, one launch
+        CK(l98k_wide_pro2(1, w->sgo, w->suo, sw, sw, R, w->shq, w->shqs, 2, w->h2, nullptr, lat, w->sel_idx, w->sel_w,
+                          topk, lat, R, w->cq, w->cqs, st));
         CK(mf_multi({{&L.up, w->up_out, d, w->cq, w->cqs}, {&L.sd, w->sd_out, d, w->shq, w->shqs}}, nullptr, nullptr,
                     R, st));
         ra = w->up_out;

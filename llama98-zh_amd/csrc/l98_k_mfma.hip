@@ -476,15 +476,20 @@ __global__ __launch_bounds__(MF_THREADS) void k_mfma_q8n(const int8_t *__restric
 // Lane l holds float4 f = l + 64 j of the row, so a quantization group is
 // an aligned lane octet.  n % 32 == 0, n <= 4096.
 #define WP_MAXJ 16
-__global__ __launch_bounds__(64) void k_wide_pro(int mode, const float *__restrict__ src,
-                                                 const float *__restrict__ src2, int src_stride,
-                                                 const int *__restrict__ sel_idx, const float *__restrict__ sel_w,
-                                                 int topk, int n, int8_t *__restrict__ xq, float *__restrict__ xqs,
-                                                 float *__restrict__ fout) {
-    EXP_TAB_LOAD(tab);
-    EXP_TAB_PUT(tab);
-    __syncthreads();
-    const int row = blockIdx.x, lane = threadIdx.x;
+struct WideProArgs {
+    const float *src, *src2;
+    const int *sel_idx;
+    const float *sel_w;
+    int8_t *xq;
+    float *xqs, *fout;
+    int mode, src_stride, topk, n;
+};
+__device__ __forceinline__ void wide_pro_body(int mode, const float *__restrict__ src, const float *__restrict__ src2,
+                                              int src_stride, const int *__restrict__ sel_idx,
+                                              const float *__restrict__ sel_w, int topk, int n,
+                                              int8_t *__restrict__ xq, float *__restrict__ xqs,
+                                              float *__restrict__ fout, int row, const float *tab) {
+    const int lane = threadIdx.x;
     const int nf = n >> 2, nb = n >> 5;
     for (int j = 0; j < WP_MAXJ; j++) {
         if (64 * j >= nf) break;                   // wave-uniform
@@ -519,6 +524,27 @@ __global__ __launch_bounds__(64) void k_wide_pro(int mode, const float *__restri
             }
         }
     }
+}
+__global__ __launch_bounds__(64) void k_wide_pro(int mode, const float *__restrict__ src,
+                                                 const float *__restrict__ src2, int src_stride,
+                                                 const int *__restrict__ sel_idx, const float *__restrict__ sel_w,
+                                                 int topk, int n, int8_t *__restrict__ xq, float *__restrict__ xqs,
+                                                 float *__restrict__ fout) {
+    EXP_TAB_LOAD(tab);
+    EXP_TAB_PUT(tab);
+    __syncthreads();
+    wide_pro_body(mode, src, src2, src_stride, sel_idx, sel_w, topk, n, xq, xqs, fout, blockIdx.x, tab);
+}
+// Two independent producers in one launch: blocks [0, rows_a) run a's rows,
+// the rest b's.
+__global__ __launch_bounds__(64) void k_wide_pro2(WideProArgs a, int rows_a, WideProArgs b) {
+    EXP_TAB_LOAD(tab);
+    EXP_TAB_PUT(tab);
+    __syncthreads();
+    const bool first = (int)blockIdx.x < rows_a;
+    const WideProArgs &p = first ? a : b;
+    wide_pro_body(p.mode, p.src, p.src2, p.src_stride, p.sel_idx, p.sel_w, p.topk, p.n, p.xq, p.xqs, p.fout,
+                  first ? blockIdx.x : blockIdx.x - rows_a, tab);
 }
 
 // ---------------------------------------------------------- host glue ---
@@ -657,6 +683,27 @@ extern "C" int l98k_mfma_gemm_grouped2(const int8_t *bank1, const float *bank1_s
     else
         hipLaunchKernelGGL(k_mfma_q8n<false>, gridn, dim3(MF_THREADS), 0, st, bank1, bank1_s, N, K, (size_t)N * K, X, Xs,
                            0, c, out1, out_stride, jobs);
+    return (int)hipGetLastError();
+}
+
+static bool wide_pro_ok(int mode, int src_stride, const int *sel_idx, const float *sel_w, int topk, int n, int rows) {
+    if (rows < 1 || n < 32 || (n & 31) || n > 4 * 64 * WP_MAXJ || mode < 0 || mode > 2) return false;
+    if (mode < 2 && (src_stride < n || (src_stride & 3))) return false;
+    if (mode == 2 && (topk < 1 || topk > MAX_TOPK || !sel_idx || !sel_w)) return false;
+    return true;
+}
+
+// Two quantizing producers (modes as l98k_wide_pro) in one launch.
+extern "C" int l98k_wide_pro2(int mode_a, const float *src_a, const float *src2_a, int stride_a, int n_a, int rows_a,
+                              int8_t *xq_a, float *xqs_a, int mode_b, const float *src_b, const float *src2_b,
+                              int stride_b, const int *sel_idx_b, const float *sel_w_b, int topk_b, int n_b,
+                              int rows_b, int8_t *xq_b, float *xqs_b, hipStream_t st) {
+    if (mode_a == 2 || !wide_pro_ok(mode_a, stride_a, nullptr, nullptr, 0, n_a, rows_a) ||
+        !wide_pro_ok(mode_b, stride_b, sel_idx_b, sel_w_b, topk_b, n_b, rows_b) || !xq_a || !xqs_a || !xq_b || !xqs_b)
+        return -1;
+    const WideProArgs a{src_a, src2_a, nullptr, nullptr, xq_a, xqs_a, nullptr, mode_a, stride_a, 0, n_a};
+    const WideProArgs b{src_b, src2_b, sel_idx_b, sel_w_b, xq_b, xqs_b, nullptr, mode_b, stride_b, topk_b, n_b};
+    hipLaunchKernelGGL(k_wide_pro2, dim3(rows_a + rows_b), dim3(64), 0, st, a, rows_a, b);
     return (int)hipGetLastError();
 }
 

@@ -179,6 +179,11 @@ int l98k_argmax_part(const unsigned long long *part, int tiles, const float *x, 
 int l98k_accept(DevCtl *ctl, const float *vhidden, int d, float *chain, int depth, int flags, hipStream_t st);
 int l98k_set_tokens(DevCtl *ctl, int op, RoundRec *hist, int hist_cap, hipStream_t st);
 int l98k_put_ctl(const DevCtl *src, DevCtl *const *dst, int n, hipStream_t st);
+// Two quantizing producers in one launch (a: mode 0 or 1, b: any mode).
+int l98k_wide_pro2(int mode_a, const float *src_a, const float *src2_a, int stride_a, int n_a, int rows_a,
+                   int8_t *xq_a, float *xqs_a, int mode_b, const float *src_b, const float *src2_b, int stride_b,
+                   const int *sel_idx_b, const float *sel_w_b, int topk_b, int n_b, int rows_b, int8_t *xq_b,
+                   float *xqs_b, hipStream_t st);
 // Item i's per floats (per % 4 == 0) from src + i * per to dst[i] (device
 // table), one launch.
 int l98k_scatter_rows(const float *src, size_t per, float *const *dst, int n, hipStream_t st);
