@@ -475,7 +475,7 @@ __global__ __launch_bounds__(1024) void k_moe_group(const int *__restrict__ sel_
                                                     int *__restrict__ ng, int *__restrict__ gexp,
                                                     int *__restrict__ goff, int *__restrict__ gcnt,
                                                     int *__restrict__ list, int *__restrict__ pair_token) {
-    __shared__ int cnt[MAX_EXPERTS], off[MAX_EXPERTS], gid[MAX_EXPERTS], cur[MAX_EXPERTS];
+    __shared__ int cnt[MAX_EXPERTS], off[MAX_EXPERTS], cur[MAX_EXPERTS];
     const int tid = threadIdx.x;
     if (tid < MAX_EXPERTS) { cnt[tid] = 0; cur[tid] = 0; }
     __syncthreads();
@@ -485,20 +485,24 @@ __global__ __launch_bounds__(1024) void k_moe_group(const int *__restrict__ sel_
         if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
     }
     __syncthreads();
-    if (tid == 0) {
-        int o = 0, g = 0;
-        for (int e = 0; e < E; e++) {
-            off[e] = o;
-            gid[e] = cnt[e] ? g : -1;
-            if (cnt[e]) {
-                gexp[g] = e;
-                goff[g] = o;
-                gcnt[g] = cnt[e];
-                g++;
-            }
-            o += cnt[e];
-        }
-        *ng = g;
+    // offsets (exclusive prefix of the counts in expert order) and group
+    // slots (rank of each present expert) on one wave: lane l takes experts
+    // l and l + 64
+    static_assert(MAX_EXPERTS <= 128, "two experts per lane");
+    if (tid < 64) {
+        const int c0 = tid < E ? cnt[tid] : 0, c1 = tid + 64 < E ? cnt[tid + 64] : 0;
+        const uint32_t i0 = wave_scan_u32((uint32_t)c0), i1 = wave_scan_u32((uint32_t)c1);
+        const int tot0 = __builtin_amdgcn_readlane((int)i0, 63);
+        const int o0 = (int)i0 - c0, o1 = tot0 + (int)i1 - c1;
+        const unsigned long long b0 = __ballot(c0 > 0), b1 = __ballot(c1 > 0);
+        const unsigned long long below = (1ull << tid) - 1ull;
+        const int n0 = __popcll(b0);
+        const int g0 = __popcll(b0 & below), g1 = n0 + __popcll(b1 & below);
+        off[tid] = o0;
+        off[tid + 64] = o1;
+        if (c0) { gexp[g0] = tid; goff[g0] = o0; gcnt[g0] = c0; }
+        if (c1) { gexp[g1] = tid + 64; goff[g1] = o1; gcnt[g1] = c1; }
+        if (tid == 0) *ng = n0 + __popcll(b1);
     }
     __syncthreads();
     for (int p = tid; p < npairs; p += blockDim.x) {
