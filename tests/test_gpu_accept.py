@@ -47,7 +47,8 @@ def test_device_argmax_matches_oracle(pkg, n):
             assert out[r] == want, (mode, r, out[r], want)
 
 
-@pytest.mark.parametrize("M,gs", [(1, 0), (2, 0), (3, 0), (4, 0), (8, 0), (1, 64), (4, 64), (1, 128), (4, 128)])
+@pytest.mark.parametrize("M,gs", [(1, 0), (2, 0), (3, 0), (4, 0), (5, 0), (6, 0), (8, 0), (1, 64), (4, 64), (6, 64),
+                                  (1, 128), (4, 128)])
 def test_gemv_argmax_epilogue_matches_oracle(pkg, M, gs):
     # The rounds' argmax: per-tile candidates from the lm_head GEMV's
     # epilogue, reduced by l98k_argmax_part, with one scale per weight row

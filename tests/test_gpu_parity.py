@@ -81,7 +81,8 @@ def test_verify_and_draft_bit_exact(pkg, tiny):
     eng.close()
 
 
-@pytest.mark.parametrize("k", [1, 3])
+# k = 4 and 5 run the 5- and 6-row instances of the verify's kernels
+@pytest.mark.parametrize("k", [1, 3, 4, 5])
 def test_spec_rounds_match(pkg, tiny, k):
     print(f"[case] spec rounds tiny k={k}", flush=True)
     prompt = pkg.prompt_tokens(0, 40, 8192)
