@@ -3,6 +3,8 @@
 // l98_devmath.h for the numeric contract).
 #include "l98_devmath.h"
 
+typedef float v4f __attribute__((ext_vector_type(4)));
+
 // ---------------------------------------------------------- KDA layer ---
 //
 // One block of 4*kd threads per head (nk == nv).  The conv phase gives
@@ -424,7 +426,8 @@ __device__ __forceinline__ void kda_step_body(const KdaStepArgs &a, int h) {
             float4 *dst = reinterpret_cast<float4 *>(a.state + (size_t)so * a.slot_stride + head_off) + tid;
 #pragma unroll
             for (int i = 0; i < RPL / 4; i++)
-                dst[i * NTHR] = make_float4(S[4 * i], S[4 * i + 1], S[4 * i + 2], S[4 * i + 3]);
+                __builtin_nontemporal_store(v4f{S[4 * i], S[4 * i + 1], S[4 * i + 2], S[4 * i + 3]},
+                                            reinterpret_cast<v4f *>(dst + i * NTHR));
         }
         so_t = so_t + 1 == a.depth ? 0 : so_t + 1;
         if (quarter == 0) {
