@@ -24,8 +24,10 @@
 #include <time.h>
 #include <unistd.h>
 
+#include <algorithm>
 #include <memory>
 #include <mutex>
+#include <numeric>
 #include <vector>
 
 #include "../../include/llama98_hip.h"
@@ -1551,6 +1553,23 @@ int mf_multi(std::initializer_list<MfOut> jobs, const int8_t *xq, const float *x
     return l98k_mfma_gemm_multi(n, W, ws, N, out, os, K, X, Xs, R, st);
 }
 
+// Orders an attention item launch (any order is correct: each item names
+// its rows and planes): the longer half of the items by span, longest first,
+// then the rest shortest first, so that blocks y and y + n/2 of the launch -
+// which share a CU when the grid fills two blocks per CU - pair a long item
+// with a short one instead of two long ones.
+static void pair_long_short(std::vector<AttnItem> &ai, const std::vector<int> &len) {
+    const int n = (int)ai.size();
+    if (n < 3) return;
+    std::vector<int> idx((size_t)n);
+    std::iota(idx.begin(), idx.end(), 0);
+    std::stable_sort(idx.begin(), idx.end(), [&](int x, int y) { return len[(size_t)x] > len[(size_t)y]; });
+    std::vector<AttnItem> out((size_t)n);
+    const int h2 = (n + 1) / 2;
+    for (int y = 0; y < n; y++) out[(size_t)y] = ai[(size_t)idx[(size_t)(y < h2 ? y : n - 1 - (y - h2))]];
+    ai.swap(out);
+}
+
 // The trunk over R rows of w->toks (device ids), grouped into sessions by
 // items (row order).  advance: KDA ring advance per token (verify) or not
 // (prefill).  capture: device rows [R][d] of the final-normed hidden, or
@@ -1582,6 +1601,7 @@ int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, 
     {
         std::vector<KdaItem> ki((size_t)n_items);
         std::vector<AttnItem> ai;
+        std::vector<int> alen;                  // each attention item's last position + 1
         for (int i = 0; i < n_items; i++) {
             const WideItem &I = items[i];
             DState *s = I.d;
@@ -1590,13 +1610,18 @@ int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, 
             max_len = I.pos0 + I.n > max_len ? I.pos0 + I.n : max_len;
             ki[i] = KdaItem{s->kda, s->conv, &s->ctl->slot_base, s->kda_slot, s->conv_slot, I.row0, I.n, s->depth, 0};
             if (prefill_items) {
-                for (int c0 = 0; c0 < I.n; c0 += MAX_CHUNK)
-                    ai.push_back(AttnItem{s->kq, s->vq, s->ks, s->vs, &s->ctl->pos_scratch, I.row0 + c0,
-                                          I.n - c0 < MAX_CHUNK ? I.n - c0 : MAX_CHUNK, s->seq_len, pos_base + c0});
+                for (int c0 = 0; c0 < I.n; c0 += MAX_CHUNK) {
+                    const int nr = I.n - c0 < MAX_CHUNK ? I.n - c0 : MAX_CHUNK;
+                    ai.push_back(AttnItem{s->kq, s->vq, s->ks, s->vs, &s->ctl->pos_scratch, I.row0 + c0, nr,
+                                          s->seq_len, pos_base + c0});
+                    alen.push_back(I.pos0 + pos_base + c0 + nr);
+                }
             } else {
                 ai.push_back(AttnItem{s->kq, s->vq, s->ks, s->vs, &s->ctl->pos_scratch, I.row0, I.n, s->seq_len, 0});
+                alen.push_back(I.pos0 + I.n);
             }
         }
+        pair_long_short(ai, alen);
         if (prefill_items) {
             attn_items = true;
             n_attn = (int)ai.size();

@@ -967,41 +967,46 @@ __global__ __launch_bounds__(512) void k_attn_av_rows(AttnArgs b, const AttnItem
 // k_attn_rows<HD, WPT>: the softmax and value sums of an item launch whose
 // K and V rows are all in the cache, 64- or 128-wide heads, positions up to
 // what the block's LDS holds (the launch checks): one block of 8 waves per
-// (q head, item), WPT waves per token (2 when every item has at most 4
-// rows), so the block holds TPB = 8 / WPT tokens; wave w takes token
-// w / WPT as its part w % WPT.
-//   1. each token's part-0 wave prepares its q head (RMSNorm(1+w) with the
+// (q head, item) holding TPB = 8 / WPT tokens (WPT = 2 when every item has
+// at most 4 rows).
+//   1. each token's first wave prepares its q head (RMSNorm(1+w) with the
 //      serial sum, NeoX rotary), as attn_prep_body does;
-//   2. the kv head's K rows are staged in chunks of AR_CH positions, once
-//      for every token of the block; each wave computes its token's scores
-//      for its positions of the chunk (the 32-group products in order, then
-//      the groups, times attn_scale), two positions interleaved when it has
-//      two;
-//   3. each token's part-0 wave takes the softmax (max by order-preserving
+//   2. scores, chunk by chunk of SCH = 512 / (HD/32) K rows: lane (position,
+//      32-group g) converts its 32 int8 of the row once and runs the group's
+//      product chain (the 32 products in order from 0) for every token of
+//      the block, times the group's scale; then lane (token, position) adds
+//      the groups in order from 0 and applies attn_scale: the additions of
+//      attn_scores_body, each in its own order, so the bits are its bits;
+//   3. each token's first wave takes the softmax (max by order-preserving
 //      key, exp, the serial loop's sum, scale);
-//   4. the V rows are staged in chunks of AR_CH positions, transposed
-//      ([d][position], scales [group][position]), and lane l of part r adds
-//      (a[p] * v[p][d]) * vs[p][d/32] for its elements d = u*64 + l
-//      (u = r, r + WPT, ...) over the positions in order, four per LDS read,
-//      the next four's reads issued before the current four's adds;
+//   4. value sums, chunk by chunk of VCH = 8192 / HD V rows staged once as
+//      fp32 (row-major, scales [group][position]): a lane takes one element
+//      d of two consecutive tokens and adds (a[p] * v[p][d]) * vs[p][d/32]
+//      to each token's sum over the positions in order, four per step (one
+//      read of v for both; the LDS reads, not the VALU, bound this phase);
 //   5. the sigmoid output gate and the per-32 quantization.
-// The arithmetic is attn_av_body's and attn_scores_body's, so the bits are.
+// Every chunk's global loads are issued into registers before the previous
+// chunk is computed (the first K chunk's before step 1, the first V chunk's
+// with the last K chunk), and stored to LDS after it.
 // LDS: the staging area (STAGE bytes), then the score rows [TPB][lp] floats
 // (dynamic).
-#define AR_CH 128
 #define AR_STATIC_MARGIN (5 * 1024)     // the kernel's static LDS (q heads, exp table) and slack
 #define AR_THREADS (MAX_CHUNK * 64)
 #define GLOBAL __attribute__((address_space(1)))     // the cache planes: global loads, not flat
 typedef int v4i_a __attribute__((ext_vector_type(4)));
+typedef float v4f_a __attribute__((ext_vector_type(4)));
 template <int HD>
 struct ArPlan {
-    static constexpr int NDP = HD / 64, NB = HD / 32, CPR = HD / 16, KS = HD + 16, VS = AR_CH + 4;
-    static constexpr int K_BYTES = AR_CH * KS + AR_CH * NB * 4;
-    static constexpr int V_BYTES = HD * VS + NB * AR_CH * 4;
+    static constexpr int NDP = HD / 64, NB = HD / 32, CPR = HD / 16, KS = HD + 16;
+    static constexpr int WPG = 8 / NB, SCH = WPG * 64;          // scores: waves per group, positions per chunk
+    static constexpr int VCH = AR_THREADS * 16 / HD, VS = HD + 4; // values: positions per chunk, floats per row
+    static constexpr int K_BYTES = SCH * KS + SCH * NB * 4 + MAX_CHUNK * NB * SCH * 4;
+    static constexpr int V_BYTES = VCH * VS * 4 + NB * VCH * 4;
     static constexpr int Q_BYTES = MAX_CHUNK * HD * 4;
     static constexpr int m2(int x, int y) { return x > y ? x : y; }
     static constexpr int STAGE = (m2(m2(K_BYTES, V_BYTES), Q_BYTES) + 15) & ~15;
-    static_assert(AR_CH * CPR % AR_THREADS == 0 && AR_CH * NB <= AR_THREADS && (HD * VS) % 16 == 0,
+    static_assert(SCH * CPR == 2 * AR_THREADS && SCH * NB == AR_THREADS && VCH * HD / 4 == 4 * AR_THREADS &&
+                      NB * VCH <= AR_THREADS && (SCH * KS) % 16 == 0 && (VCH * VS * 4) % 16 == 0,
                   "chunk staging layout");
 };
 
@@ -1010,7 +1015,8 @@ __global__ __launch_bounds__(AR_THREADS) void k_attn_rows(AttnArgs b, const Attn
                                                           int plane, int lp) {
     using P = ArPlan<HD>;
     constexpr int NDP = P::NDP, NB = P::NB, CPR = P::CPR, KS = P::KS, VS = P::VS, NTHR = AR_THREADS;
-    constexpr int TPB = MAX_CHUNK / WPT, JP = AR_CH / (64 * WPT);      // tokens per block, positions per lane
+    constexpr int SCH = P::SCH, VCH = P::VCH, WPG = P::WPG;
+    constexpr int TPB = MAX_CHUNK / WPT;                          // tokens per block
     EXP_TAB_LOAD(tab);
     extern __shared__ __align__(16) char smem[];
     __shared__ __align__(16) float s_q[TPB][HD];                 // the prepared q heads
@@ -1021,10 +1027,44 @@ __global__ __launch_bounds__(AR_THREADS) void k_attn_rows(AttnArgs b, const Attn
     const AttnArgs a = attn_item_args(b, it, plane);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, t = wave / WPT, part = wave - t * WPT;
     const int kv_mul = a.nh / a.nkv, kvh = h / kv_mul;
-    const int pos0 = *a.ctl_pos + a.pos_off, n = it.n, Lmax = pos0 + n;
+    const int pos0 = __builtin_amdgcn_readfirstlane(*a.ctl_pos + a.pos_off), n = it.n, Lmax = pos0 + n;
     const bool live = t < n, lead = live && part == 0;
     const int L = pos0 + imin(t, n - 1) + 1;
     float *arow = s_a + (size_t)t * lp;
+    const int8_t *kbase = a.kcache + kvh * HD;
+    const float *ksbase = a.kscale + kvh * NB;
+    const int8_t *vbase = a.vcache + kvh * HD;
+    const float *vsbase = a.vscale + kvh * NB;
+    const size_t rst = (size_t)a.kv_dim, sst = (size_t)(a.kv_dim >> 5);
+    // the thread's share of a K chunk (two 16-byte pieces and one scale) and
+    // of a V chunk (four 4-byte pieces f = u * NTHR + tid, row f / DPR - so a
+    // wave's pieces are whole rows, and its fp32 stores contiguous runs -
+    // and one scale for tid < VCH * NB); a piece past the chunk's end reads
+    // the chunk's last row
+    constexpr int DPR = HD / 4;
+    v4i_a kr[2];
+    int vr[4];
+    float ksv, vsv = 0.0f;
+#define AR_LOAD_K(c0)                                                                                   \
+    {                                                                                                   \
+        const int nc_ = imin(SCH, Lmax - (c0));                                                         \
+        _Pragma("unroll") for (int u = 0; u < 2; u++) {                                                 \
+            const int f = u * NTHR + tid, p = imin(f / CPR, nc_ - 1), c = f % CPR;                      \
+            kr[u] = *(const GLOBAL v4i_a *)(kbase + (size_t)((c0) + p) * rst + c * 16);                 \
+        }                                                                                               \
+        ksv = ((const GLOBAL float *)ksbase)[(size_t)((c0) + imin(tid / NB, nc_ - 1)) * sst + tid % NB]; \
+    }
+#define AR_LOAD_V(c0)                                                                                   \
+    {                                                                                                   \
+        const int nc_ = imin(VCH, Lmax - (c0));                                                         \
+        _Pragma("unroll") for (int u = 0; u < 4; u++) {                                                 \
+            const int f = u * NTHR + tid;                                                               \
+            vr[u] = *(const GLOBAL int *)(vbase + (size_t)((c0) + imin(f / DPR, nc_ - 1)) * rst + (f % DPR) * 4); \
+        }                                                                                               \
+        if (tid < VCH * NB)                                                                             \
+            vsv = ((const GLOBAL float *)vsbase)[(size_t)((c0) + imin(tid / NB, nc_ - 1)) * sst + tid % NB]; \
+    }
+    AR_LOAD_K(0);
     // 1. q heads: squares in the staging area, the serial sum, RMSNorm(1+w),
     //    rotary (partners through s_q)
     if (lead) {
@@ -1069,81 +1109,61 @@ __global__ __launch_bounds__(AR_THREADS) void k_attn_rows(AttnArgs b, const Attn
     __syncthreads();
     // 2. scores, chunk by chunk of K rows
     {
-        int8_t *s_k = reinterpret_cast<int8_t *>(stage);                              // [AR_CH][KS]
-        float *s_ks = reinterpret_cast<float *>(stage + AR_CH * KS);                   // [AR_CH][NB]
-        const int8_t *kbase = a.kcache + kvh * HD;
-        const float *ksbase = a.kscale + kvh * NB;
-        const size_t kst = (size_t)a.kv_dim, sst = (size_t)(a.kv_dim >> 5);
+        int8_t *s_k = reinterpret_cast<int8_t *>(stage);                              // [SCH][KS]
+        float *s_ks = reinterpret_cast<float *>(stage + SCH * KS);                     // [SCH][NB]
+        float *s_part = s_ks + SCH * NB;                                               // [TPB][NB][SCH]
         const float scale = a.attn_scale;
-        for (int c0 = 0; c0 < Lmax; c0 += AR_CH) {
-            const int nc = imin(AR_CH, Lmax - c0), total = nc * CPR, stotal = nc * NB;
-            constexpr int KU = AR_CH * CPR / NTHR;
-            int4 kr[KU];
+        const int g = wave / WPG, pl = (wave - g * WPG) * 64 + lane;
+        for (int c0 = 0; c0 < Lmax; c0 += SCH) {
+            const int nc = imin(SCH, Lmax - c0);
 #pragma unroll
-            for (int u = 0; u < KU; u++) {
-                const int f = imin(u * NTHR + tid, total - 1), p = f / CPR, c = f - p * CPR;
-                const v4i_a q = *(const GLOBAL v4i_a *)(kbase + (size_t)(c0 + p) * kst + c * 16);
-                kr[u] = make_int4(q.x, q.y, q.z, q.w);
+            for (int u = 0; u < 2; u++) {
+                const int f = u * NTHR + tid, p = f / CPR, c = f % CPR;
+                if (p < nc) *reinterpret_cast<v4i_a *>(s_k + p * KS + c * 16) = kr[u];
             }
-            const int sf = imin(tid, stotal - 1), sp = sf / NB, sg = sf - sp * NB;
-            const float ksv = ((const GLOBAL float *)ksbase)[(size_t)(c0 + sp) * sst + sg];
-#pragma unroll
-            for (int u = 0; u < KU; u++) {
-                const int f = u * NTHR + tid, p = f / CPR, c = f - p * CPR;
-                if (f < total) *reinterpret_cast<int4 *>(s_k + p * KS + c * 16) = kr[u];
-            }
-            if (tid < stotal) s_ks[sp * NB + sg] = ksv;
+            if (tid < nc * NB) s_ks[tid] = ksv;
             __syncthreads();
-            // the wave's positions part*64 + lane + j*64*WPT; a position past
-            // the token's end computes on row 0 and stores nothing
-            const int lim = __builtin_amdgcn_readfirstlane(imin(nc, L - c0));
-            if (live && part * 64 < lim) {
-                int pl[JP];
-                bool ok[JP];
+            if (c0 + SCH < Lmax) AR_LOAD_K(c0 + SCH) else AR_LOAD_V(0);
+            // lane (pl, g): the group's chains for every token; a position
+            // past the chunk's end computes on row 0 and is never added
+            {
+                const int pc = pl < nc ? pl : 0;
+                const v4i_a k0 = *reinterpret_cast<const v4i_a *>(s_k + pc * KS + g * 32);
+                const v4i_a k1 = *reinterpret_cast<const v4i_a *>(s_k + pc * KS + g * 32 + 16);
+                float acc[TPB];
 #pragma unroll
-                for (int j = 0; j < JP; j++) {
-                    const int q = (j * WPT + part) * 64 + lane;
-                    ok[j] = q < lim;
-                    pl[j] = ok[j] ? q : 0;
+                for (int j = 0; j < TPB; j++) acc[j] = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 32; e++) {
+                    const int w = e < 16 ? k0[e >> 2] : k1[(e - 16) >> 2];
+                    const float kf = (float)(int8_t)((w >> (8 * (e & 3))) & 0xFF);
+#pragma unroll
+                    for (int j = 0; j < TPB; j++) acc[j] += s_q[j][g * 32 + e] * kf;
                 }
-                const float *qq = s_q[t];
-                float sum[JP];
+                const float ks = s_ks[pc * NB + g];
 #pragma unroll
-                for (int j = 0; j < JP; j++) sum[j] = 0.0f;
-#pragma unroll
-                for (int dd = 0; dd < HD; dd += 32) {
-                    int4 k0[JP], k1[JP];
-#pragma unroll
-                    for (int j = 0; j < JP; j++) {
-                        k0[j] = *reinterpret_cast<const int4 *>(s_k + pl[j] * KS + dd);
-                        k1[j] = *reinterpret_cast<const int4 *>(s_k + pl[j] * KS + dd + 16);
-                    }
-                    float acc[JP];
-#pragma unroll
-                    for (int j = 0; j < JP; j++) acc[j] = 0.0f;
-#pragma unroll
-                    for (int e = 0; e < 16; e++) {
-                        const float qe = qq[dd + e];
-#pragma unroll
-                        for (int j = 0; j < JP; j++) acc[j] += qe * (float)reinterpret_cast<const int8_t *>(&k0[j])[e];
-                    }
-#pragma unroll
-                    for (int e = 0; e < 16; e++) {
-                        const float qe = qq[dd + 16 + e];
-#pragma unroll
-                        for (int j = 0; j < JP; j++) acc[j] += qe * (float)reinterpret_cast<const int8_t *>(&k1[j])[e];
-                    }
-#pragma unroll
-                    for (int j = 0; j < JP; j++) sum[j] += acc[j] * s_ks[pl[j] * NB + (dd >> 5)];
-                }
-#pragma unroll
-                for (int j = 0; j < JP; j++)
-                    if (ok[j]) arow[c0 + pl[j]] = sum[j] * scale;
+                for (int j = 0; j < TPB; j++) s_part[(j * NB + g) * SCH + pl] = acc[j] * ks;
             }
             __syncthreads();
+            // lane (token, position): the groups in order
+#pragma unroll
+            for (int r = 0; r < TPB * SCH / NTHR; r++) {
+                const int idx = r * NTHR + tid, j = idx / SCH, p = idx % SCH;
+                if (j < n && c0 + p < pos0 + j + 1 && p < nc) {
+                    float sum = 0.0f;
+#pragma unroll
+                    for (int gg = 0; gg < NB; gg++) sum += s_part[(j * NB + gg) * SCH + p];
+                    s_a[(size_t)j * lp + c0 + p] = sum * scale;
+                }
+            }
         }
     }
-    // 3. softmax of each token, by its part-0 wave: max by order-preserving
+    // the last K chunk's registers are taken here, so that no later write of
+    // a register a K prefetch could still own (on a path the compiler cannot
+    // exclude) waits for the V chunk loads in flight
+    asm volatile("" ::"v"(kr[0]), "v"(kr[1]), "v"(ksv));
+    __syncthreads();
+    // 3. softmax of each token, by its first wave: max by order-preserving
     //    key, exp, the serial loop's sum over the score row, scale (every
     //    token at once; the exact wave sum's tables would take the
     //    registers that let two blocks share a CU)
@@ -1159,93 +1179,122 @@ __global__ __launch_bounds__(AR_THREADS) void k_attn_rows(AttnArgs b, const Attn
         const float inv = (sum > 0.0f) ? 1.0f / sum : 0.0f;
         for (int p = lane; p < L; p += 64) arow[p] *= inv;
     }
-    __syncthreads();
-    // 4. value sums, chunk by chunk of V rows (transposed); the wave's
-    //    elements u = part, part + WPT, ... (NU of them)
-    constexpr int NU = NDP >= WPT ? NDP / WPT : 1;
-    const bool vwork = live && part < NDP;
-    float o[NU];
-#pragma unroll
-    for (int i = 0; i < NU; i++) o[i] = 0.0f;
+    // 4. value sums, chunk by chunk of V rows (fp32): lane l of wave w takes
+    //    element d = (w % NDH) * 64 + l of tokens t0 = 2 (w / NDH) and t0 + 1,
+    //    so each V element read feeds two chains; t0 + 1 has one position more
+    constexpr int NDH = HD / 64;                                   // waves per token pair
+    const int tp = wave / NDH, dv = (wave - tp * NDH) * 64 + lane, t0 = 2 * tp;
+    const bool vwork = tp < TPB / 2 && t0 < n, vboth = t0 + 1 < n;
+    const int La = pos0 + t0 + 1, Lb = vboth ? La + 1 : La;
+    float o0 = 0.0f, o1 = 0.0f;
     {
-        int8_t *s_vt = reinterpret_cast<int8_t *>(stage);                              // [HD][VS]
-        float *s_vst = reinterpret_cast<float *>(stage + HD * VS);                      // [NB][AR_CH]
-        const int8_t *vbase = a.vcache + kvh * HD;
-        const float *vsbase = a.vscale + kvh * NB;
-        const size_t vst = (size_t)a.kv_dim, sst = (size_t)(a.kv_dim >> 5);
-        for (int c0 = 0; c0 < Lmax; c0 += AR_CH) {
-            const int nc = imin(AR_CH, Lmax - c0), total = nc * CPR, stotal = nc * NB;
-            constexpr int KU = AR_CH * CPR / NTHR;
-            int4 vr[KU];
+        float *s_vf = reinterpret_cast<float *>(stage);                                // [VCH][VS]
+        float *s_vst = s_vf + VCH * VS;                                                // [NB][VCH]
+        for (int c0 = 0; c0 < Lmax; c0 += VCH) {
+            const int nc = imin(VCH, Lmax - c0);
+            __syncthreads();                          // the stage's previous readers are done
+            {
 #pragma unroll
-            for (int u = 0; u < KU; u++) {
-                const int f = imin(u * NTHR + tid, total - 1), p = f / CPR, c = f - p * CPR;
-                const v4i_a q = *(const GLOBAL v4i_a *)(vbase + (size_t)(c0 + p) * vst + c * 16);
-                vr[u] = make_int4(q.x, q.y, q.z, q.w);
-            }
-            const int sf = imin(tid, stotal - 1), sp = sf / NB, sg = sf - sp * NB;
-            const float vsv = ((const GLOBAL float *)vsbase)[(size_t)(c0 + sp) * sst + sg];
+                for (int u = 0; u < 4; u++) {
+                    const int f = u * NTHR + tid, p = f / DPR, c = f % DPR;
+                    if (p < nc) {
+                        v4f_a f4;
 #pragma unroll
-            for (int u = 0; u < KU; u++) {
-                const int f = u * NTHR + tid, p = f / CPR, c = f - p * CPR;
-                if (f < total) {
-                    const int w4[4] = {vr[u].x, vr[u].y, vr[u].z, vr[u].w};
-#pragma unroll
-                    for (int k = 0; k < 16; k++) s_vt[(16 * c + k) * VS + p] = (int8_t)((w4[k >> 2] >> (8 * (k & 3))) & 0xFF);
-                }
-            }
-            if (tid < stotal) s_vst[sg * AR_CH + sp] = vsv;
-            __syncthreads();
-            const int pe = __builtin_amdgcn_readfirstlane(imin(nc, L - c0));
-            if (vwork && pe > 0) {
-                const int pe4 = pe & ~3;
-                const float *ar = arow + c0;
-                const int8_t *vt[NU];
-                const float *vsr[NU];
-#pragma unroll
-                for (int i = 0; i < NU; i++) {
-                    const int d = (i * WPT + part) * 64 + lane;
-                    vt[i] = s_vt + d * VS;
-                    vsr[i] = s_vst + (d >> 5) * AR_CH;
-                }
-#pragma unroll 4
-                for (int p = 0; p < pe4; p += 4) {
-                    const float4 ap = *reinterpret_cast<const float4 *>(ar + p);
-#pragma unroll
-                    for (int i = 0; i < NU; i++) {
-                        const uint32_t vb = *reinterpret_cast<const uint32_t *>(vt[i] + p);
-                        const float4 vs = *reinterpret_cast<const float4 *>(vsr[i] + p);
-                        const float p0 = ap.x * (float)(int8_t)(vb & 0xFF) * vs.x;
-                        const float p1 = ap.y * (float)(int8_t)((vb >> 8) & 0xFF) * vs.y;
-                        const float p2 = ap.z * (float)(int8_t)((vb >> 16) & 0xFF) * vs.z;
-                        const float p3 = ap.w * (float)(int8_t)(vb >> 24) * vs.w;
-                        o[i] += p0;
-                        o[i] += p1;
-                        o[i] += p2;
-                        o[i] += p3;
+                        for (int k = 0; k < 4; k++) f4[k] = (float)(int8_t)((vr[u] >> (8 * k)) & 0xFF);
+                        *reinterpret_cast<v4f_a *>(s_vf + p * VS + c * 4) = f4;
                     }
                 }
-                for (int p = pe4; p < pe; p++)
-#pragma unroll
-                    for (int i = 0; i < NU; i++) o[i] += ar[p] * (float)vt[i][p] * vsr[i][p];
+                if (tid < nc * NB) s_vst[(tid % NB) * VCH + tid / NB] = vsv;
             }
             __syncthreads();
+            if (c0 + VCH < Lmax) AR_LOAD_V(c0 + VCH);
+            // this chunk's positions of t0 (pa) and of t0 + 1 (pb = pa or pa + 1)
+            const int pa = __builtin_amdgcn_readfirstlane(imax(0, imin(nc, La - c0)));
+            const int pb = __builtin_amdgcn_readfirstlane(imax(0, imin(nc, Lb - c0)));
+            if (vwork && pb > 0) {
+                const int pa4 = pa & ~3;
+                const float *a0 = s_a + (size_t)t0 * lp + c0, *a1 = a0 + lp;
+                const float *vsr = s_vst + (dv >> 5) * VCH, *vc = s_vf + dv;
+                // four positions a step, in two register sets: the next
+                // step's reads are issued before this step's products (past
+                // the end they read the last step again); the scheduling
+                // barrier keeps them above the products, and the empty asm
+                // after the products takes their registers, so they neither
+                // wait before the products nor fold into the next step
+#define AR_V_READ(S, q)                                                                     \
+    S##x0 = *reinterpret_cast<const v4f_a *>(a0 + (q));                                     \
+    S##x1 = *reinterpret_cast<const v4f_a *>(a1 + (q));                                     \
+    S##s = *reinterpret_cast<const v4f_a *>(vsr + (q));                                     \
+    S##v0 = vc[(q) * VS];                                                                   \
+    S##v1 = vc[((q) + 1) * VS];                                                             \
+    S##v2 = vc[((q) + 2) * VS];                                                             \
+    S##v3 = vc[((q) + 3) * VS]
+#define AR_V_STEP(S)                                                                        \
+    {                                                                                       \
+        const float q0 = S##x0[0] * S##v0 * S##s[0], q1 = S##x0[1] * S##v1 * S##s[1];       \
+        const float q2 = S##x0[2] * S##v2 * S##s[2], q3 = S##x0[3] * S##v3 * S##s[3];       \
+        const float r0 = S##x1[0] * S##v0 * S##s[0], r1 = S##x1[1] * S##v1 * S##s[1];       \
+        const float r2 = S##x1[2] * S##v2 * S##s[2], r3 = S##x1[3] * S##v3 * S##s[3];       \
+        o0 += q0;                                                                           \
+        o1 += r0;                                                                           \
+        o0 += q1;                                                                           \
+        o1 += r1;                                                                           \
+        o0 += q2;                                                                           \
+        o1 += r2;                                                                           \
+        o0 += q3;                                                                           \
+        o1 += r3;                                                                           \
+    }
+#define AR_V_HOLD(S)                                                                        \
+    asm volatile("" : "+v"(o0), "+v"(o1), "+v"(S##x0), "+v"(S##x1), "+v"(S##s), "+v"(S##v0), \
+                 "+v"(S##v1), "+v"(S##v2), "+v"(S##v3))
+                if (pa4 > 0) {
+                    v4f_a Ax0, Ax1, As, Bx0, Bx1, Bs;
+                    float Av0, Av1, Av2, Av3, Bv0, Bv1, Bv2, Bv3;
+                    AR_V_READ(A, 0);
+                    for (int p = 0;; p += 8) {
+                        AR_V_READ(B, imin(p + 4, pa4 - 4));
+                        __builtin_amdgcn_sched_barrier(0);
+                        AR_V_STEP(A);
+                        AR_V_HOLD(B);
+                        if (p + 4 >= pa4) break;
+                        AR_V_READ(A, imin(p + 8, pa4 - 4));
+                        __builtin_amdgcn_sched_barrier(0);
+                        AR_V_STEP(B);
+                        AR_V_HOLD(A);
+                        if (p + 8 >= pa4) break;
+                    }
+                }
+#undef AR_V_READ
+#undef AR_V_STEP
+#undef AR_V_HOLD
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int p = pa4 + j;
+                    if (p >= pb) break;
+                    const float v = vc[p * VS], s = vsr[p];
+                    if (p < pa) o0 += a0[p] * v * s;
+                    o1 += a1[p] * v * s;
+                }
+            }
         }
     }
+#undef AR_LOAD_K
+#undef AR_LOAD_V
     if (!vwork) return;
-    // 5. gate, quantization
+    // 5. gate, quantization (t0, then t0 + 1 when it is a row of the item)
 #pragma unroll
-    for (int i = 0; i < NU; i++) {
-        const int d = (i * WPT + part) * 64 + lane;
-        const float gate = a.qg[(size_t)t * a.qg_dim + (size_t)h * 2 * HD + HD + d];
-        const float y = o[i] * d_sigmoid(gate, tab);
-        const int col = h * HD + d;
-        if (a.out) a.out[(size_t)t * a.q_dim + col] = y;
+    for (int i = 0; i < 2; i++) {
+        if (i == 1 && !vboth) break;
+        const int tt = t0 + i;
+        const float gate = a.qg[(size_t)tt * a.qg_dim + (size_t)h * 2 * HD + HD + dv];
+        const float y = (i ? o1 : o0) * d_sigmoid(gate, tab);
+        const int col = h * HD + dv;
+        if (a.out) a.out[(size_t)tt * a.q_dim + col] = y;
         int8_t q;
         float sg;
         d_quant_group32(y, &q, &sg);
-        a.oq[(size_t)t * a.q_dim + col] = q;
-        if ((d & 31) == 0) a.oqs[(size_t)t * (a.q_dim >> 5) + (col >> 5)] = sg;
+        a.oq[(size_t)tt * a.q_dim + col] = q;
+        if ((dv & 31) == 0) a.oqs[(size_t)tt * (a.q_dim >> 5) + (col >> 5)] = sg;
     }
 }
 
