@@ -1022,7 +1022,21 @@ __global__ __launch_bounds__(AR_THREADS) void k_attn_rows(AttnArgs b, const Attn
     __shared__ __align__(16) float s_q[TPB][HD];                 // the prepared q heads
     char *stage = smem;
     float *s_a = reinterpret_cast<float *>(smem + P::STAGE);      // [TPB][lp]
-    const int h = blockIdx.x, item = blockIdx.y;
+    // block -> (q head, item): blocks go to the 8 XCDs in turn by linear
+    // index L, and L and L + B/2 share a CU; when the grid allows, XCD x
+    // takes the (item, head) pairs [x B/16, (x+1) B/16) of each half, so the
+    // q heads of a kv head (and an item's kv heads) share one L2, and the
+    // halves keep the host's long/short item pairing on each CU
+    int h = blockIdx.x, item = blockIdx.y;
+    {
+        const int B = gridDim.x * gridDim.y, hb = B >> 1;
+        if ((B & 15) == 0 && (B >> 4) % (b.nh / b.nkv) == 0) {
+            const int L = blockIdx.y * gridDim.x + blockIdx.x, hf = L >= hb ? 1 : 0, r = L - hf * hb;
+            const int lam = hf * hb + (r & 7) * (B >> 4) + (r >> 3);
+            item = lam / gridDim.x;
+            h = lam - item * gridDim.x;
+        }
+    }
     const AttnItem it = items[item];
     const AttnArgs a = attn_item_args(b, it, plane);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, t = wave / WPT, part = wave - t * WPT;

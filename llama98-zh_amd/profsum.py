@@ -51,14 +51,36 @@ def table(groups, title, total_label):
     return "\n".join(out)
 
 
+def counters(paths):
+    """Mean per dispatch of every counter in rocprofv3 --pmc CSVs, by kernel."""
+    vals = collections.defaultdict(lambda: collections.defaultdict(list))
+    for p in paths:
+        with open(p, newline="") as f:
+            for r in csv.DictReader(f):
+                vals[short(r["Kernel_Name"]).strip()][r["Counter_Name"]].append(float(r["Counter_Value"]))
+    for k, cs in vals.items():
+        print(f"### `{k}`")
+        print()
+        print("| counter | dispatches | mean per dispatch |")
+        print("|---|---:|---:|")
+        for c in sorted(cs):
+            v = cs[c]
+            print(f"| {c} | {len(v)} | {sum(v) / len(v):.0f} |")
+        print()
+
+
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("trace")
+    ap.add_argument("trace", nargs="?")
+    ap.add_argument("--counters", nargs="+", help="rocprofv3 --pmc counter CSVs: per-kernel means instead")
     ap.add_argument("--vocab", type=int, default=65536)
     ap.add_argument("--gemv-rows-per-block", type=int, default=32,
                     help="rows per GEMV tile at the lm_head's input width")
     ap.add_argument("--verify-batches", type=int, default=0, help="summarize the last N batched verifies")
     a = ap.parse_args()
+    if a.counters:
+        counters(a.counters)
+        return
     rows = load(a.trace)
     whole = collections.defaultdict(list)
     for n, s, e, g, w, *_ in rows:
