@@ -73,6 +73,45 @@ def test_configs4_batched_verify_top8_128_experts(pkg, xlserver):
         eng.close()
 
 
+def test_batched_verify_of_seven_rows_128_wide_heads(pkg, xlserver):
+    """8 sessions of configs[3]'s model verifying 7 rows each (k = 6): the
+    attention item launch takes 8 tokens per block (k_attn_rows<128, 1>: a
+    wave per token pair in the value sums, the last pair holding one row),
+    with the long/short item order and the per-XCD block mapping in effect
+    (16 q heads x 8 items); the batch equals the same sessions verified one
+    by one, bit for bit."""
+    print("[case] 8 sessions x 7 verify rows, 128-wide heads, contexts 256-2048", flush=True)
+    eng = pkg.Engine(xlserver)
+    rng = np.random.default_rng(7)
+    ctx = rng.integers(256, 2049, size=8)
+    V, rows = eng.V, 7
+    batch, single = [], []
+    try:
+        for i, n in enumerate(ctx):
+            prompt = pkg.prompt_tokens(7000 + i, int(n), V)
+            for group in (batch, single):
+                st = eng.add_session()
+                eng.session_start_on(st, prompt)
+                group.append(st)
+        toks = np.array([[(97 * i + 29 * j + 3) % V for j in range(rows)] for i in range(8)], np.int32)
+        pos0 = ctx.astype(np.int32)
+        _, out = eng.verify_batch(batch, toks, pos0)
+        d = eng.d
+        for i, st in enumerate(single):
+            t = np.ascontiguousarray(toks[i])
+            assert eng.lib.lz_forward_verify(C.byref(eng.m), C.byref(st), t.ctypes.data_as(C.POINTER(C.c_int)), rows,
+                                             int(pos0[i])) == 0
+            lg = np.ctypeslib.as_array(st.mtp_logits, shape=(pkg.L98_SPEC_K_GPU + 1, V))[:rows]
+            hd = np.ctypeslib.as_array(st.mtp_verify_hidden, shape=(pkg.L98_SPEC_K_GPU + 1, d))[:rows]
+            assert same_bits(out[i][0], lg), f"session {i} (ctx {ctx[i]}) logits: " + diff_report(out[i][0], lg)
+            assert same_bits(out[i][1], hd), f"session {i} (ctx {ctx[i]}) hidden: " + diff_report(out[i][1], hd)
+            assert batch[i].ssm_slot == st.ssm_slot
+    finally:
+        for st in batch + single:
+            eng.free_session(st)
+        eng.close()
+
+
 def test_configs2_k7_temperature_matches_restatement(pkg, base):
     g = fixture("ora_base_p512_k7_temp.json")
     print("[case] configs[2]: configs[1] model, T=0.8 top-p 0.95, k=7, 512-token prompt", flush=True)
