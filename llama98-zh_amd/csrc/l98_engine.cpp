@@ -1598,6 +1598,7 @@ int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, 
     if ((pos_base || wait_ev || rec_ev) && !prefill_items) return 1;   // only a prefill chunk is split
     int n_attn = n_items;
     int max_len = 1, max_rows = 1;          // the attention items' longest row span and most rows
+    int kda_max_n = 1;                      // the KDA items' most rows
     {
         std::vector<KdaItem> ki((size_t)n_items);
         std::vector<AttnItem> ai;
@@ -1609,6 +1610,7 @@ int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, 
             attn_items = attn_items && I.n <= MAX_CHUNK;
             max_len = I.pos0 + I.n > max_len ? I.pos0 + I.n : max_len;
             ki[i] = KdaItem{s->kda, s->conv, &s->ctl->slot_base, s->kda_slot, s->conv_slot, I.row0, I.n, s->depth, 0};
+            kda_max_n = I.n > kda_max_n ? I.n : kda_max_n;
             if (prefill_items) {
                 for (int c0 = 0; c0 < I.n; c0 += MAX_CHUNK) {
                     const int nr = I.n - c0 < MAX_CHUNK ? I.n - c0 : MAX_CHUNK;
@@ -1751,7 +1753,7 @@ int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, 
                 CK(l98k_kda_split(&a, items[0].n, kd, c.conv_kernel, st));
                 if (rec_ev) CK(hipEventRecord(rec_ev[l], st));
             } else {
-                CK(l98k_kda_items(&a, w->kitems, n_items, (size_t)li * nv * kd * c.lin_v_head_dim,
+                CK(l98k_kda_items(&a, w->kitems, n_items, kda_max_n, (size_t)li * nv * kd * c.lin_v_head_dim,
                                   (size_t)li * c.lin_conv_dim * hist, kd, c.conv_kernel, st));
             }
             CK(mf(L.ko, w->xq2, w->xqs2, R, w->blk, d, st));

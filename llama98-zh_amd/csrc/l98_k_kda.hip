@@ -446,11 +446,13 @@ __global__ __launch_bounds__(4 * KD) void k_kda_step(KdaStepArgs a) {
 
 // Several sessions' rows in one launch: block (head, item); item i is a
 // session's rows [row0, row0 + n) against its own state and conv rings
-// (layer offsets added here), in MAX_CHUNK-row sub-chunks in order (a
-// sub-chunk reads back the state and conv history the previous one wrote,
-// from the same threads).  The launch's args carry the layer's weights and
-// the row buffers at row 0.  Rows advance the ring only for n <= MAX_CHUNK.
-template <int KD, int K>
+// (layer offsets added here), in NT-row sub-chunks in order (a sub-chunk
+// reads back the state and conv history the previous one wrote, from the
+// same threads).  The launch's args carry the layer's weights and the row
+// buffers at row 0.  Rows advance the ring only for n <= NT.  NT = 4 when
+// every item has at most 4 rows (a session batch's verify at k <= 3), so
+// that the token-slot work is not done for slots no item has.
+template <int KD, int K, int NT>
 __global__ __launch_bounds__(4 * KD) void k_kda_items(KdaStepArgs b, const KdaItem *__restrict__ items,
                                                       size_t state_off, size_t conv_off) {
     const KdaItem it = items[blockIdx.y];
@@ -461,9 +463,9 @@ __global__ __launch_bounds__(4 * KD) void k_kda_items(KdaStepArgs b, const KdaIt
     a.slot_stride = it.slot_stride;
     a.conv_slot_stride = it.conv_slot_stride;
     a.depth = it.depth;
-    for (int c0 = 0; c0 < it.n; c0 += MAX_CHUNK) {
+    for (int c0 = 0; c0 < it.n; c0 += NT) {
         const int r = it.row0 + c0;
-        a.nt = imin(MAX_CHUNK, it.n - c0);
+        a.nt = imin(NT, it.n - c0);
         a.pq = b.pq + (size_t)r * b.key;
         a.pk = b.pk + (size_t)r * b.key;
         a.pv = b.pv + (size_t)r * b.value;
@@ -475,7 +477,7 @@ __global__ __launch_bounds__(4 * KD) void k_kda_items(KdaStepArgs b, const KdaIt
         a.raw_out = b.raw_out ? b.raw_out + (size_t)r * b.value : nullptr;
         a.normed_out = b.normed_out ? b.normed_out + (size_t)r * b.value : nullptr;
         if (c0) __syncthreads();
-        kda_step_body<KD, K, MAX_CHUNK>(a, blockIdx.x);
+        kda_step_body<KD, K, NT>(a, blockIdx.x);
     }
 }
 
@@ -665,13 +667,18 @@ extern "C" int l98k_kda_step(const KdaStepArgs *a, int kd, int K, hipStream_t st
     return (int)hipGetLastError();
 }
 
-extern "C" int l98k_kda_items(const KdaStepArgs *a, const KdaItem *items, int n_items, size_t state_off,
+extern "C" int l98k_kda_items(const KdaStepArgs *a, const KdaItem *items, int n_items, int max_n, size_t state_off,
                               size_t conv_off, int kd, int K, hipStream_t st) {
     if (n_items < 1 || a->rank < 32 || (a->rank & 31) || a->rank > KDA_MAX_RANK || a->key != a->nv * kd ||
         a->value != a->nv * kd || K < 2 || K > 4)
         return -1;
-#define KDA_ITEMS(KD_, K_) \
-    hipLaunchKernelGGL((k_kda_items<KD_, K_>), dim3(a->nv, n_items), dim3(4 * (KD_)), 0, st, *a, items, state_off, conv_off)
+#define KDA_ITEMS(KD_, K_)                                                                                     \
+    if (max_n <= 4)                                                                                            \
+        hipLaunchKernelGGL((k_kda_items<KD_, K_, 4>), dim3(a->nv, n_items), dim3(4 * (KD_)), 0, st, *a, items, \
+                           state_off, conv_off);                                                               \
+    else                                                                                                       \
+        hipLaunchKernelGGL((k_kda_items<KD_, K_, MAX_CHUNK>), dim3(a->nv, n_items), dim3(4 * (KD_)), 0, st, *a, \
+                           items, state_off, conv_off)
     switch (kd * 8 + K) {
     case 64 * 8 + 4: KDA_ITEMS(64, 4); break;
     case 64 * 8 + 3: KDA_ITEMS(64, 3); break;

@@ -118,8 +118,8 @@ int l98k_mtp_pre(const int8_t *emb_q, const float *emb_s, int gs, const int *tok
 int l98k_kda_step(const KdaStepArgs *a, int kd, int K, hipStream_t st);
 // The KDA step of several sessions' rows in one launch (items in device
 // memory; state_off / conv_off: the layer's offsets inside each ring slot).
-int l98k_kda_items(const KdaStepArgs *a, const KdaItem *items, int n_items, size_t state_off, size_t conv_off,
-                   int kd, int K, hipStream_t st);
+int l98k_kda_items(const KdaStepArgs *a, const KdaItem *items, int n_items, int max_n, size_t state_off,
+                   size_t conv_off, int kd, int K, hipStream_t st);
 // One session's prefill of n > MAX_CHUNK rows (no ring advance) as three
 // launches: the state-free work of every row and head at once, the
 // recurrence (one block per head), the gated norm and quantization of every
