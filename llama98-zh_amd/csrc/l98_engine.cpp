@@ -1763,9 +1763,9 @@ int wide_forward(const DModel *m, DWide *w, const WideItem *items, int n_items, 
         CK(mf_multi({{&L.router, w->rl, E}, {&L.down, w->latx, lat}, {&L.sg, w->sgo, sw}, {&L.su, w->suo, sw}},
                     w->xq, w->xqs, R, st));
         const int pairs = R * topk;
-        CK(l98k_moe_route_wide(w->rl, L.bias, E, topk, R, w->sel_idx, w->sel_w, st));
+        // routing, and the latent rows quantized for the expert GEMMs, in one launch
+        CK(l98k_moe_route_wide(w->rl, L.bias, E, topk, R, w->sel_idx, w->sel_w, w->latx, lat, w->latq, w->latqs, st));
         CK(l98k_moe_group(w->sel_idx, pairs, topk, E, w->ng, w->gexp, w->goff, w->gcnt, w->list, w->pair_token, st));
-        CK(l98k_wide_pro(0, w->latx, nullptr, lat, nullptr, nullptr, 0, lat, R, w->latq, w->latqs, st));
         const int maxg = pairs < E ? pairs : E;
         const int mean_cols = (pairs + maxg - 1) / maxg;
         CK(l98k_mfma_gemm_grouped2(L.w1.q, L.w1.s, w->h1, L.w3.q, L.w3.s, w->h3, inter, lat, w->latq, w->latqs, w->ng,

@@ -449,11 +449,17 @@ extern "C" int l98k_moe_route(const float *logits, const float *bias, int E, int
 // ------------------------------------------------------ wide routing ---
 // Routing of many token rows: block g routes rows [8 g, 8 g + 8) with the
 // in-block router above (lz_moe_route per token, src/ops_moe.c:12-163), so
-// every row's selection and weights are those of the chunked path.
+// every row's selection and weights are those of the chunked path.  With
+// lx, the same rows of the latent lx[row][lat] (lat % 32 == 0, <= 4096)
+// are quantized per 32 into lq / lqs by the block's waves, a row per wave
+// at a time, lane l taking float4 l + 64 j: the wide producers' quantize
+// mode (quant_octet), so the expert GEMMs' input takes no launch of its own.
 __global__ __launch_bounds__(GEMV_THREADS) void k_moe_route_wide(const float *__restrict__ logits,
                                                                  const float *__restrict__ bias, int E, int topk,
                                                                  int rows, int *__restrict__ sel_idx,
-                                                                 float *__restrict__ sel_w) {
+                                                                 float *__restrict__ sel_w,
+                                                                 const float *__restrict__ lx, int lat,
+                                                                 int8_t *__restrict__ lq, float *__restrict__ lqs) {
     __shared__ RouteLds rt;
     __shared__ float tab[32];
     const int r0 = blockIdx.x * MAX_CHUNK;
@@ -463,6 +469,22 @@ __global__ __launch_bounds__(GEMV_THREADS) void k_moe_route_wide(const float *__
     if (tid < nt * topk) {
         sel_idx[(size_t)r0 * topk + tid] = rt.sel[tid];
         sel_w[(size_t)r0 * topk + tid] = rt.w[tid];
+    }
+    if (lx) {
+        const int lane = tid & 63, nf = lat >> 2, nb = lat >> 5;
+        for (int r = tid >> 6; r < nt; r += GEMV_THREADS / 64) {
+            const size_t row = (size_t)(r0 + r);
+            for (int j = 0; 64 * j < nf; j++) {           // wave-uniform
+                const int f = lane + 64 * j, fc = f < nf ? f : nf - 1;
+                const float4 v = reinterpret_cast<const float4 *>(lx + row * lat)[fc];
+                float sg;
+                const uint32_t q = quant_octet(v, &sg);
+                if (f < nf) {
+                    reinterpret_cast<uint32_t *>(lq + row * lat)[f] = q;
+                    if (!(f & 7)) lqs[row * nb + (f >> 3)] = sg;
+                }
+            }
+        }
     }
 }
 
@@ -512,10 +534,11 @@ __global__ __launch_bounds__(1024) void k_moe_group(const int *__restrict__ sel_
 }
 
 extern "C" int l98k_moe_route_wide(const float *logits, const float *bias, int E, int topk, int rows, int *sel_idx,
-                                   float *sel_w, hipStream_t st) {
+                                   float *sel_w, const float *lx, int lat, int8_t *lq, float *lqs, hipStream_t st) {
     if (E < 1 || E > MAX_EXPERTS || topk < 1 || topk > MAX_TOPK || rows < 1) return -1;
+    if (lx && (!lq || !lqs || lat < 32 || (lat & 31) || lat > 4096)) return -1;
     hipLaunchKernelGGL(k_moe_route_wide, dim3((rows + MAX_CHUNK - 1) / MAX_CHUNK), dim3(GEMV_THREADS), 0, st, logits,
-                       bias, E, topk, rows, sel_idx, sel_w);
+                       bias, E, topk, rows, sel_idx, sel_w, lx, lat, lq, lqs);
     return (int)hipGetLastError();
 }
 

@@ -154,9 +154,11 @@ int l98k_moe_route(const float *logits, const float *bias, int E, int topk, int 
                    hipStream_t st);
 int l98k_moe_up(const ExpertJob *jobs, int n_jobs, const float *logits, const float *bias, int E, int topk, int nt,
                 int *sel_idx, float *sel_w, MoeGroups *grp, int *tally, int in_dim, int out_rows, hipStream_t st);
-// Routing of `rows` token rows (8-row groups through the in-block router).
+// Routing of `rows` token rows (8-row groups through the in-block router);
+// with lx, the rows' latent lx[rows][lat] quantized per 32 into lq / lqs in
+// the same launch.
 int l98k_moe_route_wide(const float *logits, const float *bias, int E, int topk, int rows, int *sel_idx, float *sel_w,
-                        hipStream_t st);
+                        const float *lx, int lat, int8_t *lq, float *lqs, hipStream_t st);
 // The pairs of a wide routing grouped by expert (tables of the grouped GEMM).
 int l98k_moe_group(const int *sel_idx, int npairs, int topk, int E, int *ng, int *gexp, int *goff, int *gcnt,
                    int *list, int *pair_token, hipStream_t st);
